@@ -1,0 +1,165 @@
+/* include/smoe.h - C ABI of the MI355X (gfx950) quantized mixture-of-experts block.
+ *
+ * The drop-in boundary for StrataMetal's per-layer MoE call: `FfnExec::run`'s interior from `mixed` to
+ * `combined` (metal/src/layer_exec.cpp:470-530) and the kernel-level calls it is built from.  Plain
+ * pointers and sizes only; no exceptions cross this boundary.  Pointers are DEVICE pointers unless a
+ * comment says otherwise.  Every entry point validates its arguments before launching anything and
+ * returns a status; a refused call launches nothing and leaves every output untouched; a call with a
+ * zero count returns SMOE_OK without launching (metal/src/router.mm:33-37, metal/src/iq.mm:150-158).
+ * All work is enqueued on `hip_stream` (a hipStream_t; NULL = the null stream): no host
+ * synchronisation, no allocation.
+ *
+ * Weight layouts are GGUF's, unchanged:
+ *   Q2_0  (ggml type 42): 18-byte blocks {fp16 d; 16 code bytes} of 64 weights, value (code - 1) * d
+ *         (include/strata/artifact/dequant.hpp:8-13,69-78).
+ *   IQ2_S (ggml type 22): 82-byte blocks of 256 weights (include/strata/artifact/gguf_reader.hpp:197-200).
+ *   A 3-D expert tensor holds expert e at e * rows * row_bytes (metal/src/layer_exec.cpp:115-120).
+ *   q8_1 activations: 36-byte blocks {fp16 d; fp16 s; int8 q[32]} (metal/include/strata/metal/iq.hpp:42-43).
+ */
+#ifndef SMOE_H
+#define SMOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+    SMOE_OK = 0,
+    SMOE_EINVAL = -1, /* a count, shape or option is out of range */
+    SMOE_ESIZE = -2,  /* a caller-provided buffer (workspace) is too small */
+    SMOE_ETYPE = -3,  /* a ggml type this block does not implement */
+    SMOE_EDEVICE = -4,/* the HIP runtime reported an error at launch */
+    SMOE_EALIGN = -5, /* a pointer is not aligned as the layout requires */
+    SMOE_ENULL = -6   /* a required pointer is NULL */
+} smoe_status;
+
+enum { SMOE_Q2_0 = 42, SMOE_IQ2_S = 22 };
+
+/* Which arithmetic contract runs the expert products. */
+enum {
+    SMOE_PATH_AUTO = 0, /* GEMV for n_tokens < 128, MFMA otherwise */
+    SMOE_PATH_GEMV = 1, /* q8_1 activations, integer dot (the decode contract) */
+    SMOE_PATH_MFMA = 2  /* bf16 activations, bf16 MFMA with exact per-block weight scales (the prefill contract) */
+};
+
+/* Layer geometry.  ModelGeometry's MoE fields (include/strata/core/layout.hpp:27-59) plus the types. */
+typedef struct {
+    int32_t n_embd;       /* H: multiple of 128 (Q2_0) / 256 (IQ2_S), at most 8192 */
+    int32_t n_ff;         /* routed expert width: multiple of 128 / 256, at most 4096 */
+    int32_t n_ff_shared;  /* shared expert width (ignored when sh_type < 0) */
+    int32_t n_expert;     /* E: 1..1024 (metal/src/router.mm:33-37) */
+    int32_t top_k;        /* k: 1..64, k <= E */
+    int32_t w_type;       /* routed experts: SMOE_Q2_0 or SMOE_IQ2_S */
+    int32_t sh_type;      /* shared expert: SMOE_Q2_0 / SMOE_IQ2_S, or -1 = no shared expert */
+    int32_t router_dtype; /* 0 = bf16 (the repo's contract: include/strata/core/layer.hpp:131-136) */
+} smoe_geom;
+
+/* One layer's tensors, all resident in device memory (4-byte aligned). */
+typedef struct {
+    const void* gate_exps;       /* ffn_gate_exps: [E][n_ff] rows of n_embd */
+    const void* up_exps;         /* ffn_up_exps:   [E][n_ff] rows of n_embd */
+    const void* down_exps;       /* ffn_down_exps: [E][n_embd] rows of n_ff */
+    const void* router;          /* ffn_gate_inp: [E][n_embd] bf16 */
+    const void* gate_sh;         /* ffn_gate_shexp: [n_ff_shared] rows of n_embd */
+    const void* up_sh;           /* ffn_up_shexp */
+    const void* down_sh;         /* ffn_down_shexp: [n_embd] rows of n_ff_shared */
+    const uint16_t* gate_inp_sh; /* ffn_gate_inp_shexp: [n_embd] bf16 */
+    const float* logit_bias;     /* [E] added to the router logits before top-k, or NULL (synthetic routing only) */
+} smoe_weights;
+
+/* Optional device copies of intermediate results (FfnTrace, metal/include/strata/metal/layer_exec.hpp:100-109).
+ * Any pointer may be NULL. */
+typedef struct {
+    float* logits;    /* [T][E] router logits (bias included) */
+    int32_t* ids;     /* [T][k] selected experts, selection order */
+    float* weights;   /* [T][k] renormalised routing weights */
+    int32_t* counts;  /* [E] pairs per expert */
+    int32_t* offsets; /* [E+1] exclusive prefix sum of counts */
+    int32_t* perm;    /* [T*k] pair index t*k+s at each dispatch position */
+    int32_t* slot;    /* [T*k] dispatch position of pair t*k+s */
+    float* sgate;     /* [T] shared expert gate dot (before the sigmoid) */
+} smoe_trace;
+
+/* ---------------------------------------------------------------------------------------------- block */
+
+/* Workspace bytes smoe_forward needs for up to `max_tokens` tokens (either path); 0 on bad geometry. */
+size_t smoe_workspace_bytes(const smoe_geom* g, int32_t max_tokens);
+
+/* y[T][n_embd] = MoE(x[T][n_embd]): router, top-k, dispatch, expert products with SwiGLU, the shared
+ * expert times sigmoid(gate_inp_shexp . x) (added only when add_shared != 0), and the weighted combine.
+ * Replaces FfnExec::run's interior (metal/src/layer_exec.cpp:470-530) and the upstream per-layer
+ * moe_layer / moe_route + moe_finish (include/strata/core/layer.hpp:140-189).  `workspace` is
+ * device memory of at least smoe_workspace_bytes(g, n_tokens) bytes, 256-byte aligned; concurrent
+ * calls need distinct workspaces. */
+smoe_status smoe_forward(const smoe_geom* g, const smoe_weights* w, const float* x, int32_t n_tokens, float* y,
+                         int32_t add_shared, void* workspace, size_t workspace_bytes, const smoe_trace* trace,
+                         void* hip_stream);
+
+/* smoe_forward with an explicit contract (SMOE_PATH_*). */
+smoe_status smoe_forward_path(const smoe_geom* g, const smoe_weights* w, const float* x, int32_t n_tokens, float* y,
+                              int32_t add_shared, void* workspace, size_t workspace_bytes, const smoe_trace* trace,
+                              int32_t path, void* hip_stream);
+
+/* ---------------------------------------------------------------------------------------------- stages */
+
+/* logits (n_tokens, n_expert) f32 -> ids, weights (n_tokens, k): softmax over every expert, top k by
+ * (logit desc, id asc), weights renormalised by max(sum, 2^-14).  k <= 64, n_expert <= 1024.
+ * Replaces router_top10 (metal/include/strata/metal/router.hpp:16). */
+smoe_status smoe_router_topk(const float* logits, int32_t n_tokens, int32_t n_expert, int32_t k, int32_t* ids,
+                             float* weights, void* hip_stream);
+
+/* x [n] f32 -> bf16 bits, round to nearest even, NaN quieted.
+ * Replaces f32_to_bf16_bulk (metal/include/strata/metal/elementwise.hpp:27). */
+smoe_status smoe_f32_to_bf16(const float* x, int64_t n, uint16_t* y, void* hip_stream);
+
+/* y[o] = sum_i f32(x[i]) * f32(w[o][i]) for n_tok rows of bf16 x; y is (n_tok, n_out).
+ * Replaces bf16_gemv (metal/include/strata/metal/bf16_gemv.hpp:25). */
+smoe_status smoe_bf16_gemv(const uint16_t* x, const uint16_t* w, float* y, int32_t n_in, int32_t n_out,
+                           int32_t n_tok, void* hip_stream);
+
+/* x [n] f32 -> q8_1 blocks (n % 32 == 0).  Replaces iq_quantize_q8_1 (metal/include/strata/metal/iq.hpp:46). */
+smoe_status smoe_quantize_q8_1(const float* x, int64_t n, uint8_t* y, void* hip_stream);
+
+/* y[c * n_out + r] = W[r] . x[c] for n_col q8_1 columns; W is n_out rows of n_in values of `type`, the first
+ * at `w + byte_off`.  Replaces iq_mmvq (metal/include/strata/metal/iq.hpp:50-51). */
+smoe_status smoe_mmvq(int32_t type, const void* w, int64_t byte_off, const uint8_t* x_q8, int32_t n_in,
+                      int32_t n_out, int32_t n_col, float* y, void* hip_stream);
+
+/* y = q8_1(silu(gate) * up), n % 32 == 0.  Replaces iq_swiglu_q8 (metal/include/strata/metal/iq.hpp:54). */
+smoe_status smoe_swiglu_q8(const float* gate, const float* up, int64_t n, uint8_t* y, void* hip_stream);
+
+/* y = sum_{s<k} w[s] * parts[s] (+ shared), one token; k <= 64.
+ * Replaces moe_combine (metal/include/strata/metal/moe_combine.hpp:15). */
+smoe_status smoe_combine(const float* parts, const float* weights, const float* shared, float* y, int32_t n_embd,
+                         int32_t k, void* hip_stream);
+
+/* ids [n_tokens][k] -> counts [E], offsets [E+1], perm [T*k], slot [T*k]: the canonical stable dispatch
+ * (ascending pair index within an expert).  Replaces prefill::fused::group
+ * (include/strata/prefill/moe_fused.hpp:46-51) with a fixed in-expert order. */
+smoe_status smoe_dispatch(const int32_t* ids, int32_t n_tokens, int32_t k, int32_t n_expert, int32_t* counts,
+                          int32_t* offsets, int32_t* perm, int32_t* slot, void* hip_stream);
+
+/* ---------------------------------------------------------------------------------------------- synthetic inputs
+ * No counterpart in the reference: the seeded generators of the benchmark configurations (counter-based
+ * SplitMix64; normals by Box-Muller).  Bitwise equal to the host generators of the test oracle. */
+smoe_status smoe_synth_blocks(int32_t type, uint64_t seed, uint64_t stream_id, int64_t n_values, float sigma,
+                              void* out, void* hip_stream);
+smoe_status smoe_synth_bf16(uint64_t seed, uint64_t stream_id, int64_t n, float sigma, uint16_t* out,
+                            void* hip_stream);
+smoe_status smoe_synth_normal(uint64_t seed, uint64_t stream_id, int64_t n, float sigma, float* out,
+                              void* hip_stream);
+
+/* ---------------------------------------------------------------------------------------------- misc */
+const char* smoe_status_str(smoe_status s);
+/* Why the last call on this thread was refused ("" after a successful call).  Owned by the library. */
+const char* smoe_last_error(void);
+/* Version of this ABI (major * 100 + minor). */
+int32_t smoe_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,449 @@
+"""oracle - CPU restatement of StrataMetal's quantized MoE block (TEST INFRASTRUCTURE ONLY).
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import this package, and only
+as the checker or the timed CPU baseline.  The product path (stratametal_amd) never imports it.
+
+The C library (oracle/liboracle.so, built by oracle/Makefile) holds the arithmetic; this module wraps it
+for numpy arrays.  `ref()` loads oracle/_ref/libsmoe_ref.so, the reference's own header-only codecs
+compiled from /root/reference (None when that build is absent).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+from dataclasses import dataclass
+from typing import Optional
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB = None
+_REF = None
+
+Q2_0 = 42
+IQ2_S = 22
+
+
+def build(quiet: bool = True) -> None:
+    """Compile oracle/liboracle.so (and oracle/_ref where the reference tree exists)."""
+    out = subprocess.run(["make", "-C", _HERE, "all"], capture_output=True, text=True)
+    if out.returncode != 0:
+        raise RuntimeError("oracle build failed:\n" + out.stdout + out.stderr)
+    if not quiet:
+        print(out.stdout)
+
+
+def _p(a: np.ndarray):
+    return a.ctypes.data_as(C.c_void_p)
+
+
+def lib():
+    global _LIB
+    if _LIB is None:
+        path = os.path.join(_HERE, "liboracle.so")
+        if not os.path.exists(path):
+            build()
+        L = C.CDLL(path)
+        vp, i64, i32, u64, f32 = C.c_void_p, C.c_int64, C.c_int, C.c_uint64, C.c_float
+        sigs = {
+            "or_f16_from_f32": (C.c_uint16, [f32]),
+            "or_f32_from_f16": (f32, [C.c_uint16]),
+            "or_bf16_from_f32": (C.c_uint16, [f32]),
+            "or_f32_from_bf16": (f32, [C.c_uint16]),
+            "or_f16_from_f32_n": (None, [vp, i64, vp]),
+            "or_f32_from_f16_n": (None, [vp, i64, vp]),
+            "or_bf16_from_f32_n": (None, [vp, i64, vp]),
+            "or_expf": (f32, [f32]),
+            "or_logf": (f32, [f32]),
+            "or_cos2pi": (f32, [f32]),
+            "or_hash": (u64, [u64, u64, u64]),
+            "or_uniform": (f32, [u64, u64, u64]),
+            "or_normal": (f32, [u64, u64, u64]),
+            "or_gen_normal": (None, [u64, u64, i64, f32, vp]),
+            "or_gen_bf16": (None, [u64, u64, i64, f32, vp]),
+            "or_gen_q2_0": (None, [u64, u64, i64, f32, vp]),
+            "or_gen_iq2_s": (None, [u64, u64, i64, f32, vp]),
+            "or_dequant_q2_0": (None, [vp, i64, vp]),
+            "or_quant_q8_1": (None, [vp, i64, vp]),
+            "or_q2_0_gemv_dev": (None, [vp, vp, i32, i32, vp]),
+            "or_q2_0_gemv_ref": (None, [vp, vp, i32, i32, vp]),
+            "or_q2_0_gemv_exact": (None, [vp, vp, i32, i32, vp]),
+            "or_q2_0_gemv_no_minus_one": (None, [vp, vp, i32, i32, vp]),
+            "or_iq2s_grid": (None, [vp]),
+            "or_iq2_s_gemv_dev": (None, [vp, vp, i32, i32, vp]),
+            "or_iq2_s_gemv_ref": (None, [vp, vp, i32, i32, vp]),
+            "or_bf16_gemv_dev": (None, [vp, vp, i32, i32, vp]),
+            "or_bf16_gemv_double": (None, [vp, vp, i32, i32, vp]),
+            "or_route_dev": (None, [vp, i32, i32, i32, vp, vp]),
+            "or_route_ref": (None, [vp, i32, i32, i32, vp, vp]),
+            "or_swiglu_q8": (None, [vp, vp, i64, vp]),
+            "or_silu_mul": (f32, [f32, f32]),
+            "or_sigmoid": (f32, [f32]),
+            "or_combine_dev": (None, [vp, vp, vp, i32, i32, vp]),
+            "or_combine_double": (None, [vp, vp, vp, i32, i32, vp]),
+            "or_dispatch": (None, [vp, i32, i32, i32, vp, vp, vp, vp]),
+            "or_moe_decode_dev": (i32, [vp, vp, vp, i32, vp, i32, vp, i32]),
+            "or_moe_decode_ref": (i32, [vp, vp, vp, i32, vp, i32, i32]),
+            "or_moe_prefill": (i32, [vp, vp, vp, i32, vp, i32, vp, i32]),
+            "or_row_bytes": (i64, [i32, i64]),
+        }
+        for name, (res, args) in sigs.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _LIB = L
+    return _LIB
+
+
+def ref():
+    """The reference's own header-only codecs (oracle/_ref), or None if that build is absent."""
+    global _REF
+    if _REF is None:
+        path = os.path.join(_HERE, "_ref", "libsmoe_ref.so")
+        if not os.path.exists(path):
+            return None
+        R = C.CDLL(path)
+        R.ref_f16_from_f32.restype = C.c_uint16
+        R.ref_f16_from_f32.argtypes = [C.c_float]
+        R.ref_f32_from_f16.restype = C.c_float
+        R.ref_f32_from_f16.argtypes = [C.c_uint16]
+        R.ref_bf16_from_f32.restype = C.c_uint16
+        R.ref_bf16_from_f32.argtypes = [C.c_float]
+        for n in ("ref_f16_from_f32_n", "ref_bf16_from_f32_n", "ref_dequantize_q2_0"):
+            getattr(R, n).restype = None
+            getattr(R, n).argtypes = [C.c_void_p, C.c_int64, C.c_void_p]
+        R.ref_f32_from_f16_all.restype = None
+        R.ref_f32_from_f16_all.argtypes = [C.c_void_p]
+        R.ref_iq2s_grid.restype = None
+        R.ref_iq2s_grid.argtypes = [C.c_void_p]
+        _REF = R
+    return _REF
+
+
+# ------------------------------------------------------------------------------------------------ codecs
+
+def f16_from_f32(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty(x.shape, np.uint16)
+    lib().or_f16_from_f32_n(_p(x), x.size, _p(y))
+    return y
+
+
+def f32_from_f16(h: np.ndarray) -> np.ndarray:
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    y = np.empty(h.shape, np.float32)
+    lib().or_f32_from_f16_n(_p(h), h.size, _p(y))
+    return y
+
+
+def bf16_from_f32(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty(x.shape, np.uint16)
+    lib().or_bf16_from_f32_n(_p(x), x.size, _p(y))
+    return y
+
+
+def f32_from_bf16(h: np.ndarray) -> np.ndarray:
+    return (np.ascontiguousarray(h, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def row_bytes(wtype: int, n: int) -> int:
+    return int(lib().or_row_bytes(wtype, n))
+
+
+# ------------------------------------------------------------------------------------------------ generators
+
+def gen_normal(seed: int, stream: int, n: int, sigma: float = 1.0) -> np.ndarray:
+    y = np.empty(n, np.float32)
+    lib().or_gen_normal(seed, stream, n, sigma, _p(y))
+    return y
+
+
+def gen_bf16(seed: int, stream: int, n: int, sigma: float) -> np.ndarray:
+    y = np.empty(n, np.uint16)
+    lib().or_gen_bf16(seed, stream, n, sigma, _p(y))
+    return y
+
+
+def gen_q2_0(seed: int, stream: int, n_blocks: int, sigma: float = 0.02) -> np.ndarray:
+    y = np.empty(n_blocks * 18, np.uint8)
+    lib().or_gen_q2_0(seed, stream, n_blocks, sigma, _p(y))
+    return y
+
+
+def gen_iq2_s(seed: int, stream: int, n_blocks: int, sigma: float = 0.02) -> np.ndarray:
+    y = np.empty(n_blocks * 82, np.uint8)
+    lib().or_gen_iq2_s(seed, stream, n_blocks, sigma, _p(y))
+    return y
+
+
+def gen_blocks(wtype: int, seed: int, stream: int, n_values: int, sigma: float = 0.02) -> np.ndarray:
+    if wtype == Q2_0:
+        return gen_q2_0(seed, stream, n_values // 64, sigma)
+    if wtype == IQ2_S:
+        return gen_iq2_s(seed, stream, n_values // 256, sigma)
+    raise ValueError(wtype)
+
+
+# ------------------------------------------------------------------------------------------------ kernels
+
+def dequant_q2_0(blocks: np.ndarray) -> np.ndarray:
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+    nb = blocks.size // 18
+    y = np.empty(nb * 64, np.float32)
+    lib().or_dequant_q2_0(_p(blocks), nb, _p(y))
+    return y
+
+
+def quant_q8_1(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32).ravel()
+    y = np.empty(x.size // 32 * 36, np.uint8)
+    lib().or_quant_q8_1(_p(x), x.size, _p(y))
+    return y
+
+
+def _gemv(fn, w, xq, n_in, n_out, dtype=np.float32):
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    xq = np.ascontiguousarray(xq, dtype=np.uint8)
+    y = np.empty(n_out, dtype)
+    fn(_p(w), _p(xq), n_in, n_out, _p(y))
+    return y
+
+
+def q2_0_gemv_dev(w, xq, n_in, n_out):
+    return _gemv(lib().or_q2_0_gemv_dev, w, xq, n_in, n_out)
+
+
+def q2_0_gemv_ref(w, xq, n_in, n_out):
+    return _gemv(lib().or_q2_0_gemv_ref, w, xq, n_in, n_out)
+
+
+def q2_0_gemv_exact(w, xq, n_in, n_out):
+    return _gemv(lib().or_q2_0_gemv_exact, w, xq, n_in, n_out, np.float64)
+
+
+def q2_0_gemv_no_minus_one(w, xq, n_in, n_out):
+    return _gemv(lib().or_q2_0_gemv_no_minus_one, w, xq, n_in, n_out)
+
+
+def iq2_s_gemv_dev(w, xq, n_in, n_out):
+    return _gemv(lib().or_iq2_s_gemv_dev, w, xq, n_in, n_out)
+
+
+def iq2_s_gemv_ref(w, xq, n_in, n_out):
+    return _gemv(lib().or_iq2_s_gemv_ref, w, xq, n_in, n_out)
+
+
+def gemv_dev(wtype, w, xq, n_in, n_out):
+    return (iq2_s_gemv_dev if wtype == IQ2_S else q2_0_gemv_dev)(w, xq, n_in, n_out)
+
+
+def iq2s_grid() -> np.ndarray:
+    g = np.empty(1024, np.uint64)
+    lib().or_iq2s_grid(_p(g))
+    return g
+
+
+def bf16_gemv_dev(xb, w, n_in, n_out):
+    xb = np.ascontiguousarray(xb, dtype=np.uint16)
+    w = np.ascontiguousarray(w, dtype=np.uint16)
+    y = np.empty(n_out, np.float32)
+    lib().or_bf16_gemv_dev(_p(xb), _p(w), n_in, n_out, _p(y))
+    return y
+
+
+def bf16_gemv_double(xb, w, n_in, n_out):
+    xb = np.ascontiguousarray(xb, dtype=np.uint16)
+    w = np.ascontiguousarray(w, dtype=np.uint16)
+    y = np.empty(n_out, np.float32)
+    lib().or_bf16_gemv_double(_p(xb), _p(w), n_in, n_out, _p(y))
+    return y
+
+
+def _route(fn, logits, k):
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    if logits.ndim == 1:
+        logits = logits[None, :]
+    T, E = logits.shape
+    ids = np.empty((T, k), np.int32)
+    w = np.empty((T, k), np.float32)
+    fn(_p(logits), T, E, k, _p(ids), _p(w))
+    return ids, w
+
+
+def route_dev(logits, k):
+    return _route(lib().or_route_dev, logits, k)
+
+
+def route_ref(logits, k):
+    return _route(lib().or_route_ref, logits, k)
+
+
+def swiglu_q8(gate, up):
+    gate = np.ascontiguousarray(gate, dtype=np.float32).ravel()
+    up = np.ascontiguousarray(up, dtype=np.float32).ravel()
+    y = np.empty(gate.size // 32 * 36, np.uint8)
+    lib().or_swiglu_q8(_p(gate), _p(up), gate.size, _p(y))
+    return y
+
+
+def combine_dev(parts, w, shared):
+    parts = np.ascontiguousarray(parts, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    k, n = parts.shape
+    y = np.empty(n, np.float32)
+    sh = None if shared is None else np.ascontiguousarray(shared, dtype=np.float32)
+    lib().or_combine_dev(_p(parts), _p(w), None if sh is None else _p(sh), n, k, _p(y))
+    return y
+
+
+def combine_double(parts, w, shared):
+    parts = np.ascontiguousarray(parts, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    k, n = parts.shape
+    y = np.empty(n, np.float32)
+    sh = None if shared is None else np.ascontiguousarray(shared, dtype=np.float32)
+    lib().or_combine_double(_p(parts), _p(w), None if sh is None else _p(sh), n, k, _p(y))
+    return y
+
+
+def dispatch(ids, n_expert):
+    ids = np.ascontiguousarray(ids, dtype=np.int32)
+    T, k = ids.shape
+    counts = np.empty(n_expert, np.int32)
+    offsets = np.empty(n_expert + 1, np.int32)
+    perm = np.empty(T * k, np.int32)
+    slot = np.empty(T * k, np.int32)
+    lib().or_dispatch(_p(ids), T, k, n_expert, _p(counts), _p(offsets), _p(perm), _p(slot))
+    return counts, offsets, perm, slot
+
+
+# ------------------------------------------------------------------------------------------------ the block
+
+class _Geom(C.Structure):
+    _fields_ = [(n, C.c_int32) for n in ("n_embd", "n_ff", "n_ff_shared", "n_expert", "top_k", "w_type", "sh_type",
+                                         "router_dtype")]
+
+
+class _Weights(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in ("gate_exps", "up_exps", "down_exps", "router", "gate_sh", "up_sh",
+                                          "down_sh", "gate_inp_sh", "logit_bias")]
+
+
+class _Trace(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in ("logits", "ids", "weights", "counts", "offsets", "perm", "slot", "xq",
+                                          "hq", "parts", "shared", "sgate")]
+
+
+@dataclass
+class Geom:
+    n_embd: int = 2048
+    n_ff: int = 512
+    n_ff_shared: int = 512
+    n_expert: int = 512
+    top_k: int = 10
+    w_type: int = Q2_0
+    sh_type: int = Q2_0
+    router_dtype: int = 0
+
+    def c(self):
+        return _Geom(self.n_embd, self.n_ff, self.n_ff_shared, self.n_expert, self.top_k, self.w_type, self.sh_type,
+                     self.router_dtype)
+
+
+@dataclass
+class Weights:
+    gate_exps: np.ndarray
+    up_exps: np.ndarray
+    down_exps: np.ndarray
+    router: np.ndarray           # uint16 bf16 [E][H]
+    gate_sh: Optional[np.ndarray] = None
+    up_sh: Optional[np.ndarray] = None
+    down_sh: Optional[np.ndarray] = None
+    gate_inp_sh: Optional[np.ndarray] = None  # uint16 bf16 [H]
+    logit_bias: Optional[np.ndarray] = None   # f32 [E]
+
+    def c(self):
+        def ptr(a):
+            return None if a is None else a.ctypes.data
+        return _Weights(ptr(self.gate_exps), ptr(self.up_exps), ptr(self.down_exps), ptr(self.router),
+                        ptr(self.gate_sh), ptr(self.up_sh), ptr(self.down_sh), ptr(self.gate_inp_sh),
+                        ptr(self.logit_bias))
+
+
+def make_weights(g: Geom, seed: int, n_expert_alloc: Optional[int] = None, zipf_bias: Optional[np.ndarray] = None,
+                 sigma: float = 0.02) -> Weights:
+    """Synthetic layer weights from the counter RNG.  Stream ids: 1 gate, 2 up, 3 down, 4 router, 5/6/7 shared
+    gate/up/down, 8 shared gate_inp.  The device generator (smoe_synth_*) uses the same streams."""
+    E = g.n_expert if n_expert_alloc is None else n_expert_alloc
+    H, F, Fs = g.n_embd, g.n_ff, g.n_ff_shared
+    gate = gen_blocks(g.w_type, seed, 1, E * F * H, sigma)
+    up = gen_blocks(g.w_type, seed, 2, E * F * H, sigma)
+    down = gen_blocks(g.w_type, seed, 3, E * H * F, sigma)
+    router = gen_bf16(seed, 4, E * H, sigma)
+    w = Weights(gate, up, down, router)
+    if g.sh_type >= 0:
+        w.gate_sh = gen_blocks(g.sh_type, seed, 5, Fs * H, sigma)
+        w.up_sh = gen_blocks(g.sh_type, seed, 6, Fs * H, sigma)
+        w.down_sh = gen_blocks(g.sh_type, seed, 7, H * Fs, sigma)
+        w.gate_inp_sh = gen_bf16(seed, 8, H, sigma)
+    if zipf_bias is not None:
+        w.logit_bias = np.ascontiguousarray(zipf_bias, dtype=np.float32)
+    return w
+
+
+def _run_block(fn, g: Geom, w: Weights, x: np.ndarray, add_shared: bool, trace: bool, n_threads: int, with_trace=True):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    T = x.shape[0]
+    y = np.empty_like(x)
+    gc, wc = g.c(), w.c()
+    tr = None
+    out = {}
+    if trace and with_trace:
+        H, E, K, F = g.n_embd, g.n_expert, g.top_k, g.n_ff
+        out = dict(logits=np.empty((T, E), np.float32), ids=np.empty((T, K), np.int32),
+                   weights=np.empty((T, K), np.float32), counts=np.empty(E, np.int32),
+                   offsets=np.empty(E + 1, np.int32), perm=np.empty(T * K, np.int32), slot=np.empty(T * K, np.int32),
+                   xq=np.empty(T * H // 32 * 36, np.uint8), hq=np.empty(T * K * F // 32 * 36, np.uint8),
+                   parts=np.empty((T * K, H), np.float32), shared=np.empty((T, H), np.float32),
+                   sgate=np.empty(T, np.float32))
+        tr = _Trace(*[out[n].ctypes.data for n in ("logits", "ids", "weights", "counts", "offsets", "perm", "slot",
+                                                   "xq", "hq", "parts", "shared", "sgate")])
+    if with_trace:
+        rc = fn(C.byref(gc), C.byref(wc), _p(x), T, _p(y), int(add_shared), None if tr is None else C.byref(tr),
+                n_threads)
+    else:
+        rc = fn(C.byref(gc), C.byref(wc), _p(x), T, _p(y), int(add_shared), n_threads)
+    if rc != 0:
+        raise ValueError(f"oracle rejected the block (rc={rc})")
+    return (y, out) if trace else y
+
+
+def moe_decode_dev(g, w, x, add_shared=True, trace=False, n_threads=1):
+    return _run_block(lib().or_moe_decode_dev, g, w, x, add_shared, trace, n_threads)
+
+
+def moe_decode_ref(g, w, x, add_shared=True, n_threads=1):
+    return _run_block(lib().or_moe_decode_ref, g, w, x, add_shared, False, n_threads, with_trace=False)
+
+
+def moe_prefill(g, w, x, add_shared=True, trace=False, n_threads=1):
+    return _run_block(lib().or_moe_prefill, g, w, x, add_shared, trace, n_threads)
+
+
+# ------------------------------------------------------------------------------------------------ metrics
+
+def rel_l1_rows(got: np.ndarray, want: np.ndarray) -> np.ndarray:
+    """Per-row sum|a-b| / sum|b| (metal/src/pack_parity.cpp:2425-2433, metal/src/iq_parity.cpp:306-313)."""
+    got = np.atleast_2d(np.asarray(got, np.float64))
+    want = np.atleast_2d(np.asarray(want, np.float64))
+    num = np.abs(got - want).sum(axis=1)
+    den = np.abs(want).sum(axis=1)
+    return np.where(den > 0, num / np.where(den > 0, den, 1.0), np.where(num == 0, 0.0, 1.0))
+
+
+def zipf_bias(n_expert: int, s: float, seed: int, scale: float = 1.0) -> np.ndarray:
+    """Logit bias b_e = scale * log(rank_e^-s) over a seeded rank permutation (config 3's Zipf routing)."""
+    ranks = np.argsort(np.argsort(gen_normal(seed, 99, n_expert)))  # a seeded permutation of 0..E-1
+    return (scale * (-s) * np.log(ranks.astype(np.float64) + 1.0)).astype(np.float32)

@@ -1,0 +1,34 @@
+// oracle/ref_shim.cpp - exports the reference's own header-only codecs and IQ2_S codebook with C linkage,
+// so tests can pin the oracle's restatements against the reference itself.  Compiled by oracle/Makefile
+// against the headers where they lie under /root/reference; nothing of the reference is copied here.
+//   include/strata/kernels/f16_bits.hpp:37-101   f16_from_f32 / f32_from_f16
+//   include/strata/kernels/bf16_bits.hpp:37-59   bf16_from_f32 / f32_from_bf16
+//   include/strata/artifact/dequant.hpp:69-78    dequantize_q2_0
+//   metal/include/strata/metal/iq_grids.hpp:5    iq2s_grid
+#include "strata/artifact/dequant.hpp"
+#include "strata/kernels/bf16_bits.hpp"
+#include "strata/kernels/f16_bits.hpp"
+#include "strata/metal/iq_grids.hpp"
+
+#include <cstdint>
+#include <cstring>
+
+extern "C" {
+uint16_t ref_f16_from_f32(float f) { return strata::kernels::f16_from_f32(f); }
+float ref_f32_from_f16(uint16_t h) { return strata::kernels::f32_from_f16(h); }
+uint16_t ref_bf16_from_f32(float f) { return strata::kernels::bf16_from_f32(f); }
+float ref_f32_from_bf16(uint16_t h) { return strata::kernels::f32_from_bf16(h); }
+void ref_f16_from_f32_n(const float* x, int64_t n, uint16_t* y) {
+    for (int64_t i = 0; i < n; ++i) y[i] = strata::kernels::f16_from_f32(x[i]);
+}
+void ref_bf16_from_f32_n(const float* x, int64_t n, uint16_t* y) {
+    for (int64_t i = 0; i < n; ++i) y[i] = strata::kernels::bf16_from_f32(x[i]);
+}
+void ref_f32_from_f16_all(float* out65536) {
+    for (uint32_t h = 0; h < 65536u; ++h) out65536[h] = strata::kernels::f32_from_f16((uint16_t) h);
+}
+void ref_dequantize_q2_0(const uint8_t* blocks, int64_t n_blocks, float* out) {
+    for (int64_t b = 0; b < n_blocks; ++b) strata::dequantize_q2_0(blocks + b * 18, out + b * 64);
+}
+void ref_iq2s_grid(uint64_t* out1024) { std::memcpy(out1024, strata::metal::iq2s_grid, sizeof(strata::metal::iq2s_grid)); }
+}

@@ -1,0 +1,298 @@
+"""stratametal_amd - MI355X (gfx950) quantized mixture-of-experts block.
+
+Python host binding of the C ABI in include/smoe.h (libsmoe.so, built by stratametal_amd/build.py).  The
+arithmetic lives in the HIP kernels; this module only passes device pointers (torch tensors supply the
+memory and the stream) and turns refused calls into exceptions, as the reference's wrappers throw
+MetalError (metal/include/strata/metal/device.hpp:28-31).  There is no CPU fallback: without the built
+library every entry point raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from dataclasses import dataclass
+from typing import Dict, Optional
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "lib", "libsmoe.so")
+_LIB = None
+
+Q2_0 = 42
+IQ2_S = 22
+PATH_AUTO, PATH_GEMV, PATH_MFMA = 0, 1, 2
+
+_STATUS = {0: "ok", -1: "invalid argument", -2: "buffer too small", -3: "unsupported ggml type",
+           -4: "HIP runtime error", -5: "misaligned pointer", -6: "NULL pointer"}
+
+
+class SmoeError(RuntimeError):
+    """A call the library refused (status != SMOE_OK); `.status` is the smoe_status code."""
+
+    def __init__(self, status: int, msg: str):
+        super().__init__(f"{_STATUS.get(status, status)}: {msg}")
+        self.status = status
+
+
+class _Geom(C.Structure):
+    _fields_ = [(n, C.c_int32) for n in ("n_embd", "n_ff", "n_ff_shared", "n_expert", "top_k", "w_type", "sh_type",
+                                         "router_dtype")]
+
+
+class _Weights(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in ("gate_exps", "up_exps", "down_exps", "router", "gate_sh", "up_sh",
+                                          "down_sh", "gate_inp_sh", "logit_bias")]
+
+
+class _Trace(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in ("logits", "ids", "weights", "counts", "offsets", "perm", "slot", "sgate")]
+
+
+def lib():
+    """The loaded libsmoe.so.  Raises ImportError when it has not been built (no fallback exists)."""
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(f"{LIB_PATH} is missing: build it with `python -m stratametal_amd.build`")
+        L = C.CDLL(LIB_PATH)
+        vp, i32, i64, u64, f32 = C.c_void_p, C.c_int32, C.c_int64, C.c_uint64, C.c_float
+        sigs = {
+            "smoe_workspace_bytes": (C.c_size_t, [vp, i32]),
+            "smoe_forward": (i32, [vp, vp, vp, i32, vp, i32, vp, C.c_size_t, vp, vp]),
+            "smoe_forward_path": (i32, [vp, vp, vp, i32, vp, i32, vp, C.c_size_t, vp, i32, vp]),
+            "smoe_router_topk": (i32, [vp, i32, i32, i32, vp, vp, vp]),
+            "smoe_f32_to_bf16": (i32, [vp, i64, vp, vp]),
+            "smoe_bf16_gemv": (i32, [vp, vp, vp, i32, i32, i32, vp]),
+            "smoe_quantize_q8_1": (i32, [vp, i64, vp, vp]),
+            "smoe_mmvq": (i32, [i32, vp, i64, vp, i32, i32, i32, vp, vp]),
+            "smoe_swiglu_q8": (i32, [vp, vp, i64, vp, vp]),
+            "smoe_combine": (i32, [vp, vp, vp, vp, i32, i32, vp]),
+            "smoe_dispatch": (i32, [vp, i32, i32, i32, vp, vp, vp, vp, vp]),
+            "smoe_synth_blocks": (i32, [i32, u64, u64, i64, f32, vp, vp]),
+            "smoe_synth_bf16": (i32, [u64, u64, i64, f32, vp, vp]),
+            "smoe_synth_normal": (i32, [u64, u64, i64, f32, vp, vp]),
+            "smoe_status_str": (C.c_char_p, [i32]),
+            "smoe_last_error": (C.c_char_p, []),
+            "smoe_abi_version": (i32, []),
+        }
+        for name, (res, args) in sigs.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _LIB = L
+    return _LIB
+
+
+def _check(status: int):
+    if status != 0:
+        raise SmoeError(status, lib().smoe_last_error().decode())
+
+
+def _ptr(t) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(stream=None) -> int:
+    import torch
+    s = torch.cuda.current_stream() if stream is None else stream
+    return s.cuda_stream
+
+
+def row_bytes(wtype: int, n: int) -> int:
+    if wtype == Q2_0:
+        return n // 64 * 18
+    if wtype == IQ2_S:
+        return n // 256 * 82
+    raise ValueError(wtype)
+
+
+@dataclass
+class Geom:
+    """Layer geometry (smoe_geom).  Defaults are the benchmark configurations' layer."""
+    n_embd: int = 2048
+    n_ff: int = 512
+    n_ff_shared: int = 512
+    n_expert: int = 512
+    top_k: int = 10
+    w_type: int = Q2_0
+    sh_type: int = Q2_0
+    router_dtype: int = 0
+
+    def c(self) -> _Geom:
+        return _Geom(self.n_embd, self.n_ff, self.n_ff_shared, self.n_expert, self.top_k, self.w_type, self.sh_type,
+                     self.router_dtype)
+
+    def expert_bytes(self) -> int:
+        return 2 * self.n_ff * row_bytes(self.w_type, self.n_embd) + self.n_embd * row_bytes(self.w_type, self.n_ff)
+
+    def shared_bytes(self) -> int:
+        if self.sh_type < 0:
+            return 0
+        return (2 * self.n_ff_shared * row_bytes(self.sh_type, self.n_embd)
+                + self.n_embd * row_bytes(self.sh_type, self.n_ff_shared))
+
+
+def workspace_bytes(g: Geom, max_tokens: int) -> int:
+    n = lib().smoe_workspace_bytes(C.byref(g.c()), max_tokens)
+    if n == 0:
+        raise SmoeError(-1, lib().smoe_last_error().decode() or "bad geometry")
+    return n
+
+
+# ------------------------------------------------------------------------------------------------ layers
+
+WEIGHT_NAMES = ("gate_exps", "up_exps", "down_exps", "router", "gate_sh", "up_sh", "down_sh", "gate_inp_sh",
+                "logit_bias")
+
+
+def synth_layer(g: Geom, seed: int, device="cuda", sigma: float = 0.02, logit_bias=None, stream=None) -> Dict:
+    """A synthetic layer generated on the device (streams: 1 gate, 2 up, 3 down, 4 router, 5/6/7 shared
+    gate/up/down, 8 shared gate_inp), bit-identical to the test oracle's host generators."""
+    import torch
+    L = lib()
+    st = _stream(stream)
+    H, F, Fs, E = g.n_embd, g.n_ff, g.n_ff_shared, g.n_expert
+
+    def blocks(t, stream_id, n_values):
+        buf = torch.empty(n_values // (64 if t == Q2_0 else 256) * (18 if t == Q2_0 else 82), dtype=torch.uint8,
+                          device=device)
+        _check(L.smoe_synth_blocks(t, seed, stream_id, n_values, sigma, buf.data_ptr(), st))
+        return buf
+
+    def bf16(stream_id, n):
+        buf = torch.empty(n, dtype=torch.int16, device=device)
+        _check(L.smoe_synth_bf16(seed, stream_id, n, sigma, buf.data_ptr(), st))
+        return buf
+
+    w = dict(gate_exps=blocks(g.w_type, 1, E * F * H), up_exps=blocks(g.w_type, 2, E * F * H),
+             down_exps=blocks(g.w_type, 3, E * H * F), router=bf16(4, E * H))
+    if g.sh_type >= 0:
+        w.update(gate_sh=blocks(g.sh_type, 5, Fs * H), up_sh=blocks(g.sh_type, 6, Fs * H),
+                 down_sh=blocks(g.sh_type, 7, H * Fs), gate_inp_sh=bf16(8, H))
+    if logit_bias is not None:
+        w["logit_bias"] = logit_bias
+    return w
+
+
+def synth_normal(seed: int, stream_id: int, n: int, sigma: float = 1.0, device="cuda", stream=None):
+    import torch
+    out = torch.empty(n, dtype=torch.float32, device=device)
+    _check(lib().smoe_synth_normal(seed, stream_id, n, sigma, out.data_ptr(), _stream(stream)))
+    return out
+
+
+def _weights_c(w: Dict) -> _Weights:
+    return _Weights(*[_ptr(w.get(n)) for n in WEIGHT_NAMES])
+
+
+class MoELayer:
+    """One layer's MoE call: the FfnExec shape (metal/include/strata/metal/layer_exec.hpp:113-140) over
+    smoe_forward.  Owns a workspace sized for `max_tokens`; weights stay the caller's tensors."""
+
+    def __init__(self, g: Geom, weights: Dict, max_tokens: int, device="cuda"):
+        import torch
+        self.g = g
+        self.w = weights
+        self._gc = g.c()
+        self._wc = _weights_c(weights)
+        self.max_tokens = max_tokens
+        self.ws_bytes = workspace_bytes(g, max_tokens)
+        self.ws = torch.empty(self.ws_bytes, dtype=torch.uint8, device=device)
+
+    def forward(self, x, y=None, add_shared: bool = True, trace: bool = False, path: int = PATH_AUTO, stream=None):
+        import torch
+        T = x.shape[0]
+        if T > self.max_tokens:
+            raise SmoeError(-2, f"{T} tokens exceed the workspace's {self.max_tokens}")
+        if y is None:
+            y = torch.empty_like(x)
+        tr = None
+        out = {}
+        if trace:
+            E, K, dev = self.g.n_expert, self.g.top_k, x.device
+            out = dict(logits=torch.empty((T, E), dtype=torch.float32, device=dev),
+                       ids=torch.empty((T, K), dtype=torch.int32, device=dev),
+                       weights=torch.empty((T, K), dtype=torch.float32, device=dev),
+                       counts=torch.empty(E, dtype=torch.int32, device=dev),
+                       offsets=torch.empty(E + 1, dtype=torch.int32, device=dev),
+                       perm=torch.empty(T * K, dtype=torch.int32, device=dev),
+                       slot=torch.empty(T * K, dtype=torch.int32, device=dev),
+                       sgate=torch.empty(T, dtype=torch.float32, device=dev))
+            tr = _Trace(*[out[n].data_ptr() for n in ("logits", "ids", "weights", "counts", "offsets", "perm", "slot",
+                                                       "sgate")])
+        _check(lib().smoe_forward_path(C.byref(self._gc), C.byref(self._wc), x.data_ptr(), T, y.data_ptr(),
+                                       int(add_shared), self.ws.data_ptr(), self.ws_bytes,
+                                       None if tr is None else C.byref(tr), path, _stream(stream)))
+        return (y, out) if trace else y
+
+    __call__ = forward
+
+
+# ------------------------------------------------------------------------------------------------ stages
+
+def router_topk(logits, k: int, stream=None):
+    import torch
+    T, E = logits.shape
+    ids = torch.empty((T, k), dtype=torch.int32, device=logits.device)
+    w = torch.empty((T, k), dtype=torch.float32, device=logits.device)
+    _check(lib().smoe_router_topk(logits.data_ptr(), T, E, k, ids.data_ptr(), w.data_ptr(), _stream(stream)))
+    return ids, w
+
+
+def f32_to_bf16(x, stream=None):
+    import torch
+    y = torch.empty(x.shape, dtype=torch.int16, device=x.device)
+    _check(lib().smoe_f32_to_bf16(x.data_ptr(), x.numel(), y.data_ptr(), _stream(stream)))
+    return y
+
+
+def bf16_gemv(x_bf16, w_bf16, n_in: int, n_out: int, stream=None):
+    import torch
+    n_tok = x_bf16.numel() // n_in
+    y = torch.empty((n_tok, n_out), dtype=torch.float32, device=x_bf16.device)
+    _check(lib().smoe_bf16_gemv(x_bf16.data_ptr(), w_bf16.data_ptr(), y.data_ptr(), n_in, n_out, n_tok,
+                                _stream(stream)))
+    return y
+
+
+def quantize_q8_1(x, stream=None):
+    import torch
+    y = torch.empty(x.numel() // 32 * 36, dtype=torch.uint8, device=x.device)
+    _check(lib().smoe_quantize_q8_1(x.data_ptr(), x.numel(), y.data_ptr(), _stream(stream)))
+    return y
+
+
+def mmvq(wtype: int, w, x_q8, n_in: int, n_out: int, n_col: int = 1, byte_off: int = 0, stream=None):
+    import torch
+    y = torch.empty((n_col, n_out), dtype=torch.float32, device=w.device)
+    _check(lib().smoe_mmvq(wtype, w.data_ptr(), byte_off, x_q8.data_ptr(), n_in, n_out, n_col, y.data_ptr(),
+                           _stream(stream)))
+    return y
+
+
+def swiglu_q8(gate, up, stream=None):
+    import torch
+    y = torch.empty(gate.numel() // 32 * 36, dtype=torch.uint8, device=gate.device)
+    _check(lib().smoe_swiglu_q8(gate.data_ptr(), up.data_ptr(), gate.numel(), y.data_ptr(), _stream(stream)))
+    return y
+
+
+def combine(parts, weights, shared=None, stream=None):
+    import torch
+    k, n = parts.shape
+    y = torch.empty(n, dtype=torch.float32, device=parts.device)
+    _check(lib().smoe_combine(parts.data_ptr(), weights.data_ptr(), _ptr(shared), y.data_ptr(), n, k,
+                              _stream(stream)))
+    return y
+
+
+def dispatch(ids, n_expert: int, stream=None):
+    import torch
+    T, k = ids.shape
+    dev = ids.device
+    counts = torch.empty(n_expert, dtype=torch.int32, device=dev)
+    offsets = torch.empty(n_expert + 1, dtype=torch.int32, device=dev)
+    perm = torch.empty(T * k, dtype=torch.int32, device=dev)
+    slot = torch.empty(T * k, dtype=torch.int32, device=dev)
+    _check(lib().smoe_dispatch(ids.data_ptr(), T, k, n_expert, counts.data_ptr(), offsets.data_ptr(),
+                               perm.data_ptr(), slot.data_ptr(), _stream(stream)))
+    return counts, offsets, perm, slot

@@ -1,0 +1,344 @@
+// stratametal_amd/csrc/smoe_api.cpp - the C ABI (include/smoe.h): argument checks, workspace layout and
+// the launch sequence.  Every refusal happens before the first launch, so a refused call leaves all
+// outputs untouched; a zero count returns before launching (metal/src/router.mm:33-37,
+// metal/src/iq.mm:150-158, metal/src/moe_combine.mm:32-34).
+#include "smoe.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "smoe_launch.hpp"
+
+namespace {
+
+thread_local std::string g_last;
+
+smoe_status fail(smoe_status s, const std::string& why) {
+    g_last = why;
+    return s;
+}
+smoe_status ok() {
+    g_last.clear();
+    return SMOE_OK;
+}
+
+constexpr size_t kAlign = 256;
+size_t up(size_t v) { return (v + kAlign - 1) & ~(kAlign - 1); }
+
+bool aligned(const void* p, size_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
+
+int row_values(int type) { return type == SMOE_Q2_0 ? 128 : type == SMOE_IQ2_S ? 256 : 0; }
+
+// GEMV-path tiling limits: a row of n_embd is at most 32 double blocks (4096 values).
+constexpr int kMaxEmbd = 4096;
+constexpr int kMaxFF = 4096;
+constexpr int kMaxExpert = 1024;
+constexpr int kMaxK = 64;
+
+smoe_status check_geom(const smoe_geom* g) {
+    if (!g) return fail(SMOE_ENULL, "geometry is NULL");
+    if (g->w_type != SMOE_Q2_0 && g->w_type != SMOE_IQ2_S)
+        return fail(SMOE_ETYPE, "routed expert type " + std::to_string(g->w_type) + " is not Q2_0 (42) or IQ2_S (22)");
+    if (g->sh_type != -1 && g->sh_type != SMOE_Q2_0 && g->sh_type != SMOE_IQ2_S)
+        return fail(SMOE_ETYPE, "shared expert type " + std::to_string(g->sh_type) + " is not Q2_0, IQ2_S or -1");
+    if (g->w_type == SMOE_IQ2_S || g->sh_type == SMOE_IQ2_S)
+        return fail(SMOE_ETYPE, "IQ2_S experts are not built in this library version");
+    if (g->router_dtype != 0) return fail(SMOE_EINVAL, "router_dtype must be 0 (bf16)");
+    if (g->n_expert < 1 || g->n_expert > kMaxExpert) return fail(SMOE_EINVAL, "n_expert must be in 1..1024");
+    if (g->top_k < 1 || g->top_k > kMaxK) return fail(SMOE_EINVAL, "top_k must be in 1..64");
+    if (g->top_k > g->n_expert) return fail(SMOE_EINVAL, "top_k exceeds n_expert");
+    const int rv = row_values(g->w_type);
+    if (g->n_embd <= 0 || g->n_embd % rv || g->n_embd > kMaxEmbd)
+        return fail(SMOE_EINVAL, "n_embd must be a positive multiple of " + std::to_string(rv) + ", at most 4096");
+    if (g->n_ff <= 0 || g->n_ff % rv || g->n_ff > kMaxFF)
+        return fail(SMOE_EINVAL, "n_ff must be a positive multiple of " + std::to_string(rv) + ", at most 4096");
+    if (g->sh_type >= 0) {
+        const int rs = row_values(g->sh_type);
+        if (g->n_embd % rs) return fail(SMOE_EINVAL, "n_embd is not a multiple of the shared type's row unit");
+        if (g->n_ff_shared <= 0 || g->n_ff_shared % rs || g->n_ff_shared > kMaxFF)
+            return fail(SMOE_EINVAL, "n_ff_shared must be a positive multiple of " + std::to_string(rs) + ", at most 4096");
+    }
+    return SMOE_OK;
+}
+
+struct Layout {
+    size_t xq, xb, logits, sg, ids, wts, counts, offsets, perm, slot, elist, nlist, hq, Y, total;
+    int hq_blocks;
+};
+
+Layout layout(const smoe_geom& g, int64_t T) {
+    Layout L{};
+    const int64_t H = g.n_embd, E = g.n_expert, K = g.top_k;
+    const int64_t P = T * K;
+    const int64_t Fmax = (g.sh_type >= 0 && g.n_ff_shared > g.n_ff) ? g.n_ff_shared : g.n_ff;
+    L.hq_blocks = (int)(Fmax / 32);
+    size_t o = 0;
+    auto take = [&](size_t bytes) {
+        const size_t at = o;
+        o = up(o + bytes);
+        return at;
+    };
+    L.xq = take((size_t)T * (H / 32) * 36);
+    L.xb = take((size_t)T * H * 2);
+    L.logits = take((size_t)T * E * 4);
+    L.sg = take((size_t)T * 4);
+    L.ids = take((size_t)P * 4);
+    L.wts = take((size_t)P * 4);
+    L.counts = take((size_t)E * 4);
+    L.offsets = take((size_t)(E + 1) * 4);
+    L.perm = take((size_t)P * 4);
+    L.slot = take((size_t)P * 4);
+    L.elist = take((size_t)(E + 1) * 4);
+    L.nlist = take(16);
+    L.hq = take((size_t)(P + T) * L.hq_blocks * 36);
+    L.Y = take((size_t)(P + T) * H * 4);
+    L.total = o;
+    return L;
+}
+
+hipStream_t stream_of(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+smoe_status launched(hipError_t e, const char* what) {
+    if (e != hipSuccess) return fail(SMOE_EDEVICE, std::string(what) + ": " + hipGetErrorString(e));
+    return SMOE_OK;
+}
+
+#define SMOE_TRY(call, what)                              \
+    do {                                                  \
+        const smoe_status _s = launched((call), (what));  \
+        if (_s != SMOE_OK) return _s;                     \
+    } while (0)
+
+}  // namespace
+
+extern "C" {
+
+const char* smoe_status_str(smoe_status s) {
+    switch (s) {
+        case SMOE_OK: return "ok";
+        case SMOE_EINVAL: return "invalid argument";
+        case SMOE_ESIZE: return "buffer too small";
+        case SMOE_ETYPE: return "unsupported ggml type";
+        case SMOE_EDEVICE: return "HIP runtime error";
+        case SMOE_EALIGN: return "misaligned pointer";
+        case SMOE_ENULL: return "NULL pointer";
+    }
+    return "unknown status";
+}
+
+const char* smoe_last_error(void) { return g_last.c_str(); }
+
+int32_t smoe_abi_version(void) { return 100; }
+
+size_t smoe_workspace_bytes(const smoe_geom* g, int32_t max_tokens) {
+    if (check_geom(g) != SMOE_OK || max_tokens < 0) return 0;
+    return layout(*g, max_tokens).total;
+}
+
+smoe_status smoe_forward_path(const smoe_geom* g, const smoe_weights* w, const float* x, int32_t n_tokens, float* y,
+                              int32_t add_shared, void* workspace, size_t workspace_bytes, const smoe_trace* trace,
+                              int32_t path, void* hip_stream) {
+    smoe_status s = check_geom(g);
+    if (s != SMOE_OK) return s;
+    if (!w) return fail(SMOE_ENULL, "weights is NULL");
+    if (n_tokens < 0) return fail(SMOE_EINVAL, "n_tokens is negative");
+    if (path < SMOE_PATH_AUTO || path > SMOE_PATH_MFMA) return fail(SMOE_EINVAL, "unknown path");
+    if ((int64_t)n_tokens * g->top_k > (1 << 24)) return fail(SMOE_EINVAL, "n_tokens * top_k exceeds 2^24");
+    if (!x || !y) return fail(SMOE_ENULL, "x or y is NULL");
+    if (!w->gate_exps || !w->up_exps || !w->down_exps || !w->router)
+        return fail(SMOE_ENULL, "a routed expert tensor or the router is NULL");
+    const bool has_sh = g->sh_type >= 0;
+    if (has_sh && (!w->gate_sh || !w->up_sh || !w->down_sh || !w->gate_inp_sh))
+        return fail(SMOE_ENULL, "a shared expert tensor is NULL (set sh_type = -1 for a layer without one)");
+    if (!aligned(x, 4) || !aligned(y, 4)) return fail(SMOE_EALIGN, "x and y must be 4-byte aligned");
+    if (!aligned(w->gate_exps, 4) || !aligned(w->up_exps, 4) || !aligned(w->down_exps, 4))
+        return fail(SMOE_EALIGN, "expert tensors must be 4-byte aligned");
+    if (!aligned(w->router, 16)) return fail(SMOE_EALIGN, "the router must be 16-byte aligned");
+    if (has_sh && (!aligned(w->gate_sh, 4) || !aligned(w->up_sh, 4) || !aligned(w->down_sh, 4) ||
+                   !aligned(w->gate_inp_sh, 16)))
+        return fail(SMOE_EALIGN, "shared tensors must be 4-byte aligned (gate_inp_shexp 16-byte)");
+    if (w->logit_bias && !aligned(w->logit_bias, 4)) return fail(SMOE_EALIGN, "logit_bias must be 4-byte aligned");
+    if (n_tokens == 0) return ok();
+    if (path == SMOE_PATH_MFMA) return fail(SMOE_EINVAL, "the MFMA path is not built in this library version");
+
+    const Layout L = layout(*g, n_tokens);
+    if (!workspace) return fail(SMOE_ENULL, "workspace is NULL");
+    if (!aligned(workspace, kAlign)) return fail(SMOE_EALIGN, "workspace must be 256-byte aligned");
+    if (workspace_bytes < L.total)
+        return fail(SMOE_ESIZE, "workspace is " + std::to_string(workspace_bytes) + " bytes, needs " +
+                                    std::to_string(L.total));
+
+    uint8_t* ws = static_cast<uint8_t*>(workspace);
+    const int T = n_tokens, H = g->n_embd, E = g->n_expert, K = g->top_k, F = g->n_ff;
+    const int Fs = has_sh ? g->n_ff_shared : 0;
+    const int P = T * K;
+    uint8_t* xq = ws + L.xq;
+    uint16_t* xb = reinterpret_cast<uint16_t*>(ws + L.xb);
+    float* logits = (trace && trace->logits) ? trace->logits : reinterpret_cast<float*>(ws + L.logits);
+    float* sg = (trace && trace->sgate) ? trace->sgate : reinterpret_cast<float*>(ws + L.sg);
+    int32_t* ids = (trace && trace->ids) ? trace->ids : reinterpret_cast<int32_t*>(ws + L.ids);
+    float* wts = (trace && trace->weights) ? trace->weights : reinterpret_cast<float*>(ws + L.wts);
+    int32_t* counts = (trace && trace->counts) ? trace->counts : reinterpret_cast<int32_t*>(ws + L.counts);
+    int32_t* offsets = (trace && trace->offsets) ? trace->offsets : reinterpret_cast<int32_t*>(ws + L.offsets);
+    int32_t* perm = (trace && trace->perm) ? trace->perm : reinterpret_cast<int32_t*>(ws + L.perm);
+    int32_t* slot = (trace && trace->slot) ? trace->slot : reinterpret_cast<int32_t*>(ws + L.slot);
+    int32_t* elist = reinterpret_cast<int32_t*>(ws + L.elist);
+    int32_t* nlist = reinterpret_cast<int32_t*>(ws + L.nlist);
+    uint8_t* hq = ws + L.hq;
+    float* Y = reinterpret_cast<float*>(ws + L.Y);
+    const hipStream_t st = stream_of(hip_stream);
+    const int max_items = (P < E ? P : E) + (has_sh ? 1 : 0);
+
+    SMOE_TRY(smoe::launch_prep(x, (int64_t)T * H, xq, xb, st), "prep");
+    SMOE_TRY(smoe::launch_router(xb, static_cast<const uint16_t*>(w->router), has_sh ? w->gate_inp_sh : nullptr,
+                                 w->logit_bias, H, E, E + (has_sh ? 1 : 0), T, logits, E, sg, st),
+             "router");
+    SMOE_TRY(smoe::launch_topk(logits, E, T, E, K, ids, wts, st), "topk");
+    SMOE_TRY(smoe::launch_dispatch(ids, P, E, counts, offsets, perm, slot, elist, nlist, st), "dispatch");
+    SMOE_TRY(smoe::launch_q2_gu(static_cast<const uint8_t*>(w->gate_exps), static_cast<const uint8_t*>(w->up_exps),
+                                static_cast<const uint8_t*>(w->gate_sh), static_cast<const uint8_t*>(w->up_sh), xq,
+                                offsets, perm, elist, nlist, K, T, H, F, Fs, has_sh ? 1 : 0, P, max_items, hq,
+                                L.hq_blocks, st),
+             "gate/up");
+    SMOE_TRY(smoe::launch_q2_down(static_cast<const uint8_t*>(w->down_exps), static_cast<const uint8_t*>(w->down_sh),
+                                  hq, L.hq_blocks, sg, offsets, elist, nlist, T, H, F, Fs, has_sh ? 1 : 0, P, max_items,
+                                  Y, st),
+             "down");
+    SMOE_TRY(smoe::launch_combine(Y, slot, wts, K, H, P, T, (has_sh && add_shared) ? 1 : 0, y, st), "combine");
+    return ok();
+}
+
+smoe_status smoe_forward(const smoe_geom* g, const smoe_weights* w, const float* x, int32_t n_tokens, float* y,
+                         int32_t add_shared, void* workspace, size_t workspace_bytes, const smoe_trace* trace,
+                         void* hip_stream) {
+    return smoe_forward_path(g, w, x, n_tokens, y, add_shared, workspace, workspace_bytes, trace, SMOE_PATH_AUTO,
+                             hip_stream);
+}
+
+// ------------------------------------------------------------------------------------------------ stages
+
+smoe_status smoe_router_topk(const float* logits, int32_t n_tokens, int32_t n_expert, int32_t k, int32_t* ids,
+                             float* weights, void* hip_stream) {
+    if (n_tokens < 0 || n_expert < 0 || k < 0) return fail(SMOE_EINVAL, "router_topk: negative size");
+    if (n_tokens == 0 || n_expert == 0 || k == 0) return ok();
+    if (k > kMaxK) return fail(SMOE_EINVAL, "router_topk: k exceeds 64");
+    if (n_expert > kMaxExpert) return fail(SMOE_EINVAL, "router_topk: n_expert exceeds 1024");
+    if (k > n_expert) return fail(SMOE_EINVAL, "router_topk: k exceeds n_expert");
+    if (!logits || !ids || !weights) return fail(SMOE_ENULL, "router_topk: NULL buffer");
+    SMOE_TRY(smoe::launch_topk(logits, n_expert, n_tokens, n_expert, k, ids, weights, stream_of(hip_stream)), "topk");
+    return ok();
+}
+
+smoe_status smoe_f32_to_bf16(const float* x, int64_t n, uint16_t* y, void* hip_stream) {
+    if (n < 0) return fail(SMOE_EINVAL, "f32_to_bf16: negative length");
+    if (n == 0) return ok();
+    if (!x || !y) return fail(SMOE_ENULL, "f32_to_bf16: NULL buffer");
+    if (n % 32) {
+        return fail(SMOE_EINVAL, "f32_to_bf16: length must be a multiple of 32");
+    }
+    SMOE_TRY(smoe::launch_prep(x, n, nullptr, y, stream_of(hip_stream)), "f32_to_bf16");
+    return ok();
+}
+
+smoe_status smoe_bf16_gemv(const uint16_t* x, const uint16_t* w, float* y, int32_t n_in, int32_t n_out, int32_t n_tok,
+                           void* hip_stream) {
+    if (n_in < 0 || n_out < 0 || n_tok < 0) return fail(SMOE_EINVAL, "bf16_gemv: negative size");
+    if (n_in == 0 || n_out == 0 || n_tok == 0) return ok();
+    if (!x || !w || !y) return fail(SMOE_ENULL, "bf16_gemv: NULL buffer");
+    if (n_in % 8 || n_in > 8192) return fail(SMOE_EINVAL, "bf16_gemv: n_in must be a multiple of 8, at most 8192");
+    if (!aligned(x, 16) || !aligned(w, 16)) return fail(SMOE_EALIGN, "bf16_gemv: x and w must be 16-byte aligned");
+    SMOE_TRY(smoe::launch_router(x, w, nullptr, nullptr, n_in, n_out, n_out, n_tok, y, n_out, nullptr,
+                                 stream_of(hip_stream)),
+             "bf16_gemv");
+    return ok();
+}
+
+smoe_status smoe_quantize_q8_1(const float* x, int64_t n, uint8_t* y, void* hip_stream) {
+    if (n < 0) return fail(SMOE_EINVAL, "quantize_q8_1: negative length");
+    if (n == 0) return ok();
+    if (n % 32) return fail(SMOE_EINVAL, "quantize_q8_1: length must be a multiple of 32");
+    if (!x || !y) return fail(SMOE_ENULL, "quantize_q8_1: NULL buffer");
+    if (!aligned(y, 4)) return fail(SMOE_EALIGN, "quantize_q8_1: y must be 4-byte aligned");
+    SMOE_TRY(smoe::launch_prep(x, n, y, nullptr, stream_of(hip_stream)), "quantize_q8_1");
+    return ok();
+}
+
+smoe_status smoe_mmvq(int32_t type, const void* w, int64_t byte_off, const uint8_t* x_q8, int32_t n_in, int32_t n_out,
+                      int32_t n_col, float* y, void* hip_stream) {
+    if (n_in < 0 || n_out < 0 || n_col < 0 || byte_off < 0) return fail(SMOE_EINVAL, "mmvq: negative size");
+    if (n_in == 0 || n_out == 0 || n_col == 0) return ok();
+    if (type != SMOE_Q2_0) return fail(SMOE_ETYPE, "mmvq: type " + std::to_string(type) + " is not built");
+    if (n_in % 128 || n_in > kMaxFF) return fail(SMOE_EINVAL, "mmvq: n_in must be a multiple of 128, at most 4096");
+    if (!w || !x_q8 || !y) return fail(SMOE_ENULL, "mmvq: NULL buffer");
+    const uint8_t* base = static_cast<const uint8_t*>(w) + byte_off;
+    if (!aligned(base, 4) || !aligned(x_q8, 4)) return fail(SMOE_EALIGN, "mmvq: w + byte_off and x must be 4-byte aligned");
+    SMOE_TRY(smoe::launch_q2_mmvq(base, x_q8, n_in, n_out, n_col, y, stream_of(hip_stream)), "mmvq");
+    return ok();
+}
+
+smoe_status smoe_swiglu_q8(const float* gate, const float* up, int64_t n, uint8_t* y, void* hip_stream) {
+    if (n < 0) return fail(SMOE_EINVAL, "swiglu_q8: negative length");
+    if (n == 0) return ok();
+    if (n % 32) return fail(SMOE_EINVAL, "swiglu_q8: length must be a multiple of 32");
+    if (!gate || !up || !y) return fail(SMOE_ENULL, "swiglu_q8: NULL buffer");
+    if (!aligned(y, 4)) return fail(SMOE_EALIGN, "swiglu_q8: y must be 4-byte aligned");
+    SMOE_TRY(smoe::launch_swiglu_q8(gate, up, n, y, stream_of(hip_stream)), "swiglu_q8");
+    return ok();
+}
+
+smoe_status smoe_combine(const float* parts, const float* weights, const float* shared, float* y, int32_t n_embd,
+                         int32_t k, void* hip_stream) {
+    if (n_embd < 0 || k < 0) return fail(SMOE_EINVAL, "combine: negative size");
+    if (n_embd == 0 || k == 0) return ok();
+    if (k > kMaxK) return fail(SMOE_EINVAL, "combine: k exceeds 64");
+    if (!parts || !weights || !y) return fail(SMOE_ENULL, "combine: NULL buffer");
+    SMOE_TRY(smoe::launch_combine_parts(parts, weights, shared, k, n_embd, y, stream_of(hip_stream)), "combine");
+    return ok();
+}
+
+smoe_status smoe_dispatch(const int32_t* ids, int32_t n_tokens, int32_t k, int32_t n_expert, int32_t* counts,
+                          int32_t* offsets, int32_t* perm, int32_t* slot, void* hip_stream) {
+    if (n_tokens < 0 || k < 0 || n_expert < 0) return fail(SMOE_EINVAL, "dispatch: negative size");
+    if (n_tokens == 0 || k == 0 || n_expert == 0) return ok();
+    if (n_expert > kMaxExpert) return fail(SMOE_EINVAL, "dispatch: n_expert exceeds 1024");
+    if ((int64_t)n_tokens * k > (1 << 24)) return fail(SMOE_EINVAL, "dispatch: more than 2^24 pairs");
+    if (!ids || !offsets || !perm || !slot) return fail(SMOE_ENULL, "dispatch: NULL buffer");
+    SMOE_TRY(smoe::launch_dispatch(ids, n_tokens * k, n_expert, counts, offsets, perm, slot, nullptr, nullptr,
+                                   stream_of(hip_stream)),
+             "dispatch");
+    return ok();
+}
+
+smoe_status smoe_synth_blocks(int32_t type, uint64_t seed, uint64_t stream_id, int64_t n_values, float sigma, void* out,
+                              void* hip_stream) {
+    if (type != SMOE_Q2_0 && type != SMOE_IQ2_S) return fail(SMOE_ETYPE, "synth_blocks: type is not Q2_0 or IQ2_S");
+    const int64_t per = type == SMOE_Q2_0 ? 64 : 256;
+    if (n_values < 0 || n_values % per) return fail(SMOE_EINVAL, "synth_blocks: n_values must be whole blocks");
+    if (n_values == 0) return ok();
+    if (!out) return fail(SMOE_ENULL, "synth_blocks: NULL buffer");
+    SMOE_TRY(smoe::launch_synth_blocks(type, seed, stream_id, n_values / per, sigma, static_cast<uint8_t*>(out),
+                                       stream_of(hip_stream)),
+             "synth_blocks");
+    return ok();
+}
+
+smoe_status smoe_synth_bf16(uint64_t seed, uint64_t stream_id, int64_t n, float sigma, uint16_t* out, void* hip_stream) {
+    if (n < 0) return fail(SMOE_EINVAL, "synth_bf16: negative length");
+    if (n == 0) return ok();
+    if (!out) return fail(SMOE_ENULL, "synth_bf16: NULL buffer");
+    SMOE_TRY(smoe::launch_synth_bf16(seed, stream_id, n, sigma, out, stream_of(hip_stream)), "synth_bf16");
+    return ok();
+}
+
+smoe_status smoe_synth_normal(uint64_t seed, uint64_t stream_id, int64_t n, float sigma, float* out, void* hip_stream) {
+    if (n < 0) return fail(SMOE_EINVAL, "synth_normal: negative length");
+    if (n == 0) return ok();
+    if (!out) return fail(SMOE_ENULL, "synth_normal: NULL buffer");
+    SMOE_TRY(smoe::launch_synth_normal(seed, stream_id, n, sigma, out, stream_of(hip_stream)), "synth_normal");
+    return ok();
+}
+
+}  // extern "C"

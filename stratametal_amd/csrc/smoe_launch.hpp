@@ -1,0 +1,37 @@
+// stratametal_amd/csrc/smoe_launch.hpp - host launchers of the MoE kernels (internal to libsmoe.so).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace smoe {
+
+size_t gemv_lds_bytes(int n_in);
+
+hipError_t launch_prep(const float* x, int64_t n, uint8_t* xq, uint16_t* xb, hipStream_t s);
+hipError_t launch_router(const uint16_t* xb, const uint16_t* W, const uint16_t* w_inp, const float* bias, int H, int E,
+                         int rows_total, int T, float* logits, int ld_logits, float* sg, hipStream_t s);
+hipError_t launch_topk(const float* logits, int ld_logits, int T, int E, int k, int32_t* ids, float* wts, hipStream_t s);
+hipError_t launch_dispatch(const int32_t* ids, int P, int E, int32_t* counts, int32_t* offsets, int32_t* perm,
+                           int32_t* slot, int32_t* elist, int32_t* n_list, hipStream_t s);
+hipError_t launch_q2_gu(const uint8_t* gate_exps, const uint8_t* up_exps, const uint8_t* gate_sh, const uint8_t* up_sh,
+                        const uint8_t* xq, const int32_t* offsets, const int32_t* perm, const int32_t* elist,
+                        const int32_t* n_list, int k, int T, int H, int F, int Fs, int has_shared, int P, int max_items,
+                        uint8_t* hq, int hq_blocks, hipStream_t s);
+hipError_t launch_q2_down(const uint8_t* down_exps, const uint8_t* down_sh, const uint8_t* hq, int hq_blocks,
+                          const float* sg, const int32_t* offsets, const int32_t* elist, const int32_t* n_list, int T,
+                          int H, int F, int Fs, int has_shared, int P, int max_items, float* Y, hipStream_t s);
+hipError_t launch_combine(const float* Y, const int32_t* slot, const float* wts, int k, int H, int P, int T,
+                          int add_shared, float* y, hipStream_t s);
+hipError_t launch_combine_parts(const float* parts, const float* wts, const float* shared, int k, int n, float* y,
+                                hipStream_t s);
+hipError_t launch_swiglu_q8(const float* gate, const float* up, int64_t n, uint8_t* y, hipStream_t s);
+hipError_t launch_q2_mmvq(const uint8_t* w, const uint8_t* xq, int n_in, int n_out, int n_col, float* y, hipStream_t s);
+
+hipError_t launch_synth_blocks(int type, uint64_t seed, uint64_t stream_id, int64_t n_blocks, float sigma, uint8_t* out,
+                               hipStream_t s);
+hipError_t launch_synth_bf16(uint64_t seed, uint64_t stream_id, int64_t n, float sigma, uint16_t* out, hipStream_t s);
+hipError_t launch_synth_normal(uint64_t seed, uint64_t stream_id, int64_t n, float sigma, float* out, hipStream_t s);
+
+}  // namespace smoe

@@ -1,0 +1,128 @@
+"""CPU tests of the C ABI: libsmoe.so loads, exports every function include/smoe.h declares, and refuses bad
+arguments (or accepts zero counts) before any HIP call, so these run without a GPU.  The pointers passed are
+never dereferenced: every case below returns during argument checking (metal/src/router_parity.cpp:195-225,
+metal/src/moe_combine_parity.cpp refusal cases)."""
+import ctypes as C
+import os
+import re
+import subprocess
+
+import pytest
+
+import stratametal_amd as S
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+FAKE = 0x10000000  # a 256-byte aligned address that is never dereferenced by a refused / empty call
+
+
+def declared_functions():
+    text = open(os.path.join(ROOT, "include", "smoe.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(smoe_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = S.lib()
+    names = declared_functions()
+    assert len(names) >= 15
+    for n in names:
+        assert hasattr(lib, n), n
+    out = subprocess.run(["nm", "-D", "--defined-only", S.LIB_PATH], capture_output=True, text=True).stdout
+    exported = set(re.findall(r" T (smoe_\w+)", out))
+    assert set(names) <= exported
+
+
+def test_abi_version_and_status_strings():
+    lib = S.lib()
+    assert lib.smoe_abi_version() == 100
+    for code in (0, -1, -2, -3, -4, -5, -6):
+        assert lib.smoe_status_str(code)
+
+
+def _ws(g):
+    return S.lib().smoe_workspace_bytes(C.byref(g.c()), 16)
+
+
+def test_workspace_size_and_geometry_refusals():
+    assert _ws(S.Geom()) > 0
+    bad = [S.Geom(top_k=65), S.Geom(n_expert=1025), S.Geom(top_k=20, n_expert=10), S.Geom(n_embd=2000),
+           S.Geom(n_ff=100), S.Geom(w_type=13), S.Geom(router_dtype=1), S.Geom(n_embd=8192)]
+    for g in bad:
+        assert _ws(g) == 0, g
+
+
+def _forward(g, T, ws_bytes=1 << 30, path=0, weights=None, add_shared=1):
+    L = S.lib()
+    w = weights if weights is not None else S._Weights(*([FAKE] * 8 + [None]))
+    return L.smoe_forward_path(C.byref(g.c()), C.byref(w), FAKE, T, FAKE, add_shared, FAKE, ws_bytes, None, path,
+                               None)
+
+
+def test_forward_refusals_before_launch():
+    g = S.Geom()
+    assert _forward(S.Geom(top_k=65), 1) == -1
+    assert _forward(S.Geom(n_expert=2048), 1) == -1
+    assert _forward(S.Geom(w_type=7), 1) == -3
+    assert _forward(g, -1) == -1
+    assert _forward(g, 1, path=9) == -1
+    assert _forward(g, 1, ws_bytes=1024) == -2
+    assert "needs" in S.lib().smoe_last_error().decode()
+    null_router = S._Weights(FAKE, FAKE, FAKE, None, FAKE, FAKE, FAKE, FAKE, None)
+    assert _forward(g, 1, weights=null_router) == -6
+    misaligned = S._Weights(FAKE + 2, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, None)
+    assert _forward(g, 1, weights=misaligned) == -5
+
+
+def test_forward_zero_tokens_returns_ok_without_launching():
+    assert _forward(S.Geom(), 0) == 0
+
+
+def test_stage_refusals_and_zero_counts():
+    L = S.lib()
+    # router: k = 65, 1025 experts, a negative count, k above n_expert (metal/src/router_parity.cpp:195-218)
+    assert L.smoe_router_topk(FAKE, 1, 128, 65, FAKE, FAKE, None) == -1
+    assert L.smoe_router_topk(FAKE, 1, 1025, 1, FAKE, FAKE, None) == -1
+    assert L.smoe_router_topk(FAKE, -1, 32, 4, FAKE, FAKE, None) == -1
+    assert L.smoe_router_topk(FAKE, 1, 4, 8, FAKE, FAKE, None) == -1
+    assert L.smoe_router_topk(FAKE, 0, 512, 10, FAKE, FAKE, None) == 0       # zero tokens: no launch
+    # combine: k = 65, negative, zero (metal/src/moe_combine_parity.cpp)
+    assert L.smoe_combine(FAKE, FAKE, None, FAKE, 16, 65, None) == -1
+    assert L.smoe_combine(FAKE, FAKE, None, FAKE, -1, 4, None) == -1
+    assert L.smoe_combine(FAKE, FAKE, None, FAKE, 0, 10, None) == 0
+    assert L.smoe_combine(FAKE, FAKE, None, FAKE, 256, 0, None) == 0
+    # q8_1 / swiglu: lengths that are not whole blocks
+    assert L.smoe_quantize_q8_1(FAKE, 33, FAKE, None) == -1
+    assert L.smoe_swiglu_q8(FAKE, FAKE, 40, FAKE, None) == -1
+    assert L.smoe_quantize_q8_1(FAKE, 0, FAKE, None) == 0
+    # mmvq: a type that is not built, a length that is not whole double blocks
+    assert L.smoe_mmvq(29, FAKE, 0, FAKE, 256, 4, 1, FAKE, None) == -3
+    assert L.smoe_mmvq(42, FAKE, 0, FAKE, 192, 4, 1, FAKE, None) == -1
+    assert L.smoe_mmvq(42, FAKE, 2, FAKE, 256, 4, 1, FAKE, None) == -5
+    assert L.smoe_mmvq(42, FAKE, 0, FAKE, 256, 0, 1, FAKE, None) == 0
+    # dispatch
+    assert L.smoe_dispatch(FAKE, 4, 10, 2000, FAKE, FAKE, FAKE, FAKE, None) == -1
+    assert L.smoe_dispatch(FAKE, 0, 10, 512, FAKE, FAKE, FAKE, FAKE, None) == 0
+    # synthetic generators
+    assert L.smoe_synth_blocks(42, 1, 1, 100, 0.02, FAKE, None) == -1
+    assert L.smoe_synth_blocks(5, 1, 1, 64, 0.02, FAKE, None) == -3
+
+
+def test_product_has_no_oracle_dependency():
+    """The product never imports, links or loads the test oracle (its CPU restatement)."""
+    pkg = os.path.join(ROOT, "stratametal_amd")
+    for dirpath, _, files in os.walk(pkg):
+        for f in files:
+            if f.endswith((".py", ".cpp", ".hip", ".hpp", ".h")):
+                text = open(os.path.join(dirpath, f)).read()
+                assert not re.search(r"^\s*(import|from)\s+oracle\b", text, re.M), f
+                assert not re.search(r'#include\s*[<"][^>"]*smoe_oracle', text), f
+                assert "liboracle" not in text, f
+    out = subprocess.run(["ldd", S.LIB_PATH], capture_output=True, text=True).stdout
+    assert "oracle" not in out
+
+
+def test_missing_library_fails_loudly(monkeypatch):
+    monkeypatch.setattr(S, "_LIB", None)
+    monkeypatch.setattr(S, "LIB_PATH", "/nonexistent/libsmoe.so")
+    with pytest.raises(ImportError):
+        S.lib()
