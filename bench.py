@@ -1,0 +1,265 @@
+#!/usr/bin/env python
+"""bench.py - MoE-layer throughput of the MI355X quantized MoE block (BASELINE.json's metric).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+A step is one MoE layer call (router, top-k, dispatch, expert products, shared expert, combine) on one batch
+of synthetic tokens.  The headline workload is BASELINE.json configs[1]: one Qwen3-Next-style layer (H 2048,
+512 Q2_0 experts + 1 shared, top-10, FF 512) at decode batch 16.  To keep the numbers honest against the
+256 MB Infinity Cache, `--layers` (default 48, ~21.7 GB) distinct layers are resident in HBM and consecutive
+steps walk through them, each layer with its own input batch, so a step's experts are not cache resident.
+The K timed steps are one captured HIP graph replay; per-stage kernel durations come from HIP events
+recorded between the kernels of the same replay.  Decode batch 1 (configs[0]'s shape) is measured the same
+way and reported under "extra".  The CPU baseline is the test oracle's C restatement of the reference's host
+path (kind "port"), timed on a bounded sample on this host's cores.
+Prints ONE JSON line.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "MoE-layer tok/s + achieved HBM GB/s vs peak, decode b=1 and prefill 512"
+HBM_PEAK_GBS = 8000.0
+
+
+def _args():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=96)
+    ap.add_argument("--warmup", type=int, default=48)
+    ap.add_argument("--layers", type=int, default=48)
+    ap.add_argument("--tokens", type=int, default=16)
+    ap.add_argument("--seed", type=int, default=20261201)
+    ap.add_argument("--no-extra", action="store_true", help="skip the decode b=1 measurement")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    return ap.parse_args()
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+class Stack:
+    """`n_layers` synthetic layers resident on the device, one workspace, a graph per token count."""
+
+    def __init__(self, S, torch, g, n_layers, seed, max_tokens):
+        self.S, self.torch, self.g = S, torch, g
+        self.layers = [S.synth_layer(g, seed + l) for l in range(n_layers)]
+        self.wc = [S._weights_c(w) for w in self.layers]
+        self.gc = g.c()
+        self.ws_bytes = S.workspace_bytes(g, max_tokens)
+        self.ws = torch.empty(self.ws_bytes, dtype=torch.uint8, device="cuda")
+        torch.cuda.synchronize()
+
+    def inputs(self, T, seed):
+        S, torch, g = self.S, self.torch, self.g
+        xs = S.synth_normal(seed, 100 + T, len(self.layers) * T * g.n_embd).view(len(self.layers), T, g.n_embd)
+        ys = torch.empty_like(xs)
+        return xs, ys
+
+    def call(self, l, x, y, T, trace=None):
+        import ctypes as C
+        S = self.S
+        st = S.lib().smoe_forward(C.byref(self.gc), C.byref(self.wc[l]), x.data_ptr(), T, y.data_ptr(), 1,
+                                  self.ws.data_ptr(), self.ws_bytes, None if trace is None else C.byref(trace),
+                                  S._stream())
+        S._check(st)
+
+
+class HipEvents:
+    """Raw hipEvent_t handles (timing enabled) from the HIP runtime, for the library's stage-event hook."""
+
+    def __init__(self):
+        import ctypes as C
+        self.C = C
+        self.hip = C.CDLL("libamdhip64.so")
+        self.hip.hipEventCreateWithFlags.argtypes = [C.POINTER(C.c_void_p), C.c_uint]
+        self.hip.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), C.c_void_p, C.c_void_p]
+        self.hip.hipEventDestroy.argtypes = [C.c_void_p]
+
+    def create(self, n):
+        out = []
+        for _ in range(n):
+            ev = self.C.c_void_p()
+            if self.hip.hipEventCreateWithFlags(self.C.byref(ev), 0) != 0:
+                raise RuntimeError("hipEventCreateWithFlags failed")
+            out.append(ev.value)
+        return out
+
+    def elapsed_ms(self, a, b):
+        ms = self.C.c_float()
+        if self.hip.hipEventElapsedTime(self.C.byref(ms), a, b) != 0:
+            raise RuntimeError("hipEventElapsedTime failed")
+        return ms.value
+
+
+def measure(S, torch, stack, T, steps, warmup, seed):
+    """Time `steps` layer calls (graph replay) at T tokens; return timings, stage durations and touched experts."""
+    g = stack.g
+    L = len(stack.layers)
+    xs, ys = stack.inputs(T, seed)
+    E = g.n_expert
+    counts = torch.zeros((steps, E), dtype=torch.int32, device="cuda")
+    he = HipEvents()
+    events = [he.create(S.STAGE_EVENTS) for _ in range(steps)]
+    evp = [(S.C.c_void_p * S.STAGE_EVENTS)(*evs) for evs in events]
+    traces = [S._Trace(None, None, None, counts[s].data_ptr(), None, None, None, None,
+                       S.C.cast(evp[s], S.C.c_void_p)) for s in range(steps)]
+    for s in range(warmup):  # eager warmup (also loads the code objects)
+        stack.call(s % L, xs[s % L], ys[s % L], T)
+    torch.cuda.synchronize()
+    # the timed graph: `steps` calls walking the resident layers
+    graph = torch.cuda.CUDAGraph()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            for s in range(steps):
+                tr = S._Trace(None, None, None, counts[s].data_ptr(), None, None, None, None, None)
+                stack.call(s % L, xs[s % L], ys[s % L], T, tr)
+    torch.cuda.synchronize()
+    graph.replay()  # one untimed replay: code and graph are resident; the timed replay below is the measurement
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    graph.replay()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    wall = t1 - t0
+    # per-kernel durations: the same steps launched on the same stream with HIP events between the kernels
+    for s in range(steps):
+        stack.call(s % L, xs[s % L], ys[s % L], T, traces[s])
+    torch.cuda.synchronize()
+    with_events = False
+    stage_ms = [[he.elapsed_ms(events[s][i], events[s][i + 1]) for i in range(S.STAGE_EVENTS - 1)]
+                for s in range(steps)]
+    step_ms = [he.elapsed_ms(events[s][0], events[s][-1]) for s in range(steps)]
+    D = (counts > 0).sum(dim=1).cpu().tolist()
+    return dict(wall=wall, stage_ms=stage_ms, step_ms=step_ms, touched=D, events_in_graph=with_events)
+
+
+def bytes_model(S, g, T, D):
+    """Algorithmic (compulsory) HBM bytes of one layer call touching D distinct experts, and of its gate/up kernel."""
+    rb_h = S.row_bytes(g.w_type, g.n_embd)
+    rb_f = S.row_bytes(g.w_type, g.n_ff)
+    sh = g.sh_type >= 0
+    Fs = g.n_ff_shared
+    xq = T * g.n_embd // 32 * 36
+    P = T * g.top_k
+    hq = (P + (T if sh else 0)) * (max(g.n_ff, Fs if sh else 0) // 32) * 36
+    gu = D * 2 * g.n_ff * rb_h + (2 * Fs * S.row_bytes(g.sh_type, g.n_embd) if sh else 0) + xq + hq
+    down = D * g.n_embd * rb_f + (g.n_embd * S.row_bytes(g.sh_type, Fs) if sh else 0) + hq + (P + T) * g.n_embd * 4
+    layer = (D * g.expert_bytes() + g.shared_bytes() + g.n_expert * g.n_embd * 2 + (g.n_embd * 2 if sh else 0)
+             + 2 * T * g.n_embd * 4)
+    return layer, gu, down
+
+
+def summarize(S, g, T, r, steps):
+    import statistics as st
+    per_stage = {name: st.fmean(r["stage_ms"][s][i] for s in range(steps)) for i, name in enumerate(S.STAGES)}
+    D = st.fmean(r["touched"])
+    layer_b, gu_b, down_b = bytes_model(S, g, T, D)
+    ms = r["wall"] * 1e3 / steps
+    return dict(tokens=T, ms_per_step=ms, tok_s=T * steps / r["wall"], touched_experts_avg=D,
+                layer_bytes_avg=layer_b, layer_gbs=layer_b / (ms * 1e-3) / 1e9,
+                stage_ms_avg=per_stage, gate_up_bytes=gu_b, down_bytes=down_b,
+                gate_up_gbs=gu_b / (per_stage["gate_up"] * 1e-3) / 1e9,
+                down_gbs=down_b / (per_stage["down"] * 1e-3) / 1e9,
+                events_in_graph=r["events_in_graph"],
+                step_event_ms_avg=st.fmean(r["step_ms"]))
+
+
+def cpu_baseline(g, T, seed, seconds):
+    """The oracle's C restatement of the reference host path (q8_1 activations, integer dots, double-free
+    device-order sums), on this host's cores, over a bounded sample of the same workload."""
+    import numpy as np
+    import oracle as O
+    threads = max(1, min(16, os.cpu_count() or 1))
+    og = O.Geom(**{k: getattr(g, k) for k in ("n_embd", "n_ff", "n_ff_shared", "n_expert", "top_k", "w_type",
+                                              "sh_type")})
+    w = O.make_weights(og, seed)
+    n = 0
+    t0 = time.perf_counter()
+    while True:
+        x = O.gen_normal(seed, 1000 + n, T * og.n_embd).reshape(T, og.n_embd)
+        O.moe_decode_dev(og, w, x, n_threads=threads)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or n >= 200:
+            break
+    try:
+        model = [l for l in open("/proc/cpuinfo") if l.startswith("model name")][0].split(":", 1)[1].strip()
+    except Exception:
+        model = "unknown"
+    return {"value": T * n / el, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"{n} layer calls of {T} tokens on one synthetic layer ({el:.1f} s), oracle/smoe_oracle.c "
+                      f"or_moe_decode_dev, {threads} OpenMP threads, {model}"}
+
+
+def main():
+    a = _args()
+    if a.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {a.gpus} is not supported (the path is "
+              f"single-GPU by design, see DESIGN.md for how it would shard)", file=sys.stderr)
+        sys.exit(2)
+    import ctypes
+    import torch
+    import stratametal_amd as S
+    S.C = ctypes
+    S.STAGE_EVENTS = 8
+    g = S.Geom()
+    t_setup = time.perf_counter()
+    stack = Stack(S, torch, g, a.layers, a.seed, max(a.tokens, 1))
+    log(f"{a.layers} layers resident ({a.layers * (g.n_expert * g.expert_bytes() + g.shared_bytes()) / 1e9:.1f} GB) "
+        f"in {time.perf_counter() - t_setup:.1f} s")
+    r16 = measure(S, torch, stack, a.tokens, a.steps, a.warmup, a.seed + 7)
+    m16 = summarize(S, g, a.tokens, r16, a.steps)
+    log("decode b=%d: %.3f ms/step, %.0f tok/s, layer %.0f GB/s, gate/up %.0f GB/s, stages %s" % (
+        a.tokens, m16["ms_per_step"], m16["tok_s"], m16["layer_gbs"], m16["gate_up_gbs"],
+        {k: round(v * 1e3, 1) for k, v in m16["stage_ms_avg"].items()}))
+    extra = {}
+    if not a.no_extra:
+        r1 = measure(S, torch, stack, 1, a.steps, a.warmup, a.seed + 11)
+        m1 = summarize(S, g, 1, r1, a.steps)
+        log("decode b=1: %.3f ms/step, %.0f tok/s, layer %.0f GB/s, stages(us) %s" % (
+            m1["ms_per_step"], m1["tok_s"], m1["layer_gbs"],
+            {k: round(v * 1e3, 1) for k, v in m1["stage_ms_avg"].items()}))
+        extra["decode_b1"] = {k: m1[k] for k in ("ms_per_step", "tok_s", "touched_experts_avg", "layer_bytes_avg",
+                                                 "layer_gbs", "stage_ms_avg", "gate_up_gbs", "down_gbs")}
+        extra["decode_b1"]["layer_hbm_frac"] = m1["layer_gbs"] / HBM_PEAK_GBS
+    extra["decode_b16_stages_ms"] = m16["stage_ms_avg"]
+    extra["decode_b16_layer_gbs"] = m16["layer_gbs"]
+    extra["decode_b16_layer_hbm_frac"] = m16["layer_gbs"] / HBM_PEAK_GBS
+    extra["touched_experts_avg"] = m16["touched_experts_avg"]
+    extra["events_in_graph"] = m16["events_in_graph"]
+    gu_ms = m16["stage_ms_avg"]["gate_up"]
+    roof = {"bound": "hbm", "kernel": "k_q2_gu (routed + shared gate/up, SwiGLU, q8_1 of h)",
+            "achieved": m16["gate_up_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": m16["gate_up_gbs"] / HBM_PEAK_GBS, "traffic": None,
+            "algorithmic_bytes_per_launch": m16["gate_up_bytes"], "avg_launch_ms": gu_ms}
+    cpu = None
+    if not a.no_cpu:
+        cpu = cpu_baseline(g, a.tokens, a.seed, a.cpu_seconds)
+        log(f"cpu baseline: {cpu['value']:.1f} tok/s on {cpu['cores']} threads")
+    out = {
+        "metric": METRIC, "value": m16["tok_s"], "unit": "tokens/s", "n_gpus": 1, "steps": a.steps,
+        "warmup": a.warmup, "ms_per_step": m16["ms_per_step"], "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int8 (q8_1 x Q2_0 integer dot, f32 scale and sums)", "data": "synthetic",
+        "config": {"workload": "BASELINE configs[1]: one Qwen3-Next-style MoE layer, decode batch 16",
+                   "tokens_per_step": a.tokens, "n_embd": g.n_embd, "n_ff": g.n_ff, "n_expert": g.n_expert,
+                   "top_k": g.top_k, "shared_experts": 1, "expert_type": "Q2_0", "router": "bf16",
+                   "resident_layers": a.layers, "parallelism": "none (1 GPU)"},
+        "roofline": roof, "cpu_baseline": cpu, "extra": extra,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

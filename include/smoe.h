@@ -81,7 +81,13 @@ typedef struct {
     int32_t* perm;    /* [T*k] pair index t*k+s at each dispatch position */
     int32_t* slot;    /* [T*k] dispatch position of pair t*k+s */
     float* sgate;     /* [T] shared expert gate dot (before the sigmoid) */
+    /* NULL, or SMOE_STAGE_EVENTS hipEvent_t recorded on hip_stream at the stage boundaries of smoe_forward
+     * (before the first kernel and after each stage: prep, router, top-k, dispatch, gate/up, down, combine),
+     * for per-stage timing (the upstream engine's event-pair stage timing, include/strata/core/layer.hpp:317-337). */
+    void* const* stage_events;
 } smoe_trace;
+
+#define SMOE_STAGE_EVENTS 8
 
 /* ---------------------------------------------------------------------------------------------- block */
 

@@ -44,7 +44,10 @@ class _Weights(C.Structure):
 
 
 class _Trace(C.Structure):
-    _fields_ = [(n, C.c_void_p) for n in ("logits", "ids", "weights", "counts", "offsets", "perm", "slot", "sgate")]
+    _fields_ = [(n, C.c_void_p) for n in ("logits", "ids", "weights", "counts", "offsets", "perm", "slot", "sgate",
+                                          "stage_events")]
+
+STAGES = ("prep", "router", "topk", "dispatch", "gate_up", "down", "combine")
 
 
 def lib():

@@ -147,13 +147,11 @@ smoe_status smoe_forward_path(const smoe_geom* g, const smoe_weights* w, const f
     if (n_tokens < 0) return fail(SMOE_EINVAL, "n_tokens is negative");
     if (path < SMOE_PATH_AUTO || path > SMOE_PATH_MFMA) return fail(SMOE_EINVAL, "unknown path");
     if ((int64_t)n_tokens * g->top_k > (1 << 24)) return fail(SMOE_EINVAL, "n_tokens * top_k exceeds 2^24");
-    if (!x || !y) return fail(SMOE_ENULL, "x or y is NULL");
     if (!w->gate_exps || !w->up_exps || !w->down_exps || !w->router)
         return fail(SMOE_ENULL, "a routed expert tensor or the router is NULL");
     const bool has_sh = g->sh_type >= 0;
     if (has_sh && (!w->gate_sh || !w->up_sh || !w->down_sh || !w->gate_inp_sh))
         return fail(SMOE_ENULL, "a shared expert tensor is NULL (set sh_type = -1 for a layer without one)");
-    if (!aligned(x, 4) || !aligned(y, 4)) return fail(SMOE_EALIGN, "x and y must be 4-byte aligned");
     if (!aligned(w->gate_exps, 4) || !aligned(w->up_exps, 4) || !aligned(w->down_exps, 4))
         return fail(SMOE_EALIGN, "expert tensors must be 4-byte aligned");
     if (!aligned(w->router, 16)) return fail(SMOE_EALIGN, "the router must be 16-byte aligned");
@@ -161,7 +159,9 @@ smoe_status smoe_forward_path(const smoe_geom* g, const smoe_weights* w, const f
                    !aligned(w->gate_inp_sh, 16)))
         return fail(SMOE_EALIGN, "shared tensors must be 4-byte aligned (gate_inp_shexp 16-byte)");
     if (w->logit_bias && !aligned(w->logit_bias, 4)) return fail(SMOE_EALIGN, "logit_bias must be 4-byte aligned");
-    if (n_tokens == 0) return ok();
+    if (n_tokens == 0) return ok();  // empty x / y may be NULL: nothing is read or written
+    if (!x || !y) return fail(SMOE_ENULL, "x or y is NULL");
+    if (!aligned(x, 4) || !aligned(y, 4)) return fail(SMOE_EALIGN, "x and y must be 4-byte aligned");
     if (path == SMOE_PATH_MFMA) return fail(SMOE_EINVAL, "the MFMA path is not built in this library version");
 
     const Layout L = layout(*g, n_tokens);
@@ -192,22 +192,43 @@ smoe_status smoe_forward_path(const smoe_geom* g, const smoe_weights* w, const f
     const hipStream_t st = stream_of(hip_stream);
     const int max_items = (P < E ? P : E) + (has_sh ? 1 : 0);
 
+    void* const* ev = trace ? trace->stage_events : nullptr;
+    int ev_i = 0;
+    auto mark = [&]() -> smoe_status {
+        if (!ev) return SMOE_OK;
+        const hipError_t e = hipEventRecord(reinterpret_cast<hipEvent_t>(ev[ev_i++]), st);
+        return launched(e, "stage event");
+    };
+#define SMOE_MARK()                          \
+    do {                                     \
+        const smoe_status _m = mark();       \
+        if (_m != SMOE_OK) return _m;        \
+    } while (0)
+    SMOE_MARK();
     SMOE_TRY(smoe::launch_prep(x, (int64_t)T * H, xq, xb, st), "prep");
+    SMOE_MARK();
     SMOE_TRY(smoe::launch_router(xb, static_cast<const uint16_t*>(w->router), has_sh ? w->gate_inp_sh : nullptr,
                                  w->logit_bias, H, E, E + (has_sh ? 1 : 0), T, logits, E, sg, st),
              "router");
+    SMOE_MARK();
     SMOE_TRY(smoe::launch_topk(logits, E, T, E, K, ids, wts, st), "topk");
+    SMOE_MARK();
     SMOE_TRY(smoe::launch_dispatch(ids, P, E, counts, offsets, perm, slot, elist, nlist, st), "dispatch");
+    SMOE_MARK();
     SMOE_TRY(smoe::launch_q2_gu(static_cast<const uint8_t*>(w->gate_exps), static_cast<const uint8_t*>(w->up_exps),
                                 static_cast<const uint8_t*>(w->gate_sh), static_cast<const uint8_t*>(w->up_sh), xq,
                                 offsets, perm, elist, nlist, K, T, H, F, Fs, has_sh ? 1 : 0, P, max_items, hq,
                                 L.hq_blocks, st),
              "gate/up");
+    SMOE_MARK();
     SMOE_TRY(smoe::launch_q2_down(static_cast<const uint8_t*>(w->down_exps), static_cast<const uint8_t*>(w->down_sh),
                                   hq, L.hq_blocks, sg, offsets, elist, nlist, T, H, F, Fs, has_sh ? 1 : 0, P, max_items,
                                   Y, st),
              "down");
+    SMOE_MARK();
     SMOE_TRY(smoe::launch_combine(Y, slot, wts, K, H, P, T, (has_sh && add_shared) ? 1 : 0, y, st), "combine");
+    SMOE_MARK();
+#undef SMOE_MARK
     return ok();
 }
 

@@ -119,8 +119,8 @@ def test_router_topk(torch, case):
     T, E = logits.shape
     ids_t = guarded(torch, T * k, torch.int32)
     w_t = guarded(torch, T * k, torch.float32)
-    S._check(S.lib().smoe_router_topk(dev(torch, logits).data_ptr(), T, E, k, ids_t.data_ptr(), w_t.data_ptr(),
-                                      S._stream()))
+    logits_t = dev(torch, logits)
+    S._check(S.lib().smoe_router_topk(logits_t.data_ptr(), T, E, k, ids_t.data_ptr(), w_t.data_ptr(), S._stream()))
     ids, w = host(torch, ids_t), host(torch, w_t)
     assert (ids[T * k:] == 7).all() and (w[T * k:] == 7.0).all()
     ids, w = ids[:T * k].reshape(T, k), w[:T * k].reshape(T, k)
@@ -181,8 +181,10 @@ def test_combine(torch, n, k, shared):
     w = (w / w.sum()).astype(np.float32)
     sh = 3.0 * O.gen_normal(31337, 3, n) if shared else None
     y = guarded(torch, n, torch.float32)
-    S._check(S.lib().smoe_combine(dev(torch, parts).data_ptr(), dev(torch, w).data_ptr(),
-                                  None if sh is None else dev(torch, sh).data_ptr(), y.data_ptr(), n, k, S._stream()))
+    parts_t, w_t = dev(torch, parts), dev(torch, w)      # held: a dropped temporary's block is reused at once
+    sh_t = None if sh is None else dev(torch, sh)
+    S._check(S.lib().smoe_combine(parts_t.data_ptr(), w_t.data_ptr(), None if sh_t is None else sh_t.data_ptr(),
+                                  y.data_ptr(), n, k, S._stream()))
     got = host(torch, y)
     assert (got[n:] == 7.0).all()
     assert np.array_equal(bits(got[:n]), bits(O.combine_dev(parts, w, sh)))
@@ -208,7 +210,7 @@ def test_dispatch_out_of_range_ids_are_not_dispatched(torch):
     ids = np.array([[0, 1], [5, 1], [9, 0]], np.int32)   # 9 >= E = 6
     counts, offsets, perm, slot = S.dispatch(dev(torch, ids), 6)
     c = host(torch, counts)
-    assert c.sum() == 5 and host(torch, slot)[5] == -1
+    assert c.sum() == 5 and host(torch, slot)[4] == -1   # pair 4 = (token 2, slot 0) has id 9
 
 
 # ------------------------------------------------------------------------------------------------ the whole block
@@ -291,7 +293,8 @@ def test_forward_zero_tokens_and_refusals_leave_output(torch):
     with pytest.raises(S.SmoeError):
         small.forward(torch.zeros((4, 256), device="cuda"), y=y)
     import ctypes as C
-    st = S.lib().smoe_forward(C.byref(g.c()), C.byref(S._weights_c(w)), torch.zeros(256 * 4, device="cuda").data_ptr(),
-                              4, y.data_ptr(), 1, small.ws.data_ptr(), small.ws_bytes, None, S._stream())
+    x4 = torch.zeros(256 * 4, device="cuda")
+    st = S.lib().smoe_forward(C.byref(g.c()), C.byref(S._weights_c(w)), x4.data_ptr(), 4, y.data_ptr(), 1,
+                              small.ws.data_ptr(), small.ws_bytes, None, S._stream())
     assert st == -2
     assert (host(torch, y) == 7.0).all()
