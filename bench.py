@@ -213,7 +213,6 @@ def main():
     import torch
     import stratametal_amd as S
     S.C = ctypes
-    S.STAGE_EVENTS = 8
     g = S.Geom()
     t_setup = time.perf_counter()
     stack = Stack(S, torch, g, a.layers, a.seed, max(a.tokens, 1))

@@ -47,8 +47,8 @@ enum {
 
 /* Layer geometry.  ModelGeometry's MoE fields (include/strata/core/layout.hpp:27-59) plus the types. */
 typedef struct {
-    int32_t n_embd;       /* H: multiple of 128 (Q2_0) / 256 (IQ2_S), at most 8192 */
-    int32_t n_ff;         /* routed expert width: multiple of 128 / 256, at most 4096 */
+    int32_t n_embd;       /* H: 128 * 2^a * b with b <= 8 (2048, 2560, 4096 ...), at most 4096 */
+    int32_t n_ff;         /* routed expert width: same form (512, 640 ...), at most 4096 */
     int32_t n_ff_shared;  /* shared expert width (ignored when sh_type < 0) */
     int32_t n_expert;     /* E: 1..1024 (metal/src/router.mm:33-37) */
     int32_t top_k;        /* k: 1..64, k <= E */
@@ -82,12 +82,13 @@ typedef struct {
     int32_t* slot;    /* [T*k] dispatch position of pair t*k+s */
     float* sgate;     /* [T] shared expert gate dot (before the sigmoid) */
     /* NULL, or SMOE_STAGE_EVENTS hipEvent_t recorded on hip_stream at the stage boundaries of smoe_forward
-     * (before the first kernel and after each stage: prep, router, top-k, dispatch, gate/up, down, combine),
+     * (before the first kernel and after each stage: router, route (q8_1 + top-k + dispatch), gate/up, down,
+     * combine),
      * for per-stage timing (the upstream engine's event-pair stage timing, include/strata/core/layer.hpp:317-337). */
     void* const* stage_events;
 } smoe_trace;
 
-#define SMOE_STAGE_EVENTS 8
+#define SMOE_STAGE_EVENTS 6
 
 /* ---------------------------------------------------------------------------------------------- block */
 

@@ -299,22 +299,39 @@ static inline float q2_partial(const uint8_t* blk, const uint8_t* xblk, int half
     return d * (float)sumi;
 }
 
-/* Device order (stratametal_amd/csrc/smoe_gemv.hip, q2_rows): one lane per "double block" of 36 bytes
- * (blocks 2g, 2g+1; half blocks 4g..4g+3).  Lane part L_g = ((P_4g + P_4g+1) + P_4g+2) + P_4g+3.
- * Row = ((L_0 + L_1) + L_2) + ... in g order.  Requires n_in % 128 == 0. */
+/* Device order (stratametal_amd/csrc/smoe_decode.hip, q2_unit_dot / row_butterfly): a row of n_in values
+ * is dpr = n_in / 128 "units" of 36 bytes (blocks 2g, 2g+1; half blocks 4g..4g+3), unit part
+ * L_g = ((P_4g + P_4g+1) + P_4g+2) + P_4g+3.  LPR = the largest power of two dividing dpr, at most 16, lanes
+ * share a row; lane l adds its units g = l, l + LPR, l + 2 LPR, ... in that order (the first assigned, not
+ * added to 0); then an xor butterfly over the LPR lanes (distance LPR/2 first).  Requires n_in % 128 == 0. */
+static int lanes_per_row(int dpr) {
+    int l = dpr & -dpr;
+    return l > 16 ? 16 : l;
+}
+
 static float q2_row_dev(const uint8_t* row, const uint8_t* xq, int n_in) {
     const int dpr = n_in / 128;
-    float acc = 0.0f;
-    for (int g = 0; g < dpr; ++g) {
-        float L = 0.0f;
-        for (int h = 0; h < 4; ++h) {
-            const int hb = 4 * g + h;
-            const float P = q2_partial(row + (size_t)(hb >> 1) * 18, xq + (size_t)hb * 36, hb & 1, 1);
-            L = h == 0 ? P : L + P;
+    const int lpr = lanes_per_row(dpr);
+    float lane[16];
+    for (int l = 0; l < lpr; ++l) {
+        float A = 0.0f;
+        for (int g = l, m = 0; g < dpr; g += lpr, ++m) {
+            float L = 0.0f;
+            for (int h = 0; h < 4; ++h) {
+                const int hb = 4 * g + h;
+                const float P = q2_partial(row + (size_t)(hb >> 1) * 18, xq + (size_t)hb * 36, hb & 1, 1);
+                L = h == 0 ? P : L + P;
+            }
+            A = m == 0 ? L : A + L;
         }
-        acc = g == 0 ? L : acc + L;
+        lane[l] = A;
     }
-    return acc;
+    for (int o = lpr / 2; o > 0; o >>= 1) {
+        float nxt[16];
+        for (int l = 0; l < lpr; ++l) nxt[l] = lane[l] + lane[l ^ o];
+        memcpy(lane, nxt, sizeof(float) * (size_t)lpr);
+    }
+    return lane[0];
 }
 
 void or_q2_0_gemv_dev(const uint8_t* w, const uint8_t* xq, int n_in, int n_out, float* y) {

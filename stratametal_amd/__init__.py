@@ -47,7 +47,8 @@ class _Trace(C.Structure):
     _fields_ = [(n, C.c_void_p) for n in ("logits", "ids", "weights", "counts", "offsets", "perm", "slot", "sgate",
                                           "stage_events")]
 
-STAGES = ("prep", "router", "topk", "dispatch", "gate_up", "down", "combine")
+STAGES = ("router", "route", "gate_up", "down", "combine")
+STAGE_EVENTS = len(STAGES) + 1
 
 
 def lib():

@@ -37,6 +37,8 @@ constexpr int kMaxEmbd = 4096;
 constexpr int kMaxFF = 4096;
 constexpr int kMaxExpert = 1024;
 constexpr int kMaxK = 64;
+// Up to this many tokens the q8_1 images, top-k and dispatch run as one work-group (k_route).
+constexpr int kFusedRouteTokens = 64;
 
 smoe_status check_geom(const smoe_geom* g) {
     if (!g) return fail(SMOE_ENULL, "geometry is NULL");
@@ -55,34 +57,43 @@ smoe_status check_geom(const smoe_geom* g) {
         return fail(SMOE_EINVAL, "n_embd must be a positive multiple of " + std::to_string(rv) + ", at most 4096");
     if (g->n_ff <= 0 || g->n_ff % rv || g->n_ff > kMaxFF)
         return fail(SMOE_EINVAL, "n_ff must be a positive multiple of " + std::to_string(rv) + ", at most 4096");
+    if (!smoe::gemv_shape_ok(g->n_embd) || !smoe::gemv_shape_ok(g->n_ff))
+        return fail(SMOE_EINVAL, "n_embd / 128 and n_ff / 128 must each be a power of two times at most 8");
     if (g->sh_type >= 0) {
         const int rs = row_values(g->sh_type);
         if (g->n_embd % rs) return fail(SMOE_EINVAL, "n_embd is not a multiple of the shared type's row unit");
         if (g->n_ff_shared <= 0 || g->n_ff_shared % rs || g->n_ff_shared > kMaxFF)
             return fail(SMOE_EINVAL, "n_ff_shared must be a positive multiple of " + std::to_string(rs) + ", at most 4096");
+        if (!smoe::down_shapes_match(g->n_ff, g->n_ff_shared))
+            return fail(SMOE_EINVAL, "n_ff_shared must split into down-row units like n_ff (same power-of-two factor)");
     }
     return SMOE_OK;
 }
 
 struct Layout {
-    size_t xq, xb, logits, sg, ids, wts, counts, offsets, perm, slot, elist, nlist, hq, Y, total;
-    int hq_blocks;
+    size_t ximg, logits, sg, ids, wts, counts, offsets, perm, slot, elist, nlist, items, himg, Y, total;
+    int h_blocks;
 };
+
+// GEMV work items: every touched expert plus the shared expert's token chunks.
+int max_items(const smoe_geom& g, int64_t T) {
+    const int64_t P = T * g.top_k;
+    return (int)((P < g.n_expert ? P : g.n_expert) + (g.sh_type >= 0 ? smoe::shared_items((int)T) : 0));
+}
 
 Layout layout(const smoe_geom& g, int64_t T) {
     Layout L{};
     const int64_t H = g.n_embd, E = g.n_expert, K = g.top_k;
     const int64_t P = T * K;
     const int64_t Fmax = (g.sh_type >= 0 && g.n_ff_shared > g.n_ff) ? g.n_ff_shared : g.n_ff;
-    L.hq_blocks = (int)(Fmax / 32);
+    L.h_blocks = (int)(Fmax / 32);
     size_t o = 0;
     auto take = [&](size_t bytes) {
         const size_t at = o;
         o = up(o + bytes);
         return at;
     };
-    L.xq = take((size_t)T * (H / 32) * 36);
-    L.xb = take((size_t)T * H * 2);
+    L.ximg = take(smoe::img_bytes(T * (H / 32)));
     L.logits = take((size_t)T * E * 4);
     L.sg = take((size_t)T * 4);
     L.ids = take((size_t)P * 4);
@@ -93,7 +104,8 @@ Layout layout(const smoe_geom& g, int64_t T) {
     L.slot = take((size_t)P * 4);
     L.elist = take((size_t)(E + 1) * 4);
     L.nlist = take(16);
-    L.hq = take((size_t)(P + T) * L.hq_blocks * 36);
+    L.items = take((size_t)max_items(g, T) * 32);
+    L.himg = take(smoe::img_bytes((P + T) * L.h_blocks));
     L.Y = take((size_t)(P + T) * H * 4);
     L.total = o;
     return L;
@@ -175,8 +187,7 @@ smoe_status smoe_forward_path(const smoe_geom* g, const smoe_weights* w, const f
     const int T = n_tokens, H = g->n_embd, E = g->n_expert, K = g->top_k, F = g->n_ff;
     const int Fs = has_sh ? g->n_ff_shared : 0;
     const int P = T * K;
-    uint8_t* xq = ws + L.xq;
-    uint16_t* xb = reinterpret_cast<uint16_t*>(ws + L.xb);
+    uint32_t* ximg = reinterpret_cast<uint32_t*>(ws + L.ximg);
     float* logits = (trace && trace->logits) ? trace->logits : reinterpret_cast<float*>(ws + L.logits);
     float* sg = (trace && trace->sgate) ? trace->sgate : reinterpret_cast<float*>(ws + L.sg);
     int32_t* ids = (trace && trace->ids) ? trace->ids : reinterpret_cast<int32_t*>(ws + L.ids);
@@ -187,10 +198,11 @@ smoe_status smoe_forward_path(const smoe_geom* g, const smoe_weights* w, const f
     int32_t* slot = (trace && trace->slot) ? trace->slot : reinterpret_cast<int32_t*>(ws + L.slot);
     int32_t* elist = reinterpret_cast<int32_t*>(ws + L.elist);
     int32_t* nlist = reinterpret_cast<int32_t*>(ws + L.nlist);
-    uint8_t* hq = ws + L.hq;
+    int4* items = reinterpret_cast<int4*>(ws + L.items);
+    uint32_t* himg = reinterpret_cast<uint32_t*>(ws + L.himg);
     float* Y = reinterpret_cast<float*>(ws + L.Y);
     const hipStream_t st = stream_of(hip_stream);
-    const int max_items = (P < E ? P : E) + (has_sh ? 1 : 0);
+    const int n_items = max_items(*g, T);
 
     void* const* ev = trace ? trace->stage_events : nullptr;
     int ev_i = 0;
@@ -205,25 +217,28 @@ smoe_status smoe_forward_path(const smoe_geom* g, const smoe_weights* w, const f
         if (_m != SMOE_OK) return _m;        \
     } while (0)
     SMOE_MARK();
-    SMOE_TRY(smoe::launch_prep(x, (int64_t)T * H, xq, xb, st), "prep");
-    SMOE_MARK();
-    SMOE_TRY(smoe::launch_router(xb, static_cast<const uint16_t*>(w->router), has_sh ? w->gate_inp_sh : nullptr,
-                                 w->logit_bias, H, E, E + (has_sh ? 1 : 0), T, logits, E, sg, st),
+    SMOE_TRY(smoe::launch_router(x, nullptr, static_cast<const uint16_t*>(w->router), has_sh ? w->gate_inp_sh : nullptr,
+                                 w->logit_bias, H, E, E + (has_sh ? 1 : 0), T, logits, E, sg, ximg, st),
              "router");
     SMOE_MARK();
-    SMOE_TRY(smoe::launch_topk(logits, E, T, E, K, ids, wts, st), "topk");
-    SMOE_MARK();
-    SMOE_TRY(smoe::launch_dispatch(ids, P, E, counts, offsets, perm, slot, elist, nlist, st), "dispatch");
+    if (T <= kFusedRouteTokens) {
+        SMOE_TRY(smoe::launch_topk_dispatch(logits, T, E, K, ids, wts, counts, offsets, perm, slot, elist, nlist, items,
+                                            n_items, has_sh ? 1 : 0, st),
+                 "route");
+    } else {
+        SMOE_TRY(smoe::launch_topk(logits, E, T, E, K, ids, wts, st), "topk");
+        SMOE_TRY(smoe::launch_dispatch(ids, P, E, counts, offsets, perm, slot, elist, nlist, items, n_items, T, K,
+                                       has_sh ? 1 : 0, st),
+                 "dispatch");
+    }
     SMOE_MARK();
     SMOE_TRY(smoe::launch_q2_gu(static_cast<const uint8_t*>(w->gate_exps), static_cast<const uint8_t*>(w->up_exps),
-                                static_cast<const uint8_t*>(w->gate_sh), static_cast<const uint8_t*>(w->up_sh), xq,
-                                offsets, perm, elist, nlist, K, T, H, F, Fs, has_sh ? 1 : 0, P, max_items, hq,
-                                L.hq_blocks, st),
+                                static_cast<const uint8_t*>(w->gate_sh), static_cast<const uint8_t*>(w->up_sh), ximg,
+                                items, perm, K, H, F, Fs, has_sh ? 1 : 0, n_items, himg, L.h_blocks, st),
              "gate/up");
     SMOE_MARK();
     SMOE_TRY(smoe::launch_q2_down(static_cast<const uint8_t*>(w->down_exps), static_cast<const uint8_t*>(w->down_sh),
-                                  hq, L.hq_blocks, sg, offsets, elist, nlist, T, H, F, Fs, has_sh ? 1 : 0, P, max_items,
-                                  Y, st),
+                                  himg, L.h_blocks, sg, items, H, F, Fs, n_items, Y, st),
              "down");
     SMOE_MARK();
     SMOE_TRY(smoe::launch_combine(Y, slot, wts, K, H, P, T, (has_sh && add_shared) ? 1 : 0, y, st), "combine");
@@ -270,8 +285,9 @@ smoe_status smoe_bf16_gemv(const uint16_t* x, const uint16_t* w, float* y, int32
     if (n_in == 0 || n_out == 0 || n_tok == 0) return ok();
     if (!x || !w || !y) return fail(SMOE_ENULL, "bf16_gemv: NULL buffer");
     if (n_in % 8 || n_in > 8192) return fail(SMOE_EINVAL, "bf16_gemv: n_in must be a multiple of 8, at most 8192");
+    if ((int64_t)n_tok * n_in % 2) return fail(SMOE_EINVAL, "bf16_gemv: odd element count");
     if (!aligned(x, 16) || !aligned(w, 16)) return fail(SMOE_EALIGN, "bf16_gemv: x and w must be 16-byte aligned");
-    SMOE_TRY(smoe::launch_router(x, w, nullptr, nullptr, n_in, n_out, n_out, n_tok, y, n_out, nullptr,
+    SMOE_TRY(smoe::launch_router(nullptr, x, w, nullptr, nullptr, n_in, n_out, n_out, n_tok, y, n_out, nullptr, nullptr,
                                  stream_of(hip_stream)),
              "bf16_gemv");
     return ok();
@@ -292,7 +308,8 @@ smoe_status smoe_mmvq(int32_t type, const void* w, int64_t byte_off, const uint8
     if (n_in < 0 || n_out < 0 || n_col < 0 || byte_off < 0) return fail(SMOE_EINVAL, "mmvq: negative size");
     if (n_in == 0 || n_out == 0 || n_col == 0) return ok();
     if (type != SMOE_Q2_0) return fail(SMOE_ETYPE, "mmvq: type " + std::to_string(type) + " is not built");
-    if (n_in % 128 || n_in > kMaxFF) return fail(SMOE_EINVAL, "mmvq: n_in must be a multiple of 128, at most 4096");
+    if (n_in > kMaxFF || !smoe::gemv_shape_ok(n_in))
+        return fail(SMOE_EINVAL, "mmvq: n_in must be 128 times a power of two times at most 8, at most 4096");
     if (!w || !x_q8 || !y) return fail(SMOE_ENULL, "mmvq: NULL buffer");
     const uint8_t* base = static_cast<const uint8_t*>(w) + byte_off;
     if (!aligned(base, 4) || !aligned(x_q8, 4)) return fail(SMOE_EALIGN, "mmvq: w + byte_off and x must be 4-byte aligned");
@@ -327,8 +344,8 @@ smoe_status smoe_dispatch(const int32_t* ids, int32_t n_tokens, int32_t k, int32
     if (n_expert > kMaxExpert) return fail(SMOE_EINVAL, "dispatch: n_expert exceeds 1024");
     if ((int64_t)n_tokens * k > (1 << 24)) return fail(SMOE_EINVAL, "dispatch: more than 2^24 pairs");
     if (!ids || !offsets || !perm || !slot) return fail(SMOE_ENULL, "dispatch: NULL buffer");
-    SMOE_TRY(smoe::launch_dispatch(ids, n_tokens * k, n_expert, counts, offsets, perm, slot, nullptr, nullptr,
-                                   stream_of(hip_stream)),
+    SMOE_TRY(smoe::launch_dispatch(ids, n_tokens * k, n_expert, counts, offsets, perm, slot, nullptr, nullptr, nullptr,
+                                   0, n_tokens, k, 0, stream_of(hip_stream)),
              "dispatch");
     return ok();
 }

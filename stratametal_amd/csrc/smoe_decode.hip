@@ -1,14 +1,12 @@
 // stratametal_amd/csrc/smoe_decode.hip - the decode-contract kernels of the MoE block (gfx950, wave64).
 //
-// Decode is a bandwidth-bound dequant-GEMV: each expert's 2-bit rows are streamed once, with coalesced
-// dword loads, unpacked in registers and multiplied with v_dot4_i32_i8 against q8_1 activations held in
-// LDS.  No MFMA.  One launch sequence per call:
-//   k_prep     x -> q8_1 (one quantisation serves routed and shared experts) and bf16 (router input)
-//   k_router   router logits + the shared expert's gate dot, one wave per weight row
-//   k_topk     softmax / top-k / renormalise, one wave per token
-//   k_dispatch canonical stable dispatch of the (token, slot) pairs, the touched-expert list
-//   k_q2_gu    per (touched expert | shared, 32 rows of h): gate and up rows, SwiGLU, q8_1 of h
-//   k_q2_down  per (touched expert | shared, 64 output rows): the down rows (times the shared gate)
+// Decode is a bandwidth-bound dequant-GEMV: each touched expert's 2-bit rows are streamed once with
+// coalesced dwordx4 loads, unpacked in registers and multiplied with v_dot4_i32_i8 against q8_1 activations
+// held in registers.  No MFMA.  The forward call is five launches:
+//   k_router   bf16(x) staged in LDS; router logits and the shared expert's gate dot, one wave per weight row
+//   k_route    one work-group: q8_1 images of x, softmax / top-k per token, canonical stable dispatch
+//   k_q2_gu    per (touched expert | shared, 32 rows of h): gate and up rows, SwiGLU, q8_1 image of h
+//   k_q2_down  per (touched expert | shared, a chunk of output rows): down rows (times the shared gate)
 //   k_combine  y = routing-weighted sum of the pair rows + the shared row
 // Reduction orders are fixed and restated on the host by the test oracle (oracle/smoe_oracle.c).
 #include "smoe_device.hpp"
@@ -16,32 +14,279 @@
 
 namespace smoe {
 
-// ------------------------------------------------------------------------------------------------ prep
-// One thread per element.  Each 32-lane half wave is one q8_1 block.  x: [n] f32 (n % 32 == 0).
-__global__ __launch_bounds__(256) void k_prep(const float* __restrict__ x, int64_t n, uint8_t* __restrict__ xq,
-                                               uint16_t* __restrict__ xb) {
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    const bool live = i < n;
-    const float v = live ? x[i] : 0.0f;
-    if (xb && live) xb[i] = (uint16_t)f32_to_bf16(v);
-    if (xq) {
-        uint32_t ds;
-        const int q = q8_1_value(v, &ds);
-        const int64_t blk = i >> 5;
-        if (((i - (threadIdx.x & 31)) < n)) q8_1_store(q, ds, xq + blk * 36);
+// ------------------------------------------------------------------------------------------------ lane exchange
+// xor exchange inside groups of up to 32 lanes without LDS traffic: DPP quad permutes for distance 1 and 2,
+// ds_swizzle (bit mode, xor mask) for 4, 8 and 16.
+template <int O>
+__device__ __forceinline__ float xor_swap(float v) {
+    const int i = __float_as_int(v);
+    int r;
+    if constexpr (O == 1) r = __builtin_amdgcn_mov_dpp(i, 0xB1, 0xF, 0xF, false);       // quad_perm [1,0,3,2]
+    else if constexpr (O == 2) r = __builtin_amdgcn_mov_dpp(i, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+    else r = __builtin_amdgcn_ds_swizzle(i, 0x1F | (O << 10));                          // lane ^ O within 32
+    return __int_as_float(r);
+}
+
+// Sum over groups of `lpr` consecutive lanes, distance lpr/2 first; every lane of a group ends with the sum.
+__device__ __forceinline__ float group_sum(float v, int lpr) {
+    if (lpr >= 16) v = v + xor_swap<8>(v);
+    if (lpr >= 8) v = v + xor_swap<4>(v);
+    if (lpr >= 4) v = v + xor_swap<2>(v);
+    if (lpr >= 2) v = v + xor_swap<1>(v);
+    return v;
+}
+
+// The xor butterfly 32, 16, ..., 1 over the whole wave (the same sums as wave_sum_xor): distance 32 through
+// ds_bpermute, the rest as in xor_swap.
+__device__ __forceinline__ float wave_sum_xor_fast(float v) {
+    v = v + __shfl_xor(v, 32, kWave);
+    v = v + xor_swap<16>(v);
+    v = v + xor_swap<8>(v);
+    v = v + xor_swap<4>(v);
+    v = v + xor_swap<2>(v);
+    v = v + xor_swap<1>(v);
+    return v;
+}
+
+// Wave maxima for order-free reductions: row rotations by DPP (8, 4, 2, 1), then the four row results read
+// into scalars.  The result is uniform.
+__device__ __forceinline__ uint32_t wave_max_u32_fast(uint32_t v) {
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xF, 0xF, false));  // row_ror:8
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x124, 0xF, 0xF, false));  // row_ror:4
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x122, 0xF, 0xF, false));  // row_ror:2
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x121, 0xF, 0xF, false));  // row_ror:1
+    const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)v, 0), b = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
+    const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)v, 32), d = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+    return max(max(a, b), max(c, d));
+}
+__device__ __forceinline__ float wave_max_fast(float v) {
+    v = __builtin_fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false)));
+    v = __builtin_fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x124, 0xF, 0xF, false)));
+    v = __builtin_fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x122, 0xF, 0xF, false)));
+    v = __builtin_fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x121, 0xF, 0xF, false)));
+    const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return __builtin_fmaxf(__builtin_fmaxf(a, b), __builtin_fmaxf(c, d));
+}
+__device__ __forceinline__ int wave_min_i32_fast(int v) {
+    v = min(v, __builtin_amdgcn_update_dpp(0, v, 0x128, 0xF, 0xF, false));
+    v = min(v, __builtin_amdgcn_update_dpp(0, v, 0x124, 0xF, 0xF, false));
+    v = min(v, __builtin_amdgcn_update_dpp(0, v, 0x122, 0xF, 0xF, false));
+    v = min(v, __builtin_amdgcn_update_dpp(0, v, 0x121, 0xF, 0xF, false));
+    const int a = __builtin_amdgcn_readlane(v, 0), b = __builtin_amdgcn_readlane(v, 16);
+    const int c = __builtin_amdgcn_readlane(v, 32), d = __builtin_amdgcn_readlane(v, 48);
+    return min(min(a, b), min(c, d));
+}
+
+__device__ __forceinline__ int lanes_per_row(int dpr) {
+    const int l = dpr & -dpr;
+    return l > 16 ? 16 : l;
+}
+
+// ------------------------------------------------------------------------------------------------ q8_1 images
+// A q8_1 block (32 activations) as the GEMV kernels read it: 12 dwords, 16-byte aligned:
+//   dwords 0..7  the 32 int8 values permuted so that dword c of each 16-group holds q[c], q[c+4], q[c+8],
+//                q[c+12] (the byte order (codes >> 2c) & 0x03030303 delivers for a 2-bit code dword);
+//   dword 8      f32 of the stored fp16 scale d; dword 9 the int sum of q; dwords 10..11 unused.
+// Built by the same quantiser as the q8_1 block (metal/shaders/iq.metal:597-627); the fp16 sum field of the
+// q8_1 block is not needed by the Q2_0 / IQ2_S dots (metal/shaders/iq.metal:152-180,444-456) and is not kept.
+constexpr int kImgDw = 12;
+
+__device__ __forceinline__ int perm_pos(int i) { return (i & 16) + 4 * (i & 3) + ((i >> 2) & 3); }
+
+// A 32-lane half wave quantises one block (lane & 31 = position) and writes its image; `sc` is 32 bytes of LDS
+// scratch owned by the half.  Every lane of the half must call it; `store` false skips the global store.
+__device__ __forceinline__ void q8_image_store(float v, bool store, uint8_t* sc, uint32_t* img) {
+    const int l32 = threadIdx.x & 31;
+    float a = __builtin_fabsf(v);
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) a = __builtin_fmaxf(a, __shfl_xor(a, o, kWave));
+    float d = a / 127.0f;
+    if (__builtin_fabsf(d) > 65504.0f) d = __builtin_copysignf(65504.0f, d);
+    int q = 0;
+    if (a != 0.0f) {
+        float r = __builtin_roundf(v / d);
+        r = r > 127.0f ? 127.0f : r;
+        r = r < -127.0f ? -127.0f : r;
+        q = (r == r) ? (int)r : 0;
+    }
+    int sq = q;
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) sq += __shfl_xor(sq, o, kWave);
+    sc[perm_pos(l32)] = (uint8_t)(int8_t)q;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (store) {
+        if (l32 < 8) img[l32] = reinterpret_cast<const uint32_t*>(sc)[l32];
+        if (l32 == 8) img[8] = f2u(f16_to_f32(f32_to_f16(d)));
+        if (l32 == 9) img[9] = (uint32_t)sq;
     }
 }
 
+// Activation registers for the four q8_1 blocks of one 36-byte weight unit.
+struct Act4 {
+    uint32_t q[4][8];
+    float d[4];
+    int sq[4];
+};
+
+__device__ __forceinline__ void load_act_img(const uint32_t* __restrict__ img, Act4& a) {
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+        const uint4* p = reinterpret_cast<const uint4*>(img + b * kImgDw);
+        const uint4 lo = p[0], hi = p[1], ds = p[2];
+        a.q[b][0] = lo.x; a.q[b][1] = lo.y; a.q[b][2] = lo.z; a.q[b][3] = lo.w;
+        a.q[b][4] = hi.x; a.q[b][5] = hi.y; a.q[b][6] = hi.z; a.q[b][7] = hi.w;
+        a.d[b] = u2f(ds.x);
+        a.sq[b] = (int)ds.y;
+    }
+}
+
+__device__ __forceinline__ void transpose4x4(uint32_t a0, uint32_t a1, uint32_t a2, uint32_t a3, uint32_t* o) {
+    const uint32_t t0 = __builtin_amdgcn_perm(a1, a0, 0x05010400u);
+    const uint32_t u0 = __builtin_amdgcn_perm(a3, a2, 0x05010400u);
+    const uint32_t t1 = __builtin_amdgcn_perm(a1, a0, 0x07030602u);
+    const uint32_t u1 = __builtin_amdgcn_perm(a3, a2, 0x07030602u);
+    o[0] = __builtin_amdgcn_perm(u0, t0, 0x05040100u);
+    o[1] = __builtin_amdgcn_perm(u0, t0, 0x07060302u);
+    o[2] = __builtin_amdgcn_perm(u1, t1, 0x05040100u);
+    o[3] = __builtin_amdgcn_perm(u1, t1, 0x07060302u);
+}
+
+// From four standard 36-byte q8_1 blocks (the stage API's input): permuted in registers.
+__device__ __forceinline__ void load_act_std(const uint8_t* __restrict__ blk, Act4& a) {
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+        uint32_t w[9];
+        __builtin_memcpy(w, __builtin_assume_aligned(blk + b * 36, 4), 36);
+        transpose4x4(w[1], w[2], w[3], w[4], a.q[b]);
+        transpose4x4(w[5], w[6], w[7], w[8], a.q[b] + 4);
+        int sq = 0;
+#pragma unroll
+        for (int i = 1; i < 9; ++i) sq = __builtin_amdgcn_sdot4((int)w[i], 0x01010101, sq, false);
+        a.d[b] = f16_to_f32(w[0] & 0xFFFFu);
+        a.sq[b] = sq;
+    }
+}
+
+// ------------------------------------------------------------------------------------------------ Q2_0 unit
+// Unit = one 36-byte double block (two Q2_0 blocks, 128 weights, dword aligned), 9 dwords:
+//   w0 = {d0, codes0[0..1]}, w1..w3 = codes0[2..13], w4 = {codes0[14..15], d1}, w5..w8 = codes1[0..15].
+// L = ((P0 + P1) + P2) + P3, P_h = (f32(d_w) * f32(d_x)) * (float) sumi_h, sumi_h = sum(code * q) - sum(q)
+// = sum((code - 1) * q) exactly (metal/shaders/iq.metal:444-456).
+__device__ __forceinline__ void load_unit(const uint8_t* p, uint32_t (&w)[9]) {
+    __builtin_memcpy(w, __builtin_assume_aligned(p, 4), 36);
+}
+
+__device__ __forceinline__ int half_dot(uint32_t a, uint32_t b, const uint32_t* X) {
+    const uint32_t M = 0x03030303u;
+    int s = 0;
+    s = __builtin_amdgcn_sdot4((int)(a & M), (int)X[0], s, false);
+    s = __builtin_amdgcn_sdot4((int)((a >> 2) & M), (int)X[1], s, false);
+    s = __builtin_amdgcn_sdot4((int)((a >> 4) & M), (int)X[2], s, false);
+    s = __builtin_amdgcn_sdot4((int)((a >> 6) & M), (int)X[3], s, false);
+    s = __builtin_amdgcn_sdot4((int)(b & M), (int)X[4], s, false);
+    s = __builtin_amdgcn_sdot4((int)((b >> 2) & M), (int)X[5], s, false);
+    s = __builtin_amdgcn_sdot4((int)((b >> 4) & M), (int)X[6], s, false);
+    s = __builtin_amdgcn_sdot4((int)((b >> 6) & M), (int)X[7], s, false);
+    return s;
+}
+
+// Marks the weight registers as rewritten, so the compiler keeps the per-column unpacking inside the column
+// loop instead of hoisting every unit's unpacked codes (4 words per code dword) and running out of registers.
+template <int NIT, int MAXUPL>
+__device__ __forceinline__ void pin_units(uint32_t (&w)[NIT][MAXUPL][9]) {
+#pragma unroll
+    for (int it = 0; it < NIT; ++it)
+#pragma unroll
+        for (int m = 0; m < MAXUPL; ++m)
+#pragma unroll
+            for (int i = 0; i < 9; ++i) asm volatile("" : "+v"(w[it][m][i]));
+}
+
+__device__ __forceinline__ float q2_unit_dot(const uint32_t (&w)[9], const Act4& a) {
+    const float d0 = f16_to_f32(w[0] & 0xFFFFu);
+    const float d1 = f16_to_f32(w[4] >> 16);
+    const uint32_t c0 = __builtin_amdgcn_alignbyte(w[1], w[0], 2);
+    const uint32_t c1 = __builtin_amdgcn_alignbyte(w[2], w[1], 2);
+    const uint32_t c2 = __builtin_amdgcn_alignbyte(w[3], w[2], 2);
+    const uint32_t c3 = __builtin_amdgcn_alignbyte(w[4], w[3], 2);
+    const float P0 = (d0 * a.d[0]) * (float)(half_dot(c0, c1, a.q[0]) - a.sq[0]);
+    const float P1 = (d0 * a.d[1]) * (float)(half_dot(c2, c3, a.q[1]) - a.sq[1]);
+    const float P2 = (d1 * a.d[2]) * (float)(half_dot(w[5], w[6], a.q[2]) - a.sq[2]);
+    const float P3 = (d1 * a.d[3]) * (float)(half_dot(w[7], w[8], a.q[3]) - a.sq[3]);
+    return ((P0 + P1) + P2) + P3;
+}
+
 // ------------------------------------------------------------------------------------------------ router
-// logits[t][row] = sum_i f32(bf16 x[t][i]) * f32(bf16 W[row][i]); row == E is the shared gate row
-// (w_inp) and goes to sg[t].  One wave per row; lane l owns the 8-element chunks l, l+64, ...; each lane
-// accumulates its chunks in element order from 0, then an xor butterfly 32..1 (oracle: or_bf16_gemv_dev).
-// Every product of two bf16 values is exact in f32, so fmaf(x, w, acc) == acc + x * w.
+// logits[t][row] = sum_i f32(bf16 x[t][i]) * f32(bf16 W[row][i]); row == E is the shared gate row (w_inp),
+// written to sg[t].  The block stages its token tile of x as bf16 in LDS (RNE, NaN quieted), then each wave
+// takes one weight row: lane l owns the 8-element chunks l, l+64, ...; accumulates them in element order from
+// 0, then an xor butterfly 32..1 (oracle: or_bf16_gemv_dev).  Every bf16 product is exact in f32, so
+// fmaf(x, w, acc) == acc + x * w.  `xf` (f32) or `xb` (bf16 bits) supplies x.  With `ximg`, the blocks of
+// the tile also write the q8_1 images of the tile's x, a share each (the decode path's activations).
 template <int MAXC>
-__global__ __launch_bounds__(256) void k_router(const uint16_t* __restrict__ xb, const uint16_t* __restrict__ W,
-                                                 const uint16_t* __restrict__ w_inp, const float* __restrict__ bias,
-                                                 int H, int E, int rows_total, int T, int tok_per_block,
-                                                 float* __restrict__ logits, int ld_logits, float* __restrict__ sg) {
+__global__ __launch_bounds__(256) void k_router(const float* __restrict__ xf, const uint16_t* __restrict__ xb,
+                                                 const uint16_t* __restrict__ W, const uint16_t* __restrict__ w_inp,
+                                                 const float* __restrict__ bias, int H, int E, int rows_total, int T,
+                                                 int tok_tile, float* __restrict__ logits, int ld_logits,
+                                                 float* __restrict__ sg, uint32_t* __restrict__ ximg) {
+    extern __shared__ __align__(16) uint32_t smem[];
+    __shared__ uint8_t qsc[8][32];
+    const int t0 = blockIdx.y * tok_tile;
+    const int nt = min(tok_tile, T - t0);
+    // stage the tile, 8 vector loads in flight per thread
+    const int n8 = nt * H / 8;  // groups of 8 values = one uint4 of bf16
+    for (int base = 0; base < n8; base += 256 * 4) {
+        uint4 v[4];
+        if (xf) {
+            float4 f[8];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int g = base + u * 256 + threadIdx.x;
+                const float4* src = reinterpret_cast<const float4*>(xf + (size_t)t0 * H) + 2 * (size_t)g;
+                if (g < n8) {
+                    f[2 * u] = src[0];
+                    f[2 * u + 1] = src[1];
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const float4 a = f[2 * u], b = f[2 * u + 1];
+                v[u] = make_uint4(f32_to_bf16(a.x) | (f32_to_bf16(a.y) << 16), f32_to_bf16(a.z) | (f32_to_bf16(a.w) << 16),
+                                  f32_to_bf16(b.x) | (f32_to_bf16(b.y) << 16), f32_to_bf16(b.z) | (f32_to_bf16(b.w) << 16));
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int g = base + u * 256 + threadIdx.x;
+                if (g < n8) v[u] = reinterpret_cast<const uint4*>(xb + (size_t)t0 * H)[g];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int g = base + u * 256 + threadIdx.x;
+            if (g < n8) reinterpret_cast<uint4*>(smem)[g] = v[u];
+        }
+    }
+    if (ximg) {  // this block's share of the tile's q8_1 images, one block per half wave
+        const int nb = nt * (H >> 5);
+        const int per = (nb + gridDim.x - 1) / gridDim.x;
+        const int b0 = blockIdx.x * per, b1 = min(nb, b0 + per);
+        const int hw = threadIdx.x >> 5;
+        for (int b = b0; b < b1; b += 8) {
+            const int bb = b + hw;
+            const bool live = bb < b1;
+            const size_t blk = (size_t)t0 * (H >> 5) + (live ? bb : b0);
+            const float v = live ? xf[blk * 32 + (threadIdx.x & 31)] : 0.0f;
+            q8_image_store(v, live, qsc[hw], ximg + blk * kImgDw);
+        }
+    }
+    __syncthreads();
+    const uint16_t* xs = reinterpret_cast<const uint16_t*>(smem);
     const int lane = threadIdx.x & 63;
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= rows_total) return;
@@ -51,117 +296,178 @@ __global__ __launch_bounds__(256) void k_router(const uint16_t* __restrict__ xb,
 #pragma unroll
     for (int j = 0; j < MAXC; ++j) {
         const int c = lane + 64 * j;
-        if (c < chunks) wv[j] = *reinterpret_cast<const uint4*>(wr + 8 * c);
-        else wv[j] = make_uint4(0, 0, 0, 0);
+        wv[j] = c < chunks ? *reinterpret_cast<const uint4*>(wr + 8 * c) : make_uint4(0, 0, 0, 0);
     }
-    const int t0 = blockIdx.y * tok_per_block;
-    const int t1 = min(T, t0 + tok_per_block);
-    for (int t = t0; t < t1; ++t) {
-        const uint16_t* xr = xb + (size_t)t * H;
-        float acc = 0.0f;
+    for (int t = 0; t < nt; t += 4) {  // four tokens at a time: four independent accumulation chains
+        const int ng = min(4, nt - t);
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int j = 0; j < MAXC; ++j) {
             const int c = lane + 64 * j;
             if (c < chunks) {
-                const uint4 xv = *reinterpret_cast<const uint4*>(xr + 8 * c);
-                const uint32_t xs[4] = {xv.x, xv.y, xv.z, xv.w};
-                const uint32_t ws[4] = {wv[j].x, wv[j].y, wv[j].z, wv[j].w};
+                const uint32_t wq[4] = {wv[j].x, wv[j].y, wv[j].z, wv[j].w};
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    acc = __builtin_fmaf(u2f(xs[q] << 16), u2f(ws[q] << 16), acc);
-                    acc = __builtin_fmaf(u2f(xs[q] & 0xFFFF0000u), u2f(ws[q] & 0xFFFF0000u), acc);
+                for (int g = 0; g < 4; ++g) {
+                    if (g < ng) {
+                        const uint4 xv = *reinterpret_cast<const uint4*>(xs + (size_t)(t + g) * H + 8 * c);
+                        const uint32_t xq[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            acc[g] = __builtin_fmaf(u2f(xq[q] << 16), u2f(wq[q] << 16), acc[g]);
+                            acc[g] = __builtin_fmaf(u2f(xq[q] & 0xFFFF0000u), u2f(wq[q] & 0xFFFF0000u), acc[g]);
+                        }
+                    }
                 }
             }
         }
-        acc = wave_sum_xor(acc);
-        if (lane == 0) {
-            if (row < E) logits[(size_t)t * ld_logits + row] = bias ? acc + bias[row] : acc;
-            else sg[t] = acc;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            if (g < ng) {
+                const float v = wave_sum_xor_fast(acc[g]);
+                if (lane == 0) {
+                    if (row < E) logits[(size_t)(t0 + t + g) * ld_logits + row] = bias ? v + bias[row] : v;
+                    else sg[t0 + t + g] = v;
+                }
+            }
         }
     }
 }
 
 // ------------------------------------------------------------------------------------------------ top-k
-__device__ __forceinline__ bool better(float av, int ai, float bv, int bi) {
-    return av > bv || (av == bv && ai < bi);
+// Orderable 32-bit key of a logit: NaN ranks as -inf, -0 as +0, then the sign-flip map, so that
+// key(a) > key(b) <=> a > b and key(a) == key(b) <=> a == b.
+__device__ __forceinline__ uint32_t order_key(float v) {
+    if (v != v) v = -__builtin_inff();
+    if (v == 0.0f) v = 0.0f;
+    const uint32_t b = f2u(v);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
-// One wave per token, E <= 1024 (16 logits per lane, lane l owns e = l + 64 j).  Selection by (logit desc,
-// id asc), a NaN logit ranks as -inf.  ex_e = exp(l_e - max); S = per-lane sums in j order, then the xor
-// butterfly; p_i = ex_i / S; w_i = p_i / max(sum of the k p_i in selection order, 2^-14)
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, o, kWave));
+    return v;
+}
+
+// Sorting networks that order a lane's slots (checked exhaustively by the 0-1 principle): the optimal
+// 19-comparator network for 8 inputs and Batcher's odd-even merge sort for 16.
+struct Cmp {
+    int a, b;
+};
+constexpr Cmp kNet8[19] = {{0, 2}, {1, 3}, {4, 6}, {5, 7}, {0, 4}, {1, 5}, {2, 6}, {3, 7}, {0, 1}, {2, 3}, {4, 5}, {6, 7}, {2, 4}, {3, 5}, {1, 4}, {3, 6}, {1, 2}, {3, 4}, {5, 6}};
+constexpr Cmp kNet16[63] = {{0, 1}, {2, 3}, {4, 5}, {6, 7}, {8, 9}, {10, 11}, {12, 13}, {14, 15}, {0, 2}, {1, 3}, {4, 6}, {5, 7}, {8, 10}, {9, 11}, {12, 14}, {13, 15}, {1, 2}, {5, 6}, {9, 10}, {13, 14}, {0, 4}, {1, 5}, {2, 6}, {3, 7}, {8, 12}, {9, 13}, {10, 14}, {11, 15}, {2, 4}, {3, 5}, {10, 12}, {11, 13}, {1, 2}, {3, 4}, {5, 6}, {9, 10}, {11, 12}, {13, 14}, {0, 8}, {1, 9}, {2, 10}, {3, 11}, {4, 12}, {5, 13}, {6, 14}, {7, 15}, {4, 8}, {5, 9}, {6, 10}, {7, 11}, {2, 4}, {3, 5}, {6, 8}, {7, 9}, {10, 12}, {11, 13}, {1, 2}, {3, 4}, {5, 6}, {7, 8}, {9, 10}, {11, 12}, {13, 14}};
+
+// One wave routes one token, E <= 64 J (lane l holds e = l + 64 j, j < J).  Selection by (logit desc, id
+// asc): each lane sorts its slots once by (key desc, slot asc); a round takes the wave maximum of the lanes'
+// head keys, the single lane holding it wins (or, on an exact tie across lanes, the lowest candidate id) and
+// pops its head.  ex_e = exp(l_e - max); S = per-lane sums in j order, then the xor butterfly 32..1;
+// p_i = ex_i / S; w_i = p_i / max(sum of the k p_i in selection order, 2^-14)
 // (metal/shaders/router.metal:30-132; oracle: or_route_dev).
+template <int J>
+__device__ void route_token_t(const float* __restrict__ l, int E, int k, int32_t* __restrict__ ids,
+                              float* __restrict__ wts) {
+    const int lane = threadIdx.x & 63;
+    uint32_t key[J];
+    float ex[J];
+    int jj[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) {  // all loads first, unconditional (clamped index), so they overlap
+        const int e = lane + 64 * j;
+        ex[j] = l[e < E ? e : E - 1];
+    }
+    float mx = -__builtin_inff();
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const bool valid = lane + 64 * j < E;
+        float v = ex[j];
+        v = (v != v || !valid) ? -__builtin_inff() : v;
+        key[j] = valid ? order_key(v) : 0u;  // 0 is below every real key (order_key(-inf) = 0x007FFFFF)
+        ex[j] = v;
+        jj[j] = j;
+        mx = __builtin_fmaxf(mx, v);
+    }
+    mx = wave_max_fast(mx);
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const bool valid = lane + 64 * j < E;
+        const float x = expf_smoe(ex[j] - mx);
+        ex[j] = valid ? x : 0.0f;
+        acc = valid ? acc + x : acc;
+    }
+    const float S = wave_sum_xor_fast(acc);
+    const Cmp* net = J == 8 ? kNet8 : kNet16;
+    constexpr int NC = J == 8 ? 19 : 63;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const int a = net[c].a, b = net[c].b;
+        const bool sw = key[b] > key[a] || (key[b] == key[a] && jj[b] < jj[a]);
+        const uint32_t ka = key[a], kb = key[b];
+        const float xa = ex[a], xb = ex[b];
+        const int ja = jj[a], jb = jj[b];
+        key[a] = sw ? kb : ka;
+        key[b] = sw ? ka : kb;
+        ex[a] = sw ? xb : xa;
+        ex[b] = sw ? xa : xb;
+        jj[a] = sw ? jb : ja;
+        jj[b] = sw ? ja : jb;
+    }
+    float my_x = 0.0f;
+    int my_id = 0;
+    for (int i = 0; i < k; ++i) {
+        const uint32_t gk = wave_max_u32_fast(key[0]);
+        const bool mine = key[0] == gk;
+        const unsigned long long tied = __ballot(mine);
+        int wid;
+        if (__popcll(tied) == 1) {
+            wid = __builtin_amdgcn_readlane(lane + 64 * jj[0], __ffsll((long long)tied) - 1);
+        } else {  // an exact tie across lanes: the lowest id among the tied heads
+            wid = wave_min_i32_fast(mine ? lane + 64 * jj[0] : 0x7FFFFFFF);
+        }
+        const int wl = wid & 63;
+        const float xw = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ex[0]), wl));
+        if (lane == i) {
+            my_x = xw;
+            my_id = wid;
+        }
+        if (lane == wl) {  // pop the head
+#pragma unroll
+            for (int j = 0; j + 1 < J; ++j) {
+                key[j] = key[j + 1];
+                ex[j] = ex[j + 1];
+                jj[j] = jj[j + 1];
+            }
+            key[J - 1] = 0u;
+        }
+    }
+    const float p = my_x / S;
+    float ssel = 0.0f;
+    for (int i = 0; i < k; ++i) ssel = ssel + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), i));
+    const float den = __builtin_fmaxf(ssel, 6.103515625e-05f);
+    if (lane < k) {
+        ids[lane] = my_id;
+        wts[lane] = p / den;
+    }
+}
+
+__device__ __forceinline__ void route_token(const float* __restrict__ l, int E, int k, int32_t* __restrict__ ids,
+                                            float* __restrict__ wts) {
+    if (E <= 512) route_token_t<8>(l, E, k, ids, wts);
+    else route_token_t<16>(l, E, k, ids, wts);
+}
+
 __global__ __launch_bounds__(64) void k_topk(const float* __restrict__ logits, int ld_logits, int T, int E, int k,
                                               int32_t* __restrict__ ids, float* __restrict__ wts) {
     const int t = blockIdx.x;
     if (t >= T) return;
-    const int lane = threadIdx.x;
-    const float* l = logits + (size_t)t * ld_logits;
-    float key[16], ex[16];
-    uint32_t taken = 0;
-    float mx = -__builtin_inff();
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-        const int e = lane + 64 * j;
-        float v = -__builtin_inff();
-        if (e < E) {
-            v = l[e];
-            if (v != v) v = -__builtin_inff();
-        } else {
-            taken |= 1u << j;
-        }
-        key[j] = v;
-        mx = __builtin_fmaxf(mx, v);
-    }
-    mx = wave_max(mx);
-    float acc = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-        ex[j] = 0.0f;
-        if (!((taken >> j) & 1u)) {
-            ex[j] = expf_smoe(key[j] - mx);
-            acc = acc + ex[j];
-        }
-    }
-    const float S = wave_sum_xor(acc);
-    float ssel = 0.0f, my_p = 0.0f;
-    for (int i = 0; i < k; ++i) {
-        float bv = -__builtin_inff(), bx = 0.0f;
-        int bi = 0x7FFFFFFF;
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            const int e = lane + 64 * j;
-            if (!((taken >> j) & 1u) && better(key[j], e, bv, bi)) {
-                bv = key[j];
-                bi = e;
-                bx = ex[j];
-            }
-        }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-            const float ov = __shfl_xor(bv, o, kWave);
-            const int oi = __shfl_xor(bi, o, kWave);
-            const float ox = __shfl_xor(bx, o, kWave);
-            if (better(ov, oi, bv, bi)) {
-                bv = ov;
-                bi = oi;
-                bx = ox;
-            }
-        }
-        if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
-        const float p = bx / S;
-        if (lane == i) my_p = p;
-        ssel = ssel + p;
-        if (lane == 0) ids[(size_t)t * k + i] = bi;
-    }
-    const float den = __builtin_fmaxf(ssel, 6.103515625e-05f);
-    if (lane < k) wts[(size_t)t * k + lane] = my_p / den;
+    route_token(logits + (size_t)t * ld_logits, E, k, ids + (size_t)t * k, wts + (size_t)t * k);
 }
 
 // ------------------------------------------------------------------------------------------------ dispatch
-// One work-group of 1024 threads.  counts by LDS atomics (order-free), offsets by an exclusive scan,
-// ranks by a ballot match inside each wave and per-wave counts in LDS, 1024 pairs per pass, so a pair's
-// position is offsets[e] + (number of earlier pairs with the same expert): the stable counting sort of the
-// oracle's or_dispatch.  Also the ascending list of touched experts.
+// Stable counting sort of the pairs i = t*k + s by expert, in one work-group of 1024 threads: counts by LDS
+// atomics (order-free), offsets by an exclusive scan, ranks by a ballot match inside each wave plus per-wave
+// counts in LDS, 1024 pairs per pass: position = offsets[e] + (number of earlier pairs with expert e) (oracle:
+// or_dispatch).  Also the ascending list of touched experts.  An out-of-range id gets slot -1.
 __device__ __forceinline__ int block_exclusive_scan_1024(int v, int* scratch /*>= 17 ints*/, int* total) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     int incl = v;
@@ -188,33 +494,45 @@ __device__ __forceinline__ int block_exclusive_scan_1024(int v, int* scratch /*>
     return r;
 }
 
-__global__ __launch_bounds__(1024) void k_dispatch(const int32_t* __restrict__ ids, int P, int E,
-                                                    int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
-                                                    int32_t* __restrict__ perm, int32_t* __restrict__ slot,
-                                                    int32_t* __restrict__ elist, int32_t* __restrict__ n_list) {
-    __shared__ int cnt[1024];
-    __shared__ int run[1024];
-    __shared__ uint8_t wcnt[16][1024];
-    __shared__ int scan_scratch[17];
+struct DispatchLds {
+    int cnt[1024];
+    int run[1024];
+    int el[1024];
+    uint8_t wcnt[16][1024];
+    int scan[17];
+};
+
+// Work-item table of the decode GEMV kernels, 8 ints per item (one 32-byte load): routed item wi < n_touched
+// {e, first, ncol, tok0 | tok1, tok2, tok3, 0} (the tokens of its first four pairs), shared-expert chunk
+// {-1, P + t0, ncol, t0 | t0 + 1, t0 + 2, t0 + 3, 0}, unused {-2, ...}.
+constexpr int kShCols = 4;
+constexpr int kItemEmpty = -2, kItemShared = -1;
+
+__device__ void dispatch_block(const int32_t* __restrict__ ids, int P, int E, int32_t* __restrict__ counts,
+                               int32_t* __restrict__ offsets, int32_t* __restrict__ perm, int32_t* __restrict__ slot,
+                               int32_t* __restrict__ elist, int32_t* __restrict__ n_list, DispatchLds& s,
+                               int4* __restrict__ items = nullptr, int max_items = 0, int T = 0, int k = 1,
+                               int has_shared = 0) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    cnt[tid] = 0;
-    for (int w = 0; w < 16; ++w) wcnt[w][tid] = 0;
+    s.cnt[tid] = 0;
+    for (int w = 0; w < 16; ++w) s.wcnt[w][tid] = 0;
     __syncthreads();
     for (int i = tid; i < P; i += 1024) {
         const int e = ids[i];
-        if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+        if (e >= 0 && e < E) atomicAdd(&s.cnt[e], 1);
     }
     __syncthreads();
-    const int c = tid < E ? cnt[tid] : 0;
+    const int c = tid < E ? s.cnt[tid] : 0;
     int total;
-    const int off = block_exclusive_scan_1024(c, scan_scratch, &total);
+    const int off = block_exclusive_scan_1024(c, s.scan, &total);
     const int flag = c > 0 ? 1 : 0;
     int n_touched;
-    const int fpos = block_exclusive_scan_1024(flag, scan_scratch, &n_touched);
+    const int fpos = block_exclusive_scan_1024(flag, s.scan, &n_touched);
     if (tid < E) {
         if (counts) counts[tid] = c;
         offsets[tid] = off;
-        run[tid] = off;
+        s.run[tid] = off;
+        if (flag) s.el[fpos] = tid;
         if (flag && elist) elist[fpos] = tid;
     }
     if (tid == 0) {
@@ -226,7 +544,7 @@ __global__ __launch_bounds__(1024) void k_dispatch(const int32_t* __restrict__ i
     for (int base = 0; base < P; base += 1024) {
         const int i = base + tid;
         const int id = i < P ? ids[i] : -1;
-        const bool valid = id >= 0 && id < E;  // an out-of-range id is not dispatched: slot[i] = -1
+        const bool valid = id >= 0 && id < E;
         const int key = valid ? id : 0;
         if (i < P && !valid) slot[i] = -1;
         unsigned long long m = __ballot(valid);
@@ -239,283 +557,317 @@ __global__ __launch_bounds__(1024) void k_dispatch(const int32_t* __restrict__ i
         const int rank_w = __popcll(m & lt);
         const int cnt_w = __popcll(m);
         const bool leader = (m & lt) == 0ull;
-        if (valid && leader) wcnt[wave][key] = (uint8_t)cnt_w;
+        if (valid && leader) s.wcnt[wave][key] = (uint8_t)cnt_w;
         __syncthreads();
         if (valid) {
-            int pos = run[key] + rank_w;
-            for (int w = 0; w < wave; ++w) pos += wcnt[w][key];
+            int pos = s.run[key] + rank_w;
+            for (int w = 0; w < wave; ++w) pos += s.wcnt[w][key];
             perm[pos] = i;
             slot[i] = pos;
         }
         __syncthreads();
         if (valid && leader) {
-            atomicAdd(&run[key], cnt_w);
-            wcnt[wave][key] = 0;
+            atomicAdd(&s.run[key], cnt_w);
+            s.wcnt[wave][key] = 0;
         }
         __syncthreads();
     }
-}
-
-// ------------------------------------------------------------------------------------------------ Q2_0 rows
-// A "unit" is one 36-byte double block (two Q2_0 blocks, 128 weights, dword aligned): 9 dwords
-//   w0 = {d0, codes0[0..1]}, w1..w3 = codes0[2..13], w4 = {codes0[14..15], d1}, w5..w8 = codes1[0..15].
-// Activations for the unit's four q8_1 blocks sit in LDS in the permuted form below.  Unit part
-// L = ((P0 + P1) + P2) + P3 with P_h = (f32(d_w) * f32(d_x)) * (float) sumi_h and
-// sumi_h = sum(code * q) - sum(q) = sum((code - 1) * q) (metal/shaders/iq.metal:444-456).
-
-// LDS image of one q8_1 block: 8 dwords of q permuted so that dword c of each 16-group holds
-// q[c], q[c+4], q[c+8], q[c+12] (the order (codes >> 2c) & 0x03030303 delivers), then f32 d, int sum q.
-constexpr int kActDw = 12;  // dwords per q8_1 block image (16-byte aligned)
-
-__device__ __forceinline__ void transpose4x4(uint32_t a0, uint32_t a1, uint32_t a2, uint32_t a3, uint32_t* o) {
-    const uint32_t t0 = __builtin_amdgcn_perm(a1, a0, 0x05010400u);  // a0b0 a1b0 a0b1 a1b1
-    const uint32_t u0 = __builtin_amdgcn_perm(a3, a2, 0x05010400u);  // a2b0 a3b0 a2b1 a3b1
-    const uint32_t t1 = __builtin_amdgcn_perm(a1, a0, 0x07030602u);  // a0b2 a1b2 a0b3 a1b3
-    const uint32_t u1 = __builtin_amdgcn_perm(a3, a2, 0x07030602u);  // a2b2 a3b2 a2b3 a3b3
-    o[0] = __builtin_amdgcn_perm(u0, t0, 0x05040100u);
-    o[1] = __builtin_amdgcn_perm(u0, t0, 0x07060302u);
-    o[2] = __builtin_amdgcn_perm(u1, t1, 0x05040100u);
-    o[3] = __builtin_amdgcn_perm(u1, t1, 0x07060302u);
-}
-
-// q8_1 block (9 dwords in global memory) -> LDS image
-__device__ __forceinline__ void stage_q8(const uint32_t* __restrict__ src, uint32_t* dst) {
-    uint32_t b[9];
-#pragma unroll
-    for (int i = 0; i < 9; ++i) b[i] = src[i];
-    uint32_t o[8];
-    transpose4x4(b[1], b[2], b[3], b[4], o);
-    transpose4x4(b[5], b[6], b[7], b[8], o + 4);
-    int sq = 0;
-#pragma unroll
-    for (int i = 1; i < 9; ++i) sq = __builtin_amdgcn_sdot4((int)b[i], 0x01010101, sq, false);
-    uint4* d4 = reinterpret_cast<uint4*>(dst);
-    d4[0] = make_uint4(o[0], o[1], o[2], o[3]);
-    d4[1] = make_uint4(o[4], o[5], o[6], o[7]);
-    d4[2] = make_uint4(f2u(f16_to_f32(b[0] & 0xFFFFu)), (uint32_t)sq, 0u, 0u);
-}
-
-__device__ __forceinline__ int q2_half_dot(uint32_t a, uint32_t b, const uint32_t* X) {
-    const uint32_t M = 0x03030303u;
-    int s = 0;
-    s = __builtin_amdgcn_sdot4((int)(a & M), (int)X[0], s, false);
-    s = __builtin_amdgcn_sdot4((int)((a >> 2) & M), (int)X[1], s, false);
-    s = __builtin_amdgcn_sdot4((int)((a >> 4) & M), (int)X[2], s, false);
-    s = __builtin_amdgcn_sdot4((int)((a >> 6) & M), (int)X[3], s, false);
-    s = __builtin_amdgcn_sdot4((int)(b & M), (int)X[4], s, false);
-    s = __builtin_amdgcn_sdot4((int)((b >> 2) & M), (int)X[5], s, false);
-    s = __builtin_amdgcn_sdot4((int)((b >> 4) & M), (int)X[6], s, false);
-    s = __builtin_amdgcn_sdot4((int)((b >> 6) & M), (int)X[7], s, false);
-    return s;
-}
-
-// act: LDS images of the unit's 4 q8_1 blocks (4 * kActDw dwords)
-__device__ __forceinline__ float q2_unit_dot(const uint32_t (&w)[9], const uint32_t* act) {
-    const float d0 = f16_to_f32(w[0] & 0xFFFFu);
-    const float d1 = f16_to_f32(w[4] >> 16);
-    uint32_t c[8];
-    c[0] = __builtin_amdgcn_alignbyte(w[1], w[0], 2);
-    c[1] = __builtin_amdgcn_alignbyte(w[2], w[1], 2);
-    c[2] = __builtin_amdgcn_alignbyte(w[3], w[2], 2);
-    c[3] = __builtin_amdgcn_alignbyte(w[4], w[3], 2);
-    c[4] = w[5];
-    c[5] = w[6];
-    c[6] = w[7];
-    c[7] = w[8];
-    float L = 0.0f;
-#pragma unroll
-    for (int h = 0; h < 4; ++h) {
-        const uint32_t* X = act + h * kActDw;
-        const uint4 x0 = *reinterpret_cast<const uint4*>(X);
-        const uint4 x1 = *reinterpret_cast<const uint4*>(X + 4);
-        const uint32_t xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-        const float dx = u2f(X[8]);
-        const int sq = (int)X[9];
-        const int sumi = q2_half_dot(c[2 * h], c[2 * h + 1], xs) - sq;
-        const float P = ((h < 2 ? d0 : d1) * dx) * (float)sumi;
-        L = h == 0 ? P : L + P;
+    if (!items) return;
+    for (int wi = tid; wi < max_items; wi += 1024) {
+        int4 a = make_int4(kItemEmpty, 0, 0, 0), b = make_int4(0, 0, 0, 0);
+        if (wi < n_touched) {
+            const int e = s.el[wi], cnt = s.cnt[e], first = s.run[e] - cnt;  // run[e] ends at offsets[e + 1]
+            int tk[4] = {0, 0, 0, 0};
+            for (int c = 0; c < 4 && c < cnt; ++c) tk[c] = perm[first + c] / k;
+            a = make_int4(e, first, cnt, tk[0]);
+            b = make_int4(tk[1], tk[2], tk[3], 0);
+        } else if (has_shared && (wi - n_touched) * kShCols < T) {
+            const int t0 = (wi - n_touched) * kShCols;
+            a = make_int4(kItemShared, P + t0, min(kShCols, T - t0), t0);
+            b = make_int4(t0 + 1, t0 + 2, t0 + 3, 0);
+        }
+        items[2 * wi] = a;
+        items[2 * wi + 1] = b;
     }
-    return L;
 }
 
-__device__ __forceinline__ void load_unit(const uint8_t* p, uint32_t (&w)[9]) {
-    // 4-byte aligned (units are 36 bytes from a 4-byte aligned tensor base)
-    const uint32_t* q = reinterpret_cast<const uint32_t*>(__builtin_assume_aligned(p, 4));
-    __builtin_memcpy(w, q, 36);
+__global__ __launch_bounds__(1024) void k_dispatch(const int32_t* __restrict__ ids, int P, int E,
+                                                    int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
+                                                    int32_t* __restrict__ perm, int32_t* __restrict__ slot,
+                                                    int32_t* __restrict__ elist, int32_t* __restrict__ n_list,
+                                                    int4* __restrict__ items, int max_items, int T, int k,
+                                                    int has_shared) {
+    __shared__ DispatchLds s;
+    dispatch_block(ids, P, E, counts, offsets, perm, slot, elist, n_list, s, items, max_items, T, k, has_shared);
 }
 
-// Column source of a GEMV tile: token / output row of column c.
-struct Cols {
-    int n;          // number of columns
-    int first;      // first slot (routed) or token (shared)
-    const int32_t* perm;  // routed: pair index at each dispatch position; null for the shared expert
-    int k;
+// ------------------------------------------------------------------------------------------------ route (fused)
+// The decode call's middle, one work-group of 1024 threads: one wave per token routes it (route_token), then
+// the dispatch of all pairs.
+__global__ __launch_bounds__(1024) void k_topk_dispatch(const float* __restrict__ logits, int T, int E, int k,
+                                                         int32_t* __restrict__ ids, float* __restrict__ wts,
+                                                         int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
+                                                         int32_t* __restrict__ perm, int32_t* __restrict__ slot,
+                                                         int32_t* __restrict__ elist, int32_t* __restrict__ n_list,
+                                                         int4* __restrict__ items, int max_items, int has_shared) {
+    __shared__ DispatchLds s;
+    const int wave = threadIdx.x >> 6;
+    for (int t = wave; t < T; t += 16) route_token(logits + (size_t)t * E, E, k, ids + (size_t)t * k, wts + (size_t)t * k);
+    __syncthreads();
+    dispatch_block(ids, T * k, E, counts, offsets, perm, slot, elist, n_list, s, items, max_items, T, k, has_shared);
+}
+
+// q8_1 images of a flat f32 vector (n % 32 == 0), one block per half wave.
+__global__ __launch_bounds__(256) void k_quant_image(const float* __restrict__ x, int64_t n, uint32_t* __restrict__ img) {
+    __shared__ uint8_t qsc[8][32];
+    const int64_t b = (int64_t)blockIdx.x * 8 + (threadIdx.x >> 5);
+    const bool live = b * 32 < n;
+    const float v = live ? x[b * 32 + (threadIdx.x & 31)] : 0.0f;
+    q8_image_store(v, live, qsc[threadIdx.x >> 5], img + (live ? b : 0) * kImgDw);
+}
+
+// ------------------------------------------------------------------------------------------------ expert GEMV
+// Row geometry: dpr = n_in / 128 units; lpr = lanes per row; upl = units per lane; rpi = 64 / lpr rows per
+// wave pass.  Lane (group, l) handles units g = l + lpr * m (m < upl) of its row.
+struct RowGeo {
+    int dpr, lpr, upl, rpi;
 };
-
-__device__ __forceinline__ int col_token(const Cols& cs, int c) {
-    return cs.perm ? cs.perm[cs.first + c] / cs.k : cs.first + c;
+__device__ __forceinline__ RowGeo row_geo(int n_in) {
+    RowGeo r;
+    r.dpr = n_in >> 7;
+    r.lpr = lanes_per_row(r.dpr);
+    r.upl = r.dpr / r.lpr;
+    r.rpi = 64 / r.lpr;
+    return r;
 }
 
-constexpr int kColBatch = 4;
+// Work item wi of the GEMV kernels, from the table the dispatch wrote: a routed expert with its pairs at
+// dispatch positions first .. first + ncol, or a chunk of the shared expert's tokens (rows P + t).  Column c
+// reads token tok(c) and writes row first + c of the pair-row buffers.
+struct Item {
+    bool shared;
+    int e, ncol, first, tok0;
+    int tk[4];
+};
+__device__ __forceinline__ bool work_item(const int4* __restrict__ items, int wi, Item& it) {
+    const int4 a = items[2 * wi], b = items[2 * wi + 1];
+    if (a.x == kItemEmpty) return false;
+    it.shared = a.x == kItemShared;
+    it.e = a.x;
+    it.first = a.y;
+    it.ncol = a.z;
+    it.tok0 = a.w;
+    it.tk[0] = a.w;
+    it.tk[1] = b.x;
+    it.tk[2] = b.y;
+    it.tk[3] = b.z;
+    return true;
+}
 
-// ------------------------------------------------------------------------------------------------ gate/up
-// Grid (FF/32, max work items).  Work item wi < n_list: routed expert elist[wi] with its pairs at
-// dispatch positions offsets[e]..offsets[e+1]; wi == n_list (when has_shared): the shared expert with
-// every token.  The block computes gate rows [32 hb, 32 hb + 32) and the same up rows for each column,
-// SwiGLU, and the q8_1 block hb of h, stored at hq[(slot or P + t) * hq_blocks + hb].
-// Row value = ((L_0 + L_1) + ...) over the row's units in order (oracle: or_q2_0_gemv_dev).
-template <int MAXU>
+__device__ __forceinline__ int item_token(const Item& it, const int32_t* perm, int k, int c) {
+    if (it.shared) return it.tok0 + c;
+    if (c < 4) return c == 0 ? it.tk[0] : c == 1 ? it.tk[1] : c == 2 ? it.tk[2] : it.tk[3];
+    return perm[it.first + c] / k;
+}
+
+// Copies the q8_1 images of `nc` columns (qb blocks each) into LDS, 16 bytes per thread per step.
+__device__ __forceinline__ void stage_images(uint32_t* act, const uint32_t* __restrict__ img, int qb, int c0, int nc,
+                                             const Item& it, const int32_t* perm, int k, bool by_token) {
+    const int per_col = qb * (kImgDw / 4);  // uint4 per column
+    for (int idx = threadIdx.x; idx < nc * per_col; idx += 256) {
+        const int c = idx / per_col, r = idx - c * per_col;
+        const int row = by_token ? item_token(it, perm, k, c0 + c) : it.first + c0 + c;
+        reinterpret_cast<uint4*>(act)[idx] = reinterpret_cast<const uint4*>(img)[(size_t)row * per_col + r];
+    }
+}
+
+constexpr int kGuCols = 8;
+
+// Gate/up + SwiGLU + q8_1 image of h.  Grid (Fmax / 32, max work items), 4 waves.  Wave w computes gate rows
+// [32 hb + 8 w, +8) (rows rho 0..7) and the same up rows (rho 8..15); the item's columns are processed in
+// stages of kGuCols: their x images are copied to LDS, every column's row values parked in LDS by the group
+// leaders, then each half wave quantises one column's 32 h values into image block hb.
+template <int NIT, int MAXUPL>
 __global__ __launch_bounds__(256) void k_q2_gu(const uint8_t* __restrict__ gate_exps, const uint8_t* __restrict__ up_exps,
                                                 const uint8_t* __restrict__ gate_sh, const uint8_t* __restrict__ up_sh,
-                                                const uint8_t* __restrict__ xq, const int32_t* __restrict__ offsets,
-                                                const int32_t* __restrict__ perm, const int32_t* __restrict__ elist,
-                                                const int32_t* __restrict__ n_list, int k, int T, int H, int F, int Fs,
-                                                int has_shared, int P, uint8_t* __restrict__ hq, int hq_blocks) {
+                                                const uint32_t* __restrict__ ximg, const int4* __restrict__ items,
+                                                const int32_t* __restrict__ perm, int k, int H, int F, int Fs,
+                                                uint32_t* __restrict__ himg, int h_blocks) {
     extern __shared__ __align__(16) uint32_t smem[];
+    __shared__ float rowv[kGuCols][64];
+    __shared__ uint8_t qsc[8][32];
+    Item item;
+    if (!work_item(items, blockIdx.y, item)) return;
     const int hb = blockIdx.x;
-    const int wi = blockIdx.y;
-    const int nl = *n_list;
-    const bool shared = has_shared && wi == nl;
-    if (wi > nl || (wi == nl && !shared)) return;
-    const int Fe = shared ? Fs : F;
+    const int Fe = item.shared ? Fs : F;
     if (hb * 32 >= Fe) return;
-    const int e = shared ? -1 : elist[wi];
-    const int dpr = H >> 7;
-    const size_t rb = (size_t)dpr * 36;
-    const uint8_t* g0 = shared ? gate_sh : gate_exps + (size_t)e * F * rb;
-    const uint8_t* u0 = shared ? up_sh : up_exps + (size_t)e * F * rb;
-    g0 += (size_t)hb * 32 * rb;
-    u0 += (size_t)hb * 32 * rb;
-    const int half_units = 32 * dpr;
-    const int nunits = 2 * half_units;
+    const RowGeo G = row_geo(H);
+    const size_t rb = (size_t)G.dpr * 36;
+    const uint8_t* g0 = item.shared ? gate_sh : gate_exps + (size_t)item.e * F * rb;
+    const uint8_t* u0 = item.shared ? up_sh : up_exps + (size_t)item.e * F * rb;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int grp = lane / G.lpr, l = lane - grp * G.lpr;
+    const int qb = H >> 5;
 
-    uint32_t w[MAXU][9];
+    uint32_t w[NIT][MAXUPL][9];
+    bool live[NIT];
 #pragma unroll
-    for (int j = 0; j < MAXU; ++j) {
-        const int u = threadIdx.x + 256 * j;
-        if (u < nunits) load_unit(u < half_units ? g0 + (size_t)u * 36 : u0 + (size_t)(u - half_units) * 36, w[j]);
+    for (int it = 0; it < NIT; ++it) {
+        const int rho = it * G.rpi + grp;  // 0..15 within the wave
+        live[it] = rho < 16;
+        const int r = 32 * hb + 8 * wave + (rho & 7);
+        const uint8_t* rowp = (rho < 8 ? g0 : u0) + (size_t)r * rb;
+#pragma unroll
+        for (int m = 0; m < MAXUPL; ++m)
+            if (live[it] && m < G.upl) load_unit(rowp + (size_t)(l + G.lpr * m) * 36, w[it][m]);
     }
 
-    Cols cs;
-    if (shared) cs = Cols{T, 0, nullptr, k};
-    else cs = Cols{offsets[e + 1] - offsets[e], offsets[e], perm, k};
-
-    const int qb_per_col = H >> 5;
-    const int lp_stride = dpr + 1;
-    uint32_t* act = smem;                                         // kColBatch * qb_per_col * kActDw
-    float* lp = reinterpret_cast<float*>(act + kColBatch * qb_per_col * kActDw);  // kColBatch * 64 * lp_stride
-    float* gu = lp + kColBatch * 64 * lp_stride;                  // kColBatch * 64
-
-    for (int c0 = 0; c0 < cs.n; c0 += kColBatch) {
-        const int nb = min(kColBatch, cs.n - c0);
-        for (int idx = threadIdx.x; idx < nb * qb_per_col; idx += 256) {
-            const int c = idx / qb_per_col, qb = idx - c * qb_per_col;
-            const int tok = col_token(cs, c0 + c);
-            stage_q8(reinterpret_cast<const uint32_t*>(xq + ((size_t)tok * qb_per_col + qb) * 36),
-                     act + (c * qb_per_col + qb) * kActDw);
-        }
+    for (int c0 = 0; c0 < item.ncol; c0 += kGuCols) {
+        const int nc = min(kGuCols, item.ncol - c0);
+        stage_images(smem, ximg, qb, c0, nc, item, perm, k, true);
         __syncthreads();
+        for (int c = 0; c < nc; ++c) {
+            const uint32_t* xt = smem + (size_t)c * qb * kImgDw;
+            pin_units(w);
+            float acc[NIT];
 #pragma unroll
-        for (int j = 0; j < MAXU; ++j) {
-            const int u = threadIdx.x + 256 * j;
-            if (u < nunits) {
-                const int r = u / dpr, g = u - r * dpr;
-                for (int c = 0; c < nb; ++c)
-                    lp[(c * 64 + r) * lp_stride + g] = q2_unit_dot(w[j], act + (c * qb_per_col + 4 * g) * kActDw);
+            for (int m = 0; m < MAXUPL; ++m) {
+                if (m < G.upl) {
+                    Act4 a;
+                    load_act_img(xt + (size_t)(4 * (l + G.lpr * m)) * kImgDw, a);
+#pragma unroll
+                    for (int it = 0; it < NIT; ++it) {
+                        const float L = q2_unit_dot(w[it][m], a);
+                        acc[it] = m == 0 ? L : acc[it] + L;
+                    }
+                }
+            }
+#pragma unroll
+            for (int it = 0; it < NIT; ++it) {
+                const float v = group_sum(acc[it], G.lpr);
+                const int rho = it * G.rpi + grp;
+                if (live[it] && l == 0) rowv[c][(rho < 8 ? 0 : 32) + 8 * wave + (rho & 7)] = v;
             }
         }
         __syncthreads();
         {
-            const int c = threadIdx.x >> 6, r = threadIdx.x & 63;
-            if (c < nb) {
-                const float* s = lp + (c * 64 + r) * lp_stride;
-                float acc = s[0];
-                for (int g = 1; g < dpr; ++g) acc = acc + s[g];
-                gu[c * 64 + r] = acc;
-            }
+            const int hw = threadIdx.x >> 5;  // half wave = column
+            const bool live_c = hw < nc;
+            const int i = lane & 31;
+            const float h = live_c ? silu_mul(rowv[hw][i], rowv[hw][32 + i]) : 0.0f;
+            const int row = item.first + c0 + (live_c ? hw : 0);
+            q8_image_store(h, live_c, qsc[hw], himg + ((size_t)row * h_blocks + hb) * kImgDw);
         }
         __syncthreads();
-        {
-            const int c = threadIdx.x >> 6, l = threadIdx.x & 63;
-            if (c < nb) {
-                const float h = l < 32 ? silu_mul(gu[c * 64 + l], gu[c * 64 + 32 + l]) : 0.0f;
-                uint32_t ds;
-                const int q = q8_1_value(h, &ds);
-                const int row = shared ? P + (c0 + c) : cs.first + c0 + c;
-                if (l < 32) q8_1_store(q, ds, hq + ((size_t)row * hq_blocks + hb) * 36);
+    }
+}
+
+// Down rows.  Grid (ceil(H / rows per block), max work items), 4 waves; a wave owns NIT passes of rpi rows.
+// The item's h images are copied to LDS `cps` columns at a time; each group leader writes its row's value to
+// Y[first + c][row] (the shared rows times sigmoid(sg[t])).
+template <int NIT, int MAXUPL>
+__global__ __launch_bounds__(256) void k_q2_down(const uint8_t* __restrict__ down_exps, const uint8_t* __restrict__ down_sh,
+                                                  const uint32_t* __restrict__ himg, int h_blocks, const float* __restrict__ sg,
+                                                  const int4* __restrict__ items, int H, int F, int Fs, int cps,
+                                                  float* __restrict__ Y) {
+    extern __shared__ __align__(16) uint32_t smem[];
+    Item item;
+    if (!work_item(items, blockIdx.y, item)) return;
+    const int Fe = item.shared ? Fs : F;
+    const RowGeo G = row_geo(Fe);
+    const int rpw = NIT * G.rpi;  // rows per wave
+    const size_t rb = (size_t)G.dpr * 36;
+    const uint8_t* base = item.shared ? down_sh : down_exps + (size_t)item.e * H * ((size_t)(F >> 7) * 36);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int grp = lane / G.lpr, l = lane - grp * G.lpr;
+    const int row0 = blockIdx.x * 4 * rpw + wave * rpw;
+
+    uint32_t w[NIT][MAXUPL][9];
+    bool live[NIT];
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+        const int r = row0 + it * G.rpi + grp;
+        live[it] = r < H;
+#pragma unroll
+        for (int m = 0; m < MAXUPL; ++m)
+            if (live[it] && m < G.upl) load_unit(base + (size_t)r * rb + (size_t)(l + G.lpr * m) * 36, w[it][m]);
+    }
+    for (int c0 = 0; c0 < item.ncol; c0 += cps) {
+        const int nc = min(cps, item.ncol - c0);
+        stage_images(smem, himg, h_blocks, c0, nc, item, nullptr, 1, false);
+        __syncthreads();
+        for (int c = 0; c < nc; ++c) {
+            const uint32_t* ht = smem + (size_t)c * h_blocks * kImgDw;
+            pin_units(w);
+            float acc[NIT];
+#pragma unroll
+            for (int m = 0; m < MAXUPL; ++m) {
+                if (m < G.upl) {
+                    Act4 a;
+                    load_act_img(ht + (size_t)(4 * (l + G.lpr * m)) * kImgDw, a);
+#pragma unroll
+                    for (int it = 0; it < NIT; ++it) {
+                        const float L = q2_unit_dot(w[it][m], a);
+                        acc[it] = m == 0 ? L : acc[it] + L;
+                    }
+                }
+            }
+            const float sig = item.shared ? sigmoid(sg[item.tok0 + c0 + c]) : 1.0f;
+#pragma unroll
+            for (int it = 0; it < NIT; ++it) {
+                float v = group_sum(acc[it], G.lpr);
+                if (item.shared) v = v * sig;
+                const int r = row0 + it * G.rpi + grp;
+                if (live[it] && l == 0) Y[(size_t)(item.first + c0 + c) * H + r] = v;
             }
         }
         __syncthreads();
     }
 }
 
-// ------------------------------------------------------------------------------------------------ down
-// Grid (H/64, max work items).  Rows [64 bx, 64 bx + 64) of the work item's down matrix against each
-// column's q8_1 h; the shared rows are multiplied by sigmoid(sg[t]) (metal/shaders/shared_expert.metal:24-32).
-template <int MAXU>
-__global__ __launch_bounds__(256) void k_q2_down(const uint8_t* __restrict__ down_exps, const uint8_t* __restrict__ down_sh,
-                                                  const uint8_t* __restrict__ hq, int hq_blocks, const float* __restrict__ sg,
-                                                  const int32_t* __restrict__ offsets, const int32_t* __restrict__ elist,
-                                                  const int32_t* __restrict__ n_list, int T, int H, int F, int Fs,
-                                                  int has_shared, int P, float* __restrict__ Y) {
-    extern __shared__ __align__(16) uint32_t smem[];
-    const int bx = blockIdx.x;
-    const int wi = blockIdx.y;
-    const int nl = *n_list;
-    const bool shared = has_shared && wi == nl;
-    if (wi > nl || (wi == nl && !shared)) return;
-    const int Fe = shared ? Fs : F;
-    const int e = shared ? -1 : elist[wi];
-    const int dpr = Fe >> 7;
-    const size_t rb = (size_t)dpr * 36;
-    const uint8_t* base = (shared ? down_sh : down_exps + (size_t)e * H * ((size_t)(F >> 7) * 36)) + (size_t)bx * 64 * rb;
-    const int nrows = min(64, H - bx * 64);
-    const int nunits = nrows * dpr;
-
-    uint32_t w[MAXU][9];
+// Generic Q2_0 GEMV over n_col columns of standard q8_1 activations (iq_mmvq's contract, metal/src/iq.mm:148-169).
+// Grid (ceil(n_out / rows per block)); same unit and lane order as the expert kernels.
+template <int NIT, int MAXUPL>
+__global__ __launch_bounds__(256) void k_q2_mmvq(const uint8_t* __restrict__ w, const uint8_t* __restrict__ xq, int n_in,
+                                                  int n_out, int n_col, float* __restrict__ y) {
+    const RowGeo G = row_geo(n_in);
+    const int rpw = NIT * G.rpi;
+    const size_t rb = (size_t)G.dpr * 36;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int grp = lane / G.lpr, l = lane - grp * G.lpr;
+    const int row0 = blockIdx.x * 4 * rpw + wave * rpw;
+    uint32_t wr[NIT][MAXUPL][9];
+    bool live[NIT];
 #pragma unroll
-    for (int j = 0; j < MAXU; ++j) {
-        const int u = threadIdx.x + 256 * j;
-        if (u < nunits) load_unit(base + (size_t)u * 36, w[j]);
+    for (int it = 0; it < NIT; ++it) {
+        const int r = row0 + it * G.rpi + grp;
+        live[it] = r < n_out;
+#pragma unroll
+        for (int m = 0; m < MAXUPL; ++m)
+            if (live[it] && m < G.upl) load_unit(w + (size_t)r * rb + (size_t)(l + G.lpr * m) * 36, wr[it][m]);
     }
-    const int ncol = shared ? T : offsets[e + 1] - offsets[e];
-    const int first = shared ? P : offsets[e];
-
-    const int qb_per_col = Fe >> 5;
-    const int lp_stride = dpr + 1;
-    uint32_t* act = smem;
-    float* lp = reinterpret_cast<float*>(act + kColBatch * qb_per_col * kActDw);
-
-    for (int c0 = 0; c0 < ncol; c0 += kColBatch) {
-        const int nb = min(kColBatch, ncol - c0);
-        for (int idx = threadIdx.x; idx < nb * qb_per_col; idx += 256) {
-            const int c = idx / qb_per_col, qb = idx - c * qb_per_col;
-            stage_q8(reinterpret_cast<const uint32_t*>(hq + ((size_t)(first + c0 + c) * hq_blocks + qb) * 36),
-                     act + (c * qb_per_col + qb) * kActDw);
-        }
-        __syncthreads();
+    const int xb = n_in >> 5;
+    for (int c = 0; c < n_col; ++c) {
+        pin_units(wr);
+        float acc[NIT];
 #pragma unroll
-        for (int j = 0; j < MAXU; ++j) {
-            const int u = threadIdx.x + 256 * j;
-            if (u < nunits) {
-                const int r = u / dpr, g = u - r * dpr;
-                for (int c = 0; c < nb; ++c)
-                    lp[(c * 64 + r) * lp_stride + g] = q2_unit_dot(w[j], act + (c * qb_per_col + 4 * g) * kActDw);
+        for (int m = 0; m < MAXUPL; ++m) {
+            if (m < G.upl) {
+                Act4 a;
+                load_act_std(xq + ((size_t)c * xb + 4 * (l + G.lpr * m)) * 36, a);
+#pragma unroll
+                for (int it = 0; it < NIT; ++it) {
+                    const float L = q2_unit_dot(wr[it][m], a);
+                    acc[it] = m == 0 ? L : acc[it] + L;
+                }
             }
         }
-        __syncthreads();
-        {
-            const int c = threadIdx.x >> 6, r = threadIdx.x & 63;
-            if (c < nb && r < nrows) {
-                const float* s = lp + (c * 64 + r) * lp_stride;
-                float acc = s[0];
-                for (int g = 1; g < dpr; ++g) acc = acc + s[g];
-                const int yrow = first + c0 + c;
-                if (shared) acc = acc * sigmoid(sg[c0 + c]);
-                Y[(size_t)yrow * H + bx * 64 + r] = acc;
-            }
+#pragma unroll
+        for (int it = 0; it < NIT; ++it) {
+            const float v = group_sum(acc[it], G.lpr);
+            const int r = row0 + it * G.rpi + grp;
+            if (live[it] && l == 0) y[(size_t)c * n_out + r] = v;
         }
-        __syncthreads();
     }
 }
 
@@ -524,15 +876,15 @@ __global__ __launch_bounds__(256) void k_q2_down(const uint8_t* __restrict__ dow
 __global__ __launch_bounds__(256) void k_combine(const float* __restrict__ Y, const int32_t* __restrict__ slot,
                                                   const float* __restrict__ wts, int k, int H, int P, int add_shared,
                                                   float* __restrict__ y) {
-    const int t = blockIdx.y;
-    const int j = blockIdx.x * 256 + threadIdx.x;
-    if (j >= H) return;
+    const int t = blockIdx.x;
     const int32_t* sl = slot + (size_t)t * k;
     const float* wt = wts + (size_t)t * k;
-    float acc = wt[0] * Y[(size_t)sl[0] * H + j];
-    for (int s = 1; s < k; ++s) acc = __builtin_fmaf(wt[s], Y[(size_t)sl[s] * H + j], acc);
-    if (add_shared) acc = acc + Y[(size_t)(P + t) * H + j];
-    y[(size_t)t * H + j] = acc;
+    for (int j = blockIdx.y * 256 + threadIdx.x; j < H; j += gridDim.y * 256) {
+        float acc = wt[0] * Y[(size_t)sl[0] * H + j];
+        for (int s = 1; s < k; ++s) acc = __builtin_fmaf(wt[s], Y[(size_t)sl[s] * H + j], acc);
+        if (add_shared) acc = acc + Y[(size_t)(P + t) * H + j];
+        y[(size_t)t * H + j] = acc;
+    }
 }
 
 // One token, parts contiguous [k][n] (the reference's moe_combine call shape).
@@ -547,7 +899,22 @@ __global__ __launch_bounds__(256) void k_combine_parts(const float* __restrict__
     y[j] = acc;
 }
 
-// SwiGLU + q8_1 over a flat vector (n % 32 == 0).
+// ------------------------------------------------------------------------------------------------ q8_1 (stage API)
+// x -> standard q8_1 blocks and/or bf16 bits, one thread per element, a q8_1 block per half wave.
+__global__ __launch_bounds__(256) void k_prep(const float* __restrict__ x, int64_t n, uint8_t* __restrict__ xq,
+                                               uint16_t* __restrict__ xb) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const bool live = i < n;
+    const float v = live ? x[i] : 0.0f;
+    if (xb && live) xb[i] = (uint16_t)f32_to_bf16(v);
+    if (xq) {
+        uint32_t ds;
+        const int q = q8_1_value(v, &ds);
+        if ((i - (threadIdx.x & 31)) < n) q8_1_store(q, ds, xq + (i >> 5) * 36);
+    }
+}
+
+// SwiGLU + standard q8_1 over a flat vector (n % 32 == 0).
 __global__ __launch_bounds__(256) void k_swiglu_q8(const float* __restrict__ gate, const float* __restrict__ up,
                                                     int64_t n, uint8_t* __restrict__ y) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -558,81 +925,65 @@ __global__ __launch_bounds__(256) void k_swiglu_q8(const float* __restrict__ gat
     if ((i - (threadIdx.x & 31)) < n) q8_1_store(q, ds, y + (i >> 5) * 36);
 }
 
-// Generic Q2_0 GEMV over n_col columns of q8_1 activations (iq_mmvq's contract, metal/src/iq.mm:148-169):
-// grid (ceil(n_out / 64), 1); same unit order as the expert kernels.
-template <int MAXU>
-__global__ __launch_bounds__(256) void k_q2_mmvq(const uint8_t* __restrict__ w, const uint8_t* __restrict__ xq, int n_in,
-                                                  int n_out, int n_col, float* __restrict__ y) {
-    extern __shared__ __align__(16) uint32_t smem[];
-    const int bx = blockIdx.x;
-    const int dpr = n_in >> 7;
-    const size_t rb = (size_t)dpr * 36;
-    const uint8_t* base = w + (size_t)bx * 64 * rb;
-    const int nrows = min(64, n_out - bx * 64);
-    const int nunits = nrows * dpr;
-    uint32_t wr[MAXU][9];
-#pragma unroll
-    for (int j = 0; j < MAXU; ++j) {
-        const int u = threadIdx.x + 256 * j;
-        if (u < nunits) load_unit(base + (size_t)u * 36, wr[j]);
-    }
-    const int qb_per_col = n_in >> 5;
-    const int lp_stride = dpr + 1;
-    uint32_t* act = smem;
-    float* lp = reinterpret_cast<float*>(act + kColBatch * qb_per_col * kActDw);
-    for (int c0 = 0; c0 < n_col; c0 += kColBatch) {
-        const int nb = min(kColBatch, n_col - c0);
-        for (int idx = threadIdx.x; idx < nb * qb_per_col; idx += 256) {
-            const int c = idx / qb_per_col, qb = idx - c * qb_per_col;
-            stage_q8(reinterpret_cast<const uint32_t*>(xq + ((size_t)(c0 + c) * qb_per_col + qb) * 36),
-                     act + (c * qb_per_col + qb) * kActDw);
-        }
-        __syncthreads();
-#pragma unroll
-        for (int j = 0; j < MAXU; ++j) {
-            const int u = threadIdx.x + 256 * j;
-            if (u < nunits) {
-                const int r = u / dpr, g = u - r * dpr;
-                for (int c = 0; c < nb; ++c)
-                    lp[(c * 64 + r) * lp_stride + g] = q2_unit_dot(wr[j], act + (c * qb_per_col + 4 * g) * kActDw);
-            }
-        }
-        __syncthreads();
-        {
-            const int c = threadIdx.x >> 6, r = threadIdx.x & 63;
-            if (c < nb && r < nrows) {
-                const float* s = lp + (c * 64 + r) * lp_stride;
-                float acc = s[0];
-                for (int g = 1; g < dpr; ++g) acc = acc + s[g];
-                y[(size_t)(c0 + c) * n_out + bx * 64 + r] = acc;
-            }
-        }
-        __syncthreads();
-    }
-}
-
 // ------------------------------------------------------------------------------------------------ launchers
 
-size_t gemv_lds_bytes(int n_in) {
-    const int dpr = n_in >> 7;
-    return (size_t)kColBatch * (n_in >> 5) * kActDw * 4 + (size_t)kColBatch * 64 * (dpr + 1) * 4 + kColBatch * 64 * 4;
+namespace {
+int lanes_per_row_host(int dpr) {
+    const int l = dpr & -dpr;
+    return l > 16 ? 16 : l;
+}
+// gate/up kernel: passes per wave (16 rows per wave), units per lane
+void gu_shape(int n_in, int& nit, int& upl) {
+    const int dpr = n_in >> 7, lpr = lanes_per_row_host(dpr);
+    upl = dpr / lpr;
+    nit = lpr >= 4 ? lpr / 4 : 1;
+}
+// row kernels: passes per wave (at least 16 rows per wave), units per lane, rows per wave
+void rows_shape(int n_in, int& nit, int& upl, int& rpw) {
+    const int dpr = n_in >> 7, lpr = lanes_per_row_host(dpr);
+    upl = dpr / lpr;
+    const int rpi = 64 / lpr;
+    nit = rpi >= 16 ? 1 : 16 / rpi;
+    rpw = nit * rpi;
+}
+}  // namespace
+
+bool gemv_shape_ok(int n_in) {
+    if (n_in <= 0 || n_in % 128) return false;
+    int nit, upl;
+    gu_shape(n_in, nit, upl);
+    return upl <= 8 && nit <= 4;
 }
 
+bool down_shapes_match(int F, int Fs) {
+    int a, b, c, d, e, f;
+    rows_shape(F, a, b, c);
+    rows_shape(Fs, d, e, f);
+    return a == d && b == e;
+}
+
+size_t img_bytes(int64_t n_blocks) { return (size_t)n_blocks * kImgDw * 4; }
+
 hipError_t launch_prep(const float* x, int64_t n, uint8_t* xq, uint16_t* xb, hipStream_t s) {
-    const unsigned blocks = (unsigned)((n + 255) / 256);
-    hipLaunchKernelGGL(k_prep, dim3(blocks), dim3(256), 0, s, x, n, xq, xb);
+    hipLaunchKernelGGL(k_prep, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, n, xq, xb);
     return hipGetLastError();
 }
 
-hipError_t launch_router(const uint16_t* xb, const uint16_t* W, const uint16_t* w_inp, const float* bias, int H, int E,
-                         int rows_total, int T, float* logits, int ld_logits, float* sg, hipStream_t s) {
+hipError_t launch_router(const float* xf, const uint16_t* xb, const uint16_t* W, const uint16_t* w_inp,
+                         const float* bias, int H, int E, int rows_total, int T, float* logits, int ld_logits, float* sg,
+                         uint32_t* ximg, hipStream_t s) {
     const int chunks = H / 8;
     const int maxc = (chunks + 63) / 64;
-    const int tok_per_block = T <= 16 ? T : 16;
-    dim3 grid((unsigned)((rows_total + 3) / 4), (unsigned)((T + tok_per_block - 1) / tok_per_block));
-#define SMOE_ROUTER(C)                                                                                         \
-    hipLaunchKernelGGL(k_router<C>, grid, dim3(256), 0, s, xb, W, w_inp, bias, H, E, rows_total, T, tok_per_block, \
-                       logits, ld_logits, sg)
+    // tokens staged per block: 4 for decode batches (more blocks, short staging), 16 (<= 64 KiB of bf16) beyond
+    int tile = T <= 64 ? 4 : 32768 / H;
+    if (tile > 16) tile = 16;
+    if (tile > T) tile = T;
+    if (tile < 1) tile = 1;
+    dim3 grid((unsigned)((rows_total + 3) / 4), (unsigned)((T + tile - 1) / tile));
+    const size_t lds = (size_t)tile * H * 2;
+#define SMOE_ROUTER(C)                                                                                          \
+    hipLaunchKernelGGL(k_router<C>, grid, dim3(256), lds, s, xf, xb, W, w_inp, bias, H, E, rows_total, T, tile, \
+                       logits, ld_logits, sg, ximg)
     if (maxc <= 2) SMOE_ROUTER(2);
     else if (maxc <= 4) SMOE_ROUTER(4);
     else if (maxc <= 8) SMOE_ROUTER(8);
@@ -647,53 +998,76 @@ hipError_t launch_topk(const float* logits, int ld_logits, int T, int E, int k, 
 }
 
 hipError_t launch_dispatch(const int32_t* ids, int P, int E, int32_t* counts, int32_t* offsets, int32_t* perm,
-                           int32_t* slot, int32_t* elist, int32_t* n_list, hipStream_t s) {
-    hipLaunchKernelGGL(k_dispatch, dim3(1), dim3(1024), 0, s, ids, P, E, counts, offsets, perm, slot, elist, n_list);
+                           int32_t* slot, int32_t* elist, int32_t* n_list, int4* items, int max_items, int T, int k,
+                           int has_shared, hipStream_t s) {
+    hipLaunchKernelGGL(k_dispatch, dim3(1), dim3(1024), 0, s, ids, P, E, counts, offsets, perm, slot, elist, n_list,
+                       items, max_items, T, k, has_shared);
     return hipGetLastError();
 }
 
+hipError_t launch_topk_dispatch(const float* logits, int T, int E, int k, int32_t* ids, float* wts, int32_t* counts,
+                                int32_t* offsets, int32_t* perm, int32_t* slot, int32_t* elist, int32_t* n_list,
+                                int4* items, int max_items, int has_shared, hipStream_t s) {
+    hipLaunchKernelGGL(k_topk_dispatch, dim3(1), dim3(1024), 0, s, logits, T, E, k, ids, wts, counts, offsets, perm,
+                       slot, elist, n_list, items, max_items, has_shared);
+    return hipGetLastError();
+}
+
+int shared_items(int T) { return (T + kShCols - 1) / kShCols; }
+
+hipError_t launch_quant_image(const float* x, int64_t n, uint32_t* img, hipStream_t s) {
+    const int64_t nb = n / 32;
+    hipLaunchKernelGGL(k_quant_image, dim3((unsigned)((nb + 7) / 8)), dim3(256), 0, s, x, n, img);
+    return hipGetLastError();
+}
+
+#define SMOE_SHAPE_DISPATCH(KERNEL_MACRO)              \
+    if (nit == 4 && upl == 1) KERNEL_MACRO(4, 1);      \
+    else if (nit == 4) KERNEL_MACRO(4, 2);             \
+    else if (nit == 2 && upl == 1) KERNEL_MACRO(2, 1); \
+    else if (nit == 2) KERNEL_MACRO(2, 4);             \
+    else if (upl <= 2) KERNEL_MACRO(1, 2);             \
+    else if (upl <= 4) KERNEL_MACRO(1, 4);             \
+    else KERNEL_MACRO(1, 8);
+
 hipError_t launch_q2_gu(const uint8_t* gate_exps, const uint8_t* up_exps, const uint8_t* gate_sh, const uint8_t* up_sh,
-                        const uint8_t* xq, const int32_t* offsets, const int32_t* perm, const int32_t* elist,
-                        const int32_t* n_list, int k, int T, int H, int F, int Fs, int has_shared, int P, int max_items,
-                        uint8_t* hq, int hq_blocks, hipStream_t s) {
+                        const uint32_t* ximg, const int4* items, const int32_t* perm, int k, int H, int F, int Fs,
+                        int has_shared, int max_items, uint32_t* himg, int h_blocks, hipStream_t s) {
     const int Fmax = has_shared && Fs > F ? Fs : F;
     dim3 grid((unsigned)(Fmax / 32), (unsigned)max_items);
-    const size_t lds = gemv_lds_bytes(H);
-    const int units = 64 * (H >> 7);
-    const int upt = (units + 255) / 256;
-#define SMOE_GU(U)                                                                                                \
-    hipLaunchKernelGGL(k_q2_gu<U>, grid, dim3(256), lds, s, gate_exps, up_exps, gate_sh, up_sh, xq, offsets, perm, \
-                       elist, n_list, k, T, H, F, Fs, has_shared, P, hq, hq_blocks)
-    if (upt <= 2) SMOE_GU(2);
-    else if (upt <= 4) SMOE_GU(4);
-    else if (upt <= 6) SMOE_GU(6);
-    else SMOE_GU(8);
+    int nit, upl;
+    gu_shape(H, nit, upl);
+    const size_t lds = (size_t)kGuCols * (H >> 5) * kImgDw * 4;
+#define SMOE_GU(N, U)                                                                                             \
+    hipLaunchKernelGGL((k_q2_gu<N, U>), grid, dim3(256), lds, s, gate_exps, up_exps, gate_sh, up_sh, ximg, items, perm, \
+                       k, H, F, Fs, himg, h_blocks)
+    SMOE_SHAPE_DISPATCH(SMOE_GU)
 #undef SMOE_GU
     return hipGetLastError();
 }
 
-hipError_t launch_q2_down(const uint8_t* down_exps, const uint8_t* down_sh, const uint8_t* hq, int hq_blocks,
-                          const float* sg, const int32_t* offsets, const int32_t* elist, const int32_t* n_list, int T,
-                          int H, int F, int Fs, int has_shared, int P, int max_items, float* Y, hipStream_t s) {
-    const int Fmax = has_shared && Fs > F ? Fs : F;
-    dim3 grid((unsigned)((H + 63) / 64), (unsigned)max_items);
-    const size_t lds = gemv_lds_bytes(Fmax);
-    const int units = 64 * (Fmax >> 7);
-    const int upt = (units + 255) / 256;
-#define SMOE_DOWN(U)                                                                                          \
-    hipLaunchKernelGGL(k_q2_down<U>, grid, dim3(256), lds, s, down_exps, down_sh, hq, hq_blocks, sg, offsets, \
-                       elist, n_list, T, H, F, Fs, has_shared, P, Y)
-    if (upt <= 1) SMOE_DOWN(1);
-    else if (upt <= 2) SMOE_DOWN(2);
-    else if (upt <= 4) SMOE_DOWN(4);
-    else SMOE_DOWN(8);
+hipError_t launch_q2_down(const uint8_t* down_exps, const uint8_t* down_sh, const uint32_t* himg, int h_blocks,
+                          const float* sg, const int4* items, int H, int F, int Fs, int max_items, float* Y,
+                          hipStream_t s) {
+    int nit, upl, rpw;
+    rows_shape(F, nit, upl, rpw);  // the caller guarantees the shared width has the same row shape
+    dim3 grid((unsigned)((H + 4 * rpw - 1) / (4 * rpw)), (unsigned)max_items);
+    const size_t col_bytes = (size_t)h_blocks * kImgDw * 4;
+    int cps = (int)(24576 / col_bytes);
+    cps = cps < 1 ? 1 : cps > 16 ? 16 : cps;
+    const size_t lds = (size_t)cps * col_bytes;
+#define SMOE_DOWN(N, U)                                                                                            \
+    hipLaunchKernelGGL((k_q2_down<N, U>), grid, dim3(256), lds, s, down_exps, down_sh, himg, h_blocks, sg, items, H, F, \
+                       Fs, cps, Y)
+    SMOE_SHAPE_DISPATCH(SMOE_DOWN)
 #undef SMOE_DOWN
     return hipGetLastError();
 }
 
 hipError_t launch_combine(const float* Y, const int32_t* slot, const float* wts, int k, int H, int P, int T,
                           int add_shared, float* y, hipStream_t s) {
-    dim3 grid((unsigned)((H + 255) / 256), (unsigned)T);
+    const int ychunks = (H + 255) / 256;
+    dim3 grid((unsigned)T, (unsigned)(ychunks < 8 ? ychunks : 8));
     hipLaunchKernelGGL(k_combine, grid, dim3(256), 0, s, Y, slot, wts, k, H, P, add_shared, y);
     return hipGetLastError();
 }
@@ -710,15 +1084,11 @@ hipError_t launch_swiglu_q8(const float* gate, const float* up, int64_t n, uint8
 }
 
 hipError_t launch_q2_mmvq(const uint8_t* w, const uint8_t* xq, int n_in, int n_out, int n_col, float* y, hipStream_t s) {
-    const size_t lds = gemv_lds_bytes(n_in);
-    const int units = 64 * (n_in >> 7);
-    const int upt = (units + 255) / 256;
-    dim3 grid((unsigned)((n_out + 63) / 64));
-#define SMOE_MMVQ(U) hipLaunchKernelGGL(k_q2_mmvq<U>, grid, dim3(256), lds, s, w, xq, n_in, n_out, n_col, y)
-    if (upt <= 1) SMOE_MMVQ(1);
-    else if (upt <= 2) SMOE_MMVQ(2);
-    else if (upt <= 4) SMOE_MMVQ(4);
-    else SMOE_MMVQ(8);
+    int nit, upl, rpw;
+    rows_shape(n_in, nit, upl, rpw);
+    dim3 grid((unsigned)((n_out + 4 * rpw - 1) / (4 * rpw)));
+#define SMOE_MMVQ(N, U) hipLaunchKernelGGL((k_q2_mmvq<N, U>), grid, dim3(256), 0, s, w, xq, n_in, n_out, n_col, y)
+    SMOE_SHAPE_DISPATCH(SMOE_MMVQ)
 #undef SMOE_MMVQ
     return hipGetLastError();
 }

@@ -66,11 +66,10 @@ __device__ __forceinline__ float bf16_to_f32(uint32_t h) { return u2f(h << 16); 
 // e^x: Cody-Waite reduction by ln 2 (split 355/512 + remainder), Taylor polynomial of degree 7 in Horner
 // form with fused multiply-adds, scaled by 2^n.  Inputs below -87 return 0, above 89 return +inf.
 __device__ inline float expf_smoe(float x) {
-    if (x != x) return x;
-    if (x > 89.0f) return __builtin_inff();
-    if (x < -87.0f) return 0.0f;
-    const float n = __builtin_rintf(x * 1.44269504088896341f);
-    float r = __builtin_fmaf(n, -0.693359375f, x);
+    // branch-free: the polynomial runs on a clamped argument and the out-of-range cases are selected after
+    const float xc = __builtin_fminf(__builtin_fmaxf(x, -87.0f), 89.0f);
+    const float n = __builtin_rintf(xc * 1.44269504088896341f);
+    float r = __builtin_fmaf(n, -0.693359375f, xc);
     r = __builtin_fmaf(n, 2.12194440e-4f, r);
     float p = 1.98412698e-4f;
     p = __builtin_fmaf(p, r, 1.38888889e-3f);
@@ -80,7 +79,10 @@ __device__ inline float expf_smoe(float x) {
     p = __builtin_fmaf(p, r, 0.5f);
     p = __builtin_fmaf(p, r, 1.0f);
     p = __builtin_fmaf(p, r, 1.0f);
-    return __builtin_ldexpf(p, (int)n);
+    float e = __builtin_ldexpf(p, (int)n);
+    e = x < -87.0f ? 0.0f : e;
+    e = x > 89.0f ? __builtin_inff() : e;
+    return x != x ? x : e;
 }
 
 // ln x for normal x > 0: x = m 2^e, m in [1/sqrt 2, sqrt 2), ln m = 2 atanh((m-1)/(m+1)) to s^11.

@@ -7,21 +7,29 @@
 
 namespace smoe {
 
-size_t gemv_lds_bytes(int n_in);
+bool gemv_shape_ok(int n_in);           // a row length the GEMV kernels tile (n_in % 128 == 0, <= 8 units per lane)
+bool down_shapes_match(int F, int Fs);   // routed and shared down rows share one launch shape
+size_t img_bytes(int64_t n_blocks);      // bytes of n_blocks q8_1 images
 
 hipError_t launch_prep(const float* x, int64_t n, uint8_t* xq, uint16_t* xb, hipStream_t s);
-hipError_t launch_router(const uint16_t* xb, const uint16_t* W, const uint16_t* w_inp, const float* bias, int H, int E,
-                         int rows_total, int T, float* logits, int ld_logits, float* sg, hipStream_t s);
+hipError_t launch_router(const float* xf, const uint16_t* xb, const uint16_t* W, const uint16_t* w_inp,
+                         const float* bias, int H, int E, int rows_total, int T, float* logits, int ld_logits, float* sg,
+                         uint32_t* ximg, hipStream_t s);
 hipError_t launch_topk(const float* logits, int ld_logits, int T, int E, int k, int32_t* ids, float* wts, hipStream_t s);
 hipError_t launch_dispatch(const int32_t* ids, int P, int E, int32_t* counts, int32_t* offsets, int32_t* perm,
-                           int32_t* slot, int32_t* elist, int32_t* n_list, hipStream_t s);
+                           int32_t* slot, int32_t* elist, int32_t* n_list, int4* items, int max_items, int T, int k,
+                           int has_shared, hipStream_t s);
+hipError_t launch_topk_dispatch(const float* logits, int T, int E, int k, int32_t* ids, float* wts, int32_t* counts,
+                                int32_t* offsets, int32_t* perm, int32_t* slot, int32_t* elist, int32_t* n_list,
+                                int4* items, int max_items, int has_shared, hipStream_t s);
+int shared_items(int T);  // shared-expert work items for T tokens
+hipError_t launch_quant_image(const float* x, int64_t n, uint32_t* img, hipStream_t s);
 hipError_t launch_q2_gu(const uint8_t* gate_exps, const uint8_t* up_exps, const uint8_t* gate_sh, const uint8_t* up_sh,
-                        const uint8_t* xq, const int32_t* offsets, const int32_t* perm, const int32_t* elist,
-                        const int32_t* n_list, int k, int T, int H, int F, int Fs, int has_shared, int P, int max_items,
-                        uint8_t* hq, int hq_blocks, hipStream_t s);
-hipError_t launch_q2_down(const uint8_t* down_exps, const uint8_t* down_sh, const uint8_t* hq, int hq_blocks,
-                          const float* sg, const int32_t* offsets, const int32_t* elist, const int32_t* n_list, int T,
-                          int H, int F, int Fs, int has_shared, int P, int max_items, float* Y, hipStream_t s);
+                        const uint32_t* ximg, const int4* items, const int32_t* perm, int k, int H, int F, int Fs,
+                        int has_shared, int max_items, uint32_t* himg, int h_blocks, hipStream_t s);
+hipError_t launch_q2_down(const uint8_t* down_exps, const uint8_t* down_sh, const uint32_t* himg, int h_blocks,
+                          const float* sg, const int4* items, int H, int F, int Fs, int max_items, float* Y,
+                          hipStream_t s);
 hipError_t launch_combine(const float* Y, const int32_t* slot, const float* wts, int k, int H, int P, int T,
                           int add_shared, float* y, hipStream_t s);
 hipError_t launch_combine_parts(const float* parts, const float* wts, const float* shared, int k, int n, float* y,
