@@ -27,6 +27,7 @@ sys.path.insert(0, ROOT)
 
 METRIC = "MoE-layer tok/s + achieved HBM GB/s vs peak, decode b=1 and prefill 512"
 HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0  # dense bf16 MFMA
 
 
 def _args():
@@ -37,7 +38,9 @@ def _args():
     ap.add_argument("--layers", type=int, default=48)
     ap.add_argument("--tokens", type=int, default=16)
     ap.add_argument("--seed", type=int, default=20261201)
-    ap.add_argument("--no-extra", action="store_true", help="skip the decode b=1 measurement")
+    ap.add_argument("--no-extra", action="store_true", help="skip the decode b=1 and prefill 512 measurements")
+    ap.add_argument("--prefill-layers", type=int, default=8)
+    ap.add_argument("--prefill-steps", type=int, default=24)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     return ap.parse_args()
@@ -50,9 +53,9 @@ def log(*a):
 class Stack:
     """`n_layers` synthetic layers resident on the device, one workspace, a graph per token count."""
 
-    def __init__(self, S, torch, g, n_layers, seed, max_tokens):
+    def __init__(self, S, torch, g, n_layers, seed, max_tokens, logit_bias=None):
         self.S, self.torch, self.g = S, torch, g
-        self.layers = [S.synth_layer(g, seed + l) for l in range(n_layers)]
+        self.layers = [S.synth_layer(g, seed + l, logit_bias=logit_bias) for l in range(n_layers)]
         self.wc = [S._weights_c(w) for w in self.layers]
         self.gc = g.c()
         self.ws_bytes = S.workspace_bytes(g, max_tokens)
@@ -161,6 +164,14 @@ def bytes_model(S, g, T, D):
     return layer, gu, down
 
 
+def prefill_flops(g, T):
+    """Dense FLOPs of one prefill call: every routed pair and shared token through gate, up and down, plus
+    the router (2 * MACs)."""
+    P = T * g.top_k
+    ex = 2 * P * 3 * g.n_embd * g.n_ff + (2 * T * 3 * g.n_embd * g.n_ff_shared if g.sh_type >= 0 else 0)
+    return ex, 2 * T * g.n_embd * (g.n_expert + (1 if g.sh_type >= 0 else 0))
+
+
 def summarize(S, g, T, r, steps):
     import statistics as st
     per_stage = {name: st.fmean(r["stage_ms"][s][i] for s in range(steps)) for i, name in enumerate(S.STAGES)}
@@ -203,6 +214,38 @@ def cpu_baseline(g, T, seed, seconds):
                       f"or_moe_decode_dev, {threads} OpenMP threads, {model}"}
 
 
+def prefill(S, torch, g, a):
+    """512 tokens per call, expert popularity Zipf(1.2) through a seeded logit bias, the MFMA
+    (prefill) contract.  `--prefill-layers` biased layers are resident (their working sets exceed the Infinity
+    Cache together); steps walk through them."""
+    T = 512
+    bias = S.zipf_bias(g.n_expert, 1.2, a.seed)
+    t0 = time.perf_counter()
+    stack = Stack(S, torch, g, a.prefill_layers, a.seed + 1000, T, logit_bias=torch.from_numpy(bias).cuda())
+    log(f"prefill: {a.prefill_layers} Zipf-biased layers resident in {time.perf_counter() - t0:.1f} s")
+    steps = a.prefill_steps
+    r = measure(S, torch, stack, T, steps, max(2, steps // 3), a.seed + 13)
+    m = summarize(S, g, T, r, steps)
+    ex_flops, router_flops = prefill_flops(g, T)
+    st = m["stage_ms_avg"]
+    mm_ms = st["gate_up"] + st["down"]
+    out = {k: m[k] for k in ("ms_per_step", "tok_s", "touched_experts_avg", "layer_bytes_avg", "layer_gbs",
+                             "stage_ms_avg")}
+    out["layer_hbm_frac"] = m["layer_gbs"] / HBM_PEAK_GBS
+    out["expert_flops"] = ex_flops
+    out["router_flops"] = router_flops
+    out["expert_gemm_tflops"] = ex_flops / (mm_ms * 1e-3) / 1e12
+    out["expert_gemm_mfma_frac"] = out["expert_gemm_tflops"] / BF16_PEAK_TFLOPS
+    out["layer_tflops"] = (ex_flops + router_flops) / (m["ms_per_step"] * 1e-3) / 1e12
+    log("prefill 512: %.3f ms/step, %.0f tok/s, layer %.0f GB/s, expert GEMMs %.0f TFLOP/s (%.1f%% of bf16 peak), "
+        "touched %.0f, stages(us) %s" % (m["ms_per_step"], m["tok_s"], m["layer_gbs"], out["expert_gemm_tflops"],
+                                          100 * out["expert_gemm_mfma_frac"], m["touched_experts_avg"],
+                                          {k: round(v * 1e3, 1) for k, v in st.items()}))
+    del stack
+    torch.cuda.empty_cache()
+    return out
+
+
 def main():
     a = _args()
     if a.gpus != 1:
@@ -233,6 +276,7 @@ def main():
         extra["decode_b1"] = {k: m1[k] for k in ("ms_per_step", "tok_s", "touched_experts_avg", "layer_bytes_avg",
                                                  "layer_gbs", "stage_ms_avg", "gate_up_gbs", "down_gbs")}
         extra["decode_b1"]["layer_hbm_frac"] = m1["layer_gbs"] / HBM_PEAK_GBS
+        extra["prefill_512"] = prefill(S, torch, g, a)
     extra["decode_b16_stages_ms"] = m16["stage_ms_avg"]
     extra["decode_b16_layer_gbs"] = m16["layer_gbs"]
     extra["decode_b16_layer_hbm_frac"] = m16["layer_gbs"] / HBM_PEAK_GBS

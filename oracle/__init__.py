@@ -445,5 +445,5 @@ def rel_l1_rows(got: np.ndarray, want: np.ndarray) -> np.ndarray:
 
 def zipf_bias(n_expert: int, s: float, seed: int, scale: float = 1.0) -> np.ndarray:
     """Logit bias b_e = scale * log(rank_e^-s) over a seeded rank permutation (config 3's Zipf routing)."""
-    ranks = np.argsort(np.argsort(gen_normal(seed, 99, n_expert)))  # a seeded permutation of 0..E-1
+    ranks = np.argsort(np.argsort(gen_normal(seed, 99, n_expert), kind="stable"), kind="stable")  # seeded permutation
     return (scale * (-s) * np.log(ranks.astype(np.float64) + 1.0)).astype(np.float32)

@@ -20,6 +20,8 @@ _LIB = None
 Q2_0 = 42
 IQ2_S = 22
 PATH_AUTO, PATH_GEMV, PATH_MFMA = 0, 1, 2
+MFMA_TOKENS = 128  # SMOE_PATH_AUTO runs the prefill (MFMA) contract from this many tokens on
+MFMA_CHUNK = 64    # columns per MFMA work item
 
 _STATUS = {0: "ok", -1: "invalid argument", -2: "buffer too small", -3: "unsupported ggml type",
            -4: "HIP runtime error", -5: "misaligned pointer", -6: "NULL pointer"}
@@ -182,6 +184,16 @@ def synth_normal(seed: int, stream_id: int, n: int, sigma: float = 1.0, device="
     out = torch.empty(n, dtype=torch.float32, device=device)
     _check(lib().smoe_synth_normal(seed, stream_id, n, sigma, out.data_ptr(), _stream(stream)))
     return out
+
+
+def zipf_bias(n_expert: int, s: float, seed: int, scale: float = 1.0):
+    """Router logit bias b_e = -scale * s * ln(rank_e + 1) over a seeded rank permutation of the experts, so
+    that expert popularity follows Zipf(s) (the prefill benchmark's routing).  The permutation ranks the
+    seeded normals of stream 99, generated on the device; f32 numpy array."""
+    import numpy as np
+    v = synth_normal(seed, 99, n_expert).cpu().numpy()
+    ranks = np.argsort(np.argsort(v, kind="stable"), kind="stable")
+    return (scale * (-s) * np.log(ranks.astype(np.float64) + 1.0)).astype(np.float32)
 
 
 def _weights_c(w: Dict) -> _Weights:

@@ -39,6 +39,8 @@ constexpr int kMaxExpert = 1024;
 constexpr int kMaxK = 64;
 // Up to this many tokens the q8_1 images, top-k and dispatch run as one work-group (k_route).
 constexpr int kFusedRouteTokens = 64;
+// SMOE_PATH_AUTO runs the MFMA (prefill) contract from this many tokens on.
+constexpr int kMfmaTokens = 128;
 
 smoe_status check_geom(const smoe_geom* g) {
     if (!g) return fail(SMOE_ENULL, "geometry is NULL");
@@ -72,13 +74,19 @@ smoe_status check_geom(const smoe_geom* g) {
 
 struct Layout {
     size_t ximg, logits, sg, ids, wts, counts, offsets, perm, slot, elist, nlist, items, himg, Y, total;
-    int h_blocks;
+    int h_blocks;  // q8_1 blocks per h row (GEMV path)
+    int h_rec;     // 64-value records per h row (MFMA path)
 };
 
-// GEMV work items: every touched expert plus the shared expert's token chunks.
-int max_items(const smoe_geom& g, int64_t T) {
+// Work items: every touched expert plus the shared expert's token chunks (GEMV path); the MFMA path splits
+// an expert's pairs and the shared tokens into chunks of mfma_chunk() columns.
+int max_items_gemv(const smoe_geom& g, int64_t T) {
     const int64_t P = T * g.top_k;
     return (int)((P < g.n_expert ? P : g.n_expert) + (g.sh_type >= 0 ? smoe::shared_items((int)T) : 0));
+}
+int max_items_mfma(const smoe_geom& g, int64_t T) {
+    const int64_t P = T * g.top_k, C = smoe::mfma_chunk();
+    return (int)((P < g.n_expert ? P : g.n_expert) + P / C + (g.sh_type >= 0 ? (T + C - 1) / C : 0));
 }
 
 Layout layout(const smoe_geom& g, int64_t T) {
@@ -87,13 +95,16 @@ Layout layout(const smoe_geom& g, int64_t T) {
     const int64_t P = T * K;
     const int64_t Fmax = (g.sh_type >= 0 && g.n_ff_shared > g.n_ff) ? g.n_ff_shared : g.n_ff;
     L.h_blocks = (int)(Fmax / 32);
+    L.h_rec = (int)(Fmax / 64);
     size_t o = 0;
     auto take = [&](size_t bytes) {
         const size_t at = o;
         o = up(o + bytes);
         return at;
     };
-    L.ximg = take(smoe::img_bytes(T * (H / 32)));
+    auto most = [](size_t a, size_t b) { return a > b ? a : b; };
+    // x: q8_1 images (GEMV) or bf16 records (MFMA); h likewise
+    L.ximg = take(most(smoe::img_bytes(T * (H / 32)), smoe::act_rec_bytes(T * (H / 64))));
     L.logits = take((size_t)T * E * 4);
     L.sg = take((size_t)T * 4);
     L.ids = take((size_t)P * 4);
@@ -104,8 +115,8 @@ Layout layout(const smoe_geom& g, int64_t T) {
     L.slot = take((size_t)P * 4);
     L.elist = take((size_t)(E + 1) * 4);
     L.nlist = take(16);
-    L.items = take((size_t)max_items(g, T) * 32);
-    L.himg = take(smoe::img_bytes((P + T) * L.h_blocks));
+    L.items = take((size_t)most(max_items_gemv(g, T), max_items_mfma(g, T)) * 32);
+    L.himg = take(most(smoe::img_bytes((P + T) * L.h_blocks), smoe::act_rec_bytes((P + T) * L.h_rec)));
     L.Y = take((size_t)(P + T) * H * 4);
     L.total = o;
     return L;
@@ -174,7 +185,7 @@ smoe_status smoe_forward_path(const smoe_geom* g, const smoe_weights* w, const f
     if (n_tokens == 0) return ok();  // empty x / y may be NULL: nothing is read or written
     if (!x || !y) return fail(SMOE_ENULL, "x or y is NULL");
     if (!aligned(x, 4) || !aligned(y, 4)) return fail(SMOE_EALIGN, "x and y must be 4-byte aligned");
-    if (path == SMOE_PATH_MFMA) return fail(SMOE_EINVAL, "the MFMA path is not built in this library version");
+    const bool mfma = path == SMOE_PATH_MFMA || (path == SMOE_PATH_AUTO && n_tokens >= kMfmaTokens);
 
     const Layout L = layout(*g, n_tokens);
     if (!workspace) return fail(SMOE_ENULL, "workspace is NULL");
@@ -202,7 +213,9 @@ smoe_status smoe_forward_path(const smoe_geom* g, const smoe_weights* w, const f
     uint32_t* himg = reinterpret_cast<uint32_t*>(ws + L.himg);
     float* Y = reinterpret_cast<float*>(ws + L.Y);
     const hipStream_t st = stream_of(hip_stream);
-    const int n_items = max_items(*g, T);
+    const int n_items = mfma ? max_items_mfma(*g, T) : max_items_gemv(*g, T);
+    const int chunk = mfma ? smoe::mfma_chunk() : (1 << 30);
+    const int sh_chunk = mfma ? smoe::mfma_chunk() : smoe::gemv_shared_chunk();
 
     void* const* ev = trace ? trace->stage_events : nullptr;
     int ev_i = 0;
@@ -218,28 +231,40 @@ smoe_status smoe_forward_path(const smoe_geom* g, const smoe_weights* w, const f
     } while (0)
     SMOE_MARK();
     SMOE_TRY(smoe::launch_router(x, nullptr, static_cast<const uint16_t*>(w->router), has_sh ? w->gate_inp_sh : nullptr,
-                                 w->logit_bias, H, E, E + (has_sh ? 1 : 0), T, logits, E, sg, ximg, st),
+                                 w->logit_bias, H, E, E + (has_sh ? 1 : 0), T, logits, E, sg, mfma ? nullptr : ximg, st),
              "router");
+    if (mfma) SMOE_TRY(smoe::launch_act_records(x, (int64_t)T * (H / 64), ximg, st), "activation records");
     SMOE_MARK();
     if (T <= kFusedRouteTokens) {
         SMOE_TRY(smoe::launch_topk_dispatch(logits, T, E, K, ids, wts, counts, offsets, perm, slot, elist, nlist, items,
-                                            n_items, has_sh ? 1 : 0, st),
+                                            n_items, has_sh ? 1 : 0, chunk, sh_chunk, st),
                  "route");
     } else {
         SMOE_TRY(smoe::launch_topk(logits, E, T, E, K, ids, wts, st), "topk");
         SMOE_TRY(smoe::launch_dispatch(ids, P, E, counts, offsets, perm, slot, elist, nlist, items, n_items, T, K,
-                                       has_sh ? 1 : 0, st),
+                                       has_sh ? 1 : 0, chunk, sh_chunk, st),
                  "dispatch");
     }
     SMOE_MARK();
-    SMOE_TRY(smoe::launch_q2_gu(static_cast<const uint8_t*>(w->gate_exps), static_cast<const uint8_t*>(w->up_exps),
-                                static_cast<const uint8_t*>(w->gate_sh), static_cast<const uint8_t*>(w->up_sh), ximg,
-                                items, perm, K, H, F, Fs, has_sh ? 1 : 0, n_items, himg, L.h_blocks, st),
-             "gate/up");
-    SMOE_MARK();
-    SMOE_TRY(smoe::launch_q2_down(static_cast<const uint8_t*>(w->down_exps), static_cast<const uint8_t*>(w->down_sh),
-                                  himg, L.h_blocks, sg, items, H, F, Fs, n_items, Y, st),
-             "down");
+    const uint8_t* ge = static_cast<const uint8_t*>(w->gate_exps);
+    const uint8_t* ue = static_cast<const uint8_t*>(w->up_exps);
+    const uint8_t* de = static_cast<const uint8_t*>(w->down_exps);
+    const uint8_t* gs = static_cast<const uint8_t*>(w->gate_sh);
+    const uint8_t* us = static_cast<const uint8_t*>(w->up_sh);
+    const uint8_t* ds = static_cast<const uint8_t*>(w->down_sh);
+    if (mfma) {
+        SMOE_TRY(smoe::launch_mm_gu(ge, ue, gs, us, ximg, items, perm, K, H, F, Fs, has_sh ? 1 : 0, n_items, himg,
+                                    L.h_rec, st),
+                 "gate/up");
+        SMOE_MARK();
+        SMOE_TRY(smoe::launch_mm_down(de, ds, himg, L.h_rec, sg, items, H, F, Fs, n_items, Y, st), "down");
+    } else {
+        SMOE_TRY(smoe::launch_q2_gu(ge, ue, gs, us, ximg, items, perm, K, H, F, Fs, has_sh ? 1 : 0, n_items, himg,
+                                    L.h_blocks, st),
+                 "gate/up");
+        SMOE_MARK();
+        SMOE_TRY(smoe::launch_q2_down(de, ds, himg, L.h_blocks, sg, items, H, F, Fs, n_items, Y, st), "down");
+    }
     SMOE_MARK();
     SMOE_TRY(smoe::launch_combine(Y, slot, wts, K, H, P, T, (has_sh && add_shared) ? 1 : 0, y, st), "combine");
     SMOE_MARK();
@@ -345,7 +370,7 @@ smoe_status smoe_dispatch(const int32_t* ids, int32_t n_tokens, int32_t k, int32
     if ((int64_t)n_tokens * k > (1 << 24)) return fail(SMOE_EINVAL, "dispatch: more than 2^24 pairs");
     if (!ids || !offsets || !perm || !slot) return fail(SMOE_ENULL, "dispatch: NULL buffer");
     SMOE_TRY(smoe::launch_dispatch(ids, n_tokens * k, n_expert, counts, offsets, perm, slot, nullptr, nullptr, nullptr,
-                                   0, n_tokens, k, 0, stream_of(hip_stream)),
+                                   0, n_tokens, k, 0, 1 << 30, smoe::gemv_shared_chunk(), stream_of(hip_stream)),
              "dispatch");
     return ok();
 }

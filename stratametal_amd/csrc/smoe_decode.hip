@@ -10,6 +10,7 @@
 //   k_combine  y = routing-weighted sum of the pair rows + the shared row
 // Reduction orders are fixed and restated on the host by the test oracle (oracle/smoe_oracle.c).
 #include "smoe_device.hpp"
+#include "smoe_items.hpp"
 #include "smoe_launch.hpp"
 
 namespace smoe {
@@ -497,22 +498,20 @@ __device__ __forceinline__ int block_exclusive_scan_1024(int v, int* scratch /*>
 struct DispatchLds {
     int cnt[1024];
     int run[1024];
+    int cb[1024];
     int el[1024];
     uint8_t wcnt[16][1024];
     int scan[17];
 };
 
-// Work-item table of the decode GEMV kernels, 8 ints per item (one 32-byte load): routed item wi < n_touched
-// {e, first, ncol, tok0 | tok1, tok2, tok3, 0} (the tokens of its first four pairs), shared-expert chunk
-// {-1, P + t0, ncol, t0 | t0 + 1, t0 + 2, t0 + 3, 0}, unused {-2, ...}.
-constexpr int kShCols = 4;
-constexpr int kItemEmpty = -2, kItemShared = -1;
-
+// With `items`, also the work-item table: expert e's pairs in chunks of at most `chunk` columns (items in
+// ascending expert order), then the shared expert's tokens in chunks of `sh_chunk`, then empty items up to
+// max_items.
 __device__ void dispatch_block(const int32_t* __restrict__ ids, int P, int E, int32_t* __restrict__ counts,
                                int32_t* __restrict__ offsets, int32_t* __restrict__ perm, int32_t* __restrict__ slot,
                                int32_t* __restrict__ elist, int32_t* __restrict__ n_list, DispatchLds& s,
                                int4* __restrict__ items = nullptr, int max_items = 0, int T = 0, int k = 1,
-                               int has_shared = 0) {
+                               int has_shared = 0, int chunk = 1 << 30, int sh_chunk = kShCols) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     s.cnt[tid] = 0;
     for (int w = 0; w < 16; ++w) s.wcnt[w][tid] = 0;
@@ -528,7 +527,11 @@ __device__ void dispatch_block(const int32_t* __restrict__ ids, int P, int E, in
     const int flag = c > 0 ? 1 : 0;
     int n_touched;
     const int fpos = block_exclusive_scan_1024(flag, s.scan, &n_touched);
+    const int nch = c > 0 ? (c - 1) / chunk + 1 : 0;
+    int n_rc;
+    const int cbase = block_exclusive_scan_1024(nch, s.scan, &n_rc);
     if (tid < E) {
+        s.cb[tid] = cbase;
         if (counts) counts[tid] = c;
         offsets[tid] = off;
         s.run[tid] = off;
@@ -573,17 +576,21 @@ __device__ void dispatch_block(const int32_t* __restrict__ ids, int P, int E, in
         __syncthreads();
     }
     if (!items) return;
-    for (int wi = tid; wi < max_items; wi += 1024) {
-        int4 a = make_int4(kItemEmpty, 0, 0, 0), b = make_int4(0, 0, 0, 0);
-        if (wi < n_touched) {
-            const int e = s.el[wi], cnt = s.cnt[e], first = s.run[e] - cnt;  // run[e] ends at offsets[e + 1]
+    if (tid < E && c > 0) {
+        for (int ch = 0; ch < nch; ++ch) {
+            const int first = off + ch * chunk, n = min(chunk, c - ch * chunk);
             int tk[4] = {0, 0, 0, 0};
-            for (int c = 0; c < 4 && c < cnt; ++c) tk[c] = perm[first + c] / k;
-            a = make_int4(e, first, cnt, tk[0]);
-            b = make_int4(tk[1], tk[2], tk[3], 0);
-        } else if (has_shared && (wi - n_touched) * kShCols < T) {
-            const int t0 = (wi - n_touched) * kShCols;
-            a = make_int4(kItemShared, P + t0, min(kShCols, T - t0), t0);
+            for (int j = 0; j < 4 && j < n; ++j) tk[j] = perm[first + j] / k;
+            items[2 * (cbase + ch)] = make_int4(tid, first, n, tk[0]);
+            items[2 * (cbase + ch) + 1] = make_int4(tk[1], tk[2], tk[3], 0);
+        }
+    }
+    const int n_sh = has_shared ? (T + sh_chunk - 1) / sh_chunk : 0;
+    for (int wi = n_rc + tid; wi < max_items; wi += 1024) {
+        int4 a = make_int4(kItemEmpty, 0, 0, 0), b = make_int4(0, 0, 0, 0);
+        if (wi < n_rc + n_sh) {
+            const int t0 = (wi - n_rc) * sh_chunk;
+            a = make_int4(kItemShared, P + t0, min(sh_chunk, T - t0), t0);
             b = make_int4(t0 + 1, t0 + 2, t0 + 3, 0);
         }
         items[2 * wi] = a;
@@ -596,9 +603,10 @@ __global__ __launch_bounds__(1024) void k_dispatch(const int32_t* __restrict__ i
                                                     int32_t* __restrict__ perm, int32_t* __restrict__ slot,
                                                     int32_t* __restrict__ elist, int32_t* __restrict__ n_list,
                                                     int4* __restrict__ items, int max_items, int T, int k,
-                                                    int has_shared) {
+                                                    int has_shared, int chunk, int sh_chunk) {
     __shared__ DispatchLds s;
-    dispatch_block(ids, P, E, counts, offsets, perm, slot, elist, n_list, s, items, max_items, T, k, has_shared);
+    dispatch_block(ids, P, E, counts, offsets, perm, slot, elist, n_list, s, items, max_items, T, k, has_shared, chunk,
+                   sh_chunk);
 }
 
 // ------------------------------------------------------------------------------------------------ route (fused)
@@ -609,12 +617,14 @@ __global__ __launch_bounds__(1024) void k_topk_dispatch(const float* __restrict_
                                                          int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
                                                          int32_t* __restrict__ perm, int32_t* __restrict__ slot,
                                                          int32_t* __restrict__ elist, int32_t* __restrict__ n_list,
-                                                         int4* __restrict__ items, int max_items, int has_shared) {
+                                                         int4* __restrict__ items, int max_items, int has_shared,
+                                                         int chunk, int sh_chunk) {
     __shared__ DispatchLds s;
     const int wave = threadIdx.x >> 6;
     for (int t = wave; t < T; t += 16) route_token(logits + (size_t)t * E, E, k, ids + (size_t)t * k, wts + (size_t)t * k);
     __syncthreads();
-    dispatch_block(ids, T * k, E, counts, offsets, perm, slot, elist, n_list, s, items, max_items, T, k, has_shared);
+    dispatch_block(ids, T * k, E, counts, offsets, perm, slot, elist, n_list, s, items, max_items, T, k, has_shared,
+                   chunk, sh_chunk);
 }
 
 // q8_1 images of a flat f32 vector (n % 32 == 0), one block per half wave.
@@ -639,35 +649,6 @@ __device__ __forceinline__ RowGeo row_geo(int n_in) {
     r.upl = r.dpr / r.lpr;
     r.rpi = 64 / r.lpr;
     return r;
-}
-
-// Work item wi of the GEMV kernels, from the table the dispatch wrote: a routed expert with its pairs at
-// dispatch positions first .. first + ncol, or a chunk of the shared expert's tokens (rows P + t).  Column c
-// reads token tok(c) and writes row first + c of the pair-row buffers.
-struct Item {
-    bool shared;
-    int e, ncol, first, tok0;
-    int tk[4];
-};
-__device__ __forceinline__ bool work_item(const int4* __restrict__ items, int wi, Item& it) {
-    const int4 a = items[2 * wi], b = items[2 * wi + 1];
-    if (a.x == kItemEmpty) return false;
-    it.shared = a.x == kItemShared;
-    it.e = a.x;
-    it.first = a.y;
-    it.ncol = a.z;
-    it.tok0 = a.w;
-    it.tk[0] = a.w;
-    it.tk[1] = b.x;
-    it.tk[2] = b.y;
-    it.tk[3] = b.z;
-    return true;
-}
-
-__device__ __forceinline__ int item_token(const Item& it, const int32_t* perm, int k, int c) {
-    if (it.shared) return it.tok0 + c;
-    if (c < 4) return c == 0 ? it.tk[0] : c == 1 ? it.tk[1] : c == 2 ? it.tk[2] : it.tk[3];
-    return perm[it.first + c] / k;
 }
 
 // Copies the q8_1 images of `nc` columns (qb blocks each) into LDS, 16 bytes per thread per step.
@@ -999,21 +980,22 @@ hipError_t launch_topk(const float* logits, int ld_logits, int T, int E, int k, 
 
 hipError_t launch_dispatch(const int32_t* ids, int P, int E, int32_t* counts, int32_t* offsets, int32_t* perm,
                            int32_t* slot, int32_t* elist, int32_t* n_list, int4* items, int max_items, int T, int k,
-                           int has_shared, hipStream_t s) {
+                           int has_shared, int chunk, int sh_chunk, hipStream_t s) {
     hipLaunchKernelGGL(k_dispatch, dim3(1), dim3(1024), 0, s, ids, P, E, counts, offsets, perm, slot, elist, n_list,
-                       items, max_items, T, k, has_shared);
+                       items, max_items, T, k, has_shared, chunk, sh_chunk);
     return hipGetLastError();
 }
 
 hipError_t launch_topk_dispatch(const float* logits, int T, int E, int k, int32_t* ids, float* wts, int32_t* counts,
                                 int32_t* offsets, int32_t* perm, int32_t* slot, int32_t* elist, int32_t* n_list,
-                                int4* items, int max_items, int has_shared, hipStream_t s) {
+                                int4* items, int max_items, int has_shared, int chunk, int sh_chunk, hipStream_t s) {
     hipLaunchKernelGGL(k_topk_dispatch, dim3(1), dim3(1024), 0, s, logits, T, E, k, ids, wts, counts, offsets, perm,
-                       slot, elist, n_list, items, max_items, has_shared);
+                       slot, elist, n_list, items, max_items, has_shared, chunk, sh_chunk);
     return hipGetLastError();
 }
 
 int shared_items(int T) { return (T + kShCols - 1) / kShCols; }
+int gemv_shared_chunk() { return kShCols; }
 
 hipError_t launch_quant_image(const float* x, int64_t n, uint32_t* img, hipStream_t s) {
     const int64_t nb = n / 32;

@@ -18,11 +18,12 @@ hipError_t launch_router(const float* xf, const uint16_t* xb, const uint16_t* W,
 hipError_t launch_topk(const float* logits, int ld_logits, int T, int E, int k, int32_t* ids, float* wts, hipStream_t s);
 hipError_t launch_dispatch(const int32_t* ids, int P, int E, int32_t* counts, int32_t* offsets, int32_t* perm,
                            int32_t* slot, int32_t* elist, int32_t* n_list, int4* items, int max_items, int T, int k,
-                           int has_shared, hipStream_t s);
+                           int has_shared, int chunk, int sh_chunk, hipStream_t s);
 hipError_t launch_topk_dispatch(const float* logits, int T, int E, int k, int32_t* ids, float* wts, int32_t* counts,
                                 int32_t* offsets, int32_t* perm, int32_t* slot, int32_t* elist, int32_t* n_list,
-                                int4* items, int max_items, int has_shared, hipStream_t s);
-int shared_items(int T);  // shared-expert work items for T tokens
+                                int4* items, int max_items, int has_shared, int chunk, int sh_chunk, hipStream_t s);
+int shared_items(int T);  // shared-expert work items for T tokens (GEMV path)
+int gemv_shared_chunk();   // shared-expert tokens per GEMV work item
 hipError_t launch_quant_image(const float* x, int64_t n, uint32_t* img, hipStream_t s);
 hipError_t launch_q2_gu(const uint8_t* gate_exps, const uint8_t* up_exps, const uint8_t* gate_sh, const uint8_t* up_sh,
                         const uint32_t* ximg, const int4* items, const int32_t* perm, int k, int H, int F, int Fs,
@@ -36,6 +37,17 @@ hipError_t launch_combine_parts(const float* parts, const float* wts, const floa
                                 hipStream_t s);
 hipError_t launch_swiglu_q8(const float* gate, const float* up, int64_t n, uint8_t* y, hipStream_t s);
 hipError_t launch_q2_mmvq(const uint8_t* w, const uint8_t* xq, int n_in, int n_out, int n_col, float* y, hipStream_t s);
+
+// prefill contract (bf16 MFMA)
+int mfma_chunk();                        // tokens per MFMA work item
+size_t act_rec_bytes(int64_t n_rec);     // bytes of n_rec 64-value activation records
+hipError_t launch_act_records(const float* x, int64_t n_rec, uint32_t* rec, hipStream_t s);
+hipError_t launch_mm_gu(const uint8_t* gate_exps, const uint8_t* up_exps, const uint8_t* gate_sh, const uint8_t* up_sh,
+                        const uint32_t* xrec, const int4* items, const int32_t* perm, int k, int H, int F, int Fs,
+                        int has_shared, int max_items, uint32_t* hrec, int h_rec, hipStream_t s);
+hipError_t launch_mm_down(const uint8_t* down_exps, const uint8_t* down_sh, const uint32_t* hrec, int h_rec,
+                          const float* sg, const int4* items, int H, int F, int Fs, int max_items, float* Y,
+                          hipStream_t s);
 
 hipError_t launch_synth_blocks(int type, uint64_t seed, uint64_t stream_id, int64_t n_blocks, float sigma, uint8_t* out,
                                hipStream_t s);

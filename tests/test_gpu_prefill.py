@@ -1,0 +1,144 @@
+"""GPU parity of the prefill contract (bf16 activations, exact Q2_0 block scales, bf16 MFMA with f32
+accumulation), through the C ABI, against the oracle's or_moe_prefill on the same seeded inputs.
+
+Routing (logits, ids, weights) and the dispatch (counts, offsets, perm, slot) are bit-exact; the output is
+within max rel_l1 1e-3 per row (metal/src/pack_parity.cpp:2425-2433; the block's gate), the oracle summing
+each row in double.  Covers the benchmark's Zipf prefill (config 3), an expert hot enough to split into
+several 128-column work items, a shared expert wider than the routed ones, a layer without a shared expert,
+a forced MFMA call below the automatic threshold, and the reference model's H=2560 / F=640 shape."""
+import os
+import sys
+
+import numpy as np
+import pytest
+
+import oracle as O
+import stratametal_amd as S
+
+pytestmark = pytest.mark.gpu
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+GUARD = 16
+TOL = 1e-3  # max rel_l1 per output row
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def torch():
+    import torch as T
+    if not T.cuda.is_available():
+        pytest.skip("no GPU")
+    S.lib()
+    return T
+
+
+def dev(torch, a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(torch, t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def bits(a):
+    a = np.ascontiguousarray(a)
+    return a.view(np.uint32) if a.dtype == np.float32 else a
+
+
+def hot_bias(E, hot, lift=10.0):
+    b = np.zeros(E, np.float32)
+    b[hot] = lift
+    return b
+
+
+CASES = [
+    # name, geometry, T, seed, add_shared, bias, path
+    ("golden small, forced MFMA", dict(n_embd=256, n_ff=128, n_ff_shared=128, n_expert=16, top_k=4), 3, 4242, True,
+     None, S.PATH_MFMA),
+    ("config 3 (prefill 512, Zipf 1.2)", {}, 512, 3, True, "zipf", S.PATH_AUTO),
+    ("hot expert split over 3 items", dict(n_embd=256, n_ff=256, n_ff_shared=128, n_expert=16, top_k=2), 300, 11,
+     True, ("hot", 5), S.PATH_AUTO),
+    ("shared wider than routed", dict(n_embd=512, n_ff=128, n_ff_shared=256, n_expert=32, top_k=4), 130, 12, True,
+     None, S.PATH_AUTO),
+    ("no shared expert", dict(n_embd=512, n_ff=256, sh_type=-1, n_expert=64, top_k=6), 200, 13, True, None,
+     S.PATH_AUTO),
+    ("shared not added", dict(n_embd=512, n_ff=256, n_expert=64, top_k=6), 129, 14, False, None, S.PATH_AUTO),
+    ("reference model shape H=2560 F=640", dict(n_embd=2560, n_ff=640, n_ff_shared=640, n_expert=64, top_k=8), 160,
+     15, True, None, S.PATH_AUTO),
+    ("7 experts top-3, 9 tokens forced", dict(n_embd=256, n_ff=256, n_ff_shared=128, n_expert=7, top_k=3), 9, 8, True,
+     None, S.PATH_MFMA),
+]
+
+_LAYERS = {}
+
+
+def layer(torch, g, seed, bias):
+    key = (tuple(vars(g).values()), seed, None if bias is None else bias.tobytes())
+    if key not in _LAYERS:
+        _LAYERS.clear()
+        w_host = O.make_weights(g, seed, zipf_bias=bias)
+        w_dev = S.synth_layer(S.Geom(**vars(g)), seed, logit_bias=None if bias is None else dev(torch, bias))
+        _LAYERS[key] = (w_host, w_dev)
+    return _LAYERS[key]
+
+
+@pytest.mark.parametrize("case", range(len(CASES)))
+def test_forward_prefill_parity(torch, case):
+    name, gkw, T, seed, add_shared, bias, path = CASES[case]
+    say(f"case: prefill {name} T={T}")
+    g = O.Geom(**gkw)
+    if bias == "zipf":
+        bias = O.zipf_bias(g.n_expert, 1.2, seed)
+    elif isinstance(bias, tuple):
+        bias = hot_bias(g.n_expert, bias[1])
+    w_host, w_dev = layer(torch, g, seed, bias)
+    x = O.gen_normal(seed, 100, T * g.n_embd).reshape(T, g.n_embd)
+    ml = S.MoELayer(S.Geom(**vars(g)), w_dev, max_tokens=T)
+    yg = torch.full((T * g.n_embd + GUARD,), 7.0, dtype=torch.float32, device="cuda")
+    yv = yg[:T * g.n_embd].view(T, g.n_embd)
+    _, tr = ml.forward(dev(torch, x), y=yv, add_shared=add_shared, trace=True, path=path)
+    got = host(torch, yg)
+    assert (got[T * g.n_embd:] == 7.0).all(), "guard words past y were written"
+    y = got[:T * g.n_embd].reshape(T, g.n_embd)
+    want, wtr = O.moe_prefill(g, w_host, x, add_shared=add_shared, trace=True, n_threads=16)
+    for k in ("logits", "ids", "weights", "counts", "offsets", "perm", "slot"):
+        assert np.array_equal(bits(host(torch, tr[k])), bits(wtr[k])), k
+    if g.sh_type >= 0:
+        assert np.array_equal(bits(host(torch, tr["sgate"])), bits(wtr["sgate"]))
+    err = O.rel_l1_rows(y, want)
+    counts = host(torch, tr["counts"])
+    say(f"  max rel_l1 {err.max():.3e} (mean {err.mean():.3e}); hottest expert {counts.max()} pairs")
+    assert err.max() <= TOL
+    if name.startswith("hot"):
+        assert counts.max() > 2 * S.MFMA_CHUNK, "the hot expert does not span three work items"
+    if name.startswith("golden"):
+        f = np.load(os.path.join(GOLD, "layer_prefill.npz"))
+        assert np.array_equal(bits(x), bits(f["x"]))
+        assert O.rel_l1_rows(y, f["y"]).max() <= TOL
+    # determinism: a repeat is bitwise identical
+    y2 = ml.forward(dev(torch, x), add_shared=add_shared, path=path)
+    assert np.array_equal(bits(host(torch, y2)), bits(y))
+
+
+def test_auto_path_switches_at_128_tokens(torch):
+    """SMOE_PATH_AUTO runs the decode contract below 128 tokens and the prefill contract from 128 on."""
+    say("case: automatic path threshold")
+    g = O.Geom(n_embd=256, n_ff=128, n_ff_shared=128, n_expert=16, top_k=4)
+    w_host, w_dev = layer(torch, g, 21, None)
+    x = O.gen_normal(21, 100, 128 * g.n_embd).reshape(128, g.n_embd)
+    ml = S.MoELayer(S.Geom(**vars(g)), w_dev, max_tokens=128)
+    y127 = host(torch, ml.forward(dev(torch, x[:127])))
+    assert np.array_equal(bits(y127), bits(O.moe_decode_dev(g, w_host, x[:127], n_threads=16)))
+    y128 = host(torch, ml.forward(dev(torch, x)))
+    assert O.rel_l1_rows(y128, O.moe_prefill(g, w_host, x, n_threads=16)).max() <= TOL
+    # and the two contracts differ (q8_1 vs bf16 activations), so the switch is observable
+    assert not np.array_equal(bits(y128[:127]), bits(y127))
+
+
+def test_zipf_bias_matches_oracle(torch):
+    say("case: zipf bias generator")
+    assert np.array_equal(S.zipf_bias(512, 1.2, 77), O.zipf_bias(512, 1.2, 77))
