@@ -230,10 +230,11 @@ smoe_status smoe_forward_path(const smoe_geom* g, const smoe_weights* w, const f
         if (_m != SMOE_OK) return _m;        \
     } while (0)
     SMOE_MARK();
-    SMOE_TRY(smoe::launch_router(x, nullptr, static_cast<const uint16_t*>(w->router), has_sh ? w->gate_inp_sh : nullptr,
-                                 w->logit_bias, H, E, E + (has_sh ? 1 : 0), T, logits, E, sg, mfma ? nullptr : ximg, st),
-             "router");
     if (mfma) SMOE_TRY(smoe::launch_act_records(x, (int64_t)T * (H / 64), ximg, st), "activation records");
+    SMOE_TRY(smoe::launch_router(x, nullptr, static_cast<const uint16_t*>(w->router), has_sh ? w->gate_inp_sh : nullptr,
+                                 w->logit_bias, H, E, E + (has_sh ? 1 : 0), T, logits, E, sg, mfma ? nullptr : ximg,
+                                 mfma ? ximg : nullptr, st),
+             "router");
     SMOE_MARK();
     if (T <= kFusedRouteTokens) {
         SMOE_TRY(smoe::launch_topk_dispatch(logits, T, E, K, ids, wts, counts, offsets, perm, slot, elist, nlist, items,
@@ -313,7 +314,7 @@ smoe_status smoe_bf16_gemv(const uint16_t* x, const uint16_t* w, float* y, int32
     if ((int64_t)n_tok * n_in % 2) return fail(SMOE_EINVAL, "bf16_gemv: odd element count");
     if (!aligned(x, 16) || !aligned(w, 16)) return fail(SMOE_EALIGN, "bf16_gemv: x and w must be 16-byte aligned");
     SMOE_TRY(smoe::launch_router(nullptr, x, w, nullptr, nullptr, n_in, n_out, n_out, n_tok, y, n_out, nullptr, nullptr,
-                                 stream_of(hip_stream)),
+                                 nullptr, stream_of(hip_stream)),
              "bf16_gemv");
     return ok();
 }

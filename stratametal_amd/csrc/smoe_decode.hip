@@ -49,6 +49,37 @@ __device__ __forceinline__ float wave_sum_xor_fast(float v) {
     return v;
 }
 
+// wave_sum_xor_fast of N independent values, stage by stage, so that the N exchanges of a stage are in
+// flight together.
+template <int N>
+__device__ __forceinline__ void wave_sum_xor_fast_n(float (&v)[N]) {
+    float t[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) t[i] = __shfl_xor(v[i], 32, kWave);
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = v[i] + t[i];
+#pragma unroll
+    for (int i = 0; i < N; ++i) t[i] = xor_swap<16>(v[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = v[i] + t[i];
+#pragma unroll
+    for (int i = 0; i < N; ++i) t[i] = xor_swap<8>(v[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = v[i] + t[i];
+#pragma unroll
+    for (int i = 0; i < N; ++i) t[i] = xor_swap<4>(v[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = v[i] + t[i];
+#pragma unroll
+    for (int i = 0; i < N; ++i) t[i] = xor_swap<2>(v[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = v[i] + t[i];
+#pragma unroll
+    for (int i = 0; i < N; ++i) t[i] = xor_swap<1>(v[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = v[i] + t[i];
+}
+
 // Wave maxima for order-free reductions: row rotations by DPP (8, 4, 2, 1), then the four row results read
 // into scalars.  The result is uniform.
 __device__ __forceinline__ uint32_t wave_max_u32_fast(uint32_t v) {
@@ -246,13 +277,11 @@ __global__ __launch_bounds__(256) void k_router(const float* __restrict__ xf, co
         if (xf) {
             float4 f[8];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int g = base + u * 256 + threadIdx.x;
+            for (int u = 0; u < 4; ++u) {  // clamped, so that every load issues back to back
+                const int g = min(base + u * 256 + (int)threadIdx.x, n8 - 1);
                 const float4* src = reinterpret_cast<const float4*>(xf + (size_t)t0 * H) + 2 * (size_t)g;
-                if (g < n8) {
-                    f[2 * u] = src[0];
-                    f[2 * u + 1] = src[1];
-                }
+                f[2 * u] = src[0];
+                f[2 * u + 1] = src[1];
             }
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
@@ -299,6 +328,7 @@ __global__ __launch_bounds__(256) void k_router(const float* __restrict__ xf, co
         const int c = lane + 64 * j;
         wv[j] = c < chunks ? *reinterpret_cast<const uint4*>(wr + 8 * c) : make_uint4(0, 0, 0, 0);
     }
+    const float bv = (bias && row < E) ? bias[row] : 0.0f;  // loaded once, outside the token loop
     for (int t = 0; t < nt; t += 4) {  // four tokens at a time: four independent accumulation chains
         const int ng = min(4, nt - t);
         float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -321,16 +351,127 @@ __global__ __launch_bounds__(256) void k_router(const float* __restrict__ xf, co
                 }
             }
         }
+        wave_sum_xor_fast_n<4>(acc);
+        if (lane == 0) {
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            if (g < ng) {
-                const float v = wave_sum_xor_fast(acc[g]);
-                if (lane == 0) {
-                    if (row < E) logits[(size_t)(t0 + t + g) * ld_logits + row] = bias ? v + bias[row] : v;
-                    else sg[t0 + t + g] = v;
+            for (int g = 0; g < 4; ++g) {
+                if (g < ng) {
+                    if (row < E) logits[(size_t)(t0 + t + g) * ld_logits + row] = bias ? acc[g] + bv : acc[g];
+                    else sg[t0 + t + g] = acc[g];
                 }
             }
         }
+    }
+}
+
+constexpr int kRecDwRouter = 36;  // dwords per 64-value activation record (the prefill path's layout)
+
+// Reduce-scatter of 64 per-lane values v[i]: at the stage of distance D (32, 16, ..., 1) a lane keeps the half
+// of its remaining items selected by its bit D and adds the partner's copy of them, so lane l ends with the
+// full sum of item l.  Each item's sum is formed by exactly the additions of the xor butterfly 32..1 (own value
+// plus the partner's at every stage, in that stage order), so it equals wave_sum_xor_fast of that item bit for
+// bit, at 63 exchanges instead of 64 x 6.
+template <int D, int N>
+__device__ __forceinline__ void rs_stage(float* v, int lane) {
+    const bool upper = (lane & D) != 0;
+#pragma unroll
+    for (int i = 0; i < N / 2; ++i) {
+        const float send = upper ? v[i] : v[i + N / 2];
+        float recv;
+        if constexpr (D == 32) recv = __shfl_xor(send, 32, kWave);
+        else recv = xor_swap<D>(send);
+        v[i] = (upper ? v[i + N / 2] : v[i]) + recv;
+    }
+}
+__device__ __forceinline__ float reduce_scatter64(float (&v)[64], int lane) {
+    rs_stage<32, 64>(v, lane);
+    rs_stage<16, 32>(v, lane);
+    rs_stage<8, 16>(v, lane);
+    rs_stage<4, 8>(v, lane);
+    rs_stage<2, 4>(v, lane);
+    rs_stage<1, 2>(v, lane);
+    return v[0];
+}
+
+// The same logits for many tokens (no q8_1 images): a work-group computes 16 rows x 16 tokens, wave w the rows
+// 16 bx + 4 w .. + 3 for all 16 tokens (x staged as bf16 in LDS).  Each lane accumulates its chunks l, l+64,
+// ... of all 64 (token, row) dots in element order (the order of k_router), then one reduce-scatter leaves
+// lane l with the dot of token l / 4, row l % 4: the logits equal k_router's bit for bit.
+// x comes as the prefill path's 64-value activation records (bf16 in MFMA order, 36 dwords each): record
+// chunk ch = 4 s + q holds natural chunk 2 q + s of its block with the element order 0 2 1 3 4 6 5 7.
+template <int MAXC>
+__global__ __launch_bounds__(256) void k_router_tile(const uint32_t* __restrict__ xrec, const uint16_t* __restrict__ W,
+                                                      const uint16_t* __restrict__ w_inp, const float* __restrict__ bias,
+                                                      int H, int E, int rows_total, int T, float* __restrict__ logits,
+                                                      int ld_logits, float* __restrict__ sg) {
+    extern __shared__ __align__(16) uint32_t smem[];
+    const int t0 = blockIdx.y * 16;
+    const int nt = min(16, T - t0);
+    // stage the tile's records (data chunks only) as [token][block][record chunk]; loads clamped to the tile's
+    // last chunk and stores to the buffer's last slot, so that every load issues back to back
+    const int n16 = nt * H / 8, cap = 16 * H / 8;
+    for (int base = 0; base < n16; base += 256 * 8) {
+        uint4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int g = min(base + u * 256 + (int)threadIdx.x, n16 - 1);  // g = (token * H/64 + block) * 8 + ch
+            v[u] = reinterpret_cast<const uint4*>(xrec + (size_t)t0 * (H >> 6) * kRecDwRouter)[(g >> 3) * 9 + (g & 7)];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) reinterpret_cast<uint4*>(smem)[min(base + u * 256 + (int)threadIdx.x, cap - 1)] = v[u];
+    }
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int row0 = blockIdx.x * 16 + wave * 4;
+    const int chunks = H >> 3;
+    const uint16_t* wr[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int row = min(row0 + r, rows_total - 1);
+        wr[r] = row < E ? W + (size_t)row * H : w_inp;
+    }
+    __syncthreads();
+    const uint16_t* xs = reinterpret_cast<const uint16_t*>(smem);
+    float acc[64];
+#pragma unroll
+    for (int i = 0; i < 64; ++i) acc[i] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < MAXC; ++j) {
+        const int c = lane + 64 * j;
+        const bool live = c < chunks;  // only the last chunk round can be partial
+        const int cc = live ? c : chunks - 1;
+        float wf[4][8];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint4 v = *reinterpret_cast<const uint4*>(wr[r] + 8 * cc);
+            const uint32_t q[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                wf[r][2 * e] = live ? u2f(q[e] << 16) : 0.0f;
+                wf[r][2 * e + 1] = live ? u2f(q[e] & 0xFFFF0000u) : 0.0f;
+            }
+        }
+        const int sc = cc & 7, xoff = 64 * (cc >> 3) + 8 * (4 * (sc & 1) + (sc >> 1));  // record position
+#pragma unroll
+        for (int t = 0; t < 16; ++t) {
+            const uint4 xv = *reinterpret_cast<const uint4*>(xs + (size_t)t * H + xoff);
+            // natural element order from the record order 0 2 1 3 4 6 5 7
+            const uint32_t d[4] = {xv.x, xv.y, xv.z, xv.w};
+            float xe[8];
+            xe[0] = u2f(d[0] << 16); xe[1] = u2f(d[1] << 16); xe[2] = u2f(d[0] & 0xFFFF0000u); xe[3] = u2f(d[1] & 0xFFFF0000u);
+            xe[4] = u2f(d[2] << 16); xe[5] = u2f(d[3] << 16); xe[6] = u2f(d[2] & 0xFFFF0000u); xe[7] = u2f(d[3] & 0xFFFF0000u);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float xv_e = live ? xe[e] : 0.0f;  // a lane past the last chunk adds 0 * 0 (acc is never -0)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) acc[4 * t + r] = __builtin_fmaf(xv_e, wf[r][e], acc[4 * t + r]);
+            }
+        }
+    }
+    const float v = reduce_scatter64(acc, lane);
+    const int t = lane >> 2, row = row0 + (lane & 3);
+    if (t < nt && row < rows_total) {
+        if (row < E) logits[(size_t)(t0 + t) * ld_logits + row] = bias ? v + bias[row] : v;
+        else sg[t0 + t] = v;
     }
 }
 
@@ -952,10 +1093,22 @@ hipError_t launch_prep(const float* x, int64_t n, uint8_t* xq, uint16_t* xb, hip
 
 hipError_t launch_router(const float* xf, const uint16_t* xb, const uint16_t* W, const uint16_t* w_inp,
                          const float* bias, int H, int E, int rows_total, int T, float* logits, int ld_logits, float* sg,
-                         uint32_t* ximg, hipStream_t s) {
+                         uint32_t* ximg, const uint32_t* xrec, hipStream_t s) {
     const int chunks = H / 8;
     const int maxc = (chunks + 63) / 64;
     // tokens staged per block: 4 for decode batches (more blocks, short staging), 16 (<= 64 KiB of bf16) beyond
+    if (xrec) {  // many tokens, x given as activation records: row x token tiles
+        const int maxc = (H / 8 + 63) / 64;
+        const size_t lds = (size_t)16 * H * 2;
+#define SMOE_ROUTER_TILE(C)                                                                                        \
+    hipLaunchKernelGGL((k_router_tile<C>), dim3((unsigned)((rows_total + 15) / 16), (unsigned)((T + 15) / 16)),      \
+                       dim3(256), lds, s, xrec, W, w_inp, bias, H, E, rows_total, T, logits, ld_logits, sg)
+        if (maxc <= 2) SMOE_ROUTER_TILE(2);
+        else if (maxc <= 4) SMOE_ROUTER_TILE(4);
+        else SMOE_ROUTER_TILE(8);
+#undef SMOE_ROUTER_TILE
+        return hipGetLastError();
+    }
     int tile = T <= 64 ? 4 : 32768 / H;
     if (tile > 16) tile = 16;
     if (tile > T) tile = T;

@@ -56,10 +56,10 @@ __device__ inline uint32_t f32_to_f16(float f) {
 
 // f32 -> bf16 bits, RNE with NaN quieted (include/strata/kernels/bf16_bits.hpp:37-47).
 __device__ __forceinline__ uint32_t f32_to_bf16(float f) {
-    uint32_t i = f2u(f);
-    if ((i & 0x7FFFFFFFu) > 0x7F800000u) return ((i >> 16) | 64u) & 0xFFFFu;
-    i += ((i >> 16) & 1u) + 0x7FFFu;
-    return i >> 16;
+    const uint32_t i = f2u(f);
+    const uint32_t rounded = (i + ((i >> 16) & 1u) + 0x7FFFu) >> 16;
+    const uint32_t quiet = ((i >> 16) | 64u) & 0xFFFFu;
+    return (i & 0x7FFFFFFFu) > 0x7F800000u ? quiet : rounded;  // a select, no branch
 }
 __device__ __forceinline__ float bf16_to_f32(uint32_t h) { return u2f(h << 16); }
 
