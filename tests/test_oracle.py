@@ -401,3 +401,42 @@ def test_contract_deviation_from_exact_fp64():
     ye = _exact_block(g, w, x, td)
     assert O.rel_l1_rows(yp, ye).max() < 1e-2
     assert O.rel_l1_rows(yd, ye).max() < 6e-2
+
+
+def _prefill_contract_fp64(g, w, x, tr, round_x=True, round_h=True):
+    """The prefill contract evaluated independently in fp64 from the pinned pieces: weights dequantised by
+    or_dequant_q2_0 (pinned against the reference's vectors), activations and h rounded by numpy's bf16 rule
+    (pinned against the reference's codec), SwiGLU and the sigmoid in fp64, the combine in fp64."""
+    H, F, Fs, K = g.n_embd, g.n_ff, g.n_ff_shared, g.top_k
+    deq = lambda b, r, c: O.dequant_q2_0(b).reshape(-1, r, c).astype(np.float64)  # noqa: E731
+    gate, up, down = deq(w.gate_exps, F, H), deq(w.up_exps, F, H), deq(w.down_exps, H, F)
+    gs, us, ds = deq(w.gate_sh, Fs, H)[0], deq(w.up_sh, Fs, H)[0], deq(w.down_sh, H, Fs)[0]
+    b16 = lambda v: O.f32_from_bf16(O.bf16_from_f32(np.asarray(v, np.float32))).astype(np.float64)  # noqa: E731
+    silu = lambda v: v / (1 + np.exp(-v))  # noqa: E731
+    y = np.zeros((x.shape[0], H))
+    for t in range(x.shape[0]):
+        xt = b16(x[t]) if round_x else x[t].astype(np.float64)
+        for s in range(K):
+            e = tr["ids"][t, s]
+            h = silu((gate[e] @ xt).astype(np.float32)) * (up[e] @ xt).astype(np.float32)
+            h = b16(h) if round_h else h
+            y[t] += float(tr["weights"][t, s]) * (down[e] @ h)
+        h = silu((gs @ xt).astype(np.float32)) * (us @ xt).astype(np.float32)
+        h = b16(h) if round_h else h
+        y[t] += (ds @ h) / (1 + np.exp(-float(tr["sgate"][t])))
+    return y
+
+
+def test_prefill_oracle_against_independent_fp64_contract():
+    """or_moe_prefill (the GPU MFMA path's checker) against the contract evaluated in fp64 from pinned pieces:
+    within 1e-5 per row.  Dropping either bf16 rounding (x or h) moves the result by ~1e-3, so both traps are
+    caught; routing is the pinned A5 router."""
+    g = O.Geom(n_embd=512, n_ff=256, n_ff_shared=256, n_expert=32, top_k=4)
+    w = O.make_weights(g, 78)
+    x = O.gen_normal(78, 100, 6 * g.n_embd).reshape(6, g.n_embd)
+    yp, tp = O.moe_prefill(g, w, x, trace=True)
+    want = _prefill_contract_fp64(g, w, x, tp)
+    assert O.rel_l1_rows(yp, want).max() < 1e-5
+    for kw in (dict(round_x=False), dict(round_h=False)):
+        trap = _prefill_contract_fp64(g, w, x, tp, **kw)
+        assert O.rel_l1_rows(yp, trap).max() > 1e-4, kw
