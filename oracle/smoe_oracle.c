@@ -442,22 +442,35 @@ static float iq2s_partial(const uint8_t* blk, const uint8_t* xblk, int ib) {
     return d * (float)sumi;
 }
 
-/* Device order: one lane per block; lane part = ((P_0 + P_1) + ...) + P_7; row = sequential over blocks. */
+/* Device order (stratametal_amd/csrc/smoe_iq2.hip): nb = n_in / 256 blocks per row, one lane per block
+ * (lanes_per_row(nb) lanes, each summing blocks l, l + lpr, ... in order); a block's lane value is
+ * ((P_0 + P_1) + ...) + P_7 over its sub-blocks; the row is the xor butterfly over the lanes, distance
+ * lpr / 2 first. */
 void or_iq2_s_gemv_dev(const uint8_t* w, const uint8_t* xq, int n_in, int n_out, float* y) {
     const int nb = n_in / 256;
+    const int lpr = lanes_per_row(nb);
     const size_t rb = (size_t)nb * 82;
     for (int r = 0; r < n_out; ++r) {
         const uint8_t* row = w + (size_t)r * rb;
-        float acc = 0.0f;
-        for (int b = 0; b < nb; ++b) {
-            float L = 0.0f;
-            for (int ib = 0; ib < 8; ++ib) {
-                const float P = iq2s_partial(row + (size_t)b * 82, xq + (size_t)(8 * b + ib) * 36, ib);
-                L = ib == 0 ? P : L + P;
+        float lane[16];
+        for (int l = 0; l < lpr; ++l) {
+            float A = 0.0f;
+            for (int b = l, m = 0; b < nb; b += lpr, ++m) {
+                float L = 0.0f;
+                for (int ib = 0; ib < 8; ++ib) {
+                    const float P = iq2s_partial(row + (size_t)b * 82, xq + (size_t)(8 * b + ib) * 36, ib);
+                    L = ib == 0 ? P : L + P;
+                }
+                A = m == 0 ? L : A + L;
             }
-            acc = b == 0 ? L : acc + L;
+            lane[l] = A;
         }
-        y[r] = acc;
+        for (int o = lpr / 2; o > 0; o >>= 1) {
+            float nxt[16];
+            for (int l = 0; l < lpr; ++l) nxt[l] = lane[l] + lane[l ^ o];
+            memcpy(lane, nxt, sizeof(float) * (size_t)lpr);
+        }
+        y[r] = lane[0];
     }
 }
 

@@ -48,8 +48,8 @@ smoe_status check_geom(const smoe_geom* g) {
         return fail(SMOE_ETYPE, "routed expert type " + std::to_string(g->w_type) + " is not Q2_0 (42) or IQ2_S (22)");
     if (g->sh_type != -1 && g->sh_type != SMOE_Q2_0 && g->sh_type != SMOE_IQ2_S)
         return fail(SMOE_ETYPE, "shared expert type " + std::to_string(g->sh_type) + " is not Q2_0, IQ2_S or -1");
-    if (g->w_type == SMOE_IQ2_S || g->sh_type == SMOE_IQ2_S)
-        return fail(SMOE_ETYPE, "IQ2_S experts are not built in this library version");
+    if (g->sh_type >= 0 && g->sh_type != g->w_type)
+        return fail(SMOE_ETYPE, "the shared expert's type must equal the routed experts' type (one activation layout)");
     if (g->router_dtype != 0) return fail(SMOE_EINVAL, "router_dtype must be 0 (bf16)");
     if (g->n_expert < 1 || g->n_expert > kMaxExpert) return fail(SMOE_EINVAL, "n_expert must be in 1..1024");
     if (g->top_k < 1 || g->top_k > kMaxK) return fail(SMOE_EINVAL, "top_k must be in 1..64");
@@ -59,15 +59,19 @@ smoe_status check_geom(const smoe_geom* g) {
         return fail(SMOE_EINVAL, "n_embd must be a positive multiple of " + std::to_string(rv) + ", at most 4096");
     if (g->n_ff <= 0 || g->n_ff % rv || g->n_ff > kMaxFF)
         return fail(SMOE_EINVAL, "n_ff must be a positive multiple of " + std::to_string(rv) + ", at most 4096");
-    if (!smoe::gemv_shape_ok(g->n_embd) || !smoe::gemv_shape_ok(g->n_ff))
-        return fail(SMOE_EINVAL, "n_embd / 128 and n_ff / 128 must each be a power of two times at most 8");
-    if (g->sh_type >= 0) {
-        const int rs = row_values(g->sh_type);
-        if (g->n_embd % rs) return fail(SMOE_EINVAL, "n_embd is not a multiple of the shared type's row unit");
-        if (g->n_ff_shared <= 0 || g->n_ff_shared % rs || g->n_ff_shared > kMaxFF)
-            return fail(SMOE_EINVAL, "n_ff_shared must be a positive multiple of " + std::to_string(rs) + ", at most 4096");
-        if (!smoe::down_shapes_match(g->n_ff, g->n_ff_shared))
+    const bool has_sh = g->sh_type >= 0;
+    if (has_sh && (g->n_ff_shared <= 0 || g->n_ff_shared % rv || g->n_ff_shared > kMaxFF))
+        return fail(SMOE_EINVAL, "n_ff_shared must be a positive multiple of " + std::to_string(rv) + ", at most 4096");
+    if (g->w_type == SMOE_Q2_0) {
+        if (!smoe::gemv_shape_ok(g->n_embd) || !smoe::gemv_shape_ok(g->n_ff))
+            return fail(SMOE_EINVAL, "n_embd / 128 and n_ff / 128 must each be a power of two times at most 8");
+        if (has_sh && !smoe::down_shapes_match(g->n_ff, g->n_ff_shared))
             return fail(SMOE_EINVAL, "n_ff_shared must split into down-row units like n_ff (same power-of-two factor)");
+    } else {
+        if (!smoe::iq2_shape_ok(g->n_embd) || !smoe::iq2_shape_ok(g->n_ff))
+            return fail(SMOE_EINVAL, "IQ2_S: n_embd and n_ff must be 512, 1024 or 2048");
+        if (has_sh && g->n_ff_shared != g->n_ff)
+            return fail(SMOE_EINVAL, "IQ2_S: n_ff_shared must equal n_ff");
     }
     return SMOE_OK;
 }
@@ -185,7 +189,9 @@ smoe_status smoe_forward_path(const smoe_geom* g, const smoe_weights* w, const f
     if (n_tokens == 0) return ok();  // empty x / y may be NULL: nothing is read or written
     if (!x || !y) return fail(SMOE_ENULL, "x or y is NULL");
     if (!aligned(x, 4) || !aligned(y, 4)) return fail(SMOE_EALIGN, "x and y must be 4-byte aligned");
-    const bool mfma = path == SMOE_PATH_MFMA || (path == SMOE_PATH_AUTO && n_tokens >= kMfmaTokens);
+    const bool iq2 = g->w_type == SMOE_IQ2_S;
+    if (iq2 && path == SMOE_PATH_MFMA) return fail(SMOE_ETYPE, "the MFMA (prefill) path is built for Q2_0 experts only");
+    const bool mfma = !iq2 && (path == SMOE_PATH_MFMA || (path == SMOE_PATH_AUTO && n_tokens >= kMfmaTokens));
 
     const Layout L = layout(*g, n_tokens);
     if (!workspace) return fail(SMOE_ENULL, "workspace is NULL");
@@ -233,7 +239,7 @@ smoe_status smoe_forward_path(const smoe_geom* g, const smoe_weights* w, const f
     if (mfma) SMOE_TRY(smoe::launch_act_records(x, (int64_t)T * (H / 64), ximg, st), "activation records");
     SMOE_TRY(smoe::launch_router(x, nullptr, static_cast<const uint16_t*>(w->router), has_sh ? w->gate_inp_sh : nullptr,
                                  w->logit_bias, H, E, E + (has_sh ? 1 : 0), T, logits, E, sg, mfma ? nullptr : ximg,
-                                 mfma ? ximg : nullptr, st),
+                                 mfma ? ximg : nullptr, iq2 ? 1 : 0, st),
              "router");
     SMOE_MARK();
     if (T <= kFusedRouteTokens) {
@@ -259,6 +265,12 @@ smoe_status smoe_forward_path(const smoe_geom* g, const smoe_weights* w, const f
                  "gate/up");
         SMOE_MARK();
         SMOE_TRY(smoe::launch_mm_down(de, ds, himg, L.h_rec, sg, items, H, F, Fs, n_items, Y, st), "down");
+    } else if (iq2) {
+        SMOE_TRY(smoe::launch_iq2_gu(ge, ue, gs, us, ximg, items, perm, K, H, F, Fs, has_sh ? 1 : 0, n_items, himg,
+                                     L.h_blocks, st),
+                 "gate/up");
+        SMOE_MARK();
+        SMOE_TRY(smoe::launch_iq2_down(de, ds, himg, L.h_blocks, sg, items, H, F, Fs, n_items, Y, st), "down");
     } else {
         SMOE_TRY(smoe::launch_q2_gu(ge, ue, gs, us, ximg, items, perm, K, H, F, Fs, has_sh ? 1 : 0, n_items, himg,
                                     L.h_blocks, st),
@@ -314,7 +326,7 @@ smoe_status smoe_bf16_gemv(const uint16_t* x, const uint16_t* w, float* y, int32
     if ((int64_t)n_tok * n_in % 2) return fail(SMOE_EINVAL, "bf16_gemv: odd element count");
     if (!aligned(x, 16) || !aligned(w, 16)) return fail(SMOE_EALIGN, "bf16_gemv: x and w must be 16-byte aligned");
     SMOE_TRY(smoe::launch_router(nullptr, x, w, nullptr, nullptr, n_in, n_out, n_out, n_tok, y, n_out, nullptr, nullptr,
-                                 nullptr, stream_of(hip_stream)),
+                                 nullptr, 0, stream_of(hip_stream)),
              "bf16_gemv");
     return ok();
 }
@@ -333,13 +345,17 @@ smoe_status smoe_mmvq(int32_t type, const void* w, int64_t byte_off, const uint8
                       int32_t n_col, float* y, void* hip_stream) {
     if (n_in < 0 || n_out < 0 || n_col < 0 || byte_off < 0) return fail(SMOE_EINVAL, "mmvq: negative size");
     if (n_in == 0 || n_out == 0 || n_col == 0) return ok();
-    if (type != SMOE_Q2_0) return fail(SMOE_ETYPE, "mmvq: type " + std::to_string(type) + " is not built");
-    if (n_in > kMaxFF || !smoe::gemv_shape_ok(n_in))
+    if (type != SMOE_Q2_0 && type != SMOE_IQ2_S)
+        return fail(SMOE_ETYPE, "mmvq: type " + std::to_string(type) + " is not Q2_0 or IQ2_S");
+    if (type == SMOE_Q2_0 && (n_in > kMaxFF || !smoe::gemv_shape_ok(n_in)))
         return fail(SMOE_EINVAL, "mmvq: n_in must be 128 times a power of two times at most 8, at most 4096");
+    if (type == SMOE_IQ2_S && !smoe::iq2_shape_ok(n_in))
+        return fail(SMOE_EINVAL, "mmvq: IQ2_S n_in must be 512, 1024 or 2048");
     if (!w || !x_q8 || !y) return fail(SMOE_ENULL, "mmvq: NULL buffer");
     const uint8_t* base = static_cast<const uint8_t*>(w) + byte_off;
     if (!aligned(base, 4) || !aligned(x_q8, 4)) return fail(SMOE_EALIGN, "mmvq: w + byte_off and x must be 4-byte aligned");
-    SMOE_TRY(smoe::launch_q2_mmvq(base, x_q8, n_in, n_out, n_col, y, stream_of(hip_stream)), "mmvq");
+    if (type == SMOE_IQ2_S) SMOE_TRY(smoe::launch_iq2_mmvq(base, x_q8, n_in, n_out, n_col, y, stream_of(hip_stream)), "mmvq");
+    else SMOE_TRY(smoe::launch_q2_mmvq(base, x_q8, n_in, n_out, n_col, y, stream_of(hip_stream)), "mmvq");
     return ok();
 }
 

@@ -1,0 +1,211 @@
+// stratametal_amd/csrc/smoe_gemv.hpp - wave helpers and the q8_1 activation images shared by the decode-path
+// GEMV kernels (Q2_0 and IQ2_S).
+#pragma once
+
+#include "smoe_device.hpp"
+#include "smoe_items.hpp"
+
+namespace smoe {
+
+// ------------------------------------------------------------------------------------------------ lane exchange
+// xor exchange inside groups of up to 32 lanes without LDS traffic: DPP quad permutes for distance 1 and 2,
+// ds_swizzle (bit mode, xor mask) for 4, 8 and 16.
+template <int O>
+__device__ __forceinline__ float xor_swap(float v) {
+    const int i = __float_as_int(v);
+    int r;
+    if constexpr (O == 1) r = __builtin_amdgcn_mov_dpp(i, 0xB1, 0xF, 0xF, false);       // quad_perm [1,0,3,2]
+    else if constexpr (O == 2) r = __builtin_amdgcn_mov_dpp(i, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+    else r = __builtin_amdgcn_ds_swizzle(i, 0x1F | (O << 10));                          // lane ^ O within 32
+    return __int_as_float(r);
+}
+
+// Sum over groups of `lpr` consecutive lanes, distance lpr/2 first; every lane of a group ends with the sum.
+__device__ __forceinline__ float group_sum(float v, int lpr) {
+    if (lpr >= 16) v = v + xor_swap<8>(v);
+    if (lpr >= 8) v = v + xor_swap<4>(v);
+    if (lpr >= 4) v = v + xor_swap<2>(v);
+    if (lpr >= 2) v = v + xor_swap<1>(v);
+    return v;
+}
+
+// The xor butterfly 32, 16, ..., 1 over the whole wave (the same sums as wave_sum_xor): distance 32 through
+// ds_bpermute, the rest as in xor_swap.
+__device__ __forceinline__ float wave_sum_xor_fast(float v) {
+    v = v + __shfl_xor(v, 32, kWave);
+    v = v + xor_swap<16>(v);
+    v = v + xor_swap<8>(v);
+    v = v + xor_swap<4>(v);
+    v = v + xor_swap<2>(v);
+    v = v + xor_swap<1>(v);
+    return v;
+}
+
+// wave_sum_xor_fast of N independent values, stage by stage, so that the N exchanges of a stage are in
+// flight together.
+template <int N>
+__device__ __forceinline__ void wave_sum_xor_fast_n(float (&v)[N]) {
+    float t[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) t[i] = __shfl_xor(v[i], 32, kWave);
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = v[i] + t[i];
+#pragma unroll
+    for (int i = 0; i < N; ++i) t[i] = xor_swap<16>(v[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = v[i] + t[i];
+#pragma unroll
+    for (int i = 0; i < N; ++i) t[i] = xor_swap<8>(v[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = v[i] + t[i];
+#pragma unroll
+    for (int i = 0; i < N; ++i) t[i] = xor_swap<4>(v[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = v[i] + t[i];
+#pragma unroll
+    for (int i = 0; i < N; ++i) t[i] = xor_swap<2>(v[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = v[i] + t[i];
+#pragma unroll
+    for (int i = 0; i < N; ++i) t[i] = xor_swap<1>(v[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = v[i] + t[i];
+}
+
+// Wave maxima for order-free reductions: row rotations by DPP (8, 4, 2, 1), then the four row results read
+// into scalars.  The result is uniform.
+__device__ __forceinline__ uint32_t wave_max_u32_fast(uint32_t v) {
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xF, 0xF, false));  // row_ror:8
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x124, 0xF, 0xF, false));  // row_ror:4
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x122, 0xF, 0xF, false));  // row_ror:2
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x121, 0xF, 0xF, false));  // row_ror:1
+    const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)v, 0), b = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
+    const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)v, 32), d = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+    return max(max(a, b), max(c, d));
+}
+__device__ __forceinline__ float wave_max_fast(float v) {
+    v = __builtin_fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false)));
+    v = __builtin_fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x124, 0xF, 0xF, false)));
+    v = __builtin_fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x122, 0xF, 0xF, false)));
+    v = __builtin_fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x121, 0xF, 0xF, false)));
+    const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return __builtin_fmaxf(__builtin_fmaxf(a, b), __builtin_fmaxf(c, d));
+}
+__device__ __forceinline__ int wave_min_i32_fast(int v) {
+    v = min(v, __builtin_amdgcn_update_dpp(0, v, 0x128, 0xF, 0xF, false));
+    v = min(v, __builtin_amdgcn_update_dpp(0, v, 0x124, 0xF, 0xF, false));
+    v = min(v, __builtin_amdgcn_update_dpp(0, v, 0x122, 0xF, 0xF, false));
+    v = min(v, __builtin_amdgcn_update_dpp(0, v, 0x121, 0xF, 0xF, false));
+    const int a = __builtin_amdgcn_readlane(v, 0), b = __builtin_amdgcn_readlane(v, 16);
+    const int c = __builtin_amdgcn_readlane(v, 32), d = __builtin_amdgcn_readlane(v, 48);
+    return min(min(a, b), min(c, d));
+}
+
+__device__ __forceinline__ int lanes_per_row(int dpr) {
+    const int l = dpr & -dpr;
+    return l > 16 ? 16 : l;
+}
+
+// ------------------------------------------------------------------------------------------------ q8_1 images
+// A q8_1 block (32 activations) as the GEMV kernels read it: 12 dwords, 16-byte aligned:
+//   dwords 0..7  the 32 int8 values permuted so that dword c of each 16-group holds q[c], q[c+4], q[c+8],
+//                q[c+12] (the byte order (codes >> 2c) & 0x03030303 delivers for a 2-bit code dword);
+//   dword 8      f32 of the stored fp16 scale d; dword 9 the int sum of q; dwords 10..11 unused.
+// Built by the same quantiser as the q8_1 block (metal/shaders/iq.metal:597-627); the fp16 sum field of the
+// q8_1 block is not needed by the Q2_0 / IQ2_S dots (metal/shaders/iq.metal:152-180,444-456) and is not kept.
+constexpr int kImgDw = 12;
+
+__device__ __forceinline__ int perm_pos(int i) { return (i & 16) + 4 * (i & 3) + ((i >> 2) & 3); }
+
+// A 32-lane half wave quantises one block (lane & 31 = position) and writes its image (`natural`: the int8
+// values in natural order, the IQ2_S kernels' layout); `sc` is 32 bytes of LDS
+// scratch owned by the half.  Every lane of the half must call it; `store` false skips the global store.
+__device__ __forceinline__ void q8_image_store(float v, bool store, uint8_t* sc, uint32_t* img, bool natural = false) {
+    const int l32 = threadIdx.x & 31;
+    float a = __builtin_fabsf(v);
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) a = __builtin_fmaxf(a, __shfl_xor(a, o, kWave));
+    float d = a / 127.0f;
+    if (__builtin_fabsf(d) > 65504.0f) d = __builtin_copysignf(65504.0f, d);
+    int q = 0;
+    if (a != 0.0f) {
+        float r = __builtin_roundf(v / d);
+        r = r > 127.0f ? 127.0f : r;
+        r = r < -127.0f ? -127.0f : r;
+        q = (r == r) ? (int)r : 0;
+    }
+    int sq = q;
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) sq += __shfl_xor(sq, o, kWave);
+    sc[natural ? l32 : perm_pos(l32)] = (uint8_t)(int8_t)q;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (store) {
+        if (l32 < 8) img[l32] = reinterpret_cast<const uint32_t*>(sc)[l32];
+        if (l32 == 8) img[8] = f2u(f16_to_f32(f32_to_f16(d)));
+        if (l32 == 9) img[9] = (uint32_t)sq;
+    }
+}
+
+// Activation registers for the four q8_1 blocks of one 36-byte weight unit.
+struct Act4 {
+    uint32_t q[4][8];
+    float d[4];
+    int sq[4];
+};
+
+__device__ __forceinline__ void load_act_img(const uint32_t* __restrict__ img, Act4& a) {
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+        const uint4* p = reinterpret_cast<const uint4*>(img + b * kImgDw);
+        const uint4 lo = p[0], hi = p[1], ds = p[2];
+        a.q[b][0] = lo.x; a.q[b][1] = lo.y; a.q[b][2] = lo.z; a.q[b][3] = lo.w;
+        a.q[b][4] = hi.x; a.q[b][5] = hi.y; a.q[b][6] = hi.z; a.q[b][7] = hi.w;
+        a.d[b] = u2f(ds.x);
+        a.sq[b] = (int)ds.y;
+    }
+}
+
+__device__ __forceinline__ void transpose4x4(uint32_t a0, uint32_t a1, uint32_t a2, uint32_t a3, uint32_t* o) {
+    const uint32_t t0 = __builtin_amdgcn_perm(a1, a0, 0x05010400u);
+    const uint32_t u0 = __builtin_amdgcn_perm(a3, a2, 0x05010400u);
+    const uint32_t t1 = __builtin_amdgcn_perm(a1, a0, 0x07030602u);
+    const uint32_t u1 = __builtin_amdgcn_perm(a3, a2, 0x07030602u);
+    o[0] = __builtin_amdgcn_perm(u0, t0, 0x05040100u);
+    o[1] = __builtin_amdgcn_perm(u0, t0, 0x07060302u);
+    o[2] = __builtin_amdgcn_perm(u1, t1, 0x05040100u);
+    o[3] = __builtin_amdgcn_perm(u1, t1, 0x07060302u);
+}
+
+// From four standard 36-byte q8_1 blocks (the stage API's input): permuted in registers.
+__device__ __forceinline__ void load_act_std(const uint8_t* __restrict__ blk, Act4& a) {
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+        uint32_t w[9];
+        __builtin_memcpy(w, __builtin_assume_aligned(blk + b * 36, 4), 36);
+        transpose4x4(w[1], w[2], w[3], w[4], a.q[b]);
+        transpose4x4(w[5], w[6], w[7], w[8], a.q[b] + 4);
+        int sq = 0;
+#pragma unroll
+        for (int i = 1; i < 9; ++i) sq = __builtin_amdgcn_sdot4((int)w[i], 0x01010101, sq, false);
+        a.d[b] = f16_to_f32(w[0] & 0xFFFFu);
+        a.sq[b] = sq;
+    }
+}
+
+// Copies the q8_1 images of `nc` columns (qb blocks each) into LDS, 16 bytes per thread per step.
+__device__ __forceinline__ void stage_images(uint32_t* act, const uint32_t* __restrict__ img, int qb, int c0, int nc,
+                                             const Item& it, const int32_t* perm, int k, bool by_token) {
+    const int per_col = qb * (kImgDw / 4);  // uint4 per column
+    for (int idx = threadIdx.x; idx < nc * per_col; idx += 256) {
+        const int c = idx / per_col, r = idx - c * per_col;
+        const int row = by_token ? item_token(it, perm, k, c0 + c) : it.first + c0 + c;
+        reinterpret_cast<uint4*>(act)[idx] = reinterpret_cast<const uint4*>(img)[(size_t)row * per_col + r];
+    }
+}
+
+}  // namespace smoe

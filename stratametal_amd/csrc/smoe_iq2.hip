@@ -1,0 +1,332 @@
+// stratametal_amd/csrc/smoe_iq2.hip - IQ2_S (ggml type 22) expert products of the decode contract (gfx950).
+//
+// IQ2_S block: 82 bytes for 256 weights: fp16 d @0, qs[32] @2 (grid index low bytes), signs[32] @34, qh[8]
+// @66 (grid index high bits, 2 per group), scales[8] @74 (two 4-bit scales per 32-weight sub-block).  The dot
+// of sub-block ib against a q8_1 block (metal/shaders/iq.metal:152-180; oracle iq2s_partial):
+//     sum0 / sum1 = integer dots of groups 0-1 / 2-3 (8 weights each, magnitude grid[idx] with signs),
+//     sumi = (sum0 * ls0 + sum1 * ls1 + (sum0 + sum1) / 2) / 4   (C integer division),
+//     P = (f32(d_w) * f32(d_x)) * (float) sumi.
+//
+// A lane owns one block of a row.  It decodes the block once per work item into 64 dwords of signed int8
+// weights (natural order), then every column costs 8 v_dot4_i32_i8 per sub-block.  The decode folds the
+// signs into the magnitude lookup: the LDS table holds each grid entry's eight magnitude indices (0..2) as
+// bytes, and one v_perm over the byte table {8, 25, 43, 0, -8, -25, -43, 0} with selector index | 4 * sign
+// yields four signed weights.
+//
+// Device order (oracle: or_iq2_s_gemv_dev): lane value L = ((P_0 + P_1) + ...) + P_7 over its block's
+// sub-blocks; the row is the xor butterfly over the row's nb lanes, distance nb / 2 first (nb = blocks per
+// row, a power of two).
+//
+// Activations are q8_1 images in natural order (image dword c holds q[4c .. 4c + 3]).
+#include "smoe_gemv.hpp"
+#include "smoe_launch.hpp"
+
+namespace smoe {
+
+namespace {
+__device__ const uint16_t kIq2sCodes[1024] = {
+#include "iq2s_grid_codes.inc"
+};
+}  // namespace
+
+constexpr uint32_t kMagPos = 0x002B1908u;  // bytes 8, 25, 43, 0
+constexpr uint32_t kMagNeg = 0x00D5E7F8u;  // bytes -8, -25, -43, 0
+
+// LDS table: entry i = the eight 2-bit magnitude indices of grid entry i, one per byte (lo: weights 0-3).
+__device__ __forceinline__ void build_grid_table(uint2* tab) {
+    for (int i = threadIdx.x; i < 1024; i += blockDim.x) {
+        const uint32_t c = kIq2sCodes[i];
+        uint32_t lo = 0, hi = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            lo |= ((c >> (2 * j)) & 3u) << (8 * j);
+            hi |= ((c >> (8 + 2 * j)) & 3u) << (8 * j);
+        }
+        tab[i] = make_uint2(lo, hi);
+    }
+}
+
+// Four signed weights from four magnitude indices (bytes) and their four sign bits.
+__device__ __forceinline__ uint32_t signed_mags(uint32_t idx4, uint32_t nib) {
+    const uint32_t sel = ((nib * 0x00810204u) & 0x04040404u) | idx4;  // sign bit j -> bit 2 of byte j
+    return __builtin_amdgcn_perm(kMagNeg, kMagPos, sel);
+}
+
+struct Iq2Block {
+    uint32_t w[64];  // signed int8 weights: dword 2 (4 ib + grp) + h = weights 8 (4 ib + grp) + 4 h .. + 3
+    uint32_t sc[2];  // the eight scale bytes
+    float d;
+};
+
+// The 82 bytes of block b of a row (rows are a whole number of block pairs, 164 bytes, so dword aligned):
+// an even block is loaded from its pair's dword 0, an odd one from dword 20 (its bytes start at byte 2 there).
+__device__ __forceinline__ void load_block_raw(const uint8_t* row, int b, uint32_t (&raw)[21], int& off) {
+    const uint8_t* p = row + (size_t)(b >> 1) * 164 + ((b & 1) ? 80 : 0);
+    __builtin_memcpy(raw, __builtin_assume_aligned(p, 4), 84);
+    off = (b & 1) ? 2 : 0;
+}
+
+__device__ __forceinline__ void decode_block(const uint32_t (&raw)[21], int off, const uint2* __restrict__ tab,
+                                             Iq2Block& B) {
+    uint32_t bw[21];  // the block's bytes from byte 0
+#pragma unroll
+    for (int j = 0; j < 20; ++j) bw[j] = __builtin_amdgcn_alignbyte(raw[j + 1], raw[j], off);
+    bw[20] = __builtin_amdgcn_alignbyte(0u, raw[20], off);
+    B.d = (float)__builtin_bit_cast(_Float16, (uint16_t)(bw[0] & 0xFFFFu));
+    const uint32_t qh0 = __builtin_amdgcn_alignbyte(bw[17], bw[16], 2);  // qh bytes 0..3
+    const uint32_t qh1 = __builtin_amdgcn_alignbyte(bw[18], bw[17], 2);  // qh bytes 4..7
+    B.sc[0] = __builtin_amdgcn_alignbyte(bw[19], bw[18], 2);
+    B.sc[1] = __builtin_amdgcn_alignbyte(bw[20], bw[19], 2);
+#pragma unroll
+    for (int ib = 0; ib < 8; ++ib) {
+        const uint32_t qsd = __builtin_amdgcn_alignbyte(bw[ib + 1], bw[ib], 2);
+        const uint32_t sgd = __builtin_amdgcn_alignbyte(bw[9 + ib], bw[8 + ib], 2);
+        const uint32_t qhb = ((ib < 4 ? qh0 : qh1) >> (8 * (ib & 3))) & 0xFFu;
+#pragma unroll
+        for (int grp = 0; grp < 4; ++grp) {
+            const uint32_t idx = ((qsd >> (8 * grp)) & 0xFFu) | (((qhb >> (2 * grp)) & 3u) << 8);
+            const uint2 e = tab[idx];
+            const uint32_t sb = (sgd >> (8 * grp)) & 0xFFu;
+            B.w[2 * (4 * ib + grp)] = signed_mags(e.x, sb & 15u);
+            B.w[2 * (4 * ib + grp) + 1] = signed_mags(e.y, sb >> 4);
+        }
+    }
+}
+
+// Marks the decoded weights as rewritten, so the compiler keeps them as they are instead of rematerialising.
+template <int NIT>
+__device__ __forceinline__ void pin_blocks(Iq2Block (&B)[NIT]) {
+#pragma unroll
+    for (int it = 0; it < NIT; ++it)
+#pragma unroll
+        for (int i = 0; i < 64; ++i) asm volatile("" : "+v"(B[it].w[i]));
+}
+
+// Sub-block ib against one natural-order q8_1 image (8 dwords of q, then f32 d).
+__device__ __forceinline__ float iq2_sub(const Iq2Block& B, int ib, const uint32_t* q, float dx) {
+    int s0 = 0, s1 = 0;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) s0 = __builtin_amdgcn_sdot4((int)B.w[8 * ib + c], (int)q[c], s0, false);
+#pragma unroll
+    for (int c = 4; c < 8; ++c) s1 = __builtin_amdgcn_sdot4((int)B.w[8 * ib + c], (int)q[c], s1, false);
+    const uint32_t scb = (B.sc[ib >> 2] >> (8 * (ib & 3))) & 0xFFu;
+    const int ls0 = (int)(scb & 15u), ls1 = (int)(scb >> 4);
+    const int sumi = (s0 * ls0 + s1 * ls1 + (s0 + s1) / 2) / 4;
+    return (B.d * dx) * (float)sumi;
+}
+
+// The block's lane value against a column's images (img = the column's image row, block b's images 8 b ..).
+__device__ __forceinline__ float iq2_block_dot_img(const Iq2Block& B, const uint32_t* img, int b) {
+    float L = 0.0f;
+#pragma unroll
+    for (int ib = 0; ib < 8; ++ib) {
+        const uint4* p = reinterpret_cast<const uint4*>(img + (size_t)(8 * b + ib) * kImgDw);
+        const uint4 lo = p[0], hi = p[1], ds = p[2];
+        const uint32_t q[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+        const float P = iq2_sub(B, ib, q, u2f(ds.x));
+        L = ib == 0 ? P : L + P;
+    }
+    return L;
+}
+
+// The same against standard 36-byte q8_1 blocks (the stage API's input).
+__device__ __forceinline__ float iq2_block_dot_std(const Iq2Block& B, const uint8_t* __restrict__ xq, int b) {
+    float L = 0.0f;
+#pragma unroll
+    for (int ib = 0; ib < 8; ++ib) {
+        uint32_t w9[9];
+        __builtin_memcpy(w9, __builtin_assume_aligned(xq + (size_t)(8 * b + ib) * 36, 4), 36);
+        const float P = iq2_sub(B, ib, w9 + 1, f16_to_f32(w9[0] & 0xFFFFu));
+        L = ib == 0 ? P : L + P;
+    }
+    return L;
+}
+
+// ------------------------------------------------------------------------------------------------ gate/up
+// Grid (Fmax / 32, work items), 4 waves.  Wave w computes gate rows [32 hb + 8 w, +8) (rho 0..7) and the
+// same up rows (rho 8..15), nb lanes per row, NIT passes of 64 / nb rows; columns in stages of kGuColsIq2:
+// their x images are copied to LDS, every column's row values parked in LDS, then each half wave quantises
+// one column's 32 h values into natural-order image block hb.
+constexpr int kGuColsIq2 = 8;
+
+template <int NIT>
+__global__ __launch_bounds__(256) void k_iq2_gu(const uint8_t* __restrict__ gate_exps, const uint8_t* __restrict__ up_exps,
+                                                 const uint8_t* __restrict__ gate_sh, const uint8_t* __restrict__ up_sh,
+                                                 const uint32_t* __restrict__ ximg, const int4* __restrict__ items,
+                                                 const int32_t* __restrict__ perm, int k, int H, int F, int Fs,
+                                                 uint32_t* __restrict__ himg, int h_blocks) {
+    extern __shared__ __align__(16) uint32_t smem[];
+    __shared__ uint2 tab[1024];
+    __shared__ float rowv[kGuColsIq2][64];
+    __shared__ uint8_t qsc[8][32];
+    Item item;
+    if (!work_item(items, blockIdx.y, item)) return;
+    const int hb = blockIdx.x;
+    const int Fe = item.shared ? Fs : F;
+    if (hb * 32 >= Fe) return;
+    build_grid_table(tab);
+    const int nb = H >> 8;
+    const size_t rb = (size_t)nb * 82;
+    const uint8_t* g0 = item.shared ? gate_sh : gate_exps + (size_t)item.e * F * rb;
+    const uint8_t* u0 = item.shared ? up_sh : up_exps + (size_t)item.e * F * rb;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int rpi = 64 / nb, grp = lane / nb, b = lane - grp * nb;
+    const int qb = H >> 5;
+    __syncthreads();
+
+    Iq2Block B[NIT];
+    bool live[NIT];
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+        const int rho = it * rpi + grp;
+        live[it] = rho < 16;
+        const int r = 32 * hb + 8 * wave + (rho & 7);
+        const uint8_t* rowp = ((rho & 8) ? u0 : g0) + (size_t)r * rb;
+        uint32_t raw[21];
+        int off;
+        load_block_raw(rowp, b, raw, off);
+        decode_block(raw, off, tab, B[it]);
+    }
+
+    for (int c0 = 0; c0 < item.ncol; c0 += kGuColsIq2) {
+        const int nc = min(kGuColsIq2, item.ncol - c0);
+        stage_images(smem, ximg, qb, c0, nc, item, perm, k, true);
+        __syncthreads();
+        for (int c = 0; c < nc; ++c) {
+            const uint32_t* xt = smem + (size_t)c * qb * kImgDw;
+            pin_blocks(B);
+#pragma unroll
+            for (int it = 0; it < NIT; ++it) {
+                const float v = group_sum(iq2_block_dot_img(B[it], xt, b), nb);
+                const int rho = it * rpi + grp;
+                if (live[it] && b == 0) rowv[c][(rho < 8 ? 0 : 32) + 8 * wave + (rho & 7)] = v;
+            }
+        }
+        __syncthreads();
+        {
+            const int hw = threadIdx.x >> 5;  // half wave = column
+            const bool live_c = hw < nc;
+            const int i = lane & 31;
+            const float h = live_c ? silu_mul(rowv[hw][i], rowv[hw][32 + i]) : 0.0f;
+            const int row = item.first + c0 + (live_c ? hw : 0);
+            q8_image_store(h, live_c, qsc[hw], himg + ((size_t)row * h_blocks + hb) * kImgDw, true);
+        }
+        __syncthreads();
+    }
+}
+
+// ------------------------------------------------------------------------------------------------ down
+// Grid (H / (4 * 64 / nbf), work items); nbf = F / 256 lanes per row, 64 / nbf rows per wave.  The item's h
+// images are copied to LDS `cps` columns at a time; each group leader writes Y[first + c][row] (the shared
+// rows times sigmoid(sg[t])).
+__global__ __launch_bounds__(256) void k_iq2_down(const uint8_t* __restrict__ down_exps, const uint8_t* __restrict__ down_sh,
+                                                   const uint32_t* __restrict__ himg, int h_blocks,
+                                                   const float* __restrict__ sg, const int4* __restrict__ items, int H,
+                                                   int F, int Fs, int cps, float* __restrict__ Y) {
+    extern __shared__ __align__(16) uint32_t smem[];
+    __shared__ uint2 tab[1024];
+    Item item;
+    if (!work_item(items, blockIdx.y, item)) return;
+    build_grid_table(tab);
+    const int Fe = item.shared ? Fs : F;
+    const int nb = Fe >> 8;
+    const size_t rb = (size_t)nb * 82;
+    const uint8_t* base = item.shared ? down_sh : down_exps + (size_t)item.e * H * ((size_t)(F >> 8) * 82);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int rpw = 64 / nb, grp = lane / nb, b = lane - grp * nb;
+    const int r = blockIdx.x * 4 * rpw + wave * rpw + grp;
+    const bool live = r < H;
+    __syncthreads();
+    Iq2Block B[1];
+    {
+        uint32_t raw[21];
+        int off;
+        load_block_raw(base + (size_t)(live ? r : 0) * rb, b, raw, off);
+        decode_block(raw, off, tab, B[0]);
+    }
+    for (int c0 = 0; c0 < item.ncol; c0 += cps) {
+        const int nc = min(cps, item.ncol - c0);
+        stage_images(smem, himg, h_blocks, c0, nc, item, nullptr, 1, false);
+        __syncthreads();
+        for (int c = 0; c < nc; ++c) {
+            const uint32_t* ht = smem + (size_t)c * h_blocks * kImgDw;
+            pin_blocks(B);
+            float v = group_sum(iq2_block_dot_img(B[0], ht, b), nb);
+            if (item.shared) v = v * sigmoid(sg[item.tok0 + c0 + c]);
+            if (live && b == 0) Y[(size_t)(item.first + c0 + c) * H + r] = v;
+        }
+        __syncthreads();
+    }
+}
+
+// Generic IQ2_S GEMV over n_col columns of standard q8_1 blocks (iq_mmvq's contract, metal/src/iq.mm:148-169).
+__global__ __launch_bounds__(256) void k_iq2_mmvq(const uint8_t* __restrict__ w, const uint8_t* __restrict__ xq, int n_in,
+                                                   int n_out, int n_col, float* __restrict__ y) {
+    __shared__ uint2 tab[1024];
+    build_grid_table(tab);
+    const int nb = n_in >> 8;
+    const size_t rb = (size_t)nb * 82;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int rpw = 64 / nb, grp = lane / nb, b = lane - grp * nb;
+    const int r = blockIdx.x * 4 * rpw + wave * rpw + grp;
+    const bool live = r < n_out;
+    __syncthreads();
+    Iq2Block B[1];
+    {
+        uint32_t raw[21];
+        int off;
+        load_block_raw(w + (size_t)(live ? r : 0) * rb, b, raw, off);
+        decode_block(raw, off, tab, B[0]);
+    }
+    const int xb = n_in >> 5;
+    for (int c = 0; c < n_col; ++c) {
+        pin_blocks(B);
+        const float v = group_sum(iq2_block_dot_std(B[0], xq + (size_t)c * xb * 36, b), nb);
+        if (live && b == 0) y[(size_t)c * n_out + r] = v;
+    }
+}
+
+// ------------------------------------------------------------------------------------------------ launchers
+// Rows the IQ2_S kernels tile: n_in = 256 nb with nb in {2, 4, 8} (a row is a whole number of block pairs,
+// one block per lane, at most 8 lanes per row).
+bool iq2_shape_ok(int n_in) {
+    if (n_in <= 0 || n_in % 256) return false;
+    const int nb = n_in / 256;
+    return nb == 2 || nb == 4 || nb == 8;
+}
+
+hipError_t launch_iq2_gu(const uint8_t* gate_exps, const uint8_t* up_exps, const uint8_t* gate_sh, const uint8_t* up_sh,
+                         const uint32_t* ximg, const int4* items, const int32_t* perm, int k, int H, int F, int Fs,
+                         int has_shared, int max_items, uint32_t* himg, int h_blocks, hipStream_t s) {
+    const int Fmax = has_shared && Fs > F ? Fs : F;
+    dim3 grid((unsigned)(Fmax / 32), (unsigned)max_items);
+    const int nb = H / 256, rpi = 64 / nb;
+    const size_t lds = (size_t)kGuColsIq2 * (H >> 5) * kImgDw * 4;
+    if (rpi >= 16) hipLaunchKernelGGL((k_iq2_gu<1>), grid, dim3(256), lds, s, gate_exps, up_exps, gate_sh, up_sh, ximg,
+                                      items, perm, k, H, F, Fs, himg, h_blocks);
+    else hipLaunchKernelGGL((k_iq2_gu<2>), grid, dim3(256), lds, s, gate_exps, up_exps, gate_sh, up_sh, ximg, items,
+                            perm, k, H, F, Fs, himg, h_blocks);
+    return hipGetLastError();
+}
+
+hipError_t launch_iq2_down(const uint8_t* down_exps, const uint8_t* down_sh, const uint32_t* himg, int h_blocks,
+                           const float* sg, const int4* items, int H, int F, int Fs, int max_items, float* Y,
+                           hipStream_t s) {
+    const int rpw = 64 / (F / 256);  // the caller guarantees the shared width has the same row shape
+    dim3 grid((unsigned)((H + 4 * rpw - 1) / (4 * rpw)), (unsigned)max_items);
+    const size_t col_bytes = (size_t)h_blocks * kImgDw * 4;
+    int cps = (int)(24576 / col_bytes);
+    cps = cps < 1 ? 1 : cps > 16 ? 16 : cps;
+    hipLaunchKernelGGL(k_iq2_down, grid, dim3(256), (size_t)cps * col_bytes, s, down_exps, down_sh, himg, h_blocks, sg,
+                       items, H, F, Fs, cps, Y);
+    return hipGetLastError();
+}
+
+hipError_t launch_iq2_mmvq(const uint8_t* w, const uint8_t* xq, int n_in, int n_out, int n_col, float* y, hipStream_t s) {
+    const int rpw = 64 / (n_in / 256);
+    dim3 grid((unsigned)((n_out + 4 * rpw - 1) / (4 * rpw)));
+    hipLaunchKernelGGL(k_iq2_mmvq, grid, dim3(256), 0, s, w, xq, n_in, n_out, n_col, y);
+    return hipGetLastError();
+}
+
+}  // namespace smoe

@@ -14,7 +14,8 @@ size_t img_bytes(int64_t n_blocks);      // bytes of n_blocks q8_1 images
 hipError_t launch_prep(const float* x, int64_t n, uint8_t* xq, uint16_t* xb, hipStream_t s);
 hipError_t launch_router(const float* xf, const uint16_t* xb, const uint16_t* W, const uint16_t* w_inp,
                          const float* bias, int H, int E, int rows_total, int T, float* logits, int ld_logits, float* sg,
-                         uint32_t* ximg, const uint32_t* xrec, hipStream_t s);  // xrec: x as activation records
+                         uint32_t* ximg, const uint32_t* xrec, int img_natural, hipStream_t s);
+// (xrec: x as activation records; img_natural: write ximg in the IQ2_S kernels' natural order)
 hipError_t launch_topk(const float* logits, int ld_logits, int T, int E, int k, int32_t* ids, float* wts, hipStream_t s);
 hipError_t launch_dispatch(const int32_t* ids, int P, int E, int32_t* counts, int32_t* offsets, int32_t* perm,
                            int32_t* slot, int32_t* elist, int32_t* n_list, int4* items, int max_items, int T, int k,
@@ -37,6 +38,16 @@ hipError_t launch_combine_parts(const float* parts, const float* wts, const floa
                                 hipStream_t s);
 hipError_t launch_swiglu_q8(const float* gate, const float* up, int64_t n, uint8_t* y, hipStream_t s);
 hipError_t launch_q2_mmvq(const uint8_t* w, const uint8_t* xq, int n_in, int n_out, int n_col, float* y, hipStream_t s);
+
+// IQ2_S (decode contract)
+bool iq2_shape_ok(int n_in);  // n_in = 256 nb, nb in {2, 4, 8}
+hipError_t launch_iq2_gu(const uint8_t* gate_exps, const uint8_t* up_exps, const uint8_t* gate_sh, const uint8_t* up_sh,
+                         const uint32_t* ximg, const int4* items, const int32_t* perm, int k, int H, int F, int Fs,
+                         int has_shared, int max_items, uint32_t* himg, int h_blocks, hipStream_t s);
+hipError_t launch_iq2_down(const uint8_t* down_exps, const uint8_t* down_sh, const uint32_t* himg, int h_blocks,
+                           const float* sg, const int4* items, int H, int F, int Fs, int max_items, float* Y,
+                           hipStream_t s);
+hipError_t launch_iq2_mmvq(const uint8_t* w, const uint8_t* xq, int n_in, int n_out, int n_col, float* y, hipStream_t s);
 
 // prefill contract (bf16 MFMA)
 int mfma_chunk();                        // tokens per MFMA work item

@@ -1,0 +1,131 @@
+"""GPU parity of the IQ2_S (ggml type 22) decode path through the C ABI, against the oracle on the same seeded
+inputs: bitwise against the device-order restatement (or_iq2_s_gemv_dev, the block chain or_moe_decode_dev);
+within 1e-5 per stage / 1e-3 per row of the reference-order chain (32-lane partials,
+metal/shaders/iq.metal:152-180,459-498).  Covers BASELINE configs[3] (batch 64, IQ2_S routed and shared
+experts, uniform routing), the stage GEMV at every supported row length, and the refusals of shapes and paths
+the IQ2_S kernels do not tile."""
+import sys
+
+import numpy as np
+import pytest
+
+import oracle as O
+import stratametal_amd as S
+
+pytestmark = pytest.mark.gpu
+GUARD = 16
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def torch():
+    import torch as T
+    if not T.cuda.is_available():
+        pytest.skip("no GPU")
+    S.lib()
+    return T
+
+
+def dev(torch, a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(torch, t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def bits(a):
+    a = np.ascontiguousarray(a)
+    return a.view(np.uint32) if a.dtype == np.float32 else a
+
+
+@pytest.mark.parametrize("n_in,n_out,n_col", [(512, 64, 1), (1024, 96, 2), (2048, 512, 3), (2048, 37, 1)])
+def test_mmvq_iq2_s_bitwise(torch, n_in, n_out, n_col):
+    say(f"case: mmvq IQ2_S {n_in}x{n_out} cols={n_col}")
+    w = O.gen_iq2_s(777, n_in + n_out, n_out * n_in // 256)
+    x = O.gen_normal(777, n_col, n_col * n_in)
+    xq = O.quant_q8_1(x)
+    y = S.mmvq(22, dev(torch, w), dev(torch, xq), n_in, n_out, n_col)
+    got = host(torch, y)
+    for c in range(n_col):
+        xc = xq[c * n_in // 32 * 36:(c + 1) * n_in // 32 * 36]
+        assert np.array_equal(bits(got[c]), bits(O.iq2_s_gemv_dev(w, xc, n_in, n_out)))
+        assert O.rel_l1_rows(got[c][None], O.iq2_s_gemv_ref(w, xc, n_in, n_out)[None])[0] <= 1e-5
+
+
+def test_mmvq_iq2_s_odd_block_offset(torch):
+    """A byte offset that starts the rows at an odd block (82 bytes, 2 mod 4) is refused as misaligned; an
+    even number of blocks in is read exactly."""
+    say("case: mmvq IQ2_S byte offset")
+    n_in, n_out = 512, 32
+    blob = O.gen_iq2_s(5, 5, 2 * n_out * n_in // 256)
+    xq = O.quant_q8_1(O.gen_normal(5, 6, n_in))
+    off = n_out * n_in // 256 * 82
+    y = S.mmvq(22, dev(torch, blob), dev(torch, xq), n_in, n_out, 1, byte_off=off)
+    assert np.array_equal(bits(host(torch, y)[0]), bits(O.iq2_s_gemv_dev(blob[off:], xq, n_in, n_out)))
+    with pytest.raises(S.SmoeError):
+        S.mmvq(22, dev(torch, blob), dev(torch, xq), n_in, n_out, 1, byte_off=82)
+
+
+CASES = [
+    # name, geometry, T, seed, add_shared
+    ("config 4 (b=64, IQ2_S, uniform)", dict(w_type=22, sh_type=22), 64, 4, True),
+    ("small IQ2_S", dict(n_embd=512, n_ff=512, n_ff_shared=512, n_expert=16, top_k=4, w_type=22, sh_type=22), 5, 41,
+     True),
+    ("IQ2_S H=1024 no shared", dict(n_embd=1024, n_ff=512, n_expert=32, top_k=6, w_type=22, sh_type=-1), 9, 42, True),
+    ("IQ2_S shared not added", dict(n_embd=512, n_ff=1024, n_ff_shared=1024, n_expert=16, top_k=2, w_type=22,
+                                    sh_type=22), 3, 43, False),
+    ("IQ2_S b=1", dict(w_type=22, sh_type=22), 1, 44, True),
+]
+
+
+@pytest.mark.parametrize("case", range(len(CASES)))
+def test_forward_iq2_s_parity(torch, case):
+    name, gkw, T, seed, add_shared = CASES[case]
+    say(f"case: forward {name} T={T}")
+    g = O.Geom(**gkw)
+    w_host = O.make_weights(g, seed)
+    w_dev = S.synth_layer(S.Geom(**vars(g)), seed)
+    x = O.gen_normal(seed, 100, T * g.n_embd).reshape(T, g.n_embd)
+    ml = S.MoELayer(S.Geom(**vars(g)), w_dev, max_tokens=T)
+    yg = torch.full((T * g.n_embd + GUARD,), 7.0, dtype=torch.float32, device="cuda")
+    yv = yg[:T * g.n_embd].view(T, g.n_embd)
+    _, tr = ml.forward(dev(torch, x), y=yv, add_shared=add_shared, trace=True)
+    got = host(torch, yg)
+    assert (got[T * g.n_embd:] == 7.0).all(), "guard words past y were written"
+    y = got[:T * g.n_embd].reshape(T, g.n_embd)
+    want, wtr = O.moe_decode_dev(g, w_host, x, add_shared=add_shared, trace=True, n_threads=16)
+    for k in ("logits", "ids", "weights", "counts", "offsets", "perm", "slot"):
+        assert np.array_equal(bits(host(torch, tr[k])), bits(wtr[k])), k
+    assert np.array_equal(bits(y), bits(want)), f"max rel {O.rel_l1_rows(y, want).max()}"
+    yref = O.moe_decode_ref(g, w_host, x, add_shared=add_shared, n_threads=16)
+    assert O.rel_l1_rows(y, yref).max() <= 1e-3
+    if name.startswith("config 4"):
+        D = int((host(torch, tr["counts"]) > 0).sum())
+        say(f"  distinct experts touched: {D}")
+        assert 300 < D < 420  # uniform routing of 64 x 10 pairs over 512 experts: E[D] ~ 367
+
+
+def test_iq2_s_refusals(torch):
+    say("case: IQ2_S refusals")
+    ok = S.Geom(n_embd=512, n_ff=512, n_ff_shared=512, n_expert=16, top_k=4, w_type=22, sh_type=22)
+    assert S.workspace_bytes(ok, 8) > 0
+    for bad in (dict(n_embd=768), dict(n_ff=256), dict(n_embd=4096), dict(n_ff_shared=1024), dict(sh_type=42)):
+        kw = dict(vars(ok)); kw.update(bad)
+        with pytest.raises(S.SmoeError):
+            S.workspace_bytes(S.Geom(**kw), 8)
+    w = S.synth_layer(ok, 3)
+    ml = S.MoELayer(ok, w, max_tokens=8)
+    with pytest.raises(S.SmoeError):
+        ml.forward(torch.zeros((4, 512), device="cuda"), path=S.PATH_MFMA)
+    # the automatic path stays on the IQ2_S GEMV kernels at prefill sizes
+    ml2 = S.MoELayer(ok, w, max_tokens=130)
+    x = O.gen_normal(9, 100, 130 * 512).reshape(130, 512)
+    y = host(torch, ml2.forward(dev(torch, x)))
+    assert np.array_equal(bits(y), bits(O.moe_decode_dev(O.Geom(**vars(ok)), O.make_weights(O.Geom(**vars(ok)), 3), x,
+                                                           n_threads=16)))
