@@ -41,6 +41,12 @@ def _args():
     ap.add_argument("--no-extra", action="store_true", help="skip the decode b=1 and prefill 512 measurements")
     ap.add_argument("--prefill-layers", type=int, default=8)
     ap.add_argument("--prefill-steps", type=int, default=24)
+    ap.add_argument("--iq2-layers", type=int, default=8)
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a plain device copy of MIB MiB five times (the reference kernel that scales the "
+                         "FETCH_SIZE / WRITE_SIZE counters to bytes), then exit")
+    ap.add_argument("--only", choices=("b1", "prefill", "iq2"), default=None,
+                    help="measure only this secondary workload (for a profiler run); prints its summary, no JSON line")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     return ap.parse_args()
@@ -246,6 +252,27 @@ def prefill(S, torch, g, a):
     return out
 
 
+def iq2_b64(S, torch, a):
+    """batch 64, IQ2_S routed and shared experts, uniform routing (no bias), decode contract.
+    `--iq2-layers` resident layers (about 0.5 GB each) so that steps do not hit the Infinity Cache."""
+    g = S.Geom(w_type=S.IQ2_S, sh_type=S.IQ2_S)
+    t0 = time.perf_counter()
+    stack = Stack(S, torch, g, a.iq2_layers, a.seed + 2000, 64)
+    log(f"IQ2_S: {a.iq2_layers} layers resident in {time.perf_counter() - t0:.1f} s")
+    steps = a.prefill_steps
+    r = measure(S, torch, stack, 64, steps, max(2, steps // 3), a.seed + 17)
+    m = summarize(S, g, 64, r, steps)
+    out = {k: m[k] for k in ("ms_per_step", "tok_s", "touched_experts_avg", "layer_bytes_avg", "layer_gbs",
+                             "stage_ms_avg", "gate_up_gbs", "down_gbs")}
+    out["layer_hbm_frac"] = m["layer_gbs"] / HBM_PEAK_GBS
+    log("IQ2_S b=64: %.3f ms/step, %.0f tok/s, layer %.0f GB/s, touched %.0f, stages(us) %s" % (
+        m["ms_per_step"], m["tok_s"], m["layer_gbs"], m["touched_experts_avg"],
+        {k: round(v * 1e3, 1) for k, v in m["stage_ms_avg"].items()}))
+    del stack
+    torch.cuda.empty_cache()
+    return out
+
+
 def main():
     a = _args()
     if a.gpus != 1:
@@ -254,13 +281,33 @@ def main():
         sys.exit(2)
     import ctypes
     import torch
+    if a.copy_calibration:
+        n = a.copy_calibration * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copied {a.copy_calibration} MiB x5")
+        return
     import stratametal_amd as S
     S.C = ctypes
     g = S.Geom()
+    if a.only == "prefill":
+        prefill(S, torch, g, a)
+        return
+    if a.only == "iq2":
+        iq2_b64(S, torch, a)
+        return
     t_setup = time.perf_counter()
     stack = Stack(S, torch, g, a.layers, a.seed, max(a.tokens, 1))
     log(f"{a.layers} layers resident ({a.layers * (g.n_expert * g.expert_bytes() + g.shared_bytes()) / 1e9:.1f} GB) "
         f"in {time.perf_counter() - t_setup:.1f} s")
+    if a.only == "b1":
+        r1 = measure(S, torch, stack, 1, a.steps, a.warmup, a.seed + 11)
+        m1 = summarize(S, g, 1, r1, a.steps)
+        log("decode b=1: %.3f ms/step, %.0f tok/s, layer %.0f GB/s" % (m1["ms_per_step"], m1["tok_s"], m1["layer_gbs"]))
+        return
     r16 = measure(S, torch, stack, a.tokens, a.steps, a.warmup, a.seed + 7)
     m16 = summarize(S, g, a.tokens, r16, a.steps)
     log("decode b=%d: %.3f ms/step, %.0f tok/s, layer %.0f GB/s, gate/up %.0f GB/s, stages %s" % (
@@ -277,6 +324,7 @@ def main():
                                                  "layer_gbs", "stage_ms_avg", "gate_up_gbs", "down_gbs")}
         extra["decode_b1"]["layer_hbm_frac"] = m1["layer_gbs"] / HBM_PEAK_GBS
         extra["prefill_512"] = prefill(S, torch, g, a)
+        extra["iq2_s_b64"] = iq2_b64(S, torch, a)
     extra["decode_b16_stages_ms"] = m16["stage_ms_avg"]
     extra["decode_b16_layer_gbs"] = m16["layer_gbs"]
     extra["decode_b16_layer_hbm_frac"] = m16["layer_gbs"] / HBM_PEAK_GBS

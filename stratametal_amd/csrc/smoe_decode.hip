@@ -51,9 +51,15 @@ __device__ __forceinline__ void pin_units(uint32_t (&w)[NIT][MAXUPL][9]) {
             for (int i = 0; i < 9; ++i) asm volatile("" : "+v"(w[it][m][i]));
 }
 
-__device__ __forceinline__ float q2_unit_dot(const uint32_t (&w)[9], const Act4& a) {
-    const float d0 = f16_to_f32(w[0] & 0xFFFFu);
-    const float d1 = f16_to_f32(w[4] >> 16);
+// The unit's two block scales (exact hardware fp16 -> f32, subnormals included), computed once per work item.
+__device__ __forceinline__ float unit_d0(const uint32_t (&w)[9]) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(w[0] & 0xFFFFu));
+}
+__device__ __forceinline__ float unit_d1(const uint32_t (&w)[9]) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(w[4] >> 16));
+}
+
+__device__ __forceinline__ float q2_unit_dot(const uint32_t (&w)[9], float d0, float d1, const Act4& a) {
     const uint32_t c0 = __builtin_amdgcn_alignbyte(w[1], w[0], 2);
     const uint32_t c1 = __builtin_amdgcn_alignbyte(w[2], w[1], 2);
     const uint32_t c2 = __builtin_amdgcn_alignbyte(w[3], w[2], 2);
@@ -82,6 +88,19 @@ __global__ __launch_bounds__(256) void k_router(const float* __restrict__ xf, co
     __shared__ uint8_t qsc[8][32];
     const int t0 = blockIdx.y * tok_tile;
     const int nt = min(tok_tile, T - t0);
+    // the wave's weight row first (clamped, every load issued), so its latency overlaps the staging below
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int rowc = min(row, rows_total - 1);
+    const uint16_t* wr = rowc < E ? W + (size_t)rowc * H : w_inp;
+    const int chunks = H >> 3;
+    uint4 wv[MAXC];
+#pragma unroll
+    for (int j = 0; j < MAXC; ++j) {
+        const int c = lane + 64 * j;
+        wv[j] = c < chunks ? *reinterpret_cast<const uint4*>(wr + 8 * c) : make_uint4(0, 0, 0, 0);
+    }
+    const float bv = (bias && rowc < E) ? bias[rowc] : 0.0f;  // loaded once, outside the token loop
     // stage the tile, 8 vector loads in flight per thread
     const int n8 = nt * H / 8;  // groups of 8 values = one uint4 of bf16
     for (int base = 0; base < n8; base += 256 * 4) {
@@ -129,18 +148,7 @@ __global__ __launch_bounds__(256) void k_router(const float* __restrict__ xf, co
     }
     __syncthreads();
     const uint16_t* xs = reinterpret_cast<const uint16_t*>(smem);
-    const int lane = threadIdx.x & 63;
-    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= rows_total) return;
-    const uint16_t* wr = row < E ? W + (size_t)row * H : w_inp;
-    const int chunks = H >> 3;
-    uint4 wv[MAXC];
-#pragma unroll
-    for (int j = 0; j < MAXC; ++j) {
-        const int c = lane + 64 * j;
-        wv[j] = c < chunks ? *reinterpret_cast<const uint4*>(wr + 8 * c) : make_uint4(0, 0, 0, 0);
-    }
-    const float bv = (bias && row < E) ? bias[row] : 0.0f;  // loaded once, outside the token loop
     for (int t = 0; t < nt; t += 4) {  // four tokens at a time: four independent accumulation chains
         const int ng = min(4, nt - t);
         float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -203,6 +211,30 @@ __device__ __forceinline__ float reduce_scatter64(float (&v)[64], int lane) {
     rs_stage<2, 4>(v, lane);
     rs_stage<1, 2>(v, lane);
     return v[0];
+}
+
+// group_sum of NIT values at once when lpr = 4 NIT (NIT = 2 or 4): a reduce-scatter over the group's upper
+// lane bits leaves lane l with the sum of value (l >> 2) & (NIT - 1), formed by exactly the butterfly's
+// additions (distance lpr / 2 first), then the last two stages as in group_sum.  NIT = 1: group_sum.
+template <int NIT>
+__device__ __forceinline__ float group_sum_rs(float (&v)[NIT], int lpr, int lane, int& item) {
+    if constexpr (NIT == 1) {
+        item = 0;
+        return group_sum(v[0], lpr);
+    } else {
+        static_assert(NIT == 2 || NIT == 4, "lpr = 4 NIT");
+        if constexpr (NIT == 4) {
+            rs_stage<8, 4>(v, lane);
+            rs_stage<4, 2>(v, lane);
+        } else {
+            rs_stage<4, 2>(v, lane);
+        }
+        float r = v[0];
+        r = r + xor_swap<2>(r);
+        r = r + xor_swap<1>(r);
+        item = (lane >> 2) & (NIT - 1);
+        return r;
+    }
 }
 
 // The same logits for many tokens (no q8_1 images): a work-group computes 16 rows x 16 tokens, wave w the rows
@@ -644,6 +676,14 @@ __global__ __launch_bounds__(256) void k_q2_gu(const uint8_t* __restrict__ gate_
         for (int m = 0; m < MAXUPL; ++m)
             if (live[it] && m < G.upl) load_unit(rowp + (size_t)(l + G.lpr * m) * 36, w[it][m]);
     }
+    float dw[NIT][MAXUPL][2];
+#pragma unroll
+    for (int it = 0; it < NIT; ++it)
+#pragma unroll
+        for (int m = 0; m < MAXUPL; ++m) {
+            dw[it][m][0] = unit_d0(w[it][m]);
+            dw[it][m][1] = unit_d1(w[it][m]);
+        }
 
     for (int c0 = 0; c0 < item.ncol; c0 += kGuCols) {
         const int nc = min(kGuCols, item.ncol - c0);
@@ -660,17 +700,16 @@ __global__ __launch_bounds__(256) void k_q2_gu(const uint8_t* __restrict__ gate_
                     load_act_img(xt + (size_t)(4 * (l + G.lpr * m)) * kImgDw, a);
 #pragma unroll
                     for (int it = 0; it < NIT; ++it) {
-                        const float L = q2_unit_dot(w[it][m], a);
+                        const float L = q2_unit_dot(w[it][m], dw[it][m][0], dw[it][m][1], a);
                         acc[it] = m == 0 ? L : acc[it] + L;
                     }
                 }
             }
-#pragma unroll
-            for (int it = 0; it < NIT; ++it) {
-                const float v = group_sum(acc[it], G.lpr);
-                const int rho = it * G.rpi + grp;
-                if (live[it] && l == 0) rowv[c][(rho < 8 ? 0 : 32) + 8 * wave + (rho & 7)] = v;
-            }
+            int it;
+            const float v = group_sum_rs<NIT>(acc, G.lpr, lane, it);
+            const int rho = it * G.rpi + grp;
+            if (rho < 16 && (l & 3) == 0 && (NIT > 1 || l == 0))
+                rowv[c][(rho < 8 ? 0 : 32) + 8 * wave + (rho & 7)] = v;
         }
         __syncthreads();
         {
@@ -715,6 +754,14 @@ __global__ __launch_bounds__(256) void k_q2_down(const uint8_t* __restrict__ dow
         for (int m = 0; m < MAXUPL; ++m)
             if (live[it] && m < G.upl) load_unit(base + (size_t)r * rb + (size_t)(l + G.lpr * m) * 36, w[it][m]);
     }
+    float dw[NIT][MAXUPL][2];
+#pragma unroll
+    for (int it = 0; it < NIT; ++it)
+#pragma unroll
+        for (int m = 0; m < MAXUPL; ++m) {
+            dw[it][m][0] = unit_d0(w[it][m]);
+            dw[it][m][1] = unit_d1(w[it][m]);
+        }
     for (int c0 = 0; c0 < item.ncol; c0 += cps) {
         const int nc = min(cps, item.ncol - c0);
         stage_images(smem, himg, h_blocks, c0, nc, item, nullptr, 1, false);
@@ -730,19 +777,17 @@ __global__ __launch_bounds__(256) void k_q2_down(const uint8_t* __restrict__ dow
                     load_act_img(ht + (size_t)(4 * (l + G.lpr * m)) * kImgDw, a);
 #pragma unroll
                     for (int it = 0; it < NIT; ++it) {
-                        const float L = q2_unit_dot(w[it][m], a);
+                        const float L = q2_unit_dot(w[it][m], dw[it][m][0], dw[it][m][1], a);
                         acc[it] = m == 0 ? L : acc[it] + L;
                     }
                 }
             }
             const float sig = item.shared ? sigmoid(sg[item.tok0 + c0 + c]) : 1.0f;
-#pragma unroll
-            for (int it = 0; it < NIT; ++it) {
-                float v = group_sum(acc[it], G.lpr);
-                if (item.shared) v = v * sig;
-                const int r = row0 + it * G.rpi + grp;
-                if (live[it] && l == 0) Y[(size_t)(item.first + c0 + c) * H + r] = v;
-            }
+            int it;
+            float v = group_sum_rs<NIT>(acc, G.lpr, lane, it);
+            if (item.shared) v = v * sig;
+            const int r = row0 + it * G.rpi + grp;
+            if (r < H && (l & 3) == 0 && (NIT > 1 || l == 0)) Y[(size_t)(item.first + c0 + c) * H + r] = v;
         }
         __syncthreads();
     }
@@ -769,6 +814,14 @@ __global__ __launch_bounds__(256) void k_q2_mmvq(const uint8_t* __restrict__ w, 
         for (int m = 0; m < MAXUPL; ++m)
             if (live[it] && m < G.upl) load_unit(w + (size_t)r * rb + (size_t)(l + G.lpr * m) * 36, wr[it][m]);
     }
+    float dw[NIT][MAXUPL][2];
+#pragma unroll
+    for (int it = 0; it < NIT; ++it)
+#pragma unroll
+        for (int m = 0; m < MAXUPL; ++m) {
+            dw[it][m][0] = unit_d0(wr[it][m]);
+            dw[it][m][1] = unit_d1(wr[it][m]);
+        }
     const int xb = n_in >> 5;
     for (int c = 0; c < n_col; ++c) {
         pin_units(wr);
@@ -780,17 +833,15 @@ __global__ __launch_bounds__(256) void k_q2_mmvq(const uint8_t* __restrict__ w, 
                 load_act_std(xq + ((size_t)c * xb + 4 * (l + G.lpr * m)) * 36, a);
 #pragma unroll
                 for (int it = 0; it < NIT; ++it) {
-                    const float L = q2_unit_dot(wr[it][m], a);
+                    const float L = q2_unit_dot(wr[it][m], dw[it][m][0], dw[it][m][1], a);
                     acc[it] = m == 0 ? L : acc[it] + L;
                 }
             }
         }
-#pragma unroll
-        for (int it = 0; it < NIT; ++it) {
-            const float v = group_sum(acc[it], G.lpr);
-            const int r = row0 + it * G.rpi + grp;
-            if (live[it] && l == 0) y[(size_t)c * n_out + r] = v;
-        }
+        int it;
+        const float v = group_sum_rs<NIT>(acc, G.lpr, lane, it);
+        const int r = row0 + it * G.rpi + grp;
+        if (r < n_out && (l & 3) == 0 && (NIT > 1 || l == 0)) y[(size_t)c * n_out + r] = v;
     }
 }
 

@@ -197,14 +197,30 @@ __device__ __forceinline__ void load_act_std(const uint8_t* __restrict__ blk, Ac
     }
 }
 
-// Copies the q8_1 images of `nc` columns (qb blocks each) into LDS, 16 bytes per thread per step.
+// Copies the q8_1 images of `nc` columns (qb blocks each) into LDS.  Four 16-byte pieces per thread per round,
+// with every address computed and every load issued (clamped to a valid piece) before the first store, so a
+// round costs one memory round trip instead of one per piece.
 __device__ __forceinline__ void stage_images(uint32_t* act, const uint32_t* __restrict__ img, int qb, int c0, int nc,
                                              const Item& it, const int32_t* perm, int k, bool by_token) {
     const int per_col = qb * (kImgDw / 4);  // uint4 per column
-    for (int idx = threadIdx.x; idx < nc * per_col; idx += 256) {
-        const int c = idx / per_col, r = idx - c * per_col;
-        const int row = by_token ? item_token(it, perm, k, c0 + c) : it.first + c0 + c;
-        reinterpret_cast<uint4*>(act)[idx] = reinterpret_cast<const uint4*>(img)[(size_t)row * per_col + r];
+    const int total = nc * per_col;
+    for (int base = 0; base < total; base += 4 * 256) {
+        int row[4], r[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int idx = min(base + j * 256 + (int)threadIdx.x, total - 1);
+            const int c = idx / per_col;
+            r[j] = idx - c * per_col;
+            row[j] = by_token ? item_token(it, perm, k, c0 + c) : it.first + c0 + c;
+        }
+        uint4 v[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = reinterpret_cast<const uint4*>(img)[(size_t)row[j] * per_col + r[j]];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int idx = base + j * 256 + (int)threadIdx.x;
+            if (idx < total) reinterpret_cast<uint4*>(act)[idx] = v[j];
+        }
     }
 }
 
