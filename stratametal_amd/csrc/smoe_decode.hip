@@ -59,6 +59,23 @@ __device__ __forceinline__ float unit_d1(const uint32_t (&w)[9]) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)(w[4] >> 16));
 }
 
+// A unit's first block (P0 + P1, activation images 0 and 1) and second block (P2, P3, images 2 and 3), so that
+// only two images are live at a time; q2_unit_dot's order is L = ((P0 + P1) + P2) + P3.
+__device__ __forceinline__ float q2_unit_first(const uint32_t (&w)[9], float d0, const Act2& a) {
+    const uint32_t c0 = __builtin_amdgcn_alignbyte(w[1], w[0], 2);
+    const uint32_t c1 = __builtin_amdgcn_alignbyte(w[2], w[1], 2);
+    const uint32_t c2 = __builtin_amdgcn_alignbyte(w[3], w[2], 2);
+    const uint32_t c3 = __builtin_amdgcn_alignbyte(w[4], w[3], 2);
+    const float P0 = (d0 * a.d[0]) * (float)(half_dot(c0, c1, a.q[0]) - a.sq[0]);
+    const float P1 = (d0 * a.d[1]) * (float)(half_dot(c2, c3, a.q[1]) - a.sq[1]);
+    return P0 + P1;
+}
+__device__ __forceinline__ float q2_unit_second(const uint32_t (&w)[9], float d1, float p01, const Act2& a) {
+    const float P2 = (d1 * a.d[0]) * (float)(half_dot(w[5], w[6], a.q[0]) - a.sq[0]);
+    const float P3 = (d1 * a.d[1]) * (float)(half_dot(w[7], w[8], a.q[1]) - a.sq[1]);
+    return (p01 + P2) + P3;
+}
+
 __device__ __forceinline__ float q2_unit_dot(const uint32_t (&w)[9], float d0, float d1, const Act4& a) {
     const uint32_t c0 = __builtin_amdgcn_alignbyte(w[1], w[0], 2);
     const uint32_t c1 = __builtin_amdgcn_alignbyte(w[2], w[1], 2);
@@ -454,30 +471,45 @@ __global__ __launch_bounds__(64) void k_topk(const float* __restrict__ logits, i
 // atomics (order-free), offsets by an exclusive scan, ranks by a ballot match inside each wave plus per-wave
 // counts in LDS, 1024 pairs per pass: position = offsets[e] + (number of earlier pairs with expert e) (oracle:
 // or_dispatch).  Also the ascending list of touched experts.  An out-of-range id gets slot -1.
-__device__ __forceinline__ int block_exclusive_scan_1024(int v, int* scratch /*>= 17 ints*/, int* total) {
+// Three exclusive scans over the 1024 threads of the block at once: shuffles inside each wave, then wave 0
+// scans the 16 wave totals with shuffles (scratch: 3 x 17 ints).
+__device__ __forceinline__ void block_exclusive_scan3_1024(const int (&v)[3], int* scratch, int (&r)[3],
+                                                           int (&total)[3]) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    int incl = v;
+    int incl[3] = {v[0], v[1], v[2]};
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
-        const int u = __shfl_up(incl, o, kWave);
-        if (lane >= o) incl += u;
-    }
-    if (lane == 63) scratch[wave] = incl;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        int run = 0;
-        for (int w = 0; w < 16; ++w) {
-            const int c = scratch[w];
-            scratch[w] = run;
-            run += c;
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+            const int u = __shfl_up(incl[j], o, kWave);
+            if (lane >= o) incl[j] += u;
         }
-        scratch[16] = run;
+    }
+    if (lane == 63) {
+#pragma unroll
+        for (int j = 0; j < 3; ++j) scratch[17 * j + wave] = incl[j];
     }
     __syncthreads();
-    const int r = scratch[wave] + incl - v;
-    *total = scratch[16];
+    if (wave == 0) {
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+            const int w = lane < 16 ? scratch[17 * j + lane] : 0;
+            int x = w;
+#pragma unroll
+            for (int o = 1; o < 16; o <<= 1) {
+                const int u = __shfl_up(x, o, kWave);
+                if (lane >= o) x += u;
+            }
+            if (lane < 16) scratch[17 * j + lane] = x - w;
+            if (lane == 15) scratch[17 * j + 16] = x;
+        }
+    }
     __syncthreads();
-    return r;
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+        r[j] = scratch[17 * j + wave] + incl[j] - v[j];
+        total[j] = scratch[17 * j + 16];
+    }
 }
 
 struct DispatchLds {
@@ -486,7 +518,7 @@ struct DispatchLds {
     int cb[1024];
     int el[1024];
     uint8_t wcnt[16][1024];
-    int scan[17];
+    int scan[3 * 17];
 };
 
 // With `items`, also the work-item table: expert e's pairs in chunks of at most `chunk` columns (items in
@@ -499,7 +531,8 @@ __device__ void dispatch_block(const int32_t* __restrict__ ids, int P, int E, in
                                int has_shared = 0, int chunk = 1 << 30, int sh_chunk = kShCols) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     s.cnt[tid] = 0;
-    for (int w = 0; w < 16; ++w) s.wcnt[w][tid] = 0;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) reinterpret_cast<uint32_t*>(&s.wcnt[0][0])[w * 1024 + tid] = 0u;
     __syncthreads();
     for (int i = tid; i < P; i += 1024) {
         const int e = ids[i];
@@ -507,14 +540,12 @@ __device__ void dispatch_block(const int32_t* __restrict__ ids, int P, int E, in
     }
     __syncthreads();
     const int c = tid < E ? s.cnt[tid] : 0;
-    int total;
-    const int off = block_exclusive_scan_1024(c, s.scan, &total);
     const int flag = c > 0 ? 1 : 0;
-    int n_touched;
-    const int fpos = block_exclusive_scan_1024(flag, s.scan, &n_touched);
     const int nch = c > 0 ? (c - 1) / chunk + 1 : 0;
-    int n_rc;
-    const int cbase = block_exclusive_scan_1024(nch, s.scan, &n_rc);
+    int sc[3], tot[3];
+    block_exclusive_scan3_1024({c, flag, nch}, s.scan, sc, tot);
+    const int off = sc[0], fpos = sc[1], cbase = sc[2];
+    const int total = tot[0], n_touched = tot[1], n_rc = tot[2];
     if (tid < E) {
         s.cb[tid] = cbase;
         if (counts) counts[tid] = c;
@@ -696,11 +727,16 @@ __global__ __launch_bounds__(256) void k_q2_gu(const uint8_t* __restrict__ gate_
 #pragma unroll
             for (int m = 0; m < MAXUPL; ++m) {
                 if (m < G.upl) {
-                    Act4 a;
-                    load_act_img(xt + (size_t)(4 * (l + G.lpr * m)) * kImgDw, a);
+                    const uint32_t* img = xt + (size_t)(4 * (l + G.lpr * m)) * kImgDw;
+                    float p01[NIT];
+                    Act2 a;
+                    load_act_img2(img, a);
+#pragma unroll
+                    for (int it = 0; it < NIT; ++it) p01[it] = q2_unit_first(w[it][m], dw[it][m][0], a);
+                    load_act_img2(img + 2 * kImgDw, a);
 #pragma unroll
                     for (int it = 0; it < NIT; ++it) {
-                        const float L = q2_unit_dot(w[it][m], dw[it][m][0], dw[it][m][1], a);
+                        const float L = q2_unit_second(w[it][m], dw[it][m][1], p01[it], a);
                         acc[it] = m == 0 ? L : acc[it] + L;
                     }
                 }
@@ -773,11 +809,16 @@ __global__ __launch_bounds__(256) void k_q2_down(const uint8_t* __restrict__ dow
 #pragma unroll
             for (int m = 0; m < MAXUPL; ++m) {
                 if (m < G.upl) {
-                    Act4 a;
-                    load_act_img(ht + (size_t)(4 * (l + G.lpr * m)) * kImgDw, a);
+                    const uint32_t* img = ht + (size_t)(4 * (l + G.lpr * m)) * kImgDw;
+                    float p01[NIT];
+                    Act2 a;
+                    load_act_img2(img, a);
+#pragma unroll
+                    for (int it = 0; it < NIT; ++it) p01[it] = q2_unit_first(w[it][m], dw[it][m][0], a);
+                    load_act_img2(img + 2 * kImgDw, a);
 #pragma unroll
                     for (int it = 0; it < NIT; ++it) {
-                        const float L = q2_unit_dot(w[it][m], dw[it][m][0], dw[it][m][1], a);
+                        const float L = q2_unit_second(w[it][m], dw[it][m][1], p01[it], a);
                         acc[it] = m == 0 ? L : acc[it] + L;
                     }
                 }

@@ -158,6 +158,24 @@ struct Act4 {
     int sq[4];
 };
 
+// Two consecutive q8_1 images (half a Q2_0 unit's activations).
+struct Act2 {
+    uint32_t q[2][8];
+    float d[2];
+    int sq[2];
+};
+__device__ __forceinline__ void load_act_img2(const uint32_t* __restrict__ img, Act2& a) {
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+        const uint4* p = reinterpret_cast<const uint4*>(img + b * kImgDw);
+        const uint4 lo = p[0], hi = p[1], ds = p[2];
+        a.q[b][0] = lo.x; a.q[b][1] = lo.y; a.q[b][2] = lo.z; a.q[b][3] = lo.w;
+        a.q[b][4] = hi.x; a.q[b][5] = hi.y; a.q[b][6] = hi.z; a.q[b][7] = hi.w;
+        a.d[b] = u2f(ds.x);
+        a.sq[b] = (int)ds.y;
+    }
+}
+
 __device__ __forceinline__ void load_act_img(const uint32_t* __restrict__ img, Act4& a) {
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
