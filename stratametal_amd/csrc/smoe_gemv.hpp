@@ -215,18 +215,20 @@ __device__ __forceinline__ void load_act_std(const uint8_t* __restrict__ blk, Ac
     }
 }
 
-// Copies the q8_1 images of `nc` columns (qb blocks each) into LDS.  Four 16-byte pieces per thread per round,
+// Copies the q8_1 images of `nc` columns (qb blocks each) into LDS (any block size).  Four 16-byte pieces per
+// thread per round,
 // with every address computed and every load issued (clamped to a valid piece) before the first store, so a
 // round costs one memory round trip instead of one per piece.
 __device__ __forceinline__ void stage_images(uint32_t* act, const uint32_t* __restrict__ img, int qb, int c0, int nc,
                                              const Item& it, const int32_t* perm, int k, bool by_token) {
     const int per_col = qb * (kImgDw / 4);  // uint4 per column
     const int total = nc * per_col;
-    for (int base = 0; base < total; base += 4 * 256) {
+    const int nt = (int)blockDim.x;
+    for (int base = 0; base < total; base += 4 * nt) {
         int row[4], r[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const int idx = min(base + j * 256 + (int)threadIdx.x, total - 1);
+            const int idx = min(base + j * nt + (int)threadIdx.x, total - 1);
             const int c = idx / per_col;
             r[j] = idx - c * per_col;
             row[j] = by_token ? item_token(it, perm, k, c0 + c) : it.first + c0 + c;
@@ -236,7 +238,7 @@ __device__ __forceinline__ void stage_images(uint32_t* act, const uint32_t* __re
         for (int j = 0; j < 4; ++j) v[j] = reinterpret_cast<const uint4*>(img)[(size_t)row[j] * per_col + r[j]];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const int idx = base + j * 256 + (int)threadIdx.x;
+            const int idx = base + j * nt + (int)threadIdx.x;
             if (idx < total) reinterpret_cast<uint4*>(act)[idx] = v[j];
         }
     }

@@ -143,64 +143,52 @@ __device__ __forceinline__ float iq2_block_dot_std(const Iq2Block& B, const uint
 }
 
 // ------------------------------------------------------------------------------------------------ gate/up
-// Grid (Fmax / 32, work items), 4 waves.  Wave w computes gate rows [32 hb + 8 w, +8) (rho 0..7) and the
-// same up rows (rho 8..15), nb lanes per row, NIT passes of 64 / nb rows; columns in stages of kGuColsIq2:
-// their x images are copied to LDS, every column's row values parked in LDS, then each half wave quantises
-// one column's 32 h values into natural-order image block hb.
-constexpr int kGuColsIq2 = 8;
-
-template <int NIT>
-__global__ __launch_bounds__(256) void k_iq2_gu(const uint8_t* __restrict__ gate_exps, const uint8_t* __restrict__ up_exps,
-                                                 const uint8_t* __restrict__ gate_sh, const uint8_t* __restrict__ up_sh,
-                                                 const uint32_t* __restrict__ ximg, const int4* __restrict__ items,
-                                                 const int32_t* __restrict__ perm, int k, int H, int F, int Fs,
-                                                 uint32_t* __restrict__ himg, int h_blocks) {
+// Grid (Fmax / 32, work items), NW = nb waves (64 NW threads).  The work-group computes gate rows
+// [32 hb, 32 hb + 32) and the same up rows: row rho = wave * (64 / nb) + lane / nb (rho < 32 gate, else up),
+// nb lanes per row, one block per lane, decoded once.  Columns go in stages of 2 NW: their x images are
+// copied to LDS, every column's 64 row values parked in LDS, then each half wave quantises one column's 32 h
+// values into natural-order image block hb.
+template <int NW>
+__global__ __launch_bounds__(64 * NW) void k_iq2_gu(const uint8_t* __restrict__ gate_exps, const uint8_t* __restrict__ up_exps,
+                                                     const uint8_t* __restrict__ gate_sh, const uint8_t* __restrict__ up_sh,
+                                                     const uint32_t* __restrict__ ximg, const int4* __restrict__ items,
+                                                     const int32_t* __restrict__ perm, int k, int H, int F, int Fs,
+                                                     uint32_t* __restrict__ himg, int h_blocks) {
+    constexpr int kCols = 2 * NW;
     extern __shared__ __align__(16) uint32_t smem[];
     __shared__ uint2 tab[1024];
-    __shared__ float rowv[kGuColsIq2][64];
-    __shared__ uint8_t qsc[8][32];
+    __shared__ float rowv[kCols][64];
+    __shared__ uint8_t qsc[kCols][32];
     Item item;
     if (!work_item(items, blockIdx.y, item)) return;
     const int hb = blockIdx.x;
     const int Fe = item.shared ? Fs : F;
     if (hb * 32 >= Fe) return;
-    build_grid_table(tab);
-    const int nb = H >> 8;
+    const int nb = H >> 8;  // == NW
     const size_t rb = (size_t)nb * 82;
-    const uint8_t* g0 = item.shared ? gate_sh : gate_exps + (size_t)item.e * F * rb;
-    const uint8_t* u0 = item.shared ? up_sh : up_exps + (size_t)item.e * F * rb;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int rpi = 64 / nb, grp = lane / nb, b = lane - grp * nb;
+    const int rho = wave * (64 / nb) + lane / nb, b = lane % nb;
+    const uint8_t* base = (rho < 32 ? (item.shared ? gate_sh : gate_exps + (size_t)item.e * F * rb)
+                                    : (item.shared ? up_sh : up_exps + (size_t)item.e * F * rb));
+    const uint8_t* rowp = base + (size_t)(32 * hb + (rho & 31)) * rb;
+    uint32_t raw[21];
+    int off;
+    load_block_raw(rowp, b, raw, off);  // issued before the table build, so its latency overlaps it
+    build_grid_table(tab);
     const int qb = H >> 5;
     __syncthreads();
+    Iq2Block B[1];
+    decode_block(raw, off, tab, B[0]);
 
-    Iq2Block B[NIT];
-    bool live[NIT];
-#pragma unroll
-    for (int it = 0; it < NIT; ++it) {
-        const int rho = it * rpi + grp;
-        live[it] = rho < 16;
-        const int r = 32 * hb + 8 * wave + (rho & 7);
-        const uint8_t* rowp = ((rho & 8) ? u0 : g0) + (size_t)r * rb;
-        uint32_t raw[21];
-        int off;
-        load_block_raw(rowp, b, raw, off);
-        decode_block(raw, off, tab, B[it]);
-    }
-
-    for (int c0 = 0; c0 < item.ncol; c0 += kGuColsIq2) {
-        const int nc = min(kGuColsIq2, item.ncol - c0);
+    for (int c0 = 0; c0 < item.ncol; c0 += kCols) {
+        const int nc = min(kCols, item.ncol - c0);
         stage_images(smem, ximg, qb, c0, nc, item, perm, k, true);
         __syncthreads();
         for (int c = 0; c < nc; ++c) {
             const uint32_t* xt = smem + (size_t)c * qb * kImgDw;
             pin_blocks(B);
-#pragma unroll
-            for (int it = 0; it < NIT; ++it) {
-                const float v = group_sum(iq2_block_dot_img(B[it], xt, b), nb);
-                const int rho = it * rpi + grp;
-                if (live[it] && b == 0) rowv[c][(rho < 8 ? 0 : 32) + 8 * wave + (rho & 7)] = v;
-            }
+            const float v = group_sum(iq2_block_dot_img(B[0], xt, b), nb);
+            if (b == 0) rowv[c][rho] = v;
         }
         __syncthreads();
         {
@@ -300,12 +288,15 @@ hipError_t launch_iq2_gu(const uint8_t* gate_exps, const uint8_t* up_exps, const
                          int has_shared, int max_items, uint32_t* himg, int h_blocks, hipStream_t s) {
     const int Fmax = has_shared && Fs > F ? Fs : F;
     dim3 grid((unsigned)(Fmax / 32), (unsigned)max_items);
-    const int nb = H / 256, rpi = 64 / nb;
-    const size_t lds = (size_t)kGuColsIq2 * (H >> 5) * kImgDw * 4;
-    if (rpi >= 16) hipLaunchKernelGGL((k_iq2_gu<1>), grid, dim3(256), lds, s, gate_exps, up_exps, gate_sh, up_sh, ximg,
-                                      items, perm, k, H, F, Fs, himg, h_blocks);
-    else hipLaunchKernelGGL((k_iq2_gu<2>), grid, dim3(256), lds, s, gate_exps, up_exps, gate_sh, up_sh, ximg, items,
-                            perm, k, H, F, Fs, himg, h_blocks);
+    const int nb = H / 256;
+    const size_t lds = (size_t)(2 * nb) * (H >> 5) * kImgDw * 4;
+#define SMOE_IQ2_GU(NW)                                                                                           \
+    hipLaunchKernelGGL((k_iq2_gu<NW>), grid, dim3(64 * (NW)), lds, s, gate_exps, up_exps, gate_sh, up_sh, ximg, items, \
+                       perm, k, H, F, Fs, himg, h_blocks)
+    if (nb == 2) SMOE_IQ2_GU(2);
+    else if (nb == 4) SMOE_IQ2_GU(4);
+    else SMOE_IQ2_GU(8);
+#undef SMOE_IQ2_GU
     return hipGetLastError();
 }
 
