@@ -335,6 +335,11 @@ def main():
             "achieved": m16["gate_up_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": m16["gate_up_gbs"] / HBM_PEAK_GBS, "traffic": None,
             "algorithmic_bytes_per_launch": m16["gate_up_bytes"], "avg_launch_ms": gu_ms}
+    tj = os.path.join(ROOT, "profiles", "decode_b16_traffic.json")
+    if os.path.exists(tj):  # HBM bytes per launch from the FETCH_SIZE / WRITE_SIZE counter runs (calibrated)
+        t = json.load(open(tj))
+        roof["traffic"] = t["traffic_bytes"]
+        roof["traffic_source"] = t["source"]
     cpu = None
     if not a.no_cpu:
         cpu = cpu_baseline(g, a.tokens, a.seed, a.cpu_seconds)

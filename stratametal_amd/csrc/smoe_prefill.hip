@@ -98,20 +98,6 @@ __device__ __forceinline__ void expand_codes(uint32_t cw, bf16x8& s0, bf16x8& s1
               __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(x, 2.0f, 3), __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(y, 2.0f, 3));
 }
 
-// One 36-byte unit (two Q2_0 blocks) of a lane's weight row, staged in LDS: codes and scales of quarter q.
-struct UnitB {
-    bf16x8 b[2][2];  // [block][step]
-    float d[2];
-};
-__device__ __forceinline__ void load_unit_b(const uint32_t* w, int q, UnitB& u) {
-    const uint32_t c0 = __builtin_amdgcn_alignbyte(w[q + 1], w[q], 2);
-    const uint32_t c1 = w[5 + q];
-    u.d[0] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[0] & 0xFFFFu));  // exact, subnormals included
-    u.d[1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[4] >> 16));
-    expand_codes(c0, u.b[0][0], u.b[0][1]);
-    expand_codes(c1, u.b[1][0], u.b[1][1]);
-}
-
 // Staging of one 128-value unit through registers: the global loads of unit u + 1 are issued before the
 // matrix work on unit u, and land in LDS after it.  Thread t loads the 36-byte unit of weight row t
 // (t < nrows) and up to kStageA 16-byte chunks of the columns' activation records: chunk idx = t + 256 m is
@@ -165,67 +151,60 @@ __device__ __forceinline__ f32x4 neg_sums(const uint32_t* act, int n, int h, int
     return f32x4{u2f(p[0]), u2f(p[kActStride]), u2f(p[2 * kActStride]), u2f(p[3 * kActStride])};
 }
 
-// acc[n] += d * (C = -A; C += A0 B0; C += A1 B1) for block h of the staged unit, every live tile n.
-template <int NT>
-__device__ __forceinline__ void mma_block(f32x4 (&acc)[NT], const bf16x8& b0, const bf16x8& b1, float d,
-                                          const uint32_t* act, int h, int ntiles, int i,
-                                          int q) {
+// One staged unit against NS weight-row sets per wave: for block h of the unit, the B operands of the NS sets
+// (lane row i of set s at LDS row rows[s]) are expanded, then every live token tile n loads its activation
+// fragments once and feeds all NS sets: acc[n][s] += d_s * (C = -A; C += A0 B0; C += A1 B1).
+template <int NS>
+__device__ __forceinline__ void mma_unit(f32x4 (&acc)[kTiles][NS], const uint32_t* wt, const int (&rows)[NS],
+                                         const uint32_t* act, int ntiles, int i, int q) {
 #pragma unroll
-    for (int n = 0; n < NT; ++n) {
-        if (n < ntiles) {
-            const uint32_t* ar = act + (16 * n + i) * kActStride + h * kRecDw;
-            const bf16x8 a0 = *reinterpret_cast<const bf16x8*>(ar + 4 * q);
-            const bf16x8 a1 = *reinterpret_cast<const bf16x8*>(ar + 16 + 4 * q);
-            f32x4 c = neg_sums(act, n, h, q);
-            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b0, c, 0, 0, 0);
-            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1, c, 0, 0, 0);
+    for (int h = 0; h < 2; ++h) {
+        bf16x8 b0[NS], b1[NS];
+        float d[NS];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) acc[n][r] = __builtin_fmaf(d, c[r], acc[n][r]);
+        for (int s = 0; s < NS; ++s) {
+            const uint32_t* w = wt + rows[s] * 9;
+            const uint32_t cw = h == 0 ? __builtin_amdgcn_alignbyte(w[q + 1], w[q], 2) : w[5 + q];
+            d[s] = h == 0 ? (float)__builtin_bit_cast(_Float16, (uint16_t)(w[0] & 0xFFFFu))
+                          : (float)__builtin_bit_cast(_Float16, (uint16_t)(w[4] >> 16));
+            expand_codes(cw, b0[s], b1[s]);
         }
-    }
-}
-
-// The same for two weight rows sharing the activation fragments (gate and up).
-template <int NT>
-__device__ __forceinline__ void mma_block2(f32x4 (&acc)[NT], f32x4 (&acc2)[NT], const UnitB& g, const UnitB& v,
-                                           const uint32_t* act, int h, int ntiles, int i,
-                                           int q) {
 #pragma unroll
-    for (int n = 0; n < NT; ++n) {
-        if (n < ntiles) {
-            const uint32_t* ar = act + (16 * n + i) * kActStride + h * kRecDw;
-            const bf16x8 a0 = *reinterpret_cast<const bf16x8*>(ar + 4 * q);
-            const bf16x8 a1 = *reinterpret_cast<const bf16x8*>(ar + 16 + 4 * q);
-            const f32x4 na = neg_sums(act, n, h, q);
-            f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, g.b[h][0], na, 0, 0, 0);
-            f32x4 c2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, v.b[h][0], na, 0, 0, 0);
-            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, g.b[h][1], c, 0, 0, 0);
-            c2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, v.b[h][1], c2, 0, 0, 0);
+        for (int n = 0; n < kTiles; ++n) {
+            if (n < ntiles) {
+                const uint32_t* ar = act + (16 * n + i) * kActStride + h * kRecDw;
+                const bf16x8 a0 = *reinterpret_cast<const bf16x8*>(ar + 4 * q);
+                const bf16x8 a1 = *reinterpret_cast<const bf16x8*>(ar + 16 + 4 * q);
+                const f32x4 na = neg_sums(act, n, h, q);
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                acc[n][r] = __builtin_fmaf(g.d[h], c[r], acc[n][r]);
-                acc2[n][r] = __builtin_fmaf(v.d[h], c2[r], acc2[n][r]);
+                for (int s = 0; s < NS; ++s) {
+                    f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b0[s], na, 0, 0, 0);
+                    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1[s], c, 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc[n][s][r] = __builtin_fmaf(d[s], c[r], acc[n][s][r]);
+                }
             }
         }
     }
 }
 
 // ------------------------------------------------------------------------------------------------ gate/up
-// Grid (Fmax / 64, work items).  Work-group rt of an item computes gate and up rows [64 rt, 64 rt + 64) for
-// the item's columns, h = bf16(silu(gate) * up), and writes record rt of each column's h row.
+// Grid (Fmax / 128, work items).  Work-group rt of an item computes gate and up rows [128 rt, 128 rt + 128)
+// for the item's columns: wave w the rows 32 w .. 32 w + 31 of each (sets 0, 1 gate; 2, 3 up), then
+// h = bf16(silu(gate) * up) into records 2 rt and 2 rt + 1 of each column's h row.
 __global__ __launch_bounds__(256) void k_mm_gu(const uint8_t* __restrict__ gate_exps, const uint8_t* __restrict__ up_exps,
                                                const uint8_t* __restrict__ gate_sh, const uint8_t* __restrict__ up_sh,
                                                const uint32_t* __restrict__ xrec, const int4* __restrict__ items,
                                                const int32_t* __restrict__ perm, int k, int H, int F, int Fs,
                                                uint32_t* __restrict__ hrec, int h_rec) {
-    __shared__ uint32_t wt[128 * 9];
+    __shared__ uint32_t wt[256 * 9];
     __shared__ __align__(16) uint32_t act[kChunk * kActStride + 4];
     __shared__ int rowidx[kChunk];
     Item item;
     if (!work_item(items, blockIdx.y, item)) return;
     const int rt = blockIdx.x;
     const int Fe = item.shared ? Fs : F;
-    if (64 * rt >= Fe) return;
+    if (128 * rt >= Fe) return;
     const int ncol = item.ncol, ntiles = (ncol + 15) >> 4;
     const int units = H >> 7;
     const size_t rb = (size_t)units * 36;
@@ -234,48 +213,47 @@ __global__ __launch_bounds__(256) void k_mm_gu(const uint8_t* __restrict__ gate_
     __syncthreads();
     Stager stg;
     {
-        const int r = tid & 127;  // threads 128.. repeat rows 0..127 without storing them
-        const uint8_t* base = r < 64 ? (item.shared ? gate_sh : gate_exps + (size_t)item.e * F * rb)
-                                     : (item.shared ? up_sh : up_exps + (size_t)item.e * F * rb);
-        stg.init(base + (size_t)(64 * rt + (r & 63)) * rb, tid < 128, xrec, rowidx, ncol, H >> 6);
+        const uint8_t* base = tid < 128 ? (item.shared ? gate_sh : gate_exps + (size_t)item.e * F * rb)
+                                        : (item.shared ? up_sh : up_exps + (size_t)item.e * F * rb);
+        stg.init(base + (size_t)(128 * rt + (tid & 127)) * rb, true, xrec, rowidx, ncol, H >> 6);
     }
     stg.load(0);
+    const int rows[4] = {32 * wave + i, 32 * wave + 16 + i, 128 + 32 * wave + i, 128 + 32 * wave + 16 + i};
 
-    f32x4 accg[kTiles], accu[kTiles];
+    f32x4 acc[kTiles][4];
 #pragma unroll
-    for (int n = 0; n < kTiles; ++n) {
-        accg[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        accu[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    }
+    for (int n = 0; n < kTiles; ++n)
+#pragma unroll
+        for (int s = 0; s < 4; ++s) acc[n][s] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     for (int u = 0; u < units; ++u) {
         stg.store(wt, reinterpret_cast<uint4*>(act));
         __syncthreads();
         if (u + 1 < units) stg.load(u + 1);
-        UnitB g, v;
-        load_unit_b(wt + (16 * wave + i) * 9, q, g);
-        load_unit_b(wt + (64 + 16 * wave + i) * 9, q, v);
-#pragma unroll
-        for (int h = 0; h < 2; ++h) mma_block2<kTiles>(accg, accu, g, v, act, h, ntiles, i, q);
+        mma_unit<4>(acc, wt, rows, act, ntiles, i, q);
         __syncthreads();
     }
-    // h tile [column][record position] as bf16 in the activation buffer
+    // h tile [column][128 rows in record order] as bf16 in the activation buffer
     uint16_t* ht = reinterpret_cast<uint16_t*>(act);
-    const int pos = rec_pos(16 * wave + i);
 #pragma unroll
-    for (int n = 0; n < kTiles; ++n) {
-        if (n < ntiles) {
+    for (int s = 0; s < 2; ++s) {
+        const int f = 32 * wave + 16 * s + i;  // row within the work-group's 128
+        const int pos = 64 * (f >> 6) + rec_pos(f & 63);
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int c = 16 * n + 4 * q + r;
-                if (c < ncol) ht[c * 64 + pos] = (uint16_t)f32_to_bf16(silu_mul(accg[n][r], accu[n][r]));
+        for (int n = 0; n < kTiles; ++n) {
+            if (n < ntiles) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int c = 16 * n + 4 * q + r;
+                    if (c < ncol) ht[c * 128 + pos] = (uint16_t)f32_to_bf16(silu_mul(acc[n][s][r], acc[n][s + 2][r]));
+                }
             }
         }
     }
     __syncthreads();
-    for (int base = 0; base < ncol * 8; base += 256) {
-        const int idx = base + tid, c = idx >> 3, ch = idx & 7;
+    for (int base = 0; base < ncol * 16; base += 256) {  // 16 chunks (two records) per column
+        const int idx = base + tid, c = idx >> 4, rr = (idx >> 3) & 1, ch = idx & 7;
         const bool live = c < ncol;
-        const uint4 v = live ? reinterpret_cast<const uint4*>(ht + c * 64)[ch] : make_uint4(0, 0, 0, 0);
+        const uint4 v = live ? reinterpret_cast<const uint4*>(ht + c * 128 + 64 * rr)[ch] : make_uint4(0, 0, 0, 0);
         const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
         float sm = 0.0f;
 #pragma unroll
@@ -284,7 +262,7 @@ __global__ __launch_bounds__(256) void k_mm_gu(const uint8_t* __restrict__ gate_
         sm = sm + __shfl_xor(sm, 2, kWave);
         sm = sm + __shfl_xor(sm, 4, kWave);
         if (live) {
-            uint32_t* dst = hrec + ((size_t)(item.first + c) * h_rec + rt) * kRecDw;
+            uint32_t* dst = hrec + ((size_t)(item.first + c) * h_rec + 2 * rt + rr) * kRecDw;
             reinterpret_cast<uint4*>(dst)[ch] = v;
             if (ch == 0) dst[32] = f2u(-sm);
         }
@@ -292,13 +270,13 @@ __global__ __launch_bounds__(256) void k_mm_gu(const uint8_t* __restrict__ gate_
 }
 
 // ------------------------------------------------------------------------------------------------ down
-// Grid (H / 64, work items).  Work-group rt computes down rows [64 rt, 64 rt + 64) of the item's columns into
-// Y[first + c] (the shared expert's rows times sigmoid(sg[t])).
+// Grid (H / 128, work items).  Work-group rt computes down rows [128 rt, 128 rt + 128) of the item's columns
+// (wave w rows 32 w .. 32 w + 31, two sets) into Y[first + c] (the shared expert's rows times sigmoid(sg[t])).
 __global__ __launch_bounds__(256) void k_mm_down(const uint8_t* __restrict__ down_exps, const uint8_t* __restrict__ down_sh,
                                                  const uint32_t* __restrict__ hrec, int h_rec, const float* __restrict__ sg,
                                                  const int4* __restrict__ items, int H, int F, int Fs,
                                                  float* __restrict__ Y) {
-    __shared__ uint32_t wt[64 * 9];
+    __shared__ uint32_t wt[128 * 9];
     __shared__ __align__(16) uint32_t act[kChunk * kActStride + 4];
     __shared__ int rowidx[kChunk];
     Item item;
@@ -314,34 +292,37 @@ __global__ __launch_bounds__(256) void k_mm_down(const uint8_t* __restrict__ dow
     Stager stg;
     {
         const uint8_t* base = item.shared ? down_sh : down_exps + (size_t)item.e * H * ((size_t)(F >> 7) * 36);
-        stg.init(base + (size_t)(64 * rt + (tid & 63)) * rb, tid < 64, hrec, rowidx, ncol, h_rec);
+        stg.init(base + (size_t)(128 * rt + (tid & 127)) * rb, tid < 128, hrec, rowidx, ncol, h_rec);
     }
     stg.load(0);
+    const int rows[2] = {32 * wave + i, 32 * wave + 16 + i};
 
-    f32x4 acc[kTiles];
+    f32x4 acc[kTiles][2];
 #pragma unroll
-    for (int n = 0; n < kTiles; ++n) acc[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int n = 0; n < kTiles; ++n)
+#pragma unroll
+        for (int s = 0; s < 2; ++s) acc[n][s] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     for (int u = 0; u < units; ++u) {
         stg.store(wt, reinterpret_cast<uint4*>(act));
         __syncthreads();
         if (u + 1 < units) stg.load(u + 1);
-        UnitB g;
-        load_unit_b(wt + (16 * wave + i) * 9, q, g);
-#pragma unroll
-        for (int h = 0; h < 2; ++h) mma_block<kTiles>(acc, g.b[h][0], g.b[h][1], g.d[h], act, h, ntiles, i, q);
+        mma_unit<2>(acc, wt, rows, act, ntiles, i, q);
         __syncthreads();
     }
-    const int col = 64 * rt + 16 * wave + i;
 #pragma unroll
-    for (int n = 0; n < kTiles; ++n) {
-        if (n < ntiles) {
+    for (int s = 0; s < 2; ++s) {
+        const int col = 128 * rt + 32 * wave + 16 * s + i;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int c = 16 * n + 4 * q + r;
-                if (c < ncol) {
-                    float v = acc[n][r];
-                    if (item.shared) v = v * sigmoid(sg[item.tok0 + c]);
-                    Y[(size_t)(item.first + c) * H + col] = v;
+        for (int n = 0; n < kTiles; ++n) {
+            if (n < ntiles) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int c = 16 * n + 4 * q + r;
+                    if (c < ncol) {
+                        float v = acc[n][s][r];
+                        if (item.shared) v = v * sigmoid(sg[item.tok0 + c]);
+                        Y[(size_t)(item.first + c) * H + col] = v;
+                    }
                 }
             }
         }
@@ -361,7 +342,7 @@ hipError_t launch_mm_gu(const uint8_t* gate_exps, const uint8_t* up_exps, const 
                         const uint32_t* xrec, const int4* items, const int32_t* perm, int k, int H, int F, int Fs,
                         int has_shared, int max_items, uint32_t* hrec, int h_rec, hipStream_t s) {
     const int Fmax = has_shared && Fs > F ? Fs : F;
-    hipLaunchKernelGGL(k_mm_gu, dim3((unsigned)(Fmax / 64), (unsigned)max_items), dim3(256), 0, s, gate_exps, up_exps,
+    hipLaunchKernelGGL(k_mm_gu, dim3((unsigned)(Fmax / 128), (unsigned)max_items), dim3(256), 0, s, gate_exps, up_exps,
                        gate_sh, up_sh, xrec, items, perm, k, H, F, Fs, hrec, h_rec);
     return hipGetLastError();
 }
@@ -369,7 +350,7 @@ hipError_t launch_mm_gu(const uint8_t* gate_exps, const uint8_t* up_exps, const 
 hipError_t launch_mm_down(const uint8_t* down_exps, const uint8_t* down_sh, const uint32_t* hrec, int h_rec,
                           const float* sg, const int4* items, int H, int F, int Fs, int max_items, float* Y,
                           hipStream_t s) {
-    hipLaunchKernelGGL(k_mm_down, dim3((unsigned)(H / 64), (unsigned)max_items), dim3(256), 0, s, down_exps, down_sh,
+    hipLaunchKernelGGL(k_mm_down, dim3((unsigned)(H / 128), (unsigned)max_items), dim3(256), 0, s, down_exps, down_sh,
                        hrec, h_rec, sg, items, H, F, Fs, Y);
     return hipGetLastError();
 }
