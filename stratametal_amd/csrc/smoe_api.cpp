@@ -37,8 +37,9 @@ constexpr int kMaxEmbd = 4096;
 constexpr int kMaxFF = 4096;
 constexpr int kMaxExpert = 1024;
 constexpr int kMaxK = 64;
-// Up to this many tokens the q8_1 images, top-k and dispatch run as one work-group (k_route).
-constexpr int kFusedRouteTokens = 64;
+// Up to this many tokens top-k and dispatch run as one work-group (k_topk_dispatch: one wave per token, at most
+// one per SIMD); beyond it the tokens are routed by one work-group each (k_topk), then dispatched (k_dispatch).
+constexpr int kFusedRouteTokens = 4;
 // SMOE_PATH_AUTO runs the MFMA (prefill) contract from this many tokens on.
 constexpr int kMfmaTokens = 128;
 

@@ -2,9 +2,11 @@
 //
 // Decode is a bandwidth-bound dequant-GEMV: each touched expert's 2-bit rows are streamed once with
 // coalesced dwordx4 loads, unpacked in registers and multiplied with v_dot4_i32_i8 against q8_1 activations
-// held in registers.  No MFMA.  The forward call is five launches:
-//   k_router   bf16(x) staged in LDS; router logits and the shared expert's gate dot, one wave per weight row
-//   k_route    one work-group: q8_1 images of x, softmax / top-k per token, canonical stable dispatch
+// held in registers.  No MFMA.  The forward call is five or six launches:
+//   k_router   bf16(x) staged in LDS; router logits and the shared expert's gate dot, one wave per weight row;
+//              also the q8_1 images of x
+//   k_topk_dispatch (up to 4 tokens) or k_topk + k_dispatch: softmax / top-k, one wave per token, then the
+//              canonical stable dispatch in one work-group
 //   k_q2_gu    per (touched expert | shared, 32 rows of h): gate and up rows, SwiGLU, q8_1 image of h
 //   k_q2_down  per (touched expert | shared, a chunk of output rows): down rows (times the shared gate)
 //   k_combine  y = routing-weighted sum of the pair rows + the shared row
@@ -367,7 +369,7 @@ constexpr Cmp kNet16[63] = {{0, 1}, {2, 3}, {4, 5}, {6, 7}, {8, 9}, {10, 11}, {1
 // p_i = ex_i / S; w_i = p_i / max(sum of the k p_i in selection order, 2^-14)
 // (metal/shaders/router.metal:30-132; oracle: or_route_dev).
 template <int J>
-__device__ void route_token_t(const float* __restrict__ l, int E, int k, int32_t* __restrict__ ids,
+__device__ __forceinline__ void route_token_t(const float* __restrict__ l, int E, int k, int32_t* __restrict__ ids,
                               float* __restrict__ wts) {
     const int lane = threadIdx.x & 63;
     uint32_t key[J];
@@ -471,47 +473,43 @@ __global__ __launch_bounds__(64) void k_topk(const float* __restrict__ logits, i
 // atomics (order-free), offsets by an exclusive scan, ranks by a ballot match inside each wave plus per-wave
 // counts in LDS, 1024 pairs per pass: position = offsets[e] + (number of earlier pairs with expert e) (oracle:
 // or_dispatch).  Also the ascending list of touched experts.  An out-of-range id gets slot -1.
-// Three exclusive scans over the 1024 threads of the block at once: shuffles inside each wave, then wave 0
-// scans the 16 wave totals with shuffles (scratch: 3 x 17 ints).
+// Inclusive prefix sum over the 64 lanes of a wave by DPP: row shifts by 1, 2, 4 and 8 (zero fill at the
+// start of each 16-lane row), then lane 15 of each row added into the next row (rows 1 and 3) and lane 31
+// into rows 2 and 3.
+__device__ __forceinline__ int wave_inclusive_scan(int x) {
+    x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, true);   // row_shr:1
+    x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, true);   // row_shr:2
+    x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, true);   // row_shr:4
+    x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, true);   // row_shr:8
+    x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xA, 0xF, false);  // row_bcast:15
+    x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xC, 0xF, false);  // row_bcast:31
+    return x;
+}
+
+// Three exclusive scans over the 1024 threads of the block at once: a DPP scan inside each wave, the 16 wave
+// totals through LDS (scratch: 3 x 17 ints), then every wave scans the totals itself (one barrier).
 __device__ __forceinline__ void block_exclusive_scan3_1024(const int (&v)[3], int* scratch, int (&r)[3],
                                                            int (&total)[3]) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    int incl[3] = {v[0], v[1], v[2]};
+    int incl[3];
 #pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-#pragma unroll
-        for (int j = 0; j < 3; ++j) {
-            const int u = __shfl_up(incl[j], o, kWave);
-            if (lane >= o) incl[j] += u;
-        }
-    }
+    for (int j = 0; j < 3; ++j) incl[j] = wave_inclusive_scan(v[j]);
     if (lane == 63) {
 #pragma unroll
         for (int j = 0; j < 3; ++j) scratch[17 * j + wave] = incl[j];
     }
     __syncthreads();
-    if (wave == 0) {
-#pragma unroll
-        for (int j = 0; j < 3; ++j) {
-            const int w = lane < 16 ? scratch[17 * j + lane] : 0;
-            int x = w;
-#pragma unroll
-            for (int o = 1; o < 16; o <<= 1) {
-                const int u = __shfl_up(x, o, kWave);
-                if (lane >= o) x += u;
-            }
-            if (lane < 16) scratch[17 * j + lane] = x - w;
-            if (lane == 15) scratch[17 * j + 16] = x;
-        }
-    }
-    __syncthreads();
 #pragma unroll
     for (int j = 0; j < 3; ++j) {
-        r[j] = scratch[17 * j + wave] + incl[j] - v[j];
-        total[j] = scratch[17 * j + 16];
+        const int x = wave_inclusive_scan(lane < 16 ? scratch[17 * j + lane] : 0);
+        const int before = wave > 0 ? __builtin_amdgcn_readlane(x, (wave - 1) & 15) : 0;
+        r[j] = before + incl[j] - v[j];
+        total[j] = __builtin_amdgcn_readlane(x, 15);
     }
 }
 
+constexpr int kDispatchIdRegs = 4;                      // passes of 1024 pairs whose ids stay in registers
+constexpr int kDispatchLdsPairs = 1024 * kDispatchIdRegs;  // pairs whose perm entry is also kept in LDS
 struct DispatchLds {
     int cnt[1024];
     int run[1024];
@@ -519,12 +517,13 @@ struct DispatchLds {
     int el[1024];
     uint8_t wcnt[16][1024];
     int scan[3 * 17];
+    int perm[kDispatchLdsPairs];  // the first pairs' dispatch order, for the work items
 };
 
 // With `items`, also the work-item table: expert e's pairs in chunks of at most `chunk` columns (items in
 // ascending expert order), then the shared expert's tokens in chunks of `sh_chunk`, then empty items up to
 // max_items.
-__device__ void dispatch_block(const int32_t* __restrict__ ids, int P, int E, int32_t* __restrict__ counts,
+__device__ __forceinline__ void dispatch_block(const int32_t* __restrict__ ids, int P, int E, int32_t* __restrict__ counts,
                                int32_t* __restrict__ offsets, int32_t* __restrict__ perm, int32_t* __restrict__ slot,
                                int32_t* __restrict__ elist, int32_t* __restrict__ n_list, DispatchLds& s,
                                int4* __restrict__ items = nullptr, int max_items = 0, int T = 0, int k = 1,
@@ -534,7 +533,13 @@ __device__ void dispatch_block(const int32_t* __restrict__ ids, int P, int E, in
 #pragma unroll
     for (int w = 0; w < 4; ++w) reinterpret_cast<uint32_t*>(&s.wcnt[0][0])[w * 1024 + tid] = 0u;
     __syncthreads();
-    for (int i = tid; i < P; i += 1024) {
+    int idr[kDispatchIdRegs];  // ids of this thread's pairs tid + 1024 j, loaded once
+#pragma unroll
+    for (int j = 0; j < kDispatchIdRegs; ++j) idr[j] = tid + 1024 * j < P ? ids[tid + 1024 * j] : -1;
+#pragma unroll
+    for (int j = 0; j < kDispatchIdRegs; ++j)
+        if (idr[j] >= 0 && idr[j] < E) atomicAdd(&s.cnt[idr[j]], 1);
+    for (int i = tid + kDispatchLdsPairs; i < P; i += 1024) {
         const int e = ids[i];
         if (e >= 0 && e < E) atomicAdd(&s.cnt[e], 1);
     }
@@ -560,9 +565,9 @@ __device__ void dispatch_block(const int32_t* __restrict__ ids, int P, int E, in
     }
     __syncthreads();
     const unsigned long long lt = (1ull << lane) - 1ull;
-    for (int base = 0; base < P; base += 1024) {
+    // one pass over pairs base .. base + 1023: rank inside the wave by ballot match, then across waves
+    auto rank_pass = [&](int base, int id) {
         const int i = base + tid;
-        const int id = i < P ? ids[i] : -1;
         const bool valid = id >= 0 && id < E;
         const int key = valid ? id : 0;
         if (i < P && !valid) slot[i] = -1;
@@ -583,6 +588,7 @@ __device__ void dispatch_block(const int32_t* __restrict__ ids, int P, int E, in
             for (int w = 0; w < wave; ++w) pos += s.wcnt[w][key];
             perm[pos] = i;
             slot[i] = pos;
+            if (pos < kDispatchLdsPairs) s.perm[pos] = i;
         }
         __syncthreads();
         if (valid && leader) {
@@ -590,13 +596,21 @@ __device__ void dispatch_block(const int32_t* __restrict__ ids, int P, int E, in
             s.wcnt[wave][key] = 0;
         }
         __syncthreads();
-    }
+    };
+#pragma unroll
+    for (int j = 0; j < kDispatchIdRegs; ++j)
+        if (1024 * j < P) rank_pass(1024 * j, idr[j]);
+    for (int base = kDispatchLdsPairs; base < P; base += 1024) rank_pass(base, base + tid < P ? ids[base + tid] : -1);
     if (!items) return;
     if (tid < E && c > 0) {
         for (int ch = 0; ch < nch; ++ch) {
             const int first = off + ch * chunk, n = min(chunk, c - ch * chunk);
             int tk[4] = {0, 0, 0, 0};
-            for (int j = 0; j < 4 && j < n; ++j) tk[j] = perm[first + j] / k;
+            if (first + 4 <= kDispatchLdsPairs) {  // two loops, so that the LDS and global loads stay apart
+                for (int j = 0; j < 4 && j < n; ++j) tk[j] = s.perm[first + j] / k;
+            } else {
+                for (int j = 0; j < 4 && j < n; ++j) tk[j] = perm[first + j] / k;
+            }
             items[2 * (cbase + ch)] = make_int4(tid, first, n, tk[0]);
             items[2 * (cbase + ch) + 1] = make_int4(tk[1], tk[2], tk[3], 0);
         }
