@@ -27,6 +27,26 @@ __device__ __forceinline__ void load_unit(const uint8_t* p, uint32_t (&w)[9]) {
     __builtin_memcpy(w, __builtin_assume_aligned(p, 4), 36);
 }
 
+// sum(code * q) of one q8_1 block against its two code dwords a (positions 0..15) and b (16..31), with the
+// block's image in the split layout: per code dword, the even codes (& 0x33333333) and the odd codes
+// (>> 2, & 0x33333333) as 4-bit lanes, 16 * sdot8(codes, qh) + udot8(codes, ql).  Exact: the sums are
+// integers well inside int32.
+__device__ __forceinline__ int half_dot_split(uint32_t a, uint32_t b, const uint32_t* X) {
+    const uint32_t M = 0x33333333u;
+    const uint32_t a0 = a & M, a1 = (a >> 2) & M, b0 = b & M, b1 = (b >> 2) & M;
+    int h = __builtin_amdgcn_sdot8((int)a0, (int)X[0], 0, false);
+    uint32_t l = __builtin_amdgcn_udot8(a0, X[1], 0u, false);
+    h = __builtin_amdgcn_sdot8((int)a1, (int)X[2], h, false);
+    l = __builtin_amdgcn_udot8(a1, X[3], l, false);
+    h = __builtin_amdgcn_sdot8((int)b0, (int)X[4], h, false);
+    l = __builtin_amdgcn_udot8(b0, X[5], l, false);
+    h = __builtin_amdgcn_sdot8((int)b1, (int)X[6], h, false);
+    l = __builtin_amdgcn_udot8(b1, X[7], l, false);
+    return h * 16 + (int)l;
+}
+
+// The same sum against 8 dwords of int8 q in the (codes >> 2c) & 0x03030303 byte order (the standard q8_1
+// activations of the stage-API GEMV, permuted on load).
 __device__ __forceinline__ int half_dot(uint32_t a, uint32_t b, const uint32_t* X) {
     const uint32_t M = 0x03030303u;
     int s = 0;
@@ -68,13 +88,13 @@ __device__ __forceinline__ float q2_unit_first(const uint32_t (&w)[9], float d0,
     const uint32_t c1 = __builtin_amdgcn_alignbyte(w[2], w[1], 2);
     const uint32_t c2 = __builtin_amdgcn_alignbyte(w[3], w[2], 2);
     const uint32_t c3 = __builtin_amdgcn_alignbyte(w[4], w[3], 2);
-    const float P0 = (d0 * a.d[0]) * (float)(half_dot(c0, c1, a.q[0]) - a.sq[0]);
-    const float P1 = (d0 * a.d[1]) * (float)(half_dot(c2, c3, a.q[1]) - a.sq[1]);
+    const float P0 = (d0 * a.d[0]) * (float)(half_dot_split(c0, c1, a.q[0]) - a.sq[0]);
+    const float P1 = (d0 * a.d[1]) * (float)(half_dot_split(c2, c3, a.q[1]) - a.sq[1]);
     return P0 + P1;
 }
 __device__ __forceinline__ float q2_unit_second(const uint32_t (&w)[9], float d1, float p01, const Act2& a) {
-    const float P2 = (d1 * a.d[0]) * (float)(half_dot(w[5], w[6], a.q[0]) - a.sq[0]);
-    const float P3 = (d1 * a.d[1]) * (float)(half_dot(w[7], w[8], a.q[1]) - a.sq[1]);
+    const float P2 = (d1 * a.d[0]) * (float)(half_dot_split(w[5], w[6], a.q[0]) - a.sq[0]);
+    const float P3 = (d1 * a.d[1]) * (float)(half_dot_split(w[7], w[8], a.q[1]) - a.sq[1]);
     return (p01 + P2) + P3;
 }
 
@@ -657,15 +677,6 @@ __global__ __launch_bounds__(1024) void k_topk_dispatch(const float* __restrict_
                    chunk, sh_chunk);
 }
 
-// q8_1 images of a flat f32 vector (n % 32 == 0), one block per half wave.
-__global__ __launch_bounds__(256) void k_quant_image(const float* __restrict__ x, int64_t n, uint32_t* __restrict__ img) {
-    __shared__ uint8_t qsc[8][32];
-    const int64_t b = (int64_t)blockIdx.x * 8 + (threadIdx.x >> 5);
-    const bool live = b * 32 < n;
-    const float v = live ? x[b * 32 + (threadIdx.x & 31)] : 0.0f;
-    q8_image_store(v, live, qsc[threadIdx.x >> 5], img + (live ? b : 0) * kImgDw);
-}
-
 // ------------------------------------------------------------------------------------------------ expert GEMV
 // Row geometry: dpr = n_in / 128 units; lpr = lanes per row; upl = units per lane; rpi = 64 / lpr rows per
 // wave pass.  Lane (group, l) handles units g = l + lpr * m (m < upl) of its row.
@@ -1057,11 +1068,6 @@ hipError_t launch_topk_dispatch(const float* logits, int T, int E, int k, int32_
 int shared_items(int T) { return (T + kShCols - 1) / kShCols; }
 int gemv_shared_chunk() { return kShCols; }
 
-hipError_t launch_quant_image(const float* x, int64_t n, uint32_t* img, hipStream_t s) {
-    const int64_t nb = n / 32;
-    hipLaunchKernelGGL(k_quant_image, dim3((unsigned)((nb + 7) / 8)), dim3(256), 0, s, x, n, img);
-    return hipGetLastError();
-}
 
 #define SMOE_SHAPE_DISPATCH(KERNEL_MACRO)              \
     if (nit == 4 && upl == 1) KERNEL_MACRO(4, 1);      \

@@ -11,13 +11,14 @@ namespace smoe {
 // xor exchange inside groups of up to 32 lanes without LDS traffic: DPP quad permutes for distance 1 and 2,
 // ds_swizzle (bit mode, xor mask) for 4, 8 and 16.
 template <int O>
+__device__ __forceinline__ int xor_swap_i(int i) {
+    if constexpr (O == 1) return __builtin_amdgcn_mov_dpp(i, 0xB1, 0xF, 0xF, false);       // quad_perm [1,0,3,2]
+    else if constexpr (O == 2) return __builtin_amdgcn_mov_dpp(i, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+    else return __builtin_amdgcn_ds_swizzle(i, 0x1F | (O << 10));                          // lane ^ O within 32
+}
+template <int O>
 __device__ __forceinline__ float xor_swap(float v) {
-    const int i = __float_as_int(v);
-    int r;
-    if constexpr (O == 1) r = __builtin_amdgcn_mov_dpp(i, 0xB1, 0xF, 0xF, false);       // quad_perm [1,0,3,2]
-    else if constexpr (O == 2) r = __builtin_amdgcn_mov_dpp(i, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
-    else r = __builtin_amdgcn_ds_swizzle(i, 0x1F | (O << 10));                          // lane ^ O within 32
-    return __int_as_float(r);
+    return __int_as_float(xor_swap_i<O>(__float_as_int(v)));
 }
 
 // Sum over groups of `lpr` consecutive lanes, distance lpr/2 first; every lane of a group ends with the sum.
@@ -111,18 +112,21 @@ __device__ __forceinline__ int lanes_per_row(int dpr) {
 
 // ------------------------------------------------------------------------------------------------ q8_1 images
 // A q8_1 block (32 activations) as the GEMV kernels read it: 12 dwords, 16-byte aligned:
-//   dwords 0..7  the 32 int8 values permuted so that dword c of each 16-group holds q[c], q[c+4], q[c+8],
-//                q[c+12] (the byte order (codes >> 2c) & 0x03030303 delivers for a 2-bit code dword);
+//   dwords 0..7  the 32 int8 values q, in one of two layouts:
+//     split (the Q2_0 kernels): each q as q = 16 qh + ql, qh = q >> 4 (signed 4-bit), ql = q & 15 (unsigned
+//       4-bit); for each 16-group g, dword 4g holds qh of positions 16g + 2i in nibble i, dword 4g + 1 their ql,
+//       dwords 4g + 2 and 4g + 3 the same for positions 16g + 2i + 1 -- the nibble order in which
+//       (codes >> 2s) & 0x33333333 delivers a 2-bit code dword (s = 0: even positions, s = 1: odd), so that
+//       sum(code * q) = 16 sdot8(codes, qh) + udot8(codes, ql) exactly;
+//     natural (the IQ2_S kernels): dword c holds q[4c .. 4c + 3];
 //   dword 8      f32 of the stored fp16 scale d; dword 9 the int sum of q; dwords 10..11 unused.
 // Built by the same quantiser as the q8_1 block (metal/shaders/iq.metal:597-627); the fp16 sum field of the
 // q8_1 block is not needed by the Q2_0 / IQ2_S dots (metal/shaders/iq.metal:152-180,444-456) and is not kept.
 constexpr int kImgDw = 12;
 
-__device__ __forceinline__ int perm_pos(int i) { return (i & 16) + 4 * (i & 3) + ((i >> 2) & 3); }
-
-// A 32-lane half wave quantises one block (lane & 31 = position) and writes its image (`natural`: the int8
-// values in natural order, the IQ2_S kernels' layout); `sc` is 32 bytes of LDS
-// scratch owned by the half.  Every lane of the half must call it; `store` false skips the global store.
+// A 32-lane half wave quantises one block (lane & 31 = position) and writes its image, split or `natural`;
+// `sc` is 32 bytes of LDS scratch owned by the half (natural layout only).  Every lane of the half must call
+// it; `store` false skips the global store.
 __device__ __forceinline__ void q8_image_store(float v, bool store, uint8_t* sc, uint32_t* img, bool natural = false) {
     const int l32 = threadIdx.x & 31;
     float a = __builtin_fabsf(v);
@@ -140,12 +144,27 @@ __device__ __forceinline__ void q8_image_store(float v, bool store, uint8_t* sc,
     int sq = q;
 #pragma unroll
     for (int o = 16; o > 0; o >>= 1) sq += __shfl_xor(sq, o, kWave);
-    sc[natural ? l32 : perm_pos(l32)] = (uint8_t)(int8_t)q;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (natural) {
+        sc[l32] = (uint8_t)(int8_t)q;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if (store && l32 < 8) img[l32] = reinterpret_cast<const uint32_t*>(sc)[l32];
+    } else {
+        // nibble (l32 & 15) >> 1 of dword 4 (l32 >> 4) + 2 (l32 & 1) (qh) and of the next one (ql): OR over
+        // the eight lanes that share the dwords (xor 2, 4, 8), then lanes 0, 1, 16 and 17 hold them
+        const int sh = 4 * ((l32 & 15) >> 1);
+        int vh = ((q >> 4) & 15) << sh, vl = (q & 15) << sh;
+        vh |= xor_swap_i<2>(vh);
+        vl |= xor_swap_i<2>(vl);
+        vh |= xor_swap_i<4>(vh);
+        vl |= xor_swap_i<4>(vl);
+        vh |= xor_swap_i<8>(vh);
+        vl |= xor_swap_i<8>(vl);
+        if (store && (l32 & 14) == 0)
+            *reinterpret_cast<uint2*>(img + 4 * (l32 >> 4) + 2 * (l32 & 1)) = make_uint2((uint32_t)vh, (uint32_t)vl);
+    }
     if (store) {
-        if (l32 < 8) img[l32] = reinterpret_cast<const uint32_t*>(sc)[l32];
         if (l32 == 8) img[8] = f2u(f16_to_f32(f32_to_f16(d)));
         if (l32 == 9) img[9] = (uint32_t)sq;
     }

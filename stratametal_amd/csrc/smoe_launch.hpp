@@ -25,7 +25,6 @@ hipError_t launch_topk_dispatch(const float* logits, int T, int E, int k, int32_
                                 int4* items, int max_items, int has_shared, int chunk, int sh_chunk, hipStream_t s);
 int shared_items(int T);  // shared-expert work items for T tokens (GEMV path)
 int gemv_shared_chunk();   // shared-expert tokens per GEMV work item
-hipError_t launch_quant_image(const float* x, int64_t n, uint32_t* img, hipStream_t s);
 hipError_t launch_q2_gu(const uint8_t* gate_exps, const uint8_t* up_exps, const uint8_t* gate_sh, const uint8_t* up_sh,
                         const uint32_t* ximg, const int4* items, const int32_t* perm, int k, int H, int F, int Fs,
                         int has_shared, int max_items, uint32_t* himg, int h_blocks, hipStream_t s);
