@@ -81,6 +81,20 @@ __device__ __forceinline__ float unit_d1(const uint32_t (&w)[9]) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)(w[4] >> 16));
 }
 
+// Every unit's two block scales; the asm barrier keeps the conversions (and so the wait for the weight loads)
+// where the call stands.
+template <int NIT, int MAXUPL>
+__device__ __forceinline__ void unit_scales(uint32_t (&w)[NIT][MAXUPL][9], float (&dw)[NIT][MAXUPL][2]) {
+    pin_units(w);
+#pragma unroll
+    for (int it = 0; it < NIT; ++it)
+#pragma unroll
+        for (int m = 0; m < MAXUPL; ++m) {
+            dw[it][m][0] = unit_d0(w[it][m]);
+            dw[it][m][1] = unit_d1(w[it][m]);
+        }
+}
+
 // A unit's first block (P0 + P1, activation images 0 and 1) and second block (P2, P3, images 2 and 3), so that
 // only two images are live at a time; q2_unit_dot's order is L = ((P0 + P1) + P2) + P3.
 __device__ __forceinline__ float q2_unit_first(const uint32_t (&w)[9], float d0, const Act2& a) {
@@ -720,31 +734,43 @@ __global__ __launch_bounds__(256) void k_q2_gu(const uint8_t* __restrict__ gate_
     const int grp = lane / G.lpr, l = lane - grp * G.lpr;
     const int qb = H >> 5;
 
+    // Weight units: every load unconditional (a dead slot reloads the row's first unit), so that the loads in
+    // flight are counted exactly.  The first column batch's image loads (L2) go out before them (HBM), so that
+    // storing the images to LDS waits for the image loads alone.
     uint32_t w[NIT][MAXUPL][9];
-    bool live[NIT];
+    auto load_weights = [&]() {
 #pragma unroll
-    for (int it = 0; it < NIT; ++it) {
-        const int rho = it * G.rpi + grp;  // 0..15 within the wave
-        live[it] = rho < 16;
-        const int r = 32 * hb + 8 * wave + (rho & 7);
-        const uint8_t* rowp = (rho < 8 ? g0 : u0) + (size_t)r * rb;
+        for (int it = 0; it < NIT; ++it) {
+            const int rho = min(it * G.rpi + grp, 15);  // 0..15 within the wave (a dead pass repeats row 15)
+            const int r = 32 * hb + 8 * wave + (rho & 7);
+            const uint8_t* rowp = (rho < 8 ? g0 : u0) + (size_t)r * rb;
 #pragma unroll
-        for (int m = 0; m < MAXUPL; ++m)
-            if (live[it] && m < G.upl) load_unit(rowp + (size_t)(l + G.lpr * m) * 36, w[it][m]);
-    }
-    float dw[NIT][MAXUPL][2];
-#pragma unroll
-    for (int it = 0; it < NIT; ++it)
-#pragma unroll
-        for (int m = 0; m < MAXUPL; ++m) {
-            dw[it][m][0] = unit_d0(w[it][m]);
-            dw[it][m][1] = unit_d1(w[it][m]);
+            for (int m = 0; m < MAXUPL; ++m) load_unit(rowp + (size_t)(m < G.upl ? l + G.lpr * m : l) * 36, w[it][m]);
         }
+    };
+    const int nc0 = min(kGuCols, item.ncol);
+    if (stage_direct(item, 0, nc0, true)) {
+        StagePieces sp;
+        stage_issue_direct(sp, ximg, qb, 0, nc0, kGuCols, 0, item, true);
+        __builtin_amdgcn_sched_barrier(0);
+        load_weights();
+        __builtin_amdgcn_sched_barrier(0);
+        stage_commit_direct(sp, smem);
+    } else {
+        load_weights();
+        stage_images(smem, ximg, qb, 0, nc0, kGuCols, item, perm, k, true, 0, 4 * 256);
+    }
+    stage_images(smem, ximg, qb, 0, nc0, kGuCols, item, perm, k, true, 4 * 256);  // rounds beyond the first
+    __syncthreads();
+    float dw[NIT][MAXUPL][2];
+    unit_scales(w, dw);
 
     for (int c0 = 0; c0 < item.ncol; c0 += kGuCols) {
         const int nc = min(kGuCols, item.ncol - c0);
-        stage_images(smem, ximg, qb, c0, nc, item, perm, k, true);
-        __syncthreads();
+        if (c0 > 0) {
+            stage_images(smem, ximg, qb, c0, nc, kGuCols, item, perm, k, true);
+            __syncthreads();
+        }
         for (int c = 0; c < nc; ++c) {
             const uint32_t* xt = smem + (size_t)c * qb * kImgDw;
             pin_units(w);
@@ -773,7 +799,7 @@ __global__ __launch_bounds__(256) void k_q2_gu(const uint8_t* __restrict__ gate_
                 rowv[c][(rho < 8 ? 0 : 32) + 8 * wave + (rho & 7)] = v;
         }
         __syncthreads();
-        {
+        if (2 * wave < nc) {  // the waves whose half waves own live columns
             const int hw = threadIdx.x >> 5;  // half wave = column
             const bool live_c = hw < nc;
             const int i = lane & 31;
@@ -781,7 +807,7 @@ __global__ __launch_bounds__(256) void k_q2_gu(const uint8_t* __restrict__ gate_
             const int row = item.first + c0 + (live_c ? hw : 0);
             q8_image_store(h, live_c, qsc[hw], himg + ((size_t)row * h_blocks + hb) * kImgDw);
         }
-        __syncthreads();
+        if (c0 + kGuCols < item.ncol) __syncthreads();
     }
 }
 
@@ -805,28 +831,32 @@ __global__ __launch_bounds__(256) void k_q2_down(const uint8_t* __restrict__ dow
     const int grp = lane / G.lpr, l = lane - grp * G.lpr;
     const int row0 = blockIdx.x * 4 * rpw + wave * rpw;
 
+    // first column batch: its image loads go out before the weight loads, which are all unconditional (a row
+    // past H reloads row H - 1; see k_q2_gu)
+    const int nc0 = min(cps, item.ncol);
+    StagePieces sp;
+    stage_issue_direct(sp, himg, h_blocks, 0, nc0, cps, 0, item, false);
+    __builtin_amdgcn_sched_barrier(0);
     uint32_t w[NIT][MAXUPL][9];
-    bool live[NIT];
 #pragma unroll
     for (int it = 0; it < NIT; ++it) {
-        const int r = row0 + it * G.rpi + grp;
-        live[it] = r < H;
+        const int r = min(row0 + it * G.rpi + grp, H - 1);
 #pragma unroll
         for (int m = 0; m < MAXUPL; ++m)
-            if (live[it] && m < G.upl) load_unit(base + (size_t)r * rb + (size_t)(l + G.lpr * m) * 36, w[it][m]);
+            load_unit(base + (size_t)r * rb + (size_t)(m < G.upl ? l + G.lpr * m : l) * 36, w[it][m]);
     }
+    __builtin_amdgcn_sched_barrier(0);
+    stage_commit_direct(sp, smem);
+    stage_images(smem, himg, h_blocks, 0, nc0, cps, item, nullptr, 1, false, 4 * 256);  // rounds beyond the first
+    __syncthreads();
     float dw[NIT][MAXUPL][2];
-#pragma unroll
-    for (int it = 0; it < NIT; ++it)
-#pragma unroll
-        for (int m = 0; m < MAXUPL; ++m) {
-            dw[it][m][0] = unit_d0(w[it][m]);
-            dw[it][m][1] = unit_d1(w[it][m]);
-        }
+    unit_scales(w, dw);
     for (int c0 = 0; c0 < item.ncol; c0 += cps) {
         const int nc = min(cps, item.ncol - c0);
-        stage_images(smem, himg, h_blocks, c0, nc, item, nullptr, 1, false);
-        __syncthreads();
+        if (c0 > 0) {
+            stage_images(smem, himg, h_blocks, c0, nc, cps, item, nullptr, 1, false);
+            __syncthreads();
+        }
         for (int c = 0; c < nc; ++c) {
             const uint32_t* ht = smem + (size_t)c * h_blocks * kImgDw;
             pin_units(w);
@@ -855,7 +885,7 @@ __global__ __launch_bounds__(256) void k_q2_down(const uint8_t* __restrict__ dow
             const int r = row0 + it * G.rpi + grp;
             if (r < H && (l & 3) == 0 && (NIT > 1 || l == 0)) Y[(size_t)(item.first + c0 + c) * H + r] = v;
         }
-        __syncthreads();
+        if (c0 + cps < item.ncol) __syncthreads();
     }
 }
 
@@ -1085,7 +1115,7 @@ hipError_t launch_q2_gu(const uint8_t* gate_exps, const uint8_t* up_exps, const 
     dim3 grid((unsigned)(Fmax / 32), (unsigned)max_items);
     int nit, upl;
     gu_shape(H, nit, upl);
-    const size_t lds = (size_t)kGuCols * (H >> 5) * kImgDw * 4;
+    const size_t lds = (size_t)kGuCols * (H >> 5) * kImgDw * 4 + 16;  // + the dead staging slot
 #define SMOE_GU(N, U)                                                                                             \
     hipLaunchKernelGGL((k_q2_gu<N, U>), grid, dim3(256), lds, s, gate_exps, up_exps, gate_sh, up_sh, ximg, items, perm, \
                        k, H, F, Fs, himg, h_blocks)
@@ -1103,7 +1133,7 @@ hipError_t launch_q2_down(const uint8_t* down_exps, const uint8_t* down_sh, cons
     const size_t col_bytes = (size_t)h_blocks * kImgDw * 4;
     int cps = (int)(24576 / col_bytes);
     cps = cps < 1 ? 1 : cps > 16 ? 16 : cps;
-    const size_t lds = (size_t)cps * col_bytes;
+    const size_t lds = (size_t)cps * col_bytes + 16;  // + the dead staging slot
 #define SMOE_DOWN(N, U)                                                                                            \
     hipLaunchKernelGGL((k_q2_down<N, U>), grid, dim3(256), lds, s, down_exps, down_sh, himg, h_blocks, sg, items, H, F, \
                        Fs, cps, Y)

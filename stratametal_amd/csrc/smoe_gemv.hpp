@@ -234,32 +234,85 @@ __device__ __forceinline__ void load_act_std(const uint8_t* __restrict__ blk, Ac
     }
 }
 
-// Copies the q8_1 images of `nc` columns (qb blocks each) into LDS (any block size).  Four 16-byte pieces per
-// thread per round,
-// with every address computed and every load issued (clamped to a valid piece) before the first store, so a
-// round costs one memory round trip instead of one per piece.
-__device__ __forceinline__ void stage_images(uint32_t* act, const uint32_t* __restrict__ img, int qb, int c0, int nc,
-                                             const Item& it, const int32_t* perm, int k, bool by_token) {
+// Copying the images of columns c0 .. c0 + nc of the item (x rows by token, or h rows first + c) into LDS,
+// column-major, in rounds of four 16-byte pieces per thread (pieces base + j * blockDim.x + tid).  A round is
+// issued into registers (stage_issue) and stored (stage_commit) separately, so that a kernel can issue its
+// weight loads in between and the stores wait for the image loads only.  Within a round every load and store
+// is unconditional (a piece past the end reloads the last one and lands in slot cap_cols * per-column pieces,
+// which the caller's LDS holds beyond its cap_cols columns), so the loads are not serialised behind branches;
+// a j with no live piece in the whole work-group is skipped.
+typedef __attribute__((ext_vector_type(4))) uint32_t img_u32x4;  // a native vector: stays in registers
+struct StagePieces {
+    img_u32x4 v[4];
+    int dst[4];
+};
+__device__ __forceinline__ void stage_issue(StagePieces& sp, const uint32_t* __restrict__ img, int qb, int c0, int nc,
+                                            int cap_cols, int base, const Item& it, const int32_t* perm, int k,
+                                            bool by_token) {
     const int per_col = qb * (kImgDw / 4);  // uint4 per column
-    const int total = nc * per_col;
+    const int total = nc * per_col, dead = cap_cols * per_col;
     const int nt = (int)blockDim.x;
-    for (int base = 0; base < total; base += 4 * nt) {
-        int row[4], r[4];
+    // rows without memory reads (h rows, shared tokens, or a routed item's first four columns), so that the
+    // image loads of all rounds go out together; otherwise item_token reads perm
+    const bool direct = !by_token || it.shared || c0 + nc <= 4;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int idx = min(base + j * nt + (int)threadIdx.x, total - 1);
+    for (int j = 0; j < 4; ++j) {
+        if (base + j * nt < total) {
+            const int raw = base + j * nt + (int)threadIdx.x;
+            const int idx = min(raw, total - 1);
             const int c = idx / per_col;
-            r[j] = idx - c * per_col;
-            row[j] = by_token ? item_token(it, perm, k, c0 + c) : it.first + c0 + c;
+            int row;
+            if (direct) row = !by_token ? it.first + c0 + c : it.shared ? it.tok0 + c0 + c : item_token_head(it, c0 + c);
+            else row = item_token(it, perm, k, c0 + c);
+            sp.v[j] = reinterpret_cast<const img_u32x4*>(img)[(size_t)row * per_col + (idx - c * per_col)];
+            sp.dst[j] = raw < total ? raw : dead;
         }
-        uint4 v[4];
+    }
+}
+__device__ __forceinline__ void stage_commit(const StagePieces& sp, uint32_t* act, int qb, int nc, int base) {
+    const int total = nc * qb * (kImgDw / 4);
+    const int nt = (int)blockDim.x;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) v[j] = reinterpret_cast<const uint4*>(img)[(size_t)row[j] * per_col + r[j]];
+    for (int j = 0; j < 4; ++j)
+        if (base + j * nt < total) reinterpret_cast<img_u32x4*>(act)[sp.dst[j]] = sp.v[j];
+}
+// Round `base` with rows that need no memory read (see stage_issue) as straight-line code: all four loads
+// unconditional (a piece past the end, or a whole j past the end, reloads the last piece and is stored to the
+// dead slot), so that the compiler counts the loads in flight exactly and a later store waits for its own load
+// alone.
+__device__ __forceinline__ void stage_issue_direct(StagePieces& sp, const uint32_t* __restrict__ img, int qb, int c0,
+                                                   int nc, int cap_cols, int base, const Item& it, bool by_token) {
+    const int per_col = qb * (kImgDw / 4);
+    const int total = nc * per_col, dead = cap_cols * per_col;
+    const int nt = (int)blockDim.x;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int idx = base + j * nt + (int)threadIdx.x;
-            if (idx < total) reinterpret_cast<uint4*>(act)[idx] = v[j];
-        }
+    for (int j = 0; j < 4; ++j) {
+        const int raw = base + j * nt + (int)threadIdx.x;
+        const int idx = min(raw, total - 1);
+        const int c = idx / per_col;
+        const int row = !by_token ? it.first + c0 + c : it.shared ? it.tok0 + c0 + c : item_token_head(it, c0 + c);
+        sp.v[j] = reinterpret_cast<const img_u32x4*>(img)[(size_t)row * per_col + (idx - c * per_col)];
+        sp.dst[j] = raw < total ? raw : dead;
+    }
+}
+__device__ __forceinline__ void stage_commit_direct(const StagePieces& sp, uint32_t* act) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) reinterpret_cast<img_u32x4*>(act)[sp.dst[j]] = sp.v[j];
+}
+// True when stage_issue_direct can serve columns c0 .. c0 + nc.
+__device__ __forceinline__ bool stage_direct(const Item& it, int c0, int nc, bool by_token) {
+    return !by_token || it.shared || c0 + nc <= 4;
+}
+
+// The rounds from `from` on, each issued and stored in turn.
+__device__ __forceinline__ void stage_images(uint32_t* act, const uint32_t* __restrict__ img, int qb, int c0, int nc,
+                                             int cap_cols, const Item& it, const int32_t* perm, int k, bool by_token,
+                                             int from = 0, int to = 1 << 30) {
+    const int total = min(nc * qb * (kImgDw / 4), to);
+    for (int base = from; base < total; base += 4 * (int)blockDim.x) {
+        StagePieces sp;
+        stage_issue(sp, img, qb, c0, nc, cap_cols, base, it, perm, k, by_token);
+        stage_commit(sp, act, qb, nc, base);
     }
 }
 

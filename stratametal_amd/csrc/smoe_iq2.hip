@@ -182,7 +182,7 @@ __global__ __launch_bounds__(64 * NW) void k_iq2_gu(const uint8_t* __restrict__ 
 
     for (int c0 = 0; c0 < item.ncol; c0 += kCols) {
         const int nc = min(kCols, item.ncol - c0);
-        stage_images(smem, ximg, qb, c0, nc, item, perm, k, true);
+        stage_images(smem, ximg, qb, c0, nc, kCols, item, perm, k, true);
         __syncthreads();
         for (int c = 0; c < nc; ++c) {
             const uint32_t* xt = smem + (size_t)c * qb * kImgDw;
@@ -234,7 +234,7 @@ __global__ __launch_bounds__(256) void k_iq2_down(const uint8_t* __restrict__ do
     }
     for (int c0 = 0; c0 < item.ncol; c0 += cps) {
         const int nc = min(cps, item.ncol - c0);
-        stage_images(smem, himg, h_blocks, c0, nc, item, nullptr, 1, false);
+        stage_images(smem, himg, h_blocks, c0, nc, cps, item, nullptr, 1, false);
         __syncthreads();
         for (int c = 0; c < nc; ++c) {
             const uint32_t* ht = smem + (size_t)c * h_blocks * kImgDw;
@@ -289,7 +289,7 @@ hipError_t launch_iq2_gu(const uint8_t* gate_exps, const uint8_t* up_exps, const
     const int Fmax = has_shared && Fs > F ? Fs : F;
     dim3 grid((unsigned)(Fmax / 32), (unsigned)max_items);
     const int nb = H / 256;
-    const size_t lds = (size_t)(2 * nb) * (H >> 5) * kImgDw * 4;
+    const size_t lds = (size_t)(2 * nb) * (H >> 5) * kImgDw * 4 + 16;  // + the dead staging slot
 #define SMOE_IQ2_GU(NW)                                                                                           \
     hipLaunchKernelGGL((k_iq2_gu<NW>), grid, dim3(64 * (NW)), lds, s, gate_exps, up_exps, gate_sh, up_sh, ximg, items, \
                        perm, k, H, F, Fs, himg, h_blocks)
@@ -308,7 +308,7 @@ hipError_t launch_iq2_down(const uint8_t* down_exps, const uint8_t* down_sh, con
     const size_t col_bytes = (size_t)h_blocks * kImgDw * 4;
     int cps = (int)(24576 / col_bytes);
     cps = cps < 1 ? 1 : cps > 16 ? 16 : cps;
-    hipLaunchKernelGGL(k_iq2_down, grid, dim3(256), (size_t)cps * col_bytes, s, down_exps, down_sh, himg, h_blocks, sg,
+    hipLaunchKernelGGL(k_iq2_down, grid, dim3(256), (size_t)cps * col_bytes + 16, s, down_exps, down_sh, himg, h_blocks, sg,
                        items, H, F, Fs, cps, Y);
     return hipGetLastError();
 }

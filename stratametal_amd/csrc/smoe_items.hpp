@@ -35,6 +35,11 @@ __device__ __forceinline__ bool work_item(const int4* __restrict__ items, int wi
     return true;
 }
 
+// The token of a routed item's column c < 4, by selects (no branch, no memory read).
+__device__ __forceinline__ int item_token_head(const Item& it, int c) {
+    return c == 0 ? it.tk[0] : c == 1 ? it.tk[1] : c == 2 ? it.tk[2] : it.tk[3];
+}
+
 __device__ __forceinline__ int item_token(const Item& it, const int32_t* perm, int k, int c) {
     if (it.shared) return it.tok0 + c;
     if (c < 4) return c == 0 ? it.tk[0] : c == 1 ? it.tk[1] : c == 2 ? it.tk[2] : it.tk[3];
