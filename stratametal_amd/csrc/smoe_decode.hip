@@ -1008,7 +1008,8 @@ void gu_shape(int n_in, int& nit, int& upl) {
     upl = dpr / lpr;
     nit = lpr >= 4 ? lpr / 4 : 1;
 }
-// row kernels: passes per wave (at least 16 rows per wave), units per lane, rows per wave
+// row kernels: passes per wave (at least 16 rows per wave; group_sum_rs needs lpr = 4 passes when there are
+// several), units per lane, rows per wave
 void rows_shape(int n_in, int& nit, int& upl, int& rpw) {
     const int dpr = n_in >> 7, lpr = lanes_per_row_host(dpr);
     upl = dpr / lpr;
@@ -1128,7 +1129,12 @@ hipError_t launch_q2_down(const uint8_t* down_exps, const uint8_t* down_sh, cons
                           const float* sg, const int4* items, int H, int F, int Fs, int max_items, float* Y,
                           hipStream_t s) {
     int nit, upl, rpw;
-    rows_shape(F, nit, upl, rpw);  // the caller guarantees the shared width has the same row shape
+    rows_shape(F, nit, upl, rpw);  // the caller guarantees the shared width has the same passes and units
+    if (Fs > 0) {                  // ... but its rows per wave may be fewer: the grid covers H rows for both
+        int a, b, rpw_s;
+        rows_shape(Fs, a, b, rpw_s);
+        rpw = rpw_s < rpw ? rpw_s : rpw;
+    }
     dim3 grid((unsigned)((H + 4 * rpw - 1) / (4 * rpw)), (unsigned)max_items);
     const size_t col_bytes = (size_t)h_blocks * kImgDw * 4;
     int cps = (int)(24576 / col_bytes);

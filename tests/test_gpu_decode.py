@@ -240,6 +240,9 @@ CASES = [
     ("shared not added", dict(n_expert=64), 5, 7, False),
     ("7 experts top-3", dict(n_embd=256, n_ff=256, n_ff_shared=128, n_expert=7, top_k=3), 9, 8, True),
     ("k = 1, E = 1", dict(n_embd=128, n_ff=128, n_ff_shared=256, n_expert=1, top_k=1), 2, 9, True),
+    # the shared down rows are packed more densely per wave than the routed ones: the grid must cover all H rows
+    ("shared wider than routed, H=2048", dict(n_embd=2048, n_ff=256, n_ff_shared=512, n_expert=32, top_k=4), 5, 10,
+     True),
 ]
 
 
