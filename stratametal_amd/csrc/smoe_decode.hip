@@ -554,9 +554,8 @@ struct DispatchLds {
     int perm[kDispatchLdsPairs];  // the first pairs' dispatch order, for the work items
 };
 
-// With `items`, also the work-item table: expert e's pairs in chunks of at most `chunk` columns (items in
-// ascending expert order), then the shared expert's tokens in chunks of `sh_chunk`, then empty items up to
-// max_items.
+// With `items`, also the work-item table: the shared expert's tokens in chunks of `sh_chunk`, then expert e's
+// pairs in chunks of at most `chunk` columns (in ascending expert order), then empty items up to max_items.
 __device__ __forceinline__ void dispatch_block(const int32_t* __restrict__ ids, int P, int E, int32_t* __restrict__ counts,
                                int32_t* __restrict__ offsets, int32_t* __restrict__ perm, int32_t* __restrict__ slot,
                                int32_t* __restrict__ elist, int32_t* __restrict__ n_list, DispatchLds& s,
@@ -636,6 +635,9 @@ __device__ __forceinline__ void dispatch_block(const int32_t* __restrict__ ids, 
         if (1024 * j < P) rank_pass(1024 * j, idr[j]);
     for (int base = kDispatchLdsPairs; base < P; base += 1024) rank_pass(base, base + tid < P ? ids[base + tid] : -1);
     if (!items) return;
+    // the shared expert's chunks first (they carry the most columns, so their work-groups start first), then the
+    // routed chunks in expert order, then empty items
+    const int n_sh = has_shared ? (T + sh_chunk - 1) / sh_chunk : 0;
     if (tid < E && c > 0) {
         for (int ch = 0; ch < nch; ++ch) {
             const int first = off + ch * chunk, n = min(chunk, c - ch * chunk);
@@ -645,15 +647,15 @@ __device__ __forceinline__ void dispatch_block(const int32_t* __restrict__ ids, 
             } else {
                 for (int j = 0; j < 4 && j < n; ++j) tk[j] = perm[first + j] / k;
             }
-            items[2 * (cbase + ch)] = make_int4(tid, first, n, tk[0]);
-            items[2 * (cbase + ch) + 1] = make_int4(tk[1], tk[2], tk[3], 0);
+            items[2 * (n_sh + cbase + ch)] = make_int4(tid, first, n, tk[0]);
+            items[2 * (n_sh + cbase + ch) + 1] = make_int4(tk[1], tk[2], tk[3], 0);
         }
     }
-    const int n_sh = has_shared ? (T + sh_chunk - 1) / sh_chunk : 0;
-    for (int wi = n_rc + tid; wi < max_items; wi += 1024) {
+    for (int wi = tid; wi < max_items; wi += 1024) {
+        if (wi >= n_sh && wi < n_sh + n_rc) continue;  // a routed chunk
         int4 a = make_int4(kItemEmpty, 0, 0, 0), b = make_int4(0, 0, 0, 0);
-        if (wi < n_rc + n_sh) {
-            const int t0 = (wi - n_rc) * sh_chunk;
+        if (wi < n_sh) {
+            const int t0 = wi * sh_chunk;
             a = make_int4(kItemShared, P + t0, min(sh_chunk, T - t0), t0);
             b = make_int4(t0 + 1, t0 + 2, t0 + 3, 0);
         }
