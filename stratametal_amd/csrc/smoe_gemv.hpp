@@ -124,14 +124,30 @@ __device__ __forceinline__ int lanes_per_row(int dpr) {
 // q8_1 block is not needed by the Q2_0 / IQ2_S dots (metal/shaders/iq.metal:152-180,444-456) and is not kept.
 constexpr int kImgDw = 12;
 
+// Maximum and sum over each 32-lane half of the wave, every lane receiving its half's result: DPP rotations
+// inside the 16-lane rows, then the other row of the half by swizzle.  Both are independent of the order of
+// combination (max of finite values, integer sum), so these equal any other reduction of the same values.
+__device__ __forceinline__ float half_max(float a) {
+    a = __builtin_fmaxf(a, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x128, 0xF, 0xF, false)));
+    a = __builtin_fmaxf(a, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x124, 0xF, 0xF, false)));
+    a = __builtin_fmaxf(a, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x122, 0xF, 0xF, false)));
+    a = __builtin_fmaxf(a, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x121, 0xF, 0xF, false)));
+    return __builtin_fmaxf(a, __int_as_float(xor_swap_i<16>(__float_as_int(a))));
+}
+__device__ __forceinline__ int half_sum_i(int v) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0x128, 0xF, 0xF, false);  // row_ror:8
+    v += __builtin_amdgcn_update_dpp(0, v, 0x124, 0xF, 0xF, false);  // row_ror:4
+    v += __builtin_amdgcn_update_dpp(0, v, 0x122, 0xF, 0xF, false);  // row_ror:2
+    v += __builtin_amdgcn_update_dpp(0, v, 0x121, 0xF, 0xF, false);  // row_ror:1
+    return v + xor_swap_i<16>(v);
+}
+
 // A 32-lane half wave quantises one block (lane & 31 = position) and writes its image, split or `natural`;
 // `sc` is 32 bytes of LDS scratch owned by the half (natural layout only).  Every lane of the half must call
 // it; `store` false skips the global store.
 __device__ __forceinline__ void q8_image_store(float v, bool store, uint8_t* sc, uint32_t* img, bool natural = false) {
     const int l32 = threadIdx.x & 31;
-    float a = __builtin_fabsf(v);
-#pragma unroll
-    for (int o = 16; o > 0; o >>= 1) a = __builtin_fmaxf(a, __shfl_xor(a, o, kWave));
+    const float a = half_max(__builtin_fabsf(v));
     float d = a / 127.0f;
     if (__builtin_fabsf(d) > 65504.0f) d = __builtin_copysignf(65504.0f, d);
     int q = 0;
@@ -141,9 +157,7 @@ __device__ __forceinline__ void q8_image_store(float v, bool store, uint8_t* sc,
         r = r < -127.0f ? -127.0f : r;
         q = (r == r) ? (int)r : 0;
     }
-    int sq = q;
-#pragma unroll
-    for (int o = 16; o > 0; o >>= 1) sq += __shfl_xor(sq, o, kWave);
+    const int sq = half_sum_i(q);
     if (natural) {
         sc[l32] = (uint8_t)(int8_t)q;
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
