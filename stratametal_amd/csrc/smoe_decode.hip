@@ -952,8 +952,23 @@ __global__ __launch_bounds__(256) void k_combine(const float* __restrict__ Y, co
     const int32_t* sl = slot + (size_t)t * k;
     const float* wt = wts + (size_t)t * k;
     for (int j = blockIdx.y * 256 + threadIdx.x; j < H; j += gridDim.y * 256) {
-        float acc = wt[0] * Y[(size_t)sl[0] * H + j];
-        for (int s = 1; s < k; ++s) acc = __builtin_fmaf(wt[s], Y[(size_t)sl[s] * H + j], acc);
+        // the pair rows 8 at a time, all loads of a batch in flight together (past k: reloads of the last row)
+        float acc = 0.0f;
+        for (int s0 = 0; s0 < k; s0 += 8) {
+            float v[8], wv[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int s = min(s0 + i, k - 1);
+                v[i] = Y[(size_t)sl[s] * H + j];
+                wv[i] = wt[s];
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int s = s0 + i;
+                if (s == 0) acc = wv[0] * v[0];
+                else if (s < k) acc = __builtin_fmaf(wv[i], v[i], acc);
+            }
+        }
         if (add_shared) acc = acc + Y[(size_t)(P + t) * H + j];
         y[(size_t)t * H + j] = acc;
     }
