@@ -881,11 +881,22 @@ __global__ __launch_bounds__(256) void k_q2_down(const uint8_t* __restrict__ dow
                 }
             }
             const float sig = item.shared ? sigmoid(sg[item.tok0 + c0 + c]) : 1.0f;
-            int it;
-            float v = group_sum_rs<NIT>(acc, G.lpr, lane, it);
-            if (item.shared) v = v * sig;
-            const int r = row0 + it * G.rpi + grp;
-            if (r < H && (l & 3) == 0 && (NIT > 1 || l == 0)) Y[(size_t)(item.first + c0 + c) * H + r] = v;
+            float* yc = Y + (size_t)(item.first + c0 + c) * H;
+            if (NIT == 1 || G.lpr == 4 * NIT) {  // one reduce-scatter: lane l ends with pass (l >> 2) & (NIT - 1)
+                int it;
+                float v = group_sum_rs<NIT>(acc, G.lpr, lane, it);
+                if (item.shared) v = v * sig;
+                const int r = row0 + it * G.rpi + grp;
+                if (r < H && (l & 3) == 0 && (NIT > 1 || l == 0)) yc[r] = v;
+            } else {  // each pass on its own: the same butterfly per row
+#pragma unroll
+                for (int it = 0; it < NIT; ++it) {
+                    float v = group_sum(acc[it], G.lpr);
+                    if (item.shared) v = v * sig;
+                    const int r = row0 + it * G.rpi + grp;
+                    if (r < H && l == 0) yc[r] = v;
+                }
+            }
         }
         if (c0 + cps < item.ncol) __syncthreads();
     }
@@ -1034,6 +1045,16 @@ void rows_shape(int n_in, int& nit, int& upl, int& rpw) {
     nit = rpi >= 16 ? 1 : 16 / rpi;
     rpw = nit * rpi;
 }
+// the down kernel: as rows_shape; with many work items (`wide`) then up to 4 passes until a lane holds 4 units
+// (a work-group streams tens of KB per staging of its h images; passes that do not fit one reduce-scatter are
+// summed one by one), with few the narrower shape keeps more work-groups in flight
+void down_shape(int n_in, bool wide, int& nit, int& upl, int& rpw) {
+    rows_shape(n_in, nit, upl, rpw);
+    if (!wide) return;
+    while (nit * upl < 4 && nit < 4) nit *= 2;
+    rpw = nit * (64 / lanes_per_row_host(n_in >> 7));
+}
+constexpr int kDownWideItems = 32;  // work items from which the down kernel takes the wide shape
 }  // namespace
 
 bool gemv_shape_ok(int n_in) {
@@ -1045,9 +1066,12 @@ bool gemv_shape_ok(int n_in) {
 
 bool down_shapes_match(int F, int Fs) {
     int a, b, c, d, e, f;
-    rows_shape(F, a, b, c);
-    rows_shape(Fs, d, e, f);
-    return a == d && b == e;
+    for (const bool wide : {false, true}) {
+        down_shape(F, wide, a, b, c);
+        down_shape(Fs, wide, d, e, f);
+        if (a != d || b != e) return false;
+    }
+    return true;
 }
 
 size_t img_bytes(int64_t n_blocks) { return (size_t)n_blocks * kImgDw * 4; }
@@ -1146,10 +1170,11 @@ hipError_t launch_q2_down(const uint8_t* down_exps, const uint8_t* down_sh, cons
                           const float* sg, const int4* items, int H, int F, int Fs, int max_items, float* Y,
                           hipStream_t s) {
     int nit, upl, rpw;
-    rows_shape(F, nit, upl, rpw);  // the caller guarantees the shared width has the same passes and units
+    const bool wide = max_items >= kDownWideItems;
+    down_shape(F, wide, nit, upl, rpw);  // the caller guarantees the shared width has the same passes and units
     if (Fs > 0) {                  // ... but its rows per wave may be fewer: the grid covers H rows for both
         int a, b, rpw_s;
-        rows_shape(Fs, a, b, rpw_s);
+        down_shape(Fs, wide, a, b, rpw_s);
         rpw = rpw_s < rpw ? rpw_s : rpw;
     }
     dim3 grid((unsigned)((H + 4 * rpw - 1) / (4 * rpw)), (unsigned)max_items);
