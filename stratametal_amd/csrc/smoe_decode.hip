@@ -129,8 +129,9 @@ __device__ __forceinline__ float q2_unit_dot(const uint32_t (&w)[9], float d0, f
 // written to sg[t].  The block stages its token tile of x as bf16 in LDS (RNE, NaN quieted), then each wave
 // takes one weight row: lane l owns the 8-element chunks l, l+64, ...; accumulates them in element order from
 // 0, then an xor butterfly 32..1 (oracle: or_bf16_gemv_dev).  Every bf16 product is exact in f32, so
-// fmaf(x, w, acc) == acc + x * w.  `xf` (f32) or `xb` (bf16 bits) supplies x.  With `ximg`, the blocks of
-// the tile also write the q8_1 images of the tile's x, a share each (the decode path's activations).
+// fmaf(x, w, acc) == acc + x * w.  `xf` (f32) or `xb` (bf16 bits) supplies x.  With `ximg`, extra blocks
+// past the row blocks write the q8_1 images of the tile's x (the decode path's activations), eight q8_1 blocks
+// each, beside the logits instead of before them.
 template <int MAXC>
 __global__ __launch_bounds__(256) void k_router(const float* __restrict__ xf, const uint16_t* __restrict__ xb,
                                                  const uint16_t* __restrict__ W, const uint16_t* __restrict__ w_inp,
@@ -141,6 +142,17 @@ __global__ __launch_bounds__(256) void k_router(const float* __restrict__ xf, co
     __shared__ uint8_t qsc[8][32];
     const int t0 = blockIdx.y * tok_tile;
     const int nt = min(tok_tile, T - t0);
+    const int row_blocks = (rows_total + 3) / 4;
+    if ((int)blockIdx.x >= row_blocks) {  // an image block: eight q8_1 blocks of the tile's x, one per half wave
+        const int hw = threadIdx.x >> 5;
+        const int nb = nt * (H >> 5);
+        const int bb = ((int)blockIdx.x - row_blocks) * 8 + hw;
+        const bool live = bb < nb;
+        const size_t blk = (size_t)t0 * (H >> 5) + (live ? bb : 0);
+        const float v = live ? xf[blk * 32 + (threadIdx.x & 31)] : 0.0f;
+        q8_image_store(v, live, qsc[hw], ximg + blk * kImgDw, img_natural != 0);
+        return;
+    }
     // the wave's weight row first (clamped, every load issued), so its latency overlaps the staging below
     const int lane = threadIdx.x & 63;
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -184,19 +196,6 @@ __global__ __launch_bounds__(256) void k_router(const float* __restrict__ xf, co
         for (int u = 0; u < 4; ++u) {
             const int g = base + u * 256 + threadIdx.x;
             if (g < n8) reinterpret_cast<uint4*>(smem)[g] = v[u];
-        }
-    }
-    if (ximg) {  // this block's share of the tile's q8_1 images, one block per half wave
-        const int nb = nt * (H >> 5);
-        const int per = (nb + gridDim.x - 1) / gridDim.x;
-        const int b0 = blockIdx.x * per, b1 = min(nb, b0 + per);
-        const int hw = threadIdx.x >> 5;
-        for (int b = b0; b < b1; b += 8) {
-            const int bb = b + hw;
-            const bool live = bb < b1;
-            const size_t blk = (size_t)t0 * (H >> 5) + (live ? bb : b0);
-            const float v = live ? xf[blk * 32 + (threadIdx.x & 31)] : 0.0f;
-            q8_image_store(v, live, qsc[hw], ximg + blk * kImgDw, img_natural != 0);
         }
     }
     __syncthreads();
@@ -1103,7 +1102,9 @@ hipError_t launch_router(const float* xf, const uint16_t* xb, const uint16_t* W,
     if (tile > 16) tile = 16;
     if (tile > T) tile = T;
     if (tile < 1) tile = 1;
-    dim3 grid((unsigned)((rows_total + 3) / 4), (unsigned)((T + tile - 1) / tile));
+    // row blocks (4 weight rows each), then with ximg the image blocks (8 q8_1 blocks of the tile each)
+    const int img_blocks = ximg ? (tile * (H / 32) + 7) / 8 : 0;
+    dim3 grid((unsigned)((rows_total + 3) / 4 + img_blocks), (unsigned)((T + tile - 1) / tile));
     const size_t lds = (size_t)tile * H * 2;
 #define SMOE_ROUTER(C)                                                                                          \
     hipLaunchKernelGGL(k_router<C>, grid, dim3(256), lds, s, xf, xb, W, w_inp, bias, H, E, rows_total, T, tile, \

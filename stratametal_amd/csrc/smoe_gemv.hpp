@@ -30,10 +30,17 @@ __device__ __forceinline__ float group_sum(float v, int lpr) {
     return v;
 }
 
-// The xor butterfly 32, 16, ..., 1 over the whole wave (the same sums as wave_sum_xor): distance 32 through
-// ds_bpermute, the rest as in xor_swap.
+// v + v[lane ^ 32] by one v_permlane32_swap: with both operands v, the two results hold the lower and the upper
+// half of v in both halves, and their sum is that addition (commutative, so bit for bit).
+__device__ __forceinline__ float add_xor32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_int(v), __float_as_int(v), false, false);
+    return __int_as_float(r[0]) + __int_as_float(r[1]);
+}
+
+// The xor butterfly 32, 16, ..., 1 over the whole wave (the same sums as wave_sum_xor): distance 32 by
+// add_xor32, the rest as in xor_swap.
 __device__ __forceinline__ float wave_sum_xor_fast(float v) {
-    v = v + __shfl_xor(v, 32, kWave);
+    v = add_xor32(v);
     v = v + xor_swap<16>(v);
     v = v + xor_swap<8>(v);
     v = v + xor_swap<4>(v);
@@ -48,9 +55,7 @@ template <int N>
 __device__ __forceinline__ void wave_sum_xor_fast_n(float (&v)[N]) {
     float t[N];
 #pragma unroll
-    for (int i = 0; i < N; ++i) t[i] = __shfl_xor(v[i], 32, kWave);
-#pragma unroll
-    for (int i = 0; i < N; ++i) v[i] = v[i] + t[i];
+    for (int i = 0; i < N; ++i) v[i] = add_xor32(v[i]);
 #pragma unroll
     for (int i = 0; i < N; ++i) t[i] = xor_swap<16>(v[i]);
 #pragma unroll
