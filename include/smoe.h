@@ -143,6 +143,19 @@ smoe_status smoe_swiglu_q8(const float* gate, const float* up, int64_t n, uint8_
 smoe_status smoe_combine(const float* parts, const float* weights, const float* shared, float* y, int32_t n_embd,
                          int32_t k, void* hip_stream);
 
+/* One expert's whole FFN on an assembled blob [gate rows | up rows | down rows] (each row n_embd values of
+ * gu_type, resp. n_ff values of d_type): gate = W_g x, up = W_u x, hq = q8_1(silu(gate) * up), y = W_d hq for
+ * n_tok q8_1 rows x_q8 of n_embd; y is (n_tok, n_embd) f32.  As the reference, the gate/up type must have
+ * 256-value blocks (here IQ2_S; a 64-value type such as Q2_0 is a down quant and refused with SMOE_ETYPE),
+ * n_ff % 32 == 0, and the blob must hold smoe_expert_bytes.  `scratch` (smoe_expert_scratch_bytes, 256-byte
+ * aligned) holds gate, up and hq; nothing is allocated.
+ * Replaces iq_expert / iq_expert_bytes (metal/include/strata/metal/iq.hpp:56-65, metal/src/iq.mm:171-199). */
+size_t smoe_expert_bytes(int32_t gu_type, int32_t d_type, int64_t n_embd, int64_t n_ff); /* 0 when refused */
+size_t smoe_expert_scratch_bytes(int64_t n_embd, int64_t n_ff, int64_t n_tok);
+smoe_status smoe_expert(const void* blob, size_t blob_bytes, const uint8_t* x_q8, int32_t gu_type, int32_t d_type,
+                        int64_t n_embd, int64_t n_ff, int64_t n_tok, float* y, void* scratch, size_t scratch_bytes,
+                        void* hip_stream);
+
 /* ids [n_tokens][k] -> counts [E], offsets [E+1], perm [T*k], slot [T*k]: the canonical stable dispatch
  * (ascending pair index within an expert).  Replaces prefill::fused::group
  * (include/strata/prefill/moe_fused.hpp:46-51) with a fixed in-expert order. */

@@ -1,0 +1,176 @@
+// include/smoe_ffn.hpp - the C++ FfnExec-shaped operator over the C ABI in smoe.h (header-only).
+//
+// Mirrors the reference's per-layer feed-forward operator, FfnExec::load / FfnExec::run
+// (metal/include/strata/metal/layer_exec.hpp:113-140), for its MoE interior (metal/src/layer_exec.cpp:470-530,
+// `mixed` to `combined`): load() takes the layer's device tensors and geometry once and owns every buffer the
+// call needs, sized for a maximum token count, so that run() allocates nothing; status codes become
+// exceptions (the reference throws MetalError, metal/include/strata/metal/device.hpp:28-31); a traced run
+// copies the stage outputs to host vectors, as FfnTrace does (layer_exec.hpp:100-109).  Uses only smoe.h and
+// the HIP runtime.
+#pragma once
+
+#include "smoe.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+#include <utility>
+#include <vector>
+
+namespace smoe {
+
+// A refused or failed call: the smoe_status and the library's reason.
+struct Error : std::runtime_error {
+    smoe_status status;
+    Error(smoe_status s, const std::string& what) : std::runtime_error(what), status(s) {}
+};
+
+inline void check(smoe_status s, const char* where) {
+    if (s != SMOE_OK) throw Error(s, std::string(where) + ": " + smoe_status_str(s) + ": " + smoe_last_error());
+}
+inline void check_hip(hipError_t e, const char* where) {
+    if (e != hipSuccess) throw Error(SMOE_EDEVICE, std::string(where) + ": " + hipGetErrorString(e));
+}
+
+// What one MoE pass produced, on the host (the MoE fields of the reference's FfnTrace, same names where they
+// correspond: route = router logits, route_w = routing weights, sgate = the shared expert's gate dot).
+struct FfnTrace {
+    std::vector<float> mixed, combined;  // [T][n_embd] input and output
+    std::vector<float> route;            // [T][n_expert]
+    std::vector<int32_t> ids;            // [T][k], selection order
+    std::vector<float> route_w;          // [T][k]
+    std::vector<float> sgate;            // [T] (before the sigmoid)
+    std::vector<int32_t> counts, offsets, perm, slot;  // the dispatch: [E], [E+1], [T*k], [T*k]
+    std::vector<float> stage_ms;         // router, route, gate/up, down, combine
+};
+
+class FfnExec {
+   public:
+    // The layer's tensors (device pointers into the loaded model, e.g. a GGUF mapping) and geometry; buffers
+    // for up to `max_tokens` tokens per run, and for tracing when `with_trace`.
+    static FfnExec load(const smoe_geom& geom, const smoe_weights& weights, int32_t max_tokens, bool with_trace = false) {
+        FfnExec f;
+        f.g_ = geom;
+        f.w_ = weights;
+        f.max_tokens_ = max_tokens;
+        f.ws_bytes_ = smoe_workspace_bytes(&f.g_, max_tokens);
+        if (f.ws_bytes_ == 0) throw Error(SMOE_EINVAL, std::string("FfnExec::load: ") + smoe_last_error());
+        check_hip(hipMalloc(&f.ws_, f.ws_bytes_), "FfnExec::load workspace");
+        if (with_trace) {
+            const size_t T = (size_t)max_tokens, E = (size_t)geom.n_expert, K = (size_t)geom.top_k;
+            f.tr_bytes_ = 4 * (T * E + 2 * T * K + E + (E + 1) + 2 * T * K + T);
+            check_hip(hipMalloc(&f.tr_, f.tr_bytes_), "FfnExec::load trace");
+            for (hipEvent_t& e : f.ev_) check_hip(hipEventCreate(&e), "FfnExec::load events");
+        }
+        return f;
+    }
+
+    FfnExec() = default;
+    FfnExec(const FfnExec&) = delete;
+    FfnExec& operator=(const FfnExec&) = delete;
+    FfnExec(FfnExec&& o) noexcept { *this = std::move(o); }
+    FfnExec& operator=(FfnExec&& o) noexcept {
+        if (this != &o) {
+            release();
+            g_ = o.g_;
+            w_ = o.w_;
+            max_tokens_ = o.max_tokens_;
+            ws_ = std::exchange(o.ws_, nullptr);
+            ws_bytes_ = std::exchange(o.ws_bytes_, 0);
+            tr_ = std::exchange(o.tr_, nullptr);
+            tr_bytes_ = std::exchange(o.tr_bytes_, 0);
+            for (int i = 0; i < SMOE_STAGE_EVENTS; ++i) ev_[i] = std::exchange(o.ev_[i], nullptr);
+        }
+        return *this;
+    }
+    ~FfnExec() { release(); }
+
+    // combined[T][n_embd] = MoE(mixed[T][n_embd]) (device pointers), the shared expert added when `add_shared`.
+    // Enqueued on `stream`; a traced run (`trace` non-null, load(with_trace)) waits for it and fills `trace`.
+    void run(const float* mixed, float* combined, int32_t n_tokens, bool add_shared, FfnTrace* trace = nullptr,
+             hipStream_t stream = nullptr) {
+        if (n_tokens > max_tokens_)
+            throw Error(SMOE_ESIZE, "FfnExec::run: " + std::to_string(n_tokens) + " tokens, loaded for " +
+                                        std::to_string(max_tokens_));
+        if (trace && !tr_) throw Error(SMOE_EINVAL, "FfnExec::run: traced run of an operator loaded without tracing");
+        smoe_trace t{};
+        void* events[SMOE_STAGE_EVENTS];
+        if (trace) {
+            t = trace_ptrs();
+            for (int i = 0; i < SMOE_STAGE_EVENTS; ++i) events[i] = ev_[i];
+            t.stage_events = events;
+        }
+        check(smoe_forward(&g_, &w_, mixed, n_tokens, combined, add_shared ? 1 : 0, ws_, ws_bytes_,
+                           trace ? &t : nullptr, stream),
+              "FfnExec::run");
+        if (!trace) return;
+        check_hip(hipStreamSynchronize(stream), "FfnExec::run sync");
+        const size_t T = (size_t)n_tokens, H = (size_t)g_.n_embd, E = (size_t)g_.n_expert, K = (size_t)g_.top_k;
+        auto get = [](auto& v, const void* src, size_t n) {
+            v.resize(n);
+            check_hip(hipMemcpy(v.data(), src, n * sizeof(v[0]), hipMemcpyDeviceToHost), "FfnExec trace copy");
+        };
+        get(trace->mixed, mixed, T * H);
+        get(trace->combined, combined, T * H);
+        get(trace->route, t.logits, T * E);
+        get(trace->ids, t.ids, T * K);
+        get(trace->route_w, t.weights, T * K);
+        get(trace->counts, t.counts, E);
+        get(trace->offsets, t.offsets, E + 1);
+        get(trace->perm, t.perm, T * K);
+        get(trace->slot, t.slot, T * K);
+        if (g_.sh_type >= 0) get(trace->sgate, t.sgate, T);
+        else trace->sgate.clear();
+        trace->stage_ms.assign(SMOE_STAGE_EVENTS - 1, 0.0f);
+        for (int i = 0; i + 1 < SMOE_STAGE_EVENTS; ++i)
+            check_hip(hipEventElapsedTime(&trace->stage_ms[i], ev_[i], ev_[i + 1]), "FfnExec stage time");
+    }
+
+    // Device bytes this operator owns (workspace and trace buffers; the weights are the caller's).
+    uint64_t gpu_bytes() const { return ws_bytes_ + tr_bytes_; }
+    const smoe_geom& geom() const { return g_; }
+
+   private:
+    smoe_trace trace_ptrs() const {
+        const size_t T = (size_t)max_tokens_, E = (size_t)g_.n_expert, K = (size_t)g_.top_k;
+        char* p = static_cast<char*>(tr_);
+        smoe_trace t{};
+        t.logits = reinterpret_cast<float*>(p);
+        p += 4 * T * E;
+        t.ids = reinterpret_cast<int32_t*>(p);
+        p += 4 * T * K;
+        t.weights = reinterpret_cast<float*>(p);
+        p += 4 * T * K;
+        t.counts = reinterpret_cast<int32_t*>(p);
+        p += 4 * E;
+        t.offsets = reinterpret_cast<int32_t*>(p);
+        p += 4 * (E + 1);
+        t.perm = reinterpret_cast<int32_t*>(p);
+        p += 4 * T * K;
+        t.slot = reinterpret_cast<int32_t*>(p);
+        p += 4 * T * K;
+        t.sgate = g_.sh_type >= 0 ? reinterpret_cast<float*>(p) : nullptr;
+        return t;
+    }
+    void release() noexcept {
+        if (ws_) (void)hipFree(ws_);
+        if (tr_) (void)hipFree(tr_);
+        for (hipEvent_t& e : ev_)
+            if (e) (void)hipEventDestroy(e);
+        ws_ = tr_ = nullptr;
+        for (hipEvent_t& e : ev_) e = nullptr;
+    }
+
+    smoe_geom g_{};
+    smoe_weights w_{};
+    int32_t max_tokens_ = 0;
+    void* ws_ = nullptr;
+    size_t ws_bytes_ = 0;
+    void* tr_ = nullptr;
+    size_t tr_bytes_ = 0;
+    hipEvent_t ev_[SMOE_STAGE_EVENTS] = {};
+};
+
+}  // namespace smoe

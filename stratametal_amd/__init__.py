@@ -73,6 +73,9 @@ def lib():
             "smoe_swiglu_q8": (i32, [vp, vp, i64, vp, vp]),
             "smoe_combine": (i32, [vp, vp, vp, vp, i32, i32, vp]),
             "smoe_dispatch": (i32, [vp, i32, i32, i32, vp, vp, vp, vp, vp]),
+            "smoe_expert_bytes": (C.c_size_t, [i32, i32, i64, i64]),
+            "smoe_expert_scratch_bytes": (C.c_size_t, [i64, i64, i64]),
+            "smoe_expert": (i32, [vp, C.c_size_t, vp, i32, i32, i64, i64, i64, vp, vp, C.c_size_t, vp]),
             "smoe_synth_blocks": (i32, [i32, u64, u64, i64, f32, vp, vp]),
             "smoe_synth_bf16": (i32, [u64, u64, i64, f32, vp, vp]),
             "smoe_synth_normal": (i32, [u64, u64, i64, f32, vp, vp]),
@@ -282,6 +285,19 @@ def mmvq(wtype: int, w, x_q8, n_in: int, n_out: int, n_col: int = 1, byte_off: i
     y = torch.empty((n_col, n_out), dtype=torch.float32, device=w.device)
     _check(lib().smoe_mmvq(wtype, w.data_ptr(), byte_off, x_q8.data_ptr(), n_in, n_out, n_col, y.data_ptr(),
                            _stream(stream)))
+    return y
+
+
+def expert(blob, x_q8, gu_type: int, d_type: int, n_embd: int, n_ff: int, n_tok: int, stream=None):
+    """One expert's FFN on a [gate | up | down] blob (smoe_expert; the reference's iq_expert)."""
+    import torch
+    L = lib()
+    scratch = torch.empty(L.smoe_expert_scratch_bytes(n_embd, n_ff, n_tok) + 256, dtype=torch.uint8,
+                          device=blob.device)
+    base = (scratch.data_ptr() + 255) & ~255
+    y = torch.empty((n_tok, n_embd), dtype=torch.float32, device=blob.device)
+    _check(L.smoe_expert(blob.data_ptr(), blob.numel(), x_q8.data_ptr(), gu_type, d_type, n_embd, n_ff, n_tok,
+                         y.data_ptr(), base, scratch.numel() - (base - scratch.data_ptr()), _stream(stream)))
     return y
 
 

@@ -18,6 +18,7 @@ CSRC = os.path.join(PKG, "csrc")
 BUILD = os.path.join(PKG, "_build")
 LIBDIR = os.path.join(PKG, "lib")
 LIB = os.path.join(LIBDIR, "libsmoe.so")
+DEMO = os.path.join(LIBDIR, "smoe_ffn_demo")  # the C++ operator (include/smoe_ffn.hpp) end to end, over libsmoe.so
 
 ARCH = "gfx950"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -57,8 +58,14 @@ def build(verbose: bool = False) -> str:
     if out.returncode != 0:
         raise RuntimeError(f"link failed:\n{out.stderr}")
     os.replace(tmp, LIB)
+    cmd = [HIPCC, *COMMON, "-x", "hip", os.path.join(CSRC, "smoe_ffn_demo.cpp"), "-L", LIBDIR, "-lsmoe",
+           "-Wl,-rpath,$ORIGIN", "-o", DEMO + ".tmp"]
+    out = subprocess.run(cmd, capture_output=True, text=True)
+    if out.returncode != 0:
+        raise RuntimeError(f"smoe_ffn_demo failed:\n{out.stderr}")
+    os.replace(DEMO + ".tmp", DEMO)
     if verbose:
-        print("built", LIB)
+        print("built", LIB, "and", DEMO)
     return LIB
 
 

@@ -159,7 +159,7 @@ const char* smoe_status_str(smoe_status s) {
 
 const char* smoe_last_error(void) { return g_last.c_str(); }
 
-int32_t smoe_abi_version(void) { return 100; }
+int32_t smoe_abi_version(void) { return 101; }
 
 size_t smoe_workspace_bytes(const smoe_geom* g, int32_t max_tokens) {
     if (check_geom(g) != SMOE_OK || max_tokens < 0) return 0;
@@ -367,6 +367,81 @@ smoe_status smoe_swiglu_q8(const float* gate, const float* up, int64_t n, uint8_
     if (!gate || !up || !y) return fail(SMOE_ENULL, "swiglu_q8: NULL buffer");
     if (!aligned(y, 4)) return fail(SMOE_EALIGN, "swiglu_q8: y must be 4-byte aligned");
     SMOE_TRY(smoe::launch_swiglu_q8(gate, up, n, y, stream_of(hip_stream)), "swiglu_q8");
+    return ok();
+}
+
+namespace {
+int64_t type_row_bytes(int32_t type, int64_t n) {
+    return type == SMOE_Q2_0 ? n / 64 * 18 : type == SMOE_IQ2_S ? n / 256 * 82 : -1;
+}
+// The reference's iq_expert_bytes checks (metal/src/iq.mm:171-180); "" when the expert is well formed.
+std::string expert_refusal(int32_t gu_type, int32_t d_type, int64_t n_embd, int64_t n_ff, smoe_status& code) {
+    code = SMOE_ETYPE;
+    if ((gu_type != SMOE_Q2_0 && gu_type != SMOE_IQ2_S) || (d_type != SMOE_Q2_0 && d_type != SMOE_IQ2_S))
+        return "expert: type is not Q2_0 or IQ2_S";
+    if (gu_type != SMOE_IQ2_S) return "expert: gate type is a down quant (64-value blocks)";
+    code = SMOE_EINVAL;
+    if (n_embd <= 0 || n_ff <= 0) return "expert: empty expert";
+    if (n_ff % 32) return "expert: n_ff must be a multiple of 32";
+    if (!smoe::iq2_shape_ok((int)n_embd) || n_embd > kMaxEmbd) return "expert: IQ2_S n_embd must be 512, 1024 or 2048";
+    if (d_type == SMOE_Q2_0 && (n_ff > kMaxFF || !smoe::gemv_shape_ok((int)n_ff)))
+        return "expert: Q2_0 n_ff must be 128 times a power of two times at most 8";
+    if (d_type == SMOE_IQ2_S && !smoe::iq2_shape_ok((int)n_ff)) return "expert: IQ2_S n_ff must be 512, 1024 or 2048";
+    return "";
+}
+}  // namespace
+
+size_t smoe_expert_bytes(int32_t gu_type, int32_t d_type, int64_t n_embd, int64_t n_ff) {
+    smoe_status code;
+    const std::string why = expert_refusal(gu_type, d_type, n_embd, n_ff, code);
+    if (!why.empty()) {
+        fail(code, why);
+        return 0;
+    }
+    ok();
+    return (size_t)(2 * n_ff * type_row_bytes(gu_type, n_embd) + n_embd * type_row_bytes(d_type, n_ff));
+}
+
+size_t smoe_expert_scratch_bytes(int64_t n_embd, int64_t n_ff, int64_t n_tok) {
+    (void)n_embd;
+    if (n_tok < 0 || n_ff < 0) return 0;
+    const size_t f32 = up((size_t)(n_tok * n_ff * 4));
+    return 2 * f32 + up((size_t)(n_tok * (n_ff / 32) * 36));
+}
+
+smoe_status smoe_expert(const void* blob, size_t blob_bytes, const uint8_t* x_q8, int32_t gu_type, int32_t d_type,
+                        int64_t n_embd, int64_t n_ff, int64_t n_tok, float* y, void* scratch, size_t scratch_bytes,
+                        void* hip_stream) {
+    if (n_tok == 0) return ok();
+    if (n_tok < 0) return fail(SMOE_EINVAL, "expert: negative token count");
+    if (n_tok > (1 << 20)) return fail(SMOE_EINVAL, "expert: more than 2^20 tokens");
+    smoe_status code;
+    const std::string why = expert_refusal(gu_type, d_type, n_embd, n_ff, code);
+    if (!why.empty()) return fail(code, why);
+    const size_t need = (size_t)(2 * n_ff * type_row_bytes(gu_type, n_embd) + n_embd * type_row_bytes(d_type, n_ff));
+    if (blob_bytes < need)
+        return fail(SMOE_ESIZE, "expert blob is " + std::to_string(blob_bytes) + " bytes, needs " + std::to_string(need));
+    const size_t sneed = smoe_expert_scratch_bytes(n_embd, n_ff, n_tok);
+    if (scratch_bytes < sneed)
+        return fail(SMOE_ESIZE, "expert scratch is " + std::to_string(scratch_bytes) + " bytes, needs " + std::to_string(sneed));
+    if (!blob || !x_q8 || !y || !scratch) return fail(SMOE_ENULL, "expert: NULL buffer");
+    if (!aligned(blob, 4) || !aligned(x_q8, 4) || !aligned(y, 4)) return fail(SMOE_EALIGN, "expert: buffers must be 4-byte aligned");
+    if (!aligned(scratch, kAlign)) return fail(SMOE_EALIGN, "expert: scratch must be 256-byte aligned");
+    uint8_t* sc = static_cast<uint8_t*>(scratch);
+    const size_t f32 = up((size_t)(n_tok * n_ff * 4));
+    float* gate = reinterpret_cast<float*>(sc);
+    float* upv = reinterpret_cast<float*>(sc + f32);
+    uint8_t* hq = sc + 2 * f32;
+    const int64_t up_off = n_ff * type_row_bytes(gu_type, n_embd), down_off = 2 * up_off;
+    const uint8_t* b = static_cast<const uint8_t*>(blob);
+    const hipStream_t st = stream_of(hip_stream);
+    if (gu_type == SMOE_IQ2_S) {
+        SMOE_TRY(smoe::launch_iq2_mmvq(b, x_q8, (int)n_embd, (int)n_ff, (int)n_tok, gate, st), "expert gate");
+        SMOE_TRY(smoe::launch_iq2_mmvq(b + up_off, x_q8, (int)n_embd, (int)n_ff, (int)n_tok, upv, st), "expert up");
+    }
+    SMOE_TRY(smoe::launch_swiglu_q8(gate, upv, n_tok * n_ff, hq, st), "expert swiglu");
+    if (d_type == SMOE_IQ2_S) SMOE_TRY(smoe::launch_iq2_mmvq(b + down_off, hq, (int)n_ff, (int)n_embd, (int)n_tok, y, st), "expert down");
+    else SMOE_TRY(smoe::launch_q2_mmvq(b + down_off, hq, (int)n_ff, (int)n_embd, (int)n_tok, y, st), "expert down");
     return ok();
 }
 

@@ -1,0 +1,88 @@
+// stratametal_amd/csrc/smoe_ffn_demo.cpp - the C++ operator (include/smoe_ffn.hpp) end to end: a seeded
+// synthetic layer generated on the device (the same streams as stratametal_amd.synth_layer: 1 gate, 2 up,
+// 3 down, 4 router, 5/6/7 shared gate/up/down, 8 shared gate_inp; x from stream 100), one traced
+// FfnExec::run, and the trace written to a file for the host check.
+//
+//   smoe_ffn_demo OUT n_tokens seed n_embd n_ff n_ff_shared n_expert top_k
+//
+// OUT receives, little-endian: int32 T, H, E, K; f32 combined [T][H]; int32 ids [T][K]; f32 route_w [T][K];
+// int32 counts [E]; f32 stage_ms [5].
+#include "smoe_ffn.hpp"
+
+#include <cstdio>
+#include <cstdlib>
+
+namespace {
+void* dev_alloc(size_t bytes) {
+    void* p = nullptr;
+    smoe::check_hip(hipMalloc(&p, bytes), "hipMalloc");
+    return p;
+}
+size_t block_bytes(int32_t type, int64_t n) { return type == SMOE_Q2_0 ? n / 64 * 18 : n / 256 * 82; }
+}  // namespace
+
+int main(int argc, char** argv) {
+    if (argc != 9) {
+        std::fprintf(stderr, "usage: %s OUT n_tokens seed n_embd n_ff n_ff_shared n_expert top_k\n", argv[0]);
+        return 2;
+    }
+    try {
+        const int32_t T = std::atoi(argv[2]);
+        const uint64_t seed = std::strtoull(argv[3], nullptr, 10);
+        smoe_geom g{};
+        g.n_embd = std::atoi(argv[4]);
+        g.n_ff = std::atoi(argv[5]);
+        g.n_ff_shared = std::atoi(argv[6]);
+        g.n_expert = std::atoi(argv[7]);
+        g.top_k = std::atoi(argv[8]);
+        g.w_type = SMOE_Q2_0;
+        g.sh_type = SMOE_Q2_0;
+        g.router_dtype = 0;
+        const int64_t H = g.n_embd, F = g.n_ff, Fs = g.n_ff_shared, E = g.n_expert;
+        const float sigma = 0.02f;
+        auto blocks = [&](uint64_t stream_id, int64_t n) {
+            void* p = dev_alloc(block_bytes(SMOE_Q2_0, n));
+            smoe::check(smoe_synth_blocks(SMOE_Q2_0, seed, stream_id, n, sigma, p, nullptr), "synth blocks");
+            return p;
+        };
+        auto bf16 = [&](uint64_t stream_id, int64_t n) {
+            void* p = dev_alloc((size_t)n * 2);
+            smoe::check(smoe_synth_bf16(seed, stream_id, n, sigma, static_cast<uint16_t*>(p), nullptr), "synth bf16");
+            return static_cast<const uint16_t*>(p);
+        };
+        smoe_weights w{};
+        w.gate_exps = blocks(1, E * F * H);
+        w.up_exps = blocks(2, E * F * H);
+        w.down_exps = blocks(3, E * H * F);
+        w.router = bf16(4, E * H);
+        w.gate_sh = blocks(5, Fs * H);
+        w.up_sh = blocks(6, Fs * H);
+        w.down_sh = blocks(7, H * Fs);
+        w.gate_inp_sh = bf16(8, H);
+        float* x = static_cast<float*>(dev_alloc((size_t)T * H * 4));
+        float* y = static_cast<float*>(dev_alloc((size_t)T * H * 4));
+        smoe::check(smoe_synth_normal(seed, 100, (int64_t)T * H, 1.0f, x, nullptr), "synth x");
+
+        smoe::FfnExec ffn = smoe::FfnExec::load(g, w, T, /*with_trace*/ true);
+        smoe::FfnTrace tr;
+        ffn.run(x, y, T, /*add_shared*/ true, &tr);
+
+        FILE* f = std::fopen(argv[1], "wb");
+        if (!f) throw std::runtime_error(std::string("cannot open ") + argv[1]);
+        const int32_t hdr[4] = {T, g.n_embd, g.n_expert, g.top_k};
+        std::fwrite(hdr, 4, 4, f);
+        std::fwrite(tr.combined.data(), 4, tr.combined.size(), f);
+        std::fwrite(tr.ids.data(), 4, tr.ids.size(), f);
+        std::fwrite(tr.route_w.data(), 4, tr.route_w.size(), f);
+        std::fwrite(tr.counts.data(), 4, tr.counts.size(), f);
+        std::fwrite(tr.stage_ms.data(), 4, tr.stage_ms.size(), f);
+        std::fclose(f);
+        std::printf("FfnExec: %d tokens, %llu device bytes owned, stages (ms):", T, (unsigned long long)ffn.gpu_bytes());
+        for (float m : tr.stage_ms) std::printf(" %.4f", m);
+        std::printf("\n");
+    } catch (const std::exception& e) {
+        std::fprintf(stderr, "smoe_ffn_demo: %s\n", e.what());
+        return 1;
+    }
+    return 0;
+}

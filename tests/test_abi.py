@@ -34,7 +34,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_status_strings():
     lib = S.lib()
-    assert lib.smoe_abi_version() == 100
+    assert lib.smoe_abi_version() == 101
     for code in (0, -1, -2, -3, -4, -5, -6):
         assert lib.smoe_status_str(code)
 
@@ -126,3 +126,24 @@ def test_missing_library_fails_loudly(monkeypatch):
     monkeypatch.setattr(S, "LIB_PATH", "/nonexistent/libsmoe.so")
     with pytest.raises(ImportError):
         S.lib()
+
+
+def test_expert_sizes_and_refusals():
+    L = S.lib()
+    # the reference's iq_expert_bytes: 2 * n_ff * gate row + n_embd * down row (metal/src/iq.mm:171-180)
+    assert L.smoe_expert_bytes(S.IQ2_S, S.Q2_0, 2048, 512) == 2 * 512 * (2048 // 256 * 82) + 2048 * (512 // 64 * 18)
+    assert L.smoe_expert_bytes(S.IQ2_S, S.IQ2_S, 2048, 512) == 2 * 512 * 656 + 2048 * (512 // 256 * 82)
+    assert L.smoe_expert_bytes(S.Q2_0, S.Q2_0, 2048, 512) == 0
+    assert b"down quant" in L.smoe_last_error()
+    assert L.smoe_expert_bytes(S.IQ2_S, S.Q2_0, 2048, 0) == 0
+    assert L.smoe_expert_bytes(S.IQ2_S, 13, 2048, 512) == 0
+    need = L.smoe_expert_bytes(S.IQ2_S, S.Q2_0, 2048, 512)
+    sc = L.smoe_expert_scratch_bytes(2048, 512, 4)
+    args = lambda blob_bytes, gu, n_tok, sc_bytes: (FAKE, blob_bytes, FAKE, gu, S.Q2_0, 2048, 512, n_tok, FAKE, FAKE,
+                                                    sc_bytes, None)
+    assert L.smoe_expert(*args(need, S.IQ2_S, 0, 0)) == 0          # zero tokens: nothing to do
+    assert L.smoe_expert(*args(need, S.IQ2_S, -1, sc)) == -1       # negative count
+    assert L.smoe_expert(*args(need, S.Q2_0, 4, sc)) == -3         # a 64-value gate type
+    assert L.smoe_expert(*args(need - 1, S.IQ2_S, 4, sc)) == -2    # blob too small
+    assert f"expert blob is {need - 1} bytes, needs {need}".encode() in L.smoe_last_error()
+    assert L.smoe_expert(*args(need, S.IQ2_S, 4, sc - 1)) == -2    # scratch too small

@@ -129,3 +129,27 @@ def test_iq2_s_refusals(torch):
     y = host(torch, ml2.forward(dev(torch, x)))
     assert np.array_equal(bits(y), bits(O.moe_decode_dev(O.Geom(**vars(ok)), O.make_weights(O.Geom(**vars(ok)), 3), x,
                                                            n_threads=16)))
+
+
+@pytest.mark.parametrize("d_type,n_ff,n_tok", [(42, 512, 3), (22, 512, 2), (42, 1024, 1)])
+def test_expert_blob_bitwise(torch, d_type, n_ff, n_tok):
+    """smoe_expert (the reference's iq_expert): gate and up IQ2_S rows, SwiGLU to q8_1, down rows of d_type, on
+    one [gate | up | down] blob; bitwise against the oracle's stage functions composed the same way
+    (metal/src/iq.mm:182-199)."""
+    say(f"case: expert blob d_type={d_type} n_ff={n_ff} n_tok={n_tok}")
+    n_embd = 2048
+    g = O.gen_iq2_s(61, 1, n_ff * n_embd // 256)
+    u = O.gen_iq2_s(61, 2, n_ff * n_embd // 256)
+    d = O.gen_q2_0(61, 3, n_embd * n_ff // 64) if d_type == 42 else O.gen_iq2_s(61, 3, n_embd * n_ff // 256)
+    blob = np.concatenate([g.view(np.uint8).ravel(), u.view(np.uint8).ravel(), d.view(np.uint8).ravel()])
+    assert blob.size == S.lib().smoe_expert_bytes(22, d_type, n_embd, n_ff)
+    xq = O.quant_q8_1(O.gen_normal(61, 4, n_tok * n_embd))
+    y = host(torch, S.expert(dev(torch, blob), dev(torch, xq), 22, d_type, n_embd, n_ff, n_tok))
+    xb = n_embd // 32 * 36
+    gate = np.concatenate([O.iq2_s_gemv_dev(g, xq[c * xb:(c + 1) * xb], n_embd, n_ff) for c in range(n_tok)])
+    up = np.concatenate([O.iq2_s_gemv_dev(u, xq[c * xb:(c + 1) * xb], n_embd, n_ff) for c in range(n_tok)])
+    hq = O.swiglu_q8(gate, up)
+    hb = n_ff // 32 * 36
+    for c in range(n_tok):
+        want = O.gemv_dev(d_type, d, hq[c * hb:(c + 1) * hb], n_ff, n_embd)
+        assert np.array_equal(bits(y[c]), bits(want)), c
