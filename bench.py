@@ -45,9 +45,11 @@ def _args():
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB five times (the reference kernel that scales the "
                          "FETCH_SIZE / WRITE_SIZE counters to bytes), then exit")
-    ap.add_argument("--only", choices=("b1", "prefill", "iq2"), default=None,
+    ap.add_argument("--only", choices=("b1", "prefill", "iq2", "stack"), default=None,
                     help="measure only this secondary workload (for a profiler run); prints its summary, no JSON line")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--stack-prefill", type=int, default=4096, help="prefill tokens of the 48-layer stack")
+    ap.add_argument("--stack-decode", type=int, default=64, help="decode steps of the 48-layer stack")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     return ap.parse_args()
 
@@ -252,6 +254,81 @@ def prefill(S, torch, g, a):
     return out
 
 
+def stack48(S, torch, g, stack, a):
+    """the resident layers chained as x_{l+1} = RMSNorm(x_l + MoE_l(x_l)) (unit weight, eps 1e-6):
+    one `--stack-prefill` token prefill through every layer (the MFMA contract), then `--stack-decode` decode
+    steps at batch 1 (each step one graph of every layer and junction, replayed on a fresh token)."""
+    import ctypes as C
+    L = len(stack.layers)
+    H, Tp, steps = g.n_embd, a.stack_prefill, a.stack_decode
+    ws_bytes = S.workspace_bytes(g, Tp)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
+    lib = S.lib()
+
+    def layer(l, x, y, T):
+        S._check(lib.smoe_forward(C.byref(stack.gc), C.byref(stack.wc[l]), x.data_ptr(), T, y.data_ptr(), 1,
+                                  ws.data_ptr(), ws_bytes, None, S._stream()))
+        S.residual_rmsnorm(x, y, 1e-6, out=x)
+
+    x0 = S.synth_normal(a.seed + 40, 100, Tp * H).view(Tp, H)
+    x = torch.empty_like(x0)
+    y = torch.empty_like(x0)
+    times = []
+    for rep in range(2):  # the first pass loads code and warms the allocator; the second is the measurement
+        x.copy_(x0)
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        ev0.record()
+        for l in range(L):
+            layer(l, x, y, Tp)
+        ev1.record()
+        torch.cuda.synchronize()
+        times.append(ev0.elapsed_time(ev1))
+    pre_ms = times[-1]
+    ex_flops, router_flops = prefill_flops(g, Tp)
+    out = {"layers": L, "prefill_tokens": Tp, "prefill_ms": pre_ms, "prefill_tok_s": Tp / (pre_ms * 1e-3),
+           "prefill_tflops": L * (ex_flops + router_flops) / (pre_ms * 1e-3) / 1e12,
+           "prefill_out_finite": bool(torch.isfinite(x).all().item())}
+    # decode: one graph per step over every layer, replayed on fresh tokens
+    xs = S.synth_normal(a.seed + 41, 100, steps * H).view(steps, H)
+    xin = torch.empty((1, H), dtype=torch.float32, device="cuda")
+    yb = torch.empty((1, H), dtype=torch.float32, device="cuda")
+    xin.copy_(xs[0:1])
+    for l in range(L):  # eager pass (code and workspace warm)
+        layer(l, xin, yb, 1)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    gs = torch.cuda.Stream()
+    gs.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(gs):
+        with torch.cuda.graph(graph, stream=gs):
+            for l in range(L):
+                layer(l, xin, yb, 1)
+    torch.cuda.synchronize()
+    xin.copy_(xs[0:1])
+    graph.replay()
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for s in range(steps):
+        xin.copy_(xs[s:s + 1])
+        graph.replay()
+    ev1.record()
+    torch.cuda.synchronize()
+    dec_ms = ev0.elapsed_time(ev1)
+    per_tok = dec_ms / steps
+    tok_bytes = L * bytes_model(S, g, 1, g.top_k)[0]
+    out.update({"decode_steps": steps, "decode_ms_per_token": per_tok, "decode_tok_s": 1e3 / per_tok,
+                "decode_bytes_per_token": tok_bytes, "decode_gbs": tok_bytes / (per_tok * 1e-3) / 1e9})
+    out["decode_hbm_frac"] = out["decode_gbs"] / HBM_PEAK_GBS
+    log("stack of %d: prefill %d tokens %.2f ms (%.0f tok/s, %.0f TFLOP/s), decode %.3f ms/token (%.0f tok/s, "
+        "%.0f GB/s)" % (L, Tp, pre_ms, out["prefill_tok_s"], out["prefill_tflops"], per_tok, out["decode_tok_s"],
+                        out["decode_gbs"]))
+    del ws, x, y, x0
+    torch.cuda.empty_cache()
+    return out
+
+
 def iq2_b64(S, torch, a):
     """batch 64, IQ2_S routed and shared experts, uniform routing (no bias), decode contract.
     `--iq2-layers` resident layers (about 0.5 GB each) so that steps do not hit the Infinity Cache."""
@@ -303,6 +380,9 @@ def main():
     stack = Stack(S, torch, g, a.layers, a.seed, max(a.tokens, 1))
     log(f"{a.layers} layers resident ({a.layers * (g.n_expert * g.expert_bytes() + g.shared_bytes()) / 1e9:.1f} GB) "
         f"in {time.perf_counter() - t_setup:.1f} s")
+    if a.only == "stack":
+        stack48(S, torch, g, stack, a)
+        return
     if a.only == "b1":
         r1 = measure(S, torch, stack, 1, a.steps, a.warmup, a.seed + 11)
         m1 = summarize(S, g, 1, r1, a.steps)
@@ -323,6 +403,7 @@ def main():
         extra["decode_b1"] = {k: m1[k] for k in ("ms_per_step", "tok_s", "touched_experts_avg", "layer_bytes_avg",
                                                  "layer_gbs", "stage_ms_avg", "gate_up_gbs", "down_gbs")}
         extra["decode_b1"]["layer_hbm_frac"] = m1["layer_gbs"] / HBM_PEAK_GBS
+        extra["stack48"] = stack48(S, torch, g, stack, a)
         extra["prefill_512"] = prefill(S, torch, g, a)
         extra["iq2_s_b64"] = iq2_b64(S, torch, a)
     extra["decode_b16_stages_ms"] = m16["stage_ms_avg"]

@@ -162,6 +162,14 @@ smoe_status smoe_expert(const void* blob, size_t blob_bytes, const uint8_t* x_q8
 smoe_status smoe_dispatch(const int32_t* ids, int32_t n_tokens, int32_t k, int32_t n_expert, int32_t* counts,
                           int32_t* offsets, int32_t* perm, int32_t* slot, void* hip_stream);
 
+/* out[t] = RMSNorm(x[t] + r[t]) with unit weight for n_rows rows of n <= 4096 f32 (r may be NULL; out may
+ * alias x): the layer junction of the stacked benchmark configuration, x_{l+1} = RMSNorm(x_l + MoE_l(x_l)),
+ * eps 1e-6 there.  No counterpart in the reference's MoE block (its layer walk normalises in the
+ * hyper-connection read, out of this block's scope); the row sum's order is fixed and restated by the test
+ * oracle. */
+smoe_status smoe_residual_rmsnorm(const float* x, const float* r, int32_t n_rows, int32_t n, float eps, float* out,
+                                  void* hip_stream);
+
 /* ---------------------------------------------------------------------------------------------- synthetic inputs
  * No counterpart in the reference: the seeded generators of the benchmark configurations (counter-based
  * SplitMix64; normals by Box-Muller).  Bitwise equal to the host generators of the test oracle. */

@@ -81,6 +81,7 @@ def lib():
             "or_silu_mul": (f32, [f32, f32]),
             "or_sigmoid": (f32, [f32]),
             "or_combine_dev": (None, [vp, vp, vp, i32, i32, vp]),
+            "or_residual_rmsnorm_dev": (None, [vp, vp, i32, i32, C.c_float, vp]),
             "or_combine_double": (None, [vp, vp, vp, i32, i32, vp]),
             "or_dispatch": (None, [vp, i32, i32, i32, vp, vp, vp, vp]),
             "or_moe_decode_dev": (i32, [vp, vp, vp, i32, vp, i32, vp, i32]),
@@ -296,6 +297,16 @@ def combine_dev(parts, w, shared):
     sh = None if shared is None else np.ascontiguousarray(shared, dtype=np.float32)
     lib().or_combine_dev(_p(parts), _p(w), None if sh is None else _p(sh), n, k, _p(y))
     return y
+
+
+def residual_rmsnorm_dev(x, r=None, eps: float = 1e-6):
+    """RMSNorm(x + r) per row, unit weight, in the device's order (the stacked configuration's junction)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    n = x.shape[-1]
+    rr = None if r is None else np.ascontiguousarray(r, dtype=np.float32)
+    out = np.empty_like(x)
+    lib().or_residual_rmsnorm_dev(_p(x), None if rr is None else _p(rr), x.size // n, n, eps, _p(out))
+    return out
 
 
 def combine_double(parts, w, shared):

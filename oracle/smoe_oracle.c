@@ -670,6 +670,42 @@ void or_combine_double(const float* parts, const float* w, const float* shared, 
 }
 
 /* ------------------------------------------------------------------------------------------------ */
+/* The stacked benchmark configuration's layer junction, x_{l+1} = RMSNorm(x_l + MoE_l(x_l)) with unit weight
+ * (the configuration's definition; the reference's MoE block has no such call).  Device order
+ * (stratametal_amd/csrc/smoe_decode.hip, k_residual_rmsnorm): s_j = x_j + r_j (s_j = x_j when r is NULL);
+ * thread i of 256 accumulates fmaf(s_j, s_j, acc) over j = i, i + 256, ... from 0; the 64 threads of each
+ * wave combine by the xor butterfly 32..1; the four wave sums add as ((w0 + w1) + w2) + w3;
+ * out_j = s_j * (1 / sqrtf(ss / n + eps)), IEEE division and square root. */
+void or_residual_rmsnorm_dev(const float* x, const float* r, int n_rows, int n, float eps, float* out) {
+    for (int t = 0; t < n_rows; ++t) {
+        const float* xr = x + (size_t)t * n;
+        const float* rr = r ? r + (size_t)t * n : NULL;
+        float th[256];
+        for (int i = 0; i < 256; ++i) {
+            float acc = 0.0f;
+            for (int j = i; j < n; j += 256) {
+                const float sj = rr ? xr[j] + rr[j] : xr[j];
+                acc = fmaf(sj, sj, acc);
+            }
+            th[i] = acc;
+        }
+        float ws[4];
+        for (int w = 0; w < 4; ++w) {
+            float* lane = th + 64 * w;
+            for (int o = 32; o > 0; o >>= 1) {
+                float nxt[64];
+                for (int l = 0; l < 64; ++l) nxt[l] = lane[l] + lane[l ^ o];
+                memcpy(lane, nxt, sizeof nxt);
+            }
+            ws[w] = lane[0];
+        }
+        const float ss = ((ws[0] + ws[1]) + ws[2]) + ws[3];
+        const float inv = 1.0f / sqrtf(ss / (float)n + eps);
+        for (int j = 0; j < n; ++j) out[(size_t)t * n + j] = (rr ? xr[j] + rr[j] : xr[j]) * inv;
+    }
+}
+
+/* ------------------------------------------------------------------------------------------------ */
 /* A10. Canonical dispatch: pair i = t*k + s; counts by expert; offsets = exclusive scan in ascending
  * expert; perm = stable counting sort (ascending i within an expert); slot[i] = position of i in perm.
  * The reference leaves the order open (include/strata/prefill/moe_fused.hpp:46-48); this fixes it. */

@@ -80,6 +80,7 @@ float or_silu_mul(float g, float u);
 float or_sigmoid(float z);
 
 /* ---- A9: combine */
+void or_residual_rmsnorm_dev(const float* x, const float* r, int n_rows, int n, float eps, float* out);
 void or_combine_dev(const float* parts, const float* w, const float* shared, int n_embd, int k, float* y);
 void or_combine_double(const float* parts, const float* w, const float* shared, int n_embd, int k, float* y);
 

@@ -74,6 +74,7 @@ def lib():
             "smoe_combine": (i32, [vp, vp, vp, vp, i32, i32, vp]),
             "smoe_dispatch": (i32, [vp, i32, i32, i32, vp, vp, vp, vp, vp]),
             "smoe_expert_bytes": (C.c_size_t, [i32, i32, i64, i64]),
+            "smoe_residual_rmsnorm": (i32, [vp, vp, i32, i32, f32, vp, vp]),
             "smoe_expert_scratch_bytes": (C.c_size_t, [i64, i64, i64]),
             "smoe_expert": (i32, [vp, C.c_size_t, vp, i32, i32, i64, i64, i64, vp, vp, C.c_size_t, vp]),
             "smoe_synth_blocks": (i32, [i32, u64, u64, i64, f32, vp, vp]),
@@ -299,6 +300,15 @@ def expert(blob, x_q8, gu_type: int, d_type: int, n_embd: int, n_ff: int, n_tok:
     _check(L.smoe_expert(blob.data_ptr(), blob.numel(), x_q8.data_ptr(), gu_type, d_type, n_embd, n_ff, n_tok,
                          y.data_ptr(), base, scratch.numel() - (base - scratch.data_ptr()), _stream(stream)))
     return y
+
+
+def residual_rmsnorm(x, r=None, eps: float = 1e-6, out=None, stream=None):
+    """RMSNorm(x + r) row by row with unit weight (smoe_residual_rmsnorm); `out` may be `x`."""
+    import torch
+    n = x.shape[-1]
+    out = torch.empty_like(x) if out is None else out
+    _check(lib().smoe_residual_rmsnorm(x.data_ptr(), _ptr(r), x.numel() // n, n, eps, out.data_ptr(), _stream(stream)))
+    return out
 
 
 def swiglu_q8(gate, up, stream=None):

@@ -159,7 +159,7 @@ const char* smoe_status_str(smoe_status s) {
 
 const char* smoe_last_error(void) { return g_last.c_str(); }
 
-int32_t smoe_abi_version(void) { return 101; }
+int32_t smoe_abi_version(void) { return 102; }
 
 size_t smoe_workspace_bytes(const smoe_geom* g, int32_t max_tokens) {
     if (check_geom(g) != SMOE_OK || max_tokens < 0) return 0;
@@ -442,6 +442,17 @@ smoe_status smoe_expert(const void* blob, size_t blob_bytes, const uint8_t* x_q8
     SMOE_TRY(smoe::launch_swiglu_q8(gate, upv, n_tok * n_ff, hq, st), "expert swiglu");
     if (d_type == SMOE_IQ2_S) SMOE_TRY(smoe::launch_iq2_mmvq(b + down_off, hq, (int)n_ff, (int)n_embd, (int)n_tok, y, st), "expert down");
     else SMOE_TRY(smoe::launch_q2_mmvq(b + down_off, hq, (int)n_ff, (int)n_embd, (int)n_tok, y, st), "expert down");
+    return ok();
+}
+
+smoe_status smoe_residual_rmsnorm(const float* x, const float* r, int32_t n_rows, int32_t n, float eps, float* out,
+                                  void* hip_stream) {
+    if (n_rows < 0 || n < 0) return fail(SMOE_EINVAL, "residual_rmsnorm: negative size");
+    if (n_rows == 0 || n == 0) return ok();
+    if (n > 4096) return fail(SMOE_EINVAL, "residual_rmsnorm: rows longer than 4096");
+    if (!(eps >= 0.0f)) return fail(SMOE_EINVAL, "residual_rmsnorm: eps must be non-negative");
+    if (!x || !out) return fail(SMOE_ENULL, "residual_rmsnorm: NULL buffer");
+    SMOE_TRY(smoe::launch_residual_rmsnorm(x, r, n_rows, n, eps, out, stream_of(hip_stream)), "residual_rmsnorm");
     return ok();
 }
 

@@ -31,6 +31,8 @@ hipError_t launch_q2_gu(const uint8_t* gate_exps, const uint8_t* up_exps, const 
 hipError_t launch_q2_down(const uint8_t* down_exps, const uint8_t* down_sh, const uint32_t* himg, int h_blocks,
                           const float* sg, const int4* items, int H, int F, int Fs, int max_items, float* Y,
                           hipStream_t s);
+hipError_t launch_residual_rmsnorm(const float* x, const float* r, int n_rows, int n, float eps, float* out,
+                                   hipStream_t s);
 hipError_t launch_combine(const float* Y, const int32_t* slot, const float* wts, int k, int H, int P, int T,
                           int add_shared, float* y, hipStream_t s);
 hipError_t launch_combine_parts(const float* parts, const float* wts, const float* shared, int k, int n, float* y,

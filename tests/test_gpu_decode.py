@@ -301,3 +301,14 @@ def test_forward_zero_tokens_and_refusals_leave_output(torch):
                               small.ws.data_ptr(), small.ws_bytes, None, S._stream())
     assert st == -2
     assert (host(torch, y) == 7.0).all()
+
+
+@pytest.mark.parametrize("rows,n,with_r,inplace", [(16, 2048, True, False), (3, 2560, True, True), (5, 300, False, False),
+                                                   (1, 4096, True, False)])
+def test_residual_rmsnorm_bitwise(torch, rows, n, with_r, inplace):
+    say(f"case: residual_rmsnorm rows={rows} n={n} r={with_r} inplace={inplace}")
+    x = O.gen_normal(9, n, rows * n).reshape(rows, n)
+    r = O.gen_normal(9, n + 7, rows * n).reshape(rows, n) if with_r else None
+    xd = dev(torch, x)
+    out = S.residual_rmsnorm(xd, None if r is None else dev(torch, r), 1e-6, out=xd if inplace else None)
+    assert np.array_equal(bits(host(torch, out)), bits(O.residual_rmsnorm_dev(x, r, 1e-6)))

@@ -440,3 +440,23 @@ def test_prefill_oracle_against_independent_fp64_contract():
     for kw in (dict(round_x=False), dict(round_h=False)):
         trap = _prefill_contract_fp64(g, w, x, tp, **kw)
         assert O.rel_l1_rows(yp, trap).max() > 1e-4, kw
+
+
+@pytest.mark.parametrize("n", [2048, 2560, 128, 300])
+def test_residual_rmsnorm_pinned(n):
+    """The stacked configuration's junction RMSNorm(x + r): against the float64 formula, the closed form of a
+    constant row, and (eps = 0) exact invariance under a power-of-two scale of the input."""
+    x = O.gen_normal(8, n, 4 * n).reshape(4, n)
+    r = O.gen_normal(8, n + 1, 4 * n).reshape(4, n)
+    y = O.residual_rmsnorm_dev(x, r)
+    s = x.astype(np.float64) + r
+    ref = s / np.sqrt((s * s).mean(-1, keepdims=True) + 1e-6)
+    assert np.abs(y - ref).max() <= 1e-6 * np.abs(ref).max()
+    y0 = O.residual_rmsnorm_dev(x)  # r = NULL: RMSNorm(x)
+    ref0 = x / np.sqrt((x.astype(np.float64) ** 2).mean(-1, keepdims=True) + 1e-6)
+    assert np.abs(y0 - ref0).max() <= 1e-6 * np.abs(ref0).max()
+    c = np.full((1, n), 0.75, np.float32)
+    assert np.allclose(O.residual_rmsnorm_dev(c), 0.75 / np.sqrt(0.5625 + 1e-6), rtol=2e-7, atol=0)
+    a = O.residual_rmsnorm_dev(x, r, eps=0.0)
+    b = O.residual_rmsnorm_dev(4 * x, 4 * r, eps=0.0)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
