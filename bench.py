@@ -100,7 +100,8 @@ class HipEvents:
         out = []
         for _ in range(n):
             ev = self.C.c_void_p()
-            if self.hip.hipEventCreateWithFlags(self.C.byref(ev), 0) != 0:
+            # no system-scope fence at record (no cache writeback between kernels): the events only time kernels
+            if self.hip.hipEventCreateWithFlags(self.C.byref(ev), 0x20000000) != 0:  # hipEventDisableSystemFence
                 raise RuntimeError("hipEventCreateWithFlags failed")
             out.append(ev.value)
         return out
