@@ -403,7 +403,7 @@ constexpr Cmp kNet16[63] = {{0, 1}, {2, 3}, {4, 5}, {6, 7}, {8, 9}, {10, 11}, {1
 // (metal/shaders/router.metal:30-132; oracle: or_route_dev).
 template <int J>
 __device__ __forceinline__ void route_token_t(const float* __restrict__ l, int E, int k, int32_t* __restrict__ ids,
-                              float* __restrict__ wts) {
+                              float* __restrict__ wts, int32_t* ids_lds = nullptr) {
     const int lane = threadIdx.x & 63;
     uint32_t key[J];
     float ex[J];
@@ -485,13 +485,14 @@ __device__ __forceinline__ void route_token_t(const float* __restrict__ l, int E
     if (lane < k) {
         ids[lane] = my_id;
         wts[lane] = p / den;
+        if (ids_lds) ids_lds[lane] = my_id;
     }
 }
 
 __device__ __forceinline__ void route_token(const float* __restrict__ l, int E, int k, int32_t* __restrict__ ids,
-                                            float* __restrict__ wts) {
-    if (E <= 512) route_token_t<8>(l, E, k, ids, wts);
-    else route_token_t<16>(l, E, k, ids, wts);
+                                            float* __restrict__ wts, int32_t* ids_lds = nullptr) {
+    if (E <= 512) route_token_t<8>(l, E, k, ids, wts, ids_lds);
+    else route_token_t<16>(l, E, k, ids, wts, ids_lds);
 }
 
 __global__ __launch_bounds__(64) void k_topk(const float* __restrict__ logits, int ld_logits, int T, int E, int k,
@@ -675,21 +676,119 @@ __global__ __launch_bounds__(1024) void k_dispatch(const int32_t* __restrict__ i
 }
 
 // ------------------------------------------------------------------------------------------------ route (fused)
-// The decode call's middle, one work-group of 1024 threads: one wave per token routes it (route_token), then
-// the dispatch of all pairs.
-__global__ __launch_bounds__(1024) void k_topk_dispatch(const float* __restrict__ logits, int T, int E, int k,
-                                                         int32_t* __restrict__ ids, float* __restrict__ wts,
-                                                         int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
-                                                         int32_t* __restrict__ perm, int32_t* __restrict__ slot,
-                                                         int32_t* __restrict__ elist, int32_t* __restrict__ n_list,
-                                                         int4* __restrict__ items, int max_items, int has_shared,
-                                                         int chunk, int sh_chunk) {
-    __shared__ DispatchLds s;
-    const int wave = threadIdx.x >> 6;
-    for (int t = wave; t < T; t += 16) route_token(logits + (size_t)t * E, E, k, ids + (size_t)t * k, wts + (size_t)t * k);
+// The decode call's middle for up to 4 tokens, one work-group of 256 threads: wave t routes token t
+// (route_token, its ids also into LDS), then the dispatch of the T * k <= 256 pairs with the results of
+// dispatch_block: thread i owns experts 4i .. 4i + 3 for the counts, offsets and touched list (one block
+// scan), thread p owns pair p, whose rank within its expert is the number of earlier pairs with the same
+// expert; the work-item table as dispatch_block's (shared chunks first).
+constexpr int kSmallPairs = 256;
+struct SmallDispatchLds {
+    int ids[kSmallPairs];
+    int perm[kSmallPairs];
+    int cnt[1024];
+    int off[1024];
+    int scan[3 * 4];
+};
+__global__ __launch_bounds__(256) void k_topk_dispatch(const float* __restrict__ logits, int T, int E, int k,
+                                                        int32_t* __restrict__ ids, float* __restrict__ wts,
+                                                        int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
+                                                        int32_t* __restrict__ perm, int32_t* __restrict__ slot,
+                                                        int32_t* __restrict__ elist, int32_t* __restrict__ n_list,
+                                                        int4* __restrict__ items, int max_items, int has_shared,
+                                                        int chunk, int sh_chunk) {
+    __shared__ SmallDispatchLds s;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int P = T * k;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) s.cnt[tid + 256 * j] = 0;
+    if (wave < T) route_token(logits + (size_t)wave * E, E, k, ids + (size_t)wave * k, wts + (size_t)wave * k,
+                              s.ids + wave * k);
     __syncthreads();
-    dispatch_block(ids, T * k, E, counts, offsets, perm, slot, elist, n_list, s, items, max_items, T, k, has_shared,
-                   chunk, sh_chunk);
+    const int id = tid < P ? s.ids[tid] : -1;
+    const bool valid = id >= 0 && id < E;
+    if (valid) atomicAdd(&s.cnt[id], 1);
+    if (tid < P && !valid) slot[tid] = -1;
+    __syncthreads();
+    // experts 4 tid .. 4 tid + 3: counts, touched flags and item chunks, then one scan of the three sums
+    int c[4], nch[4];
+    int v[3] = {0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int e = 4 * tid + j;
+        c[j] = e < E ? s.cnt[e] : 0;
+        nch[j] = c[j] > 0 ? (c[j] - 1) / chunk + 1 : 0;
+        v[0] += c[j];
+        v[1] += c[j] > 0 ? 1 : 0;
+        v[2] += nch[j];
+    }
+    int excl[3], total[3];
+#pragma unroll
+    for (int q = 0; q < 3; ++q) {
+        const int incl = wave_inclusive_scan(v[q]);
+        if (lane == 63) s.scan[4 * q + wave] = incl;
+        excl[q] = incl - v[q];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < 3; ++q) {
+        const int w0 = s.scan[4 * q], w1 = s.scan[4 * q + 1], w2 = s.scan[4 * q + 2], w3 = s.scan[4 * q + 3];
+        excl[q] += (wave > 0 ? w0 : 0) + (wave > 1 ? w1 : 0) + (wave > 2 ? w2 : 0);
+        total[q] = w0 + w1 + w2 + w3;
+    }
+    const int n_sh = has_shared ? (T + sh_chunk - 1) / sh_chunk : 0;
+    const int n_rc = total[2];
+    int run_off = excl[0], run_flag = excl[1], run_item = excl[2];
+    int first_of[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int e = 4 * tid + j;
+        first_of[j] = run_off;
+        if (e < E) {
+            s.off[e] = run_off;
+            if (counts) counts[e] = c[j];
+            offsets[e] = run_off;
+            if (c[j] > 0 && elist) elist[run_flag] = e;
+        }
+        run_off += c[j];
+        run_flag += c[j] > 0 ? 1 : 0;
+    }
+    if (tid == 0) {
+        offsets[E] = total[0];
+        if (n_list) *n_list = total[1];
+    }
+    __syncthreads();
+    if (valid) {  // rank = earlier pairs with the same expert (ascending pair order within an expert)
+        int rank = 0;
+        for (int q = 0; q < tid; ++q) rank += s.ids[q] == id ? 1 : 0;
+        const int pos = s.off[id] + rank;
+        perm[pos] = tid;
+        slot[tid] = pos;
+        s.perm[pos] = tid;
+    }
+    __syncthreads();
+    if (!items) return;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        for (int ch = 0; ch < nch[j]; ++ch) {
+            const int first = first_of[j] + ch * chunk, n = min(chunk, c[j] - ch * chunk);
+            int tk[4] = {0, 0, 0, 0};
+            for (int q = 0; q < 4 && q < n; ++q) tk[q] = s.perm[first + q] / k;
+            items[2 * (n_sh + run_item + ch)] = make_int4(4 * tid + j, first, n, tk[0]);
+            items[2 * (n_sh + run_item + ch) + 1] = make_int4(tk[1], tk[2], tk[3], 0);
+        }
+        run_item += nch[j];
+    }
+    for (int wi = tid; wi < max_items; wi += 256) {
+        if (wi >= n_sh && wi < n_sh + n_rc) continue;  // a routed chunk
+        int4 a = make_int4(kItemEmpty, 0, 0, 0), b = make_int4(0, 0, 0, 0);
+        if (wi < n_sh) {
+            const int t0 = wi * sh_chunk;
+            a = make_int4(kItemShared, P + t0, min(sh_chunk, T - t0), t0);
+            b = make_int4(t0 + 1, t0 + 2, t0 + 3, 0);
+        }
+        items[2 * wi] = a;
+        items[2 * wi + 1] = b;
+    }
 }
 
 // ------------------------------------------------------------------------------------------------ expert GEMV
@@ -1175,7 +1274,7 @@ hipError_t launch_dispatch(const int32_t* ids, int P, int E, int32_t* counts, in
 hipError_t launch_topk_dispatch(const float* logits, int T, int E, int k, int32_t* ids, float* wts, int32_t* counts,
                                 int32_t* offsets, int32_t* perm, int32_t* slot, int32_t* elist, int32_t* n_list,
                                 int4* items, int max_items, int has_shared, int chunk, int sh_chunk, hipStream_t s) {
-    hipLaunchKernelGGL(k_topk_dispatch, dim3(1), dim3(1024), 0, s, logits, T, E, k, ids, wts, counts, offsets, perm,
+    hipLaunchKernelGGL(k_topk_dispatch, dim3(1), dim3(256), 0, s, logits, T, E, k, ids, wts, counts, offsets, perm,
                        slot, elist, n_list, items, max_items, has_shared, chunk, sh_chunk);
     return hipGetLastError();
 }
