@@ -29,6 +29,9 @@ COMMON = [
     "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-ffp-contract=off",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-munsafe-fp-atomics",
+    # MFMA results in VGPRs: the prefill kernels scale every block's MFMA result on the VALU, and in AGPRs
+    # each element would first be copied out with v_accvgpr_read
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-I", os.path.join(ROOT, "include"), "-I", CSRC,
     "-Wall", "-Wno-unused-result",
 ]
