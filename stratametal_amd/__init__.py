@@ -21,7 +21,7 @@ Q2_0 = 42
 IQ2_S = 22
 PATH_AUTO, PATH_GEMV, PATH_MFMA = 0, 1, 2
 MFMA_TOKENS = 128  # SMOE_PATH_AUTO runs the prefill (MFMA) contract from this many tokens on
-MFMA_CHUNK = 64    # columns per MFMA work item
+MFMA_CHUNK = 128   # columns per MFMA work item
 
 _STATUS = {0: "ok", -1: "invalid argument", -2: "buffer too small", -3: "unsupported ggml type",
            -4: "HIP runtime error", -5: "misaligned pointer", -6: "NULL pointer"}

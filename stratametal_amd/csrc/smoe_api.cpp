@@ -240,7 +240,7 @@ smoe_status smoe_forward_path(const smoe_geom* g, const smoe_weights* w, const f
     if (mfma) SMOE_TRY(smoe::launch_act_records(x, (int64_t)T * (H / 64), ximg, st), "activation records");
     SMOE_TRY(smoe::launch_router(x, nullptr, static_cast<const uint16_t*>(w->router), has_sh ? w->gate_inp_sh : nullptr,
                                  w->logit_bias, H, E, E + (has_sh ? 1 : 0), T, logits, E, sg, mfma ? nullptr : ximg,
-                                 mfma ? ximg : nullptr, iq2 ? 1 : 0, st),
+                                 mfma ? 1 : 0, iq2 ? 1 : 0, st),
              "router");
     SMOE_MARK();
     if (T <= kFusedRouteTokens) {
@@ -261,11 +261,13 @@ smoe_status smoe_forward_path(const smoe_geom* g, const smoe_weights* w, const f
     const uint8_t* us = static_cast<const uint8_t*>(w->up_sh);
     const uint8_t* ds = static_cast<const uint8_t*>(w->down_sh);
     if (mfma) {
-        SMOE_TRY(smoe::launch_mm_gu(ge, ue, gs, us, ximg, items, perm, K, H, F, Fs, has_sh ? 1 : 0, n_items, himg,
-                                    L.h_rec, st),
+        SMOE_TRY(smoe::launch_mm_gu(ge, ue, gs, us, ximg, (int64_t)T * (H / 64), items, perm, K, H, F, Fs,
+                                    has_sh ? 1 : 0, n_items, himg, L.h_rec, st),
                  "gate/up");
         SMOE_MARK();
-        SMOE_TRY(smoe::launch_mm_down(de, ds, himg, L.h_rec, sg, items, H, F, Fs, n_items, Y, st), "down");
+        SMOE_TRY(smoe::launch_mm_down(de, ds, himg, (int64_t)(P + T) * L.h_rec, L.h_rec, sg, items, H, F, Fs, n_items,
+                                      Y, st),
+                 "down");
     } else if (iq2) {
         SMOE_TRY(smoe::launch_iq2_gu(ge, ue, gs, us, ximg, items, perm, K, H, F, Fs, has_sh ? 1 : 0, n_items, himg,
                                      L.h_blocks, st),
@@ -327,7 +329,7 @@ smoe_status smoe_bf16_gemv(const uint16_t* x, const uint16_t* w, float* y, int32
     if ((int64_t)n_tok * n_in % 2) return fail(SMOE_EINVAL, "bf16_gemv: odd element count");
     if (!aligned(x, 16) || !aligned(w, 16)) return fail(SMOE_EALIGN, "bf16_gemv: x and w must be 16-byte aligned");
     SMOE_TRY(smoe::launch_router(nullptr, x, w, nullptr, nullptr, n_in, n_out, n_out, n_tok, y, n_out, nullptr, nullptr,
-                                 nullptr, 0, stream_of(hip_stream)),
+                                 0, 0, stream_of(hip_stream)),
              "bf16_gemv");
     return ok();
 }

@@ -236,7 +236,6 @@ __global__ __launch_bounds__(256) void k_router(const float* __restrict__ xf, co
     }
 }
 
-constexpr int kRecDwRouter = 36;  // dwords per 64-value activation record (the prefill path's layout)
 
 // Reduce-scatter of 64 per-lane values v[i]: at the stage of distance D (32, 16, ..., 1) a lane keeps the half
 // of its remaining items selected by its bit D and adds the partner's copy of them, so lane l ends with the
@@ -293,28 +292,34 @@ __device__ __forceinline__ float group_sum_rs(float (&v)[NIT], int lpr, int lane
 // 16 bx + 4 w .. + 3 for all 16 tokens (x staged as bf16 in LDS).  Each lane accumulates its chunks l, l+64,
 // ... of all 64 (token, row) dots in element order (the order of k_router), then one reduce-scatter leaves
 // lane l with the dot of token l / 4, row l % 4: the logits equal k_router's bit for bit.
-// x comes as the prefill path's 64-value activation records (bf16 in MFMA order, 36 dwords each): record
-// chunk ch = 4 s + q holds natural chunk 2 q + s of its block with the element order 0 2 1 3 4 6 5 7.
 template <int MAXC>
-__global__ __launch_bounds__(256) void k_router_tile(const uint32_t* __restrict__ xrec, const uint16_t* __restrict__ W,
+__global__ __launch_bounds__(256) void k_router_tile(const float* __restrict__ x, const uint16_t* __restrict__ W,
                                                       const uint16_t* __restrict__ w_inp, const float* __restrict__ bias,
                                                       int H, int E, int rows_total, int T, float* __restrict__ logits,
                                                       int ld_logits, float* __restrict__ sg) {
     extern __shared__ __align__(16) uint32_t smem[];
     const int t0 = blockIdx.y * 16;
     const int nt = min(16, T - t0);
-    // stage the tile's records (data chunks only) as [token][block][record chunk]; loads clamped to the tile's
-    // last chunk and stores to the buffer's last slot, so that every load issues back to back
-    const int n16 = nt * H / 8, cap = 16 * H / 8;
-    for (int base = 0; base < n16; base += 256 * 8) {
-        uint4 v[8];
+    // stage the tile's x as bf16 [token][H]; loads clamped to the tile's last 8-value chunk and stores to the
+    // buffer's last slot, so that every load issues back to back
+    const int n8 = nt * H / 8, cap = 16 * H / 8;
+    const float4* xs4 = reinterpret_cast<const float4*>(x + (size_t)t0 * H);
+    for (int base = 0; base < n8; base += 256 * 4) {
+        float4 v[4][2];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const int g = min(base + u * 256 + (int)threadIdx.x, n16 - 1);  // g = (token * H/64 + block) * 8 + ch
-            v[u] = reinterpret_cast<const uint4*>(xrec + (size_t)t0 * (H >> 6) * kRecDwRouter)[(g >> 3) * 9 + (g & 7)];
+        for (int u = 0; u < 4; ++u) {
+            const int g = min(base + u * 256 + (int)threadIdx.x, n8 - 1);  // g = token * H/8 + chunk
+            v[u][0] = xs4[2 * g];
+            v[u][1] = xs4[2 * g + 1];
         }
 #pragma unroll
-        for (int u = 0; u < 8; ++u) reinterpret_cast<uint4*>(smem)[min(base + u * 256 + (int)threadIdx.x, cap - 1)] = v[u];
+        for (int u = 0; u < 4; ++u) {
+            const uint4 b = make_uint4(f32_to_bf16(v[u][0].x) | (f32_to_bf16(v[u][0].y) << 16),
+                                       f32_to_bf16(v[u][0].z) | (f32_to_bf16(v[u][0].w) << 16),
+                                       f32_to_bf16(v[u][1].x) | (f32_to_bf16(v[u][1].y) << 16),
+                                       f32_to_bf16(v[u][1].z) | (f32_to_bf16(v[u][1].w) << 16));
+            reinterpret_cast<uint4*>(smem)[min(base + u * 256 + (int)threadIdx.x, cap - 1)] = b;
+        }
     }
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int row0 = blockIdx.x * 16 + wave * 4;
@@ -346,15 +351,16 @@ __global__ __launch_bounds__(256) void k_router_tile(const uint32_t* __restrict_
                 wf[r][2 * e + 1] = live ? u2f(q[e] & 0xFFFF0000u) : 0.0f;
             }
         }
-        const int sc = cc & 7, xoff = 64 * (cc >> 3) + 8 * (4 * (sc & 1) + (sc >> 1));  // record position
 #pragma unroll
         for (int t = 0; t < 16; ++t) {
-            const uint4 xv = *reinterpret_cast<const uint4*>(xs + (size_t)t * H + xoff);
-            // natural element order from the record order 0 2 1 3 4 6 5 7
+            const uint4 xv = *reinterpret_cast<const uint4*>(xs + (size_t)t * H + 8 * cc);
             const uint32_t d[4] = {xv.x, xv.y, xv.z, xv.w};
             float xe[8];
-            xe[0] = u2f(d[0] << 16); xe[1] = u2f(d[1] << 16); xe[2] = u2f(d[0] & 0xFFFF0000u); xe[3] = u2f(d[1] & 0xFFFF0000u);
-            xe[4] = u2f(d[2] << 16); xe[5] = u2f(d[3] << 16); xe[6] = u2f(d[2] & 0xFFFF0000u); xe[7] = u2f(d[3] & 0xFFFF0000u);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                xe[2 * e] = u2f(d[e] << 16);
+                xe[2 * e + 1] = u2f(d[e] & 0xFFFF0000u);
+            }
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 const float xv_e = live ? xe[e] : 0.0f;  // a lane past the last chunk adds 0 * 0 (acc is never -0)
@@ -547,15 +553,16 @@ constexpr int kDispatchLdsPairs = 1024 * kDispatchIdRegs;  // pairs whose perm e
 struct DispatchLds {
     int cnt[1024];
     int run[1024];
-    int cb[1024];
     int el[1024];
     uint8_t wcnt[16][1024];
     int scan[3 * 17];
     int perm[kDispatchLdsPairs];  // the first pairs' dispatch order, for the work items
 };
 
-// With `items`, also the work-item table: the shared expert's tokens in chunks of `sh_chunk`, then expert e's
-// pairs in chunks of at most `chunk` columns (in ascending expert order), then empty items up to max_items.
+// With `items`, also the work-item table: the shared expert's tokens in chunks of `sh_chunk`, then the routed
+// experts' pairs in chunks of at most `chunk` columns, longest first: every expert's full chunks, then the
+// remainders of more than chunk / 2 columns, then the shorter remainders (each class in ascending expert
+// order), then empty items up to max_items.  The longest work-groups start first.
 __device__ __forceinline__ void dispatch_block(const int32_t* __restrict__ ids, int P, int E, int32_t* __restrict__ counts,
                                int32_t* __restrict__ offsets, int32_t* __restrict__ perm, int32_t* __restrict__ slot,
                                int32_t* __restrict__ elist, int32_t* __restrict__ n_list, DispatchLds& s,
@@ -579,13 +586,16 @@ __device__ __forceinline__ void dispatch_block(const int32_t* __restrict__ ids, 
     __syncthreads();
     const int c = tid < E ? s.cnt[tid] : 0;
     const int flag = c > 0 ? 1 : 0;
-    const int nch = c > 0 ? (c - 1) / chunk + 1 : 0;
+    const int nfull = c / chunk, rem = c - nfull * chunk;
+    const int wide = rem > (chunk >> 1) ? 1 : 0, narrow = rem > 0 && !wide ? 1 : 0;
     int sc[3], tot[3];
-    block_exclusive_scan3_1024({c, flag, nch}, s.scan, sc, tot);
-    const int off = sc[0], fpos = sc[1], cbase = sc[2];
-    const int total = tot[0], n_touched = tot[1], n_rc = tot[2];
+    // 11-bit fields (E <= 1024): touched flag, wide remainder, narrow remainder
+    block_exclusive_scan3_1024({c, flag | (wide << 11) | (narrow << 22), nfull}, s.scan, sc, tot);
+    const int off = sc[0], fpos = sc[1] & 0x7FF, fbase = sc[2];
+    const int total = tot[0], n_touched = tot[1] & 0x7FF, n_full = tot[2];
+    const int n_wide = (tot[1] >> 11) & 0x7FF, n_rc = n_full + n_wide + ((tot[1] >> 22) & 0x7FF);
+    const int rbase = wide ? n_full + ((sc[1] >> 11) & 0x7FF) : n_full + n_wide + ((sc[1] >> 22) & 0x7FF);
     if (tid < E) {
-        s.cb[tid] = cbase;
         if (counts) counts[tid] = c;
         offsets[tid] = off;
         s.run[tid] = off;
@@ -639,16 +649,18 @@ __device__ __forceinline__ void dispatch_block(const int32_t* __restrict__ ids, 
     // routed chunks in expert order, then empty items
     const int n_sh = has_shared ? (T + sh_chunk - 1) / sh_chunk : 0;
     if (tid < E && c > 0) {
-        for (int ch = 0; ch < nch; ++ch) {
+        for (int ch = 0; ch <= nfull; ++ch) {
             const int first = off + ch * chunk, n = min(chunk, c - ch * chunk);
+            if (n == 0) break;
             int tk[4] = {0, 0, 0, 0};
             if (first + 4 <= kDispatchLdsPairs) {  // two loops, so that the LDS and global loads stay apart
                 for (int j = 0; j < 4 && j < n; ++j) tk[j] = s.perm[first + j] / k;
             } else {
                 for (int j = 0; j < 4 && j < n; ++j) tk[j] = perm[first + j] / k;
             }
-            items[2 * (n_sh + cbase + ch)] = make_int4(tid, first, n, tk[0]);
-            items[2 * (n_sh + cbase + ch) + 1] = make_int4(tk[1], tk[2], tk[3], 0);
+            const int wi = n_sh + (ch < nfull ? fbase + ch : rbase);
+            items[2 * wi] = make_int4(tid, first, n, tk[0]);
+            items[2 * wi + 1] = make_int4(tk[1], tk[2], tk[3], 0);
         }
     }
     for (int wi = tid; wi < max_items; wi += 1024) {
@@ -1223,16 +1235,16 @@ hipError_t launch_prep(const float* x, int64_t n, uint8_t* xq, uint16_t* xb, hip
 
 hipError_t launch_router(const float* xf, const uint16_t* xb, const uint16_t* W, const uint16_t* w_inp,
                          const float* bias, int H, int E, int rows_total, int T, float* logits, int ld_logits, float* sg,
-                         uint32_t* ximg, const uint32_t* xrec, int img_natural, hipStream_t s) {
+                         uint32_t* ximg, int tile_rows, int img_natural, hipStream_t s) {
     const int chunks = H / 8;
     const int maxc = (chunks + 63) / 64;
     // tokens staged per block: 4 for decode batches (more blocks, short staging), 16 (<= 64 KiB of bf16) beyond
-    if (xrec) {  // many tokens, x given as activation records: row x token tiles
+    if (tile_rows) {  // many tokens: row x token tiles
         const int maxc = (H / 8 + 63) / 64;
         const size_t lds = (size_t)16 * H * 2;
 #define SMOE_ROUTER_TILE(C)                                                                                        \
     hipLaunchKernelGGL((k_router_tile<C>), dim3((unsigned)((rows_total + 15) / 16), (unsigned)((T + 15) / 16)),      \
-                       dim3(256), lds, s, xrec, W, w_inp, bias, H, E, rows_total, T, logits, ld_logits, sg)
+                       dim3(256), lds, s, xf, W, w_inp, bias, H, E, rows_total, T, logits, ld_logits, sg)
         if (maxc <= 2) SMOE_ROUTER_TILE(2);
         else if (maxc <= 4) SMOE_ROUTER_TILE(4);
         else SMOE_ROUTER_TILE(8);

@@ -1,27 +1,28 @@
-// stratametal_amd/csrc/smoe_prefill.hip - the prefill contract's expert products on bf16 MFMA (gfx950).
+// stratametal_amd/csrc/smoe_prefill.hip - the prefill contract's expert products on the matrix cores (gfx950).
 //
 // Contract (oracle: or_moe_prefill): activations rounded to bf16; Q2_0 weights used exactly as
 // (code - 1) * f32(d); SwiGLU in f32; h rounded to bf16 for the down product; f32 accumulation.  The
 // reference's float prompt path is a dequantising GEMM (include/strata/prefill/gemm.hpp:28-40,
 // include/strata/prefill/kernels.hpp:54-57,97-98, include/strata/prefill/moe_fused.hpp:52-62).
 //
-// How the exact weights reach the matrix cores.  A 64-weight block contributes
-//     d * sum_k (c_k - 1) a_k = d * (sum_k c_k a_k - A),   A = sum_k a_k,
-// so the MFMA B operand is the raw code c in {0, 1, 2, 3} (exact in bf16; one v_cvt_scalef32_pk_bf16_fp4
-// turns a byte of two 2-bit codes, masked into the low bits of two fp4 nibbles, into two bf16 values with the
-// scale 2: fp4 e2m1 nibble c has the value c / 2), the accumulator input of the block's first MFMA is -A
-// (carried with every activation record), and the block's f32 result is scaled by d into the running sum.
+// How the exact products reach the matrix cores: both operands are fp16 and the MFMA is
+// v_mfma_f32_16x16x32_f16 (exact products, f32 sums).
+//  - An activation a is its bf16 value held in fp16, which is exact for 2^-17 <= |a| < 65520 (fp16 keeps 11
+//    significant bits and reaches 2^-24; bf16 has 8).  Smaller magnitudes round in fp16 (an error below 2^-25
+//    per element); larger ones do not fit: the contract's activations and h are required to stay below 65520.
+//  - A weight (c - 1) * d, c in {0, 1, 2, 3}, d the block's fp16 scale, is one of {-d, 0, d, 2d}: exact in fp16
+//    (for |d| < 32752).  It is made in two steps: v_cvt_scalef32_pk_f16_fp4 turns a byte of two 2-bit codes,
+//    masked into the low bits of two fp4 nibbles, into the fp16 pair (c0, c1) (nibble c is the e2m1 value c / 2,
+//    scale 2), then v_pk_fma_f16(c, d, -d) gives (c - 1) * d with one rounding of an exact value.
+// The K loop is one chain of MFMAs per output tile; nothing in it waits for an MFMA result.
 //
-// Activation records.  Each 64-value block of an activation row (x for gate/up, h for down) is one 144-byte
-// record: 64 bf16 in MFMA order, then -A as f32, then 12 unused bytes.  Position p = 32 s + 8 q + e holds
-// element 16 q + 8 s + pi(e), pi = (0 2 1 3 4 6 5 7): the order in which a lane of quarter q meets the
-// codes of code dword q of the block in the two 32-deep MFMA steps s.
+// Activation records.  Each 64-value block of an activation row (x for gate/up, h for down) is one 128-byte
+// record of 64 fp16 in MFMA order: position p = 32 s + 8 q + e holds element 16 q + 8 s + pi(e),
+// pi = (0 2 1 3 4 6 5 7), the order in which a lane of quarter q meets the codes of code dword q of the block
+// in the two 32-deep MFMA steps s.
 //
-// MFMA tiles (v_mfma_f32_16x16x32_bf16, lane l = 16 q + i): A[i][k] = activation of token i, B[k][j] = code
-// of weight row j, C[4 q + r][j] in register r.  A work-group of 4 waves owns 64 weight rows (gate/up: 64
-// rows of each) and a work item of at most 128 tokens (8 tiles of 16); each wave owns 16 rows and every tile.
-// The raw Q2_0 rows and the tile's activation records are staged in LDS one 128-value unit (two blocks) at a
-// time; the codes are expanded in registers and reused across the token tiles.
+// MFMA tiles (lane l = 16 q + i): A[i][k] = activation of column (token) i, B[k][j] = weight of row j,
+// C[4 q + r][j] in register r.
 #include "smoe_device.hpp"
 #include "smoe_items.hpp"
 #include "smoe_launch.hpp"
@@ -30,298 +31,392 @@
 
 namespace smoe {
 
-typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
-typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(2))) _Float16 f16x2;
+typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
 typedef __attribute__((ext_vector_type(4))) float f32x4;
 
-constexpr int kRecDw = 36;       // dwords per activation record
-constexpr int kChunk = 64;       // tokens per work item
-constexpr int kTiles = kChunk / 16;
-constexpr int kActStride = 76;   // LDS dwords per staged token: two records + 4 dwords against bank conflicts
+constexpr int kRecBytes = 128;   // bytes per 64-value activation record
+constexpr int kChunk = 128;      // columns (tokens) per work item
 
 __device__ __forceinline__ int perm8(int e) { return (e == 1 || e == 5) ? e + 1 : (e == 2 || e == 6) ? e - 1 : e; }
 // record position of block element kappa (pi is an involution)
 __device__ __forceinline__ int rec_pos(int kappa) {
     return 32 * ((kappa >> 3) & 1) + 8 * (kappa >> 4) + perm8(kappa & 7);
 }
+// fp16 bits of the bf16 rounding of v
+__device__ __forceinline__ uint32_t bf16_as_f16(float v) {
+    return __builtin_bit_cast(uint16_t, (_Float16)bf16_to_f32(f32_to_bf16(v)));
+}
 
 // ------------------------------------------------------------------------------------------------ records of x
-// One thread per 8 positions (a 16-byte chunk) of a record; eight consecutive lanes form one record and add
-// their chunk sums by an xor butterfly for -A.
+// One thread per 8 positions (a 16-byte chunk) of a record.
 __global__ __launch_bounds__(256) void k_act_records(const float* __restrict__ x, int64_t n_rec,
                                                      uint32_t* __restrict__ rec) {
     const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
     const int64_t r = g >> 3;
+    if (r >= n_rec) return;
     const int ch = (int)(g & 7);
-    const bool live = r < n_rec;
     const int s = ch >> 2, q = ch & 3;
-    float v[8];
-    if (live) {
-        const float4* src = reinterpret_cast<const float4*>(x + r * 64 + 16 * q + 8 * s);
-        const float4 lo = src[0], hi = src[1];
-        v[0] = lo.x; v[1] = lo.y; v[2] = lo.z; v[3] = lo.w;
-        v[4] = hi.x; v[5] = hi.y; v[6] = hi.z; v[7] = hi.w;
-    } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = 0.0f;
-    }
+    const float4* src = reinterpret_cast<const float4*>(x + r * 64 + 16 * q + 8 * s);
+    const float4 lo = src[0], hi = src[1];
+    const float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
     uint32_t b[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) b[e] = f32_to_bf16(v[perm8(e)]);
-    float sm = 0.0f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) sm = sm + bf16_to_f32(b[e]);
-    sm = sm + __shfl_xor(sm, 1, kWave);
-    sm = sm + __shfl_xor(sm, 2, kWave);
-    sm = sm + __shfl_xor(sm, 4, kWave);
-    if (live) {
-        uint32_t* dst = rec + r * kRecDw;
-        reinterpret_cast<uint4*>(dst)[ch] = make_uint4(b[0] | (b[1] << 16), b[2] | (b[3] << 16), b[4] | (b[5] << 16),
-                                                       b[6] | (b[7] << 16));
-        if (ch == 0) dst[32] = f2u(-sm);
-    }
+    for (int e = 0; e < 8; ++e) b[e] = bf16_as_f16(v[perm8(e)]);
+    reinterpret_cast<uint4*>(rec + r * (kRecBytes / 4))[ch] =
+        make_uint4(b[0] | (b[1] << 16), b[2] | (b[3] << 16), b[4] | (b[5] << 16), b[6] | (b[7] << 16));
 }
 
 // ------------------------------------------------------------------------------------------------ codes -> B
-__device__ __forceinline__ bf16x8 cat4(bf16x2 a, bf16x2 b, bf16x2 c, bf16x2 d) {
+__device__ __forceinline__ f16x8 cat4(f16x2 a, f16x2 b, f16x2 c, f16x2 d) {
     return __builtin_shufflevector(__builtin_shufflevector(a, b, 0, 1, 2, 3), __builtin_shufflevector(c, d, 0, 1, 2, 3),
                                    0, 1, 2, 3, 4, 5, 6, 7);
 }
+// (c - 1) * d for a pair of codes c (as fp16 values)
+__device__ __forceinline__ f16x2 scale_pair(f16x2 c, f16x2 d, f16x2 nd) { return __builtin_elementwise_fma(c, d, nd); }
 
-// Code dword cw (16 codes) -> the B operands of the two 32-deep steps: x holds codes 0, 2 of each byte in
-// the low bits of its nibbles, y codes 1, 3.
-__device__ __forceinline__ void expand_codes(uint32_t cw, bf16x8& s0, bf16x8& s1) {
+// Code dword cw (16 codes) of a block with scale d (fp16 bits) -> the B operands of the two 32-deep steps:
+// x holds codes 0, 2 of each byte in the low bits of its nibbles, y codes 1, 3.
+__device__ __forceinline__ void expand_codes(uint32_t cw, uint32_t dbits, f16x8& s0, f16x8& s1) {
     const uint32_t x = cw & 0x33333333u, y = (cw >> 2) & 0x33333333u;
-    s0 = cat4(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(x, 2.0f, 0), __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(y, 2.0f, 0),
-              __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(x, 2.0f, 1), __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(y, 2.0f, 1));
-    s1 = cat4(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(x, 2.0f, 2), __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(y, 2.0f, 2),
-              __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(x, 2.0f, 3), __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(y, 2.0f, 3));
+    const uint32_t dd = dbits | (dbits << 16);
+    const f16x2 d = __builtin_bit_cast(f16x2, dd), nd = __builtin_bit_cast(f16x2, dd ^ 0x80008000u);
+    s0 = cat4(scale_pair(__builtin_amdgcn_cvt_scalef32_pk_f16_fp4(x, 2.0f, 0), d, nd),
+              scale_pair(__builtin_amdgcn_cvt_scalef32_pk_f16_fp4(y, 2.0f, 0), d, nd),
+              scale_pair(__builtin_amdgcn_cvt_scalef32_pk_f16_fp4(x, 2.0f, 1), d, nd),
+              scale_pair(__builtin_amdgcn_cvt_scalef32_pk_f16_fp4(y, 2.0f, 1), d, nd));
+    s1 = cat4(scale_pair(__builtin_amdgcn_cvt_scalef32_pk_f16_fp4(x, 2.0f, 2), d, nd),
+              scale_pair(__builtin_amdgcn_cvt_scalef32_pk_f16_fp4(y, 2.0f, 2), d, nd),
+              scale_pair(__builtin_amdgcn_cvt_scalef32_pk_f16_fp4(x, 2.0f, 3), d, nd),
+              scale_pair(__builtin_amdgcn_cvt_scalef32_pk_f16_fp4(y, 2.0f, 3), d, nd));
 }
 
-// Staging of one 128-value unit through registers: the global loads of unit u + 1 are issued before the
-// matrix work on unit u, and land in LDS after it.  Thread t loads the 36-byte unit of weight row t
-// (t < nrows) and up to kStageA 16-byte chunks of the columns' activation records: chunk idx = t + 256 m is
-// column idx / 18, record (idx % 18) / 9 of the unit, 16-byte piece idx % 9 (piece 8 carries -A).
-constexpr int kStageA = (kChunk * 18 + 255) / 256;
-constexpr int kDeadSlot = kChunk * (kActStride / 4);  // 16-byte slot past the staged columns
+// Staging.  Both operands reach LDS by buffer loads that write LDS directly (`buffer_load_dwordx4 ... lds`:
+// lane L of an instruction lands at M0 + 16 L), several stages deep: while the waves multiply stage u, the
+// loads of the next stages are in flight.  A stage is one 128-value unit (two blocks) of K:
+//   activations: the item's columns x 17 pieces of 16 bytes (the column's two records, then one pad piece
+//                that spreads the columns over the LDS banks);
+//   weights:     256 rows x a 48-byte window holding the row's 36-byte unit (the window starts at the 16-byte
+//                boundary at or below the unit, 4 (u % 4) bytes before it).
+// Every wave issues the same number of instructions per stage (those past the real ones land in a dummy slot),
+// so `s_waitcnt vmcnt(n * slots)` means "my loads of all but the n newest stages are done"; the barrier after
+// it makes everyone's visible.  Columns past the item and pad pieces read at an offset beyond the buffer
+// (range-checked: no memory access, zeros written), so a short item moves only its own activation bytes.
+//
+// Two work-group shapes share one LDS ring (the item's column count picks one):
+//   wide (65..128 columns): 3 stages of 128 columns; wave w owns rows of row group w % 4 (four 16-row sets) and
+//                           columns 64 (w / 4) .. + 63;
+//   narrow (<= 64 columns): 5 stages of 64 columns; wave w owns the rows of row group w (two sets) and every column.
+constexpr int kTokPieces = 17;
+constexpr int kWgRows = 256;
+constexpr int kWPieces = kWgRows * 3;
+constexpr int kWIns = kWPieces / 64;
+constexpr int kWaves = 8;
+constexpr uint32_t kOob = 0x80000000u;
+constexpr int kRing = 148480;           // bytes of the stage ring
+constexpr int kDummy = kRing;           // 1 KB landing slot of the padding instructions
+constexpr int kLds = kRing + 1024;
 
-struct Stager {
-    const uint8_t* wrow;            // this thread's weight row (a valid row for every thread; stored if has_w)
-    const uint32_t* __restrict__ recs;
-    bool has_w;
-    uint32_t src[kStageA];          // dword offset of chunk m in unit 0 (0 when unused: a harmless valid load)
-    int dst[kStageA];               // 16-byte slot in the staged activations (kDeadSlot when unused)
-    uint32_t w[9];
-    uint4 a[kStageA];
+template <bool WIDE>
+struct Shape {
+    static constexpr int kTok = WIDE ? 128 : 64;
+    static constexpr int kStages = WIDE ? 3 : 5;
+    static constexpr int NS = WIDE ? 4 : 2;
+    static constexpr int kAPieces = kTok * kTokPieces;
+    static constexpr int kAIns = kAPieces / 64;
+    static constexpr int kASlots = (kAIns + kWaves - 1) / kWaves;
+    static constexpr int kWSlots = (kWIns + kWaves - 1) / kWaves;
+    static constexpr int kSlots = kASlots + kWSlots;
+    static constexpr int kABytes = kAPieces * 16;
+    static constexpr int kStage = kABytes + kWPieces * 16;
+    static_assert(kAPieces % 64 == 0 && kWPieces % 64 == 0, "whole DMA instructions");
+    static_assert(kStages * kStage <= kRing, "ring");
+    static_assert((kStages - 2) * kSlots <= 63, "vmcnt range");
+};
 
-    // Every load and store is unconditional (unused slots read a valid address and land in a dead slot) so that
-    // the loads issue back to back and the stores need no branches.
-    __device__ void init(const uint8_t* row, bool has_row, const uint32_t* r, const int* rowidx, int ncol,
-                         int rec_per_row) {
-        wrow = row;
-        has_w = has_row;
-        recs = r;
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+
+// Raw buffer resource over [base, base + bytes) (no swizzle, no stride; out-of-range lanes read nothing).
+__device__ __forceinline__ i32x4 buffer_rsrc(const void* base, uint32_t bytes) {
+    const uint64_t b = reinterpret_cast<uint64_t>(base);
+    return i32x4{(int)(uint32_t)b, (int)(uint32_t)(b >> 32), (int)bytes, 0x00020000};
+}
+__device__ __forceinline__ uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t)(const lds_u8*)p; }
+// M0 is written one instruction before the load that reads it (one wait state for LDS DMA).
+__device__ __forceinline__ void dma16(uint32_t lds, uint32_t voff, i32x4 rsrc, uint32_t soff) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(lds), "v"(voff),
+                 "s"(rsrc), "s"(soff)
+                 : "memory", "m0");
+}
+template <int N>
+__device__ __forceinline__ void vmcnt() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+// Wait until this wave's loads of all but the `after` newest stages are done.
+template <int SLOTS>
+__device__ __forceinline__ void wait_stages(int after) {
+    switch (after) {
+        case 0: vmcnt<0>(); break;
+        case 1: vmcnt<SLOTS>(); break;
+        case 2: vmcnt<2 * SLOTS>(); break;
+        default: vmcnt<3 * SLOTS>(); break;
+    }
+}
+
+// One wave's DMA plan: per slot the byte offset within a stage (uniform; -1 for the dummy) and the lane's
+// buffer offset at unit 0.
+template <bool WIDE>
+struct MmPlan {
+    using S = Shape<WIDE>;
+    uint32_t a_off[S::kASlots], w_off[S::kWSlots];
+    int a_at[S::kASlots], w_at[S::kWSlots];
+    int w_up[S::kWSlots];  // the slot's rows are the second tensor's (up rows)
+
+    // rowidx: activation row of each column; rpr: records per activation row; rb: weight row bytes; split: rows
+    // of the first weight tensor (gate/up: 128; down: 256, i.e. one tensor).
+    __device__ __forceinline__ void init(const int* rowidx, int wave, int lane, int ncol, int rpr, uint32_t rb,
+                                         int split) {
 #pragma unroll
-        for (int m = 0; m < kStageA; ++m) {
-            const int idx = (int)threadIdx.x + 256 * m, c = idx / 18, p = idx - 18 * c, h = p >= 9 ? 1 : 0,
-                      ch = p - 9 * h;
-            const bool live = c < ncol;
-            src[m] = live ? (uint32_t)(((size_t)rowidx[c] * rec_per_row + h) * kRecDw + 4 * ch) : 0u;
-            dst[m] = live ? c * (kActStride / 4) + h * (kRecDw / 4) + ch : kDeadSlot;
+        for (int m = 0; m < S::kASlots; ++m) {
+            const int j = wave + kWaves * m;
+            const int P = 64 * j + lane, t = P / kTokPieces, p = P - kTokPieces * t;
+            const bool live = j < S::kAIns && t < ncol && p < 16;
+            const int row = rowidx[t < ncol ? t : 0];
+            a_off[m] = live ? (uint32_t)(row * rpr * kRecBytes + 16 * p) : kOob;
+            a_at[m] = j < S::kAIns ? 1024 * j : -1;
+        }
+#pragma unroll
+        for (int m = 0; m < S::kWSlots; ++m) {
+            const int j = wave + kWaves * m;
+            const int P = 64 * j + lane, row = P / 3, p = P - 3 * row;
+            const bool real = j < kWIns;
+            const int r = row >= split ? row - split : row;
+            w_up[m] = 64 * j >= 3 * split ? 1 : 0;  // whole instructions: 3 * split is a multiple of 64
+            w_off[m] = real ? (uint32_t)r * rb + 16u * p : kOob;
+            w_at[m] = real ? S::kABytes + 1024 * j : -1;
         }
     }
-    __device__ void load(int u) {
-        __builtin_memcpy(w, __builtin_assume_aligned(wrow + (size_t)u * 36, 4), 36);
+
+    // Issue unit u into ring stage b.
+    __device__ __forceinline__ void issue(uint32_t lds0, int b, int u, i32x4 ra, i32x4 rw0, i32x4 rw1) const {
+        const uint32_t st = (uint32_t)(b * S::kStage);
+        const uint32_t sa = __builtin_amdgcn_readfirstlane((uint32_t)u * (2 * kRecBytes));
+        const uint32_t sw = __builtin_amdgcn_readfirstlane((uint32_t)(36 * u - 4 * (u & 3)));
 #pragma unroll
-        for (int m = 0; m < kStageA; ++m) a[m] = *reinterpret_cast<const uint4*>(recs + src[m] + (size_t)u * 2 * kRecDw);
-    }
-    __device__ void store(uint32_t* wt, uint4* act) const {
-        if (has_w) {
-#pragma unroll
-            for (int i = 0; i < 9; ++i) wt[threadIdx.x * 9 + i] = w[i];
+        for (int m = 0; m < S::kASlots; ++m) {
+            const uint32_t at = a_at[m] < 0 ? (uint32_t)kDummy : st + (uint32_t)a_at[m];
+            dma16(__builtin_amdgcn_readfirstlane(lds0 + at), a_off[m], ra, sa);
         }
 #pragma unroll
-        for (int m = 0; m < kStageA; ++m) act[dst[m]] = a[m];
+        for (int m = 0; m < S::kWSlots; ++m) {
+            const uint32_t at = w_at[m] < 0 ? (uint32_t)kDummy : st + (uint32_t)w_at[m];
+            dma16(__builtin_amdgcn_readfirstlane(lds0 + at), w_off[m], w_up[m] ? rw1 : rw0, sw);
+        }
     }
 };
 
-// -A of block h for the four tokens 4 q .. 4 q + 3 of tile n (record dword 32 of each token's staged record)
-__device__ __forceinline__ f32x4 neg_sums(const uint32_t* act, int n, int h, int q) {
-    const uint32_t* p = act + (16 * n + 4 * q) * kActStride + h * kRecDw + 32;
-    return f32x4{u2f(p[0]), u2f(p[kActStride]), u2f(p[2 * kActStride]), u2f(p[3 * kActStride])};
-}
-
-// One staged unit against NS weight-row sets per wave: for block h of the unit, the B operands of the NS sets
-// (lane row i of set s at LDS row rows[s]) are expanded, then every live token tile n loads its activation
-// fragments once and feeds all NS sets: acc[n][s] += d_s * (C = -A; C += A0 B0; C += A1 B1).
-template <int NS>
-__device__ __forceinline__ void mma_unit(f32x4 (&acc)[kTiles][NS], const uint32_t* wt, const int (&rows)[NS],
-                                         const uint32_t* act, int ntiles, int i, int q) {
+// One staged unit: the activation fragments of all NT column tiles (columns tok0 + 16 n ..) are loaded first;
+// then for each block h and row set s (LDS row rows[s]; the unit starts `wofs` dwords into the row's window)
+// the set's B operands are expanded and fed to every tile: acc[n][s] += A0 B0 + A1 B1.  Set s + 1 is expanded
+// while the matrix cores work on set s.
+template <int NS, int NT>
+__device__ __forceinline__ void mm_unit(f32x4 (&acc)[4][NS], const uint32_t* W, int wofs, const int (&rows)[NS],
+                                        const uint4* A, int tok0, int i, int q) {
+    f16x8 a[2][NT][2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int n = 0; n < NT; ++n) {
+            const uint4* ar = A + (tok0 + 16 * n + i) * kTokPieces + 8 * h;
+            a[h][n][0] = __builtin_bit_cast(f16x8, ar[q]);
+            a[h][n][1] = __builtin_bit_cast(f16x8, ar[4 + q]);
+        }
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-        bf16x8 b0[NS], b1[NS];
-        float d[NS];
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
-            const uint32_t* w = wt + rows[s] * 9;
+            const uint32_t* w = W + rows[s] * 12 + wofs;
             const uint32_t cw = h == 0 ? __builtin_amdgcn_alignbyte(w[q + 1], w[q], 2) : w[5 + q];
-            d[s] = h == 0 ? (float)__builtin_bit_cast(_Float16, (uint16_t)(w[0] & 0xFFFFu))
-                          : (float)__builtin_bit_cast(_Float16, (uint16_t)(w[4] >> 16));
-            expand_codes(cw, b0[s], b1[s]);
-        }
+            const uint32_t db = h == 0 ? (w[0] & 0xFFFFu) : (w[4] >> 16);
+            f16x8 b0, b1;
+            expand_codes(cw, db, b0, b1);
 #pragma unroll
-        for (int n = 0; n < kTiles; ++n) {
-            if (n < ntiles) {
-                const uint32_t* ar = act + (16 * n + i) * kActStride + h * kRecDw;
-                const bf16x8 a0 = *reinterpret_cast<const bf16x8*>(ar + 4 * q);
-                const bf16x8 a1 = *reinterpret_cast<const bf16x8*>(ar + 16 + 4 * q);
-                const f32x4 na = neg_sums(act, n, h, q);
-#pragma unroll
-                for (int s = 0; s < NS; ++s) {
-                    f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b0[s], na, 0, 0, 0);
-                    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1[s], c, 0, 0, 0);
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) acc[n][s][r] = __builtin_fmaf(d[s], c[r], acc[n][s][r]);
-                }
+            for (int n = 0; n < NT; ++n) {
+                acc[n][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[h][n][0], b0, acc[n][s], 0, 0, 0);
+                acc[n][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[h][n][1], b1, acc[n][s], 0, 0, 0);
             }
         }
+    }
+}
+
+// The K loop of both kernels: units of 128 values through the ring, kStages - 1 units in flight.  NT: the
+// wave's live column tiles.
+template <bool WIDE, int NT>
+__device__ __forceinline__ void mm_loop_nt(f32x4 (&acc)[4][Shape<WIDE>::NS], uint8_t* lds, const MmPlan<WIDE>& pl,
+                                           int units, i32x4 ra, i32x4 rw0, i32x4 rw1,
+                                           const int (&rows)[Shape<WIDE>::NS], int tok0, int i, int q) {
+    using S = Shape<WIDE>;
+    constexpr int ST = S::kStages;
+    const uint32_t lds0 = lds_addr(lds);
+#pragma unroll
+    for (int b = 0; b < ST - 1; ++b)
+        if (b < units) pl.issue(lds0, b, b, ra, rw0, rw1);
+    int b = 0;  // ring stage of unit u
+    for (int u = 0; u < units; ++u) {
+        wait_stages<S::kSlots>(min(ST - 2, units - 1 - u));
+        __syncthreads();  // unit u is in LDS for everyone; everyone is done with unit u - 1
+        if (u + ST - 1 < units) pl.issue(lds0, b == 0 ? ST - 1 : b - 1, u + ST - 1, ra, rw0, rw1);
+        const uint8_t* stg = lds + b * S::kStage;
+        mm_unit<S::NS, NT>(acc, reinterpret_cast<const uint32_t*>(stg + S::kABytes), u & 3, rows,
+                           reinterpret_cast<const uint4*>(stg), tok0, i, q);
+        b = b + 1 == ST ? 0 : b + 1;
+    }
+}
+
+template <bool WIDE>
+__device__ __forceinline__ void mm_loop(f32x4 (&acc)[4][Shape<WIDE>::NS], uint8_t* lds, const MmPlan<WIDE>& pl,
+                                        int units, i32x4 ra, i32x4 rw0, i32x4 rw1,
+                                        const int (&rows)[Shape<WIDE>::NS], int tok0, int ntiles, int i, int q) {
+#pragma unroll
+    for (int n = 0; n < 4; ++n)
+#pragma unroll
+        for (int s = 0; s < Shape<WIDE>::NS; ++s) acc[n][s] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    switch (ntiles) {  // wave-uniform; every wave has 1 .. 4 live tiles
+        case 1: mm_loop_nt<WIDE, 1>(acc, lds, pl, units, ra, rw0, rw1, rows, tok0, i, q); break;
+        case 2: mm_loop_nt<WIDE, 2>(acc, lds, pl, units, ra, rw0, rw1, rows, tok0, i, q); break;
+        case 3: mm_loop_nt<WIDE, 3>(acc, lds, pl, units, ra, rw0, rw1, rows, tok0, i, q); break;
+        default: mm_loop_nt<WIDE, 4>(acc, lds, pl, units, ra, rw0, rw1, rows, tok0, i, q); break;
     }
 }
 
 // ------------------------------------------------------------------------------------------------ gate/up
-// Grid (Fmax / 128, work items).  Work-group rt of an item computes gate and up rows [128 rt, 128 rt + 128)
-// for the item's columns: wave w the rows 32 w .. 32 w + 31 of each (sets 0, 1 gate; 2, 3 up), then
-// h = bf16(silu(gate) * up) into records 2 rt and 2 rt + 1 of each column's h row.
-__global__ __launch_bounds__(256) void k_mm_gu(const uint8_t* __restrict__ gate_exps, const uint8_t* __restrict__ up_exps,
-                                               const uint8_t* __restrict__ gate_sh, const uint8_t* __restrict__ up_sh,
-                                               const uint32_t* __restrict__ xrec, const int4* __restrict__ items,
-                                               const int32_t* __restrict__ perm, int k, int H, int F, int Fs,
-                                               uint32_t* __restrict__ hrec, int h_rec) {
-    __shared__ uint32_t wt[256 * 9];
-    __shared__ __align__(16) uint32_t act[kChunk * kActStride + 4];
-    __shared__ int rowidx[kChunk];
-    Item item;
-    if (!work_item(items, blockIdx.y, item)) return;
+// Grid (Fmax / 128, work items), 8 waves.  Work-group rt computes gate and up rows [128 rt, 128 rt + 128) for the
+// item's (at most 128) columns, then h = bf16(silu(gate) * up) into records 2 rt and 2 rt + 1 of each column's h
+// row.  Wide: wave w has gate rows 32 (w % 4) .. + 31 (sets 0, 1) and the same up rows (sets 2, 3); narrow: gate
+// rows 16 w .. + 15 (set 0) and the same up rows (set 1).
+template <bool WIDE>
+__device__ __forceinline__ void mm_gu_body(uint8_t* lds, const int* rowidx, const Item& item, int ncol,
+                                           const uint8_t* g0, const uint8_t* u0, const uint32_t* xrec,
+                                           uint32_t xrec_bytes, int H, uint32_t* hrec, int h_rec) {
+    using S = Shape<WIDE>;
+    constexpr int NS = S::NS;
     const int rt = blockIdx.x;
-    const int Fe = item.shared ? Fs : F;
-    if (128 * rt >= Fe) return;
-    const int ncol = item.ncol, ntiles = (ncol + 15) >> 4;
     const int units = H >> 7;
-    const size_t rb = (size_t)units * 36;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, i = lane & 15, q = lane >> 4;
-    for (int c = tid; c < ncol; c += 256) rowidx[c] = item_token(item, perm, k, c);
-    __syncthreads();
-    Stager stg;
-    {
-        const uint8_t* base = tid < 128 ? (item.shared ? gate_sh : gate_exps + (size_t)item.e * F * rb)
-                                        : (item.shared ? up_sh : up_exps + (size_t)item.e * F * rb);
-        stg.init(base + (size_t)(128 * rt + (tid & 127)) * rb, true, xrec, rowidx, ncol, H >> 6);
+    const uint32_t rb = (uint32_t)units * 36u;
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, i = lane & 15,
+              q = lane >> 4;
+    MmPlan<WIDE> pl;
+    pl.init(rowidx, wave, lane, ncol, H >> 6, rb, 128);
+    const i32x4 ra = buffer_rsrc(xrec, xrec_bytes);
+    const i32x4 rg0 = buffer_rsrc(g0 + (size_t)128 * rt * rb, 128u * rb);
+    const i32x4 ru0 = buffer_rsrc(u0 + (size_t)128 * rt * rb, 128u * rb);
+    int rows[NS];
+    int fbase;  // first of the wave's gate rows within the work-group's 128
+    if constexpr (WIDE) {
+        fbase = 32 * (wave & 3);
+        rows[0] = fbase + i;
+        rows[1] = fbase + 16 + i;
+        rows[2] = 128 + fbase + i;
+        rows[3] = 128 + fbase + 16 + i;
+    } else {
+        fbase = 16 * wave;
+        rows[0] = fbase + i;
+        rows[1] = 128 + fbase + i;
     }
-    stg.load(0);
-    const int rows[4] = {32 * wave + i, 32 * wave + 16 + i, 128 + 32 * wave + i, 128 + 32 * wave + 16 + i};
-
-    f32x4 acc[kTiles][4];
+    const int tok0 = WIDE ? 64 * (wave >> 2) : 0;
+    const int ntiles = min(4, max(0, (ncol - tok0 + 15) >> 4));
+    f32x4 acc[4][NS];
+    mm_loop<WIDE>(acc, lds, pl, units, ra, rg0, ru0, rows, tok0, ntiles, i, q);
+    __syncthreads();  // every wave is done with the ring: its start becomes the h tile
+    // h tile [column][128 rows in record order] as fp16 bits of bf16 values
+    uint16_t* ht = reinterpret_cast<uint16_t*>(lds);
 #pragma unroll
-    for (int n = 0; n < kTiles; ++n)
-#pragma unroll
-        for (int s = 0; s < 4; ++s) acc[n][s] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    for (int u = 0; u < units; ++u) {
-        stg.store(wt, reinterpret_cast<uint4*>(act));
-        __syncthreads();
-        if (u + 1 < units) stg.load(u + 1);
-        mma_unit<4>(acc, wt, rows, act, ntiles, i, q);
-        __syncthreads();
-    }
-    // h tile [column][128 rows in record order] as bf16 in the activation buffer
-    uint16_t* ht = reinterpret_cast<uint16_t*>(act);
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-        const int f = 32 * wave + 16 * s + i;  // row within the work-group's 128
+    for (int s = 0; s < NS / 2; ++s) {
+        const int f = fbase + 16 * s + i;
         const int pos = 64 * (f >> 6) + rec_pos(f & 63);
 #pragma unroll
-        for (int n = 0; n < kTiles; ++n) {
+        for (int n = 0; n < 4; ++n) {
             if (n < ntiles) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const int c = 16 * n + 4 * q + r;
-                    if (c < ncol) ht[c * 128 + pos] = (uint16_t)f32_to_bf16(silu_mul(acc[n][s][r], acc[n][s + 2][r]));
+                    const int c = tok0 + 16 * n + 4 * q + r;
+                    if (c < ncol) ht[c * 128 + pos] = (uint16_t)bf16_as_f16(silu_mul(acc[n][s][r], acc[n][s + NS / 2][r]));
                 }
             }
         }
     }
     __syncthreads();
-    for (int base = 0; base < ncol * 16; base += 256) {  // 16 chunks (two records) per column
-        const int idx = base + tid, c = idx >> 4, rr = (idx >> 3) & 1, ch = idx & 7;
-        const bool live = c < ncol;
-        const uint4 v = live ? reinterpret_cast<const uint4*>(ht + c * 128 + 64 * rr)[ch] : make_uint4(0, 0, 0, 0);
-        const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
-        float sm = 0.0f;
-#pragma unroll
-        for (int m = 0; m < 4; ++m) sm = (sm + u2f(wv[m] << 16)) + u2f(wv[m] & 0xFFFF0000u);
-        sm = sm + __shfl_xor(sm, 1, kWave);
-        sm = sm + __shfl_xor(sm, 2, kWave);
-        sm = sm + __shfl_xor(sm, 4, kWave);
-        if (live) {
-            uint32_t* dst = hrec + ((size_t)(item.first + c) * h_rec + 2 * rt + rr) * kRecDw;
-            reinterpret_cast<uint4*>(dst)[ch] = v;
-            if (ch == 0) dst[32] = f2u(-sm);
-        }
+    for (int idx = tid; idx < ncol * 16; idx += 512) {  // 16 chunks (two records) per column
+        const int c = idx >> 4, rr = (idx >> 3) & 1, ch = idx & 7;
+        const uint4 v = reinterpret_cast<const uint4*>(ht + c * 128 + 64 * rr)[ch];
+        reinterpret_cast<uint4*>(hrec + ((size_t)(item.first + c) * h_rec + 2 * rt + rr) * (kRecBytes / 4))[ch] = v;
     }
 }
 
-// ------------------------------------------------------------------------------------------------ down
-// Grid (H / 128, work items).  Work-group rt computes down rows [128 rt, 128 rt + 128) of the item's columns
-// (wave w rows 32 w .. 32 w + 31, two sets) into Y[first + c] (the shared expert's rows times sigmoid(sg[t])).
-__global__ __launch_bounds__(256) void k_mm_down(const uint8_t* __restrict__ down_exps, const uint8_t* __restrict__ down_sh,
-                                                 const uint32_t* __restrict__ hrec, int h_rec, const float* __restrict__ sg,
-                                                 const int4* __restrict__ items, int H, int F, int Fs,
-                                                 float* __restrict__ Y) {
-    __shared__ uint32_t wt[128 * 9];
-    __shared__ __align__(16) uint32_t act[kChunk * kActStride + 4];
+__global__ __launch_bounds__(512) void k_mm_gu(const uint8_t* __restrict__ gate_exps, const uint8_t* __restrict__ up_exps,
+                                               const uint8_t* __restrict__ gate_sh, const uint8_t* __restrict__ up_sh,
+                                               const uint32_t* __restrict__ xrec, uint32_t xrec_bytes,
+                                               const int4* __restrict__ items, const int32_t* __restrict__ perm, int k,
+                                               int H, int F, int Fs, uint32_t* __restrict__ hrec, int h_rec) {
+    __shared__ __align__(16) uint8_t lds[kLds];
     __shared__ int rowidx[kChunk];
     Item item;
     if (!work_item(items, blockIdx.y, item)) return;
-    const int rt = blockIdx.x;
     const int Fe = item.shared ? Fs : F;
-    const int ncol = item.ncol, ntiles = (ncol + 15) >> 4;
-    const int units = Fe >> 7;
-    const size_t rb = (size_t)units * 36;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, i = lane & 15, q = lane >> 4;
-    for (int c = tid; c < ncol; c += 256) rowidx[c] = item.first + c;
+    if (128 * (int)blockIdx.x >= Fe) return;
+    const int ncol = item.ncol;
+    if ((int)threadIdx.x < ncol) rowidx[threadIdx.x] = item_token(item, perm, k, threadIdx.x);
     __syncthreads();
-    Stager stg;
-    {
-        const uint8_t* base = item.shared ? down_sh : down_exps + (size_t)item.e * H * ((size_t)(F >> 7) * 36);
-        stg.init(base + (size_t)(128 * rt + (tid & 127)) * rb, tid < 128, hrec, rowidx, ncol, h_rec);
-    }
-    stg.load(0);
-    const int rows[2] = {32 * wave + i, 32 * wave + 16 + i};
+    const size_t rb = (size_t)(H >> 7) * 36;
+    const uint8_t* g0 = item.shared ? gate_sh : gate_exps + (size_t)item.e * F * rb;
+    const uint8_t* u0 = item.shared ? up_sh : up_exps + (size_t)item.e * F * rb;
+    if (ncol > 64) mm_gu_body<true>(lds, rowidx, item, ncol, g0, u0, xrec, xrec_bytes, H, hrec, h_rec);
+    else mm_gu_body<false>(lds, rowidx, item, ncol, g0, u0, xrec, xrec_bytes, H, hrec, h_rec);
+}
 
-    f32x4 acc[kTiles][2];
+// ------------------------------------------------------------------------------------------------ down
+// Grid (H / 256, work items), 8 waves.  Work-group rt computes down rows [256 rt, 256 rt + 256) of the item's
+// columns into Y[first + c] (the shared expert's rows times sigmoid(sg[t])).  Wide: wave w has rows
+// 64 (w % 4) .. + 63 (four sets); narrow: rows 32 w .. + 31 (two sets).
+template <bool WIDE>
+__device__ __forceinline__ void mm_down_body(uint8_t* lds, const int* rowidx, const Item& item, int ncol, int units,
+                                             const uint8_t* d0, const uint32_t* hrec, uint32_t hrec_bytes, int h_rec,
+                                             const float* sg, int H, float* Y) {
+    using S = Shape<WIDE>;
+    constexpr int NS = S::NS;
+    const int rt = blockIdx.x;
+    const uint32_t rb = (uint32_t)units * 36u;
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, i = lane & 15,
+              q = lane >> 4;
+    MmPlan<WIDE> pl;
+    pl.init(rowidx, wave, lane, ncol, h_rec, rb, kWgRows);
+    const int nrows = min(kWgRows, H - kWgRows * rt);
+    const i32x4 ra = buffer_rsrc(hrec, hrec_bytes);
+    const i32x4 rd = buffer_rsrc(d0 + (size_t)kWgRows * rt * rb, (uint32_t)nrows * rb);
+    int rows[NS];
+    const int r0 = WIDE ? 64 * (wave & 3) : 32 * wave;
 #pragma unroll
-    for (int n = 0; n < kTiles; ++n)
+    for (int s = 0; s < NS; ++s) rows[s] = r0 + 16 * s + i;
+    const int tok0 = WIDE ? 64 * (wave >> 2) : 0;
+    const int ntiles = min(4, max(0, (ncol - tok0 + 15) >> 4));
+    f32x4 acc[4][NS];
+    mm_loop<WIDE>(acc, lds, pl, units, ra, rd, rd, rows, tok0, ntiles, i, q);
 #pragma unroll
-        for (int s = 0; s < 2; ++s) acc[n][s] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    for (int u = 0; u < units; ++u) {
-        stg.store(wt, reinterpret_cast<uint4*>(act));
-        __syncthreads();
-        if (u + 1 < units) stg.load(u + 1);
-        mma_unit<2>(acc, wt, rows, act, ntiles, i, q);
-        __syncthreads();
-    }
+    for (int s = 0; s < NS; ++s) {
+        const int row = kWgRows * rt + rows[s];
+        if (row < H) {
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
-        const int col = 128 * rt + 32 * wave + 16 * s + i;
+            for (int n = 0; n < 4; ++n) {
+                if (n < ntiles) {
 #pragma unroll
-        for (int n = 0; n < kTiles; ++n) {
-            if (n < ntiles) {
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int c = 16 * n + 4 * q + r;
-                    if (c < ncol) {
-                        float v = acc[n][s][r];
-                        if (item.shared) v = v * sigmoid(sg[item.tok0 + c]);
-                        Y[(size_t)(item.first + c) * H + col] = v;
+                    for (int r = 0; r < 4; ++r) {
+                        const int c = tok0 + 16 * n + 4 * q + r;
+                        if (c < ncol) {
+                            float v = acc[n][s][r];
+                            if (item.shared) v = v * sigmoid(sg[item.tok0 + c]);
+                            Y[(size_t)(item.first + c) * H + row] = v;
+                        }
                     }
                 }
             }
@@ -329,9 +424,27 @@ __global__ __launch_bounds__(256) void k_mm_down(const uint8_t* __restrict__ dow
     }
 }
 
+__global__ __launch_bounds__(512) void k_mm_down(const uint8_t* __restrict__ down_exps, const uint8_t* __restrict__ down_sh,
+                                                 const uint32_t* __restrict__ hrec, uint32_t hrec_bytes, int h_rec,
+                                                 const float* __restrict__ sg, const int4* __restrict__ items, int H,
+                                                 int F, int Fs, float* __restrict__ Y) {
+    __shared__ __align__(16) uint8_t lds[kLds];
+    __shared__ int rowidx[kChunk];
+    Item item;
+    if (!work_item(items, blockIdx.y, item)) return;
+    const int Fe = item.shared ? Fs : F;
+    const int ncol = item.ncol;
+    if ((int)threadIdx.x < ncol) rowidx[threadIdx.x] = item.first + threadIdx.x;
+    __syncthreads();
+    const int units = Fe >> 7;
+    const uint8_t* d0 = item.shared ? down_sh : down_exps + (size_t)item.e * H * ((size_t)(F >> 7) * 36);
+    if (ncol > 64) mm_down_body<true>(lds, rowidx, item, ncol, units, d0, hrec, hrec_bytes, h_rec, sg, H, Y);
+    else mm_down_body<false>(lds, rowidx, item, ncol, units, d0, hrec, hrec_bytes, h_rec, sg, H, Y);
+}
+
 // ------------------------------------------------------------------------------------------------ launchers
 int mfma_chunk() { return kChunk; }
-size_t act_rec_bytes(int64_t n_rec) { return (size_t)n_rec * kRecDw * 4; }
+size_t act_rec_bytes(int64_t n_rec) { return (size_t)n_rec * kRecBytes; }
 
 hipError_t launch_act_records(const float* x, int64_t n_rec, uint32_t* rec, hipStream_t s) {
     hipLaunchKernelGGL(k_act_records, dim3((unsigned)((n_rec * 8 + 255) / 256)), dim3(256), 0, s, x, n_rec, rec);
@@ -339,19 +452,23 @@ hipError_t launch_act_records(const float* x, int64_t n_rec, uint32_t* rec, hipS
 }
 
 hipError_t launch_mm_gu(const uint8_t* gate_exps, const uint8_t* up_exps, const uint8_t* gate_sh, const uint8_t* up_sh,
-                        const uint32_t* xrec, const int4* items, const int32_t* perm, int k, int H, int F, int Fs,
-                        int has_shared, int max_items, uint32_t* hrec, int h_rec, hipStream_t s) {
+                        const uint32_t* xrec, int64_t n_xrec, const int4* items, const int32_t* perm, int k, int H,
+                        int F, int Fs, int has_shared, int max_items, uint32_t* hrec, int h_rec, hipStream_t s) {
     const int Fmax = has_shared && Fs > F ? Fs : F;
-    hipLaunchKernelGGL(k_mm_gu, dim3((unsigned)(Fmax / 128), (unsigned)max_items), dim3(256), 0, s, gate_exps, up_exps,
-                       gate_sh, up_sh, xrec, items, perm, k, H, F, Fs, hrec, h_rec);
+    const size_t bytes = act_rec_bytes(n_xrec);
+    if (bytes >= kOob) return hipErrorInvalidValue;  // buffer offsets are 31-bit
+    hipLaunchKernelGGL(k_mm_gu, dim3((unsigned)(Fmax / 128), (unsigned)max_items), dim3(512), 0, s, gate_exps, up_exps,
+                       gate_sh, up_sh, xrec, (uint32_t)bytes, items, perm, k, H, F, Fs, hrec, h_rec);
     return hipGetLastError();
 }
 
-hipError_t launch_mm_down(const uint8_t* down_exps, const uint8_t* down_sh, const uint32_t* hrec, int h_rec,
-                          const float* sg, const int4* items, int H, int F, int Fs, int max_items, float* Y,
+hipError_t launch_mm_down(const uint8_t* down_exps, const uint8_t* down_sh, const uint32_t* hrec, int64_t n_hrec,
+                          int h_rec, const float* sg, const int4* items, int H, int F, int Fs, int max_items, float* Y,
                           hipStream_t s) {
-    hipLaunchKernelGGL(k_mm_down, dim3((unsigned)(H / 128), (unsigned)max_items), dim3(256), 0, s, down_exps, down_sh,
-                       hrec, h_rec, sg, items, H, F, Fs, Y);
+    const size_t bytes = act_rec_bytes(n_hrec);
+    if (bytes >= kOob) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_mm_down, dim3((unsigned)((H + kWgRows - 1) / kWgRows), (unsigned)max_items), dim3(512), 0, s,
+                       down_exps, down_sh, hrec, (uint32_t)bytes, h_rec, sg, items, H, F, Fs, Y);
     return hipGetLastError();
 }
 
