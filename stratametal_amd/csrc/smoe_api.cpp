@@ -243,7 +243,13 @@ smoe_status smoe_forward_path(const smoe_geom* g, const smoe_weights* w, const f
                                  mfma ? 1 : 0, iq2 ? 1 : 0, st),
              "router");
     SMOE_MARK();
-    if (T <= kFusedRouteTokens) {
+    // batches of at most kFusedRouteTokens tokens on the Q2_0 GEMV path: the gate/up kernel routes the batch itself,
+    // and (when the batch's h images fit in LDS) the down kernel applies the combine
+    const bool small = !mfma && !iq2 && T <= kFusedRouteTokens;
+    const bool small_down = small && smoe::down_combine_ok(T, K, L.h_blocks);
+    if (small) {
+        // no route kernel: the stage boundary marks stay, the route stage is empty
+    } else if (T <= kFusedRouteTokens) {
         SMOE_TRY(smoe::launch_topk_dispatch(logits, T, E, K, ids, wts, counts, offsets, perm, slot, elist, nlist, items,
                                             n_items, has_sh ? 1 : 0, chunk, sh_chunk, st),
                  "route");
@@ -275,14 +281,26 @@ smoe_status smoe_forward_path(const smoe_geom* g, const smoe_weights* w, const f
         SMOE_MARK();
         SMOE_TRY(smoe::launch_iq2_down(de, ds, himg, L.h_blocks, sg, items, H, F, Fs, n_items, Y, st), "down");
     } else {
-        SMOE_TRY(smoe::launch_q2_gu(ge, ue, gs, us, ximg, items, perm, K, H, F, Fs, has_sh ? 1 : 0, n_items, himg,
-                                    L.h_blocks, st),
-                 "gate/up");
+        if (small)
+            SMOE_TRY(smoe::launch_q2_gu_route(ge, ue, gs, us, ximg, logits, T, E, K, H, F, Fs, has_sh ? 1 : 0, ids, wts,
+                                              counts, offsets, perm, slot, elist, nlist, items, n_items, himg,
+                                              L.h_blocks, st),
+                     "route + gate/up");
+        else
+            SMOE_TRY(smoe::launch_q2_gu(ge, ue, gs, us, ximg, items, perm, K, H, F, Fs, has_sh ? 1 : 0, n_items, himg,
+                                        L.h_blocks, st),
+                     "gate/up");
         SMOE_MARK();
-        SMOE_TRY(smoe::launch_q2_down(de, ds, himg, L.h_blocks, sg, items, H, F, Fs, n_items, Y, st), "down");
+        if (small_down)
+            SMOE_TRY(smoe::launch_q2_down_combine(de, ds, himg, L.h_blocks, sg, items, n_items, H, F, Fs, slot, wts, T, K,
+                                                  (has_sh && add_shared) ? 1 : 0, y, st),
+                     "down + combine");
+        else
+            SMOE_TRY(smoe::launch_q2_down(de, ds, himg, L.h_blocks, sg, items, H, F, Fs, n_items, Y, st), "down");
     }
     SMOE_MARK();
-    SMOE_TRY(smoe::launch_combine(Y, slot, wts, K, H, P, T, (has_sh && add_shared) ? 1 : 0, y, st), "combine");
+    if (!small_down)
+        SMOE_TRY(smoe::launch_combine(Y, slot, wts, K, H, P, T, (has_sh && add_shared) ? 1 : 0, y, st), "combine");
     SMOE_MARK();
 #undef SMOE_MARK
     return ok();

@@ -489,8 +489,10 @@ __device__ __forceinline__ void route_token_t(const float* __restrict__ l, int E
     for (int i = 0; i < k; ++i) ssel = ssel + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), i));
     const float den = __builtin_fmaxf(ssel, 6.103515625e-05f);
     if (lane < k) {
-        ids[lane] = my_id;
-        wts[lane] = p / den;
+        if (ids) {  // NULL: the ids go to LDS only
+            ids[lane] = my_id;
+            wts[lane] = p / den;
+        }
         if (ids_lds) ids_lds[lane] = my_id;
     }
 }
@@ -699,27 +701,32 @@ struct SmallDispatchLds {
     int perm[kSmallPairs];
     int cnt[1024];
     int off[1024];
+    int el[1024];  // touched experts, ascending
     int scan[3 * 4];
+    int n_touched;
 };
-__global__ __launch_bounds__(256) void k_topk_dispatch(const float* __restrict__ logits, int T, int E, int k,
-                                                        int32_t* __restrict__ ids, float* __restrict__ wts,
-                                                        int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
-                                                        int32_t* __restrict__ perm, int32_t* __restrict__ slot,
-                                                        int32_t* __restrict__ elist, int32_t* __restrict__ n_list,
-                                                        int4* __restrict__ items, int max_items, int has_shared,
-                                                        int chunk, int sh_chunk) {
-    __shared__ SmallDispatchLds s;
+
+// Every thread of a 256-thread work-group calls it.  With `store` false nothing is written to global memory and
+// the work-item table is not built: the work-group keeps the routing in LDS (s.ids, s.cnt, s.off, s.el,
+// s.n_touched, s.perm = pair of each dispatch position) for its own use.  Ends with a barrier.
+__device__ __forceinline__ void small_route_dispatch(const float* __restrict__ logits, int T, int E, int k, bool store,
+                                                     int32_t* __restrict__ ids, float* __restrict__ wts,
+                                                     int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
+                                                     int32_t* __restrict__ perm, int32_t* __restrict__ slot,
+                                                     int32_t* __restrict__ elist, int32_t* __restrict__ n_list,
+                                                     int4* __restrict__ items, int max_items, int has_shared, int chunk,
+                                                     int sh_chunk, SmallDispatchLds& s) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int P = T * k;
 #pragma unroll
     for (int j = 0; j < 4; ++j) s.cnt[tid + 256 * j] = 0;
-    if (wave < T) route_token(logits + (size_t)wave * E, E, k, ids + (size_t)wave * k, wts + (size_t)wave * k,
-                              s.ids + wave * k);
+    if (wave < T) route_token(logits + (size_t)wave * E, E, k, store ? ids + (size_t)wave * k : nullptr,
+                              store ? wts + (size_t)wave * k : nullptr, s.ids + wave * k);
     __syncthreads();
     const int id = tid < P ? s.ids[tid] : -1;
     const bool valid = id >= 0 && id < E;
     if (valid) atomicAdd(&s.cnt[id], 1);
-    if (tid < P && !valid) slot[tid] = -1;
+    if (store && tid < P && !valid) slot[tid] = -1;
     __syncthreads();
     // experts 4 tid .. 4 tid + 3: counts, touched flags and item chunks, then one scan of the three sums
     int c[4], nch[4];
@@ -757,28 +764,36 @@ __global__ __launch_bounds__(256) void k_topk_dispatch(const float* __restrict__
         first_of[j] = run_off;
         if (e < E) {
             s.off[e] = run_off;
-            if (counts) counts[e] = c[j];
-            offsets[e] = run_off;
-            if (c[j] > 0 && elist) elist[run_flag] = e;
+            if (c[j] > 0) s.el[run_flag] = e;
+            if (store) {
+                if (counts) counts[e] = c[j];
+                offsets[e] = run_off;
+                if (c[j] > 0 && elist) elist[run_flag] = e;
+            }
         }
         run_off += c[j];
         run_flag += c[j] > 0 ? 1 : 0;
     }
     if (tid == 0) {
-        offsets[E] = total[0];
-        if (n_list) *n_list = total[1];
+        s.n_touched = total[1];
+        if (store) {
+            offsets[E] = total[0];
+            if (n_list) *n_list = total[1];
+        }
     }
     __syncthreads();
     if (valid) {  // rank = earlier pairs with the same expert (ascending pair order within an expert)
         int rank = 0;
         for (int q = 0; q < tid; ++q) rank += s.ids[q] == id ? 1 : 0;
         const int pos = s.off[id] + rank;
-        perm[pos] = tid;
-        slot[tid] = pos;
         s.perm[pos] = tid;
+        if (store) {
+            perm[pos] = tid;
+            slot[tid] = pos;
+        }
     }
     __syncthreads();
-    if (!items) return;
+    if (!store || !items) return;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         for (int ch = 0; ch < nch[j]; ++ch) {
@@ -803,6 +818,18 @@ __global__ __launch_bounds__(256) void k_topk_dispatch(const float* __restrict__
     }
 }
 
+__global__ __launch_bounds__(256) void k_topk_dispatch(const float* __restrict__ logits, int T, int E, int k,
+                                                        int32_t* __restrict__ ids, float* __restrict__ wts,
+                                                        int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
+                                                        int32_t* __restrict__ perm, int32_t* __restrict__ slot,
+                                                        int32_t* __restrict__ elist, int32_t* __restrict__ n_list,
+                                                        int4* __restrict__ items, int max_items, int has_shared,
+                                                        int chunk, int sh_chunk) {
+    __shared__ SmallDispatchLds s;
+    small_route_dispatch(logits, T, E, k, true, ids, wts, counts, offsets, perm, slot, elist, n_list, items, max_items,
+                         has_shared, chunk, sh_chunk, s);
+}
+
 // ------------------------------------------------------------------------------------------------ expert GEMV
 // Row geometry: dpr = n_in / 128 units; lpr = lanes per row; upl = units per lane; rpi = 64 / lpr rows per
 // wave pass.  Lane (group, l) handles units g = l + lpr * m (m < upl) of its row.
@@ -824,20 +851,16 @@ constexpr int kGuCols = 8;
 // [32 hb + 8 w, +8) (rows rho 0..7) and the same up rows (rho 8..15); the item's columns are processed in
 // stages of kGuCols: their x images are copied to LDS, every column's row values parked in LDS by the group
 // leaders, then each half wave quantises one column's 32 h values into image block hb.
+// The work-group's item: `smem` is the kernel's dynamic LDS (the image staging area).
 template <int NIT, int MAXUPL>
-__global__ __launch_bounds__(256) void k_q2_gu(const uint8_t* __restrict__ gate_exps, const uint8_t* __restrict__ up_exps,
-                                                const uint8_t* __restrict__ gate_sh, const uint8_t* __restrict__ up_sh,
-                                                const uint32_t* __restrict__ ximg, const int4* __restrict__ items,
-                                                const int32_t* __restrict__ perm, int k, int H, int F, int Fs,
-                                                uint32_t* __restrict__ himg, int h_blocks) {
-    extern __shared__ __align__(16) uint32_t smem[];
+__device__ __forceinline__ void q2_gu_item(const Item& item, uint32_t* smem, const uint8_t* __restrict__ gate_exps,
+                                           const uint8_t* __restrict__ up_exps, const uint8_t* __restrict__ gate_sh,
+                                           const uint8_t* __restrict__ up_sh, const uint32_t* __restrict__ ximg,
+                                           const int32_t* __restrict__ perm, int k, int H, int F,
+                                           uint32_t* __restrict__ himg, int h_blocks) {
     __shared__ float rowv[kGuCols][64];
     __shared__ uint8_t qsc[8][32];
-    Item item;
-    if (!work_item(items, blockIdx.y, item)) return;
     const int hb = blockIdx.x;
-    const int Fe = item.shared ? Fs : F;
-    if (hb * 32 >= Fe) return;
     const RowGeo G = row_geo(H);
     const size_t rb = (size_t)G.dpr * 36;
     const uint8_t* g0 = item.shared ? gate_sh : gate_exps + (size_t)item.e * F * rb;
@@ -921,6 +944,67 @@ __global__ __launch_bounds__(256) void k_q2_gu(const uint8_t* __restrict__ gate_
         }
         if (c0 + kGuCols < item.ncol) __syncthreads();
     }
+}
+
+template <int NIT, int MAXUPL>
+__global__ __launch_bounds__(256) void k_q2_gu(const uint8_t* __restrict__ gate_exps, const uint8_t* __restrict__ up_exps,
+                                                const uint8_t* __restrict__ gate_sh, const uint8_t* __restrict__ up_sh,
+                                                const uint32_t* __restrict__ ximg, const int4* __restrict__ items,
+                                                const int32_t* __restrict__ perm, int k, int H, int F, int Fs,
+                                                uint32_t* __restrict__ himg, int h_blocks) {
+    extern __shared__ __align__(16) uint32_t smem[];
+    Item item;
+    if (!work_item(items, blockIdx.y, item)) return;
+    if ((int)blockIdx.x * 32 >= (item.shared ? Fs : F)) return;
+    q2_gu_item<NIT, MAXUPL>(item, smem, gate_exps, up_exps, gate_sh, up_sh, ximg, perm, k, H, F, himg, h_blocks);
+}
+
+// Gate/up of a batch of at most kShCols tokens straight from the logits, with no route kernel before it.  Grid
+// (Fmax / 32, max work items) as k_q2_gu.  The shared expert's work-groups (item 0 with a shared expert) start
+// at once; every other work-group routes and dispatches the batch itself (small_route_dispatch, into LDS) and
+// takes as its item the (y - n_sh)-th touched expert in ascending order -- the item dispatch_block would have
+// written there.  Work-group (0, n_sh) also writes the routing, the dispatch and the work-item table for the
+// kernels after it.
+template <int NIT, int MAXUPL>
+__global__ __launch_bounds__(256) void k_q2_gu_route(
+    const uint8_t* __restrict__ gate_exps, const uint8_t* __restrict__ up_exps, const uint8_t* __restrict__ gate_sh,
+    const uint8_t* __restrict__ up_sh, const uint32_t* __restrict__ ximg, const float* __restrict__ logits, int T,
+    int E, int k, int H, int F, int Fs, int has_shared, int32_t* __restrict__ ids, float* __restrict__ wts,
+    int32_t* __restrict__ counts, int32_t* __restrict__ offsets, int32_t* __restrict__ perm,
+    int32_t* __restrict__ slot, int32_t* __restrict__ elist, int32_t* __restrict__ n_list, int4* __restrict__ items,
+    int max_items, uint32_t* __restrict__ himg, int h_blocks) {
+    extern __shared__ __align__(16) uint32_t smem[];
+    const int n_sh = has_shared ? 1 : 0;
+    const int P = T * k;
+    Item item;
+    if ((int)blockIdx.y < n_sh) {
+        if ((int)blockIdx.x * 32 >= Fs) return;
+        item.shared = true;
+        item.e = kItemShared;
+        item.first = P;
+        item.ncol = T;
+        item.tok0 = 0;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) item.tk[c] = c;
+    } else {
+        if ((int)blockIdx.x * 32 >= F) return;
+        SmallDispatchLds& s = *reinterpret_cast<SmallDispatchLds*>(smem);
+        const bool writer = blockIdx.x == 0 && (int)blockIdx.y == n_sh;
+        small_route_dispatch(logits, T, E, k, writer, ids, wts, counts, offsets, perm, slot, elist, n_list, items,
+                             max_items, has_shared, 1 << 30, kShCols, s);
+        const int y = (int)blockIdx.y - n_sh;
+        if (y >= s.n_touched) return;  // uniform: no expert for this item
+        const int e = s.el[y];
+        item.shared = false;
+        item.e = e;
+        item.first = s.off[e];
+        item.ncol = s.cnt[e];  // at most T <= 4: a token picks an expert once
+#pragma unroll
+        for (int c = 0; c < 4; ++c) item.tk[c] = c < item.ncol ? s.perm[item.first + c] / k : 0;
+        item.tok0 = item.tk[0];
+        __syncthreads();  // every thread has read s before the staging reuses the space
+    }
+    q2_gu_item<NIT, MAXUPL>(item, smem, gate_exps, up_exps, gate_sh, up_sh, ximg, perm, k, H, F, himg, h_blocks);
 }
 
 // Down rows.  Grid (ceil(H / rows per block), max work items), 4 waves; a wave owns NIT passes of rpi rows.
@@ -1009,6 +1093,122 @@ __global__ __launch_bounds__(256) void k_q2_down(const uint8_t* __restrict__ dow
             }
         }
         if (c0 + cps < item.ncol) __syncthreads();
+    }
+}
+
+// Down rows and the combine of a batch of at most kShCols tokens in one kernel.  Grid (ceil(H / kDcRows)), 4
+// waves.  Work-group b owns output rows [kDcRows b, + kDcRows) of every item: the h images of all P + T pair rows
+// go to LDS; the tasks (item i, pass p: rows p rpi .. + rpi - 1 of the block's rows, rpi = 64 / lpr of the
+// item's row length) are dealt to the waves round robin, a wave holding the weight units of NT tasks (at most
+// MAXUPL units per lane each, NT * MAXUPL <= 8) at once.  Each row value is formed as k_q2_down forms it (the
+// lane's units in order, the butterfly over its lpr lanes, shared rows times sigmoid(sg)) and parked in LDS;
+// then y[t][row] as k_combine forms it: w0 * Y[slot0], fma in selection order, + the shared row.
+constexpr int kDcRows = 16;
+constexpr size_t kDownCombineLds = 96 * 1024;  // images + rows of the batch
+template <int MAXUPL, int NT>
+__global__ __launch_bounds__(256) void k_q2_down_combine(
+    const uint8_t* __restrict__ down_exps, const uint8_t* __restrict__ down_sh, const uint32_t* __restrict__ himg,
+    int h_blocks, const float* __restrict__ sg, const int4* __restrict__ items, int n_items, int npass, int H, int F,
+    int Fs, const int32_t* __restrict__ slot, const float* __restrict__ wts, int T, int k, int add_shared,
+    float* __restrict__ y) {
+    typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
+    extern __shared__ __align__(16) uint32_t smem[];
+    __shared__ int s_slot[kSmallPairs];
+    __shared__ float s_wts[kSmallPairs];
+    const int P = T * k, rows = P + T;
+    const int pieces = rows * h_blocks * (kImgDw / 4);  // 16-byte pieces of the images
+    float* Ys = reinterpret_cast<float*>(smem + (size_t)pieces * 4);  // [rows][kDcRows]
+    const int r0 = blockIdx.x * kDcRows;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int n_tasks = n_items * npass;
+
+    // the images' first 1024 pieces, the routing slots and weights: loads issued before the weight loads, so that
+    // their LDS stores wait for them alone
+    u32x4 pre[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) pre[j] = reinterpret_cast<const u32x4*>(himg)[min(j * 256 + tid, pieces - 1)];
+    const int sl = slot[min(tid, P - 1)];
+    const float wt = wts[min(tid, P - 1)];
+    __builtin_amdgcn_sched_barrier(0);
+
+    for (int tb = 0; tb < n_tasks; tb += 4 * NT) {
+        Item it[NT];
+        bool live[NT];
+        int lpr[NT], upl[NT], rloc[NT];
+        uint32_t w[NT][MAXUPL][9];
+#pragma unroll
+        for (int q = 0; q < NT; ++q) {
+            const int j = tb + 4 * q + wave;  // wave-uniform task
+            const int i = j < n_tasks ? j / npass : 0, p = j < n_tasks ? j - i * npass : 0;
+            live[q] = j < n_tasks && work_item(items, i, it[q]);
+            const bool sh = live[q] && it[q].shared;
+            const RowGeo G = row_geo(sh ? Fs : F);
+            lpr[q] = G.lpr;
+            upl[q] = G.upl;
+            live[q] = live[q] && p * G.rpi < kDcRows;
+            const int grp = lane / G.lpr, l = lane - grp * G.lpr;
+            rloc[q] = p * G.rpi + grp;
+            const size_t rb = (size_t)G.dpr * 36;
+            const uint8_t* base = sh ? down_sh : down_exps + (size_t)(live[q] ? it[q].e : 0) * H * ((size_t)(F >> 7) * 36);
+            const int r = min(r0 + min(rloc[q], kDcRows - 1), H - 1);  // every load in bounds
+#pragma unroll
+            for (int m = 0; m < MAXUPL; ++m)
+                load_unit(base + (size_t)r * rb + (size_t)(m < G.upl ? l + G.lpr * m : l) * 36, w[q][m]);
+        }
+        if (tb == 0) {
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if (j * 256 + tid < pieces) reinterpret_cast<u32x4*>(smem)[j * 256 + tid] = pre[j];
+            for (int i = 1024 + tid; i < pieces; i += 256)
+                reinterpret_cast<u32x4*>(smem)[i] = reinterpret_cast<const u32x4*>(himg)[i];
+            if (tid < P) {
+                s_slot[tid] = sl;
+                s_wts[tid] = wt;
+            }
+            __syncthreads();
+        }
+        float dw[NT][MAXUPL][2];
+        unit_scales(w, dw);
+#pragma unroll
+        for (int q = 0; q < NT; ++q) {
+            if (!live[q]) continue;  // wave-uniform
+            const int grp = lane / lpr[q], l = lane - grp * lpr[q];
+            const bool store = rloc[q] < kDcRows && r0 + rloc[q] < H && l == 0;
+            for (int c = 0; c < it[q].ncol; ++c) {
+                const uint32_t* ht = smem + (size_t)(it[q].first + c) * h_blocks * kImgDw;
+                pin_units(w);
+                float acc = 0.0f;
+#pragma unroll
+                for (int m = 0; m < MAXUPL; ++m) {
+                    if (m < upl[q]) {
+                        const uint32_t* img = ht + (size_t)(4 * (l + lpr[q] * m)) * kImgDw;
+                        Act2 a;
+                        load_act_img2(img, a);
+                        const float p01 = q2_unit_first(w[q][m], dw[q][m][0], a);
+                        load_act_img2(img + 2 * kImgDw, a);
+                        const float L = q2_unit_second(w[q][m], dw[q][m][1], p01, a);
+                        acc = m == 0 ? L : acc + L;
+                    }
+                }
+                float v = group_sum(acc, lpr[q]);
+                if (it[q].shared) v = v * sigmoid(sg[it[q].tok0 + c]);
+                if (store) Ys[(it[q].first + c) * kDcRows + rloc[q]] = v;
+            }
+        }
+    }
+    __syncthreads();
+    if (tid < T * kDcRows) {
+        const int t = tid / kDcRows, rl = tid - t * kDcRows;
+        if (r0 + rl < H) {
+            float acc = 0.0f;
+            for (int s = 0; s < k; ++s) {
+                const float v = Ys[s_slot[t * k + s] * kDcRows + rl], wv = s_wts[t * k + s];
+                acc = s == 0 ? wv * v : __builtin_fmaf(wv, v, acc);
+            }
+            if (add_shared) acc = acc + Ys[(P + t) * kDcRows + rl];
+            y[(size_t)t * H + r0 + rl] = acc;
+        }
     }
 }
 
@@ -1341,6 +1541,63 @@ hipError_t launch_q2_down(const uint8_t* down_exps, const uint8_t* down_sh, cons
                        Fs, cps, Y)
     SMOE_SHAPE_DISPATCH(SMOE_DOWN)
 #undef SMOE_DOWN
+    return hipGetLastError();
+}
+
+hipError_t launch_q2_gu_route(const uint8_t* gate_exps, const uint8_t* up_exps, const uint8_t* gate_sh,
+                              const uint8_t* up_sh, const uint32_t* ximg, const float* logits, int T, int E, int k, int H,
+                              int F, int Fs, int has_shared, int32_t* ids, float* wts, int32_t* counts,
+                              int32_t* offsets, int32_t* perm, int32_t* slot, int32_t* elist, int32_t* n_list,
+                              int4* items, int max_items, uint32_t* himg, int h_blocks, hipStream_t s) {
+    if (T < 1 || T > kShCols || T * k > kSmallPairs || E > 1024) return hipErrorInvalidValue;
+    const int Fmax = has_shared && Fs > F ? Fs : F;
+    dim3 grid((unsigned)(Fmax / 32), (unsigned)max_items);
+    int nit, upl;
+    gu_shape(H, nit, upl);
+    size_t lds = (size_t)kGuCols * (H >> 5) * kImgDw * 4 + 16;
+    if (lds < sizeof(SmallDispatchLds)) lds = sizeof(SmallDispatchLds);
+#define SMOE_GUR(N, U)                                                                                             \
+    hipLaunchKernelGGL((k_q2_gu_route<N, U>), grid, dim3(256), lds, s, gate_exps, up_exps, gate_sh, up_sh, ximg,   \
+                       logits, T, E, k, H, F, Fs, has_shared, ids, wts, counts, offsets, perm, slot, elist, n_list, \
+                       items, max_items, himg, h_blocks)
+    SMOE_SHAPE_DISPATCH(SMOE_GUR)
+#undef SMOE_GUR
+    return hipGetLastError();
+}
+
+size_t down_combine_lds(int T, int k, int h_blocks) {
+    const size_t rows = (size_t)T * k + T;
+    return rows * h_blocks * kImgDw * 4 + rows * kDcRows * 4;
+}
+
+bool down_combine_ok(int T, int k, int h_blocks) {
+    return T >= 1 && T <= kShCols && T * k <= kSmallPairs && down_combine_lds(T, k, h_blocks) <= kDownCombineLds;
+}
+
+hipError_t launch_q2_down_combine(const uint8_t* down_exps, const uint8_t* down_sh, const uint32_t* himg, int h_blocks,
+                                  const float* sg, const int4* items, int n_items, int H, int F, int Fs,
+                                  const int32_t* slot, const float* wts, int T, int k, int add_shared, float* y,
+                                  hipStream_t s) {
+    if (!down_combine_ok(T, k, h_blocks)) return hipErrorInvalidValue;
+    int npass = 1, maxupl = 1;
+    for (const int Fe : {F, Fs}) {
+        if (Fe <= 0) continue;
+        const int dpr = Fe >> 7, lpr = lanes_per_row_host(dpr), rpi = 64 / lpr;
+        const int np = (kDcRows + rpi - 1) / rpi, u = dpr / lpr;
+        npass = np > npass ? np : npass;
+        maxupl = u > maxupl ? u : maxupl;
+    }
+    if (maxupl > 8) return hipErrorInvalidValue;
+    dim3 grid((unsigned)((H + kDcRows - 1) / kDcRows));
+    const size_t lds = down_combine_lds(T, k, h_blocks);
+#define SMOE_DC(U, N)                                                                                               \
+    hipLaunchKernelGGL((k_q2_down_combine<U, N>), grid, dim3(256), lds, s, down_exps, down_sh, himg, h_blocks, sg, \
+                       items, n_items, npass, H, F, Fs, slot, wts, T, k, add_shared, y)
+    if (maxupl == 1) SMOE_DC(1, 4);
+    else if (maxupl == 2) SMOE_DC(2, 4);
+    else if (maxupl <= 4) SMOE_DC(4, 2);
+    else SMOE_DC(8, 1);
+#undef SMOE_DC
     return hipGetLastError();
 }
 

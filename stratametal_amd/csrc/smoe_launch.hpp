@@ -31,6 +31,18 @@ hipError_t launch_q2_gu(const uint8_t* gate_exps, const uint8_t* up_exps, const 
 hipError_t launch_q2_down(const uint8_t* down_exps, const uint8_t* down_sh, const uint32_t* himg, int h_blocks,
                           const float* sg, const int4* items, int H, int F, int Fs, int max_items, float* Y,
                           hipStream_t s);
+// batches of at most 4 tokens: gate/up that routes the batch itself (no route kernel before it), and down rows
+// with the combine (no combine kernel after it) when the batch's h images fit in LDS
+hipError_t launch_q2_gu_route(const uint8_t* gate_exps, const uint8_t* up_exps, const uint8_t* gate_sh,
+                              const uint8_t* up_sh, const uint32_t* ximg, const float* logits, int T, int E, int k, int H,
+                              int F, int Fs, int has_shared, int32_t* ids, float* wts, int32_t* counts,
+                              int32_t* offsets, int32_t* perm, int32_t* slot, int32_t* elist, int32_t* n_list,
+                              int4* items, int max_items, uint32_t* himg, int h_blocks, hipStream_t s);
+bool down_combine_ok(int T, int k, int h_blocks);
+hipError_t launch_q2_down_combine(const uint8_t* down_exps, const uint8_t* down_sh, const uint32_t* himg, int h_blocks,
+                                  const float* sg, const int4* items, int n_items, int H, int F, int Fs,
+                                  const int32_t* slot, const float* wts, int T, int k, int add_shared, float* y,
+                                  hipStream_t s);
 hipError_t launch_residual_rmsnorm(const float* x, const float* r, int n_rows, int n, float eps, float* out,
                                    hipStream_t s);
 hipError_t launch_combine(const float* Y, const int32_t* slot, const float* wts, int k, int H, int P, int T,
