@@ -406,8 +406,9 @@ constexpr Cmp kNet16[63] = {{0, 1}, {2, 3}, {4, 5}, {6, 7}, {8, 9}, {10, 11}, {1
 // head keys, the single lane holding it wins (or, on an exact tie across lanes, the lowest candidate id) and
 // pops its head.  ex_e = exp(l_e - max); S = per-lane sums in j order, then the xor butterfly 32..1;
 // p_i = ex_i / S; w_i = p_i / max(sum of the k p_i in selection order, 2^-14)
-// (metal/shaders/router.metal:30-132; oracle: or_route_dev).
-template <int J>
+// (metal/shaders/router.metal:30-132; oracle: or_route_dev).  With WTS false only the ids are formed (the
+// selection never reads the probabilities).
+template <int J, bool WTS = true>
 __device__ __forceinline__ void route_token_t(const float* __restrict__ l, int E, int k, int32_t* __restrict__ ids,
                               float* __restrict__ wts, int32_t* ids_lds = nullptr) {
     const int lane = threadIdx.x & 63;
@@ -430,16 +431,19 @@ __device__ __forceinline__ void route_token_t(const float* __restrict__ l, int E
         jj[j] = j;
         mx = __builtin_fmaxf(mx, v);
     }
-    mx = wave_max_fast(mx);
-    float acc = 0.0f;
+    float S = 0.0f;
+    if constexpr (WTS) {
+        mx = wave_max_fast(mx);
+        float acc = 0.0f;
 #pragma unroll
-    for (int j = 0; j < J; ++j) {
-        const bool valid = lane + 64 * j < E;
-        const float x = expf_smoe(ex[j] - mx);
-        ex[j] = valid ? x : 0.0f;
-        acc = valid ? acc + x : acc;
+        for (int j = 0; j < J; ++j) {
+            const bool valid = lane + 64 * j < E;
+            const float x = expf_smoe(ex[j] - mx);
+            ex[j] = valid ? x : 0.0f;
+            acc = valid ? acc + x : acc;
+        }
+        S = wave_sum_xor_fast(acc);
     }
-    const float S = wave_sum_xor_fast(acc);
     const Cmp* net = J == 8 ? kNet8 : kNet16;
     constexpr int NC = J == 8 ? 19 : 63;
 #pragma unroll
@@ -451,8 +455,10 @@ __device__ __forceinline__ void route_token_t(const float* __restrict__ l, int E
         const int ja = jj[a], jb = jj[b];
         key[a] = sw ? kb : ka;
         key[b] = sw ? ka : kb;
-        ex[a] = sw ? xb : xa;
-        ex[b] = sw ? xa : xb;
+        if constexpr (WTS) {
+            ex[a] = sw ? xb : xa;
+            ex[b] = sw ? xa : xb;
+        }
         jj[a] = sw ? jb : ja;
         jj[b] = sw ? ja : jb;
     }
@@ -469,38 +475,43 @@ __device__ __forceinline__ void route_token_t(const float* __restrict__ l, int E
             wid = wave_min_i32_fast(mine ? lane + 64 * jj[0] : 0x7FFFFFFF);
         }
         const int wl = wid & 63;
-        const float xw = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ex[0]), wl));
-        if (lane == i) {
-            my_x = xw;
-            my_id = wid;
+        if constexpr (WTS) {
+            const float xw = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ex[0]), wl));
+            if (lane == i) my_x = xw;
         }
+        if (lane == i) my_id = wid;
         if (lane == wl) {  // pop the head
 #pragma unroll
             for (int j = 0; j + 1 < J; ++j) {
                 key[j] = key[j + 1];
-                ex[j] = ex[j + 1];
+                if constexpr (WTS) ex[j] = ex[j + 1];
                 jj[j] = jj[j + 1];
             }
             key[J - 1] = 0u;
         }
     }
-    const float p = my_x / S;
-    float ssel = 0.0f;
-    for (int i = 0; i < k; ++i) ssel = ssel + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), i));
-    const float den = __builtin_fmaxf(ssel, 6.103515625e-05f);
-    if (lane < k) {
-        if (ids) {  // NULL: the ids go to LDS only
+    if constexpr (WTS) {
+        const float p = my_x / S;
+        float ssel = 0.0f;
+        for (int i = 0; i < k; ++i) ssel = ssel + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), i));
+        const float den = __builtin_fmaxf(ssel, 6.103515625e-05f);
+        if (lane < k && ids) {  // NULL: the ids go to LDS only
             ids[lane] = my_id;
             wts[lane] = p / den;
         }
-        if (ids_lds) ids_lds[lane] = my_id;
     }
+    if (lane < k && ids_lds) ids_lds[lane] = my_id;
 }
 
 __device__ __forceinline__ void route_token(const float* __restrict__ l, int E, int k, int32_t* __restrict__ ids,
                                             float* __restrict__ wts, int32_t* ids_lds = nullptr) {
     if (E <= 512) route_token_t<8>(l, E, k, ids, wts, ids_lds);
     else route_token_t<16>(l, E, k, ids, wts, ids_lds);
+}
+// The ids alone, into LDS.
+__device__ __forceinline__ void route_token_ids(const float* __restrict__ l, int E, int k, int32_t* ids_lds) {
+    if (E <= 512) route_token_t<8, false>(l, E, k, nullptr, nullptr, ids_lds);
+    else route_token_t<16, false>(l, E, k, nullptr, nullptr, ids_lds);
 }
 
 __global__ __launch_bounds__(64) void k_topk(const float* __restrict__ logits, int ld_logits, int T, int E, int k,
@@ -851,8 +862,9 @@ constexpr int kGuCols = 8;
 // [32 hb + 8 w, +8) (rows rho 0..7) and the same up rows (rho 8..15); the item's columns are processed in
 // stages of kGuCols: their x images are copied to LDS, every column's row values parked in LDS by the group
 // leaders, then each half wave quantises one column's 32 h values into image block hb.
-// The work-group's item: `smem` is the kernel's dynamic LDS (the image staging area).
-template <int NIT, int MAXUPL>
+// The work-group's item: `smem` is the kernel's dynamic LDS (the image staging area).  PRESTAGED: the images of
+// every token are already in LDS, token t in column slot t (batches of at most 4 tokens).
+template <int NIT, int MAXUPL, bool PRESTAGED = false>
 __device__ __forceinline__ void q2_gu_item(const Item& item, uint32_t* smem, const uint8_t* __restrict__ gate_exps,
                                            const uint8_t* __restrict__ up_exps, const uint8_t* __restrict__ gate_sh,
                                            const uint8_t* __restrict__ up_sh, const uint32_t* __restrict__ ximg,
@@ -884,30 +896,34 @@ __device__ __forceinline__ void q2_gu_item(const Item& item, uint32_t* smem, con
         }
     };
     const int nc0 = min(kGuCols, item.ncol);
-    if (stage_direct(item, 0, nc0, true)) {
-        StagePieces sp;
-        stage_issue_direct(sp, ximg, qb, 0, nc0, kGuCols, 0, item, true);
-        __builtin_amdgcn_sched_barrier(0);
+    if constexpr (PRESTAGED) {
         load_weights();
-        __builtin_amdgcn_sched_barrier(0);
-        stage_commit_direct(sp, smem);
     } else {
-        load_weights();
-        stage_images(smem, ximg, qb, 0, nc0, kGuCols, item, perm, k, true, 0, 4 * 256);
+        if (stage_direct(item, 0, nc0, true)) {
+            StagePieces sp;
+            stage_issue_direct(sp, ximg, qb, 0, nc0, kGuCols, 0, item, true);
+            __builtin_amdgcn_sched_barrier(0);
+            load_weights();
+            __builtin_amdgcn_sched_barrier(0);
+            stage_commit_direct(sp, smem);
+        } else {
+            load_weights();
+            stage_images(smem, ximg, qb, 0, nc0, kGuCols, item, perm, k, true, 0, 4 * 256);
+        }
+        stage_images(smem, ximg, qb, 0, nc0, kGuCols, item, perm, k, true, 4 * 256);  // rounds beyond the first
+        __syncthreads();
     }
-    stage_images(smem, ximg, qb, 0, nc0, kGuCols, item, perm, k, true, 4 * 256);  // rounds beyond the first
-    __syncthreads();
     float dw[NIT][MAXUPL][2];
     unit_scales(w, dw);
 
     for (int c0 = 0; c0 < item.ncol; c0 += kGuCols) {
         const int nc = min(kGuCols, item.ncol - c0);
-        if (c0 > 0) {
+        if (!PRESTAGED && c0 > 0) {
             stage_images(smem, ximg, qb, c0, nc, kGuCols, item, perm, k, true);
             __syncthreads();
         }
         for (int c = 0; c < nc; ++c) {
-            const uint32_t* xt = smem + (size_t)c * qb * kImgDw;
+            const uint32_t* xt = smem + (size_t)(PRESTAGED ? item_token_head(item, c) : c) * qb * kImgDw;
             pin_units(w);
             float acc[NIT];
 #pragma unroll
@@ -960,11 +976,18 @@ __global__ __launch_bounds__(256) void k_q2_gu(const uint8_t* __restrict__ gate_
 }
 
 // Gate/up of a batch of at most kShCols tokens straight from the logits, with no route kernel before it.  Grid
-// (Fmax / 32, max work items) as k_q2_gu.  The shared expert's work-groups (item 0 with a shared expert) start
-// at once; every other work-group routes and dispatches the batch itself (small_route_dispatch, into LDS) and
-// takes as its item the (y - n_sh)-th touched expert in ascending order -- the item dispatch_block would have
-// written there.  Work-group (0, n_sh) also writes the routing, the dispatch and the work-item table for the
-// kernels after it.
+// (Fmax / 32, max work items + 1).  Every work-group first loads the images of all T tokens (they reach LDS while
+// the routing runs).  The shared expert's work-groups (item 0 with a shared expert) start the expert at once;
+// every other work-group routes the batch itself (ids only, one wave per token) and takes as its item the
+// (y - n_sh)-th touched expert in ascending order, with its pairs in ascending pair order -- the item
+// dispatch_block writes there.  The last row of work-groups (y = max_items) only routes, dispatches and writes
+// the routing, the dispatch and the work-item table for the kernels after it.
+struct GuRouteLds {
+    int ids[kSmallPairs];
+    int lt[kSmallPairs];     // pairs with a smaller expert id
+    int first[kSmallPairs];  // 1 for the first pair of its expert
+    int item[8];             // e (-1: none), first, ncol, tk[0..3]
+};
 template <int NIT, int MAXUPL>
 __global__ __launch_bounds__(256) void k_q2_gu_route(
     const uint8_t* __restrict__ gate_exps, const uint8_t* __restrict__ up_exps, const uint8_t* __restrict__ gate_sh,
@@ -973,12 +996,33 @@ __global__ __launch_bounds__(256) void k_q2_gu_route(
     int32_t* __restrict__ counts, int32_t* __restrict__ offsets, int32_t* __restrict__ perm,
     int32_t* __restrict__ slot, int32_t* __restrict__ elist, int32_t* __restrict__ n_list, int4* __restrict__ items,
     int max_items, uint32_t* __restrict__ himg, int h_blocks) {
+    typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
     extern __shared__ __align__(16) uint32_t smem[];
     const int n_sh = has_shared ? 1 : 0;
+    const int tid = threadIdx.x, wave = tid >> 6;
+    if ((int)blockIdx.y == max_items) {
+        if (blockIdx.x == 0)
+            small_route_dispatch(logits, T, E, k, true, ids, wts, counts, offsets, perm, slot, elist, n_list, items,
+                                 max_items, has_shared, 1 << 30, kShCols, *reinterpret_cast<SmallDispatchLds*>(smem));
+        return;
+    }
+    const bool shared_wg = (int)blockIdx.y < n_sh;
+    if ((int)blockIdx.x * 32 >= (shared_wg ? Fs : F)) return;
+    const int qb = H >> 5;
+    const int pieces = T * qb * (kImgDw / 4);  // at most 4 * 128 * 3
+    u32x4 pre[6];
+#pragma unroll
+    for (int j = 0; j < 6; ++j)
+        if (j * 256 + tid < pieces) pre[j] = reinterpret_cast<const u32x4*>(ximg)[j * 256 + tid];
+    GuRouteLds& L = *reinterpret_cast<GuRouteLds*>(smem + kGuCols * qb * kImgDw + 4);
     const int P = T * k;
+    if (!shared_wg && wave < T) route_token_ids(logits + (size_t)wave * E, E, k, L.ids + wave * k);
+#pragma unroll
+    for (int j = 0; j < 6; ++j)
+        if (j * 256 + tid < pieces) reinterpret_cast<u32x4*>(smem)[j * 256 + tid] = pre[j];
+    __syncthreads();
     Item item;
-    if ((int)blockIdx.y < n_sh) {
-        if ((int)blockIdx.x * 32 >= Fs) return;
+    if (shared_wg) {
         item.shared = true;
         item.e = kItemShared;
         item.first = P;
@@ -986,25 +1030,81 @@ __global__ __launch_bounds__(256) void k_q2_gu_route(
         item.tok0 = 0;
 #pragma unroll
         for (int c = 0; c < 4; ++c) item.tk[c] = c;
-    } else {
-        if ((int)blockIdx.x * 32 >= F) return;
-        SmallDispatchLds& s = *reinterpret_cast<SmallDispatchLds*>(smem);
-        const bool writer = blockIdx.x == 0 && (int)blockIdx.y == n_sh;
-        small_route_dispatch(logits, T, E, k, writer, ids, wts, counts, offsets, perm, slot, elist, n_list, items,
-                             max_items, has_shared, 1 << 30, kShCols, s);
-        const int y = (int)blockIdx.y - n_sh;
-        if (y >= s.n_touched) return;  // uniform: no expert for this item
-        const int e = s.el[y];
+    } else if (P <= 64) {
+        // every wave on its own, lane p holding pair p: counts by broadcasting each pair's id (no LDS loop)
+        const int lane = tid & 63;
+        const int id = lane < P ? L.ids[lane] : 0x7FFFFFFF;
+        int lt = 0, cnt = 0, fst = 1;
+        for (int q = 0; q < P; ++q) {
+            const int o = __builtin_amdgcn_readlane(id, q);
+            lt += o < id ? 1 : 0;
+            cnt += o == id ? 1 : 0;
+            fst = (q < lane && o == id) ? 0 : fst;
+        }
+        const unsigned long long firsts = __ballot(lane < P && fst);
+        int rank = 0;  // touched experts below id
+        for (unsigned long long m = firsts; m; m &= m - 1) {
+            const int q = __builtin_ctzll(m);
+            rank += __builtin_amdgcn_readlane(id, q) < id ? 1 : 0;
+        }
+        const unsigned long long own = __ballot(lane < P && fst && rank == (int)blockIdx.y - n_sh);
+        if (own == 0ull) return;  // uniform: no expert for this item
+        const int ol = __builtin_ctzll(own);
         item.shared = false;
-        item.e = e;
-        item.first = s.off[e];
-        item.ncol = s.cnt[e];  // at most T <= 4: a token picks an expert once
+        item.e = __builtin_amdgcn_readlane(id, ol);
+        item.first = __builtin_amdgcn_readlane(lt, ol);
+        item.ncol = __builtin_amdgcn_readlane(cnt, ol);  // at most T <= 4: a token picks an expert once
+        unsigned long long pm = __ballot(lane < P && id == item.e);  // its pairs, ascending
 #pragma unroll
-        for (int c = 0; c < 4; ++c) item.tk[c] = c < item.ncol ? s.perm[item.first + c] / k : 0;
+        for (int c = 0; c < 4; ++c) {
+            item.tk[c] = pm ? __builtin_ctzll(pm) / k : 0;
+            pm &= pm - 1;
+        }
         item.tok0 = item.tk[0];
-        __syncthreads();  // every thread has read s before the staging reuses the space
+    } else {
+        const int id = tid < P ? L.ids[tid] : 0;
+        if (tid < P) {
+            int lt = 0, fst = 1;
+            for (int q = 0; q < P; ++q) {
+                const int o = L.ids[q];
+                lt += o < id ? 1 : 0;
+                fst = (q < tid && o == id) ? 0 : fst;
+            }
+            L.lt[tid] = lt;
+            L.first[tid] = fst;
+        }
+        if (tid == 0) L.item[0] = -1;
+        __syncthreads();
+        const int y = (int)blockIdx.y - n_sh;
+        if (tid < P && L.first[tid]) {
+            int rank = 0;  // touched experts below id
+            for (int q = 0; q < P; ++q) rank += (L.first[q] && L.ids[q] < id) ? 1 : 0;
+            if (rank == y) {
+                int n = 0, tk[4] = {0, 0, 0, 0};
+                for (int q = 0; q < P; ++q) {
+                    if (L.ids[q] == id) {
+                        if (n < 4) tk[n] = q / k;
+                        ++n;
+                    }
+                }
+                L.item[0] = id;
+                L.item[1] = L.lt[tid];
+                L.item[2] = n;
+#pragma unroll
+                for (int c = 0; c < 4; ++c) L.item[3 + c] = tk[c];
+            }
+        }
+        __syncthreads();
+        if (L.item[0] < 0) return;  // uniform: no expert for this item
+        item.shared = false;
+        item.e = L.item[0];
+        item.first = L.item[1];
+        item.ncol = L.item[2];  // at most T <= 4: a token picks an expert once
+#pragma unroll
+        for (int c = 0; c < 4; ++c) item.tk[c] = L.item[3 + c];
+        item.tok0 = item.tk[0];
     }
-    q2_gu_item<NIT, MAXUPL>(item, smem, gate_exps, up_exps, gate_sh, up_sh, ximg, perm, k, H, F, himg, h_blocks);
+    q2_gu_item<NIT, MAXUPL, true>(item, smem, gate_exps, up_exps, gate_sh, up_sh, ximg, perm, k, H, F, himg, h_blocks);
 }
 
 // Down rows.  Grid (ceil(H / rows per block), max work items), 4 waves; a wave owns NIT passes of rpi rows.
@@ -1551,10 +1651,10 @@ hipError_t launch_q2_gu_route(const uint8_t* gate_exps, const uint8_t* up_exps, 
                               int4* items, int max_items, uint32_t* himg, int h_blocks, hipStream_t s) {
     if (T < 1 || T > kShCols || T * k > kSmallPairs || E > 1024) return hipErrorInvalidValue;
     const int Fmax = has_shared && Fs > F ? Fs : F;
-    dim3 grid((unsigned)(Fmax / 32), (unsigned)max_items);
+    dim3 grid((unsigned)(Fmax / 32), (unsigned)max_items + 1);  // + the writer row
     int nit, upl;
     gu_shape(H, nit, upl);
-    size_t lds = (size_t)kGuCols * (H >> 5) * kImgDw * 4 + 16;
+    size_t lds = (size_t)kGuCols * (H >> 5) * kImgDw * 4 + 16 + sizeof(GuRouteLds);
     if (lds < sizeof(SmallDispatchLds)) lds = sizeof(SmallDispatchLds);
 #define SMOE_GUR(N, U)                                                                                             \
     hipLaunchKernelGGL((k_q2_gu_route<N, U>), grid, dim3(256), lds, s, gate_exps, up_exps, gate_sh, up_sh, ximg,   \
