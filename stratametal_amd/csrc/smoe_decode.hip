@@ -1010,10 +1010,13 @@ __global__ __launch_bounds__(256) void k_q2_gu_route(
     if ((int)blockIdx.x * 32 >= (shared_wg ? Fs : F)) return;
     const int qb = H >> 5;
     const int pieces = T * qb * (kImgDw / 4);  // at most 4 * 128 * 3
+    const int npre = (pieces + 255) >> 8;      // uniform
+    // unconditional loads (clamped index; a branch around a load makes the compiler wait for it), so that the
+    // logits loads below go out behind them without waiting
     u32x4 pre[6];
 #pragma unroll
     for (int j = 0; j < 6; ++j)
-        if (j * 256 + tid < pieces) pre[j] = reinterpret_cast<const u32x4*>(ximg)[j * 256 + tid];
+        pre[j] = reinterpret_cast<const u32x4*>(ximg)[min(min(j, npre - 1) * 256 + tid, pieces - 1)];
     GuRouteLds& L = *reinterpret_cast<GuRouteLds*>(smem + kGuCols * qb * kImgDw + 4);
     const int P = T * k;
     if (!shared_wg && wave < T) route_token_ids(logits + (size_t)wave * E, E, k, L.ids + wave * k);
@@ -1205,6 +1208,7 @@ __global__ __launch_bounds__(256) void k_q2_down(const uint8_t* __restrict__ dow
 // then y[t][row] as k_combine forms it: w0 * Y[slot0], fma in selection order, + the shared row.
 constexpr int kDcRows = 16;
 constexpr size_t kDownCombineLds = 96 * 1024;  // images + rows of the batch
+constexpr int kDcItems = 384;                  // work items whose table entries fit in LDS
 template <int MAXUPL, int NT>
 __global__ __launch_bounds__(256) void k_q2_down_combine(
     const uint8_t* __restrict__ down_exps, const uint8_t* __restrict__ down_sh, const uint32_t* __restrict__ himg,
@@ -1215,21 +1219,38 @@ __global__ __launch_bounds__(256) void k_q2_down_combine(
     extern __shared__ __align__(16) uint32_t smem[];
     __shared__ int s_slot[kSmallPairs];
     __shared__ float s_wts[kSmallPairs];
+    __shared__ int4 s_items[2 * kDcItems];
     const int P = T * k, rows = P + T;
     const int pieces = rows * h_blocks * (kImgDw / 4);  // 16-byte pieces of the images
     float* Ys = reinterpret_cast<float*>(smem + (size_t)pieces * 4);  // [rows][kDcRows]
     const int r0 = blockIdx.x * kDcRows;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int n_tasks = n_items * npass;
 
-    // the images' first 1024 pieces, the routing slots and weights: loads issued before the weight loads, so that
-    // their LDS stores wait for them alone
+    // the first 1024 image pieces, the item table, the routing slots and weights: unconditional loads (clamped
+    // indices), all in flight together, then one barrier before any weight load
     u32x4 pre[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) pre[j] = reinterpret_cast<const u32x4*>(himg)[min(j * 256 + tid, pieces - 1)];
+    int4 itv[3];
+#pragma unroll
+    for (int j = 0; j < 3; ++j) itv[j] = items[min(j * 256 + tid, 2 * n_items - 1)];
     const int sl = slot[min(tid, P - 1)];
     const float wt = wts[min(tid, P - 1)];
-    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        if (j * 256 + tid < pieces) reinterpret_cast<u32x4*>(smem)[j * 256 + tid] = pre[j];
+#pragma unroll
+    for (int j = 0; j < 3; ++j)
+        if (j * 256 + tid < 2 * n_items) s_items[j * 256 + tid] = itv[j];
+    if (tid < P) {
+        s_slot[tid] = sl;
+        s_wts[tid] = wt;
+    }
+    for (int i = 1024 + tid; i < pieces; i += 256)
+        reinterpret_cast<u32x4*>(smem)[i] = reinterpret_cast<const u32x4*>(himg)[i];
+    __syncthreads();
 
     for (int tb = 0; tb < n_tasks; tb += 4 * NT) {
         Item it[NT];
@@ -1240,7 +1261,13 @@ __global__ __launch_bounds__(256) void k_q2_down_combine(
         for (int q = 0; q < NT; ++q) {
             const int j = tb + 4 * q + wave;  // wave-uniform task
             const int i = j < n_tasks ? j / npass : 0, p = j < n_tasks ? j - i * npass : 0;
-            live[q] = j < n_tasks && work_item(items, i, it[q]);
+            const int4 ia = s_items[2 * i];
+            live[q] = j < n_tasks && ia.x != kItemEmpty;
+            it[q].shared = ia.x == kItemShared;
+            it[q].e = ia.x;
+            it[q].first = ia.y;
+            it[q].ncol = ia.z;
+            it[q].tok0 = ia.w;
             const bool sh = live[q] && it[q].shared;
             const RowGeo G = row_geo(sh ? Fs : F);
             lpr[q] = G.lpr;
@@ -1254,19 +1281,6 @@ __global__ __launch_bounds__(256) void k_q2_down_combine(
 #pragma unroll
             for (int m = 0; m < MAXUPL; ++m)
                 load_unit(base + (size_t)r * rb + (size_t)(m < G.upl ? l + G.lpr * m : l) * 36, w[q][m]);
-        }
-        if (tb == 0) {
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                if (j * 256 + tid < pieces) reinterpret_cast<u32x4*>(smem)[j * 256 + tid] = pre[j];
-            for (int i = 1024 + tid; i < pieces; i += 256)
-                reinterpret_cast<u32x4*>(smem)[i] = reinterpret_cast<const u32x4*>(himg)[i];
-            if (tid < P) {
-                s_slot[tid] = sl;
-                s_wts[tid] = wt;
-            }
-            __syncthreads();
         }
         float dw[NT][MAXUPL][2];
         unit_scales(w, dw);
@@ -1673,6 +1687,7 @@ size_t down_combine_lds(int T, int k, int h_blocks) {
 bool down_combine_ok(int T, int k, int h_blocks) {
     return T >= 1 && T <= kShCols && T * k <= kSmallPairs && down_combine_lds(T, k, h_blocks) <= kDownCombineLds;
 }
+static_assert(kSmallPairs + kShCols <= kDcItems && 2 * kDcItems <= 3 * 256, "the item table of a small batch in LDS");
 
 hipError_t launch_q2_down_combine(const uint8_t* down_exps, const uint8_t* down_sh, const uint32_t* himg, int h_blocks,
                                   const float* sg, const int4* items, int n_items, int H, int F, int Fs,
