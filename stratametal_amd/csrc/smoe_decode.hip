@@ -969,8 +969,10 @@ __global__ __launch_bounds__(256) void k_q2_gu(const uint8_t* __restrict__ gate_
                                                 const int32_t* __restrict__ perm, int k, int H, int F, int Fs,
                                                 uint32_t* __restrict__ himg, int h_blocks) {
     extern __shared__ __align__(16) uint32_t smem[];
+    asm volatile("" ::"s"(gate_exps), "s"(up_exps), "s"(gate_sh), "s"(up_sh), "s"(ximg), "s"(himg), "s"(perm), "s"(k),
+                 "s"(H), "s"(F), "s"(Fs), "s"(h_blocks));  // every kernarg loaded before the item
     Item item;
-    if (!work_item(items, blockIdx.y, item)) return;
+    if (!work_item_uniform(items, blockIdx.y, item)) return;
     if ((int)blockIdx.x * 32 >= (item.shared ? Fs : F)) return;
     q2_gu_item<NIT, MAXUPL>(item, smem, gate_exps, up_exps, gate_sh, up_sh, ximg, perm, k, H, F, himg, h_blocks);
 }
@@ -1119,8 +1121,10 @@ __global__ __launch_bounds__(256) void k_q2_down(const uint8_t* __restrict__ dow
                                                   const int4* __restrict__ items, int H, int F, int Fs, int cps,
                                                   float* __restrict__ Y) {
     extern __shared__ __align__(16) uint32_t smem[];
+    asm volatile("" ::"s"(down_exps), "s"(down_sh), "s"(himg), "s"(sg), "s"(Y), "s"(h_blocks), "s"(H), "s"(F),
+                 "s"(Fs), "s"(cps));  // every kernarg loaded before the item
     Item item;
-    if (!work_item(items, blockIdx.y, item)) return;
+    if (!work_item_uniform(items, blockIdx.y, item)) return;
     const int Fe = item.shared ? Fs : F;
     const RowGeo G = row_geo(Fe);
     const int rpw = NIT * G.rpi;  // rows per wave

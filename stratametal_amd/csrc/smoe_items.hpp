@@ -35,6 +35,26 @@ __device__ __forceinline__ bool work_item(const int4* __restrict__ items, int wi
     return true;
 }
 
+// work_item for a work-group-uniform wi: the whole 32-byte entry in one scalar load, all of it in SGPRs before the
+// test (so that the compiler does not split the load around the branch and wait twice).
+__device__ __forceinline__ bool work_item_uniform(const int4* __restrict__ items, int wi, Item& it) {
+    typedef int v8i __attribute__((ext_vector_type(8)));
+    v8i v = *reinterpret_cast<const v8i*>(items + 2 * wi);
+    asm volatile("" : "+s"(v));
+    const int4 a = make_int4(v[0], v[1], v[2], v[3]), b = make_int4(v[4], v[5], v[6], v[7]);
+    if (a.x == kItemEmpty) return false;
+    it.shared = a.x == kItemShared;
+    it.e = a.x;
+    it.first = a.y;
+    it.ncol = a.z;
+    it.tok0 = a.w;
+    it.tk[0] = a.w;
+    it.tk[1] = b.x;
+    it.tk[2] = b.y;
+    it.tk[3] = b.z;
+    return true;
+}
+
 // The token of a routed item's column c < 4, by selects (no branch, no memory read).
 __device__ __forceinline__ int item_token_head(const Item& it, int c) {
     return c == 0 ? it.tk[0] : c == 1 ? it.tk[1] : c == 2 ? it.tk[2] : it.tk[3];
