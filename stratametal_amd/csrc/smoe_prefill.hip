@@ -103,10 +103,13 @@ __device__ __forceinline__ void expand_codes(uint32_t cw, uint32_t dbits, f16x8&
 // it makes everyone's visible.  Columns past the item and pad pieces read at an offset beyond the buffer
 // (range-checked: no memory access, zeros written), so a short item moves only its own activation bytes.
 //
-// Two work-group shapes share one LDS ring (the item's column count picks one):
+// Three work-group shapes share one LDS ring (the item's column count picks one):
 //   wide (65..128 columns): 3 stages of 128 columns; wave w owns rows of row group w % 4 (four 16-row sets) and
 //                           columns 64 (w / 4) .. + 63;
-//   narrow (<= 64 columns): 5 stages of 64 columns; wave w owns the rows of row group w (two sets) and every column.
+//   narrow (17..64 columns): 5 stages of 64 columns; wave w owns the rows of row group w (two sets) and every
+//                           column;
+//   thin (<= 16 columns):   8 stages of 16 columns (more weight stages in flight for the streaming work-groups),
+//                           rows as narrow.
 constexpr int kTokPieces = 17;
 constexpr int kWgRows = 256;
 constexpr int kWPieces = kWgRows * 3;
@@ -117,12 +120,15 @@ constexpr int kRing = 148480;           // bytes of the stage ring
 constexpr int kDummy = kRing;           // 1 KB landing slot of the padding instructions
 constexpr int kLds = kRing + 1024;
 
-template <bool WIDE>
+// MODE 0 (thin, <= 16 columns): 8 stages of 16 columns, rows as narrow.
+enum { kThin = 0, kNarrow = 1, kWide = 2 };
+template <int MODE>
 struct Shape {
-    static constexpr int kTok = WIDE ? 128 : 64;
-    static constexpr int kStages = WIDE ? 3 : 5;
+    static constexpr bool WIDE = MODE == kWide;
+    static constexpr int kTok = MODE == kWide ? 128 : MODE == kNarrow ? 64 : 16;
+    static constexpr int kStages = MODE == kWide ? 3 : MODE == kNarrow ? 5 : 8;
     static constexpr int NS = WIDE ? 4 : 2;
-    static constexpr int kAPieces = kTok * kTokPieces;
+    static constexpr int kAPieces = (kTok * kTokPieces + 63) / 64 * 64;  // whole DMA instructions
     static constexpr int kAIns = kAPieces / 64;
     static constexpr int kASlots = (kAIns + kWaves - 1) / kWaves;
     static constexpr int kWSlots = (kWIns + kWaves - 1) / kWaves;
@@ -132,6 +138,7 @@ struct Shape {
     static_assert(kAPieces % 64 == 0 && kWPieces % 64 == 0, "whole DMA instructions");
     static_assert(kStages * kStage <= kRing, "ring");
     static_assert((kStages - 2) * kSlots <= 63, "vmcnt range");
+    static_assert(kStages - 2 <= 6, "wait_stages cases");
 };
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
@@ -160,15 +167,18 @@ __device__ __forceinline__ void wait_stages(int after) {
         case 0: vmcnt<0>(); break;
         case 1: vmcnt<SLOTS>(); break;
         case 2: vmcnt<2 * SLOTS>(); break;
-        default: vmcnt<3 * SLOTS>(); break;
+        case 3: vmcnt<3 * SLOTS>(); break;
+        case 4: vmcnt<4 * SLOTS>(); break;
+        case 5: vmcnt<5 * SLOTS>(); break;
+        default: vmcnt<6 * SLOTS>(); break;
     }
 }
 
 // One wave's DMA plan: per slot the byte offset within a stage (uniform; -1 for the dummy) and the lane's
 // buffer offset at unit 0.
-template <bool WIDE>
+template <int MODE>
 struct MmPlan {
-    using S = Shape<WIDE>;
+    using S = Shape<MODE>;
     uint32_t a_off[S::kASlots], w_off[S::kWSlots];
     int a_at[S::kASlots], w_at[S::kWSlots];
     int w_up[S::kWSlots];  // the slot's rows are the second tensor's (up rows)
@@ -252,11 +262,11 @@ __device__ __forceinline__ void mm_unit(f32x4 (&acc)[4][NS], const uint32_t* W, 
 
 // The K loop of both kernels: units of 128 values through the ring, kStages - 1 units in flight.  NT: the
 // wave's live column tiles.
-template <bool WIDE, int NT>
-__device__ __forceinline__ void mm_loop_nt(f32x4 (&acc)[4][Shape<WIDE>::NS], uint8_t* lds, const MmPlan<WIDE>& pl,
+template <int MODE, int NT>
+__device__ __forceinline__ void mm_loop_nt(f32x4 (&acc)[4][Shape<MODE>::NS], uint8_t* lds, const MmPlan<MODE>& pl,
                                            int units, i32x4 ra, i32x4 rw0, i32x4 rw1,
-                                           const int (&rows)[Shape<WIDE>::NS], int tok0, int i, int q) {
-    using S = Shape<WIDE>;
+                                           const int (&rows)[Shape<MODE>::NS], int tok0, int i, int q) {
+    using S = Shape<MODE>;
     constexpr int ST = S::kStages;
     const uint32_t lds0 = lds_addr(lds);
 #pragma unroll
@@ -274,19 +284,23 @@ __device__ __forceinline__ void mm_loop_nt(f32x4 (&acc)[4][Shape<WIDE>::NS], uin
     }
 }
 
-template <bool WIDE>
-__device__ __forceinline__ void mm_loop(f32x4 (&acc)[4][Shape<WIDE>::NS], uint8_t* lds, const MmPlan<WIDE>& pl,
+template <int MODE>
+__device__ __forceinline__ void mm_loop(f32x4 (&acc)[4][Shape<MODE>::NS], uint8_t* lds, const MmPlan<MODE>& pl,
                                         int units, i32x4 ra, i32x4 rw0, i32x4 rw1,
-                                        const int (&rows)[Shape<WIDE>::NS], int tok0, int ntiles, int i, int q) {
+                                        const int (&rows)[Shape<MODE>::NS], int tok0, int ntiles, int i, int q) {
 #pragma unroll
     for (int n = 0; n < 4; ++n)
 #pragma unroll
-        for (int s = 0; s < Shape<WIDE>::NS; ++s) acc[n][s] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int s = 0; s < Shape<MODE>::NS; ++s) acc[n][s] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    if constexpr (MODE == kThin) {  // one tile
+        mm_loop_nt<MODE, 1>(acc, lds, pl, units, ra, rw0, rw1, rows, tok0, i, q);
+        return;
+    }
     switch (ntiles) {  // wave-uniform; every wave has 1 .. 4 live tiles
-        case 1: mm_loop_nt<WIDE, 1>(acc, lds, pl, units, ra, rw0, rw1, rows, tok0, i, q); break;
-        case 2: mm_loop_nt<WIDE, 2>(acc, lds, pl, units, ra, rw0, rw1, rows, tok0, i, q); break;
-        case 3: mm_loop_nt<WIDE, 3>(acc, lds, pl, units, ra, rw0, rw1, rows, tok0, i, q); break;
-        default: mm_loop_nt<WIDE, 4>(acc, lds, pl, units, ra, rw0, rw1, rows, tok0, i, q); break;
+        case 1: mm_loop_nt<MODE, 1>(acc, lds, pl, units, ra, rw0, rw1, rows, tok0, i, q); break;
+        case 2: mm_loop_nt<MODE, 2>(acc, lds, pl, units, ra, rw0, rw1, rows, tok0, i, q); break;
+        case 3: mm_loop_nt<MODE, 3>(acc, lds, pl, units, ra, rw0, rw1, rows, tok0, i, q); break;
+        default: mm_loop_nt<MODE, 4>(acc, lds, pl, units, ra, rw0, rw1, rows, tok0, i, q); break;
     }
 }
 
@@ -295,18 +309,26 @@ __device__ __forceinline__ void mm_loop(f32x4 (&acc)[4][Shape<WIDE>::NS], uint8_
 // item's (at most 128) columns, then h = bf16(silu(gate) * up) into records 2 rt and 2 rt + 1 of each column's h
 // row.  Wide: wave w has gate rows 32 (w % 4) .. + 31 (sets 0, 1) and the same up rows (sets 2, 3); narrow: gate
 // rows 16 w .. + 15 (set 0) and the same up rows (set 1).
-template <bool WIDE>
+// SwiGLU of the prefill contract: silu(g) * u with the hardware exp2 and reciprocal (a few ulp).  h is rounded to
+// bf16 next and the contract is held to 1e-3 per row; the decode contract keeps silu_mul's exact order.
+__device__ __forceinline__ float silu_mul_fast(float g, float u) {
+    const float e = __builtin_amdgcn_exp2f(g * -1.44269504088896341f);
+    return (g * __builtin_amdgcn_rcpf(1.0f + e)) * u;
+}
+
+template <int MODE>
 __device__ __forceinline__ void mm_gu_body(uint8_t* lds, const int* rowidx, const Item& item, int ncol,
                                            const uint8_t* g0, const uint8_t* u0, const uint32_t* xrec,
                                            uint32_t xrec_bytes, int H, uint32_t* hrec, int h_rec) {
-    using S = Shape<WIDE>;
+    using S = Shape<MODE>;
+    constexpr bool WIDE = S::WIDE;
     constexpr int NS = S::NS;
     const int rt = blockIdx.x;
     const int units = H >> 7;
     const uint32_t rb = (uint32_t)units * 36u;
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, i = lane & 15,
               q = lane >> 4;
-    MmPlan<WIDE> pl;
+    MmPlan<MODE> pl;
     pl.init(rowidx, wave, lane, ncol, H >> 6, rb, 128);
     const i32x4 ra = buffer_rsrc(xrec, xrec_bytes);
     const i32x4 rg0 = buffer_rsrc(g0 + (size_t)128 * rt * rb, 128u * rb);
@@ -327,7 +349,7 @@ __device__ __forceinline__ void mm_gu_body(uint8_t* lds, const int* rowidx, cons
     const int tok0 = WIDE ? 64 * (wave >> 2) : 0;
     const int ntiles = min(4, max(0, (ncol - tok0 + 15) >> 4));
     f32x4 acc[4][NS];
-    mm_loop<WIDE>(acc, lds, pl, units, ra, rg0, ru0, rows, tok0, ntiles, i, q);
+    mm_loop<MODE>(acc, lds, pl, units, ra, rg0, ru0, rows, tok0, ntiles, i, q);
     __syncthreads();  // every wave is done with the ring: its start becomes the h tile
     // h tile [column][128 rows in record order] as fp16 bits of bf16 values
     uint16_t* ht = reinterpret_cast<uint16_t*>(lds);
@@ -341,7 +363,7 @@ __device__ __forceinline__ void mm_gu_body(uint8_t* lds, const int* rowidx, cons
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const int c = tok0 + 16 * n + 4 * q + r;
-                    if (c < ncol) ht[c * 128 + pos] = (uint16_t)bf16_as_f16(silu_mul(acc[n][s][r], acc[n][s + NS / 2][r]));
+                    if (c < ncol) ht[c * 128 + pos] = (uint16_t)bf16_as_f16(silu_mul_fast(acc[n][s][r], acc[n][s + NS / 2][r]));
                 }
             }
         }
@@ -371,25 +393,27 @@ __global__ __launch_bounds__(512) void k_mm_gu(const uint8_t* __restrict__ gate_
     const size_t rb = (size_t)(H >> 7) * 36;
     const uint8_t* g0 = item.shared ? gate_sh : gate_exps + (size_t)item.e * F * rb;
     const uint8_t* u0 = item.shared ? up_sh : up_exps + (size_t)item.e * F * rb;
-    if (ncol > 64) mm_gu_body<true>(lds, rowidx, item, ncol, g0, u0, xrec, xrec_bytes, H, hrec, h_rec);
-    else mm_gu_body<false>(lds, rowidx, item, ncol, g0, u0, xrec, xrec_bytes, H, hrec, h_rec);
+    if (ncol > 64) mm_gu_body<kWide>(lds, rowidx, item, ncol, g0, u0, xrec, xrec_bytes, H, hrec, h_rec);
+    else if (ncol > 16) mm_gu_body<kNarrow>(lds, rowidx, item, ncol, g0, u0, xrec, xrec_bytes, H, hrec, h_rec);
+    else mm_gu_body<kThin>(lds, rowidx, item, ncol, g0, u0, xrec, xrec_bytes, H, hrec, h_rec);
 }
 
 // ------------------------------------------------------------------------------------------------ down
 // Grid (H / 256, work items), 8 waves.  Work-group rt computes down rows [256 rt, 256 rt + 256) of the item's
 // columns into Y[first + c] (the shared expert's rows times sigmoid(sg[t])).  Wide: wave w has rows
 // 64 (w % 4) .. + 63 (four sets); narrow: rows 32 w .. + 31 (two sets).
-template <bool WIDE>
+template <int MODE>
 __device__ __forceinline__ void mm_down_body(uint8_t* lds, const int* rowidx, const Item& item, int ncol, int units,
                                              const uint8_t* d0, const uint32_t* hrec, uint32_t hrec_bytes, int h_rec,
                                              const float* sg, int H, float* Y) {
-    using S = Shape<WIDE>;
+    using S = Shape<MODE>;
+    constexpr bool WIDE = S::WIDE;
     constexpr int NS = S::NS;
     const int rt = blockIdx.x;
     const uint32_t rb = (uint32_t)units * 36u;
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, i = lane & 15,
               q = lane >> 4;
-    MmPlan<WIDE> pl;
+    MmPlan<MODE> pl;
     pl.init(rowidx, wave, lane, ncol, h_rec, rb, kWgRows);
     const int nrows = min(kWgRows, H - kWgRows * rt);
     const i32x4 ra = buffer_rsrc(hrec, hrec_bytes);
@@ -401,7 +425,7 @@ __device__ __forceinline__ void mm_down_body(uint8_t* lds, const int* rowidx, co
     const int tok0 = WIDE ? 64 * (wave >> 2) : 0;
     const int ntiles = min(4, max(0, (ncol - tok0 + 15) >> 4));
     f32x4 acc[4][NS];
-    mm_loop<WIDE>(acc, lds, pl, units, ra, rd, rd, rows, tok0, ntiles, i, q);
+    mm_loop<MODE>(acc, lds, pl, units, ra, rd, rd, rows, tok0, ntiles, i, q);
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
         const int row = kWgRows * rt + rows[s];
@@ -438,8 +462,9 @@ __global__ __launch_bounds__(512) void k_mm_down(const uint8_t* __restrict__ dow
     __syncthreads();
     const int units = Fe >> 7;
     const uint8_t* d0 = item.shared ? down_sh : down_exps + (size_t)item.e * H * ((size_t)(F >> 7) * 36);
-    if (ncol > 64) mm_down_body<true>(lds, rowidx, item, ncol, units, d0, hrec, hrec_bytes, h_rec, sg, H, Y);
-    else mm_down_body<false>(lds, rowidx, item, ncol, units, d0, hrec, hrec_bytes, h_rec, sg, H, Y);
+    if (ncol > 64) mm_down_body<kWide>(lds, rowidx, item, ncol, units, d0, hrec, hrec_bytes, h_rec, sg, H, Y);
+    else if (ncol > 16) mm_down_body<kNarrow>(lds, rowidx, item, ncol, units, d0, hrec, hrec_bytes, h_rec, sg, H, Y);
+    else mm_down_body<kThin>(lds, rowidx, item, ncol, units, d0, hrec, hrec_bytes, h_rec, sg, H, Y);
 }
 
 // ------------------------------------------------------------------------------------------------ launchers
