@@ -862,57 +862,69 @@ constexpr int kGuCols = 8;
 // [32 hb + 8 w, +8) (rows rho 0..7) and the same up rows (rho 8..15); the item's columns are processed in
 // stages of kGuCols: their x images are copied to LDS, every column's row values parked in LDS by the group
 // leaders, then each half wave quantises one column's 32 h values into image block hb.
-// The work-group's item: `smem` is the kernel's dynamic LDS (the image staging area).  PRESTAGED: the images of
-// every token are already in LDS, token t in column slot t (batches of at most 4 tokens).
-template <int NIT, int MAXUPL, bool PRESTAGED = false>
-__device__ __forceinline__ void q2_gu_item(const Item& item, uint32_t* smem, const uint8_t* __restrict__ gate_exps,
-                                           const uint8_t* __restrict__ up_exps, const uint8_t* __restrict__ gate_sh,
-                                           const uint8_t* __restrict__ up_sh, const uint32_t* __restrict__ ximg,
-                                           const int32_t* __restrict__ perm, int k, int H, int F,
-                                           uint32_t* __restrict__ himg, int h_blocks) {
-    __shared__ float rowv[kGuCols][64];
-    __shared__ uint8_t qsc[8][32];
-    const int hb = blockIdx.x;
+// Pieces of a gate/up work unit (work item `item`, rows 32 hb .. + 31 of gate and of up), shared by the one-shot
+// kernels and the pipelined one.  Weight units: every load unconditional (a dead slot reloads the row's first
+// unit), so that the loads in flight are counted exactly.
+template <int NIT, int MAXUPL>
+__device__ __forceinline__ void gu_load_weights(const Item& item, int hb, const uint8_t* __restrict__ gate_exps,
+                                                const uint8_t* __restrict__ up_exps, const uint8_t* __restrict__ gate_sh,
+                                                const uint8_t* __restrict__ up_sh, int H, int F,
+                                                uint32_t (&w)[NIT][MAXUPL][9]) {
     const RowGeo G = row_geo(H);
     const size_t rb = (size_t)G.dpr * 36;
     const uint8_t* g0 = item.shared ? gate_sh : gate_exps + (size_t)item.e * F * rb;
     const uint8_t* u0 = item.shared ? up_sh : up_exps + (size_t)item.e * F * rb;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int grp = lane / G.lpr, l = lane - grp * G.lpr;
-    const int qb = H >> 5;
-
-    // Weight units: every load unconditional (a dead slot reloads the row's first unit), so that the loads in
-    // flight are counted exactly.  The first column batch's image loads (L2) go out before them (HBM), so that
-    // storing the images to LDS waits for the image loads alone.
-    uint32_t w[NIT][MAXUPL][9];
-    auto load_weights = [&]() {
 #pragma unroll
-        for (int it = 0; it < NIT; ++it) {
-            const int rho = min(it * G.rpi + grp, 15);  // 0..15 within the wave (a dead pass repeats row 15)
-            const int r = 32 * hb + 8 * wave + (rho & 7);
-            const uint8_t* rowp = (rho < 8 ? g0 : u0) + (size_t)r * rb;
+    for (int it = 0; it < NIT; ++it) {
+        const int rho = min(it * G.rpi + grp, 15);  // 0..15 within the wave (a dead pass repeats row 15)
+        const int r = 32 * hb + 8 * wave + (rho & 7);
+        const uint8_t* rowp = (rho < 8 ? g0 : u0) + (size_t)r * rb;
 #pragma unroll
-            for (int m = 0; m < MAXUPL; ++m) load_unit(rowp + (size_t)(m < G.upl ? l + G.lpr * m : l) * 36, w[it][m]);
-        }
-    };
-    const int nc0 = min(kGuCols, item.ncol);
-    if constexpr (PRESTAGED) {
-        load_weights();
-    } else {
-        if (stage_direct(item, 0, nc0, true)) {
-            StagePieces sp;
-            stage_issue_direct(sp, ximg, qb, 0, nc0, kGuCols, 0, item, true);
-            __builtin_amdgcn_sched_barrier(0);
-            load_weights();
-            __builtin_amdgcn_sched_barrier(0);
-            stage_commit_direct(sp, smem);
-        } else {
-            load_weights();
-            stage_images(smem, ximg, qb, 0, nc0, kGuCols, item, perm, k, true, 0, 4 * 256);
-        }
-        stage_images(smem, ximg, qb, 0, nc0, kGuCols, item, perm, k, true, 4 * 256);  // rounds beyond the first
-        __syncthreads();
+        for (int m = 0; m < MAXUPL; ++m) load_unit(rowp + (size_t)(m < G.upl ? l + G.lpr * m : l) * 36, w[it][m]);
     }
+}
+
+// The unit's loads: the first column batch's image loads (L2) into registers when their rows need no memory read,
+// then the weight loads (HBM), so that committing the images waits for the image loads alone.  Returns whether
+// the images were issued (else gu_commit stages them itself).
+template <int NIT, int MAXUPL>
+__device__ __forceinline__ bool gu_issue(const Item& item, int hb, const uint8_t* __restrict__ gate_exps,
+                                         const uint8_t* __restrict__ up_exps, const uint8_t* __restrict__ gate_sh,
+                                         const uint8_t* __restrict__ up_sh, const uint32_t* __restrict__ ximg, int H,
+                                         int F, StagePieces& sp, uint32_t (&w)[NIT][MAXUPL][9]) {
+    const int nc0 = min(kGuCols, item.ncol);
+    const bool direct = stage_direct(item, 0, nc0, true);
+    if (direct) stage_issue_direct(sp, ximg, H >> 5, 0, nc0, kGuCols, 0, item, true);
+    __builtin_amdgcn_sched_barrier(0);
+    gu_load_weights<NIT, MAXUPL>(item, hb, gate_exps, up_exps, gate_sh, up_sh, H, F, w);
+    __builtin_amdgcn_sched_barrier(0);
+    return direct;
+}
+
+// The first column batch's images into `smem` (the caller synchronises after).
+__device__ __forceinline__ void gu_commit(const Item& item, bool direct, const StagePieces& sp, uint32_t* smem,
+                                          const uint32_t* __restrict__ ximg, const int32_t* __restrict__ perm, int k,
+                                          int H) {
+    const int qb = H >> 5, nc0 = min(kGuCols, item.ncol);
+    if (direct) stage_commit_direct(sp, smem);
+    else stage_images(smem, ximg, qb, 0, nc0, kGuCols, item, perm, k, true, 0, 4 * 256);
+    stage_images(smem, ximg, qb, 0, nc0, kGuCols, item, perm, k, true, 4 * 256);  // rounds beyond the first
+}
+
+// Dots of every column of the unit (the first batch already in `smem`, later batches staged here), SwiGLU, q8_1
+// image of h.  PRESTAGED: the images of every token are in LDS, token t in column slot t (batches of at most 4
+// tokens).
+template <int NIT, int MAXUPL, bool PRESTAGED>
+__device__ __forceinline__ void gu_compute(const Item& item, int hb, uint32_t* smem, uint32_t (&w)[NIT][MAXUPL][9],
+                                           const uint32_t* __restrict__ ximg, const int32_t* __restrict__ perm, int k,
+                                           int H, uint32_t* __restrict__ himg, int h_blocks, float (&rowv)[kGuCols][64],
+                                           uint8_t (&qsc)[8][32]) {
+    const RowGeo G = row_geo(H);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int grp = lane / G.lpr, l = lane - grp * G.lpr;
+    const int qb = H >> 5;
     float dw[NIT][MAXUPL][2];
     unit_scales(w, dw);
 
@@ -960,6 +972,29 @@ __device__ __forceinline__ void q2_gu_item(const Item& item, uint32_t* smem, con
         }
         if (c0 + kGuCols < item.ncol) __syncthreads();
     }
+}
+
+// The work-group's item, one unit (rows block blockIdx.x): `smem` is the kernel's dynamic LDS (the image staging
+// area).
+template <int NIT, int MAXUPL, bool PRESTAGED = false>
+__device__ __forceinline__ void q2_gu_item(const Item& item, uint32_t* smem, const uint8_t* __restrict__ gate_exps,
+                                           const uint8_t* __restrict__ up_exps, const uint8_t* __restrict__ gate_sh,
+                                           const uint8_t* __restrict__ up_sh, const uint32_t* __restrict__ ximg,
+                                           const int32_t* __restrict__ perm, int k, int H, int F,
+                                           uint32_t* __restrict__ himg, int h_blocks) {
+    __shared__ float rowv[kGuCols][64];
+    __shared__ uint8_t qsc[8][32];
+    const int hb = blockIdx.x;
+    uint32_t w[NIT][MAXUPL][9];
+    if constexpr (PRESTAGED) {
+        gu_load_weights<NIT, MAXUPL>(item, hb, gate_exps, up_exps, gate_sh, up_sh, H, F, w);
+    } else {
+        StagePieces sp;
+        const bool direct = gu_issue<NIT, MAXUPL>(item, hb, gate_exps, up_exps, gate_sh, up_sh, ximg, H, F, sp, w);
+        gu_commit(item, direct, sp, smem, ximg, perm, k, H);
+        __syncthreads();
+    }
+    gu_compute<NIT, MAXUPL, PRESTAGED>(item, hb, smem, w, ximg, perm, k, H, himg, h_blocks, rowv, qsc);
 }
 
 template <int NIT, int MAXUPL>
