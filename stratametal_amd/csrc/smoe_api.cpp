@@ -40,6 +40,9 @@ constexpr int kMaxK = 64;
 // Up to this many tokens top-k and dispatch run as one work-group (k_topk_dispatch: one wave per token, at most
 // one per SIMD); beyond it the tokens are routed by one work-group each (k_topk), then dispatched (k_dispatch).
 constexpr int kFusedRouteTokens = 4;
+// From this many pairs the dispatch runs as three launches over chunks of 1024 pairs (k_dispatch_hist,
+// k_dispatch_scan, k_dispatch_rank) instead of one work-group.
+constexpr int kDispatchMultiPairs = 2048;
 // SMOE_PATH_AUTO runs the MFMA (prefill) contract from this many tokens on.
 constexpr int kMfmaTokens = 128;
 
@@ -78,7 +81,7 @@ smoe_status check_geom(const smoe_geom* g) {
 }
 
 struct Layout {
-    size_t ximg, logits, sg, ids, wts, counts, offsets, perm, slot, elist, nlist, items, himg, Y, total;
+    size_t ximg, logits, sg, ids, wts, counts, offsets, perm, slot, elist, nlist, items, himg, Y, dwork, total;
     int h_blocks;  // q8_1 blocks per h row (GEMV path)
     int h_rec;     // 64-value records per h row (MFMA path)
 };
@@ -123,6 +126,7 @@ Layout layout(const smoe_geom& g, int64_t T) {
     L.items = take((size_t)most(max_items_gemv(g, T), max_items_mfma(g, T)) * 32);
     L.himg = take(most(smoe::img_bytes((P + T) * L.h_blocks), smoe::act_rec_bytes((P + T) * L.h_rec)));
     L.Y = take((size_t)(P + T) * H * 4);
+    L.dwork = take(smoe::dispatch_work_bytes(P, (int)E));  // chunk histograms of the many-pair dispatch
     L.total = o;
     return L;
 }
@@ -255,9 +259,15 @@ smoe_status smoe_forward_path(const smoe_geom* g, const smoe_weights* w, const f
                  "route");
     } else {
         SMOE_TRY(smoe::launch_topk(logits, E, T, E, K, ids, wts, st), "topk");
-        SMOE_TRY(smoe::launch_dispatch(ids, P, E, counts, offsets, perm, slot, elist, nlist, items, n_items, T, K,
-                                       has_sh ? 1 : 0, chunk, sh_chunk, st),
-                 "dispatch");
+        if (P > kDispatchMultiPairs)
+            SMOE_TRY(smoe::launch_dispatch_multi(ids, P, E, counts, offsets, perm, slot, elist, nlist, items, n_items,
+                                                 T, K, has_sh ? 1 : 0, chunk, sh_chunk,
+                                                 reinterpret_cast<int32_t*>(ws + L.dwork), st),
+                     "dispatch");
+        else
+            SMOE_TRY(smoe::launch_dispatch(ids, P, E, counts, offsets, perm, slot, elist, nlist, items, n_items, T, K,
+                                           has_sh ? 1 : 0, chunk, sh_chunk, st),
+                     "dispatch");
     }
     SMOE_MARK();
     const uint8_t* ge = static_cast<const uint8_t*>(w->gate_exps);

@@ -700,6 +700,138 @@ __global__ __launch_bounds__(1024) void k_dispatch(const int32_t* __restrict__ i
                    sh_chunk);
 }
 
+// ------------------------------------------------------------------------------------------------ dispatch (many pairs)
+// The same stable counting sort in three launches, for many pairs: chunk c holds pairs 1024 c .. 1024 c + 1023.
+//   k_dispatch_hist:  per chunk, the expert histogram (LDS atomics) -> hist[c][e];
+//   k_dispatch_scan:  one work-group: per expert the total, the offsets, the touched list and the work-item table
+//                     (dispatch_block's classes and order), then hist[c][e] <- the position of chunk c's first pair
+//                     of expert e (offset + the counts of the chunks before), and each expert's first full item and
+//                     remainder item;
+//   k_dispatch_rank:  per chunk, dispatch_block's rank pass from those positions: perm, slot, and the first four
+//                     tokens of every work item.
+// Within an expert the pairs stay in ascending pair order: chunks in order, and inside a chunk by ballot ranks.
+constexpr int kDispatchChunk = 1024;
+
+__global__ __launch_bounds__(1024) void k_dispatch_hist(const int32_t* __restrict__ ids, int P, int E,
+                                                         int32_t* __restrict__ hist) {
+    __shared__ int cnt[1024];
+    const int tid = threadIdx.x, c = blockIdx.x;
+    cnt[tid] = 0;
+    const int i = c * kDispatchChunk + tid;
+    const int e = i < P ? ids[i] : -1;
+    __syncthreads();
+    if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+    __syncthreads();
+    if (tid < E) hist[(size_t)c * E + tid] = cnt[tid];
+}
+
+__global__ __launch_bounds__(1024) void k_dispatch_scan(int32_t* __restrict__ hist, int n_chunks, int P, int E,
+                                                         int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
+                                                         int32_t* __restrict__ elist, int32_t* __restrict__ n_list,
+                                                         int4* __restrict__ items, int32_t* __restrict__ item_of,
+                                                         int max_items, int T, int has_shared, int chunk, int sh_chunk) {
+    __shared__ int scan[3 * 17];
+    const int tid = threadIdx.x;
+    int c = 0;
+    if (tid < E)
+        for (int ch = 0; ch < n_chunks; ++ch) c += hist[(size_t)ch * E + tid];
+    const int flag = c > 0 ? 1 : 0;
+    const int nfull = c / chunk, rem = c - nfull * chunk;
+    const int wide = rem > (chunk >> 1) ? 1 : 0, narrow = rem > 0 && !wide ? 1 : 0;
+    int sc[3], tot[3];
+    block_exclusive_scan3_1024({c, flag | (wide << 11) | (narrow << 22), nfull}, scan, sc, tot);
+    const int off = sc[0], fpos = sc[1] & 0x7FF, fbase = sc[2];
+    const int total = tot[0], n_touched = tot[1] & 0x7FF, n_full = tot[2];
+    const int n_wide = (tot[1] >> 11) & 0x7FF, n_rc = n_full + n_wide + ((tot[1] >> 22) & 0x7FF);
+    const int rbase = wide ? n_full + ((sc[1] >> 11) & 0x7FF) : n_full + n_wide + ((sc[1] >> 22) & 0x7FF);
+    const int n_sh = has_shared ? (T + sh_chunk - 1) / sh_chunk : 0;
+    if (tid < E) {
+        if (counts) counts[tid] = c;
+        offsets[tid] = off;
+        if (flag && elist) elist[fpos] = tid;
+        item_of[tid] = n_sh + fbase;      // the expert's first full item
+        item_of[E + tid] = n_sh + rbase;  // its remainder item
+        int run = off;
+        for (int ch = 0; ch < n_chunks; ++ch) {
+            const int h = hist[(size_t)ch * E + tid];
+            hist[(size_t)ch * E + tid] = run;
+            run += h;
+        }
+        if (c > 0 && items) {  // the tokens are filled in by k_dispatch_rank
+            for (int q = 0; q <= nfull; ++q) {
+                const int first = off + q * chunk, n = min(chunk, c - q * chunk);
+                if (n == 0) break;
+                const int wi = n_sh + (q < nfull ? fbase + q : rbase);
+                items[2 * wi] = make_int4(tid, first, n, 0);
+                items[2 * wi + 1] = make_int4(0, 0, 0, 0);
+            }
+        }
+    }
+    if (tid == 0) {
+        offsets[E] = total;
+        if (n_list) *n_list = n_touched;
+    }
+    if (!items) return;
+    for (int wi = tid; wi < max_items; wi += 1024) {
+        if (wi >= n_sh && wi < n_sh + n_rc) continue;  // a routed chunk
+        int4 a = make_int4(kItemEmpty, 0, 0, 0), b = make_int4(0, 0, 0, 0);
+        if (wi < n_sh) {
+            const int t0 = wi * sh_chunk;
+            a = make_int4(kItemShared, P + t0, min(sh_chunk, T - t0), t0);
+            b = make_int4(t0 + 1, t0 + 2, t0 + 3, 0);
+        }
+        items[2 * wi] = a;
+        items[2 * wi + 1] = b;
+    }
+}
+
+struct RankLds {
+    int run[1024];
+    uint8_t wcnt[16][1024];
+};
+__global__ __launch_bounds__(1024) void k_dispatch_rank(const int32_t* __restrict__ ids, int P, int E,
+                                                         const int32_t* __restrict__ base, const int32_t* __restrict__ counts,
+                                                         const int32_t* __restrict__ offsets,
+                                                         const int32_t* __restrict__ item_of, int32_t* __restrict__ perm,
+                                                         int32_t* __restrict__ slot, int4* __restrict__ items, int k,
+                                                         int chunk) {
+    __shared__ RankLds s;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, c = blockIdx.x;
+    const int i = c * kDispatchChunk + tid;
+    const int id = i < P ? ids[i] : -1;
+    s.run[tid] = tid < E ? base[(size_t)c * E + tid] : 0;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) reinterpret_cast<uint32_t*>(&s.wcnt[0][0])[w * 1024 + tid] = 0u;
+    const bool valid = id >= 0 && id < E;
+    const int key = valid ? id : 0;
+    if (i < P && !valid) slot[i] = -1;
+    __syncthreads();
+    // rank inside the wave by ballot match on the 10 id bits, then the counts of the earlier waves
+    unsigned long long m = __ballot(valid);
+#pragma unroll
+    for (int b = 0; b < 10; ++b) {
+        const bool bit = (key >> b) & 1;
+        const unsigned long long bal = __ballot(bit);
+        m &= bit ? bal : ~bal;
+    }
+    const unsigned long long lt = (1ull << lane) - 1ull;
+    const int rank_w = __popcll(m & lt);
+    if (valid && (m & lt) == 0ull) s.wcnt[wave][key] = (uint8_t)__popcll(m);
+    __syncthreads();
+    if (!valid) return;
+    int pos = s.run[key] + rank_w;
+    for (int w = 0; w < wave; ++w) pos += s.wcnt[w][key];
+    perm[pos] = i;
+    slot[i] = pos;
+    if (!items) return;
+    const int j = pos - offsets[key];  // position inside the expert
+    const int q = j / chunk, jj = j - q * chunk;
+    if (jj < 4) {  // one of the first four pairs of its work item: the item's token field
+        const int wi = q < counts[key] / chunk ? item_of[key] + q : item_of[E + key];
+        reinterpret_cast<int32_t*>(items)[8 * wi + 3 + jj] = i / k;
+    }
+}
+
 // ------------------------------------------------------------------------------------------------ route (fused)
 // The decode call's middle for up to 4 tokens, one work-group of 256 threads: wave t routes token t
 // (route_token, its ids also into LDS), then the dispatch of the T * k <= 256 pairs with the results of
@@ -1633,6 +1765,26 @@ hipError_t launch_dispatch(const int32_t* ids, int P, int E, int32_t* counts, in
                            int has_shared, int chunk, int sh_chunk, hipStream_t s) {
     hipLaunchKernelGGL(k_dispatch, dim3(1), dim3(1024), 0, s, ids, P, E, counts, offsets, perm, slot, elist, n_list,
                        items, max_items, T, k, has_shared, chunk, sh_chunk);
+    return hipGetLastError();
+}
+
+size_t dispatch_work_bytes(int64_t P, int E) {
+    const int64_t chunks = (P + kDispatchChunk - 1) / kDispatchChunk;
+    return (size_t)(chunks * E + 2 * (int64_t)E) * 4;
+}
+
+hipError_t launch_dispatch_multi(const int32_t* ids, int P, int E, int32_t* counts, int32_t* offsets, int32_t* perm,
+                                 int32_t* slot, int32_t* elist, int32_t* n_list, int4* items, int max_items, int T,
+                                 int k, int has_shared, int chunk, int sh_chunk, int32_t* work, hipStream_t s) {
+    if (!counts) return hipErrorInvalidValue;  // the rank pass reads them
+    const int chunks = (P + kDispatchChunk - 1) / kDispatchChunk;
+    int32_t* hist = work;
+    int32_t* item_of = work + (size_t)chunks * E;
+    hipLaunchKernelGGL(k_dispatch_hist, dim3((unsigned)chunks), dim3(1024), 0, s, ids, P, E, hist);
+    hipLaunchKernelGGL(k_dispatch_scan, dim3(1), dim3(1024), 0, s, hist, chunks, P, E, counts, offsets, elist, n_list,
+                       items, item_of, max_items, T, has_shared, chunk, sh_chunk);
+    hipLaunchKernelGGL(k_dispatch_rank, dim3((unsigned)chunks), dim3(1024), 0, s, ids, P, E, hist, counts, offsets,
+                       item_of, perm, slot, items, k, chunk);
     return hipGetLastError();
 }
 

@@ -20,6 +20,12 @@ hipError_t launch_topk(const float* logits, int ld_logits, int T, int E, int k, 
 hipError_t launch_dispatch(const int32_t* ids, int P, int E, int32_t* counts, int32_t* offsets, int32_t* perm,
                            int32_t* slot, int32_t* elist, int32_t* n_list, int4* items, int max_items, int T, int k,
                            int has_shared, int chunk, int sh_chunk, hipStream_t s);
+// the same dispatch in three launches for many pairs (chunk histograms, one scan, chunk ranks); `work` holds
+// dispatch_work_bytes(P, E)
+size_t dispatch_work_bytes(int64_t P, int E);
+hipError_t launch_dispatch_multi(const int32_t* ids, int P, int E, int32_t* counts, int32_t* offsets, int32_t* perm,
+                                 int32_t* slot, int32_t* elist, int32_t* n_list, int4* items, int max_items, int T,
+                                 int k, int has_shared, int chunk, int sh_chunk, int32_t* work, hipStream_t s);
 hipError_t launch_topk_dispatch(const float* logits, int T, int E, int k, int32_t* ids, float* wts, int32_t* counts,
                                 int32_t* offsets, int32_t* perm, int32_t* slot, int32_t* elist, int32_t* n_list,
                                 int4* items, int max_items, int has_shared, int chunk, int sh_chunk, hipStream_t s);

@@ -243,6 +243,8 @@ CASES = [
     # the shared down rows are packed more densely per wave than the routed ones: the grid must cover all H rows
     ("shared wider than routed, H=2048", dict(n_embd=2048, n_ff=256, n_ff_shared=512, n_expert=32, top_k=4), 5, 10,
      True),
+    # 3200 pairs: the dispatch runs as chunk histograms, one scan and chunk ranks
+    ("many pairs, top-32", dict(n_embd=256, n_ff=128, n_ff_shared=128, n_expert=128, top_k=32), 100, 17, True),
 ]
 
 

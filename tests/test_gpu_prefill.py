@@ -71,6 +71,9 @@ CASES = [
      15, True, None, S.PATH_AUTO),
     ("7 experts top-3, 9 tokens forced", dict(n_embd=256, n_ff=256, n_ff_shared=128, n_expert=7, top_k=3), 9, 8, True,
      None, S.PATH_MFMA),
+    # 20000 pairs over 20 dispatch chunks, a hot expert whose pairs span every chunk and many work items
+    ("many pairs, hot expert", dict(n_embd=256, n_ff=128, n_ff_shared=128, n_expert=64, top_k=8), 2500, 16, True,
+     ("hot", 9), S.PATH_AUTO),
 ]
 
 _LAYERS = {}
