@@ -81,7 +81,7 @@ smoe_status check_geom(const smoe_geom* g) {
 }
 
 struct Layout {
-    size_t ximg, logits, sg, ids, wts, counts, offsets, perm, slot, elist, nlist, items, himg, Y, dwork, total;
+    size_t ximg, xbf, logits, sg, ids, wts, counts, offsets, perm, slot, elist, nlist, items, himg, Y, dwork, total;
     int h_blocks;  // q8_1 blocks per h row (GEMV path)
     int h_rec;     // 64-value records per h row (MFMA path)
 };
@@ -113,6 +113,7 @@ Layout layout(const smoe_geom& g, int64_t T) {
     auto most = [](size_t a, size_t b) { return a > b ? a : b; };
     // x: q8_1 images (GEMV) or bf16 records (MFMA); h likewise
     L.ximg = take(most(smoe::img_bytes(T * (H / 32)), smoe::act_rec_bytes(T * (H / 64))));
+    L.xbf = take((size_t)T * H * 2);  // bf16 x of the MFMA path (the router's exact operand)
     L.logits = take((size_t)T * E * 4);
     L.sg = take((size_t)T * 4);
     L.ids = take((size_t)P * 4);
@@ -241,8 +242,9 @@ smoe_status smoe_forward_path(const smoe_geom* g, const smoe_weights* w, const f
         if (_m != SMOE_OK) return _m;        \
     } while (0)
     SMOE_MARK();
-    if (mfma) SMOE_TRY(smoe::launch_act_records(x, (int64_t)T * (H / 64), ximg, st), "activation records");
-    SMOE_TRY(smoe::launch_router(x, nullptr, static_cast<const uint16_t*>(w->router), has_sh ? w->gate_inp_sh : nullptr,
+    uint16_t* xbf = mfma ? reinterpret_cast<uint16_t*>(ws + L.xbf) : nullptr;
+    if (mfma) SMOE_TRY(smoe::launch_act_records(x, (int64_t)T * (H / 64), ximg, xbf, st), "activation records");
+    SMOE_TRY(smoe::launch_router(x, xbf, static_cast<const uint16_t*>(w->router), has_sh ? w->gate_inp_sh : nullptr,
                                  w->logit_bias, H, E, E + (has_sh ? 1 : 0), T, logits, E, sg, mfma ? nullptr : ximg,
                                  mfma ? 1 : 0, iq2 ? 1 : 0, st),
              "router");

@@ -293,17 +293,28 @@ __device__ __forceinline__ float group_sum_rs(float (&v)[NIT], int lpr, int lane
 // ... of all 64 (token, row) dots in element order (the order of k_router), then one reduce-scatter leaves
 // lane l with the dot of token l / 4, row l % 4: the logits equal k_router's bit for bit.
 template <int MAXC>
-__global__ __launch_bounds__(256) void k_router_tile(const float* __restrict__ x, const uint16_t* __restrict__ W,
+__global__ __launch_bounds__(256) void k_router_tile(const float* __restrict__ x, const uint16_t* __restrict__ xb,
+                                                      const uint16_t* __restrict__ W,
                                                       const uint16_t* __restrict__ w_inp, const float* __restrict__ bias,
                                                       int H, int E, int rows_total, int T, float* __restrict__ logits,
                                                       int ld_logits, float* __restrict__ sg) {
     extern __shared__ __align__(16) uint32_t smem[];
     const int t0 = blockIdx.y * 16;
     const int nt = min(16, T - t0);
-    // stage the tile's x as bf16 [token][H]; loads clamped to the tile's last 8-value chunk and stores to the
-    // buffer's last slot, so that every load issues back to back
+    // stage the tile's x as bf16 [token][H] (from `xb` when given, else rounded from x here); loads clamped to the
+    // tile's last 8-value chunk and stores to the buffer's last slot, so that every load issues back to back
     const int n8 = nt * H / 8, cap = 16 * H / 8;
     const float4* xs4 = reinterpret_cast<const float4*>(x + (size_t)t0 * H);
+    if (xb) {
+        const uint4* xb4 = reinterpret_cast<const uint4*>(xb + (size_t)t0 * H);
+        for (int base = 0; base < n8; base += 256 * 8) {
+            uint4 v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = xb4[min(base + u * 256 + (int)threadIdx.x, n8 - 1)];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) reinterpret_cast<uint4*>(smem)[min(base + u * 256 + (int)threadIdx.x, cap - 1)] = v[u];
+        }
+    } else
     for (int base = 0; base < n8; base += 256 * 4) {
         float4 v[4][2];
 #pragma unroll
@@ -1729,7 +1740,7 @@ hipError_t launch_router(const float* xf, const uint16_t* xb, const uint16_t* W,
         const size_t lds = (size_t)16 * H * 2;
 #define SMOE_ROUTER_TILE(C)                                                                                        \
     hipLaunchKernelGGL((k_router_tile<C>), dim3((unsigned)((rows_total + 15) / 16), (unsigned)((T + 15) / 16)),      \
-                       dim3(256), lds, s, xf, W, w_inp, bias, H, E, rows_total, T, logits, ld_logits, sg)
+                       dim3(256), lds, s, xf, xb, W, w_inp, bias, H, E, rows_total, T, logits, ld_logits, sg)
         if (maxc <= 2) SMOE_ROUTER_TILE(2);
         else if (maxc <= 4) SMOE_ROUTER_TILE(4);
         else SMOE_ROUTER_TILE(8);

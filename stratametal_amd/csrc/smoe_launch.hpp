@@ -15,7 +15,8 @@ hipError_t launch_prep(const float* x, int64_t n, uint8_t* xq, uint16_t* xb, hip
 hipError_t launch_router(const float* xf, const uint16_t* xb, const uint16_t* W, const uint16_t* w_inp,
                          const float* bias, int H, int E, int rows_total, int T, float* logits, int ld_logits, float* sg,
                          uint32_t* ximg, int tile_rows, int img_natural, hipStream_t s);
-// (tile_rows: many tokens, row x token tiles from xf; img_natural: write ximg in the IQ2_S kernels' natural order)
+// (tile_rows: many tokens, row x token tiles from xb when given, else from xf; img_natural: write ximg in the IQ2_S
+// kernels' natural order)
 hipError_t launch_topk(const float* logits, int ld_logits, int T, int E, int k, int32_t* ids, float* wts, hipStream_t s);
 hipError_t launch_dispatch(const int32_t* ids, int P, int E, int32_t* counts, int32_t* offsets, int32_t* perm,
                            int32_t* slot, int32_t* elist, int32_t* n_list, int4* items, int max_items, int T, int k,
@@ -71,7 +72,7 @@ hipError_t launch_iq2_mmvq(const uint8_t* w, const uint8_t* xq, int n_in, int n_
 // prefill contract (bf16 MFMA)
 int mfma_chunk();                        // tokens per MFMA work item
 size_t act_rec_bytes(int64_t n_rec);     // bytes of n_rec 64-value activation records
-hipError_t launch_act_records(const float* x, int64_t n_rec, uint32_t* rec, hipStream_t s);
+hipError_t launch_act_records(const float* x, int64_t n_rec, uint32_t* rec, uint16_t* xb, hipStream_t s);  // xb: bf16 copy or NULL
 hipError_t launch_mm_gu(const uint8_t* gate_exps, const uint8_t* up_exps, const uint8_t* gate_sh, const uint8_t* up_sh,
                         const uint32_t* xrec, int64_t n_xrec, const int4* items, const int32_t* perm, int k, int H,
                         int F, int Fs, int has_shared, int max_items, uint32_t* hrec, int h_rec, hipStream_t s);

@@ -49,9 +49,10 @@ __device__ __forceinline__ uint32_t bf16_as_f16(float v) {
 }
 
 // ------------------------------------------------------------------------------------------------ records of x
-// One thread per 8 positions (a 16-byte chunk) of a record.
+// One thread per 8 positions (a 16-byte chunk) of a record.  With `xb`, the same 8 values also as bf16 bits in
+// natural order (the router's exact operand).
 __global__ __launch_bounds__(256) void k_act_records(const float* __restrict__ x, int64_t n_rec,
-                                                     uint32_t* __restrict__ rec) {
+                                                     uint32_t* __restrict__ rec, uint16_t* __restrict__ xb) {
     const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
     const int64_t r = g >> 3;
     if (r >= n_rec) return;
@@ -60,6 +61,13 @@ __global__ __launch_bounds__(256) void k_act_records(const float* __restrict__ x
     const float4* src = reinterpret_cast<const float4*>(x + r * 64 + 16 * q + 8 * s);
     const float4 lo = src[0], hi = src[1];
     const float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+    if (xb) {
+        uint32_t h[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) h[e] = f32_to_bf16(v[e]);
+        *reinterpret_cast<uint4*>(xb + r * 64 + 16 * q + 8 * s) =
+            make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16));
+    }
     uint32_t b[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) b[e] = bf16_as_f16(v[perm8(e)]);
@@ -471,8 +479,8 @@ __global__ __launch_bounds__(512) void k_mm_down(const uint8_t* __restrict__ dow
 int mfma_chunk() { return kChunk; }
 size_t act_rec_bytes(int64_t n_rec) { return (size_t)n_rec * kRecBytes; }
 
-hipError_t launch_act_records(const float* x, int64_t n_rec, uint32_t* rec, hipStream_t s) {
-    hipLaunchKernelGGL(k_act_records, dim3((unsigned)((n_rec * 8 + 255) / 256)), dim3(256), 0, s, x, n_rec, rec);
+hipError_t launch_act_records(const float* x, int64_t n_rec, uint32_t* rec, uint16_t* xb, hipStream_t s) {
+    hipLaunchKernelGGL(k_act_records, dim3((unsigned)((n_rec * 8 + 255) / 256)), dim3(256), 0, s, x, n_rec, rec, xb);
     return hipGetLastError();
 }
 
