@@ -32,17 +32,27 @@ __device__ const uint16_t kIq2sCodes[1024] = {
 constexpr uint32_t kMagPos = 0x002B1908u;  // bytes 8, 25, 43, 0
 constexpr uint32_t kMagNeg = 0x00D5E7F8u;  // bytes -8, -25, -43, 0
 
-// LDS table: entry i = the eight 2-bit magnitude indices of grid entry i, one per byte (lo: weights 0-3).
-__device__ __forceinline__ void build_grid_table(uint2* tab) {
-    for (int i = threadIdx.x; i < 1024; i += blockDim.x) {
-        const uint32_t c = kIq2sCodes[i];
+// LDS table: entry i = the eight 2-bit magnitude indices of grid entry i, one per byte (lo: weights 0-3).  Built
+// in two steps so that a kernel can issue the code loads first and its other loads behind them: grid_codes_load
+// (entries tid + NTH j, unconditional), grid_table_store (waits for those loads alone).
+template <int NTH>
+__device__ __forceinline__ void grid_codes_load(uint32_t (&c)[1024 / NTH]) {
+#pragma unroll
+    for (int j = 0; j < 1024 / NTH; ++j) c[j] = kIq2sCodes[threadIdx.x + NTH * j];
+}
+template <int NTH>
+__device__ __forceinline__ void grid_table_store(const uint32_t (&c)[1024 / NTH], uint2* tab) {
+#pragma unroll
+    for (int j = 0; j < 1024 / NTH; ++j) {
+        uint32_t cj = c[j];
+        asm volatile("" : "+v"(cj));  // the unpacking (and so the wait for the code load) stays where the call stands
         uint32_t lo = 0, hi = 0;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            lo |= ((c >> (2 * j)) & 3u) << (8 * j);
-            hi |= ((c >> (8 + 2 * j)) & 3u) << (8 * j);
+        for (int q = 0; q < 4; ++q) {
+            lo |= ((cj >> (2 * q)) & 3u) << (8 * q);
+            hi |= ((cj >> (8 + 2 * q)) & 3u) << (8 * q);
         }
-        tab[i] = make_uint2(lo, hi);
+        tab[threadIdx.x + NTH * j] = make_uint2(lo, hi);
     }
 }
 
@@ -171,19 +181,39 @@ __global__ __launch_bounds__(64 * NW) void k_iq2_gu(const uint8_t* __restrict__ 
     const uint8_t* base = (rho < 32 ? (item.shared ? gate_sh : gate_exps + (size_t)item.e * F * rb)
                                     : (item.shared ? up_sh : up_exps + (size_t)item.e * F * rb));
     const uint8_t* rowp = base + (size_t)(32 * hb + (rho & 31)) * rb;
+    const int qb = H >> 5;
+    // loads in the order their data is needed: the grid codes, the first column batch's images (when their rows
+    // need no memory read), then the weights; the table store waits for the codes alone, the image commit for
+    // the images alone
+    uint32_t codes[1024 / (64 * NW)];
+    grid_codes_load<64 * NW>(codes);
+    const int nc0 = min(kCols, item.ncol);
     uint32_t raw[21];
     int off;
-    load_block_raw(rowp, b, raw, off);  // issued before the table build, so its latency overlaps it
-    build_grid_table(tab);
-    const int qb = H >> 5;
+    if (stage_direct(item, 0, nc0, true)) {  // straight-line inside each branch, so no wait lands between the loads
+        StagePieces sp;
+        stage_issue_direct(sp, ximg, qb, 0, nc0, kCols, 0, item, true);
+        __builtin_amdgcn_sched_barrier(0);
+        load_block_raw(rowp, b, raw, off);
+        __builtin_amdgcn_sched_barrier(0);
+        grid_table_store<64 * NW>(codes, tab);
+        stage_commit_direct(sp, smem);
+    } else {
+        load_block_raw(rowp, b, raw, off);
+        grid_table_store<64 * NW>(codes, tab);
+        stage_images(smem, ximg, qb, 0, nc0, kCols, item, perm, k, true, 0, 4 * 64 * NW);
+    }
+    stage_images(smem, ximg, qb, 0, nc0, kCols, item, perm, k, true, 4 * 64 * NW);  // rounds beyond the first
     __syncthreads();
     Iq2Block B[1];
     decode_block(raw, off, tab, B[0]);
 
     for (int c0 = 0; c0 < item.ncol; c0 += kCols) {
         const int nc = min(kCols, item.ncol - c0);
-        stage_images(smem, ximg, qb, c0, nc, kCols, item, perm, k, true);
-        __syncthreads();
+        if (c0 > 0) {
+            stage_images(smem, ximg, qb, c0, nc, kCols, item, perm, k, true);
+            __syncthreads();
+        }
         for (int c = 0; c < nc; ++c) {
             const uint32_t* xt = smem + (size_t)c * qb * kImgDw;
             pin_blocks(B);
@@ -215,7 +245,6 @@ __global__ __launch_bounds__(256) void k_iq2_down(const uint8_t* __restrict__ do
     __shared__ uint2 tab[1024];
     Item item;
     if (!work_item(items, blockIdx.y, item)) return;
-    build_grid_table(tab);
     const int Fe = item.shared ? Fs : F;
     const int nb = Fe >> 8;
     const size_t rb = (size_t)nb * 82;
@@ -224,18 +253,30 @@ __global__ __launch_bounds__(256) void k_iq2_down(const uint8_t* __restrict__ do
     const int rpw = 64 / nb, grp = lane / nb, b = lane - grp * nb;
     const int r = blockIdx.x * 4 * rpw + wave * rpw + grp;
     const bool live = r < H;
+    // loads in the order their data is needed (see k_iq2_gu): grid codes, the first column batch's h images,
+    // then the weights
+    uint32_t codes[4];
+    grid_codes_load<256>(codes);
+    const int nc0 = min(cps, item.ncol);
+    StagePieces sp;
+    stage_issue_direct(sp, himg, h_blocks, 0, nc0, cps, 0, item, false);
+    __builtin_amdgcn_sched_barrier(0);
+    uint32_t raw[21];
+    int off;
+    load_block_raw(base + (size_t)(live ? r : 0) * rb, b, raw, off);
+    __builtin_amdgcn_sched_barrier(0);
+    grid_table_store<256>(codes, tab);
+    stage_commit_direct(sp, smem);
+    stage_images(smem, himg, h_blocks, 0, nc0, cps, item, nullptr, 1, false, 4 * 256);  // rounds beyond the first
     __syncthreads();
     Iq2Block B[1];
-    {
-        uint32_t raw[21];
-        int off;
-        load_block_raw(base + (size_t)(live ? r : 0) * rb, b, raw, off);
-        decode_block(raw, off, tab, B[0]);
-    }
+    decode_block(raw, off, tab, B[0]);
     for (int c0 = 0; c0 < item.ncol; c0 += cps) {
         const int nc = min(cps, item.ncol - c0);
-        stage_images(smem, himg, h_blocks, c0, nc, cps, item, nullptr, 1, false);
-        __syncthreads();
+        if (c0 > 0) {
+            stage_images(smem, himg, h_blocks, c0, nc, cps, item, nullptr, 1, false);
+            __syncthreads();
+        }
         for (int c = 0; c < nc; ++c) {
             const uint32_t* ht = smem + (size_t)c * h_blocks * kImgDw;
             pin_blocks(B);
@@ -251,7 +292,11 @@ __global__ __launch_bounds__(256) void k_iq2_down(const uint8_t* __restrict__ do
 __global__ __launch_bounds__(256) void k_iq2_mmvq(const uint8_t* __restrict__ w, const uint8_t* __restrict__ xq, int n_in,
                                                    int n_out, int n_col, float* __restrict__ y) {
     __shared__ uint2 tab[1024];
-    build_grid_table(tab);
+    {
+        uint32_t codes[4];
+        grid_codes_load<256>(codes);
+        grid_table_store<256>(codes, tab);
+    }
     const int nb = n_in >> 8;
     const size_t rb = (size_t)nb * 82;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
