@@ -1565,22 +1565,33 @@ __global__ __launch_bounds__(256) void k_q2_mmvq(const uint8_t* __restrict__ w, 
 __global__ __launch_bounds__(256) void k_combine(const float* __restrict__ Y, const int32_t* __restrict__ slot,
                                                   const float* __restrict__ wts, int k, int H, int P, int add_shared,
                                                   float* __restrict__ y) {
+    asm volatile("" ::"s"(Y), "s"(slot), "s"(wts), "s"(y), "s"(k), "s"(H), "s"(P), "s"(add_shared));  // kernargs now
     const int t = blockIdx.x;
     const int32_t* sl = slot + (size_t)t * k;
     const float* wt = wts + (size_t)t * k;
-    for (int j = blockIdx.y * 256 + threadIdx.x; j < H; j += gridDim.y * 256) {
-        // the pair rows 8 at a time, all loads of a batch in flight together (past k: reloads of the last row)
-        float acc = 0.0f;
-        for (int s0 = 0; s0 < k; s0 += 8) {
-            float v[8], wv[8];
+    // the first 16 slots and weights in one go (scalar loads, past k: the last one again), so that the row loads
+    // of the first two batches wait for one round trip
+    int sl16[16];
+    float wt16[16];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < 16; ++i) {
+        sl16[i] = sl[min(i, k - 1)];
+        wt16[i] = wt[min(i, k - 1)];
+    }
+    for (int j = blockIdx.y * 256 + threadIdx.x; j < H; j += gridDim.y * 256) {
+        // the pair rows 16 at a time, all loads of a batch in flight together (past k: reloads of the last row)
+        float acc = 0.0f;
+        for (int s0 = 0; s0 < k; s0 += 16) {
+            float v[16], wv[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
                 const int s = min(s0 + i, k - 1);
-                v[i] = Y[(size_t)sl[s] * H + j];
-                wv[i] = wt[s];
+                const int r = s0 == 0 ? sl16[i] : sl[s];
+                v[i] = Y[(size_t)r * H + j];
+                wv[i] = s0 == 0 ? wt16[i] : wt[s];
             }
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
+            for (int i = 0; i < 16; ++i) {
                 const int s = s0 + i;
                 if (s == 0) acc = wv[0] * v[0];
                 else if (s < k) acc = __builtin_fmaf(wv[i], v[i], acc);
