@@ -189,12 +189,12 @@ struct MmPlan {
     using S = Shape<MODE>;
     uint32_t a_off[S::kASlots], w_off[S::kWSlots];
     int a_at[S::kASlots], w_at[S::kWSlots];
-    int w_up[S::kWSlots];  // the slot's rows are the second tensor's (up rows)
+    i32x4 w_rsrc[S::kWSlots];  // the slot's weight tensor (the up rows' for the second half of gate/up)
 
     // rowidx: activation row of each column; rpr: records per activation row; rb: weight row bytes; split: rows
-    // of the first weight tensor (gate/up: 128; down: 256, i.e. one tensor).
+    // of the first weight tensor (gate/up: 128; down: 256, i.e. one tensor); rw0 / rw1: the two weight tensors.
     __device__ __forceinline__ void init(const int* rowidx, int wave, int lane, int ncol, int rpr, uint32_t rb,
-                                         int split) {
+                                         int split, i32x4 rw0, i32x4 rw1) {
 #pragma unroll
         for (int m = 0; m < S::kASlots; ++m) {
             const int j = wave + kWaves * m;
@@ -210,14 +210,14 @@ struct MmPlan {
             const int P = 64 * j + lane, row = P / 3, p = P - 3 * row;
             const bool real = j < kWIns;
             const int r = row >= split ? row - split : row;
-            w_up[m] = 64 * j >= 3 * split ? 1 : 0;  // whole instructions: 3 * split is a multiple of 64
+            w_rsrc[m] = 64 * j >= 3 * split ? rw1 : rw0;  // whole instructions: 3 * split is a multiple of 64
             w_off[m] = real ? (uint32_t)r * rb + 16u * p : kOob;
             w_at[m] = real ? S::kABytes + 1024 * j : -1;
         }
     }
 
     // Issue unit u into ring stage b.
-    __device__ __forceinline__ void issue(uint32_t lds0, int b, int u, i32x4 ra, i32x4 rw0, i32x4 rw1) const {
+    __device__ __forceinline__ void issue(uint32_t lds0, int b, int u, i32x4 ra) const {
         const uint32_t st = (uint32_t)(b * S::kStage);
         const uint32_t sa = __builtin_amdgcn_readfirstlane((uint32_t)u * (2 * kRecBytes));
         const uint32_t sw = __builtin_amdgcn_readfirstlane((uint32_t)(36 * u - 4 * (u & 3)));
@@ -229,7 +229,7 @@ struct MmPlan {
 #pragma unroll
         for (int m = 0; m < S::kWSlots; ++m) {
             const uint32_t at = w_at[m] < 0 ? (uint32_t)kDummy : st + (uint32_t)w_at[m];
-            dma16(__builtin_amdgcn_readfirstlane(lds0 + at), w_off[m], w_up[m] ? rw1 : rw0, sw);
+            dma16(__builtin_amdgcn_readfirstlane(lds0 + at), w_off[m], w_rsrc[m], sw);
         }
     }
 };
@@ -272,19 +272,30 @@ __device__ __forceinline__ void mm_unit(f32x4 (&acc)[4][NS], const uint32_t* W, 
 // wave's live column tiles.
 template <int MODE, int NT>
 __device__ __forceinline__ void mm_loop_nt(f32x4 (&acc)[4][Shape<MODE>::NS], uint8_t* lds, const MmPlan<MODE>& pl,
-                                           int units, i32x4 ra, i32x4 rw0, i32x4 rw1,
-                                           const int (&rows)[Shape<MODE>::NS], int tok0, int i, int q) {
+                                           int units, i32x4 ra, const int (&rows)[Shape<MODE>::NS], int tok0, int i,
+                                           int q) {
     using S = Shape<MODE>;
     constexpr int ST = S::kStages;
     const uint32_t lds0 = lds_addr(lds);
 #pragma unroll
     for (int b = 0; b < ST - 1; ++b)
-        if (b < units) pl.issue(lds0, b, b, ra, rw0, rw1);
-    int b = 0;  // ring stage of unit u
-    for (int u = 0; u < units; ++u) {
-        wait_stages<S::kSlots>(min(ST - 2, units - 1 - u));
+        if (b < units) pl.issue(lds0, b, b, ra);
+    int b = 0, u = 0;  // ring stage of unit u
+    // steady state: every iteration consumes unit u, with the ST - 2 units after it still in flight, and issues
+    // unit u + ST - 1 (a constant wait, no test)
+    for (; u + ST - 1 < units; ++u) {
+        vmcnt<(ST - 2) * S::kSlots>();
         __syncthreads();  // unit u is in LDS for everyone; everyone is done with unit u - 1
-        if (u + ST - 1 < units) pl.issue(lds0, b == 0 ? ST - 1 : b - 1, u + ST - 1, ra, rw0, rw1);
+        pl.issue(lds0, b == 0 ? ST - 1 : b - 1, u + ST - 1, ra);
+        const uint8_t* stg = lds + b * S::kStage;
+        mm_unit<S::NS, NT>(acc, reinterpret_cast<const uint32_t*>(stg + S::kABytes), u & 3, rows,
+                           reinterpret_cast<const uint4*>(stg), tok0, i, q);
+        b = b + 1 == ST ? 0 : b + 1;
+    }
+    // the last units (all of them when there are fewer than ST - 1): nothing left to issue, the waits shrink
+    for (; u < units; ++u) {
+        wait_stages<S::kSlots>(units - 1 - u);
+        __syncthreads();
         const uint8_t* stg = lds + b * S::kStage;
         mm_unit<S::NS, NT>(acc, reinterpret_cast<const uint32_t*>(stg + S::kABytes), u & 3, rows,
                            reinterpret_cast<const uint4*>(stg), tok0, i, q);
@@ -294,21 +305,21 @@ __device__ __forceinline__ void mm_loop_nt(f32x4 (&acc)[4][Shape<MODE>::NS], uin
 
 template <int MODE>
 __device__ __forceinline__ void mm_loop(f32x4 (&acc)[4][Shape<MODE>::NS], uint8_t* lds, const MmPlan<MODE>& pl,
-                                        int units, i32x4 ra, i32x4 rw0, i32x4 rw1,
-                                        const int (&rows)[Shape<MODE>::NS], int tok0, int ntiles, int i, int q) {
+                                        int units, i32x4 ra, const int (&rows)[Shape<MODE>::NS], int tok0, int ntiles,
+                                        int i, int q) {
 #pragma unroll
     for (int n = 0; n < 4; ++n)
 #pragma unroll
         for (int s = 0; s < Shape<MODE>::NS; ++s) acc[n][s] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     if constexpr (MODE == kThin) {  // one tile
-        mm_loop_nt<MODE, 1>(acc, lds, pl, units, ra, rw0, rw1, rows, tok0, i, q);
+        mm_loop_nt<MODE, 1>(acc, lds, pl, units, ra, rows, tok0, i, q);
         return;
     }
     switch (ntiles) {  // wave-uniform; every wave has 1 .. 4 live tiles
-        case 1: mm_loop_nt<MODE, 1>(acc, lds, pl, units, ra, rw0, rw1, rows, tok0, i, q); break;
-        case 2: mm_loop_nt<MODE, 2>(acc, lds, pl, units, ra, rw0, rw1, rows, tok0, i, q); break;
-        case 3: mm_loop_nt<MODE, 3>(acc, lds, pl, units, ra, rw0, rw1, rows, tok0, i, q); break;
-        default: mm_loop_nt<MODE, 4>(acc, lds, pl, units, ra, rw0, rw1, rows, tok0, i, q); break;
+        case 1: mm_loop_nt<MODE, 1>(acc, lds, pl, units, ra, rows, tok0, i, q); break;
+        case 2: mm_loop_nt<MODE, 2>(acc, lds, pl, units, ra, rows, tok0, i, q); break;
+        case 3: mm_loop_nt<MODE, 3>(acc, lds, pl, units, ra, rows, tok0, i, q); break;
+        default: mm_loop_nt<MODE, 4>(acc, lds, pl, units, ra, rows, tok0, i, q); break;
     }
 }
 
@@ -336,11 +347,11 @@ __device__ __forceinline__ void mm_gu_body(uint8_t* lds, const int* rowidx, cons
     const uint32_t rb = (uint32_t)units * 36u;
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, i = lane & 15,
               q = lane >> 4;
-    MmPlan<MODE> pl;
-    pl.init(rowidx, wave, lane, ncol, H >> 6, rb, 128);
     const i32x4 ra = buffer_rsrc(xrec, xrec_bytes);
     const i32x4 rg0 = buffer_rsrc(g0 + (size_t)128 * rt * rb, 128u * rb);
     const i32x4 ru0 = buffer_rsrc(u0 + (size_t)128 * rt * rb, 128u * rb);
+    MmPlan<MODE> pl;
+    pl.init(rowidx, wave, lane, ncol, H >> 6, rb, 128, rg0, ru0);
     int rows[NS];
     int fbase;  // first of the wave's gate rows within the work-group's 128
     if constexpr (WIDE) {
@@ -357,7 +368,7 @@ __device__ __forceinline__ void mm_gu_body(uint8_t* lds, const int* rowidx, cons
     const int tok0 = WIDE ? 64 * (wave >> 2) : 0;
     const int ntiles = min(4, max(0, (ncol - tok0 + 15) >> 4));
     f32x4 acc[4][NS];
-    mm_loop<MODE>(acc, lds, pl, units, ra, rg0, ru0, rows, tok0, ntiles, i, q);
+    mm_loop<MODE>(acc, lds, pl, units, ra, rows, tok0, ntiles, i, q);
     __syncthreads();  // every wave is done with the ring: its start becomes the h tile
     // h tile [column][128 rows in record order] as fp16 bits of bf16 values
     uint16_t* ht = reinterpret_cast<uint16_t*>(lds);
@@ -421,11 +432,11 @@ __device__ __forceinline__ void mm_down_body(uint8_t* lds, const int* rowidx, co
     const uint32_t rb = (uint32_t)units * 36u;
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, i = lane & 15,
               q = lane >> 4;
-    MmPlan<MODE> pl;
-    pl.init(rowidx, wave, lane, ncol, h_rec, rb, kWgRows);
     const int nrows = min(kWgRows, H - kWgRows * rt);
     const i32x4 ra = buffer_rsrc(hrec, hrec_bytes);
     const i32x4 rd = buffer_rsrc(d0 + (size_t)kWgRows * rt * rb, (uint32_t)nrows * rb);
+    MmPlan<MODE> pl;
+    pl.init(rowidx, wave, lane, ncol, h_rec, rb, kWgRows, rd, rd);
     int rows[NS];
     const int r0 = WIDE ? 64 * (wave & 3) : 32 * wave;
 #pragma unroll
@@ -433,7 +444,7 @@ __device__ __forceinline__ void mm_down_body(uint8_t* lds, const int* rowidx, co
     const int tok0 = WIDE ? 64 * (wave >> 2) : 0;
     const int ntiles = min(4, max(0, (ncol - tok0 + 15) >> 4));
     f32x4 acc[4][NS];
-    mm_loop<MODE>(acc, lds, pl, units, ra, rd, rd, rows, tok0, ntiles, i, q);
+    mm_loop<MODE>(acc, lds, pl, units, ra, rows, tok0, ntiles, i, q);
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
         const int row = kWgRows * rt + rows[s];
