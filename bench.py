@@ -258,7 +258,9 @@ def prefill(S, torch, g, a):
 def stack48(S, torch, g, stack, a):
     """the resident layers chained as x_{l+1} = RMSNorm(x_l + MoE_l(x_l)) (unit weight, eps 1e-6):
     one `--stack-prefill` token prefill through every layer (the MFMA contract), then `--stack-decode` decode
-    steps at batch 1 (each step one graph of every layer and junction, replayed on a fresh token)."""
+    steps at batch 1 (each step one graph of every layer and junction, replayed on a fresh token).  Each
+    junction after the first layer runs inside the next layer's call (smoe_forward_residual, bitwise equal to
+    the separate junction and call), the last one on its own."""
     import ctypes as C
     L = len(stack.layers)
     H, Tp, steps = g.n_embd, a.stack_prefill, a.stack_decode
@@ -266,13 +268,22 @@ def stack48(S, torch, g, stack, a):
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
     lib = S.lib()
 
-    def layer(l, x, y, T):
-        S._check(lib.smoe_forward(C.byref(stack.gc), C.byref(stack.wc[l]), x.data_ptr(), T, y.data_ptr(), 1,
+    def chain(xa, xb, y, T):
+        """Every layer on xa (xb the other junction buffer, y the layer output); the final x ends in xa or xb."""
+        S._check(lib.smoe_forward(C.byref(stack.gc), C.byref(stack.wc[0]), xa.data_ptr(), T, y.data_ptr(), 1,
                                   ws.data_ptr(), ws_bytes, None, S._stream()))
-        S.residual_rmsnorm(x, y, 1e-6, out=x)
+        cur, nxt = xa, xb
+        for l in range(1, L):
+            S._check(lib.smoe_forward_residual(C.byref(stack.gc), C.byref(stack.wc[l]), cur.data_ptr(),
+                                               y.data_ptr(), C.c_float(1e-6), nxt.data_ptr(), T, y.data_ptr(), 1,
+                                               ws.data_ptr(), ws_bytes, None, S._stream()))
+            cur, nxt = nxt, cur
+        S.residual_rmsnorm(cur, y, 1e-6, out=cur)
+        return cur
 
     x0 = S.synth_normal(a.seed + 40, 100, Tp * H).view(Tp, H)
     x = torch.empty_like(x0)
+    x2 = torch.empty_like(x0)
     y = torch.empty_like(x0)
     times = []
     for rep in range(2):  # the first pass loads code and warms the allocator; the second is the measurement
@@ -280,8 +291,7 @@ def stack48(S, torch, g, stack, a):
         ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
         ev0.record()
-        for l in range(L):
-            layer(l, x, y, Tp)
+        xl = chain(x, x2, y, Tp)
         ev1.record()
         torch.cuda.synchronize()
         times.append(ev0.elapsed_time(ev1))
@@ -289,22 +299,21 @@ def stack48(S, torch, g, stack, a):
     ex_flops, router_flops = prefill_flops(g, Tp)
     out = {"layers": L, "prefill_tokens": Tp, "prefill_ms": pre_ms, "prefill_tok_s": Tp / (pre_ms * 1e-3),
            "prefill_tflops": L * (ex_flops + router_flops) / (pre_ms * 1e-3) / 1e12,
-           "prefill_out_finite": bool(torch.isfinite(x).all().item())}
+           "prefill_out_finite": bool(torch.isfinite(xl).all().item())}
     # decode: one graph per step over every layer, replayed on fresh tokens
     xs = S.synth_normal(a.seed + 41, 100, steps * H).view(steps, H)
     xin = torch.empty((1, H), dtype=torch.float32, device="cuda")
+    xalt = torch.empty((1, H), dtype=torch.float32, device="cuda")
     yb = torch.empty((1, H), dtype=torch.float32, device="cuda")
     xin.copy_(xs[0:1])
-    for l in range(L):  # eager pass (code and workspace warm)
-        layer(l, xin, yb, 1)
+    chain(xin, xalt, yb, 1)  # eager pass (code and workspace warm)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     gs = torch.cuda.Stream()
     gs.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(gs):
         with torch.cuda.graph(graph, stream=gs):
-            for l in range(L):
-                layer(l, xin, yb, 1)
+            chain(xin, xalt, yb, 1)
     torch.cuda.synchronize()
     xin.copy_(xs[0:1])
     graph.replay()
@@ -325,7 +334,7 @@ def stack48(S, torch, g, stack, a):
     log("stack of %d: prefill %d tokens %.2f ms (%.0f tok/s, %.0f TFLOP/s), decode %.3f ms/token (%.0f tok/s, "
         "%.0f GB/s)" % (L, Tp, pre_ms, out["prefill_tok_s"], out["prefill_tflops"], per_tok, out["decode_tok_s"],
                         out["decode_gbs"]))
-    del ws, x, y, x0
+    del ws, x, x2, y, x0
     torch.cuda.empty_cache()
     return out
 

@@ -110,6 +110,16 @@ smoe_status smoe_forward_path(const smoe_geom* g, const smoe_weights* w, const f
                               int32_t add_shared, void* workspace, size_t workspace_bytes, const smoe_trace* trace,
                               int32_t path, void* hip_stream);
 
+/* The stacked configuration's layer junction fused into the next layer's call: x = RMSNorm(x_prev + r_prev)
+ * (unit weight; as smoe_residual_rmsnorm forms it) is written to x, then y = MoE(x) as smoe_forward.  On the
+ * decode (GEMV) path the norm is formed inside the router kernel; on the prefill path a junction kernel runs
+ * first.  Bitwise equal to smoe_residual_rmsnorm followed by smoe_forward.  x must not overlap x_prev, r_prev
+ * or y (y may be r_prev); x_prev, r_prev and x 16-byte aligned.  No counterpart in the reference's MoE block
+ * (its layer walk normalises in the hyper-connection read, out of this block's scope). */
+smoe_status smoe_forward_residual(const smoe_geom* g, const smoe_weights* w, const float* x_prev, const float* r_prev,
+                                  float eps, float* x, int32_t n_tokens, float* y, int32_t add_shared,
+                                  void* workspace, size_t workspace_bytes, const smoe_trace* trace, void* hip_stream);
+
 /* ---------------------------------------------------------------------------------------------- stages */
 
 /* logits (n_tokens, n_expert) f32 -> ids, weights (n_tokens, k): softmax over every expert, top k by

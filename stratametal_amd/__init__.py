@@ -65,6 +65,7 @@ def lib():
             "smoe_workspace_bytes": (C.c_size_t, [vp, i32]),
             "smoe_forward": (i32, [vp, vp, vp, i32, vp, i32, vp, C.c_size_t, vp, vp]),
             "smoe_forward_path": (i32, [vp, vp, vp, i32, vp, i32, vp, C.c_size_t, vp, i32, vp]),
+            "smoe_forward_residual": (i32, [vp, vp, vp, vp, f32, vp, i32, vp, i32, vp, C.c_size_t, vp, vp]),
             "smoe_router_topk": (i32, [vp, i32, i32, i32, vp, vp, vp]),
             "smoe_f32_to_bf16": (i32, [vp, i64, vp, vp]),
             "smoe_bf16_gemv": (i32, [vp, vp, vp, i32, i32, i32, vp]),
@@ -243,6 +244,20 @@ class MoELayer:
                                        int(add_shared), self.ws.data_ptr(), self.ws_bytes,
                                        None if tr is None else C.byref(tr), path, _stream(stream)))
         return (y, out) if trace else y
+
+    def forward_residual(self, x_prev, r_prev, x, y=None, eps: float = 1e-6, add_shared: bool = True, stream=None):
+        """The stack junction fused into this layer's call: x = RMSNorm(x_prev + r_prev) (written to `x`), then
+        y = MoE(x) (smoe_forward_residual).  `x` must not overlap x_prev, r_prev or y; y may be r_prev."""
+        import torch
+        T = x.shape[0]
+        if T > self.max_tokens:
+            raise SmoeError(-2, f"{T} tokens exceed the workspace's {self.max_tokens}")
+        if y is None:
+            y = torch.empty_like(x)
+        _check(lib().smoe_forward_residual(C.byref(self._gc), C.byref(self._wc), x_prev.data_ptr(), r_prev.data_ptr(),
+                                           eps, x.data_ptr(), T, y.data_ptr(), int(add_shared), self.ws.data_ptr(),
+                                           self.ws_bytes, None, _stream(stream)))
+        return y
 
     __call__ = forward
 

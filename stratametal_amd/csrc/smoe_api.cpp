@@ -164,16 +164,25 @@ const char* smoe_status_str(smoe_status s) {
 
 const char* smoe_last_error(void) { return g_last.c_str(); }
 
-int32_t smoe_abi_version(void) { return 102; }
+int32_t smoe_abi_version(void) { return 103; }
 
 size_t smoe_workspace_bytes(const smoe_geom* g, int32_t max_tokens) {
     if (check_geom(g) != SMOE_OK || max_tokens < 0) return 0;
     return layout(*g, max_tokens).total;
 }
 
-smoe_status smoe_forward_path(const smoe_geom* g, const smoe_weights* w, const float* x, int32_t n_tokens, float* y,
-                              int32_t add_shared, void* workspace, size_t workspace_bytes, const smoe_trace* trace,
-                              int32_t path, void* hip_stream) {
+namespace {
+bool overlaps(const void* a, const void* b, size_t bytes) {
+    const uintptr_t x = reinterpret_cast<uintptr_t>(a), z = reinterpret_cast<uintptr_t>(b);
+    return x < z + bytes && z < x + bytes;
+}
+
+// The forward call; with x_prev, x = RMSNorm(x_prev + r_prev) is formed first (fused into the router kernel on the
+// GEMV path, a junction kernel before the call on the MFMA path) and written to x.
+smoe_status forward_impl(const smoe_geom* g, const smoe_weights* w, float* x_io, int32_t n_tokens, float* y,
+                         int32_t add_shared, void* workspace, size_t workspace_bytes, const smoe_trace* trace,
+                         int32_t path, void* hip_stream, const float* x_prev, const float* r_prev, float eps) {
+    const float* x = x_io;
     smoe_status s = check_geom(g);
     if (s != SMOE_OK) return s;
     if (!w) return fail(SMOE_ENULL, "weights is NULL");
@@ -195,6 +204,15 @@ smoe_status smoe_forward_path(const smoe_geom* g, const smoe_weights* w, const f
     if (n_tokens == 0) return ok();  // empty x / y may be NULL: nothing is read or written
     if (!x || !y) return fail(SMOE_ENULL, "x or y is NULL");
     if (!aligned(x, 4) || !aligned(y, 4)) return fail(SMOE_EALIGN, "x and y must be 4-byte aligned");
+    if (x_prev) {
+        const size_t bytes = (size_t)n_tokens * g->n_embd * 4;
+        if (!r_prev) return fail(SMOE_ENULL, "r_prev is NULL");
+        if (g->n_embd > 4096) return fail(SMOE_EINVAL, "the fused junction takes rows up to 4096");
+        if (!aligned(x_prev, 16) || !aligned(r_prev, 16) || !aligned(x, 16))
+            return fail(SMOE_EALIGN, "x_prev, r_prev and x must be 16-byte aligned");
+        if (overlaps(x, x_prev, bytes) || overlaps(x, r_prev, bytes) || overlaps(x, y, bytes))
+            return fail(SMOE_EINVAL, "x must not overlap x_prev, r_prev or y");
+    }
     const bool iq2 = g->w_type == SMOE_IQ2_S;
     if (iq2 && path == SMOE_PATH_MFMA) return fail(SMOE_ETYPE, "the MFMA (prefill) path is built for Q2_0 experts only");
     const bool mfma = !iq2 && (path == SMOE_PATH_MFMA || (path == SMOE_PATH_AUTO && n_tokens >= kMfmaTokens));
@@ -242,11 +260,15 @@ smoe_status smoe_forward_path(const smoe_geom* g, const smoe_weights* w, const f
         if (_m != SMOE_OK) return _m;        \
     } while (0)
     SMOE_MARK();
+    if (x_prev && mfma)  // the junction first, then the call on its output
+        SMOE_TRY(smoe::launch_residual_rmsnorm(x_prev, r_prev, T, H, eps, x_io, st), "residual rmsnorm");
+    const bool fused_norm = x_prev && !mfma;
     uint16_t* xbf = mfma ? reinterpret_cast<uint16_t*>(ws + L.xbf) : nullptr;
     if (mfma) SMOE_TRY(smoe::launch_act_records(x, (int64_t)T * (H / 64), ximg, xbf, st), "activation records");
-    SMOE_TRY(smoe::launch_router(x, xbf, static_cast<const uint16_t*>(w->router), has_sh ? w->gate_inp_sh : nullptr,
-                                 w->logit_bias, H, E, E + (has_sh ? 1 : 0), T, logits, E, sg, mfma ? nullptr : ximg,
-                                 mfma ? 1 : 0, iq2 ? 1 : 0, st),
+    SMOE_TRY(smoe::launch_router(fused_norm ? x_prev : x, xbf, static_cast<const uint16_t*>(w->router),
+                                 has_sh ? w->gate_inp_sh : nullptr, w->logit_bias, H, E, E + (has_sh ? 1 : 0), T, logits,
+                                 E, sg, mfma ? nullptr : ximg, mfma ? 1 : 0, iq2 ? 1 : 0, st,
+                                 fused_norm ? r_prev : nullptr, eps, fused_norm ? x_io : nullptr),
              "router");
     SMOE_MARK();
     // batches of at most kFusedRouteTokens tokens on the Q2_0 GEMV path: the gate/up kernel routes the batch itself,
@@ -316,6 +338,22 @@ smoe_status smoe_forward_path(const smoe_geom* g, const smoe_weights* w, const f
     SMOE_MARK();
 #undef SMOE_MARK
     return ok();
+}
+}  // namespace
+
+smoe_status smoe_forward_path(const smoe_geom* g, const smoe_weights* w, const float* x, int32_t n_tokens, float* y,
+                              int32_t add_shared, void* workspace, size_t workspace_bytes, const smoe_trace* trace,
+                              int32_t path, void* hip_stream) {
+    return forward_impl(g, w, const_cast<float*>(x), n_tokens, y, add_shared, workspace, workspace_bytes, trace, path,
+                        hip_stream, nullptr, nullptr, 0.0f);
+}
+
+smoe_status smoe_forward_residual(const smoe_geom* g, const smoe_weights* w, const float* x_prev, const float* r_prev,
+                                  float eps, float* x, int32_t n_tokens, float* y, int32_t add_shared, void* workspace,
+                                  size_t workspace_bytes, const smoe_trace* trace, void* hip_stream) {
+    if (n_tokens > 0 && (!x_prev || !x)) return fail(SMOE_ENULL, "x_prev or x is NULL");
+    return forward_impl(g, w, x, n_tokens, y, add_shared, workspace, workspace_bytes, trace, SMOE_PATH_AUTO, hip_stream,
+                        x_prev, r_prev, eps);
 }
 
 smoe_status smoe_forward(const smoe_geom* g, const smoe_weights* w, const float* x, int32_t n_tokens, float* y,

@@ -132,43 +132,114 @@ __device__ __forceinline__ float q2_unit_dot(const uint32_t (&w)[9], float d0, f
 // fmaf(x, w, acc) == acc + x * w.  `xf` (f32) or `xb` (bf16 bits) supplies x.  With `ximg`, extra blocks
 // past the row blocks write the q8_1 images of the tile's x (the decode path's activations), eight q8_1 blocks
 // each, beside the logits instead of before them.
+// With `rprev` (the layer junction of a stack, fused; rows up to 4096): x = RMSNorm(xf + rprev) with unit
+// weight, formed as k_residual_rmsnorm forms it -- every work-group takes the scale of each token of its tile in
+// that order (per thread an fma chain over elements tid + 256 m, the wave butterfly, the wave sums in order)
+// while its weight row (or its image values) is in flight; a row block then stages x = (xf + rprev) * scale
+// from the same registers, an image block quantises its own (xf + rprev) * scale; row block 0 of each token
+// tile writes x to `xout`.
 template <int MAXC>
 __global__ __launch_bounds__(256) void k_router(const float* __restrict__ xf, const uint16_t* __restrict__ xb,
                                                  const uint16_t* __restrict__ W, const uint16_t* __restrict__ w_inp,
                                                  const float* __restrict__ bias, int H, int E, int rows_total, int T,
                                                  int tok_tile, float* __restrict__ logits, int ld_logits,
-                                                 float* __restrict__ sg, uint32_t* __restrict__ ximg, int img_natural) {
+                                                 float* __restrict__ sg, uint32_t* __restrict__ ximg, int img_natural,
+                                                 const float* __restrict__ rprev, float eps, float* __restrict__ xout) {
     extern __shared__ __align__(16) uint32_t smem[];
     __shared__ uint8_t qsc[8][32];
+    __shared__ float inv_s[16];
+    __shared__ float wsum_s[4][4];
     const int t0 = blockIdx.y * tok_tile;
     const int nt = min(tok_tile, T - t0);
     const int row_blocks = (rows_total + 3) / 4;
-    if ((int)blockIdx.x >= row_blocks) {  // an image block: eight q8_1 blocks of the tile's x, one per half wave
-        const int hw = threadIdx.x >> 5;
-        const int nb = nt * (H >> 5);
-        const int bb = ((int)blockIdx.x - row_blocks) * 8 + hw;
-        const bool live = bb < nb;
-        const size_t blk = (size_t)t0 * (H >> 5) + (live ? bb : 0);
-        const float v = live ? xf[blk * 32 + (threadIdx.x & 31)] : 0.0f;
-        q8_image_store(v, live, qsc[hw], ximg + blk * kImgDw, img_natural != 0);
-        return;
+    const bool img_block = (int)blockIdx.x >= row_blocks;  // uniform
+    const int tid = threadIdx.x;
+    // an image block: eight q8_1 blocks of the tile's x, one per half wave; its values are loaded first
+    const int hw = tid >> 5;
+    const int bb = ((int)blockIdx.x - row_blocks) * 8 + hw;
+    const bool live = img_block && bb < nt * (H >> 5);
+    const size_t blk = (size_t)t0 * (H >> 5) + (live ? bb : 0);
+    float iv = 0.0f, ir = 0.0f;
+    if (img_block) {
+        iv = live ? xf[blk * 32 + (tid & 31)] : 0.0f;
+        if (rprev && live) ir = rprev[blk * 32 + (tid & 31)];
     }
-    // the wave's weight row first (clamped, every load issued), so its latency overlaps the staging below
-    const int lane = threadIdx.x & 63;
-    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    // a row block: the wave's weight row (clamped, every load issued), in flight during the staging below
+    const int lane = tid & 63;
+    const int row = blockIdx.x * 4 + (tid >> 6);
     const int rowc = min(row, rows_total - 1);
     const uint16_t* wr = rowc < E ? W + (size_t)rowc * H : w_inp;
     const int chunks = H >> 3;
     uint4 wv[MAXC];
+    float bv = 0.0f;
+    if (!img_block) {
 #pragma unroll
-    for (int j = 0; j < MAXC; ++j) {
-        const int c = lane + 64 * j;
-        wv[j] = c < chunks ? *reinterpret_cast<const uint4*>(wr + 8 * c) : make_uint4(0, 0, 0, 0);
+        for (int j = 0; j < MAXC; ++j) {
+            const int c = lane + 64 * j;
+            wv[j] = c < chunks ? *reinterpret_cast<const uint4*>(wr + 8 * c) : make_uint4(0, 0, 0, 0);
+        }
+        bv = (bias && rowc < E) ? bias[rowc] : 0.0f;  // loaded once, outside the token loop
     }
-    const float bv = (bias && rowc < E) ? bias[rowc] : 0.0f;  // loaded once, outside the token loop
+    uint16_t* xs16 = reinterpret_cast<uint16_t*>(smem);
+    if (MAXC <= 8 && rprev) {  // the fused junction, 4 tokens at a time; a row block stages s * scale from registers
+        for (int tb = 0; tb < nt; tb += 4) {
+            constexpr int NM = MAXC <= 8 ? 2 * MAXC : 1;
+            float sv[4][NM];
+            float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                if (tb + g < nt) {
+                    const float* xr = xf + (size_t)(t0 + tb + g) * H;
+                    const float* rr = rprev + (size_t)(t0 + tb + g) * H;
+#pragma unroll
+                    for (int m = 0; m < NM; ++m) {  // 2 MAXC * 256 >= H
+                        const int j = tid + 256 * m;
+                        const int jc = j < H ? j : H - 1;
+                        sv[g][m] = xr[jc] + rr[jc];
+                        if (j < H) acc[g] = __builtin_fmaf(sv[g][m], sv[g][m], acc[g]);
+                    }
+                }
+            }
+            wave_sum_xor_fast_n<4>(acc);
+            if ((tid & 63) == 0) {
+#pragma unroll
+                for (int g = 0; g < 4; ++g) wsum_s[g][tid >> 6] = acc[g];
+            }
+            __syncthreads();
+            if (tid < 4 && tb + tid < nt) {
+                const float ss = ((wsum_s[tid][0] + wsum_s[tid][1]) + wsum_s[tid][2]) + wsum_s[tid][3];
+                inv_s[tb + tid] = 1.0f / __builtin_sqrtf(ss / (float)H + eps);
+            }
+            __syncthreads();
+            if (!img_block) {
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    if (tb + g < nt) {
+                        const float sc = inv_s[tb + g];
+                        float* xo = xout + (size_t)(t0 + tb + g) * H;
+#pragma unroll
+                        for (int m = 0; m < NM; ++m) {
+                            const int j = tid + 256 * m;
+                            if (j < H) {
+                                const float v = sv[g][m] * sc;
+                                xs16[(size_t)(tb + g) * H + j] = (uint16_t)f32_to_bf16(v);
+                                if (blockIdx.x == 0) xo[j] = v;
+                            }
+                        }
+                    }
+                }
+            }
+        }
+    }
+    if (img_block) {
+        float v = iv;
+        if (rprev && live) v = (iv + ir) * inv_s[bb / (H >> 5)];
+        q8_image_store(v, live, qsc[hw], ximg + blk * kImgDw, img_natural != 0);
+        return;
+    }
     // stage the tile, 8 vector loads in flight per thread
     const int n8 = nt * H / 8;  // groups of 8 values = one uint4 of bf16
-    for (int base = 0; base < n8; base += 256 * 4) {
+    for (int base = 0; !rprev && base < n8; base += 256 * 4) {
         uint4 v[4];
         if (xf) {
             float4 f[8];
@@ -1742,7 +1813,10 @@ hipError_t launch_prep(const float* x, int64_t n, uint8_t* xq, uint16_t* xb, hip
 
 hipError_t launch_router(const float* xf, const uint16_t* xb, const uint16_t* W, const uint16_t* w_inp,
                          const float* bias, int H, int E, int rows_total, int T, float* logits, int ld_logits, float* sg,
-                         uint32_t* ximg, int tile_rows, int img_natural, hipStream_t s) {
+                         uint32_t* ximg, int tile_rows, int img_natural, hipStream_t s, const float* rprev, float eps,
+                         float* xout) {
+    // the fused junction is the row-per-wave path's, for rows up to 4096
+    if (rprev && (tile_rows || !xf || H > 4096)) return hipErrorInvalidValue;
     const int chunks = H / 8;
     const int maxc = (chunks + 63) / 64;
     // tokens staged per block: 4 for decode batches (more blocks, short staging), 16 (<= 64 KiB of bf16) beyond
@@ -1768,7 +1842,7 @@ hipError_t launch_router(const float* xf, const uint16_t* xb, const uint16_t* W,
     const size_t lds = (size_t)tile * H * 2;
 #define SMOE_ROUTER(C)                                                                                          \
     hipLaunchKernelGGL(k_router<C>, grid, dim3(256), lds, s, xf, xb, W, w_inp, bias, H, E, rows_total, T, tile, \
-                       logits, ld_logits, sg, ximg, img_natural)
+                       logits, ld_logits, sg, ximg, img_natural, rprev, eps, xout)
     if (maxc <= 2) SMOE_ROUTER(2);
     else if (maxc <= 4) SMOE_ROUTER(4);
     else if (maxc <= 8) SMOE_ROUTER(8);

@@ -14,9 +14,10 @@ size_t img_bytes(int64_t n_blocks);      // bytes of n_blocks q8_1 images
 hipError_t launch_prep(const float* x, int64_t n, uint8_t* xq, uint16_t* xb, hipStream_t s);
 hipError_t launch_router(const float* xf, const uint16_t* xb, const uint16_t* W, const uint16_t* w_inp,
                          const float* bias, int H, int E, int rows_total, int T, float* logits, int ld_logits, float* sg,
-                         uint32_t* ximg, int tile_rows, int img_natural, hipStream_t s);
+                         uint32_t* ximg, int tile_rows, int img_natural, hipStream_t s, const float* rprev = nullptr,
+                         float eps = 0.0f, float* xout = nullptr);
 // (tile_rows: many tokens, row x token tiles from xb when given, else from xf; img_natural: write ximg in the IQ2_S
-// kernels' natural order)
+// kernels' natural order; rprev: the fused stack junction, x = RMSNorm(xf + rprev) written to xout)
 hipError_t launch_topk(const float* logits, int ld_logits, int T, int E, int k, int32_t* ids, float* wts, hipStream_t s);
 hipError_t launch_dispatch(const int32_t* ids, int P, int E, int32_t* counts, int32_t* offsets, int32_t* perm,
                            int32_t* slot, int32_t* elist, int32_t* n_list, int4* items, int max_items, int T, int k,

@@ -34,7 +34,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_status_strings():
     lib = S.lib()
-    assert lib.smoe_abi_version() == 102
+    assert lib.smoe_abi_version() == 103
     for code in (0, -1, -2, -3, -4, -5, -6):
         assert lib.smoe_status_str(code)
 
@@ -75,6 +75,26 @@ def test_forward_refusals_before_launch():
 
 def test_forward_zero_tokens_returns_ok_without_launching():
     assert _forward(S.Geom(), 0) == 0
+
+
+def test_forward_residual_refusals_before_launch():
+    """The fused stack junction refuses an x that overlaps x_prev, r_prev or y, a NULL r_prev and misaligned rows
+    before any launch; zero tokens return at once."""
+    L, g = S.lib(), S.Geom()
+    w = S._Weights(*([FAKE] * 8 + [None]))
+    R, X, Y = FAKE + (1 << 24), FAKE + (2 << 24), FAKE + (3 << 24)
+
+    def call(xp, rp, x, y, T=1):
+        return L.smoe_forward_residual(C.byref(g.c()), C.byref(w), xp, rp, 1e-6, x, T, y, 1, FAKE, 1 << 30, None,
+                                       None)
+
+    assert call(FAKE, R, X, Y, T=0) == 0
+    assert call(FAKE, R, FAKE, Y) == -1
+    assert call(FAKE, R, R + 256, Y) == -1
+    assert call(FAKE, R, X, X) == -1
+    assert call(FAKE, None, X, Y) == -6
+    assert call(None, R, X, Y) == -6
+    assert call(FAKE, R, X + 4, Y) == -5
 
 
 def test_stage_refusals_and_zero_counts():

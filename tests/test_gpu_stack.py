@@ -1,7 +1,8 @@
 """The stacked configuration (x_{l+1} = RMSNorm(x_l + MoE_l(x_l)), unit weight, eps 1e-6,
 over seeded layers) on a small stack through the C ABI: the decode contract bit for bit against the oracle's
 chain (or_moe_decode_dev, or_residual_rmsnorm_dev); the prefill contract layer by layer on the GPU's own layer
-inputs, routing exact and each layer within 1e-3 per row of or_moe_prefill, the junction bit for bit."""
+inputs, routing exact and each layer within 1e-3 per row of or_moe_prefill, the junction bit for bit; the fused
+junction (smoe_forward_residual) bit for bit against the junction and the call made apart."""
 import sys
 
 import numpy as np
@@ -81,3 +82,57 @@ def test_stack_prefill_layers_on_gpu_inputs(torch):
         yg = host(torch, y)
         xd = S.residual_rmsnorm(xd, y, EPS)
         assert np.array_equal(bits(host(torch, xd)), bits(O.residual_rmsnorm_dev(xg, yg, EPS))), l
+
+
+FUSED = [  # T, geometry, path the call takes
+    (1, GEOM, "GEMV, one token (fused into the routing gu kernel's router)"),
+    (3, GEOM, "GEMV, small batch"),
+    (5, GEOM, "GEMV, routed through the dispatch"),
+    (100, GEOM, "GEMV, token tiles of 16"),
+    (130, GEOM, "MFMA (junction kernel, then the call)"),
+    (1, {}, "GEMV, the bench geometry"),
+    (4, dict(n_embd=2560, n_ff=640, n_ff_shared=640, n_expert=64), "GEMV, H=2560"),
+]
+
+
+@pytest.mark.parametrize("case", range(len(FUSED)))
+def test_fused_junction_matches_separate_calls(torch, case):
+    T, gkw, what = FUSED[case]
+    say(f"case: fused junction T={T} {gkw or 'default'} ({what})")
+    g = S.Geom(**gkw)
+    H = g.n_embd
+    ml = S.MoELayer(g, S.synth_layer(g, 900 + case), max_tokens=T)
+    xp = O.gen_normal(80 + case, 100, T * H).reshape(T, H)
+    rp = O.gen_normal(81 + case, 100, T * H).reshape(T, H)
+    xpd, rpd = dev(torch, xp), dev(torch, rp)
+    x_ref = S.residual_rmsnorm(xpd, rpd, EPS)
+    y_ref = ml.forward(x_ref)
+    x = torch.full_like(xpd, 7.0)
+    y = ml.forward_residual(xpd, rpd, x, eps=EPS)
+    assert np.array_equal(bits(host(torch, x)), bits(O.residual_rmsnorm_dev(xp, rp, EPS))), "junction vs oracle"
+    assert np.array_equal(bits(host(torch, x)), bits(host(torch, x_ref))), "junction"
+    assert np.array_equal(bits(host(torch, y)), bits(host(torch, y_ref))), "layer output"
+    # y may be r_prev (the stack's own buffer reuse); x_prev and r_prev are left as they were otherwise
+    r2 = rpd.clone()
+    x2 = torch.empty_like(xpd)
+    ml.forward_residual(xpd, r2, x2, y=r2, eps=EPS)
+    assert np.array_equal(bits(host(torch, r2)), bits(host(torch, y_ref)))
+    assert np.array_equal(bits(host(torch, x2)), bits(host(torch, x_ref)))
+    assert np.array_equal(bits(host(torch, xpd)), bits(xp))
+
+
+def test_fused_stack_decode_chain_bitwise(torch):
+    say("case: stack of 3 with fused junctions, decode T=2")
+    T = 2
+    g, hostw, layers = stack(torch, T)
+    x = O.gen_normal(79, 100, T * g.n_embd).reshape(T, g.n_embd)
+    bufs = [dev(torch, x), torch.empty((T, g.n_embd), dtype=torch.float32, device="cuda")]
+    y = layers[0].forward(bufs[0], add_shared=True)
+    xh = x
+    yh = O.moe_decode_dev(g, hostw[0], xh, add_shared=True)
+    for l in range(1, N_LAYERS):
+        layers[l].forward_residual(bufs[(l - 1) % 2], y, bufs[l % 2], y=y, eps=EPS)
+        xh = O.residual_rmsnorm_dev(xh, yh, EPS)
+        yh = O.moe_decode_dev(g, hostw[l], xh, add_shared=True)
+        assert np.array_equal(bits(host(torch, bufs[l % 2])), bits(xh)), f"layer {l} junction"
+        assert np.array_equal(bits(host(torch, y)), bits(yh)), f"layer {l} MoE"
