@@ -417,10 +417,12 @@ __global__ __launch_bounds__(256) void k_router_tile(const float* __restrict__ x
     float acc[64];
 #pragma unroll
     for (int i = 0; i < 64; ++i) acc[i] = 0.0f;
-#pragma unroll
-    for (int j = 0; j < MAXC; ++j) {
+    // one chunk round; PARTIAL (only the last round can be): a lane past the last chunk adds 0 * 0 (acc is
+    // never -0), the other rounds need no masks
+    auto round = [&](int j, auto partial) {
+        constexpr bool PARTIAL = decltype(partial)::value;
         const int c = lane + 64 * j;
-        const bool live = c < chunks;  // only the last chunk round can be partial
+        const bool live = !PARTIAL || c < chunks;
         const int cc = live ? c : chunks - 1;
         float wf[4][8];
 #pragma unroll
@@ -445,11 +447,17 @@ __global__ __launch_bounds__(256) void k_router_tile(const float* __restrict__ x
             }
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                const float xv_e = live ? xe[e] : 0.0f;  // a lane past the last chunk adds 0 * 0 (acc is never -0)
+                const float xv_e = live ? xe[e] : 0.0f;
 #pragma unroll
                 for (int r = 0; r < 4; ++r) acc[4 * t + r] = __builtin_fmaf(xv_e, wf[r][e], acc[4 * t + r]);
             }
         }
+    };
+#pragma unroll
+    for (int j = 0; j < MAXC; ++j) {
+        if (64 * j >= chunks) break;  // uniform
+        if (64 * (j + 1) <= chunks) round(j, std::integral_constant<bool, false>{});
+        else round(j, std::integral_constant<bool, true>{});
     }
     const float v = reduce_scatter64(acc, lane);
     const int t = lane >> 2, row = row0 + (lane & 3);
@@ -621,26 +629,57 @@ __device__ __forceinline__ int wave_inclusive_scan(int x) {
     return x;
 }
 
-// Three exclusive scans over the 1024 threads of the block at once: a DPP scan inside each wave, the 16 wave
-// totals through LDS (scratch: 3 x 17 ints), then every wave scans the totals itself (one barrier).
-__device__ __forceinline__ void block_exclusive_scan3_1024(const int (&v)[3], int* scratch, int (&r)[3],
-                                                           int (&total)[3]) {
+// N exclusive scans over the 1024 threads of the block at once: a DPP scan inside each wave, the 16 wave
+// totals through LDS (scratch: N x 17 ints), then every wave scans the totals itself (one barrier).
+template <int N>
+__device__ __forceinline__ void block_exclusive_scan_1024(const int (&v)[N], int* scratch, int (&r)[N],
+                                                          int (&total)[N]) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    int incl[3];
+    int incl[N];
 #pragma unroll
-    for (int j = 0; j < 3; ++j) incl[j] = wave_inclusive_scan(v[j]);
+    for (int j = 0; j < N; ++j) incl[j] = wave_inclusive_scan(v[j]);
     if (lane == 63) {
 #pragma unroll
-        for (int j = 0; j < 3; ++j) scratch[17 * j + wave] = incl[j];
+        for (int j = 0; j < N; ++j) scratch[17 * j + wave] = incl[j];
     }
     __syncthreads();
 #pragma unroll
-    for (int j = 0; j < 3; ++j) {
+    for (int j = 0; j < N; ++j) {
         const int x = wave_inclusive_scan(lane < 16 ? scratch[17 * j + lane] : 0);
         const int before = wave > 0 ? __builtin_amdgcn_readlane(x, (wave - 1) & 15) : 0;
         r[j] = before + incl[j] - v[j];
         total[j] = __builtin_amdgcn_readlane(x, 15);
     }
+}
+
+// Per expert (thread tid < E of a 1024-thread block, c its pair count): the exclusive offsets, the position in
+// the touched list and the work-item classes of its pairs in chunks of at most `chunk` columns, longest first:
+// every expert's full chunks, then the remainders of more than chunk / 2 columns, then those of more than
+// chunk / 8, then the rest (each class in ascending expert order).  The longest work-groups start first, and
+// the short streaming ones fill in last.  (16-bit fields: E <= 1024.)
+struct ItemClasses {
+    int off, fpos, fbase, rbase, total, n_touched, n_full, n_rc;
+};
+__device__ __forceinline__ ItemClasses item_classes(int c, int chunk, int* scratch) {
+    const int flag = c > 0 ? 1 : 0;
+    const int nfull = c / chunk, rem = c - nfull * chunk;
+    const int wide = rem > (chunk >> 1) ? 1 : 0, mid = !wide && rem > (chunk >> 3) ? 1 : 0,
+              thin = rem > 0 && !wide && !mid ? 1 : 0;
+    int sc[4], tot[4];
+    block_exclusive_scan_1024<4>({c, flag | (wide << 16), mid | (thin << 16), nfull}, scratch, sc, tot);
+    ItemClasses ic;
+    ic.off = sc[0];
+    ic.fpos = sc[1] & 0xFFFF;
+    ic.fbase = sc[3];
+    ic.total = tot[0];
+    ic.n_touched = tot[1] & 0xFFFF;
+    ic.n_full = tot[3];
+    const int n_wide = tot[1] >> 16, n_mid = tot[2] & 0xFFFF, n_thin = tot[2] >> 16;
+    ic.n_rc = ic.n_full + n_wide + n_mid + n_thin;
+    ic.rbase = wide  ? ic.n_full + (sc[1] >> 16)
+               : mid ? ic.n_full + n_wide + (sc[2] & 0xFFFF)
+                     : ic.n_full + n_wide + n_mid + (sc[2] >> 16);
+    return ic;
 }
 
 constexpr int kDispatchIdRegs = 4;                      // passes of 1024 pairs whose ids stay in registers
@@ -650,14 +689,12 @@ struct DispatchLds {
     int run[1024];
     int el[1024];
     uint8_t wcnt[16][1024];
-    int scan[3 * 17];
+    int scan[4 * 17];
     int perm[kDispatchLdsPairs];  // the first pairs' dispatch order, for the work items
 };
 
 // With `items`, also the work-item table: the shared expert's tokens in chunks of `sh_chunk`, then the routed
-// experts' pairs in chunks of at most `chunk` columns, longest first: every expert's full chunks, then the
-// remainders of more than chunk / 2 columns, then the shorter remainders (each class in ascending expert
-// order), then empty items up to max_items.  The longest work-groups start first.
+// experts' pairs in the classes of item_classes, then empty items up to max_items.
 __device__ __forceinline__ void dispatch_block(const int32_t* __restrict__ ids, int P, int E, int32_t* __restrict__ counts,
                                int32_t* __restrict__ offsets, int32_t* __restrict__ perm, int32_t* __restrict__ slot,
                                int32_t* __restrict__ elist, int32_t* __restrict__ n_list, DispatchLds& s,
@@ -681,15 +718,10 @@ __device__ __forceinline__ void dispatch_block(const int32_t* __restrict__ ids, 
     __syncthreads();
     const int c = tid < E ? s.cnt[tid] : 0;
     const int flag = c > 0 ? 1 : 0;
-    const int nfull = c / chunk, rem = c - nfull * chunk;
-    const int wide = rem > (chunk >> 1) ? 1 : 0, narrow = rem > 0 && !wide ? 1 : 0;
-    int sc[3], tot[3];
-    // 11-bit fields (E <= 1024): touched flag, wide remainder, narrow remainder
-    block_exclusive_scan3_1024({c, flag | (wide << 11) | (narrow << 22), nfull}, s.scan, sc, tot);
-    const int off = sc[0], fpos = sc[1] & 0x7FF, fbase = sc[2];
-    const int total = tot[0], n_touched = tot[1] & 0x7FF, n_full = tot[2];
-    const int n_wide = (tot[1] >> 11) & 0x7FF, n_rc = n_full + n_wide + ((tot[1] >> 22) & 0x7FF);
-    const int rbase = wide ? n_full + ((sc[1] >> 11) & 0x7FF) : n_full + n_wide + ((sc[1] >> 22) & 0x7FF);
+    const int nfull = c / chunk;
+    const ItemClasses ic = item_classes(c, chunk, s.scan);
+    const int off = ic.off, fpos = ic.fpos, fbase = ic.fbase, rbase = ic.rbase;
+    const int total = ic.total, n_touched = ic.n_touched, n_rc = ic.n_rc;
     if (tid < E) {
         if (counts) counts[tid] = c;
         offsets[tid] = off;
@@ -812,20 +844,16 @@ __global__ __launch_bounds__(1024) void k_dispatch_scan(int32_t* __restrict__ hi
                                                          int32_t* __restrict__ elist, int32_t* __restrict__ n_list,
                                                          int4* __restrict__ items, int32_t* __restrict__ item_of,
                                                          int max_items, int T, int has_shared, int chunk, int sh_chunk) {
-    __shared__ int scan[3 * 17];
+    __shared__ int scan[4 * 17];
     const int tid = threadIdx.x;
     int c = 0;
     if (tid < E)
         for (int ch = 0; ch < n_chunks; ++ch) c += hist[(size_t)ch * E + tid];
     const int flag = c > 0 ? 1 : 0;
-    const int nfull = c / chunk, rem = c - nfull * chunk;
-    const int wide = rem > (chunk >> 1) ? 1 : 0, narrow = rem > 0 && !wide ? 1 : 0;
-    int sc[3], tot[3];
-    block_exclusive_scan3_1024({c, flag | (wide << 11) | (narrow << 22), nfull}, scan, sc, tot);
-    const int off = sc[0], fpos = sc[1] & 0x7FF, fbase = sc[2];
-    const int total = tot[0], n_touched = tot[1] & 0x7FF, n_full = tot[2];
-    const int n_wide = (tot[1] >> 11) & 0x7FF, n_rc = n_full + n_wide + ((tot[1] >> 22) & 0x7FF);
-    const int rbase = wide ? n_full + ((sc[1] >> 11) & 0x7FF) : n_full + n_wide + ((sc[1] >> 22) & 0x7FF);
+    const int nfull = c / chunk;
+    const ItemClasses ic = item_classes(c, chunk, scan);
+    const int off = ic.off, fpos = ic.fpos, fbase = ic.fbase, rbase = ic.rbase;
+    const int total = ic.total, n_touched = ic.n_touched, n_rc = ic.n_rc;
     const int n_sh = has_shared ? (T + sh_chunk - 1) / sh_chunk : 0;
     if (tid < E) {
         if (counts) counts[tid] = c;

@@ -74,6 +74,10 @@ CASES = [
     # 20000 pairs over 20 dispatch chunks, a hot expert whose pairs span every chunk and many work items
     ("many pairs, hot expert", dict(n_embd=256, n_ff=128, n_ff_shared=128, n_expert=64, top_k=8), 2500, 16, True,
      ("hot", 9), S.PATH_AUTO),
+    # 1024 experts, every one touched, almost all with a remainder item of 2..64 columns: the item-class counts
+    # reach 1024 (the packed scan fields must hold it)
+    ("1024 experts all touched", dict(n_embd=256, n_ff=128, n_ff_shared=128, n_expert=1024, top_k=8), 2048, 18,
+     True, None, S.PATH_AUTO),
 ]
 
 _LAYERS = {}
@@ -118,6 +122,8 @@ def test_forward_prefill_parity(torch, case):
     assert err.max() <= TOL
     if name.startswith("hot"):
         assert counts.max() > 2 * S.MFMA_CHUNK, "the hot expert does not span three work items"
+    if name.startswith("1024"):
+        assert (counts > 0).all() and counts.max() <= S.MFMA_CHUNK // 2, "not every expert holds a short remainder"
     if name.startswith("golden"):
         f = np.load(os.path.join(GOLD, "layer_prefill.npz"))
         assert np.array_equal(bits(x), bits(f["x"]))
