@@ -116,33 +116,43 @@ __device__ __forceinline__ void expand_codes(uint32_t cw, uint32_t dbits, f16x8&
 //                           columns 64 (w / 4) .. + 63;
 //   narrow (17..64 columns): 5 stages of 64 columns; wave w owns the rows of row group w (two sets) and every
 //                           column;
-//   thin (<= 16 columns):   8 stages of 16 columns (more weight stages in flight for the streaming work-groups),
-//                           rows as narrow.
-constexpr int kTokPieces = 17;
+//   thin (<= 16 columns):   2 stages of four units each for 16 columns, rows as narrow: these work-groups stream
+//                           weights, and a four-unit stage brings each row's weights as one 144-byte window
+//                           (its columns as 65 pieces: 8 records and a pad).  They run at ~13 GB/s of weights
+//                           per CU whatever the depth (a third stage for 8 columns was slower), so the depth
+//                           stays at one stage in flight.
 constexpr int kWgRows = 256;
-constexpr int kWPieces = kWgRows * 3;
-constexpr int kWIns = kWPieces / 64;
 constexpr int kWaves = 8;
 constexpr uint32_t kOob = 0x80000000u;
 constexpr int kRing = 148480;           // bytes of the stage ring
 constexpr int kDummy = kRing;           // 1 KB landing slot of the padding instructions
 constexpr int kLds = kRing + 1024;
 
-// MODE 0 (thin, <= 16 columns): 8 stages of 16 columns, rows as narrow.
+// MODE 0 (thin, <= kThinCols columns): stages of four units each (see below), rows as narrow.
 enum { kThin = 0, kNarrow = 1, kWide = 2 };
+constexpr int kThinCols = 16;
 template <int MODE>
 struct Shape {
     static constexpr bool WIDE = MODE == kWide;
-    static constexpr int kTok = MODE == kWide ? 128 : MODE == kNarrow ? 64 : 16;
-    static constexpr int kStages = MODE == kWide ? 3 : MODE == kNarrow ? 5 : 8;
+    static constexpr int kTok = MODE == kWide ? 128 : MODE == kNarrow ? 64 : kThinCols;
+    static constexpr int kStages = MODE == kWide ? 3 : MODE == kNarrow ? 5 : 2;
     static constexpr int NS = WIDE ? 4 : 2;
-    static constexpr int kAPieces = (kTok * kTokPieces + 63) / 64 * 64;  // whole DMA instructions
+    // units of 128 values per stage: the thin shape streams weights, four units at a time, so that a row's
+    // weights arrive as one 144-byte window (16-byte aligned, 9 pieces) instead of four 48-byte ones
+    static constexpr int UPS = MODE == kThin ? 4 : 1;
+    static constexpr int kColPieces = 16 * UPS + 1;                // a column's records, then one pad piece
+    static constexpr int kRowPieces = UPS == 1 ? 3 : 9 * UPS / 4;  // a row's weight window
+    static constexpr int kRowDw = 4 * kRowPieces;
+    static constexpr int kAPieces = (kTok * kColPieces + 63) / 64 * 64;  // whole DMA instructions
     static constexpr int kAIns = kAPieces / 64;
+    static constexpr int kWPieces = kWgRows * kRowPieces;
+    static constexpr int kWIns = kWPieces / 64;
     static constexpr int kASlots = (kAIns + kWaves - 1) / kWaves;
     static constexpr int kWSlots = (kWIns + kWaves - 1) / kWaves;
     static constexpr int kSlots = kASlots + kWSlots;
     static constexpr int kABytes = kAPieces * 16;
     static constexpr int kStage = kABytes + kWPieces * 16;
+    static_assert(UPS == 1 || UPS == 4, "one or four units per stage");
     static_assert(kAPieces % 64 == 0 && kWPieces % 64 == 0, "whole DMA instructions");
     static_assert(kStages * kStage <= kRing, "ring");
     static_assert((kStages - 2) * kSlots <= 63, "vmcnt range");
@@ -198,8 +208,8 @@ struct MmPlan {
 #pragma unroll
         for (int m = 0; m < S::kASlots; ++m) {
             const int j = wave + kWaves * m;
-            const int P = 64 * j + lane, t = P / kTokPieces, p = P - kTokPieces * t;
-            const bool live = j < S::kAIns && t < ncol && p < 16;
+            const int P = 64 * j + lane, t = P / S::kColPieces, p = P - S::kColPieces * t;
+            const bool live = j < S::kAIns && t < ncol && p < 16 * S::UPS;
             const int row = rowidx[t < ncol ? t : 0];
             a_off[m] = live ? (uint32_t)(row * rpr * kRecBytes + 16 * p) : kOob;
             a_at[m] = j < S::kAIns ? 1024 * j : -1;
@@ -207,20 +217,22 @@ struct MmPlan {
 #pragma unroll
         for (int m = 0; m < S::kWSlots; ++m) {
             const int j = wave + kWaves * m;
-            const int P = 64 * j + lane, row = P / 3, p = P - 3 * row;
-            const bool real = j < kWIns;
+            const int P = 64 * j + lane, row = P / S::kRowPieces, p = P - S::kRowPieces * row;
+            const bool real = j < S::kWIns;
             const int r = row >= split ? row - split : row;
-            w_rsrc[m] = 64 * j >= 3 * split ? rw1 : rw0;  // whole instructions: 3 * split is a multiple of 64
+            static_assert((S::kRowPieces * 128) % 64 == 0, "whole instructions per weight tensor");
+            w_rsrc[m] = 64 * j >= S::kRowPieces * split ? rw1 : rw0;  // whole instructions per tensor
             w_off[m] = real ? (uint32_t)r * rb + 16u * p : kOob;
             w_at[m] = real ? S::kABytes + 1024 * j : -1;
         }
     }
 
-    // Issue unit u into ring stage b.
+    // Issue the stage of units u .. u + UPS - 1 into ring stage b (u a multiple of UPS).  One unit: the row's
+    // 48-byte window starts at the 16-byte boundary at or below the unit; four: at the unit (36 u = 144 u / 4).
     __device__ __forceinline__ void issue(uint32_t lds0, int b, int u, i32x4 ra) const {
         const uint32_t st = (uint32_t)(b * S::kStage);
         const uint32_t sa = __builtin_amdgcn_readfirstlane((uint32_t)u * (2 * kRecBytes));
-        const uint32_t sw = __builtin_amdgcn_readfirstlane((uint32_t)(36 * u - 4 * (u & 3)));
+        const uint32_t sw = __builtin_amdgcn_readfirstlane((uint32_t)(S::UPS == 1 ? 36 * u - 4 * (u & 3) : 36 * u));
 #pragma unroll
         for (int m = 0; m < S::kASlots; ++m) {
             const uint32_t at = a_at[m] < 0 ? (uint32_t)kDummy : st + (uint32_t)a_at[m];
@@ -234,11 +246,12 @@ struct MmPlan {
     }
 };
 
-// One staged unit: the activation fragments of all NT column tiles (columns tok0 + 16 n ..) are loaded first;
-// then for each block h and row set s (LDS row rows[s]; the unit starts `wofs` dwords into the row's window)
+// One staged unit: the activation fragments of all NT column tiles (columns tok0 + 16 n ..; CP pieces per column
+// in LDS, A at the unit's first piece) are loaded first; then for each block h and row set s (LDS row rows[s] of
+// RD dwords; the unit starts `wofs` dwords into the row's window)
 // the set's B operands are expanded and fed to every tile: acc[n][s] += A0 B0 + A1 B1.  Set s + 1 is expanded
 // while the matrix cores work on set s.
-template <int NS, int NT>
+template <int NS, int NT, int CP = 17, int RD = 12>
 __device__ __forceinline__ void mm_unit(f32x4 (&acc)[4][NS], const uint32_t* W, int wofs, const int (&rows)[NS],
                                         const uint4* A, int tok0, int i, int q) {
     f16x8 a[2][NT][2];
@@ -246,7 +259,7 @@ __device__ __forceinline__ void mm_unit(f32x4 (&acc)[4][NS], const uint32_t* W, 
     for (int h = 0; h < 2; ++h)
 #pragma unroll
         for (int n = 0; n < NT; ++n) {
-            const uint4* ar = A + (tok0 + 16 * n + i) * kTokPieces + 8 * h;
+            const uint4* ar = A + (tok0 + 16 * n + i) * CP + 8 * h;
             a[h][n][0] = __builtin_bit_cast(f16x8, ar[q]);
             a[h][n][1] = __builtin_bit_cast(f16x8, ar[4 + q]);
         }
@@ -254,7 +267,7 @@ __device__ __forceinline__ void mm_unit(f32x4 (&acc)[4][NS], const uint32_t* W, 
     for (int h = 0; h < 2; ++h) {
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
-            const uint32_t* w = W + rows[s] * 12 + wofs;
+            const uint32_t* w = W + rows[s] * RD + wofs;
             const uint32_t cw = h == 0 ? __builtin_amdgcn_alignbyte(w[q + 1], w[q], 2) : w[5 + q];
             const uint32_t db = h == 0 ? (w[0] & 0xFFFFu) : (w[4] >> 16);
             f16x8 b0, b1;
@@ -268,8 +281,8 @@ __device__ __forceinline__ void mm_unit(f32x4 (&acc)[4][NS], const uint32_t* W, 
     }
 }
 
-// The K loop of both kernels: units of 128 values through the ring, kStages - 1 units in flight.  NT: the
-// wave's live column tiles.
+// The K loop of both kernels: stages of UPS units of 128 values through the ring, kStages - 1 stages in flight.
+// NT: the wave's live column tiles.
 template <int MODE, int NT>
 __device__ __forceinline__ void mm_loop_nt(f32x4 (&acc)[4][Shape<MODE>::NS], uint8_t* lds, const MmPlan<MODE>& pl,
                                            int units, i32x4 ra, const int (&rows)[Shape<MODE>::NS], int tok0, int i,
@@ -277,28 +290,38 @@ __device__ __forceinline__ void mm_loop_nt(f32x4 (&acc)[4][Shape<MODE>::NS], uin
     using S = Shape<MODE>;
     constexpr int ST = S::kStages;
     const uint32_t lds0 = lds_addr(lds);
+    const int nst = (units + S::UPS - 1) / S::UPS;
+    auto stage = [&](int g, int b) {  // the units of stage g, in ring stage b
+        const uint8_t* stg = lds + b * S::kStage;
+        const uint32_t* W = reinterpret_cast<const uint32_t*>(stg + S::kABytes);
+        const uint4* A = reinterpret_cast<const uint4*>(stg);
+        if constexpr (S::UPS == 1) {
+            mm_unit<S::NS, NT>(acc, W, g & 3, rows, A, tok0, i, q);
+        } else {
+#pragma unroll
+            for (int uu = 0; uu < S::UPS; ++uu)
+                if (S::UPS * g + uu < units)
+                    mm_unit<S::NS, NT, S::kColPieces, S::kRowDw>(acc, W, 9 * uu, rows, A + 16 * uu, tok0, i, q);
+        }
+    };
 #pragma unroll
     for (int b = 0; b < ST - 1; ++b)
-        if (b < units) pl.issue(lds0, b, b, ra);
-    int b = 0, u = 0;  // ring stage of unit u
-    // steady state: every iteration consumes unit u, with the ST - 2 units after it still in flight, and issues
-    // unit u + ST - 1 (a constant wait, no test)
-    for (; u + ST - 1 < units; ++u) {
+        if (b < nst) pl.issue(lds0, b, S::UPS * b, ra);
+    int b = 0, g = 0;  // ring stage of stage g
+    // steady state: every iteration consumes stage g, with the ST - 2 stages after it still in flight, and issues
+    // stage g + ST - 1 (a constant wait, no test)
+    for (; g + ST - 1 < nst; ++g) {
         vmcnt<(ST - 2) * S::kSlots>();
-        __syncthreads();  // unit u is in LDS for everyone; everyone is done with unit u - 1
-        pl.issue(lds0, b == 0 ? ST - 1 : b - 1, u + ST - 1, ra);
-        const uint8_t* stg = lds + b * S::kStage;
-        mm_unit<S::NS, NT>(acc, reinterpret_cast<const uint32_t*>(stg + S::kABytes), u & 3, rows,
-                           reinterpret_cast<const uint4*>(stg), tok0, i, q);
+        __syncthreads();  // stage g is in LDS for everyone; everyone is done with stage g - 1
+        pl.issue(lds0, b == 0 ? ST - 1 : b - 1, S::UPS * (g + ST - 1), ra);
+        stage(g, b);
         b = b + 1 == ST ? 0 : b + 1;
     }
-    // the last units (all of them when there are fewer than ST - 1): nothing left to issue, the waits shrink
-    for (; u < units; ++u) {
-        wait_stages<S::kSlots>(units - 1 - u);
+    // the last stages (all of them when there are fewer than ST - 1): nothing left to issue, the waits shrink
+    for (; g < nst; ++g) {
+        wait_stages<S::kSlots>(nst - 1 - g);
         __syncthreads();
-        const uint8_t* stg = lds + b * S::kStage;
-        mm_unit<S::NS, NT>(acc, reinterpret_cast<const uint32_t*>(stg + S::kABytes), u & 3, rows,
-                           reinterpret_cast<const uint4*>(stg), tok0, i, q);
+        stage(g, b);
         b = b + 1 == ST ? 0 : b + 1;
     }
 }
@@ -413,7 +436,7 @@ __global__ __launch_bounds__(512) void k_mm_gu(const uint8_t* __restrict__ gate_
     const uint8_t* g0 = item.shared ? gate_sh : gate_exps + (size_t)item.e * F * rb;
     const uint8_t* u0 = item.shared ? up_sh : up_exps + (size_t)item.e * F * rb;
     if (ncol > 64) mm_gu_body<kWide>(lds, rowidx, item, ncol, g0, u0, xrec, xrec_bytes, H, hrec, h_rec);
-    else if (ncol > 16) mm_gu_body<kNarrow>(lds, rowidx, item, ncol, g0, u0, xrec, xrec_bytes, H, hrec, h_rec);
+    else if (ncol > kThinCols) mm_gu_body<kNarrow>(lds, rowidx, item, ncol, g0, u0, xrec, xrec_bytes, H, hrec, h_rec);
     else mm_gu_body<kThin>(lds, rowidx, item, ncol, g0, u0, xrec, xrec_bytes, H, hrec, h_rec);
 }
 
@@ -482,7 +505,7 @@ __global__ __launch_bounds__(512) void k_mm_down(const uint8_t* __restrict__ dow
     const int units = Fe >> 7;
     const uint8_t* d0 = item.shared ? down_sh : down_exps + (size_t)item.e * H * ((size_t)(F >> 7) * 36);
     if (ncol > 64) mm_down_body<kWide>(lds, rowidx, item, ncol, units, d0, hrec, hrec_bytes, h_rec, sg, H, Y);
-    else if (ncol > 16) mm_down_body<kNarrow>(lds, rowidx, item, ncol, units, d0, hrec, hrec_bytes, h_rec, sg, H, Y);
+    else if (ncol > kThinCols) mm_down_body<kNarrow>(lds, rowidx, item, ncol, units, d0, hrec, hrec_bytes, h_rec, sg, H, Y);
     else mm_down_body<kThin>(lds, rowidx, item, ncol, units, d0, hrec, hrec_bytes, h_rec, sg, H, Y);
 }
 
