@@ -112,15 +112,15 @@ __device__ __forceinline__ void expand_codes(uint32_t cw, uint32_t dbits, f16x8&
 // (range-checked: no memory access, zeros written), so a short item moves only its own activation bytes.
 //
 // Three work-group shapes share one LDS ring (the item's column count picks one):
-//   wide (65..128 columns): 3 stages of 128 columns; wave w owns rows of row group w % 4 (four 16-row sets) and
-//                           columns 64 (w / 4) .. + 63;
-//   narrow (17..64 columns): 5 stages of 64 columns; wave w owns the rows of row group w (two sets) and every
-//                           column;
+//   wide (65..128 columns): 3 stages of 128 columns;
+//   narrow (17..64 columns): 5 stages of 64 columns;
 //   thin (<= 16 columns):   2 stages of four units each for 16 columns, rows as narrow: these work-groups stream
 //                           weights, and a four-unit stage brings each row's weights as one 144-byte window
 //                           (its columns as 65 pieces: 8 records and a pad).  They run at ~13 GB/s of weights
 //                           per CU whatever the depth (a third stage for 8 columns was slower), so the depth
 //                           stays at one stage in flight.
+// In every shape wave w owns two 16-row sets (gate/up: gate rows 16 w .. + 15 and the same up rows; down: rows
+// 32 w .. + 31) and every column, so each row's codes are expanded once per work-group.
 constexpr int kWgRows = 256;
 constexpr int kWaves = 8;
 constexpr uint32_t kOob = 0x80000000u;
@@ -130,13 +130,14 @@ constexpr int kLds = kRing + 1024;
 
 // MODE 0 (thin, <= kThinCols columns): stages of four units each (see below), rows as narrow.
 enum { kThin = 0, kNarrow = 1, kWide = 2 };
+constexpr int kMaxTiles = 8;  // column tiles of 16 per wave at most (the wide shape's 128 columns)
 constexpr int kThinCols = 16;
 template <int MODE>
 struct Shape {
-    static constexpr bool WIDE = MODE == kWide;
     static constexpr int kTok = MODE == kWide ? 128 : MODE == kNarrow ? 64 : kThinCols;
+    static constexpr int MT = (kTok + 15) / 16;  // column tiles of a wave: every wave has every column
     static constexpr int kStages = MODE == kWide ? 3 : MODE == kNarrow ? 5 : 2;
-    static constexpr int NS = WIDE ? 4 : 2;
+    static constexpr int NS = 2;
     // units of 128 values per stage: the thin shape streams weights, four units at a time, so that a row's
     // weights arrive as one 144-byte window (16-byte aligned, 9 pieces) instead of four 48-byte ones
     static constexpr int UPS = MODE == kThin ? 4 : 1;
@@ -252,7 +253,7 @@ struct MmPlan {
 // the set's B operands are expanded and fed to every tile: acc[n][s] += A0 B0 + A1 B1.  Set s + 1 is expanded
 // while the matrix cores work on set s.
 template <int NS, int NT, int CP = 17, int RD = 12>
-__device__ __forceinline__ void mm_unit(f32x4 (&acc)[4][NS], const uint32_t* W, int wofs, const int (&rows)[NS],
+__device__ __forceinline__ void mm_unit(f32x4 (&acc)[kMaxTiles][NS], const uint32_t* W, int wofs, const int (&rows)[NS],
                                         const uint4* A, int tok0, int i, int q) {
     f16x8 a[2][NT][2];
 #pragma unroll
@@ -284,7 +285,7 @@ __device__ __forceinline__ void mm_unit(f32x4 (&acc)[4][NS], const uint32_t* W, 
 // The K loop of both kernels: stages of UPS units of 128 values through the ring, kStages - 1 stages in flight.
 // NT: the wave's live column tiles.
 template <int MODE, int NT>
-__device__ __forceinline__ void mm_loop_nt(f32x4 (&acc)[4][Shape<MODE>::NS], uint8_t* lds, const MmPlan<MODE>& pl,
+__device__ __forceinline__ void mm_loop_nt(f32x4 (&acc)[kMaxTiles][Shape<MODE>::NS], uint8_t* lds, const MmPlan<MODE>& pl,
                                            int units, i32x4 ra, const int (&rows)[Shape<MODE>::NS], int tok0, int i,
                                            int q) {
     using S = Shape<MODE>;
@@ -327,30 +328,37 @@ __device__ __forceinline__ void mm_loop_nt(f32x4 (&acc)[4][Shape<MODE>::NS], uin
 }
 
 template <int MODE>
-__device__ __forceinline__ void mm_loop(f32x4 (&acc)[4][Shape<MODE>::NS], uint8_t* lds, const MmPlan<MODE>& pl,
+__device__ __forceinline__ void mm_loop(f32x4 (&acc)[kMaxTiles][Shape<MODE>::NS], uint8_t* lds, const MmPlan<MODE>& pl,
                                         int units, i32x4 ra, const int (&rows)[Shape<MODE>::NS], int tok0, int ntiles,
                                         int i, int q) {
 #pragma unroll
-    for (int n = 0; n < 4; ++n)
+    for (int n = 0; n < kMaxTiles; ++n)
 #pragma unroll
         for (int s = 0; s < Shape<MODE>::NS; ++s) acc[n][s] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     if constexpr (MODE == kThin) {  // one tile
         mm_loop_nt<MODE, 1>(acc, lds, pl, units, ra, rows, tok0, i, q);
         return;
-    }
-    switch (ntiles) {  // wave-uniform; every wave has 1 .. 4 live tiles
-        case 1: mm_loop_nt<MODE, 1>(acc, lds, pl, units, ra, rows, tok0, i, q); break;
-        case 2: mm_loop_nt<MODE, 2>(acc, lds, pl, units, ra, rows, tok0, i, q); break;
-        case 3: mm_loop_nt<MODE, 3>(acc, lds, pl, units, ra, rows, tok0, i, q); break;
-        default: mm_loop_nt<MODE, 4>(acc, lds, pl, units, ra, rows, tok0, i, q); break;
+    } else if constexpr (MODE == kNarrow) {
+        switch (ntiles) {  // work-group-uniform: 2 .. 4 live tiles
+            case 1: mm_loop_nt<MODE, 1>(acc, lds, pl, units, ra, rows, tok0, i, q); break;
+            case 2: mm_loop_nt<MODE, 2>(acc, lds, pl, units, ra, rows, tok0, i, q); break;
+            case 3: mm_loop_nt<MODE, 3>(acc, lds, pl, units, ra, rows, tok0, i, q); break;
+            default: mm_loop_nt<MODE, 4>(acc, lds, pl, units, ra, rows, tok0, i, q); break;
+        }
+    } else {
+        switch (ntiles) {  // work-group-uniform: 5 .. 8 live tiles
+            case 5: mm_loop_nt<MODE, 5>(acc, lds, pl, units, ra, rows, tok0, i, q); break;
+            case 6: mm_loop_nt<MODE, 6>(acc, lds, pl, units, ra, rows, tok0, i, q); break;
+            case 7: mm_loop_nt<MODE, 7>(acc, lds, pl, units, ra, rows, tok0, i, q); break;
+            default: mm_loop_nt<MODE, 8>(acc, lds, pl, units, ra, rows, tok0, i, q); break;
+        }
     }
 }
 
 // ------------------------------------------------------------------------------------------------ gate/up
 // Grid (Fmax / 128, work items), 8 waves.  Work-group rt computes gate and up rows [128 rt, 128 rt + 128) for the
 // item's (at most 128) columns, then h = bf16(silu(gate) * up) into records 2 rt and 2 rt + 1 of each column's h
-// row.  Wide: wave w has gate rows 32 (w % 4) .. + 31 (sets 0, 1) and the same up rows (sets 2, 3); narrow: gate
-// rows 16 w .. + 15 (set 0) and the same up rows (set 1).
+// row.  Wave w has gate rows 16 w .. + 15 (set 0) and the same up rows (set 1).
 // SwiGLU of the prefill contract: silu(g) * u with the hardware exp2 and reciprocal (a few ulp).  h is rounded to
 // bf16 next and the contract is held to 1e-3 per row; the decode contract keeps silu_mul's exact order.
 __device__ __forceinline__ float silu_mul_fast(float g, float u) {
@@ -363,7 +371,6 @@ __device__ __forceinline__ void mm_gu_body(uint8_t* lds, const int* rowidx, cons
                                            const uint8_t* g0, const uint8_t* u0, const uint32_t* xrec,
                                            uint32_t xrec_bytes, int H, uint32_t* hrec, int h_rec) {
     using S = Shape<MODE>;
-    constexpr bool WIDE = S::WIDE;
     constexpr int NS = S::NS;
     const int rt = blockIdx.x;
     const int units = H >> 7;
@@ -376,21 +383,12 @@ __device__ __forceinline__ void mm_gu_body(uint8_t* lds, const int* rowidx, cons
     MmPlan<MODE> pl;
     pl.init(rowidx, wave, lane, ncol, H >> 6, rb, 128, rg0, ru0);
     int rows[NS];
-    int fbase;  // first of the wave's gate rows within the work-group's 128
-    if constexpr (WIDE) {
-        fbase = 32 * (wave & 3);
-        rows[0] = fbase + i;
-        rows[1] = fbase + 16 + i;
-        rows[2] = 128 + fbase + i;
-        rows[3] = 128 + fbase + 16 + i;
-    } else {
-        fbase = 16 * wave;
-        rows[0] = fbase + i;
-        rows[1] = 128 + fbase + i;
-    }
-    const int tok0 = WIDE ? 64 * (wave >> 2) : 0;
-    const int ntiles = min(4, max(0, (ncol - tok0 + 15) >> 4));
-    f32x4 acc[4][NS];
+    const int fbase = 16 * wave;  // first of the wave's gate rows within the work-group's 128
+    rows[0] = fbase + i;
+    rows[1] = 128 + fbase + i;
+    const int tok0 = 0;
+    const int ntiles = min(S::MT, (ncol + 15) >> 4);
+    f32x4 acc[kMaxTiles][NS];
     mm_loop<MODE>(acc, lds, pl, units, ra, rows, tok0, ntiles, i, q);
     __syncthreads();  // every wave is done with the ring: its start becomes the h tile
     // h tile [column][128 rows in record order] as fp16 bits of bf16 values
@@ -400,7 +398,7 @@ __device__ __forceinline__ void mm_gu_body(uint8_t* lds, const int* rowidx, cons
         const int f = fbase + 16 * s + i;
         const int pos = 64 * (f >> 6) + rec_pos(f & 63);
 #pragma unroll
-        for (int n = 0; n < 4; ++n) {
+        for (int n = 0; n < S::MT; ++n) {
             if (n < ntiles) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
@@ -442,14 +440,13 @@ __global__ __launch_bounds__(512) void k_mm_gu(const uint8_t* __restrict__ gate_
 
 // ------------------------------------------------------------------------------------------------ down
 // Grid (H / 256, work items), 8 waves.  Work-group rt computes down rows [256 rt, 256 rt + 256) of the item's
-// columns into Y[first + c] (the shared expert's rows times sigmoid(sg[t])).  Wide: wave w has rows
-// 64 (w % 4) .. + 63 (four sets); narrow: rows 32 w .. + 31 (two sets).
+// columns into Y[first + c] (the shared expert's rows times sigmoid(sg[t])).  Wave w has rows 32 w .. + 31
+// (two sets).
 template <int MODE>
 __device__ __forceinline__ void mm_down_body(uint8_t* lds, const int* rowidx, const Item& item, int ncol, int units,
                                              const uint8_t* d0, const uint32_t* hrec, uint32_t hrec_bytes, int h_rec,
                                              const float* sg, int H, float* Y) {
     using S = Shape<MODE>;
-    constexpr bool WIDE = S::WIDE;
     constexpr int NS = S::NS;
     const int rt = blockIdx.x;
     const uint32_t rb = (uint32_t)units * 36u;
@@ -461,19 +458,19 @@ __device__ __forceinline__ void mm_down_body(uint8_t* lds, const int* rowidx, co
     MmPlan<MODE> pl;
     pl.init(rowidx, wave, lane, ncol, h_rec, rb, kWgRows, rd, rd);
     int rows[NS];
-    const int r0 = WIDE ? 64 * (wave & 3) : 32 * wave;
+    const int r0 = 32 * wave;
 #pragma unroll
     for (int s = 0; s < NS; ++s) rows[s] = r0 + 16 * s + i;
-    const int tok0 = WIDE ? 64 * (wave >> 2) : 0;
-    const int ntiles = min(4, max(0, (ncol - tok0 + 15) >> 4));
-    f32x4 acc[4][NS];
+    const int tok0 = 0;
+    const int ntiles = min(S::MT, (ncol + 15) >> 4);
+    f32x4 acc[kMaxTiles][NS];
     mm_loop<MODE>(acc, lds, pl, units, ra, rows, tok0, ntiles, i, q);
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
         const int row = kWgRows * rt + rows[s];
         if (row < H) {
 #pragma unroll
-            for (int n = 0; n < 4; ++n) {
+            for (int n = 0; n < S::MT; ++n) {
                 if (n < ntiles) {
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
