@@ -1701,6 +1701,56 @@ __global__ __launch_bounds__(256) void k_combine(const float* __restrict__ Y, co
     }
 }
 
+// The same combine four neighbouring elements per thread (16-byte loads and stores; every element's sum is
+// formed exactly as above).  H % 4 == 0, y 16-byte aligned.
+__global__ __launch_bounds__(256) void k_combine4(const float* __restrict__ Y, const int32_t* __restrict__ slot,
+                                                   const float* __restrict__ wts, int k, int H, int P, int add_shared,
+                                                   float* __restrict__ y) {
+    asm volatile("" ::"s"(Y), "s"(slot), "s"(wts), "s"(y), "s"(k), "s"(H), "s"(P), "s"(add_shared));  // kernargs now
+    const int t = blockIdx.x;
+    const int32_t* sl = slot + (size_t)t * k;
+    const float* wt = wts + (size_t)t * k;
+    int sl16[16];
+    float wt16[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        sl16[i] = sl[min(i, k - 1)];
+        wt16[i] = wt[min(i, k - 1)];
+    }
+    const int H4 = H >> 2;
+    for (int j = blockIdx.y * 256 + threadIdx.x; j < H4; j += gridDim.y * 256) {
+        float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        for (int s0 = 0; s0 < k; s0 += 16) {
+            float4 v[16];
+            float wv[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int s = min(s0 + i, k - 1);
+                const int r = s0 == 0 ? sl16[i] : sl[s];
+                v[i] = reinterpret_cast<const float4*>(Y + (size_t)r * H)[j];
+                wv[i] = s0 == 0 ? wt16[i] : wt[s];
+            }
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int s = s0 + i;
+                if (s == 0) {
+                    acc = make_float4(wv[0] * v[0].x, wv[0] * v[0].y, wv[0] * v[0].z, wv[0] * v[0].w);
+                } else if (s < k) {
+                    acc.x = __builtin_fmaf(wv[i], v[i].x, acc.x);
+                    acc.y = __builtin_fmaf(wv[i], v[i].y, acc.y);
+                    acc.z = __builtin_fmaf(wv[i], v[i].z, acc.z);
+                    acc.w = __builtin_fmaf(wv[i], v[i].w, acc.w);
+                }
+            }
+        }
+        if (add_shared) {
+            const float4 sh = reinterpret_cast<const float4*>(Y + (size_t)(P + t) * H)[j];
+            acc = make_float4(acc.x + sh.x, acc.y + sh.y, acc.z + sh.z, acc.w + sh.w);
+        }
+        reinterpret_cast<float4*>(y + (size_t)t * H)[j] = acc;
+    }
+}
+
 // out[t] = RMSNorm(x[t] + r[t]) with unit weight (r may be NULL): s = x + r in f32; ss = sum of s^2 with
 // thread i of the row's work-group accumulating fmaf(s_j, s_j, acc) over j = i, i + 256, ... in order, then
 // the wave butterfly 32..1, then the wave sums ((w0 + w1) + w2) + w3; out = s * (1 / sqrt(ss / n + eps)) with
@@ -2033,6 +2083,12 @@ hipError_t launch_q2_down_combine(const uint8_t* down_exps, const uint8_t* down_
 
 hipError_t launch_combine(const float* Y, const int32_t* slot, const float* wts, int k, int H, int P, int T,
                           int add_shared, float* y, hipStream_t s) {
+    if (H % 4 == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0 && (reinterpret_cast<uintptr_t>(Y) & 15) == 0) {
+        const int ychunks = (H / 4 + 255) / 256;
+        dim3 grid((unsigned)T, (unsigned)(ychunks < 8 ? ychunks : 8));
+        hipLaunchKernelGGL(k_combine4, grid, dim3(256), 0, s, Y, slot, wts, k, H, P, add_shared, y);
+        return hipGetLastError();
+    }
     const int ychunks = (H + 255) / 256;
     dim3 grid((unsigned)T, (unsigned)(ychunks < 8 ? ychunks : 8));
     hipLaunchKernelGGL(k_combine, grid, dim3(256), 0, s, Y, slot, wts, k, H, P, add_shared, y);
