@@ -364,7 +364,8 @@ def main():
     a = _args()
     if a.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {a.gpus} is not supported (the path is "
-              f"single-GPU by design, see DESIGN.md for how it would shard)", file=sys.stderr)
+              f"single-GPU by design; across GPUs it would shard by expert, with an all-to-all of the "
+              f"dispatched rows each way)", file=sys.stderr)
         sys.exit(2)
     import ctypes
     import torch
