@@ -260,11 +260,13 @@ smoe_status forward_impl(const smoe_geom* g, const smoe_weights* w, float* x_io,
         if (_m != SMOE_OK) return _m;        \
     } while (0)
     SMOE_MARK();
-    if (x_prev && mfma)  // the junction first, then the call on its output
-        SMOE_TRY(smoe::launch_residual_rmsnorm(x_prev, r_prev, T, H, eps, x_io, st), "residual rmsnorm");
     const bool fused_norm = x_prev && !mfma;
     uint16_t* xbf = mfma ? reinterpret_cast<uint16_t*>(ws + L.xbf) : nullptr;
-    if (mfma) SMOE_TRY(smoe::launch_act_records(x, (int64_t)T * (H / 64), ximg, xbf, st), "activation records");
+    // the prefill path's junction and the records of its output in one launch, before the call on that output
+    if (x_prev && mfma)
+        SMOE_TRY(smoe::launch_junction_records(x_prev, r_prev, T, H, eps, x_io, ximg, xbf, st), "junction records");
+    if (mfma && !x_prev)
+        SMOE_TRY(smoe::launch_act_records(x, (int64_t)T * (H / 64), ximg, xbf, st), "activation records");
     SMOE_TRY(smoe::launch_router(fused_norm ? x_prev : x, xbf, static_cast<const uint16_t*>(w->router),
                                  has_sh ? w->gate_inp_sh : nullptr, w->logit_bias, H, E, E + (has_sh ? 1 : 0), T, logits,
                                  E, sg, mfma ? nullptr : ximg, mfma ? 1 : 0, iq2 ? 1 : 0, st,

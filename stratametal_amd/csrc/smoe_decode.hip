@@ -1751,40 +1751,14 @@ __global__ __launch_bounds__(256) void k_combine4(const float* __restrict__ Y, c
     }
 }
 
-// out[t] = RMSNorm(x[t] + r[t]) with unit weight (r may be NULL): s = x + r in f32; ss = sum of s^2 with
-// thread i of the row's work-group accumulating fmaf(s_j, s_j, acc) over j = i, i + 256, ... in order, then
-// the wave butterfly 32..1, then the wave sums ((w0 + w1) + w2) + w3; out = s * (1 / sqrt(ss / n + eps)) with
-// IEEE division and square root (oracle: or_residual_rmsnorm_dev).  The stacked configuration's layer
-// junction x_{l+1} = RMSNorm(x_l + MoE_l(x_l)).  Each thread writes only elements it read, after the row
-// sum, so out may alias x.
-constexpr int kNormPer = 16;  // elements per thread: rows up to 4096
-__global__ __launch_bounds__(256) void k_residual_rmsnorm(const float* __restrict__ x, const float* __restrict__ r,
-                                                           int n, float eps, float* out) {
+// out[t] = RMSNorm(x[t] + r[t]) with unit weight (r may be NULL), one work-group per row (residual_rmsnorm_row:
+// the order of or_residual_rmsnorm_dev; out may alias x).  The stacked configuration's layer junction
+// x_{l+1} = RMSNorm(x_l + MoE_l(x_l)).
+__global__ __launch_bounds__(256) void k_residual_rmsnorm(const float* x, const float* r, int n, float eps,
+                                                           float* out) {
     __shared__ float wsum[4];
-    const float* xr = x + (size_t)blockIdx.x * n;
-    const float* rr = r ? r + (size_t)blockIdx.x * n : nullptr;
-    float v[kNormPer];
-    float acc = 0.0f;
-#pragma unroll
-    for (int m = 0; m < kNormPer; ++m) {
-        const int j = (int)threadIdx.x + 256 * m;
-        const int jc = j < n ? j : n - 1;  // clamped, so that every load issues
-        float sj = xr[jc];
-        if (rr) sj = sj + rr[jc];
-        v[m] = sj;
-        if (j < n) acc = __builtin_fmaf(sj, sj, acc);
-    }
-    acc = wave_sum_xor_fast(acc);
-    if ((threadIdx.x & 63) == 0) wsum[threadIdx.x >> 6] = acc;
-    __syncthreads();
-    const float ss = ((wsum[0] + wsum[1]) + wsum[2]) + wsum[3];
-    const float inv = 1.0f / __builtin_sqrtf(ss / (float)n + eps);
-    float* o = out + (size_t)blockIdx.x * n;
-#pragma unroll
-    for (int m = 0; m < kNormPer; ++m) {
-        const int j = (int)threadIdx.x + 256 * m;
-        if (j < n) o[j] = v[m] * inv;
-    }
+    residual_rmsnorm_row(x + (size_t)blockIdx.x * n, r ? r + (size_t)blockIdx.x * n : nullptr, n, eps,
+                         out + (size_t)blockIdx.x * n, wsum);
 }
 
 hipError_t launch_residual_rmsnorm(const float* x, const float* r, int n_rows, int n, float eps, float* out,

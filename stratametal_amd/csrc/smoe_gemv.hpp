@@ -335,4 +335,38 @@ __device__ __forceinline__ void stage_images(uint32_t* act, const uint32_t* __re
     }
 }
 
+// out[j] = RMSNorm(x + r)[j] of one row with unit weight (r may be NULL), by a 256-thread work-group: s = x + r in
+// f32; ss = sum of s^2 with thread i accumulating fmaf(s_j, s_j, acc) over j = i, i + 256, ... in order, then the
+// wave butterfly 32..1, then the wave sums ((w0 + w1) + w2) + w3; out = s * (1 / sqrt(ss / n + eps)) with IEEE
+// division and square root (oracle: or_residual_rmsnorm_dev).  Each thread writes only elements it read, after
+// the row sum, so out may alias x.  With `row` (LDS, n floats) the outputs also go there.  n <= 4096.
+constexpr int kNormPer = 16;  // elements per thread: rows up to 4096
+__device__ __forceinline__ void residual_rmsnorm_row(const float* xr, const float* rr, int n, float eps, float* o,
+                                                     float* wsum, float* row = nullptr) {
+    float v[kNormPer];
+    float acc = 0.0f;
+#pragma unroll
+    for (int m = 0; m < kNormPer; ++m) {
+        const int j = (int)threadIdx.x + 256 * m;
+        const int jc = j < n ? j : n - 1;  // clamped, so that every load issues
+        float sj = xr[jc];
+        if (rr) sj = sj + rr[jc];
+        v[m] = sj;
+        if (j < n) acc = __builtin_fmaf(sj, sj, acc);
+    }
+    acc = wave_sum_xor_fast(acc);
+    if ((threadIdx.x & 63) == 0) wsum[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    const float ss = ((wsum[0] + wsum[1]) + wsum[2]) + wsum[3];
+    const float inv = 1.0f / __builtin_sqrtf(ss / (float)n + eps);
+#pragma unroll
+    for (int m = 0; m < kNormPer; ++m) {
+        const int j = (int)threadIdx.x + 256 * m;
+        if (j < n) {
+            o[j] = v[m] * inv;
+            if (row) row[j] = v[m] * inv;
+        }
+    }
+}
+
 }  // namespace smoe

@@ -73,6 +73,8 @@ hipError_t launch_iq2_mmvq(const uint8_t* w, const uint8_t* xq, int n_in, int n_
 // prefill contract (bf16 MFMA)
 int mfma_chunk();                        // tokens per MFMA work item
 size_t act_rec_bytes(int64_t n_rec);     // bytes of n_rec 64-value activation records
+hipError_t launch_junction_records(const float* x, const float* r, int n_rows, int n, float eps, float* out,
+                                   uint32_t* rec, uint16_t* xb, hipStream_t s);
 hipError_t launch_act_records(const float* x, int64_t n_rec, uint32_t* rec, uint16_t* xb, hipStream_t s);  // xb: bf16 copy or NULL
 hipError_t launch_mm_gu(const uint8_t* gate_exps, const uint8_t* up_exps, const uint8_t* gate_sh, const uint8_t* up_sh,
                         const uint32_t* xrec, int64_t n_xrec, const int4* items, const int32_t* perm, int k, int H,

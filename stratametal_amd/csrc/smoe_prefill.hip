@@ -24,6 +24,7 @@
 // MFMA tiles (lane l = 16 q + i): A[i][k] = activation of column (token) i, B[k][j] = weight of row j,
 // C[4 q + r][j] in register r.
 #include "smoe_device.hpp"
+#include "smoe_gemv.hpp"
 #include "smoe_items.hpp"
 #include "smoe_launch.hpp"
 
@@ -49,18 +50,12 @@ __device__ __forceinline__ uint32_t bf16_as_f16(float v) {
 }
 
 // ------------------------------------------------------------------------------------------------ records of x
-// One thread per 8 positions (a 16-byte chunk) of a record.  With `xb`, the same 8 values also as bf16 bits in
-// natural order (the router's exact operand).
-__global__ __launch_bounds__(256) void k_act_records(const float* __restrict__ x, int64_t n_rec,
-                                                     uint32_t* __restrict__ rec, uint16_t* __restrict__ xb) {
-    const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    const int64_t r = g >> 3;
-    if (r >= n_rec) return;
-    const int ch = (int)(g & 7);
+// Chunk ch (8 positions, 16 bytes) of record r from the 8 values it holds, v[e] = element 16 q + 8 s + e of the
+// record's 64-value block (s = ch / 4, q = ch % 4); with `xb`, the same 8 values also as bf16 bits in natural order
+// (the router's exact operand).
+__device__ __forceinline__ void store_record_chunk(const float (&v)[8], int64_t r, int ch, uint32_t* __restrict__ rec,
+                                                   uint16_t* __restrict__ xb) {
     const int s = ch >> 2, q = ch & 3;
-    const float4* src = reinterpret_cast<const float4*>(x + r * 64 + 16 * q + 8 * s);
-    const float4 lo = src[0], hi = src[1];
-    const float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
     if (xb) {
         uint32_t h[8];
 #pragma unroll
@@ -73,6 +68,40 @@ __global__ __launch_bounds__(256) void k_act_records(const float* __restrict__ x
     for (int e = 0; e < 8; ++e) b[e] = bf16_as_f16(v[perm8(e)]);
     reinterpret_cast<uint4*>(rec + r * (kRecBytes / 4))[ch] =
         make_uint4(b[0] | (b[1] << 16), b[2] | (b[3] << 16), b[4] | (b[5] << 16), b[6] | (b[7] << 16));
+}
+
+// One thread per 8 positions (a 16-byte chunk) of a record.
+__global__ __launch_bounds__(256) void k_act_records(const float* __restrict__ x, int64_t n_rec,
+                                                     uint32_t* __restrict__ rec, uint16_t* __restrict__ xb) {
+    const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t r = g >> 3;
+    if (r >= n_rec) return;
+    const int ch = (int)(g & 7);
+    const float4* src = reinterpret_cast<const float4*>(x + r * 64 + 16 * (ch & 3) + 8 * (ch >> 2));
+    const float4 lo = src[0], hi = src[1];
+    const float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+    store_record_chunk(v, r, ch, rec, xb);
+}
+
+// The stack junction of the prefill path and the records of its output in one launch, one work-group per row:
+// x = RMSNorm(x_prev + r_prev) exactly as k_residual_rmsnorm forms it (written to `out`), then the row's
+// records and bf16 copy exactly as k_act_records forms them from x, read back from LDS.  n <= 4096, n % 64 == 0.
+__global__ __launch_bounds__(256) void k_junction_records(const float* __restrict__ x, const float* __restrict__ r,
+                                                          int n, float eps, float* __restrict__ out,
+                                                          uint32_t* __restrict__ rec, uint16_t* __restrict__ xb) {
+    __shared__ float wsum[4];
+    __shared__ __align__(16) float row[4096];
+    residual_rmsnorm_row(x + (size_t)blockIdx.x * n, r + (size_t)blockIdx.x * n, n, eps, out + (size_t)blockIdx.x * n,
+                         wsum, row);
+    __syncthreads();
+    const int rpr = n >> 6;
+    for (int g = threadIdx.x; g < rpr * 8; g += 256) {
+        const int rl = g >> 3, ch = g & 7;
+        const float4* src = reinterpret_cast<const float4*>(row + rl * 64 + 16 * (ch & 3) + 8 * (ch >> 2));
+        const float4 lo = src[0], hi = src[1];
+        const float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+        store_record_chunk(v, (int64_t)blockIdx.x * rpr + rl, ch, rec, xb);
+    }
 }
 
 // ------------------------------------------------------------------------------------------------ codes -> B
@@ -509,6 +538,13 @@ __global__ __launch_bounds__(512) void k_mm_down(const uint8_t* __restrict__ dow
 // ------------------------------------------------------------------------------------------------ launchers
 int mfma_chunk() { return kChunk; }
 size_t act_rec_bytes(int64_t n_rec) { return (size_t)n_rec * kRecBytes; }
+
+hipError_t launch_junction_records(const float* x, const float* r, int n_rows, int n, float eps, float* out,
+                                   uint32_t* rec, uint16_t* xb, hipStream_t s) {
+    if (n > 4096 || n % 64 || !r) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_junction_records, dim3((unsigned)n_rows), dim3(256), 0, s, x, r, n, eps, out, rec, xb);
+    return hipGetLastError();
+}
 
 hipError_t launch_act_records(const float* x, int64_t n_rec, uint32_t* rec, uint16_t* xb, hipStream_t s) {
     hipLaunchKernelGGL(k_act_records, dim3((unsigned)((n_rec * 8 + 255) / 256)), dim3(256), 0, s, x, n_rec, rec, xb);
