@@ -1754,16 +1754,21 @@ __global__ __launch_bounds__(256) void k_combine4(const float* __restrict__ Y, c
 // out[t] = RMSNorm(x[t] + r[t]) with unit weight (r may be NULL), one work-group per row (residual_rmsnorm_row:
 // the order of or_residual_rmsnorm_dev; out may alias x).  The stacked configuration's layer junction
 // x_{l+1} = RMSNorm(x_l + MoE_l(x_l)).
+template <bool VEC>
 __global__ __launch_bounds__(256) void k_residual_rmsnorm(const float* x, const float* r, int n, float eps,
                                                            float* out) {
     __shared__ float wsum[4];
-    residual_rmsnorm_row(x + (size_t)blockIdx.x * n, r ? r + (size_t)blockIdx.x * n : nullptr, n, eps,
-                         out + (size_t)blockIdx.x * n, wsum);
+    __shared__ __align__(16) float row[VEC ? 4096 : 1];
+    residual_rmsnorm_row<VEC>(x + (size_t)blockIdx.x * n, r ? r + (size_t)blockIdx.x * n : nullptr, n, eps,
+                              out + (size_t)blockIdx.x * n, wsum, VEC ? row : nullptr);
 }
 
 hipError_t launch_residual_rmsnorm(const float* x, const float* r, int n_rows, int n, float eps, float* out,
                                    hipStream_t s) {
-    hipLaunchKernelGGL(k_residual_rmsnorm, dim3((unsigned)n_rows), dim3(256), 0, s, x, r, n, eps, out);
+    const bool vec = n % 4 == 0 && ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(r) |
+                                     reinterpret_cast<uintptr_t>(out)) & 15) == 0;
+    if (vec) hipLaunchKernelGGL(k_residual_rmsnorm<true>, dim3((unsigned)n_rows), dim3(256), 0, s, x, r, n, eps, out);
+    else hipLaunchKernelGGL(k_residual_rmsnorm<false>, dim3((unsigned)n_rows), dim3(256), 0, s, x, r, n, eps, out);
     return hipGetLastError();
 }
 

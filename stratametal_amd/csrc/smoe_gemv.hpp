@@ -338,19 +338,39 @@ __device__ __forceinline__ void stage_images(uint32_t* act, const uint32_t* __re
 // out[j] = RMSNorm(x + r)[j] of one row with unit weight (r may be NULL), by a 256-thread work-group: s = x + r in
 // f32; ss = sum of s^2 with thread i accumulating fmaf(s_j, s_j, acc) over j = i, i + 256, ... in order, then the
 // wave butterfly 32..1, then the wave sums ((w0 + w1) + w2) + w3; out = s * (1 / sqrt(ss / n + eps)) with IEEE
-// division and square root (oracle: or_residual_rmsnorm_dev).  Each thread writes only elements it read, after
-// the row sum, so out may alias x.  With `row` (LDS, n floats) the outputs also go there.  n <= 4096.
+// division and square root (oracle: or_residual_rmsnorm_dev).  n <= 4096.  VEC (x, r, out 16-byte aligned,
+// n % 4 == 0): the row is read with 16-byte loads into `row` (LDS, n floats), summed from there in the same
+// order, and written from there with 16-byte stores; `row` then holds the outputs.  Otherwise each thread reads
+// and writes its own elements (`row`, if given, receives the outputs).  Every load precedes every store, so out
+// may alias x.
 constexpr int kNormPer = 16;  // elements per thread: rows up to 4096
+template <bool VEC>
 __device__ __forceinline__ void residual_rmsnorm_row(const float* xr, const float* rr, int n, float eps, float* o,
-                                                     float* wsum, float* row = nullptr) {
+                                                     float* wsum, float* row) {
     float v[kNormPer];
     float acc = 0.0f;
+    if constexpr (VEC) {
+        for (int c = (int)threadIdx.x; c < (n >> 2); c += 256) {
+            float4 a = reinterpret_cast<const float4*>(xr)[c];
+            if (rr) {
+                const float4 b = reinterpret_cast<const float4*>(rr)[c];
+                a = make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+            }
+            reinterpret_cast<float4*>(row)[c] = a;
+        }
+        __syncthreads();
+    }
 #pragma unroll
     for (int m = 0; m < kNormPer; ++m) {
         const int j = (int)threadIdx.x + 256 * m;
         const int jc = j < n ? j : n - 1;  // clamped, so that every load issues
-        float sj = xr[jc];
-        if (rr) sj = sj + rr[jc];
+        float sj;
+        if constexpr (VEC) {
+            sj = row[jc];
+        } else {
+            sj = xr[jc];
+            if (rr) sj = sj + rr[jc];
+        }
         v[m] = sj;
         if (j < n) acc = __builtin_fmaf(sj, sj, acc);
     }
@@ -363,9 +383,18 @@ __device__ __forceinline__ void residual_rmsnorm_row(const float* xr, const floa
     for (int m = 0; m < kNormPer; ++m) {
         const int j = (int)threadIdx.x + 256 * m;
         if (j < n) {
-            o[j] = v[m] * inv;
-            if (row) row[j] = v[m] * inv;
+            if constexpr (VEC) {
+                row[j] = v[m] * inv;
+            } else {
+                o[j] = v[m] * inv;
+                if (row) row[j] = v[m] * inv;
+            }
         }
+    }
+    if constexpr (VEC) {
+        __syncthreads();
+        for (int c = (int)threadIdx.x; c < (n >> 2); c += 256)
+            reinterpret_cast<float4*>(o)[c] = reinterpret_cast<const float4*>(row)[c];
     }
 }
 

@@ -85,14 +85,15 @@ __global__ __launch_bounds__(256) void k_act_records(const float* __restrict__ x
 
 // The stack junction of the prefill path and the records of its output in one launch, one work-group per row:
 // x = RMSNorm(x_prev + r_prev) exactly as k_residual_rmsnorm forms it (written to `out`), then the row's
-// records and bf16 copy exactly as k_act_records forms them from x, read back from LDS.  n <= 4096, n % 64 == 0.
+// records and bf16 copy exactly as k_act_records forms them from x, read back from LDS.  n <= 4096, n % 64 == 0,
+// x, r and out 16-byte aligned.
 __global__ __launch_bounds__(256) void k_junction_records(const float* __restrict__ x, const float* __restrict__ r,
                                                           int n, float eps, float* __restrict__ out,
                                                           uint32_t* __restrict__ rec, uint16_t* __restrict__ xb) {
     __shared__ float wsum[4];
     __shared__ __align__(16) float row[4096];
-    residual_rmsnorm_row(x + (size_t)blockIdx.x * n, r + (size_t)blockIdx.x * n, n, eps, out + (size_t)blockIdx.x * n,
-                         wsum, row);
+    residual_rmsnorm_row<true>(x + (size_t)blockIdx.x * n, r + (size_t)blockIdx.x * n, n, eps,
+                               out + (size_t)blockIdx.x * n, wsum, row);
     __syncthreads();
     const int rpr = n >> 6;
     for (int g = threadIdx.x; g < rpr * 8; g += 256) {
@@ -541,7 +542,9 @@ size_t act_rec_bytes(int64_t n_rec) { return (size_t)n_rec * kRecBytes; }
 
 hipError_t launch_junction_records(const float* x, const float* r, int n_rows, int n, float eps, float* out,
                                    uint32_t* rec, uint16_t* xb, hipStream_t s) {
-    if (n > 4096 || n % 64 || !r) return hipErrorInvalidValue;
+    if (n > 4096 || n % 64 || !r ||
+        ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(r) | reinterpret_cast<uintptr_t>(out)) & 15))
+        return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_junction_records, dim3((unsigned)n_rows), dim3(256), 0, s, x, r, n, eps, out, rec, xb);
     return hipGetLastError();
 }
