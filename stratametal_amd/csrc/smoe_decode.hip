@@ -847,8 +847,17 @@ __global__ __launch_bounds__(1024) void k_dispatch_scan(int32_t* __restrict__ hi
     __shared__ int scan[4 * 17];
     const int tid = threadIdx.x;
     int c = 0;
-    if (tid < E)
-        for (int ch = 0; ch < n_chunks; ++ch) c += hist[(size_t)ch * E + tid];
+    if (tid < E) {  // the chunks' counts, eight loads in flight at a time
+        int ch = 0;
+        for (; ch + 8 <= n_chunks; ch += 8) {
+            int h[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) h[u] = hist[(size_t)(ch + u) * E + tid];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) c += h[u];
+        }
+        for (; ch < n_chunks; ++ch) c += hist[(size_t)ch * E + tid];
+    }
     const int flag = c > 0 ? 1 : 0;
     const int nfull = c / chunk;
     const ItemClasses ic = item_classes(c, chunk, scan);
@@ -862,7 +871,18 @@ __global__ __launch_bounds__(1024) void k_dispatch_scan(int32_t* __restrict__ hi
         item_of[tid] = n_sh + fbase;      // the expert's first full item
         item_of[E + tid] = n_sh + rbase;  // its remainder item
         int run = off;
-        for (int ch = 0; ch < n_chunks; ++ch) {
+        int ch = 0;
+        for (; ch + 8 <= n_chunks; ch += 8) {
+            int h[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) h[u] = hist[(size_t)(ch + u) * E + tid];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                hist[(size_t)(ch + u) * E + tid] = run;
+                run += h[u];
+            }
+        }
+        for (; ch < n_chunks; ++ch) {
             const int h = hist[(size_t)ch * E + tid];
             hist[(size_t)ch * E + tid] = run;
             run += h;
