@@ -1722,7 +1722,9 @@ __global__ __launch_bounds__(256) void k_combine(const float* __restrict__ Y, co
 }
 
 // The same combine four neighbouring elements per thread (16-byte loads and stores; every element's sum is
-// formed exactly as above).  H % 4 == 0, y 16-byte aligned.
+// formed exactly as above), NB pair rows per batch (NB >= k where k <= 16, so that no batch reloads rows).
+// H % 4 == 0, y 16-byte aligned.
+template <int NB>
 __global__ __launch_bounds__(256) void k_combine4(const float* __restrict__ Y, const int32_t* __restrict__ slot,
                                                    const float* __restrict__ wts, int k, int H, int P, int add_shared,
                                                    float* __restrict__ y) {
@@ -1730,28 +1732,28 @@ __global__ __launch_bounds__(256) void k_combine4(const float* __restrict__ Y, c
     const int t = blockIdx.x;
     const int32_t* sl = slot + (size_t)t * k;
     const float* wt = wts + (size_t)t * k;
-    int sl16[16];
-    float wt16[16];
+    int slb[NB];
+    float wtb[NB];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        sl16[i] = sl[min(i, k - 1)];
-        wt16[i] = wt[min(i, k - 1)];
+    for (int i = 0; i < NB; ++i) {
+        slb[i] = sl[min(i, k - 1)];
+        wtb[i] = wt[min(i, k - 1)];
     }
     const int H4 = H >> 2;
     for (int j = blockIdx.y * 256 + threadIdx.x; j < H4; j += gridDim.y * 256) {
         float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        for (int s0 = 0; s0 < k; s0 += 16) {
-            float4 v[16];
-            float wv[16];
+        for (int s0 = 0; s0 < k; s0 += NB) {
+            float4 v[NB];
+            float wv[NB];
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
+            for (int i = 0; i < NB; ++i) {
                 const int s = min(s0 + i, k - 1);
-                const int r = s0 == 0 ? sl16[i] : sl[s];
+                const int r = s0 == 0 ? slb[i] : sl[s];
                 v[i] = reinterpret_cast<const float4*>(Y + (size_t)r * H)[j];
-                wv[i] = s0 == 0 ? wt16[i] : wt[s];
+                wv[i] = s0 == 0 ? wtb[i] : wt[s];
             }
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
+            for (int i = 0; i < NB; ++i) {
                 const int s = s0 + i;
                 if (s == 0) {
                     acc = make_float4(wv[0] * v[0].x, wv[0] * v[0].y, wv[0] * v[0].z, wv[0] * v[0].w);
@@ -2085,7 +2087,10 @@ hipError_t launch_combine(const float* Y, const int32_t* slot, const float* wts,
     if (H % 4 == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0 && (reinterpret_cast<uintptr_t>(Y) & 15) == 0) {
         const int ychunks = (H / 4 + 255) / 256;
         dim3 grid((unsigned)T, (unsigned)(ychunks < 8 ? ychunks : 8));
-        hipLaunchKernelGGL(k_combine4, grid, dim3(256), 0, s, Y, slot, wts, k, H, P, add_shared, y);
+        if (k <= 4) hipLaunchKernelGGL(k_combine4<4>, grid, dim3(256), 0, s, Y, slot, wts, k, H, P, add_shared, y);
+        else if (k <= 8) hipLaunchKernelGGL(k_combine4<8>, grid, dim3(256), 0, s, Y, slot, wts, k, H, P, add_shared, y);
+        else if (k <= 12) hipLaunchKernelGGL(k_combine4<12>, grid, dim3(256), 0, s, Y, slot, wts, k, H, P, add_shared, y);
+        else hipLaunchKernelGGL(k_combine4<16>, grid, dim3(256), 0, s, Y, slot, wts, k, H, P, add_shared, y);
         return hipGetLastError();
     }
     const int ychunks = (H + 255) / 256;
