@@ -1854,13 +1854,15 @@ void rows_shape(int n_in, int& nit, int& upl, int& rpw) {
     nit = rpi >= 16 ? 1 : 16 / rpi;
     rpw = nit * rpi;
 }
-// the down kernel: as rows_shape; with many work items (`wide`) then up to 4 passes until a lane holds 4 units
+// the down kernel: as rows_shape; with many work items (`wide`) then up to 4 passes until a lane holds 2 units
 // (a work-group streams tens of KB per staging of its h images; passes that do not fit one reduce-scatter are
-// summed one by one), with few the narrower shape keeps more work-groups in flight
+// summed one by one), with few the narrower shape keeps more work-groups in flight.  Two units per lane, not 4
+// nor 1, at decode b=16 (F = 512): 11.8 us against 13.6 and 13.8 -- the grid runs as two rounds of resident
+// work-groups, so one round's dots overlap the next round's loads.
 void down_shape(int n_in, bool wide, int& nit, int& upl, int& rpw) {
     rows_shape(n_in, nit, upl, rpw);
     if (!wide) return;
-    while (nit * upl < 4 && nit < 4) nit *= 2;
+    while (nit * upl < 2 && nit < 4) nit *= 2;
     rpw = nit * (64 / lanes_per_row_host(n_in >> 7));
 }
 constexpr int kDownWideItems = 32;  // work items from which the down kernel takes the wide shape
