@@ -3,23 +3,28 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
 
-A step is one MoE layer call (router, top-k, dispatch, expert products, shared expert, combine) on one batch
-of synthetic tokens.  The headline workload is BASELINE.json configs[1]: one Qwen3-Next-style layer (H 2048,
-512 Q2_0 experts + 1 shared, top-10, FF 512) at decode batch 16.  To keep the numbers honest against the
-256 MB Infinity Cache, `--layers` (default 48, ~21.7 GB) distinct layers are resident in HBM and consecutive
-steps walk through them, each layer with its own input batch, so a step's experts are not cache resident.
-The K timed steps are one captured HIP graph replay; per-stage kernel durations come from HIP events
-recorded between the kernels of the same replay.  Decode batch 1 (configs[0]'s shape) is measured the same
-way and reported under "extra".  The CPU baseline is the test oracle's C restatement of the reference's host
-path (kind "port"), timed on a bounded sample on this host's cores.
+A step is one MoE layer call (router, top-k, dispatch, expert products, shared expert, combine) on one batch of
+synthetic tokens.  The headline workload is BASELINE.json configs[0]: one Qwen3-Next-style layer (H 2048, 512 Q2_0
+experts + 1 shared, top-10, FF 512) decoding one token.  `--layers` (default 48, ~21.7 GB) distinct layers are
+resident in HBM and consecutive steps walk through them, each with its own token; the K timed steps are one
+captured HIP graph replay, and a 1 GiB write between replays empties the 256 MB Infinity Cache (MALL), so every
+step reads its layer's bytes from HBM.  Per-stage kernel durations come from HIP events recorded on the launch
+stream between the kernels of an eager pass of the same steps (also after a flush).  The JSON line's `roofline` is
+the dominant decode kernel's; `roofline_prefill_512` is the prefill GEMM's (configs[2], the metric's second half).
+`extra` holds decode batch 16, prefill 512 with Zipf(1.2) routing, IQ2_S batch 64
+(configs[3]) and the 48-layer stack.  The CPU baseline is the test oracle's C restatement of the
+reference's host path organised as the reference's CPU pool (kind "port"), built for and timed on this host.
 Prints ONE JSON line.
 """
 from __future__ import annotations
 
 import argparse
+import hashlib
 import json
 import os
+import subprocess
 import sys
+import tempfile
 import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
@@ -28,6 +33,7 @@ sys.path.insert(0, ROOT)
 METRIC = "MoE-layer tok/s + achieved HBM GB/s vs peak, decode b=1 and prefill 512"
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0  # dense bf16 MFMA
+FLUSH_BYTES = 1 << 30      # four times the MALL
 
 
 def _args():
@@ -36,26 +42,46 @@ def _args():
     ap.add_argument("--steps", type=int, default=96)
     ap.add_argument("--warmup", type=int, default=48)
     ap.add_argument("--layers", type=int, default=48)
-    ap.add_argument("--tokens", type=int, default=16)
     ap.add_argument("--seed", type=int, default=20261201)
-    ap.add_argument("--no-extra", action="store_true", help="skip the decode b=1 and prefill 512 measurements")
+    ap.add_argument("--no-extra", action="store_true", help="only the headline (decode b=1)")
     ap.add_argument("--prefill-layers", type=int, default=8)
     ap.add_argument("--prefill-steps", type=int, default=24)
     ap.add_argument("--iq2-layers", type=int, default=8)
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB five times (the reference kernel that scales the "
                          "FETCH_SIZE / WRITE_SIZE counters to bytes), then exit")
-    ap.add_argument("--only", choices=("b1", "prefill", "iq2", "stack"), default=None,
-                    help="measure only this secondary workload (for a profiler run); prints its summary, no JSON line")
+    ap.add_argument("--only", choices=("b1", "b16", "prefill", "iq2", "stack"), default=None,
+                    help="measure only this workload (for a profiler run); prints its summary, no JSON line")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--stack-prefill", type=int, default=4096, help="prefill tokens of the 48-layer stack")
     ap.add_argument("--stack-decode", type=int, default=64, help="decode steps of the 48-layer stack")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-seconds", type=float, default=3.0, help="CPU baseline seconds per (workload, threads)")
     return ap.parse_args()
 
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
+
+
+def source_digest():
+    """sha256 of the library's sources: a profile summary applies to the build whose digest it records."""
+    h = hashlib.sha256()
+    d = os.path.join(ROOT, "stratametal_amd", "csrc")
+    for f in sorted(os.listdir(d)):
+        h.update(f.encode())
+        h.update(open(os.path.join(d, f), "rb").read())
+    return h.hexdigest()[:16]
+
+
+def profile_record(name, kernel):
+    """A committed counter summary (profiles/<name>.json) for `kernel`, if it was taken from the current sources."""
+    p = os.path.join(ROOT, "profiles", name + ".json")
+    if not os.path.exists(p):
+        return None
+    rec = json.load(open(p))
+    if rec.get("source_digest") != source_digest() or not rec.get("kernel", "").startswith(kernel):
+        return None
+    return rec
 
 
 class Stack:
@@ -71,10 +97,9 @@ class Stack:
         torch.cuda.synchronize()
 
     def inputs(self, T, seed):
-        S, torch, g = self.S, self.torch, self.g
+        S, g = self.S, self.g
         xs = S.synth_normal(seed, 100 + T, len(self.layers) * T * g.n_embd).view(len(self.layers), T, g.n_embd)
-        ys = torch.empty_like(xs)
-        return xs, ys
+        return xs, self.torch.empty_like(xs)
 
     def call(self, l, x, y, T, trace=None):
         import ctypes as C
@@ -94,7 +119,6 @@ class HipEvents:
         self.hip = C.CDLL("libamdhip64.so")
         self.hip.hipEventCreateWithFlags.argtypes = [C.POINTER(C.c_void_p), C.c_uint]
         self.hip.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), C.c_void_p, C.c_void_p]
-        self.hip.hipEventDestroy.argtypes = [C.c_void_p]
 
     def create(self, n):
         out = []
@@ -113,8 +137,19 @@ class HipEvents:
         return ms.value
 
 
-def measure(S, torch, stack, T, steps, warmup, seed):
-    """Time `steps` layer calls (graph replay) at T tokens; return timings, stage durations and touched experts."""
+class Flush:
+    """A 1 GiB buffer rewritten between timed passes, so that no layer's bytes are left in the MALL or L2."""
+
+    def __init__(self, torch):
+        self.buf = torch.zeros(FLUSH_BYTES // 4, dtype=torch.float32, device="cuda")
+
+    def __call__(self):
+        self.buf.add_(1.0)
+
+
+def measure(S, torch, stack, T, steps, warmup, seed, flush):
+    """Time `steps` layer calls at T tokens (one graph replay, caches flushed first); return the wall time, the
+    replay's event time, per-stage durations of an eager pass with stage events, and the touched experts."""
     g = stack.g
     L = len(stack.layers)
     xs, ys = stack.inputs(T, seed)
@@ -128,7 +163,6 @@ def measure(S, torch, stack, T, steps, warmup, seed):
     for s in range(warmup):  # eager warmup (also loads the code objects)
         stack.call(s % L, xs[s % L], ys[s % L], T)
     torch.cuda.synchronize()
-    # the timed graph: `steps` calls walking the resident layers
     graph = torch.cuda.CUDAGraph()
     stream = torch.cuda.Stream()
     stream.wait_stream(torch.cuda.current_stream())
@@ -138,27 +172,34 @@ def measure(S, torch, stack, T, steps, warmup, seed):
                 tr = S._Trace(None, None, None, counts[s].data_ptr(), None, None, None, None, None)
                 stack.call(s % L, xs[s % L], ys[s % L], T, tr)
     torch.cuda.synchronize()
-    graph.replay()  # one untimed replay: code and graph are resident; the timed replay below is the measurement
+    graph.replay()  # untimed: code and graph resident
+    flush()
     torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
+    e0.record()
     graph.replay()
+    e1.record()
     torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    wall = t1 - t0
-    # per-kernel durations: the same steps launched on the same stream with HIP events between the kernels
+    wall = time.perf_counter() - t0
+    replay_ms = e0.elapsed_time(e1)
+    # per-kernel durations: the same steps launched eagerly on the same stream, HIP events between the kernels
+    flush()
+    torch.cuda.synchronize()
     for s in range(steps):
         stack.call(s % L, xs[s % L], ys[s % L], T, traces[s])
     torch.cuda.synchronize()
-    with_events = False
     stage_ms = [[he.elapsed_ms(events[s][i], events[s][i + 1]) for i in range(S.STAGE_EVENTS - 1)]
                 for s in range(steps)]
     step_ms = [he.elapsed_ms(events[s][0], events[s][-1]) for s in range(steps)]
     D = (counts > 0).sum(dim=1).cpu().tolist()
-    return dict(wall=wall, stage_ms=stage_ms, step_ms=step_ms, touched=D, events_in_graph=with_events)
+    return dict(wall=wall, replay_ms=replay_ms, stage_ms=stage_ms, step_ms=step_ms, touched=D)
 
 
 def bytes_model(S, g, T, D):
-    """Algorithmic (compulsory) HBM bytes of one layer call touching D distinct experts, and of its gate/up kernel."""
+    """Algorithmic (compulsory) HBM bytes of one layer call touching D distinct experts, and of its gate/up and
+    down kernels: weights of the touched experts and the shared expert, the router, x and y, and the activation
+    images the kernels exchange (q8_1 images of x and h; the down kernel's f32 rows when they go through HBM)."""
     rb_h = S.row_bytes(g.w_type, g.n_embd)
     rb_f = S.row_bytes(g.w_type, g.n_ff)
     sh = g.sh_type >= 0
@@ -174,11 +215,13 @@ def bytes_model(S, g, T, D):
 
 
 def prefill_flops(g, T):
-    """Dense FLOPs of one prefill call: every routed pair and shared token through gate, up and down, plus
-    the router (2 * MACs)."""
+    """Dense FLOPs of one prefill call (2 * MACs): every routed pair and shared token through gate, up and down;
+    the gate/up part alone; and the router."""
     P = T * g.top_k
-    ex = 2 * P * 3 * g.n_embd * g.n_ff + (2 * T * 3 * g.n_embd * g.n_ff_shared if g.sh_type >= 0 else 0)
-    return ex, 2 * T * g.n_embd * (g.n_expert + (1 if g.sh_type >= 0 else 0))
+    sh = g.sh_type >= 0
+    gu = 2 * P * 2 * g.n_embd * g.n_ff + (2 * T * 2 * g.n_embd * g.n_ff_shared if sh else 0)
+    down = 2 * P * g.n_embd * g.n_ff + (2 * T * g.n_embd * g.n_ff_shared if sh else 0)
+    return gu + down, gu, 2 * T * g.n_embd * (g.n_expert + (1 if sh else 0))
 
 
 def summarize(S, g, T, r, steps):
@@ -187,69 +230,63 @@ def summarize(S, g, T, r, steps):
     D = st.fmean(r["touched"])
     layer_b, gu_b, down_b = bytes_model(S, g, T, D)
     ms = r["wall"] * 1e3 / steps
-    return dict(tokens=T, ms_per_step=ms, tok_s=T * steps / r["wall"], touched_experts_avg=D,
-                layer_bytes_avg=layer_b, layer_gbs=layer_b / (ms * 1e-3) / 1e9,
+    gu_ms, down_ms = per_stage["gate_up"], per_stage["down"]
+    return dict(tokens=T, ms_per_step=ms, tok_s=T * steps / r["wall"], gpu_ms_per_step=r["replay_ms"] / steps,
+                touched_experts_avg=D, layer_bytes_avg=layer_b, layer_gbs=layer_b / (ms * 1e-3) / 1e9,
+                layer_hbm_frac=layer_b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
                 stage_ms_avg=per_stage, gate_up_bytes=gu_b, down_bytes=down_b,
-                gate_up_gbs=gu_b / (per_stage["gate_up"] * 1e-3) / 1e9,
-                down_gbs=down_b / (per_stage["down"] * 1e-3) / 1e9,
-                events_in_graph=r["events_in_graph"],
+                gate_up_gbs=gu_b / (gu_ms * 1e-3) / 1e9 if gu_ms > 0 else None,
+                down_gbs=down_b / (down_ms * 1e-3) / 1e9 if down_ms > 0 else None,
                 step_event_ms_avg=st.fmean(r["step_ms"]))
 
 
-def cpu_baseline(g, T, seed, seconds):
-    """The oracle's C restatement of the reference host path (q8_1 activations, integer dots, double-free
-    device-order sums), on this host's cores, over a bounded sample of the same workload."""
-    import numpy as np
-    import oracle as O
-    threads = max(1, min(16, os.cpu_count() or 1))
-    og = O.Geom(**{k: getattr(g, k) for k in ("n_embd", "n_ff", "n_ff_shared", "n_expert", "top_k", "w_type",
-                                              "sh_type")})
-    w = O.make_weights(og, seed)
-    n = 0
-    t0 = time.perf_counter()
-    while True:
-        x = O.gen_normal(seed, 1000 + n, T * og.n_embd).reshape(T, og.n_embd)
-        O.moe_decode_dev(og, w, x, n_threads=threads)
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= seconds or n >= 200:
-            break
-    try:
-        model = [l for l in open("/proc/cpuinfo") if l.startswith("model name")][0].split(":", 1)[1].strip()
-    except Exception:
-        model = "unknown"
-    return {"value": T * n / el, "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"{n} layer calls of {T} tokens on one synthetic layer ({el:.1f} s), oracle/smoe_oracle.c "
-                      f"or_moe_decode_dev, {threads} OpenMP threads, {model}"}
+def stage_line(name, m):
+    return "%s: %.4f ms/step (GPU %.4f), %.0f tok/s, layer %.0f GB/s, touched %.1f, stages(us) %s" % (
+        name, m["ms_per_step"], m["gpu_ms_per_step"], m["tok_s"], m["layer_gbs"], m["touched_experts_avg"],
+        {k: round(v * 1e3, 2) for k, v in m["stage_ms_avg"].items()})
 
 
-def prefill(S, torch, g, a):
-    """512 tokens per call, expert popularity Zipf(1.2) through a seeded logit bias, the MFMA
-    (prefill) contract.  `--prefill-layers` biased layers are resident (their working sets exceed the Infinity
-    Cache together); steps walk through them."""
+def decode(S, torch, stack, T, a, flush, seed_off):
+    r = measure(S, torch, stack, T, a.steps, a.warmup, a.seed + seed_off, flush)
+    m = summarize(S, stack.g, T, r, a.steps)
+    log(stage_line(f"decode b={T}", m))
+    return m
+
+
+def prefill(S, torch, g, a, flush):
+    """512 tokens per call, expert popularity Zipf(1.2) through a fitted router logit bias, the MFMA
+    (prefill) contract.  `--prefill-layers` biased layers are resident; steps walk through them."""
     T = 512
-    bias = S.zipf_bias(g.n_expert, 1.2, a.seed)
+    bias = S.zipf_bias(g.n_expert, 1.2, a.seed, n_tokens=T, top_k=g.top_k, n_embd=g.n_embd)
     t0 = time.perf_counter()
     stack = Stack(S, torch, g, a.prefill_layers, a.seed + 1000, T, logit_bias=torch.from_numpy(bias).cuda())
     log(f"prefill: {a.prefill_layers} Zipf-biased layers resident in {time.perf_counter() - t0:.1f} s")
     steps = a.prefill_steps
-    r = measure(S, torch, stack, T, steps, max(2, steps // 3), a.seed + 13)
+    r = measure(S, torch, stack, T, steps, max(2, steps // 3), a.seed + 13, flush)
     m = summarize(S, g, T, r, steps)
-    ex_flops, router_flops = prefill_flops(g, T)
+    ex_flops, gu_flops, router_flops = prefill_flops(g, T)
     st = m["stage_ms_avg"]
     mm_ms = st["gate_up"] + st["down"]
-    out = {k: m[k] for k in ("ms_per_step", "tok_s", "touched_experts_avg", "layer_bytes_avg", "layer_gbs",
-                             "stage_ms_avg")}
-    out["layer_hbm_frac"] = m["layer_gbs"] / HBM_PEAK_GBS
+    out = {k: m[k] for k in ("ms_per_step", "gpu_ms_per_step", "tok_s", "touched_experts_avg", "layer_bytes_avg",
+                             "layer_gbs", "layer_hbm_frac", "stage_ms_avg")}
     out["expert_flops"] = ex_flops
     out["router_flops"] = router_flops
     out["expert_gemm_tflops"] = ex_flops / (mm_ms * 1e-3) / 1e12
     out["expert_gemm_mfma_frac"] = out["expert_gemm_tflops"] / BF16_PEAK_TFLOPS
     out["layer_tflops"] = (ex_flops + router_flops) / (m["ms_per_step"] * 1e-3) / 1e12
-    log("prefill 512: %.3f ms/step, %.0f tok/s, layer %.0f GB/s, expert GEMMs %.0f TFLOP/s (%.1f%% of bf16 peak), "
-        "touched %.0f, stages(us) %s" % (m["ms_per_step"], m["tok_s"], m["layer_gbs"], out["expert_gemm_tflops"],
-                                          100 * out["expert_gemm_mfma_frac"], m["touched_experts_avg"],
-                                          {k: round(v * 1e3, 1) for k, v in st.items()}))
+    gu_tf = gu_flops / (st["gate_up"] * 1e-3) / 1e12
+    roof = {"bound": "mfma", "kernel": "k_mm_gu (routed + shared gate/up, SwiGLU, bf16 h records)",
+            "achieved": gu_tf, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": gu_tf / BF16_PEAK_TFLOPS,
+            "traffic": None, "useful_flops_per_launch": gu_flops, "avg_launch_ms": st["gate_up"],
+            "mfma_busy": None}
+    rec = profile_record("prefill512_counters", "smoe::k_mm_gu")
+    if rec:
+        roof["traffic"] = rec.get("traffic_bytes")
+        roof["mfma_busy"] = rec.get("mfma_busy")
+        roof["counters_source"] = "profiles/prefill512_counters.md"
+    out["roofline"] = roof
+    log(stage_line("prefill 512", m) + ", expert GEMMs %.0f TFLOP/s (%.1f%% of bf16 peak), k_mm_gu %.0f TFLOP/s"
+        % (out["expert_gemm_tflops"], 100 * out["expert_gemm_mfma_frac"], gu_tf))
     del stack
     torch.cuda.empty_cache()
     return out
@@ -296,7 +333,7 @@ def stack48(S, torch, g, stack, a):
         torch.cuda.synchronize()
         times.append(ev0.elapsed_time(ev1))
     pre_ms = times[-1]
-    ex_flops, router_flops = prefill_flops(g, Tp)
+    ex_flops, _, router_flops = prefill_flops(g, Tp)
     out = {"layers": L, "prefill_tokens": Tp, "prefill_ms": pre_ms, "prefill_tok_s": Tp / (pre_ms * 1e-3),
            "prefill_tflops": L * (ex_flops + router_flops) / (pre_ms * 1e-3) / 1e12,
            "prefill_out_finite": bool(torch.isfinite(xl).all().item())}
@@ -339,7 +376,7 @@ def stack48(S, torch, g, stack, a):
     return out
 
 
-def iq2_b64(S, torch, a):
+def iq2_b64(S, torch, a, flush):
     """batch 64, IQ2_S routed and shared experts, uniform routing (no bias), decode contract.
     `--iq2-layers` resident layers (about 0.5 GB each) so that steps do not hit the Infinity Cache."""
     g = S.Geom(w_type=S.IQ2_S, sh_type=S.IQ2_S)
@@ -347,17 +384,63 @@ def iq2_b64(S, torch, a):
     stack = Stack(S, torch, g, a.iq2_layers, a.seed + 2000, 64)
     log(f"IQ2_S: {a.iq2_layers} layers resident in {time.perf_counter() - t0:.1f} s")
     steps = a.prefill_steps
-    r = measure(S, torch, stack, 64, steps, max(2, steps // 3), a.seed + 17)
+    r = measure(S, torch, stack, 64, steps, max(2, steps // 3), a.seed + 17, flush)
     m = summarize(S, g, 64, r, steps)
-    out = {k: m[k] for k in ("ms_per_step", "tok_s", "touched_experts_avg", "layer_bytes_avg", "layer_gbs",
-                             "stage_ms_avg", "gate_up_gbs", "down_gbs")}
-    out["layer_hbm_frac"] = m["layer_gbs"] / HBM_PEAK_GBS
-    log("IQ2_S b=64: %.3f ms/step, %.0f tok/s, layer %.0f GB/s, touched %.0f, stages(us) %s" % (
-        m["ms_per_step"], m["tok_s"], m["layer_gbs"], m["touched_experts_avg"],
-        {k: round(v * 1e3, 1) for k, v in m["stage_ms_avg"].items()}))
+    out = {k: m[k] for k in ("ms_per_step", "gpu_ms_per_step", "tok_s", "touched_experts_avg", "layer_bytes_avg",
+                             "layer_gbs", "layer_hbm_frac", "stage_ms_avg", "gate_up_gbs", "down_gbs")}
+    log(stage_line("IQ2_S b=64", m))
     del stack
     torch.cuda.empty_cache()
     return out
+
+
+def cpu_baseline(S, a):
+    """The reference CPU path, restated: the test oracle's decode contract organised as the reference's CPU pool
+    (flat (expert, row-range) jobs per stage, one worker per core, each weight row decoded once for all of its
+    expert's tokens; oracle/smoe_cpu_pool.c), compiled with -O3 -march=native for this host and timed on it, with
+    every core of this GPU's share and with 1 thread, on configs[0] (b=1), configs[1] (b=16) and configs[3]
+    (IQ2_S b=64), each on one synthetic layer with a fresh batch per call."""
+    import oracle as O
+    cores = max(1, min(16, len(os.sched_getaffinity(0))))
+    tmp = tempfile.mkdtemp(prefix="smoe_cpu_")
+    lib_path = os.path.join(tmp, "liboracle_native.so")
+    built = subprocess.run(["make", "-s", "-C", os.path.join(ROOT, "oracle"), "native", f"OUT={lib_path}"],
+                           capture_output=True, text=True)
+    if built.returncode == 0:
+        lib, flags = O.load_library(lib_path), "-O3 -march=native"
+    else:
+        lib, flags = O.lib(), "-O3 -march=x86-64-v3 (the native build failed)"
+    try:
+        model = [l for l in open("/proc/cpuinfo") if l.startswith("model name")][0].split(":", 1)[1].strip()
+    except (OSError, IndexError):
+        model = "unknown"
+    out = {"cores": cores, "nproc": os.cpu_count(), "cpu_model": model, "build": flags}
+    work = [("b1", O.Geom(), 1), ("b16", O.Geom(), 16), ("iq2_s_b64", O.Geom(w_type=O.IQ2_S, sh_type=O.IQ2_S), 64)]
+    for name, og, T in work:
+        w = O.make_weights(og, a.seed + 3000)
+        sg = S.Geom(**{k: getattr(og, k) for k in ("n_embd", "n_ff", "n_ff_shared", "n_expert", "top_k", "w_type",
+                                                   "sh_type")})
+        for threads in (cores, 1):
+            n, el, D_sum = 0, 0.0, 0.0
+            while el < a.cpu_seconds and n < 400:
+                x = O.gen_normal(a.seed + 3001, 1000 + n, T * og.n_embd).reshape(T, og.n_embd)
+                t0 = time.perf_counter()
+                O.moe_decode_pool(og, w, x, n_threads=threads, library=lib)
+                el += time.perf_counter() - t0
+                n += 1
+            # bytes: the expected distinct experts of uniform top-k routing (the seeded router is close to it)
+            E, K = og.n_expert, og.top_k
+            D = E * (1 - (1 - K / E) ** T)
+            tok_s = T * n / el
+            gbs = bytes_model(S, sg, T, D)[0] * n / el / 1e9
+            out[f"{name}_threads{threads}"] = {"tok_s": tok_s, "layer_gbs": gbs, "calls": n, "seconds": el}
+            log(f"cpu baseline {name}, {threads} threads: {tok_s:.1f} tok/s, {gbs:.2f} GB/s ({n} calls)")
+    head = out[f"b1_threads{cores}"]
+    return {"value": head["tok_s"], "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": (f"configs[0] (decode b=1): {head['calls']} layer calls on one synthetic layer, each on a fresh "
+                       f"token ({head['seconds']:.1f} s), oracle/smoe_cpu_pool.c (the reference host path as the "
+                       f"reference CPU pool runs it), {flags}, {cores} OpenMP threads on {model}"),
+            "detail": out}
 
 
 def main():
@@ -381,70 +464,62 @@ def main():
     import stratametal_amd as S
     S.C = ctypes
     g = S.Geom()
+    flush = Flush(torch)
     if a.only == "prefill":
-        prefill(S, torch, g, a)
+        prefill(S, torch, g, a, flush)
         return
     if a.only == "iq2":
-        iq2_b64(S, torch, a)
+        iq2_b64(S, torch, a, flush)
         return
     t_setup = time.perf_counter()
-    stack = Stack(S, torch, g, a.layers, a.seed, max(a.tokens, 1))
+    stack = Stack(S, torch, g, a.layers, a.seed, 16)
     log(f"{a.layers} layers resident ({a.layers * (g.n_expert * g.expert_bytes() + g.shared_bytes()) / 1e9:.1f} GB) "
         f"in {time.perf_counter() - t_setup:.1f} s")
     if a.only == "stack":
         stack48(S, torch, g, stack, a)
         return
-    if a.only == "b1":
-        r1 = measure(S, torch, stack, 1, a.steps, a.warmup, a.seed + 11)
-        m1 = summarize(S, g, 1, r1, a.steps)
-        log("decode b=1: %.3f ms/step, %.0f tok/s, layer %.0f GB/s" % (m1["ms_per_step"], m1["tok_s"], m1["layer_gbs"]))
+    if a.only == "b16":
+        decode(S, torch, stack, 16, a, flush, 7)
         return
-    r16 = measure(S, torch, stack, a.tokens, a.steps, a.warmup, a.seed + 7)
-    m16 = summarize(S, g, a.tokens, r16, a.steps)
-    log("decode b=%d: %.3f ms/step, %.0f tok/s, layer %.0f GB/s, gate/up %.0f GB/s, stages %s" % (
-        a.tokens, m16["ms_per_step"], m16["tok_s"], m16["layer_gbs"], m16["gate_up_gbs"],
-        {k: round(v * 1e3, 1) for k, v in m16["stage_ms_avg"].items()}))
+    m1 = decode(S, torch, stack, 1, a, flush, 11)
+    if a.only == "b1":
+        return
     extra = {}
     if not a.no_extra:
-        r1 = measure(S, torch, stack, 1, a.steps, a.warmup, a.seed + 11)
-        m1 = summarize(S, g, 1, r1, a.steps)
-        log("decode b=1: %.3f ms/step, %.0f tok/s, layer %.0f GB/s, stages(us) %s" % (
-            m1["ms_per_step"], m1["tok_s"], m1["layer_gbs"],
-            {k: round(v * 1e3, 1) for k, v in m1["stage_ms_avg"].items()}))
-        extra["decode_b1"] = {k: m1[k] for k in ("ms_per_step", "tok_s", "touched_experts_avg", "layer_bytes_avg",
-                                                 "layer_gbs", "stage_ms_avg", "gate_up_gbs", "down_gbs")}
-        extra["decode_b1"]["layer_hbm_frac"] = m1["layer_gbs"] / HBM_PEAK_GBS
+        m16 = decode(S, torch, stack, 16, a, flush, 7)
+        extra["decode_b16"] = {k: m16[k] for k in ("ms_per_step", "gpu_ms_per_step", "tok_s", "touched_experts_avg",
+                                                   "layer_bytes_avg", "layer_gbs", "layer_hbm_frac", "stage_ms_avg",
+                                                   "gate_up_gbs", "down_gbs")}
         extra["stack48"] = stack48(S, torch, g, stack, a)
-        extra["prefill_512"] = prefill(S, torch, g, a)
-        extra["iq2_s_b64"] = iq2_b64(S, torch, a)
-    extra["decode_b16_stages_ms"] = m16["stage_ms_avg"]
-    extra["decode_b16_layer_gbs"] = m16["layer_gbs"]
-    extra["decode_b16_layer_hbm_frac"] = m16["layer_gbs"] / HBM_PEAK_GBS
-    extra["touched_experts_avg"] = m16["touched_experts_avg"]
-    extra["events_in_graph"] = m16["events_in_graph"]
-    gu_ms = m16["stage_ms_avg"]["gate_up"]
-    roof = {"bound": "hbm", "kernel": "k_q2_gu (routed + shared gate/up, SwiGLU, q8_1 of h)",
-            "achieved": m16["gate_up_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": m16["gate_up_gbs"] / HBM_PEAK_GBS, "traffic": None,
-            "algorithmic_bytes_per_launch": m16["gate_up_bytes"], "avg_launch_ms": gu_ms}
-    tj = os.path.join(ROOT, "profiles", "decode_b16_traffic.json")
-    if os.path.exists(tj):  # HBM bytes per launch from the FETCH_SIZE / WRITE_SIZE counter runs (calibrated)
-        t = json.load(open(tj))
-        roof["traffic"] = t["traffic_bytes"]
-        roof["traffic_source"] = t["source"]
-    cpu = None
-    if not a.no_cpu:
-        cpu = cpu_baseline(g, a.tokens, a.seed, a.cpu_seconds)
-        log(f"cpu baseline: {cpu['value']:.1f} tok/s on {cpu['cores']} threads")
+        del stack
+        torch.cuda.empty_cache()
+        extra["prefill_512"] = prefill(S, torch, g, a, flush)
+        extra["iq2_s_b64"] = iq2_b64(S, torch, a, flush)
+    extra["decode_b1"] = {k: m1[k] for k in ("gpu_ms_per_step", "touched_experts_avg", "layer_bytes_avg", "layer_gbs",
+                                             "layer_hbm_frac", "stage_ms_avg", "step_event_ms_avg", "gate_up_gbs",
+                                             "down_gbs")}
+    gu_ms = m1["stage_ms_avg"]["gate_up"]
+    roof = {"bound": "hbm",
+            "kernel": "k_q2_gu_route (routes the token, then routed + shared gate/up, SwiGLU, q8_1 of h)",
+            "achieved": m1["gate_up_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": m1["gate_up_gbs"] / HBM_PEAK_GBS, "traffic": None,
+            "algorithmic_bytes_per_launch": m1["gate_up_bytes"], "avg_launch_ms": gu_ms}
+    rec = profile_record("decode_b1_traffic", "smoe::k_q2_gu_route")
+    if rec:  # HBM bytes per launch from the FETCH_SIZE / WRITE_SIZE counter runs (calibrated), same sources only
+        roof["traffic"] = rec["traffic_bytes"]
+        roof["traffic_source"] = "profiles/decode_b1_traffic.md"
+    cpu = None if a.no_cpu else cpu_baseline(S, a)
     out = {
-        "metric": METRIC, "value": m16["tok_s"], "unit": "tokens/s", "n_gpus": 1, "steps": a.steps,
-        "warmup": a.warmup, "ms_per_step": m16["ms_per_step"], "higher_is_better": True, "scaling": "weak",
+        "metric": METRIC, "value": m1["tok_s"], "unit": "tokens/s", "n_gpus": 1, "steps": a.steps,
+        "warmup": a.warmup, "ms_per_step": m1["ms_per_step"], "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "int8 (q8_1 x Q2_0 integer dot, f32 scale and sums)", "data": "synthetic",
-        "config": {"workload": "BASELINE configs[1]: one Qwen3-Next-style MoE layer, decode batch 16",
-                   "tokens_per_step": a.tokens, "n_embd": g.n_embd, "n_ff": g.n_ff, "n_expert": g.n_expert,
+        "config": {"workload": "BASELINE configs[0]: one Qwen3-Next-style MoE layer decoding 1 token",
+                   "tokens_per_step": 1, "n_embd": g.n_embd, "n_ff": g.n_ff, "n_expert": g.n_expert,
                    "top_k": g.top_k, "shared_experts": 1, "expert_type": "Q2_0", "router": "bf16",
-                   "resident_layers": a.layers, "parallelism": "none (1 GPU)"},
-        "roofline": roof, "cpu_baseline": cpu, "extra": extra,
+                   "resident_layers": a.layers, "cache": "1 GiB rewritten before the timed replay",
+                   "parallelism": "none (1 GPU)"},
+        "roofline": roof, "roofline_prefill_512": extra.get("prefill_512", {}).get("roofline"),
+        "cpu_baseline": cpu, "extra": extra,
     }
     print(json.dumps(out), flush=True)
 

@@ -45,56 +45,61 @@ def lib():
         if not os.path.exists(path):
             build()
         L = C.CDLL(path)
-        vp, i64, i32, u64, f32 = C.c_void_p, C.c_int64, C.c_int, C.c_uint64, C.c_float
-        sigs = {
-            "or_f16_from_f32": (C.c_uint16, [f32]),
-            "or_f32_from_f16": (f32, [C.c_uint16]),
-            "or_bf16_from_f32": (C.c_uint16, [f32]),
-            "or_f32_from_bf16": (f32, [C.c_uint16]),
-            "or_f16_from_f32_n": (None, [vp, i64, vp]),
-            "or_f32_from_f16_n": (None, [vp, i64, vp]),
-            "or_bf16_from_f32_n": (None, [vp, i64, vp]),
-            "or_expf": (f32, [f32]),
-            "or_logf": (f32, [f32]),
-            "or_cos2pi": (f32, [f32]),
-            "or_hash": (u64, [u64, u64, u64]),
-            "or_uniform": (f32, [u64, u64, u64]),
-            "or_normal": (f32, [u64, u64, u64]),
-            "or_gen_normal": (None, [u64, u64, i64, f32, vp]),
-            "or_gen_bf16": (None, [u64, u64, i64, f32, vp]),
-            "or_gen_q2_0": (None, [u64, u64, i64, f32, vp]),
-            "or_gen_iq2_s": (None, [u64, u64, i64, f32, vp]),
-            "or_dequant_q2_0": (None, [vp, i64, vp]),
-            "or_quant_q8_1": (None, [vp, i64, vp]),
-            "or_q2_0_gemv_dev": (None, [vp, vp, i32, i32, vp]),
-            "or_q2_0_gemv_ref": (None, [vp, vp, i32, i32, vp]),
-            "or_q2_0_gemv_exact": (None, [vp, vp, i32, i32, vp]),
-            "or_q2_0_gemv_no_minus_one": (None, [vp, vp, i32, i32, vp]),
-            "or_iq2s_grid": (None, [vp]),
-            "or_iq2_s_gemv_dev": (None, [vp, vp, i32, i32, vp]),
-            "or_iq2_s_gemv_ref": (None, [vp, vp, i32, i32, vp]),
-            "or_bf16_gemv_dev": (None, [vp, vp, i32, i32, vp]),
-            "or_bf16_gemv_double": (None, [vp, vp, i32, i32, vp]),
-            "or_route_dev": (None, [vp, i32, i32, i32, vp, vp]),
-            "or_route_ref": (None, [vp, i32, i32, i32, vp, vp]),
-            "or_swiglu_q8": (None, [vp, vp, i64, vp]),
-            "or_silu_mul": (f32, [f32, f32]),
-            "or_sigmoid": (f32, [f32]),
-            "or_combine_dev": (None, [vp, vp, vp, i32, i32, vp]),
-            "or_residual_rmsnorm_dev": (None, [vp, vp, i32, i32, C.c_float, vp]),
-            "or_combine_double": (None, [vp, vp, vp, i32, i32, vp]),
-            "or_dispatch": (None, [vp, i32, i32, i32, vp, vp, vp, vp]),
-            "or_moe_decode_dev": (i32, [vp, vp, vp, i32, vp, i32, vp, i32]),
-            "or_moe_decode_ref": (i32, [vp, vp, vp, i32, vp, i32, i32]),
-            "or_moe_prefill": (i32, [vp, vp, vp, i32, vp, i32, vp, i32]),
-            "or_row_bytes": (i64, [i32, i64]),
-        }
-        for name, (res, args) in sigs.items():
-            fn = getattr(L, name)
-            fn.restype = res
-            fn.argtypes = args
+        _set_sigs(L)
         _LIB = L
     return _LIB
+
+
+def _set_sigs(L):
+    vp, i64, i32, u64, f32 = C.c_void_p, C.c_int64, C.c_int, C.c_uint64, C.c_float
+    sigs = {
+        "or_f16_from_f32": (C.c_uint16, [f32]),
+        "or_f32_from_f16": (f32, [C.c_uint16]),
+        "or_bf16_from_f32": (C.c_uint16, [f32]),
+        "or_f32_from_bf16": (f32, [C.c_uint16]),
+        "or_f16_from_f32_n": (None, [vp, i64, vp]),
+        "or_f32_from_f16_n": (None, [vp, i64, vp]),
+        "or_bf16_from_f32_n": (None, [vp, i64, vp]),
+        "or_expf": (f32, [f32]),
+        "or_logf": (f32, [f32]),
+        "or_cos2pi": (f32, [f32]),
+        "or_hash": (u64, [u64, u64, u64]),
+        "or_uniform": (f32, [u64, u64, u64]),
+        "or_normal": (f32, [u64, u64, u64]),
+        "or_gen_normal": (None, [u64, u64, i64, f32, vp]),
+        "or_gen_bf16": (None, [u64, u64, i64, f32, vp]),
+        "or_gen_q2_0": (None, [u64, u64, i64, f32, vp]),
+        "or_gen_iq2_s": (None, [u64, u64, i64, f32, vp]),
+        "or_dequant_q2_0": (None, [vp, i64, vp]),
+        "or_quant_q8_1": (None, [vp, i64, vp]),
+        "or_q2_0_gemv_dev": (None, [vp, vp, i32, i32, vp]),
+        "or_q2_0_gemv_ref": (None, [vp, vp, i32, i32, vp]),
+        "or_q2_0_gemv_exact": (None, [vp, vp, i32, i32, vp]),
+        "or_q2_0_gemv_no_minus_one": (None, [vp, vp, i32, i32, vp]),
+        "or_iq2s_grid": (None, [vp]),
+        "or_iq2_s_gemv_dev": (None, [vp, vp, i32, i32, vp]),
+        "or_iq2_s_gemv_ref": (None, [vp, vp, i32, i32, vp]),
+        "or_bf16_gemv_dev": (None, [vp, vp, i32, i32, vp]),
+        "or_bf16_gemv_double": (None, [vp, vp, i32, i32, vp]),
+        "or_route_dev": (None, [vp, i32, i32, i32, vp, vp]),
+        "or_route_ref": (None, [vp, i32, i32, i32, vp, vp]),
+        "or_swiglu_q8": (None, [vp, vp, i64, vp]),
+        "or_silu_mul": (f32, [f32, f32]),
+        "or_sigmoid": (f32, [f32]),
+        "or_combine_dev": (None, [vp, vp, vp, i32, i32, vp]),
+        "or_residual_rmsnorm_dev": (None, [vp, vp, i32, i32, C.c_float, vp]),
+        "or_combine_double": (None, [vp, vp, vp, i32, i32, vp]),
+        "or_dispatch": (None, [vp, i32, i32, i32, vp, vp, vp, vp]),
+        "or_moe_decode_dev": (i32, [vp, vp, vp, i32, vp, i32, vp, i32]),
+        "or_moe_decode_ref": (i32, [vp, vp, vp, i32, vp, i32, i32]),
+        "or_moe_prefill": (i32, [vp, vp, vp, i32, vp, i32, vp, i32]),
+        "or_moe_decode_pool": (i32, [vp, vp, vp, i32, vp, i32, i32]),
+        "or_row_bytes": (i64, [i32, i64]),
+    }
+    for name, (res, args) in sigs.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
 
 
 def ref():
@@ -439,6 +444,20 @@ def moe_decode_ref(g, w, x, add_shared=True, n_threads=1):
     return _run_block(lib().or_moe_decode_ref, g, w, x, add_shared, False, n_threads, with_trace=False)
 
 
+def moe_decode_pool(g, w, x, add_shared=True, n_threads=1, library=None):
+    """The decode contract as the pooled CPU baseline computes it (bitwise equal to moe_decode_dev).  `library`:
+    another build of the oracle (bench.py's -march=native one) with the same signatures."""
+    L = lib() if library is None else library
+    return _run_block(L.or_moe_decode_pool, g, w, x, add_shared, False, n_threads, with_trace=False)
+
+
+def load_library(path: str):
+    """A build of the oracle at `path` (e.g. `make native OUT=path`), with the signatures set as in lib()."""
+    L = C.CDLL(path)
+    _set_sigs(L)
+    return L
+
+
 def moe_prefill(g, w, x, add_shared=True, trace=False, n_threads=1):
     return _run_block(lib().or_moe_prefill, g, w, x, add_shared, trace, n_threads)
 
@@ -452,9 +471,3 @@ def rel_l1_rows(got: np.ndarray, want: np.ndarray) -> np.ndarray:
     num = np.abs(got - want).sum(axis=1)
     den = np.abs(want).sum(axis=1)
     return np.where(den > 0, num / np.where(den > 0, den, 1.0), np.where(num == 0, 0.0, 1.0))
-
-
-def zipf_bias(n_expert: int, s: float, seed: int, scale: float = 1.0) -> np.ndarray:
-    """Logit bias b_e = scale * log(rank_e^-s) over a seeded rank permutation (config 3's Zipf routing)."""
-    ranks = np.argsort(np.argsort(gen_normal(seed, 99, n_expert), kind="stable"), kind="stable")  # seeded permutation
-    return (scale * (-s) * np.log(ranks.astype(np.float64) + 1.0)).astype(np.float32)

@@ -129,6 +129,12 @@ int or_moe_decode_ref(const or_geom* g, const or_weights* w, const float* x, int
 int or_moe_prefill(const or_geom* g, const or_weights* w, const float* x, int n_tok, float* y, int add_shared,
                    const or_trace* tr, int n_threads);
 
+/* The decode contract again, bitwise equal to or_moe_decode_dev, organised as the reference CPU path's pool
+ * (flat (expert, row-range) job batches, each weight row decoded once for all of its expert's tokens): the timed
+ * CPU baseline (oracle/smoe_cpu_pool.c).  n_threads <= 0 keeps the OpenMP default. */
+int or_moe_decode_pool(const or_geom* g, const or_weights* w, const float* x, int n_tok, float* y, int add_shared,
+                       int n_threads);
+
 /* Byte sizes */
 int64_t or_row_bytes(int type, int64_t n);
 

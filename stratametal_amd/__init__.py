@@ -9,6 +9,7 @@ library every entry point raises.
 from __future__ import annotations
 
 import ctypes as C
+import functools
 import os
 from dataclasses import dataclass
 from typing import Dict, Optional
@@ -102,6 +103,25 @@ def _ptr(t) -> Optional[int]:
     return None if t is None else t.data_ptr()
 
 
+def _need(t, name: str, dtype, shape=None, numel=None):
+    """Refuse, before any launch, a tensor the kernels would misread or run past: it must be on a GPU, contiguous,
+    of `dtype`, and (when given) of `shape` or at least `numel` elements."""
+    import torch
+    if not isinstance(t, torch.Tensor):
+        raise SmoeError(-1, f"{name} is not a tensor")
+    if t.dtype != dtype:
+        raise SmoeError(-1, f"{name} is {t.dtype}, needs {dtype}")
+    if not t.is_contiguous():
+        raise SmoeError(-5, f"{name} is not contiguous")
+    if shape is not None and tuple(t.shape) != tuple(shape):
+        raise SmoeError(-2, f"{name} has shape {tuple(t.shape)}, needs {tuple(shape)}")
+    if numel is not None and t.numel() < numel:
+        raise SmoeError(-2, f"{name} has {t.numel()} elements, needs {numel}")
+    if t.device.type != "cuda":
+        raise SmoeError(-1, f"{name} is on {t.device}, not a GPU")
+    return t
+
+
 def _stream(stream=None) -> int:
     import torch
     s = torch.cuda.current_stream() if stream is None else stream
@@ -191,14 +211,55 @@ def synth_normal(seed: int, stream_id: int, n: int, sigma: float = 1.0, device="
     return out
 
 
-def zipf_bias(n_expert: int, s: float, seed: int, scale: float = 1.0):
-    """Router logit bias b_e = -scale * s * ln(rank_e + 1) over a seeded rank permutation of the experts, so
-    that expert popularity follows Zipf(s) (the prefill benchmark's routing).  The permutation ranks the
-    seeded normals of stream 99, generated on the device; f32 numpy array."""
+def zipf_targets(n_expert: int, s: float, n_tokens: int, top_k: int):
+    """Expected pairs per popularity rank r = 1 .. n_expert under Zipf(s): C * r^-s, capped at n_tokens (a token
+    picks an expert at most once), with C such that the counts sum to n_tokens * top_k."""
     import numpy as np
-    v = synth_normal(seed, 99, n_expert).cpu().numpy()
-    ranks = np.argsort(np.argsort(v, kind="stable"), kind="stable")
-    return (scale * (-s) * np.log(ranks.astype(np.float64) + 1.0)).astype(np.float32)
+    r = np.arange(1, n_expert + 1, dtype=np.float64)
+    lo, hi = 0.0, float(n_tokens) * top_k * n_expert
+    for _ in range(200):
+        c = 0.5 * (lo + hi)
+        if np.minimum(n_tokens, c * r ** -s).sum() < n_tokens * top_k:
+            lo = c
+        else:
+            hi = c
+    return np.minimum(n_tokens, 0.5 * (lo + hi) * r ** -s)
+
+
+@functools.lru_cache(maxsize=8)
+def _zipf_bias_cached(n_expert, s, seed, n_tokens, top_k, sigma, sims, iters):
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    rank_of = rng.permutation(n_expert)  # expert e has popularity rank rank_of[e]
+    want = zipf_targets(n_expert, s, n_tokens, top_k) * (sims / n_tokens)
+    tgt = np.clip(np.rint(want).astype(np.int64), 0, sims - 1)
+    eps = rng.standard_normal((sims, n_expert)) * sigma
+    b = np.log(want / want.mean()) * sigma
+    cols = np.arange(n_expert)
+    for _ in range(iters):
+        z = eps + b
+        head = -np.partition(-z, top_k, axis=1)[:, :top_k + 1]
+        head.sort(axis=1)
+        vk, vk1 = head[:, 1], head[:, 0]  # each token's k-th and (k+1)-th largest score
+        # with the other experts' scores fixed, token t picks e iff b_e > (its k-th largest without e) - eps_te
+        d = np.sort(np.where(z >= vk[:, None], vk1[:, None], vk[:, None]) - eps, axis=0)
+        lo = np.where(tgt > 0, d[np.maximum(tgt - 1, 0), cols], d[0] - sigma)
+        hi = np.where(tgt < sims, d[np.minimum(tgt, sims - 1), cols], d[-1] + sigma)
+        b = b + 0.5 * (0.5 * (lo + hi) - b)
+    return b[rank_of].astype(np.float32)
+
+
+def zipf_bias(n_expert: int = 512, s: float = 1.2, seed: int = 1, n_tokens: int = 512, top_k: int = 10,
+              n_embd: int = 2048, w_sigma: float = 0.02, sims: int = 4096, iters: int = 24):
+    """Router logit bias of the prefill benchmark's routing: expert popularity follows
+    Zipf(s) over a seeded rank permutation of the experts, i.e. the expected pairs of the rank-r expert are
+    zipf_targets(...)[r-1] (hot experts take every token, many take none).  For x ~ N(0, 1) and router rows
+    ~ N(0, w_sigma^2) a token's logits are close to independent N(0, sigma^2), sigma = w_sigma * sqrt(n_embd); the
+    bias is fitted to that model by simulating `sims` tokens with fixed noise and solving, expert by expert, for
+    the bias at which exactly its target share of the simulated tokens ranks it in their top k (damped
+    fixed-point iterations).  Host-side and deterministic; an f32 numpy array of n_expert."""
+    sigma = w_sigma * float(n_embd) ** 0.5
+    return _zipf_bias_cached(n_expert, float(s), seed, n_tokens, top_k, sigma, sims, iters).copy()
 
 
 def _weights_c(w: Dict) -> _Weights:
@@ -221,11 +282,15 @@ class MoELayer:
 
     def forward(self, x, y=None, add_shared: bool = True, trace: bool = False, path: int = PATH_AUTO, stream=None):
         import torch
+        if x.dim() != 2:
+            raise SmoeError(-1, f"x must be (tokens, {self.g.n_embd}), got {tuple(x.shape)}")
         T = x.shape[0]
+        _need(x, "x", torch.float32, shape=(T, self.g.n_embd))
         if T > self.max_tokens:
             raise SmoeError(-2, f"{T} tokens exceed the workspace's {self.max_tokens}")
         if y is None:
             y = torch.empty_like(x)
+        _need(y, "y", torch.float32, numel=T * self.g.n_embd)
         tr = None
         out = {}
         if trace:
@@ -249,11 +314,17 @@ class MoELayer:
         """The stack junction fused into this layer's call: x = RMSNorm(x_prev + r_prev) (written to `x`), then
         y = MoE(x) (smoe_forward_residual).  `x` must not overlap x_prev, r_prev or y; y may be r_prev."""
         import torch
+        if x.dim() != 2:
+            raise SmoeError(-1, f"x must be (tokens, {self.g.n_embd}), got {tuple(x.shape)}")
         T = x.shape[0]
+        shape = (T, self.g.n_embd)
+        for t, name in ((x_prev, "x_prev"), (r_prev, "r_prev"), (x, "x")):
+            _need(t, name, torch.float32, shape=shape)
         if T > self.max_tokens:
             raise SmoeError(-2, f"{T} tokens exceed the workspace's {self.max_tokens}")
         if y is None:
             y = torch.empty_like(x)
+        _need(y, "y", torch.float32, numel=T * self.g.n_embd)
         _check(lib().smoe_forward_residual(C.byref(self._gc), C.byref(self._wc), x_prev.data_ptr(), r_prev.data_ptr(),
                                            eps, x.data_ptr(), T, y.data_ptr(), int(add_shared), self.ws.data_ptr(),
                                            self.ws_bytes, None, _stream(stream)))
@@ -266,7 +337,10 @@ class MoELayer:
 
 def router_topk(logits, k: int, stream=None):
     import torch
+    if logits.dim() != 2:
+        raise SmoeError(-1, "logits must be (tokens, experts)")
     T, E = logits.shape
+    _need(logits, "logits", torch.float32)
     ids = torch.empty((T, k), dtype=torch.int32, device=logits.device)
     w = torch.empty((T, k), dtype=torch.float32, device=logits.device)
     _check(lib().smoe_router_topk(logits.data_ptr(), T, E, k, ids.data_ptr(), w.data_ptr(), _stream(stream)))
@@ -275,6 +349,7 @@ def router_topk(logits, k: int, stream=None):
 
 def f32_to_bf16(x, stream=None):
     import torch
+    _need(x, "x", torch.float32)
     y = torch.empty(x.shape, dtype=torch.int16, device=x.device)
     _check(lib().smoe_f32_to_bf16(x.data_ptr(), x.numel(), y.data_ptr(), _stream(stream)))
     return y
@@ -282,6 +357,10 @@ def f32_to_bf16(x, stream=None):
 
 def bf16_gemv(x_bf16, w_bf16, n_in: int, n_out: int, stream=None):
     import torch
+    _need(x_bf16, "x_bf16", torch.int16)
+    _need(w_bf16, "w_bf16", torch.int16, numel=n_in * n_out)
+    if n_in <= 0 or x_bf16.numel() % n_in:
+        raise SmoeError(-1, f"x_bf16 holds {x_bf16.numel()} values, not whole rows of {n_in}")
     n_tok = x_bf16.numel() // n_in
     y = torch.empty((n_tok, n_out), dtype=torch.float32, device=x_bf16.device)
     _check(lib().smoe_bf16_gemv(x_bf16.data_ptr(), w_bf16.data_ptr(), y.data_ptr(), n_in, n_out, n_tok,
@@ -291,6 +370,7 @@ def bf16_gemv(x_bf16, w_bf16, n_in: int, n_out: int, stream=None):
 
 def quantize_q8_1(x, stream=None):
     import torch
+    _need(x, "x", torch.float32)
     y = torch.empty(x.numel() // 32 * 36, dtype=torch.uint8, device=x.device)
     _check(lib().smoe_quantize_q8_1(x.data_ptr(), x.numel(), y.data_ptr(), _stream(stream)))
     return y
@@ -298,6 +378,8 @@ def quantize_q8_1(x, stream=None):
 
 def mmvq(wtype: int, w, x_q8, n_in: int, n_out: int, n_col: int = 1, byte_off: int = 0, stream=None):
     import torch
+    _need(w, "w", torch.uint8, numel=byte_off + n_out * row_bytes(wtype, n_in) if wtype in (Q2_0, IQ2_S) else None)
+    _need(x_q8, "x_q8", torch.uint8, numel=n_col * (n_in // 32) * 36)
     y = torch.empty((n_col, n_out), dtype=torch.float32, device=w.device)
     _check(lib().smoe_mmvq(wtype, w.data_ptr(), byte_off, x_q8.data_ptr(), n_in, n_out, n_col, y.data_ptr(),
                            _stream(stream)))
@@ -307,6 +389,8 @@ def mmvq(wtype: int, w, x_q8, n_in: int, n_out: int, n_col: int = 1, byte_off: i
 def expert(blob, x_q8, gu_type: int, d_type: int, n_embd: int, n_ff: int, n_tok: int, stream=None):
     """One expert's FFN on a [gate | up | down] blob (smoe_expert; the reference's iq_expert)."""
     import torch
+    _need(blob, "blob", torch.uint8)
+    _need(x_q8, "x_q8", torch.uint8, numel=n_tok * (n_embd // 32) * 36)
     L = lib()
     scratch = torch.empty(L.smoe_expert_scratch_bytes(n_embd, n_ff, n_tok) + 256, dtype=torch.uint8,
                           device=blob.device)
@@ -320,14 +404,20 @@ def expert(blob, x_q8, gu_type: int, d_type: int, n_embd: int, n_ff: int, n_tok:
 def residual_rmsnorm(x, r=None, eps: float = 1e-6, out=None, stream=None):
     """RMSNorm(x + r) row by row with unit weight (smoe_residual_rmsnorm); `out` may be `x`."""
     import torch
+    _need(x, "x", torch.float32)
     n = x.shape[-1]
+    if r is not None:
+        _need(r, "r", torch.float32, shape=x.shape)
     out = torch.empty_like(x) if out is None else out
+    _need(out, "out", torch.float32, shape=x.shape)
     _check(lib().smoe_residual_rmsnorm(x.data_ptr(), _ptr(r), x.numel() // n, n, eps, out.data_ptr(), _stream(stream)))
     return out
 
 
 def swiglu_q8(gate, up, stream=None):
     import torch
+    _need(gate, "gate", torch.float32)
+    _need(up, "up", torch.float32, shape=gate.shape)
     y = torch.empty(gate.numel() // 32 * 36, dtype=torch.uint8, device=gate.device)
     _check(lib().smoe_swiglu_q8(gate.data_ptr(), up.data_ptr(), gate.numel(), y.data_ptr(), _stream(stream)))
     return y
@@ -335,7 +425,13 @@ def swiglu_q8(gate, up, stream=None):
 
 def combine(parts, weights, shared=None, stream=None):
     import torch
+    if parts.dim() != 2:
+        raise SmoeError(-1, "parts must be (k, n_embd)")
+    _need(parts, "parts", torch.float32)
     k, n = parts.shape
+    _need(weights, "weights", torch.float32, numel=k)
+    if shared is not None:
+        _need(shared, "shared", torch.float32, numel=n)
     y = torch.empty(n, dtype=torch.float32, device=parts.device)
     _check(lib().smoe_combine(parts.data_ptr(), weights.data_ptr(), _ptr(shared), y.data_ptr(), n, k,
                               _stream(stream)))
@@ -344,6 +440,9 @@ def combine(parts, weights, shared=None, stream=None):
 
 def dispatch(ids, n_expert: int, stream=None):
     import torch
+    if ids.dim() != 2:
+        raise SmoeError(-1, "ids must be (tokens, k)")
+    _need(ids, "ids", torch.int32)
     T, k = ids.shape
     dev = ids.device
     counts = torch.empty(n_expert, dtype=torch.int32, device=dev)

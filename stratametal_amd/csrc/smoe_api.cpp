@@ -6,6 +6,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <cmath>
 #include <cstdio>
 #include <cstring>
 #include <string>
@@ -45,6 +46,8 @@ constexpr int kFusedRouteTokens = 4;
 constexpr int kDispatchMultiPairs = 2048;
 // SMOE_PATH_AUTO runs the MFMA (prefill) contract from this many tokens on.
 constexpr int kMfmaTokens = 128;
+// The MFMA kernels' buffer offsets into the activation and h records are 31-bit.
+constexpr size_t kMfmaRecordLimit = (size_t)1 << 31;
 
 smoe_status check_geom(const smoe_geom* g) {
     if (!g) return fail(SMOE_ENULL, "geometry is NULL");
@@ -218,6 +221,13 @@ smoe_status forward_impl(const smoe_geom* g, const smoe_weights* w, float* x_io,
     const bool mfma = !iq2 && (path == SMOE_PATH_MFMA || (path == SMOE_PATH_AUTO && n_tokens >= kMfmaTokens));
 
     const Layout L = layout(*g, n_tokens);
+    if (mfma) {  // the MFMA kernels address the activation and h records with 31-bit buffer offsets
+        const int64_t P = (int64_t)n_tokens * g->top_k;
+        if (smoe::act_rec_bytes((int64_t)n_tokens * (g->n_embd / 64)) >= kMfmaRecordLimit ||
+            smoe::act_rec_bytes((P + n_tokens) * L.h_rec) >= kMfmaRecordLimit)
+            return fail(SMOE_EINVAL, "the MFMA path's activation or h records of " + std::to_string(n_tokens) +
+                                         " tokens exceed 2 GiB; split the batch");
+    }
     if (!workspace) return fail(SMOE_ENULL, "workspace is NULL");
     if (!aligned(workspace, kAlign)) return fail(SMOE_EALIGN, "workspace must be 256-byte aligned");
     if (workspace_bytes < L.total)
@@ -354,6 +364,7 @@ smoe_status smoe_forward_residual(const smoe_geom* g, const smoe_weights* w, con
                                   float eps, float* x, int32_t n_tokens, float* y, int32_t add_shared, void* workspace,
                                   size_t workspace_bytes, const smoe_trace* trace, void* hip_stream) {
     if (n_tokens > 0 && (!x_prev || !x)) return fail(SMOE_ENULL, "x_prev or x is NULL");
+    if (!(eps >= 0.0f) || eps == INFINITY) return fail(SMOE_EINVAL, "forward_residual: eps must be finite and non-negative");
     return forward_impl(g, w, x, n_tokens, y, add_shared, workspace, workspace_bytes, trace, SMOE_PATH_AUTO, hip_stream,
                         x_prev, r_prev, eps);
 }
@@ -522,7 +533,7 @@ smoe_status smoe_residual_rmsnorm(const float* x, const float* r, int32_t n_rows
     if (n_rows < 0 || n < 0) return fail(SMOE_EINVAL, "residual_rmsnorm: negative size");
     if (n_rows == 0 || n == 0) return ok();
     if (n > 4096) return fail(SMOE_EINVAL, "residual_rmsnorm: rows longer than 4096");
-    if (!(eps >= 0.0f)) return fail(SMOE_EINVAL, "residual_rmsnorm: eps must be non-negative");
+    if (!(eps >= 0.0f) || eps == INFINITY) return fail(SMOE_EINVAL, "residual_rmsnorm: eps must be finite and non-negative");
     if (!x || !out) return fail(SMOE_ENULL, "residual_rmsnorm: NULL buffer");
     SMOE_TRY(smoe::launch_residual_rmsnorm(x, r, n_rows, n, eps, out, stream_of(hip_stream)), "residual_rmsnorm");
     return ok();

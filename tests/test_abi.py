@@ -167,3 +167,24 @@ def test_expert_sizes_and_refusals():
     assert L.smoe_expert(*args(need - 1, S.IQ2_S, 4, sc)) == -2    # blob too small
     assert f"expert blob is {need - 1} bytes, needs {need}".encode() in L.smoe_last_error()
     assert L.smoe_expert(*args(need, S.IQ2_S, 4, sc - 1)) == -2    # scratch too small
+
+
+def test_binding_refuses_bad_tensors_before_launch():
+    """The Python binding checks dtype, contiguity, shape and device before any ctypes call (a wrong tensor would
+    make the kernels read or write past its end)."""
+    import torch
+    x = torch.zeros((4, 64), dtype=torch.float32)
+    cases = [
+        (lambda: S.quantize_q8_1(x.half()), "float16"),
+        (lambda: S.quantize_q8_1(x.t()), "contiguous"),
+        (lambda: S.quantize_q8_1(x), "not a GPU"),
+        (lambda: S.residual_rmsnorm(x.double()), "float64"),
+        (lambda: S.combine(x[:, ::2], None), "contiguous"),
+        (lambda: S.dispatch(torch.zeros((4, 2), dtype=torch.int64), 8), "int64"),
+        (lambda: S.router_topk(torch.zeros(8), 2), "(tokens, experts)"),
+        (lambda: S.mmvq(S.Q2_0, torch.zeros(10, dtype=torch.uint8), None, 128, 4), "elements"),
+    ]
+    for fn, why in cases:
+        with pytest.raises(S.SmoeError) as e:
+            fn()
+        assert why in str(e.value), (why, str(e.value))

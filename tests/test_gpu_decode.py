@@ -197,7 +197,7 @@ def test_dispatch_bitwise(torch, T, k, E, zipf):
     say(f"case: dispatch T={T} k={k} E={E} zipf={zipf}")
     logits = O.gen_normal(5, T, T * E).reshape(T, E)
     if zipf:
-        logits = logits + O.zipf_bias(E, 1.2, 5, scale=1.0)[None, :]
+        logits = logits + S.zipf_bias(E, 1.2, 5, n_tokens=T, top_k=k, n_embd=1, w_sigma=1.0)[None, :]
     ids, _ = O.route_dev(logits, k)
     counts, offsets, perm, slot = S.dispatch(dev(torch, ids), E)
     want = O.dispatch(ids, E)
@@ -314,3 +314,25 @@ def test_residual_rmsnorm_bitwise(torch, rows, n, with_r, inplace):
     xd = dev(torch, x)
     out = S.residual_rmsnorm(xd, None if r is None else dev(torch, r), 1e-6, out=xd if inplace else None)
     assert np.array_equal(bits(host(torch, out)), bits(O.residual_rmsnorm_dev(x, r, 1e-6)))
+
+
+def test_layer_binding_refuses_bad_tensors(torch):
+    """MoELayer.forward / forward_residual refuse a float16, non-contiguous, narrower or host tensor (x or y)
+    before any launch; y keeps its contents."""
+    say("case: binding refusals")
+    g = S.Geom(n_embd=256, n_ff=128, n_ff_shared=128, n_expert=16, top_k=4)
+    layer = S.MoELayer(g, S.synth_layer(g, 3), max_tokens=4)
+    x = torch.zeros((2, 256), dtype=torch.float32, device="cuda")
+    y = torch.full((2, 256), 7.0, device="cuda")
+    bad_x = [x.half(), torch.zeros((256, 2), device="cuda").t(), x[:, :128].contiguous(), x.cpu(), x[0]]
+    for bx in bad_x:
+        with pytest.raises(S.SmoeError):
+            layer.forward(bx, y)
+    for by in (y.half(), y[:, :128].contiguous(), y.cpu(), y.t()):
+        with pytest.raises(S.SmoeError):
+            layer.forward(x, by)
+    with pytest.raises(S.SmoeError):
+        layer.forward_residual(x.half(), x, torch.empty_like(x), y)
+    with pytest.raises(S.SmoeError):
+        layer.forward_residual(x, x[:1], torch.empty_like(x), y)
+    assert bool((host(torch, y) == 7.0).all())

@@ -460,3 +460,26 @@ def test_residual_rmsnorm_pinned(n):
     a = O.residual_rmsnorm_dev(x, r, eps=0.0)
     b = O.residual_rmsnorm_dev(4 * x, 4 * r, eps=0.0)
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_cpu_pool_baseline_equals_device_order_oracle():
+    """The timed CPU baseline (oracle/smoe_cpu_pool.c: the decode contract in (expert, row-range) job batches,
+    weight rows decoded once per expert for all of its tokens) is bitwise the device-order oracle it restates, for
+    both weight types, with and without the shared expert, on one thread and several."""
+    for wt, H, F in ((O.Q2_0, 256, 128), (O.Q2_0, 512, 384), (O.IQ2_S, 512, 512)):
+        for sh in (wt, -1):
+            g = O.Geom(n_embd=H, n_ff=F, n_ff_shared=F, n_expert=16, top_k=4, w_type=wt, sh_type=sh)
+            w = O.make_weights(g, 11 + H)
+            for T in (1, 3, 9):
+                x = O.gen_normal(3, 100 + T, T * H).reshape(T, H)
+                want = O.moe_decode_dev(g, w, x)
+                for th in (1, 4):
+                    got = O.moe_decode_pool(g, w, x, n_threads=th)
+                    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (wt, H, sh, T, th)
+    # a shared expert wider than the routed ones, and add_shared off
+    g = O.Geom(n_embd=256, n_ff=128, n_ff_shared=256, n_expert=8, top_k=2)
+    w = O.make_weights(g, 5)
+    x = O.gen_normal(4, 1, 5 * 256).reshape(5, 256)
+    for add in (True, False):
+        assert np.array_equal(O.moe_decode_pool(g, w, x, add_shared=add, n_threads=3).view(np.uint32),
+                              O.moe_decode_dev(g, w, x, add_shared=add).view(np.uint32))
