@@ -120,6 +120,23 @@ smoe_status smoe_forward_residual(const smoe_geom* g, const smoe_weights* w, con
                                   float eps, float* x, int32_t n_tokens, float* y, int32_t add_shared,
                                   void* workspace, size_t workspace_bytes, const smoe_trace* trace, void* hip_stream);
 
+/* ---------------------------------------------------------------------------------------------- no allocation */
+
+/* Bytes of the library's static device scratch (one array per GPU, held from the library's load until the
+ * process ends). */
+#define SMOE_STATIC_SCRATCH_BYTES (32u << 20)
+
+/* smoe_forward (SMOE_PATH_AUTO) with the library's own static device scratch in place of a caller workspace: it
+ * calls no hipMalloc, hipFree or other allocating routine, so it suits callers that cannot allocate (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  No counterpart in the reference.
+ * Limit: a call whose smoe_workspace_bytes(g, n_tokens) exceeds SMOE_STATIC_SCRATCH_BYTES is refused with
+ * SMOE_ESIZE (at the benchmark geometry, H 2048 / E 512 / k 10 / FF 512, that is 299 tokens).
+ * `hip_stream` must belong to the current device.  Every call on one GPU shares that GPU's scratch and leaves
+ * its contents behind: calls that overlap in time on one GPU (other streams, other host threads) race, so the
+ * caller serialises them.  The first call on a device looks up the scratch's device address once. */
+smoe_status smoe_forward_static(const smoe_geom* g, const smoe_weights* w, const float* x, int32_t n_tokens, float* y,
+                                int32_t add_shared, const smoe_trace* trace, void* hip_stream);
+
 /* ---------------------------------------------------------------------------------------------- stages */
 
 /* logits (n_tokens, n_expert) f32 -> ids, weights (n_tokens, k): softmax over every expert, top k by

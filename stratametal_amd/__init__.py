@@ -67,6 +67,7 @@ def lib():
             "smoe_forward": (i32, [vp, vp, vp, i32, vp, i32, vp, C.c_size_t, vp, vp]),
             "smoe_forward_path": (i32, [vp, vp, vp, i32, vp, i32, vp, C.c_size_t, vp, i32, vp]),
             "smoe_forward_residual": (i32, [vp, vp, vp, vp, f32, vp, i32, vp, i32, vp, C.c_size_t, vp, vp]),
+            "smoe_forward_static": (i32, [vp, vp, vp, i32, vp, i32, vp, vp]),
             "smoe_router_topk": (i32, [vp, i32, i32, i32, vp, vp, vp]),
             "smoe_f32_to_bf16": (i32, [vp, i64, vp, vp]),
             "smoe_bf16_gemv": (i32, [vp, vp, vp, i32, i32, i32, vp]),

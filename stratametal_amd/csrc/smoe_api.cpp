@@ -9,6 +9,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "smoe_launch.hpp"
@@ -374,6 +375,68 @@ smoe_status smoe_forward(const smoe_geom* g, const smoe_weights* w, const float*
                          void* hip_stream) {
     return smoe_forward_path(g, w, x, n_tokens, y, add_shared, workspace, workspace_bytes, trace, SMOE_PATH_AUTO,
                              hip_stream);
+}
+
+}  // extern "C"
+
+// ------------------------------------------------------------------------------------------------ no allocation
+// smoe_forward_static's scratch: one copy of this array lives on every GPU the library runs on, from the code
+// object's load until the process ends.  Host code never passes `scratch` itself to a kernel (in host code the
+// name is a host-side stand-in, not a device address): it uses the device address hipGetSymbolAddress returns,
+// looked up once per device on that device's first call.
+static __device__ __align__(256) uint8_t scratch[SMOE_STATIC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];
+
+// The device address of the current device's copy of `scratch`, or NULL with the reason in g_last.
+void* device_scratch() {
+    int dev = -1;
+    const hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) {
+        fail(SMOE_EDEVICE, std::string("hipGetDevice: ") + hipGetErrorString(e));
+        return nullptr;
+    }
+    if (dev < 0 || dev >= kMaxDevices) {
+        fail(SMOE_EDEVICE, "device ordinal " + std::to_string(dev) + " is beyond the library's 64");
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        const hipError_t r = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (r != hipSuccess || !p) {
+            fail(SMOE_EDEVICE, std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(r));
+            return nullptr;
+        }
+        g_scratch_ptr[dev] = p;
+    }
+    return g_scratch_ptr[dev];
+}
+}  // namespace
+
+extern "C" {
+
+smoe_status smoe_forward_static(const smoe_geom* g, const smoe_weights* w, const float* x, int32_t n_tokens, float* y,
+                                int32_t add_shared, const smoe_trace* trace, void* hip_stream) {
+    smoe_status s = check_geom(g);
+    if (s != SMOE_OK) return s;
+    if (n_tokens < 0) return fail(SMOE_EINVAL, "n_tokens is negative");
+    if ((int64_t)n_tokens * g->top_k > (1 << 24)) return fail(SMOE_EINVAL, "n_tokens * top_k exceeds 2^24");
+    if (n_tokens == 0) return forward_impl(g, w, const_cast<float*>(x), 0, y, add_shared, nullptr, 0, trace,
+                                           SMOE_PATH_AUTO, hip_stream, nullptr, nullptr, 0.0f);
+    const size_t need = layout(*g, n_tokens).total;
+    if (need > SMOE_STATIC_SCRATCH_BYTES)
+        return fail(SMOE_ESIZE, std::to_string(n_tokens) + " tokens need " + std::to_string(need) +
+                                    " bytes of scratch; the static scratch holds " +
+                                    std::to_string((size_t)SMOE_STATIC_SCRATCH_BYTES) +
+                                    " (call smoe_forward with a workspace for this batch)");
+    void* ws = device_scratch();
+    if (!ws) return SMOE_EDEVICE;
+    return forward_impl(g, w, const_cast<float*>(x), n_tokens, y, add_shared, ws, SMOE_STATIC_SCRATCH_BYTES, trace,
+                        SMOE_PATH_AUTO, hip_stream, nullptr, nullptr, 0.0f);
 }
 
 // ------------------------------------------------------------------------------------------------ stages

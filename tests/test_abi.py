@@ -169,6 +169,25 @@ def test_expert_sizes_and_refusals():
     assert L.smoe_expert(*args(need, S.IQ2_S, 4, sc - 1)) == -2    # scratch too small
 
 
+def test_forward_static_refusals_before_launch():
+    """The no-allocation entry point refuses a batch whose workspace exceeds the static scratch (with the limit in
+    the message) and bad geometry before any HIP call; zero tokens return at once."""
+    L, g = S.lib(), S.Geom()
+    w = S._Weights(*([FAKE] * 8 + [None]))
+
+    def call(gg, T):
+        return L.smoe_forward_static(C.byref(gg.c()), C.byref(w), FAKE, T, FAKE, 1, None, None)
+
+    assert call(g, 0) == 0
+    assert call(g, -1) == -1
+    assert call(S.Geom(top_k=65), 1) == -1
+    limit = 32 << 20
+    T = next(t for t in range(1, 4096) if L.smoe_workspace_bytes(C.byref(g.c()), t) > limit)
+    assert T > 128  # covers every decode batch and the smallest prefill batches of the benchmark geometry
+    assert call(g, T) == -2
+    assert str(limit).encode() in L.smoe_last_error()
+
+
 def test_binding_refuses_bad_tensors_before_launch():
     """The Python binding checks dtype, contiguity, shape and device before any ctypes call (a wrong tensor would
     make the kernels read or write past its end)."""
