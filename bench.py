@@ -224,11 +224,26 @@ def prefill_flops(g, T):
     return gu + down, gu, 2 * T * g.n_embd * (g.n_expert + (1 if sh else 0))
 
 
+def fused_small(g, T):
+    """Batches of at most 4 Q2_0 tokens run as the router plus one launch (k_q2_moe_small: routing, gate/up, down and
+    the combine) at the benchmark geometry."""
+    return T <= 4 and g.w_type == 42
+
+
+def fused_bytes(g, T, D):
+    """Algorithmic HBM bytes of k_q2_moe_small: the gate, up and down rows of the D touched experts and of the shared
+    expert, the q8_1 images of x and the logits it reads, and y (the h images stay on chip: LDS and the exchange)."""
+    return (D * g.expert_bytes() + g.shared_bytes() + T * g.n_embd // 32 * 48 + T * g.n_expert * 4
+            + T * g.n_embd * 4)
+
+
 def summarize(S, g, T, r, steps):
     import statistics as st
     per_stage = {name: st.fmean(r["stage_ms"][s][i] for s in range(steps)) for i, name in enumerate(S.STAGES)}
     D = st.fmean(r["touched"])
     layer_b, gu_b, down_b = bytes_model(S, g, T, D)
+    if fused_small(g, T):  # the gate_up stage is the one fused launch; the down and combine stages are empty
+        gu_b, down_b = fused_bytes(g, T, D), 0
     ms = r["wall"] * 1e3 / steps
     gu_ms, down_ms = per_stage["gate_up"], per_stage["down"]
     return dict(tokens=T, ms_per_step=ms, tok_s=T * steps / r["wall"], gpu_ms_per_step=r["replay_ms"] / steps,
@@ -236,7 +251,7 @@ def summarize(S, g, T, r, steps):
                 layer_hbm_frac=layer_b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
                 stage_ms_avg=per_stage, gate_up_bytes=gu_b, down_bytes=down_b,
                 gate_up_gbs=gu_b / (gu_ms * 1e-3) / 1e9 if gu_ms > 0 else None,
-                down_gbs=down_b / (down_ms * 1e-3) / 1e9 if down_ms > 0 else None,
+                down_gbs=down_b / (down_ms * 1e-3) / 1e9 if down_ms > 0 and down_b else None,
                 step_event_ms_avg=st.fmean(r["step_ms"]))
 
 
@@ -500,11 +515,12 @@ def main():
                                              "down_gbs")}
     gu_ms = m1["stage_ms_avg"]["gate_up"]
     roof = {"bound": "hbm",
-            "kernel": "k_q2_gu_route (routes the token, then routed + shared gate/up, SwiGLU, q8_1 of h)",
+            "kernel": "k_q2_moe_small (routes the token; routed + shared gate/up, SwiGLU, q8_1 of h; down rows and the "
+                      "combine)",
             "achieved": m1["gate_up_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": m1["gate_up_gbs"] / HBM_PEAK_GBS, "traffic": None,
             "algorithmic_bytes_per_launch": m1["gate_up_bytes"], "avg_launch_ms": gu_ms}
-    rec = profile_record("decode_b1_traffic", "smoe::k_q2_gu_route")
+    rec = profile_record("decode_b1_traffic", "smoe::k_q2_moe_small")
     if rec:  # HBM bytes per launch from the FETCH_SIZE / WRITE_SIZE counter runs (calibrated), same sources only
         roof["traffic"] = rec["traffic_bytes"]
         roof["traffic_source"] = "profiles/decode_b1_traffic.md"

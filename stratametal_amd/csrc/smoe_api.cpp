@@ -85,7 +85,8 @@ smoe_status check_geom(const smoe_geom* g) {
 }
 
 struct Layout {
-    size_t ximg, xbf, logits, sg, ids, wts, counts, offsets, perm, slot, elist, nlist, items, himg, Y, dwork, total;
+    size_t ximg, xbf, logits, sg, ids, wts, counts, offsets, perm, slot, elist, nlist, items, himg, Y, dwork, xchg,
+        total;
     int h_blocks;  // q8_1 blocks per h row (GEMV path)
     int h_rec;     // 64-value records per h row (MFMA path)
 };
@@ -132,6 +133,10 @@ Layout layout(const smoe_geom& g, int64_t T) {
     L.himg = take(most(smoe::img_bytes((P + T) * L.h_blocks), smoe::act_rec_bytes((P + T) * L.h_rec)));
     L.Y = take((size_t)(P + T) * H * 4);
     L.dwork = take(smoe::dispatch_work_bytes(P, (int)E));  // chunk histograms of the many-pair dispatch
+    // the h exchange of the fused small-batch launch, sized for its largest batch whatever T is (so that a workspace
+    // sized for max_tokens holds every smaller call's layout)
+    L.xchg = take(smoe::moe_small_xchg_bytes(kFusedRouteTokens, (int)K, max_items_gemv(g, kFusedRouteTokens),
+                                             L.h_blocks));
     L.total = o;
     return L;
 }
@@ -181,12 +186,10 @@ bool overlaps(const void* a, const void* b, size_t bytes) {
     return x < z + bytes && z < x + bytes;
 }
 
-// The forward call; with x_prev, x = RMSNorm(x_prev + r_prev) is formed first (fused into the router kernel on the
-// GEMV path, a junction kernel before the call on the MFMA path) and written to x.
-smoe_status forward_impl(const smoe_geom* g, const smoe_weights* w, float* x_io, int32_t n_tokens, float* y,
-                         int32_t add_shared, void* workspace, size_t workspace_bytes, const smoe_trace* trace,
-                         int32_t path, void* hip_stream, const float* x_prev, const float* r_prev, float eps) {
-    const float* x = x_io;
+// Every check of a block call that can refuse it, made before its first launch.
+smoe_status check_forward(const smoe_geom* g, const smoe_weights* w, const float* x, int32_t n_tokens, const float* y,
+                          const void* workspace, size_t workspace_bytes, int32_t path, const float* x_prev,
+                          const float* r_prev) {
     smoe_status s = check_geom(g);
     if (s != SMOE_OK) return s;
     if (!w) return fail(SMOE_ENULL, "weights is NULL");
@@ -234,6 +237,21 @@ smoe_status forward_impl(const smoe_geom* g, const smoe_weights* w, float* x_io,
     if (workspace_bytes < L.total)
         return fail(SMOE_ESIZE, "workspace is " + std::to_string(workspace_bytes) + " bytes, needs " +
                                     std::to_string(L.total));
+    return SMOE_OK;
+}
+
+// The forward call; with x_prev, x = RMSNorm(x_prev + r_prev) is formed first (fused into the router kernel on the
+// GEMV path, a junction kernel before the call on the MFMA path) and written to x.
+smoe_status forward_impl(const smoe_geom* g, const smoe_weights* w, float* x_io, int32_t n_tokens, float* y,
+                         int32_t add_shared, void* workspace, size_t workspace_bytes, const smoe_trace* trace,
+                         int32_t path, void* hip_stream, const float* x_prev, const float* r_prev, float eps) {
+    const float* x = x_io;
+    smoe_status s = check_forward(g, w, x, n_tokens, y, workspace, workspace_bytes, path, x_prev, r_prev);
+    if (s != SMOE_OK || n_tokens == 0) return s == SMOE_OK ? ok() : s;
+    const bool has_sh = g->sh_type >= 0;
+    const bool iq2 = g->w_type == SMOE_IQ2_S;
+    const bool mfma = !iq2 && (path == SMOE_PATH_MFMA || (path == SMOE_PATH_AUTO && n_tokens >= kMfmaTokens));
+    const Layout L = layout(*g, n_tokens);
 
     uint8_t* ws = static_cast<uint8_t*>(workspace);
     const int T = n_tokens, H = g->n_embd, E = g->n_expert, K = g->top_k, F = g->n_ff;
@@ -272,6 +290,14 @@ smoe_status forward_impl(const smoe_geom* g, const smoe_weights* w, float* x_io,
     } while (0)
     SMOE_MARK();
     const bool fused_norm = x_prev && !mfma;
+    // batches of at most kFusedRouteTokens tokens on the Q2_0 GEMV path: the gate/up kernel routes the batch itself,
+    // and (when the batch's h images fit in LDS) the down kernel applies the combine; where the shapes allow, both
+    // run as one launch whose exchange words the router kernel clears
+    const bool small = !mfma && !iq2 && T <= kFusedRouteTokens;
+    const bool small_down = small && smoe::down_combine_ok(T, K, L.h_blocks);
+    const bool fused = small_down && smoe::moe_small_ok(T, K, H, F, Fs, has_sh ? 1 : 0, L.h_blocks);
+    uint8_t* xchg = ws + L.xchg;
+    const size_t xchg_bytes = fused ? smoe::moe_small_xchg_bytes(T, K, n_items, L.h_blocks) : 0;
     uint16_t* xbf = mfma ? reinterpret_cast<uint16_t*>(ws + L.xbf) : nullptr;
     // the prefill path's junction and the records of its output in one launch, before the call on that output
     if (x_prev && mfma)
@@ -281,13 +307,10 @@ smoe_status forward_impl(const smoe_geom* g, const smoe_weights* w, float* x_io,
     SMOE_TRY(smoe::launch_router(fused_norm ? x_prev : x, xbf, static_cast<const uint16_t*>(w->router),
                                  has_sh ? w->gate_inp_sh : nullptr, w->logit_bias, H, E, E + (has_sh ? 1 : 0), T, logits,
                                  E, sg, mfma ? nullptr : ximg, mfma ? 1 : 0, iq2 ? 1 : 0, st,
-                                 fused_norm ? r_prev : nullptr, eps, fused_norm ? x_io : nullptr),
+                                 fused_norm ? r_prev : nullptr, eps, fused_norm ? x_io : nullptr,
+                                 fused ? reinterpret_cast<uint4*>(xchg) : nullptr, (int)(xchg_bytes / 16)),
              "router");
     SMOE_MARK();
-    // batches of at most kFusedRouteTokens tokens on the Q2_0 GEMV path: the gate/up kernel routes the batch itself,
-    // and (when the batch's h images fit in LDS) the down kernel applies the combine
-    const bool small = !mfma && !iq2 && T <= kFusedRouteTokens;
-    const bool small_down = small && smoe::down_combine_ok(T, K, L.h_blocks);
     if (small) {
         // no route kernel: the stage boundary marks stay, the route stage is empty
     } else if (T <= kFusedRouteTokens) {
@@ -327,6 +350,12 @@ smoe_status forward_impl(const smoe_geom* g, const smoe_weights* w, float* x_io,
                  "gate/up");
         SMOE_MARK();
         SMOE_TRY(smoe::launch_iq2_down(de, ds, himg, L.h_blocks, sg, items, H, F, Fs, n_items, Y, st), "down");
+    } else if (fused) {
+        SMOE_TRY(smoe::launch_q2_moe_small(ge, ue, gs, us, de, ds, ximg, logits, sg, T, E, K, H, F, Fs, has_sh ? 1 : 0,
+                                           ids, wts, counts, offsets, perm, slot, elist, nlist, items, n_items, L.h_blocks,
+                                           xchg, (has_sh && add_shared) ? 1 : 0, y, st),
+                 "route + gate/up + down + combine");
+        SMOE_MARK();  // gate/up, down and combine are one launch: the later stage boundaries are empty
     } else {
         if (small)
             SMOE_TRY(smoe::launch_q2_gu_route(ge, ue, gs, us, ximg, logits, T, E, K, H, F, Fs, has_sh ? 1 : 0, ids, wts,

@@ -144,11 +144,16 @@ __global__ __launch_bounds__(256) void k_router(const float* __restrict__ xf, co
                                                  const float* __restrict__ bias, int H, int E, int rows_total, int T,
                                                  int tok_tile, float* __restrict__ logits, int ld_logits,
                                                  float* __restrict__ sg, uint32_t* __restrict__ ximg, int img_natural,
-                                                 const float* __restrict__ rprev, float eps, float* __restrict__ xout) {
+                                                 const float* __restrict__ rprev, float eps, float* __restrict__ xout,
+                                                 uint4* __restrict__ clear, int clear_n16) {
     extern __shared__ __align__(16) uint32_t smem[];
     __shared__ uint8_t qsc[8][32];
     __shared__ float inv_s[16];
     __shared__ float wsum_s[4][4];
+    // the exchange words of the kernel after this one (k_q2_moe_small), cleared: no launch reads them before it
+    for (int i = ((int)blockIdx.y * (int)gridDim.x + (int)blockIdx.x) * 256 + (int)threadIdx.x; i < clear_n16;
+         i += (int)(gridDim.x * gridDim.y) * 256)
+        clear[i] = make_uint4(0u, 0u, 0u, 0u);
     const int t0 = blockIdx.y * tok_tile;
     const int nt = min(tok_tile, T - t0);
     const int row_blocks = (rows_total + 3) / 4;
@@ -467,6 +472,19 @@ __global__ __launch_bounds__(256) void k_router_tile(const float* __restrict__ x
     }
 }
 
+// Inclusive prefix sum over the 64 lanes of a wave by DPP: row shifts by 1, 2, 4 and 8 (zero fill at the
+// start of each 16-lane row), then lane 15 of each row added into the next row (rows 1 and 3) and lane 31
+// into rows 2 and 3.
+__device__ __forceinline__ int wave_inclusive_scan(int x) {
+    x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, true);   // row_shr:1
+    x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, true);   // row_shr:2
+    x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, true);   // row_shr:4
+    x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, true);   // row_shr:8
+    x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xA, 0xF, false);  // row_bcast:15
+    x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xC, 0xF, false);  // row_bcast:31
+    return x;
+}
+
 // ------------------------------------------------------------------------------------------------ top-k
 // Orderable 32-bit key of a logit: NaN ranks as -inf, -0 as +0, then the sign-flip map, so that
 // key(a) > key(b) <=> a > b and key(a) == key(b) <=> a == b.
@@ -500,7 +518,7 @@ constexpr Cmp kNet16[63] = {{0, 1}, {2, 3}, {4, 5}, {6, 7}, {8, 9}, {10, 11}, {1
 // selection never reads the probabilities).
 template <int J, bool WTS = true>
 __device__ __forceinline__ void route_token_t(const float* __restrict__ l, int E, int k, int32_t* __restrict__ ids,
-                              float* __restrict__ wts, int32_t* ids_lds = nullptr) {
+                              float* __restrict__ wts, int32_t* ids_lds = nullptr, float* wts_lds = nullptr) {
     const int lane = threadIdx.x & 63;
     uint32_t key[J];
     float ex[J];
@@ -589,14 +607,16 @@ __device__ __forceinline__ void route_token_t(const float* __restrict__ l, int E
             ids[lane] = my_id;
             wts[lane] = p / den;
         }
+        if (lane < k && wts_lds) wts_lds[lane] = p / den;
     }
     if (lane < k && ids_lds) ids_lds[lane] = my_id;
 }
 
 __device__ __forceinline__ void route_token(const float* __restrict__ l, int E, int k, int32_t* __restrict__ ids,
-                                            float* __restrict__ wts, int32_t* ids_lds = nullptr) {
-    if (E <= 512) route_token_t<8>(l, E, k, ids, wts, ids_lds);
-    else route_token_t<16>(l, E, k, ids, wts, ids_lds);
+                                            float* __restrict__ wts, int32_t* ids_lds = nullptr,
+                                            float* wts_lds = nullptr) {
+    if (E <= 512) route_token_t<8>(l, E, k, ids, wts, ids_lds, wts_lds);
+    else route_token_t<16>(l, E, k, ids, wts, ids_lds, wts_lds);
 }
 // The ids alone, into LDS.
 __device__ __forceinline__ void route_token_ids(const float* __restrict__ l, int E, int k, int32_t* ids_lds) {
@@ -616,19 +636,6 @@ __global__ __launch_bounds__(64) void k_topk(const float* __restrict__ logits, i
 // atomics (order-free), offsets by an exclusive scan, ranks by a ballot match inside each wave plus per-wave
 // counts in LDS, 1024 pairs per pass: position = offsets[e] + (number of earlier pairs with expert e) (oracle:
 // or_dispatch).  Also the ascending list of touched experts.  An out-of-range id gets slot -1.
-// Inclusive prefix sum over the 64 lanes of a wave by DPP: row shifts by 1, 2, 4 and 8 (zero fill at the
-// start of each 16-lane row), then lane 15 of each row added into the next row (rows 1 and 3) and lane 31
-// into rows 2 and 3.
-__device__ __forceinline__ int wave_inclusive_scan(int x) {
-    x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, true);   // row_shr:1
-    x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, true);   // row_shr:2
-    x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, true);   // row_shr:4
-    x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, true);   // row_shr:8
-    x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xA, 0xF, false);  // row_bcast:15
-    x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xC, 0xF, false);  // row_bcast:31
-    return x;
-}
-
 // N exclusive scans over the 1024 threads of the block at once: a DPP scan inside each wave, the 16 wave
 // totals through LDS (scratch: N x 17 ints), then every wave scans the totals itself (one barrier).
 template <int N>
@@ -971,6 +978,7 @@ __global__ __launch_bounds__(1024) void k_dispatch_rank(const int32_t* __restric
 constexpr int kSmallPairs = 256;
 struct SmallDispatchLds {
     int ids[kSmallPairs];
+    float wts[kSmallPairs];
     int perm[kSmallPairs];
     int cnt[1024];
     int off[1024];
@@ -980,7 +988,7 @@ struct SmallDispatchLds {
 };
 
 // Every thread of a 256-thread work-group calls it.  With `store` false nothing is written to global memory and
-// the work-item table is not built: the work-group keeps the routing in LDS (s.ids, s.cnt, s.off, s.el,
+// the work-item table is not built: the work-group keeps the routing in LDS (s.ids, s.wts, s.cnt, s.off, s.el,
 // s.n_touched, s.perm = pair of each dispatch position) for its own use.  Ends with a barrier.
 __device__ __forceinline__ void small_route_dispatch(const float* __restrict__ logits, int T, int E, int k, bool store,
                                                      int32_t* __restrict__ ids, float* __restrict__ wts,
@@ -994,7 +1002,7 @@ __device__ __forceinline__ void small_route_dispatch(const float* __restrict__ l
 #pragma unroll
     for (int j = 0; j < 4; ++j) s.cnt[tid + 256 * j] = 0;
     if (wave < T) route_token(logits + (size_t)wave * E, E, k, store ? ids + (size_t)wave * k : nullptr,
-                              store ? wts + (size_t)wave * k : nullptr, s.ids + wave * k);
+                              store ? wts + (size_t)wave * k : nullptr, s.ids + wave * k, s.wts + wave * k);
     __syncthreads();
     const int id = tid < P ? s.ids[tid] : -1;
     const bool valid = id >= 0 && id < E;
@@ -1182,7 +1190,7 @@ template <int NIT, int MAXUPL, bool PRESTAGED>
 __device__ __forceinline__ void gu_compute(const Item& item, int hb, uint32_t* smem, uint32_t (&w)[NIT][MAXUPL][9],
                                            const uint32_t* __restrict__ ximg, const int32_t* __restrict__ perm, int k,
                                            int H, uint32_t* __restrict__ himg, int h_blocks, float (&rowv)[kGuCols][64],
-                                           uint8_t (&qsc)[8][32]) {
+                                           uint8_t (&qsc)[8][32], uint64_t* __restrict__ xchg) {
     const RowGeo G = row_geo(H);
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int grp = lane / G.lpr, l = lane - grp * G.lpr;
@@ -1230,23 +1238,25 @@ __device__ __forceinline__ void gu_compute(const Item& item, int hb, uint32_t* s
             const int i = lane & 31;
             const float h = live_c ? silu_mul(rowv[hw][i], rowv[hw][32 + i]) : 0.0f;
             const int row = item.first + c0 + (live_c ? hw : 0);
-            q8_image_store(h, live_c, qsc[hw], himg + ((size_t)row * h_blocks + hb) * kImgDw);
+            if (xchg)
+                q8_image_store(h, live_c, qsc[hw], nullptr, false, xchg + ((size_t)row * h_blocks + hb) * kXchgSlots);
+            else
+                q8_image_store(h, live_c, qsc[hw], himg + ((size_t)row * h_blocks + hb) * kImgDw);
         }
         if (c0 + kGuCols < item.ncol) __syncthreads();
     }
 }
 
-// The work-group's item, one unit (rows block blockIdx.x): `smem` is the kernel's dynamic LDS (the image staging
-// area).
+// The work-group's item, one unit (rows block hb): `smem` is the kernel's dynamic LDS (the image staging area).
+// With `xchg` the h images go to the tagged exchange words instead of himg.
 template <int NIT, int MAXUPL, bool PRESTAGED = false>
-__device__ __forceinline__ void q2_gu_item(const Item& item, uint32_t* smem, const uint8_t* __restrict__ gate_exps,
+__device__ __forceinline__ void q2_gu_item(const Item& item, int hb, uint32_t* smem, const uint8_t* __restrict__ gate_exps,
                                            const uint8_t* __restrict__ up_exps, const uint8_t* __restrict__ gate_sh,
                                            const uint8_t* __restrict__ up_sh, const uint32_t* __restrict__ ximg,
                                            const int32_t* __restrict__ perm, int k, int H, int F,
-                                           uint32_t* __restrict__ himg, int h_blocks) {
+                                           uint32_t* __restrict__ himg, int h_blocks, uint64_t* __restrict__ xchg = nullptr) {
     __shared__ float rowv[kGuCols][64];
     __shared__ uint8_t qsc[8][32];
-    const int hb = blockIdx.x;
     uint32_t w[NIT][MAXUPL][9];
     if constexpr (PRESTAGED) {
         gu_load_weights<NIT, MAXUPL>(item, hb, gate_exps, up_exps, gate_sh, up_sh, H, F, w);
@@ -1256,7 +1266,7 @@ __device__ __forceinline__ void q2_gu_item(const Item& item, uint32_t* smem, con
         gu_commit(item, direct, sp, smem, ximg, perm, k, H);
         __syncthreads();
     }
-    gu_compute<NIT, MAXUPL, PRESTAGED>(item, hb, smem, w, ximg, perm, k, H, himg, h_blocks, rowv, qsc);
+    gu_compute<NIT, MAXUPL, PRESTAGED>(item, hb, smem, w, ximg, perm, k, H, himg, h_blocks, rowv, qsc, xchg);
 }
 
 template <int NIT, int MAXUPL>
@@ -1271,7 +1281,8 @@ __global__ __launch_bounds__(256) void k_q2_gu(const uint8_t* __restrict__ gate_
     Item item;
     if (!work_item_uniform(items, blockIdx.y, item)) return;
     if ((int)blockIdx.x * 32 >= (item.shared ? Fs : F)) return;
-    q2_gu_item<NIT, MAXUPL>(item, smem, gate_exps, up_exps, gate_sh, up_sh, ximg, perm, k, H, F, himg, h_blocks);
+    q2_gu_item<NIT, MAXUPL>(item, blockIdx.x, smem, gate_exps, up_exps, gate_sh, up_sh, ximg, perm, k, H, F, himg,
+                            h_blocks);
 }
 
 // Gate/up of a batch of at most kShCols tokens straight from the logits, with no route kernel before it.  Grid
@@ -1287,26 +1298,28 @@ struct GuRouteLds {
     int first[kSmallPairs];  // 1 for the first pair of its expert
     int item[8];             // e (-1: none), first, ncol, tk[0..3]
 };
+// One work-group of k_q2_gu_route / k_q2_moe_small: work item y (shared first, then the touched experts in
+// ascending order; y = max_items is the writer), rows block hb of h.  Returns whether it computed a unit (false:
+// no expert for this item, or rows past the expert's width); with `xchg` the h images go to the exchange words.
 template <int NIT, int MAXUPL>
-__global__ __launch_bounds__(256) void k_q2_gu_route(
-    const uint8_t* __restrict__ gate_exps, const uint8_t* __restrict__ up_exps, const uint8_t* __restrict__ gate_sh,
-    const uint8_t* __restrict__ up_sh, const uint32_t* __restrict__ ximg, const float* __restrict__ logits, int T,
-    int E, int k, int H, int F, int Fs, int has_shared, int32_t* __restrict__ ids, float* __restrict__ wts,
-    int32_t* __restrict__ counts, int32_t* __restrict__ offsets, int32_t* __restrict__ perm,
-    int32_t* __restrict__ slot, int32_t* __restrict__ elist, int32_t* __restrict__ n_list, int4* __restrict__ items,
-    int max_items, uint32_t* __restrict__ himg, int h_blocks) {
+__device__ __forceinline__ bool gu_route_wg(
+    int y, int hb, uint32_t* smem, const uint8_t* __restrict__ gate_exps, const uint8_t* __restrict__ up_exps,
+    const uint8_t* __restrict__ gate_sh, const uint8_t* __restrict__ up_sh, const uint32_t* __restrict__ ximg,
+    const float* __restrict__ logits, int T, int E, int k, int H, int F, int Fs, int has_shared,
+    int32_t* __restrict__ ids, float* __restrict__ wts, int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
+    int32_t* __restrict__ perm, int32_t* __restrict__ slot, int32_t* __restrict__ elist, int32_t* __restrict__ n_list,
+    int4* __restrict__ items, int max_items, uint32_t* __restrict__ himg, int h_blocks, uint64_t* __restrict__ xchg) {
     typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
-    extern __shared__ __align__(16) uint32_t smem[];
     const int n_sh = has_shared ? 1 : 0;
     const int tid = threadIdx.x, wave = tid >> 6;
-    if ((int)blockIdx.y == max_items) {
-        if (blockIdx.x == 0)
+    if (y == max_items) {
+        if (hb == 0)
             small_route_dispatch(logits, T, E, k, true, ids, wts, counts, offsets, perm, slot, elist, n_list, items,
                                  max_items, has_shared, 1 << 30, kShCols, *reinterpret_cast<SmallDispatchLds*>(smem));
-        return;
+        return false;
     }
-    const bool shared_wg = (int)blockIdx.y < n_sh;
-    if ((int)blockIdx.x * 32 >= (shared_wg ? Fs : F)) return;
+    const bool shared_wg = y < n_sh;
+    if (hb * 32 >= (shared_wg ? Fs : F)) return false;
     const int qb = H >> 5;
     const int pieces = T * qb * (kImgDw / 4);  // at most 4 * 128 * 3
     const int npre = (pieces + 255) >> 8;      // uniform
@@ -1349,8 +1362,8 @@ __global__ __launch_bounds__(256) void k_q2_gu_route(
             const int q = __builtin_ctzll(m);
             rank += __builtin_amdgcn_readlane(id, q) < id ? 1 : 0;
         }
-        const unsigned long long own = __ballot(lane < P && fst && rank == (int)blockIdx.y - n_sh);
-        if (own == 0ull) return;  // uniform: no expert for this item
+        const unsigned long long own = __ballot(lane < P && fst && rank == y - n_sh);
+        if (own == 0ull) return false;  // uniform: no expert for this item
         const int ol = __builtin_ctzll(own);
         item.shared = false;
         item.e = __builtin_amdgcn_readlane(id, ol);
@@ -1377,11 +1390,11 @@ __global__ __launch_bounds__(256) void k_q2_gu_route(
         }
         if (tid == 0) L.item[0] = -1;
         __syncthreads();
-        const int y = (int)blockIdx.y - n_sh;
+        const int yr = y - n_sh;
         if (tid < P && L.first[tid]) {
             int rank = 0;  // touched experts below id
             for (int q = 0; q < P; ++q) rank += (L.first[q] && L.ids[q] < id) ? 1 : 0;
-            if (rank == y) {
+            if (rank == yr) {
                 int n = 0, tk[4] = {0, 0, 0, 0};
                 for (int q = 0; q < P; ++q) {
                     if (L.ids[q] == id) {
@@ -1397,7 +1410,7 @@ __global__ __launch_bounds__(256) void k_q2_gu_route(
             }
         }
         __syncthreads();
-        if (L.item[0] < 0) return;  // uniform: no expert for this item
+        if (L.item[0] < 0) return false;  // uniform: no expert for this item
         item.shared = false;
         item.e = L.item[0];
         item.first = L.item[1];
@@ -1406,7 +1419,23 @@ __global__ __launch_bounds__(256) void k_q2_gu_route(
         for (int c = 0; c < 4; ++c) item.tk[c] = L.item[3 + c];
         item.tok0 = item.tk[0];
     }
-    q2_gu_item<NIT, MAXUPL, true>(item, smem, gate_exps, up_exps, gate_sh, up_sh, ximg, perm, k, H, F, himg, h_blocks);
+    q2_gu_item<NIT, MAXUPL, true>(item, hb, smem, gate_exps, up_exps, gate_sh, up_sh, ximg, perm, k, H, F, himg,
+                                  h_blocks, xchg);
+    return true;
+}
+
+template <int NIT, int MAXUPL>
+__global__ __launch_bounds__(256) void k_q2_gu_route(
+    const uint8_t* __restrict__ gate_exps, const uint8_t* __restrict__ up_exps, const uint8_t* __restrict__ gate_sh,
+    const uint8_t* __restrict__ up_sh, const uint32_t* __restrict__ ximg, const float* __restrict__ logits, int T,
+    int E, int k, int H, int F, int Fs, int has_shared, int32_t* __restrict__ ids, float* __restrict__ wts,
+    int32_t* __restrict__ counts, int32_t* __restrict__ offsets, int32_t* __restrict__ perm,
+    int32_t* __restrict__ slot, int32_t* __restrict__ elist, int32_t* __restrict__ n_list, int4* __restrict__ items,
+    int max_items, uint32_t* __restrict__ himg, int h_blocks) {
+    extern __shared__ __align__(16) uint32_t smem[];
+    gu_route_wg<NIT, MAXUPL>(blockIdx.y, blockIdx.x, smem, gate_exps, up_exps, gate_sh, up_sh, ximg, logits, T, E, k, H,
+                             F, Fs, has_shared, ids, wts, counts, offsets, perm, slot, elist, n_list, items, max_items,
+                             himg, h_blocks, nullptr);
 }
 
 // Down rows.  Grid (ceil(H / rows per block), max work items), 4 waves; a wave owns NIT passes of rpi rows.
@@ -1510,49 +1539,20 @@ __global__ __launch_bounds__(256) void k_q2_down(const uint8_t* __restrict__ dow
 constexpr int kDcRows = 16;
 constexpr size_t kDownCombineLds = 96 * 1024;  // images + rows of the batch
 constexpr int kDcItems = 384;                  // work items whose table entries fit in LDS
-template <int MAXUPL, int NT>
-__global__ __launch_bounds__(256) void k_q2_down_combine(
-    const uint8_t* __restrict__ down_exps, const uint8_t* __restrict__ down_sh, const uint32_t* __restrict__ himg,
-    int h_blocks, const float* __restrict__ sg, const int4* __restrict__ items, int n_items, int npass, int H, int F,
-    int Fs, const int32_t* __restrict__ slot, const float* __restrict__ wts, int T, int k, int add_shared,
-    float* __restrict__ y) {
-    typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
-    extern __shared__ __align__(16) uint32_t smem[];
-    __shared__ int s_slot[kSmallPairs];
-    __shared__ float s_wts[kSmallPairs];
-    __shared__ int4 s_items[2 * kDcItems];
-    const int P = T * k, rows = P + T;
-    const int pieces = rows * h_blocks * (kImgDw / 4);  // 16-byte pieces of the images
-    float* Ys = reinterpret_cast<float*>(smem + (size_t)pieces * 4);  // [rows][kDcRows]
-    const int r0 = blockIdx.x * kDcRows;
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int n_tasks = n_items * npass;
-
-    // the first 1024 image pieces, the item table, the routing slots and weights: unconditional loads (clamped
-    // indices), all in flight together, then one barrier before any weight load
-    u32x4 pre[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) pre[j] = reinterpret_cast<const u32x4*>(himg)[min(j * 256 + tid, pieces - 1)];
-    int4 itv[3];
-#pragma unroll
-    for (int j = 0; j < 3; ++j) itv[j] = items[min(j * 256 + tid, 2 * n_items - 1)];
-    const int sl = slot[min(tid, P - 1)];
-    const float wt = wts[min(tid, P - 1)];
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-        if (j * 256 + tid < pieces) reinterpret_cast<u32x4*>(smem)[j * 256 + tid] = pre[j];
-#pragma unroll
-    for (int j = 0; j < 3; ++j)
-        if (j * 256 + tid < 2 * n_items) s_items[j * 256 + tid] = itv[j];
-    if (tid < P) {
-        s_slot[tid] = sl;
-        s_wts[tid] = wt;
-    }
-    for (int i = 1024 + tid; i < pieces; i += 256)
-        reinterpret_cast<u32x4*>(smem)[i] = reinterpret_cast<const u32x4*>(himg)[i];
-    __syncthreads();
-
+// The task loop and the combine of the small-batch down kernels: the h images of every pair row in `img` (LDS),
+// the row values parked in Ys, the item table, routing slots and weights, and the shared gate dots `sg` in LDS.  `before_compute` runs once, after
+// the first batch's weight loads were issued and before any weight or image is read (k_q2_moe_small waits for its
+// h images there); it must end with a barrier when it writes LDS.
+template <int MAXUPL, int NT, class Prep>
+__device__ __forceinline__ void down_combine_tasks(const uint8_t* __restrict__ down_exps,
+                                                   const uint8_t* __restrict__ down_sh, const uint32_t* img, float* Ys,
+                                                   const int4* s_items, const int* s_slot, const float* s_wts,
+                                                   int n_items, int npass, int r0, int H, int F, int Fs,
+                                                   const float* sg, int T, int k, int add_shared,
+                                                   int h_blocks, float* __restrict__ y, Prep before_compute) {
+    const int lane = threadIdx.x & 63, tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n_tasks = n_items * npass, P = T * k;
     for (int tb = 0; tb < n_tasks; tb += 4 * NT) {
         Item it[NT];
         bool live[NT];
@@ -1583,30 +1583,44 @@ __global__ __launch_bounds__(256) void k_q2_down_combine(
             for (int m = 0; m < MAXUPL; ++m)
                 load_unit(base + (size_t)r * rb + (size_t)(m < G.upl ? l + G.lpr * m : l) * 36, w[q][m]);
         }
+        if (tb == 0) before_compute();  // work-group uniform: every wave runs the first batch
         float dw[NT][MAXUPL][2];
         unit_scales(w, dw);
+        // a row value of one column of one task: the lane's units in order, then the butterfly over its lpr lanes
+        auto row_value = [&](int q, int c) {
+            const int grp = lane / lpr[q], l = lane - grp * lpr[q];
+            const uint32_t* ht = img + (size_t)(it[q].first + c) * h_blocks * kImgDw;
+            float acc = 0.0f;
+#pragma unroll
+            for (int m = 0; m < MAXUPL; ++m) {
+                if (m < upl[q]) {
+                    const uint32_t* im = ht + (size_t)(4 * (l + lpr[q] * m)) * kImgDw;
+                    Act2 a;
+                    load_act_img2(im, a);
+                    const float p01 = q2_unit_first(w[q][m], dw[q][m][0], a);
+                    load_act_img2(im + 2 * kImgDw, a);
+                    const float L = q2_unit_second(w[q][m], dw[q][m][1], p01, a);
+                    acc = m == 0 ? L : acc + L;
+                }
+            }
+            return group_sum(acc, lpr[q]);
+        };
+        // the first column of every task at once, with no branch between them (a dead task works on item 0's first
+        // column and stores nothing), so that the tasks' LDS reads and dots overlap; further columns task by task
+        float v0[NT];
+#pragma unroll
+        for (int q = 0; q < NT; ++q) v0[q] = row_value(q, 0);
 #pragma unroll
         for (int q = 0; q < NT; ++q) {
             if (!live[q]) continue;  // wave-uniform
-            const int grp = lane / lpr[q], l = lane - grp * lpr[q];
+            const int l = lane % lpr[q];
             const bool store = rloc[q] < kDcRows && r0 + rloc[q] < H && l == 0;
             for (int c = 0; c < it[q].ncol; ++c) {
-                const uint32_t* ht = smem + (size_t)(it[q].first + c) * h_blocks * kImgDw;
-                pin_units(w);
-                float acc = 0.0f;
-#pragma unroll
-                for (int m = 0; m < MAXUPL; ++m) {
-                    if (m < upl[q]) {
-                        const uint32_t* img = ht + (size_t)(4 * (l + lpr[q] * m)) * kImgDw;
-                        Act2 a;
-                        load_act_img2(img, a);
-                        const float p01 = q2_unit_first(w[q][m], dw[q][m][0], a);
-                        load_act_img2(img + 2 * kImgDw, a);
-                        const float L = q2_unit_second(w[q][m], dw[q][m][1], p01, a);
-                        acc = m == 0 ? L : acc + L;
-                    }
+                float v = v0[q];
+                if (c > 0) {
+                    pin_units(w);
+                    v = row_value(q, c);
                 }
-                float v = group_sum(acc, lpr[q]);
                 if (it[q].shared) v = v * sigmoid(sg[it[q].tok0 + c]);
                 if (store) Ys[(it[q].first + c) * kDcRows + rloc[q]] = v;
             }
@@ -1624,6 +1638,213 @@ __global__ __launch_bounds__(256) void k_q2_down_combine(
             if (add_shared) acc = acc + Ys[(P + t) * kDcRows + rl];
             y[(size_t)t * H + r0 + rl] = acc;
         }
+    }
+}
+
+template <int MAXUPL, int NT>
+__global__ __launch_bounds__(256) void k_q2_down_combine(
+    const uint8_t* __restrict__ down_exps, const uint8_t* __restrict__ down_sh, const uint32_t* __restrict__ himg,
+    int h_blocks, const float* __restrict__ sg, const int4* __restrict__ items, int n_items, int npass, int H, int F,
+    int Fs, const int32_t* __restrict__ slot, const float* __restrict__ wts, int T, int k, int add_shared,
+    float* __restrict__ y) {
+    typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
+    extern __shared__ __align__(16) uint32_t smem[];
+    __shared__ int s_slot[kSmallPairs];
+    __shared__ float s_wts[kSmallPairs];
+    __shared__ int4 s_items[2 * kDcItems];
+    __shared__ float s_sg[kShCols];
+    const int P = T * k, rows = P + T;
+    const int pieces = rows * h_blocks * (kImgDw / 4);  // 16-byte pieces of the images
+    float* Ys = reinterpret_cast<float*>(smem + (size_t)pieces * 4);  // [rows][kDcRows]
+    const int r0 = blockIdx.x * kDcRows;
+    const int tid = threadIdx.x;
+
+    // the first 1024 image pieces, the item table, the routing slots and weights: unconditional loads (clamped
+    // indices), all in flight together, then one barrier before any weight load
+    u32x4 pre[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) pre[j] = reinterpret_cast<const u32x4*>(himg)[min(j * 256 + tid, pieces - 1)];
+    int4 itv[3];
+#pragma unroll
+    for (int j = 0; j < 3; ++j) itv[j] = items[min(j * 256 + tid, 2 * n_items - 1)];
+    const int sl = slot[min(tid, P - 1)];
+    const float wt = wts[min(tid, P - 1)];
+    const float sgv = sg[min(tid, T - 1)];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        if (j * 256 + tid < pieces) reinterpret_cast<u32x4*>(smem)[j * 256 + tid] = pre[j];
+    if (tid < T) s_sg[tid] = sgv;
+#pragma unroll
+    for (int j = 0; j < 3; ++j)
+        if (j * 256 + tid < 2 * n_items) s_items[j * 256 + tid] = itv[j];
+    if (tid < P) {
+        s_slot[tid] = sl;
+        s_wts[tid] = wt;
+    }
+    for (int i = 1024 + tid; i < pieces; i += 256)
+        reinterpret_cast<u32x4*>(smem)[i] = reinterpret_cast<const u32x4*>(himg)[i];
+    __syncthreads();
+
+    down_combine_tasks<MAXUPL, NT>(down_exps, down_sh, smem, Ys, s_items, s_slot, s_wts, n_items, npass, r0, H, F, Fs,
+                                   s_sg, T, k, add_shared, h_blocks, y, [] {});
+}
+
+// ------------------------------------------------------------------------------------------------ fused small batch
+// The decode layer of a batch of at most kShCols tokens after the router, in one launch (k_q2_gu_route's gate/up
+// work-groups, then k_q2_down_combine's down work-groups), so that the down rows' weight loads run beside the
+// gate/up work instead of after a kernel boundary.  1-D grid: work-groups y * hbn + hb (y < max_items: item y,
+// rows block hb; y = max_items, hb = 0: the writer of the routing, dispatch and item table), then the down
+// work-groups, each owning kDcRows output rows of every item.  A down work-group routes the batch itself (ids and
+// weights in LDS, bitwise the writer's) and issues its first batch of weight loads before it waits for h.  The h
+// images pass through the workspace: every image dword in a tagged 64-bit word (q8_image_store with xchg), each
+// checked by itself, so no fence is needed; the router kernel of the same call cleared the words.  The down
+// work-groups come last in the grid: on every XCD all gate/up work-groups are dispatched before any down
+// work-group that waits for them, and a down work-group gives up after a bounded wait (its rows are then NaN).
+constexpr int kSpinLimit = 100000;
+
+template <int NIT, int MAXUPL, int DMAXUPL, int DNT>
+__global__ __launch_bounds__(256) void k_q2_moe_small(
+    const uint8_t* __restrict__ gate_exps, const uint8_t* __restrict__ up_exps, const uint8_t* __restrict__ gate_sh,
+    const uint8_t* __restrict__ up_sh, const uint8_t* __restrict__ down_exps, const uint8_t* __restrict__ down_sh,
+    const uint32_t* __restrict__ ximg, const float* __restrict__ logits, const float* __restrict__ sg, int T, int E,
+    int k, int H, int F, int Fs, int has_shared, int32_t* __restrict__ ids, float* __restrict__ wts,
+    int32_t* __restrict__ counts, int32_t* __restrict__ offsets, int32_t* __restrict__ perm,
+    int32_t* __restrict__ slot, int32_t* __restrict__ elist, int32_t* __restrict__ n_list, int4* __restrict__ items,
+    int max_items, int h_blocks, uint64_t* __restrict__ xchg, int npass, int add_shared, float* __restrict__ y) {
+    extern __shared__ __align__(16) uint32_t smem[];
+    __shared__ int s_slot[kSmallPairs];
+    __shared__ float s_wts[kSmallPairs];
+    __shared__ int4 s_items[2 * kDcItems];
+    __shared__ int s_ids[64];
+    __shared__ float s_sg[kShCols];
+    __shared__ int s_bad, s_nt;
+    const int hbn = h_blocks;  // rows blocks of the widest expert
+    const int n_gu = max_items * hbn + 1;
+    const int id = blockIdx.x, tid = threadIdx.x;
+    if (id < n_gu) {  // gate/up (or the writer)
+        const int yi = id / hbn, hb = id - yi * hbn;
+        gu_route_wg<NIT, MAXUPL>(yi, hb, smem, gate_exps, up_exps, gate_sh, up_sh, ximg, logits, T, E, k, H, F, Fs,
+                                 has_shared, ids, wts, counts, offsets, perm, slot, elist, n_list, items, max_items,
+                                 nullptr, h_blocks, xchg);
+        return;
+    }
+    // down rows r0 .. r0 + kDcRows - 1 of every item, then the combine
+    const int r0 = (id - n_gu) * kDcRows;
+    const int P = T * k, n_sh = has_shared ? 1 : 0;
+    const int rows = P + n_sh * T;
+    const int lane = tid & 63, wave = tid >> 6;
+    float* Ys = reinterpret_cast<float*>(smem + (size_t)(P + T) * h_blocks * kImgDw);
+    if (tid == 0) {
+        s_bad = 0;
+        if (has_shared) {
+            s_items[0] = make_int4(kItemShared, P, T, 0);
+            s_items[1] = make_int4(1, 2, 3, 0);
+        }
+    }
+    if (tid < T) s_sg[tid] = sg[tid];
+    if (P <= 64) {
+        // the batch's routing (one wave per token: ids and weights, bitwise the writer's), then one wave derives the
+        // dispatch and the item table by cross-lane counts, lane p holding pair p: its slot is the pairs with a
+        // smaller expert id plus the earlier pairs with its own; an expert's item sits at its rank among the
+        // touched experts
+        if (wave < T) route_token(logits + (size_t)wave * E, E, k, nullptr, nullptr, s_ids + wave * k, s_wts + wave * k);
+        __syncthreads();
+        if (wave == 0) {
+            const int me = lane < P ? s_ids[lane] : 0x7FFFFFFF;
+            int lt = 0, before = 0, cnt = 0, tk0 = 0, tk1 = 0, tk2 = 0, tk3 = 0;
+            for (int q = 0; q < P; ++q) {
+                const int o = __builtin_amdgcn_readlane(me, q);
+                lt += o < me ? 1 : 0;
+                if (o == me) {
+                    tk0 = cnt == 0 ? q / k : tk0;
+                    tk1 = cnt == 1 ? q / k : tk1;
+                    tk2 = cnt == 2 ? q / k : tk2;
+                    tk3 = cnt == 3 ? q / k : tk3;
+                    before += q < lane ? 1 : 0;
+                    ++cnt;
+                }
+            }
+            const bool fst = lane < P && before == 0;
+            const unsigned long long firsts = __ballot(fst);
+            int rank = 0;
+            for (unsigned long long m = firsts; m; m &= m - 1)
+                rank += __builtin_amdgcn_readlane(me, __builtin_ctzll(m)) < me ? 1 : 0;
+            if (lane < P) s_slot[lane] = lt + before;
+            if (fst) {
+                s_items[2 * (n_sh + rank)] = make_int4(me, lt, cnt, tk0);
+                s_items[2 * (n_sh + rank) + 1] = make_int4(tk1, tk2, tk3, 0);
+            }
+            if (lane == 0) s_nt = __popcll(firsts);
+        }
+    } else {
+        SmallDispatchLds& R = *reinterpret_cast<SmallDispatchLds*>(Ys + (size_t)(P + T) * kDcRows);
+        small_route_dispatch(logits, T, E, k, false, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
+                             nullptr, nullptr, 0, has_shared, 1 << 30, kShCols, R);
+        for (int j = tid; j < R.n_touched; j += 256) {
+            const int e = R.el[j], first = R.off[e], n = R.cnt[e];
+            int tk[4] = {0, 0, 0, 0};
+            for (int q = 0; q < 4 && q < n; ++q) tk[q] = R.perm[first + q] / k;
+            s_items[2 * (n_sh + j)] = make_int4(e, first, n, tk[0]);
+            s_items[2 * (n_sh + j) + 1] = make_int4(tk[1], tk[2], tk[3], 0);
+        }
+        if (tid < P) {
+            s_slot[R.perm[tid]] = tid;
+            s_wts[tid] = R.wts[tid];
+        }
+        if (tid == 0) s_nt = R.n_touched;
+    }
+    __syncthreads();
+    const int n_items = n_sh + s_nt;
+    auto wait_h = [&] {
+        // every image word of the batch's h rows, eight per thread at a time: all loads in flight together (they
+        // go out behind this work-group's weight loads, so they return once those have), then the words whose tag
+        // is not set yet are read again until it is (a bounded wait)
+        const int words = rows * h_blocks * kXchgSlots;
+        bool ok = true;
+        for (int base = 0; base < words; base += 8 * 256) {
+            uint64_t v[8];
+            int at[8];
+            bool need[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int i = base + j * 256 + tid;
+                const int blk = i / kXchgSlots;
+                const int r = blk / h_blocks, hb = blk - r * h_blocks;
+                need[j] = i < words && hb * 32 < (r < P ? F : Fs);
+                at[j] = min(i, words - 1);
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = need[j] ? xchg_get(xchg + at[j]) : (1ull << 32);
+            for (int spin = 0;; ++spin) {
+                bool all = true;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) all = all && (!need[j] || (v[j] >> 32) == 1u);
+                if (all) break;
+                if (spin == kSpinLimit) {
+                    ok = false;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(4);
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    if (need[j] && (v[j] >> 32) != 1u) v[j] = xchg_get(xchg + at[j]);
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int i = base + j * 256 + tid;
+                const int blk = i / kXchgSlots, wd = i - blk * kXchgSlots;
+                if (need[j]) smem[(size_t)blk * kImgDw + wd] = (uint32_t)v[j];
+            }
+        }
+        if (!ok) s_bad = 1;
+        __syncthreads();
+    };
+    down_combine_tasks<DMAXUPL, DNT>(down_exps, down_sh, smem, Ys, s_items, s_slot, s_wts, n_items, npass, r0, H, F,
+                                     Fs, s_sg, T, k, add_shared, h_blocks, y, wait_h);
+    __syncthreads();
+    if (s_bad && tid < T * kDcRows) {  // a producer never arrived: the rows are not valid
+        const int t = tid / kDcRows, rl = tid - t * kDcRows;
+        if (r0 + rl < H) y[(size_t)t * H + r0 + rl] = __builtin_nanf("");
     }
 }
 
@@ -1895,9 +2116,10 @@ hipError_t launch_prep(const float* x, int64_t n, uint8_t* xq, uint16_t* xb, hip
 hipError_t launch_router(const float* xf, const uint16_t* xb, const uint16_t* W, const uint16_t* w_inp,
                          const float* bias, int H, int E, int rows_total, int T, float* logits, int ld_logits, float* sg,
                          uint32_t* ximg, int tile_rows, int img_natural, hipStream_t s, const float* rprev, float eps,
-                         float* xout) {
-    // the fused junction is the row-per-wave path's, for rows up to 4096
+                         float* xout, uint4* clear, int clear_n16) {
+    // the fused junction is the row-per-wave path's, for rows up to 4096; so is the clearing of the exchange
     if (rprev && (tile_rows || !xf || H > 4096)) return hipErrorInvalidValue;
+    if (clear_n16 && (tile_rows || !clear)) return hipErrorInvalidValue;
     const int chunks = H / 8;
     const int maxc = (chunks + 63) / 64;
     // tokens staged per block: 4 for decode batches (more blocks, short staging), 16 (<= 64 KiB of bf16) beyond
@@ -1923,7 +2145,7 @@ hipError_t launch_router(const float* xf, const uint16_t* xb, const uint16_t* W,
     const size_t lds = (size_t)tile * H * 2;
 #define SMOE_ROUTER(C)                                                                                          \
     hipLaunchKernelGGL(k_router<C>, grid, dim3(256), lds, s, xf, xb, W, w_inp, bias, H, E, rows_total, T, tile, \
-                       logits, ld_logits, sg, ximg, img_natural, rprev, eps, xout)
+                       logits, ld_logits, sg, ximg, img_natural, rprev, eps, xout, clear, clear_n16)
     if (maxc <= 2) SMOE_ROUTER(2);
     else if (maxc <= 4) SMOE_ROUTER(4);
     else if (maxc <= 8) SMOE_ROUTER(8);
@@ -2081,6 +2303,76 @@ hipError_t launch_q2_down_combine(const uint8_t* down_exps, const uint8_t* down_
     else if (maxupl <= 4) SMOE_DC(4, 2);
     else SMOE_DC(8, 1);
 #undef SMOE_DC
+    return hipGetLastError();
+}
+
+size_t moe_small_lds(int T, int k, int H, int h_blocks) {
+    const size_t rows = (size_t)T * k + T;
+    const size_t down = rows * h_blocks * kImgDw * 4 + rows * kDcRows * 4 + sizeof(SmallDispatchLds);
+    size_t gu = (size_t)kGuCols * (H >> 5) * kImgDw * 4 + 16 + sizeof(GuRouteLds);
+    if (gu < sizeof(SmallDispatchLds)) gu = sizeof(SmallDispatchLds);
+    return down > gu ? down : gu;
+}
+
+size_t moe_small_xchg_bytes(int T, int k, int max_items, int h_blocks) {
+    const size_t rows = (size_t)T * k + T;
+    (void)max_items;
+    const size_t bytes = rows * h_blocks * kXchgSlots * 8;
+    return (bytes + 15) / 16 * 16;
+}
+
+bool moe_small_ok(int T, int k, int H, int F, int Fs, int has_shared, int h_blocks) {
+    if (!down_combine_ok(T, k, h_blocks)) return false;
+    if (moe_small_lds(T, k, H, h_blocks) > 96 * 1024) return false;
+    int nit, upl;
+    gu_shape(H, nit, upl);
+    for (const int Fe : {F, has_shared ? Fs : 0}) {
+        if (Fe <= 0) continue;
+        const int dpr = Fe >> 7, lpr = lanes_per_row_host(dpr);
+        if (dpr / lpr > 2) return false;  // down rows of at most 2 units per lane (F up to 1024 x 2^a)
+    }
+    return true;
+}
+
+hipError_t launch_q2_moe_small(const uint8_t* gate_exps, const uint8_t* up_exps, const uint8_t* gate_sh,
+                               const uint8_t* up_sh, const uint8_t* down_exps, const uint8_t* down_sh,
+                               const uint32_t* ximg, const float* logits, const float* sg, int T, int E, int k, int H,
+                               int F, int Fs, int has_shared, int32_t* ids, float* wts, int32_t* counts,
+                               int32_t* offsets, int32_t* perm, int32_t* slot, int32_t* elist, int32_t* n_list,
+                               int4* items, int max_items, int h_blocks, uint8_t* xchg, int add_shared, float* y,
+                               hipStream_t s) {
+    if (T < 1 || T > kShCols || T * k > kSmallPairs || E > 1024 || max_items + 1 > kDcItems ||
+        !moe_small_ok(T, k, H, F, Fs, has_shared, h_blocks))
+        return hipErrorInvalidValue;
+    int npass = 1, dmaxupl = 1;
+    for (const int Fe : {F, has_shared ? Fs : 0}) {
+        if (Fe <= 0) continue;
+        const int dpr = Fe >> 7, lpr = lanes_per_row_host(dpr), rpi = 64 / lpr;
+        const int np = (kDcRows + rpi - 1) / rpi, u = dpr / lpr;
+        npass = np > npass ? np : npass;
+        dmaxupl = u > dmaxupl ? u : dmaxupl;
+    }
+    uint64_t* xw = reinterpret_cast<uint64_t*>(xchg);
+    const int n_gu = max_items * h_blocks + 1;
+    dim3 grid((unsigned)(n_gu + (H + kDcRows - 1) / kDcRows));
+    int nit, upl;
+    gu_shape(H, nit, upl);
+    const size_t lds = moe_small_lds(T, k, H, h_blocks);
+#define SMOE_MS(N, U)                                                                                                \
+    do {                                                                                                             \
+        if (dmaxupl == 1)                                                                                            \
+            hipLaunchKernelGGL((k_q2_moe_small<N, U, 1, 4>), grid, dim3(256), lds, s, gate_exps, up_exps, gate_sh,    \
+                               up_sh, down_exps, down_sh, ximg, logits, sg, T, E, k, H, F, Fs, has_shared, ids, wts,  \
+                               counts, offsets, perm, slot, elist, n_list, items, max_items, h_blocks, xw, npass,      \
+                               add_shared, y);                                                                \
+        else                                                                                                         \
+            hipLaunchKernelGGL((k_q2_moe_small<N, U, 2, 4>), grid, dim3(256), lds, s, gate_exps, up_exps, gate_sh,    \
+                               up_sh, down_exps, down_sh, ximg, logits, sg, T, E, k, H, F, Fs, has_shared, ids, wts,  \
+                               counts, offsets, perm, slot, elist, n_list, items, max_items, h_blocks, xw, npass,      \
+                               add_shared, y);                                                                \
+    } while (0)
+    SMOE_SHAPE_DISPATCH(SMOE_MS)
+#undef SMOE_MS
     return hipGetLastError();
 }
 

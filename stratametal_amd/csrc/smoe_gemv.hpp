@@ -147,10 +147,23 @@ __device__ __forceinline__ int half_sum_i(int v) {
     return v + xor_swap_i<16>(v);
 }
 
+// The h image exchange of the fused small-batch layer (k_q2_moe_small): image dwords 0..9 of a block, each in a
+// 64-bit word {dword, tag} written and read as one agent-scope atomic, tag 1 once written (the router kernel of the
+// same call clears the words first), so that every word is checked by itself and needs no fence.
+constexpr int kXchgSlots = 10;
+__device__ __forceinline__ void xchg_put(uint64_t* w, uint32_t v) {
+    __hip_atomic_store(w, (uint64_t)v | (1ull << 32), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t xchg_get(const uint64_t* w) {
+    return __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // A 32-lane half wave quantises one block (lane & 31 = position) and writes its image, split or `natural`;
 // `sc` is 32 bytes of LDS scratch owned by the half (natural layout only).  Every lane of the half must call
-// it; `store` false skips the global store.
-__device__ __forceinline__ void q8_image_store(float v, bool store, uint8_t* sc, uint32_t* img, bool natural = false) {
+// it; `store` false skips the global store.  With `xchg` (split layout only) the image goes to kXchgSlots
+// tagged exchange words instead of `img`.
+__device__ __forceinline__ void q8_image_store(float v, bool store, uint8_t* sc, uint32_t* img, bool natural = false,
+                                               uint64_t* xchg = nullptr) {
     const int l32 = threadIdx.x & 31;
     const float a = half_max(__builtin_fabsf(v));
     float d = a / 127.0f;
@@ -180,12 +193,20 @@ __device__ __forceinline__ void q8_image_store(float v, bool store, uint8_t* sc,
         vl |= xor_swap_i<4>(vl);
         vh |= xor_swap_i<8>(vh);
         vl |= xor_swap_i<8>(vl);
-        if (store && (l32 & 14) == 0)
-            *reinterpret_cast<uint2*>(img + 4 * (l32 >> 4) + 2 * (l32 & 1)) = make_uint2((uint32_t)vh, (uint32_t)vl);
+        if (store && (l32 & 14) == 0) {
+            const int i0 = 4 * (l32 >> 4) + 2 * (l32 & 1);
+            if (xchg) {
+                xchg_put(xchg + i0, (uint32_t)vh);
+                xchg_put(xchg + i0 + 1, (uint32_t)vl);
+            } else {
+                *reinterpret_cast<uint2*>(img + i0) = make_uint2((uint32_t)vh, (uint32_t)vl);
+            }
+        }
     }
-    if (store) {
-        if (l32 == 8) img[8] = f2u(f16_to_f32(f32_to_f16(d)));
-        if (l32 == 9) img[9] = (uint32_t)sq;
+    if (store && (l32 == 8 || l32 == 9)) {
+        const uint32_t w = l32 == 8 ? f2u(f16_to_f32(f32_to_f16(d))) : (uint32_t)sq;
+        if (xchg) xchg_put(xchg + l32, w);
+        else img[l32] = w;
     }
 }
 

@@ -15,9 +15,10 @@ hipError_t launch_prep(const float* x, int64_t n, uint8_t* xq, uint16_t* xb, hip
 hipError_t launch_router(const float* xf, const uint16_t* xb, const uint16_t* W, const uint16_t* w_inp,
                          const float* bias, int H, int E, int rows_total, int T, float* logits, int ld_logits, float* sg,
                          uint32_t* ximg, int tile_rows, int img_natural, hipStream_t s, const float* rprev = nullptr,
-                         float eps = 0.0f, float* xout = nullptr);
+                         float eps = 0.0f, float* xout = nullptr, uint4* clear = nullptr, int clear_n16 = 0);
 // (tile_rows: many tokens, row x token tiles from xb when given, else from xf; img_natural: write ximg in the IQ2_S
-// kernels' natural order; rprev: the fused stack junction, x = RMSNorm(xf + rprev) written to xout)
+// kernels' natural order; rprev: the fused stack junction, x = RMSNorm(xf + rprev) written to xout; clear: 16-byte
+// units zeroed for the exchange of the k_q2_moe_small launch after it)
 hipError_t launch_topk(const float* logits, int ld_logits, int T, int E, int k, int32_t* ids, float* wts, hipStream_t s);
 hipError_t launch_dispatch(const int32_t* ids, int P, int E, int32_t* counts, int32_t* offsets, int32_t* perm,
                            int32_t* slot, int32_t* elist, int32_t* n_list, int4* items, int max_items, int T, int k,
@@ -51,6 +52,17 @@ hipError_t launch_q2_down_combine(const uint8_t* down_exps, const uint8_t* down_
                                   const float* sg, const int4* items, int n_items, int H, int F, int Fs,
                                   const int32_t* slot, const float* wts, int T, int k, int add_shared, float* y,
                                   hipStream_t s);
+// the two above in one launch (k_q2_moe_small): gate/up work-groups hand their h images to down-and-combine
+// work-groups through `xchg` (moe_small_xchg_bytes, cleared by the router launch before it)
+bool moe_small_ok(int T, int k, int H, int F, int Fs, int has_shared, int h_blocks);
+size_t moe_small_xchg_bytes(int T, int k, int max_items, int h_blocks);
+hipError_t launch_q2_moe_small(const uint8_t* gate_exps, const uint8_t* up_exps, const uint8_t* gate_sh,
+                               const uint8_t* up_sh, const uint8_t* down_exps, const uint8_t* down_sh,
+                               const uint32_t* ximg, const float* logits, const float* sg, int T, int E, int k, int H,
+                               int F, int Fs, int has_shared, int32_t* ids, float* wts, int32_t* counts,
+                               int32_t* offsets, int32_t* perm, int32_t* slot, int32_t* elist, int32_t* n_list,
+                               int4* items, int max_items, int h_blocks, uint8_t* xchg, int add_shared, float* y,
+                               hipStream_t s);
 hipError_t launch_residual_rmsnorm(const float* x, const float* r, int n_rows, int n, float eps, float* out,
                                    hipStream_t s);
 hipError_t launch_combine(const float* Y, const int32_t* slot, const float* wts, int k, int H, int P, int T,

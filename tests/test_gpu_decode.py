@@ -245,6 +245,14 @@ CASES = [
      True),
     # 3200 pairs: the dispatch runs as chunk histograms, one scan and chunk ranks
     ("many pairs, top-32", dict(n_embd=256, n_ff=128, n_ff_shared=128, n_expert=128, top_k=32), 100, 17, True),
+    # batches of at most 4 tokens run as the router plus one fused launch (gate/up and down-with-combine
+    # work-groups exchanging h through tagged words): its variants
+    ("fused, no shared expert, T=2", dict(sh_type=-1, n_expert=64), 2, 21, True),
+    ("fused, shared not added, T=4", {}, 4, 22, False),
+    ("fused, 96 pairs (the down work-groups' LDS dispatch)",
+     dict(n_embd=256, n_ff=128, n_ff_shared=128, n_expert=128, top_k=32), 3, 23, True),
+    ("fused, shared wider than routed, T=3", dict(n_embd=2048, n_ff=256, n_ff_shared=512, n_expert=32, top_k=4), 3,
+     24, True),
 ]
 
 
