@@ -120,6 +120,49 @@ smoe_status smoe_forward_residual(const smoe_geom* g, const smoe_weights* w, con
                                   float eps, float* x, int32_t n_tokens, float* y, int32_t add_shared,
                                   void* workspace, size_t workspace_bytes, const smoe_trace* trace, void* hip_stream);
 
+/* ---------------------------------------------------------------------------------------------- layer ends */
+
+/* The hyper-connection ends of the layer call: FfnExec::run reads the MoE block's input from hc residual streams
+ * through the gated residual (gr_read) and adds the block's output back onto every stream (gr_write)
+ * (metal/src/layer_exec.cpp:469,531; metal/include/strata/metal/gr.hpp:22-48).  Per token R is [hc][n_embd] f32:
+ *   xn = R * rs_c * norm (rs_c = 1 / sqrt(mean(R_c^2) + eps)), act = bf16(xn);
+ *   lq = bf16(silu((act . down_r) / hc)); mixed_d = (sum_c xn_cd * sigmoid(lq . up_{c n_embd + d})) / hc;
+ *   inject_c = act . inject_c;   out_cd = R_cd + y_d * 2 sigmoid(inject_c / hc).
+ * Shapes: n_embd % 8 == 0 and at most 4096, hc <= 8, hc * n_embd <= 16384, hc_lr % 8 == 0 and at most 2048. */
+typedef struct {
+    int32_t hc;             /* residual streams (the reference model's 4: include/strata/core/layout.hpp:48-49) */
+    int32_t hc_lr;          /* width of the gate's low-rank projection (320) */
+    float eps;              /* the per-stream RMSNorm's epsilon (FfnExec::run passes 1e-6) */
+    const float* norm;      /* hc_norm: [hc][n_embd] f32, the stored (1 + w) */
+    const uint16_t* down;   /* hc_down: [hc_lr][hc * n_embd] bf16 */
+    const uint16_t* up;     /* hc_up: [hc * n_embd][hc_lr] bf16 */
+    const uint16_t* inject; /* hc_inj: [hc][hc * n_embd] bf16 */
+} smoe_hc;
+
+/* Workspace bytes of smoe_hc_read for up to max_tokens tokens (0 on a bad shape). */
+size_t smoe_hc_read_workspace_bytes(const smoe_hc* hc, int32_t n_embd, int32_t max_tokens);
+
+/* gr_read for n_tokens tokens: R [T][hc][n_embd] -> mixed [T][n_embd], inject [T][hc] (inject may be NULL: the
+ * final mixer, nothing written).  Replaces gr_read (metal/include/strata/metal/gr.hpp:44-46) with bf16 activations. */
+smoe_status smoe_hc_read(const smoe_hc* hc, int32_t n_embd, const float* R, int32_t n_tokens, float* mixed,
+                         float* inject, void* workspace, size_t workspace_bytes, void* hip_stream);
+
+/* gr_write: R_out[t][c][d] = R[t][c][d] + y[t][d] * 2 sigmoid(inject[t][c] / hc); R_out may be R.
+ * Replaces gr_write (metal/include/strata/metal/gr.hpp:48). */
+smoe_status smoe_hc_write(const smoe_hc* hc, int32_t n_embd, const float* R, const float* y, const float* inject,
+                          int32_t n_tokens, float* R_out, void* hip_stream);
+
+/* Workspace bytes of smoe_ffn_run for up to max_tokens tokens (0 on bad geometry). */
+size_t smoe_ffn_workspace_bytes(const smoe_geom* g, const smoe_hc* hc, int32_t max_tokens);
+
+/* The whole layer call FfnExec::run(residual, out, add_shared, trace) (metal/include/strata/metal/layer_exec.hpp:
+ * 135-137, metal/src/layer_exec.cpp:462-531): gr_read of the residual streams, the MoE block on `mixed`
+ * (smoe_forward, SMOE_PATH_AUTO), gr_write of its output back onto the streams.  residual and out are
+ * [T][hc][n_embd] f32 (out may be residual); `trace` covers the MoE block as in smoe_forward. */
+smoe_status smoe_ffn_run(const smoe_geom* g, const smoe_weights* w, const smoe_hc* hc, const float* residual,
+                         int32_t n_tokens, float* out, int32_t add_shared, void* workspace, size_t workspace_bytes,
+                         const smoe_trace* trace, void* hip_stream);
+
 /* ---------------------------------------------------------------------------------------------- no allocation */
 
 /* Bytes of the library's static device scratch (one array per GPU, held from the library's load until the

@@ -1,8 +1,8 @@
 // include/smoe_ffn.hpp - the C++ FfnExec-shaped operator over the C ABI in smoe.h (header-only).
 //
 // Mirrors the reference's per-layer feed-forward operator, FfnExec::load / FfnExec::run
-// (metal/include/strata/metal/layer_exec.hpp:113-140), for its MoE interior (metal/src/layer_exec.cpp:470-530,
-// `mixed` to `combined`): load() takes the layer's device tensors and geometry once and owns every buffer the
+// (metal/include/strata/metal/layer_exec.hpp:113-140): run() is its MoE interior (metal/src/layer_exec.cpp:470-530,
+// `mixed` to `combined`), run_layer() the whole call with the hyper-connection ends around it; load() takes the layer's device tensors and geometry once and owns every buffer the
 // call needs, sized for a maximum token count, so that run() allocates nothing; status codes become
 // exceptions (the reference throws MetalError, metal/include/strata/metal/device.hpp:28-31); a traced run
 // copies the stage outputs to host vectors, as FfnTrace does (layer_exec.hpp:100-109).  Uses only smoe.h and
@@ -50,12 +50,19 @@ class FfnExec {
    public:
     // The layer's tensors (device pointers into the loaded model, e.g. a GGUF mapping) and geometry; buffers
     // for up to `max_tokens` tokens per run, and for tracing when `with_trace`.
-    static FfnExec load(const smoe_geom& geom, const smoe_weights& weights, int32_t max_tokens, bool with_trace = false) {
+    // With `hc` (the layer's hyper-connection tensors) the operator also runs the whole layer call, run_layer.
+    static FfnExec load(const smoe_geom& geom, const smoe_weights& weights, int32_t max_tokens, bool with_trace = false,
+                        const smoe_hc* hc = nullptr) {
         FfnExec f;
         f.g_ = geom;
         f.w_ = weights;
         f.max_tokens_ = max_tokens;
-        f.ws_bytes_ = smoe_workspace_bytes(&f.g_, max_tokens);
+        if (hc) {
+            f.hc_ = *hc;
+            f.has_hc_ = true;
+        }
+        // the layer call's workspace begins with the block's own, so one buffer serves run and run_layer
+        f.ws_bytes_ = hc ? smoe_ffn_workspace_bytes(&f.g_, hc, max_tokens) : smoe_workspace_bytes(&f.g_, max_tokens);
         if (f.ws_bytes_ == 0) throw Error(SMOE_EINVAL, std::string("FfnExec::load: ") + smoe_last_error());
         check_hip(hipMalloc(&f.ws_, f.ws_bytes_), "FfnExec::load workspace");
         if (with_trace) {
@@ -76,6 +83,8 @@ class FfnExec {
             release();
             g_ = o.g_;
             w_ = o.w_;
+            hc_ = o.hc_;
+            has_hc_ = o.has_hc_;
             max_tokens_ = o.max_tokens_;
             ws_ = std::exchange(o.ws_, nullptr);
             ws_bytes_ = std::exchange(o.ws_bytes_, 0);
@@ -128,6 +137,19 @@ class FfnExec {
             check_hip(hipEventElapsedTime(&trace->stage_ms[i], ev_[i], ev_[i + 1]), "FfnExec stage time");
     }
 
+    // The whole layer call of the reference's FfnExec::run(residual, out, add_shared) (metal/src/layer_exec.cpp:
+    // 462-531): gr_read of the residual streams [T][hc][n_embd], the MoE block, gr_write of its output onto every
+    // stream into out (which may be residual).  Needs load(..., hc).
+    void run_layer(const float* residual, float* out, int32_t n_tokens, bool add_shared, hipStream_t stream = nullptr) {
+        if (!has_hc_) throw Error(SMOE_EINVAL, "FfnExec::run_layer: operator loaded without hyper-connection tensors");
+        if (n_tokens > max_tokens_)
+            throw Error(SMOE_ESIZE, "FfnExec::run_layer: " + std::to_string(n_tokens) + " tokens, loaded for " +
+                                        std::to_string(max_tokens_));
+        check(smoe_ffn_run(&g_, &w_, &hc_, residual, n_tokens, out, add_shared ? 1 : 0, ws_, ws_bytes_, nullptr,
+                           stream),
+              "FfnExec::run_layer");
+    }
+
     // Device bytes this operator owns (workspace and trace buffers; the weights are the caller's).
     uint64_t gpu_bytes() const { return ws_bytes_ + tr_bytes_; }
     const smoe_geom& geom() const { return g_; }
@@ -165,6 +187,8 @@ class FfnExec {
 
     smoe_geom g_{};
     smoe_weights w_{};
+    smoe_hc hc_{};
+    bool has_hc_ = false;
     int32_t max_tokens_ = 0;
     void* ws_ = nullptr;
     size_t ws_bytes_ = 0;

@@ -94,6 +94,9 @@ def _set_sigs(L):
         "or_moe_decode_ref": (i32, [vp, vp, vp, i32, vp, i32, i32]),
         "or_moe_prefill": (i32, [vp, vp, vp, i32, vp, i32, vp, i32]),
         "or_moe_decode_pool": (i32, [vp, vp, vp, i32, vp, i32, i32]),
+        "or_hc_read_dev": (i32, [vp, i32, i32, i32, i32, f32, vp, vp, vp, vp, vp, vp]),
+        "or_hc_read_ref": (i32, [vp, i32, i32, i32, i32, f32, vp, vp, vp, vp, i32, vp, vp]),
+        "or_hc_write_dev": (None, [vp, vp, vp, i32, i32, i32, vp]),
         "or_row_bytes": (i64, [i32, i64]),
     }
     for name, (res, args) in sigs.items():
@@ -471,3 +474,62 @@ def rel_l1_rows(got: np.ndarray, want: np.ndarray) -> np.ndarray:
     num = np.abs(got - want).sum(axis=1)
     den = np.abs(want).sum(axis=1)
     return np.where(den > 0, num / np.where(den > 0, den, 1.0), np.where(num == 0, 0.0, 1.0))
+
+
+# ------------------------------------------------------------------------------------------------ layer ends
+
+@dataclass
+class HcWeights:
+    """The hyper-connection tensors of one layer: norm [hc][n] f32 (the stored 1 + w), down [hc_lr][hc n], up
+    [hc n][hc_lr] and inject [hc][hc n] bf16 bits."""
+    hc: int
+    hc_lr: int
+    eps: float
+    norm: np.ndarray
+    down: np.ndarray
+    up: np.ndarray
+    inject: np.ndarray
+
+
+def make_hc(n: int, hc: int, hc_lr: int, seed: int, eps: float = 1e-6) -> HcWeights:
+    """Seeded hyper-connection tensors: norm = 1 + 0.1 N(0,1) in f32, down/up N(0, 0.2^2), inject N(0, 0.05^2) as bf16
+    (the reference test's fixture scales, metal/src/gr_parity.cpp:170-200), from the counter generator."""
+    hd = hc * n
+    norm = (np.float32(1.0) + gen_normal(seed, 30, hd, 0.1)).astype(np.float32)
+    return HcWeights(hc, hc_lr, eps, norm, gen_bf16(seed, 31, hc_lr * hd, 0.2), gen_bf16(seed, 32, hd * hc_lr, 0.2),
+                     gen_bf16(seed, 33, hc * hd, 0.05))
+
+
+def hc_read_dev(R: np.ndarray, n: int, w: HcWeights):
+    R = np.ascontiguousarray(R, dtype=np.float32)
+    T = R.size // (w.hc * n)
+    mixed = np.empty((T, n), np.float32)
+    inject = np.empty((T, w.hc), np.float32)
+    rc = lib().or_hc_read_dev(_p(R), T, n, w.hc, w.hc_lr, w.eps, _p(w.norm), _p(w.down), _p(w.up), _p(w.inject),
+                              _p(mixed), _p(inject))
+    if rc != 0:
+        raise ValueError("oracle rejected the hyper-connection shape")
+    return mixed, inject
+
+
+def hc_read_ref(R: np.ndarray, n: int, w: HcWeights, round_act: bool = True):
+    R = np.ascontiguousarray(R, dtype=np.float32)
+    T = R.size // (w.hc * n)
+    mixed = np.empty((T, n), np.float32)
+    inject = np.empty((T, w.hc), np.float32)
+    rc = lib().or_hc_read_ref(_p(R), T, n, w.hc, w.hc_lr, w.eps, _p(w.norm), _p(w.down), _p(w.up), _p(w.inject),
+                              int(round_act), _p(mixed), _p(inject))
+    if rc != 0:
+        raise ValueError("oracle rejected the hyper-connection shape")
+    return mixed, inject
+
+
+def hc_write_dev(R: np.ndarray, y: np.ndarray, inject: np.ndarray, n: int, hc: int):
+    R = np.ascontiguousarray(R, dtype=np.float32)
+    y = np.ascontiguousarray(y, dtype=np.float32)
+    inject = np.ascontiguousarray(inject, dtype=np.float32)
+    T = R.size // (hc * n)
+    out = np.empty_like(R)
+    lib().or_hc_write_dev(_p(R), _p(y), _p(inject), T, n, hc, _p(out))
+    return out
+

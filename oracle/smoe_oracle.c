@@ -983,3 +983,160 @@ int or_moe_prefill(const or_geom* g, const or_weights* w, const float* x, int T,
     free(perm); free(slot); free(parts); free(shared);
     return 0;
 }
+
+/* ------------------------------------------------------------------------------------------------ */
+/* The hyper-connection ends of FfnExec::run (metal/src/layer_exec.cpp:469,531): gr_read before the block and
+ * gr_write after it (metal/include/strata/metal/gr.hpp:1-48, metal/shaders/gr.metal, metal/src/gr.mm:85-155), one
+ * token at a time; R is [hc][n] (stream c at c * n).
+ *   xn = R * rs_c * w_norm (rs_c = 1 / sqrt(mean(R_c^2) + eps), the stored (1 + w) weight), act = bf16(xn);
+ *   proj_r = act . down_r (r < hc_lr), lo = silu(proj / hc), lq = bf16(lo);
+ *   gate_i = lq . up_i (i < hc * n), mixed_d = (sum_c xn_cd * sigmoid(gate_cd)) / hc;
+ *   inject_c = act . inj_c;  out_cd = R_cd + y_d * 2 sigmoid(inject_c / hc).
+ *
+ * Device order (stratametal_amd/csrc/smoe_hc.hip): per stream, thread i of 256 adds fmaf(v, v, acc) over
+ * d = i, i + 256, ... from 0, the xor butterfly 32..1 over each wave, the four wave sums ((w0 + w1) + w2) + w3;
+ * rs = 1 / sqrtf(ss / n + eps); xn = (R * rs) * w_norm.  The products with down and inj in the router's order
+ * (or_bf16_gemv_dev); the products with up with 8 lanes per row: lane l adds the 8-element chunks l, l + 8, ...
+ * (fma in element order from 0), then the xor butterfly 4, 2, 1.  silu(z) = z / (1 + exp(-z)) and sigmoid with
+ * or_expf; mixed = (((0 + g_0) + g_1) + ...) / hc in stream order. */
+
+static float stream_rs_dev(const float* r, int n, float eps) {
+    float th[256];
+    for (int i = 0; i < 256; ++i) {
+        float acc = 0.0f;
+        for (int d = i; d < n; d += 256) acc = fmaf(r[d], r[d], acc);
+        th[i] = acc;
+    }
+    float ws[4];
+    for (int w = 0; w < 4; ++w) {
+        float* lane = th + 64 * w;
+        for (int o = 32; o > 0; o >>= 1) {
+            float nxt[64];
+            for (int l = 0; l < 64; ++l) nxt[l] = lane[l] + lane[l ^ o];
+            memcpy(lane, nxt, sizeof nxt);
+        }
+        ws[w] = lane[0];
+    }
+    const float ss = ((ws[0] + ws[1]) + ws[2]) + ws[3];
+    return 1.0f / sqrtf(ss / (float)n + eps);
+}
+
+/* y[r] = x . w_r over n_in bf16 values with `lanes` lanes per row (lanes a power of two, at most 64). */
+static void bf16_gemv_lanes(const uint16_t* xb, const uint16_t* w, int n_in, int n_out, int lanes, float* y) {
+    const int chunks = n_in / 8;
+    for (int r = 0; r < n_out; ++r) {
+        const uint16_t* row = w + (size_t)r * n_in;
+        float lane[64];
+        for (int l = 0; l < lanes; ++l) {
+            float acc = 0.0f;
+            for (int c = l; c < chunks; c += lanes)
+                for (int i = 0; i < 8; ++i) acc = acc + or_f32_from_bf16(xb[8 * c + i]) * or_f32_from_bf16(row[8 * c + i]);
+            lane[l] = acc;
+        }
+        for (int o = lanes / 2; o > 0; o >>= 1) {
+            float nxt[64];
+            for (int l = 0; l < lanes; ++l) nxt[l] = lane[l] + lane[l ^ o];
+            memcpy(lane, nxt, sizeof(float) * (size_t)lanes);
+        }
+        y[r] = lane[0];
+    }
+}
+
+int or_hc_read_dev(const float* R, int n_tok, int n, int hc, int hc_lr, float eps, const float* norm,
+                   const uint16_t* down, const uint16_t* up, const uint16_t* inj, float* mixed, float* inject) {
+    if (n_tok < 0 || n <= 0 || hc <= 0 || hc_lr <= 0 || n % 8 || hc_lr % 8) return -1;
+    const int hd = hc * n;
+    float* xn = (float*)malloc(sizeof(float) * (size_t)hd);
+    uint16_t* act = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)hd);
+    float* proj = (float*)malloc(sizeof(float) * (size_t)hc_lr);
+    uint16_t* lq = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)hc_lr);
+    float* gate = (float*)malloc(sizeof(float) * (size_t)hd);
+    for (int t = 0; t < n_tok; ++t) {
+        const float* Rt = R + (size_t)t * hd;
+        for (int c = 0; c < hc; ++c) {
+            const float rs = stream_rs_dev(Rt + (size_t)c * n, n, eps);
+            for (int d = 0; d < n; ++d) {
+                const int i = c * n + d;
+                xn[i] = (Rt[i] * rs) * norm[i];
+                act[i] = or_bf16_from_f32(xn[i]);
+            }
+        }
+        or_bf16_gemv_dev(act, down, hd, hc_lr, proj);
+        if (inject) or_bf16_gemv_dev(act, inj, hd, hc, inject + (size_t)t * hc);
+        for (int r = 0; r < hc_lr; ++r) {
+            const float z = proj[r] / (float)hc;
+            lq[r] = or_bf16_from_f32(z / (1.0f + or_expf(-z)));
+        }
+        bf16_gemv_lanes(lq, up, hc_lr, hd, 8, gate);
+        for (int d = 0; d < n; ++d) {
+            float m = 0.0f;
+            for (int c = 0; c < hc; ++c) m = m + xn[c * n + d] * or_sigmoid(gate[c * n + d]);
+            mixed[(size_t)t * n + d] = m / (float)hc;
+        }
+    }
+    free(xn); free(act); free(proj); free(lq); free(gate);
+    return 0;
+}
+
+/* The reference's host gr_read (metal/src/pack_parity.cpp:7929-7969, metal/src/gr_parity.cpp:95-168): the norm
+ * and every product in double, libm exp; `round_act` false keeps xn and lo in f32 (the fp32_act contract). */
+int or_hc_read_ref(const float* R, int n_tok, int n, int hc, int hc_lr, float eps, const float* norm,
+                   const uint16_t* down, const uint16_t* up, const uint16_t* inj, int round_act, float* mixed,
+                   float* inject) {
+    if (n_tok < 0 || n <= 0 || hc <= 0 || hc_lr <= 0) return -1;
+    const int hd = hc * n;
+    float* xn = (float*)malloc(sizeof(float) * (size_t)hd);
+    float* act = (float*)malloc(sizeof(float) * (size_t)hd);
+    float* lq = (float*)malloc(sizeof(float) * (size_t)hc_lr);
+    for (int t = 0; t < n_tok; ++t) {
+        const float* Rt = R + (size_t)t * hd;
+        for (int c = 0; c < hc; ++c) {
+            double ms = 0.0;
+            for (int d = 0; d < n; ++d) ms += (double)Rt[c * n + d] * (double)Rt[c * n + d];
+            ms /= (double)n;
+            const float rs = (float)(1.0 / sqrt(ms + (double)eps));
+            for (int d = 0; d < n; ++d) {
+                const int i = c * n + d;
+                xn[i] = Rt[i] * rs * norm[i];
+                act[i] = round_act ? or_f32_from_bf16(or_bf16_from_f32(xn[i])) : xn[i];
+            }
+        }
+        for (int r = 0; r < hc_lr; ++r) {
+            double a = 0.0;
+            for (int i = 0; i < hd; ++i) a += (double)act[i] * (double)or_f32_from_bf16(down[(size_t)r * hd + i]);
+            const float z = (float)a / (float)hc;
+            const float lo = z / (1.0f + expf(-z));
+            lq[r] = round_act ? or_f32_from_bf16(or_bf16_from_f32(lo)) : lo;
+        }
+        for (int d = 0; d < n; ++d) {
+            float m = 0.0f;
+            for (int c = 0; c < hc; ++c) {
+                const int i = c * n + d;
+                double a = 0.0;
+                for (int r = 0; r < hc_lr; ++r) a += (double)lq[r] * (double)or_f32_from_bf16(up[(size_t)i * hc_lr + r]);
+                m += xn[i] * (1.0f / (1.0f + expf(-(float)a)));
+            }
+            mixed[(size_t)t * n + d] = m / (float)hc;
+        }
+        if (inject)
+            for (int c = 0; c < hc; ++c) {
+                double a = 0.0;
+                for (int i = 0; i < hd; ++i) a += (double)act[i] * (double)or_f32_from_bf16(inj[(size_t)c * hd + i]);
+                inject[(size_t)t * hc + c] = (float)a;
+            }
+    }
+    free(xn); free(act); free(lq);
+    return 0;
+}
+
+/* gr_write (metal/shaders/gr.metal:106-117): out_cd = R_cd + y_d * (2 * s_c), s_c = 1 / (1 + exp(-inject_c / hc)). */
+void or_hc_write_dev(const float* R, const float* y, const float* inject, int n_tok, int n, int hc, float* out) {
+    for (int t = 0; t < n_tok; ++t)
+        for (int c = 0; c < hc; ++c) {
+            const float s = or_sigmoid(inject[(size_t)t * hc + c] / (float)hc);
+            for (int d = 0; d < n; ++d) {
+                const size_t i = ((size_t)t * hc + c) * n + d;
+                out[i] = R[i] + y[(size_t)t * n + d] * (2.0f * s);
+            }
+        }
+}

@@ -135,6 +135,14 @@ int or_moe_prefill(const or_geom* g, const or_weights* w, const float* x, int n_
 int or_moe_decode_pool(const or_geom* g, const or_weights* w, const float* x, int n_tok, float* y, int add_shared,
                        int n_threads);
 
+/* The hyper-connection ends (gr_read / gr_write, one token each; R is [n_tok][hc][n]).  `inject` may be NULL. */
+int or_hc_read_dev(const float* R, int n_tok, int n, int hc, int hc_lr, float eps, const float* norm,
+                   const uint16_t* down, const uint16_t* up, const uint16_t* inj, float* mixed, float* inject);
+int or_hc_read_ref(const float* R, int n_tok, int n, int hc, int hc_lr, float eps, const float* norm,
+                   const uint16_t* down, const uint16_t* up, const uint16_t* inj, int round_act, float* mixed,
+                   float* inject);
+void or_hc_write_dev(const float* R, const float* y, const float* inject, int n_tok, int n, int hc, float* out);
+
 /* Byte sizes */
 int64_t or_row_bytes(int type, int64_t n);
 

@@ -50,6 +50,11 @@ class _Trace(C.Structure):
     _fields_ = [(n, C.c_void_p) for n in ("logits", "ids", "weights", "counts", "offsets", "perm", "slot", "sgate",
                                           "stage_events")]
 
+class _Hc(C.Structure):
+    _fields_ = [("hc", C.c_int32), ("hc_lr", C.c_int32), ("eps", C.c_float), ("norm", C.c_void_p),
+                ("down", C.c_void_p), ("up", C.c_void_p), ("inject", C.c_void_p)]
+
+
 STAGES = ("router", "route", "gate_up", "down", "combine")
 STAGE_EVENTS = len(STAGES) + 1
 
@@ -68,6 +73,11 @@ def lib():
             "smoe_forward_path": (i32, [vp, vp, vp, i32, vp, i32, vp, C.c_size_t, vp, i32, vp]),
             "smoe_forward_residual": (i32, [vp, vp, vp, vp, f32, vp, i32, vp, i32, vp, C.c_size_t, vp, vp]),
             "smoe_forward_static": (i32, [vp, vp, vp, i32, vp, i32, vp, vp]),
+            "smoe_hc_read_workspace_bytes": (C.c_size_t, [vp, i32, i32]),
+            "smoe_hc_read": (i32, [vp, i32, vp, i32, vp, vp, vp, C.c_size_t, vp]),
+            "smoe_hc_write": (i32, [vp, i32, vp, vp, vp, i32, vp, vp]),
+            "smoe_ffn_workspace_bytes": (C.c_size_t, [vp, vp, i32]),
+            "smoe_ffn_run": (i32, [vp, vp, vp, vp, i32, vp, i32, vp, C.c_size_t, vp, vp]),
             "smoe_router_topk": (i32, [vp, i32, i32, i32, vp, vp, vp]),
             "smoe_f32_to_bf16": (i32, [vp, i64, vp, vp]),
             "smoe_bf16_gemv": (i32, [vp, vp, vp, i32, i32, i32, vp]),
@@ -332,6 +342,99 @@ class MoELayer:
         return y
 
     __call__ = forward
+
+
+# ------------------------------------------------------------------------------------------------ layer ends
+
+class HyperConnection:
+    """The gated-residual ends of the layer call (smoe_hc_read / smoe_hc_write), the gr_read / gr_write pair of
+    FfnExec::run (metal/include/strata/metal/gr.hpp:44-48).  `norm` is [hc * n_embd] f32 (the stored 1 + w);
+    `down` [hc_lr][hc * n_embd], `up` [hc * n_embd][hc_lr] and `inject` [hc][hc * n_embd] are bf16 bits (int16)."""
+
+    def __init__(self, n_embd: int, hc: int, hc_lr: int, norm, down, up, inject, eps: float = 1e-6):
+        import torch
+        hd = hc * n_embd
+        _need(norm, "norm", torch.float32, numel=hd)
+        for t, name, k in ((down, "down", hc_lr * hd), (up, "up", hd * hc_lr), (inject, "inject", hc * hd)):
+            _need(t, name, torch.int16, numel=k)
+        self.n_embd, self.hc, self.hc_lr, self.eps = n_embd, hc, hc_lr, eps
+        self.tensors = (norm, down, up, inject)
+        self._c = _Hc(hc, hc_lr, eps, norm.data_ptr(), down.data_ptr(), up.data_ptr(), inject.data_ptr())
+        self._ws = None
+
+    def _stream_tensor(self, R, name="R"):
+        import torch
+        if R.dim() != 3 or tuple(R.shape[1:]) != (self.hc, self.n_embd):
+            raise SmoeError(-1, f"{name} must be (tokens, {self.hc}, {self.n_embd}), got {tuple(R.shape)}")
+        return _need(R, name, torch.float32)
+
+    def read(self, R, mixed=None, inject=None, stream=None):
+        """mixed [T][n_embd], inject [T][hc] of the streams R [T][hc][n_embd]."""
+        import torch
+        R = self._stream_tensor(R)
+        T = R.shape[0]
+        if mixed is None:
+            mixed = torch.empty((T, self.n_embd), dtype=torch.float32, device=R.device)
+        if inject is None:
+            inject = torch.empty((T, self.hc), dtype=torch.float32, device=R.device)
+        _need(mixed, "mixed", torch.float32, numel=T * self.n_embd)
+        _need(inject, "inject", torch.float32, numel=T * self.hc)
+        n = lib().smoe_hc_read_workspace_bytes(C.byref(self._c), self.n_embd, max(T, 1))
+        if n == 0:
+            raise SmoeError(-1, lib().smoe_last_error().decode() or "bad hyper-connection shape")
+        if self._ws is None or self._ws.numel() < n:
+            self._ws = torch.empty(n, dtype=torch.uint8, device=R.device)
+        _check(lib().smoe_hc_read(C.byref(self._c), self.n_embd, R.data_ptr(), T, mixed.data_ptr(), inject.data_ptr(),
+                                  self._ws.data_ptr(), self._ws.numel(), _stream(stream)))
+        return mixed, inject
+
+    def write(self, R, y, inject, out=None, stream=None):
+        """out = R + y * 2 sigmoid(inject / hc) on every stream; `out` may be R."""
+        import torch
+        R = self._stream_tensor(R)
+        T = R.shape[0]
+        _need(y, "y", torch.float32, numel=T * self.n_embd)
+        _need(inject, "inject", torch.float32, numel=T * self.hc)
+        if out is None:
+            out = torch.empty_like(R)
+        _need(out, "out", torch.float32, numel=R.numel())
+        _check(lib().smoe_hc_write(C.byref(self._c), self.n_embd, R.data_ptr(), y.data_ptr(), inject.data_ptr(), T,
+                                   out.data_ptr(), _stream(stream)))
+        return out
+
+
+class FfnLayer:
+    """FfnExec::run(residual, out, add_shared, trace) (metal/include/strata/metal/layer_exec.hpp:135-137): gr_read of
+    the residual streams, the MoE block, gr_write back onto the streams, in one smoe_ffn_run call.  Owns a workspace
+    sized for `max_tokens`."""
+
+    def __init__(self, g: Geom, weights: Dict, hc: HyperConnection, max_tokens: int, device="cuda"):
+        import torch
+        if hc.n_embd != g.n_embd:
+            raise SmoeError(-1, f"hyper connection width {hc.n_embd} != n_embd {g.n_embd}")
+        self.g, self.w, self.hc = g, weights, hc
+        self._gc, self._wc = g.c(), _weights_c(weights)
+        self.max_tokens = max_tokens
+        self.ws_bytes = lib().smoe_ffn_workspace_bytes(C.byref(self._gc), C.byref(hc._c), max_tokens)
+        if self.ws_bytes == 0:
+            raise SmoeError(-1, lib().smoe_last_error().decode() or "bad geometry")
+        self.ws = torch.empty(self.ws_bytes, dtype=torch.uint8, device=device)
+
+    def run(self, residual, out=None, add_shared: bool = True, stream=None):
+        import torch
+        R = self.hc._stream_tensor(residual, "residual")
+        T = R.shape[0]
+        if T > self.max_tokens:
+            raise SmoeError(-2, f"{T} tokens exceed the workspace's {self.max_tokens}")
+        if out is None:
+            out = torch.empty_like(R)
+        _need(out, "out", torch.float32, numel=R.numel())
+        _check(lib().smoe_ffn_run(C.byref(self._gc), C.byref(self._wc), C.byref(self.hc._c), R.data_ptr(), T,
+                                  out.data_ptr(), int(add_shared), self.ws.data_ptr(), self.ws_bytes, None,
+                                  _stream(stream)))
+        return out
+
+    __call__ = run
 
 
 # ------------------------------------------------------------------------------------------------ stages

@@ -173,7 +173,7 @@ const char* smoe_status_str(smoe_status s) {
 
 const char* smoe_last_error(void) { return g_last.c_str(); }
 
-int32_t smoe_abi_version(void) { return 103; }
+int32_t smoe_abi_version(void) { return 104; }
 
 size_t smoe_workspace_bytes(const smoe_geom* g, int32_t max_tokens) {
     if (check_geom(g) != SMOE_OK || max_tokens < 0) return 0;
@@ -186,7 +186,8 @@ bool overlaps(const void* a, const void* b, size_t bytes) {
     return x < z + bytes && z < x + bytes;
 }
 
-// Every check of a block call that can refuse it, made before its first launch.
+// Every check of a block call that can refuse it, made before its first launch (smoe_ffn_run runs it ahead of
+// its own first launch too).
 smoe_status check_forward(const smoe_geom* g, const smoe_weights* w, const float* x, int32_t n_tokens, const float* y,
                           const void* workspace, size_t workspace_bytes, int32_t path, const float* x_prev,
                           const float* r_prev) {
@@ -404,6 +405,151 @@ smoe_status smoe_forward(const smoe_geom* g, const smoe_weights* w, const float*
                          void* hip_stream) {
     return smoe_forward_path(g, w, x, n_tokens, y, add_shared, workspace, workspace_bytes, trace, SMOE_PATH_AUTO,
                              hip_stream);
+}
+
+}  // extern "C"
+
+// ------------------------------------------------------------------------------------------------ layer ends
+namespace {
+// gr_read's scratch: proj [T][hc_lr] and rs [T][hc]
+struct HcLayout {
+    size_t proj, rs, total;
+};
+HcLayout hc_layout(const smoe_hc& h, int64_t T) {
+    HcLayout L{};
+    size_t o = 0;
+    L.proj = o;
+    o = up(o + (size_t)T * h.hc_lr * 4);
+    L.rs = o;
+    o = up(o + (size_t)T * h.hc * 4);
+    L.total = o;
+    return L;
+}
+
+smoe_status check_hc(const smoe_hc* h, int32_t n_embd) {
+    if (!h) return fail(SMOE_ENULL, "hyper-connection weights are NULL");
+    if (!smoe::hc_shape_ok(n_embd, h->hc, h->hc_lr))
+        return fail(SMOE_EINVAL, "hyper connection: n_embd % 8 == 0 and <= 4096, hc in 1..8, hc * n_embd <= 16384, "
+                                 "hc_lr % 8 == 0 and <= 2048");
+    if (!(h->eps >= 0.0f) || h->eps == INFINITY) return fail(SMOE_EINVAL, "hyper connection: eps must be finite and >= 0");
+    if (!h->norm || !h->down || !h->up || !h->inject) return fail(SMOE_ENULL, "a hyper-connection tensor is NULL");
+    if (!aligned(h->norm, 4) || !aligned(h->down, 16) || !aligned(h->up, 16) || !aligned(h->inject, 16))
+        return fail(SMOE_EALIGN, "hyper-connection tensors: norm 4-byte, down/up/inject 16-byte aligned");
+    return SMOE_OK;
+}
+}  // namespace
+
+extern "C" {
+
+size_t smoe_hc_read_workspace_bytes(const smoe_hc* hc, int32_t n_embd, int32_t max_tokens) {
+    if (check_hc(hc, n_embd) != SMOE_OK || max_tokens < 0) return 0;
+    return hc_layout(*hc, max_tokens).total;
+}
+
+smoe_status smoe_hc_read(const smoe_hc* hc, int32_t n_embd, const float* R, int32_t n_tokens, float* mixed,
+                         float* inject, void* workspace, size_t workspace_bytes, void* hip_stream) {
+    smoe_status s = check_hc(hc, n_embd);
+    if (s != SMOE_OK) return s;
+    if (n_tokens < 0) return fail(SMOE_EINVAL, "hc_read: negative token count");
+    if (n_tokens == 0) return ok();
+    if (!R || !mixed || !workspace) return fail(SMOE_ENULL, "hc_read: NULL buffer");
+    if (!aligned(R, 4) || !aligned(mixed, 4) || (inject && !aligned(inject, 4)) || !aligned(workspace, kAlign))
+        return fail(SMOE_EALIGN, "hc_read: R, mixed, inject 4-byte, workspace 256-byte aligned");
+    const HcLayout L = hc_layout(*hc, n_tokens);
+    if (workspace_bytes < L.total)
+        return fail(SMOE_ESIZE, "hc_read workspace is " + std::to_string(workspace_bytes) + " bytes, needs " +
+                                    std::to_string(L.total));
+    uint8_t* ws = static_cast<uint8_t*>(workspace);
+    SMOE_TRY(smoe::launch_hc_read(const_cast<float*>(R), hc->norm, hc->down, hc->up, hc->inject, n_tokens, n_embd,
+                                  hc->hc, hc->hc_lr, hc->eps, reinterpret_cast<float*>(ws + L.proj),
+                                  reinterpret_cast<float*>(ws + L.rs), mixed, inject, nullptr, nullptr, nullptr,
+                                  stream_of(hip_stream)),
+             "hc_read");
+    return ok();
+}
+
+smoe_status smoe_hc_write(const smoe_hc* hc, int32_t n_embd, const float* R, const float* y, const float* inject,
+                          int32_t n_tokens, float* R_out, void* hip_stream) {
+    if (!hc) return fail(SMOE_ENULL, "hyper-connection geometry is NULL");
+    if (n_embd < 0 || n_tokens < 0 || hc->hc < 0) return fail(SMOE_EINVAL, "hc_write: negative size");
+    if (n_embd == 0 || n_tokens == 0 || hc->hc == 0) return ok();
+    if ((int64_t)n_tokens * hc->hc * n_embd > ((int64_t)1 << 38)) return fail(SMOE_EINVAL, "hc_write: too many values");
+    if (!R || !y || !inject || !R_out) return fail(SMOE_ENULL, "hc_write: NULL buffer");
+    if (!aligned(R, 4) || !aligned(y, 4) || !aligned(inject, 4) || !aligned(R_out, 4))
+        return fail(SMOE_EALIGN, "hc_write: R, y, inject and R_out must be 4-byte aligned");
+    SMOE_TRY(smoe::launch_hc_write(R, y, inject, n_tokens, n_embd, hc->hc, R_out, stream_of(hip_stream)), "hc_write");
+    return ok();
+}
+
+}  // extern "C"
+
+namespace {
+// smoe_ffn_run's workspace: the block's own, then mixed [T][n], inject [T][hc], y [T][n], gr_read's scratch
+struct FfnLayout {
+    size_t moe, mixed, inject, y, hc, total;
+};
+FfnLayout ffn_layout(const smoe_geom& g, const smoe_hc& h, int64_t T) {
+    FfnLayout L{};
+    size_t o = 0;
+    L.moe = o;
+    o = up(o + layout(g, T).total);
+    L.mixed = o;
+    o = up(o + (size_t)T * g.n_embd * 4);
+    L.inject = o;
+    o = up(o + (size_t)T * h.hc * 4);
+    L.y = o;
+    o = up(o + (size_t)T * g.n_embd * 4);
+    L.hc = o;
+    o = up(o + hc_layout(h, T).total);
+    L.total = o;
+    return L;
+}
+}  // namespace
+
+extern "C" {
+
+size_t smoe_ffn_workspace_bytes(const smoe_geom* g, const smoe_hc* hc, int32_t max_tokens) {
+    if (check_geom(g) != SMOE_OK || max_tokens < 0) return 0;
+    if (check_hc(hc, g->n_embd) != SMOE_OK) return 0;
+    return ffn_layout(*g, *hc, max_tokens).total;
+}
+
+smoe_status smoe_ffn_run(const smoe_geom* g, const smoe_weights* w, const smoe_hc* hc, const float* residual,
+                         int32_t n_tokens, float* out, int32_t add_shared, void* workspace, size_t workspace_bytes,
+                         const smoe_trace* trace, void* hip_stream) {
+    smoe_status s = check_geom(g);
+    if (s != SMOE_OK) return s;
+    s = check_hc(hc, g->n_embd);
+    if (s != SMOE_OK) return s;
+    if (n_tokens < 0) return fail(SMOE_EINVAL, "ffn_run: negative token count");
+    if (n_tokens == 0) return ok();
+    if (!residual || !out || !workspace) return fail(SMOE_ENULL, "ffn_run: NULL buffer");
+    if (!aligned(residual, 4) || !aligned(out, 4) || !aligned(workspace, kAlign))
+        return fail(SMOE_EALIGN, "ffn_run: residual and out 4-byte, workspace 256-byte aligned");
+    const FfnLayout L = ffn_layout(*g, *hc, n_tokens);
+    if (workspace_bytes < L.total)
+        return fail(SMOE_ESIZE, "ffn_run workspace is " + std::to_string(workspace_bytes) + " bytes, needs " +
+                                    std::to_string(L.total));
+    uint8_t* ws = static_cast<uint8_t*>(workspace);
+    float* mixed = reinterpret_cast<float*>(ws + L.mixed);
+    float* inj = reinterpret_cast<float*>(ws + L.inject);
+    float* yb = reinterpret_cast<float*>(ws + L.y);
+    // every check of the block itself before the first launch
+    const size_t moe_bytes = layout(*g, n_tokens).total;
+    s = check_forward(g, w, mixed, n_tokens, yb, ws + L.moe, moe_bytes, SMOE_PATH_AUTO, nullptr, nullptr);
+    if (s != SMOE_OK) return s;
+    const HcLayout H = hc_layout(*hc, n_tokens);
+    SMOE_TRY(smoe::launch_hc_read(const_cast<float*>(residual), hc->norm, hc->down, hc->up, hc->inject, n_tokens,
+                                  g->n_embd, hc->hc, hc->hc_lr, hc->eps,
+                                  reinterpret_cast<float*>(ws + L.hc + H.proj), reinterpret_cast<float*>(ws + L.hc + H.rs),
+                                  mixed, inj, nullptr, nullptr, nullptr, stream_of(hip_stream)),
+             "hc_read");
+    s = forward_impl(g, w, mixed, n_tokens, yb, add_shared, ws + L.moe, moe_bytes, trace, SMOE_PATH_AUTO, hip_stream,
+                     nullptr, nullptr, 0.0f);
+    if (s != SMOE_OK) return s;
+    SMOE_TRY(smoe::launch_hc_write(residual, yb, inj, n_tokens, g->n_embd, hc->hc, out, stream_of(hip_stream)),
+             "hc_write");
+    return ok();
 }
 
 }  // extern "C"

@@ -1,16 +1,19 @@
 // stratametal_amd/csrc/smoe_ffn_demo.cpp - the C++ operator (include/smoe_ffn.hpp) end to end: a seeded
 // synthetic layer generated on the device (the same streams as stratametal_amd.synth_layer: 1 gate, 2 up,
 // 3 down, 4 router, 5/6/7 shared gate/up/down, 8 shared gate_inp; x from stream 100), one traced
-// FfnExec::run, and the trace written to a file for the host check.
+// FfnExec::run, and the trace written to a file for the host check; then the whole layer call (run_layer) on 4
+// residual streams with hc_lr 320 (hyper-connection tensors from streams 30 norm = 1 + N(0, 0.1^2), 31 down and
+// 32 up N(0, 0.2^2), 33 inject N(0, 0.05^2); the streams from stream 101).
 //
 //   smoe_ffn_demo OUT n_tokens seed n_embd n_ff n_ff_shared n_expert top_k
 //
 // OUT receives, little-endian: int32 T, H, E, K; f32 combined [T][H]; int32 ids [T][K]; f32 route_w [T][K];
-// int32 counts [E]; f32 stage_ms [5].
+// int32 counts [E]; f32 stage_ms [5]; f32 layer output [T][4][H].
 #include "smoe_ffn.hpp"
 
 #include <cstdio>
 #include <cstdlib>
+#include <vector>
 
 namespace {
 void* dev_alloc(size_t bytes) {
@@ -63,9 +66,31 @@ int main(int argc, char** argv) {
         float* y = static_cast<float*>(dev_alloc((size_t)T * H * 4));
         smoe::check(smoe_synth_normal(seed, 100, (int64_t)T * H, 1.0f, x, nullptr), "synth x");
 
-        smoe::FfnExec ffn = smoe::FfnExec::load(g, w, T, /*with_trace*/ true);
+        const int32_t hc_n = 4, hc_lr = 320;
+        const int64_t hd = (int64_t)hc_n * H;
+        std::vector<float> norm_h((size_t)hd);
+        float* norm = static_cast<float*>(dev_alloc((size_t)hd * 4));
+        smoe::check(smoe_synth_normal(seed, 30, hd, 0.1f, norm, nullptr), "synth hc norm");
+        smoe::check_hip(hipMemcpy(norm_h.data(), norm, (size_t)hd * 4, hipMemcpyDeviceToHost), "norm copy");
+        for (float& v : norm_h) v = 1.0f + v;  // the stored (1 + w)
+        smoe::check_hip(hipMemcpy(norm, norm_h.data(), (size_t)hd * 4, hipMemcpyHostToDevice), "norm copy");
+        auto bf16_s = [&](uint64_t stream_id, int64_t n, float s) {
+            void* p = dev_alloc((size_t)n * 2);
+            smoe::check(smoe_synth_bf16(seed, stream_id, n, s, static_cast<uint16_t*>(p), nullptr), "synth bf16");
+            return static_cast<const uint16_t*>(p);
+        };
+        smoe_hc hc{hc_n, hc_lr, 1e-6f, norm, bf16_s(31, hc_lr * hd, 0.2f), bf16_s(32, hd * hc_lr, 0.2f),
+                   bf16_s(33, hc_n * hd, 0.05f)};
+        float* R = static_cast<float*>(dev_alloc((size_t)T * hd * 4));
+        float* out = static_cast<float*>(dev_alloc((size_t)T * hd * 4));
+        smoe::check(smoe_synth_normal(seed, 101, (int64_t)T * hd, 1.0f, R, nullptr), "synth residual");
+
+        smoe::FfnExec ffn = smoe::FfnExec::load(g, w, T, /*with_trace*/ true, &hc);
         smoe::FfnTrace tr;
         ffn.run(x, y, T, /*add_shared*/ true, &tr);
+        ffn.run_layer(R, out, T, /*add_shared*/ true);
+        std::vector<float> out_h((size_t)T * hd);
+        smoe::check_hip(hipMemcpy(out_h.data(), out, out_h.size() * 4, hipMemcpyDeviceToHost), "layer output copy");
 
         FILE* f = std::fopen(argv[1], "wb");
         if (!f) throw std::runtime_error(std::string("cannot open ") + argv[1]);
@@ -76,6 +101,7 @@ int main(int argc, char** argv) {
         std::fwrite(tr.route_w.data(), 4, tr.route_w.size(), f);
         std::fwrite(tr.counts.data(), 4, tr.counts.size(), f);
         std::fwrite(tr.stage_ms.data(), 4, tr.stage_ms.size(), f);
+        std::fwrite(out_h.data(), 4, out_h.size(), f);
         std::fclose(f);
         std::printf("FfnExec: %d tokens, %llu device bytes owned, stages (ms):", T, (unsigned long long)ffn.gpu_bytes());
         for (float m : tr.stage_ms) std::printf(" %.4f", m);

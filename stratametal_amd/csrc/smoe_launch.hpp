@@ -95,6 +95,15 @@ hipError_t launch_mm_down(const uint8_t* down_exps, const uint8_t* down_sh, cons
                           int h_rec, const float* sg, const int4* items, int H, int F, int Fs, int max_items, float* Y,
                           hipStream_t s);
 
+// the hyper-connection ends (smoe_hc.hip): gr_read (two launches; proj [T][hc_lr] and rs [T][hc] are scratch; with
+// rprev, R = rprev + yprev * 2 sigmoid(injprev / hc) is formed and stored first) and gr_write
+bool hc_shape_ok(int n, int hc, int hc_lr);
+hipError_t launch_hc_read(float* R, const float* norm, const uint16_t* down, const uint16_t* up, const uint16_t* inj,
+                          int n_tok, int n, int hc, int hc_lr, float eps, float* proj, float* rs, float* mixed,
+                          float* inject, const float* rprev, const float* yprev, const float* injprev, hipStream_t s);
+hipError_t launch_hc_write(const float* R, const float* y, const float* inject, int n_tok, int n, int hc, float* out,
+                           hipStream_t s);
+
 hipError_t launch_synth_blocks(int type, uint64_t seed, uint64_t stream_id, int64_t n_blocks, float sigma, uint8_t* out,
                                hipStream_t s);
 hipError_t launch_synth_bf16(uint64_t seed, uint64_t stream_id, int64_t n, float sigma, uint16_t* out, hipStream_t s);

@@ -1,7 +1,8 @@
 """The C++ FfnExec-shaped operator (include/smoe_ffn.hpp, the reference's FfnExec::load / FfnExec::run,
 metal/include/strata/metal/layer_exec.hpp:113-140) end to end: stratametal_amd/lib/smoe_ffn_demo loads a
-seeded synthetic layer through it, runs one traced call and writes the trace; the same layer and input through
-the Python binding must give the same bits (combined output, ids, routing weights, counts)."""
+seeded synthetic layer through it, runs one traced call and writes the trace, then the whole layer call with the
+hyper-connection ends (FfnExec::run_layer); the same layer and inputs through the Python binding must give the same
+bits (combined output, ids, routing weights, counts, the layer's residual streams)."""
 import os
 import subprocess
 import sys
@@ -9,6 +10,8 @@ import tempfile
 
 import numpy as np
 import pytest
+
+import oracle as O
 
 import stratametal_amd as S
 
@@ -50,6 +53,7 @@ def test_cpp_operator_matches_python_binding(torch, T, seed, geom):
     rw = take(np.float32, T * K).reshape(T, K)
     counts = take(np.int32, E)
     stage_ms = take(np.float32, 5)
+    layer_out = take(np.float32, T * 4 * H).reshape(T, 4, H)
     assert o == len(raw) and (stage_ms >= 0).all()
 
     g = S.Geom(n_embd=H, n_ff=F, n_ff_shared=Fs, n_expert=E, top_k=K)
@@ -62,3 +66,12 @@ def test_cpp_operator_matches_python_binding(torch, T, seed, geom):
     assert np.array_equal(ids, tr["ids"].cpu().numpy().reshape(T, K))
     assert np.array_equal(rw.view(np.uint32), tr["weights"].cpu().numpy().reshape(T, K).view(np.uint32))
     assert np.array_equal(counts, tr["counts"].cpu().numpy())
+    # the layer call: the same hyper-connection tensors (the oracle's generators equal the device ones bitwise)
+    hw = O.make_hc(H, 4, 320, seed)
+    up = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    hcd = S.HyperConnection(H, 4, 320, up(hw.norm), up(hw.down.view(np.int16)), up(hw.up.view(np.int16)),
+                            up(hw.inject.view(np.int16)), eps=1e-6)
+    R = S.synth_normal(seed, 101, T * 4 * H).reshape(T, 4, H)
+    got = S.FfnLayer(g, w, hcd, max_tokens=T).run(R)
+    torch.cuda.synchronize()
+    assert np.array_equal(layer_out.view(np.uint32), got.cpu().numpy().view(np.uint32))
