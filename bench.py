@@ -87,14 +87,24 @@ def profile_record(name, kernel):
 class Stack:
     """`n_layers` synthetic layers resident on the device, one workspace, a graph per token count."""
 
-    def __init__(self, S, torch, g, n_layers, seed, max_tokens, logit_bias=None):
-        self.S, self.torch, self.g = S, torch, g
-        self.layers = [S.synth_layer(g, seed + l, logit_bias=logit_bias) for l in range(n_layers)]
+    def __init__(self, S, torch, g, n_layers, seed, max_tokens, logit_bias=None, layers=None):
+        self.S, self.torch, self.g, self.seed, self.max_tokens = S, torch, g, seed, max_tokens
+        self.layers = layers if layers is not None else [S.synth_layer(g, seed + l, logit_bias=logit_bias)
+                                                         for l in range(n_layers)]
         self.wc = [S._weights_c(w) for w in self.layers]
         self.gc = g.c()
         self.ws_bytes = S.workspace_bytes(g, max_tokens)
         self.ws = torch.empty(self.ws_bytes, dtype=torch.uint8, device="cuda")
         torch.cuda.synchronize()
+
+    def with_f32_router(self):
+        """The same layers with the literal configs[0]'s f32 router (router_dtype 1): the expert tensors are shared,
+        each router is the f32 the bf16 one was rounded from (synth_layer's stream 4)."""
+        S, g = self.S, self.g
+        g32 = S.Geom(**dict(vars(g), router_dtype=S.ROUTER_F32))
+        layers = [dict(w, router=S.synth_normal(self.seed + l, 4, g.n_expert * g.n_embd, 0.02))
+                  for l, w in enumerate(self.layers)]
+        return Stack(S, self.torch, g32, len(layers), self.seed, self.max_tokens, layers=layers)
 
     def inputs(self, T, seed):
         S, g = self.S, self.g
@@ -209,8 +219,8 @@ def bytes_model(S, g, T, D):
     hq = (P + (T if sh else 0)) * (max(g.n_ff, Fs if sh else 0) // 32) * 36
     gu = D * 2 * g.n_ff * rb_h + (2 * Fs * S.row_bytes(g.sh_type, g.n_embd) if sh else 0) + xq + hq
     down = D * g.n_embd * rb_f + (g.n_embd * S.row_bytes(g.sh_type, Fs) if sh else 0) + hq + (P + T) * g.n_embd * 4
-    layer = (D * g.expert_bytes() + g.shared_bytes() + g.n_expert * g.n_embd * 2 + (g.n_embd * 2 if sh else 0)
-             + 2 * T * g.n_embd * 4)
+    router_b = g.n_expert * g.n_embd * (4 if g.router_dtype == 1 else 2)
+    layer = (D * g.expert_bytes() + g.shared_bytes() + router_b + (g.n_embd * 2 if sh else 0) + 2 * T * g.n_embd * 4)
     return layer, gu, down
 
 
@@ -264,7 +274,7 @@ def stage_line(name, m):
 def decode(S, torch, stack, T, a, flush, seed_off):
     r = measure(S, torch, stack, T, a.steps, a.warmup, a.seed + seed_off, flush)
     m = summarize(S, stack.g, T, r, a.steps)
-    log(stage_line(f"decode b={T}", m))
+    log(stage_line(f"decode b={T}" + (" (f32 router)" if stack.g.router_dtype == 1 else ""), m))
     return m
 
 
@@ -501,6 +511,13 @@ def main():
         return
     extra = {}
     if not a.no_extra:
+        # the literal configs[0]: the same layers and tokens with the f32 router (4 MiB of router rows per layer)
+        st32 = stack.with_f32_router()
+        m1f = decode(S, torch, st32, 1, a, flush, 11)
+        extra["decode_b1_f32_router"] = {k: m1f[k] for k in ("ms_per_step", "gpu_ms_per_step", "tok_s",
+                                                             "touched_experts_avg", "layer_bytes_avg", "layer_gbs",
+                                                             "layer_hbm_frac", "stage_ms_avg")}
+        del st32
         m16 = decode(S, torch, stack, 16, a, flush, 7)
         extra["decode_b16"] = {k: m16[k] for k in ("ms_per_step", "gpu_ms_per_step", "tok_s", "touched_experts_avg",
                                                    "layer_bytes_avg", "layer_gbs", "layer_hbm_frac", "stage_ms_avg",

@@ -42,8 +42,13 @@ enum { SMOE_Q2_0 = 42, SMOE_IQ2_S = 22 };
 enum {
     SMOE_PATH_AUTO = 0, /* GEMV for n_tokens < 128, MFMA otherwise */
     SMOE_PATH_GEMV = 1, /* q8_1 activations, integer dot (the decode contract) */
-    SMOE_PATH_MFMA = 2  /* bf16 activations, bf16 MFMA with exact per-block weight scales (the prefill contract) */
+    SMOE_PATH_MFMA = 2  /* bf16 activations, bf16 MFMA with exact per-block weight scales (the prefill contract);
+                           the matrix cores take bf16 activations and h as fp16, which holds them below 65520 in
+                           magnitude (smoe_trace.overflow reports tokens beyond), and block scales below 32752 */
 };
+
+#define SMOE_ROUTER_BF16 0
+#define SMOE_ROUTER_F32 1
 
 /* Layer geometry.  ModelGeometry's MoE fields (include/strata/core/layout.hpp:27-59) plus the types. */
 typedef struct {
@@ -54,7 +59,9 @@ typedef struct {
     int32_t top_k;        /* k: 1..64, k <= E */
     int32_t w_type;       /* routed experts: SMOE_Q2_0 or SMOE_IQ2_S */
     int32_t sh_type;      /* shared expert: SMOE_Q2_0 / SMOE_IQ2_S, or -1 = no shared expert */
-    int32_t router_dtype; /* 0 = bf16 (the repo's contract: include/strata/core/layer.hpp:131-136) */
+    int32_t router_dtype; /* 0 = bf16 (the repo's contract: include/strata/core/layer.hpp:131-136); 1 = f32 router
+                             weights and f32 activations in the router (the literal benchmark configuration; the
+                             shared gate stays bf16); SMOE_ROUTER_F32 */
 } smoe_geom;
 
 /* One layer's tensors, all resident in device memory (4-byte aligned). */
@@ -62,7 +69,7 @@ typedef struct {
     const void* gate_exps;       /* ffn_gate_exps: [E][n_ff] rows of n_embd */
     const void* up_exps;         /* ffn_up_exps:   [E][n_ff] rows of n_embd */
     const void* down_exps;       /* ffn_down_exps: [E][n_embd] rows of n_ff */
-    const void* router;          /* ffn_gate_inp: [E][n_embd] bf16 */
+    const void* router;          /* ffn_gate_inp: [E][n_embd] bf16, or f32 with router_dtype 1 (16-byte aligned) */
     const void* gate_sh;         /* ffn_gate_shexp: [n_ff_shared] rows of n_embd */
     const void* up_sh;           /* ffn_up_shexp */
     const void* down_sh;         /* ffn_down_shexp: [n_embd] rows of n_ff_shared */
@@ -86,6 +93,17 @@ typedef struct {
      * combine),
      * for per-stage timing (the upstream engine's event-pair stage timing, include/strata/core/layer.hpp:317-337). */
     void* const* stage_events;
+    /* The expert stages (FfnTrace's exq, ehq, edown and shared).  A call asking for any of xq, hq, parts or shared
+     * runs the decode path's unfused kernels (top-k and dispatch, gate/up, down, combine; the same bits as the fused
+     * launches of small batches). */
+    uint8_t* xq;      /* [T][n_embd/32] q8_1 blocks (36 bytes: fp16 d, fp16 s, 32 int8) of x (decode path only) */
+    uint8_t* hq;      /* [T*k][n_ff/32] q8_1 blocks of each pair's h, by dispatch position (decode path only) */
+    float* parts;     /* [T*k][n_embd] each pair's expert output before its routing weight, by dispatch position */
+    float* shared;    /* [T][n_embd] the shared expert's output times sigmoid(sgate) (layers with a shared expert) */
+    /* [1] 0, or a mask of the prefill path's operand limits met: bit 0 -- an activation whose bf16 value is 65520
+     * or more in magnitude (finite x), bit 1 -- such an h value.  The matrix cores take these as fp16, so the
+     * affected tokens' outputs are then not the prefill contract's (inf or NaN).  0 on the decode path. */
+    int32_t* overflow;
 } smoe_trace;
 
 #define SMOE_STAGE_EVENTS 6

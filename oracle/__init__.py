@@ -81,6 +81,8 @@ def _set_sigs(L):
         "or_iq2_s_gemv_ref": (None, [vp, vp, i32, i32, vp]),
         "or_bf16_gemv_dev": (None, [vp, vp, i32, i32, vp]),
         "or_bf16_gemv_double": (None, [vp, vp, i32, i32, vp]),
+        "or_f32_gemv_dev": (None, [vp, vp, i32, i32, vp]),
+        "or_f32_gemv_double": (None, [vp, vp, i32, i32, vp]),
         "or_route_dev": (None, [vp, i32, i32, i32, vp, vp]),
         "or_route_ref": (None, [vp, i32, i32, i32, vp, vp]),
         "or_swiglu_q8": (None, [vp, vp, i64, vp]),
@@ -270,6 +272,23 @@ def bf16_gemv_double(xb, w, n_in, n_out):
     return y
 
 
+def f32_gemv_dev(x, w, n_in, n_out):
+    """The f32 router's device order (router_dtype 1): 4-element chunks per lane, fused multiply-adds."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    y = np.empty(n_out, np.float32)
+    lib().or_f32_gemv_dev(_p(x), _p(w), n_in, n_out, _p(y))
+    return y
+
+
+def f32_gemv_double(x, w, n_in, n_out):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    y = np.empty(n_out, np.float32)
+    lib().or_f32_gemv_double(_p(x), _p(w), n_in, n_out, _p(y))
+    return y
+
+
 def _route(fn, logits, k):
     logits = np.ascontiguousarray(logits, dtype=np.float32)
     if logits.ndim == 1:
@@ -376,7 +395,7 @@ class Weights:
     gate_exps: np.ndarray
     up_exps: np.ndarray
     down_exps: np.ndarray
-    router: np.ndarray           # uint16 bf16 [E][H]
+    router: np.ndarray           # uint16 bf16 [E][H], or f32 [E][H] when router_dtype is 1
     gate_sh: Optional[np.ndarray] = None
     up_sh: Optional[np.ndarray] = None
     down_sh: Optional[np.ndarray] = None
@@ -400,7 +419,8 @@ def make_weights(g: Geom, seed: int, n_expert_alloc: Optional[int] = None, zipf_
     gate = gen_blocks(g.w_type, seed, 1, E * F * H, sigma)
     up = gen_blocks(g.w_type, seed, 2, E * F * H, sigma)
     down = gen_blocks(g.w_type, seed, 3, E * H * F, sigma)
-    router = gen_bf16(seed, 4, E * H, sigma)
+    # the router is generated in f32 and stored as bf16 (the repo's contract) unless router_dtype is 1
+    router = gen_normal(seed, 4, E * H, sigma) if g.router_dtype == 1 else gen_bf16(seed, 4, E * H, sigma)
     w = Weights(gate, up, down, router)
     if g.sh_type >= 0:
         w.gate_sh = gen_blocks(g.sh_type, seed, 5, Fs * H, sigma)

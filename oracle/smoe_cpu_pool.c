@@ -154,6 +154,7 @@ int or_moe_decode_pool(const or_geom* g, const or_weights* w, const float* x, in
     const int64_t grow = or_row_bytes(g->w_type, H), drow = or_row_bytes(g->w_type, F);
     const int64_t sgrow = has_sh ? or_row_bytes(g->sh_type, H) : 0, sdrow = has_sh ? or_row_bytes(g->sh_type, Fs) : 0;
     if (grow <= 0 || drow <= 0 || (has_sh && (sgrow <= 0 || sdrow <= 0))) return -1;
+    if (g->router_dtype != 0 && (g->router_dtype != 1 || H % 4)) return -1;
     if ((g->w_type == 42 && (H % 128 || F % 128)) || (has_sh && g->sh_type == 42 && Fs % 128)) return -1;
 #ifdef _OPENMP
     if (n_threads > 0) omp_set_num_threads(n_threads);
@@ -200,7 +201,10 @@ int or_moe_decode_pool(const or_geom* g, const or_weights* w, const float* x, in
         const int nr = E - r0 < kRouterRows ? E - r0 : kRouterRows;
         for (int t = 0; t < T; ++t) {
             float* lo = logits + (size_t)t * E + r0;
-            or_bf16_gemv_dev(xb + (size_t)t * H, w->router + (size_t)r0 * H, H, nr, lo);
+            if (g->router_dtype == 1)
+                or_f32_gemv_dev(x + (size_t)t * H, (const float*)(const void*)w->router + (size_t)r0 * H, H, nr, lo);
+            else
+                or_bf16_gemv_dev(xb + (size_t)t * H, w->router + (size_t)r0 * H, H, nr, lo);
             if (w->logit_bias)
                 for (int r = 0; r < nr; ++r) lo[r] = lo[r] + w->logit_bias[r0 + r];
         }

@@ -531,6 +531,40 @@ void or_bf16_gemv_dev(const uint16_t* xb, const uint16_t* w, int n_in, int n_out
     }
 }
 
+/* The f32 router of the literal benchmark configuration (router_dtype 1: "Router weight fp32", BASELINE configs[0];
+ * no counterpart in the reference, whose router is bf16, include/strata/core/layer.hpp:128-137):
+ * logits[e] = sum_i x_i * W[e][i] with x and W in f32.  Device order (k_router<MAXC, true>): four consecutive
+ * elements form a chunk; lane l owns chunks l, l+64, ... and fuses each product into its accumulator in element
+ * order (fmaf: one rounding per step), then the xor butterfly 32..1. */
+void or_f32_gemv_dev(const float* x, const float* w, int n_in, int n_out, float* y) {
+    const int chunks = n_in / 4;
+    for (int r = 0; r < n_out; ++r) {
+        const float* row = w + (size_t)r * n_in;
+        float lane[64];
+        for (int l = 0; l < 64; ++l) {
+            float acc = 0.0f;
+            for (int c = l; c < chunks; c += 64)
+                for (int i = 0; i < 4; ++i) acc = fmaf(x[4 * c + i], row[4 * c + i], acc);
+            lane[l] = acc;
+        }
+        for (int o = 32; o > 0; o >>= 1) {
+            float nxt[64];
+            for (int i = 0; i < 64; ++i) nxt[i] = lane[i] + lane[i ^ o];
+            memcpy(lane, nxt, sizeof lane);
+        }
+        y[r] = lane[0];
+    }
+}
+
+/* The f32 router as the reference's host computes its router: a double sum cast to f32. */
+void or_f32_gemv_double(const float* x, const float* w, int n_in, int n_out, float* y) {
+    for (int r = 0; r < n_out; ++r) {
+        double acc = 0.0;
+        for (int i = 0; i < n_in; ++i) acc += (double)x[i] * (double)w[(size_t)r * n_in + i];
+        y[r] = (float)acc;
+    }
+}
+
 /* The reference's host router product: a double sum cast to f32 (metal/src/pack_parity.cpp:3795-3799). */
 void or_bf16_gemv_double(const uint16_t* xb, const uint16_t* w, int n_in, int n_out, float* y) {
     for (int r = 0; r < n_out; ++r) {
@@ -733,6 +767,8 @@ void or_dispatch(const int32_t* ids, int n_tok, int k, int n_expert, int32_t* co
 
 static int geom_ok(const or_geom* g) {
     if (g->n_embd <= 0 || g->n_ff <= 0 || g->n_expert <= 0 || g->top_k <= 0 || g->top_k > g->n_expert) return 0;
+    if (g->router_dtype != 0 && g->router_dtype != 1) return 0;
+    if (g->router_dtype == 1 && g->n_embd % 4) return 0;
     if (or_row_bytes(g->w_type, g->n_embd) <= 0 || or_row_bytes(g->w_type, g->n_ff) <= 0) return 0;
     if (g->sh_type >= 0 && (or_row_bytes(g->sh_type, g->n_embd) <= 0 || or_row_bytes(g->sh_type, g->n_ff_shared) <= 0))
         return 0;
@@ -769,6 +805,21 @@ static void expert_chain(int type, const uint8_t* gw, const uint8_t* uw, const u
     free(hq);
 }
 
+/* Router logits of one token: bf16 x and W (router_dtype 0, the repo's contract) or f32 x and W (1). */
+static void router_logits(const or_geom* g, const or_weights* w, const float* x, const uint16_t* xb, int dev,
+                          float* out) {
+    const int H = g->n_embd, E = g->n_expert;
+    if (g->router_dtype == 1) {
+        const float* W = (const float*)(const void*)w->router;
+        if (dev) or_f32_gemv_dev(x, W, H, E, out);
+        else or_f32_gemv_double(x, W, H, E, out);
+    } else if (dev) {
+        or_bf16_gemv_dev(xb, w->router, H, E, out);
+    } else {
+        or_bf16_gemv_double(xb, w->router, H, E, out);
+    }
+}
+
 static int moe_decode(const or_geom* g, const or_weights* w, const float* x, int T, float* y, int add_shared,
                       const or_trace* tr, int n_threads, int dev) {
     if (!geom_ok(g) || T < 0) return -1;
@@ -798,8 +849,7 @@ static int moe_decode(const or_geom* g, const or_weights* w, const float* x, int
         or_bf16_from_f32_n(x + (size_t)t * H, H, xb + (size_t)t * H);
     }
     for (int t = 0; t < T; ++t) {
-        if (dev) or_bf16_gemv_dev(xb + (size_t)t * H, w->router, H, E, logits + (size_t)t * E);
-        else or_bf16_gemv_double(xb + (size_t)t * H, w->router, H, E, logits + (size_t)t * E);
+        router_logits(g, w, x + (size_t)t * H, xb + (size_t)t * H, dev, logits + (size_t)t * E);
         if (w->logit_bias)
             for (int e = 0; e < E; ++e) logits[(size_t)t * E + e] = logits[(size_t)t * E + e] + w->logit_bias[e];
         if (has_sh) {
@@ -920,7 +970,7 @@ int or_moe_prefill(const or_geom* g, const or_weights* w, const float* x, int T,
         xa[i] = or_f32_from_bf16(xb[i]);
     }
     for (int t = 0; t < T; ++t) {
-        or_bf16_gemv_dev(xb + (size_t)t * H, w->router, H, E, logits + (size_t)t * E);
+        router_logits(g, w, x + (size_t)t * H, xb + (size_t)t * H, 1, logits + (size_t)t * E);
         if (w->logit_bias)
             for (int e = 0; e < E; ++e) logits[(size_t)t * E + e] = logits[(size_t)t * E + e] + w->logit_bias[e];
         if (has_sh) or_bf16_gemv_dev(xb + (size_t)t * H, w->gate_inp_sh, H, 1, sg + t);

@@ -71,6 +71,8 @@ void or_iq2_s_gemv_ref(const uint8_t* w, const uint8_t* xq, int n_in, int n_out,
 /* ---- A5: router GEMV and top-k */
 void or_bf16_gemv_dev(const uint16_t* xb, const uint16_t* w, int n_in, int n_out, float* y);
 void or_bf16_gemv_double(const uint16_t* xb, const uint16_t* w, int n_in, int n_out, float* y);
+void or_f32_gemv_dev(const float* x, const float* w, int n_in, int n_out, float* y);
+void or_f32_gemv_double(const float* x, const float* w, int n_in, int n_out, float* y);
 void or_route_dev(const float* logits, int n_tok, int n_expert, int k, int32_t* ids, float* w);
 void or_route_ref(const float* logits, int n_tok, int n_expert, int k, int32_t* ids, float* w);
 
@@ -98,7 +100,7 @@ typedef struct {
 
 typedef struct {
     const uint8_t *gate_exps, *up_exps, *down_exps;
-    const uint16_t* router;
+    const uint16_t* router; /* [E][H] bf16, or f32 when router_dtype is 1 */
     const uint8_t *gate_sh, *up_sh, *down_sh;
     const uint16_t* gate_inp_sh;
     const float* logit_bias;

@@ -21,6 +21,7 @@ _LIB = None
 Q2_0 = 42
 IQ2_S = 22
 PATH_AUTO, PATH_GEMV, PATH_MFMA = 0, 1, 2
+ROUTER_BF16, ROUTER_F32 = 0, 1  # smoe_geom.router_dtype
 MFMA_TOKENS = 128  # SMOE_PATH_AUTO runs the prefill (MFMA) contract from this many tokens on
 MFMA_CHUNK = 128   # columns per MFMA work item
 
@@ -48,7 +49,7 @@ class _Weights(C.Structure):
 
 class _Trace(C.Structure):
     _fields_ = [(n, C.c_void_p) for n in ("logits", "ids", "weights", "counts", "offsets", "perm", "slot", "sgate",
-                                          "stage_events")]
+                                          "stage_events", "xq", "hq", "parts", "shared", "overflow")]
 
 class _Hc(C.Structure):
     _fields_ = [("hc", C.c_int32), ("hc_lr", C.c_int32), ("eps", C.c_float), ("norm", C.c_void_p),
@@ -205,8 +206,11 @@ def synth_layer(g: Geom, seed: int, device="cuda", sigma: float = 0.02, logit_bi
         _check(L.smoe_synth_bf16(seed, stream_id, n, sigma, buf.data_ptr(), st))
         return buf
 
+    # the router is generated in f32 and kept in f32 (router_dtype 1) or stored as bf16 (the repo's contract)
+    router = synth_normal(seed, 4, E * H, sigma, device=device, stream=stream) if g.router_dtype == ROUTER_F32 \
+        else bf16(4, E * H)
     w = dict(gate_exps=blocks(g.w_type, 1, E * F * H), up_exps=blocks(g.w_type, 2, E * F * H),
-             down_exps=blocks(g.w_type, 3, E * H * F), router=bf16(4, E * H))
+             down_exps=blocks(g.w_type, 3, E * H * F), router=router)
     if g.sh_type >= 0:
         w.update(gate_sh=blocks(g.sh_type, 5, Fs * H), up_sh=blocks(g.sh_type, 6, Fs * H),
                  down_sh=blocks(g.sh_type, 7, H * Fs), gate_inp_sh=bf16(8, H))
@@ -291,7 +295,12 @@ class MoELayer:
         self.ws_bytes = workspace_bytes(g, max_tokens)
         self.ws = torch.empty(self.ws_bytes, dtype=torch.uint8, device=device)
 
-    def forward(self, x, y=None, add_shared: bool = True, trace: bool = False, path: int = PATH_AUTO, stream=None):
+    def forward(self, x, y=None, add_shared: bool = True, trace: bool = False, path: int = PATH_AUTO, stream=None,
+                stages: bool = False):
+        """y = MoE(x).  With `trace`, also returns the routing and the dispatch (logits, ids, weights, counts,
+        offsets, perm, slot, sgate); with `stages` as well, the expert stages (xq, hq: q8_1 blocks of x and of each
+        pair's h on the decode path; parts, shared: each pair's expert output and the shared expert's, by dispatch
+        position) and the prefill path's fp16 `overflow` mask -- the decode path then runs its unfused kernels."""
         import torch
         if x.dim() != 2:
             raise SmoeError(-1, f"x must be (tokens, {self.g.n_embd}), got {tuple(x.shape)}")
@@ -314,8 +323,16 @@ class MoELayer:
                        perm=torch.empty(T * K, dtype=torch.int32, device=dev),
                        slot=torch.empty(T * K, dtype=torch.int32, device=dev),
                        sgate=torch.empty(T, dtype=torch.float32, device=dev))
-            tr = _Trace(*[out[n].data_ptr() for n in ("logits", "ids", "weights", "counts", "offsets", "perm", "slot",
-                                                       "sgate")])
+            names = ["logits", "ids", "weights", "counts", "offsets", "perm", "slot", "sgate"]
+            if stages:
+                H, F = self.g.n_embd, self.g.n_ff
+                out.update(xq=torch.empty((T, H // 32 * 36), dtype=torch.uint8, device=dev),
+                           hq=torch.empty((T * K, F // 32 * 36), dtype=torch.uint8, device=dev),
+                           parts=torch.empty((T * K, H), dtype=torch.float32, device=dev),
+                           shared=torch.empty((T, H), dtype=torch.float32, device=dev),
+                           overflow=torch.full((1,), -1, dtype=torch.int32, device=dev))
+            tr = _Trace(*[out[n].data_ptr() for n in names], None,
+                        *[out[n].data_ptr() if stages else None for n in ("xq", "hq", "parts", "shared", "overflow")])
         _check(lib().smoe_forward_path(C.byref(self._gc), C.byref(self._wc), x.data_ptr(), T, y.data_ptr(),
                                        int(add_shared), self.ws.data_ptr(), self.ws_bytes,
                                        None if tr is None else C.byref(tr), path, _stream(stream)))

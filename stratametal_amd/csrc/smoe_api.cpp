@@ -58,7 +58,8 @@ smoe_status check_geom(const smoe_geom* g) {
         return fail(SMOE_ETYPE, "shared expert type " + std::to_string(g->sh_type) + " is not Q2_0, IQ2_S or -1");
     if (g->sh_type >= 0 && g->sh_type != g->w_type)
         return fail(SMOE_ETYPE, "the shared expert's type must equal the routed experts' type (one activation layout)");
-    if (g->router_dtype != 0) return fail(SMOE_EINVAL, "router_dtype must be 0 (bf16)");
+    if (g->router_dtype != SMOE_ROUTER_BF16 && g->router_dtype != SMOE_ROUTER_F32)
+        return fail(SMOE_EINVAL, "router_dtype must be 0 (bf16) or 1 (f32)");
     if (g->n_expert < 1 || g->n_expert > kMaxExpert) return fail(SMOE_EINVAL, "n_expert must be in 1..1024");
     if (g->top_k < 1 || g->top_k > kMaxK) return fail(SMOE_EINVAL, "top_k must be in 1..64");
     if (g->top_k > g->n_expert) return fail(SMOE_EINVAL, "top_k exceeds n_expert");
@@ -86,9 +87,10 @@ smoe_status check_geom(const smoe_geom* g) {
 
 struct Layout {
     size_t ximg, xbf, logits, sg, ids, wts, counts, offsets, perm, slot, elist, nlist, items, himg, Y, dwork, xchg,
-        total;
+        oflags, total;
     int h_blocks;  // q8_1 blocks per h row (GEMV path)
     int h_rec;     // 64-value records per h row (MFMA path)
+    int64_t n_xflags, n_hflags;  // the MFMA path's per-work-group overflow flags (a trace asking for the mask)
 };
 
 // Work items: every touched expert plus the shared expert's token chunks (GEMV path); the MFMA path splits
@@ -137,6 +139,9 @@ Layout layout(const smoe_geom& g, int64_t T) {
     // sized for max_tokens holds every smaller call's layout)
     L.xchg = take(smoe::moe_small_xchg_bytes(kFusedRouteTokens, (int)K, max_items_gemv(g, kFusedRouteTokens),
                                              L.h_blocks));
+    L.n_xflags = most(smoe::act_records_blocks(T * (H / 64)), T);
+    L.n_hflags = (Fmax / 128) * (int64_t)max_items_mfma(g, T);
+    L.oflags = take((size_t)(L.n_xflags + L.n_hflags) * 4);
     L.total = o;
     return L;
 }
@@ -173,7 +178,7 @@ const char* smoe_status_str(smoe_status s) {
 
 const char* smoe_last_error(void) { return g_last.c_str(); }
 
-int32_t smoe_abi_version(void) { return 104; }
+int32_t smoe_abi_version(void) { return 105; }
 
 size_t smoe_workspace_bytes(const smoe_geom* g, int32_t max_tokens) {
     if (check_geom(g) != SMOE_OK || max_tokens < 0) return 0;
@@ -291,10 +296,14 @@ smoe_status forward_impl(const smoe_geom* g, const smoe_weights* w, float* x_io,
     } while (0)
     SMOE_MARK();
     const bool fused_norm = x_prev && !mfma;
+    // the expert stages of the trace: the decode path's unfused kernels, so that every stage lands in memory
+    const bool stages = trace && (trace->xq || trace->hq || trace->parts || trace->shared);
+    int32_t* xflags = (trace && trace->overflow && mfma) ? reinterpret_cast<int32_t*>(ws + L.oflags) : nullptr;
+    int32_t* hflags = xflags ? xflags + L.n_xflags : nullptr;
     // batches of at most kFusedRouteTokens tokens on the Q2_0 GEMV path: the gate/up kernel routes the batch itself,
     // and (when the batch's h images fit in LDS) the down kernel applies the combine; where the shapes allow, both
     // run as one launch whose exchange words the router kernel clears
-    const bool small = !mfma && !iq2 && T <= kFusedRouteTokens;
+    const bool small = !mfma && !iq2 && !stages && T <= kFusedRouteTokens;
     const bool small_down = small && smoe::down_combine_ok(T, K, L.h_blocks);
     const bool fused = small_down && smoe::moe_small_ok(T, K, H, F, Fs, has_sh ? 1 : 0, L.h_blocks);
     uint8_t* xchg = ws + L.xchg;
@@ -302,14 +311,17 @@ smoe_status forward_impl(const smoe_geom* g, const smoe_weights* w, float* x_io,
     uint16_t* xbf = mfma ? reinterpret_cast<uint16_t*>(ws + L.xbf) : nullptr;
     // the prefill path's junction and the records of its output in one launch, before the call on that output
     if (x_prev && mfma)
-        SMOE_TRY(smoe::launch_junction_records(x_prev, r_prev, T, H, eps, x_io, ximg, xbf, st), "junction records");
+        SMOE_TRY(smoe::launch_junction_records(x_prev, r_prev, T, H, eps, x_io, ximg, xbf, st, xflags),
+                 "junction records");
     if (mfma && !x_prev)
-        SMOE_TRY(smoe::launch_act_records(x, (int64_t)T * (H / 64), ximg, xbf, st), "activation records");
-    SMOE_TRY(smoe::launch_router(fused_norm ? x_prev : x, xbf, static_cast<const uint16_t*>(w->router),
+        SMOE_TRY(smoe::launch_act_records(x, (int64_t)T * (H / 64), ximg, xbf, st, xflags), "activation records");
+    // the f32 router (router_dtype 1) reads f32 x on the row-per-wave path, also for many tokens
+    const bool f32r = g->router_dtype == SMOE_ROUTER_F32;
+    SMOE_TRY(smoe::launch_router(fused_norm ? x_prev : x, f32r ? nullptr : xbf, w->router,
                                  has_sh ? w->gate_inp_sh : nullptr, w->logit_bias, H, E, E + (has_sh ? 1 : 0), T, logits,
-                                 E, sg, mfma ? nullptr : ximg, mfma ? 1 : 0, iq2 ? 1 : 0, st,
+                                 E, sg, mfma ? nullptr : ximg, (mfma && !f32r) ? 1 : 0, iq2 ? 1 : 0, st,
                                  fused_norm ? r_prev : nullptr, eps, fused_norm ? x_io : nullptr,
-                                 fused ? reinterpret_cast<uint4*>(xchg) : nullptr, (int)(xchg_bytes / 16)),
+                                 fused ? reinterpret_cast<uint4*>(xchg) : nullptr, (int)(xchg_bytes / 16), f32r ? 1 : 0),
              "router");
     SMOE_MARK();
     if (small) {
@@ -337,9 +349,10 @@ smoe_status forward_impl(const smoe_geom* g, const smoe_weights* w, float* x_io,
     const uint8_t* gs = static_cast<const uint8_t*>(w->gate_sh);
     const uint8_t* us = static_cast<const uint8_t*>(w->up_sh);
     const uint8_t* ds = static_cast<const uint8_t*>(w->down_sh);
+    uint8_t* hq = (trace && !mfma) ? trace->hq : nullptr;
     if (mfma) {
         SMOE_TRY(smoe::launch_mm_gu(ge, ue, gs, us, ximg, (int64_t)T * (H / 64), items, perm, K, H, F, Fs,
-                                    has_sh ? 1 : 0, n_items, himg, L.h_rec, st),
+                                    has_sh ? 1 : 0, n_items, himg, L.h_rec, st, hflags),
                  "gate/up");
         SMOE_MARK();
         SMOE_TRY(smoe::launch_mm_down(de, ds, himg, (int64_t)(P + T) * L.h_rec, L.h_rec, sg, items, H, F, Fs, n_items,
@@ -347,7 +360,7 @@ smoe_status forward_impl(const smoe_geom* g, const smoe_weights* w, float* x_io,
                  "down");
     } else if (iq2) {
         SMOE_TRY(smoe::launch_iq2_gu(ge, ue, gs, us, ximg, items, perm, K, H, F, Fs, has_sh ? 1 : 0, n_items, himg,
-                                     L.h_blocks, st),
+                                     L.h_blocks, st, hq, P),
                  "gate/up");
         SMOE_MARK();
         SMOE_TRY(smoe::launch_iq2_down(de, ds, himg, L.h_blocks, sg, items, H, F, Fs, n_items, Y, st), "down");
@@ -365,7 +378,7 @@ smoe_status forward_impl(const smoe_geom* g, const smoe_weights* w, float* x_io,
                      "route + gate/up");
         else
             SMOE_TRY(smoe::launch_q2_gu(ge, ue, gs, us, ximg, items, perm, K, H, F, Fs, has_sh ? 1 : 0, n_items, himg,
-                                        L.h_blocks, st),
+                                        L.h_blocks, st, hq, P),
                      "gate/up");
         SMOE_MARK();
         if (small_down)
@@ -380,6 +393,19 @@ smoe_status forward_impl(const smoe_geom* g, const smoe_weights* w, float* x_io,
         SMOE_TRY(smoe::launch_combine(Y, slot, wts, K, H, P, T, (has_sh && add_shared) ? 1 : 0, y, st), "combine");
     SMOE_MARK();
 #undef SMOE_MARK
+    // the trace's expert stages and overflow mask, after the last stage event
+    if (trace) {
+        if (trace->xq && !mfma)
+            SMOE_TRY(smoe::launch_prep(x_io, (int64_t)T * H, trace->xq, nullptr, st), "trace xq");
+        if (trace->parts) SMOE_TRY(smoe::launch_copy_f32(Y, (int64_t)P * H, trace->parts, st), "trace parts");
+        if (trace->shared && has_sh)
+            SMOE_TRY(smoe::launch_copy_f32(Y + (size_t)P * H, (int64_t)T * H, trace->shared, st), "trace shared");
+        if (trace->overflow)
+            SMOE_TRY(smoe::launch_flags_mask(xflags, xflags ? (x_prev ? T : smoe::act_records_blocks((int64_t)T * (H / 64))) : 0, hflags,
+                                             hflags ? (int64_t)(F > Fs ? F : Fs) / 128 * n_items : 0, trace->overflow,
+                                             st),
+                     "trace overflow");
+    }
     return ok();
 }
 }  // namespace

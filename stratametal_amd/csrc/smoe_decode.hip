@@ -138,9 +138,13 @@ __device__ __forceinline__ float q2_unit_dot(const uint32_t (&w)[9], float d0, f
 // while its weight row (or its image values) is in flight; a row block then stages x = (xf + rprev) * scale
 // from the same registers, an image block quantises its own (xf + rprev) * scale; row block 0 of each token
 // tile writes x to `xout`.
-template <int MAXC>
+// F32 (router_dtype 1, the literal benchmark configuration's f32 router): x is staged in LDS as f32 and an expert
+// row is f32: lane l owns the 4-element chunks l, l+64, ... and fuses each product into its accumulator in element
+// order (fmaf, one rounding per step; oracle: or_f32_gemv_dev), then the same butterfly.  The shared gate row
+// stays bf16: its x values are rounded to bf16 from the f32 tile, so that sg equals the bf16 kernel's bit for bit.
+template <int MAXC, bool F32>
 __global__ __launch_bounds__(256) void k_router(const float* __restrict__ xf, const uint16_t* __restrict__ xb,
-                                                 const uint16_t* __restrict__ W, const uint16_t* __restrict__ w_inp,
+                                                 const void* __restrict__ W, const uint16_t* __restrict__ w_inp,
                                                  const float* __restrict__ bias, int H, int E, int rows_total, int T,
                                                  int tok_tile, float* __restrict__ logits, int ld_logits,
                                                  float* __restrict__ sg, uint32_t* __restrict__ ximg, int img_natural,
@@ -173,22 +177,28 @@ __global__ __launch_bounds__(256) void k_router(const float* __restrict__ xf, co
     const int lane = tid & 63;
     const int row = blockIdx.x * 4 + (tid >> 6);
     const int rowc = min(row, rows_total - 1);
-    const uint16_t* wr = rowc < E ? W + (size_t)rowc * H : w_inp;
-    const int chunks = H >> 3;
+    const bool frow = F32 && rowc < E;  // an f32 weight row: 4 values per 16-byte chunk (wave-uniform)
+    const uint8_t* wr = rowc < E ? static_cast<const uint8_t*>(W) + (size_t)rowc * H * (F32 ? 4 : 2)
+                                 : reinterpret_cast<const uint8_t*>(w_inp);
+    const int chunks = H >> 3;                      // 8-value bf16 chunks
+    const int wchunks = frow ? H >> 2 : chunks;     // 16-byte chunks of this wave's row
     uint4 wv[MAXC];
     float bv = 0.0f;
     if (!img_block) {
 #pragma unroll
         for (int j = 0; j < MAXC; ++j) {
             const int c = lane + 64 * j;
-            wv[j] = c < chunks ? *reinterpret_cast<const uint4*>(wr + 8 * c) : make_uint4(0, 0, 0, 0);
+            wv[j] = c < wchunks ? *reinterpret_cast<const uint4*>(wr + 16 * c) : make_uint4(0, 0, 0, 0);
         }
         bv = (bias && rowc < E) ? bias[rowc] : 0.0f;  // loaded once, outside the token loop
     }
     uint16_t* xs16 = reinterpret_cast<uint16_t*>(smem);
-    if (MAXC <= 8 && rprev) {  // the fused junction, 4 tokens at a time; a row block stages s * scale from registers
+    float* xs32 = reinterpret_cast<float*>(smem);
+    // values of a row per thread of the junction: 256 NM >= H (8 values per bf16 chunk, 4 per f32 chunk)
+    constexpr int NMJ = F32 ? MAXC : 2 * MAXC;
+    if (NMJ <= 16 && rprev) {  // the fused junction, 4 tokens at a time; a row block stages s * scale from registers
         for (int tb = 0; tb < nt; tb += 4) {
-            constexpr int NM = MAXC <= 8 ? 2 * MAXC : 1;
+            constexpr int NM = NMJ <= 16 ? NMJ : 1;
             float sv[4][NM];
             float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -227,7 +237,8 @@ __global__ __launch_bounds__(256) void k_router(const float* __restrict__ xf, co
                             const int j = tid + 256 * m;
                             if (j < H) {
                                 const float v = sv[g][m] * sc;
-                                xs16[(size_t)(tb + g) * H + j] = (uint16_t)f32_to_bf16(v);
+                                if constexpr (F32) xs32[(size_t)(tb + g) * H + j] = v;
+                                else xs16[(size_t)(tb + g) * H + j] = (uint16_t)f32_to_bf16(v);
                                 if (blockIdx.x == 0) xo[j] = v;
                             }
                         }
@@ -243,8 +254,24 @@ __global__ __launch_bounds__(256) void k_router(const float* __restrict__ xf, co
         return;
     }
     // stage the tile, 8 vector loads in flight per thread
+    if constexpr (F32) {  // f32 as it is (xf is given)
+        const int n4 = nt * H / 4;
+        for (int base = 0; !rprev && base < n4; base += 256 * 8) {
+            float4 f[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int g = min(base + u * 256 + (int)threadIdx.x, n4 - 1);
+                f[u] = reinterpret_cast<const float4*>(xf + (size_t)t0 * H)[g];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int g = base + u * 256 + threadIdx.x;
+                if (g < n4) reinterpret_cast<float4*>(smem)[g] = f[u];
+            }
+        }
+    }
     const int n8 = nt * H / 8;  // groups of 8 values = one uint4 of bf16
-    for (int base = 0; !rprev && base < n8; base += 256 * 4) {
+    for (int base = 0; !F32 && !rprev && base < n8; base += 256 * 4) {
         uint4 v[4];
         if (xf) {
             float4 f[8];
@@ -280,8 +307,53 @@ __global__ __launch_bounds__(256) void k_router(const float* __restrict__ xf, co
     for (int t = 0; t < nt; t += 4) {  // four tokens at a time: four independent accumulation chains
         const int ng = min(4, nt - t);
         float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if constexpr (F32) {
+            if (frow) {
 #pragma unroll
-        for (int j = 0; j < MAXC; ++j) {
+                for (int j = 0; j < MAXC; ++j) {
+                    const int c = lane + 64 * j;
+                    if (c < wchunks) {
+                        const float w4[4] = {u2f(wv[j].x), u2f(wv[j].y), u2f(wv[j].z), u2f(wv[j].w)};
+#pragma unroll
+                        for (int g = 0; g < 4; ++g) {
+                            if (g < ng) {
+                                const float4 xv = *reinterpret_cast<const float4*>(xs32 + (size_t)(t + g) * H + 4 * c);
+                                acc[g] = __builtin_fmaf(xv.x, w4[0], acc[g]);
+                                acc[g] = __builtin_fmaf(xv.y, w4[1], acc[g]);
+                                acc[g] = __builtin_fmaf(xv.z, w4[2], acc[g]);
+                                acc[g] = __builtin_fmaf(xv.w, w4[3], acc[g]);
+                            }
+                        }
+                    }
+                }
+            } else {  // the shared gate row: bf16(x) * bf16 w_inp, exact products in the bf16 kernel's order
+#pragma unroll
+                for (int j = 0; j < MAXC; ++j) {
+                    const int c = lane + 64 * j;
+                    if (c < chunks) {
+                        const uint32_t wq[4] = {wv[j].x, wv[j].y, wv[j].z, wv[j].w};
+#pragma unroll
+                        for (int g = 0; g < 4; ++g) {
+                            if (g < ng) {
+                                const float* xr = xs32 + (size_t)(t + g) * H + 8 * c;
+                                const float4 a = reinterpret_cast<const float4*>(xr)[0];
+                                const float4 b = reinterpret_cast<const float4*>(xr)[1];
+                                const float xv8[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+                                for (int q = 0; q < 4; ++q) {
+                                    const float x0 = u2f(f32_to_bf16(xv8[2 * q]) << 16);
+                                    const float x1 = u2f(f32_to_bf16(xv8[2 * q + 1]) << 16);
+                                    acc[g] = __builtin_fmaf(x0, u2f(wq[q] << 16), acc[g]);
+                                    acc[g] = __builtin_fmaf(x1, u2f(wq[q] & 0xFFFF0000u), acc[g]);
+                                }
+                            }
+                        }
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < MAXC && !F32; ++j) {
             const int c = lane + 64 * j;
             if (c < chunks) {
                 const uint32_t wq[4] = {wv[j].x, wv[j].y, wv[j].z, wv[j].w};
@@ -1186,11 +1258,12 @@ __device__ __forceinline__ void gu_commit(const Item& item, bool direct, const S
 // Dots of every column of the unit (the first batch already in `smem`, later batches staged here), SwiGLU, q8_1
 // image of h.  PRESTAGED: the images of every token are in LDS, token t in column slot t (batches of at most 4
 // tokens).
-template <int NIT, int MAXUPL, bool PRESTAGED>
+template <int NIT, int MAXUPL, bool PRESTAGED, bool HQ = false>
 __device__ __forceinline__ void gu_compute(const Item& item, int hb, uint32_t* smem, uint32_t (&w)[NIT][MAXUPL][9],
                                            const uint32_t* __restrict__ ximg, const int32_t* __restrict__ perm, int k,
                                            int H, uint32_t* __restrict__ himg, int h_blocks, float (&rowv)[kGuCols][64],
-                                           uint8_t (&qsc)[8][32], uint64_t* __restrict__ xchg) {
+                                           uint8_t (&qsc)[8][32], uint64_t* __restrict__ xchg, uint8_t* __restrict__ hq,
+                                           int hq_rows, int hq_blocks) {
     const RowGeo G = row_geo(H);
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int grp = lane / G.lpr, l = lane - grp * G.lpr;
@@ -1242,6 +1315,11 @@ __device__ __forceinline__ void gu_compute(const Item& item, int hb, uint32_t* s
                 q8_image_store(h, live_c, qsc[hw], nullptr, false, xchg + ((size_t)row * h_blocks + hb) * kXchgSlots);
             else
                 q8_image_store(h, live_c, qsc[hw], himg + ((size_t)row * h_blocks + hb) * kImgDw);
+            if constexpr (HQ) {  // the trace's standard q8_1 block of a pair's h (k_prep's quantiser: s = f32 sum of h)
+                uint32_t ds;
+                const int q = q8_1_value(h, &ds);
+                q8_1_store(q, ds, hq + ((size_t)row * hq_blocks + hb) * 36, live_c && row < hq_rows);
+            }
         }
         if (c0 + kGuCols < item.ncol) __syncthreads();
     }
@@ -1249,12 +1327,13 @@ __device__ __forceinline__ void gu_compute(const Item& item, int hb, uint32_t* s
 
 // The work-group's item, one unit (rows block hb): `smem` is the kernel's dynamic LDS (the image staging area).
 // With `xchg` the h images go to the tagged exchange words instead of himg.
-template <int NIT, int MAXUPL, bool PRESTAGED = false>
+template <int NIT, int MAXUPL, bool PRESTAGED = false, bool HQ = false>
 __device__ __forceinline__ void q2_gu_item(const Item& item, int hb, uint32_t* smem, const uint8_t* __restrict__ gate_exps,
                                            const uint8_t* __restrict__ up_exps, const uint8_t* __restrict__ gate_sh,
                                            const uint8_t* __restrict__ up_sh, const uint32_t* __restrict__ ximg,
                                            const int32_t* __restrict__ perm, int k, int H, int F,
-                                           uint32_t* __restrict__ himg, int h_blocks, uint64_t* __restrict__ xchg = nullptr) {
+                                           uint32_t* __restrict__ himg, int h_blocks, uint64_t* __restrict__ xchg = nullptr,
+                                           uint8_t* __restrict__ hq = nullptr, int hq_rows = 0) {
     __shared__ float rowv[kGuCols][64];
     __shared__ uint8_t qsc[8][32];
     uint32_t w[NIT][MAXUPL][9];
@@ -1266,23 +1345,25 @@ __device__ __forceinline__ void q2_gu_item(const Item& item, int hb, uint32_t* s
         gu_commit(item, direct, sp, smem, ximg, perm, k, H);
         __syncthreads();
     }
-    gu_compute<NIT, MAXUPL, PRESTAGED>(item, hb, smem, w, ximg, perm, k, H, himg, h_blocks, rowv, qsc, xchg);
+    gu_compute<NIT, MAXUPL, PRESTAGED, HQ>(item, hb, smem, w, ximg, perm, k, H, himg, h_blocks, rowv, qsc, xchg, hq,
+                                           hq_rows, F >> 5);
 }
 
-template <int NIT, int MAXUPL>
+template <int NIT, int MAXUPL, bool HQ>
 __global__ __launch_bounds__(256) void k_q2_gu(const uint8_t* __restrict__ gate_exps, const uint8_t* __restrict__ up_exps,
                                                 const uint8_t* __restrict__ gate_sh, const uint8_t* __restrict__ up_sh,
                                                 const uint32_t* __restrict__ ximg, const int4* __restrict__ items,
                                                 const int32_t* __restrict__ perm, int k, int H, int F, int Fs,
-                                                uint32_t* __restrict__ himg, int h_blocks) {
+                                                uint32_t* __restrict__ himg, int h_blocks, uint8_t* __restrict__ hq,
+                                                int hq_rows) {
     extern __shared__ __align__(16) uint32_t smem[];
     asm volatile("" ::"s"(gate_exps), "s"(up_exps), "s"(gate_sh), "s"(up_sh), "s"(ximg), "s"(himg), "s"(perm), "s"(k),
                  "s"(H), "s"(F), "s"(Fs), "s"(h_blocks));  // every kernarg loaded before the item
     Item item;
     if (!work_item_uniform(items, blockIdx.y, item)) return;
     if ((int)blockIdx.x * 32 >= (item.shared ? Fs : F)) return;
-    q2_gu_item<NIT, MAXUPL>(item, blockIdx.x, smem, gate_exps, up_exps, gate_sh, up_sh, ximg, perm, k, H, F, himg,
-                            h_blocks);
+    q2_gu_item<NIT, MAXUPL, false, HQ>(item, blockIdx.x, smem, gate_exps, up_exps, gate_sh, up_sh, ximg, perm, k, H, F,
+                                       himg, h_blocks, nullptr, hq, hq_rows);
 }
 
 // Gate/up of a batch of at most kShCols tokens straight from the logits, with no route kernel before it.  Grid
@@ -2113,13 +2194,34 @@ hipError_t launch_prep(const float* x, int64_t n, uint8_t* xq, uint16_t* xb, hip
     return hipGetLastError();
 }
 
-hipError_t launch_router(const float* xf, const uint16_t* xb, const uint16_t* W, const uint16_t* w_inp,
+hipError_t launch_router(const float* xf, const uint16_t* xb, const void* W, const uint16_t* w_inp,
                          const float* bias, int H, int E, int rows_total, int T, float* logits, int ld_logits, float* sg,
                          uint32_t* ximg, int tile_rows, int img_natural, hipStream_t s, const float* rprev, float eps,
-                         float* xout, uint4* clear, int clear_n16) {
+                         float* xout, uint4* clear, int clear_n16, int w_f32) {
     // the fused junction is the row-per-wave path's, for rows up to 4096; so is the clearing of the exchange
     if (rprev && (tile_rows || !xf || H > 4096)) return hipErrorInvalidValue;
     if (clear_n16 && (tile_rows || !clear)) return hipErrorInvalidValue;
+    // the f32 router runs on the row-per-wave path from f32 x
+    if (w_f32 && (tile_rows || !xf || H % 4 || H > 4096)) return hipErrorInvalidValue;
+    if (w_f32) {
+        const int maxc4 = (H / 4 + 63) / 64;
+        int tile = T <= 64 ? 4 : 16384 / H;  // f32 tile in LDS: at most 64 KiB
+        if (tile > 16) tile = 16;
+        if (tile > T) tile = T;
+        if (tile < 1) tile = 1;
+        const int img_blocks = ximg ? (tile * (H / 32) + 7) / 8 : 0;
+        dim3 grid((unsigned)((rows_total + 3) / 4 + img_blocks), (unsigned)((T + tile - 1) / tile));
+        const size_t lds = (size_t)tile * H * 4;
+#define SMOE_ROUTER_F32(C)                                                                                          \
+    hipLaunchKernelGGL((k_router<C, true>), grid, dim3(256), lds, s, xf, xb, W, w_inp, bias, H, E, rows_total, T,   \
+                       tile, logits, ld_logits, sg, ximg, img_natural, rprev, eps, xout, clear, clear_n16)
+        if (maxc4 <= 2) SMOE_ROUTER_F32(2);
+        else if (maxc4 <= 4) SMOE_ROUTER_F32(4);
+        else if (maxc4 <= 8) SMOE_ROUTER_F32(8);
+        else SMOE_ROUTER_F32(16);
+#undef SMOE_ROUTER_F32
+        return hipGetLastError();
+    }
     const int chunks = H / 8;
     const int maxc = (chunks + 63) / 64;
     // tokens staged per block: 4 for decode batches (more blocks, short staging), 16 (<= 64 KiB of bf16) beyond
@@ -2128,7 +2230,8 @@ hipError_t launch_router(const float* xf, const uint16_t* xb, const uint16_t* W,
         const size_t lds = (size_t)16 * H * 2;
 #define SMOE_ROUTER_TILE(C)                                                                                        \
     hipLaunchKernelGGL((k_router_tile<C>), dim3((unsigned)((rows_total + 15) / 16), (unsigned)((T + 15) / 16)),      \
-                       dim3(256), lds, s, xf, xb, W, w_inp, bias, H, E, rows_total, T, logits, ld_logits, sg)
+                       dim3(256), lds, s, xf, xb, static_cast<const uint16_t*>(W), w_inp, bias, H, E, rows_total, T, \
+                       logits, ld_logits, sg)
         if (maxc <= 2) SMOE_ROUTER_TILE(2);
         else if (maxc <= 4) SMOE_ROUTER_TILE(4);
         else SMOE_ROUTER_TILE(8);
@@ -2144,7 +2247,7 @@ hipError_t launch_router(const float* xf, const uint16_t* xb, const uint16_t* W,
     dim3 grid((unsigned)((rows_total + 3) / 4 + img_blocks), (unsigned)((T + tile - 1) / tile));
     const size_t lds = (size_t)tile * H * 2;
 #define SMOE_ROUTER(C)                                                                                          \
-    hipLaunchKernelGGL(k_router<C>, grid, dim3(256), lds, s, xf, xb, W, w_inp, bias, H, E, rows_total, T, tile, \
+    hipLaunchKernelGGL((k_router<C, false>), grid, dim3(256), lds, s, xf, xb, W, w_inp, bias, H, E, rows_total, T, tile, \
                        logits, ld_logits, sg, ximg, img_natural, rprev, eps, xout, clear, clear_n16)
     if (maxc <= 2) SMOE_ROUTER(2);
     else if (maxc <= 4) SMOE_ROUTER(4);
@@ -2210,15 +2313,21 @@ int gemv_shared_chunk() { return kShCols; }
 
 hipError_t launch_q2_gu(const uint8_t* gate_exps, const uint8_t* up_exps, const uint8_t* gate_sh, const uint8_t* up_sh,
                         const uint32_t* ximg, const int4* items, const int32_t* perm, int k, int H, int F, int Fs,
-                        int has_shared, int max_items, uint32_t* himg, int h_blocks, hipStream_t s) {
+                        int has_shared, int max_items, uint32_t* himg, int h_blocks, hipStream_t s, uint8_t* hq,
+                        int hq_rows) {
     const int Fmax = has_shared && Fs > F ? Fs : F;
     dim3 grid((unsigned)(Fmax / 32), (unsigned)max_items);
     int nit, upl;
     gu_shape(H, nit, upl);
     const size_t lds = (size_t)kGuCols * (H >> 5) * kImgDw * 4 + 16;  // + the dead staging slot
-#define SMOE_GU(N, U)                                                                                             \
-    hipLaunchKernelGGL((k_q2_gu<N, U>), grid, dim3(256), lds, s, gate_exps, up_exps, gate_sh, up_sh, ximg, items, perm, \
-                       k, H, F, Fs, himg, h_blocks)
+    // the traced variant (hq: the trace's q8_1 of h) is its own instantiation: the plain kernel keeps its registers
+#define SMOE_GU(N, U)                                                                                                \
+    if (hq)                                                                                                          \
+        hipLaunchKernelGGL((k_q2_gu<N, U, true>), grid, dim3(256), lds, s, gate_exps, up_exps, gate_sh, up_sh, ximg,  \
+                           items, perm, k, H, F, Fs, himg, h_blocks, hq, hq_rows);                                   \
+    else                                                                                                             \
+        hipLaunchKernelGGL((k_q2_gu<N, U, false>), grid, dim3(256), lds, s, gate_exps, up_exps, gate_sh, up_sh, ximg, \
+                           items, perm, k, H, F, Fs, himg, h_blocks, nullptr, 0)
     SMOE_SHAPE_DISPATCH(SMOE_GU)
 #undef SMOE_GU
     return hipGetLastError();

@@ -190,8 +190,9 @@ __device__ __forceinline__ int q8_1_value(float v, uint32_t* ds) {
 }
 
 // Packs the 32 int8 of a half wave into a q8_1 block in global memory: lanes 0..7 of the half write
-// one dword each of q, lane 0 also the {d, s} dword.  Every lane of the half must call it.
-__device__ __forceinline__ void q8_1_store(int q, uint32_t ds, uint8_t* blk) {
+// one dword each of q, lane 0 also the {d, s} dword.  Every lane of the half must call it; `store` false (the same
+// for the whole half) writes nothing.
+__device__ __forceinline__ void q8_1_store(int q, uint32_t ds, uint8_t* blk, bool store = true) {
     const int l32 = threadIdx.x & 31;
     const int base = threadIdx.x & 32;
     // gather bytes 4j..4j+3 into lane j
@@ -203,8 +204,8 @@ __device__ __forceinline__ void q8_1_store(int q, uint32_t ds, uint8_t* blk) {
         word |= v << (8 * b);
     }
     uint32_t* p = reinterpret_cast<uint32_t*>(blk);
-    if (l32 < 8) p[1 + l32] = word;
-    if (l32 == 0) p[0] = ds;
+    if (store && l32 < 8) p[1 + l32] = word;
+    if (store && l32 == 0) p[0] = ds;
 }
 
 }  // namespace smoe

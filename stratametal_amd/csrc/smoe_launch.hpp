@@ -12,13 +12,14 @@ bool down_shapes_match(int F, int Fs);   // routed and shared down rows share on
 size_t img_bytes(int64_t n_blocks);      // bytes of n_blocks q8_1 images
 
 hipError_t launch_prep(const float* x, int64_t n, uint8_t* xq, uint16_t* xb, hipStream_t s);
-hipError_t launch_router(const float* xf, const uint16_t* xb, const uint16_t* W, const uint16_t* w_inp,
+hipError_t launch_router(const float* xf, const uint16_t* xb, const void* W, const uint16_t* w_inp,
                          const float* bias, int H, int E, int rows_total, int T, float* logits, int ld_logits, float* sg,
                          uint32_t* ximg, int tile_rows, int img_natural, hipStream_t s, const float* rprev = nullptr,
-                         float eps = 0.0f, float* xout = nullptr, uint4* clear = nullptr, int clear_n16 = 0);
+                         float eps = 0.0f, float* xout = nullptr, uint4* clear = nullptr, int clear_n16 = 0,
+                         int w_f32 = 0);
 // (tile_rows: many tokens, row x token tiles from xb when given, else from xf; img_natural: write ximg in the IQ2_S
 // kernels' natural order; rprev: the fused stack junction, x = RMSNorm(xf + rprev) written to xout; clear: 16-byte
-// units zeroed for the exchange of the k_q2_moe_small launch after it)
+// units zeroed for the exchange of the k_q2_moe_small launch after it; w_f32: W is f32 (router_dtype 1), x from xf)
 hipError_t launch_topk(const float* logits, int ld_logits, int T, int E, int k, int32_t* ids, float* wts, hipStream_t s);
 hipError_t launch_dispatch(const int32_t* ids, int P, int E, int32_t* counts, int32_t* offsets, int32_t* perm,
                            int32_t* slot, int32_t* elist, int32_t* n_list, int4* items, int max_items, int T, int k,
@@ -36,7 +37,8 @@ int shared_items(int T);  // shared-expert work items for T tokens (GEMV path)
 int gemv_shared_chunk();   // shared-expert tokens per GEMV work item
 hipError_t launch_q2_gu(const uint8_t* gate_exps, const uint8_t* up_exps, const uint8_t* gate_sh, const uint8_t* up_sh,
                         const uint32_t* ximg, const int4* items, const int32_t* perm, int k, int H, int F, int Fs,
-                        int has_shared, int max_items, uint32_t* himg, int h_blocks, hipStream_t s);
+                        int has_shared, int max_items, uint32_t* himg, int h_blocks, hipStream_t s,
+                        uint8_t* hq = nullptr, int hq_rows = 0);  // hq: the trace's q8_1 of the first hq_rows h rows
 hipError_t launch_q2_down(const uint8_t* down_exps, const uint8_t* down_sh, const uint32_t* himg, int h_blocks,
                           const float* sg, const int4* items, int H, int F, int Fs, int max_items, float* Y,
                           hipStream_t s);
@@ -76,7 +78,8 @@ hipError_t launch_q2_mmvq(const uint8_t* w, const uint8_t* xq, int n_in, int n_o
 bool iq2_shape_ok(int n_in);  // n_in = 256 nb, nb in {2, 4, 8}
 hipError_t launch_iq2_gu(const uint8_t* gate_exps, const uint8_t* up_exps, const uint8_t* gate_sh, const uint8_t* up_sh,
                          const uint32_t* ximg, const int4* items, const int32_t* perm, int k, int H, int F, int Fs,
-                         int has_shared, int max_items, uint32_t* himg, int h_blocks, hipStream_t s);
+                         int has_shared, int max_items, uint32_t* himg, int h_blocks, hipStream_t s,
+                         uint8_t* hq = nullptr, int hq_rows = 0);
 hipError_t launch_iq2_down(const uint8_t* down_exps, const uint8_t* down_sh, const uint32_t* himg, int h_blocks,
                            const float* sg, const int4* items, int H, int F, int Fs, int max_items, float* Y,
                            hipStream_t s);
@@ -85,12 +88,21 @@ hipError_t launch_iq2_mmvq(const uint8_t* w, const uint8_t* xq, int n_in, int n_
 // prefill contract (bf16 MFMA)
 int mfma_chunk();                        // tokens per MFMA work item
 size_t act_rec_bytes(int64_t n_rec);     // bytes of n_rec 64-value activation records
+// flags (or NULL): one int32 per work-group, 1 when one of its values is beyond the fp16 operands (65520 or more);
+// act_records_blocks(n_rec) words for k_act_records, n_rows for k_junction_records, (Fmax / 128) * max_items for
+// k_mm_gu; launch_flags_mask folds them into the trace's overflow mask
 hipError_t launch_junction_records(const float* x, const float* r, int n_rows, int n, float eps, float* out,
-                                   uint32_t* rec, uint16_t* xb, hipStream_t s);
-hipError_t launch_act_records(const float* x, int64_t n_rec, uint32_t* rec, uint16_t* xb, hipStream_t s);  // xb: bf16 copy or NULL
+                                   uint32_t* rec, uint16_t* xb, hipStream_t s, int32_t* flags = nullptr);
+int64_t act_records_blocks(int64_t n_rec);
+hipError_t launch_act_records(const float* x, int64_t n_rec, uint32_t* rec, uint16_t* xb, hipStream_t s,
+                              int32_t* flags = nullptr);  // xb: bf16 copy or NULL
 hipError_t launch_mm_gu(const uint8_t* gate_exps, const uint8_t* up_exps, const uint8_t* gate_sh, const uint8_t* up_sh,
                         const uint32_t* xrec, int64_t n_xrec, const int4* items, const int32_t* perm, int k, int H,
-                        int F, int Fs, int has_shared, int max_items, uint32_t* hrec, int h_rec, hipStream_t s);
+                        int F, int Fs, int has_shared, int max_items, uint32_t* hrec, int h_rec, hipStream_t s,
+                        int32_t* flags = nullptr);
+// dst[i] = src[i] for n floats (trace copies)
+hipError_t launch_copy_f32(const float* src, int64_t n, float* dst, hipStream_t s);
+hipError_t launch_flags_mask(const int32_t* fx, int64_t nx, const int32_t* fh, int64_t nh, int32_t* out, hipStream_t s);
 hipError_t launch_mm_down(const uint8_t* down_exps, const uint8_t* down_sh, const uint32_t* hrec, int64_t n_hrec,
                           int h_rec, const float* sg, const int4* items, int H, int F, int Fs, int max_items, float* Y,
                           hipStream_t s);

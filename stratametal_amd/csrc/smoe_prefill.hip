@@ -70,17 +70,38 @@ __device__ __forceinline__ void store_record_chunk(const float (&v)[8], int64_t 
         make_uint4(b[0] | (b[1] << 16), b[2] | (b[3] << 16), b[4] | (b[5] << 16), b[6] | (b[7] << 16));
 }
 
-// One thread per 8 positions (a 16-byte chunk) of a record.
+// Whether a finite value's bf16 rounding lies beyond fp16 (65520 or more in magnitude: the MFMA operand would be
+// inf); the per-work-group flags of such values feed smoe_trace.overflow.
+__device__ __forceinline__ bool f16_overflow(float v) {
+    return __builtin_isfinite(v) && !(__builtin_fabsf(bf16_to_f32(f32_to_bf16(v))) < 65520.0f);
+}
+__device__ __forceinline__ bool f16_overflow8(const float (&v)[8]) {
+    bool o = false;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o |= f16_overflow(v[e]);
+    return o;
+}
+
+// One thread per 8 positions (a 16-byte chunk) of a record.  With `flags`, work-group b writes flags[b] = whether
+// any of its values is an fp16 overflow.
 __global__ __launch_bounds__(256) void k_act_records(const float* __restrict__ x, int64_t n_rec,
-                                                     uint32_t* __restrict__ rec, uint16_t* __restrict__ xb) {
+                                                     uint32_t* __restrict__ rec, uint16_t* __restrict__ xb,
+                                                     int32_t* __restrict__ flags) {
     const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
     const int64_t r = g >> 3;
-    if (r >= n_rec) return;
-    const int ch = (int)(g & 7);
-    const float4* src = reinterpret_cast<const float4*>(x + r * 64 + 16 * (ch & 3) + 8 * (ch >> 2));
-    const float4 lo = src[0], hi = src[1];
-    const float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-    store_record_chunk(v, r, ch, rec, xb);
+    bool ovf = false;
+    if (r < n_rec) {
+        const int ch = (int)(g & 7);
+        const float4* src = reinterpret_cast<const float4*>(x + r * 64 + 16 * (ch & 3) + 8 * (ch >> 2));
+        const float4 lo = src[0], hi = src[1];
+        const float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+        store_record_chunk(v, r, ch, rec, xb);
+        ovf = f16_overflow8(v);
+    }
+    if (flags) {
+        const int any = __syncthreads_or(ovf ? 1 : 0);
+        if (threadIdx.x == 0) flags[blockIdx.x] = any ? 1 : 0;
+    }
 }
 
 // The stack junction of the prefill path and the records of its output in one launch, one work-group per row:
@@ -89,19 +110,26 @@ __global__ __launch_bounds__(256) void k_act_records(const float* __restrict__ x
 // x, r and out 16-byte aligned.
 __global__ __launch_bounds__(256) void k_junction_records(const float* __restrict__ x, const float* __restrict__ r,
                                                           int n, float eps, float* __restrict__ out,
-                                                          uint32_t* __restrict__ rec, uint16_t* __restrict__ xb) {
+                                                          uint32_t* __restrict__ rec, uint16_t* __restrict__ xb,
+                                                          int32_t* __restrict__ flags) {
     __shared__ float wsum[4];
     __shared__ __align__(16) float row[4096];
     residual_rmsnorm_row<true>(x + (size_t)blockIdx.x * n, r + (size_t)blockIdx.x * n, n, eps,
                                out + (size_t)blockIdx.x * n, wsum, row);
     __syncthreads();
     const int rpr = n >> 6;
+    bool ovf = false;
     for (int g = threadIdx.x; g < rpr * 8; g += 256) {
         const int rl = g >> 3, ch = g & 7;
         const float4* src = reinterpret_cast<const float4*>(row + rl * 64 + 16 * (ch & 3) + 8 * (ch >> 2));
         const float4 lo = src[0], hi = src[1];
         const float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
         store_record_chunk(v, (int64_t)blockIdx.x * rpr + rl, ch, rec, xb);
+        ovf |= f16_overflow8(v);
+    }
+    if (flags) {
+        const int any = __syncthreads_or(ovf ? 1 : 0);
+        if (threadIdx.x == 0) flags[blockIdx.x] = any ? 1 : 0;
     }
 }
 
@@ -399,7 +427,7 @@ __device__ __forceinline__ float silu_mul_fast(float g, float u) {
 template <int MODE>
 __device__ __forceinline__ void mm_gu_body(uint8_t* lds, const int* rowidx, const Item& item, int ncol,
                                            const uint8_t* g0, const uint8_t* u0, const uint32_t* xrec,
-                                           uint32_t xrec_bytes, int H, uint32_t* hrec, int h_rec) {
+                                           uint32_t xrec_bytes, int H, uint32_t* hrec, int h_rec, int32_t* flag) {
     using S = Shape<MODE>;
     constexpr int NS = S::NS;
     const int rt = blockIdx.x;
@@ -423,6 +451,7 @@ __device__ __forceinline__ void mm_gu_body(uint8_t* lds, const int* rowidx, cons
     __syncthreads();  // every wave is done with the ring: its start becomes the h tile
     // h tile [column][128 rows in record order] as fp16 bits of bf16 values
     uint16_t* ht = reinterpret_cast<uint16_t*>(lds);
+    bool ovf = false;
 #pragma unroll
     for (int s = 0; s < NS / 2; ++s) {
         const int f = fbase + 16 * s + i;
@@ -433,12 +462,21 @@ __device__ __forceinline__ void mm_gu_body(uint8_t* lds, const int* rowidx, cons
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const int c = tok0 + 16 * n + 4 * q + r;
-                    if (c < ncol) ht[c * 128 + pos] = (uint16_t)bf16_as_f16(silu_mul_fast(acc[n][s][r], acc[n][s + NS / 2][r]));
+                    if (c < ncol) {
+                        const float h = silu_mul_fast(acc[n][s][r], acc[n][s + NS / 2][r]);
+                        ht[c * 128 + pos] = (uint16_t)bf16_as_f16(h);
+                        if (flag) ovf |= f16_overflow(h);
+                    }
                 }
             }
         }
     }
-    __syncthreads();
+    if (flag) {
+        const int any = __syncthreads_or(ovf ? 1 : 0);
+        if (threadIdx.x == 0) *flag = any ? 1 : 0;
+    } else {
+        __syncthreads();
+    }
     for (int idx = tid; idx < ncol * 16; idx += 512) {  // 16 chunks (two records) per column
         const int c = idx >> 4, rr = (idx >> 3) & 1, ch = idx & 7;
         const uint4 v = reinterpret_cast<const uint4*>(ht + c * 128 + 64 * rr)[ch];
@@ -450,22 +488,32 @@ __global__ __launch_bounds__(512) void k_mm_gu(const uint8_t* __restrict__ gate_
                                                const uint8_t* __restrict__ gate_sh, const uint8_t* __restrict__ up_sh,
                                                const uint32_t* __restrict__ xrec, uint32_t xrec_bytes,
                                                const int4* __restrict__ items, const int32_t* __restrict__ perm, int k,
-                                               int H, int F, int Fs, uint32_t* __restrict__ hrec, int h_rec) {
+                                               int H, int F, int Fs, uint32_t* __restrict__ hrec, int h_rec,
+                                               int32_t* __restrict__ flags) {
     __shared__ __align__(16) uint8_t lds[kLds];
     __shared__ int rowidx[kChunk];
+    // with `flags`, this work-group's word: whether one of its h values is an fp16 overflow (0 when it has no work)
+    int32_t* flag = flags ? flags + (size_t)blockIdx.y * gridDim.x + blockIdx.x : nullptr;
     Item item;
-    if (!work_item(items, blockIdx.y, item)) return;
+    if (!work_item(items, blockIdx.y, item)) {
+        if (flag && threadIdx.x == 0) *flag = 0;
+        return;
+    }
     const int Fe = item.shared ? Fs : F;
-    if (128 * (int)blockIdx.x >= Fe) return;
+    if (128 * (int)blockIdx.x >= Fe) {
+        if (flag && threadIdx.x == 0) *flag = 0;
+        return;
+    }
     const int ncol = item.ncol;
     if ((int)threadIdx.x < ncol) rowidx[threadIdx.x] = item_token(item, perm, k, threadIdx.x);
     __syncthreads();
     const size_t rb = (size_t)(H >> 7) * 36;
     const uint8_t* g0 = item.shared ? gate_sh : gate_exps + (size_t)item.e * F * rb;
     const uint8_t* u0 = item.shared ? up_sh : up_exps + (size_t)item.e * F * rb;
-    if (ncol > 64) mm_gu_body<kWide>(lds, rowidx, item, ncol, g0, u0, xrec, xrec_bytes, H, hrec, h_rec);
-    else if (ncol > kThinCols) mm_gu_body<kNarrow>(lds, rowidx, item, ncol, g0, u0, xrec, xrec_bytes, H, hrec, h_rec);
-    else mm_gu_body<kThin>(lds, rowidx, item, ncol, g0, u0, xrec, xrec_bytes, H, hrec, h_rec);
+    if (ncol > 64) mm_gu_body<kWide>(lds, rowidx, item, ncol, g0, u0, xrec, xrec_bytes, H, hrec, h_rec, flag);
+    else if (ncol > kThinCols)
+        mm_gu_body<kNarrow>(lds, rowidx, item, ncol, g0, u0, xrec, xrec_bytes, H, hrec, h_rec, flag);
+    else mm_gu_body<kThin>(lds, rowidx, item, ncol, g0, u0, xrec, xrec_bytes, H, hrec, h_rec, flag);
 }
 
 // ------------------------------------------------------------------------------------------------ down
@@ -541,27 +589,61 @@ int mfma_chunk() { return kChunk; }
 size_t act_rec_bytes(int64_t n_rec) { return (size_t)n_rec * kRecBytes; }
 
 hipError_t launch_junction_records(const float* x, const float* r, int n_rows, int n, float eps, float* out,
-                                   uint32_t* rec, uint16_t* xb, hipStream_t s) {
+                                   uint32_t* rec, uint16_t* xb, hipStream_t s, int32_t* flags) {
     if (n > 4096 || n % 64 || !r ||
         ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(r) | reinterpret_cast<uintptr_t>(out)) & 15))
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_junction_records, dim3((unsigned)n_rows), dim3(256), 0, s, x, r, n, eps, out, rec, xb);
+    hipLaunchKernelGGL(k_junction_records, dim3((unsigned)n_rows), dim3(256), 0, s, x, r, n, eps, out, rec, xb, flags);
     return hipGetLastError();
 }
 
-hipError_t launch_act_records(const float* x, int64_t n_rec, uint32_t* rec, uint16_t* xb, hipStream_t s) {
-    hipLaunchKernelGGL(k_act_records, dim3((unsigned)((n_rec * 8 + 255) / 256)), dim3(256), 0, s, x, n_rec, rec, xb);
+int64_t act_records_blocks(int64_t n_rec) { return (n_rec * 8 + 255) / 256; }
+
+hipError_t launch_act_records(const float* x, int64_t n_rec, uint32_t* rec, uint16_t* xb, hipStream_t s,
+                              int32_t* flags) {
+    hipLaunchKernelGGL(k_act_records, dim3((unsigned)act_records_blocks(n_rec)), dim3(256), 0, s, x, n_rec, rec, xb,
+                       flags);
     return hipGetLastError();
 }
 
 hipError_t launch_mm_gu(const uint8_t* gate_exps, const uint8_t* up_exps, const uint8_t* gate_sh, const uint8_t* up_sh,
                         const uint32_t* xrec, int64_t n_xrec, const int4* items, const int32_t* perm, int k, int H,
-                        int F, int Fs, int has_shared, int max_items, uint32_t* hrec, int h_rec, hipStream_t s) {
+                        int F, int Fs, int has_shared, int max_items, uint32_t* hrec, int h_rec, hipStream_t s,
+                        int32_t* flags) {
     const int Fmax = has_shared && Fs > F ? Fs : F;
     const size_t bytes = act_rec_bytes(n_xrec);
     if (bytes >= kOob) return hipErrorInvalidValue;  // buffer offsets are 31-bit
     hipLaunchKernelGGL(k_mm_gu, dim3((unsigned)(Fmax / 128), (unsigned)max_items), dim3(512), 0, s, gate_exps, up_exps,
-                       gate_sh, up_sh, xrec, (uint32_t)bytes, items, perm, k, H, F, Fs, hrec, h_rec);
+                       gate_sh, up_sh, xrec, (uint32_t)bytes, items, perm, k, H, F, Fs, hrec, h_rec, flags);
+    return hipGetLastError();
+}
+
+__global__ __launch_bounds__(256) void k_copy_f32(const float* __restrict__ src, int64_t n, float* __restrict__ dst) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) dst[i] = src[i];
+}
+
+hipError_t launch_copy_f32(const float* src, int64_t n, float* dst, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    int64_t blocks = (n + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    hipLaunchKernelGGL(k_copy_f32, dim3((unsigned)blocks), dim3(256), 0, s, src, n, dst);
+    return hipGetLastError();
+}
+
+// The overflow mask of smoe_trace: bit 0 when a flag of fx is set, bit 1 when one of fh is (one work-group).
+__global__ __launch_bounds__(256) void k_flags_mask(const int32_t* __restrict__ fx, int64_t nx,
+                                                    const int32_t* __restrict__ fh, int64_t nh, int32_t* __restrict__ out) {
+    int ax = 0, ah = 0;
+    for (int64_t i = threadIdx.x; i < nx; i += 256) ax |= fx[i];
+    for (int64_t i = threadIdx.x; i < nh; i += 256) ah |= fh[i];
+    ax = __syncthreads_or(ax);
+    ah = __syncthreads_or(ah);
+    if (threadIdx.x == 0) *out = (ax ? 1 : 0) | (ah ? 2 : 0);
+}
+
+hipError_t launch_flags_mask(const int32_t* fx, int64_t nx, const int32_t* fh, int64_t nh, int32_t* out,
+                             hipStream_t s) {
+    hipLaunchKernelGGL(k_flags_mask, dim3(1), dim3(256), 0, s, fx, nx, fh, nh, out);
     return hipGetLastError();
 }
 

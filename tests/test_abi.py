@@ -34,7 +34,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_status_strings():
     lib = S.lib()
-    assert lib.smoe_abi_version() == 104
+    assert lib.smoe_abi_version() == 105
     for code in (0, -1, -2, -3, -4, -5, -6):
         assert lib.smoe_status_str(code)
 
@@ -45,8 +45,9 @@ def _ws(g):
 
 def test_workspace_size_and_geometry_refusals():
     assert _ws(S.Geom()) > 0
+    assert _ws(S.Geom(router_dtype=1)) > 0  # the f32 router
     bad = [S.Geom(top_k=65), S.Geom(n_expert=1025), S.Geom(top_k=20, n_expert=10), S.Geom(n_embd=2000),
-           S.Geom(n_ff=100), S.Geom(w_type=13), S.Geom(router_dtype=1), S.Geom(n_embd=8192)]
+           S.Geom(n_ff=100), S.Geom(w_type=13), S.Geom(router_dtype=2), S.Geom(router_dtype=-1), S.Geom(n_embd=8192)]
     for g in bad:
         assert _ws(g) == 0, g
 

@@ -253,6 +253,15 @@ CASES = [
      dict(n_embd=256, n_ff=128, n_ff_shared=128, n_expert=128, top_k=32), 3, 23, True),
     ("fused, shared wider than routed, T=3", dict(n_embd=2048, n_ff=256, n_ff_shared=512, n_expert=32, top_k=4), 3,
      24, True),
+    # the f32 router of the literal configs[0] (router_dtype 1): f32 weights and activations in the router
+    ("f32 router, config 1 (decode b=1)", dict(router_dtype=1), 1, 41, True),
+    ("f32 router, fused T=3", dict(router_dtype=1, n_expert=64), 3, 42, True),
+    ("f32 router, b=16", dict(router_dtype=1, n_expert=64), 16, 43, True),
+    ("f32 router, H=4096", dict(router_dtype=1, n_embd=4096, n_ff=256, n_ff_shared=256, n_expert=16, top_k=4), 5, 44,
+     True),
+    ("f32 router, 70 tokens in tiles of 16", dict(router_dtype=1, n_embd=256, n_ff=128, n_ff_shared=128, n_expert=16,
+                                                  top_k=4), 70, 45, True),
+    ("f32 router, no shared expert", dict(router_dtype=1, sh_type=-1, n_expert=64), 2, 46, True),
 ]
 
 
@@ -291,6 +300,41 @@ def test_forward_decode_parity(torch, case):
     # determinism: a repeat is bitwise identical
     y2 = ml.forward(dev(torch, x), add_shared=add_shared)
     assert np.array_equal(bits(host(torch, y2)), bits(y))
+
+
+STAGE_CASES = [
+    # name, geometry, T, seed, add_shared: the expert stages of the trace (FfnTrace's exq, ehq, edown, shared)
+    ("stages, config 1 (decode b=1)", {}, 1, 51, True),
+    ("stages, small batch T=3 (the fused launch's stages)", dict(n_expert=64), 3, 52, True),
+    ("stages, b=16, shared not added", dict(n_expert=64), 16, 53, False),
+    ("stages, no shared expert", dict(n_embd=256, n_ff=128, n_ff_shared=128, n_expert=16, top_k=4, sh_type=-1), 5, 54,
+     True),
+    ("stages, IQ2_S", dict(n_embd=512, n_ff=512, n_ff_shared=512, n_expert=16, top_k=4, w_type=22, sh_type=22), 6, 55,
+     True),
+]
+
+
+@pytest.mark.parametrize("case", range(len(STAGE_CASES)))
+def test_forward_trace_stages_bitwise(torch, case):
+    """A traced call with the expert stages: xq, hq, parts and shared bitwise against the oracle's own trace; y
+    bitwise the same as the untraced call (the fused small-batch launch when it applies) and the oracle's."""
+    name, gkw, T, seed, add_shared = STAGE_CASES[case]
+    say(f"case: forward {name}")
+    g = O.Geom(**gkw)
+    w_host, w_dev = layer(torch, g, seed)
+    x = O.gen_normal(seed, 100, T * g.n_embd).reshape(T, g.n_embd)
+    ml = S.MoELayer(S.Geom(**vars(g)), w_dev, max_tokens=T)
+    y_plain = host(torch, ml.forward(dev(torch, x), add_shared=add_shared))
+    y, tr = ml.forward(dev(torch, x), add_shared=add_shared, trace=True, stages=True)
+    want, wtr = O.moe_decode_dev(g, w_host, x, add_shared=add_shared, trace=True, n_threads=8)
+    assert np.array_equal(bits(host(torch, y)), bits(want))
+    assert np.array_equal(bits(y_plain), bits(want))
+    assert np.array_equal(host(torch, tr["xq"]).ravel(), wtr["xq"].ravel()), "xq"
+    assert np.array_equal(host(torch, tr["hq"]).ravel(), wtr["hq"].ravel()), "hq"
+    assert np.array_equal(bits(host(torch, tr["parts"])), bits(wtr["parts"])), "parts"
+    if g.sh_type >= 0:
+        assert np.array_equal(bits(host(torch, tr["shared"])), bits(wtr["shared"])), "shared"
+    assert host(torch, tr["overflow"])[0] == 0
 
 
 def test_forward_zero_tokens_and_refusals_leave_output(torch):

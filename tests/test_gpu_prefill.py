@@ -78,6 +78,10 @@ CASES = [
     # reach 1024 (the packed scan fields must hold it)
     ("1024 experts all touched", dict(n_embd=256, n_ff=128, n_ff_shared=128, n_expert=1024, top_k=8), 2048, 18,
      True, None, S.PATH_AUTO),
+    # the f32 router (router_dtype 1) on the prefill path: the row-per-wave router over f32 token tiles
+    ("f32 router, prefill 512 Zipf 1.2", dict(router_dtype=1), 512, 19, True, "zipf", S.PATH_AUTO),
+    ("f32 router, 200 tokens", dict(router_dtype=1, n_embd=512, n_ff=256, n_expert=64, top_k=6), 200, 20, True, None,
+     S.PATH_AUTO),
 ]
 
 _LAYERS = {}
@@ -131,6 +135,37 @@ def test_forward_prefill_parity(torch, case):
     # determinism: a repeat is bitwise identical
     y2 = ml.forward(dev(torch, x), add_shared=add_shared, path=path)
     assert np.array_equal(bits(host(torch, y2)), bits(y))
+
+
+def test_trace_stages_and_fp16_overflow_mask(torch):
+    """The prefill path's trace: parts and shared within the contract's 1e-3 per row of the oracle's; the overflow
+    mask 0 for ordinary inputs, bit 0 for a token whose activations reach the fp16 limit (65520), bit 1 for one
+    whose h does, the other tokens' outputs unaffected; the decode path reports 0 on the same inputs."""
+    say("case: prefill trace stages and fp16 overflow mask")
+    g = O.Geom(n_embd=256, n_ff=128, n_ff_shared=128, n_expert=16, top_k=4)
+    w_host, w_dev = layer(torch, g, 31, None)
+    T = 160
+    ml = S.MoELayer(S.Geom(**vars(g)), w_dev, max_tokens=T)
+    x = O.gen_normal(31, 100, T * g.n_embd).reshape(T, g.n_embd)
+    y, tr = ml.forward(dev(torch, x), trace=True, stages=True)
+    want, wtr = O.moe_prefill(g, w_host, x, trace=True, n_threads=16)
+    assert host(torch, tr["overflow"])[0] == 0
+    assert O.rel_l1_rows(host(torch, y), want).max() <= TOL
+    assert O.rel_l1_rows(host(torch, tr["parts"]), wtr["parts"]).max() <= TOL
+    assert O.rel_l1_rows(host(torch, tr["shared"]), wtr["shared"]).max() <= TOL
+    for bad, scale, bit in ((7, 1e5, 1), (9, 1e3, 2)):
+        xb = x.copy()
+        xb[bad] *= scale
+        yb, trb = ml.forward(dev(torch, xb), trace=True, stages=True)
+        mask = int(host(torch, trb["overflow"])[0])
+        assert mask == bit, (scale, mask)
+        yw = O.moe_prefill(g, w_host, xb, n_threads=16)
+        assert np.isfinite(yw).all(), "the oracle holds the contract beyond the fp16 limit"
+        keep = np.arange(T) != bad
+        assert O.rel_l1_rows(host(torch, yb)[keep], yw[keep]).max() <= TOL
+        # the decode path has no such limit: it reports 0 on the same tokens
+        _, trd = ml.forward(dev(torch, xb[bad - 2:bad + 2]), trace=True, stages=True)
+        assert host(torch, trd["overflow"])[0] == 0
 
 
 def test_auto_path_switches_at_128_tokens(torch):

@@ -92,6 +92,10 @@ FUSED = [  # T, geometry, path the call takes
     (130, GEOM, "MFMA (junction kernel, then the call)"),
     (1, {}, "GEMV, the bench geometry"),
     (4, dict(n_embd=2560, n_ff=640, n_ff_shared=640, n_expert=64), "GEMV, H=2560"),
+    # the f32 router (router_dtype 1): the junction stages f32 values
+    (1, dict(router_dtype=1), "GEMV, f32 router, the bench geometry"),
+    (100, dict(GEOM, router_dtype=1), "GEMV, f32 router, token tiles"),
+    (130, dict(GEOM, router_dtype=1), "MFMA, f32 router"),
 ]
 
 

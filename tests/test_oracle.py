@@ -296,6 +296,37 @@ def test_router_gemv_orders():
     assert O.rel_l1_rows(dev[None], dbl[None])[0] <= 1e-5
 
 
+def test_f32_router_gemv_orders():
+    """The f32 router (router_dtype 1, the literal configs[0]): the device order against an exact float64 product,
+    the reference-style double sum, a brute-force restatement of the lane order on a small row, and the trap that
+    rounding x or W to bf16 (the repo's contract) is observable."""
+    H, E = 2048, 64
+    x = O.gen_normal(1, 1, H, 1.0)
+    W = O.gen_normal(1, 2, E * H, 0.02)
+    dev = O.f32_gemv_dev(x, W, H, E)
+    dbl = O.f32_gemv_double(x, W, H, E)
+    exact = W.reshape(E, H).astype(np.float64) @ x.astype(np.float64)
+    assert O.rel_l1_rows(dev[None], exact[None])[0] < 1e-6
+    assert O.rel_l1_rows(dev[None], dbl[None])[0] <= 1e-5
+    assert np.array_equal(dbl, exact.astype(np.float32))
+    bf = O.bf16_gemv_dev(O.bf16_from_f32(x), O.bf16_from_f32(W), H, E)
+    assert O.rel_l1_rows(bf[None], exact[None])[0] > 1e-3
+    # the lane order by hand: lane l fuses the products of chunks l, l + 64, ... in element order, then the butterfly
+    n = 512
+    xs, ws = x[:n], W[:n]
+    lanes = []
+    for l in range(64):
+        acc = np.float32(0.0)
+        for c in range(l, n // 4, 64):
+            for i in range(4):
+                acc = np.float32(np.float64(xs[4 * c + i]) * np.float64(ws[4 * c + i]) + np.float64(acc))
+        lanes.append(acc)
+    lanes = np.array(lanes, np.float32)
+    for o in (32, 16, 8, 4, 2, 1):
+        lanes = (lanes + lanes[np.arange(64) ^ o]).astype(np.float32)
+    assert O.f32_gemv_dev(xs, ws, n, 1)[0] == lanes[0]
+
+
 # ------------------------------------------------------------------------------------------------ A6 / A7 / A9 / A10
 
 def test_swiglu_trap_silu_on_up_is_observable():
@@ -427,6 +458,22 @@ def _prefill_contract_fp64(g, w, x, tr, round_x=True, round_h=True):
     return y
 
 
+def test_prefill_oracle_beyond_the_fp16_operand_limit():
+    """The prefill contract itself has no fp16 limit: a token whose activations reach 1e5 (beyond the device's fp16
+    MFMA operands, which the trace's overflow mask reports) stays finite in the oracle, and the other tokens are as
+    without it."""
+    g = O.Geom(n_embd=256, n_ff=128, n_ff_shared=128, n_expert=16, top_k=4)
+    w = O.make_weights(g, 31)
+    x = O.gen_normal(31, 100, 6 * 256).reshape(6, 256)
+    y = O.moe_prefill(g, w, x)
+    xb = x.copy()
+    xb[2] *= 1e5
+    yb = O.moe_prefill(g, w, xb)
+    assert np.isfinite(yb).all() and np.abs(yb[2]).max() > 65520.0
+    keep = np.arange(6) != 2
+    assert np.array_equal(yb[keep].view(np.uint32), y[keep].view(np.uint32))
+
+
 def test_prefill_oracle_against_independent_fp64_contract():
     """or_moe_prefill (the GPU MFMA path's checker) against the contract evaluated in fp64 from pinned pieces:
     within 1e-5 per row.  Dropping either bf16 rounding (x or h) moves the result by ~1e-3, so both traps are
@@ -483,3 +530,13 @@ def test_cpu_pool_baseline_equals_device_order_oracle():
     for add in (True, False):
         assert np.array_equal(O.moe_decode_pool(g, w, x, add_shared=add, n_threads=3).view(np.uint32),
                               O.moe_decode_dev(g, w, x, add_shared=add).view(np.uint32))
+    # the f32 router (router_dtype 1)
+    g = O.Geom(n_embd=256, n_ff=128, n_ff_shared=128, n_expert=16, top_k=4, router_dtype=1)
+    w = O.make_weights(g, 6)
+    assert w.router.dtype == np.float32
+    x = O.gen_normal(4, 2, 3 * 256).reshape(3, 256)
+    want = O.moe_decode_dev(g, w, x)
+    assert np.array_equal(O.moe_decode_pool(g, w, x, n_threads=2).view(np.uint32), want.view(np.uint32))
+    # and the router type is observable: the bf16 router of the same generator routes differently somewhere
+    gb = O.Geom(n_embd=256, n_ff=128, n_ff_shared=128, n_expert=16, top_k=4)
+    assert not np.array_equal(O.moe_decode_dev(gb, O.make_weights(gb, 6), x).view(np.uint32), want.view(np.uint32))
