@@ -206,6 +206,13 @@ smoe_status smoe_forward_static(const smoe_geom* g, const smoe_weights* w, const
 smoe_status smoe_router_topk(const float* logits, int32_t n_tokens, int32_t n_expert, int32_t k, int32_t* ids,
                              float* weights, void* hip_stream);
 
+/* The router-margin diagnostic (metal/src/forward.cpp:441-513), for reading an expert-id mismatch: per token, the
+ * k-th and (k+1)-th experts ranked by softmax probability (ties to the lower id), stats [T][4] = {p_k - p_k1 (the
+ * margin, before renormalisation), logits[id_k] - logits[id_k1], p_k, p_k1}, ids [T][2] = {id_k, id_k1}.
+ * 1 <= k < n_expert <= 1024. */
+smoe_status smoe_router_margin(const float* logits, int32_t n_tokens, int32_t n_expert, int32_t k, float* stats,
+                               int32_t* ids, void* hip_stream);
+
 /* x [n] f32 -> bf16 bits, round to nearest even, NaN quieted.
  * Replaces f32_to_bf16_bulk (metal/include/strata/metal/elementwise.hpp:27). */
 smoe_status smoe_f32_to_bf16(const float* x, int64_t n, uint16_t* y, void* hip_stream);

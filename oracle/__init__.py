@@ -82,6 +82,7 @@ def _set_sigs(L):
         "or_bf16_gemv_dev": (None, [vp, vp, i32, i32, vp]),
         "or_bf16_gemv_double": (None, [vp, vp, i32, i32, vp]),
         "or_f32_gemv_dev": (None, [vp, vp, i32, i32, vp]),
+        "or_router_margin_dev": (i32, [vp, i32, i32, i32, vp, vp]),
         "or_f32_gemv_double": (None, [vp, vp, i32, i32, vp]),
         "or_route_dev": (None, [vp, i32, i32, i32, vp, vp]),
         "or_route_ref": (None, [vp, i32, i32, i32, vp, vp]),
@@ -298,6 +299,18 @@ def _route(fn, logits, k):
     w = np.empty((T, k), np.float32)
     fn(_p(logits), T, E, k, _p(ids), _p(w))
     return ids, w
+
+
+def router_margin_dev(logits, k):
+    """The router-margin diagnostic in the device order: stats [T][4] = (p_k - p_k1, logit gap, p_k, p_k1) and
+    ids [T][2] = (id_k, id_k1) of the k-th and (k+1)-th experts by probability."""
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    T, E = logits.shape
+    stats = np.empty((T, 4), np.float32)
+    ids = np.empty((T, 2), np.int32)
+    if lib().or_router_margin_dev(_p(logits), T, E, k, _p(stats), _p(ids)) != 0:
+        raise ValueError("router margin needs 1 <= k < n_expert")
+    return stats, ids
 
 
 def route_dev(logits, k):

@@ -631,6 +631,60 @@ void or_route_dev(const float* logits, int n_tok, int n_expert, int k, int32_t* 
     free(taken);
 }
 
+/* The router-margin diagnostic (metal/src/forward.cpp:441-513): per token, the k-th and (k+1)-th experts ranked
+ * by softmax probability (strict greater-than, so a tie keeps the lower id), p_k - p_k1 before renormalisation,
+ * and their logit gap.  Device order (k_router_margin): ex and S as or_route_dev forms them, p_e = ex_e / S.
+ * stats [T][4] = {p_k - p_k1, l_k - l_k1, p_k, p_k1} (a NaN logit counts as -inf); ids [T][2] = {id_k, id_k1}. */
+int or_router_margin_dev(const float* logits, int n_tok, int n_expert, int k, float* stats, int32_t* ids) {
+    if (k < 1 || n_expert < k + 1) return -1;
+    float* key = (float*)malloc(sizeof(float) * (size_t)n_expert);
+    float* p = (float*)malloc(sizeof(float) * (size_t)n_expert);
+    char* taken = (char*)malloc((size_t)n_expert);
+    for (int t = 0; t < n_tok; ++t) {
+        const float* l = logits + (size_t)t * n_expert;
+        float mx = -INFINITY;
+        for (int e = 0; e < n_expert; ++e) {
+            key[e] = (l[e] != l[e]) ? -INFINITY : l[e];
+            mx = fmaxf(mx, key[e]);
+            taken[e] = 0;
+        }
+        float lane[64];
+        for (int j = 0; j < 64; ++j) {
+            float acc = 0.0f;
+            for (int e = j; e < n_expert; e += 64) {
+                p[e] = or_expf(key[e] - mx);
+                acc = acc + p[e];
+            }
+            lane[j] = acc;
+        }
+        for (int o = 32; o > 0; o >>= 1) {
+            float nxt[64];
+            for (int i = 0; i < 64; ++i) nxt[i] = lane[i] + lane[i ^ o];
+            memcpy(lane, nxt, sizeof lane);
+        }
+        for (int e = 0; e < n_expert; ++e) p[e] = p[e] / lane[0];
+        int pick[2] = {0, 0};
+        for (int i = 0; i <= k; ++i) {
+            int bi = -1;
+            for (int e = 0; e < n_expert; ++e)
+                if (!taken[e] && (bi < 0 || p[e] > p[bi])) bi = e;
+            taken[bi] = 1;
+            if (i >= k - 1) pick[i - (k - 1)] = bi;
+        }
+        float* st = stats + (size_t)t * 4;
+        st[0] = p[pick[0]] - p[pick[1]];
+        st[1] = key[pick[0]] - key[pick[1]];
+        st[2] = p[pick[0]];
+        st[3] = p[pick[1]];
+        ids[(size_t)t * 2] = pick[0];
+        ids[(size_t)t * 2 + 1] = pick[1];
+    }
+    free(key);
+    free(p);
+    free(taken);
+    return 0;
+}
+
 /* The reference's host routing, metal/src/router_parity.cpp:48-72 and metal/src/pack_parity.cpp:5144-5166:
  * double softmax over every expert, a stable descending sort (ties keep the lower id), the first k,
  * renormalised by max(sum, 2^-14) in double. */

@@ -74,6 +74,7 @@ void or_bf16_gemv_double(const uint16_t* xb, const uint16_t* w, int n_in, int n_
 void or_f32_gemv_dev(const float* x, const float* w, int n_in, int n_out, float* y);
 void or_f32_gemv_double(const float* x, const float* w, int n_in, int n_out, float* y);
 void or_route_dev(const float* logits, int n_tok, int n_expert, int k, int32_t* ids, float* w);
+int or_router_margin_dev(const float* logits, int n_tok, int n_expert, int k, float* stats, int32_t* ids);
 void or_route_ref(const float* logits, int n_tok, int n_expert, int k, int32_t* ids, float* w);
 
 /* ---- A6: SwiGLU + q8_1 requant */

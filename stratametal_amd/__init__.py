@@ -80,6 +80,7 @@ def lib():
             "smoe_ffn_workspace_bytes": (C.c_size_t, [vp, vp, i32]),
             "smoe_ffn_run": (i32, [vp, vp, vp, vp, i32, vp, i32, vp, C.c_size_t, vp, vp]),
             "smoe_router_topk": (i32, [vp, i32, i32, i32, vp, vp, vp]),
+            "smoe_router_margin": (i32, [vp, i32, i32, i32, vp, vp, vp]),
             "smoe_f32_to_bf16": (i32, [vp, i64, vp, vp]),
             "smoe_bf16_gemv": (i32, [vp, vp, vp, i32, i32, i32, vp]),
             "smoe_quantize_q8_1": (i32, [vp, i64, vp, vp]),
@@ -466,6 +467,20 @@ def router_topk(logits, k: int, stream=None):
     w = torch.empty((T, k), dtype=torch.float32, device=logits.device)
     _check(lib().smoe_router_topk(logits.data_ptr(), T, E, k, ids.data_ptr(), w.data_ptr(), _stream(stream)))
     return ids, w
+
+
+def router_margin(logits, k: int, stream=None):
+    """The router-margin diagnostic (smoe_router_margin): stats (T, 4) = (p_k - p_k1, logit gap, p_k, p_k1) and
+    ids (T, 2) = (id_k, id_k1) of the k-th and (k+1)-th experts by softmax probability."""
+    import torch
+    if logits.dim() != 2:
+        raise SmoeError(-1, "logits must be (tokens, n_expert)")
+    _need(logits, "logits", torch.float32)
+    T, E = logits.shape
+    stats = torch.empty((T, 4), dtype=torch.float32, device=logits.device)
+    ids = torch.empty((T, 2), dtype=torch.int32, device=logits.device)
+    _check(lib().smoe_router_margin(logits.data_ptr(), T, E, k, stats.data_ptr(), ids.data_ptr(), _stream(stream)))
+    return stats, ids
 
 
 def f32_to_bf16(x, stream=None):

@@ -178,7 +178,7 @@ const char* smoe_status_str(smoe_status s) {
 
 const char* smoe_last_error(void) { return g_last.c_str(); }
 
-int32_t smoe_abi_version(void) { return 105; }
+int32_t smoe_abi_version(void) { return 106; }
 
 size_t smoe_workspace_bytes(const smoe_geom* g, int32_t max_tokens) {
     if (check_geom(g) != SMOE_OK || max_tokens < 0) return 0;
@@ -651,6 +651,20 @@ smoe_status smoe_router_topk(const float* logits, int32_t n_tokens, int32_t n_ex
     if (k > n_expert) return fail(SMOE_EINVAL, "router_topk: k exceeds n_expert");
     if (!logits || !ids || !weights) return fail(SMOE_ENULL, "router_topk: NULL buffer");
     SMOE_TRY(smoe::launch_topk(logits, n_expert, n_tokens, n_expert, k, ids, weights, stream_of(hip_stream)), "topk");
+    return ok();
+}
+
+smoe_status smoe_router_margin(const float* logits, int32_t n_tokens, int32_t n_expert, int32_t k, float* stats,
+                               int32_t* ids, void* hip_stream) {
+    if (n_tokens < 0 || n_expert < 0 || k < 0) return fail(SMOE_EINVAL, "router_margin: negative size");
+    if (n_tokens == 0) return ok();
+    if (k < 1 || k >= n_expert) return fail(SMOE_EINVAL, "router_margin: needs 1 <= k < n_expert");
+    if (n_expert > kMaxExpert) return fail(SMOE_EINVAL, "router_margin: n_expert exceeds 1024");
+    if (!logits || !stats || !ids) return fail(SMOE_ENULL, "router_margin: NULL buffer");
+    if (!aligned(logits, 4) || !aligned(stats, 4) || !aligned(ids, 4))
+        return fail(SMOE_EALIGN, "router_margin: buffers must be 4-byte aligned");
+    SMOE_TRY(smoe::launch_router_margin(logits, n_tokens, n_expert, k, stats, ids, stream_of(hip_stream)),
+             "router_margin");
     return ok();
 }
 

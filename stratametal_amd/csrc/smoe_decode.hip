@@ -696,6 +696,80 @@ __device__ __forceinline__ void route_token_ids(const float* __restrict__ l, int
     else route_token_t<16, false>(l, E, k, nullptr, nullptr, ids_lds);
 }
 
+// The router-margin diagnostic (metal/src/forward.cpp:441-513), one wave per token: ex and S as route_token_t forms
+// them, p = ex / S, then k + 1 rounds of a wave argmax over the untaken (p desc, id asc); rounds k - 1 and k give
+// stats[t] = {p_k - p_k1, l_k - l_k1, p_k, p_k1} and ids[t] = {id_k, id_k1} (oracle: or_router_margin_dev).
+template <int J>
+__global__ __launch_bounds__(64) void k_router_margin(const float* __restrict__ logits, int E, int k,
+                                                       float* __restrict__ stats, int32_t* __restrict__ ids) {
+    const int lane = threadIdx.x;
+    const float* l = logits + (size_t)blockIdx.x * E;
+    float key[J], p[J];
+    float mx = -__builtin_inff();
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const int e = lane + 64 * j;
+        const float v = e < E ? l[e] : -__builtin_inff();
+        key[j] = v != v ? -__builtin_inff() : v;
+        mx = __builtin_fmaxf(mx, key[j]);
+    }
+    mx = wave_max_fast(mx);
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const bool valid = lane + 64 * j < E;
+        const float x = expf_smoe(key[j] - mx);
+        p[j] = valid ? x : 0.0f;
+        acc = valid ? acc + x : acc;
+    }
+    const float S = wave_sum_xor_fast(acc);
+#pragma unroll
+    for (int j = 0; j < J; ++j) p[j] = lane + 64 * j < E ? p[j] / S : -__builtin_inff();  // -inf: never picked
+    int pick[2] = {0, 0};
+    float pk[2] = {0.0f, 0.0f}, lk[2] = {0.0f, 0.0f};
+    for (int i = 0; i <= k; ++i) {
+        int bj = 0;  // the lane's best untaken slot: (p desc, id asc)
+#pragma unroll
+        for (int j = 1; j < J; ++j) bj = p[j] > p[bj] ? j : bj;
+        float bp = p[0], bk = key[0];
+#pragma unroll
+        for (int j = 1; j < J; ++j) {
+            bp = j == bj ? p[j] : bp;
+            bk = j == bj ? key[j] : bk;
+        }
+        const float gp = wave_max_fast(bp);
+        const int wid = wave_min_i32_fast(bp == gp ? lane + 64 * bj : 0x7FFFFFFF);
+        if (i >= k - 1) {
+            const int at = i - (k - 1);
+            pick[at] = wid;
+            pk[at] = gp;
+            lk[at] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bk), wid & 63));
+        }
+        if (lane == (wid & 63)) {
+#pragma unroll
+            for (int j = 0; j < J; ++j)
+                if (j == (wid >> 6)) p[j] = -__builtin_inff();
+        }
+    }
+    if (lane == 0) {
+        float* st = stats + (size_t)blockIdx.x * 4;
+        st[0] = pk[0] - pk[1];
+        st[1] = lk[0] - lk[1];
+        st[2] = pk[0];
+        st[3] = pk[1];
+        ids[(size_t)blockIdx.x * 2] = pick[0];
+        ids[(size_t)blockIdx.x * 2 + 1] = pick[1];
+    }
+}
+
+hipError_t launch_router_margin(const float* logits, int T, int E, int k, float* stats, int32_t* ids, hipStream_t s) {
+    if (E > 1024 || k < 1 || k >= E || T <= 0) return hipErrorInvalidValue;
+    if (E <= 64) hipLaunchKernelGGL((k_router_margin<1>), dim3((unsigned)T), dim3(64), 0, s, logits, E, k, stats, ids);
+    else if (E <= 512) hipLaunchKernelGGL((k_router_margin<8>), dim3((unsigned)T), dim3(64), 0, s, logits, E, k, stats, ids);
+    else hipLaunchKernelGGL((k_router_margin<16>), dim3((unsigned)T), dim3(64), 0, s, logits, E, k, stats, ids);
+    return hipGetLastError();
+}
+
 __global__ __launch_bounds__(64) void k_topk(const float* __restrict__ logits, int ld_logits, int T, int E, int k,
                                               int32_t* __restrict__ ids, float* __restrict__ wts) {
     const int t = blockIdx.x;

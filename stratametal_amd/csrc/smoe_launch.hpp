@@ -21,6 +21,7 @@ hipError_t launch_router(const float* xf, const uint16_t* xb, const void* W, con
 // kernels' natural order; rprev: the fused stack junction, x = RMSNorm(xf + rprev) written to xout; clear: 16-byte
 // units zeroed for the exchange of the k_q2_moe_small launch after it; w_f32: W is f32 (router_dtype 1), x from xf)
 hipError_t launch_topk(const float* logits, int ld_logits, int T, int E, int k, int32_t* ids, float* wts, hipStream_t s);
+hipError_t launch_router_margin(const float* logits, int T, int E, int k, float* stats, int32_t* ids, hipStream_t s);
 hipError_t launch_dispatch(const int32_t* ids, int P, int E, int32_t* counts, int32_t* offsets, int32_t* perm,
                            int32_t* slot, int32_t* elist, int32_t* n_list, int4* items, int max_items, int T, int k,
                            int has_shared, int chunk, int sh_chunk, hipStream_t s);

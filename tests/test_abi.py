@@ -34,7 +34,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_status_strings():
     lib = S.lib()
-    assert lib.smoe_abi_version() == 105
+    assert lib.smoe_abi_version() == 106
     for code in (0, -1, -2, -3, -4, -5, -6):
         assert lib.smoe_status_str(code)
 
@@ -106,6 +106,12 @@ def test_stage_refusals_and_zero_counts():
     assert L.smoe_router_topk(FAKE, -1, 32, 4, FAKE, FAKE, None) == -1
     assert L.smoe_router_topk(FAKE, 1, 4, 8, FAKE, FAKE, None) == -1
     assert L.smoe_router_topk(FAKE, 0, 512, 10, FAKE, FAKE, None) == 0       # zero tokens: no launch
+    assert L.smoe_router_margin(FAKE, 1, 10, 10, FAKE, FAKE, None) == -1     # needs k < n_expert
+    assert L.smoe_router_margin(FAKE, 1, 1025, 10, FAKE, FAKE, None) == -1
+    assert L.smoe_router_margin(FAKE, 1, 512, 0, FAKE, FAKE, None) == -1
+    assert L.smoe_router_margin(None, 1, 512, 10, FAKE, FAKE, None) == -6
+    assert L.smoe_router_margin(FAKE + 2, 1, 512, 10, FAKE, FAKE, None) == -5
+    assert L.smoe_router_margin(FAKE, 0, 512, 10, FAKE, FAKE, None) == 0     # zero tokens: no launch
     # combine: k = 65, negative, zero (metal/src/moe_combine_parity.cpp)
     assert L.smoe_combine(FAKE, FAKE, None, FAKE, 16, 65, None) == -1
     assert L.smoe_combine(FAKE, FAKE, None, FAKE, -1, 4, None) == -1

@@ -291,6 +291,10 @@ def test_forward_decode_parity(torch, case):
     assert np.array_equal(bits(y), bits(want)), f"max rel {O.rel_l1_rows(y, want).max()}"
     # the reference's own checks: host routing on the device logits, and the reference-order chain
     ids_r, w_r = O.route_ref(host(torch, tr["logits"]), g.top_k)
+    if not np.array_equal(ids_r, host(torch, tr["ids"])) and g.top_k < g.n_expert:
+        st, _ = S.router_margin(tr["logits"], g.top_k)  # the diagnostic beside the mismatch
+        pytest.fail(f"ids differ from the reference routing; smallest k-th/(k+1)-th margin "
+                    f"{host(torch, st)[:, 0].min():.3e}")
     assert np.array_equal(ids_r, host(torch, tr["ids"]))
     assert np.max(np.abs(host(torch, tr["weights"]) - w_r) / np.abs(w_r)) <= 1e-5
     yref = O.moe_decode_ref(g, w_host, x, add_shared=add_shared, n_threads=8)
@@ -335,6 +339,21 @@ def test_forward_trace_stages_bitwise(torch, case):
     if g.sh_type >= 0:
         assert np.array_equal(bits(host(torch, tr["shared"])), bits(wtr["shared"])), "shared"
     assert host(torch, tr["overflow"])[0] == 0
+
+
+@pytest.mark.parametrize("T,E,K", [(37, 512, 10), (5, 1000, 1), (4, 64, 63), (3, 100, 7)])
+def test_router_margin_bitwise(torch, T, E, K):
+    """The router-margin diagnostic (smoe_router_margin) bitwise against the oracle's device order, including rows
+    of exact ties."""
+    say(f"case: router margin T={T} E={E} k={K}")
+    l = (O.gen_normal(T + E, 7, T * E) * 0.9).reshape(T, E)
+    l[0] = 0.25                       # all equal: ids k-1, k, margin 0
+    if T > 2:
+        l[1, :12] = l[1].max() + 1.0  # a 12-way tie at the top
+    st, ids = S.router_margin(dev(torch, l), K)
+    wst, wids = O.router_margin_dev(l, K)
+    assert np.array_equal(host(torch, ids), wids)
+    assert np.array_equal(bits(host(torch, st)), bits(wst))
 
 
 def test_forward_zero_tokens_and_refusals_leave_output(torch):

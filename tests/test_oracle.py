@@ -269,6 +269,38 @@ def test_router_known_answers():
     assert K / E > 6.103515625e-05
 
 
+def test_router_margin_pinned():
+    """The router-margin diagnostic (metal/src/forward.cpp:441-513): a closed form on geometric logits, the all-equal
+    tie, a float64 evaluation on random logits, and the rule that the ranking is the routing's own."""
+    E, K = 512, 10
+    # logits -0.1 e: p_e proportional to exp(-0.1 e), the k-th and (k+1)-th are experts k-1 and k
+    l = (-0.1 * np.arange(E)).astype(np.float32)[None]
+    st, ids = O.router_margin_dev(l, K)
+    ll = l[0].astype(np.float64)
+    p = np.exp(ll - ll.max()) / np.exp(ll - ll.max()).sum()
+    assert list(ids[0]) == [K - 1, K]
+    assert abs(st[0, 0] - (p[K - 1] - p[K])) <= 1e-7 and abs(st[0, 2] - p[K - 1]) <= 1e-7
+    assert st[0, 1] == np.float32(l[0, K - 1] - l[0, K])
+    # all equal: ids k-1 and k (ties to the lower id), margin exactly 0, p = 1/E
+    st, ids = O.router_margin_dev(np.full((3, E), 0.5, np.float32), K)
+    assert (ids == [K - 1, K]).all() and (st[:, 0] == 0).all() and np.allclose(st[:, 2], 1.0 / E, rtol=1e-6)
+    # random logits: ids are the routing's k-th pick and its (k+1)-th; the margin within 1e-7 of float64
+    T = 64
+    lr = (O.gen_normal(9, 9, T * E) * 0.9).reshape(T, E)
+    st, ids = O.router_margin_dev(lr, K)
+    ids11, _ = O.route_dev(lr, K + 1)
+    assert (ids[:, 0] == ids11[:, K - 1]).all() and (ids[:, 1] == ids11[:, K]).all()
+    l64 = lr.astype(np.float64)
+    p64 = np.exp(l64 - l64.max(axis=1, keepdims=True))
+    p64 /= p64.sum(axis=1, keepdims=True)
+    rows = np.arange(T)
+    m64 = p64[rows, ids[:, 0]] - p64[rows, ids[:, 1]]
+    assert np.abs(st[:, 0] - m64).max() <= 1e-7
+    assert np.array_equal(st[:, 1], (lr[rows, ids[:, 0]] - lr[rows, ids[:, 1]]).astype(np.float32))
+    with pytest.raises(ValueError):
+        O.router_margin_dev(lr[:, :10], 10)
+
+
 @pytest.mark.parametrize("T,E,K", [(64, 512, 10), (4, 7, 3), (4, 1024, 10), (2, 64, 64)])
 def test_route_device_order_matches_reference_routing(T, E, K):
     logits = O.gen_normal(2024, E + K, T * E).reshape(T, E)
