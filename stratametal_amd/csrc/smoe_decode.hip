@@ -11,6 +11,8 @@
 //   k_q2_down  per (touched expert | shared, a chunk of output rows): down rows (times the shared gate)
 //   k_combine  y = routing-weighted sum of the pair rows + the shared row
 // Reduction orders are fixed and restated on the host by the test oracle (oracle/smoe_oracle.c).
+#include <utility>
+
 #include "smoe_device.hpp"
 #include "smoe_items.hpp"
 #include "smoe_gemv.hpp"
@@ -684,16 +686,149 @@ __device__ __forceinline__ void route_token_t(const float* __restrict__ l, int E
     if (lane < k && ids_lds) ids_lds[lane] = my_id;
 }
 
+// The same selection with few instructions in the wave's serial path (route_token_t's rounds each pop a sorted head
+// in every lane): theta = the k-th largest lane maximum (a bitwise search over ballot counts), so that at least k
+// keys are >= theta; those candidates (C of them, usually a few more than k) are compacted into lanes c < C in
+// ascending id order through `cand` (64 LDS entries of this wave); each candidate's rank is the number of
+// candidates with a larger key or an equal key at a lower id, which is its selection round.  ok is false (nothing
+// formed; the caller runs route_token_t) when more than 64 keys reach theta (ties across many experts).
+// Lane i < k ends with the i-th selection (sel_id, and with WTS its weight, formed as route_token_t forms it:
+// ex = expf(v - max) of the selected logit over S, the same lane sums and butterfly); lane c < C holds candidate c
+// (cid) and its rank (crank; >= k: not selected; 64 for lanes past C).
+// One step of route_fast_t's rank: the candidate in lane ^ S (within 32 lanes) counts when its (key, position) is
+// ahead of this lane's.
+template <int S>
+__device__ __forceinline__ void rank_xor_step(uint32_t ck, uint64_t self, int lane, int& r) {
+    const uint32_t pk = (uint32_t)__builtin_amdgcn_ds_swizzle((int)ck, 0x1F | (S << 10));
+    r += (((uint64_t)pk << 32) | (uint32_t)(63 - (lane ^ S))) > self ? 1 : 0;
+}
+template <int... S>
+__device__ __forceinline__ void rank_xor_steps(uint32_t ck, uint64_t self, int lane, int& r,
+                                               std::integer_sequence<int, S...>) {
+    (rank_xor_step<S + 1>(ck, self, lane, r), ...);
+}
+
+struct FastRoute {
+    bool ok;
+    int sel_id, cid, crank;
+    float sel_w;
+};
+template <int J, bool WTS>
+__device__ __forceinline__ FastRoute route_fast_t(const float* __restrict__ l, int E, int k, uint2* cand) {
+    const int lane = threadIdx.x & 63;
+    FastRoute R;
+    float x[J];
+    uint32_t key[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const int e = lane + 64 * j;
+        x[j] = l[e < E ? e : E - 1];
+    }
+    uint32_t m = 0u;
+    float mx = -__builtin_inff();
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const bool valid = lane + 64 * j < E;
+        float v = x[j];
+        v = (v != v || !valid) ? -__builtin_inff() : v;
+        key[j] = valid ? order_key(v) : 0u;
+        x[j] = v;
+        m = max(m, key[j]);
+        mx = __builtin_fmaxf(mx, v);
+    }
+    // theta = the k-th largest lane maximum: at least k keys reach it, and every key above the k-th largest does
+    const uint32_t th = (uint32_t)__builtin_amdgcn_readlane((int)wave_sort_desc_u32(m), k - 1);
+    unsigned long long bj[J];
+    int C = 0;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        bj[j] = __ballot(key[j] >= th);
+        C += __popcll(bj[j]);
+    }
+    R.ok = C >= k && C <= 64;
+    if (!R.ok) return R;  // uniform
+    int base = 0;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        if (key[j] >= th) {
+            const int pos = base + __builtin_amdgcn_mbcnt_hi((uint32_t)(bj[j] >> 32),
+                                                             __builtin_amdgcn_mbcnt_lo((uint32_t)bj[j], 0u));
+            cand[pos] = make_uint2(key[j], (uint32_t)(lane + 64 * j));
+        }
+        base += __popcll(bj[j]);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    const uint2 c = cand[lane < C ? lane : 0];
+    const uint32_t ck = lane < C ? c.x : 0u;
+    // rank: (key, position) pairs ordered by key, then the lower position (lower id) first; up to 32 candidates by
+    // independent xor exchanges (lanes past C hold key 0, below every key), beyond that one candidate per step
+    int r = 0;
+    const uint64_t self = ((uint64_t)ck << 32) | (uint32_t)(63 - lane);
+    if (C <= 16) {
+        rank_xor_steps(ck, self, lane, r, std::make_integer_sequence<int, 15>{});
+    } else if (C <= 32) {
+        rank_xor_steps(ck, self, lane, r, std::make_integer_sequence<int, 31>{});
+    } else {
+        for (int q = 0; q < C; ++q) {
+            const uint32_t sk = (uint32_t)__builtin_amdgcn_readlane((int)ck, q);
+            r += (sk > ck || (sk == ck && q < lane)) ? 1 : 0;
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    R.cid = (int)c.y;
+    R.crank = lane < C ? r : 64;
+    const int to = lane < C ? r : lane;  // candidate ranks and the lanes past C: a permutation of 0..63
+    R.sel_id = __builtin_amdgcn_ds_permute(4 * to, (int)c.y);
+    R.sel_w = 0.0f;
+    if constexpr (WTS) {
+        const uint32_t skey = (uint32_t)__builtin_amdgcn_ds_permute(4 * to, (int)ck);
+        mx = wave_max_fast(mx);
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const bool valid = lane + 64 * j < E;
+            const float ex = expf_smoe(x[j] - mx);
+            acc = valid ? acc + ex : acc;
+        }
+        const float S = wave_sum_xor_fast(acc);
+        const float v = u2f((skey & 0x80000000u) ? (skey & 0x7FFFFFFFu) : ~skey);  // order_key inverted
+        const float p = lane < k ? expf_smoe(v - mx) / S : 0.0f;
+        float ssel = 0.0f;
+        for (int i = 0; i < k; ++i) ssel = ssel + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), i));
+        R.sel_w = p / __builtin_fmaxf(ssel, 6.103515625e-05f);
+    }
+    return R;
+}
+
+// route_token_t's outputs by route_fast_t, or by route_token_t itself when the fast selection declines.
+template <int J, bool WTS>
+__device__ __forceinline__ void route_token_any(const float* __restrict__ l, int E, int k, int32_t* __restrict__ ids,
+                                                float* __restrict__ wts, int32_t* ids_lds, float* wts_lds) {
+    __shared__ uint2 s_cand[4][64];
+    const int lane = threadIdx.x & 63;
+    const FastRoute R = route_fast_t<J, WTS>(l, E, k, s_cand[(threadIdx.x >> 6) & 3]);
+    if (!R.ok) {
+        route_token_t<J, WTS>(l, E, k, ids, wts, ids_lds, wts_lds);
+        return;
+    }
+    if (lane < k) {
+        if (ids) ids[lane] = R.sel_id;
+        if (WTS && wts) wts[lane] = R.sel_w;
+        if (ids_lds) ids_lds[lane] = R.sel_id;
+        if (WTS && wts_lds) wts_lds[lane] = R.sel_w;
+    }
+}
+
 __device__ __forceinline__ void route_token(const float* __restrict__ l, int E, int k, int32_t* __restrict__ ids,
                                             float* __restrict__ wts, int32_t* ids_lds = nullptr,
                                             float* wts_lds = nullptr) {
-    if (E <= 512) route_token_t<8>(l, E, k, ids, wts, ids_lds, wts_lds);
-    else route_token_t<16>(l, E, k, ids, wts, ids_lds, wts_lds);
+    if (E <= 512) route_token_any<8, true>(l, E, k, ids, wts, ids_lds, wts_lds);
+    else route_token_any<16, true>(l, E, k, ids, wts, ids_lds, wts_lds);
 }
 // The ids alone, into LDS.
 __device__ __forceinline__ void route_token_ids(const float* __restrict__ l, int E, int k, int32_t* ids_lds) {
-    if (E <= 512) route_token_t<8, false>(l, E, k, nullptr, nullptr, ids_lds);
-    else route_token_t<16, false>(l, E, k, nullptr, nullptr, ids_lds);
+    if (E <= 512) route_token_any<8, false>(l, E, k, nullptr, nullptr, ids_lds, nullptr);
+    else route_token_any<16, false>(l, E, k, nullptr, nullptr, ids_lds, nullptr);
 }
 
 // The router-margin diagnostic (metal/src/forward.cpp:441-513), one wave per token: ex and S as route_token_t forms
@@ -1486,13 +1621,50 @@ __device__ __forceinline__ bool gu_route_wg(
         pre[j] = reinterpret_cast<const u32x4*>(ximg)[min(min(j, npre - 1) * 256 + tid, pieces - 1)];
     GuRouteLds& L = *reinterpret_cast<GuRouteLds*>(smem + kGuCols * qb * kImgDw + 4);
     const int P = T * k;
-    if (!shared_wg && wave < T) route_token_ids(logits + (size_t)wave * E, E, k, L.ids + wave * k);
+    // one token: wave 0 routes it and takes the item from the candidates (the y-th selected id in ascending order,
+    // its one pair at dispatch position y); L.item[7] = 1 when the fast selection declined (then the ids are in
+    // L.ids and the general path below finds the item)
+    const bool one = !shared_wg && T == 1 && k <= 64;
+    if (one && wave == 0) {
+        __shared__ uint2 s_cand1[64];
+        const FastRoute R = E <= 512 ? route_fast_t<8, false>(logits, E, k, s_cand1)
+                                     : route_fast_t<16, false>(logits, E, k, s_cand1);
+        const int lane = tid & 63;
+        if (R.ok) {
+            const bool sel = R.crank < k;
+            const unsigned long long sm = __ballot(sel);
+            const int yc = __builtin_amdgcn_mbcnt_hi((uint32_t)(sm >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)sm, 0u));
+            const unsigned long long own = __ballot(sel && yc == y - n_sh);
+            if (lane == 0) {
+                L.item[0] = own ? __builtin_amdgcn_readlane(R.cid, __builtin_ctzll(own)) : -1;
+                L.item[1] = y - n_sh;
+                L.item[2] = 1;
+                L.item[3] = L.item[4] = L.item[5] = L.item[6] = 0;
+                L.item[7] = 0;
+            }
+        } else {
+            if (E <= 512) route_token_t<8, false>(logits, E, k, nullptr, nullptr, L.ids);
+            else route_token_t<16, false>(logits, E, k, nullptr, nullptr, L.ids);
+            if (lane == 0) L.item[7] = 1;
+        }
+    } else if (!shared_wg && !one && wave < T) {
+        route_token_ids(logits + (size_t)wave * E, E, k, L.ids + wave * k);
+    }
 #pragma unroll
     for (int j = 0; j < 6; ++j)
         if (j * 256 + tid < pieces) reinterpret_cast<u32x4*>(smem)[j * 256 + tid] = pre[j];
     __syncthreads();
     Item item;
-    if (shared_wg) {
+    if (one && L.item[7] == 0) {
+        if (L.item[0] < 0) return false;  // uniform: no expert for this item
+        item.shared = false;
+        item.e = L.item[0];
+        item.first = L.item[1];
+        item.ncol = 1;
+        item.tok0 = 0;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) item.tk[c] = 0;
+    } else if (shared_wg) {
         item.shared = true;
         item.e = kItemShared;
         item.first = P;
@@ -1897,7 +2069,36 @@ __global__ __launch_bounds__(256) void k_q2_moe_small(
         }
     }
     if (tid < T) s_sg[tid] = sg[tid];
-    if (P <= 64) {
+    // one token: wave 0 routes it with weights; candidate c (ascending id), selected at rank r, is the token's pair r
+    // and the y-th touched expert (y = selected candidates below c), so its dispatch position is y
+    __shared__ int s_fast;
+    const bool one = T == 1 && k <= 64;
+    if (one) {
+        if (wave == 0) {
+            __shared__ uint2 s_cand1[64];
+            const FastRoute R = E <= 512 ? route_fast_t<8, true>(logits, E, k, s_cand1)
+                                         : route_fast_t<16, true>(logits, E, k, s_cand1);
+            if (R.ok) {
+                const bool sel = R.crank < k;
+                const unsigned long long sm = __ballot(sel);
+                const int yc = __builtin_amdgcn_mbcnt_hi((uint32_t)(sm >> 32),
+                                                         __builtin_amdgcn_mbcnt_lo((uint32_t)sm, 0u));
+                if (sel) {
+                    s_slot[R.crank] = yc;
+                    s_items[2 * (n_sh + yc)] = make_int4(R.cid, yc, 1, 0);
+                    s_items[2 * (n_sh + yc) + 1] = make_int4(0, 0, 0, 0);
+                }
+                if (lane < k) s_wts[lane] = R.sel_w;
+            }
+            if (lane == 0) {
+                s_fast = R.ok ? 1 : 0;
+                s_nt = k;
+            }
+        }
+        __syncthreads();
+    }
+    if (one && s_fast) {
+    } else if (P <= 64) {
         // the batch's routing (one wave per token: ids and weights, bitwise the writer's), then one wave derives the
         // dispatch and the item table by cross-lane counts, lane p holding pair p: its slot is the pairs with a
         // smaller expert id plus the earlier pairs with its own; an expert's item sits at its rank among the

@@ -21,6 +21,54 @@ __device__ __forceinline__ float xor_swap(float v) {
     return __int_as_float(xor_swap_i<O>(__float_as_int(v)));
 }
 
+// The value of lane ^ D (D a power of two below 64), by VALU lane moves only: quad permutes (1, 2), the half-row
+// mirror (lane ^ 7) then the quad reversal (lane ^ 3) for 4, the row rotation by 8 (within 16 lanes it is lane ^ 8),
+// and for 16 and 32 a permlane swap of the value with itself (the partner is the half the lane did not keep).
+template <int D>
+__device__ __forceinline__ uint32_t xor_lane(uint32_t v) {
+    const int i = (int)v;
+    if constexpr (D == 1) return (uint32_t)__builtin_amdgcn_mov_dpp(i, 0xB1, 0xF, 0xF, false);
+    else if constexpr (D == 2) return (uint32_t)__builtin_amdgcn_mov_dpp(i, 0x4E, 0xF, 0xF, false);
+    else if constexpr (D == 4)
+        return (uint32_t)__builtin_amdgcn_mov_dpp(__builtin_amdgcn_mov_dpp(i, 0x141, 0xF, 0xF, false), 0x1B, 0xF, 0xF,
+                                                  false);
+    else if constexpr (D == 8) return (uint32_t)__builtin_amdgcn_mov_dpp(i, 0x128, 0xF, 0xF, false);
+    else if constexpr (D == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(i, i, false, false);
+        return (uint32_t)((threadIdx.x & 16) ? r[0] : r[1]);
+    } else {
+        static_assert(D == 32, "xor_lane: D is a power of two below 64");
+        const auto r = __builtin_amdgcn_permlane32_swap(i, i, false, false);
+        return (uint32_t)((threadIdx.x & 32) ? r[0] : r[1]);
+    }
+}
+__device__ __forceinline__ uint32_t xor_lane_d(uint32_t v, int d) {  // d constant after unrolling
+    switch (d) {
+        case 1: return xor_lane<1>(v);
+        case 2: return xor_lane<2>(v);
+        case 4: return xor_lane<4>(v);
+        case 8: return xor_lane<8>(v);
+        case 16: return xor_lane<16>(v);
+        default: return xor_lane<32>(v);
+    }
+}
+
+// Bitonic sort of one value per lane over the wave, descending (lane 0 the largest): 21 compare-exchange stages on
+// the VALU, no scalar round trip.
+__device__ __forceinline__ uint32_t wave_sort_desc_u32(uint32_t v) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int size = 2; size <= 64; size <<= 1) {
+#pragma unroll
+        for (int d = size >> 1; d > 0; d >>= 1) {
+            const uint32_t p = xor_lane_d(v, d);
+            const bool take_max = ((lane & d) == 0) != ((lane & size) != 0);
+            v = take_max ? max(v, p) : min(v, p);
+        }
+    }
+    return v;
+}
+
 // Sum over groups of `lpr` consecutive lanes, distance lpr/2 first; every lane of a group ends with the sum.
 __device__ __forceinline__ float group_sum(float v, int lpr) {
     if (lpr >= 16) v = v + xor_swap<8>(v);
