@@ -15,6 +15,10 @@
  *   IQ2_S (ggml type 22): 82-byte blocks of 256 weights (include/strata/artifact/gguf_reader.hpp:197-200).
  *   A 3-D expert tensor holds expert e at e * rows * row_bytes (metal/src/layer_exec.cpp:115-120).
  *   q8_1 activations: 36-byte blocks {fp16 d; fp16 s; int8 q[32]} (metal/include/strata/metal/iq.hpp:42-43).
+ *   The other native types of real layers (the shared expert's projections, the down quants), GGUF's blocks:
+ *   Q8_0 (8, 34 B / 32), Q4_0 (2, 18 B / 32), Q5_0 (6, 22 B / 32), IQ4_NL (20, 18 B / 32), IQ4_XS (23, 136 B / 256),
+ *   Q3_K (11, 110 B / 256), Q4_K (12, 144 B / 256), Q5_K (13, 176 B / 256), Q6_K (14, 210 B / 256)
+ *   (include/strata/artifact/dequant.hpp:81-280).
  */
 #ifndef SMOE_H
 #define SMOE_H
@@ -37,6 +41,10 @@ typedef enum {
 } smoe_status;
 
 enum { SMOE_Q2_0 = 42, SMOE_IQ2_S = 22 };
+enum {
+    SMOE_Q8_0 = 8, SMOE_Q4_0 = 2, SMOE_Q5_0 = 6, SMOE_IQ4_NL = 20, SMOE_IQ4_XS = 23,
+    SMOE_Q3_K = 11, SMOE_Q4_K = 12, SMOE_Q5_K = 13, SMOE_Q6_K = 14
+};
 
 /* Which arithmetic contract runs the expert products. */
 enum {
@@ -58,10 +66,18 @@ typedef struct {
     int32_t n_expert;     /* E: 1..1024 (metal/src/router.mm:33-37) */
     int32_t top_k;        /* k: 1..64, k <= E */
     int32_t w_type;       /* routed experts: SMOE_Q2_0 or SMOE_IQ2_S */
-    int32_t sh_type;      /* shared expert: SMOE_Q2_0 / SMOE_IQ2_S, or -1 = no shared expert */
+    int32_t sh_type;      /* shared expert: its type (any type below), or -1 = no shared expert */
     int32_t router_dtype; /* 0 = bf16 (the repo's contract: include/strata/core/layer.hpp:131-136); 1 = f32 router
                              weights and f32 activations in the router (the literal benchmark configuration; the
                              shared gate stays bf16); SMOE_ROUTER_F32 */
+    /* The shared expert's gate, up and down projections in their own types (0: sh_type), as real layers store
+     * them (include/strata/kernels/shared_expert.hpp:54-58: NativeSharedWeights).  A shared expert whose three
+     * types all equal w_type runs inside the expert kernels; any other one (a "native" shared expert: Q2_0, IQ2_S
+     * or the SMOE_Q8_0 .. SMOE_Q6_K types, each projection its own) runs the q8_1 GEMV contract on every path
+     * (x as q8_1 blocks, the types' integer dots in the reference's 32-lane order, SwiGLU + q8_1, down times
+     * sigmoid(gate_inp_shexp . x)).  n_ff_shared % 32 == 0; each projection's row length a whole number of its
+     * blocks (Q2_0: 128 * 2^a * b, b <= 8; IQ2_S: 512, 1024 or 2048); n_ff_shared at most 4096. */
+    int32_t sh_gate_type, sh_up_type, sh_down_type;
 } smoe_geom;
 
 /* One layer's tensors, all resident in device memory (4-byte aligned). */
@@ -226,7 +242,9 @@ smoe_status smoe_bf16_gemv(const uint16_t* x, const uint16_t* w, float* y, int32
 smoe_status smoe_quantize_q8_1(const float* x, int64_t n, uint8_t* y, void* hip_stream);
 
 /* y[c * n_out + r] = W[r] . x[c] for n_col q8_1 columns; W is n_out rows of n_in values of `type`, the first
- * at `w + byte_off`.  Replaces iq_mmvq (metal/include/strata/metal/iq.hpp:50-51). */
+ * at `w + byte_off`.  Types: Q2_0, IQ2_S, and SMOE_Q8_0 .. SMOE_Q6_K (n_in a multiple of the type's block: 32 or
+ * 256; w + byte_off 4-byte aligned).  Replaces iq_mmvq (metal/include/strata/metal/iq.hpp:50-51; its per-type
+ * dots metal/shaders/iq.metal:224-513). */
 smoe_status smoe_mmvq(int32_t type, const void* w, int64_t byte_off, const uint8_t* x_q8, int32_t n_in,
                       int32_t n_out, int32_t n_col, float* y, void* hip_stream);
 

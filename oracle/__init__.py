@@ -101,6 +101,12 @@ def _set_sigs(L):
         "or_hc_read_ref": (i32, [vp, i32, i32, i32, i32, f32, vp, vp, vp, vp, i32, vp, vp]),
         "or_hc_write_dev": (None, [vp, vp, vp, i32, i32, i32, vp]),
         "or_row_bytes": (i64, [i32, i64]),
+        "or_native_type": (i32, [i32]),
+        "or_native_row_bytes": (i64, [i32, i64]),
+        "or_native_dequant": (i32, [i32, vp, i64, vp]),
+        "or_native_part": (f32, [i32, vp, vp, i32]),
+        "or_native_gemv": (i32, [i32, vp, vp, i32, i32, i32, vp]),
+        "or_native_gemv_double": (i32, [i32, vp, vp, i32, i32, i32, vp]),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(L, name)
@@ -129,6 +135,8 @@ def ref():
         R.ref_f32_from_f16_all.argtypes = [C.c_void_p]
         R.ref_iq2s_grid.restype = None
         R.ref_iq2s_grid.argtypes = [C.c_void_p]
+        R.ref_dequantize.restype = C.c_int
+        R.ref_dequantize.argtypes = [C.c_int, C.c_void_p, C.c_int64, C.c_void_p]
         _REF = R
     return _REF
 
@@ -190,12 +198,68 @@ def gen_iq2_s(seed: int, stream: int, n_blocks: int, sigma: float = 0.02) -> np.
     return y
 
 
+# The other native GGUF types: (values per block, bytes per block, fp16 scale fields, scale divisor) -- the divisor
+# keeps the dequantised weights near sigma (a block value is d times a code of this size).
+Q8_0, Q4_0, Q5_0, IQ4_NL, IQ4_XS, Q3_K, Q4_K, Q5_K, Q6_K = 8, 2, 6, 20, 23, 11, 12, 13, 14
+NATIVE = {Q8_0: (32, 34, (0,), 64.0), Q4_0: (32, 18, (0,), 8.0), Q5_0: (32, 22, (0,), 16.0),
+          IQ4_NL: (32, 18, (0,), 64.0), IQ4_XS: (256, 136, (0,), 2000.0), Q3_K: (256, 110, (108,), 100.0),
+          Q4_K: (256, 144, (0, 2), 500.0), Q5_K: (256, 176, (0, 2), 500.0), Q6_K: (256, 210, (208,), 2000.0)}
+
+
+def gen_native_blocks(wtype: int, seed: int, stream: int, n_values: int, sigma: float = 0.02) -> np.ndarray:
+    """Random blocks of a native type: uniform code and scale bytes, fp16 scale fields RNE-fp16 of
+    |N(0, sigma / divisor)| (no inf or NaN scales).  numpy's PCG64 seeded from (seed, stream)."""
+    qk, nb, fields, div = NATIVE[wtype]
+    assert n_values % qk == 0
+    n_blocks = n_values // qk
+    rng = np.random.Generator(np.random.PCG64([seed, stream, wtype]))
+    b = rng.integers(0, 256, size=(n_blocks, nb), dtype=np.uint8)
+    for f in fields:
+        d = f16_from_f32(np.abs(rng.normal(0.0, sigma / div, n_blocks)).astype(np.float32))
+        b[:, f:f + 2] = d.view(np.uint8).reshape(n_blocks, 2)
+    return b.ravel()
+
+
 def gen_blocks(wtype: int, seed: int, stream: int, n_values: int, sigma: float = 0.02) -> np.ndarray:
     if wtype == Q2_0:
         return gen_q2_0(seed, stream, n_values // 64, sigma)
     if wtype == IQ2_S:
         return gen_iq2_s(seed, stream, n_values // 256, sigma)
+    if wtype in NATIVE:
+        return gen_native_blocks(wtype, seed, stream, n_values, sigma)
     raise ValueError(wtype)
+
+
+def native_row_bytes(wtype: int, n: int) -> int:
+    return int(lib().or_native_row_bytes(wtype, n))
+
+
+def native_dequant(wtype: int, blocks: np.ndarray, n_values: int) -> np.ndarray:
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+    y = np.empty(n_values, np.float32)
+    assert lib().or_native_dequant(wtype, _p(blocks), n_values, _p(y)) == 0
+    return y
+
+
+def ref_dequantize(wtype: int, blocks: np.ndarray, n_values: int) -> Optional[np.ndarray]:
+    """The reference's own dequantiser (oracle/_ref), or None when that build is absent."""
+    R = ref()
+    if R is None:
+        return None
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+    y = np.empty(n_values, np.float32)
+    assert R.ref_dequantize(wtype, _p(blocks), n_values, _p(y)) == 0
+    return y
+
+
+def native_gemv(wtype: int, w, xq, n_in: int, n_out: int, n_col: int = 1, double: bool = False) -> np.ndarray:
+    """y[c][r] for n_col q8_1 columns: the 32-lane MMVQ order (or, with double, the dequantised double sums)."""
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    xq = np.ascontiguousarray(xq, dtype=np.uint8)
+    y = np.empty((n_col, n_out), np.float32)
+    fn = lib().or_native_gemv_double if double else lib().or_native_gemv
+    assert fn(wtype, _p(w), _p(xq), n_in, n_out, n_col, _p(y)) == 0
+    return y
 
 
 # ------------------------------------------------------------------------------------------------ kernels
@@ -374,7 +438,7 @@ def dispatch(ids, n_expert):
 
 class _Geom(C.Structure):
     _fields_ = [(n, C.c_int32) for n in ("n_embd", "n_ff", "n_ff_shared", "n_expert", "top_k", "w_type", "sh_type",
-                                         "router_dtype")]
+                                         "router_dtype", "sh_gate_type", "sh_up_type", "sh_down_type")]
 
 
 class _Weights(C.Structure):
@@ -397,10 +461,17 @@ class Geom:
     w_type: int = Q2_0
     sh_type: int = Q2_0
     router_dtype: int = 0
+    sh_gate_type: int = 0  # the shared expert's projections in their own native types (0: sh_type)
+    sh_up_type: int = 0
+    sh_down_type: int = 0
 
     def c(self):
         return _Geom(self.n_embd, self.n_ff, self.n_ff_shared, self.n_expert, self.top_k, self.w_type, self.sh_type,
-                     self.router_dtype)
+                     self.router_dtype, self.sh_gate_type, self.sh_up_type, self.sh_down_type)
+
+    def shared_types(self):
+        """(gate, up, down) types of the shared expert."""
+        return tuple(t if t else self.sh_type for t in (self.sh_gate_type, self.sh_up_type, self.sh_down_type))
 
 
 @dataclass
@@ -436,9 +507,10 @@ def make_weights(g: Geom, seed: int, n_expert_alloc: Optional[int] = None, zipf_
     router = gen_normal(seed, 4, E * H, sigma) if g.router_dtype == 1 else gen_bf16(seed, 4, E * H, sigma)
     w = Weights(gate, up, down, router)
     if g.sh_type >= 0:
-        w.gate_sh = gen_blocks(g.sh_type, seed, 5, Fs * H, sigma)
-        w.up_sh = gen_blocks(g.sh_type, seed, 6, Fs * H, sigma)
-        w.down_sh = gen_blocks(g.sh_type, seed, 7, H * Fs, sigma)
+        tg, tu, td = g.shared_types()
+        w.gate_sh = gen_blocks(tg, seed, 5, Fs * H, sigma)
+        w.up_sh = gen_blocks(tu, seed, 6, Fs * H, sigma)
+        w.down_sh = gen_blocks(td, seed, 7, H * Fs, sigma)
         w.gate_inp_sh = gen_bf16(seed, 8, H, sigma)
     if zipf_bias is not None:
         w.logit_bias = np.ascontiguousarray(zipf_bias, dtype=np.float32)

@@ -4,6 +4,8 @@
 //   include/strata/kernels/f16_bits.hpp:37-101   f16_from_f32 / f32_from_f16
 //   include/strata/kernels/bf16_bits.hpp:37-59   bf16_from_f32 / f32_from_bf16
 //   include/strata/artifact/dequant.hpp:69-78    dequantize_q2_0
+//   include/strata/artifact/dequant.hpp:81-280   the other native types (Q8_0, Q4_0, Q5_0, IQ4_NL, Q6_K, Q4_K,
+//                                                Q5_K, Q3_K, IQ4_XS)
 //   metal/include/strata/metal/iq_grids.hpp:5    iq2s_grid
 #include "strata/artifact/dequant.hpp"
 #include "strata/kernels/bf16_bits.hpp"
@@ -29,6 +31,26 @@ void ref_f32_from_f16_all(float* out65536) {
 }
 void ref_dequantize_q2_0(const uint8_t* blocks, int64_t n_blocks, float* out) {
     for (int64_t b = 0; b < n_blocks; ++b) strata::dequantize_q2_0(blocks + b * 18, out + b * 64);
+}
+// n_values of ggml `type` from its blocks; returns -1 for a type the reference does not dequantise here
+int ref_dequantize(int type, const uint8_t* blocks, int64_t n_values, float* out) {
+    int qk = 0, bytes = 0;
+    void (*fn)(const uint8_t*, float*) = nullptr;
+    switch (type) {
+        case 8: qk = 32; bytes = 34; fn = strata::dequantize_q8_0; break;
+        case 2: qk = 32; bytes = 18; fn = strata::dequantize_q4_0; break;
+        case 6: qk = 32; bytes = 22; fn = strata::dequantize_q5_0; break;
+        case 20: qk = 32; bytes = 18; fn = strata::dequantize_iq4_nl; break;
+        case 23: qk = 256; bytes = 136; fn = strata::dequantize_iq4_xs; break;
+        case 11: qk = 256; bytes = 110; fn = strata::dequantize_q3_K; break;
+        case 12: qk = 256; bytes = 144; fn = strata::dequantize_q4_K; break;
+        case 13: qk = 256; bytes = 176; fn = strata::dequantize_q5_K; break;
+        case 14: qk = 256; bytes = 210; fn = strata::dequantize_q6_K; break;
+        default: return -1;
+    }
+    if (n_values % qk) return -1;
+    for (int64_t b = 0; b < n_values / qk; ++b) fn(blocks + b * bytes, out + b * qk);
+    return 0;
 }
 void ref_iq2s_grid(uint64_t* out1024) { std::memcpy(out1024, strata::metal::iq2s_grid, sizeof(strata::metal::iq2s_grid)); }
 }

@@ -494,11 +494,13 @@ void or_iq2_s_gemv_ref(const uint8_t* w, const uint8_t* xq, int n_in, int n_out,
 }
 
 static void gemv_dev(int type, const uint8_t* w, const uint8_t* xq, int n_in, int n_out, float* y) {
-    if (type == 22) or_iq2_s_gemv_dev(w, xq, n_in, n_out, y);
+    if (or_native_type(type)) or_native_gemv(type, w, xq, n_in, n_out, 1, y);
+    else if (type == 22) or_iq2_s_gemv_dev(w, xq, n_in, n_out, y);
     else or_q2_0_gemv_dev(w, xq, n_in, n_out, y);
 }
 static void gemv_ref(int type, const uint8_t* w, const uint8_t* xq, int n_in, int n_out, float* y) {
-    if (type == 22) or_iq2_s_gemv_ref(w, xq, n_in, n_out, y);
+    if (or_native_type(type)) or_native_gemv(type, w, xq, n_in, n_out, 1, y);
+    else if (type == 22) or_iq2_s_gemv_ref(w, xq, n_in, n_out, y);
     else or_q2_0_gemv_ref(w, xq, n_in, n_out, y);
 }
 
@@ -819,14 +821,55 @@ void or_dispatch(const int32_t* ids, int n_tok, int k, int n_expert, int32_t* co
  * bf16 router product, top-k, q8_1 of x, for each selected expert gate/up, SwiGLU + q8_1, down; the
  * shared expert (gate/up/SwiGLU/down, times sigmoid of the bf16 gate_inp_shexp dot); the combine. */
 
+/* the shared expert's projection types (0 in the geometry: sh_type); `native` when any differs from the routed type */
+static int sh_gate_t(const or_geom* g) { return g->sh_gate_type ? g->sh_gate_type : g->sh_type; }
+static int sh_up_t(const or_geom* g) { return g->sh_up_type ? g->sh_up_type : g->sh_type; }
+static int sh_down_t(const or_geom* g) { return g->sh_down_type ? g->sh_down_type : g->sh_type; }
+static int sh_native(const or_geom* g) {
+    return g->sh_type >= 0 && (sh_gate_t(g) != g->w_type || sh_up_t(g) != g->w_type || sh_down_t(g) != g->w_type);
+}
+static int64_t any_row_bytes(int type, int64_t n) {
+    return or_native_type(type) ? or_native_row_bytes(type, n) : or_row_bytes(type, n);
+}
+
 static int geom_ok(const or_geom* g) {
     if (g->n_embd <= 0 || g->n_ff <= 0 || g->n_expert <= 0 || g->top_k <= 0 || g->top_k > g->n_expert) return 0;
     if (g->router_dtype != 0 && g->router_dtype != 1) return 0;
     if (g->router_dtype == 1 && g->n_embd % 4) return 0;
     if (or_row_bytes(g->w_type, g->n_embd) <= 0 || or_row_bytes(g->w_type, g->n_ff) <= 0) return 0;
-    if (g->sh_type >= 0 && (or_row_bytes(g->sh_type, g->n_embd) <= 0 || or_row_bytes(g->sh_type, g->n_ff_shared) <= 0))
+    if (g->sh_type >= 0 && (any_row_bytes(sh_gate_t(g), g->n_embd) <= 0 || any_row_bytes(sh_up_t(g), g->n_embd) <= 0 ||
+                            any_row_bytes(sh_down_t(g), g->n_ff_shared) <= 0 || g->n_ff_shared % 32))
         return 0;
     return 1;
+}
+
+/* The shared expert on the q8_1 contract with each projection in its own type: gate, up, SwiGLU + q8_1, down. */
+static void shared_chain(const or_geom* g, const or_weights* w, const uint8_t* xq, float* out, int dev) {
+    const int H = g->n_embd, F = g->n_ff_shared;
+    float* gate = (float*)malloc(sizeof(float) * (size_t)F);
+    float* up = (float*)malloc(sizeof(float) * (size_t)F);
+    uint8_t* hq = (uint8_t*)malloc((size_t)F / 32 * 36);
+    if (dev) {
+        gemv_dev(sh_gate_t(g), w->gate_sh, xq, H, F, gate);
+        gemv_dev(sh_up_t(g), w->up_sh, xq, H, F, up);
+        or_swiglu_q8(gate, up, F, hq);
+        gemv_dev(sh_down_t(g), w->down_sh, hq, F, H, out);
+    } else {
+        gemv_ref(sh_gate_t(g), w->gate_sh, xq, H, F, gate);
+        gemv_ref(sh_up_t(g), w->up_sh, xq, H, F, up);
+        float h[32];
+        for (int b = 0; b < F / 32; ++b) {
+            for (int i = 0; i < 32; ++i) {
+                const float gv = gate[b * 32 + i];
+                h[i] = (gv / (1.0f + expf(-gv))) * up[b * 32 + i];
+            }
+            quant_block(h, hq + (size_t)b * 36);
+        }
+        gemv_ref(sh_down_t(g), w->down_sh, hq, F, H, out);
+    }
+    free(gate);
+    free(up);
+    free(hq);
 }
 
 static void expert_chain(int type, const uint8_t* gw, const uint8_t* uw, const uint8_t* dw, int H, int F,
@@ -929,7 +972,8 @@ static int moe_decode(const or_geom* g, const or_weights* w, const float* x, int
         } else {
             const int t = job - T * K;
             float* sh = shared + (size_t)t * H;
-            expert_chain(g->sh_type, w->gate_sh, w->up_sh, w->down_sh, H, Fs, xq + t * xqb, sh, NULL, dev);
+            if (sh_native(g)) shared_chain(g, w, xq + t * xqb, sh, dev);
+            else expert_chain(g->sh_type, w->gate_sh, w->up_sh, w->down_sh, H, Fs, xq + t * xqb, sh, NULL, dev);
             const float sig = dev ? or_sigmoid(sg[t]) : 1.0f / (1.0f + expf(-sg[t]));
             for (int j = 0; j < H; ++j) sh[j] = sh[j] * sig;
         }
@@ -1002,7 +1046,7 @@ static void q2_rows_bf16act(const uint8_t* w, const float* a /* bf16-valued */, 
 int or_moe_prefill(const or_geom* g, const or_weights* w, const float* x, int T, float* y, int add_shared,
                    const or_trace* tr, int n_threads) {
     if (!geom_ok(g) || T < 0) return -1;
-    if (g->w_type != 42 || (g->sh_type >= 0 && g->sh_type != 42)) return -2;
+    if (g->w_type != 42 || (g->sh_type >= 0 && g->sh_type != 42 && !sh_native(g))) return -2;
     if (T == 0) return 0;
     const int H = g->n_embd, F = g->n_ff, Fs = g->n_ff_shared, E = g->n_expert, K = g->top_k;
     const int64_t grow = or_row_bytes(42, H), drow = or_row_bytes(42, F);
@@ -1041,6 +1085,16 @@ int or_moe_prefill(const or_geom* g, const or_weights* w, const float* x, int T,
         const int t = is_sh ? job - T * K : job / K;
         const int Fj = is_sh ? Fs : F;
         const uint8_t *gw, *uw, *dw;
+        if (is_sh && sh_native(g)) {
+            uint8_t* xq = (uint8_t*)malloc((size_t)H / 32 * 36);
+            or_quant_q8_1(x + (size_t)t * H, H, xq);
+            float* out = shared + (size_t)t * H;
+            shared_chain(g, w, xq, out, 1);
+            const float sig = or_sigmoid(sg[t]);
+            for (int j = 0; j < H; ++j) out[j] = out[j] * sig;
+            free(xq);
+            continue;
+        }
         if (is_sh) {
             gw = w->gate_sh; uw = w->up_sh; dw = w->down_sh;
         } else {

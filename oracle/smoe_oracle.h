@@ -87,6 +87,15 @@ void or_residual_rmsnorm_dev(const float* x, const float* r, int n_rows, int n, 
 void or_combine_dev(const float* parts, const float* w, const float* shared, int n_embd, int k, float* y);
 void or_combine_double(const float* parts, const float* w, const float* shared, int n_embd, int k, float* y);
 
+/* ---- the other native GGUF types (oracle/smoe_native.c): 8 Q8_0, 2 Q4_0, 6 Q5_0, 20 IQ4_NL, 23 IQ4_XS,
+ * 11 Q3_K, 12 Q4_K, 13 Q5_K, 14 Q6_K */
+int or_native_type(int type);
+int64_t or_native_row_bytes(int type, int64_t n); /* -1: not a native type or n not a whole number of blocks */
+int or_native_dequant(int type, const uint8_t* blocks, int64_t n_values, float* out);
+float or_native_part(int type, const uint8_t* blk, const uint8_t* x0, int iqs);
+int or_native_gemv(int type, const uint8_t* w, const uint8_t* xq, int n_in, int n_out, int n_col, float* y);
+int or_native_gemv_double(int type, const uint8_t* w, const uint8_t* xq, int n_in, int n_out, int n_col, float* y);
+
 /* ---- A10: canonical dispatch */
 void or_dispatch(const int32_t* ids, int n_tok, int k, int n_expert, int32_t* counts, int32_t* offsets,
                  int32_t* perm, int32_t* slot);
@@ -97,6 +106,9 @@ typedef struct {
     int32_t w_type;  /* 42 = Q2_0, 22 = IQ2_S (routed experts) */
     int32_t sh_type; /* 42 / 22, or -1 = no shared expert */
     int32_t router_dtype;
+    /* the shared expert's projections in their own native types (0: sh_type); any type other than the routed one
+     * makes the shared expert a native one, run on the q8_1 GEMV contract of smoe_native.c in both paths */
+    int32_t sh_gate_type, sh_up_type, sh_down_type;
 } or_geom;
 
 typedef struct {

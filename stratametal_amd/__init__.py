@@ -39,7 +39,7 @@ class SmoeError(RuntimeError):
 
 class _Geom(C.Structure):
     _fields_ = [(n, C.c_int32) for n in ("n_embd", "n_ff", "n_ff_shared", "n_expert", "top_k", "w_type", "sh_type",
-                                         "router_dtype")]
+                                         "router_dtype", "sh_gate_type", "sh_up_type", "sh_down_type")]
 
 
 class _Weights(C.Structure):
@@ -141,11 +141,20 @@ def _stream(stream=None) -> int:
     return s.cuda_stream
 
 
+# the other native GGUF types (smoe.h): type -> (values per block, bytes per block)
+Q8_0, Q4_0, Q5_0, IQ4_NL, IQ4_XS, Q3_K, Q4_K, Q5_K, Q6_K = 8, 2, 6, 20, 23, 11, 12, 13, 14
+NATIVE_BLOCKS = {Q8_0: (32, 34), Q4_0: (32, 18), Q5_0: (32, 22), IQ4_NL: (32, 18), IQ4_XS: (256, 136),
+                 Q3_K: (256, 110), Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210)}
+
+
 def row_bytes(wtype: int, n: int) -> int:
     if wtype == Q2_0:
         return n // 64 * 18
     if wtype == IQ2_S:
         return n // 256 * 82
+    if wtype in NATIVE_BLOCKS:
+        qk, nb = NATIVE_BLOCKS[wtype]
+        return n // qk * nb
     raise ValueError(wtype)
 
 
@@ -160,10 +169,18 @@ class Geom:
     w_type: int = Q2_0
     sh_type: int = Q2_0
     router_dtype: int = 0
+    # the shared expert's gate, up and down projections in their own native types (0: sh_type)
+    sh_gate_type: int = 0
+    sh_up_type: int = 0
+    sh_down_type: int = 0
 
     def c(self) -> _Geom:
         return _Geom(self.n_embd, self.n_ff, self.n_ff_shared, self.n_expert, self.top_k, self.w_type, self.sh_type,
-                     self.router_dtype)
+                     self.router_dtype, self.sh_gate_type, self.sh_up_type, self.sh_down_type)
+
+    def shared_types(self):
+        """(gate, up, down) types of the shared expert."""
+        return tuple(t if t else self.sh_type for t in (self.sh_gate_type, self.sh_up_type, self.sh_down_type))
 
     def expert_bytes(self) -> int:
         return 2 * self.n_ff * row_bytes(self.w_type, self.n_embd) + self.n_embd * row_bytes(self.w_type, self.n_ff)
@@ -171,8 +188,9 @@ class Geom:
     def shared_bytes(self) -> int:
         if self.sh_type < 0:
             return 0
-        return (2 * self.n_ff_shared * row_bytes(self.sh_type, self.n_embd)
-                + self.n_embd * row_bytes(self.sh_type, self.n_ff_shared))
+        tg, tu, td = self.shared_types()
+        return (self.n_ff_shared * (row_bytes(tg, self.n_embd) + row_bytes(tu, self.n_embd))
+                + self.n_embd * row_bytes(td, self.n_ff_shared))
 
 
 def workspace_bytes(g: Geom, max_tokens: int) -> int:
@@ -213,8 +231,11 @@ def synth_layer(g: Geom, seed: int, device="cuda", sigma: float = 0.02, logit_bi
     w = dict(gate_exps=blocks(g.w_type, 1, E * F * H), up_exps=blocks(g.w_type, 2, E * F * H),
              down_exps=blocks(g.w_type, 3, E * H * F), router=router)
     if g.sh_type >= 0:
-        w.update(gate_sh=blocks(g.sh_type, 5, Fs * H), up_sh=blocks(g.sh_type, 6, Fs * H),
-                 down_sh=blocks(g.sh_type, 7, H * Fs), gate_inp_sh=bf16(8, H))
+        if any(t not in (Q2_0, IQ2_S) for t in g.shared_types()):
+            raise ValueError("synth_layer generates Q2_0 and IQ2_S blocks only; upload other native types' blocks")
+        tg, tu, td = g.shared_types()
+        w.update(gate_sh=blocks(tg, 5, Fs * H), up_sh=blocks(tu, 6, Fs * H),
+                 down_sh=blocks(td, 7, H * Fs), gate_inp_sh=bf16(8, H))
     if logit_bias is not None:
         w["logit_bias"] = logit_bias
     return w
@@ -514,7 +535,7 @@ def quantize_q8_1(x, stream=None):
 
 def mmvq(wtype: int, w, x_q8, n_in: int, n_out: int, n_col: int = 1, byte_off: int = 0, stream=None):
     import torch
-    _need(w, "w", torch.uint8, numel=byte_off + n_out * row_bytes(wtype, n_in) if wtype in (Q2_0, IQ2_S) else None)
+    _need(w, "w", torch.uint8, numel=byte_off + n_out * row_bytes(wtype, n_in))
     _need(x_q8, "x_q8", torch.uint8, numel=n_col * (n_in // 32) * 36)
     y = torch.empty((n_col, n_out), dtype=torch.float32, device=w.device)
     _check(lib().smoe_mmvq(wtype, w.data_ptr(), byte_off, x_q8.data_ptr(), n_in, n_out, n_col, y.data_ptr(),

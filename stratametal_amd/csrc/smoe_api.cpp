@@ -34,6 +34,17 @@ bool aligned(const void* p, size_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
 
 int row_values(int type) { return type == SMOE_Q2_0 ? 128 : type == SMOE_IQ2_S ? 256 : 0; }
 
+// The shared expert's projection types (0 in the geometry: sh_type).  A shared expert whose three types equal the
+// routed type runs inside the expert kernels ("fused"); any other runs the q8_1 GEMV chain ("native").
+int sh_gate_t(const smoe_geom& g) { return g.sh_gate_type ? g.sh_gate_type : g.sh_type; }
+int sh_up_t(const smoe_geom& g) { return g.sh_up_type ? g.sh_up_type : g.sh_type; }
+int sh_down_t(const smoe_geom& g) { return g.sh_down_type ? g.sh_down_type : g.sh_type; }
+bool sh_native(const smoe_geom& g) {
+    return g.sh_type >= 0 && (sh_gate_t(g) != g.w_type || sh_up_t(g) != g.w_type || sh_down_t(g) != g.w_type);
+}
+bool sh_fused(const smoe_geom& g) { return g.sh_type >= 0 && !sh_native(g); }
+bool gemv_type(int t) { return t == SMOE_Q2_0 || t == SMOE_IQ2_S || smoe::native_type(t); }
+
 // GEMV-path tiling limits: a row of n_embd is at most 32 double blocks (4096 values).
 constexpr int kMaxEmbd = 4096;
 constexpr int kMaxFF = 4096;
@@ -54,10 +65,11 @@ smoe_status check_geom(const smoe_geom* g) {
     if (!g) return fail(SMOE_ENULL, "geometry is NULL");
     if (g->w_type != SMOE_Q2_0 && g->w_type != SMOE_IQ2_S)
         return fail(SMOE_ETYPE, "routed expert type " + std::to_string(g->w_type) + " is not Q2_0 (42) or IQ2_S (22)");
-    if (g->sh_type != -1 && g->sh_type != SMOE_Q2_0 && g->sh_type != SMOE_IQ2_S)
-        return fail(SMOE_ETYPE, "shared expert type " + std::to_string(g->sh_type) + " is not Q2_0, IQ2_S or -1");
-    if (g->sh_type >= 0 && g->sh_type != g->w_type)
-        return fail(SMOE_ETYPE, "the shared expert's type must equal the routed experts' type (one activation layout)");
+    if (g->sh_type != -1 && !gemv_type(g->sh_type))
+        return fail(SMOE_ETYPE, "shared expert type " + std::to_string(g->sh_type) + " is not a supported type or -1");
+    for (const int t : {g->sh_gate_type, g->sh_up_type, g->sh_down_type})
+        if (t != 0 && !gemv_type(t))
+            return fail(SMOE_ETYPE, "shared projection type " + std::to_string(t) + " is not a supported type");
     if (g->router_dtype != SMOE_ROUTER_BF16 && g->router_dtype != SMOE_ROUTER_F32)
         return fail(SMOE_EINVAL, "router_dtype must be 0 (bf16) or 1 (f32)");
     if (g->n_expert < 1 || g->n_expert > kMaxExpert) return fail(SMOE_EINVAL, "n_expert must be in 1..1024");
@@ -68,9 +80,24 @@ smoe_status check_geom(const smoe_geom* g) {
         return fail(SMOE_EINVAL, "n_embd must be a positive multiple of " + std::to_string(rv) + ", at most 4096");
     if (g->n_ff <= 0 || g->n_ff % rv || g->n_ff > kMaxFF)
         return fail(SMOE_EINVAL, "n_ff must be a positive multiple of " + std::to_string(rv) + ", at most 4096");
-    const bool has_sh = g->sh_type >= 0;
+    const bool has_sh = sh_fused(*g), nat = sh_native(*g);
     if (has_sh && (g->n_ff_shared <= 0 || g->n_ff_shared % rv || g->n_ff_shared > kMaxFF))
         return fail(SMOE_EINVAL, "n_ff_shared must be a positive multiple of " + std::to_string(rv) + ", at most 4096");
+    if (nat) {  // each projection's rows a whole number of its blocks, in a shape its GEMV tiles
+        const int Fs = g->n_ff_shared;
+        if (Fs <= 0 || Fs % 32 || Fs > kMaxFF)
+            return fail(SMOE_EINVAL, "a native shared expert's n_ff_shared must be a positive multiple of 32, at most 4096");
+        const struct { int type, n; const char* what; } proj[3] = {
+            {sh_gate_t(*g), g->n_embd, "gate"}, {sh_up_t(*g), g->n_embd, "up"}, {sh_down_t(*g), Fs, "down"}};
+        for (const auto& p : proj) {
+            const bool ok = p.type == SMOE_Q2_0    ? (p.n % 128 == 0 && p.n <= kMaxFF && smoe::gemv_shape_ok(p.n))
+                            : p.type == SMOE_IQ2_S ? smoe::iq2_shape_ok(p.n)
+                                                   : smoe::native_row_bytes(p.type, p.n) > 0;
+            if (!ok)
+                return fail(SMOE_EINVAL, std::string("shared ") + p.what + " rows of " + std::to_string(p.n) +
+                                             " values do not fit type " + std::to_string(p.type) + "'s blocks");
+        }
+    }
     if (g->w_type == SMOE_Q2_0) {
         if (!smoe::gemv_shape_ok(g->n_embd) || !smoe::gemv_shape_ok(g->n_ff))
             return fail(SMOE_EINVAL, "n_embd / 128 and n_ff / 128 must each be a power of two times at most 8");
@@ -87,7 +114,7 @@ smoe_status check_geom(const smoe_geom* g) {
 
 struct Layout {
     size_t ximg, xbf, logits, sg, ids, wts, counts, offsets, perm, slot, elist, nlist, items, himg, Y, dwork, xchg,
-        oflags, total;
+        oflags, nxq, ngu, nhq, total;
     int h_blocks;  // q8_1 blocks per h row (GEMV path)
     int h_rec;     // 64-value records per h row (MFMA path)
     int64_t n_xflags, n_hflags;  // the MFMA path's per-work-group overflow flags (a trace asking for the mask)
@@ -97,18 +124,18 @@ struct Layout {
 // an expert's pairs and the shared tokens into chunks of mfma_chunk() columns.
 int max_items_gemv(const smoe_geom& g, int64_t T) {
     const int64_t P = T * g.top_k;
-    return (int)((P < g.n_expert ? P : g.n_expert) + (g.sh_type >= 0 ? smoe::shared_items((int)T) : 0));
+    return (int)((P < g.n_expert ? P : g.n_expert) + (sh_fused(g) ? smoe::shared_items((int)T) : 0));
 }
 int max_items_mfma(const smoe_geom& g, int64_t T) {
     const int64_t P = T * g.top_k, C = smoe::mfma_chunk();
-    return (int)((P < g.n_expert ? P : g.n_expert) + P / C + (g.sh_type >= 0 ? (T + C - 1) / C : 0));
+    return (int)((P < g.n_expert ? P : g.n_expert) + P / C + (sh_fused(g) ? (T + C - 1) / C : 0));
 }
 
 Layout layout(const smoe_geom& g, int64_t T) {
     Layout L{};
     const int64_t H = g.n_embd, E = g.n_expert, K = g.top_k;
     const int64_t P = T * K;
-    const int64_t Fmax = (g.sh_type >= 0 && g.n_ff_shared > g.n_ff) ? g.n_ff_shared : g.n_ff;
+    const int64_t Fmax = (sh_fused(g) && g.n_ff_shared > g.n_ff) ? g.n_ff_shared : g.n_ff;
     L.h_blocks = (int)(Fmax / 32);
     L.h_rec = (int)(Fmax / 64);
     size_t o = 0;
@@ -142,6 +169,12 @@ Layout layout(const smoe_geom& g, int64_t T) {
     L.n_xflags = most(smoe::act_records_blocks(T * (H / 64)), T);
     L.n_hflags = (Fmax / 128) * (int64_t)max_items_mfma(g, T);
     L.oflags = take((size_t)(L.n_xflags + L.n_hflags) * 4);
+    if (sh_native(g)) {  // the native shared expert's chain: x as q8_1 blocks, gate and up rows, q8_1 of h
+        const int64_t Fs = g.n_ff_shared;
+        L.nxq = take((size_t)T * (H / 32) * 36);
+        L.ngu = take((size_t)2 * T * Fs * 4);
+        L.nhq = take((size_t)T * (Fs / 32) * 36);
+    }
     L.total = o;
     return L;
 }
@@ -178,7 +211,7 @@ const char* smoe_status_str(smoe_status s) {
 
 const char* smoe_last_error(void) { return g_last.c_str(); }
 
-int32_t smoe_abi_version(void) { return 106; }
+int32_t smoe_abi_version(void) { return 107; }
 
 size_t smoe_workspace_bytes(const smoe_geom* g, int32_t max_tokens) {
     if (check_geom(g) != SMOE_OK || max_tokens < 0) return 0;
@@ -254,14 +287,16 @@ smoe_status forward_impl(const smoe_geom* g, const smoe_weights* w, float* x_io,
     const float* x = x_io;
     smoe_status s = check_forward(g, w, x, n_tokens, y, workspace, workspace_bytes, path, x_prev, r_prev);
     if (s != SMOE_OK || n_tokens == 0) return s == SMOE_OK ? ok() : s;
-    const bool has_sh = g->sh_type >= 0;
+    const bool has_sh = g->sh_type >= 0;  // the router's shared gate row
+    const bool nat = sh_native(*g);         // the shared expert as its own q8_1 GEMV chain, into Y's shared rows
+    const bool shf = has_sh && !nat;        // the shared expert inside the expert kernels
     const bool iq2 = g->w_type == SMOE_IQ2_S;
     const bool mfma = !iq2 && (path == SMOE_PATH_MFMA || (path == SMOE_PATH_AUTO && n_tokens >= kMfmaTokens));
     const Layout L = layout(*g, n_tokens);
 
     uint8_t* ws = static_cast<uint8_t*>(workspace);
     const int T = n_tokens, H = g->n_embd, E = g->n_expert, K = g->top_k, F = g->n_ff;
-    const int Fs = has_sh ? g->n_ff_shared : 0;
+    const int Fs = shf ? g->n_ff_shared : 0;
     const int P = T * K;
     uint32_t* ximg = reinterpret_cast<uint32_t*>(ws + L.ximg);
     float* logits = (trace && trace->logits) ? trace->logits : reinterpret_cast<float*>(ws + L.logits);
@@ -305,7 +340,7 @@ smoe_status forward_impl(const smoe_geom* g, const smoe_weights* w, float* x_io,
     // run as one launch whose exchange words the router kernel clears
     const bool small = !mfma && !iq2 && !stages && T <= kFusedRouteTokens;
     const bool small_down = small && smoe::down_combine_ok(T, K, L.h_blocks);
-    const bool fused = small_down && smoe::moe_small_ok(T, K, H, F, Fs, has_sh ? 1 : 0, L.h_blocks);
+    const bool fused = small_down && smoe::moe_small_ok(T, K, H, F, Fs, shf ? 1 : 0, L.h_blocks);
     uint8_t* xchg = ws + L.xchg;
     const size_t xchg_bytes = fused ? smoe::moe_small_xchg_bytes(T, K, n_items, L.h_blocks) : 0;
     uint16_t* xbf = mfma ? reinterpret_cast<uint16_t*>(ws + L.xbf) : nullptr;
@@ -328,18 +363,18 @@ smoe_status forward_impl(const smoe_geom* g, const smoe_weights* w, float* x_io,
         // no route kernel: the stage boundary marks stay, the route stage is empty
     } else if (T <= kFusedRouteTokens) {
         SMOE_TRY(smoe::launch_topk_dispatch(logits, T, E, K, ids, wts, counts, offsets, perm, slot, elist, nlist, items,
-                                            n_items, has_sh ? 1 : 0, chunk, sh_chunk, st),
+                                            n_items, shf ? 1 : 0, chunk, sh_chunk, st),
                  "route");
     } else {
         SMOE_TRY(smoe::launch_topk(logits, E, T, E, K, ids, wts, st), "topk");
         if (P > kDispatchMultiPairs)
             SMOE_TRY(smoe::launch_dispatch_multi(ids, P, E, counts, offsets, perm, slot, elist, nlist, items, n_items,
-                                                 T, K, has_sh ? 1 : 0, chunk, sh_chunk,
+                                                 T, K, shf ? 1 : 0, chunk, sh_chunk,
                                                  reinterpret_cast<int32_t*>(ws + L.dwork), st),
                      "dispatch");
         else
             SMOE_TRY(smoe::launch_dispatch(ids, P, E, counts, offsets, perm, slot, elist, nlist, items, n_items, T, K,
-                                           has_sh ? 1 : 0, chunk, sh_chunk, st),
+                                           shf ? 1 : 0, chunk, sh_chunk, st),
                      "dispatch");
     }
     SMOE_MARK();
@@ -352,45 +387,67 @@ smoe_status forward_impl(const smoe_geom* g, const smoe_weights* w, float* x_io,
     uint8_t* hq = (trace && !mfma) ? trace->hq : nullptr;
     if (mfma) {
         SMOE_TRY(smoe::launch_mm_gu(ge, ue, gs, us, ximg, (int64_t)T * (H / 64), items, perm, K, H, F, Fs,
-                                    has_sh ? 1 : 0, n_items, himg, L.h_rec, st, hflags),
+                                    shf ? 1 : 0, n_items, himg, L.h_rec, st, hflags),
                  "gate/up");
         SMOE_MARK();
         SMOE_TRY(smoe::launch_mm_down(de, ds, himg, (int64_t)(P + T) * L.h_rec, L.h_rec, sg, items, H, F, Fs, n_items,
                                       Y, st),
                  "down");
     } else if (iq2) {
-        SMOE_TRY(smoe::launch_iq2_gu(ge, ue, gs, us, ximg, items, perm, K, H, F, Fs, has_sh ? 1 : 0, n_items, himg,
+        SMOE_TRY(smoe::launch_iq2_gu(ge, ue, gs, us, ximg, items, perm, K, H, F, Fs, shf ? 1 : 0, n_items, himg,
                                      L.h_blocks, st, hq, P),
                  "gate/up");
         SMOE_MARK();
         SMOE_TRY(smoe::launch_iq2_down(de, ds, himg, L.h_blocks, sg, items, H, F, Fs, n_items, Y, st), "down");
     } else if (fused) {
-        SMOE_TRY(smoe::launch_q2_moe_small(ge, ue, gs, us, de, ds, ximg, logits, sg, T, E, K, H, F, Fs, has_sh ? 1 : 0,
+        SMOE_TRY(smoe::launch_q2_moe_small(ge, ue, gs, us, de, ds, ximg, logits, sg, T, E, K, H, F, Fs, shf ? 1 : 0,
                                            ids, wts, counts, offsets, perm, slot, elist, nlist, items, n_items, L.h_blocks,
-                                           xchg, (has_sh && add_shared) ? 1 : 0, y, st),
+                                           xchg, (shf && add_shared) ? 1 : 0, y, st),
                  "route + gate/up + down + combine");
         SMOE_MARK();  // gate/up, down and combine are one launch: the later stage boundaries are empty
     } else {
         if (small)
-            SMOE_TRY(smoe::launch_q2_gu_route(ge, ue, gs, us, ximg, logits, T, E, K, H, F, Fs, has_sh ? 1 : 0, ids, wts,
+            SMOE_TRY(smoe::launch_q2_gu_route(ge, ue, gs, us, ximg, logits, T, E, K, H, F, Fs, shf ? 1 : 0, ids, wts,
                                               counts, offsets, perm, slot, elist, nlist, items, n_items, himg,
                                               L.h_blocks, st),
                      "route + gate/up");
         else
-            SMOE_TRY(smoe::launch_q2_gu(ge, ue, gs, us, ximg, items, perm, K, H, F, Fs, has_sh ? 1 : 0, n_items, himg,
+            SMOE_TRY(smoe::launch_q2_gu(ge, ue, gs, us, ximg, items, perm, K, H, F, Fs, shf ? 1 : 0, n_items, himg,
                                         L.h_blocks, st, hq, P),
                      "gate/up");
         SMOE_MARK();
         if (small_down)
             SMOE_TRY(smoe::launch_q2_down_combine(de, ds, himg, L.h_blocks, sg, items, n_items, H, F, Fs, slot, wts, T, K,
-                                                  (has_sh && add_shared) ? 1 : 0, y, st),
+                                                  (shf && add_shared) ? 1 : 0, y, st),
                      "down + combine");
         else
             SMOE_TRY(smoe::launch_q2_down(de, ds, himg, L.h_blocks, sg, items, H, F, Fs, n_items, Y, st), "down");
     }
     SMOE_MARK();
+    if (nat) {  // the native shared expert: q8_1 of x, gate and up, SwiGLU + q8_1, down times sigmoid(sg) into Y[P + t]
+        const int Fn = g->n_ff_shared;
+        uint8_t* nxq = ws + L.nxq;
+        float* ngu = reinterpret_cast<float*>(ws + L.ngu);
+        uint8_t* nhq = ws + L.nhq;
+        SMOE_TRY(smoe::launch_prep(x_io, (int64_t)T * H, nxq, nullptr, st), "shared q8_1");
+        auto gemv = [&](int type, const void* wt, const uint8_t* xq, int n_in, int n_out, float* out,
+                        const float* gate) -> hipError_t {
+            const uint8_t* wb = static_cast<const uint8_t*>(wt);
+            if (smoe::native_type(type)) return smoe::launch_mmvq_native(type, wb, xq, n_in, n_out, T, out, n_out, gate, st);
+            hipError_t e = type == SMOE_IQ2_S ? smoe::launch_iq2_mmvq(wb, xq, n_in, n_out, T, out, st)
+                                              : smoe::launch_q2_mmvq(wb, xq, n_in, n_out, T, out, st);
+            if (e == hipSuccess && gate) e = smoe::launch_sigmoid_rows(out, T, n_out, gate, st);
+            return e;
+        };
+        SMOE_TRY(gemv(sh_gate_t(*g), w->gate_sh, nxq, H, Fn, ngu, nullptr), "shared gate");
+        SMOE_TRY(gemv(sh_up_t(*g), w->up_sh, nxq, H, Fn, ngu + (size_t)T * Fn, nullptr), "shared up");
+        SMOE_TRY(smoe::launch_swiglu_q8(ngu, ngu + (size_t)T * Fn, (int64_t)T * Fn, nhq, st), "shared swiglu");
+        SMOE_TRY(gemv(sh_down_t(*g), w->down_sh, nhq, Fn, H, Y + (size_t)P * H, sg), "shared down");
+    }
     if (!small_down)
         SMOE_TRY(smoe::launch_combine(Y, slot, wts, K, H, P, T, (has_sh && add_shared) ? 1 : 0, y, st), "combine");
+    else if (nat && add_shared)  // the fused combine left the shared rows out: the same last addition, after it
+        SMOE_TRY(smoe::launch_add_rows(y, Y + (size_t)P * H, T, H, st), "shared add");
     SMOE_MARK();
 #undef SMOE_MARK
     // the trace's expert stages and overflow mask, after the last stage event
@@ -707,8 +764,10 @@ smoe_status smoe_mmvq(int32_t type, const void* w, int64_t byte_off, const uint8
                       int32_t n_col, float* y, void* hip_stream) {
     if (n_in < 0 || n_out < 0 || n_col < 0 || byte_off < 0) return fail(SMOE_EINVAL, "mmvq: negative size");
     if (n_in == 0 || n_out == 0 || n_col == 0) return ok();
-    if (type != SMOE_Q2_0 && type != SMOE_IQ2_S)
-        return fail(SMOE_ETYPE, "mmvq: type " + std::to_string(type) + " is not Q2_0 or IQ2_S");
+    if (!gemv_type(type))
+        return fail(SMOE_ETYPE, "mmvq: type " + std::to_string(type) + " has no GEMV here");
+    if (smoe::native_type(type) && smoe::native_row_bytes(type, n_in) <= 0)
+        return fail(SMOE_EINVAL, "mmvq: n_in must be a multiple of " + std::to_string(smoe::native_block_values(type)));
     if (type == SMOE_Q2_0 && (n_in > kMaxFF || !smoe::gemv_shape_ok(n_in)))
         return fail(SMOE_EINVAL, "mmvq: n_in must be 128 times a power of two times at most 8, at most 4096");
     if (type == SMOE_IQ2_S && !smoe::iq2_shape_ok(n_in))
@@ -716,7 +775,10 @@ smoe_status smoe_mmvq(int32_t type, const void* w, int64_t byte_off, const uint8
     if (!w || !x_q8 || !y) return fail(SMOE_ENULL, "mmvq: NULL buffer");
     const uint8_t* base = static_cast<const uint8_t*>(w) + byte_off;
     if (!aligned(base, 4) || !aligned(x_q8, 4)) return fail(SMOE_EALIGN, "mmvq: w + byte_off and x must be 4-byte aligned");
-    if (type == SMOE_IQ2_S) SMOE_TRY(smoe::launch_iq2_mmvq(base, x_q8, n_in, n_out, n_col, y, stream_of(hip_stream)), "mmvq");
+    if (smoe::native_type(type))
+        SMOE_TRY(smoe::launch_mmvq_native(type, base, x_q8, n_in, n_out, n_col, y, n_out, nullptr, stream_of(hip_stream)),
+                 "mmvq");
+    else if (type == SMOE_IQ2_S) SMOE_TRY(smoe::launch_iq2_mmvq(base, x_q8, n_in, n_out, n_col, y, stream_of(hip_stream)), "mmvq");
     else SMOE_TRY(smoe::launch_q2_mmvq(base, x_q8, n_in, n_out, n_col, y, stream_of(hip_stream)), "mmvq");
     return ok();
 }

@@ -73,6 +73,15 @@ hipError_t launch_combine(const float* Y, const int32_t* slot, const float* wts,
 hipError_t launch_combine_parts(const float* parts, const float* wts, const float* shared, int k, int n, float* y,
                                 hipStream_t s);
 hipError_t launch_swiglu_q8(const float* gate, const float* up, int64_t n, uint8_t* y, hipStream_t s);
+// the other native GGUF types (smoe_native.hip): Q8_0 8, Q4_0 2, Q5_0 6, IQ4_NL 20, IQ4_XS 23, Q3_K 11, Q4_K 12,
+// Q5_K 13, Q6_K 14; y[c * ldy + r], times sigmoid(sg[c]) when sg is given
+bool native_type(int type);
+int native_block_values(int type);
+int64_t native_row_bytes(int type, int64_t n);  // -1: not native, or n not a whole number of blocks
+hipError_t launch_mmvq_native(int type, const uint8_t* w, const uint8_t* xq, int n_in, int n_out, int n_col, float* y,
+                              int ldy, const float* sg, hipStream_t s);
+hipError_t launch_sigmoid_rows(float* y, int T, int n, const float* sg, hipStream_t s);  // y[t][.] *= sigmoid(sg[t])
+hipError_t launch_add_rows(float* y, const float* r, int T, int n, hipStream_t s);       // y[t][.] += r[t][.]
 hipError_t launch_q2_mmvq(const uint8_t* w, const uint8_t* xq, int n_in, int n_out, int n_col, float* y, hipStream_t s);
 
 // IQ2_S (decode contract)

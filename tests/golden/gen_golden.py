@@ -9,6 +9,11 @@ codecs_ref.npz       f16 / bf16 encodings of edge-case floats and Q2_0 dequantis
 layer_small.npz      one small seeded layer through the oracle's device-order decode contract: input, output,
                      routing trace and sha256 of every generated tensor (pins the generators and the chain).
 layer_prefill.npz    the same layer through the prefill contract (bf16 activations, exact block scales).
+native_ref.npz       blocks of the other native GGUF types (Q8_0, Q4_0, Q5_0, IQ4_NL, IQ4_XS, Q3_K, Q4_K, Q5_K, Q6_K)
+                     and their values as the REFERENCE's own dequantisers give them (include/strata/artifact/
+                     dequant.hpp:81-280 through oracle/_ref), edge scales included.
+
+    python tests/golden/gen_golden.py native     # writes native_ref.npz alone
 """
 import hashlib
 import os
@@ -83,5 +88,34 @@ def main():
         print(f, os.path.getsize(os.path.join(HERE, f)), "bytes")
 
 
+def native_blocks(t: int) -> np.ndarray:
+    """Seeded blocks of type t plus edge scale fields: the smallest subnormal, -0, 65504, and a zero block."""
+    qk, nb, fields, _ = O.NATIVE[t]
+    b = O.gen_native_blocks(t, 20261202, 77, 12 * qk).reshape(12, nb).copy()
+    for f in fields:
+        b[0, f:f + 2] = [0x01, 0x00]
+        b[1, f:f + 2] = [0x00, 0x80]
+        b[2, f:f + 2] = [0xFF, 0x7B]
+    b[3] = 0
+    return b.ravel()
+
+
+def main_native():
+    O.build()
+    if O.ref() is None:
+        raise SystemExit("oracle/_ref is not built (needs /root/reference): cannot write the reference vectors")
+    out = {}
+    for t in sorted(O.NATIVE):
+        b = native_blocks(t)
+        n = b.size // O.NATIVE[t][1] * O.NATIVE[t][0]
+        out[f"blocks_{t}"] = b
+        out[f"values_{t}"] = O.ref_dequantize(t, b, n)
+    np.savez_compressed(os.path.join(HERE, "native_ref.npz"), **out)
+    print("native_ref.npz", os.path.getsize(os.path.join(HERE, "native_ref.npz")), "bytes")
+
+
 if __name__ == "__main__":
-    main()
+    if len(sys.argv) > 1 and sys.argv[1] == "native":
+        main_native()
+    else:
+        main()

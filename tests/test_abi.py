@@ -34,7 +34,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_status_strings():
     lib = S.lib()
-    assert lib.smoe_abi_version() == 106
+    assert lib.smoe_abi_version() == 107
     for code in (0, -1, -2, -3, -4, -5, -6):
         assert lib.smoe_status_str(code)
 
@@ -214,3 +214,17 @@ def test_binding_refuses_bad_tensors_before_launch():
         with pytest.raises(S.SmoeError) as e:
             fn()
         assert why in str(e.value), (why, str(e.value))
+
+
+def test_native_shared_geometry_refusals():
+    """A shared expert in its own native types: rows must be whole blocks of each projection's type, n_ff_shared a
+    multiple of 32, every type one with a GEMV here; the workspace query refuses (returns 0) otherwise."""
+    L = S.lib()
+    ok = S.Geom(sh_type=S.Q3_K, sh_down_type=S.IQ4_NL)
+    assert L.smoe_workspace_bytes(C.byref(ok.c()), 4) > 0
+    for kw in (dict(sh_type=S.Q4_K, n_ff_shared=640),       # Q4_K down rows of 640 values: not whole 256-blocks
+               dict(sh_type=S.Q8_0, n_ff_shared=48),        # n_ff_shared not a multiple of 32
+               dict(sh_type=S.Q8_0, sh_down_type=1),        # F16: no GEMV here
+               dict(sh_type=S.Q2_0, sh_gate_type=S.IQ2_S, n_embd=4096)):  # IQ2_S rows of 4096
+        g = S.Geom(**kw)
+        assert L.smoe_workspace_bytes(C.byref(g.c()), 4) == 0, kw

@@ -115,7 +115,8 @@ def test_iq2_s_refusals(torch):
     say("case: IQ2_S refusals")
     ok = S.Geom(n_embd=512, n_ff=512, n_ff_shared=512, n_expert=16, top_k=4, w_type=22, sh_type=22)
     assert S.workspace_bytes(ok, 8) > 0
-    for bad in (dict(n_embd=768), dict(n_ff=256), dict(n_embd=4096), dict(n_ff_shared=1024), dict(sh_type=42)):
+    # (a Q2_0 shared expert beside IQ2_S experts is a native shared expert now: tests/test_gpu_native.py)
+    for bad in (dict(n_embd=768), dict(n_ff=256), dict(n_embd=4096), dict(n_ff_shared=1024)):
         kw = dict(vars(ok)); kw.update(bad)
         with pytest.raises(S.SmoeError):
             S.workspace_bytes(S.Geom(**kw), 8)
