@@ -197,6 +197,61 @@ smoe_status smoe_ffn_run(const smoe_geom* g, const smoe_weights* w, const smoe_h
                          int32_t n_tokens, float* out, int32_t add_shared, void* workspace, size_t workspace_bytes,
                          const smoe_trace* trace, void* hip_stream);
 
+/* ---------------------------------------------------------------------------------------------- GGUF models */
+
+/* A model in GGUF v3 files, read on the host: every shard of a split model (`<stem>-NNNNN-of-MMMMM.gguf`, any
+ * shard's path opens all; the metadata in shard 1), mapped read-only.  Replaces GgufFile / GgufModel and
+ * ModelTensors (include/strata/artifact/gguf_reader.hpp:340-566, metal/include/strata/metal/layer_tensors.hpp:87-212).
+ * Refused: a missing shard, bad magic, a version other than 3, a header that ends early, a tensor listed twice or
+ * in two shards, split.count / split.no / split.tensors.count that disagree. */
+typedef struct smoe_model smoe_model;
+
+typedef struct {
+    int32_t type;         /* ggml type */
+    int32_t n_dims;
+    int32_t shard;        /* the shard holding it (0 = the first) */
+    int32_t reserved;
+    uint64_t ne[4];       /* GGUF order: ne[0] is a row (it varies fastest); unused dimensions are 1 */
+    uint64_t bytes;       /* payload bytes */
+    uint64_t file_offset; /* byte offset of the payload in its shard */
+    const void* host;     /* the payload in the read-only mapping (valid until smoe_model_close) */
+} smoe_tensor_info;
+
+smoe_status smoe_model_open(const char* any_shard_path, smoe_model** out);
+void smoe_model_close(smoe_model* m);
+int32_t smoe_model_n_shards(const smoe_model* m);
+int64_t smoe_model_n_tensors(const smoe_model* m);
+/* A tensor by its full name (blk.<layer>.<suffix> for a layer's), refused when absent, of a type without a known
+ * block size, or not inside its file. */
+smoe_status smoe_model_tensor(const smoe_model* m, const char* name, smoe_tensor_info* info);
+/* The i-th tensor (shard by shard, directory order) and its name (name_cap bytes, NUL included). */
+smoe_status smoe_model_tensor_at(const smoe_model* m, int64_t i, char* name, size_t name_cap, smoe_tensor_info* info);
+/* Metadata of the first shard: an integer or bool value (an array: its element count), or a string. */
+smoe_status smoe_model_meta_u64(const smoe_model* m, const char* key, uint64_t* value);
+smoe_status smoe_model_meta_str(const smoe_model* m, const char* key, char* buf, size_t cap);
+
+/* One layer's MoE block from the model, the tensor side of FfnExec::load (metal/src/layer_exec.cpp:369-431):
+ * blk.<layer>.ffn_{gate,up,down}_exps, ffn_gate_inp, and with_shared the shared expert's ffn_{gate,up,down}_shexp
+ * and ffn_gate_inp_shexp (each projection its own type), and the hyper-connection tensors hc_ffn_{norm,down,up,
+ * inject} when present (all four or none).  The geometry comes from the tensors' shapes and types (ffn_gate_inp
+ * BF16: router_dtype 0, F32: 1; ffn_gate_inp_shexp BF16, or F32 rounded to bf16 on upload), top_k from the call
+ * (> 0) or the model's <general.architecture>.expert_used_count; the plan is refused when the block does not take
+ * the geometry (smoe_workspace_bytes's checks). */
+typedef struct {
+    smoe_geom geom;
+    smoe_hc hc;          /* hc, hc_lr and eps 1e-6 of the hyper-connection tensors (hc 0: none); pointers NULL */
+    size_t device_bytes; /* bytes smoe_layer_upload writes */
+    size_t off[12];      /* slot offsets in the device buffer (256-byte aligned) */
+    int32_t layer, with_shared;
+} smoe_layer_plan;
+
+smoe_status smoe_layer_plan_for(const smoe_model* m, int32_t layer, int32_t top_k, int32_t with_shared,
+                                smoe_layer_plan* plan);
+/* Copies the planned tensors into `device` (256-byte aligned, at least plan->device_bytes) on hip_stream and waits
+ * for the copies; fills `w` (device pointers into `device`) and, when `hc` is given, the hyper-connection tensors. */
+smoe_status smoe_layer_upload(const smoe_model* m, const smoe_layer_plan* plan, void* device, size_t device_bytes,
+                              smoe_weights* w, smoe_hc* hc, void* hip_stream);
+
 /* ---------------------------------------------------------------------------------------------- no allocation */
 
 /* Bytes of the library's static device scratch (one array per GPU, held from the library's load until the

@@ -137,6 +137,8 @@ def ref():
         R.ref_iq2s_grid.argtypes = [C.c_void_p]
         R.ref_dequantize.restype = C.c_int
         R.ref_dequantize.argtypes = [C.c_int, C.c_void_p, C.c_int64, C.c_void_p]
+        R.ref_gguf_list.restype = C.c_int
+        R.ref_gguf_list.argtypes = [C.c_char_p, C.c_char_p, C.c_size_t]
         _REF = R
     return _REF
 
@@ -637,4 +639,14 @@ def hc_write_dev(R: np.ndarray, y: np.ndarray, inject: np.ndarray, n: int, hc: i
     out = np.empty_like(R)
     lib().or_hc_write_dev(_p(R), _p(y), _p(inject), T, n, hc, _p(out))
     return out
+
+
+def ref_gguf_list(path: str):
+    """The reference reader's listing of a GGUF model (oracle/_ref): (status, text), or None without _ref."""
+    R = ref()
+    if R is None:
+        return None
+    buf = C.create_string_buffer(1 << 20)
+    rc = R.ref_gguf_list(path.encode(), buf, 1 << 20)
+    return rc, buf.value.decode()
 

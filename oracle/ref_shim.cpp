@@ -7,13 +7,17 @@
 //   include/strata/artifact/dequant.hpp:81-280   the other native types (Q8_0, Q4_0, Q5_0, IQ4_NL, Q6_K, Q4_K,
 //                                                Q5_K, Q3_K, IQ4_XS)
 //   metal/include/strata/metal/iq_grids.hpp:5    iq2s_grid
+//   include/strata/artifact/gguf_reader.hpp       GgufModel (GgufFile, split shards, tensor_payload_bytes)
 #include "strata/artifact/dequant.hpp"
+#include "strata/artifact/gguf_reader.hpp"
 #include "strata/kernels/bf16_bits.hpp"
 #include "strata/kernels/f16_bits.hpp"
 #include "strata/metal/iq_grids.hpp"
 
 #include <cstdint>
+#include <cstdio>
 #include <cstring>
+#include <string>
 
 extern "C" {
 uint16_t ref_f16_from_f32(float f) { return strata::kernels::f16_from_f32(f); }
@@ -53,4 +57,29 @@ int ref_dequantize(int type, const uint8_t* blocks, int64_t n_values, float* out
     return 0;
 }
 void ref_iq2s_grid(uint64_t* out1024) { std::memcpy(out1024, strata::metal::iq2s_grid, sizeof(strata::metal::iq2s_grid)); }
+// The reference reader's view of a model (any shard's path): per shard "shard <i> <data_start> <n_tensors>", then per
+// tensor "<name> <type> <n_dims> <ne...> <offset> <payload bytes> <in bounds>"; -1 with "ERR <why>" when it refuses.
+int ref_gguf_list(const char* path, char* out, size_t cap) {
+    try {
+        strata::GgufModel m = strata::GgufModel::open(path);
+        std::string s;
+        for (size_t i = 0; i < m.size(); ++i) {
+            const strata::GgufFile& f = m.shard(i);
+            s += "shard " + std::to_string(i) + " " + std::to_string(f.data_start()) + " " +
+                 std::to_string(f.tensors().size()) + "\n";
+            for (const auto& t : f.tensors()) {
+                s += t.name + " " + std::to_string(t.type) + " " + std::to_string(t.shape.size());
+                for (uint64_t d : t.shape) s += " " + std::to_string(d);
+                s += " " + std::to_string(t.offset) + " " + std::to_string(strata::tensor_payload_bytes(t)) + " " +
+                     (m.in_bounds(t, i) ? "1" : "0") + "\n";
+            }
+        }
+        if (s.size() + 1 > cap) return -2;
+        std::memcpy(out, s.c_str(), s.size() + 1);
+        return 0;
+    } catch (const std::exception& e) {
+        std::snprintf(out, cap, "ERR %s", e.what());
+        return -1;
+    }
+}
 }

@@ -98,6 +98,16 @@ def lib():
             "smoe_status_str": (C.c_char_p, [i32]),
             "smoe_last_error": (C.c_char_p, []),
             "smoe_abi_version": (i32, []),
+            "smoe_model_open": (i32, [C.c_char_p, C.POINTER(vp)]),
+            "smoe_model_close": (None, [vp]),
+            "smoe_model_n_shards": (i32, [vp]),
+            "smoe_model_n_tensors": (i64, [vp]),
+            "smoe_model_tensor": (i32, [vp, C.c_char_p, vp]),
+            "smoe_model_tensor_at": (i32, [vp, i64, C.c_char_p, C.c_size_t, vp]),
+            "smoe_model_meta_u64": (i32, [vp, C.c_char_p, C.POINTER(u64)]),
+            "smoe_model_meta_str": (i32, [vp, C.c_char_p, C.c_char_p, C.c_size_t]),
+            "smoe_layer_plan_for": (i32, [vp, i32, i32, i32, vp]),
+            "smoe_layer_upload": (i32, [vp, vp, vp, C.c_size_t, vp, vp, vp]),
         }
         for name, (res, args) in sigs.items():
             fn = getattr(L, name)
@@ -609,3 +619,129 @@ def dispatch(ids, n_expert: int, stream=None):
     _check(lib().smoe_dispatch(ids.data_ptr(), T, k, n_expert, counts.data_ptr(), offsets.data_ptr(),
                                perm.data_ptr(), slot.data_ptr(), _stream(stream)))
     return counts, offsets, perm, slot
+
+
+# ------------------------------------------------------------------------------------------------ GGUF models
+
+class _TensorInfo(C.Structure):
+    _fields_ = [("type", C.c_int32), ("n_dims", C.c_int32), ("shard", C.c_int32), ("reserved", C.c_int32),
+                ("ne", C.c_uint64 * 4), ("bytes", C.c_uint64), ("file_offset", C.c_uint64), ("host", C.c_void_p)]
+
+
+class _LayerPlan(C.Structure):
+    _fields_ = [("geom", _Geom), ("hc", _Hc), ("device_bytes", C.c_size_t), ("off", C.c_size_t * 12),
+                ("layer", C.c_int32), ("with_shared", C.c_int32)]
+
+
+@dataclass
+class TensorInfo:
+    name: str
+    type: int
+    shape: tuple           # GGUF order: shape[0] is a row
+    shard: int
+    bytes: int
+    file_offset: int
+
+
+class Model:
+    """A GGUF v3 model on the host (smoe_model_*: every shard of a split model, mapped read-only), its tensors by
+    name, its metadata, and one layer's MoE tensors loaded into device memory (smoe_layer_plan_for /
+    smoe_layer_upload, the tensor side of the reference's FfnExec::load)."""
+
+    def __init__(self, path: str):
+        self._h = C.c_void_p()
+        _check(lib().smoe_model_open(path.encode(), C.byref(self._h)))
+
+    def close(self):
+        if self._h:
+            lib().smoe_model_close(self._h)
+            self._h = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def n_shards(self) -> int:
+        return int(lib().smoe_model_n_shards(self._h))
+
+    def _info(self, name: str, ti: _TensorInfo) -> TensorInfo:
+        return TensorInfo(name, ti.type, tuple(int(ti.ne[d]) for d in range(ti.n_dims)), ti.shard, int(ti.bytes),
+                          int(ti.file_offset))
+
+    def tensors(self):
+        out = []
+        for i in range(int(lib().smoe_model_n_tensors(self._h))):
+            buf = C.create_string_buffer(4096)
+            ti = _TensorInfo()
+            _check(lib().smoe_model_tensor_at(self._h, i, buf, 4096, C.byref(ti)))
+            out.append(self._info(buf.value.decode(), ti))
+        return out
+
+    def tensor(self, name: str) -> TensorInfo:
+        ti = _TensorInfo()
+        _check(lib().smoe_model_tensor(self._h, name.encode(), C.byref(ti)))
+        return self._info(name, ti)
+
+    def tensor_bytes(self, name: str) -> bytes:
+        """The payload as the mapping holds it (a copy)."""
+        ti = _TensorInfo()
+        _check(lib().smoe_model_tensor(self._h, name.encode(), C.byref(ti)))
+        return C.string_at(ti.host, ti.bytes)
+
+    def meta_u64(self, key: str) -> int:
+        v = C.c_uint64()
+        _check(lib().smoe_model_meta_u64(self._h, key.encode(), C.byref(v)))
+        return int(v.value)
+
+    def meta_str(self, key: str) -> str:
+        buf = C.create_string_buffer(1 << 16)
+        _check(lib().smoe_model_meta_str(self._h, key.encode(), buf, 1 << 16))
+        return buf.value.decode()
+
+    def plan(self, layer: int, top_k: int = 0, with_shared: bool = True) -> _LayerPlan:
+        p = _LayerPlan()
+        _check(lib().smoe_layer_plan_for(self._h, layer, top_k, int(with_shared), C.byref(p)))
+        return p
+
+    def load_layer(self, layer: int, top_k: int = 0, with_shared: bool = True, with_hc: bool = False,
+                   device="cuda", stream=None):
+        """(Geom, weights dict of device tensors, HyperConnection or None) of one layer; the weights are views of
+        one device buffer the returned dict also keeps (key "_buffer")."""
+        import torch
+        p = self.plan(layer, top_k, with_shared)
+        buf = torch.empty(p.device_bytes + 256, dtype=torch.uint8, device=device)
+        base = (buf.data_ptr() + 255) & ~255
+        w, hc = _Weights(), _Hc()
+        _check(lib().smoe_layer_upload(self._h, C.byref(p), base, p.device_bytes, C.byref(w),
+                                       C.byref(hc) if with_hc else None, _stream(stream)))
+        gc = p.geom
+        g = Geom(gc.n_embd, gc.n_ff, gc.n_ff_shared, gc.n_expert, gc.top_k, gc.w_type, gc.sh_type, gc.router_dtype,
+                 gc.sh_gate_type, gc.sh_up_type, gc.sh_down_type)
+
+        def view(ptr, nbytes):
+            o = ptr - buf.data_ptr()
+            return buf[o:o + nbytes]
+
+        H, F, E, Fs = g.n_embd, g.n_ff, g.n_expert, g.n_ff_shared
+        sizes = dict(gate_exps=E * F * row_bytes(g.w_type, H), up_exps=E * F * row_bytes(g.w_type, H),
+                     down_exps=E * H * row_bytes(g.w_type, F),
+                     router=E * H * (4 if g.router_dtype == ROUTER_F32 else 2))
+        weights = {n: view(getattr(w, n), sizes[n]) for n in sizes}
+        if with_shared:
+            weights.update(gate_sh=view(w.gate_sh, Fs * row_bytes(g.sh_gate_type, H)),
+                           up_sh=view(w.up_sh, Fs * row_bytes(g.sh_up_type, H)),
+                           down_sh=view(w.down_sh, H * row_bytes(g.sh_down_type, Fs)),
+                           gate_inp_sh=view(w.gate_inp_sh, H * 2))
+        weights["_buffer"] = buf
+        hcx = None
+        if with_hc:
+            hd = hc.hc * H
+            hcx = HyperConnection(H, hc.hc, hc.hc_lr, view(hc.norm, hd * 4).view(torch.float32),
+                                  view(hc.down, hc.hc_lr * hd * 2).view(torch.int16),
+                                  view(hc.up, hd * hc.hc_lr * 2).view(torch.int16),
+                                  view(hc.inject, hc.hc * hd * 2).view(torch.int16), eps=float(hc.eps))
+        return g, weights, hcx
+

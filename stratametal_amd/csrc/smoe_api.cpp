@@ -194,6 +194,11 @@ smoe_status launched(hipError_t e, const char* what) {
 
 }  // namespace
 
+namespace smoe {
+// The thread's last error for the other translation units of the library (the model reader).
+smoe_status report(smoe_status s, const std::string& why) { return s == SMOE_OK ? ok() : fail(s, why); }
+}  // namespace smoe
+
 extern "C" {
 
 const char* smoe_status_str(smoe_status s) {
@@ -211,7 +216,7 @@ const char* smoe_status_str(smoe_status s) {
 
 const char* smoe_last_error(void) { return g_last.c_str(); }
 
-int32_t smoe_abi_version(void) { return 107; }
+int32_t smoe_abi_version(void) { return 108; }
 
 size_t smoe_workspace_bytes(const smoe_geom* g, int32_t max_tokens) {
     if (check_geom(g) != SMOE_OK || max_tokens < 0) return 0;
