@@ -252,6 +252,65 @@ smoe_status smoe_layer_plan_for(const smoe_model* m, int32_t layer, int32_t top_
 smoe_status smoe_layer_upload(const smoe_model* m, const smoe_layer_plan* plan, void* device, size_t device_bytes,
                               smoe_weights* w, smoe_hc* hc, void* hip_stream);
 
+/* ---------------------------------------------------------------------------------------------- expert tier */
+
+/* Routed experts addressed one pointer each: expert e's blob is [gate rows | up rows | down rows] of the routed
+ * type (n_ff rows of n_embd values twice, then n_embd rows of n_ff values), the layout of NativeExpertLayout
+ * (include/strata/kernels/iq_kernels.hpp:56-65).  A table `expert_ptr` [n_expert] of device-readable addresses
+ * (HBM, or pinned host memory the GPU reads over the bus) holds each expert's blob, 0 for an expert the table does
+ * not hold.  Every result is bitwise the block's decode contract (smoe_forward's routed pair rows and output). */
+size_t smoe_expert_blob_bytes(const smoe_geom* g); /* 0 when the geometry is refused */
+/* Copies expert `expert`'s rows from the planes of `w` into `blob` (smoe_expert_blob_bytes) on hip_stream. */
+smoe_status smoe_expert_pack(const smoe_geom* g, const smoe_weights* w, int32_t expert, void* blob, void* hip_stream);
+
+/* The hit/miss split on the device.  Entry i of ids[n] (T tokens x k_per_tok, flattened: token i / k_per_tok) is a
+ * hit when expert_ptr[ids[i]] != 0, else (no blob, or an id outside [0, n_expert)) a miss.  Hits are grouped by
+ * expert, groups in ascending expert id and a group's entries in ascending i: group g's blob grp_ptr[g], expert
+ * grp_expert[g] (may be NULL), entries [grp_start[g], grp_start[g + 1]) with ent_dst[j] = i and ent_tok[j] =
+ * i / k_per_tok.  Misses go to miss_dst in ascending i.  counts [4] = {groups, hit entries, misses, 0}, all on the
+ * device (nothing is read back).  Sizes: grp_ptr, grp_expert min(n, n_expert); grp_start that + 1; ent_dst,
+ * ent_tok, miss_dst n.  n <= 4096, n_expert <= 1024.  Replaces moe_hit_select / moe_hit_select_multi /
+ * moe_group_resident (include/strata/kernels/s2_expert_grouped.hpp:92-112). */
+smoe_status smoe_expert_group(const int32_t* ids, int32_t n, int32_t k_per_tok, int32_t n_expert,
+                              const uint64_t* expert_ptr, uint64_t* grp_ptr, int32_t* grp_start, int32_t* grp_expert,
+                              int32_t* ent_dst, int32_t* ent_tok, int32_t* miss_dst, int32_t* counts,
+                              void* hip_stream);
+
+/* Grouped experts: group g < counts[0] (at most cap_groups) has its blob at grp_ptr[g] and the entries
+ * [grp_start[g], grp_start[g + 1]) (within [0, cap_entries)); entry j reads token ent_tok[j]'s activation (x_q8_1:
+ * n_tokens rows of n_embd / 32 q8_1 blocks, smoe_quantize_q8_1's format) and writes the expert's output (before the
+ * routing weight) to row ent_dst[j] of out (n_out_rows rows of n_embd f32).  Each blob row is read once for all of
+ * its group's entries.  The lists are read on the device and checked there: an entry whose token or row is out of
+ * range, and a group whose blob is 0, write nothing.  The launch is sized by the caps, so a captured graph replays
+ * for any lists.  Sizes: grp_ptr cap_groups, grp_start cap_groups + 1, ent_dst and ent_tok cap_entries.
+ * Replaces moe_grouped_s2 / native_expert_grouped / moe_hit_grouped_s2_dev (s2_expert_grouped.hpp:104-108,
+ * iq_kernels.hpp:70-80). */
+size_t smoe_expert_grouped_workspace_bytes(const smoe_geom* g, int32_t n_tokens, int32_t cap_groups,
+                                           int32_t cap_entries);
+smoe_status smoe_expert_grouped(const smoe_geom* g, const uint64_t* grp_ptr, const int32_t* grp_start,
+                                const int32_t* ent_dst, const int32_t* ent_tok, const int32_t* counts,
+                                int32_t cap_groups, int32_t cap_entries, const uint8_t* x_q8_1, int32_t n_tokens,
+                                float* out, int32_t n_out_rows, void* workspace, size_t workspace_bytes,
+                                void* hip_stream);
+
+/* The verify window with the hit/miss split: n_tokens tokens (n_tokens * top_k <= 4096) through the layer, the
+ * routed experts from the table.  smoe_verify_begin runs the router and the routing (ids, weights [T][k], as
+ * smoe_forward's), the split (miss_dst, counts as smoe_expert_group), the hits into rows[i] (i = t * k + s, the
+ * entry's row) and the shared expert into rows[T * k + t] (times sigmoid of its gate): rows is [(T * k + T)][n_embd]
+ * f32.  The caller then writes each miss's row (rows[miss_dst[j]], j < counts[2]: its own expert pool, or
+ * smoe_expert_grouped over another table), and smoe_verify_end forms y [T][n_embd] from rows and weights as
+ * smoe_forward's combine does.  w->gate_exps / up_exps / down_exps are not read (may be NULL).  Both calls take the
+ * same workspace (smoe_verify_workspace_bytes of at least n_tokens).  With every expert in the table, begin + end
+ * give smoe_forward's y bitwise; a miss computed by smoe_expert_grouped gives the same row as a hit.
+ * Replaces the verify window's moe_hit_select_multi + moe_hit_grouped_s2_multi + moe_hit_add + moe_combine
+ * (s2_expert_grouped.hpp:92-99). */
+size_t smoe_verify_workspace_bytes(const smoe_geom* g, int32_t max_tokens);
+smoe_status smoe_verify_begin(const smoe_geom* g, const smoe_weights* w, const uint64_t* expert_ptr, const float* x,
+                              int32_t n_tokens, float* rows, int32_t* ids, float* weights, int32_t* miss_dst,
+                              int32_t* counts, void* workspace, size_t workspace_bytes, void* hip_stream);
+smoe_status smoe_verify_end(const smoe_geom* g, int32_t n_tokens, const float* rows, const float* weights,
+                            int32_t add_shared, float* y, void* workspace, size_t workspace_bytes, void* hip_stream);
+
 /* ---------------------------------------------------------------------------------------------- no allocation */
 
 /* Bytes of the library's static device scratch (one array per GPU, held from the library's load until the

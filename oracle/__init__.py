@@ -13,7 +13,7 @@ import ctypes as C
 import os
 import subprocess
 from dataclasses import dataclass
-from typing import Optional
+from typing import Dict, Optional
 
 import numpy as np
 
@@ -107,6 +107,8 @@ def _set_sigs(L):
         "or_native_part": (f32, [i32, vp, vp, i32]),
         "or_native_gemv": (i32, [i32, vp, vp, i32, i32, i32, vp]),
         "or_native_gemv_double": (i32, [i32, vp, vp, i32, i32, i32, vp]),
+        "or_expert_group": (i32, [vp, i32, i32, i32, vp, vp, vp, vp, vp, vp, vp]),
+        "or_expert_dev": (i32, [i32, vp, i32, i32, vp, vp]),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(L, name)
@@ -649,4 +651,40 @@ def ref_gguf_list(path: str):
     buf = C.create_string_buffer(1 << 20)
     rc = R.ref_gguf_list(path.encode(), buf, 1 << 20)
     return rc, buf.value.decode()
+
+
+# ---- the expert tier (smoe_cache.c)
+
+def expert_group(ids: np.ndarray, kpt: int, n_expert: int, resident: np.ndarray) -> Dict:
+    """The oracle's hit/miss split and grouping: grp_expert, grp_start, ent_dst, ent_tok, miss_dst, counts."""
+    ids = np.ascontiguousarray(ids, dtype=np.int32).ravel()
+    res = np.ascontiguousarray(resident, dtype=np.uint8)
+    n = ids.size
+    G = max(1, min(n, n_expert))
+    out = dict(grp_expert=np.full(G, -1, np.int32), grp_start=np.zeros(G + 1, np.int32),
+               ent_dst=np.full(max(n, 1), -1, np.int32), ent_tok=np.full(max(n, 1), -1, np.int32),
+               miss_dst=np.full(max(n, 1), -1, np.int32), counts=np.zeros(4, np.int32))
+    rc = lib().or_expert_group(_p(ids), n, kpt, n_expert, _p(res), _p(out["grp_expert"]), _p(out["grp_start"]),
+                               _p(out["ent_dst"]), _p(out["ent_tok"]), _p(out["miss_dst"]), _p(out["counts"]))
+    if rc != 0:
+        raise ValueError("or_expert_group refused its arguments")
+    return out
+
+
+def expert_blob(g, w, e: int) -> np.ndarray:
+    """Expert e's blob [gate rows | up rows | down rows] from the planes of the host weights."""
+    gu = row_bytes(g.w_type, g.n_embd) * g.n_ff
+    dn = row_bytes(g.w_type, g.n_ff) * g.n_embd
+    return np.concatenate([w.gate_exps[e * gu:(e + 1) * gu], w.up_exps[e * gu:(e + 1) * gu],
+                           w.down_exps[e * dn:(e + 1) * dn]])
+
+
+def expert_dev(wtype: int, blob: np.ndarray, H: int, F: int, xq_row: np.ndarray) -> np.ndarray:
+    """One routed expert on one token's q8_1 row under the decode contract."""
+    out = np.empty(H, np.float32)
+    b = np.ascontiguousarray(blob, dtype=np.uint8)
+    x = np.ascontiguousarray(xq_row, dtype=np.uint8)
+    if lib().or_expert_dev(wtype, _p(b), H, F, _p(x), _p(out)) != 0:
+        raise ValueError("or_expert_dev: type is not Q2_0 or IQ2_S")
+    return out
 

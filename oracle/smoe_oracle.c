@@ -902,6 +902,14 @@ static void expert_chain(int type, const uint8_t* gw, const uint8_t* uw, const u
     free(hq);
 }
 
+/* One routed expert on a blob [gate rows | up rows | down rows] of `type`, one token's q8_1 row xq. */
+int or_expert_dev(int type, const uint8_t* blob, int H, int F, const uint8_t* xq, float* out) {
+    if (type != 42 && type != 22) return -1;
+    const int64_t gu = or_row_bytes(type, H) * F;
+    expert_chain(type, blob, blob + gu, blob + 2 * gu, H, F, xq, out, NULL, 1);
+    return 0;
+}
+
 /* Router logits of one token: bf16 x and W (router_dtype 0, the repo's contract) or f32 x and W (1). */
 static void router_logits(const or_geom* g, const or_weights* w, const float* x, const uint16_t* xb, int dev,
                           float* out) {

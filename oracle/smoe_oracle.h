@@ -100,6 +100,12 @@ int or_native_gemv_double(int type, const uint8_t* w, const uint8_t* xq, int n_i
 void or_dispatch(const int32_t* ids, int n_tok, int k, int n_expert, int32_t* counts, int32_t* offsets,
                  int32_t* perm, int32_t* slot);
 
+/* ---- the expert tier (smoe_cache.c): the hit/miss split and grouping; one routed expert on a blob
+ * [gate rows | up rows | down rows] under the decode contract */
+int or_expert_group(const int32_t* ids, int n, int kpt, int n_expert, const uint8_t* resident, int32_t* grp_expert,
+                    int32_t* grp_start, int32_t* ent_dst, int32_t* ent_tok, int32_t* miss_dst, int32_t* counts);
+int or_expert_dev(int type, const uint8_t* blob, int H, int F, const uint8_t* xq, float* out);
+
 /* ---- the whole block */
 typedef struct {
     int32_t n_embd, n_ff, n_ff_shared, n_expert, top_k;

@@ -108,6 +108,14 @@ def lib():
             "smoe_model_meta_str": (i32, [vp, C.c_char_p, C.c_char_p, C.c_size_t]),
             "smoe_layer_plan_for": (i32, [vp, i32, i32, i32, vp]),
             "smoe_layer_upload": (i32, [vp, vp, vp, C.c_size_t, vp, vp, vp]),
+            "smoe_expert_blob_bytes": (C.c_size_t, [vp]),
+            "smoe_expert_pack": (i32, [vp, vp, i32, vp, vp]),
+            "smoe_expert_group": (i32, [vp, i32, i32, i32, vp, vp, vp, vp, vp, vp, vp, vp, vp]),
+            "smoe_expert_grouped_workspace_bytes": (C.c_size_t, [vp, i32, i32, i32]),
+            "smoe_expert_grouped": (i32, [vp, vp, vp, vp, vp, vp, i32, i32, vp, i32, vp, i32, vp, C.c_size_t, vp]),
+            "smoe_verify_workspace_bytes": (C.c_size_t, [vp, i32]),
+            "smoe_verify_begin": (i32, [vp, vp, vp, vp, i32, vp, vp, vp, vp, vp, vp, C.c_size_t, vp]),
+            "smoe_verify_end": (i32, [vp, i32, vp, vp, i32, vp, vp, C.c_size_t, vp]),
         }
         for name, (res, args) in sigs.items():
             fn = getattr(L, name)
@@ -744,4 +752,117 @@ class Model:
                                   view(hc.up, hd * hc.hc_lr * 2).view(torch.int16),
                                   view(hc.inject, hc.hc * hd * 2).view(torch.int16), eps=float(hc.eps))
         return g, weights, hcx
+
+
+# ------------------------------------------------------------------------------------------------ expert tier
+
+def expert_blob_bytes(g: Geom) -> int:
+    """Bytes of one routed expert's blob [gate rows | up rows | down rows] (smoe_expert_blob_bytes)."""
+    n = int(lib().smoe_expert_blob_bytes(C.byref(g.c())))
+    if n == 0:
+        raise SmoeError(-1, lib().smoe_last_error().decode())
+    return n
+
+
+def pack_expert(g: Geom, weights: Dict, expert: int, blob, stream=None):
+    """Copies expert `expert`'s rows from the planes in `weights` into `blob` (uint8, expert_blob_bytes)."""
+    import torch
+    _need(blob, "blob", torch.uint8, numel=expert_blob_bytes(g))
+    _check(lib().smoe_expert_pack(C.byref(g.c()), C.byref(_weights_c(weights)), expert, blob.data_ptr(),
+                                  _stream(stream)))
+    return blob
+
+
+def expert_table(ptrs, device="cuda"):
+    """A device table of one blob address per expert (0: not held) from a list of tensors or None."""
+    import torch
+    a = [0 if t is None else t.data_ptr() for t in ptrs]
+    return torch.tensor(a, dtype=torch.int64, device=device)
+
+
+def expert_group(ids, k_per_tok: int, n_expert: int, table, stream=None) -> Dict:
+    """The hit/miss split of the routed entries `ids` (int32, T * k_per_tok) by the expert table (int64 device
+    addresses, 0 = not held), on the device (smoe_expert_group): grp_ptr, grp_expert, grp_start, ent_dst,
+    ent_tok, miss_dst and counts {groups, hits, misses, 0}."""
+    import torch
+    _need(ids, "ids", torch.int32)
+    _need(table, "table", torch.int64, numel=n_expert)
+    n = ids.numel()
+    G = max(1, min(n, n_expert))
+    dev = ids.device
+    out = dict(grp_ptr=torch.zeros(G, dtype=torch.int64, device=dev),
+               grp_expert=torch.full((G,), -1, dtype=torch.int32, device=dev),
+               grp_start=torch.zeros(G + 1, dtype=torch.int32, device=dev),
+               ent_dst=torch.full((max(n, 1),), -1, dtype=torch.int32, device=dev),
+               ent_tok=torch.full((max(n, 1),), -1, dtype=torch.int32, device=dev),
+               miss_dst=torch.full((max(n, 1),), -1, dtype=torch.int32, device=dev),
+               counts=torch.zeros(4, dtype=torch.int32, device=dev))
+    _check(lib().smoe_expert_group(ids.data_ptr(), n, k_per_tok, n_expert, table.data_ptr(),
+                                   out["grp_ptr"].data_ptr(), out["grp_start"].data_ptr(),
+                                   out["grp_expert"].data_ptr(), out["ent_dst"].data_ptr(), out["ent_tok"].data_ptr(),
+                                   out["miss_dst"].data_ptr(), out["counts"].data_ptr(), _stream(stream)))
+    return out
+
+
+def expert_grouped(g: Geom, groups: Dict, x_q8, n_tokens: int, out, cap_groups: int = None, cap_entries: int = None,
+                   stream=None):
+    """Grouped expert evaluation (smoe_expert_grouped) over the lists in `groups` (expert_group's keys): each
+    entry's expert output row written to out[ent_dst] (out: (rows, n_embd) f32)."""
+    import torch
+    cg = groups["grp_ptr"].numel() if cap_groups is None else cap_groups
+    ce = groups["ent_dst"].numel() if cap_entries is None else cap_entries
+    _need(x_q8, "x_q8", torch.uint8, numel=n_tokens * (g.n_embd // 32) * 36)
+    _need(out, "out", torch.float32)
+    nb = int(lib().smoe_expert_grouped_workspace_bytes(C.byref(g.c()), n_tokens, cg, ce))
+    ws = torch.empty(max(nb, 1), dtype=torch.uint8, device=out.device)
+    _check(lib().smoe_expert_grouped(C.byref(g.c()), groups["grp_ptr"].data_ptr(), groups["grp_start"].data_ptr(),
+                                     groups["ent_dst"].data_ptr(), groups["ent_tok"].data_ptr(),
+                                     groups["counts"].data_ptr(), cg, ce, x_q8.data_ptr(), n_tokens, out.data_ptr(),
+                                     out.shape[0], ws.data_ptr(), nb, _stream(stream)))
+    return out
+
+
+class VerifyWindow:
+    """The verify window with the hit/miss split (smoe_verify_begin / smoe_verify_end): `begin` routes the tokens,
+    computes the hits from the expert table and the shared expert into rows, and returns the misses for the caller
+    to fill; `end` combines the rows into y."""
+
+    def __init__(self, g: Geom, weights: Dict, max_tokens: int, device="cuda"):
+        import torch
+        self.g, self.w = g, weights
+        self._gc, self._wc = g.c(), _weights_c(weights)
+        self.ws_bytes = int(lib().smoe_verify_workspace_bytes(C.byref(self._gc), max_tokens))
+        if self.ws_bytes == 0:
+            raise SmoeError(-1, f"verify window refused for {max_tokens} tokens: {lib().smoe_last_error().decode()}")
+        self.ws = torch.empty(self.ws_bytes, dtype=torch.uint8, device=device)
+        self.max_tokens = max_tokens
+
+    def begin(self, x, table, stream=None) -> Dict:
+        import torch
+        _need(x, "x", torch.float32)
+        T, H, K = x.shape[0], self.g.n_embd, self.g.top_k
+        if T > self.max_tokens:
+            raise SmoeError(-1, f"{T} tokens exceed the window's {self.max_tokens}")
+        _need(table, "table", torch.int64, numel=self.g.n_expert)
+        dev = x.device
+        r = dict(rows=torch.zeros((T * K + T, H), dtype=torch.float32, device=dev),
+                 ids=torch.empty((T, K), dtype=torch.int32, device=dev),
+                 weights=torch.empty((T, K), dtype=torch.float32, device=dev),
+                 miss_dst=torch.full((max(T * K, 1),), -1, dtype=torch.int32, device=dev),
+                 counts=torch.zeros(4, dtype=torch.int32, device=dev))
+        _check(lib().smoe_verify_begin(C.byref(self._gc), C.byref(self._wc), table.data_ptr(), x.data_ptr(), T,
+                                       r["rows"].data_ptr(), r["ids"].data_ptr(), r["weights"].data_ptr(),
+                                       r["miss_dst"].data_ptr(), r["counts"].data_ptr(), self.ws.data_ptr(),
+                                       self.ws_bytes, _stream(stream)))
+        return r
+
+    def end(self, r: Dict, add_shared: bool = True, y=None, stream=None):
+        import torch
+        T = r["ids"].shape[0]
+        if y is None:
+            y = torch.empty((T, self.g.n_embd), dtype=torch.float32, device=r["rows"].device)
+        _check(lib().smoe_verify_end(C.byref(self._gc), T, r["rows"].data_ptr(), r["weights"].data_ptr(),
+                                     int(add_shared), y.data_ptr(), self.ws.data_ptr(), self.ws_bytes,
+                                     _stream(stream)))
+        return y
 

@@ -36,8 +36,8 @@ COMMON = [
     "-Wall", "-Wno-unused-result",
 ]
 
-SOURCES = ["smoe_decode.hip", "smoe_prefill.hip", "smoe_iq2.hip", "smoe_hc.hip", "smoe_native.hip", "smoe_synth.hip",
-           "smoe_api.cpp", "smoe_gguf.cpp"]
+SOURCES = ["smoe_decode.hip", "smoe_prefill.hip", "smoe_iq2.hip", "smoe_hc.hip", "smoe_native.hip", "smoe_cache.hip",
+           "smoe_synth.hip", "smoe_api.cpp", "smoe_gguf.cpp"]
 
 
 def _compile(src: str) -> str:

@@ -216,7 +216,7 @@ const char* smoe_status_str(smoe_status s) {
 
 const char* smoe_last_error(void) { return g_last.c_str(); }
 
-int32_t smoe_abi_version(void) { return 108; }
+int32_t smoe_abi_version(void) { return 109; }
 
 size_t smoe_workspace_bytes(const smoe_geom* g, int32_t max_tokens) {
     if (check_geom(g) != SMOE_OK || max_tokens < 0) return 0;
@@ -227,6 +227,11 @@ namespace {
 bool overlaps(const void* a, const void* b, size_t bytes) {
     const uintptr_t x = reinterpret_cast<uintptr_t>(a), z = reinterpret_cast<uintptr_t>(b);
     return x < z + bytes && z < x + bytes;
+}
+// [a, a + na) and [b, b + nb) share a byte
+bool overlaps_n(const void* a, size_t na, const void* b, size_t nb) {
+    const uintptr_t x = reinterpret_cast<uintptr_t>(a), z = reinterpret_cast<uintptr_t>(b);
+    return x < z + nb && z < x + na;
 }
 
 // Every check of a block call that can refuse it, made before its first launch (smoe_ffn_run runs it ahead of
@@ -281,6 +286,37 @@ smoe_status check_forward(const smoe_geom* g, const smoe_weights* w, const float
     if (workspace_bytes < L.total)
         return fail(SMOE_ESIZE, "workspace is " + std::to_string(workspace_bytes) + " bytes, needs " +
                                     std::to_string(L.total));
+    return SMOE_OK;
+}
+
+#define SMOE_TRY_S(call)                    \
+    do {                                    \
+        const smoe_status _s = (call);      \
+        if (_s != SMOE_OK) return _s;       \
+    } while (0)
+
+// The native shared expert (its projections in their own types): q8_1 of x, gate and up, SwiGLU + q8_1, down
+// times sigmoid(sg[t]) into out[t] (T rows of n_embd), in the workspace's native-chain slots.
+smoe_status native_shared(const smoe_geom& g, const smoe_weights* w, const float* x, int T, uint8_t* ws,
+                          const Layout& L, float* out, const float* sg, hipStream_t st) {
+    const int H = g.n_embd, Fn = g.n_ff_shared;
+    uint8_t* nxq = ws + L.nxq;
+    float* ngu = reinterpret_cast<float*>(ws + L.ngu);
+    uint8_t* nhq = ws + L.nhq;
+    SMOE_TRY(smoe::launch_prep(x, (int64_t)T * H, nxq, nullptr, st), "shared q8_1");
+    auto gemv = [&](int type, const void* wt, const uint8_t* xq, int n_in, int n_out, float* y,
+                    const float* gate) -> hipError_t {
+        const uint8_t* wb = static_cast<const uint8_t*>(wt);
+        if (smoe::native_type(type)) return smoe::launch_mmvq_native(type, wb, xq, n_in, n_out, T, y, n_out, gate, st);
+        hipError_t e = type == SMOE_IQ2_S ? smoe::launch_iq2_mmvq(wb, xq, n_in, n_out, T, y, st)
+                                          : smoe::launch_q2_mmvq(wb, xq, n_in, n_out, T, y, st);
+        if (e == hipSuccess && gate) e = smoe::launch_sigmoid_rows(y, T, n_out, gate, st);
+        return e;
+    };
+    SMOE_TRY(gemv(sh_gate_t(g), w->gate_sh, nxq, H, Fn, ngu, nullptr), "shared gate");
+    SMOE_TRY(gemv(sh_up_t(g), w->up_sh, nxq, H, Fn, ngu + (size_t)T * Fn, nullptr), "shared up");
+    SMOE_TRY(smoe::launch_swiglu_q8(ngu, ngu + (size_t)T * Fn, (int64_t)T * Fn, nhq, st), "shared swiglu");
+    SMOE_TRY(gemv(sh_down_t(g), w->down_sh, nhq, Fn, H, out, sg), "shared down");
     return SMOE_OK;
 }
 
@@ -429,26 +465,7 @@ smoe_status forward_impl(const smoe_geom* g, const smoe_weights* w, float* x_io,
             SMOE_TRY(smoe::launch_q2_down(de, ds, himg, L.h_blocks, sg, items, H, F, Fs, n_items, Y, st), "down");
     }
     SMOE_MARK();
-    if (nat) {  // the native shared expert: q8_1 of x, gate and up, SwiGLU + q8_1, down times sigmoid(sg) into Y[P + t]
-        const int Fn = g->n_ff_shared;
-        uint8_t* nxq = ws + L.nxq;
-        float* ngu = reinterpret_cast<float*>(ws + L.ngu);
-        uint8_t* nhq = ws + L.nhq;
-        SMOE_TRY(smoe::launch_prep(x_io, (int64_t)T * H, nxq, nullptr, st), "shared q8_1");
-        auto gemv = [&](int type, const void* wt, const uint8_t* xq, int n_in, int n_out, float* out,
-                        const float* gate) -> hipError_t {
-            const uint8_t* wb = static_cast<const uint8_t*>(wt);
-            if (smoe::native_type(type)) return smoe::launch_mmvq_native(type, wb, xq, n_in, n_out, T, out, n_out, gate, st);
-            hipError_t e = type == SMOE_IQ2_S ? smoe::launch_iq2_mmvq(wb, xq, n_in, n_out, T, out, st)
-                                              : smoe::launch_q2_mmvq(wb, xq, n_in, n_out, T, out, st);
-            if (e == hipSuccess && gate) e = smoe::launch_sigmoid_rows(out, T, n_out, gate, st);
-            return e;
-        };
-        SMOE_TRY(gemv(sh_gate_t(*g), w->gate_sh, nxq, H, Fn, ngu, nullptr), "shared gate");
-        SMOE_TRY(gemv(sh_up_t(*g), w->up_sh, nxq, H, Fn, ngu + (size_t)T * Fn, nullptr), "shared up");
-        SMOE_TRY(smoe::launch_swiglu_q8(ngu, ngu + (size_t)T * Fn, (int64_t)T * Fn, nhq, st), "shared swiglu");
-        SMOE_TRY(gemv(sh_down_t(*g), w->down_sh, nhq, Fn, H, Y + (size_t)P * H, sg), "shared down");
-    }
+    if (nat) SMOE_TRY_S(native_shared(*g, w, x_io, T, ws, L, Y + (size_t)P * H, sg, st));
     if (!small_down)
         SMOE_TRY(smoe::launch_combine(Y, slot, wts, K, H, P, T, (has_sh && add_shared) ? 1 : 0, y, st), "combine");
     else if (nat && add_shared)  // the fused combine left the shared rows out: the same last addition, after it
@@ -933,6 +950,279 @@ smoe_status smoe_synth_normal(uint64_t seed, uint64_t stream_id, int64_t n, floa
     if (n == 0) return ok();
     if (!out) return fail(SMOE_ENULL, "synth_normal: NULL buffer");
     SMOE_TRY(smoe::launch_synth_normal(seed, stream_id, n, sigma, out, stream_of(hip_stream)), "synth_normal");
+    return ok();
+}
+
+}  // extern "C"
+
+// ------------------------------------------------------------------------------------------------ expert tier
+namespace {
+
+int64_t routed_row_bytes(int type, int64_t n) { return type == SMOE_Q2_0 ? n / 64 * 18 : n / 256 * 82; }
+
+// [gate rows | up rows | down rows] of one routed expert
+size_t blob_bytes(const smoe_geom& g) {
+    return (size_t)(2 * (int64_t)g.n_ff * routed_row_bytes(g.w_type, g.n_embd) +
+                    (int64_t)g.n_embd * routed_row_bytes(g.w_type, g.n_ff));
+}
+
+// smoe_expert_grouped's workspace: x images, the item table, the checked tokens and rows, the h images
+struct GroupedLayout {
+    size_t ximg, items, etok, edst, himg, total;
+};
+GroupedLayout grouped_layout(const smoe_geom& g, int64_t T, int64_t cap_groups, int64_t cap_entries) {
+    GroupedLayout L{};
+    size_t o = 0;
+    auto take = [&](size_t bytes) {
+        const size_t at = o;
+        o = up(o + bytes);
+        return at;
+    };
+    L.ximg = take(smoe::img_bytes(T * (g.n_embd / 32)));
+    L.items = take((size_t)cap_groups * 32);
+    L.etok = take((size_t)cap_entries * 4);
+    L.edst = take((size_t)cap_entries * 4);
+    L.himg = take(smoe::img_bytes(cap_entries * (g.n_ff / 32)));
+    L.total = o;
+    return L;
+}
+
+// The verify window's workspace: the router's outputs, the group lists, the item table (groups, then the shared
+// chunks of a fused shared expert), the h images of every entry and shared token, the combine's slots, and the
+// native shared expert's chain (in `nat`, whose other offsets are unused).
+struct VerifyLayout {
+    size_t ximg, logits, sg, grp_ptr, grp_start, ent_dst, ent_tok, items, himg, slot, total;
+    int cap_groups, n_items, h_blocks;
+    Layout nat;
+};
+VerifyLayout verify_layout(const smoe_geom& g, int64_t T) {
+    VerifyLayout L{};
+    const int64_t H = g.n_embd, E = g.n_expert, P = T * g.top_k;
+    const int64_t Fmax = (sh_fused(g) && g.n_ff_shared > g.n_ff) ? g.n_ff_shared : g.n_ff;
+    L.cap_groups = (int)(P < E ? P : E);
+    L.n_items = L.cap_groups + (sh_fused(g) ? smoe::shared_items((int)T) : 0);
+    L.h_blocks = (int)(Fmax / 32);
+    size_t o = 0;
+    auto take = [&](size_t bytes) {
+        const size_t at = o;
+        o = up(o + bytes);
+        return at;
+    };
+    L.ximg = take(smoe::img_bytes(T * (H / 32)));
+    L.logits = take((size_t)T * E * 4);
+    L.sg = take((size_t)T * 4);
+    L.grp_ptr = take((size_t)L.cap_groups * 8);
+    L.grp_start = take((size_t)(L.cap_groups + 1) * 4);
+    L.ent_dst = take((size_t)P * 4);
+    L.ent_tok = take((size_t)P * 4);
+    L.items = take((size_t)L.n_items * 32);
+    L.himg = take(smoe::img_bytes((P + T) * L.h_blocks));
+    L.slot = take((size_t)P * 4);
+    if (sh_native(g)) {
+        const int64_t Fs = g.n_ff_shared;
+        L.nat.nxq = take((size_t)T * (H / 32) * 36);
+        L.nat.ngu = take((size_t)2 * T * Fs * 4);
+        L.nat.nhq = take((size_t)T * (Fs / 32) * 36);
+    }
+    L.total = o;
+    return L;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t smoe_expert_blob_bytes(const smoe_geom* g) { return check_geom(g) == SMOE_OK ? blob_bytes(*g) : 0; }
+
+smoe_status smoe_expert_pack(const smoe_geom* g, const smoe_weights* w, int32_t expert, void* blob, void* hip_stream) {
+    smoe_status s = check_geom(g);
+    if (s != SMOE_OK) return s;
+    if (!w || !w->gate_exps || !w->up_exps || !w->down_exps || !blob)
+        return fail(SMOE_ENULL, "expert_pack: NULL routed planes or blob");
+    if (expert < 0 || expert >= g->n_expert) return fail(SMOE_EINVAL, "expert_pack: expert id out of range");
+    const size_t gu = (size_t)g->n_ff * (size_t)routed_row_bytes(g->w_type, g->n_embd);
+    const size_t dn = (size_t)g->n_embd * (size_t)routed_row_bytes(g->w_type, g->n_ff);
+    uint8_t* b = static_cast<uint8_t*>(blob);
+    const hipStream_t st = stream_of(hip_stream);
+    SMOE_TRY(hipMemcpyAsync(b, static_cast<const uint8_t*>(w->gate_exps) + (size_t)expert * gu, gu, hipMemcpyDefault, st),
+             "expert_pack gate");
+    SMOE_TRY(hipMemcpyAsync(b + gu, static_cast<const uint8_t*>(w->up_exps) + (size_t)expert * gu, gu, hipMemcpyDefault,
+                            st),
+             "expert_pack up");
+    SMOE_TRY(hipMemcpyAsync(b + 2 * gu, static_cast<const uint8_t*>(w->down_exps) + (size_t)expert * dn, dn,
+                            hipMemcpyDefault, st),
+             "expert_pack down");
+    return ok();
+}
+
+smoe_status smoe_expert_group(const int32_t* ids, int32_t n, int32_t k_per_tok, int32_t n_expert,
+                              const uint64_t* expert_ptr, uint64_t* grp_ptr, int32_t* grp_start, int32_t* grp_expert,
+                              int32_t* ent_dst, int32_t* ent_tok, int32_t* miss_dst, int32_t* counts,
+                              void* hip_stream) {
+    if (n < 0 || n > smoe::kMaxGroupEntries) return fail(SMOE_EINVAL, "expert_group: n must be in 0..4096");
+    if (k_per_tok < 1) return fail(SMOE_EINVAL, "expert_group: k_per_tok must be at least 1");
+    if (n_expert < 1 || n_expert > smoe::kMaxGroupExperts) return fail(SMOE_EINVAL, "expert_group: n_expert must be in 1..1024");
+    if (!expert_ptr || !grp_ptr || !grp_start || !ent_dst || !ent_tok || !miss_dst || !counts || (n > 0 && !ids))
+        return fail(SMOE_ENULL, "expert_group: NULL buffer");
+    if (!aligned(expert_ptr, 8) || !aligned(grp_ptr, 8)) return fail(SMOE_EALIGN, "expert_group: pointer tables must be 8-byte aligned");
+    SMOE_TRY(smoe::launch_expert_group(ids, n, k_per_tok, n_expert, expert_ptr, grp_ptr, grp_start, grp_expert, ent_dst,
+                                       ent_tok, miss_dst, counts, nullptr, 0, 0, n, 0, nullptr, stream_of(hip_stream)),
+             "expert_group");
+    return ok();
+}
+
+size_t smoe_expert_grouped_workspace_bytes(const smoe_geom* g, int32_t n_tokens, int32_t cap_groups,
+                                           int32_t cap_entries) {
+    if (check_geom(g) != SMOE_OK || n_tokens < 0 || cap_groups < 0 || cap_entries < 0) return 0;
+    return grouped_layout(*g, n_tokens, cap_groups, cap_entries).total;
+}
+
+smoe_status smoe_expert_grouped(const smoe_geom* g, const uint64_t* grp_ptr, const int32_t* grp_start,
+                                const int32_t* ent_dst, const int32_t* ent_tok, const int32_t* counts,
+                                int32_t cap_groups, int32_t cap_entries, const uint8_t* x_q8_1, int32_t n_tokens,
+                                float* out, int32_t n_out_rows, void* workspace, size_t workspace_bytes,
+                                void* hip_stream) {
+    smoe_status s = check_geom(g);
+    if (s != SMOE_OK) return s;
+    if (n_tokens < 0 || cap_groups < 0 || cap_entries < 0 || n_out_rows < 0)
+        return fail(SMOE_EINVAL, "expert_grouped: negative size");
+    if (cap_groups > (1 << 20) || cap_entries > (1 << 24)) return fail(SMOE_EINVAL, "expert_grouped: caps too large");
+    if (n_tokens == 0 || cap_groups == 0 || cap_entries == 0 || n_out_rows == 0) return ok();
+    if (!grp_ptr || !grp_start || !ent_dst || !ent_tok || !counts || !x_q8_1 || !out || !workspace)
+        return fail(SMOE_ENULL, "expert_grouped: NULL buffer");
+    const GroupedLayout L = grouped_layout(*g, n_tokens, cap_groups, cap_entries);
+    if (workspace_bytes < L.total) return fail(SMOE_ESIZE, "expert_grouped: workspace too small");
+    if (!aligned(workspace, kAlign)) return fail(SMOE_EALIGN, "expert_grouped: workspace must be 256-byte aligned");
+    if (!aligned(grp_ptr, 8) || !aligned(x_q8_1, 4) || !aligned(out, 4))
+        return fail(SMOE_EALIGN, "expert_grouped: grp_ptr must be 8-byte and x, out 4-byte aligned");
+    const int H = g->n_embd, F = g->n_ff;
+    const bool iq2 = g->w_type == SMOE_IQ2_S;
+    uint8_t* ws = static_cast<uint8_t*>(workspace);
+    uint32_t* ximg = reinterpret_cast<uint32_t*>(ws + L.ximg);
+    int4* items = reinterpret_cast<int4*>(ws + L.items);
+    int32_t* etok = reinterpret_cast<int32_t*>(ws + L.etok);
+    int32_t* edst = reinterpret_cast<int32_t*>(ws + L.edst);
+    uint32_t* himg = reinterpret_cast<uint32_t*>(ws + L.himg);
+    const int hb = F / 32;
+    const hipStream_t st = stream_of(hip_stream);
+    SMOE_TRY(smoe::launch_q8_images(x_q8_1, (int64_t)n_tokens * (H / 32), iq2 ? 1 : 0, ximg, st), "grouped images");
+    SMOE_TRY(smoe::launch_group_items(grp_ptr, grp_start, ent_tok, ent_dst, counts, cap_groups, cap_entries, n_tokens,
+                                      n_out_rows, items, etok, edst, st),
+             "grouped items");
+    if (iq2) {
+        SMOE_TRY(smoe::launch_iq2_gu(nullptr, nullptr, nullptr, nullptr, ximg, items, etok, 1, H, F, 0, 0, cap_groups,
+                                     himg, hb, st, nullptr, 0, grp_ptr),
+                 "grouped gate/up");
+        SMOE_TRY(smoe::launch_iq2_down(nullptr, nullptr, himg, hb, nullptr, items, H, F, 0, cap_groups, out, st,
+                                       grp_ptr, edst),
+                 "grouped down");
+    } else {
+        SMOE_TRY(smoe::launch_q2_gu(nullptr, nullptr, nullptr, nullptr, ximg, items, etok, 1, H, F, 0, 0, cap_groups,
+                                    himg, hb, st, nullptr, 0, grp_ptr),
+                 "grouped gate/up");
+        SMOE_TRY(smoe::launch_q2_down(nullptr, nullptr, himg, hb, nullptr, items, H, F, 0, cap_groups, out, st, grp_ptr,
+                                      edst),
+                 "grouped down");
+    }
+    return ok();
+}
+
+size_t smoe_verify_workspace_bytes(const smoe_geom* g, int32_t max_tokens) {
+    if (check_geom(g) != SMOE_OK || max_tokens < 0 || (int64_t)max_tokens * g->top_k > smoe::kMaxGroupEntries) return 0;
+    return verify_layout(*g, max_tokens).total;
+}
+
+smoe_status smoe_verify_begin(const smoe_geom* g, const smoe_weights* w, const uint64_t* expert_ptr, const float* x,
+                              int32_t n_tokens, float* rows, int32_t* ids, float* weights, int32_t* miss_dst,
+                              int32_t* counts, void* workspace, size_t workspace_bytes, void* hip_stream) {
+    smoe_status s = check_geom(g);
+    if (s != SMOE_OK) return s;
+    if (!w) return fail(SMOE_ENULL, "verify_begin: weights is NULL");
+    if (n_tokens < 0) return fail(SMOE_EINVAL, "verify_begin: n_tokens is negative");
+    if ((int64_t)n_tokens * g->top_k > smoe::kMaxGroupEntries)
+        return fail(SMOE_EINVAL, "verify_begin: n_tokens * top_k exceeds 4096");
+    if (n_tokens == 0) return ok();
+    const bool has_sh = g->sh_type >= 0, nat = sh_native(*g), shf = has_sh && !nat;
+    if (!w->router) return fail(SMOE_ENULL, "verify_begin: the router is NULL");
+    if (has_sh && (!w->gate_sh || !w->up_sh || !w->down_sh || !w->gate_inp_sh))
+        return fail(SMOE_ENULL, "verify_begin: a shared expert tensor is NULL (set sh_type = -1 for a layer without one)");
+    if (!expert_ptr || !x || !rows || !ids || !weights || !miss_dst || !counts || !workspace)
+        return fail(SMOE_ENULL, "verify_begin: NULL buffer");
+    const VerifyLayout L = verify_layout(*g, n_tokens);
+    if (workspace_bytes < L.total) return fail(SMOE_ESIZE, "verify_begin: workspace too small");
+    if (!aligned(workspace, kAlign)) return fail(SMOE_EALIGN, "verify_begin: workspace must be 256-byte aligned");
+    if (!aligned(expert_ptr, 8) || !aligned(x, 16) || !aligned(rows, 4) || !aligned(ids, 4) || !aligned(weights, 4))
+        return fail(SMOE_EALIGN, "verify_begin: expert_ptr 8-byte, x 16-byte, rows, ids and weights 4-byte aligned");
+    const int T = n_tokens, H = g->n_embd, E = g->n_expert, K = g->top_k, F = g->n_ff, P = T * K;
+    const int Fs = shf ? g->n_ff_shared : 0;
+    if (overlaps_n(x, (size_t)T * H * 4, rows, (size_t)(P + T) * H * 4))
+        return fail(SMOE_EINVAL, "verify_begin: rows overlaps x");
+    const bool iq2 = g->w_type == SMOE_IQ2_S, f32r = g->router_dtype == SMOE_ROUTER_F32;
+    uint8_t* ws = static_cast<uint8_t*>(workspace);
+    uint32_t* ximg = reinterpret_cast<uint32_t*>(ws + L.ximg);
+    float* logits = reinterpret_cast<float*>(ws + L.logits);
+    float* sg = reinterpret_cast<float*>(ws + L.sg);
+    uint64_t* grp_ptr = reinterpret_cast<uint64_t*>(ws + L.grp_ptr);
+    int32_t* grp_start = reinterpret_cast<int32_t*>(ws + L.grp_start);
+    int32_t* ent_dst = reinterpret_cast<int32_t*>(ws + L.ent_dst);
+    int32_t* ent_tok = reinterpret_cast<int32_t*>(ws + L.ent_tok);
+    int4* items = reinterpret_cast<int4*>(ws + L.items);
+    uint32_t* himg = reinterpret_cast<uint32_t*>(ws + L.himg);
+    const hipStream_t st = stream_of(hip_stream);
+    // the router as the block's decode path runs it (the same x images, logits, shared gate dots and routing)
+    SMOE_TRY(smoe::launch_router(x, nullptr, w->router, has_sh ? w->gate_inp_sh : nullptr, w->logit_bias, H, E,
+                                 E + (has_sh ? 1 : 0), T, logits, E, sg, ximg, 0, iq2 ? 1 : 0, st, nullptr, 0.0f,
+                                 nullptr, nullptr, 0, f32r ? 1 : 0),
+             "verify router");
+    SMOE_TRY(smoe::launch_topk(logits, E, T, E, K, ids, weights, st), "verify topk");
+    SMOE_TRY(smoe::launch_expert_group(ids, P, K, E, expert_ptr, grp_ptr, grp_start, nullptr, ent_dst, ent_tok,
+                                       miss_dst, counts, items, L.cap_groups, L.n_items - L.cap_groups, P, T, nullptr,
+                                       st),
+             "verify split");
+    const uint8_t* gs = static_cast<const uint8_t*>(w->gate_sh);
+    const uint8_t* us = static_cast<const uint8_t*>(w->up_sh);
+    const uint8_t* ds = static_cast<const uint8_t*>(w->down_sh);
+    if (iq2) {
+        SMOE_TRY(smoe::launch_iq2_gu(nullptr, nullptr, gs, us, ximg, items, ent_tok, 1, H, F, Fs, shf ? 1 : 0, L.n_items,
+                                     himg, L.h_blocks, st, nullptr, 0, grp_ptr),
+                 "verify gate/up");
+        SMOE_TRY(smoe::launch_iq2_down(nullptr, ds, himg, L.h_blocks, sg, items, H, F, Fs, L.n_items, rows, st, grp_ptr,
+                                       ent_dst),
+                 "verify down");
+    } else {
+        SMOE_TRY(smoe::launch_q2_gu(nullptr, nullptr, gs, us, ximg, items, ent_tok, 1, H, F, Fs, shf ? 1 : 0, L.n_items,
+                                    himg, L.h_blocks, st, nullptr, 0, grp_ptr),
+                 "verify gate/up");
+        SMOE_TRY(smoe::launch_q2_down(nullptr, ds, himg, L.h_blocks, sg, items, H, F, Fs, L.n_items, rows, st, grp_ptr,
+                                      ent_dst),
+                 "verify down");
+    }
+    if (nat) SMOE_TRY_S(native_shared(*g, w, x, T, ws, L.nat, rows + (size_t)P * H, sg, st));
+    return ok();
+}
+
+smoe_status smoe_verify_end(const smoe_geom* g, int32_t n_tokens, const float* rows, const float* weights,
+                            int32_t add_shared, float* y, void* workspace, size_t workspace_bytes, void* hip_stream) {
+    smoe_status s = check_geom(g);
+    if (s != SMOE_OK) return s;
+    if (n_tokens < 0) return fail(SMOE_EINVAL, "verify_end: n_tokens is negative");
+    if ((int64_t)n_tokens * g->top_k > smoe::kMaxGroupEntries)
+        return fail(SMOE_EINVAL, "verify_end: n_tokens * top_k exceeds 4096");
+    if (n_tokens == 0) return ok();
+    if (!rows || !weights || !y || !workspace) return fail(SMOE_ENULL, "verify_end: NULL buffer");
+    const VerifyLayout L = verify_layout(*g, n_tokens);
+    if (workspace_bytes < L.total) return fail(SMOE_ESIZE, "verify_end: workspace too small");
+    if (!aligned(workspace, kAlign)) return fail(SMOE_EALIGN, "verify_end: workspace must be 256-byte aligned");
+    if (!aligned(rows, 4) || !aligned(weights, 4) || !aligned(y, 4))
+        return fail(SMOE_EALIGN, "verify_end: rows, weights and y must be 4-byte aligned");
+    const int T = n_tokens, H = g->n_embd, K = g->top_k, P = T * K;
+    if (overlaps_n(y, (size_t)T * H * 4, rows, (size_t)(P + T) * H * 4))
+        return fail(SMOE_EINVAL, "verify_end: y overlaps rows");
+    int32_t* slot = reinterpret_cast<int32_t*>(static_cast<uint8_t*>(workspace) + L.slot);
+    const hipStream_t st = stream_of(hip_stream);
+    SMOE_TRY(smoe::launch_iota(slot, P, st), "verify slots");
+    SMOE_TRY(smoe::launch_combine(rows, slot, weights, K, H, P, T, (g->sh_type >= 0 && add_shared) ? 1 : 0, y, st),
+             "verify combine");
     return ok();
 }
 

@@ -546,19 +546,6 @@ __global__ __launch_bounds__(256) void k_router_tile(const float* __restrict__ x
     }
 }
 
-// Inclusive prefix sum over the 64 lanes of a wave by DPP: row shifts by 1, 2, 4 and 8 (zero fill at the
-// start of each 16-lane row), then lane 15 of each row added into the next row (rows 1 and 3) and lane 31
-// into rows 2 and 3.
-__device__ __forceinline__ int wave_inclusive_scan(int x) {
-    x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, true);   // row_shr:1
-    x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, true);   // row_shr:2
-    x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, true);   // row_shr:4
-    x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, true);   // row_shr:8
-    x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xA, 0xF, false);  // row_bcast:15
-    x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xC, 0xF, false);  // row_bcast:31
-    return x;
-}
-
 // ------------------------------------------------------------------------------------------------ top-k
 // Orderable 32-bit key of a logit: NaN ranks as -inf, -0 as +0, then the sign-flip map, so that
 // key(a) > key(b) <=> a > b and key(a) == key(b) <=> a == b.
@@ -917,29 +904,6 @@ __global__ __launch_bounds__(64) void k_topk(const float* __restrict__ logits, i
 // atomics (order-free), offsets by an exclusive scan, ranks by a ballot match inside each wave plus per-wave
 // counts in LDS, 1024 pairs per pass: position = offsets[e] + (number of earlier pairs with expert e) (oracle:
 // or_dispatch).  Also the ascending list of touched experts.  An out-of-range id gets slot -1.
-// N exclusive scans over the 1024 threads of the block at once: a DPP scan inside each wave, the 16 wave
-// totals through LDS (scratch: N x 17 ints), then every wave scans the totals itself (one barrier).
-template <int N>
-__device__ __forceinline__ void block_exclusive_scan_1024(const int (&v)[N], int* scratch, int (&r)[N],
-                                                          int (&total)[N]) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    int incl[N];
-#pragma unroll
-    for (int j = 0; j < N; ++j) incl[j] = wave_inclusive_scan(v[j]);
-    if (lane == 63) {
-#pragma unroll
-        for (int j = 0; j < N; ++j) scratch[17 * j + wave] = incl[j];
-    }
-    __syncthreads();
-#pragma unroll
-    for (int j = 0; j < N; ++j) {
-        const int x = wave_inclusive_scan(lane < 16 ? scratch[17 * j + lane] : 0);
-        const int before = wave > 0 ? __builtin_amdgcn_readlane(x, (wave - 1) & 15) : 0;
-        r[j] = before + incl[j] - v[j];
-        total[j] = __builtin_amdgcn_readlane(x, 15);
-    }
-}
-
 // Per expert (thread tid < E of a 1024-thread block, c its pair count): the exclusive offsets, the position in
 // the touched list and the work-item classes of its pairs in chunks of at most `chunk` columns, longest first:
 // every expert's full chunks, then the remainders of more than chunk / 2 columns, then those of more than
@@ -1564,13 +1528,18 @@ __global__ __launch_bounds__(256) void k_q2_gu(const uint8_t* __restrict__ gate_
                                                 const uint32_t* __restrict__ ximg, const int4* __restrict__ items,
                                                 const int32_t* __restrict__ perm, int k, int H, int F, int Fs,
                                                 uint32_t* __restrict__ himg, int h_blocks, uint8_t* __restrict__ hq,
-                                                int hq_rows) {
+                                                int hq_rows, const uint64_t* __restrict__ eptr) {
     extern __shared__ __align__(16) uint32_t smem[];
     asm volatile("" ::"s"(gate_exps), "s"(up_exps), "s"(gate_sh), "s"(up_sh), "s"(ximg), "s"(himg), "s"(perm), "s"(k),
                  "s"(H), "s"(F), "s"(Fs), "s"(h_blocks));  // every kernarg loaded before the item
     Item item;
     if (!work_item_uniform(items, blockIdx.y, item)) return;
     if ((int)blockIdx.x * 32 >= (item.shared ? Fs : F)) return;
+    if (eptr && !item.shared) {  // a pointer per routed item: its blob holds the gate rows, then the up rows
+        gate_exps = reinterpret_cast<const uint8_t*>(eptr[item.e]);
+        up_exps = gate_exps + (size_t)F * ((size_t)(H >> 7) * 36);
+        item.e = 0;
+    }
     q2_gu_item<NIT, MAXUPL, false, HQ>(item, blockIdx.x, smem, gate_exps, up_exps, gate_sh, up_sh, ximg, perm, k, H, F,
                                        himg, h_blocks, nullptr, hq, hq_rows);
 }
@@ -1772,7 +1741,8 @@ template <int NIT, int MAXUPL>
 __global__ __launch_bounds__(256) void k_q2_down(const uint8_t* __restrict__ down_exps, const uint8_t* __restrict__ down_sh,
                                                   const uint32_t* __restrict__ himg, int h_blocks, const float* __restrict__ sg,
                                                   const int4* __restrict__ items, int H, int F, int Fs, int cps,
-                                                  float* __restrict__ Y) {
+                                                  float* __restrict__ Y, const uint64_t* __restrict__ eptr,
+                                                  const int32_t* __restrict__ dmap) {
     extern __shared__ __align__(16) uint32_t smem[];
     asm volatile("" ::"s"(down_exps), "s"(down_sh), "s"(himg), "s"(sg), "s"(Y), "s"(h_blocks), "s"(H), "s"(F),
                  "s"(Fs), "s"(cps));  // every kernarg loaded before the item
@@ -1782,7 +1752,10 @@ __global__ __launch_bounds__(256) void k_q2_down(const uint8_t* __restrict__ dow
     const RowGeo G = row_geo(Fe);
     const int rpw = NIT * G.rpi;  // rows per wave
     const size_t rb = (size_t)G.dpr * 36;
-    const uint8_t* base = item.shared ? down_sh : down_exps + (size_t)item.e * H * ((size_t)(F >> 7) * 36);
+    const uint8_t* base =
+        item.shared ? down_sh
+        : eptr      ? reinterpret_cast<const uint8_t*>(eptr[item.e]) + (size_t)2 * F * ((size_t)(H >> 7) * 36)
+                    : down_exps + (size_t)item.e * H * ((size_t)(F >> 7) * 36);
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int grp = lane / G.lpr, l = lane - grp * G.lpr;
     const int row0 = blockIdx.x * 4 * rpw + wave * rpw;
@@ -1835,20 +1808,21 @@ __global__ __launch_bounds__(256) void k_q2_down(const uint8_t* __restrict__ dow
                 }
             }
             const float sig = item.shared ? sigmoid(sg[item.tok0 + c0 + c]) : 1.0f;
-            float* yc = Y + (size_t)(item.first + c0 + c) * H;
+            const int orow = (dmap && !item.shared) ? dmap[item.first + c0 + c] : item.first + c0 + c;
+            float* yc = Y + (size_t)orow * H;
             if (NIT == 1 || G.lpr == 4 * NIT) {  // one reduce-scatter: lane l ends with pass (l >> 2) & (NIT - 1)
                 int it;
                 float v = group_sum_rs<NIT>(acc, G.lpr, lane, it);
                 if (item.shared) v = v * sig;
                 const int r = row0 + it * G.rpi + grp;
-                if (r < H && (l & 3) == 0 && (NIT > 1 || l == 0)) yc[r] = v;
+                if (orow >= 0 && r < H && (l & 3) == 0 && (NIT > 1 || l == 0)) yc[r] = v;
             } else {  // each pass on its own: the same butterfly per row
 #pragma unroll
                 for (int it = 0; it < NIT; ++it) {
                     float v = group_sum(acc[it], G.lpr);
                     if (item.shared) v = v * sig;
                     const int r = row0 + it * G.rpi + grp;
-                    if (r < H && l == 0) yc[r] = v;
+                    if (orow >= 0 && r < H && l == 0) yc[r] = v;
                 }
             }
         }
@@ -2589,7 +2563,7 @@ int gemv_shared_chunk() { return kShCols; }
 hipError_t launch_q2_gu(const uint8_t* gate_exps, const uint8_t* up_exps, const uint8_t* gate_sh, const uint8_t* up_sh,
                         const uint32_t* ximg, const int4* items, const int32_t* perm, int k, int H, int F, int Fs,
                         int has_shared, int max_items, uint32_t* himg, int h_blocks, hipStream_t s, uint8_t* hq,
-                        int hq_rows) {
+                        int hq_rows, const uint64_t* eptr) {
     const int Fmax = has_shared && Fs > F ? Fs : F;
     dim3 grid((unsigned)(Fmax / 32), (unsigned)max_items);
     int nit, upl;
@@ -2599,10 +2573,10 @@ hipError_t launch_q2_gu(const uint8_t* gate_exps, const uint8_t* up_exps, const 
 #define SMOE_GU(N, U)                                                                                                \
     if (hq)                                                                                                          \
         hipLaunchKernelGGL((k_q2_gu<N, U, true>), grid, dim3(256), lds, s, gate_exps, up_exps, gate_sh, up_sh, ximg,  \
-                           items, perm, k, H, F, Fs, himg, h_blocks, hq, hq_rows);                                   \
+                           items, perm, k, H, F, Fs, himg, h_blocks, hq, hq_rows, eptr);                             \
     else                                                                                                             \
         hipLaunchKernelGGL((k_q2_gu<N, U, false>), grid, dim3(256), lds, s, gate_exps, up_exps, gate_sh, up_sh, ximg, \
-                           items, perm, k, H, F, Fs, himg, h_blocks, nullptr, 0)
+                           items, perm, k, H, F, Fs, himg, h_blocks, nullptr, 0, eptr)
     SMOE_SHAPE_DISPATCH(SMOE_GU)
 #undef SMOE_GU
     return hipGetLastError();
@@ -2610,7 +2584,7 @@ hipError_t launch_q2_gu(const uint8_t* gate_exps, const uint8_t* up_exps, const 
 
 hipError_t launch_q2_down(const uint8_t* down_exps, const uint8_t* down_sh, const uint32_t* himg, int h_blocks,
                           const float* sg, const int4* items, int H, int F, int Fs, int max_items, float* Y,
-                          hipStream_t s) {
+                          hipStream_t s, const uint64_t* eptr, const int32_t* dmap) {
     int nit, upl, rpw;
     const bool wide = max_items >= kDownWideItems;
     down_shape(F, wide, nit, upl, rpw);  // the caller guarantees the shared width has the same passes and units
@@ -2626,7 +2600,7 @@ hipError_t launch_q2_down(const uint8_t* down_exps, const uint8_t* down_sh, cons
     const size_t lds = (size_t)cps * col_bytes + 16;  // + the dead staging slot
 #define SMOE_DOWN(N, U)                                                                                            \
     hipLaunchKernelGGL((k_q2_down<N, U>), grid, dim3(256), lds, s, down_exps, down_sh, himg, h_blocks, sg, items, H, F, \
-                       Fs, cps, Y)
+                       Fs, cps, Y, eptr, dmap)
     SMOE_SHAPE_DISPATCH(SMOE_DOWN)
 #undef SMOE_DOWN
     return hipGetLastError();

@@ -208,4 +208,40 @@ __device__ __forceinline__ void q8_1_store(int q, uint32_t ds, uint8_t* blk, boo
     if (store && l32 == 0) p[0] = ds;
 }
 
+// Inclusive prefix sum over the 64 lanes of a wave by DPP: row shifts by 1, 2, 4 and 8 (zero fill at the
+// start of each 16-lane row), then lane 15 of each row added into the next row (rows 1 and 3) and lane 31
+// into rows 2 and 3.
+__device__ __forceinline__ int wave_inclusive_scan(int x) {
+    x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, true);   // row_shr:1
+    x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, true);   // row_shr:2
+    x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, true);   // row_shr:4
+    x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, true);   // row_shr:8
+    x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xA, 0xF, false);  // row_bcast:15
+    x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xC, 0xF, false);  // row_bcast:31
+    return x;
+}
+
+// N exclusive scans over the 1024 threads of the block at once: a DPP scan inside each wave, the 16 wave
+// totals through LDS (scratch: N x 17 ints), then every wave scans the totals itself (one barrier).
+template <int N>
+__device__ __forceinline__ void block_exclusive_scan_1024(const int (&v)[N], int* scratch, int (&r)[N],
+                                                          int (&total)[N]) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    int incl[N];
+#pragma unroll
+    for (int j = 0; j < N; ++j) incl[j] = wave_inclusive_scan(v[j]);
+    if (lane == 63) {
+#pragma unroll
+        for (int j = 0; j < N; ++j) scratch[17 * j + wave] = incl[j];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+        const int x = wave_inclusive_scan(lane < 16 ? scratch[17 * j + lane] : 0);
+        const int before = wave > 0 ? __builtin_amdgcn_readlane(x, (wave - 1) & 15) : 0;
+        r[j] = before + incl[j] - v[j];
+        total[j] = __builtin_amdgcn_readlane(x, 15);
+    }
+}
+
 }  // namespace smoe

@@ -164,7 +164,7 @@ __global__ __launch_bounds__(64 * NW) void k_iq2_gu(const uint8_t* __restrict__ 
                                                      const uint32_t* __restrict__ ximg, const int4* __restrict__ items,
                                                      const int32_t* __restrict__ perm, int k, int H, int F, int Fs,
                                                      uint32_t* __restrict__ himg, int h_blocks, uint8_t* __restrict__ hq,
-                                                     int hq_rows) {
+                                                     int hq_rows, const uint64_t* __restrict__ eptr) {
     constexpr int kCols = 2 * NW;
     extern __shared__ __align__(16) uint32_t smem[];
     __shared__ uint2 tab[1024];
@@ -179,6 +179,11 @@ __global__ __launch_bounds__(64 * NW) void k_iq2_gu(const uint8_t* __restrict__ 
     const size_t rb = (size_t)nb * 82;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int rho = wave * (64 / nb) + lane / nb, b = lane % nb;
+    if (eptr && !item.shared) {  // a pointer per routed item: its blob holds the gate rows, then the up rows
+        gate_exps = reinterpret_cast<const uint8_t*>(eptr[item.e]);
+        up_exps = gate_exps + (size_t)F * rb;
+        item.e = 0;
+    }
     const uint8_t* base = (rho < 32 ? (item.shared ? gate_sh : gate_exps + (size_t)item.e * F * rb)
                                     : (item.shared ? up_sh : up_exps + (size_t)item.e * F * rb));
     const uint8_t* rowp = base + (size_t)(32 * hb + (rho & 31)) * rb;
@@ -246,7 +251,8 @@ __global__ __launch_bounds__(64 * NW) void k_iq2_gu(const uint8_t* __restrict__ 
 __global__ __launch_bounds__(256) void k_iq2_down(const uint8_t* __restrict__ down_exps, const uint8_t* __restrict__ down_sh,
                                                    const uint32_t* __restrict__ himg, int h_blocks,
                                                    const float* __restrict__ sg, const int4* __restrict__ items, int H,
-                                                   int F, int Fs, int cps, float* __restrict__ Y) {
+                                                   int F, int Fs, int cps, float* __restrict__ Y,
+                                                   const uint64_t* __restrict__ eptr, const int32_t* __restrict__ dmap) {
     extern __shared__ __align__(16) uint32_t smem[];
     __shared__ uint2 tab[1024];
     Item item;
@@ -254,7 +260,10 @@ __global__ __launch_bounds__(256) void k_iq2_down(const uint8_t* __restrict__ do
     const int Fe = item.shared ? Fs : F;
     const int nb = Fe >> 8;
     const size_t rb = (size_t)nb * 82;
-    const uint8_t* base = item.shared ? down_sh : down_exps + (size_t)item.e * H * ((size_t)(F >> 8) * 82);
+    const uint8_t* base =
+        item.shared ? down_sh
+        : eptr      ? reinterpret_cast<const uint8_t*>(eptr[item.e]) + (size_t)2 * F * ((size_t)(H >> 8) * 82)
+                    : down_exps + (size_t)item.e * H * ((size_t)(F >> 8) * 82);
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int rpw = 64 / nb, grp = lane / nb, b = lane - grp * nb;
     const int r = blockIdx.x * 4 * rpw + wave * rpw + grp;
@@ -288,7 +297,8 @@ __global__ __launch_bounds__(256) void k_iq2_down(const uint8_t* __restrict__ do
             pin_blocks(B);
             float v = group_sum(iq2_block_dot_img(B[0], ht, b), nb);
             if (item.shared) v = v * sigmoid(sg[item.tok0 + c0 + c]);
-            if (live && b == 0) Y[(size_t)(item.first + c0 + c) * H + r] = v;
+            const int orow = (dmap && !item.shared) ? dmap[item.first + c0 + c] : item.first + c0 + c;
+            if (orow >= 0 && live && b == 0) Y[(size_t)orow * H + r] = v;
         }
         __syncthreads();
     }
@@ -337,14 +347,14 @@ bool iq2_shape_ok(int n_in) {
 hipError_t launch_iq2_gu(const uint8_t* gate_exps, const uint8_t* up_exps, const uint8_t* gate_sh, const uint8_t* up_sh,
                          const uint32_t* ximg, const int4* items, const int32_t* perm, int k, int H, int F, int Fs,
                          int has_shared, int max_items, uint32_t* himg, int h_blocks, hipStream_t s, uint8_t* hq,
-                         int hq_rows) {
+                         int hq_rows, const uint64_t* eptr) {
     const int Fmax = has_shared && Fs > F ? Fs : F;
     dim3 grid((unsigned)(Fmax / 32), (unsigned)max_items);
     const int nb = H / 256;
     const size_t lds = (size_t)(2 * nb) * (H >> 5) * kImgDw * 4 + 16;  // + the dead staging slot
 #define SMOE_IQ2_GU(NW)                                                                                           \
     hipLaunchKernelGGL((k_iq2_gu<NW>), grid, dim3(64 * (NW)), lds, s, gate_exps, up_exps, gate_sh, up_sh, ximg, items, \
-                       perm, k, H, F, Fs, himg, h_blocks, hq, hq_rows)
+                       perm, k, H, F, Fs, himg, h_blocks, hq, hq_rows, eptr)
     if (nb == 2) SMOE_IQ2_GU(2);
     else if (nb == 4) SMOE_IQ2_GU(4);
     else SMOE_IQ2_GU(8);
@@ -354,14 +364,14 @@ hipError_t launch_iq2_gu(const uint8_t* gate_exps, const uint8_t* up_exps, const
 
 hipError_t launch_iq2_down(const uint8_t* down_exps, const uint8_t* down_sh, const uint32_t* himg, int h_blocks,
                            const float* sg, const int4* items, int H, int F, int Fs, int max_items, float* Y,
-                           hipStream_t s) {
+                           hipStream_t s, const uint64_t* eptr, const int32_t* dmap) {
     const int rpw = 64 / (F / 256);  // the caller guarantees the shared width has the same row shape
     dim3 grid((unsigned)((H + 4 * rpw - 1) / (4 * rpw)), (unsigned)max_items);
     const size_t col_bytes = (size_t)h_blocks * kImgDw * 4;
     int cps = (int)(24576 / col_bytes);
     cps = cps < 1 ? 1 : cps > 16 ? 16 : cps;
     hipLaunchKernelGGL(k_iq2_down, grid, dim3(256), (size_t)cps * col_bytes + 16, s, down_exps, down_sh, himg, h_blocks, sg,
-                       items, H, F, Fs, cps, Y);
+                       items, H, F, Fs, cps, Y, eptr, dmap);
     return hipGetLastError();
 }
 

@@ -39,10 +39,13 @@ int gemv_shared_chunk();   // shared-expert tokens per GEMV work item
 hipError_t launch_q2_gu(const uint8_t* gate_exps, const uint8_t* up_exps, const uint8_t* gate_sh, const uint8_t* up_sh,
                         const uint32_t* ximg, const int4* items, const int32_t* perm, int k, int H, int F, int Fs,
                         int has_shared, int max_items, uint32_t* himg, int h_blocks, hipStream_t s,
-                        uint8_t* hq = nullptr, int hq_rows = 0);  // hq: the trace's q8_1 of the first hq_rows h rows
+                        uint8_t* hq = nullptr, int hq_rows = 0, const uint64_t* eptr = nullptr);
 hipError_t launch_q2_down(const uint8_t* down_exps, const uint8_t* down_sh, const uint32_t* himg, int h_blocks,
                           const float* sg, const int4* items, int H, int F, int Fs, int max_items, float* Y,
-                          hipStream_t s);
+                          hipStream_t s, const uint64_t* eptr = nullptr, const int32_t* dmap = nullptr);
+// (hq: the trace's q8_1 of the first hq_rows h rows.  eptr: the expert table of the grouped calls -- routed item e
+// reads the blob at eptr[e], [gate rows | up rows | down rows], instead of the planes; dmap: routed column row
+// first + c of the down kernels is written to Y row dmap[first + c])
 // batches of at most 4 tokens: gate/up that routes the batch itself (no route kernel before it), and down rows
 // with the combine (no combine kernel after it) when the batch's h images fit in LDS
 hipError_t launch_q2_gu_route(const uint8_t* gate_exps, const uint8_t* up_exps, const uint8_t* gate_sh,
@@ -89,10 +92,10 @@ bool iq2_shape_ok(int n_in);  // n_in = 256 nb, nb in {2, 4, 8}
 hipError_t launch_iq2_gu(const uint8_t* gate_exps, const uint8_t* up_exps, const uint8_t* gate_sh, const uint8_t* up_sh,
                          const uint32_t* ximg, const int4* items, const int32_t* perm, int k, int H, int F, int Fs,
                          int has_shared, int max_items, uint32_t* himg, int h_blocks, hipStream_t s,
-                         uint8_t* hq = nullptr, int hq_rows = 0);
+                         uint8_t* hq = nullptr, int hq_rows = 0, const uint64_t* eptr = nullptr);
 hipError_t launch_iq2_down(const uint8_t* down_exps, const uint8_t* down_sh, const uint32_t* himg, int h_blocks,
                            const float* sg, const int4* items, int H, int F, int Fs, int max_items, float* Y,
-                           hipStream_t s);
+                           hipStream_t s, const uint64_t* eptr = nullptr, const int32_t* dmap = nullptr);
 hipError_t launch_iq2_mmvq(const uint8_t* w, const uint8_t* xq, int n_in, int n_out, int n_col, float* y, hipStream_t s);
 
 // prefill contract (bf16 MFMA)
@@ -125,6 +128,22 @@ hipError_t launch_hc_read(float* R, const float* norm, const uint16_t* down, con
                           float* inject, const float* rprev, const float* yprev, const float* injprev, hipStream_t s);
 hipError_t launch_hc_write(const float* R, const float* y, const float* inject, int n_tok, int n, int hc, float* out,
                            hipStream_t s);
+
+// the expert tier (smoe_cache.hip): routed entries grouped by a table of one blob pointer per expert (at most
+// kMaxGroupExperts experts and kMaxGroupEntries entries), with the expert kernels' item table (group g = item g,
+// then n_sh_items shared chunks) and the identity slots of the rows' combine when asked; caller-made lists checked
+// into an item table; q8_1 blocks into activation images
+constexpr int kMaxGroupExperts = 1024;
+constexpr int kMaxGroupEntries = 4096;
+hipError_t launch_expert_group(const int32_t* ids, int n, int kpt, int E, const uint64_t* eptr, uint64_t* grp_ptr,
+                               int32_t* grp_start, int32_t* grp_expert, int32_t* ent_dst, int32_t* ent_tok,
+                               int32_t* miss_dst, int32_t* counts, int4* items, int cap_groups, int n_sh_items, int P,
+                               int T, int32_t* slot_id, hipStream_t s);
+hipError_t launch_group_items(const uint64_t* grp_ptr, const int32_t* grp_start, const int32_t* ent_tok,
+                              const int32_t* ent_dst, const int32_t* counts, int cap_groups, int cap_entries, int n_tok,
+                              int n_rows, int4* items, int32_t* etok, int32_t* edst, hipStream_t s);
+hipError_t launch_q8_images(const uint8_t* xq, int64_t n_blocks, int natural, uint32_t* img, hipStream_t s);
+hipError_t launch_iota(int32_t* p, int n, hipStream_t s);
 
 hipError_t launch_synth_blocks(int type, uint64_t seed, uint64_t stream_id, int64_t n_blocks, float sigma, uint8_t* out,
                                hipStream_t s);

@@ -34,7 +34,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_status_strings():
     lib = S.lib()
-    assert lib.smoe_abi_version() == 108
+    assert lib.smoe_abi_version() == 109
     for code in (0, -1, -2, -3, -4, -5, -6):
         assert lib.smoe_status_str(code)
 
