@@ -1451,13 +1451,13 @@ __device__ __forceinline__ void gu_compute(const Item& item, int hb, uint32_t* s
             __syncthreads();
         }
         for (int c = 0; c < nc; ++c) {
-            const uint32_t* xt = smem + (size_t)(PRESTAGED ? item_token_head(item, c) : c) * qb * kImgDw;
+            const uint32_t* xt = smem + (size_t)(PRESTAGED ? item_token_head(item, c) : c) * qb * kImgLdsDw;
             pin_units(w);
             float acc[NIT];
 #pragma unroll
             for (int m = 0; m < MAXUPL; ++m) {
                 if (m < G.upl) {
-                    const uint32_t* img = xt + (size_t)(4 * (l + G.lpr * m)) * kImgDw;
+                    const uint32_t* img = xt + (size_t)(l + G.lpr * m) * kUnitLdsDw;
                     float p01[NIT];
                     Act2 a;
                     load_act_img2(img, a);
@@ -1588,7 +1588,7 @@ __device__ __forceinline__ bool gu_route_wg(
 #pragma unroll
     for (int j = 0; j < 6; ++j)
         pre[j] = reinterpret_cast<const u32x4*>(ximg)[min(min(j, npre - 1) * 256 + tid, pieces - 1)];
-    GuRouteLds& L = *reinterpret_cast<GuRouteLds*>(smem + kGuCols * qb * kImgDw + 4);
+    GuRouteLds& L = *reinterpret_cast<GuRouteLds*>(smem + kGuCols * qb * kImgLdsDw + 4);
     const int P = T * k;
     // one token: wave 0 routes it and takes the item from the candidates (the y-th selected id in ascending order,
     // its one pair at dispatch position y); L.item[7] = 1 when the fast selection declined (then the ids are in
@@ -1621,7 +1621,7 @@ __device__ __forceinline__ bool gu_route_wg(
     }
 #pragma unroll
     for (int j = 0; j < 6; ++j)
-        if (j * 256 + tid < pieces) reinterpret_cast<u32x4*>(smem)[j * 256 + tid] = pre[j];
+        if (j * 256 + tid < pieces) reinterpret_cast<u32x4*>(smem)[lds_piece(j * 256 + tid)] = pre[j];
     __syncthreads();
     Item item;
     if (one && L.item[7] == 0) {
@@ -1787,13 +1787,13 @@ __global__ __launch_bounds__(256) void k_q2_down(const uint8_t* __restrict__ dow
             __syncthreads();
         }
         for (int c = 0; c < nc; ++c) {
-            const uint32_t* ht = smem + (size_t)c * h_blocks * kImgDw;
+            const uint32_t* ht = smem + (size_t)c * h_blocks * kImgLdsDw;
             pin_units(w);
             float acc[NIT];
 #pragma unroll
             for (int m = 0; m < MAXUPL; ++m) {
                 if (m < G.upl) {
-                    const uint32_t* img = ht + (size_t)(4 * (l + G.lpr * m)) * kImgDw;
+                    const uint32_t* img = ht + (size_t)(l + G.lpr * m) * kUnitLdsDw;
                     float p01[NIT];
                     Act2 a;
                     load_act_img2(img, a);
@@ -1888,14 +1888,16 @@ __device__ __forceinline__ void down_combine_tasks(const uint8_t* __restrict__ d
         float dw[NT][MAXUPL][2];
         unit_scales(w, dw);
         // a row value of one column of one task: the lane's units in order, then the butterfly over its lpr lanes
+        // (a unit per lane always exists, so the first one is taken without a test; the row's butterfly selects its
+        // additions: the tasks' chains interleave with no branch between them)
         auto row_value = [&](int q, int c) {
-            const int grp = lane / lpr[q], l = lane - grp * lpr[q];
-            const uint32_t* ht = img + (size_t)(it[q].first + c) * h_blocks * kImgDw;
+            const int l = lane & (lpr[q] - 1);  // lpr is a power of two
+            const uint32_t* ht = img + (size_t)(it[q].first + c) * h_blocks * kImgLdsDw;
             float acc = 0.0f;
 #pragma unroll
             for (int m = 0; m < MAXUPL; ++m) {
-                if (m < upl[q]) {
-                    const uint32_t* im = ht + (size_t)(4 * (l + lpr[q] * m)) * kImgDw;
+                if (m == 0 || m < upl[q]) {
+                    const uint32_t* im = ht + (size_t)(l + lpr[q] * m) * kUnitLdsDw;
                     Act2 a;
                     load_act_img2(im, a);
                     const float p01 = q2_unit_first(w[q][m], dw[q][m][0], a);
@@ -1904,7 +1906,7 @@ __device__ __forceinline__ void down_combine_tasks(const uint8_t* __restrict__ d
                     acc = m == 0 ? L : acc + L;
                 }
             }
-            return group_sum(acc, lpr[q]);
+            return group_sum_sel(acc, lpr[q]);
         };
         // the first column of every task at once, with no branch between them (a dead task works on item 0's first
         // column and stores nothing), so that the tasks' LDS reads and dots overlap; further columns task by task
@@ -1956,7 +1958,7 @@ __global__ __launch_bounds__(256) void k_q2_down_combine(
     __shared__ float s_sg[kShCols];
     const int P = T * k, rows = P + T;
     const int pieces = rows * h_blocks * (kImgDw / 4);  // 16-byte pieces of the images
-    float* Ys = reinterpret_cast<float*>(smem + (size_t)pieces * 4);  // [rows][kDcRows]
+    float* Ys = reinterpret_cast<float*>(smem + (size_t)lds_piece(pieces) * 4);  // [rows][kDcRows]
     const int r0 = blockIdx.x * kDcRows;
     const int tid = threadIdx.x;
 
@@ -1973,7 +1975,7 @@ __global__ __launch_bounds__(256) void k_q2_down_combine(
     const float sgv = sg[min(tid, T - 1)];
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-        if (j * 256 + tid < pieces) reinterpret_cast<u32x4*>(smem)[j * 256 + tid] = pre[j];
+        if (j * 256 + tid < pieces) reinterpret_cast<u32x4*>(smem)[lds_piece(j * 256 + tid)] = pre[j];
     if (tid < T) s_sg[tid] = sgv;
 #pragma unroll
     for (int j = 0; j < 3; ++j)
@@ -1983,7 +1985,7 @@ __global__ __launch_bounds__(256) void k_q2_down_combine(
         s_wts[tid] = wt;
     }
     for (int i = 1024 + tid; i < pieces; i += 256)
-        reinterpret_cast<u32x4*>(smem)[i] = reinterpret_cast<const u32x4*>(himg)[i];
+        reinterpret_cast<u32x4*>(smem)[lds_piece(i)] = reinterpret_cast<const u32x4*>(himg)[i];
     __syncthreads();
 
     down_combine_tasks<MAXUPL, NT>(down_exps, down_sh, smem, Ys, s_items, s_slot, s_wts, n_items, npass, r0, H, F, Fs,
@@ -2034,7 +2036,7 @@ __global__ __launch_bounds__(256) void k_q2_moe_small(
     const int P = T * k, n_sh = has_shared ? 1 : 0;
     const int rows = P + n_sh * T;
     const int lane = tid & 63, wave = tid >> 6;
-    float* Ys = reinterpret_cast<float*>(smem + (size_t)(P + T) * h_blocks * kImgDw);
+    float* Ys = reinterpret_cast<float*>(smem + (size_t)(P + T) * h_blocks * kImgLdsDw);
     if (tid == 0) {
         s_bad = 0;
         if (has_shared) {
@@ -2163,7 +2165,7 @@ __global__ __launch_bounds__(256) void k_q2_moe_small(
             for (int j = 0; j < 8; ++j) {
                 const int i = base + j * 256 + tid;
                 const int blk = i / kXchgSlots, wd = i - blk * kXchgSlots;
-                if (need[j]) smem[(size_t)blk * kImgDw + wd] = (uint32_t)v[j];
+                if (need[j]) smem[(size_t)lds_blk(blk) + wd] = (uint32_t)v[j];
             }
         }
         if (!ok) s_bad = 1;
@@ -2568,7 +2570,7 @@ hipError_t launch_q2_gu(const uint8_t* gate_exps, const uint8_t* up_exps, const 
     dim3 grid((unsigned)(Fmax / 32), (unsigned)max_items);
     int nit, upl;
     gu_shape(H, nit, upl);
-    const size_t lds = (size_t)kGuCols * (H >> 5) * kImgDw * 4 + 16;  // + the dead staging slot
+    const size_t lds = (size_t)kGuCols * (H >> 5) * kImgLdsDw * 4 + 16;  // + the dead staging slot
     // the traced variant (hq: the trace's q8_1 of h) is its own instantiation: the plain kernel keeps its registers
 #define SMOE_GU(N, U)                                                                                                \
     if (hq)                                                                                                          \
@@ -2594,7 +2596,7 @@ hipError_t launch_q2_down(const uint8_t* down_exps, const uint8_t* down_sh, cons
         rpw = rpw_s < rpw ? rpw_s : rpw;
     }
     dim3 grid((unsigned)((H + 4 * rpw - 1) / (4 * rpw)), (unsigned)max_items);
-    const size_t col_bytes = (size_t)h_blocks * kImgDw * 4;
+    const size_t col_bytes = (size_t)h_blocks * kImgLdsDw * 4;
     int cps = (int)(24576 / col_bytes);
     cps = cps < 1 ? 1 : cps > 16 ? 16 : cps;
     const size_t lds = (size_t)cps * col_bytes + 16;  // + the dead staging slot
@@ -2616,7 +2618,7 @@ hipError_t launch_q2_gu_route(const uint8_t* gate_exps, const uint8_t* up_exps, 
     dim3 grid((unsigned)(Fmax / 32), (unsigned)max_items + 1);  // + the writer row
     int nit, upl;
     gu_shape(H, nit, upl);
-    size_t lds = (size_t)kGuCols * (H >> 5) * kImgDw * 4 + 16 + sizeof(GuRouteLds);
+    size_t lds = (size_t)kGuCols * (H >> 5) * kImgLdsDw * 4 + 16 + sizeof(GuRouteLds);
     if (lds < sizeof(SmallDispatchLds)) lds = sizeof(SmallDispatchLds);
 #define SMOE_GUR(N, U)                                                                                             \
     hipLaunchKernelGGL((k_q2_gu_route<N, U>), grid, dim3(256), lds, s, gate_exps, up_exps, gate_sh, up_sh, ximg,   \
@@ -2629,7 +2631,7 @@ hipError_t launch_q2_gu_route(const uint8_t* gate_exps, const uint8_t* up_exps, 
 
 size_t down_combine_lds(int T, int k, int h_blocks) {
     const size_t rows = (size_t)T * k + T;
-    return rows * h_blocks * kImgDw * 4 + rows * kDcRows * 4;
+    return rows * h_blocks * kImgLdsDw * 4 + rows * kDcRows * 4;
 }
 
 bool down_combine_ok(int T, int k, int h_blocks) {
@@ -2666,8 +2668,8 @@ hipError_t launch_q2_down_combine(const uint8_t* down_exps, const uint8_t* down_
 
 size_t moe_small_lds(int T, int k, int H, int h_blocks) {
     const size_t rows = (size_t)T * k + T;
-    const size_t down = rows * h_blocks * kImgDw * 4 + rows * kDcRows * 4 + sizeof(SmallDispatchLds);
-    size_t gu = (size_t)kGuCols * (H >> 5) * kImgDw * 4 + 16 + sizeof(GuRouteLds);
+    const size_t down = rows * h_blocks * kImgLdsDw * 4 + rows * kDcRows * 4 + sizeof(SmallDispatchLds);
+    size_t gu = (size_t)kGuCols * (H >> 5) * kImgLdsDw * 4 + 16 + sizeof(GuRouteLds);
     if (gu < sizeof(SmallDispatchLds)) gu = sizeof(SmallDispatchLds);
     return down > gu ? down : gu;
 }

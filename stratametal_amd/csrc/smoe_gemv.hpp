@@ -78,6 +78,20 @@ __device__ __forceinline__ float group_sum(float v, int lpr) {
     return v;
 }
 
+// group_sum with the lanes per row as data: every distance is exchanged and each addition kept or not by a
+// select (the same additions as group_sum), so that the sums of several rows interleave with no branch between.
+__device__ __forceinline__ float group_sum_sel(float v, int lpr) {
+    float t = xor_swap<8>(v);
+    v = lpr >= 16 ? v + t : v;
+    t = xor_swap<4>(v);
+    v = lpr >= 8 ? v + t : v;
+    t = xor_swap<2>(v);
+    v = lpr >= 4 ? v + t : v;
+    t = xor_swap<1>(v);
+    v = lpr >= 2 ? v + t : v;
+    return v;
+}
+
 // v + v[lane ^ 32] by one v_permlane32_swap: with both operands v, the two results hold the lower and the upper
 // half of v in both halves, and their sum is that addition (commutative, so bit for bit).
 __device__ __forceinline__ float add_xor32(float v) {
@@ -176,6 +190,16 @@ __device__ __forceinline__ int lanes_per_row(int dpr) {
 // Built by the same quantiser as the q8_1 block (metal/shaders/iq.metal:597-627); the fp16 sum field of the
 // q8_1 block is not needed by the Q2_0 / IQ2_S dots (metal/shaders/iq.metal:152-180,444-456) and is not kept.
 constexpr int kImgDw = 12;
+
+// Images staged in LDS: every unit of four images (192 bytes) is followed by 16 bytes of padding, so that the
+// lanes of a row group, which read consecutive units, start on different LDS banks (unpadded, the 192-byte
+// stride put 4 or 8 of them on the same banks).  Image B of a staged region (column-major, a column a whole
+// number of units) starts at dword lds_blk(B); a column of qb images spans qb * kImgLdsDw dwords; unit u of a
+// column starts at dword u * kUnitLdsDw; the 16-byte pieces of the unpadded order land at lds_piece(p).
+constexpr int kImgLdsDw = 13;
+constexpr int kUnitLdsDw = 4 * kImgDw + 4;
+__host__ __device__ __forceinline__ int lds_blk(int b) { return kImgDw * b + 4 * (b >> 2); }
+__host__ __device__ __forceinline__ int lds_piece(int p) { return p + p / 12; }
 
 // Maximum and sum over each 32-lane half of the wave, every lane receiving its half's result: DPP rotations
 // inside the 16-lane rows, then the other row of the half by swizzle.  Both are independent of the order of
@@ -362,7 +386,7 @@ __device__ __forceinline__ void stage_commit(const StagePieces& sp, uint32_t* ac
     const int nt = (int)blockDim.x;
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-        if (base + j * nt < total) reinterpret_cast<img_u32x4*>(act)[sp.dst[j]] = sp.v[j];
+        if (base + j * nt < total) reinterpret_cast<img_u32x4*>(act)[lds_piece(sp.dst[j])] = sp.v[j];
 }
 // Round `base` with rows that need no memory read (see stage_issue) as straight-line code: all four loads
 // unconditional (a piece past the end, or a whole j past the end, reloads the last piece and is stored to the
@@ -385,7 +409,7 @@ __device__ __forceinline__ void stage_issue_direct(StagePieces& sp, const uint32
 }
 __device__ __forceinline__ void stage_commit_direct(const StagePieces& sp, uint32_t* act) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) reinterpret_cast<img_u32x4*>(act)[sp.dst[j]] = sp.v[j];
+    for (int j = 0; j < 4; ++j) reinterpret_cast<img_u32x4*>(act)[lds_piece(sp.dst[j])] = sp.v[j];
 }
 // True when stage_issue_direct can serve columns c0 .. c0 + nc.
 __device__ __forceinline__ bool stage_direct(const Item& it, int c0, int nc, bool by_token) {

@@ -23,42 +23,52 @@
 
 namespace smoe {
 
+// The grid as LDS wants it, built at compile time from the codes: entry i = the eight 2-bit magnitude indices of
+// grid entry i, one per byte (low dword: weights 0-3).  A work-group copies the 8 KB into LDS with 16-byte loads.
 namespace {
-__device__ const uint16_t kIq2sCodes[1024] = {
+constexpr uint16_t kIq2sCodeList[1024] = {
 #include "iq2s_grid_codes.inc"
 };
+struct Iq2sTable {
+    uint64_t e[1024];
+};
+constexpr Iq2sTable make_iq2s_table() {
+    Iq2sTable t{};
+    for (int i = 0; i < 1024; ++i) {
+        const uint32_t c = kIq2sCodeList[i];
+        uint64_t lo = 0, hi = 0;
+        for (int q = 0; q < 4; ++q) {
+            lo |= (uint64_t)((c >> (2 * q)) & 3u) << (8 * q);
+            hi |= (uint64_t)((c >> (8 + 2 * q)) & 3u) << (8 * q);
+        }
+        t.e[i] = lo | (hi << 32);
+    }
+    return t;
+}
+__device__ const Iq2sTable kIq2sTab = make_iq2s_table();
 }  // namespace
 
 constexpr uint32_t kMagPos = 0x002B1908u;  // bytes 8, 25, 43, 0
 constexpr uint32_t kMagNeg = 0x00D5E7F8u;  // bytes -8, -25, -43, 0
 
-// LDS table: entry i = the eight 2-bit magnitude indices of grid entry i, one per byte (lo: weights 0-3).  Built
-// in two steps so that a kernel can issue the code loads first and its other loads behind them: grid_codes_load
-// (entries tid + NTH j, unconditional), grid_table_store (waits for those loads alone).
+// The LDS table in two steps, so that a kernel can issue the table loads first and its other loads behind them:
+// grid_codes_load (16-byte pieces tid + NTH j, unconditional), grid_table_store (waits for those loads alone).
 template <int NTH>
-__device__ __forceinline__ void grid_codes_load(uint32_t (&c)[1024 / NTH]) {
+__device__ __forceinline__ void grid_codes_load(uint4 (&c)[512 / NTH]) {
+    const uint4* src = reinterpret_cast<const uint4*>(kIq2sTab.e);
 #pragma unroll
-    for (int j = 0; j < 1024 / NTH; ++j) c[j] = kIq2sCodes[threadIdx.x + NTH * j];
+    for (int j = 0; j < 512 / NTH; ++j) c[j] = src[threadIdx.x + NTH * j];
 }
 template <int NTH>
-__device__ __forceinline__ void grid_table_store(const uint32_t (&c)[1024 / NTH], uint2* tab) {
+__device__ __forceinline__ void grid_table_store(const uint4 (&c)[512 / NTH], uint2* tab) {
 #pragma unroll
-    for (int j = 0; j < 1024 / NTH; ++j) {
-        uint32_t cj = c[j];
-        asm volatile("" : "+v"(cj));  // the unpacking (and so the wait for the code load) stays where the call stands
-        uint32_t lo = 0, hi = 0;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            lo |= ((cj >> (2 * q)) & 3u) << (8 * q);
-            hi |= ((cj >> (8 + 2 * q)) & 3u) << (8 * q);
-        }
-        tab[threadIdx.x + NTH * j] = make_uint2(lo, hi);
-    }
+    for (int j = 0; j < 512 / NTH; ++j) reinterpret_cast<uint4*>(tab)[threadIdx.x + NTH * j] = c[j];
 }
 
 // Four signed weights from four magnitude indices (bytes) and their four sign bits.
 __device__ __forceinline__ uint32_t signed_mags(uint32_t idx4, uint32_t nib) {
-    const uint32_t sel = ((nib * 0x00810204u) & 0x04040404u) | idx4;  // sign bit j -> bit 2 of byte j
+    // sign bit j -> bit 2 of byte j (a 24-bit multiply: nib < 16, the product < 2^28)
+    const uint32_t sel = (__umul24(nib, 0x00810204u) & 0x04040404u) | idx4;
     return __builtin_amdgcn_perm(kMagNeg, kMagPos, sel);
 }
 
@@ -121,7 +131,8 @@ __device__ __forceinline__ float iq2_sub(const Iq2Block& B, int ib, const uint32
     for (int c = 4; c < 8; ++c) s1 = __builtin_amdgcn_sdot4((int)B.w[8 * ib + c], (int)q[c], s1, false);
     const uint32_t scb = (B.sc[ib >> 2] >> (8 * (ib & 3))) & 0xFFu;
     const int ls0 = (int)(scb & 15u), ls1 = (int)(scb >> 4);
-    const int sumi = (s0 * ls0 + s1 * ls1 + (s0 + s1) / 2) / 4;
+    // 24-bit multiplies: |s| <= 16 * 43 * 127 < 2^23 and ls <= 15, so the products are exact
+    const int sumi = (__mul24(s0, ls0) + __mul24(s1, ls1) + (s0 + s1) / 2) / 4;
     return (B.d * dx) * (float)sumi;
 }
 
@@ -130,7 +141,7 @@ __device__ __forceinline__ float iq2_block_dot_img(const Iq2Block& B, const uint
     float L = 0.0f;
 #pragma unroll
     for (int ib = 0; ib < 8; ++ib) {
-        const uint4* p = reinterpret_cast<const uint4*>(img + (size_t)(8 * b + ib) * kImgDw);
+        const uint4* p = reinterpret_cast<const uint4*>(img + (size_t)lds_blk(8 * b + ib));
         const uint4 lo = p[0], hi = p[1], ds = p[2];
         const uint32_t q[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
         const float P = iq2_sub(B, ib, q, u2f(ds.x));
@@ -191,7 +202,7 @@ __global__ __launch_bounds__(64 * NW) void k_iq2_gu(const uint8_t* __restrict__ 
     // loads in the order their data is needed: the grid codes, the first column batch's images (when their rows
     // need no memory read), then the weights; the table store waits for the codes alone, the image commit for
     // the images alone
-    uint32_t codes[1024 / (64 * NW)];
+    uint4 codes[512 / (64 * NW)];
     grid_codes_load<64 * NW>(codes);
     const int nc0 = min(kCols, item.ncol);
     uint32_t raw[21];
@@ -221,7 +232,7 @@ __global__ __launch_bounds__(64 * NW) void k_iq2_gu(const uint8_t* __restrict__ 
             __syncthreads();
         }
         for (int c = 0; c < nc; ++c) {
-            const uint32_t* xt = smem + (size_t)c * qb * kImgDw;
+            const uint32_t* xt = smem + (size_t)c * qb * kImgLdsDw;
             pin_blocks(B);
             const float v = group_sum(iq2_block_dot_img(B[0], xt, b), nb);
             if (b == 0) rowv[c][rho] = v;
@@ -270,7 +281,7 @@ __global__ __launch_bounds__(256) void k_iq2_down(const uint8_t* __restrict__ do
     const bool live = r < H;
     // loads in the order their data is needed (see k_iq2_gu): grid codes, the first column batch's h images,
     // then the weights
-    uint32_t codes[4];
+    uint4 codes[2];
     grid_codes_load<256>(codes);
     const int nc0 = min(cps, item.ncol);
     StagePieces sp;
@@ -293,7 +304,7 @@ __global__ __launch_bounds__(256) void k_iq2_down(const uint8_t* __restrict__ do
             __syncthreads();
         }
         for (int c = 0; c < nc; ++c) {
-            const uint32_t* ht = smem + (size_t)c * h_blocks * kImgDw;
+            const uint32_t* ht = smem + (size_t)c * h_blocks * kImgLdsDw;
             pin_blocks(B);
             float v = group_sum(iq2_block_dot_img(B[0], ht, b), nb);
             if (item.shared) v = v * sigmoid(sg[item.tok0 + c0 + c]);
@@ -309,7 +320,7 @@ __global__ __launch_bounds__(256) void k_iq2_mmvq(const uint8_t* __restrict__ w,
                                                    int n_out, int n_col, float* __restrict__ y) {
     __shared__ uint2 tab[1024];
     {
-        uint32_t codes[4];
+        uint4 codes[2];
         grid_codes_load<256>(codes);
         grid_table_store<256>(codes, tab);
     }
@@ -351,7 +362,7 @@ hipError_t launch_iq2_gu(const uint8_t* gate_exps, const uint8_t* up_exps, const
     const int Fmax = has_shared && Fs > F ? Fs : F;
     dim3 grid((unsigned)(Fmax / 32), (unsigned)max_items);
     const int nb = H / 256;
-    const size_t lds = (size_t)(2 * nb) * (H >> 5) * kImgDw * 4 + 16;  // + the dead staging slot
+    const size_t lds = (size_t)(2 * nb) * (H >> 5) * kImgLdsDw * 4 + 16;  // + the dead staging slot
 #define SMOE_IQ2_GU(NW)                                                                                           \
     hipLaunchKernelGGL((k_iq2_gu<NW>), grid, dim3(64 * (NW)), lds, s, gate_exps, up_exps, gate_sh, up_sh, ximg, items, \
                        perm, k, H, F, Fs, himg, h_blocks, hq, hq_rows, eptr)
@@ -367,7 +378,7 @@ hipError_t launch_iq2_down(const uint8_t* down_exps, const uint8_t* down_sh, con
                            hipStream_t s, const uint64_t* eptr, const int32_t* dmap) {
     const int rpw = 64 / (F / 256);  // the caller guarantees the shared width has the same row shape
     dim3 grid((unsigned)((H + 4 * rpw - 1) / (4 * rpw)), (unsigned)max_items);
-    const size_t col_bytes = (size_t)h_blocks * kImgDw * 4;
+    const size_t col_bytes = (size_t)h_blocks * kImgLdsDw * 4;
     int cps = (int)(24576 / col_bytes);
     cps = cps < 1 ? 1 : cps > 16 ? 16 : cps;
     hipLaunchKernelGGL(k_iq2_down, grid, dim3(256), (size_t)cps * col_bytes + 16, s, down_exps, down_sh, himg, h_blocks, sg,
