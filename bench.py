@@ -300,18 +300,38 @@ def prefill(S, torch, g, a, flush):
     out["expert_gemm_mfma_frac"] = out["expert_gemm_tflops"] / BF16_PEAK_TFLOPS
     out["layer_tflops"] = (ex_flops + router_flops) / (m["ms_per_step"] * 1e-3) / 1e12
     gu_tf = gu_flops / (st["gate_up"] * 1e-3) / 1e12
-    roof = {"bound": "mfma", "kernel": "k_mm_gu (routed + shared gate/up, SwiGLU, bf16 h records)",
-            "achieved": gu_tf, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": gu_tf / BF16_PEAK_TFLOPS,
-            "traffic": None, "useful_flops_per_launch": gu_flops, "avg_launch_ms": st["gate_up"],
-            "mfma_busy": None}
+    # the binding roof of k_mm_gu: its compulsory bytes (the touched experts' and the shared expert's gate and up
+    # rows, x as fp16 records, h records written) at 8 TB/s against its useful FLOPs at 2.5 PFLOP/s; with Zipf(1.2)
+    # routing most touched experts get a few tokens, and the weight bytes take longer than the matrix work
+    D = m["touched_experts_avg"]
+    P = T * g.top_k
+    rb_h = S.row_bytes(g.w_type, g.n_embd)
+    gu_bytes = (D * 2 * g.n_ff * rb_h + 2 * g.n_ff_shared * S.row_bytes(g.sh_type, g.n_embd) + T * g.n_embd * 2
+                + (P + T) * max(g.n_ff, g.n_ff_shared) * 2)
+    t_hbm_us = gu_bytes / (HBM_PEAK_GBS * 1e9) * 1e6
+    t_mfma_us = gu_flops / (BF16_PEAK_TFLOPS * 1e12) * 1e6
+    gu_gbs = gu_bytes / (st["gate_up"] * 1e-3) / 1e9
+    common = {"kernel": "k_mm_gu (routed + shared gate/up, SwiGLU, bf16 h records)", "traffic": None,
+              "algorithmic_bytes_per_launch": gu_bytes, "useful_flops_per_launch": gu_flops,
+              "avg_launch_ms": st["gate_up"], "roof_us": {"hbm": t_hbm_us, "mfma": t_mfma_us},
+              "mfma_tflops": gu_tf, "mfma_frac": gu_tf / BF16_PEAK_TFLOPS, "hbm_gbs": gu_gbs,
+              "hbm_frac": gu_gbs / HBM_PEAK_GBS, "mfma_busy": None}
+    if t_hbm_us >= t_mfma_us:
+        roof = dict({"bound": "hbm", "achieved": gu_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": gu_gbs / HBM_PEAK_GBS}, **common)
+    else:
+        roof = dict({"bound": "mfma", "achieved": gu_tf, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": gu_tf / BF16_PEAK_TFLOPS}, **common)
     rec = profile_record("prefill512_counters", "smoe::k_mm_gu")
     if rec:
         roof["traffic"] = rec.get("traffic_bytes")
         roof["mfma_busy"] = rec.get("mfma_busy")
         roof["counters_source"] = "profiles/prefill512_counters.md"
     out["roofline"] = roof
-    log(stage_line("prefill 512", m) + ", expert GEMMs %.0f TFLOP/s (%.1f%% of bf16 peak), k_mm_gu %.0f TFLOP/s"
-        % (out["expert_gemm_tflops"], 100 * out["expert_gemm_mfma_frac"], gu_tf))
+    log(stage_line("prefill 512", m) + ", expert GEMMs %.0f TFLOP/s (%.1f%% of bf16 peak), k_mm_gu %.0f TFLOP/s, "
+        "%.0f GB/s (%s-bound: roofs %.1f us HBM, %.1f us MFMA)"
+        % (out["expert_gemm_tflops"], 100 * out["expert_gemm_mfma_frac"], gu_tf, gu_gbs, roof["bound"], t_hbm_us,
+           t_mfma_us))
     del stack
     torch.cuda.empty_cache()
     return out
