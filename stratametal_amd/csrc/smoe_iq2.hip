@@ -29,8 +29,10 @@ namespace {
 constexpr uint16_t kIq2sCodeList[1024] = {
 #include "iq2s_grid_codes.inc"
 };
+constexpr int kIq2sTabEntries = 1024;
+constexpr int kIq2sTabPieces = kIq2sTabEntries / 2;  // 16-byte pieces
 struct Iq2sTable {
-    uint64_t e[1024];
+    uint64_t e[kIq2sTabEntries];
 };
 constexpr Iq2sTable make_iq2s_table() {
     Iq2sTable t{};
@@ -53,21 +55,31 @@ constexpr uint32_t kMagNeg = 0x00D5E7F8u;  // bytes -8, -25, -43, 0
 
 // The LDS table in two steps, so that a kernel can issue the table loads first and its other loads behind them:
 // grid_codes_load (16-byte pieces tid + NTH j, unconditional), grid_table_store (waits for those loads alone).
+// Pieces per thread of the table copy (the last round is partial).
 template <int NTH>
-__device__ __forceinline__ void grid_codes_load(uint4 (&c)[512 / NTH]) {
+constexpr int kTabRounds = (kIq2sTabPieces + NTH - 1) / NTH;
+template <int NTH>
+__device__ __forceinline__ void grid_codes_load(uint4 (&c)[kTabRounds<NTH>]) {
     const uint4* src = reinterpret_cast<const uint4*>(kIq2sTab.e);
 #pragma unroll
-    for (int j = 0; j < 512 / NTH; ++j) c[j] = src[threadIdx.x + NTH * j];
+    for (int j = 0; j < kTabRounds<NTH>; ++j) {
+        const int i = (int)threadIdx.x + NTH * j;
+        c[j] = src[i < kIq2sTabPieces ? i : 0];
+    }
 }
 template <int NTH>
-__device__ __forceinline__ void grid_table_store(const uint4 (&c)[512 / NTH], uint2* tab) {
+__device__ __forceinline__ void grid_table_store(const uint4 (&c)[kTabRounds<NTH>], uint2* tab) {
 #pragma unroll
-    for (int j = 0; j < 512 / NTH; ++j) reinterpret_cast<uint4*>(tab)[threadIdx.x + NTH * j] = c[j];
+    for (int j = 0; j < kTabRounds<NTH>; ++j) {
+        const int i = (int)threadIdx.x + NTH * j;
+        if (i < kIq2sTabPieces) reinterpret_cast<uint4*>(tab)[i] = c[j];
+    }
 }
 
 // Four signed weights from four magnitude indices (bytes) and their four sign bits.
 __device__ __forceinline__ uint32_t signed_mags(uint32_t idx4, uint32_t nib) {
-    // sign bit j -> bit 2 of byte j (a 24-bit multiply: nib < 16, the product < 2^28)
+    // sign bit j -> bit 2 of byte j (a 24-bit multiply: nib < 16, the product < 2^28, the four partial products
+    // in disjoint bits)
     const uint32_t sel = (__umul24(nib, 0x00810204u) & 0x04040404u) | idx4;
     return __builtin_amdgcn_perm(kMagNeg, kMagPos, sel);
 }
@@ -78,33 +90,35 @@ struct Iq2Block {
     float d;
 };
 
-// The 82 bytes of block b of a row (rows are a whole number of block pairs, 164 bytes, so dword aligned):
-// an even block is loaded from its pair's dword 0, an odd one from dword 20 (its bytes start at byte 2 there).
-__device__ __forceinline__ void load_block_raw(const uint8_t* row, int b, uint32_t (&raw)[21], int& off) {
-    const uint8_t* p = row + (size_t)(b >> 1) * 164 + ((b & 1) ? 80 : 0);
-    __builtin_memcpy(raw, __builtin_assume_aligned(p, 4), 84);
-    off = (b & 1) ? 2 : 0;
+// Block b of a row (rows are a whole number of block pairs, 164 bytes, so dword aligned).  Every field after the
+// scale (qs @2, signs @34, qh @66, scales @74) starts at byte 2 modulo 4, so the block is loaded so that each
+// field dword is one alignbyte of two raw dwords with a per-lane shift: an even block's 80 bytes from its first
+// byte (shift 2), an odd block's from its byte 2 (shift 0, the pair's bytes 84 .. 163); raw[20] is the pair's
+// dword 20 for both (the even block's bytes 80-83, the odd block's scale in its high half).  Returns the shift.
+__device__ __forceinline__ uint32_t load_block_raw(const uint8_t* row, int b, uint32_t (&raw)[21]) {
+    const uint8_t* pair = row + (size_t)(b >> 1) * 164;
+    __builtin_memcpy(raw, __builtin_assume_aligned(pair + ((b & 1) ? 84 : 0), 4), 80);
+    raw[20] = *reinterpret_cast<const uint32_t*>(__builtin_assume_aligned(pair + 80, 4));
+    return (b & 1) ? 0u : 2u;
 }
 
-__device__ __forceinline__ void decode_block(const uint32_t (&raw)[21], int off, const uint2* __restrict__ tab,
+__device__ __forceinline__ void decode_block(const uint32_t (&raw)[21], uint32_t sh, const uint2* __restrict__ tab,
                                              Iq2Block& B) {
-    uint32_t bw[21];  // the block's bytes from byte 0
-#pragma unroll
-    for (int j = 0; j < 20; ++j) bw[j] = __builtin_amdgcn_alignbyte(raw[j + 1], raw[j], off);
-    bw[20] = __builtin_amdgcn_alignbyte(0u, raw[20], off);
-    B.d = (float)__builtin_bit_cast(_Float16, (uint16_t)(bw[0] & 0xFFFFu));
-    const uint32_t qh0 = __builtin_amdgcn_alignbyte(bw[17], bw[16], 2);  // qh bytes 0..3
-    const uint32_t qh1 = __builtin_amdgcn_alignbyte(bw[18], bw[17], 2);  // qh bytes 4..7
-    B.sc[0] = __builtin_amdgcn_alignbyte(bw[19], bw[18], 2);
-    B.sc[1] = __builtin_amdgcn_alignbyte(bw[20], bw[19], 2);
+    // field dword m (m = 0 .. 19 from byte 2: qs 0-7, signs 8-15, qh 16-17, scales 18-19)
+    auto fd = [&](int m) { return __builtin_amdgcn_alignbyte(raw[m + 1], raw[m], sh); };
+    const uint32_t dbits = sh ? (raw[0] & 0xFFFFu) : (raw[20] >> 16);
+    B.d = (float)__builtin_bit_cast(_Float16, (uint16_t)dbits);
+    const uint32_t qh0 = fd(16), qh1 = fd(17);  // qh bytes 0..3, 4..7
+    B.sc[0] = fd(18);
+    B.sc[1] = fd(19);
 #pragma unroll
     for (int ib = 0; ib < 8; ++ib) {
-        const uint32_t qsd = __builtin_amdgcn_alignbyte(bw[ib + 1], bw[ib], 2);
-        const uint32_t sgd = __builtin_amdgcn_alignbyte(bw[9 + ib], bw[8 + ib], 2);
-        const uint32_t qhb = ((ib < 4 ? qh0 : qh1) >> (8 * (ib & 3))) & 0xFFu;
+        const uint32_t qsd = fd(ib);
+        const uint32_t sgd = fd(8 + ib);
+        const uint32_t qhd = ib < 4 ? qh0 : qh1;
 #pragma unroll
         for (int grp = 0; grp < 4; ++grp) {
-            const uint32_t idx = ((qsd >> (8 * grp)) & 0xFFu) | (((qhb >> (2 * grp)) & 3u) << 8);
+            const uint32_t idx = ((qsd >> (8 * grp)) & 0xFFu) | (((qhd >> (8 * (ib & 3) + 2 * grp)) & 3u) << 8);
             const uint2 e = tab[idx];
             const uint32_t sb = (sgd >> (8 * grp)) & 0xFFu;
             B.w[2 * (4 * ib + grp)] = signed_mags(e.x, sb & 15u);
@@ -132,7 +146,8 @@ __device__ __forceinline__ float iq2_sub(const Iq2Block& B, int ib, const uint32
     const uint32_t scb = (B.sc[ib >> 2] >> (8 * (ib & 3))) & 0xFFu;
     const int ls0 = (int)(scb & 15u), ls1 = (int)(scb >> 4);
     // 24-bit multiplies: |s| <= 16 * 43 * 127 < 2^23 and ls <= 15, so the products are exact
-    const int sumi = (__mul24(s0, ls0) + __mul24(s1, ls1) + (s0 + s1) / 2) / 4;
+    const int v = __mul24(s0, ls0) + __mul24(s1, ls1) + (s0 + s1) / 2;
+    const int sumi = (v + (int)(((uint32_t)v >> 31) * 3u)) >> 2;  // v / 4, truncated toward zero
     return (B.d * dx) * (float)sumi;
 }
 
@@ -178,7 +193,7 @@ __global__ __launch_bounds__(64 * NW) void k_iq2_gu(const uint8_t* __restrict__ 
                                                      int hq_rows, const uint64_t* __restrict__ eptr) {
     constexpr int kCols = 2 * NW;
     extern __shared__ __align__(16) uint32_t smem[];
-    __shared__ uint2 tab[1024];
+    __shared__ uint2 tab[kIq2sTabEntries];
     __shared__ float rowv[kCols][64];
     __shared__ uint8_t qsc[kCols][32];
     Item item;
@@ -202,21 +217,21 @@ __global__ __launch_bounds__(64 * NW) void k_iq2_gu(const uint8_t* __restrict__ 
     // loads in the order their data is needed: the grid codes, the first column batch's images (when their rows
     // need no memory read), then the weights; the table store waits for the codes alone, the image commit for
     // the images alone
-    uint4 codes[512 / (64 * NW)];
+    uint4 codes[kTabRounds<64 * NW>];
     grid_codes_load<64 * NW>(codes);
     const int nc0 = min(kCols, item.ncol);
     uint32_t raw[21];
-    int off;
+    uint32_t off;
     if (stage_direct(item, 0, nc0, true)) {  // straight-line inside each branch, so no wait lands between the loads
         StagePieces sp;
         stage_issue_direct(sp, ximg, qb, 0, nc0, kCols, 0, item, true);
         __builtin_amdgcn_sched_barrier(0);
-        load_block_raw(rowp, b, raw, off);
+        off = load_block_raw(rowp, b, raw);
         __builtin_amdgcn_sched_barrier(0);
         grid_table_store<64 * NW>(codes, tab);
         stage_commit_direct(sp, smem);
     } else {
-        load_block_raw(rowp, b, raw, off);
+        off = load_block_raw(rowp, b, raw);
         grid_table_store<64 * NW>(codes, tab);
         stage_images(smem, ximg, qb, 0, nc0, kCols, item, perm, k, true, 0, 4 * 64 * NW);
     }
@@ -265,7 +280,7 @@ __global__ __launch_bounds__(256) void k_iq2_down(const uint8_t* __restrict__ do
                                                    int F, int Fs, int cps, float* __restrict__ Y,
                                                    const uint64_t* __restrict__ eptr, const int32_t* __restrict__ dmap) {
     extern __shared__ __align__(16) uint32_t smem[];
-    __shared__ uint2 tab[1024];
+    __shared__ uint2 tab[kIq2sTabEntries];
     Item item;
     if (!work_item(items, blockIdx.y, item)) return;
     const int Fe = item.shared ? Fs : F;
@@ -281,15 +296,15 @@ __global__ __launch_bounds__(256) void k_iq2_down(const uint8_t* __restrict__ do
     const bool live = r < H;
     // loads in the order their data is needed (see k_iq2_gu): grid codes, the first column batch's h images,
     // then the weights
-    uint4 codes[2];
+    uint4 codes[kTabRounds<256>];
     grid_codes_load<256>(codes);
     const int nc0 = min(cps, item.ncol);
     StagePieces sp;
     stage_issue_direct(sp, himg, h_blocks, 0, nc0, cps, 0, item, false);
     __builtin_amdgcn_sched_barrier(0);
     uint32_t raw[21];
-    int off;
-    load_block_raw(base + (size_t)(live ? r : 0) * rb, b, raw, off);
+    uint32_t off;
+    off = load_block_raw(base + (size_t)(live ? r : 0) * rb, b, raw);
     __builtin_amdgcn_sched_barrier(0);
     grid_table_store<256>(codes, tab);
     stage_commit_direct(sp, smem);
@@ -318,9 +333,9 @@ __global__ __launch_bounds__(256) void k_iq2_down(const uint8_t* __restrict__ do
 // Generic IQ2_S GEMV over n_col columns of standard q8_1 blocks (iq_mmvq's contract, metal/src/iq.mm:148-169).
 __global__ __launch_bounds__(256) void k_iq2_mmvq(const uint8_t* __restrict__ w, const uint8_t* __restrict__ xq, int n_in,
                                                    int n_out, int n_col, float* __restrict__ y) {
-    __shared__ uint2 tab[1024];
+    __shared__ uint2 tab[kIq2sTabEntries];
     {
-        uint4 codes[2];
+        uint4 codes[kTabRounds<256>];
         grid_codes_load<256>(codes);
         grid_table_store<256>(codes, tab);
     }
@@ -334,8 +349,8 @@ __global__ __launch_bounds__(256) void k_iq2_mmvq(const uint8_t* __restrict__ w,
     Iq2Block B[1];
     {
         uint32_t raw[21];
-        int off;
-        load_block_raw(w + (size_t)(live ? r : 0) * rb, b, raw, off);
+        uint32_t off;
+        off = load_block_raw(w + (size_t)(live ? r : 0) * rb, b, raw);
         decode_block(raw, off, tab, B[0]);
     }
     const int xb = n_in >> 5;

@@ -82,6 +82,11 @@ CASES = [
     ("f32 router, prefill 512 Zipf 1.2", dict(router_dtype=1), 512, 19, True, "zipf", S.PATH_AUTO),
     ("f32 router, 200 tokens", dict(router_dtype=1, n_embd=512, n_ff=256, n_expert=64, top_k=6), 200, 20, True, None,
      S.PATH_AUTO),
+    # about three pairs per expert at the configs' geometry: nearly every routed item (and the shared remainder
+    # chunk of 32) is a thin work item
+    ("config geometry, 160 tokens (thin items)", {}, 160, 21, True, None, S.PATH_AUTO),
+    ("H=1024 F=512, 136 tokens (thin items, a shared remainder of 8)",
+     dict(n_embd=1024, n_ff=512, n_ff_shared=512, n_expert=128, top_k=4), 136, 22, True, None, S.PATH_AUTO),
 ]
 
 _LAYERS = {}
