@@ -282,7 +282,8 @@ smoe_status smoe_expert_group(const int32_t* ids, int32_t n, int32_t k_per_tok, 
  * routing weight) to row ent_dst[j] of out (n_out_rows rows of n_embd f32).  Each blob row is read once for all of
  * its group's entries.  The lists are read on the device and checked there: an entry whose token or row is out of
  * range, and a group whose blob is 0, write nothing.  The launch is sized by the caps, so a captured graph replays
- * for any lists.  Sizes: grp_ptr cap_groups, grp_start cap_groups + 1, ent_dst and ent_tok cap_entries.
+ * for any lists.  Sizes: grp_ptr cap_groups, grp_start cap_groups + 1, ent_dst and ent_tok cap_entries
+ * (cap_groups <= 65535, cap_entries <= 2^24).
  * Replaces moe_grouped_s2 / native_expert_grouped / moe_hit_grouped_s2_dev (s2_expert_grouped.hpp:104-108,
  * iq_kernels.hpp:70-80). */
 size_t smoe_expert_grouped_workspace_bytes(const smoe_geom* g, int32_t n_tokens, int32_t cap_groups,

@@ -1086,7 +1086,9 @@ smoe_status smoe_expert_grouped(const smoe_geom* g, const uint64_t* grp_ptr, con
     if (s != SMOE_OK) return s;
     if (n_tokens < 0 || cap_groups < 0 || cap_entries < 0 || n_out_rows < 0)
         return fail(SMOE_EINVAL, "expert_grouped: negative size");
-    if (cap_groups > (1 << 20) || cap_entries > (1 << 24)) return fail(SMOE_EINVAL, "expert_grouped: caps too large");
+    // one work-group row per group: the launch's second grid dimension holds at most 65535
+    if (cap_groups > 65535 || cap_entries > (1 << 24))
+        return fail(SMOE_EINVAL, "expert_grouped: cap_groups must be at most 65535 and cap_entries at most 2^24");
     if (n_tokens == 0 || cap_groups == 0 || cap_entries == 0 || n_out_rows == 0) return ok();
     if (!grp_ptr || !grp_start || !ent_dst || !ent_tok || !counts || !x_q8_1 || !out || !workspace)
         return fail(SMOE_ENULL, "expert_grouped: NULL buffer");

@@ -208,6 +208,9 @@ struct Shard {
             t.offset = c.get<uint64_t>();
         }
         if (const MetaValue* a = get("general.alignment"); a && a->u) alignment = a->u;
+        // an alignment beyond the file puts the data section past its end (and keeps the rounding below from
+        // wrapping around)
+        if (alignment > size) throw std::runtime_error("GGUF: " + path + ": the data section starts past the end");
         data_start = (c.pos() + alignment - 1) / alignment * alignment;
         if (data_start > size) throw std::runtime_error("GGUF: " + path + ": the data section starts past the end");
     }
@@ -417,6 +420,8 @@ smoe_status plan_layer(const smoe_model* m, int layer, int top_k, int with_share
         return report(SMOE_EINVAL, "layer " + std::to_string(layer) + ": only some of the hc_ffn tensors are present");
     if (n_hc == 4) {
         const uint64_t hc = P.hinj.t->ne[1], lr = P.hdown.t->ne[1];
+        if (hc == 0 || hc > 64 || lr == 0 || lr > 65536)  // bounds that keep the products below exact
+            return report(SMOE_EINVAL, "layer " + std::to_string(layer) + ": implausible hc_ffn stream counts");
         if (P.hdown.t->type != kGgufBf16 || P.hup.t->type != kGgufBf16 || P.hinj.t->type != kGgufBf16 ||
             P.hnorm.t->type != kGgufF32)
             return report(SMOE_ETYPE, "layer " + std::to_string(layer) + ": hc_ffn_{down,up,inject} must be BF16 and "

@@ -142,6 +142,7 @@ def bad_files(tmp_path):
     deep = (W.ARRAY, [(W.ARRAY, [(W.ARRAY, [(W.U8, [1])])])])
     one("nesting", W.build([("deep", W.ARRAY, deep)], []), "nested")
     one("alignstart", W.build([("general.alignment", W.U32, 1 << 20)], []), "past the end")
+    one("alignhuge", W.build([("general.alignment", W.U64, 1 << 63)], []), "past the end")
     one("short", b"GGUF\x03\x00", "too short")
     # the header cut short at several places: inside the counts, a key, a value, the tensor directory
     hdr_end = len(W.build(meta_all(), ts)) - sum(len(t.data) for t in ts) - 64
@@ -155,6 +156,16 @@ def test_refused_files(tmp_path):
     for name, p, frag in bad_files(tmp_path):
         with pytest.raises(RuntimeError, match=frag):
             S.Model(p)
+
+
+def test_alignment_that_would_wrap_refused(tmp_path):
+    """An alignment so large that rounding the data section's start up wraps past 2^64 refuses the file (it
+    would otherwise put the data section at the file's start)."""
+    smoe()
+    p = tmp_path / "wrap.gguf"
+    p.write_bytes(W.build([("general.alignment", W.U64, (1 << 64) - 8)], []))
+    with pytest.raises(RuntimeError, match="past the end"):
+        S.Model(str(p))
 
 
 def test_every_truncation_refused(tmp_path):
@@ -395,7 +406,9 @@ def test_layer_plan_refusals(tmp_path):
                      (swap("blk.0.hc_ffn_inject.weight", type_=W.T_F32,
                            data=np.zeros(4 * 4 * H, np.float32)), "must be BF16"),
                      (swap("blk.0.hc_ffn_norm.weight", ne=(4 * H - 1,), data=np.zeros(4 * H - 1, np.float32)),
-                      "disagree")):
+                      "disagree"),
+                     (swap("blk.0.hc_ffn_inject.weight", ne=(65 * H, 65), data=np.zeros(65 * 65 * H, np.uint16)),
+                      "implausible hc_ffn")):
         with pytest.raises(RuntimeError, match=frag):
             model(ts).plan(0, top_k=2)
     # a geometry the block does not run: the library's own reason

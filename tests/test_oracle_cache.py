@@ -127,6 +127,8 @@ def test_expert_grouped_and_verify_refusals():
     call = lambda cg=8, ce=16, T=4, wsb=ws, out=FAKE, x=FAKE, ws_p=FAKE: L.smoe_expert_grouped(
         C.byref(gc), FAKE, FAKE, FAKE, FAKE, FAKE, cg, ce, x, T, out, 8, ws_p, wsb, None)
     assert call(cg=-1) == -1
+    assert call(cg=65536) == -1  # one grid row per group: at most 65535
+    assert call(ce=(1 << 24) + 1) == -1
     assert call(wsb=ws - 1) == -2
     assert call(out=None) == -6
     assert call(ws_p=FAKE + 64) == -5
