@@ -444,7 +444,8 @@ def cpu_baseline(S, a):
     (flat (expert, row-range) jobs per stage, one worker per core, each weight row decoded once for all of its
     expert's tokens; oracle/smoe_cpu_pool.c), compiled with -O3 -march=native for this host and timed on it, with
     every core of this GPU's share and with 1 thread, on configs[0] (b=1), configs[1] (b=16) and configs[3]
-    (IQ2_S b=64), each on one synthetic layer with a fresh batch per call."""
+    (IQ2_S b=64), each on one synthetic layer with a fresh batch per call; and configs[2] (prefill 512) through the
+    oracle's prefill contract."""
     import oracle as O
     cores = max(1, min(16, len(os.sched_getaffinity(0))))
     tmp = tempfile.mkdtemp(prefix="smoe_cpu_")
@@ -480,6 +481,20 @@ def cpu_baseline(S, a):
             gbs = bytes_model(S, sg, T, D)[0] * n / el / 1e9
             out[f"{name}_threads{threads}"] = {"tok_s": tok_s, "layer_gbs": gbs, "calls": n, "seconds": el}
             log(f"cpu baseline {name}, {threads} threads: {tok_s:.1f} tok/s, {gbs:.2f} GB/s ({n} calls)")
+    # configs[2] (prefill 512, Zipf(1.2) routing as in the GPU leg): the oracle's prefill contract (or_moe_prefill,
+    # OpenMP over tokens, each token's experts in turn), the whole batch with every core and a 64-token sample of
+    # the same batch with one thread
+    og = O.Geom()
+    bias = S.zipf_bias(og.n_expert, 1.2, a.seed, n_tokens=512, top_k=og.top_k, n_embd=og.n_embd)
+    w = O.make_weights(og, a.seed + 3000, zipf_bias=bias)
+    x = O.gen_normal(a.seed + 3002, 1, 512 * og.n_embd).reshape(512, og.n_embd)
+    for threads, T in ((cores, 512), (1, 64)):
+        t0 = time.perf_counter()
+        O.moe_prefill(og, w, x[:T], n_threads=threads)
+        el = time.perf_counter() - t0
+        out[f"prefill512_threads{threads}"] = {"tok_s": T / el, "tokens": T, "seconds": el,
+                                               "path": "oracle or_moe_prefill (liboracle.so)"}
+        log(f"cpu baseline prefill512, {threads} threads: {T / el:.1f} tok/s ({T} tokens)")
     head = out[f"b1_threads{cores}"]
     return {"value": head["tok_s"], "unit": "tokens/s", "cores": cores, "kind": "port",
             "sample": (f"configs[0] (decode b=1): {head['calls']} layer calls on one synthetic layer, each on a fresh "
