@@ -811,6 +811,16 @@ def expert_grouped(g: Geom, groups: Dict, x_q8, n_tokens: int, out, cap_groups: 
     import torch
     cg = groups["grp_ptr"].numel() if cap_groups is None else cap_groups
     ce = groups["ent_dst"].numel() if cap_entries is None else cap_entries
+    # the kernels read the lists up to the caps: every list must hold them
+    lists = (("grp_ptr", torch.int64, cg), ("grp_start", torch.int32, cg + 1), ("ent_dst", torch.int32, ce),
+             ("ent_tok", torch.int32, ce), ("counts", torch.int32, 2))
+    for key, _, n in lists:
+        if groups[key].numel() < n:
+            raise SmoeError(-2, f"{key} has {groups[key].numel()} elements, needs {n}")
+    if out.dim() != 2 or out.shape[1] != g.n_embd:
+        raise SmoeError(-2, f"out has shape {tuple(out.shape)}, needs (rows, {g.n_embd})")
+    for key, dtype, n in lists:
+        _need(groups[key], key, dtype, numel=n)
     _need(x_q8, "x_q8", torch.uint8, numel=n_tokens * (g.n_embd // 32) * 36)
     _need(out, "out", torch.float32)
     nb = int(lib().smoe_expert_grouped_workspace_bytes(C.byref(g.c()), n_tokens, cg, ce))
@@ -841,6 +851,8 @@ class VerifyWindow:
         import torch
         _need(x, "x", torch.float32)
         T, H, K = x.shape[0], self.g.n_embd, self.g.top_k
+        if x.dim() != 2 or x.shape[1] != H:
+            raise SmoeError(-2, f"x has shape {tuple(x.shape)}, needs (tokens, {H})")
         if T > self.max_tokens:
             raise SmoeError(-1, f"{T} tokens exceed the window's {self.max_tokens}")
         _need(table, "table", torch.int64, numel=self.g.n_expert)
@@ -858,9 +870,12 @@ class VerifyWindow:
 
     def end(self, r: Dict, add_shared: bool = True, y=None, stream=None):
         import torch
-        T = r["ids"].shape[0]
+        T, H, K = r["ids"].shape[0], self.g.n_embd, self.g.top_k
+        _need(r["rows"], "rows", torch.float32, numel=(T * K + T) * H)
+        _need(r["weights"], "weights", torch.float32, numel=T * K)
         if y is None:
-            y = torch.empty((T, self.g.n_embd), dtype=torch.float32, device=r["rows"].device)
+            y = torch.empty((T, H), dtype=torch.float32, device=r["rows"].device)
+        _need(y, "y", torch.float32, numel=T * H)
         _check(lib().smoe_verify_end(C.byref(self._gc), T, r["rows"].data_ptr(), r["weights"].data_ptr(),
                                      int(add_shared), y.data_ptr(), self.ws.data_ptr(), self.ws_bytes,
                                      _stream(stream)))

@@ -155,3 +155,21 @@ def test_expert_grouped_and_verify_refusals():
     assert end(T=-1) == -1 and end(T=0) == 0
     assert end(wsb=vws - 1) == -2
     assert end(y=FAKE) == -1  # y overlaps rows
+
+
+def test_python_binding_refuses_short_lists():
+    """The grouped-experts and verify-window bindings refuse, before any launch, lists shorter than the caps and
+    activations of the wrong width (CPU tensors: the size checks come before the device check)."""
+    import torch
+    g = S.Geom(n_embd=256, n_ff=128, n_ff_shared=128, n_expert=8, top_k=2)
+    groups = dict(grp_ptr=torch.zeros(4, dtype=torch.int64), grp_start=torch.zeros(5, dtype=torch.int32),
+                  ent_dst=torch.zeros(8, dtype=torch.int32), ent_tok=torch.zeros(8, dtype=torch.int32),
+                  counts=torch.zeros(4, dtype=torch.int32))
+    x = torch.zeros(4 * (256 // 32) * 36, dtype=torch.uint8)
+    out = torch.zeros((8, 256), dtype=torch.float32)
+    with pytest.raises(S.SmoeError, match="grp_ptr has 4 elements, needs 5"):
+        S.expert_grouped(g, groups, x, 4, out, cap_groups=5)
+    with pytest.raises(S.SmoeError, match="ent_tok has 8 elements, needs 9"):
+        S.expert_grouped(g, dict(groups, ent_dst=torch.zeros(9, dtype=torch.int32)), x, 4, out)
+    with pytest.raises(S.SmoeError, match="out has shape"):
+        S.expert_grouped(g, groups, x, 4, torch.zeros((8, 128), dtype=torch.float32))
