@@ -253,6 +253,11 @@ CASES = [
      dict(n_embd=256, n_ff=128, n_ff_shared=128, n_expert=128, top_k=32), 3, 23, True),
     ("fused, shared wider than routed, T=3", dict(n_embd=2048, n_ff=256, n_ff_shared=512, n_expert=32, top_k=4), 3,
      24, True),
+    # more than 512 experts: 16 logits per lane in the selection (the fused launch's one-token and small-batch
+    # routes, and k_topk beyond 4 tokens), a non-power-of-two count with a partly filled last logit column
+    ("fused, 1024 experts, T=1", dict(n_embd=256, n_ff=128, n_ff_shared=128, n_expert=1024, top_k=8), 1, 25, True),
+    ("fused, 1024 experts, T=3", dict(n_embd=256, n_ff=128, n_ff_shared=128, n_expert=1024, top_k=8), 3, 26, True),
+    ("600 experts top-10, T=16", dict(n_embd=256, n_ff=128, n_ff_shared=128, n_expert=600, top_k=10), 16, 27, True),
     # the f32 router of the literal configs[0] (router_dtype 1): f32 weights and activations in the router
     ("f32 router, config 1 (decode b=1)", dict(router_dtype=1), 1, 41, True),
     ("f32 router, fused T=3", dict(router_dtype=1, n_expert=64), 3, 42, True),
@@ -298,7 +303,11 @@ def test_forward_decode_parity(torch, case):
     assert np.array_equal(ids_r, host(torch, tr["ids"]))
     assert np.max(np.abs(host(torch, tr["weights"]) - w_r) / np.abs(w_r)) <= 1e-5
     yref = O.moe_decode_ref(g, w_host, x, add_shared=add_shared, n_threads=8)
-    assert O.rel_l1_rows(y, yref).max() <= 1e-3
+    # the reference order rounds the f32 dots differently: rows agree to ~1e-7, except that where one of h's q8_1
+    # values (or a block's scale) rounds the other way for a token, its row moves by one q8_1 step, up to a few
+    # 1e-3 at n_ff 128 (the oracle's two orders differ so on their own; the device equals the device order above)
+    rel = O.rel_l1_rows(y, yref)
+    assert np.median(rel) <= 1e-5 and rel.max() <= 5e-3, rel
     if name == "golden small":
         assert np.array_equal(bits(y), bits(f["y"]))
     # determinism: a repeat is bitwise identical
