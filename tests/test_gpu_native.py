@@ -133,7 +133,8 @@ def test_forward_native_shared_decode(torch, case):
     assert np.array_equal(bits(host(torch, tr2["shared"])), bits(wtr["shared"]))
     # the reference-order chain within its own bound
     yref = O.moe_decode_ref(g, w_host, x, add_shared=add_shared, n_threads=8)
-    assert O.rel_l1_rows(host(torch, y), yref).max() <= 1e-3
+    rel = O.rel_l1_rows(host(torch, y), yref)  # one q8_1 step of h at most where a value rounds the other way
+    assert np.median(rel) <= 1e-5 and rel.max() <= 5e-3, rel
 
 
 def test_forward_native_shared_prefill(torch):

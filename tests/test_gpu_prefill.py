@@ -85,6 +85,8 @@ CASES = [
     # about three pairs per expert at the configs' geometry: nearly every routed item (and the shared remainder
     # chunk of 32) is a thin work item
     ("config geometry, 160 tokens (thin items)", {}, 160, 21, True, None, S.PATH_AUTO),
+    ("600 experts top-10, 300 tokens", dict(n_embd=256, n_ff=128, n_ff_shared=128, n_expert=600, top_k=10), 300, 23,
+     True, None, S.PATH_AUTO),
     ("H=1024 F=512, 136 tokens (thin items, a shared remainder of 8)",
      dict(n_embd=1024, n_ff=512, n_ff_shared=512, n_expert=128, top_k=4), 136, 22, True, None, S.PATH_AUTO),
 ]
