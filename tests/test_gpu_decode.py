@@ -258,6 +258,11 @@ CASES = [
     ("fused, 1024 experts, T=1", dict(n_embd=256, n_ff=128, n_ff_shared=128, n_expert=1024, top_k=8), 1, 25, True),
     ("fused, 1024 experts, T=3", dict(n_embd=256, n_ff=128, n_ff_shared=128, n_expert=1024, top_k=8), 3, 26, True),
     ("600 experts top-10, T=16", dict(n_embd=256, n_ff=128, n_ff_shared=128, n_expert=600, top_k=10), 16, 27, True),
+    # wider intermediate rows: the fused launch at n_ff 1024; at n_ff 2048 its down rows would take more than two
+    # units per lane, so the small batch runs as the three-launch path
+    ("n_ff 1024, T=1", dict(n_embd=1024, n_ff=1024, n_ff_shared=1024, n_expert=64, top_k=8), 1, 28, True),
+    ("n_ff 2048, T=2", dict(n_embd=512, n_ff=2048, n_ff_shared=2048, n_expert=32, top_k=4), 2, 29, True),
+    ("n_ff 2048, b=16", dict(n_embd=512, n_ff=2048, n_ff_shared=2048, n_expert=32, top_k=4), 16, 30, True),
     # the f32 router of the literal configs[0] (router_dtype 1): f32 weights and activations in the router
     ("f32 router, config 1 (decode b=1)", dict(router_dtype=1), 1, 41, True),
     ("f32 router, fused T=3", dict(router_dtype=1, n_expert=64), 3, 42, True),
