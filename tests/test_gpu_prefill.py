@@ -87,6 +87,11 @@ CASES = [
     ("config geometry, 160 tokens (thin items)", {}, 160, 21, True, None, S.PATH_AUTO),
     ("600 experts top-10, 300 tokens", dict(n_embd=256, n_ff=128, n_ff_shared=128, n_expert=600, top_k=10), 300, 23,
      True, None, S.PATH_AUTO),
+    # long down K loops (16 units) and 16 gate/up row blocks; the widest rows of the router tile (H 4096)
+    ("n_ff 2048, 200 tokens", dict(n_embd=512, n_ff=2048, n_ff_shared=2048, n_expert=32, top_k=4), 200, 24, True,
+     None, S.PATH_AUTO),
+    ("H=4096, 140 tokens", dict(n_embd=4096, n_ff=256, n_ff_shared=256, n_expert=16, top_k=4), 140, 25, True, None,
+     S.PATH_AUTO),
     ("H=1024 F=512, 136 tokens (thin items, a shared remainder of 8)",
      dict(n_embd=1024, n_ff=512, n_ff_shared=512, n_expert=128, top_k=4), 136, 22, True, None, S.PATH_AUTO),
 ]
