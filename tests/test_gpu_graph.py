@@ -3,7 +3,8 @@ router + the fused small-batch launch; three tokens; sixteen tokens: router, top
 combine; 160 tokens: the MFMA contract) is captured once and replayed three times, with the program's own eager
 calls and synchronisations between the replays, and every replay's outputs equal the eager calls' bit for bit.
 The calls share one workspace, so a replay also shows that no launch depends on what an earlier one left there
-(the fused launch's exchange words are cleared inside the call, by a kernel, not by a memset node)."""
+(the fused launch's exchange words are cleared inside the call, by a kernel, not by a memset node).  Also: the
+other call sequences under capture, and calls on two streams at once."""
 import sys
 
 import numpy as np
@@ -117,3 +118,28 @@ def test_graph_replays_other_paths(torch):
         lr.forward(x[1])
         torch.cuda.synchronize()
     assert all(bool(torch.isfinite(w).all()) for w in want.values())
+
+
+def test_concurrent_calls_on_two_streams(torch):
+    """Two layers with their own workspaces called on two streams (default priority) with no synchronisation
+    between them, at 1 token (the fused launch, whose down work-groups wait for the h words of their own launch),
+    16 and 130 tokens: every output equals the same calls run one after another, bit for bit."""
+    say("case: concurrent calls on two streams, 1/16/130 tokens")
+    g = S.Geom()
+    H = g.n_embd
+    layers = [S.MoELayer(g, S.synth_layer(g, 7700 + i), max_tokens=130) for i in range(2)]
+    for T in (1, 16, 130):
+        xs = [S.synth_normal(7800 + 10 * T + i, 100, T * H).view(T, H) for i in range(2)]
+        want = [layers[i].forward(xs[i]) for i in range(2)]
+        torch.cuda.synchronize()
+        streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+        for s in streams:
+            s.wait_stream(torch.cuda.current_stream())
+        got = [None, None]
+        for rep in range(4):  # the two streams' launches interleave
+            for i in range(2):
+                with torch.cuda.stream(streams[i]):
+                    got[i] = layers[i].forward(xs[i])
+        torch.cuda.synchronize()
+        for i in range(2):
+            assert torch.equal(got[i].view(torch.int32), want[i].view(torch.int32)), (T, i)
