@@ -186,19 +186,23 @@ constexpr int kRing = 148480;           // bytes of the stage ring
 constexpr int kDummy = kRing;           // 1 KB landing slot of the padding instructions
 constexpr int kLds = kRing + 1024;
 
-// MODE 0 (thin, <= kThinCols columns): stages of four units each (see below), rows as narrow.
-enum { kThin = 0, kNarrow = 1, kWide = 2 };
+// MODE 0 (thin, <= kThinCols columns): stages of four units each (see below), rows as narrow.  MODE 3 is the same
+// shape with a ring of one stage: k_mm_down_thin takes 55 KB of LDS, so two of its work-groups share a CU and one's
+// loads overlap the other's products (measured: the thin down items 8 us faster at the benchmark's prefill; the
+// same split of gate/up, whose thin work-groups stream four stages, gained nothing).
+enum { kThin = 0, kNarrow = 1, kWide = 2, kThin1 = 3 };
 constexpr int kMaxTiles = 8;  // column tiles of 16 per wave at most (the wide shape's 128 columns)
 constexpr int kThinCols = 16;
 template <int MODE>
 struct Shape {
+    static constexpr bool kIsThin = MODE == kThin || MODE == kThin1;
     static constexpr int kTok = MODE == kWide ? 128 : MODE == kNarrow ? 64 : kThinCols;
     static constexpr int MT = (kTok + 15) / 16;  // column tiles of a wave: every wave has every column
-    static constexpr int kStages = MODE == kWide ? 3 : MODE == kNarrow ? 5 : 2;
+    static constexpr int kStages = MODE == kWide ? 3 : MODE == kNarrow ? 5 : MODE == kThin ? 2 : 1;
     static constexpr int NS = 2;
     // units of 128 values per stage: the thin shape streams weights, four units at a time, so that a row's
     // weights arrive as one 144-byte window (16-byte aligned, 9 pieces) instead of four 48-byte ones
-    static constexpr int UPS = MODE == kThin ? 4 : 1;
+    static constexpr int UPS = kIsThin ? 4 : 1;
     static constexpr int kColPieces = 16 * UPS + 1;                // a column's records, then one pad piece
     static constexpr int kRowPieces = UPS == 1 ? 3 : 9 * UPS / 4;  // a row's weight window
     static constexpr int kRowDw = 4 * kRowPieces;
@@ -211,9 +215,11 @@ struct Shape {
     static constexpr int kSlots = kASlots + kWSlots;
     static constexpr int kABytes = kAPieces * 16;
     static constexpr int kStage = kABytes + kWPieces * 16;
+    static constexpr int kDummyAt = MODE == kThin1 ? kStages * kStage : kDummy;  // the padding instructions' slot
+    static constexpr int kLdsBytes = kDummyAt + 1024;
     static_assert(UPS == 1 || UPS == 4, "one or four units per stage");
     static_assert(kAPieces % 64 == 0 && kWPieces % 64 == 0, "whole DMA instructions");
-    static_assert(kStages * kStage <= kRing, "ring");
+    static_assert(kStages * kStage <= kRing && kLdsBytes <= kLds, "ring");
     static_assert((kStages - 2) * kSlots <= 63, "vmcnt range");
     static_assert(kStages - 2 <= 6, "wait_stages cases");
 };
@@ -294,12 +300,12 @@ struct MmPlan {
         const uint32_t sw = __builtin_amdgcn_readfirstlane((uint32_t)(S::UPS == 1 ? 36 * u - 4 * (u & 3) : 36 * u));
 #pragma unroll
         for (int m = 0; m < S::kASlots; ++m) {
-            const uint32_t at = a_at[m] < 0 ? (uint32_t)kDummy : st + (uint32_t)a_at[m];
+            const uint32_t at = a_at[m] < 0 ? (uint32_t)S::kDummyAt : st + (uint32_t)a_at[m];
             dma16(__builtin_amdgcn_readfirstlane(lds0 + at), a_off[m], ra, sa);
         }
 #pragma unroll
         for (int m = 0; m < S::kWSlots; ++m) {
-            const uint32_t at = w_at[m] < 0 ? (uint32_t)kDummy : st + (uint32_t)w_at[m];
+            const uint32_t at = w_at[m] < 0 ? (uint32_t)S::kDummyAt : st + (uint32_t)w_at[m];
             dma16(__builtin_amdgcn_readfirstlane(lds0 + at), w_off[m], w_rsrc[m], sw);
         }
     }
@@ -363,25 +369,35 @@ __device__ __forceinline__ void mm_loop_nt(f32x4 (&acc)[kMaxTiles][Shape<MODE>::
                     mm_unit<S::NS, NT, S::kColPieces, S::kRowDw>(acc, W, 9 * uu, rows, A + 16 * uu, tok0, i, q);
         }
     };
+    if constexpr (ST == 1) {  // one ring stage: load, wait, multiply; the CU's other work-group fills the gaps
+        for (int g = 0; g < nst; ++g) {
+            if (g) __syncthreads();  // everyone is done with stage g - 1
+            pl.issue(lds0, 0, S::UPS * g, ra);
+            vmcnt<0>();
+            __syncthreads();
+            stage(g, 0);
+        }
+    } else {
 #pragma unroll
-    for (int b = 0; b < ST - 1; ++b)
-        if (b < nst) pl.issue(lds0, b, S::UPS * b, ra);
-    int b = 0, g = 0;  // ring stage of stage g
-    // steady state: every iteration consumes stage g, with the ST - 2 stages after it still in flight, and issues
-    // stage g + ST - 1 (a constant wait, no test)
-    for (; g + ST - 1 < nst; ++g) {
-        vmcnt<(ST - 2) * S::kSlots>();
-        __syncthreads();  // stage g is in LDS for everyone; everyone is done with stage g - 1
-        pl.issue(lds0, b == 0 ? ST - 1 : b - 1, S::UPS * (g + ST - 1), ra);
-        stage(g, b);
-        b = b + 1 == ST ? 0 : b + 1;
-    }
-    // the last stages (all of them when there are fewer than ST - 1): nothing left to issue, the waits shrink
-    for (; g < nst; ++g) {
-        wait_stages<S::kSlots>(nst - 1 - g);
-        __syncthreads();
-        stage(g, b);
-        b = b + 1 == ST ? 0 : b + 1;
+        for (int b = 0; b < ST - 1; ++b)
+            if (b < nst) pl.issue(lds0, b, S::UPS * b, ra);
+        int b = 0, g = 0;  // ring stage of stage g
+        // steady state: every iteration consumes stage g, with the ST - 2 stages after it still in flight, and issues
+        // stage g + ST - 1 (a constant wait, no test)
+        for (; g + ST - 1 < nst; ++g) {
+            vmcnt<(ST - 2) * S::kSlots>();
+            __syncthreads();  // stage g is in LDS for everyone; everyone is done with stage g - 1
+            pl.issue(lds0, b == 0 ? ST - 1 : b - 1, S::UPS * (g + ST - 1), ra);
+            stage(g, b);
+            b = b + 1 == ST ? 0 : b + 1;
+        }
+        // the last stages (all of them when there are fewer than ST - 1): nothing left to issue, the waits shrink
+        for (; g < nst; ++g) {
+            wait_stages<S::kSlots>(nst - 1 - g);
+            __syncthreads();
+            stage(g, b);
+            b = b + 1 == ST ? 0 : b + 1;
+        }
     }
 }
 
@@ -393,7 +409,7 @@ __device__ __forceinline__ void mm_loop(f32x4 (&acc)[kMaxTiles][Shape<MODE>::NS]
     for (int n = 0; n < kMaxTiles; ++n)
 #pragma unroll
         for (int s = 0; s < Shape<MODE>::NS; ++s) acc[n][s] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    if constexpr (MODE == kThin) {  // one tile
+    if constexpr (Shape<MODE>::kIsThin) {  // one tile
         mm_loop_nt<MODE, 1>(acc, lds, pl, units, ra, rows, tok0, i, q);
         return;
     } else if constexpr (MODE == kNarrow) {
@@ -575,13 +591,34 @@ __global__ __launch_bounds__(512) void k_mm_down(const uint8_t* __restrict__ dow
     if (!work_item(items, blockIdx.y, item)) return;
     const int Fe = item.shared ? Fs : F;
     const int ncol = item.ncol;
+    if (ncol <= kThinCols) return;  // k_mm_down_thin's
     if ((int)threadIdx.x < ncol) rowidx[threadIdx.x] = item.first + threadIdx.x;
     __syncthreads();
     const int units = Fe >> 7;
     const uint8_t* d0 = item.shared ? down_sh : down_exps + (size_t)item.e * H * ((size_t)(F >> 7) * 36);
     if (ncol > 64) mm_down_body<kWide>(lds, rowidx, item, ncol, units, d0, hrec, hrec_bytes, h_rec, sg, H, Y);
-    else if (ncol > kThinCols) mm_down_body<kNarrow>(lds, rowidx, item, ncol, units, d0, hrec, hrec_bytes, h_rec, sg, H, Y);
-    else mm_down_body<kThin>(lds, rowidx, item, ncol, units, d0, hrec, hrec_bytes, h_rec, sg, H, Y);
+    else mm_down_body<kNarrow>(lds, rowidx, item, ncol, units, d0, hrec, hrec_bytes, h_rec, sg, H, Y);
+}
+
+// The thin items (<= kThinCols columns) on k_mm_down's grid, launched after it: one-stage ring (55 KB of LDS), two
+// work-groups per CU.  A thin down work-group's K is one stage at n_ff <= 512, so it would otherwise hold a CU idle
+// while its only stage loads.
+__global__ __launch_bounds__(512) void k_mm_down_thin(const uint8_t* __restrict__ down_exps,
+                                                      const uint8_t* __restrict__ down_sh,
+                                                      const uint32_t* __restrict__ hrec, uint32_t hrec_bytes, int h_rec,
+                                                      const float* __restrict__ sg, const int4* __restrict__ items,
+                                                      int H, int F, int Fs, float* __restrict__ Y) {
+    __shared__ __align__(16) uint8_t lds[Shape<kThin1>::kLdsBytes];
+    __shared__ int rowidx[kThinCols];
+    Item item;
+    if (!work_item(items, blockIdx.y, item) || item.ncol > kThinCols) return;
+    const int Fe = item.shared ? Fs : F;
+    const int ncol = item.ncol;
+    if ((int)threadIdx.x < ncol) rowidx[threadIdx.x] = item.first + threadIdx.x;
+    __syncthreads();
+    const int units = Fe >> 7;
+    const uint8_t* d0 = item.shared ? down_sh : down_exps + (size_t)item.e * H * ((size_t)(F >> 7) * 36);
+    mm_down_body<kThin1>(lds, rowidx, item, ncol, units, d0, hrec, hrec_bytes, h_rec, sg, H, Y);
 }
 
 // ------------------------------------------------------------------------------------------------ launchers
@@ -652,8 +689,12 @@ hipError_t launch_mm_down(const uint8_t* down_exps, const uint8_t* down_sh, cons
                           hipStream_t s) {
     const size_t bytes = act_rec_bytes(n_hrec);
     if (bytes >= kOob) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_mm_down, dim3((unsigned)((H + kWgRows - 1) / kWgRows), (unsigned)max_items), dim3(512), 0, s,
-                       down_exps, down_sh, hrec, (uint32_t)bytes, h_rec, sg, items, H, F, Fs, Y);
+    // the thin items after the others: their kernel's smaller LDS lets two work-groups share a CU
+    const dim3 grid((unsigned)((H + kWgRows - 1) / kWgRows), (unsigned)max_items);
+    hipLaunchKernelGGL(k_mm_down, grid, dim3(512), 0, s, down_exps, down_sh, hrec, (uint32_t)bytes, h_rec, sg, items, H,
+                       F, Fs, Y);
+    hipLaunchKernelGGL(k_mm_down_thin, grid, dim3(512), 0, s, down_exps, down_sh, hrec, (uint32_t)bytes, h_rec, sg,
+                       items, H, F, Fs, Y);
     return hipGetLastError();
 }
 

@@ -94,6 +94,9 @@ CASES = [
      S.PATH_AUTO),
     ("H=1024 F=512, 136 tokens (thin items, a shared remainder of 8)",
      dict(n_embd=1024, n_ff=512, n_ff_shared=512, n_expert=128, top_k=4), 136, 22, True, None, S.PATH_AUTO),
+    # H 1536: 12 units (three four-unit thin stages); n_ff 384: three gate/up row blocks, down rows of three units
+    ("H=1536 F=384, 150 tokens", dict(n_embd=1536, n_ff=384, n_ff_shared=384, n_expert=64, top_k=4), 150, 26, True,
+     None, S.PATH_AUTO),
 ]
 
 _LAYERS = {}
