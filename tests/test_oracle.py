@@ -203,6 +203,16 @@ def test_iq2s_grid_matches_reference(codecs):
     assert sha(O.iq2s_grid()) == "e1aa1473412b0552c2174c30ef22ab4073f6a181b85a17056e8249bd2932fd88"
 
 
+def test_iq2s_codebook_copies_identical():
+    """The kernels compile their own copy of the codebook table; it is the oracle's pinned one, byte for byte."""
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    with open(os.path.join(root, "oracle", "iq2s_grid_codes.inc"), "rb") as f:
+        pinned = f.read()
+    with open(os.path.join(root, "stratametal_amd", "csrc", "iq2s_grid_codes.inc"), "rb") as f:
+        kernels = f.read()
+    assert kernels == pinned
+
+
 def _iq2s_brute(w, xq, n_in, n_out):
     grid = O.iq2s_grid()
     rb = n_in // 256 * 82
