@@ -120,6 +120,14 @@ typedef struct {
      * or more in magnitude (finite x), bit 1 -- such an h value.  The matrix cores take these as fp16, so the
      * affected tokens' outputs are then not the prefill contract's (inf or NaN).  0 on the decode path. */
     int32_t* overflow;
+    /* More of FfnTrace's expert stages (egate, eup; sgate, sup, sh_hq), for the reference's stage-wise check
+     * (metal/src/pack_parity.cpp:8584-8600): the products of each stage from the device's own q8_1 inputs.  Decode
+     * path only; asking for any of them runs the unfused kernels, as above. */
+    float* egate;     /* [T*k][n_ff] each pair's gate dots (before SwiGLU), by dispatch position */
+    float* eup;       /* [T*k][n_ff] each pair's up dots */
+    float* sgu;       /* [2][T][n_ff_shared] the shared expert's gate dots, then its up dots (layers with a shared
+                         expert) */
+    uint8_t* shq;     /* [T][n_ff_shared/32] q8_1 blocks of the shared expert's h (layers with a shared expert) */
 } smoe_trace;
 
 #define SMOE_STAGE_EVENTS 6

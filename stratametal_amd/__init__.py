@@ -49,7 +49,8 @@ class _Weights(C.Structure):
 
 class _Trace(C.Structure):
     _fields_ = [(n, C.c_void_p) for n in ("logits", "ids", "weights", "counts", "offsets", "perm", "slot", "sgate",
-                                          "stage_events", "xq", "hq", "parts", "shared", "overflow")]
+                                          "stage_events", "xq", "hq", "parts", "shared", "overflow", "egate", "eup",
+                                          "sgu", "shq")]
 
 class _Hc(C.Structure):
     _fields_ = [("hc", C.c_int32), ("hc_lr", C.c_int32), ("eps", C.c_float), ("norm", C.c_void_p),
@@ -339,8 +340,10 @@ class MoELayer:
                 stages: bool = False):
         """y = MoE(x).  With `trace`, also returns the routing and the dispatch (logits, ids, weights, counts,
         offsets, perm, slot, sgate); with `stages` as well, the expert stages (xq, hq: q8_1 blocks of x and of each
-        pair's h on the decode path; parts, shared: each pair's expert output and the shared expert's, by dispatch
-        position) and the prefill path's fp16 `overflow` mask -- the decode path then runs its unfused kernels."""
+        pair's h on the decode path; egate, eup: each pair's gate and up dots; sgu, shq: the shared expert's gate and
+        up dots ([2][T][n_ff_shared]) and the q8_1 blocks of its h; parts, shared: each pair's expert output and the
+        shared expert's, by dispatch position) and the prefill path's fp16 `overflow` mask -- the decode path then
+        runs its unfused kernels."""
         import torch
         if x.dim() != 2:
             raise SmoeError(-1, f"x must be (tokens, {self.g.n_embd}), got {tuple(x.shape)}")
@@ -365,14 +368,19 @@ class MoELayer:
                        sgate=torch.empty(T, dtype=torch.float32, device=dev))
             names = ["logits", "ids", "weights", "counts", "offsets", "perm", "slot", "sgate"]
             if stages:
-                H, F = self.g.n_embd, self.g.n_ff
+                H, F, Fs = self.g.n_embd, self.g.n_ff, max(self.g.n_ff_shared, 32)
                 out.update(xq=torch.empty((T, H // 32 * 36), dtype=torch.uint8, device=dev),
                            hq=torch.empty((T * K, F // 32 * 36), dtype=torch.uint8, device=dev),
                            parts=torch.empty((T * K, H), dtype=torch.float32, device=dev),
                            shared=torch.empty((T, H), dtype=torch.float32, device=dev),
-                           overflow=torch.full((1,), -1, dtype=torch.int32, device=dev))
+                           overflow=torch.full((1,), -1, dtype=torch.int32, device=dev),
+                           egate=torch.empty((T * K, F), dtype=torch.float32, device=dev),
+                           eup=torch.empty((T * K, F), dtype=torch.float32, device=dev),
+                           sgu=torch.empty((2, T, Fs), dtype=torch.float32, device=dev),
+                           shq=torch.empty((T, Fs // 32 * 36), dtype=torch.uint8, device=dev))
             tr = _Trace(*[out[n].data_ptr() for n in names], None,
-                        *[out[n].data_ptr() if stages else None for n in ("xq", "hq", "parts", "shared", "overflow")])
+                        *[out[n].data_ptr() if stages else None
+                          for n in ("xq", "hq", "parts", "shared", "overflow", "egate", "eup", "sgu", "shq")])
         _check(lib().smoe_forward_path(C.byref(self._gc), C.byref(self._wc), x.data_ptr(), T, y.data_ptr(),
                                        int(add_shared), self.ws.data_ptr(), self.ws_bytes,
                                        None if tr is None else C.byref(tr), path, _stream(stream)))

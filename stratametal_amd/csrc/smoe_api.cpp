@@ -373,7 +373,8 @@ smoe_status forward_impl(const smoe_geom* g, const smoe_weights* w, float* x_io,
     SMOE_MARK();
     const bool fused_norm = x_prev && !mfma;
     // the expert stages of the trace: the decode path's unfused kernels, so that every stage lands in memory
-    const bool stages = trace && (trace->xq || trace->hq || trace->parts || trace->shared);
+    const bool stages = trace && (trace->xq || trace->hq || trace->parts || trace->shared || trace->egate ||
+                                  trace->eup || trace->sgu || trace->shq);
     int32_t* xflags = (trace && trace->overflow && mfma) ? reinterpret_cast<int32_t*>(ws + L.oflags) : nullptr;
     int32_t* hflags = xflags ? xflags + L.n_xflags : nullptr;
     // batches of at most kFusedRouteTokens tokens on the Q2_0 GEMV path: the gate/up kernel routes the batch itself,
@@ -425,7 +426,19 @@ smoe_status forward_impl(const smoe_geom* g, const smoe_weights* w, float* x_io,
     const uint8_t* gs = static_cast<const uint8_t*>(w->gate_sh);
     const uint8_t* us = static_cast<const uint8_t*>(w->up_sh);
     const uint8_t* ds = static_cast<const uint8_t*>(w->down_sh);
-    uint8_t* hq = (trace && !mfma) ? trace->hq : nullptr;
+    // the expert stages of a traced decode-path call, written by the gate/up kernels
+    smoe::StageOut so{};
+    if (trace && !mfma) {
+        so.hq = trace->hq;
+        so.egate = trace->egate;
+        so.eup = trace->eup;
+        if (!nat) {
+            so.sgu = trace->sgu;
+            so.shq = trace->shq;
+        }
+        so.P = P;
+        so.T = T;
+    }
     if (mfma) {
         SMOE_TRY(smoe::launch_mm_gu(ge, ue, gs, us, ximg, (int64_t)T * (H / 64), items, perm, K, H, F, Fs,
                                     shf ? 1 : 0, n_items, himg, L.h_rec, st, hflags),
@@ -436,7 +449,7 @@ smoe_status forward_impl(const smoe_geom* g, const smoe_weights* w, float* x_io,
                  "down");
     } else if (iq2) {
         SMOE_TRY(smoe::launch_iq2_gu(ge, ue, gs, us, ximg, items, perm, K, H, F, Fs, shf ? 1 : 0, n_items, himg,
-                                     L.h_blocks, st, hq, P),
+                                     L.h_blocks, st, &so),
                  "gate/up");
         SMOE_MARK();
         SMOE_TRY(smoe::launch_iq2_down(de, ds, himg, L.h_blocks, sg, items, H, F, Fs, n_items, Y, st), "down");
@@ -454,7 +467,7 @@ smoe_status forward_impl(const smoe_geom* g, const smoe_weights* w, float* x_io,
                      "route + gate/up");
         else
             SMOE_TRY(smoe::launch_q2_gu(ge, ue, gs, us, ximg, items, perm, K, H, F, Fs, shf ? 1 : 0, n_items, himg,
-                                        L.h_blocks, st, hq, P),
+                                        L.h_blocks, st, &so),
                      "gate/up");
         SMOE_MARK();
         if (small_down)
@@ -479,6 +492,17 @@ smoe_status forward_impl(const smoe_geom* g, const smoe_weights* w, float* x_io,
         if (trace->parts) SMOE_TRY(smoe::launch_copy_f32(Y, (int64_t)P * H, trace->parts, st), "trace parts");
         if (trace->shared && has_sh)
             SMOE_TRY(smoe::launch_copy_f32(Y + (size_t)P * H, (int64_t)T * H, trace->shared, st), "trace shared");
+        if (nat && !mfma) {  // the native shared chain's own stages: its gate and up dots, the q8_1 of its h
+            const int Fn = g->n_ff_shared;
+            if (trace->sgu)
+                SMOE_TRY(smoe::launch_copy_f32(reinterpret_cast<const float*>(ws + L.ngu), 2 * (int64_t)T * Fn,
+                                               trace->sgu, st),
+                         "trace shared gate/up");
+            if (trace->shq)  // 36-byte blocks: whole dwords
+                SMOE_TRY(smoe::launch_copy_f32(reinterpret_cast<const float*>(ws + L.nhq), (int64_t)T * (Fn / 32) * 9,
+                                               reinterpret_cast<float*>(trace->shq), st),
+                         "trace shared h");
+        }
         if (trace->overflow)
             SMOE_TRY(smoe::launch_flags_mask(xflags, xflags ? (x_prev ? T : smoe::act_records_blocks((int64_t)T * (H / 64))) : 0, hflags,
                                              hflags ? (int64_t)(F > Fs ? F : Fs) / 128 * n_items : 0, trace->overflow,
@@ -1113,14 +1137,14 @@ smoe_status smoe_expert_grouped(const smoe_geom* g, const uint64_t* grp_ptr, con
              "grouped items");
     if (iq2) {
         SMOE_TRY(smoe::launch_iq2_gu(nullptr, nullptr, nullptr, nullptr, ximg, items, etok, 1, H, F, 0, 0, cap_groups,
-                                     himg, hb, st, nullptr, 0, grp_ptr),
+                                     himg, hb, st, nullptr, grp_ptr),
                  "grouped gate/up");
         SMOE_TRY(smoe::launch_iq2_down(nullptr, nullptr, himg, hb, nullptr, items, H, F, 0, cap_groups, out, st,
                                        grp_ptr, edst),
                  "grouped down");
     } else {
         SMOE_TRY(smoe::launch_q2_gu(nullptr, nullptr, nullptr, nullptr, ximg, items, etok, 1, H, F, 0, 0, cap_groups,
-                                    himg, hb, st, nullptr, 0, grp_ptr),
+                                    himg, hb, st, nullptr, grp_ptr),
                  "grouped gate/up");
         SMOE_TRY(smoe::launch_q2_down(nullptr, nullptr, himg, hb, nullptr, items, H, F, 0, cap_groups, out, st, grp_ptr,
                                       edst),
@@ -1186,14 +1210,14 @@ smoe_status smoe_verify_begin(const smoe_geom* g, const smoe_weights* w, const u
     const uint8_t* ds = static_cast<const uint8_t*>(w->down_sh);
     if (iq2) {
         SMOE_TRY(smoe::launch_iq2_gu(nullptr, nullptr, gs, us, ximg, items, ent_tok, 1, H, F, Fs, shf ? 1 : 0, L.n_items,
-                                     himg, L.h_blocks, st, nullptr, 0, grp_ptr),
+                                     himg, L.h_blocks, st, nullptr, grp_ptr),
                  "verify gate/up");
         SMOE_TRY(smoe::launch_iq2_down(nullptr, ds, himg, L.h_blocks, sg, items, H, F, Fs, L.n_items, rows, st, grp_ptr,
                                        ent_dst),
                  "verify down");
     } else {
         SMOE_TRY(smoe::launch_q2_gu(nullptr, nullptr, gs, us, ximg, items, ent_tok, 1, H, F, Fs, shf ? 1 : 0, L.n_items,
-                                    himg, L.h_blocks, st, nullptr, 0, grp_ptr),
+                                    himg, L.h_blocks, st, nullptr, grp_ptr),
                  "verify gate/up");
         SMOE_TRY(smoe::launch_q2_down(nullptr, ds, himg, L.h_blocks, sg, items, H, F, Fs, L.n_items, rows, st, grp_ptr,
                                       ent_dst),

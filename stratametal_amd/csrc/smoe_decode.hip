@@ -1435,8 +1435,8 @@ template <int NIT, int MAXUPL, bool PRESTAGED, bool HQ = false>
 __device__ __forceinline__ void gu_compute(const Item& item, int hb, uint32_t* smem, uint32_t (&w)[NIT][MAXUPL][9],
                                            const uint32_t* __restrict__ ximg, const int32_t* __restrict__ perm, int k,
                                            int H, uint32_t* __restrict__ himg, int h_blocks, float (&rowv)[kGuCols][64],
-                                           uint8_t (&qsc)[8][32], uint64_t* __restrict__ xchg, uint8_t* __restrict__ hq,
-                                           int hq_rows, int hq_blocks) {
+                                           uint8_t (&qsc)[8][32], uint64_t* __restrict__ xchg, const StageOut& so,
+                                           int F, int Fs) {
     const RowGeo G = row_geo(H);
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int grp = lane / G.lpr, l = lane - grp * G.lpr;
@@ -1488,11 +1488,8 @@ __device__ __forceinline__ void gu_compute(const Item& item, int hb, uint32_t* s
                 q8_image_store(h, live_c, qsc[hw], nullptr, false, xchg + ((size_t)row * h_blocks + hb) * kXchgSlots);
             else
                 q8_image_store(h, live_c, qsc[hw], himg + ((size_t)row * h_blocks + hb) * kImgDw);
-            if constexpr (HQ) {  // the trace's standard q8_1 block of a pair's h (k_prep's quantiser: s = f32 sum of h)
-                uint32_t ds;
-                const int q = q8_1_value(h, &ds);
-                q8_1_store(q, ds, hq + ((size_t)row * hq_blocks + hb) * 36, live_c && row < hq_rows);
-            }
+            if constexpr (HQ)  // the trace's stages: gate and up dots, the standard q8_1 block of h (k_prep's quantiser)
+                stage_store(so, row, hb, live_c ? rowv[hw][i] : 0.0f, live_c ? rowv[hw][32 + i] : 0.0f, h, live_c, F, Fs);
         }
         if (c0 + kGuCols < item.ncol) __syncthreads();
     }
@@ -1506,7 +1503,7 @@ __device__ __forceinline__ void q2_gu_item(const Item& item, int hb, uint32_t* s
                                            const uint8_t* __restrict__ up_sh, const uint32_t* __restrict__ ximg,
                                            const int32_t* __restrict__ perm, int k, int H, int F,
                                            uint32_t* __restrict__ himg, int h_blocks, uint64_t* __restrict__ xchg = nullptr,
-                                           uint8_t* __restrict__ hq = nullptr, int hq_rows = 0) {
+                                           StageOut so = {}, int Fs = 0) {
     __shared__ float rowv[kGuCols][64];
     __shared__ uint8_t qsc[8][32];
     uint32_t w[NIT][MAXUPL][9];
@@ -1518,8 +1515,8 @@ __device__ __forceinline__ void q2_gu_item(const Item& item, int hb, uint32_t* s
         gu_commit(item, direct, sp, smem, ximg, perm, k, H);
         __syncthreads();
     }
-    gu_compute<NIT, MAXUPL, PRESTAGED, HQ>(item, hb, smem, w, ximg, perm, k, H, himg, h_blocks, rowv, qsc, xchg, hq,
-                                           hq_rows, F >> 5);
+    gu_compute<NIT, MAXUPL, PRESTAGED, HQ>(item, hb, smem, w, ximg, perm, k, H, himg, h_blocks, rowv, qsc, xchg, so, F,
+                                           Fs);
 }
 
 template <int NIT, int MAXUPL, bool HQ>
@@ -1527,8 +1524,8 @@ __global__ __launch_bounds__(256) void k_q2_gu(const uint8_t* __restrict__ gate_
                                                 const uint8_t* __restrict__ gate_sh, const uint8_t* __restrict__ up_sh,
                                                 const uint32_t* __restrict__ ximg, const int4* __restrict__ items,
                                                 const int32_t* __restrict__ perm, int k, int H, int F, int Fs,
-                                                uint32_t* __restrict__ himg, int h_blocks, uint8_t* __restrict__ hq,
-                                                int hq_rows, const uint64_t* __restrict__ eptr) {
+                                                uint32_t* __restrict__ himg, int h_blocks, const StageOut so,
+                                                const uint64_t* __restrict__ eptr) {
     extern __shared__ __align__(16) uint32_t smem[];
     asm volatile("" ::"s"(gate_exps), "s"(up_exps), "s"(gate_sh), "s"(up_sh), "s"(ximg), "s"(himg), "s"(perm), "s"(k),
                  "s"(H), "s"(F), "s"(Fs), "s"(h_blocks));  // every kernarg loaded before the item
@@ -1541,7 +1538,7 @@ __global__ __launch_bounds__(256) void k_q2_gu(const uint8_t* __restrict__ gate_
         item.e = 0;
     }
     q2_gu_item<NIT, MAXUPL, false, HQ>(item, blockIdx.x, smem, gate_exps, up_exps, gate_sh, up_sh, ximg, perm, k, H, F,
-                                       himg, h_blocks, nullptr, hq, hq_rows);
+                                       himg, h_blocks, nullptr, so, Fs);
 }
 
 // Gate/up of a batch of at most kShCols tokens straight from the logits, with no route kernel before it.  Grid
@@ -2564,21 +2561,23 @@ int gemv_shared_chunk() { return kShCols; }
 
 hipError_t launch_q2_gu(const uint8_t* gate_exps, const uint8_t* up_exps, const uint8_t* gate_sh, const uint8_t* up_sh,
                         const uint32_t* ximg, const int4* items, const int32_t* perm, int k, int H, int F, int Fs,
-                        int has_shared, int max_items, uint32_t* himg, int h_blocks, hipStream_t s, uint8_t* hq,
-                        int hq_rows, const uint64_t* eptr) {
+                        int has_shared, int max_items, uint32_t* himg, int h_blocks, hipStream_t s, const StageOut* so,
+                        const uint64_t* eptr) {
     const int Fmax = has_shared && Fs > F ? Fs : F;
     dim3 grid((unsigned)(Fmax / 32), (unsigned)max_items);
     int nit, upl;
     gu_shape(H, nit, upl);
     const size_t lds = (size_t)kGuCols * (H >> 5) * kImgLdsDw * 4 + 16;  // + the dead staging slot
-    // the traced variant (hq: the trace's q8_1 of h) is its own instantiation: the plain kernel keeps its registers
+    // the traced variant (the trace's expert stages) is its own instantiation: the plain kernel keeps its registers
+    const StageOut none{};
+    const bool traced = so && so->any();
 #define SMOE_GU(N, U)                                                                                                \
-    if (hq)                                                                                                          \
+    if (traced)                                                                                                      \
         hipLaunchKernelGGL((k_q2_gu<N, U, true>), grid, dim3(256), lds, s, gate_exps, up_exps, gate_sh, up_sh, ximg,  \
-                           items, perm, k, H, F, Fs, himg, h_blocks, hq, hq_rows, eptr);                             \
+                           items, perm, k, H, F, Fs, himg, h_blocks, *so, eptr);                                     \
     else                                                                                                             \
         hipLaunchKernelGGL((k_q2_gu<N, U, false>), grid, dim3(256), lds, s, gate_exps, up_exps, gate_sh, up_sh, ximg, \
-                           items, perm, k, H, F, Fs, himg, h_blocks, nullptr, 0, eptr)
+                           items, perm, k, H, F, Fs, himg, h_blocks, none, eptr)
     SMOE_SHAPE_DISPATCH(SMOE_GU)
 #undef SMOE_GU
     return hipGetLastError();

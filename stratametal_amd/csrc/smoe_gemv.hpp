@@ -4,6 +4,7 @@
 
 #include "smoe_device.hpp"
 #include "smoe_items.hpp"
+#include "smoe_launch.hpp"
 
 namespace smoe {
 
@@ -488,6 +489,33 @@ __device__ __forceinline__ void residual_rmsnorm_row(const float* xr, const floa
         __syncthreads();
         for (int c = (int)threadIdx.x; c < (n >> 2); c += 256)
             reinterpret_cast<float4*>(o)[c] = reinterpret_cast<const float4*>(row)[c];
+    }
+}
+
+// The expert stages of a traced call for one column's 32 values of h (half wave = column, lane & 31 = value i of
+// rows block hb): the gate and up dots g, u and the q8_1 block of h, at pair row `row` (dispatch position; rows from
+// so.P are the shared expert's tokens).  Every lane of the half must call it (the quantiser exchanges lanes); `live`
+// is the same for the whole half.
+__device__ __forceinline__ void stage_store(const StageOut& so, int row, int hb, float g, float u, float h, bool live,
+                                            int F, int Fs) {
+    const int i = threadIdx.x & 31;
+    uint32_t ds;
+    const int q = q8_1_value(h, &ds);
+    const bool routed = row < so.P;
+    const int t = row - so.P;
+    const bool ok = live && (routed || t < so.T);
+    const int width = routed ? F : Fs;
+    uint8_t* hqb = routed ? so.hq : so.shq;
+    const size_t r = routed ? (size_t)row : (size_t)t;
+    if (hqb) q8_1_store(q, ds, hqb + (r * (size_t)(width >> 5) + hb) * 36, ok);
+    const size_t e = r * (size_t)width + (size_t)hb * 32 + i;
+    if (ok && routed) {
+        if (so.egate) so.egate[e] = g;
+        if (so.eup) so.eup[e] = u;
+    }
+    if (ok && !routed && so.sgu) {
+        so.sgu[e] = g;
+        so.sgu[(size_t)so.T * Fs + e] = u;
     }
 }
 

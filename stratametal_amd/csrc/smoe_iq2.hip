@@ -189,8 +189,8 @@ __global__ __launch_bounds__(64 * NW) void k_iq2_gu(const uint8_t* __restrict__ 
                                                      const uint8_t* __restrict__ gate_sh, const uint8_t* __restrict__ up_sh,
                                                      const uint32_t* __restrict__ ximg, const int4* __restrict__ items,
                                                      const int32_t* __restrict__ perm, int k, int H, int F, int Fs,
-                                                     uint32_t* __restrict__ himg, int h_blocks, uint8_t* __restrict__ hq,
-                                                     int hq_rows, const uint64_t* __restrict__ eptr) {
+                                                     uint32_t* __restrict__ himg, int h_blocks, const StageOut so,
+                                                     const uint64_t* __restrict__ eptr) {
     constexpr int kCols = 2 * NW;
     extern __shared__ __align__(16) uint32_t smem[];
     __shared__ uint2 tab[kIq2sTabEntries];
@@ -260,11 +260,8 @@ __global__ __launch_bounds__(64 * NW) void k_iq2_gu(const uint8_t* __restrict__ 
             const float h = live_c ? silu_mul(rowv[hw][i], rowv[hw][32 + i]) : 0.0f;
             const int row = item.first + c0 + (live_c ? hw : 0);
             q8_image_store(h, live_c, qsc[hw], himg + ((size_t)row * h_blocks + hb) * kImgDw, true);
-            if (hq) {  // the trace's standard q8_1 block of a pair's h
-                uint32_t ds;
-                const int q = q8_1_value(h, &ds);
-                q8_1_store(q, ds, hq + ((size_t)row * (F >> 5) + hb) * 36, live_c && row < hq_rows);
-            }
+            if (so.any())  // the trace's stages: gate and up dots, the standard q8_1 block of h
+                stage_store(so, row, hb, live_c ? rowv[hw][i] : 0.0f, live_c ? rowv[hw][32 + i] : 0.0f, h, live_c, F, Fs);
         }
         __syncthreads();
     }
@@ -372,15 +369,15 @@ bool iq2_shape_ok(int n_in) {
 
 hipError_t launch_iq2_gu(const uint8_t* gate_exps, const uint8_t* up_exps, const uint8_t* gate_sh, const uint8_t* up_sh,
                          const uint32_t* ximg, const int4* items, const int32_t* perm, int k, int H, int F, int Fs,
-                         int has_shared, int max_items, uint32_t* himg, int h_blocks, hipStream_t s, uint8_t* hq,
-                         int hq_rows, const uint64_t* eptr) {
+                         int has_shared, int max_items, uint32_t* himg, int h_blocks, hipStream_t s, const StageOut* so,
+                         const uint64_t* eptr) {
     const int Fmax = has_shared && Fs > F ? Fs : F;
     dim3 grid((unsigned)(Fmax / 32), (unsigned)max_items);
     const int nb = H / 256;
     const size_t lds = (size_t)(2 * nb) * (H >> 5) * kImgLdsDw * 4 + 16;  // + the dead staging slot
 #define SMOE_IQ2_GU(NW)                                                                                           \
     hipLaunchKernelGGL((k_iq2_gu<NW>), grid, dim3(64 * (NW)), lds, s, gate_exps, up_exps, gate_sh, up_sh, ximg, items, \
-                       perm, k, H, F, Fs, himg, h_blocks, hq, hq_rows, eptr)
+                       perm, k, H, F, Fs, himg, h_blocks, so ? *so : StageOut{}, eptr)
     if (nb == 2) SMOE_IQ2_GU(2);
     else if (nb == 4) SMOE_IQ2_GU(4);
     else SMOE_IQ2_GU(8);

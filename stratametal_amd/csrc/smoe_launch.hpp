@@ -7,6 +7,19 @@
 
 namespace smoe {
 
+// Where the gate/up kernels of a traced call write the expert stages (smoe_trace's hq, egate, eup, sgu, shq; any
+// may be NULL).  Row r < P of the pair rows is the routed pair at dispatch position r, row P + t the shared expert's
+// token t (t < T).
+struct StageOut {
+    uint8_t* hq;     // [P][F/32] q8_1 blocks of h
+    float* egate;    // [P][F] gate dots
+    float* eup;      // [P][F] up dots
+    float* sgu;      // [2][T][Fs]: the shared expert's gate dots, then its up dots
+    uint8_t* shq;    // [T][Fs/32] q8_1 blocks of the shared expert's h
+    int P, T;
+    __host__ __device__ bool any() const { return hq || egate || eup || sgu || shq; }
+};
+
 bool gemv_shape_ok(int n_in);           // a row length the GEMV kernels tile (n_in % 128 == 0, <= 8 units per lane)
 bool down_shapes_match(int F, int Fs);   // routed and shared down rows share one launch shape
 size_t img_bytes(int64_t n_blocks);      // bytes of n_blocks q8_1 images
@@ -39,11 +52,11 @@ int gemv_shared_chunk();   // shared-expert tokens per GEMV work item
 hipError_t launch_q2_gu(const uint8_t* gate_exps, const uint8_t* up_exps, const uint8_t* gate_sh, const uint8_t* up_sh,
                         const uint32_t* ximg, const int4* items, const int32_t* perm, int k, int H, int F, int Fs,
                         int has_shared, int max_items, uint32_t* himg, int h_blocks, hipStream_t s,
-                        uint8_t* hq = nullptr, int hq_rows = 0, const uint64_t* eptr = nullptr);
+                        const StageOut* so = nullptr, const uint64_t* eptr = nullptr);
 hipError_t launch_q2_down(const uint8_t* down_exps, const uint8_t* down_sh, const uint32_t* himg, int h_blocks,
                           const float* sg, const int4* items, int H, int F, int Fs, int max_items, float* Y,
                           hipStream_t s, const uint64_t* eptr = nullptr, const int32_t* dmap = nullptr);
-// (hq: the trace's q8_1 of the first hq_rows h rows.  eptr: the expert table of the grouped calls -- routed item e
+// (so: the expert stages of a traced call.  eptr: the expert table of the grouped calls -- routed item e
 // reads the blob at eptr[e], [gate rows | up rows | down rows], instead of the planes; dmap: routed column row
 // first + c of the down kernels is written to Y row dmap[first + c])
 // batches of at most 4 tokens: gate/up that routes the batch itself (no route kernel before it), and down rows
@@ -92,7 +105,7 @@ bool iq2_shape_ok(int n_in);  // n_in = 256 nb, nb in {2, 4, 8}
 hipError_t launch_iq2_gu(const uint8_t* gate_exps, const uint8_t* up_exps, const uint8_t* gate_sh, const uint8_t* up_sh,
                          const uint32_t* ximg, const int4* items, const int32_t* perm, int k, int H, int F, int Fs,
                          int has_shared, int max_items, uint32_t* himg, int h_blocks, hipStream_t s,
-                         uint8_t* hq = nullptr, int hq_rows = 0, const uint64_t* eptr = nullptr);
+                         const StageOut* so = nullptr, const uint64_t* eptr = nullptr);
 hipError_t launch_iq2_down(const uint8_t* down_exps, const uint8_t* down_sh, const uint32_t* himg, int h_blocks,
                            const float* sg, const int4* items, int H, int F, int Fs, int max_items, float* Y,
                            hipStream_t s, const uint64_t* eptr = nullptr, const int32_t* dmap = nullptr);

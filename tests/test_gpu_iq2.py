@@ -10,6 +10,7 @@ import numpy as np
 import pytest
 
 import oracle as O
+import stagewise as SW
 import stratametal_amd as S
 
 pytestmark = pytest.mark.gpu
@@ -108,10 +109,12 @@ def test_forward_iq2_s_parity(torch, case):
     for k in ("logits", "ids", "weights", "counts", "offsets", "perm", "slot"):
         assert np.array_equal(bits(host(torch, tr[k])), bits(wtr[k])), k
     assert np.array_equal(bits(y), bits(want)), f"max rel {O.rel_l1_rows(y, want).max()}"
-    yref = O.moe_decode_ref(g, w_host, x, add_shared=add_shared, n_threads=16)
-    # the reference order: rows agree closely except one q8_1 step of h where a value rounds the other way
-    rel = O.rel_l1_rows(y, yref)
-    assert np.median(rel) <= 1e-5 and rel.max() <= 5e-3, rel
+    # north_star's 1e-3 per row against the reference-order chain, or the reference's stage-wise check for a row
+    # beyond it
+    def stages():
+        yy, st = ml.forward(dev(torch, x), add_shared=add_shared, trace=True, stages=True)
+        return {k: host(torch, v) for k, v in st.items()}, host(torch, yy)
+    SW.reference_order_gate(g, w_host, x, y, add_shared, stages, say, n_threads=16)
     if name.startswith("config 4"):
         D = int((host(torch, tr["counts"]) > 0).sum())
         say(f"  distinct experts touched: {D}")

@@ -13,6 +13,7 @@ import numpy as np
 import pytest
 
 import oracle as O
+import stagewise as SW
 import stratametal_amd as S
 
 pytestmark = pytest.mark.gpu
@@ -131,10 +132,12 @@ def test_forward_native_shared_decode(torch, case):
     y2, tr2 = ml.forward(dev(torch, x), add_shared=add_shared, trace=True, stages=True)
     assert np.array_equal(bits(host(torch, y2)), bits(want))
     assert np.array_equal(bits(host(torch, tr2["shared"])), bits(wtr["shared"]))
-    # the reference-order chain within its own bound
-    yref = O.moe_decode_ref(g, w_host, x, add_shared=add_shared, n_threads=8)
-    rel = O.rel_l1_rows(host(torch, y), yref)  # one q8_1 step of h at most where a value rounds the other way
-    assert np.median(rel) <= 1e-5 and rel.max() <= 5e-3, rel
+    # the reference-order chain: 1e-3 per row, or the reference's stage-wise check for a row beyond it
+    htr2 = {k: host(torch, v) for k, v in tr2.items()}
+    rep = SW.stagewise(g, w_host, x, htr2, host(torch, y2), add_shared)
+    say(f"  stage-wise: {rep.summary()}")
+    assert rep.ok(), rep.summary()
+    SW.reference_order_gate(g, w_host, x, host(torch, y), add_shared, lambda: (htr2, host(torch, y2)), say)
 
 
 def test_forward_native_shared_prefill(torch):
