@@ -7,8 +7,8 @@ A step is one MoE layer call (router, top-k, dispatch, expert products, shared e
 synthetic tokens.  The headline workload is BASELINE.json configs[0]: one Qwen3-Next-style layer (H 2048, 512 Q2_0
 experts + 1 shared, top-10, FF 512) decoding one token.  `--layers` (default 48, ~21.7 GB) distinct layers are
 resident in HBM and consecutive steps walk through them, each with its own token; the K timed steps are one
-captured HIP graph replay, and a 1 GiB write between replays empties the 256 MB Infinity Cache (MALL), so every
-step reads its layer's bytes from HBM.  Per-stage kernel durations come from HIP events recorded on the launch
+captured HIP graph replay, and a 1 GiB read between replays empties the 256 MB Infinity Cache (MALL) of the layers'
+bytes, so every step reads its layer's bytes from HBM.  Per-stage kernel durations come from HIP events recorded on the launch
 stream between the kernels of an eager pass of the same steps (also after a flush).  The JSON line's `roofline` is
 the dominant decode kernel's; `roofline_prefill_512` is the prefill GEMM's (configs[2], the metric's second half).
 `extra` holds decode batch 16, prefill 512 with Zipf(1.2) routing, IQ2_S batch 64
@@ -53,6 +53,8 @@ def _args():
     ap.add_argument("--only", choices=("b1", "b16", "prefill", "iq2", "stack"), default=None,
                     help="measure only this workload (for a profiler run); prints its summary, no JSON line")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--flush", choices=("read", "write"), default="read",
+                    help="how the 1 GiB cache flush between timed passes touches its buffer")
     ap.add_argument("--stack-prefill", type=int, default=4096, help="prefill tokens of the 48-layer stack")
     ap.add_argument("--stack-decode", type=int, default=64, help="decode steps of the 48-layer stack")
     ap.add_argument("--cpu-seconds", type=float, default=3.0, help="CPU baseline seconds per (workload, threads)")
@@ -148,13 +150,19 @@ class HipEvents:
 
 
 class Flush:
-    """A 1 GiB buffer rewritten between timed passes, so that no layer's bytes are left in the MALL or L2."""
+    """A 1 GiB buffer read (or, with --flush write, rewritten) between timed passes, so that no layer's bytes are
+    left in the MALL or L2.  Reading leaves clean lines behind: a rewrite leaves the MALL full of dirty lines whose
+    write-back then competes with the timed steps' reads."""
 
-    def __init__(self, torch):
+    def __init__(self, torch, mode="read"):
         self.buf = torch.zeros(FLUSH_BYTES // 4, dtype=torch.float32, device="cuda")
+        self.mode = mode
 
     def __call__(self):
-        self.buf.add_(1.0)
+        if self.mode == "write":
+            self.buf.add_(1.0)
+        else:
+            self.sink = self.buf.sum()
 
 
 def measure(S, torch, stack, T, steps, warmup, seed, flush):
@@ -524,7 +532,7 @@ def main():
     import stratametal_amd as S
     S.C = ctypes
     g = S.Geom()
-    flush = Flush(torch)
+    flush = Flush(torch, a.flush)
     if a.only == "prefill":
         prefill(S, torch, g, a, flush)
         return
@@ -584,7 +592,7 @@ def main():
         "config": {"workload": "BASELINE configs[0]: one Qwen3-Next-style MoE layer decoding 1 token",
                    "tokens_per_step": 1, "n_embd": g.n_embd, "n_ff": g.n_ff, "n_expert": g.n_expert,
                    "top_k": g.top_k, "shared_experts": 1, "expert_type": "Q2_0", "router": "bf16",
-                   "resident_layers": a.layers, "cache": "1 GiB rewritten before the timed replay",
+                   "resident_layers": a.layers, "cache": f"1 GiB {'read' if a.flush == 'read' else 'rewritten'} before the timed replay",
                    "parallelism": "none (1 GPU)"},
         "roofline": roof, "roofline_prefill_512": extra.get("prefill_512", {}).get("roofline"),
         "cpu_baseline": cpu, "extra": extra,

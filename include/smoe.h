@@ -116,9 +116,10 @@ typedef struct {
     uint8_t* hq;      /* [T*k][n_ff/32] q8_1 blocks of each pair's h, by dispatch position (decode path only) */
     float* parts;     /* [T*k][n_embd] each pair's expert output before its routing weight, by dispatch position */
     float* shared;    /* [T][n_embd] the shared expert's output times sigmoid(sgate) (layers with a shared expert) */
-    /* [1] 0, or a mask of the prefill path's operand limits met: bit 0 -- an activation whose bf16 value is 65520
-     * or more in magnitude (finite x), bit 1 -- such an h value.  The matrix cores take these as fp16, so the
-     * affected tokens' outputs are then not the prefill contract's (inf or NaN).  0 on the decode path. */
+    /* [1] the call's status mask (smoe_forward_status's): 0, or bit 0 -- an activation whose bf16 value is 65520 or
+     * more in magnitude (finite x) met the prefill path's fp16 operands, bit 1 -- such an h value (the affected
+     * tokens' outputs are then not the prefill contract's: inf or NaN), bit 2 -- a bounded wait of the fused decode
+     * launch gave up (the rows of its down work-groups are NaN). */
     int32_t* overflow;
     /* More of FfnTrace's expert stages (egate, eup; sgate, sup, sh_hq), for the reference's stage-wise check
      * (metal/src/pack_parity.cpp:8584-8600): the products of each stage from the device's own q8_1 inputs.  Decode
@@ -134,6 +135,11 @@ typedef struct {
 
 /* ---------------------------------------------------------------------------------------------- block */
 
+/* Bits of a call's status mask (smoe_forward_status, smoe_trace.overflow). */
+#define SMOE_STATUS_X_FP16 1 /* an activation at or beyond 65520 in magnitude met the prefill path's fp16 operands */
+#define SMOE_STATUS_H_FP16 2 /* such an h value */
+#define SMOE_STATUS_WAIT 4   /* a bounded wait of the fused decode launch gave up: its down work-groups' y rows are NaN */
+
 /* Workspace bytes smoe_forward needs for up to `max_tokens` tokens (either path); 0 on bad geometry. */
 size_t smoe_workspace_bytes(const smoe_geom* g, int32_t max_tokens);
 
@@ -142,7 +148,11 @@ size_t smoe_workspace_bytes(const smoe_geom* g, int32_t max_tokens);
  * Replaces FfnExec::run's interior (metal/src/layer_exec.cpp:470-530) and the upstream per-layer
  * moe_layer / moe_route + moe_finish (include/strata/core/layer.hpp:140-189).  `workspace` is
  * device memory of at least smoe_workspace_bytes(g, n_tokens) bytes, 256-byte aligned; concurrent
- * calls need distinct workspaces. */
+ * calls need distinct workspaces.  A call takes at most 65535 tokens (n_tokens * top_k at most 2^24).
+ * Batches of at most 4 tokens on the decode path run as the router launch and one launch of the rest, whose down
+ * work-groups wait for the gate/up work-groups' h (a bounded wait).  Should a wait give up (a producer never arrived,
+ * e.g. its work-group was starved of a CU for ~0.1 s), the affected rows of y are NaN and smoe_forward_status reports
+ * SMOE_STATUS_WAIT; the call still returns SMOE_OK, as no host synchronisation happens on the call path. */
 smoe_status smoe_forward(const smoe_geom* g, const smoe_weights* w, const float* x, int32_t n_tokens, float* y,
                          int32_t add_shared, void* workspace, size_t workspace_bytes, const smoe_trace* trace,
                          void* hip_stream);
@@ -336,6 +346,19 @@ smoe_status smoe_verify_end(const smoe_geom* g, int32_t n_tokens, const float* r
  * caller serialises them.  The first call on a device looks up the scratch's device address once. */
 smoe_status smoe_forward_static(const smoe_geom* g, const smoe_weights* w, const float* x, int32_t n_tokens, float* y,
                                 int32_t add_shared, const smoe_trace* trace, void* hip_stream);
+
+/* The status of the last block call enqueued on `workspace` (smoe_forward, smoe_forward_path, smoe_forward_residual,
+ * smoe_ffn_run; NULL: the current GPU's scratch of smoe_forward_static), folded on hip_stream into *status (device
+ * memory, one int32) after that call: 0, or a mask of the SMOE_STATUS_* bits above.  The affected tokens' outputs are
+ * then not the contract's; the caller can rerun them (on SMOE_PATH_GEMV for the fp16 bits).  The library keeps the
+ * flag places of the last call on each of its 64 most recent workspaces (a workspace beyond them: SMOE_EINVAL).  No
+ * counterpart in the reference (its prompt path shares the fp16 limit, include/strata/prefill/kernels.hpp:97-98). */
+smoe_status smoe_forward_status(const void* workspace, int32_t* status, void* hip_stream);
+
+/* The bound of the fused decode launch's waits, in polls (each a memory round trip, ~1 us): polls > 0 sets it, 0
+ * restores the default (100000), a negative value makes every wait give up at once -- for tests of the give-up path.
+ * Returns the previous bound.  Applies to launches enqueued after it (a captured graph keeps its own). */
+int32_t smoe_set_wait_limit(int32_t polls);
 
 /* ---------------------------------------------------------------------------------------------- stages */
 

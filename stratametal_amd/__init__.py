@@ -58,6 +58,13 @@ class _Hc(C.Structure):
 
 
 STAGES = ("router", "route", "gate_up", "down", "combine")
+STATUS_X_FP16, STATUS_H_FP16, STATUS_WAIT = 1, 2, 4  # bits of a call's status mask (smoe.h SMOE_STATUS_*)
+
+
+def set_wait_limit(polls: int) -> int:
+    """The bound of the fused decode launch's waits (smoe_set_wait_limit): polls > 0 sets it, 0 restores the default,
+    a negative value makes every wait give up at once (tests of the give-up path).  Returns the previous bound."""
+    return int(lib().smoe_set_wait_limit(int(polls)))
 STAGE_EVENTS = len(STAGES) + 1
 
 
@@ -75,6 +82,8 @@ def lib():
             "smoe_forward_path": (i32, [vp, vp, vp, i32, vp, i32, vp, C.c_size_t, vp, i32, vp]),
             "smoe_forward_residual": (i32, [vp, vp, vp, vp, f32, vp, i32, vp, i32, vp, C.c_size_t, vp, vp]),
             "smoe_forward_static": (i32, [vp, vp, vp, i32, vp, i32, vp, vp]),
+            "smoe_forward_status": (i32, [vp, vp, vp]),
+            "smoe_set_wait_limit": (i32, [i32]),
             "smoe_hc_read_workspace_bytes": (C.c_size_t, [vp, i32, i32]),
             "smoe_hc_read": (i32, [vp, i32, vp, i32, vp, vp, vp, C.c_size_t, vp]),
             "smoe_hc_write": (i32, [vp, i32, vp, vp, vp, i32, vp, vp]),
@@ -385,6 +394,15 @@ class MoELayer:
                                        int(add_shared), self.ws.data_ptr(), self.ws_bytes,
                                        None if tr is None else C.byref(tr), path, _stream(stream)))
         return (y, out) if trace else y
+
+    def status(self, stream=None):
+        """The status mask of the last call on this layer's workspace (smoe_forward_status), as a device int32
+        tensor: 0, or STATUS_X_FP16 | STATUS_H_FP16 (the prefill path's fp16 operand limits) | STATUS_WAIT (a
+        fused decode launch's wait gave up; its rows are NaN)."""
+        import torch
+        out = torch.full((1,), -1, dtype=torch.int32, device=self.ws.device)
+        _check(lib().smoe_forward_status(self.ws.data_ptr(), out.data_ptr(), _stream(stream)))
+        return out
 
     def forward_residual(self, x_prev, r_prev, x, y=None, eps: float = 1e-6, add_shared: bool = True, stream=None):
         """The stack junction fused into this layer's call: x = RMSNorm(x_prev + r_prev) (written to `x`), then

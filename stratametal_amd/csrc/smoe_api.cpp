@@ -114,7 +114,7 @@ smoe_status check_geom(const smoe_geom* g) {
 
 struct Layout {
     size_t ximg, xbf, logits, sg, ids, wts, counts, offsets, perm, slot, elist, nlist, items, himg, Y, dwork, xchg,
-        oflags, nxq, ngu, nhq, total;
+        oflags, status, nxq, ngu, nhq, total;
     int h_blocks;  // q8_1 blocks per h row (GEMV path)
     int h_rec;     // 64-value records per h row (MFMA path)
     int64_t n_xflags, n_hflags;  // the MFMA path's per-work-group overflow flags (a trace asking for the mask)
@@ -122,6 +122,8 @@ struct Layout {
 
 // Work items: every touched expert plus the shared expert's token chunks (GEMV path); the MFMA path splits
 // an expert's pairs and the shared tokens into chunks of mfma_chunk() columns.
+constexpr int64_t kMaxGridY = 65535;  // the largest y dimension of a launch grid
+
 int max_items_gemv(const smoe_geom& g, int64_t T) {
     const int64_t P = T * g.top_k;
     return (int)((P < g.n_expert ? P : g.n_expert) + (sh_fused(g) ? smoe::shared_items((int)T) : 0));
@@ -169,6 +171,7 @@ Layout layout(const smoe_geom& g, int64_t T) {
     L.n_xflags = most(smoe::act_records_blocks(T * (H / 64)), T);
     L.n_hflags = (Fmax / 128) * (int64_t)max_items_mfma(g, T);
     L.oflags = take((size_t)(L.n_xflags + L.n_hflags) * 4);
+    L.status = take((size_t)smoe::fused_status_words((int)H) * 4);  // the fused decode launch's wait flags
     if (sh_native(g)) {  // the native shared expert's chain: x as q8_1 blocks, gate and up rows, q8_1 of h
         const int64_t Fs = g.n_ff_shared;
         L.nxq = take((size_t)T * (H / 32) * 36);
@@ -273,6 +276,14 @@ smoe_status check_forward(const smoe_geom* g, const smoe_weights* w, const float
     if (iq2 && path == SMOE_PATH_MFMA) return fail(SMOE_ETYPE, "the MFMA (prefill) path is built for Q2_0 experts only");
     const bool mfma = !iq2 && (path == SMOE_PATH_MFMA || (path == SMOE_PATH_AUTO && n_tokens >= kMfmaTokens));
 
+    // grids take tokens and work items on their y dimension, at most 65535: refused here, before any launch
+    if (n_tokens > kMaxGridY)
+        return fail(SMOE_EINVAL, std::to_string(n_tokens) + " tokens exceed " + std::to_string(kMaxGridY) +
+                                     " per call; split the batch");
+    const int64_t n_items = mfma ? max_items_mfma(*g, n_tokens) : max_items_gemv(*g, n_tokens);
+    if (n_items > kMaxGridY)
+        return fail(SMOE_EINVAL, std::to_string(n_items) + " expert work items exceed " + std::to_string(kMaxGridY) +
+                                     " per call; split the batch");
     const Layout L = layout(*g, n_tokens);
     if (mfma) {  // the MFMA kernels address the activation and h records with 31-bit buffer offsets
         const int64_t P = (int64_t)n_tokens * g->top_k;
@@ -294,6 +305,63 @@ smoe_status check_forward(const smoe_geom* g, const smoe_weights* w, const float
         const smoe_status _s = (call);      \
         if (_s != SMOE_OK) return _s;       \
     } while (0)
+
+// Where a call left its flag words in the workspace: the prefill path's fp16 operand flags of its records kernel and
+// k_mm_gu (bits 0 and 1 of the status mask), the fused decode launch's wait flags, one per down work-group (bit 2).
+struct FlagWords {
+    const void* ws = nullptr;
+    size_t x = 0, h = 0, w = 0;  // byte offsets in the workspace
+    int64_t nx = 0, nh = 0, nw = 0;
+};
+void flag_words(const smoe_geom& g, const Layout& L, int T, bool mfma, bool fused, bool junction, const void* ws,
+                FlagWords& f) {
+    f = FlagWords{};
+    f.ws = ws;
+    const int H = g.n_embd, F = g.n_ff, Fs = sh_fused(g) ? g.n_ff_shared : 0;
+    if (mfma) {
+        f.x = L.oflags;
+        f.nx = junction ? T : smoe::act_records_blocks((int64_t)T * (H / 64));
+        f.h = L.oflags + (size_t)L.n_xflags * 4;
+        f.nh = (int64_t)(F > Fs ? F : Fs) / 128 * max_items_mfma(g, T);
+    }
+    if (fused) {
+        f.w = L.status;
+        f.nw = smoe::fused_status_words(H);
+    }
+}
+smoe_status fold_status(const FlagWords& f, int32_t* out, hipStream_t st) {
+    const uint8_t* ws = static_cast<const uint8_t*>(f.ws);
+    SMOE_TRY(smoe::launch_flags_mask(reinterpret_cast<const int32_t*>(ws + f.x), f.nx,
+                                     reinterpret_cast<const int32_t*>(ws + f.h), f.nh, out, st,
+                                     reinterpret_cast<const int32_t*>(ws + f.w), f.nw),
+             "status mask");
+    return SMOE_OK;
+}
+
+// The flag words of the last call enqueued on each of the most recent workspaces (smoe_forward_status's table).
+constexpr int kFlagTable = 64;
+std::mutex g_flag_mu;
+FlagWords g_flag_table[kFlagTable];
+int g_flag_next = 0;
+void remember_flags(const FlagWords& f) {
+    std::lock_guard<std::mutex> lock(g_flag_mu);
+    for (FlagWords& e : g_flag_table)
+        if (e.ws == f.ws) {
+            e = f;
+            return;
+        }
+    g_flag_table[g_flag_next] = f;
+    g_flag_next = (g_flag_next + 1) % kFlagTable;
+}
+bool recall_flags(const void* ws, FlagWords& f) {
+    std::lock_guard<std::mutex> lock(g_flag_mu);
+    for (const FlagWords& e : g_flag_table)
+        if (e.ws && e.ws == ws) {
+            f = e;
+            return true;
+        }
+    return false;
+}
 
 // The native shared expert (its projections in their own types): q8_1 of x, gate and up, SwiGLU + q8_1, down
 // times sigmoid(sg[t]) into out[t] (T rows of n_embd), in the workspace's native-chain slots.
@@ -375,14 +443,16 @@ smoe_status forward_impl(const smoe_geom* g, const smoe_weights* w, float* x_io,
     // the expert stages of the trace: the decode path's unfused kernels, so that every stage lands in memory
     const bool stages = trace && (trace->xq || trace->hq || trace->parts || trace->shared || trace->egate ||
                                   trace->eup || trace->sgu || trace->shq);
-    int32_t* xflags = (trace && trace->overflow && mfma) ? reinterpret_cast<int32_t*>(ws + L.oflags) : nullptr;
+    // the prefill path's per-work-group flags of its fp16 operand limits (folded by a trace or smoe_forward_status)
+    int32_t* xflags = mfma ? reinterpret_cast<int32_t*>(ws + L.oflags) : nullptr;
     int32_t* hflags = xflags ? xflags + L.n_xflags : nullptr;
     // batches of at most kFusedRouteTokens tokens on the Q2_0 GEMV path: the gate/up kernel routes the batch itself,
     // and (when the batch's h images fit in LDS) the down kernel applies the combine; where the shapes allow, both
-    // run as one launch whose exchange words the router kernel clears
+    // run as one launch whose exchange words the router kernel clears (its down work-groups' wait flags: wflags)
     const bool small = !mfma && !iq2 && !stages && T <= kFusedRouteTokens;
     const bool small_down = small && smoe::down_combine_ok(T, K, L.h_blocks);
     const bool fused = small_down && smoe::moe_small_ok(T, K, H, F, Fs, shf ? 1 : 0, L.h_blocks);
+    int32_t* wflags = fused ? reinterpret_cast<int32_t*>(ws + L.status) : nullptr;
     uint8_t* xchg = ws + L.xchg;
     const size_t xchg_bytes = fused ? smoe::moe_small_xchg_bytes(T, K, n_items, L.h_blocks) : 0;
     uint16_t* xbf = mfma ? reinterpret_cast<uint16_t*>(ws + L.xbf) : nullptr;
@@ -456,7 +526,7 @@ smoe_status forward_impl(const smoe_geom* g, const smoe_weights* w, float* x_io,
     } else if (fused) {
         SMOE_TRY(smoe::launch_q2_moe_small(ge, ue, gs, us, de, ds, ximg, logits, sg, T, E, K, H, F, Fs, shf ? 1 : 0,
                                            ids, wts, counts, offsets, perm, slot, elist, nlist, items, n_items, L.h_blocks,
-                                           xchg, (shf && add_shared) ? 1 : 0, y, st),
+                                           xchg, (shf && add_shared) ? 1 : 0, y, wflags, st),
                  "route + gate/up + down + combine");
         SMOE_MARK();  // gate/up, down and combine are one launch: the later stage boundaries are empty
     } else {
@@ -485,6 +555,9 @@ smoe_status forward_impl(const smoe_geom* g, const smoe_weights* w, float* x_io,
         SMOE_TRY(smoe::launch_add_rows(y, Y + (size_t)P * H, T, H, st), "shared add");
     SMOE_MARK();
 #undef SMOE_MARK
+    FlagWords flags;
+    flag_words(*g, L, T, mfma, fused, x_prev != nullptr, workspace, flags);
+    remember_flags(flags);
     // the trace's expert stages and overflow mask, after the last stage event
     if (trace) {
         if (trace->xq && !mfma)
@@ -503,11 +576,7 @@ smoe_status forward_impl(const smoe_geom* g, const smoe_weights* w, float* x_io,
                                                reinterpret_cast<float*>(trace->shq), st),
                          "trace shared h");
         }
-        if (trace->overflow)
-            SMOE_TRY(smoe::launch_flags_mask(xflags, xflags ? (x_prev ? T : smoe::act_records_blocks((int64_t)T * (H / 64))) : 0, hflags,
-                                             hflags ? (int64_t)(F > Fs ? F : Fs) / 128 * n_items : 0, trace->overflow,
-                                             st),
-                     "trace overflow");
+        if (trace->overflow) SMOE_TRY_S(fold_status(flags, trace->overflow, st));
     }
     return ok();
 }
@@ -741,6 +810,25 @@ smoe_status smoe_forward_static(const smoe_geom* g, const smoe_weights* w, const
     if (!ws) return SMOE_EDEVICE;
     return forward_impl(g, w, const_cast<float*>(x), n_tokens, y, add_shared, ws, SMOE_STATIC_SCRATCH_BYTES, trace,
                         SMOE_PATH_AUTO, hip_stream, nullptr, nullptr, 0.0f);
+}
+
+smoe_status smoe_forward_status(const void* workspace, int32_t* status, void* hip_stream) {
+    if (!status) return fail(SMOE_ENULL, "forward_status: status is NULL");
+    if (!aligned(status, 4)) return fail(SMOE_EALIGN, "forward_status: status must be 4-byte aligned");
+    const void* ws = workspace ? workspace : device_scratch();
+    if (!ws) return SMOE_EDEVICE;
+    FlagWords f;
+    if (!recall_flags(ws, f))
+        return fail(SMOE_EINVAL, "forward_status: no call on this workspace is known (the library keeps the last " +
+                                     std::to_string(kFlagTable) + " workspaces)");
+    SMOE_TRY_S(fold_status(f, status, stream_of(hip_stream)));
+    return ok();
+}
+
+int32_t smoe_set_wait_limit(int32_t polls) {
+    const int32_t prev = smoe::wait_limit();
+    smoe::set_wait_limit(polls < 0 ? -1 : polls == 0 ? smoe::default_wait_limit() : polls);
+    return prev;
 }
 
 // ------------------------------------------------------------------------------------------------ stages

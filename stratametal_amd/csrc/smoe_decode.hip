@@ -11,6 +11,7 @@
 //   k_q2_down  per (touched expert | shared, a chunk of output rows): down rows (times the shared gate)
 //   k_combine  y = routing-weighted sum of the pair rows + the shared row
 // Reduction orders are fixed and restated on the host by the test oracle (oracle/smoe_oracle.c).
+#include <atomic>
 #include <utility>
 
 #include "smoe_device.hpp"
@@ -144,6 +145,242 @@ __device__ __forceinline__ float q2_unit_dot(const uint32_t (&w)[9], float d0, f
 // row is f32: lane l owns the 4-element chunks l, l+64, ... and fuses each product into its accumulator in element
 // order (fmaf, one rounding per step; oracle: or_f32_gemv_dev), then the same butterfly.  The shared gate row
 // stays bf16: its x values are rounded to bf16 from the f32 tile, so that sg equals the bf16 kernel's bit for bit.
+// The pieces of a router work-group (k_router).
+// One wave's weight row (row block rb, wave w: row 4 rb + w, clamped), loaded with every load issued.
+template <int MAXC, bool F32>
+struct RouterRow {
+    uint4 wv[MAXC];
+    float bv;
+    int row;       // rows_total or more: a dead wave (stores nothing)
+    bool frow;     // an f32 weight row (wave-uniform)
+    int wchunks;   // 16-byte chunks of the row
+};
+template <int MAXC, bool F32>
+__device__ __forceinline__ void router_row_load(const void* __restrict__ W, const uint16_t* __restrict__ w_inp,
+                                                const float* __restrict__ bias, int H, int E, int rows_total, int rb,
+                                                RouterRow<MAXC, F32>& R) {
+    const int lane = threadIdx.x & 63;
+    R.row = rb * 4 + (int)(threadIdx.x >> 6);
+    const int rowc = min(R.row, rows_total - 1);
+    R.frow = F32 && rowc < E;
+    const uint8_t* wr = rowc < E ? static_cast<const uint8_t*>(W) + (size_t)rowc * H * (F32 ? 4 : 2)
+                                 : reinterpret_cast<const uint8_t*>(w_inp);
+    R.wchunks = R.frow ? H >> 2 : H >> 3;
+#pragma unroll
+    for (int j = 0; j < MAXC; ++j) {
+        const int c = lane + 64 * j;
+        R.wv[j] = c < R.wchunks ? *reinterpret_cast<const uint4*>(wr + 16 * c) : make_uint4(0, 0, 0, 0);
+    }
+    R.bv = (bias && rowc < E) ? bias[rowc] : 0.0f;  // loaded once, outside the token loop
+}
+
+// The fused junction for tokens t0 .. t0 + nt - 1, four at a time: every thread holds xf + rprev of elements
+// tid + 256 m; the sums of squares in k_residual_rmsnorm's order give inv_s[t - t0]; with `stage` the scaled rows go
+// to the LDS tile (bf16, or f32 with F32), and with `xout` to xout.  Every thread of the work-group calls it.
+template <int NMJ, bool F32>
+__device__ __forceinline__ void router_junction(const float* __restrict__ xf, const float* __restrict__ rprev, int t0,
+                                                int nt, int H, float eps, bool stage, float* __restrict__ xout,
+                                                uint32_t* smem, float* inv_s, float (&wsum_s)[4][4]) {
+    const int tid = threadIdx.x;
+    uint16_t* xs16 = reinterpret_cast<uint16_t*>(smem);
+    float* xs32 = reinterpret_cast<float*>(smem);
+    for (int tb = 0; tb < nt; tb += 4) {
+        constexpr int NM = NMJ <= 16 ? NMJ : 1;
+        float sv[4][NM];
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            if (tb + g < nt) {
+                const float* xr = xf + (size_t)(t0 + tb + g) * H;
+                const float* rr = rprev + (size_t)(t0 + tb + g) * H;
+#pragma unroll
+                for (int m = 0; m < NM; ++m) {  // 256 NM >= H
+                    const int j = tid + 256 * m;
+                    const int jc = j < H ? j : H - 1;
+                    sv[g][m] = xr[jc] + rr[jc];
+                    if (j < H) acc[g] = __builtin_fmaf(sv[g][m], sv[g][m], acc[g]);
+                }
+            }
+        }
+        wave_sum_xor_fast_n<4>(acc);
+        if ((tid & 63) == 0) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) wsum_s[g][tid >> 6] = acc[g];
+        }
+        __syncthreads();
+        if (tid < 4 && tb + tid < nt) {
+            const float ss = ((wsum_s[tid][0] + wsum_s[tid][1]) + wsum_s[tid][2]) + wsum_s[tid][3];
+            inv_s[tb + tid] = 1.0f / __builtin_sqrtf(ss / (float)H + eps);
+        }
+        __syncthreads();
+        if (stage) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                if (tb + g < nt) {
+                    const float sc = inv_s[tb + g];
+                    float* xo = xout ? xout + (size_t)(t0 + tb + g) * H : nullptr;
+#pragma unroll
+                    for (int m = 0; m < NM; ++m) {
+                        const int j = tid + 256 * m;
+                        if (j < H) {
+                            const float v = sv[g][m] * sc;
+                            if constexpr (F32) xs32[(size_t)(tb + g) * H + j] = v;
+                            else xs16[(size_t)(tb + g) * H + j] = (uint16_t)f32_to_bf16(v);
+                            if (xo) xo[j] = v;
+                        }
+                    }
+                }
+            }
+        }
+    }
+}
+
+// The token tile of x into LDS (no junction): f32 as it is with F32, else bf16 (from xf, or the bf16 bits xb),
+// 8 vector loads in flight per thread.  The caller synchronises after.
+template <bool F32>
+__device__ __forceinline__ void router_stage(const float* __restrict__ xf, const uint16_t* __restrict__ xb, int t0,
+                                             int nt, int H, uint32_t* smem) {
+    if constexpr (F32) {
+        const int n4 = nt * H / 4;
+        for (int base = 0; base < n4; base += 256 * 8) {
+            float4 f[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int g = min(base + u * 256 + (int)threadIdx.x, n4 - 1);
+                f[u] = reinterpret_cast<const float4*>(xf + (size_t)t0 * H)[g];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int g = base + u * 256 + threadIdx.x;
+                if (g < n4) reinterpret_cast<float4*>(smem)[g] = f[u];
+            }
+        }
+    } else {
+        const int n8 = nt * H / 8;  // groups of 8 values = one uint4 of bf16
+        for (int base = 0; base < n8; base += 256 * 4) {
+            uint4 v[4];
+            if (xf) {
+                float4 f[8];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {  // clamped, so that every load issues back to back
+                    const int g = min(base + u * 256 + (int)threadIdx.x, n8 - 1);
+                    const float4* src = reinterpret_cast<const float4*>(xf + (size_t)t0 * H) + 2 * (size_t)g;
+                    f[2 * u] = src[0];
+                    f[2 * u + 1] = src[1];
+                }
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const float4 a = f[2 * u], b = f[2 * u + 1];
+                    v[u] = make_uint4(f32_to_bf16(a.x) | (f32_to_bf16(a.y) << 16),
+                                      f32_to_bf16(a.z) | (f32_to_bf16(a.w) << 16),
+                                      f32_to_bf16(b.x) | (f32_to_bf16(b.y) << 16),
+                                      f32_to_bf16(b.z) | (f32_to_bf16(b.w) << 16));
+                }
+            } else {
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int g = base + u * 256 + threadIdx.x;
+                    if (g < n8) v[u] = reinterpret_cast<const uint4*>(xb + (size_t)t0 * H)[g];
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int g = base + u * 256 + threadIdx.x;
+                if (g < n8) reinterpret_cast<uint4*>(smem)[g] = v[u];
+            }
+        }
+    }
+}
+
+// The wave's row against every token of the staged tile, NG tokens at a time (NG independent chains; each token's
+// chain is the same for any NG); lane 0 calls store(row, t, value) with the bias added to an expert row (row < E; row
+// E is the shared gate).
+template <int MAXC, bool F32, int NG = 4, class Store>
+__device__ __forceinline__ void router_row_dots(const RouterRow<MAXC, F32>& R, const uint32_t* smem, int H, int E,
+                                                int rows_total, int nt, bool has_bias, Store store) {
+    const int lane = threadIdx.x & 63;
+    const uint16_t* xs = reinterpret_cast<const uint16_t*>(smem);
+    const float* xs32 = reinterpret_cast<const float*>(smem);
+    const int chunks = H >> 3;
+    if (R.row >= rows_total) return;
+    for (int t = 0; t < nt; t += NG) {
+        const int ng = min(NG, nt - t);
+        float acc[NG];
+#pragma unroll
+        for (int g = 0; g < NG; ++g) acc[g] = 0.0f;
+        if constexpr (F32) {
+            if (R.frow) {
+#pragma unroll
+                for (int j = 0; j < MAXC; ++j) {
+                    const int c = lane + 64 * j;
+                    if (c < R.wchunks) {
+                        const float w4[4] = {u2f(R.wv[j].x), u2f(R.wv[j].y), u2f(R.wv[j].z), u2f(R.wv[j].w)};
+#pragma unroll
+                        for (int g = 0; g < NG; ++g) {
+                            if (g < ng) {
+                                const float4 xv = *reinterpret_cast<const float4*>(xs32 + (size_t)(t + g) * H + 4 * c);
+                                acc[g] = __builtin_fmaf(xv.x, w4[0], acc[g]);
+                                acc[g] = __builtin_fmaf(xv.y, w4[1], acc[g]);
+                                acc[g] = __builtin_fmaf(xv.z, w4[2], acc[g]);
+                                acc[g] = __builtin_fmaf(xv.w, w4[3], acc[g]);
+                            }
+                        }
+                    }
+                }
+            } else {  // the shared gate row: bf16(x) * bf16 w_inp, exact products in the bf16 kernel's order
+#pragma unroll
+                for (int j = 0; j < MAXC; ++j) {
+                    const int c = lane + 64 * j;
+                    if (c < chunks) {
+                        const uint32_t wq[4] = {R.wv[j].x, R.wv[j].y, R.wv[j].z, R.wv[j].w};
+#pragma unroll
+                        for (int g = 0; g < NG; ++g) {
+                            if (g < ng) {
+                                const float* xr = xs32 + (size_t)(t + g) * H + 8 * c;
+                                const float4 a = reinterpret_cast<const float4*>(xr)[0];
+                                const float4 b = reinterpret_cast<const float4*>(xr)[1];
+                                const float xv8[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+                                for (int q = 0; q < 4; ++q) {
+                                    const float x0 = u2f(f32_to_bf16(xv8[2 * q]) << 16);
+                                    const float x1 = u2f(f32_to_bf16(xv8[2 * q + 1]) << 16);
+                                    acc[g] = __builtin_fmaf(x0, u2f(wq[q] << 16), acc[g]);
+                                    acc[g] = __builtin_fmaf(x1, u2f(wq[q] & 0xFFFF0000u), acc[g]);
+                                }
+                            }
+                        }
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < MAXC && !F32; ++j) {
+            const int c = lane + 64 * j;
+            if (c < chunks) {
+                const uint32_t wq[4] = {R.wv[j].x, R.wv[j].y, R.wv[j].z, R.wv[j].w};
+#pragma unroll
+                for (int g = 0; g < NG; ++g) {
+                    if (g < ng) {
+                        const uint4 xv = *reinterpret_cast<const uint4*>(xs + (size_t)(t + g) * H + 8 * c);
+                        const uint32_t xq[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            acc[g] = __builtin_fmaf(u2f(xq[q] << 16), u2f(wq[q] << 16), acc[g]);
+                            acc[g] = __builtin_fmaf(u2f(xq[q] & 0xFFFF0000u), u2f(wq[q] & 0xFFFF0000u), acc[g]);
+                        }
+                    }
+                }
+            }
+        }
+        wave_sum_xor_fast_n<NG>(acc);
+        if (lane == 0) {
+#pragma unroll
+            for (int g = 0; g < NG; ++g)
+                if (g < ng) store(R.row, t + g, (has_bias && R.row < E) ? acc[g] + R.bv : acc[g]);
+        }
+    }
+}
+
 template <int MAXC, bool F32>
 __global__ __launch_bounds__(256) void k_router(const float* __restrict__ xf, const uint16_t* __restrict__ xb,
                                                  const void* __restrict__ W, const uint16_t* __restrict__ w_inp,
@@ -176,214 +413,25 @@ __global__ __launch_bounds__(256) void k_router(const float* __restrict__ xf, co
         if (rprev && live) ir = rprev[blk * 32 + (tid & 31)];
     }
     // a row block: the wave's weight row (clamped, every load issued), in flight during the staging below
-    const int lane = tid & 63;
-    const int row = blockIdx.x * 4 + (tid >> 6);
-    const int rowc = min(row, rows_total - 1);
-    const bool frow = F32 && rowc < E;  // an f32 weight row: 4 values per 16-byte chunk (wave-uniform)
-    const uint8_t* wr = rowc < E ? static_cast<const uint8_t*>(W) + (size_t)rowc * H * (F32 ? 4 : 2)
-                                 : reinterpret_cast<const uint8_t*>(w_inp);
-    const int chunks = H >> 3;                      // 8-value bf16 chunks
-    const int wchunks = frow ? H >> 2 : chunks;     // 16-byte chunks of this wave's row
-    uint4 wv[MAXC];
-    float bv = 0.0f;
-    if (!img_block) {
-#pragma unroll
-        for (int j = 0; j < MAXC; ++j) {
-            const int c = lane + 64 * j;
-            wv[j] = c < wchunks ? *reinterpret_cast<const uint4*>(wr + 16 * c) : make_uint4(0, 0, 0, 0);
-        }
-        bv = (bias && rowc < E) ? bias[rowc] : 0.0f;  // loaded once, outside the token loop
-    }
-    uint16_t* xs16 = reinterpret_cast<uint16_t*>(smem);
-    float* xs32 = reinterpret_cast<float*>(smem);
+    RouterRow<MAXC, F32> R;
+    if (!img_block) router_row_load<MAXC, F32>(W, w_inp, bias, H, E, rows_total, blockIdx.x, R);
     // values of a row per thread of the junction: 256 NM >= H (8 values per bf16 chunk, 4 per f32 chunk)
     constexpr int NMJ = F32 ? MAXC : 2 * MAXC;
-    if (NMJ <= 16 && rprev) {  // the fused junction, 4 tokens at a time; a row block stages s * scale from registers
-        for (int tb = 0; tb < nt; tb += 4) {
-            constexpr int NM = NMJ <= 16 ? NMJ : 1;
-            float sv[4][NM];
-            float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                if (tb + g < nt) {
-                    const float* xr = xf + (size_t)(t0 + tb + g) * H;
-                    const float* rr = rprev + (size_t)(t0 + tb + g) * H;
-#pragma unroll
-                    for (int m = 0; m < NM; ++m) {  // 2 MAXC * 256 >= H
-                        const int j = tid + 256 * m;
-                        const int jc = j < H ? j : H - 1;
-                        sv[g][m] = xr[jc] + rr[jc];
-                        if (j < H) acc[g] = __builtin_fmaf(sv[g][m], sv[g][m], acc[g]);
-                    }
-                }
-            }
-            wave_sum_xor_fast_n<4>(acc);
-            if ((tid & 63) == 0) {
-#pragma unroll
-                for (int g = 0; g < 4; ++g) wsum_s[g][tid >> 6] = acc[g];
-            }
-            __syncthreads();
-            if (tid < 4 && tb + tid < nt) {
-                const float ss = ((wsum_s[tid][0] + wsum_s[tid][1]) + wsum_s[tid][2]) + wsum_s[tid][3];
-                inv_s[tb + tid] = 1.0f / __builtin_sqrtf(ss / (float)H + eps);
-            }
-            __syncthreads();
-            if (!img_block) {
-#pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    if (tb + g < nt) {
-                        const float sc = inv_s[tb + g];
-                        float* xo = xout + (size_t)(t0 + tb + g) * H;
-#pragma unroll
-                        for (int m = 0; m < NM; ++m) {
-                            const int j = tid + 256 * m;
-                            if (j < H) {
-                                const float v = sv[g][m] * sc;
-                                if constexpr (F32) xs32[(size_t)(tb + g) * H + j] = v;
-                                else xs16[(size_t)(tb + g) * H + j] = (uint16_t)f32_to_bf16(v);
-                                if (blockIdx.x == 0) xo[j] = v;
-                            }
-                        }
-                    }
-                }
-            }
-        }
-    }
+    if (NMJ <= 16 && rprev)  // the fused junction; a row block stages s * scale from registers
+        router_junction<NMJ, F32>(xf, rprev, t0, nt, H, eps, !img_block, blockIdx.x == 0 ? xout : nullptr, smem, inv_s,
+                                  wsum_s);
     if (img_block) {
         float v = iv;
         if (rprev && live) v = (iv + ir) * inv_s[bb / (H >> 5)];
         q8_image_store(v, live, qsc[hw], ximg + blk * kImgDw, img_natural != 0);
         return;
     }
-    // stage the tile, 8 vector loads in flight per thread
-    if constexpr (F32) {  // f32 as it is (xf is given)
-        const int n4 = nt * H / 4;
-        for (int base = 0; !rprev && base < n4; base += 256 * 8) {
-            float4 f[8];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const int g = min(base + u * 256 + (int)threadIdx.x, n4 - 1);
-                f[u] = reinterpret_cast<const float4*>(xf + (size_t)t0 * H)[g];
-            }
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const int g = base + u * 256 + threadIdx.x;
-                if (g < n4) reinterpret_cast<float4*>(smem)[g] = f[u];
-            }
-        }
-    }
-    const int n8 = nt * H / 8;  // groups of 8 values = one uint4 of bf16
-    for (int base = 0; !F32 && !rprev && base < n8; base += 256 * 4) {
-        uint4 v[4];
-        if (xf) {
-            float4 f[8];
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {  // clamped, so that every load issues back to back
-                const int g = min(base + u * 256 + (int)threadIdx.x, n8 - 1);
-                const float4* src = reinterpret_cast<const float4*>(xf + (size_t)t0 * H) + 2 * (size_t)g;
-                f[2 * u] = src[0];
-                f[2 * u + 1] = src[1];
-            }
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const float4 a = f[2 * u], b = f[2 * u + 1];
-                v[u] = make_uint4(f32_to_bf16(a.x) | (f32_to_bf16(a.y) << 16), f32_to_bf16(a.z) | (f32_to_bf16(a.w) << 16),
-                                  f32_to_bf16(b.x) | (f32_to_bf16(b.y) << 16), f32_to_bf16(b.z) | (f32_to_bf16(b.w) << 16));
-            }
-        } else {
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int g = base + u * 256 + threadIdx.x;
-                if (g < n8) v[u] = reinterpret_cast<const uint4*>(xb + (size_t)t0 * H)[g];
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int g = base + u * 256 + threadIdx.x;
-            if (g < n8) reinterpret_cast<uint4*>(smem)[g] = v[u];
-        }
-    }
+    if (!rprev) router_stage<F32>(xf, xb, t0, nt, H, smem);  // (F32: xf is given)
     __syncthreads();
-    const uint16_t* xs = reinterpret_cast<const uint16_t*>(smem);
-    if (row >= rows_total) return;
-    for (int t = 0; t < nt; t += 4) {  // four tokens at a time: four independent accumulation chains
-        const int ng = min(4, nt - t);
-        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        if constexpr (F32) {
-            if (frow) {
-#pragma unroll
-                for (int j = 0; j < MAXC; ++j) {
-                    const int c = lane + 64 * j;
-                    if (c < wchunks) {
-                        const float w4[4] = {u2f(wv[j].x), u2f(wv[j].y), u2f(wv[j].z), u2f(wv[j].w)};
-#pragma unroll
-                        for (int g = 0; g < 4; ++g) {
-                            if (g < ng) {
-                                const float4 xv = *reinterpret_cast<const float4*>(xs32 + (size_t)(t + g) * H + 4 * c);
-                                acc[g] = __builtin_fmaf(xv.x, w4[0], acc[g]);
-                                acc[g] = __builtin_fmaf(xv.y, w4[1], acc[g]);
-                                acc[g] = __builtin_fmaf(xv.z, w4[2], acc[g]);
-                                acc[g] = __builtin_fmaf(xv.w, w4[3], acc[g]);
-                            }
-                        }
-                    }
-                }
-            } else {  // the shared gate row: bf16(x) * bf16 w_inp, exact products in the bf16 kernel's order
-#pragma unroll
-                for (int j = 0; j < MAXC; ++j) {
-                    const int c = lane + 64 * j;
-                    if (c < chunks) {
-                        const uint32_t wq[4] = {wv[j].x, wv[j].y, wv[j].z, wv[j].w};
-#pragma unroll
-                        for (int g = 0; g < 4; ++g) {
-                            if (g < ng) {
-                                const float* xr = xs32 + (size_t)(t + g) * H + 8 * c;
-                                const float4 a = reinterpret_cast<const float4*>(xr)[0];
-                                const float4 b = reinterpret_cast<const float4*>(xr)[1];
-                                const float xv8[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-                                for (int q = 0; q < 4; ++q) {
-                                    const float x0 = u2f(f32_to_bf16(xv8[2 * q]) << 16);
-                                    const float x1 = u2f(f32_to_bf16(xv8[2 * q + 1]) << 16);
-                                    acc[g] = __builtin_fmaf(x0, u2f(wq[q] << 16), acc[g]);
-                                    acc[g] = __builtin_fmaf(x1, u2f(wq[q] & 0xFFFF0000u), acc[g]);
-                                }
-                            }
-                        }
-                    }
-                }
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < MAXC && !F32; ++j) {
-            const int c = lane + 64 * j;
-            if (c < chunks) {
-                const uint32_t wq[4] = {wv[j].x, wv[j].y, wv[j].z, wv[j].w};
-#pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    if (g < ng) {
-                        const uint4 xv = *reinterpret_cast<const uint4*>(xs + (size_t)(t + g) * H + 8 * c);
-                        const uint32_t xq[4] = {xv.x, xv.y, xv.z, xv.w};
-#pragma unroll
-                        for (int q = 0; q < 4; ++q) {
-                            acc[g] = __builtin_fmaf(u2f(xq[q] << 16), u2f(wq[q] << 16), acc[g]);
-                            acc[g] = __builtin_fmaf(u2f(xq[q] & 0xFFFF0000u), u2f(wq[q] & 0xFFFF0000u), acc[g]);
-                        }
-                    }
-                }
-            }
-        }
-        wave_sum_xor_fast_n<4>(acc);
-        if (lane == 0) {
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                if (g < ng) {
-                    if (row < E) logits[(size_t)(t0 + t + g) * ld_logits + row] = bias ? acc[g] + bv : acc[g];
-                    else sg[t0 + t + g] = acc[g];
-                }
-            }
-        }
-    }
+    router_row_dots<MAXC, F32>(R, smem, H, E, rows_total, nt, bias != nullptr, [&](int row, int t, float v) {
+        if (row < E) logits[(size_t)(t0 + t) * ld_logits + row] = v;
+        else sg[t0 + t] = v;
+    });
 }
 
 
@@ -1557,35 +1605,17 @@ struct GuRouteLds {
 // One work-group of k_q2_gu_route / k_q2_moe_small: work item y (shared first, then the touched experts in
 // ascending order; y = max_items is the writer), rows block hb of h.  Returns whether it computed a unit (false:
 // no expert for this item, or rows past the expert's width); with `xchg` the h images go to the exchange words.
-template <int NIT, int MAXUPL>
-__device__ __forceinline__ bool gu_route_wg(
-    int y, int hb, uint32_t* smem, const uint8_t* __restrict__ gate_exps, const uint8_t* __restrict__ up_exps,
-    const uint8_t* __restrict__ gate_sh, const uint8_t* __restrict__ up_sh, const uint32_t* __restrict__ ximg,
-    const float* __restrict__ logits, int T, int E, int k, int H, int F, int Fs, int has_shared,
-    int32_t* __restrict__ ids, float* __restrict__ wts, int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
-    int32_t* __restrict__ perm, int32_t* __restrict__ slot, int32_t* __restrict__ elist, int32_t* __restrict__ n_list,
-    int4* __restrict__ items, int max_items, uint32_t* __restrict__ himg, int h_blocks, uint64_t* __restrict__ xchg) {
-    typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
+// The routing and the work item of a gate/up work-group of the small-batch launches (item y: the shared expert
+// first, then the touched experts in ascending order, with their pairs in ascending pair order -- the item
+// dispatch_block writes there), from the logits `lg` ([T][E], global memory or LDS; wave t routes token t).
+// `commit` runs after the routing and before the barrier that publishes it (the caller's staging of the x images).
+// Returns whether the work-group has an expert (uniform; false after the barrier when its item has none).
+template <class Commit>
+__device__ __forceinline__ bool gu_route_item(int y, GuRouteLds& L, const float* lg, int T, int E, int k,
+                                              int has_shared, Item& item, Commit commit) {
     const int n_sh = has_shared ? 1 : 0;
     const int tid = threadIdx.x, wave = tid >> 6;
-    if (y == max_items) {
-        if (hb == 0)
-            small_route_dispatch(logits, T, E, k, true, ids, wts, counts, offsets, perm, slot, elist, n_list, items,
-                                 max_items, has_shared, 1 << 30, kShCols, *reinterpret_cast<SmallDispatchLds*>(smem));
-        return false;
-    }
     const bool shared_wg = y < n_sh;
-    if (hb * 32 >= (shared_wg ? Fs : F)) return false;
-    const int qb = H >> 5;
-    const int pieces = T * qb * (kImgDw / 4);  // at most 4 * 128 * 3
-    const int npre = (pieces + 255) >> 8;      // uniform
-    // unconditional loads (clamped index; a branch around a load makes the compiler wait for it), so that the
-    // logits loads below go out behind them without waiting
-    u32x4 pre[6];
-#pragma unroll
-    for (int j = 0; j < 6; ++j)
-        pre[j] = reinterpret_cast<const u32x4*>(ximg)[min(min(j, npre - 1) * 256 + tid, pieces - 1)];
-    GuRouteLds& L = *reinterpret_cast<GuRouteLds*>(smem + kGuCols * qb * kImgLdsDw + 4);
     const int P = T * k;
     // one token: wave 0 routes it and takes the item from the candidates (the y-th selected id in ascending order,
     // its one pair at dispatch position y); L.item[7] = 1 when the fast selection declined (then the ids are in
@@ -1593,8 +1623,8 @@ __device__ __forceinline__ bool gu_route_wg(
     const bool one = !shared_wg && T == 1 && k <= 64;
     if (one && wave == 0) {
         __shared__ uint2 s_cand1[64];
-        const FastRoute R = E <= 512 ? route_fast_t<8, false>(logits, E, k, s_cand1)
-                                     : route_fast_t<16, false>(logits, E, k, s_cand1);
+        const FastRoute R = E <= 512 ? route_fast_t<8, false>(lg, E, k, s_cand1)
+                                     : route_fast_t<16, false>(lg, E, k, s_cand1);
         const int lane = tid & 63;
         if (R.ok) {
             const bool sel = R.crank < k;
@@ -1609,18 +1639,15 @@ __device__ __forceinline__ bool gu_route_wg(
                 L.item[7] = 0;
             }
         } else {
-            if (E <= 512) route_token_t<8, false>(logits, E, k, nullptr, nullptr, L.ids);
-            else route_token_t<16, false>(logits, E, k, nullptr, nullptr, L.ids);
+            if (E <= 512) route_token_t<8, false>(lg, E, k, nullptr, nullptr, L.ids);
+            else route_token_t<16, false>(lg, E, k, nullptr, nullptr, L.ids);
             if (lane == 0) L.item[7] = 1;
         }
     } else if (!shared_wg && !one && wave < T) {
-        route_token_ids(logits + (size_t)wave * E, E, k, L.ids + wave * k);
+        route_token_ids(lg + (size_t)wave * E, E, k, L.ids + wave * k);
     }
-#pragma unroll
-    for (int j = 0; j < 6; ++j)
-        if (j * 256 + tid < pieces) reinterpret_cast<u32x4*>(smem)[lds_piece(j * 256 + tid)] = pre[j];
+    commit();
     __syncthreads();
-    Item item;
     if (one && L.item[7] == 0) {
         if (L.item[0] < 0) return false;  // uniform: no expert for this item
         item.shared = false;
@@ -1712,7 +1739,46 @@ __device__ __forceinline__ bool gu_route_wg(
         for (int c = 0; c < 4; ++c) item.tk[c] = L.item[3 + c];
         item.tok0 = item.tk[0];
     }
-    q2_gu_item<NIT, MAXUPL, true>(item, hb, smem, gate_exps, up_exps, gate_sh, up_sh, ximg, perm, k, H, F, himg,
+    return true;
+}
+
+template <int NIT, int MAXUPL>
+__device__ __forceinline__ bool gu_route_wg(
+    int y, int hb, uint32_t* smem, const uint8_t* __restrict__ gate_exps, const uint8_t* __restrict__ up_exps,
+    const uint8_t* __restrict__ gate_sh, const uint8_t* __restrict__ up_sh, const uint32_t* __restrict__ ximg,
+    const float* __restrict__ logits, int T, int E, int k, int H, int F, int Fs, int has_shared,
+    int32_t* __restrict__ ids, float* __restrict__ wts, int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
+    int32_t* __restrict__ perm, int32_t* __restrict__ slot, int32_t* __restrict__ elist, int32_t* __restrict__ n_list,
+    int4* __restrict__ items, int max_items, uint32_t* __restrict__ himg, int h_blocks, uint64_t* __restrict__ xchg) {
+    typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
+    const int n_sh = has_shared ? 1 : 0;
+    const int tid = threadIdx.x;
+    if (y == max_items) {
+        if (hb == 0)
+            small_route_dispatch(logits, T, E, k, true, ids, wts, counts, offsets, perm, slot, elist, n_list, items,
+                                 max_items, has_shared, 1 << 30, kShCols, *reinterpret_cast<SmallDispatchLds*>(smem));
+        return false;
+    }
+    const bool shared_wg = y < n_sh;
+    if (hb * 32 >= (shared_wg ? Fs : F)) return false;
+    const int qb = H >> 5;
+    const int pieces = T * qb * (kImgDw / 4);  // at most 4 * 128 * 3
+    const int npre = (pieces + 255) >> 8;      // uniform
+    // unconditional loads (clamped index; a branch around a load makes the compiler wait for it), so that the
+    // logits loads of the routing go out behind them without waiting
+    u32x4 pre[6];
+#pragma unroll
+    for (int j = 0; j < 6; ++j)
+        pre[j] = reinterpret_cast<const u32x4*>(ximg)[min(min(j, npre - 1) * 256 + tid, pieces - 1)];
+    GuRouteLds& L = *reinterpret_cast<GuRouteLds*>(smem + kGuCols * qb * kImgLdsDw + 4);
+    Item item;
+    const bool has = gu_route_item(y, L, logits, T, E, k, has_shared, item, [&] {
+#pragma unroll
+        for (int j = 0; j < 6; ++j)
+            if (j * 256 + tid < pieces) reinterpret_cast<u32x4*>(smem)[lds_piece(j * 256 + tid)] = pre[j];
+    });
+    if (!has) return false;
+    q2_gu_item<NIT, MAXUPL, true>(item, hb, smem, gate_exps, up_exps, gate_sh, up_sh, ximg, nullptr, k, H, F, himg,
                                   h_blocks, xchg);
     return true;
 }
@@ -1999,58 +2065,52 @@ __global__ __launch_bounds__(256) void k_q2_down_combine(
 // images pass through the workspace: every image dword in a tagged 64-bit word (q8_image_store with xchg), each
 // checked by itself, so no fence is needed; the router kernel of the same call cleared the words.  The down
 // work-groups come last in the grid: on every XCD all gate/up work-groups are dispatched before any down
-// work-group that waits for them, and a down work-group gives up after a bounded wait (its rows are then NaN).
-constexpr int kSpinLimit = 100000;
+// work-group that waits for them, and a down work-group gives up after a bounded wait (its rows are then NaN and
+// its status word is 1; every down work-group writes its status word, 0 when it did not give up).
+constexpr int kSpinLimit = 100000;  // polls of a bounded wait (each a round trip of ~1 us): ~0.1 s
 
-template <int NIT, int MAXUPL, int DMAXUPL, int DNT>
-__global__ __launch_bounds__(256) void k_q2_moe_small(
-    const uint8_t* __restrict__ gate_exps, const uint8_t* __restrict__ up_exps, const uint8_t* __restrict__ gate_sh,
-    const uint8_t* __restrict__ up_sh, const uint8_t* __restrict__ down_exps, const uint8_t* __restrict__ down_sh,
-    const uint32_t* __restrict__ ximg, const float* __restrict__ logits, const float* __restrict__ sg, int T, int E,
-    int k, int H, int F, int Fs, int has_shared, int32_t* __restrict__ ids, float* __restrict__ wts,
-    int32_t* __restrict__ counts, int32_t* __restrict__ offsets, int32_t* __restrict__ perm,
-    int32_t* __restrict__ slot, int32_t* __restrict__ elist, int32_t* __restrict__ n_list, int4* __restrict__ items,
-    int max_items, int h_blocks, uint64_t* __restrict__ xchg, int npass, int add_shared, float* __restrict__ y) {
-    extern __shared__ __align__(16) uint32_t smem[];
+// A bounded wait's end: `spin` polls done, all there or not.  A limit below zero gives up at once, without
+// looking (the host's give-up switch, smoe_set_wait_limit, for tests of the give-up path).
+__device__ __forceinline__ bool wait_gives_up(int spin, int limit) { return limit < 0 || spin >= limit; }
+
+// The down work-group of the small-batch launches: rows r0 .. r0 + kDcRows - 1 of every item, then the combine.
+// It routes the batch itself from the logits `lg` ([T][E]) and takes the shared gate dots from `sgv` (at least T),
+// then issues its first batch of weight loads, waits for the h words (tag 1; a bounded wait), and forms its rows and
+// y.  `gave` (uniform): an earlier wait of the caller's gave up -- the work-group then writes NaN
+// rows without waiting.  status[r0 / kDcRows] = 1 when the rows are NaN, else 0.
+template <int DMAXUPL, int DNT>
+__device__ __forceinline__ void down_wg(int r0, uint32_t* smem, const float* lg, const float* sgv, bool gave,
+                                        const uint8_t* __restrict__ down_exps, const uint8_t* __restrict__ down_sh,
+                                        int T, int E, int k, int H, int F, int Fs, int has_shared, int h_blocks,
+                                        const uint64_t* __restrict__ xchg, int spin_limit, int npass, int add_shared,
+                                        float* __restrict__ y, int32_t* __restrict__ status) {
     __shared__ int s_slot[kSmallPairs];
     __shared__ float s_wts[kSmallPairs];
     __shared__ int4 s_items[2 * kDcItems];
     __shared__ int s_ids[64];
     __shared__ float s_sg[kShCols];
-    __shared__ int s_bad, s_nt;
-    const int hbn = h_blocks;  // rows blocks of the widest expert
-    const int n_gu = max_items * hbn + 1;
-    const int id = blockIdx.x, tid = threadIdx.x;
-    if (id < n_gu) {  // gate/up (or the writer)
-        const int yi = id / hbn, hb = id - yi * hbn;
-        gu_route_wg<NIT, MAXUPL>(yi, hb, smem, gate_exps, up_exps, gate_sh, up_sh, ximg, logits, T, E, k, H, F, Fs,
-                                 has_shared, ids, wts, counts, offsets, perm, slot, elist, n_list, items, max_items,
-                                 nullptr, h_blocks, xchg);
-        return;
-    }
-    // down rows r0 .. r0 + kDcRows - 1 of every item, then the combine
-    const int r0 = (id - n_gu) * kDcRows;
+    __shared__ int s_bad, s_nt, s_fast;
+    const int tid = threadIdx.x;
     const int P = T * k, n_sh = has_shared ? 1 : 0;
     const int rows = P + n_sh * T;
     const int lane = tid & 63, wave = tid >> 6;
     float* Ys = reinterpret_cast<float*>(smem + (size_t)(P + T) * h_blocks * kImgLdsDw);
     if (tid == 0) {
-        s_bad = 0;
+        s_bad = gave ? 1 : 0;
         if (has_shared) {
             s_items[0] = make_int4(kItemShared, P, T, 0);
             s_items[1] = make_int4(1, 2, 3, 0);
         }
     }
-    if (tid < T) s_sg[tid] = sg[tid];
+    if (tid < T) s_sg[tid] = sgv[tid];
     // one token: wave 0 routes it with weights; candidate c (ascending id), selected at rank r, is the token's pair r
     // and the y-th touched expert (y = selected candidates below c), so its dispatch position is y
-    __shared__ int s_fast;
     const bool one = T == 1 && k <= 64;
     if (one) {
         if (wave == 0) {
             __shared__ uint2 s_cand1[64];
-            const FastRoute R = E <= 512 ? route_fast_t<8, true>(logits, E, k, s_cand1)
-                                         : route_fast_t<16, true>(logits, E, k, s_cand1);
+            const FastRoute R = E <= 512 ? route_fast_t<8, true>(lg, E, k, s_cand1)
+                                         : route_fast_t<16, true>(lg, E, k, s_cand1);
             if (R.ok) {
                 const bool sel = R.crank < k;
                 const unsigned long long sm = __ballot(sel);
@@ -2076,7 +2136,7 @@ __global__ __launch_bounds__(256) void k_q2_moe_small(
         // dispatch and the item table by cross-lane counts, lane p holding pair p: its slot is the pairs with a
         // smaller expert id plus the earlier pairs with its own; an expert's item sits at its rank among the
         // touched experts
-        if (wave < T) route_token(logits + (size_t)wave * E, E, k, nullptr, nullptr, s_ids + wave * k, s_wts + wave * k);
+        if (wave < T) route_token(lg + (size_t)wave * E, E, k, nullptr, nullptr, s_ids + wave * k, s_wts + wave * k);
         __syncthreads();
         if (wave == 0) {
             const int me = lane < P ? s_ids[lane] : 0x7FFFFFFF;
@@ -2107,7 +2167,7 @@ __global__ __launch_bounds__(256) void k_q2_moe_small(
         }
     } else {
         SmallDispatchLds& R = *reinterpret_cast<SmallDispatchLds*>(Ys + (size_t)(P + T) * kDcRows);
-        small_route_dispatch(logits, T, E, k, false, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
+        small_route_dispatch(lg, T, E, k, false, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
                              nullptr, nullptr, 0, has_shared, 1 << 30, kShCols, R);
         for (int j = tid; j < R.n_touched; j += 256) {
             const int e = R.el[j], first = R.off[e], n = R.cnt[e];
@@ -2129,8 +2189,8 @@ __global__ __launch_bounds__(256) void k_q2_moe_small(
         // go out behind this work-group's weight loads, so they return once those have), then the words whose tag
         // is not set yet are read again until it is (a bounded wait)
         const int words = rows * h_blocks * kXchgSlots;
-        bool ok = true;
-        for (int base = 0; base < words; base += 8 * 256) {
+        bool ok = !gave && spin_limit >= 0;
+        for (int base = 0; ok && base < words; base += 8 * 256) {
             uint64_t v[8];
             int at[8];
             bool need[8];
@@ -2149,7 +2209,7 @@ __global__ __launch_bounds__(256) void k_q2_moe_small(
 #pragma unroll
                 for (int j = 0; j < 8; ++j) all = all && (!need[j] || (v[j] >> 32) == 1u);
                 if (all) break;
-                if (spin == kSpinLimit) {
+                if (wait_gives_up(spin, spin_limit)) {
                     ok = false;
                     break;
                 }
@@ -2175,6 +2235,32 @@ __global__ __launch_bounds__(256) void k_q2_moe_small(
         const int t = tid / kDcRows, rl = tid - t * kDcRows;
         if (r0 + rl < H) y[(size_t)t * H + r0 + rl] = __builtin_nanf("");
     }
+    if (status && tid == 0) status[r0 / kDcRows] = s_bad;
+}
+
+template <int NIT, int MAXUPL, int DMAXUPL, int DNT>
+__global__ __launch_bounds__(256) void k_q2_moe_small(
+    const uint8_t* __restrict__ gate_exps, const uint8_t* __restrict__ up_exps, const uint8_t* __restrict__ gate_sh,
+    const uint8_t* __restrict__ up_sh, const uint8_t* __restrict__ down_exps, const uint8_t* __restrict__ down_sh,
+    const uint32_t* __restrict__ ximg, const float* __restrict__ logits, const float* __restrict__ sg, int T, int E,
+    int k, int H, int F, int Fs, int has_shared, int32_t* __restrict__ ids, float* __restrict__ wts,
+    int32_t* __restrict__ counts, int32_t* __restrict__ offsets, int32_t* __restrict__ perm,
+    int32_t* __restrict__ slot, int32_t* __restrict__ elist, int32_t* __restrict__ n_list, int4* __restrict__ items,
+    int max_items, int h_blocks, uint64_t* __restrict__ xchg, int npass, int add_shared, float* __restrict__ y,
+    int spin_limit, int32_t* __restrict__ status) {
+    extern __shared__ __align__(16) uint32_t smem[];
+    const int hbn = h_blocks;  // rows blocks of the widest expert
+    const int n_gu = max_items * hbn + 1;
+    const int id = blockIdx.x;
+    if (id < n_gu) {  // gate/up (or the writer)
+        const int yi = id / hbn, hb = id - yi * hbn;
+        gu_route_wg<NIT, MAXUPL>(yi, hb, smem, gate_exps, up_exps, gate_sh, up_sh, ximg, logits, T, E, k, H, F, Fs,
+                                 has_shared, ids, wts, counts, offsets, perm, slot, elist, n_list, items, max_items,
+                                 nullptr, h_blocks, xchg);
+        return;
+    }
+    down_wg<DMAXUPL, DNT>((id - n_gu) * kDcRows, smem, logits, sg, false, down_exps, down_sh, T, E, k, H, F, Fs,
+                          has_shared, h_blocks, xchg, spin_limit, npass, add_shared, y, status);
 }
 
 // Generic Q2_0 GEMV over n_col columns of standard q8_1 activations (iq_mmvq's contract, metal/src/iq.mm:148-169).
@@ -2693,17 +2779,17 @@ bool moe_small_ok(int T, int k, int H, int F, int Fs, int has_shared, int h_bloc
     return true;
 }
 
-hipError_t launch_q2_moe_small(const uint8_t* gate_exps, const uint8_t* up_exps, const uint8_t* gate_sh,
-                               const uint8_t* up_sh, const uint8_t* down_exps, const uint8_t* down_sh,
-                               const uint32_t* ximg, const float* logits, const float* sg, int T, int E, int k, int H,
-                               int F, int Fs, int has_shared, int32_t* ids, float* wts, int32_t* counts,
-                               int32_t* offsets, int32_t* perm, int32_t* slot, int32_t* elist, int32_t* n_list,
-                               int4* items, int max_items, int h_blocks, uint8_t* xchg, int add_shared, float* y,
-                               hipStream_t s) {
-    if (T < 1 || T > kShCols || T * k > kSmallPairs || E > 1024 || max_items + 1 > kDcItems ||
-        !moe_small_ok(T, k, H, F, Fs, has_shared, h_blocks))
-        return hipErrorInvalidValue;
-    int npass = 1, dmaxupl = 1;
+namespace {
+std::atomic<int> g_wait_limit{kSpinLimit};
+}
+int wait_limit() { return g_wait_limit.load(std::memory_order_relaxed); }
+int default_wait_limit() { return kSpinLimit; }
+void set_wait_limit(int limit) { g_wait_limit.store(limit, std::memory_order_relaxed); }
+
+// down rows: passes per wave and units per lane of the widest of the routed and shared down rows
+static void small_down_shape(int F, int Fs, int has_shared, int& npass, int& dmaxupl) {
+    npass = 1;
+    dmaxupl = 1;
     for (const int Fe : {F, has_shared ? Fs : 0}) {
         if (Fe <= 0) continue;
         const int dpr = Fe >> 7, lpr = lanes_per_row_host(dpr), rpi = 64 / lpr;
@@ -2711,29 +2797,46 @@ hipError_t launch_q2_moe_small(const uint8_t* gate_exps, const uint8_t* up_exps,
         npass = np > npass ? np : npass;
         dmaxupl = u > dmaxupl ? u : dmaxupl;
     }
+}
+
+hipError_t launch_q2_moe_small(const uint8_t* gate_exps, const uint8_t* up_exps, const uint8_t* gate_sh,
+                               const uint8_t* up_sh, const uint8_t* down_exps, const uint8_t* down_sh,
+                               const uint32_t* ximg, const float* logits, const float* sg, int T, int E, int k, int H,
+                               int F, int Fs, int has_shared, int32_t* ids, float* wts, int32_t* counts,
+                               int32_t* offsets, int32_t* perm, int32_t* slot, int32_t* elist, int32_t* n_list,
+                               int4* items, int max_items, int h_blocks, uint8_t* xchg, int add_shared, float* y,
+                               int32_t* status, hipStream_t s) {
+    if (T < 1 || T > kShCols || T * k > kSmallPairs || E > 1024 || max_items + 1 > kDcItems ||
+        !moe_small_ok(T, k, H, F, Fs, has_shared, h_blocks))
+        return hipErrorInvalidValue;
+    int npass, dmaxupl;
+    small_down_shape(F, Fs, has_shared, npass, dmaxupl);
     uint64_t* xw = reinterpret_cast<uint64_t*>(xchg);
     const int n_gu = max_items * h_blocks + 1;
     dim3 grid((unsigned)(n_gu + (H + kDcRows - 1) / kDcRows));
     int nit, upl;
     gu_shape(H, nit, upl);
     const size_t lds = moe_small_lds(T, k, H, h_blocks);
+    const int spin = wait_limit();
 #define SMOE_MS(N, U)                                                                                                \
     do {                                                                                                             \
         if (dmaxupl == 1)                                                                                            \
             hipLaunchKernelGGL((k_q2_moe_small<N, U, 1, 4>), grid, dim3(256), lds, s, gate_exps, up_exps, gate_sh,    \
                                up_sh, down_exps, down_sh, ximg, logits, sg, T, E, k, H, F, Fs, has_shared, ids, wts,  \
                                counts, offsets, perm, slot, elist, n_list, items, max_items, h_blocks, xw, npass,      \
-                               add_shared, y);                                                                \
+                               add_shared, y, spin, status);                                                          \
         else                                                                                                         \
             hipLaunchKernelGGL((k_q2_moe_small<N, U, 2, 4>), grid, dim3(256), lds, s, gate_exps, up_exps, gate_sh,    \
                                up_sh, down_exps, down_sh, ximg, logits, sg, T, E, k, H, F, Fs, has_shared, ids, wts,  \
                                counts, offsets, perm, slot, elist, n_list, items, max_items, h_blocks, xw, npass,      \
-                               add_shared, y);                                                                \
+                               add_shared, y, spin, status);                                                          \
     } while (0)
     SMOE_SHAPE_DISPATCH(SMOE_MS)
 #undef SMOE_MS
     return hipGetLastError();
 }
+
+int fused_status_words(int H) { return (H + kDcRows - 1) / kDcRows; }
 
 hipError_t launch_combine(const float* Y, const int32_t* slot, const float* wts, int k, int H, int P, int T,
                           int add_shared, float* y, hipStream_t s) {

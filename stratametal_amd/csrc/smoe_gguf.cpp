@@ -193,7 +193,8 @@ struct Shard {
         for (uint64_t i = 0; i < n_kv; ++i) {
             std::string k = c.str();
             const uint32_t t = c.get<uint32_t>();
-            meta[k] = read_value(c, t, 0);
+            MetaValue v = read_value(c, t, 0);
+            meta.emplace(std::move(k), std::move(v));  // a repeated key keeps its first value, as the reference's map does
         }
         std::map<std::string, int> seen;
         tensors.resize((size_t)n_tensors);
@@ -335,6 +336,17 @@ std::string layer_name(int layer, const char* suffix) { return "blk." + std::to_
 
 constexpr int kGgufF32 = 0, kGgufF16 = 1, kGgufBf16 = 30;
 
+// A type the block's q8_1 GEMV contract runs for a shared projection: Q2_0, IQ2_S and the native types of smoe.h.
+bool gemv_type(uint32_t t) {
+    switch (t) {
+        case SMOE_Q2_0: case SMOE_IQ2_S: case SMOE_Q8_0: case SMOE_Q4_0: case SMOE_Q5_0: case SMOE_IQ4_NL:
+        case SMOE_IQ4_XS: case SMOE_Q3_K: case SMOE_Q4_K: case SMOE_Q5_K: case SMOE_Q6_K:
+            return true;
+        default:
+            return false;
+    }
+}
+
 // One tensor of the layer, resolved and checked (type, shape), or a refusal.
 struct Part {
     const TensorDesc* t = nullptr;
@@ -362,6 +374,10 @@ smoe_status plan_layer(const smoe_model* m, int layer, int top_k, int with_share
     if ((s = find_part(m, layer, "ffn_down_exps.weight", true, P.down)) != SMOE_OK) return s;
     if ((s = find_part(m, layer, "ffn_gate_inp.weight", true, P.router)) != SMOE_OK) return s;
     const uint64_t H = P.gate.t->ne[0], F = P.gate.t->ne[1], E = P.gate.t->ne[2];
+    // every dimension is narrowed to int32 below: refuse what would not survive it
+    constexpr uint64_t kDimMax = 0x7FFFFFFFu;
+    if (H > kDimMax || F > kDimMax || E > kDimMax)
+        return report(SMOE_EINVAL, "layer " + std::to_string(layer) + ": ffn_gate_exps has a dimension beyond int32");
     auto shape = [&](const Part& p, uint64_t a, uint64_t b, uint64_t c, const char* what) -> smoe_status {
         if (p.t->ne[0] != a || p.t->ne[1] != b || p.t->ne[2] != c || p.t->ne[3] != 1)
             return report(SMOE_EINVAL, "layer " + std::to_string(layer) + ": " + p.t->name + " has not the shape of " +
@@ -388,6 +404,7 @@ smoe_status plan_layer(const smoe_model* m, int layer, int top_k, int with_share
         const MetaValue* arch = m->shards[0]->get("general.architecture");
         const MetaValue* ku = arch ? m->shards[0]->get(arch->s + ".expert_used_count") : nullptr;
         if (!ku) return report(SMOE_EINVAL, "no top_k given and the model declares no <architecture>.expert_used_count");
+        if (ku->u > 64) return report(SMOE_EINVAL, "<architecture>.expert_used_count is beyond 64");
         top_k = (int)ku->u;
     }
     g.top_k = top_k;
@@ -397,6 +414,14 @@ smoe_status plan_layer(const smoe_model* m, int layer, int top_k, int with_share
         if ((s = find_part(m, layer, "ffn_down_shexp.weight", true, P.dsh)) != SMOE_OK) return s;
         if ((s = find_part(m, layer, "ffn_gate_inp_shexp.weight", true, P.ginp)) != SMOE_OK) return s;
         const uint64_t Fs = P.gsh.t->ne[1];
+        if (Fs > kDimMax)
+            return report(SMOE_EINVAL, "layer " + std::to_string(layer) + ": ffn_gate_shexp has a dimension beyond int32");
+        // each shared projection must be a type the block's GEMV contract implements: smoe_geom reads a zero
+        // projection type as "the shared expert's type", so GGML type 0 (F32) must not reach it
+        for (const Part* q : {&P.gsh, &P.ush, &P.dsh})
+            if (!gemv_type(q->t->type))
+                return report(SMOE_ETYPE, "layer " + std::to_string(layer) + ": " + q->t->name + " is of GGML type " +
+                                              std::to_string(q->t->type) + ", which the shared expert does not run");
         if ((s = shape(P.gsh, H, Fs, 1, "[n_embd][n_ff_shared]")) != SMOE_OK) return s;
         if ((s = shape(P.ush, H, Fs, 1, "[n_embd][n_ff_shared]")) != SMOE_OK) return s;
         if ((s = shape(P.dsh, Fs, H, 1, "[n_ff_shared][n_embd]")) != SMOE_OK) return s;

@@ -81,7 +81,11 @@ hipError_t launch_q2_moe_small(const uint8_t* gate_exps, const uint8_t* up_exps,
                                int F, int Fs, int has_shared, int32_t* ids, float* wts, int32_t* counts,
                                int32_t* offsets, int32_t* perm, int32_t* slot, int32_t* elist, int32_t* n_list,
                                int4* items, int max_items, int h_blocks, uint8_t* xchg, int add_shared, float* y,
-                               hipStream_t s);
+                               int32_t* status, hipStream_t s);
+int fused_status_words(int H);  // wait flags of k_q2_moe_small, one per down work-group
+int wait_limit();                 // the bounded waits' poll limit (default_wait_limit(), or the host's switch)
+void set_wait_limit(int limit);   // (below zero: every wait gives up at once)
+int default_wait_limit();
 hipError_t launch_residual_rmsnorm(const float* x, const float* r, int n_rows, int n, float eps, float* out,
                                    hipStream_t s);
 hipError_t launch_combine(const float* Y, const int32_t* slot, const float* wts, int k, int H, int P, int T,
@@ -128,7 +132,8 @@ hipError_t launch_mm_gu(const uint8_t* gate_exps, const uint8_t* up_exps, const 
                         int32_t* flags = nullptr);
 // dst[i] = src[i] for n floats (trace copies)
 hipError_t launch_copy_f32(const float* src, int64_t n, float* dst, hipStream_t s);
-hipError_t launch_flags_mask(const int32_t* fx, int64_t nx, const int32_t* fh, int64_t nh, int32_t* out, hipStream_t s);
+hipError_t launch_flags_mask(const int32_t* fx, int64_t nx, const int32_t* fh, int64_t nh, int32_t* out,
+                             hipStream_t s, const int32_t* fw = nullptr, int64_t nw = 0);
 hipError_t launch_mm_down(const uint8_t* down_exps, const uint8_t* down_sh, const uint32_t* hrec, int64_t n_hrec,
                           int h_rec, const float* sg, const int4* items, int H, int F, int Fs, int max_items, float* Y,
                           hipStream_t s);

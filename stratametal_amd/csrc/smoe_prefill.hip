@@ -668,19 +668,24 @@ hipError_t launch_copy_f32(const float* src, int64_t n, float* dst, hipStream_t 
 }
 
 // The overflow mask of smoe_trace: bit 0 when a flag of fx is set, bit 1 when one of fh is (one work-group).
+// The call's status mask from its flag words: bit 0 any x flag, bit 1 any h flag (the prefill path's fp16 operand
+// limits), bit 2 any wait flag (a fused decode launch's bounded wait gave up).
 __global__ __launch_bounds__(256) void k_flags_mask(const int32_t* __restrict__ fx, int64_t nx,
-                                                    const int32_t* __restrict__ fh, int64_t nh, int32_t* __restrict__ out) {
-    int ax = 0, ah = 0;
+                                                    const int32_t* __restrict__ fh, int64_t nh,
+                                                    const int32_t* __restrict__ fw, int64_t nw, int32_t* __restrict__ out) {
+    int ax = 0, ah = 0, aw = 0;
     for (int64_t i = threadIdx.x; i < nx; i += 256) ax |= fx[i];
     for (int64_t i = threadIdx.x; i < nh; i += 256) ah |= fh[i];
+    for (int64_t i = threadIdx.x; i < nw; i += 256) aw |= fw[i];
     ax = __syncthreads_or(ax);
     ah = __syncthreads_or(ah);
-    if (threadIdx.x == 0) *out = (ax ? 1 : 0) | (ah ? 2 : 0);
+    aw = __syncthreads_or(aw);
+    if (threadIdx.x == 0) *out = (ax ? 1 : 0) | (ah ? 2 : 0) | (aw ? 4 : 0);
 }
 
 hipError_t launch_flags_mask(const int32_t* fx, int64_t nx, const int32_t* fh, int64_t nh, int32_t* out,
-                             hipStream_t s) {
-    hipLaunchKernelGGL(k_flags_mask, dim3(1), dim3(256), 0, s, fx, nx, fh, nh, out);
+                             hipStream_t s, const int32_t* fw, int64_t nw) {
+    hipLaunchKernelGGL(k_flags_mask, dim3(1), dim3(256), 0, s, fx, nx, fh, nh, fw, nw, out);
     return hipGetLastError();
 }
 

@@ -72,6 +72,11 @@ def test_forward_refusals_before_launch():
     assert _forward(g, 1, weights=null_router) == -6
     misaligned = S._Weights(FAKE + 2, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, None)
     assert _forward(g, 1, weights=misaligned) == -5
+    # launch grids hold at most 65535 tokens or work items on their y dimension: refused before the first launch
+    small = S.Geom(n_embd=256, n_ff=128, n_ff_shared=128, n_expert=64, top_k=64)
+    assert _forward(small, 65536, path=2) == -1
+    assert "split the batch" in S.lib().smoe_last_error().decode()
+    assert _forward(small, 65536, path=1) == -1
 
 
 def test_forward_zero_tokens_returns_ok_without_launching():

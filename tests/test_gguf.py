@@ -414,3 +414,32 @@ def test_layer_plan_refusals(tmp_path):
     # a geometry the block does not run: the library's own reason
     with pytest.raises(RuntimeError, match="top_k"):
         model(full).plan(0, top_k=9)
+    # a shared projection of a type the block does not run: an F32 (GGML type 0) or F16 plane is refused, never read
+    # as the shared expert's own type (a zero type in smoe_geom means "as sh_type")
+    Fs = g.n_ff_shared
+    for name, ne in (("blk.0.ffn_down_shexp.weight", (Fs, H)), ("blk.0.ffn_up_shexp.weight", (H, Fs))):
+        for t in (W.T_F32, W.T_F16):
+            data = np.zeros(Fs * H, np.float32 if t == W.T_F32 else np.float16)
+            with pytest.raises(RuntimeError, match=f"GGML type {t}"):
+                model(swap(name, type_=t, data=data)).plan(0, top_k=2)
+    # a dimension beyond int32 (it would narrow to a geometry the block accepts) and a top_k beyond 64 are refused
+    # (the plane's 1.2 GB payload is a hole of a sparse file: nothing is written and nothing is read)
+    big = [W.Tensor(t.name, (2 ** 32 + H, 1, 1), t.type, b"", offset=0) if t.name == "blk.0.ffn_gate_exps.weight"
+           else t for t in full]
+    pbig = W.write(tmp_path / "big.gguf", arch, big)
+    os.truncate(pbig, os.path.getsize(pbig) + (2 ** 32 + H) // 64 * 18)
+    with pytest.raises(RuntimeError, match="beyond int32"):
+        S.Model(pbig).plan(0, top_k=2)
+    with pytest.raises(RuntimeError, match="beyond 64"):
+        model(full, arch + [("qwen4exp.expert_used_count", W.U64, 2 ** 32 + 2)]).plan(0)
+
+
+def test_repeated_metadata_key_keeps_the_first(tmp_path):
+    """A key listed twice keeps its first value, as the reference reader's map (emplace) does."""
+    smoe()
+    g = small_geom()
+    w = O.make_weights(g, 13)
+    meta = [("general.architecture", W.STRING, "qwen4exp"), ("qwen4exp.expert_used_count", W.U32, 2),
+            ("qwen4exp.expert_used_count", W.U32, 3)]
+    m = S.Model(W.write(tmp_path / "dup.gguf", meta, W.layer_tensors(g, w, 0)))
+    assert m.plan(0).geom.top_k == 2

@@ -279,6 +279,9 @@ CASES = [
     ("f32 router, 70 tokens in tiles of 16", dict(router_dtype=1, n_embd=256, n_ff=128, n_ff_shared=128, n_expert=16,
                                                   top_k=4), 70, 45, True),
     ("f32 router, no shared expert", dict(router_dtype=1, sh_type=-1, n_expert=64), 2, 46, True),
+    # the f32 router of 4096 values at a small batch (its widest tile in the fused launch's stage of the router)
+    ("f32 router, H=4096, T=2",
+     dict(router_dtype=1, n_embd=4096, n_ff=256, n_ff_shared=256, n_expert=16, top_k=4), 2, 47, True),
 ]
 
 
