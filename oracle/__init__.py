@@ -96,6 +96,7 @@ def _set_sigs(L):
         "or_moe_decode_dev": (i32, [vp, vp, vp, i32, vp, i32, vp, i32]),
         "or_moe_decode_ref": (i32, [vp, vp, vp, i32, vp, i32, i32]),
         "or_moe_prefill": (i32, [vp, vp, vp, i32, vp, i32, vp, i32]),
+        "or_moe_prefill_logits": (i32, [vp, vp, vp, i32, vp, vp, vp, i32, vp, i32]),
         "or_moe_decode_pool": (i32, [vp, vp, vp, i32, vp, i32, i32]),
         "or_hc_read_dev": (i32, [vp, i32, i32, i32, i32, f32, vp, vp, vp, vp, vp, vp]),
         "or_hc_read_ref": (i32, [vp, i32, i32, i32, i32, f32, vp, vp, vp, vp, i32, vp, vp]),
@@ -570,8 +571,19 @@ def load_library(path: str):
     return L
 
 
-def moe_prefill(g, w, x, add_shared=True, trace=False, n_threads=1):
-    return _run_block(lib().or_moe_prefill, g, w, x, add_shared, trace, n_threads)
+def moe_prefill(g, w, x, add_shared=True, trace=False, n_threads=1, logits=None, sgate=None):
+    """The prefill contract.  With `logits` ([T][E], bias included) and `sgate` ([T]) the router's outputs are taken
+    as given -- the device's own, whose matrix-core sums are in the hardware's order -- and routed in the device
+    order."""
+    if logits is None:
+        return _run_block(lib().or_moe_prefill, g, w, x, add_shared, trace, n_threads)
+    lg = np.ascontiguousarray(logits, dtype=np.float32)
+    sgv = None if sgate is None else np.ascontiguousarray(sgate, dtype=np.float32)
+    assert lg.shape == (np.asarray(x).shape[0], g.n_expert)
+
+    def fn(gc, wc, xp, T, yp, add, trp, nth):
+        return lib().or_moe_prefill_logits(gc, wc, xp, T, _p(lg), None if sgv is None else _p(sgv), yp, add, trp, nth)
+    return _run_block(fn, g, w, x, add_shared, trace, n_threads)
 
 
 # ------------------------------------------------------------------------------------------------ metrics

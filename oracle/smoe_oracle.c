@@ -1053,6 +1053,14 @@ static void q2_rows_bf16act(const uint8_t* w, const float* a /* bf16-valued */, 
 
 int or_moe_prefill(const or_geom* g, const or_weights* w, const float* x, int T, float* y, int add_shared,
                    const or_trace* tr, int n_threads) {
+    return or_moe_prefill_logits(g, w, x, T, NULL, NULL, y, add_shared, tr, n_threads);
+}
+
+/* The prefill contract with the router's logits (bias included) and the shared gate dots given: the device's own, for
+ * the device path whose router runs on the matrix cores (their f32 sums are in the hardware's order).  The routing of
+ * the given logits is the device order's (or_route_dev).  NULL: the oracle's own router (router_logits). */
+int or_moe_prefill_logits(const or_geom* g, const or_weights* w, const float* x, int T, const float* logits_in,
+                          const float* sg_in, float* y, int add_shared, const or_trace* tr, int n_threads) {
     if (!geom_ok(g) || T < 0) return -1;
     if (g->w_type != 42 || (g->sh_type >= 0 && g->sh_type != 42 && !sh_native(g))) return -2;
     if (T == 0) return 0;
@@ -1076,6 +1084,11 @@ int or_moe_prefill(const or_geom* g, const or_weights* w, const float* x, int T,
         xa[i] = or_f32_from_bf16(xb[i]);
     }
     for (int t = 0; t < T; ++t) {
+        if (logits_in) {
+            memcpy(logits + (size_t)t * E, logits_in + (size_t)t * E, sizeof(float) * (size_t)E);
+            if (has_sh) sg[t] = sg_in ? sg_in[t] : 0.0f;
+            continue;
+        }
         router_logits(g, w, x + (size_t)t * H, xb + (size_t)t * H, 1, logits + (size_t)t * E);
         if (w->logit_bias)
             for (int e = 0; e < E; ++e) logits[(size_t)t * E + e] = logits[(size_t)t * E + e] + w->logit_bias[e];

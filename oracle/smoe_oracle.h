@@ -149,6 +149,9 @@ int or_moe_decode_ref(const or_geom* g, const or_weights* w, const float* x, int
 /* Prefill contract (bf16 activations, exact per-block weight scale), double accumulation. */
 int or_moe_prefill(const or_geom* g, const or_weights* w, const float* x, int n_tok, float* y, int add_shared,
                    const or_trace* tr, int n_threads);
+/* The same with the router's logits [T][E] (bias included) and the shared gate dots [T] given (NULL: computed). */
+int or_moe_prefill_logits(const or_geom* g, const or_weights* w, const float* x, int n_tok, const float* logits,
+                          const float* sgate, float* y, int add_shared, const or_trace* tr, int n_threads);
 
 /* The decode contract again, bitwise equal to or_moe_decode_dev, organised as the reference CPU path's pool
  * (flat (expert, row-range) job batches, each weight row decoded once for all of its expert's tokens): the timed

@@ -435,11 +435,9 @@ __global__ __launch_bounds__(256) void k_router(const float* __restrict__ xf, co
 }
 
 
-// Reduce-scatter of 64 per-lane values v[i]: at the stage of distance D (32, 16, ..., 1) a lane keeps the half
-// of its remaining items selected by its bit D and adds the partner's copy of them, so lane l ends with the
-// full sum of item l.  Each item's sum is formed by exactly the additions of the xor butterfly 32..1 (own value
-// plus the partner's at every stage, in that stage order), so it equals wave_sum_xor_fast of that item bit for
-// bit, at 63 exchanges instead of 64 x 6.
+// One stage of a reduce-scatter over per-lane values v[0 .. N): at distance D a lane keeps the half of its items
+// selected by its bit D and adds the partner's copy of them, so every item's sum is formed by exactly the additions
+// of the xor butterfly (own value plus the partner's at every stage, in that stage order).
 template <int D, int N>
 __device__ __forceinline__ void rs_stage(float* v, int lane) {
     const bool upper = (lane & D) != 0;
@@ -451,15 +449,6 @@ __device__ __forceinline__ void rs_stage(float* v, int lane) {
         else recv = xor_swap<D>(send);
         v[i] = (upper ? v[i + N / 2] : v[i]) + recv;
     }
-}
-__device__ __forceinline__ float reduce_scatter64(float (&v)[64], int lane) {
-    rs_stage<32, 64>(v, lane);
-    rs_stage<16, 32>(v, lane);
-    rs_stage<8, 16>(v, lane);
-    rs_stage<4, 8>(v, lane);
-    rs_stage<2, 4>(v, lane);
-    rs_stage<1, 2>(v, lane);
-    return v[0];
 }
 
 // group_sum of NIT values at once when lpr = 4 NIT (NIT = 2 or 4): a reduce-scatter over the group's upper
@@ -483,114 +472,6 @@ __device__ __forceinline__ float group_sum_rs(float (&v)[NIT], int lpr, int lane
         r = r + xor_swap<1>(r);
         item = (lane >> 2) & (NIT - 1);
         return r;
-    }
-}
-
-// The same logits for many tokens (no q8_1 images): a work-group computes 16 rows x 16 tokens, wave w the rows
-// 16 bx + 4 w .. + 3 for all 16 tokens (x staged as bf16 in LDS).  Each lane accumulates its chunks l, l+64,
-// ... of all 64 (token, row) dots in element order (the order of k_router), then one reduce-scatter leaves
-// lane l with the dot of token l / 4, row l % 4: the logits equal k_router's bit for bit.
-template <int MAXC>
-__global__ __launch_bounds__(256) void k_router_tile(const float* __restrict__ x, const uint16_t* __restrict__ xb,
-                                                      const uint16_t* __restrict__ W,
-                                                      const uint16_t* __restrict__ w_inp, const float* __restrict__ bias,
-                                                      int H, int E, int rows_total, int T, float* __restrict__ logits,
-                                                      int ld_logits, float* __restrict__ sg) {
-    extern __shared__ __align__(16) uint32_t smem[];
-    const int t0 = blockIdx.y * 16;
-    const int nt = min(16, T - t0);
-    // stage the tile's x as bf16 [token][H] (from `xb` when given, else rounded from x here); loads clamped to the
-    // tile's last 8-value chunk and stores to the buffer's last slot, so that every load issues back to back
-    const int n8 = nt * H / 8, cap = 16 * H / 8;
-    const float4* xs4 = reinterpret_cast<const float4*>(x + (size_t)t0 * H);
-    if (xb) {
-        const uint4* xb4 = reinterpret_cast<const uint4*>(xb + (size_t)t0 * H);
-        for (int base = 0; base < n8; base += 256 * 8) {
-            uint4 v[8];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) v[u] = xb4[min(base + u * 256 + (int)threadIdx.x, n8 - 1)];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) reinterpret_cast<uint4*>(smem)[min(base + u * 256 + (int)threadIdx.x, cap - 1)] = v[u];
-        }
-    } else
-    for (int base = 0; base < n8; base += 256 * 4) {
-        float4 v[4][2];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int g = min(base + u * 256 + (int)threadIdx.x, n8 - 1);  // g = token * H/8 + chunk
-            v[u][0] = xs4[2 * g];
-            v[u][1] = xs4[2 * g + 1];
-        }
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const uint4 b = make_uint4(f32_to_bf16(v[u][0].x) | (f32_to_bf16(v[u][0].y) << 16),
-                                       f32_to_bf16(v[u][0].z) | (f32_to_bf16(v[u][0].w) << 16),
-                                       f32_to_bf16(v[u][1].x) | (f32_to_bf16(v[u][1].y) << 16),
-                                       f32_to_bf16(v[u][1].z) | (f32_to_bf16(v[u][1].w) << 16));
-            reinterpret_cast<uint4*>(smem)[min(base + u * 256 + (int)threadIdx.x, cap - 1)] = b;
-        }
-    }
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int row0 = blockIdx.x * 16 + wave * 4;
-    const int chunks = H >> 3;
-    const uint16_t* wr[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int row = min(row0 + r, rows_total - 1);
-        wr[r] = row < E ? W + (size_t)row * H : w_inp;
-    }
-    __syncthreads();
-    const uint16_t* xs = reinterpret_cast<const uint16_t*>(smem);
-    float acc[64];
-#pragma unroll
-    for (int i = 0; i < 64; ++i) acc[i] = 0.0f;
-    // one chunk round; PARTIAL (only the last round can be): a lane past the last chunk adds 0 * 0 (acc is
-    // never -0), the other rounds need no masks
-    auto round = [&](int j, auto partial) {
-        constexpr bool PARTIAL = decltype(partial)::value;
-        const int c = lane + 64 * j;
-        const bool live = !PARTIAL || c < chunks;
-        const int cc = live ? c : chunks - 1;
-        float wf[4][8];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const uint4 v = *reinterpret_cast<const uint4*>(wr[r] + 8 * cc);
-            const uint32_t q[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                wf[r][2 * e] = live ? u2f(q[e] << 16) : 0.0f;
-                wf[r][2 * e + 1] = live ? u2f(q[e] & 0xFFFF0000u) : 0.0f;
-            }
-        }
-#pragma unroll
-        for (int t = 0; t < 16; ++t) {
-            const uint4 xv = *reinterpret_cast<const uint4*>(xs + (size_t)t * H + 8 * cc);
-            const uint32_t d[4] = {xv.x, xv.y, xv.z, xv.w};
-            float xe[8];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                xe[2 * e] = u2f(d[e] << 16);
-                xe[2 * e + 1] = u2f(d[e] & 0xFFFF0000u);
-            }
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const float xv_e = live ? xe[e] : 0.0f;
-#pragma unroll
-                for (int r = 0; r < 4; ++r) acc[4 * t + r] = __builtin_fmaf(xv_e, wf[r][e], acc[4 * t + r]);
-            }
-        }
-    };
-#pragma unroll
-    for (int j = 0; j < MAXC; ++j) {
-        if (64 * j >= chunks) break;  // uniform
-        if (64 * (j + 1) <= chunks) round(j, std::integral_constant<bool, false>{});
-        else round(j, std::integral_constant<bool, true>{});
-    }
-    const float v = reduce_scatter64(acc, lane);
-    const int t = lane >> 2, row = row0 + (lane & 3);
-    if (t < nt && row < rows_total) {
-        if (row < E) logits[(size_t)(t0 + t) * ld_logits + row] = bias ? v + bias[row] : v;
-        else sg[t0 + t] = v;
     }
 }
 
@@ -2559,19 +2440,9 @@ hipError_t launch_router(const float* xf, const uint16_t* xb, const void* W, con
     const int chunks = H / 8;
     const int maxc = (chunks + 63) / 64;
     // tokens staged per block: 4 for decode batches (more blocks, short staging), 16 (<= 64 KiB of bf16) beyond
-    if (tile_rows) {  // many tokens: row x token tiles
-        const int maxc = (H / 8 + 63) / 64;
-        const size_t lds = (size_t)16 * H * 2;
-#define SMOE_ROUTER_TILE(C)                                                                                        \
-    hipLaunchKernelGGL((k_router_tile<C>), dim3((unsigned)((rows_total + 15) / 16), (unsigned)((T + 15) / 16)),      \
-                       dim3(256), lds, s, xf, xb, static_cast<const uint16_t*>(W), w_inp, bias, H, E, rows_total, T, \
-                       logits, ld_logits, sg)
-        if (maxc <= 2) SMOE_ROUTER_TILE(2);
-        else if (maxc <= 4) SMOE_ROUTER_TILE(4);
-        else SMOE_ROUTER_TILE(8);
-#undef SMOE_ROUTER_TILE
-        return hipGetLastError();
-    }
+    if (tile_rows)  // many tokens: bf16 x and W on the matrix cores
+        return launch_router_mfma(xb, static_cast<const uint16_t*>(W), w_inp, bias, H, E, rows_total, T, logits,
+                                  ld_logits, sg, s);
     int tile = T <= 64 ? 4 : 32768 / H;
     if (tile > 16) tile = 16;
     if (tile > T) tile = T;

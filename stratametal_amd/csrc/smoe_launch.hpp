@@ -30,9 +30,12 @@ hipError_t launch_router(const float* xf, const uint16_t* xb, const void* W, con
                          uint32_t* ximg, int tile_rows, int img_natural, hipStream_t s, const float* rprev = nullptr,
                          float eps = 0.0f, float* xout = nullptr, uint4* clear = nullptr, int clear_n16 = 0,
                          int w_f32 = 0);
-// (tile_rows: many tokens, row x token tiles from xb when given, else from xf; img_natural: write ximg in the IQ2_S
+// (tile_rows: many tokens, bf16 xb and W on the matrix cores (launch_router_mfma); img_natural: write ximg in the IQ2_S
 // kernels' natural order; rprev: the fused stack junction, x = RMSNorm(xf + rprev) written to xout; clear: 16-byte
 // units zeroed for the exchange of the k_q2_moe_small launch after it; w_f32: W is f32 (router_dtype 1), x from xf)
+// the prefill path's router on the matrix cores (bf16 x and W; row E is w_inp, into sg): f32 sums in the MFMA's order
+hipError_t launch_router_mfma(const uint16_t* xb, const uint16_t* W, const uint16_t* w_inp, const float* bias, int H,
+                              int E, int rows_total, int T, float* logits, int ld_logits, float* sg, hipStream_t s);
 hipError_t launch_topk(const float* logits, int ld_logits, int T, int E, int k, int32_t* ids, float* wts, hipStream_t s);
 hipError_t launch_router_margin(const float* logits, int T, int E, int k, float* stats, int32_t* ids, hipStream_t s);
 hipError_t launch_dispatch(const int32_t* ids, int P, int E, int32_t* counts, int32_t* offsets, int32_t* perm,

@@ -29,6 +29,7 @@
 #include "smoe_launch.hpp"
 
 #include <climits>
+#include <type_traits>
 
 namespace smoe {
 
@@ -640,6 +641,132 @@ hipError_t launch_act_records(const float* x, int64_t n_rec, uint32_t* rec, uint
                               int32_t* flags) {
     hipLaunchKernelGGL(k_act_records, dim3((unsigned)act_records_blocks(n_rec)), dim3(256), 0, s, x, n_rec, rec, xb,
                        flags);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------------------------------------ router
+// The prefill path's router on the matrix cores (bf16 routers, from kMfmaTokens tokens): logits[t][e] =
+// sum_h bf16(x[t][h]) * bf16(W[e][h]) (+ bias[e]), and row E (w_inp) the shared gate sg[t].
+// v_mfma_f32_16x16x32_bf16: every bf16 product is exact in f32; the sums are the matrix core's f32 accumulation, in
+// the hardware's order, so the logits are the exact dot to ~1e-7 relative (not bit for bit the decode path's router);
+// the routing and dispatch of the device's logits are exact.
+// Work-group tile: 32 tokens x 64 rows; wave w takes rows 16 w .. 16 w + 15 of the 32 tokens (two 16 x 16 tiles; lane
+// 16 q + i: A[i][8 q + e] = x of token i, B[8 q + e][j] = weight row j, C[4 q + r][j] in register r).  K runs in
+// chunks of 128 through two LDS buffers (rows at a 272-byte pitch: a 16-row fragment read covers the 64 banks once);
+// every thread keeps the global loads of the next two chunks in flight, one barrier per chunk.  At 512 tokens the grid
+// is 144 work-groups, so the kernel is bound by load latency (one round trip per two chunks), not by the matrix cores:
+// the chunk is as deep as the registers of two chunks in flight allow.  The work-groups of one token block take
+// consecutive row blocks on one XCD (linear id mod 8), so that the block's x rows are read from memory once per XCD
+// and then from its L2.
+constexpr int kRtTok = 32, kRtRows = 64, kRtK = 128, kRtPitch = kRtK * 2 + 16;
+constexpr int kRtPieces = kRtK / 8, kRtPass = 256 / kRtPieces;  // 16-byte pieces per row; rows per pass of 256 threads
+constexpr int kRtLa = kRtTok / kRtPass, kRtLb = kRtRows / kRtPass;  // a thread's x and weight pieces per chunk
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(256) void k_router_mfma(const uint16_t* __restrict__ xb, const uint16_t* __restrict__ W,
+                                                      const uint16_t* __restrict__ w_inp, const float* __restrict__ bias,
+                                                      int H, int E, int rows_total, int T, int n_tb, int n_rb,
+                                                      float* __restrict__ logits, int ld_logits, float* __restrict__ sg) {
+    __shared__ __align__(16) uint8_t sa[2][kRtTok * kRtPitch];
+    __shared__ __align__(16) uint8_t sb[2][kRtRows * kRtPitch];
+    const int id = blockIdx.x;
+    const int tb = (id & 7) + 8 * ((id >> 3) / n_rb), rb = (id >> 3) % n_rb;
+    if (tb >= n_tb) return;  // (the grid pads the token blocks to a multiple of 8)
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int q = lane >> 4, i = lane & 15;
+    const int t0 = tb * kRtTok, r0 = rb * kRtRows;
+    // a thread's 16-byte pieces of a chunk: piece tid % kRtPieces of x rows and weight rows tid / kRtPieces + kRtPass j
+    // (rows clamped: the tail's loads stay in bounds, its results are not stored)
+    const int pc = tid % kRtPieces, pr = tid / kRtPieces;
+    const uint16_t* asrc[kRtLa];
+    const uint16_t* bsrc[kRtLb];
+#pragma unroll
+    for (int j = 0; j < kRtLa; ++j) asrc[j] = xb + (size_t)min(t0 + pr + kRtPass * j, T - 1) * H + 8 * pc;
+#pragma unroll
+    for (int j = 0; j < kRtLb; ++j) {
+        const int r = min(r0 + pr + kRtPass * j, rows_total - 1);
+        bsrc[j] = (r < E ? W + (size_t)r * H : w_inp) + 8 * pc;
+    }
+    u32x4 ra[2][kRtLa], rw[2][kRtLb];
+    auto load = [&](auto slot, int k0) {
+        constexpr int P = decltype(slot)::value;
+#pragma unroll
+        for (int j = 0; j < kRtLa; ++j) ra[P][j] = *reinterpret_cast<const u32x4*>(asrc[j] + k0);
+#pragma unroll
+        for (int j = 0; j < kRtLb; ++j) rw[P][j] = *reinterpret_cast<const u32x4*>(bsrc[j] + k0);
+    };
+    auto stash = [&](auto slot) {  // register slot P into LDS buffer P
+        constexpr int P = decltype(slot)::value;
+#pragma unroll
+        for (int j = 0; j < kRtLa; ++j)
+            *reinterpret_cast<u32x4*>(&sa[P][(pr + kRtPass * j) * kRtPitch + 16 * pc]) = ra[P][j];
+#pragma unroll
+        for (int j = 0; j < kRtLb; ++j)
+            *reinterpret_cast<u32x4*>(&sb[P][(pr + kRtPass * j) * kRtPitch + 16 * pc]) = rw[P][j];
+    };
+    using Zero = std::integral_constant<int, 0>;
+    using One = std::integral_constant<int, 1>;
+    const int nk = H / kRtK;
+    load(Zero{}, 0);
+    load(One{}, min(1, nk - 1) * kRtK);
+    stash(Zero{});
+    __syncthreads();
+    f32x4 acc[2];
+#pragma unroll
+    for (int m = 0; m < 2; ++m) acc[m] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    // chunk c lives in register slot c & 1 and LDS buffer c & 1; the loop is unrolled by two so that every register
+    // slot is a constant (an indexed slot would wait for its loads at once)
+    auto chunk = [&](int kc, auto parity) {
+        constexpr int P = decltype(parity)::value;
+        using Q = std::integral_constant<int, 1 - P>;
+        // chunk kc + 2's loads go out now (unconditionally, past the end the last chunk again: a load under a branch
+        // would make the wait below count the loads in flight as zero); chunk kc + 1's, issued a chunk ago, reach LDS
+        // after the products
+        load(parity, min(kc + 2, nk - 1) * kRtK);
+        __builtin_amdgcn_sched_barrier(0);  // (the loads stay ahead of the products and of the stash below)
+#pragma unroll
+        for (int st = 0; st < kRtK / 32; ++st) {  // the chunk's 32-deep steps
+            const bf16x8 b = __builtin_bit_cast(
+                bf16x8, *reinterpret_cast<const u32x4*>(&sb[P][(16 * wave + i) * kRtPitch + 2 * (32 * st + 8 * q)]));
+#pragma unroll
+            for (int m = 0; m < 2; ++m) {
+                const bf16x8 a = __builtin_bit_cast(
+                    bf16x8, *reinterpret_cast<const u32x4*>(&sa[P][(16 * m + i) * kRtPitch + 2 * (32 * st + 8 * q)]));
+                acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc[m], 0, 0, 0);
+            }
+        }
+        stash(Q{});  // (past the end: a copy nobody reads)
+        __syncthreads();
+    };
+    int kc = 0;
+    for (; kc + 1 < nk; kc += 2) {
+        chunk(kc, Zero{});
+        chunk(kc + 1, One{});
+    }
+    if (kc < nk) chunk(kc, Zero{});  // an odd chunk count's last chunk
+    const int row = r0 + 16 * wave + i;
+    if (row >= rows_total) return;
+    const float bv = (bias && row < E) ? bias[row] : 0.0f;
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int t = t0 + 16 * m + 4 * q + r;
+            if (t >= T) continue;
+            if (row < E) logits[(size_t)t * ld_logits + row] = bias ? acc[m][r] + bv : acc[m][r];
+            else sg[t] = acc[m][r];
+        }
+}
+
+hipError_t launch_router_mfma(const uint16_t* xb, const uint16_t* W, const uint16_t* w_inp, const float* bias, int H,
+                              int E, int rows_total, int T, float* logits, int ld_logits, float* sg, hipStream_t s) {
+    if (H % kRtK || T < 1 || rows_total < E || rows_total > E + 1 || (rows_total > E && !w_inp))
+        return hipErrorInvalidValue;
+    const int n_tb = (T + kRtTok - 1) / kRtTok, n_rb = (rows_total + kRtRows - 1) / kRtRows;
+    const int n_tb8 = (n_tb + 7) / 8 * 8;
+    hipLaunchKernelGGL(k_router_mfma, dim3((unsigned)(n_tb8 * n_rb)), dim3(256), 0, s, xb, W, w_inp, bias, H, E,
+                       rows_total, T, n_tb, n_rb, logits, ld_logits, sg);
     return hipGetLastError();
 }
 

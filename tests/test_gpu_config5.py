@@ -20,6 +20,7 @@ import numpy as np
 import pytest
 
 import oracle as O
+import prefill_check as PC
 import stratametal_amd as S
 
 pytestmark = pytest.mark.gpu
@@ -68,19 +69,16 @@ def test_config5_layer_prefill_4096(torch):
     y, tr = ml.forward(dev(torch, x), trace=True)
     yg = host(torch, y)
     assert np.isfinite(yg).all()
-    # routing of every token: the device-order router (bf16 products in the device's order), top-k, dispatch
-    xb = O.bf16_from_f32(x)
-    logits = np.stack([O.bf16_gemv_dev(xb[t], w_host.router, H, E) for t in range(T_PREFILL)])
-    sg = np.array([O.bf16_gemv_dev(xb[t], w_host.gate_inp_sh, H, 1)[0] for t in range(T_PREFILL)], np.float32)
-    ids, wts = O.route_dev(logits, K)
-    counts, offsets, perm, slot = O.dispatch(ids, E)
-    want = dict(logits=logits, sgate=sg, ids=ids, weights=wts, counts=counts, offsets=offsets, perm=perm, slot=slot)
-    for k, v in want.items():
-        assert np.array_equal(bits(host(torch, tr[k]).reshape(-1)), bits(np.asarray(v).reshape(-1))), k
-    say(f"  routing exact; {int((counts > 0).sum())} experts touched, hottest {int(counts.max())} pairs")
-    # output rows: every 32nd token through the oracle's prefill contract
+    # the router on the matrix cores: every 32nd token's logits within 1e-5 of the exact dot, the routing and the
+    # dispatch of every token exactly the device order's of the device's logits
+    htr = {k: host(torch, v) for k, v in tr.items()}
     rows = np.arange(0, T_PREFILL, 32)
-    ref = O.moe_prefill(g, w_host, x[rows], n_threads=16)
+    worst = PC.router_stagewise(g, w_host, x, htr, rows=rows)
+    counts = htr["counts"]
+    say(f"  routing exact; logits {worst:.2e} from the exact dot; {int((counts > 0).sum())} experts touched, "
+        f"hottest {int(counts.max())} pairs")
+    # output rows: every 32nd token through the prefill contract routed from the same logits
+    ref = PC.prefill_want(g, w_host, x, htr, rows=rows, n_threads=16)
     err = O.rel_l1_rows(yg[rows], ref)
     say(f"  {len(rows)} rows: max rel_l1 {err.max():.3e} (mean {err.mean():.3e})")
     assert err.max() <= TOL

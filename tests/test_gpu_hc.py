@@ -158,7 +158,12 @@ def test_ffn_run_parity(torch, case):
     got = got[:T * hc * n].reshape(T, hc, n)
     mixed, inj = O.hc_read_dev(R, n, hw)
     if T >= S.MFMA_TOKENS:
-        y = O.moe_prefill(g, w_host, mixed, add_shared=add_shared, n_threads=16)
+        # the prefill path's router runs on the matrix cores (logits within ~1e-7 of the exact dot): with every
+        # token's k-th / (k+1)-th logit gap far above that, its routing is the oracle's
+        y, otr = O.moe_prefill(g, w_host, mixed, add_shared=add_shared, trace=True, n_threads=16)
+        top = -np.sort(-otr["logits"], axis=1)
+        gap = (top[:, g.top_k - 1] - top[:, g.top_k]) / np.abs(otr["logits"]).max(axis=1)
+        assert gap.min() > 1e-4, f"a token sits at a routing tie ({gap.min():.2e}): choose another seed"
         want = O.hc_write_dev(R, y, inj, n, hc)
         # the block's prefill contract holds per row within 1e-3 of the oracle; the write adds it to the streams
         yg = (got - R) / (2.0 / (1.0 + np.exp(-inj.astype(np.float64) / hc)))[:, :, None]

@@ -6,13 +6,14 @@
 - A layer whose shared expert is stored in its own types (gate, up and down each its own, as real layers:
   include/strata/kernels/shared_expert.hpp:54-58): decode bitwise against or_moe_decode_dev on every decode launch
   shape (the fused small batch, its unfused kernels, many tokens), the shared expert's output rows bitwise; the
-  prefill path within 1e-3 per row of or_moe_prefill with routing exact."""
+  prefill path within 1e-3 per row of or_moe_prefill routed from the device's logits (tests/prefill_check.py)."""
 import sys
 
 import numpy as np
 import pytest
 
 import oracle as O
+import prefill_check as PC
 import stagewise as SW
 import stratametal_amd as S
 
@@ -148,7 +149,7 @@ def test_forward_native_shared_prefill(torch):
     x = O.gen_normal(seed, 100, T * g.n_embd).reshape(T, g.n_embd)
     ml = S.MoELayer(S.Geom(**vars(g)), w_dev, max_tokens=T)
     y, tr = ml.forward(dev(torch, x), trace=True, path=S.PATH_MFMA)
-    want, wtr = O.moe_prefill(g, w_host, x, trace=True, n_threads=8)
-    for k in ("ids", "weights"):
-        assert np.array_equal(bits(host(torch, tr[k])), bits(wtr[k])), k
+    htr = {k: host(torch, v) for k, v in tr.items()}
+    PC.router_stagewise(g, w_host, x, htr)  # the router on the matrix cores; the routing of its logits exact
+    want = PC.prefill_want(g, w_host, x, htr, n_threads=8)
     assert O.rel_l1_rows(host(torch, y), want).max() <= 1e-3

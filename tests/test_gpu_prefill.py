@@ -1,9 +1,11 @@
 """GPU parity of the prefill contract (bf16 activations, exact Q2_0 block scales, bf16 MFMA with f32
 accumulation), through the C ABI, against the oracle's or_moe_prefill on the same seeded inputs.
 
-Routing (logits, ids, weights) and the dispatch (counts, offsets, perm, slot) are bit-exact; the output is
-within max rel_l1 1e-3 per row (metal/src/pack_parity.cpp:2425-2433; the block's gate), the oracle summing
-each row in double.  Covers the benchmark's Zipf prefill (config 3), an expert hot enough to split into
+The router runs on the matrix cores (bf16 routers): its logits are within 1e-5 rel_l1 per token of the exact dot,
+and the routing (ids, weights) and the dispatch (counts, offsets, perm, slot) of the device's logits are bit-exact
+(tests/prefill_check.py); the f32 router's logits are the oracle's bits.  The output is within max rel_l1 1e-3 per
+row (metal/src/pack_parity.cpp:2425-2433; the block's gate) of the contract routed from the same logits, the oracle
+summing each row in double.  Covers the benchmark's Zipf prefill (config 3), an expert hot enough to split into
 several 128-column work items, a shared expert wider than the routed ones, a layer without a shared expert,
 a forced MFMA call below the automatic threshold, and the reference model's H=2560 / F=640 shape."""
 import os
@@ -13,6 +15,7 @@ import numpy as np
 import pytest
 
 import oracle as O
+import prefill_check as PC
 import stratametal_amd as S
 
 pytestmark = pytest.mark.gpu
@@ -130,14 +133,18 @@ def test_forward_prefill_parity(torch, case):
     got = host(torch, yg)
     assert (got[T * g.n_embd:] == 7.0).all(), "guard words past y were written"
     y = got[:T * g.n_embd].reshape(T, g.n_embd)
-    want, wtr = O.moe_prefill(g, w_host, x, add_shared=add_shared, trace=True, n_threads=16)
-    for k in ("logits", "ids", "weights", "counts", "offsets", "perm", "slot"):
-        assert np.array_equal(bits(host(torch, tr[k])), bits(wtr[k])), k
-    if g.sh_type >= 0:
-        assert np.array_equal(bits(host(torch, tr["sgate"])), bits(wtr["sgate"]))
+    htr = {k: host(torch, v) for k, v in tr.items()}
+    # the router stage by stage (its logits on the matrix cores, the routing of those logits exact), then the block
+    # against the prefill contract routed from the same logits
+    worst = PC.router_stagewise(g, w_host, x, htr)
+    want = PC.prefill_want(g, w_host, x, htr, add_shared=add_shared, n_threads=16)
+    if g.router_dtype == 1:  # the f32 router runs row per wave on every path: the oracle's bits
+        _, wtr = O.moe_prefill(g, w_host, x, add_shared=add_shared, trace=True, n_threads=16)
+        assert np.array_equal(bits(htr["logits"]), bits(wtr["logits"]))
     err = O.rel_l1_rows(y, want)
     counts = host(torch, tr["counts"])
-    say(f"  max rel_l1 {err.max():.3e} (mean {err.mean():.3e}); hottest expert {counts.max()} pairs")
+    say(f"  max rel_l1 {err.max():.3e} (mean {err.mean():.3e}); logits {worst:.2e} from the exact dot; "
+        f"hottest expert {counts.max()} pairs")
     assert err.max() <= TOL
     if name.startswith("hot"):
         assert counts.max() > 2 * S.MFMA_CHUNK, "the hot expert does not span three work items"
@@ -163,7 +170,9 @@ def test_trace_stages_and_fp16_overflow_mask(torch):
     ml = S.MoELayer(S.Geom(**vars(g)), w_dev, max_tokens=T)
     x = O.gen_normal(31, 100, T * g.n_embd).reshape(T, g.n_embd)
     y, tr = ml.forward(dev(torch, x), trace=True, stages=True)
-    want, wtr = O.moe_prefill(g, w_host, x, trace=True, n_threads=16)
+    htr = {k: host(torch, v) for k, v in tr.items()}
+    PC.router_stagewise(g, w_host, x, htr)
+    want, wtr = PC.prefill_want(g, w_host, x, htr, trace=True, n_threads=16)
     assert host(torch, tr["overflow"])[0] == 0
     assert O.rel_l1_rows(host(torch, y), want).max() <= TOL
     assert O.rel_l1_rows(host(torch, tr["parts"]), wtr["parts"]).max() <= TOL
@@ -174,7 +183,7 @@ def test_trace_stages_and_fp16_overflow_mask(torch):
         yb, trb = ml.forward(dev(torch, xb), trace=True, stages=True)
         mask = int(host(torch, trb["overflow"])[0])
         assert mask == bit, (scale, mask)
-        yw = O.moe_prefill(g, w_host, xb, n_threads=16)
+        yw = PC.prefill_want(g, w_host, xb, {k: host(torch, v) for k, v in trb.items()}, n_threads=16)
         assert np.isfinite(yw).all(), "the oracle holds the contract beyond the fp16 limit"
         keep = np.arange(T) != bad
         assert O.rel_l1_rows(host(torch, yb)[keep], yw[keep]).max() <= TOL
@@ -192,7 +201,10 @@ def test_auto_path_switches_at_128_tokens(torch):
     ml = S.MoELayer(S.Geom(**vars(g)), w_dev, max_tokens=128)
     y127 = host(torch, ml.forward(dev(torch, x[:127])))
     assert np.array_equal(bits(y127), bits(O.moe_decode_dev(g, w_host, x[:127], n_threads=16)))
-    y128 = host(torch, ml.forward(dev(torch, x)))
-    assert O.rel_l1_rows(y128, O.moe_prefill(g, w_host, x, n_threads=16)).max() <= TOL
+    y128, tr = ml.forward(dev(torch, x), trace=True)
+    htr = {k: host(torch, v) for k, v in tr.items()}
+    PC.router_stagewise(g, w_host, x, htr)
+    y128 = host(torch, y128)
+    assert O.rel_l1_rows(y128, PC.prefill_want(g, w_host, x, htr, n_threads=16)).max() <= TOL
     # and the two contracts differ (q8_1 vs bf16 activations), so the switch is observable
     assert not np.array_equal(bits(y128[:127]), bits(y127))

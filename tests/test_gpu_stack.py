@@ -9,6 +9,7 @@ import numpy as np
 import pytest
 
 import oracle as O
+import prefill_check as PC
 import stratametal_amd as S
 
 pytestmark = pytest.mark.gpu
@@ -74,8 +75,9 @@ def test_stack_prefill_layers_on_gpu_inputs(torch):
     for l in range(N_LAYERS):
         xg = host(torch, xd)
         y, tr = layers[l].forward(xd, add_shared=True, trace=True, path=S.PATH_MFMA)
-        want, wtr = O.moe_prefill(g, hostw[l], xg, add_shared=True, trace=True, n_threads=16)
-        assert np.array_equal(host(torch, tr["ids"]).reshape(-1), np.asarray(wtr["ids"]).reshape(-1)), l
+        htr = {k: host(torch, v) for k, v in tr.items()}
+        PC.router_stagewise(g, hostw[l], xg, htr)
+        want = PC.prefill_want(g, hostw[l], xg, htr, add_shared=True, n_threads=16)
         err = O.rel_l1_rows(host(torch, y), want)
         say(f"  layer {l}: max rel_l1 {err.max():.3e}")
         assert err.max() <= 1e-3
