@@ -1425,19 +1425,21 @@ __device__ __forceinline__ void gu_compute(const Item& item, int hb, uint32_t* s
 }
 
 // The work-group's item, one unit (rows block hb): `smem` is the kernel's dynamic LDS (the image staging area).
-// With `xchg` the h images go to the tagged exchange words instead of himg.
+// With `xchg` the h images go to the tagged exchange words instead of himg.  `sync_after_loads` (PRESTAGED): the
+// staged images are published by a barrier here, after the weight loads were issued.
 template <int NIT, int MAXUPL, bool PRESTAGED = false, bool HQ = false>
 __device__ __forceinline__ void q2_gu_item(const Item& item, int hb, uint32_t* smem, const uint8_t* __restrict__ gate_exps,
                                            const uint8_t* __restrict__ up_exps, const uint8_t* __restrict__ gate_sh,
                                            const uint8_t* __restrict__ up_sh, const uint32_t* __restrict__ ximg,
                                            const int32_t* __restrict__ perm, int k, int H, int F,
                                            uint32_t* __restrict__ himg, int h_blocks, uint64_t* __restrict__ xchg = nullptr,
-                                           StageOut so = {}, int Fs = 0) {
+                                           StageOut so = {}, int Fs = 0, bool sync_after_loads = false) {
     __shared__ float rowv[kGuCols][64];
     __shared__ uint8_t qsc[8][32];
     uint32_t w[NIT][MAXUPL][9];
     if constexpr (PRESTAGED) {
         gu_load_weights<NIT, MAXUPL>(item, hb, gate_exps, up_exps, gate_sh, up_sh, H, F, w);
+        if (sync_after_loads) __syncthreads();  // uniform
     } else {
         StagePieces sp;
         const bool direct = gu_issue<NIT, MAXUPL>(item, hb, gate_exps, up_exps, gate_sh, up_sh, ximg, H, F, sp, w);
@@ -1490,55 +1492,53 @@ struct GuRouteLds {
 // first, then the touched experts in ascending order, with their pairs in ascending pair order -- the item
 // dispatch_block writes there), from the logits `lg` ([T][E], global memory or LDS; wave t routes token t).
 // `commit` runs after the routing and before the barrier that publishes it (the caller's staging of the x images).
-// Returns whether the work-group has an expert (uniform; false after the barrier when its item has none).
+// Returns whether the work-group has an expert (uniform; false after the barrier when its item has none).  `synced`
+// false: the one-token fast path returned without that barrier (every wave routed the token itself), and the caller
+// synchronises before it reads what `commit` wrote.
 template <class Commit>
 __device__ __forceinline__ bool gu_route_item(int y, GuRouteLds& L, const float* lg, int T, int E, int k,
-                                              int has_shared, Item& item, Commit commit) {
+                                              int has_shared, Item& item, Commit commit, bool& synced) {
     const int n_sh = has_shared ? 1 : 0;
     const int tid = threadIdx.x, wave = tid >> 6;
     const bool shared_wg = y < n_sh;
     const int P = T * k;
-    // one token: wave 0 routes it and takes the item from the candidates (the y-th selected id in ascending order,
-    // its one pair at dispatch position y); L.item[7] = 1 when the fast selection declined (then the ids are in
-    // L.ids and the general path below finds the item)
+    synced = true;
+    // one token: every wave routes it (the same selection in each, from the same logits) and takes the item from
+    // the candidates (the y-th selected id in ascending order, its one pair at dispatch position y), so that no
+    // barrier stands between the routing and the item's weight loads; when the fast selection declines (in every
+    // wave alike), wave 0 writes the ids to L.ids and the general path below finds the item
     const bool one = !shared_wg && T == 1 && k <= 64;
-    if (one && wave == 0) {
-        __shared__ uint2 s_cand1[64];
-        const FastRoute R = E <= 512 ? route_fast_t<8, false>(lg, E, k, s_cand1)
-                                     : route_fast_t<16, false>(lg, E, k, s_cand1);
-        const int lane = tid & 63;
-        if (R.ok) {
+    if (one) {
+        __shared__ uint2 s_cand1[4][64];
+        const FastRoute R = E <= 512 ? route_fast_t<8, false>(lg, E, k, s_cand1[wave])
+                                     : route_fast_t<16, false>(lg, E, k, s_cand1[wave]);
+        if (R.ok) {  // uniform over the work-group
             const bool sel = R.crank < k;
             const unsigned long long sm = __ballot(sel);
             const int yc = __builtin_amdgcn_mbcnt_hi((uint32_t)(sm >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)sm, 0u));
             const unsigned long long own = __ballot(sel && yc == y - n_sh);
-            if (lane == 0) {
-                L.item[0] = own ? __builtin_amdgcn_readlane(R.cid, __builtin_ctzll(own)) : -1;
-                L.item[1] = y - n_sh;
-                L.item[2] = 1;
-                L.item[3] = L.item[4] = L.item[5] = L.item[6] = 0;
-                L.item[7] = 0;
-            }
-        } else {
+            commit();
+            synced = false;
+            if (own == 0ull) return false;  // uniform: no expert for this item
+            item.shared = false;
+            item.e = __builtin_amdgcn_readlane(R.cid, __builtin_ctzll(own));
+            item.first = y - n_sh;
+            item.ncol = 1;
+            item.tok0 = 0;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) item.tk[c] = 0;
+            return true;
+        }
+        if (wave == 0) {
             if (E <= 512) route_token_t<8, false>(lg, E, k, nullptr, nullptr, L.ids);
             else route_token_t<16, false>(lg, E, k, nullptr, nullptr, L.ids);
-            if (lane == 0) L.item[7] = 1;
         }
-    } else if (!shared_wg && !one && wave < T) {
+    } else if (!shared_wg && wave < T) {
         route_token_ids(lg + (size_t)wave * E, E, k, L.ids + wave * k);
     }
     commit();
     __syncthreads();
-    if (one && L.item[7] == 0) {
-        if (L.item[0] < 0) return false;  // uniform: no expert for this item
-        item.shared = false;
-        item.e = L.item[0];
-        item.first = L.item[1];
-        item.ncol = 1;
-        item.tok0 = 0;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) item.tk[c] = 0;
-    } else if (shared_wg) {
+    if (shared_wg) {
         item.shared = true;
         item.e = kItemShared;
         item.first = P;
@@ -1653,14 +1653,19 @@ __device__ __forceinline__ bool gu_route_wg(
         pre[j] = reinterpret_cast<const u32x4*>(ximg)[min(min(j, npre - 1) * 256 + tid, pieces - 1)];
     GuRouteLds& L = *reinterpret_cast<GuRouteLds*>(smem + kGuCols * qb * kImgLdsDw + 4);
     Item item;
-    const bool has = gu_route_item(y, L, logits, T, E, k, has_shared, item, [&] {
+    bool synced;
+    const bool has = gu_route_item(
+        y, L, logits, T, E, k, has_shared, item,
+        [&] {
 #pragma unroll
-        for (int j = 0; j < 6; ++j)
-            if (j * 256 + tid < pieces) reinterpret_cast<u32x4*>(smem)[lds_piece(j * 256 + tid)] = pre[j];
-    });
+            for (int j = 0; j < 6; ++j)
+                if (j * 256 + tid < pieces) reinterpret_cast<u32x4*>(smem)[lds_piece(j * 256 + tid)] = pre[j];
+        },
+        synced);
     if (!has) return false;
+    // (unsynchronised routing: the weight loads go out first, then the barrier that publishes the images)
     q2_gu_item<NIT, MAXUPL, true>(item, hb, smem, gate_exps, up_exps, gate_sh, up_sh, ximg, nullptr, k, H, F, himg,
-                                  h_blocks, xchg);
+                                  h_blocks, xchg, {}, 0, !synced);
     return true;
 }
 
@@ -2689,9 +2694,16 @@ hipError_t launch_q2_moe_small(const uint8_t* gate_exps, const uint8_t* up_exps,
     gu_shape(H, nit, upl);
     const size_t lds = moe_small_lds(T, k, H, h_blocks);
     const int spin = wait_limit();
+    // (a down work-group's tasks in one batch of three per wave when they fit: the b = 1 layer's 11 items)
+    const bool d3 = dmaxupl == 1 && max_items * npass <= 12;
 #define SMOE_MS(N, U)                                                                                                \
     do {                                                                                                             \
-        if (dmaxupl == 1)                                                                                            \
+        if (d3)                                                                                                      \
+            hipLaunchKernelGGL((k_q2_moe_small<N, U, 1, 3>), grid, dim3(256), lds, s, gate_exps, up_exps, gate_sh,    \
+                               up_sh, down_exps, down_sh, ximg, logits, sg, T, E, k, H, F, Fs, has_shared, ids, wts,  \
+                               counts, offsets, perm, slot, elist, n_list, items, max_items, h_blocks, xw, npass,      \
+                               add_shared, y, spin, status);                                                          \
+        else if (dmaxupl == 1)                                                                                       \
             hipLaunchKernelGGL((k_q2_moe_small<N, U, 1, 4>), grid, dim3(256), lds, s, gate_exps, up_exps, gate_sh,    \
                                up_sh, down_exps, down_sh, ximg, logits, sg, T, E, k, H, F, Fs, has_shared, ids, wts,  \
                                counts, offsets, perm, slot, elist, n_list, items, max_items, h_blocks, xw, npass,      \
