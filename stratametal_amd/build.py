@@ -32,6 +32,10 @@ COMMON = [
     # MFMA results in VGPRs: the prefill kernels scale every block's MFMA result on the VALU, and in AGPRs
     # each element would first be copied out with v_accvgpr_read
     "-mllvm", "-amdgpu-mfma-vgpr-form",
+    # the first 14 dwords of every kernel's arguments arrive in SGPRs with the wave (gfx950 kernarg preloading;
+    # the code object keeps a prologue that loads them itself where the firmware does not preload), so the
+    # decode kernels issue their first loads without a scalar round trip to the argument buffer
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
     "-I", os.path.join(ROOT, "include"), "-I", CSRC,
     "-Wall", "-Wno-unused-result",
 ]

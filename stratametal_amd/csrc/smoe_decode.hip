@@ -382,21 +382,19 @@ __device__ __forceinline__ void router_row_dots(const RouterRow<MAXC, F32>& R, c
 }
 
 template <int MAXC, bool F32>
-__global__ __launch_bounds__(256) void k_router(const float* __restrict__ xf, const uint16_t* __restrict__ xb,
+// (The arguments a work-group reads before its first loads come first: the library is built with kernel-argument
+// preloading, so the first 14 dwords arrive in SGPRs with the wave instead of by a scalar load from memory.)
+__global__ __launch_bounds__(256) void k_router(int H, int E, int rows_total, int T, int tok_tile, int clear_n16,
                                                  const void* __restrict__ W, const uint16_t* __restrict__ w_inp,
-                                                 const float* __restrict__ bias, int H, int E, int rows_total, int T,
-                                                 int tok_tile, float* __restrict__ logits, int ld_logits,
-                                                 float* __restrict__ sg, uint32_t* __restrict__ ximg, int img_natural,
-                                                 const float* __restrict__ rprev, float eps, float* __restrict__ xout,
-                                                 uint4* __restrict__ clear, int clear_n16) {
+                                                 const float* __restrict__ bias, const float* __restrict__ xf,
+                                                 const uint16_t* __restrict__ xb, float* __restrict__ logits,
+                                                 int ld_logits, float* __restrict__ sg, uint32_t* __restrict__ ximg,
+                                                 int img_natural, const float* __restrict__ rprev, float eps,
+                                                 float* __restrict__ xout, uint4* __restrict__ clear) {
     extern __shared__ __align__(16) uint32_t smem[];
     __shared__ uint8_t qsc[8][32];
     __shared__ float inv_s[16];
     __shared__ float wsum_s[4][4];
-    // the exchange words of the kernel after this one (k_q2_moe_small), cleared: no launch reads them before it
-    for (int i = ((int)blockIdx.y * (int)gridDim.x + (int)blockIdx.x) * 256 + (int)threadIdx.x; i < clear_n16;
-         i += (int)(gridDim.x * gridDim.y) * 256)
-        clear[i] = make_uint4(0u, 0u, 0u, 0u);
     const int t0 = blockIdx.y * tok_tile;
     const int nt = min(tok_tile, T - t0);
     const int row_blocks = (rows_total + 3) / 4;
@@ -415,6 +413,10 @@ __global__ __launch_bounds__(256) void k_router(const float* __restrict__ xf, co
     // a row block: the wave's weight row (clamped, every load issued), in flight during the staging below
     RouterRow<MAXC, F32> R;
     if (!img_block) router_row_load<MAXC, F32>(W, w_inp, bias, H, E, rows_total, blockIdx.x, R);
+    // the exchange words of the kernel after this one (k_q2_moe_small), cleared: no launch reads them before it
+    for (int i = ((int)blockIdx.y * (int)gridDim.x + (int)blockIdx.x) * 256 + (int)threadIdx.x; i < clear_n16;
+         i += (int)(gridDim.x * gridDim.y) * 256)
+        clear[i] = make_uint4(0u, 0u, 0u, 0u);
     // values of a row per thread of the junction: 256 NM >= H (8 values per bf16 chunk, 4 per f32 chunk)
     constexpr int NMJ = F32 ? MAXC : 2 * MAXC;
     if (NMJ <= 16 && rprev)  // the fused junction; a row block stages s * scale from registers
@@ -2125,14 +2127,16 @@ __device__ __forceinline__ void down_wg(int r0, uint32_t* smem, const float* lg,
 }
 
 template <int NIT, int MAXUPL, int DMAXUPL, int DNT>
+// (The arguments of the role split, the image loads and the routing come first: the first 14 dwords arrive
+// preloaded in SGPRs.)
 __global__ __launch_bounds__(256) void k_q2_moe_small(
+    int max_items, int h_blocks, int T, int E, int k, int H, int F, int Fs, int has_shared,
+    const uint32_t* __restrict__ ximg, const float* __restrict__ logits, const float* __restrict__ sg,
     const uint8_t* __restrict__ gate_exps, const uint8_t* __restrict__ up_exps, const uint8_t* __restrict__ gate_sh,
     const uint8_t* __restrict__ up_sh, const uint8_t* __restrict__ down_exps, const uint8_t* __restrict__ down_sh,
-    const uint32_t* __restrict__ ximg, const float* __restrict__ logits, const float* __restrict__ sg, int T, int E,
-    int k, int H, int F, int Fs, int has_shared, int32_t* __restrict__ ids, float* __restrict__ wts,
-    int32_t* __restrict__ counts, int32_t* __restrict__ offsets, int32_t* __restrict__ perm,
-    int32_t* __restrict__ slot, int32_t* __restrict__ elist, int32_t* __restrict__ n_list, int4* __restrict__ items,
-    int max_items, int h_blocks, uint64_t* __restrict__ xchg, int npass, int add_shared, float* __restrict__ y,
+    int32_t* __restrict__ ids, float* __restrict__ wts, int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
+    int32_t* __restrict__ perm, int32_t* __restrict__ slot, int32_t* __restrict__ elist, int32_t* __restrict__ n_list,
+    int4* __restrict__ items, uint64_t* __restrict__ xchg, int npass, int add_shared, float* __restrict__ y,
     int spin_limit, int32_t* __restrict__ status) {
     extern __shared__ __align__(16) uint32_t smem[];
     const int hbn = h_blocks;  // rows blocks of the widest expert
@@ -2433,8 +2437,8 @@ hipError_t launch_router(const float* xf, const uint16_t* xb, const void* W, con
         dim3 grid((unsigned)((rows_total + 3) / 4 + img_blocks), (unsigned)((T + tile - 1) / tile));
         const size_t lds = (size_t)tile * H * 4;
 #define SMOE_ROUTER_F32(C)                                                                                          \
-    hipLaunchKernelGGL((k_router<C, true>), grid, dim3(256), lds, s, xf, xb, W, w_inp, bias, H, E, rows_total, T,   \
-                       tile, logits, ld_logits, sg, ximg, img_natural, rprev, eps, xout, clear, clear_n16)
+    hipLaunchKernelGGL((k_router<C, true>), grid, dim3(256), lds, s, H, E, rows_total, T, tile, clear_n16, W, w_inp, \
+                       bias, xf, xb, logits, ld_logits, sg, ximg, img_natural, rprev, eps, xout, clear)
         if (maxc4 <= 2) SMOE_ROUTER_F32(2);
         else if (maxc4 <= 4) SMOE_ROUTER_F32(4);
         else if (maxc4 <= 8) SMOE_ROUTER_F32(8);
@@ -2457,8 +2461,8 @@ hipError_t launch_router(const float* xf, const uint16_t* xb, const void* W, con
     dim3 grid((unsigned)((rows_total + 3) / 4 + img_blocks), (unsigned)((T + tile - 1) / tile));
     const size_t lds = (size_t)tile * H * 2;
 #define SMOE_ROUTER(C)                                                                                          \
-    hipLaunchKernelGGL((k_router<C, false>), grid, dim3(256), lds, s, xf, xb, W, w_inp, bias, H, E, rows_total, T, tile, \
-                       logits, ld_logits, sg, ximg, img_natural, rprev, eps, xout, clear, clear_n16)
+    hipLaunchKernelGGL((k_router<C, false>), grid, dim3(256), lds, s, H, E, rows_total, T, tile, clear_n16, W, w_inp, \
+                       bias, xf, xb, logits, ld_logits, sg, ximg, img_natural, rprev, eps, xout, clear)
     if (maxc <= 2) SMOE_ROUTER(2);
     else if (maxc <= 4) SMOE_ROUTER(4);
     else if (maxc <= 8) SMOE_ROUTER(8);
@@ -2699,19 +2703,19 @@ hipError_t launch_q2_moe_small(const uint8_t* gate_exps, const uint8_t* up_exps,
 #define SMOE_MS(N, U)                                                                                                \
     do {                                                                                                             \
         if (d3)                                                                                                      \
-            hipLaunchKernelGGL((k_q2_moe_small<N, U, 1, 3>), grid, dim3(256), lds, s, gate_exps, up_exps, gate_sh,    \
-                               up_sh, down_exps, down_sh, ximg, logits, sg, T, E, k, H, F, Fs, has_shared, ids, wts,  \
-                               counts, offsets, perm, slot, elist, n_list, items, max_items, h_blocks, xw, npass,      \
+            hipLaunchKernelGGL((k_q2_moe_small<N, U, 1, 3>), grid, dim3(256), lds, s, max_items, h_blocks, T, E, k,  \
+                               H, F, Fs, has_shared, ximg, logits, sg, gate_exps, up_exps, gate_sh, up_sh, down_exps, \
+                               down_sh, ids, wts, counts, offsets, perm, slot, elist, n_list, items, xw, npass,       \
                                add_shared, y, spin, status);                                                          \
         else if (dmaxupl == 1)                                                                                       \
-            hipLaunchKernelGGL((k_q2_moe_small<N, U, 1, 4>), grid, dim3(256), lds, s, gate_exps, up_exps, gate_sh,    \
-                               up_sh, down_exps, down_sh, ximg, logits, sg, T, E, k, H, F, Fs, has_shared, ids, wts,  \
-                               counts, offsets, perm, slot, elist, n_list, items, max_items, h_blocks, xw, npass,      \
+            hipLaunchKernelGGL((k_q2_moe_small<N, U, 1, 4>), grid, dim3(256), lds, s, max_items, h_blocks, T, E, k,  \
+                               H, F, Fs, has_shared, ximg, logits, sg, gate_exps, up_exps, gate_sh, up_sh, down_exps, \
+                               down_sh, ids, wts, counts, offsets, perm, slot, elist, n_list, items, xw, npass,       \
                                add_shared, y, spin, status);                                                          \
         else                                                                                                         \
-            hipLaunchKernelGGL((k_q2_moe_small<N, U, 2, 4>), grid, dim3(256), lds, s, gate_exps, up_exps, gate_sh,    \
-                               up_sh, down_exps, down_sh, ximg, logits, sg, T, E, k, H, F, Fs, has_shared, ids, wts,  \
-                               counts, offsets, perm, slot, elist, n_list, items, max_items, h_blocks, xw, npass,      \
+            hipLaunchKernelGGL((k_q2_moe_small<N, U, 2, 4>), grid, dim3(256), lds, s, max_items, h_blocks, T, E, k,  \
+                               H, F, Fs, has_shared, ximg, logits, sg, gate_exps, up_exps, gate_sh, up_sh, down_exps, \
+                               down_sh, ids, wts, counts, offsets, perm, slot, elist, n_list, items, xw, npass,       \
                                add_shared, y, spin, status);                                                          \
     } while (0)
     SMOE_SHAPE_DISPATCH(SMOE_MS)
