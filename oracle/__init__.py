@@ -26,7 +26,8 @@ IQ2_S = 22
 
 
 def build(quiet: bool = True) -> None:
-    """Compile oracle/liboracle.so (and oracle/_ref where the reference tree exists)."""
+    """Compile oracle/liboracle.so, its sanitized twin oracle/_asan/liboracle.so, and oracle/_ref where the reference
+    tree exists."""
     out = subprocess.run(["make", "-C", _HERE, "all"], capture_output=True, text=True)
     if out.returncode != 0:
         raise RuntimeError("oracle build failed:\n" + out.stdout + out.stderr)
@@ -41,7 +42,8 @@ def _p(a: np.ndarray):
 def lib():
     global _LIB
     if _LIB is None:
-        path = os.path.join(_HERE, "liboracle.so")
+        # SMOE_ORACLE_LIB: another build of the same library (the sanitized oracle/_asan/liboracle.so)
+        path = os.environ.get("SMOE_ORACLE_LIB") or os.path.join(_HERE, "liboracle.so")
         if not os.path.exists(path):
             build()
         L = C.CDLL(path)

@@ -164,7 +164,7 @@ float or_native_part(int type, const uint8_t* blk, const uint8_t* x0, int iqs) {
             const uint8_t* ql = blk + (q5 ? 48 : 16);
             const int byte = 16 * bq8_offset + 4 * qoff;
             const int32_t v0 = u32le(ql + byte), v1 = u32le(ql + byte + 16);
-            int32_t vh0 = 0, vh1 = 0;
+            uint32_t vh0 = 0, vh1 = 0;  // (unsigned: the high-bit shifts below are defined)
             if (q5) {
                 vh0 = u32le(blk + 16 + 4 * qoff) >> bq8_offset;
                 vh1 = u32le(blk + 32 + 4 * qoff) >> bq8_offset;

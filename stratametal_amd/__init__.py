@@ -15,7 +15,8 @@ from dataclasses import dataclass
 from typing import Dict, Optional
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "lib", "libsmoe.so")
+# SMOE_LIB names another build of the same library (the host-sanitized lib/libsmoe_asan.so, for tests/test_sanitize.py)
+LIB_PATH = os.environ.get("SMOE_LIB") or os.path.join(_HERE, "lib", "libsmoe.so")
 _LIB = None
 
 Q2_0 = 42

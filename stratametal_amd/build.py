@@ -55,6 +55,42 @@ def _compile(src: str) -> str:
     return obj
 
 
+# The host-sanitized library (AddressSanitizer + UndefinedBehaviorSanitizer on the host code of the C ABI and the
+# GGUF reader; the kernels as built above): lib/libsmoe_asan.so, for tests/test_sanitize.py, which runs the CPU tests
+# on it (and on a sanitized build of the test checker) under the clang sanitizer runtime.  Never loaded by the
+# product path.
+LIB_ASAN = os.path.join(LIBDIR, "libsmoe_asan.so")
+HOST_SOURCES = ["smoe_api.cpp", "smoe_gguf.cpp"]
+SANITIZE = [f for opt in ("-fsanitize=address", "-fsanitize=undefined", "-fno-sanitize-recover=undefined",
+                          "-fno-omit-frame-pointer") for f in ("-Xarch_host", opt)]
+
+
+def _compile_asan(src: str) -> str:
+    obj = os.path.join(BUILD, "asan", os.path.splitext(src)[0] + ".o")
+    cmd = [HIPCC, "-x", "hip", *COMMON, *SANITIZE, "-c", os.path.join(CSRC, src), "-o", obj]
+    out = subprocess.run(cmd, capture_output=True, text=True)
+    if out.returncode != 0:
+        raise RuntimeError(f"hipcc (sanitized host) failed on {src}:\n{out.stderr}")
+    return obj
+
+
+def build_sanitized(verbose: bool = False) -> str:
+    """lib/libsmoe_asan.so from the kernel objects of build() and sanitized host objects."""
+    os.makedirs(os.path.join(BUILD, "asan"), exist_ok=True)
+    with cf.ThreadPoolExecutor(max_workers=len(HOST_SOURCES)) as ex:
+        host = list(ex.map(_compile_asan, HOST_SOURCES))
+    kern = [os.path.join(BUILD, os.path.splitext(s)[0] + ".o") for s in SOURCES if s not in HOST_SOURCES]
+    tmp = LIB_ASAN + ".tmp"
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-shared-libsan", *SANITIZE, "-o", tmp, *host, *kern]
+    out = subprocess.run(cmd, capture_output=True, text=True)
+    if out.returncode != 0:
+        raise RuntimeError(f"sanitized link failed:\n{out.stderr}")
+    os.replace(tmp, LIB_ASAN)
+    if verbose:
+        print("built", LIB_ASAN)
+    return LIB_ASAN
+
+
 def build(verbose: bool = False) -> str:
     os.makedirs(BUILD, exist_ok=True)
     os.makedirs(LIBDIR, exist_ok=True)
