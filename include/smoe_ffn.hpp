@@ -2,8 +2,9 @@
 //
 // Mirrors the reference's per-layer feed-forward operator, FfnExec::load / FfnExec::run
 // (metal/include/strata/metal/layer_exec.hpp:113-140): run() is its MoE interior (metal/src/layer_exec.cpp:470-530,
-// `mixed` to `combined`), run_layer() the whole call with the hyper-connection ends around it; load() takes the layer's device tensors and geometry once and owns every buffer the
-// call needs, sized for a maximum token count, so that run() allocates nothing; status codes become
+// `mixed` to `combined`), run_layer() the whole call with the hyper-connection ends around it; load() takes the
+// layer's device tensors and geometry, or the layer of an open GGUF model and the model geometry, once and owns
+// every buffer the call needs, sized for a maximum token count, so that run() allocates nothing; status codes become
 // exceptions (the reference throws MetalError, metal/include/strata/metal/device.hpp:28-31); a traced run
 // copies the stage outputs to host vectors, as FfnTrace does (layer_exec.hpp:100-109).  Uses only smoe.h and
 // the HIP runtime.
@@ -46,8 +47,58 @@ struct FfnTrace {
     std::vector<float> stage_ms;         // router, route, gate/up, down, combine
 };
 
+// The MoE and hyper-connection fields of the reference's model geometry (strata::core::ModelGeometry,
+// include/strata/core/layout.hpp:27-55) that a layer's tensors must match; hc 0: no check of the hyper-connection
+// shapes.
+struct ModelGeometry {
+    int64_t n_embd = 0, n_ff = 0, n_expert = 0;
+    int64_t hc = 0, hc_lr = 0;
+};
+
 class FfnExec {
    public:
+    // The reference's FfnExec::load(model, layer, geometry, with_shared) (metal/src/layer_exec.cpp:369-452): layer
+    // `layer`'s MoE tensors from an open model (smoe_model_open: blk.<layer>.ffn_{gate,up,down}_exps,
+    // ffn_gate_inp, with_shared the shared expert's planes and gate, and the hyper-connection tensors when the
+    // file has them), checked against `geom` (a routed plane of another shape is refused, as the reference's
+    // expert_spans refuses it), copied into device memory this operator owns, and the operator loaded on them for
+    // up to `max_tokens` tokens per run.  top_k 0: the model's <arch>.expert_used_count.  The copies are
+    // complete when load returns (the mapping may be closed after).
+    static FfnExec load(const smoe_model* model, int32_t layer, const ModelGeometry& geom, bool with_shared,
+                        int32_t max_tokens, bool with_trace = false, int32_t top_k = 0, hipStream_t stream = nullptr) {
+        smoe_layer_plan plan{};
+        check(smoe_layer_plan_for(model, layer, top_k, with_shared ? 1 : 0, &plan), "FfnExec::load plan");
+        const smoe_geom& g = plan.geom;
+        auto mismatch = [&](const char* what, int64_t have, int64_t want) {
+            if (have != want)
+                throw Error(SMOE_EINVAL, "FfnExec::load: layer " + std::to_string(layer) + " has " + what + " " +
+                                             std::to_string(have) + ", the geometry says " + std::to_string(want));
+        };
+        mismatch("n_embd", g.n_embd, geom.n_embd);
+        mismatch("n_ff", g.n_ff, geom.n_ff);
+        mismatch("n_expert", g.n_expert, geom.n_expert);
+        if (geom.hc > 0) {
+            mismatch("hc", plan.hc.hc, geom.hc);
+            mismatch("hc_lr", plan.hc.hc_lr, geom.hc_lr);
+        }
+        void* buf = nullptr;
+        check_hip(hipMalloc(&buf, plan.device_bytes), "FfnExec::load weights");
+        try {
+            smoe_weights w{};
+            smoe_hc hc{};
+            const bool has_hc = plan.hc.hc > 0;
+            check(smoe_layer_upload(model, &plan, buf, plan.device_bytes, &w, has_hc ? &hc : nullptr, stream),
+                  "FfnExec::load upload");
+            FfnExec f = load(g, w, max_tokens, with_trace, has_hc ? &hc : nullptr);
+            f.wbuf_ = buf;
+            f.wbuf_bytes_ = plan.device_bytes;
+            return f;
+        } catch (...) {
+            (void)hipFree(buf);
+            throw;
+        }
+    }
+
     // The layer's tensors (device pointers into the loaded model, e.g. a GGUF mapping) and geometry; buffers
     // for up to `max_tokens` tokens per run, and for tracing when `with_trace`.
     // With `hc` (the layer's hyper-connection tensors) the operator also runs the whole layer call, run_layer.
@@ -90,6 +141,8 @@ class FfnExec {
             ws_bytes_ = std::exchange(o.ws_bytes_, 0);
             tr_ = std::exchange(o.tr_, nullptr);
             tr_bytes_ = std::exchange(o.tr_bytes_, 0);
+            wbuf_ = std::exchange(o.wbuf_, nullptr);
+            wbuf_bytes_ = std::exchange(o.wbuf_bytes_, 0);
             for (int i = 0; i < SMOE_STAGE_EVENTS; ++i) ev_[i] = std::exchange(o.ev_[i], nullptr);
         }
         return *this;
@@ -150,8 +203,9 @@ class FfnExec {
               "FfnExec::run_layer");
     }
 
-    // Device bytes this operator owns (workspace and trace buffers; the weights are the caller's).
-    uint64_t gpu_bytes() const { return ws_bytes_ + tr_bytes_; }
+    // Device bytes this operator owns (workspace and trace buffers, and the layer's tensors when it loaded them
+    // from a model; otherwise the weights are the caller's).
+    uint64_t gpu_bytes() const { return ws_bytes_ + tr_bytes_ + wbuf_bytes_; }
     const smoe_geom& geom() const { return g_; }
 
    private:
@@ -179,6 +233,9 @@ class FfnExec {
     void release() noexcept {
         if (ws_) (void)hipFree(ws_);
         if (tr_) (void)hipFree(tr_);
+        if (wbuf_) (void)hipFree(wbuf_);
+        wbuf_ = nullptr;
+        wbuf_bytes_ = 0;
         for (hipEvent_t& e : ev_)
             if (e) (void)hipEventDestroy(e);
         ws_ = tr_ = nullptr;
@@ -194,6 +251,8 @@ class FfnExec {
     size_t ws_bytes_ = 0;
     void* tr_ = nullptr;
     size_t tr_bytes_ = 0;
+    void* wbuf_ = nullptr;  // the layer's tensors, when loaded from a model
+    size_t wbuf_bytes_ = 0;
     hipEvent_t ev_[SMOE_STAGE_EVENTS] = {};
 };
 

@@ -130,3 +130,64 @@ def test_gguf_upload_refusals(torch, tmp_path):
     assert not host(torch, buf).any(), "a refused upload wrote"
     assert L.smoe_layer_upload(m._h, C.byref(p), base, p.device_bytes, C.byref(wc), None, st) == 0
     assert host(torch, buf).any()
+
+
+def _demo_out(raw, T, H, E, K, n_layer):
+    hdr = np.frombuffer(raw[:16], np.int32)
+    assert list(hdr) == [T, H, E, K]
+    o = 16
+    parts = []
+    for dtype, n in ((np.float32, T * H), (np.int32, T * K), (np.float32, T * K), (np.int32, E), (np.float32, 5),
+                     (np.float32, n_layer)):
+        parts.append(np.frombuffer(raw[o:o + 4 * n], dtype))
+        o += 4 * n
+    assert o == len(raw)
+    return parts
+
+
+def test_cpp_operator_loads_a_gguf_layer(torch, tmp_path):
+    """The C++ operator's load(model, layer, geometry, with_shared) (FfnExec::load, metal/src/layer_exec.cpp:
+    369-452) on a GGUF layer with hyper-connection tensors: its traced run and its layer call give the bits of the
+    Python binding on the same file and inputs; a geometry the layer does not have is refused."""
+    import os
+    import subprocess
+    demo = os.path.join(os.path.dirname(S.LIB_PATH), "smoe_ffn_demo")
+    assert os.path.exists(demo), "smoe_ffn_demo is not built (python -m stratametal_amd.build)"
+    g = O.Geom(n_expert=64, top_k=8)
+    seed, layer, T = 84, 3, 7
+    say(f"case: C++ FfnExec::load from GGUF, T={T}")
+    w = O.make_weights(g, seed)
+    hc = hc_arrays(g.n_embd, seed=seed)
+    ts = W.layer_tensors(g, w, layer, hc=hc) + W.layer_tensors(g, w, layer + 1)
+    meta = [("general.architecture", W.STRING, "qwen4exp"), ("qwen4exp.expert_used_count", W.U32, g.top_k)]
+    path = str(W.write(tmp_path / "m.gguf", meta, ts))
+    out = str(tmp_path / "out.bin")
+    H, E, K, n_hc, lr = g.n_embd, g.n_expert, g.top_k, hc[0], hc[1]
+    args = [demo, "--gguf", out, path, str(layer), str(T), str(seed), str(H), str(g.n_ff), str(E), str(n_hc),
+            str(lr), "1"]
+    r = subprocess.run(args, capture_output=True, text=True, timeout=120)
+    sys.stdout.write(r.stdout)
+    assert r.returncode == 0, r.stderr
+    comb, ids, rw, counts, stage_ms, lay = _demo_out(open(out, "rb").read(), T, H, E, K, T * n_hc * H)
+    assert (stage_ms >= 0).all()
+
+    m = S.Model(path)
+    gl, wd, hcx = m.load_layer(layer, with_hc=True)
+    x = S.synth_normal(seed, 100, T * H).reshape(T, H)
+    ml = S.MoELayer(gl, wd, max_tokens=T)
+    y, tr = ml.forward(x, add_shared=True, trace=True)
+    assert np.array_equal(comb.view(np.uint32), bits(host(torch, y)).ravel())
+    assert np.array_equal(ids, host(torch, tr["ids"]).ravel())
+    assert np.array_equal(rw.view(np.uint32), bits(host(torch, tr["weights"])).ravel())
+    assert np.array_equal(counts, host(torch, tr["counts"]))
+    # the oracle's bits on the file's arrays, as the forward test above checks them
+    assert np.array_equal(comb.view(np.uint32), bits(O.moe_decode_dev(g, w, host(torch, x), n_threads=8)).ravel())
+    R = S.synth_normal(seed, 101, T * n_hc * H).reshape(T, n_hc, H)
+    got = S.FfnLayer(gl, wd, hcx, max_tokens=T).run(R)
+    assert np.array_equal(lay.view(np.uint32), bits(host(torch, got)).ravel())
+    m.close()
+
+    bad = list(args)
+    bad[8] = str(2 * g.n_ff)  # n_ff the layer does not have
+    r = subprocess.run(bad, capture_output=True, text=True, timeout=120)
+    assert r.returncode == 1 and "the geometry says" in r.stderr, (r.returncode, r.stderr)
