@@ -21,6 +21,31 @@
 
 namespace smoe {
 
+// ------------------------------------------------------------------------------------------------ phase stamps
+// The decode timeline (python -m stratametal_amd.timeline): built with SMOE_STAMPS defined (lib/libsmoe_stamps.so,
+// never the product library), thread 0 of a work-group writes the 100 MHz clock (s_memrealtime) into slot i of its
+// 32-slot row of the stamp buffer (rows [kernel][work-group]: kernel 0 the router, 1 the fused decode launch);
+// SMOE_STAMP_AFTER first waits for a value (so that the stamp marks its arrival).  Without SMOE_STAMPS every stamp
+// compiles to nothing.
+#if defined(SMOE_STAMPS)
+__constant__ uint64_t* g_stamp;  // (constant memory: a scalar load, no wait on the vector loads in flight)
+#define SMOE_STAMP_VAL(k, i, v)                                                                      \
+    do {                                                                                             \
+        if (threadIdx.x == 0 && g_stamp) g_stamp[((size_t)(k) * 4096 + blockIdx.x) * 32 + (i)] = (v); \
+    } while (0)
+#define SMOE_STAMP(k, i) SMOE_STAMP_VAL(k, i, __builtin_amdgcn_s_memrealtime())
+#define SMOE_STAMP_AFTER(k, i, x)                                                 \
+    do {                                                                          \
+        const int stamp_v_ = __builtin_amdgcn_readfirstlane((int)(x));            \
+        asm volatile("" ::"s"(stamp_v_));                                         \
+        SMOE_STAMP(k, i);                                                         \
+    } while (0)
+#else
+#define SMOE_STAMP_VAL(k, i, v) ((void)0)
+#define SMOE_STAMP(k, i) ((void)0)
+#define SMOE_STAMP_AFTER(k, i, x) ((void)0)
+#endif
+
 // ------------------------------------------------------------------------------------------------ Q2_0 unit
 // Unit = one 36-byte double block (two Q2_0 blocks, 128 weights, dword aligned), 9 dwords:
 //   w0 = {d0, codes0[0..1]}, w1..w3 = codes0[2..13], w4 = {codes0[14..15], d1}, w5..w8 = codes1[0..15].
@@ -381,6 +406,49 @@ __device__ __forceinline__ void router_row_dots(const RouterRow<MAXC, F32>& R, c
     }
 }
 
+// One token against the wave's bf16 row with x read straight into registers (no LDS tile, no barrier): lane l loads
+// the f32 values of its chunks l + 64 j right behind its weight loads, rounds them to bf16 as router_stage does, and
+// forms the same chain and butterfly as router_row_dots for that token, so the logit is the same bits.
+template <int MAXC>
+struct RouterX1 {
+    float4 x[MAXC][2];
+};
+template <int MAXC>
+__device__ __forceinline__ void router_x1_load(const float* __restrict__ xr, int H, RouterX1<MAXC>& X) {
+    const int lane = threadIdx.x & 63, chunks = H >> 3;
+#pragma unroll
+    for (int j = 0; j < MAXC; ++j) {  // clamped: every load issues back to back
+        const int c = min(lane + 64 * j, chunks - 1);
+        X.x[j][0] = reinterpret_cast<const float4*>(xr)[2 * c];
+        X.x[j][1] = reinterpret_cast<const float4*>(xr)[2 * c + 1];
+    }
+}
+template <int MAXC, class Store>
+__device__ __forceinline__ void router_row_dot1(const RouterRow<MAXC, false>& R, const RouterX1<MAXC>& X, int H, int E,
+                                                int rows_total, bool has_bias, Store store) {
+    const int lane = threadIdx.x & 63;
+    const int chunks = H >> 3;
+    if (R.row >= rows_total) return;
+    float acc[1] = {0.0f};
+#pragma unroll
+    for (int j = 0; j < MAXC; ++j) {
+        const int c = lane + 64 * j;
+        if (c < chunks) {
+            const uint32_t wq[4] = {R.wv[j].x, R.wv[j].y, R.wv[j].z, R.wv[j].w};
+            const float4 a = X.x[j][0], b = X.x[j][1];
+            const uint32_t xq[4] = {f32_to_bf16(a.x) | (f32_to_bf16(a.y) << 16), f32_to_bf16(a.z) | (f32_to_bf16(a.w) << 16),
+                                    f32_to_bf16(b.x) | (f32_to_bf16(b.y) << 16), f32_to_bf16(b.z) | (f32_to_bf16(b.w) << 16)};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                acc[0] = __builtin_fmaf(u2f(xq[q] << 16), u2f(wq[q] << 16), acc[0]);
+                acc[0] = __builtin_fmaf(u2f(xq[q] & 0xFFFF0000u), u2f(wq[q] & 0xFFFF0000u), acc[0]);
+            }
+        }
+    }
+    wave_sum_xor_fast_n<1>(acc);
+    if (lane == 0) store(R.row, 0, (has_bias && R.row < E) ? acc[0] + R.bv : acc[0]);
+}
+
 template <int MAXC, bool F32>
 // (The arguments a work-group reads before its first loads come first: the library is built with kernel-argument
 // preloading, so the first 14 dwords arrive in SGPRs with the wave instead of by a scalar load from memory.)
@@ -395,6 +463,7 @@ __global__ __launch_bounds__(256) void k_router(int H, int E, int rows_total, in
     __shared__ uint8_t qsc[8][32];
     __shared__ float inv_s[16];
     __shared__ float wsum_s[4][4];
+    SMOE_STAMP(0, 2);
     const int t0 = blockIdx.y * tok_tile;
     const int nt = min(tok_tile, T - t0);
     const int row_blocks = (rows_total + 3) / 4;
@@ -413,6 +482,10 @@ __global__ __launch_bounds__(256) void k_router(int H, int E, int rows_total, in
     // a row block: the wave's weight row (clamped, every load issued), in flight during the staging below
     RouterRow<MAXC, F32> R;
     if (!img_block) router_row_load<MAXC, F32>(W, w_inp, bias, H, E, rows_total, blockIdx.x, R);
+    // one token of f32 x without the junction (decode at batch 1): x straight into registers, no LDS tile
+    const bool x1 = !F32 && nt == 1 && xf != nullptr && rprev == nullptr;  // uniform
+    RouterX1<MAXC> X1;
+    if (x1 && !img_block) router_x1_load<MAXC>(xf + (size_t)t0 * H, H, X1);
     // the exchange words of the kernel after this one (k_q2_moe_small), cleared: no launch reads them before it
     for (int i = ((int)blockIdx.y * (int)gridDim.x + (int)blockIdx.x) * 256 + (int)threadIdx.x; i < clear_n16;
          i += (int)(gridDim.x * gridDim.y) * 256)
@@ -428,12 +501,23 @@ __global__ __launch_bounds__(256) void k_router(int H, int E, int rows_total, in
         q8_image_store(v, live, qsc[hw], ximg + blk * kImgDw, img_natural != 0);
         return;
     }
-    if (!rprev) router_stage<F32>(xf, xb, t0, nt, H, smem);  // (F32: xf is given)
-    __syncthreads();
-    router_row_dots<MAXC, F32>(R, smem, H, E, rows_total, nt, bias != nullptr, [&](int row, int t, float v) {
+    auto store = [&](int row, int t, float v) {
         if (row < E) logits[(size_t)(t0 + t) * ld_logits + row] = v;
         else sg[t0 + t] = v;
-    });
+    };
+    if constexpr (!F32) {
+        if (x1) {
+            SMOE_STAMP(0, 3);
+            router_row_dot1<MAXC>(R, X1, H, E, rows_total, bias != nullptr, store);
+            SMOE_STAMP(0, 10);
+            return;
+        }
+    }
+    if (!rprev) router_stage<F32>(xf, xb, t0, nt, H, smem);  // (F32: xf is given)
+    __syncthreads();
+    SMOE_STAMP(0, 3);
+    router_row_dots<MAXC, F32>(R, smem, H, E, rows_total, nt, bias != nullptr, store);
+    SMOE_STAMP(0, 10);
 }
 
 
@@ -654,6 +738,7 @@ __device__ __forceinline__ FastRoute route_fast_t(const float* __restrict__ l, i
         m = max(m, key[j]);
         mx = __builtin_fmaxf(mx, v);
     }
+    SMOE_STAMP_AFTER(1, 13, m);  // the logits are in registers
     // theta = the k-th largest lane maximum: at least k keys reach it, and every key above the k-th largest does
     const uint32_t th = (uint32_t)__builtin_amdgcn_readlane((int)wave_sort_desc_u32(m), k - 1);
     unsigned long long bj[J];
@@ -1374,6 +1459,7 @@ __device__ __forceinline__ void gu_compute(const Item& item, int hb, uint32_t* s
     const int qb = H >> 5;
     float dw[NIT][MAXUPL][2];
     unit_scales(w, dw);
+    SMOE_STAMP(1, 7);  // the weights are in registers
 
     for (int c0 = 0; c0 < item.ncol; c0 += kGuCols) {
         const int nc = min(kGuCols, item.ncol - c0);
@@ -1514,6 +1600,7 @@ __device__ __forceinline__ bool gu_route_item(int y, GuRouteLds& L, const float*
         __shared__ uint2 s_cand1[4][64];
         const FastRoute R = E <= 512 ? route_fast_t<8, false>(lg, E, k, s_cand1[wave])
                                      : route_fast_t<16, false>(lg, E, k, s_cand1[wave]);
+        SMOE_STAMP(1, 14);
         if (R.ok) {  // uniform over the work-group
             const bool sel = R.crank < k;
             const unsigned long long sm = __ballot(sel);
@@ -1644,6 +1731,7 @@ __device__ __forceinline__ bool gu_route_wg(
     }
     const bool shared_wg = y < n_sh;
     if (hb * 32 >= (shared_wg ? Fs : F)) return false;
+    SMOE_STAMP_VAL(1, 0, shared_wg ? 1 : 2);  // role: gate/up of the shared expert (1) or of a routed one (2)
     const int qb = H >> 5;
     const int pieces = T * qb * (kImgDw / 4);  // at most 4 * 128 * 3
     const int npre = (pieces + 255) >> 8;      // uniform
@@ -1664,10 +1752,15 @@ __device__ __forceinline__ bool gu_route_wg(
                 if (j * 256 + tid < pieces) reinterpret_cast<u32x4*>(smem)[lds_piece(j * 256 + tid)] = pre[j];
         },
         synced);
-    if (!has) return false;
+    SMOE_STAMP(1, 6);  // the item is known
+    if (!has) {
+        SMOE_STAMP_VAL(1, 0, 9);  // role: no expert for this item
+        return false;
+    }
     // (unsynchronised routing: the weight loads go out first, then the barrier that publishes the images)
     q2_gu_item<NIT, MAXUPL, true>(item, hb, smem, gate_exps, up_exps, gate_sh, up_sh, ximg, nullptr, k, H, F, himg,
                                   h_blocks, xchg, {}, 0, !synced);
+    SMOE_STAMP(1, 10);
     return true;
 }
 
@@ -1864,6 +1957,7 @@ __device__ __forceinline__ void down_combine_tasks(const uint8_t* __restrict__ d
         float v0[NT];
 #pragma unroll
         for (int q = 0; q < NT; ++q) v0[q] = row_value(q, 0);
+        if (tb == 0) SMOE_STAMP(1, 11);  // the first row values are formed
 #pragma unroll
         for (int q = 0; q < NT; ++q) {
             if (!live[q]) continue;  // wave-uniform
@@ -1881,6 +1975,7 @@ __device__ __forceinline__ void down_combine_tasks(const uint8_t* __restrict__ d
         }
     }
     __syncthreads();
+    SMOE_STAMP(1, 12);  // every task's row values are parked
     if (tid < T * kDcRows) {
         const int t = tid / kDcRows, rl = tid - t * kDcRows;
         if (r0 + rl < H) {
@@ -1991,6 +2086,7 @@ __device__ __forceinline__ void down_wg(int r0, uint32_t* smem, const float* lg,
         }
     }
     if (tid < T) s_sg[tid] = sgv[tid];
+    SMOE_STAMP(1, 4);
     // one token: wave 0 routes it with weights; candidate c (ascending id), selected at rank r, is the token's pair r
     // and the y-th touched expert (y = selected candidates below c), so its dispatch position is y
     const bool one = T == 1 && k <= 64;
@@ -1999,6 +2095,7 @@ __device__ __forceinline__ void down_wg(int r0, uint32_t* smem, const float* lg,
             __shared__ uint2 s_cand1[64];
             const FastRoute R = E <= 512 ? route_fast_t<8, true>(lg, E, k, s_cand1)
                                          : route_fast_t<16, true>(lg, E, k, s_cand1);
+            SMOE_STAMP(1, 14);
             if (R.ok) {
                 const bool sel = R.crank < k;
                 const unsigned long long sm = __ballot(sel);
@@ -2071,6 +2168,7 @@ __device__ __forceinline__ void down_wg(int r0, uint32_t* smem, const float* lg,
         if (tid == 0) s_nt = R.n_touched;
     }
     __syncthreads();
+    SMOE_STAMP(1, 6);  // the items are known
     const int n_items = n_sh + s_nt;
     auto wait_h = [&] {
         // every image word of the batch's h rows, eight per thread at a time: all loads in flight together (they
@@ -2113,8 +2211,10 @@ __device__ __forceinline__ void down_wg(int r0, uint32_t* smem, const float* lg,
                 if (need[j]) smem[(size_t)lds_blk(blk) + wd] = (uint32_t)v[j];
             }
         }
+        SMOE_STAMP(1, 8);  // this thread's h words arrived
         if (!ok) s_bad = 1;
         __syncthreads();
+        SMOE_STAMP(1, 9);  // every h word arrived
     };
     down_combine_tasks<DMAXUPL, DNT>(down_exps, down_sh, smem, Ys, s_items, s_slot, s_wts, n_items, npass, r0, H, F,
                                      Fs, s_sg, T, k, add_shared, h_blocks, y, wait_h);
@@ -2124,6 +2224,7 @@ __device__ __forceinline__ void down_wg(int r0, uint32_t* smem, const float* lg,
         if (r0 + rl < H) y[(size_t)t * H + r0 + rl] = __builtin_nanf("");
     }
     if (status && tid == 0) status[r0 / kDcRows] = s_bad;
+    SMOE_STAMP(1, 10);
 }
 
 template <int NIT, int MAXUPL, int DMAXUPL, int DNT>
@@ -2142,6 +2243,16 @@ __global__ __launch_bounds__(256) void k_q2_moe_small(
     const int hbn = h_blocks;  // rows blocks of the widest expert
     const int n_gu = max_items * hbn + 1;
     const int id = blockIdx.x;
+    SMOE_STAMP(1, 2);
+#if defined(SMOE_STAMPS)
+    {
+        uint32_t xcc;
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+        SMOE_STAMP_VAL(1, 1, xcc);  // the XCD
+    }
+    if (id >= n_gu) SMOE_STAMP_VAL(1, 0, 4);  // role: down
+    else if (id / hbn == max_items) SMOE_STAMP_VAL(1, 0, 3);  // role: the writer
+#endif
     if (id < n_gu) {  // gate/up (or the writer)
         const int yi = id / hbn, hb = id - yi * hbn;
         gu_route_wg<NIT, MAXUPL>(yi, hb, smem, gate_exps, up_exps, gate_sh, up_sh, ximg, logits, T, E, k, H, F, Fs,
@@ -2764,3 +2875,10 @@ hipError_t launch_q2_mmvq(const uint8_t* w, const uint8_t* xq, int n_in, int n_o
 }
 
 }  // namespace smoe
+
+#if defined(SMOE_STAMPS)
+// The stamp buffer of the timeline build (device memory of 2 x 4096 x 32 u64, or NULL to stop stamping).
+extern "C" int smoe_debug_set_stamps(void* p) {
+    return (int)hipMemcpyToSymbol(HIP_SYMBOL(smoe::g_stamp), &p, sizeof(p));
+}
+#endif
