@@ -24,7 +24,7 @@ from . import build as B
 LIB_STAMPS = os.path.join(B.LIBDIR, "libsmoe_stamps.so")
 ROLES = {0: "router", 1: "gate/up (shared)", 2: "gate/up (routed)", 9: "gate/up (no expert)", 3: "writer",
          4: "down"}
-PHASES = [(2, "start"), (3, "x staged"), (4, "sg loaded"), (13, "logits in registers"), (14, "routed"),
+PHASES = [(2, "start"), (3, "dots begin"), (4, "sg loaded"), (13, "logits in registers"), (14, "routed"),
           (6, "item known"), (7, "weights in registers"), (8, "h words polled"), (9, "h seen"),
           (11, "first rows formed"), (12, "rows parked"), (10, "end")]
 
