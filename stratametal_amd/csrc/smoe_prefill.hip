@@ -441,13 +441,25 @@ __device__ __forceinline__ float silu_mul_fast(float g, float u) {
     return (g * __builtin_amdgcn_rcpf(1.0f + e)) * u;
 }
 
+// The expert GEMMs' 1-D grids: work-group id -> (work item y, row block rb).  The dispatcher deals linear ids round
+// robin over the 8 XCDs, so the n_rb row blocks of item y are given the ids 8 (n_rb (y / 8) + rb) + y % 8: one XCD,
+// dispatched back to back, reading the item's activation records from memory once and then from that XCD's L2 (a 2-D
+// grid of (row block, item) put each row block of an item on another XCD).  The grid holds n_rb * (max_items rounded
+// up to 8) work-groups; false past max_items.
+__device__ __forceinline__ bool xcd_item(int n_rb, int max_items, int& y, int& rb) {
+    const int id = blockIdx.x, xcd = id & 7, slot = id >> 3, g = slot / n_rb;
+    y = 8 * g + xcd;
+    rb = slot - n_rb * g;
+    return y < max_items;
+}
+inline unsigned xcd_grid(int n_rb, int max_items) { return (unsigned)(n_rb * ((max_items + 7) / 8) * 8); }
+
 template <int MODE>
-__device__ __forceinline__ void mm_gu_body(uint8_t* lds, const int* rowidx, const Item& item, int ncol,
+__device__ __forceinline__ void mm_gu_body(uint8_t* lds, const int* rowidx, const Item& item, int ncol, int rt,
                                            const uint8_t* g0, const uint8_t* u0, const uint32_t* xrec,
                                            uint32_t xrec_bytes, int H, uint32_t* hrec, int h_rec, int32_t* flag) {
     using S = Shape<MODE>;
     constexpr int NS = S::NS;
-    const int rt = blockIdx.x;
     const int units = H >> 7;
     const uint32_t rb = (uint32_t)units * 36u;
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, i = lane & 15,
@@ -504,20 +516,22 @@ __device__ __forceinline__ void mm_gu_body(uint8_t* lds, const int* rowidx, cons
 __global__ __launch_bounds__(512) void k_mm_gu(const uint8_t* __restrict__ gate_exps, const uint8_t* __restrict__ up_exps,
                                                const uint8_t* __restrict__ gate_sh, const uint8_t* __restrict__ up_sh,
                                                const uint32_t* __restrict__ xrec, uint32_t xrec_bytes,
-                                               const int4* __restrict__ items, const int32_t* __restrict__ perm, int k,
-                                               int H, int F, int Fs, uint32_t* __restrict__ hrec, int h_rec,
-                                               int32_t* __restrict__ flags) {
+                                               const int4* __restrict__ items, int max_items, int n_rb,
+                                               const int32_t* __restrict__ perm, int k, int H, int F, int Fs,
+                                               uint32_t* __restrict__ hrec, int h_rec, int32_t* __restrict__ flags) {
     __shared__ __align__(16) uint8_t lds[kLds];
     __shared__ int rowidx[kChunk];
+    int y, rt;
+    if (!xcd_item(n_rb, max_items, y, rt)) return;
     // with `flags`, this work-group's word: whether one of its h values is an fp16 overflow (0 when it has no work)
-    int32_t* flag = flags ? flags + (size_t)blockIdx.y * gridDim.x + blockIdx.x : nullptr;
+    int32_t* flag = flags ? flags + (size_t)y * n_rb + rt : nullptr;
     Item item;
-    if (!work_item(items, blockIdx.y, item)) {
+    if (!work_item(items, y, item)) {
         if (flag && threadIdx.x == 0) *flag = 0;
         return;
     }
     const int Fe = item.shared ? Fs : F;
-    if (128 * (int)blockIdx.x >= Fe) {
+    if (128 * rt >= Fe) {
         if (flag && threadIdx.x == 0) *flag = 0;
         return;
     }
@@ -527,10 +541,10 @@ __global__ __launch_bounds__(512) void k_mm_gu(const uint8_t* __restrict__ gate_
     const size_t rb = (size_t)(H >> 7) * 36;
     const uint8_t* g0 = item.shared ? gate_sh : gate_exps + (size_t)item.e * F * rb;
     const uint8_t* u0 = item.shared ? up_sh : up_exps + (size_t)item.e * F * rb;
-    if (ncol > 64) mm_gu_body<kWide>(lds, rowidx, item, ncol, g0, u0, xrec, xrec_bytes, H, hrec, h_rec, flag);
+    if (ncol > 64) mm_gu_body<kWide>(lds, rowidx, item, ncol, rt, g0, u0, xrec, xrec_bytes, H, hrec, h_rec, flag);
     else if (ncol > kThinCols)
-        mm_gu_body<kNarrow>(lds, rowidx, item, ncol, g0, u0, xrec, xrec_bytes, H, hrec, h_rec, flag);
-    else mm_gu_body<kThin>(lds, rowidx, item, ncol, g0, u0, xrec, xrec_bytes, H, hrec, h_rec, flag);
+        mm_gu_body<kNarrow>(lds, rowidx, item, ncol, rt, g0, u0, xrec, xrec_bytes, H, hrec, h_rec, flag);
+    else mm_gu_body<kThin>(lds, rowidx, item, ncol, rt, g0, u0, xrec, xrec_bytes, H, hrec, h_rec, flag);
 }
 
 // ------------------------------------------------------------------------------------------------ down
@@ -539,11 +553,10 @@ __global__ __launch_bounds__(512) void k_mm_gu(const uint8_t* __restrict__ gate_
 // (two sets).
 template <int MODE>
 __device__ __forceinline__ void mm_down_body(uint8_t* lds, const int* rowidx, const Item& item, int ncol, int units,
-                                             const uint8_t* d0, const uint32_t* hrec, uint32_t hrec_bytes, int h_rec,
-                                             const float* sg, int H, float* Y) {
+                                             int rt, const uint8_t* d0, const uint32_t* hrec, uint32_t hrec_bytes,
+                                             int h_rec, const float* sg, int H, float* Y) {
     using S = Shape<MODE>;
     constexpr int NS = S::NS;
-    const int rt = blockIdx.x;
     const uint32_t rb = (uint32_t)units * 36u;
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, i = lane & 15,
               q = lane >> 4;
@@ -584,12 +597,15 @@ __device__ __forceinline__ void mm_down_body(uint8_t* lds, const int* rowidx, co
 
 __global__ __launch_bounds__(512) void k_mm_down(const uint8_t* __restrict__ down_exps, const uint8_t* __restrict__ down_sh,
                                                  const uint32_t* __restrict__ hrec, uint32_t hrec_bytes, int h_rec,
-                                                 const float* __restrict__ sg, const int4* __restrict__ items, int H,
-                                                 int F, int Fs, float* __restrict__ Y) {
+                                                 const float* __restrict__ sg, const int4* __restrict__ items,
+                                                 int max_items, int n_rb, int H, int F, int Fs,
+                                                 float* __restrict__ Y) {
     __shared__ __align__(16) uint8_t lds[kLds];
     __shared__ int rowidx[kChunk];
+    int y, rt;
+    if (!xcd_item(n_rb, max_items, y, rt)) return;
     Item item;
-    if (!work_item(items, blockIdx.y, item)) return;
+    if (!work_item(items, y, item)) return;
     const int Fe = item.shared ? Fs : F;
     const int ncol = item.ncol;
     if (ncol <= kThinCols) return;  // k_mm_down_thin's
@@ -597,8 +613,8 @@ __global__ __launch_bounds__(512) void k_mm_down(const uint8_t* __restrict__ dow
     __syncthreads();
     const int units = Fe >> 7;
     const uint8_t* d0 = item.shared ? down_sh : down_exps + (size_t)item.e * H * ((size_t)(F >> 7) * 36);
-    if (ncol > 64) mm_down_body<kWide>(lds, rowidx, item, ncol, units, d0, hrec, hrec_bytes, h_rec, sg, H, Y);
-    else mm_down_body<kNarrow>(lds, rowidx, item, ncol, units, d0, hrec, hrec_bytes, h_rec, sg, H, Y);
+    if (ncol > 64) mm_down_body<kWide>(lds, rowidx, item, ncol, units, rt, d0, hrec, hrec_bytes, h_rec, sg, H, Y);
+    else mm_down_body<kNarrow>(lds, rowidx, item, ncol, units, rt, d0, hrec, hrec_bytes, h_rec, sg, H, Y);
 }
 
 // The thin items (<= kThinCols columns) on k_mm_down's grid, launched after it: one-stage ring (55 KB of LDS), two
@@ -608,18 +624,21 @@ __global__ __launch_bounds__(512) void k_mm_down_thin(const uint8_t* __restrict_
                                                       const uint8_t* __restrict__ down_sh,
                                                       const uint32_t* __restrict__ hrec, uint32_t hrec_bytes, int h_rec,
                                                       const float* __restrict__ sg, const int4* __restrict__ items,
-                                                      int H, int F, int Fs, float* __restrict__ Y) {
+                                                      int max_items, int n_rb, int H, int F, int Fs,
+                                                      float* __restrict__ Y) {
     __shared__ __align__(16) uint8_t lds[Shape<kThin1>::kLdsBytes];
     __shared__ int rowidx[kThinCols];
+    int y, rt;
+    if (!xcd_item(n_rb, max_items, y, rt)) return;
     Item item;
-    if (!work_item(items, blockIdx.y, item) || item.ncol > kThinCols) return;
+    if (!work_item(items, y, item) || item.ncol > kThinCols) return;
     const int Fe = item.shared ? Fs : F;
     const int ncol = item.ncol;
     if ((int)threadIdx.x < ncol) rowidx[threadIdx.x] = item.first + threadIdx.x;
     __syncthreads();
     const int units = Fe >> 7;
     const uint8_t* d0 = item.shared ? down_sh : down_exps + (size_t)item.e * H * ((size_t)(F >> 7) * 36);
-    mm_down_body<kThin1>(lds, rowidx, item, ncol, units, d0, hrec, hrec_bytes, h_rec, sg, H, Y);
+    mm_down_body<kThin1>(lds, rowidx, item, ncol, units, rt, d0, hrec, hrec_bytes, h_rec, sg, H, Y);
 }
 
 // ------------------------------------------------------------------------------------------------ launchers
@@ -777,8 +796,9 @@ hipError_t launch_mm_gu(const uint8_t* gate_exps, const uint8_t* up_exps, const 
     const int Fmax = has_shared && Fs > F ? Fs : F;
     const size_t bytes = act_rec_bytes(n_xrec);
     if (bytes >= kOob) return hipErrorInvalidValue;  // buffer offsets are 31-bit
-    hipLaunchKernelGGL(k_mm_gu, dim3((unsigned)(Fmax / 128), (unsigned)max_items), dim3(512), 0, s, gate_exps, up_exps,
-                       gate_sh, up_sh, xrec, (uint32_t)bytes, items, perm, k, H, F, Fs, hrec, h_rec, flags);
+    const int n_rb = Fmax / 128;
+    hipLaunchKernelGGL(k_mm_gu, dim3(xcd_grid(n_rb, max_items)), dim3(512), 0, s, gate_exps, up_exps, gate_sh, up_sh,
+                       xrec, (uint32_t)bytes, items, max_items, n_rb, perm, k, H, F, Fs, hrec, h_rec, flags);
     return hipGetLastError();
 }
 
@@ -822,11 +842,12 @@ hipError_t launch_mm_down(const uint8_t* down_exps, const uint8_t* down_sh, cons
     const size_t bytes = act_rec_bytes(n_hrec);
     if (bytes >= kOob) return hipErrorInvalidValue;
     // the thin items after the others: their kernel's smaller LDS lets two work-groups share a CU
-    const dim3 grid((unsigned)((H + kWgRows - 1) / kWgRows), (unsigned)max_items);
-    hipLaunchKernelGGL(k_mm_down, grid, dim3(512), 0, s, down_exps, down_sh, hrec, (uint32_t)bytes, h_rec, sg, items, H,
-                       F, Fs, Y);
+    const int n_rb = (H + kWgRows - 1) / kWgRows;
+    const dim3 grid(xcd_grid(n_rb, max_items));
+    hipLaunchKernelGGL(k_mm_down, grid, dim3(512), 0, s, down_exps, down_sh, hrec, (uint32_t)bytes, h_rec, sg, items,
+                       max_items, n_rb, H, F, Fs, Y);
     hipLaunchKernelGGL(k_mm_down_thin, grid, dim3(512), 0, s, down_exps, down_sh, hrec, (uint32_t)bytes, h_rec, sg,
-                       items, H, F, Fs, Y);
+                       items, max_items, n_rb, H, F, Fs, Y);
     return hipGetLastError();
 }
 
