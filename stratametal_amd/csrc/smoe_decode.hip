@@ -472,7 +472,7 @@ __global__ __launch_bounds__(256) void k_router(int H, int E, int rows_total, in
     // an image block: eight q8_1 blocks of the tile's x, one per half wave; its values are loaded first
     const int hw = tid >> 5;
     const int bb = ((int)blockIdx.x - row_blocks) * 8 + hw;
-    const bool live = img_block && bb < nt * (H >> 5);
+    const bool live = img_block && ximg != nullptr && bb < nt * (H >> 5);  // (the grid may pad past the image blocks)
     const size_t blk = (size_t)t0 * (H >> 5) + (live ? bb : 0);
     float iv = 0.0f, ir = 0.0f;
     if (img_block) {
@@ -2529,6 +2529,13 @@ hipError_t launch_prep(const float* x, int64_t n, uint8_t* xq, uint16_t* xb, hip
     return hipGetLastError();
 }
 
+// The router grid's x extent: with several token tiles, rounded up to a multiple of 8, so that the token tiles of a
+// row block (linear ids x + g * grid.x) are dealt to one XCD and its weight rows come from that XCD's L2 after the
+// first tile (the padding blocks are image blocks past the images: they do nothing).
+static unsigned router_grid_x(int blocks, int T, int tile) {
+    return (unsigned)(T > tile ? (blocks + 7) / 8 * 8 : blocks);
+}
+
 hipError_t launch_router(const float* xf, const uint16_t* xb, const void* W, const uint16_t* w_inp,
                          const float* bias, int H, int E, int rows_total, int T, float* logits, int ld_logits, float* sg,
                          uint32_t* ximg, int tile_rows, int img_natural, hipStream_t s, const float* rprev, float eps,
@@ -2545,7 +2552,7 @@ hipError_t launch_router(const float* xf, const uint16_t* xb, const void* W, con
         if (tile > T) tile = T;
         if (tile < 1) tile = 1;
         const int img_blocks = ximg ? (tile * (H / 32) + 7) / 8 : 0;
-        dim3 grid((unsigned)((rows_total + 3) / 4 + img_blocks), (unsigned)((T + tile - 1) / tile));
+        dim3 grid(router_grid_x((rows_total + 3) / 4 + img_blocks, T, tile), (unsigned)((T + tile - 1) / tile));
         const size_t lds = (size_t)tile * H * 4;
 #define SMOE_ROUTER_F32(C)                                                                                          \
     hipLaunchKernelGGL((k_router<C, true>), grid, dim3(256), lds, s, H, E, rows_total, T, tile, clear_n16, W, w_inp, \
@@ -2569,7 +2576,7 @@ hipError_t launch_router(const float* xf, const uint16_t* xb, const void* W, con
     if (tile < 1) tile = 1;
     // row blocks (4 weight rows each), then with ximg the image blocks (8 q8_1 blocks of the tile each)
     const int img_blocks = ximg ? (tile * (H / 32) + 7) / 8 : 0;
-    dim3 grid((unsigned)((rows_total + 3) / 4 + img_blocks), (unsigned)((T + tile - 1) / tile));
+    dim3 grid(router_grid_x((rows_total + 3) / 4 + img_blocks, T, tile), (unsigned)((T + tile - 1) / tile));
     const size_t lds = (size_t)tile * H * 2;
 #define SMOE_ROUTER(C)                                                                                          \
     hipLaunchKernelGGL((k_router<C, false>), grid, dim3(256), lds, s, H, E, rows_total, T, tile, clear_n16, W, w_inp, \
