@@ -1955,8 +1955,26 @@ __device__ __forceinline__ void down_combine_tasks(const uint8_t* __restrict__ d
         // the first column of every task at once, with no branch between them (a dead task works on item 0's first
         // column and stores nothing), so that the tasks' LDS reads and dots overlap; further columns task by task
         float v0[NT];
+        if constexpr (MAXUPL == 1) {
+            // one unit per lane: every task's two image halves are read from LDS before any dot, so the tasks share
+            // one LDS round trip instead of two each (row_value's arithmetic, in its order)
+            Act2 a0[NT], a1[NT];
 #pragma unroll
-        for (int q = 0; q < NT; ++q) v0[q] = row_value(q, 0);
+            for (int q = 0; q < NT; ++q) {
+                const int l = lane & (lpr[q] - 1);
+                const uint32_t* im = img + (size_t)it[q].first * h_blocks * kImgLdsDw + (size_t)l * kUnitLdsDw;
+                load_act_img2(im, a0[q]);
+                load_act_img2(im + 2 * kImgDw, a1[q]);
+            }
+#pragma unroll
+            for (int q = 0; q < NT; ++q) {
+                const float p01 = q2_unit_first(w[q][0], dw[q][0][0], a0[q]);
+                v0[q] = group_sum_sel(q2_unit_second(w[q][0], dw[q][0][1], p01, a1[q]), lpr[q]);
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < NT; ++q) v0[q] = row_value(q, 0);
+        }
         if (tb == 0) SMOE_STAMP(1, 11);  // the first row values are formed
 #pragma unroll
         for (int q = 0; q < NT; ++q) {
