@@ -1476,14 +1476,15 @@ __device__ __forceinline__ void gu_compute(const Item& item, int hb, uint32_t* s
                 if (m < G.upl) {
                     const uint32_t* img = xt + (size_t)(l + G.lpr * m) * kUnitLdsDw;
                     float p01[NIT];
-                    Act2 a;
+                    // both image halves before the dots (one LDS round trip)
+                    Act2 a, b;
                     load_act_img2(img, a);
+                    load_act_img2(img + 2 * kImgDw, b);
 #pragma unroll
                     for (int it = 0; it < NIT; ++it) p01[it] = q2_unit_first(w[it][m], dw[it][m][0], a);
-                    load_act_img2(img + 2 * kImgDw, a);
 #pragma unroll
                     for (int it = 0; it < NIT; ++it) {
-                        const float L = q2_unit_second(w[it][m], dw[it][m][1], p01[it], a);
+                        const float L = q2_unit_second(w[it][m], dw[it][m][1], p01[it], b);
                         acc[it] = m == 0 ? L : acc[it] + L;
                     }
                 }
