@@ -449,6 +449,69 @@ __device__ __forceinline__ void router_row_dot1(const RouterRow<MAXC, false>& R,
     if (lane == 0) store(R.row, 0, (has_bias && R.row < E) ? acc[0] + R.bv : acc[0]);
 }
 
+// The same for the f32 router (RouterRow<MAXC, true>): an f32 row's lane takes the 4-value chunks l + 64 j (x[j]), the
+// shared gate row (bf16) the 8-value chunks l + 64 j (x[2 j], x[2 j + 1], rounded to bf16), as router_row_dots
+// forms them for one token.
+template <int MAXC>
+struct RouterX1F {
+    float4 x[MAXC];
+};
+template <int MAXC>
+__device__ __forceinline__ void router_x1f_load(const float* __restrict__ xr, int H, bool frow, RouterX1F<MAXC>& X) {
+    const int lane = threadIdx.x & 63;
+    if (frow) {  // wave-uniform
+        const int chunks = H >> 2;
+#pragma unroll
+        for (int j = 0; j < MAXC; ++j) X.x[j] = reinterpret_cast<const float4*>(xr)[min(lane + 64 * j, chunks - 1)];
+    } else {
+        const int chunks = H >> 3;
+#pragma unroll
+        for (int j = 0; j < MAXC / 2; ++j) {
+            const int c = min(lane + 64 * j, chunks - 1);
+            X.x[2 * j] = reinterpret_cast<const float4*>(xr)[2 * c];
+            X.x[2 * j + 1] = reinterpret_cast<const float4*>(xr)[2 * c + 1];
+        }
+    }
+}
+template <int MAXC, class Store>
+__device__ __forceinline__ void router_row_dot1f(const RouterRow<MAXC, true>& R, const RouterX1F<MAXC>& X, int H, int E,
+                                                 int rows_total, bool has_bias, Store store) {
+    const int lane = threadIdx.x & 63;
+    if (R.row >= rows_total) return;
+    float acc[1] = {0.0f};
+    if (R.frow) {
+#pragma unroll
+        for (int j = 0; j < MAXC; ++j) {
+            if (lane + 64 * j < R.wchunks) {
+                const float4 xv = X.x[j];
+                acc[0] = __builtin_fmaf(xv.x, u2f(R.wv[j].x), acc[0]);
+                acc[0] = __builtin_fmaf(xv.y, u2f(R.wv[j].y), acc[0]);
+                acc[0] = __builtin_fmaf(xv.z, u2f(R.wv[j].z), acc[0]);
+                acc[0] = __builtin_fmaf(xv.w, u2f(R.wv[j].w), acc[0]);
+            }
+        }
+    } else {
+        const int chunks = H >> 3;
+#pragma unroll
+        for (int j = 0; j < MAXC / 2; ++j) {
+            if (lane + 64 * j < chunks) {
+                const uint32_t wq[4] = {R.wv[j].x, R.wv[j].y, R.wv[j].z, R.wv[j].w};
+                const float4 a = X.x[2 * j], b = X.x[2 * j + 1];
+                const float xv8[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const float x0 = u2f(f32_to_bf16(xv8[2 * q]) << 16);
+                    const float x1 = u2f(f32_to_bf16(xv8[2 * q + 1]) << 16);
+                    acc[0] = __builtin_fmaf(x0, u2f(wq[q] << 16), acc[0]);
+                    acc[0] = __builtin_fmaf(x1, u2f(wq[q] & 0xFFFF0000u), acc[0]);
+                }
+            }
+        }
+    }
+    wave_sum_xor_fast_n<1>(acc);
+    if (lane == 0) store(R.row, 0, (has_bias && R.row < E) ? acc[0] + R.bv : acc[0]);
+}
+
 template <int MAXC, bool F32>
 // (The arguments a work-group reads before its first loads come first: the library is built with kernel-argument
 // preloading, so the first 14 dwords arrive in SGPRs with the wave instead of by a scalar load from memory.)
@@ -483,9 +546,14 @@ __global__ __launch_bounds__(256) void k_router(int H, int E, int rows_total, in
     RouterRow<MAXC, F32> R;
     if (!img_block) router_row_load<MAXC, F32>(W, w_inp, bias, H, E, rows_total, blockIdx.x, R);
     // one token of f32 x without the junction (decode at batch 1): x straight into registers, no LDS tile
-    const bool x1 = !F32 && nt == 1 && xf != nullptr && rprev == nullptr;  // uniform
+    const bool x1 = nt == 1 && xf != nullptr && rprev == nullptr;  // uniform
     RouterX1<MAXC> X1;
-    if (x1 && !img_block) router_x1_load<MAXC>(xf + (size_t)t0 * H, H, X1);
+    RouterX1F<MAXC> X1F;
+    if constexpr (F32) {
+        if (x1 && !img_block) router_x1f_load<MAXC>(xf + (size_t)t0 * H, H, R.frow, X1F);
+    } else {
+        if (x1 && !img_block) router_x1_load<MAXC>(xf + (size_t)t0 * H, H, X1);
+    }
     // the exchange words of the kernel after this one (k_q2_moe_small), cleared: no launch reads them before it
     for (int i = ((int)blockIdx.y * (int)gridDim.x + (int)blockIdx.x) * 256 + (int)threadIdx.x; i < clear_n16;
          i += (int)(gridDim.x * gridDim.y) * 256)
@@ -505,13 +573,12 @@ __global__ __launch_bounds__(256) void k_router(int H, int E, int rows_total, in
         if (row < E) logits[(size_t)(t0 + t) * ld_logits + row] = v;
         else sg[t0 + t] = v;
     };
-    if constexpr (!F32) {
-        if (x1) {
-            SMOE_STAMP(0, 3);
-            router_row_dot1<MAXC>(R, X1, H, E, rows_total, bias != nullptr, store);
-            SMOE_STAMP(0, 10);
-            return;
-        }
+    if (x1) {
+        SMOE_STAMP(0, 3);
+        if constexpr (F32) router_row_dot1f<MAXC>(R, X1F, H, E, rows_total, bias != nullptr, store);
+        else router_row_dot1<MAXC>(R, X1, H, E, rows_total, bias != nullptr, store);
+        SMOE_STAMP(0, 10);
+        return;
     }
     if (!rprev) router_stage<F32>(xf, xb, t0, nt, H, smem);  // (F32: xf is given)
     __syncthreads();
