@@ -327,6 +327,27 @@ def test_forward_decode_parity(torch, case):
     assert np.array_equal(bits(host(torch, y2)), bits(y))
 
 
+@pytest.mark.parametrize("router_dtype,T", [(0, 1), (1, 1), (0, 3), (1, 2)])
+def test_forward_decode_with_logit_bias(torch, router_dtype, T):
+    """A router logit bias (the Zipf-biased routing of the prefill benchmark) at one token, where the router reads x
+    straight into registers (bf16 and f32 routers), and in the fused small batch: bitwise the oracle's device order,
+    and the routing is the biased one (the bias moves the selection)."""
+    say(f"case: logit bias, router_dtype={router_dtype} T={T}")
+    g = O.Geom(router_dtype=router_dtype, n_expert=64)
+    bias = S.zipf_bias(g.n_expert, 1.2, 7, n_tokens=16, top_k=g.top_k, n_embd=g.n_embd, w_sigma=0.02)
+    w_host, w_dev = layer(torch, g, 61 + router_dtype, bias=bias)
+    x = O.gen_normal(62, 100, T * g.n_embd).reshape(T, g.n_embd)
+    ml = S.MoELayer(S.Geom(**vars(g)), w_dev, max_tokens=T)
+    y, tr = ml.forward(dev(torch, x), add_shared=True, trace=True)
+    want, wtr = O.moe_decode_dev(g, w_host, x, add_shared=True, trace=True, n_threads=8)
+    for k in ("logits", "ids", "weights"):
+        assert np.array_equal(bits(host(torch, tr[k])), bits(wtr[k])), k
+    assert np.array_equal(bits(host(torch, y)), bits(want))
+    unbiased = O.moe_decode_dev(g, O.make_weights(g, 61 + router_dtype), x, add_shared=True, trace=True,
+                                n_threads=8)[1]
+    assert not np.array_equal(unbiased["ids"], wtr["ids"]), "the bias must change the selection"
+
+
 STAGE_CASES = [
     # name, geometry, T, seed, add_shared: the expert stages of the trace (FfnTrace's exq, ehq, edown, shared)
     ("stages, config 1 (decode b=1)", {}, 1, 51, True),
