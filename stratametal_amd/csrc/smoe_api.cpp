@@ -60,6 +60,9 @@ constexpr int kDispatchMultiPairs = 2048;
 constexpr int kMfmaTokens = 128;
 // The MFMA kernels' buffer offsets into the activation and h records are 31-bit.
 constexpr size_t kMfmaRecordLimit = (size_t)1 << 31;
+// The prefill path's Y (f32 per-pair rows) from this size on is stored and read with streaming accesses (half the
+// 256 MB Infinity Cache).
+constexpr size_t kYStreamBytes = (size_t)128 << 20;
 
 smoe_status check_geom(const smoe_geom* g) {
     if (!g) return fail(SMOE_ENULL, "geometry is NULL");
@@ -424,6 +427,11 @@ smoe_status forward_impl(const smoe_geom* g, const smoe_weights* w, float* x_io,
     const hipStream_t st = stream_of(hip_stream);
     const int n_items = mfma ? max_items_mfma(*g, T) : max_items_gemv(*g, T);
     const int chunk = mfma ? smoe::mfma_chunk() : (1 << 30);
+    // the prefill path's per-pair rows Y past kYStreamBytes: the down kernels store them and the combine reads them
+    // (and writes y) with streaming accesses, which keep them out of the XCDs' L2 (measured at 4096 tokens of the
+    // benchmark's layer, 369 MB of Y: 50 us less per layer; at 512 tokens, 46 MB, the combine reads Y back from the
+    // Infinity Cache and the streaming loads cost it 1.5 us)
+    const bool y_stream = mfma && (size_t)(P + T) * (size_t)H * sizeof(float) > kYStreamBytes;
     const int sh_chunk = mfma ? smoe::mfma_chunk() : smoe::gemv_shared_chunk();
 
     void* const* ev = trace ? trace->stage_events : nullptr;
@@ -515,7 +523,7 @@ smoe_status forward_impl(const smoe_geom* g, const smoe_weights* w, float* x_io,
                  "gate/up");
         SMOE_MARK();
         SMOE_TRY(smoe::launch_mm_down(de, ds, himg, (int64_t)(P + T) * L.h_rec, L.h_rec, sg, items, H, F, Fs, n_items,
-                                      Y, st),
+                                      Y, y_stream ? 1 : 0, st),
                  "down");
     } else if (iq2) {
         SMOE_TRY(smoe::launch_iq2_gu(ge, ue, gs, us, ximg, items, perm, K, H, F, Fs, shf ? 1 : 0, n_items, himg,
@@ -550,7 +558,9 @@ smoe_status forward_impl(const smoe_geom* g, const smoe_weights* w, float* x_io,
     SMOE_MARK();
     if (nat) SMOE_TRY_S(native_shared(*g, w, x_io, T, ws, L, Y + (size_t)P * H, sg, st));
     if (!small_down)
-        SMOE_TRY(smoe::launch_combine(Y, slot, wts, K, H, P, T, (has_sh && add_shared) ? 1 : 0, y, st), "combine");
+        SMOE_TRY(smoe::launch_combine(Y, slot, wts, K, H, P, T, (has_sh && add_shared) ? 1 : 0, y, st,
+                                      y_stream ? 1 : 0),
+                 "combine");
     else if (nat && add_shared)  // the fused combine left the shared rows out: the same last addition, after it
         SMOE_TRY(smoe::launch_add_rows(y, Y + (size_t)P * H, T, H, st), "shared add");
     SMOE_MARK();

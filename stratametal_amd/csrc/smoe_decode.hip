@@ -2446,12 +2446,21 @@ __global__ __launch_bounds__(256) void k_combine(const float* __restrict__ Y, co
 
 // The same combine four neighbouring elements per thread (16-byte loads and stores; every element's sum is
 // formed exactly as above), NB pair rows per batch (NB >= k where k <= 16, so that no batch reloads rows).
-// H % 4 == 0, y 16-byte aligned.
-template <int NB>
+// H % 4 == 0, y 16-byte aligned.  NT: Y read and y written with streaming accesses (a Y larger than the caches).
+template <int NB, bool NT>
 __global__ __launch_bounds__(256) void k_combine4(const float* __restrict__ Y, const int32_t* __restrict__ slot,
                                                    const float* __restrict__ wts, int k, int H, int P, int add_shared,
                                                    float* __restrict__ y) {
     asm volatile("" ::"s"(Y), "s"(slot), "s"(wts), "s"(y), "s"(k), "s"(H), "s"(P), "s"(add_shared));  // kernargs now
+    typedef float vf4 __attribute__((ext_vector_type(4)));
+    auto ld = [](const float* p) -> float4 {
+        if constexpr (NT) {
+            const vf4 v = __builtin_nontemporal_load(reinterpret_cast<const vf4*>(p));
+            return make_float4(v.x, v.y, v.z, v.w);
+        } else {
+            return *reinterpret_cast<const float4*>(p);
+        }
+    };
     const int t = blockIdx.x;
     const int32_t* sl = slot + (size_t)t * k;
     const float* wt = wts + (size_t)t * k;
@@ -2472,7 +2481,7 @@ __global__ __launch_bounds__(256) void k_combine4(const float* __restrict__ Y, c
             for (int i = 0; i < NB; ++i) {
                 const int s = min(s0 + i, k - 1);
                 const int r = s0 == 0 ? slb[i] : sl[s];
-                v[i] = reinterpret_cast<const float4*>(Y + (size_t)r * H)[j];
+                v[i] = ld(Y + (size_t)r * H + 4 * j);
                 wv[i] = s0 == 0 ? wtb[i] : wt[s];
             }
 #pragma unroll
@@ -2489,10 +2498,13 @@ __global__ __launch_bounds__(256) void k_combine4(const float* __restrict__ Y, c
             }
         }
         if (add_shared) {
-            const float4 sh = reinterpret_cast<const float4*>(Y + (size_t)(P + t) * H)[j];
+            const float4 sh = ld(Y + (size_t)(P + t) * H + 4 * j);
             acc = make_float4(acc.x + sh.x, acc.y + sh.y, acc.z + sh.z, acc.w + sh.w);
         }
-        reinterpret_cast<float4*>(y + (size_t)t * H)[j] = acc;
+        if constexpr (NT)
+            __builtin_nontemporal_store(vf4{acc.x, acc.y, acc.z, acc.w}, reinterpret_cast<vf4*>(y + (size_t)t * H) + j);
+        else
+            reinterpret_cast<float4*>(y + (size_t)t * H)[j] = acc;
     }
 }
 
@@ -2930,14 +2942,20 @@ hipError_t launch_q2_moe_small(const uint8_t* gate_exps, const uint8_t* up_exps,
 int fused_status_words(int H) { return (H + kDcRows - 1) / kDcRows; }
 
 hipError_t launch_combine(const float* Y, const int32_t* slot, const float* wts, int k, int H, int P, int T,
-                          int add_shared, float* y, hipStream_t s) {
+                          int add_shared, float* y, hipStream_t s, int nt) {
     if (H % 4 == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0 && (reinterpret_cast<uintptr_t>(Y) & 15) == 0) {
         const int ychunks = (H / 4 + 255) / 256;
         dim3 grid((unsigned)T, (unsigned)(ychunks < 8 ? ychunks : 8));
-        if (k <= 4) hipLaunchKernelGGL(k_combine4<4>, grid, dim3(256), 0, s, Y, slot, wts, k, H, P, add_shared, y);
-        else if (k <= 8) hipLaunchKernelGGL(k_combine4<8>, grid, dim3(256), 0, s, Y, slot, wts, k, H, P, add_shared, y);
-        else if (k <= 12) hipLaunchKernelGGL(k_combine4<12>, grid, dim3(256), 0, s, Y, slot, wts, k, H, P, add_shared, y);
-        else hipLaunchKernelGGL(k_combine4<16>, grid, dim3(256), 0, s, Y, slot, wts, k, H, P, add_shared, y);
+#define SMOE_C4(NB)                                                                                                   \
+    do {                                                                                                               \
+        if (nt) hipLaunchKernelGGL((k_combine4<NB, true>), grid, dim3(256), 0, s, Y, slot, wts, k, H, P, add_shared, y); \
+        else hipLaunchKernelGGL((k_combine4<NB, false>), grid, dim3(256), 0, s, Y, slot, wts, k, H, P, add_shared, y);  \
+    } while (0)
+        if (k <= 4) SMOE_C4(4);
+        else if (k <= 8) SMOE_C4(8);
+        else if (k <= 12) SMOE_C4(12);
+        else SMOE_C4(16);
+#undef SMOE_C4
         return hipGetLastError();
     }
     const int ychunks = (H + 255) / 256;

@@ -91,8 +91,9 @@ void set_wait_limit(int limit);   // (below zero: every wait gives up at once)
 int default_wait_limit();
 hipError_t launch_residual_rmsnorm(const float* x, const float* r, int n_rows, int n, float eps, float* out,
                                    hipStream_t s);
+// nt: Y is read and y written with streaming (nontemporal) accesses, for a Y larger than the caches
 hipError_t launch_combine(const float* Y, const int32_t* slot, const float* wts, int k, int H, int P, int T,
-                          int add_shared, float* y, hipStream_t s);
+                          int add_shared, float* y, hipStream_t s, int nt = 0);
 hipError_t launch_combine_parts(const float* parts, const float* wts, const float* shared, int k, int n, float* y,
                                 hipStream_t s);
 hipError_t launch_swiglu_q8(const float* gate, const float* up, int64_t n, uint8_t* y, hipStream_t s);
@@ -139,7 +140,7 @@ hipError_t launch_flags_mask(const int32_t* fx, int64_t nx, const int32_t* fh, i
                              hipStream_t s, const int32_t* fw = nullptr, int64_t nw = 0);
 hipError_t launch_mm_down(const uint8_t* down_exps, const uint8_t* down_sh, const uint32_t* hrec, int64_t n_hrec,
                           int h_rec, const float* sg, const int4* items, int H, int F, int Fs, int max_items, float* Y,
-                          hipStream_t s);
+                          int nt, hipStream_t s);  // nt: streaming stores of Y
 
 // the hyper-connection ends (smoe_hc.hip): gr_read (two launches; proj [T][hc_lr] and rs [T][hc] are scratch; with
 // rprev, R = rprev + yprev * 2 sigmoid(injprev / hc) is formed and stored first) and gr_write

@@ -21,8 +21,9 @@
 // pi = (0 2 1 3 4 6 5 7), the order in which a lane of quarter q meets the codes of code dword q of the block
 // in the two 32-deep MFMA steps s.
 //
-// MFMA tiles (lane l = 16 q + i): A[i][k] = activation of column (token) i, B[k][j] = weight of row j,
-// C[4 q + r][j] in register r.
+// MFMA tiles (lane l = 16 q + i): A[i][k] = weight of row i, B[k][j] = activation of column (token) j,
+// C[4 q + r][j] in register r: a lane holds four consecutive rows of one column, which the epilogues store as one
+// piece (measured: down 82 -> 72 us at the benchmark's prefill 512, whose stores had been one dword per row).
 #include "smoe_device.hpp"
 #include "smoe_gemv.hpp"
 #include "smoe_items.hpp"
@@ -315,7 +316,7 @@ struct MmPlan {
 // One staged unit: the activation fragments of all NT column tiles (columns tok0 + 16 n ..; CP pieces per column
 // in LDS, A at the unit's first piece) are loaded first; then for each block h and row set s (LDS row rows[s] of
 // RD dwords; the unit starts `wofs` dwords into the row's window)
-// the set's B operands are expanded and fed to every tile: acc[n][s] += A0 B0 + A1 B1.  Set s + 1 is expanded
+// the set's weight operands are expanded and fed to every tile: acc[n][s] += W0 A0 + W1 A1.  Set s + 1 is expanded
 // while the matrix cores work on set s.
 template <int NS, int NT, int CP = 17, int RD = 12>
 __device__ __forceinline__ void mm_unit(f32x4 (&acc)[kMaxTiles][NS], const uint32_t* W, int wofs, const int (&rows)[NS],
@@ -340,8 +341,8 @@ __device__ __forceinline__ void mm_unit(f32x4 (&acc)[kMaxTiles][NS], const uint3
             expand_codes(cw, db, b0, b1);
 #pragma unroll
             for (int n = 0; n < NT; ++n) {
-                acc[n][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[h][n][0], b0, acc[n][s], 0, 0, 0);
-                acc[n][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[h][n][1], b1, acc[n][s], 0, 0, 0);
+                acc[n][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(b0, a[h][n][0], acc[n][s], 0, 0, 0);
+                acc[n][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(b1, a[h][n][1], acc[n][s], 0, 0, 0);
             }
         }
     }
@@ -479,25 +480,25 @@ __device__ __forceinline__ void mm_gu_body(uint8_t* lds, const int* rowidx, cons
     mm_loop<MODE>(acc, lds, pl, units, ra, rows, tok0, ntiles, i, q);
     __syncthreads();  // every wave is done with the ring: its start becomes the h tile
     // h tile [column][128 rows in record order] as fp16 bits of bf16 values
+    // lane (q, i) holds rows fbase + 4 q .. + 3 of column 16 n + i: their record positions are one aligned group of
+    // four, in the order (0 2 1 3), written as one 8-byte store
     uint16_t* ht = reinterpret_cast<uint16_t*>(lds);
     bool ovf = false;
+    static_assert(NS == 2, "one gate set and one up set");
+    const int f4 = fbase + 4 * q;
+    const int pos4 = 64 * (f4 >> 6) + rec_pos(f4 & 63);
 #pragma unroll
-    for (int s = 0; s < NS / 2; ++s) {
-        const int f = fbase + 16 * s + i;
-        const int pos = 64 * (f >> 6) + rec_pos(f & 63);
+    for (int n = 0; n < S::MT; ++n) {
+        const int c = tok0 + 16 * n + i;
+        if (n < ntiles && c < ncol) {
+            uint32_t hb[4];
 #pragma unroll
-        for (int n = 0; n < S::MT; ++n) {
-            if (n < ntiles) {
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int c = tok0 + 16 * n + 4 * q + r;
-                    if (c < ncol) {
-                        const float h = silu_mul_fast(acc[n][s][r], acc[n][s + NS / 2][r]);
-                        ht[c * 128 + pos] = (uint16_t)bf16_as_f16(h);
-                        if (flag) ovf |= f16_overflow(h);
-                    }
-                }
+            for (int r = 0; r < 4; ++r) {
+                const float h = silu_mul_fast(acc[n][0][r], acc[n][1][r]);
+                hb[r] = bf16_as_f16(h);
+                if (flag) ovf |= f16_overflow(h);
             }
+            *reinterpret_cast<uint2*>(ht + c * 128 + pos4) = make_uint2(hb[0] | (hb[2] << 16), hb[1] | (hb[3] << 16));
         }
     }
     if (flag) {
@@ -554,7 +555,7 @@ __global__ __launch_bounds__(512) void k_mm_gu(const uint8_t* __restrict__ gate_
 template <int MODE>
 __device__ __forceinline__ void mm_down_body(uint8_t* lds, const int* rowidx, const Item& item, int ncol, int units,
                                              int rt, const uint8_t* d0, const uint32_t* hrec, uint32_t hrec_bytes,
-                                             int h_rec, const float* sg, int H, float* Y) {
+                                             int h_rec, const float* sg, int H, float* Y, bool nt) {
     using S = Shape<MODE>;
     constexpr int NS = S::NS;
     const uint32_t rb = (uint32_t)units * 36u;
@@ -573,22 +574,23 @@ __device__ __forceinline__ void mm_down_body(uint8_t* lds, const int* rowidx, co
     const int ntiles = min(S::MT, (ncol + 15) >> 4);
     f32x4 acc[kMaxTiles][NS];
     mm_loop<MODE>(acc, lds, pl, units, ra, rows, tok0, ntiles, i, q);
+    // lane (q, i) holds rows r0 + 16 s + 4 q .. + 3 of column 16 n + i: one 16-byte store (H % 128 == 0); with `nt`
+    // a streaming store (Y larger than the caches: its lines would evict the records and weights other work-groups of
+    // this XCD still read)
 #pragma unroll
-    for (int s = 0; s < NS; ++s) {
-        const int row = kWgRows * rt + rows[s];
-        if (row < H) {
+    for (int n = 0; n < S::MT; ++n) {
+        const int c = tok0 + 16 * n + i;
+        if (n < ntiles && c < ncol) {
+            const float gs = item.shared ? sigmoid(sg[item.tok0 + c]) : 1.0f;
 #pragma unroll
-            for (int n = 0; n < S::MT; ++n) {
-                if (n < ntiles) {
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const int c = tok0 + 16 * n + 4 * q + r;
-                        if (c < ncol) {
-                            float v = acc[n][s][r];
-                            if (item.shared) v = v * sigmoid(sg[item.tok0 + c]);
-                            Y[(size_t)(item.first + c) * H + row] = v;
-                        }
-                    }
+            for (int s = 0; s < NS; ++s) {
+                const int row = kWgRows * rt + r0 + 16 * s + 4 * q;
+                if (row < H) {
+                    f32x4 v = acc[n][s];
+                    if (item.shared) v = f32x4{v[0] * gs, v[1] * gs, v[2] * gs, v[3] * gs};
+                    f32x4* dst = reinterpret_cast<f32x4*>(Y + (size_t)(item.first + c) * H + row);
+                    if (nt) __builtin_nontemporal_store(v, dst);
+                    else *dst = v;
                 }
             }
         }
@@ -599,7 +601,7 @@ __global__ __launch_bounds__(512) void k_mm_down(const uint8_t* __restrict__ dow
                                                  const uint32_t* __restrict__ hrec, uint32_t hrec_bytes, int h_rec,
                                                  const float* __restrict__ sg, const int4* __restrict__ items,
                                                  int max_items, int n_rb, int H, int F, int Fs,
-                                                 float* __restrict__ Y) {
+                                                 float* __restrict__ Y, int nt) {
     __shared__ __align__(16) uint8_t lds[kLds];
     __shared__ int rowidx[kChunk];
     int y, rt;
@@ -613,8 +615,8 @@ __global__ __launch_bounds__(512) void k_mm_down(const uint8_t* __restrict__ dow
     __syncthreads();
     const int units = Fe >> 7;
     const uint8_t* d0 = item.shared ? down_sh : down_exps + (size_t)item.e * H * ((size_t)(F >> 7) * 36);
-    if (ncol > 64) mm_down_body<kWide>(lds, rowidx, item, ncol, units, rt, d0, hrec, hrec_bytes, h_rec, sg, H, Y);
-    else mm_down_body<kNarrow>(lds, rowidx, item, ncol, units, rt, d0, hrec, hrec_bytes, h_rec, sg, H, Y);
+    if (ncol > 64) mm_down_body<kWide>(lds, rowidx, item, ncol, units, rt, d0, hrec, hrec_bytes, h_rec, sg, H, Y, nt);
+    else mm_down_body<kNarrow>(lds, rowidx, item, ncol, units, rt, d0, hrec, hrec_bytes, h_rec, sg, H, Y, nt);
 }
 
 // The thin items (<= kThinCols columns) on k_mm_down's grid, launched after it: one-stage ring (55 KB of LDS), two
@@ -625,7 +627,7 @@ __global__ __launch_bounds__(512) void k_mm_down_thin(const uint8_t* __restrict_
                                                       const uint32_t* __restrict__ hrec, uint32_t hrec_bytes, int h_rec,
                                                       const float* __restrict__ sg, const int4* __restrict__ items,
                                                       int max_items, int n_rb, int H, int F, int Fs,
-                                                      float* __restrict__ Y) {
+                                                      float* __restrict__ Y, int nt) {
     __shared__ __align__(16) uint8_t lds[Shape<kThin1>::kLdsBytes];
     __shared__ int rowidx[kThinCols];
     int y, rt;
@@ -638,7 +640,7 @@ __global__ __launch_bounds__(512) void k_mm_down_thin(const uint8_t* __restrict_
     __syncthreads();
     const int units = Fe >> 7;
     const uint8_t* d0 = item.shared ? down_sh : down_exps + (size_t)item.e * H * ((size_t)(F >> 7) * 36);
-    mm_down_body<kThin1>(lds, rowidx, item, ncol, units, rt, d0, hrec, hrec_bytes, h_rec, sg, H, Y);
+    mm_down_body<kThin1>(lds, rowidx, item, ncol, units, rt, d0, hrec, hrec_bytes, h_rec, sg, H, Y, nt);
 }
 
 // ------------------------------------------------------------------------------------------------ launchers
@@ -838,16 +840,16 @@ hipError_t launch_flags_mask(const int32_t* fx, int64_t nx, const int32_t* fh, i
 
 hipError_t launch_mm_down(const uint8_t* down_exps, const uint8_t* down_sh, const uint32_t* hrec, int64_t n_hrec,
                           int h_rec, const float* sg, const int4* items, int H, int F, int Fs, int max_items, float* Y,
-                          hipStream_t s) {
+                          int nt, hipStream_t s) {
     const size_t bytes = act_rec_bytes(n_hrec);
     if (bytes >= kOob) return hipErrorInvalidValue;
     // the thin items after the others: their kernel's smaller LDS lets two work-groups share a CU
     const int n_rb = (H + kWgRows - 1) / kWgRows;
     const dim3 grid(xcd_grid(n_rb, max_items));
     hipLaunchKernelGGL(k_mm_down, grid, dim3(512), 0, s, down_exps, down_sh, hrec, (uint32_t)bytes, h_rec, sg, items,
-                       max_items, n_rb, H, F, Fs, Y);
+                       max_items, n_rb, H, F, Fs, Y, nt);
     hipLaunchKernelGGL(k_mm_down_thin, grid, dim3(512), 0, s, down_exps, down_sh, hrec, (uint32_t)bytes, h_rec, sg,
-                       items, max_items, n_rb, H, F, Fs, Y);
+                       items, max_items, n_rb, H, F, Fs, Y, nt);
     return hipGetLastError();
 }
 
