@@ -182,6 +182,10 @@ __device__ __forceinline__ void expand_codes(uint32_t cw, uint32_t dbits, f16x8&
 // In every shape wave w owns two 16-row sets (gate/up: gate rows 16 w .. + 15 and the same up rows; down: rows
 // 32 w .. + 31) and every column, so each row's codes are expanded once per work-group.
 constexpr int kWgRows = 256;
+// Down work-groups (other than thin) take kDownRbw consecutive row blocks of their item, one K loop over all of
+// them: the ring runs on across the row blocks, so the next block's first stages load while the last units and
+// the stores of the one before run (a down K loop is only n_ff / 128 units).
+constexpr int kDownRbw = 2;
 constexpr int kWaves = 8;
 constexpr uint32_t kOob = 0x80000000u;
 constexpr int kRing = 148480;           // bytes of the stage ring
@@ -267,6 +271,13 @@ struct MmPlan {
     uint32_t a_off[S::kASlots], w_off[S::kWSlots];
     int a_at[S::kASlots], w_at[S::kWSlots];
     i32x4 w_rsrc[S::kWSlots];  // the slot's weight tensor (the up rows' for the second half of gate/up)
+    // a work-group that runs several row blocks (down, one weight tensor): unit u of the K loop is unit u % upr of
+    // row block u / upr, whose weight rows are the rbs bytes from wbase + (u / upr) rbs (of wbytes in all); each row
+    // block gets a buffer resource of its own, so rows past the tensor read as zeros (one row block: upr = the K
+    // loop's units, and w_rsrc as set by init)
+    int upr = 1 << 30;
+    uint32_t rbs = 0, wbytes = 0;
+    const uint8_t* wbase = nullptr;
 
     // rowidx: activation row of each column; rpr: records per activation row; rb: weight row bytes; split: rows
     // of the first weight tensor (gate/up: 128; down: 256, i.e. one tensor); rw0 / rw1: the two weight tensors.
@@ -298,8 +309,11 @@ struct MmPlan {
     // 48-byte window starts at the 16-byte boundary at or below the unit; four: at the unit (36 u = 144 u / 4).
     __device__ __forceinline__ void issue(uint32_t lds0, int b, int u, i32x4 ra) const {
         const uint32_t st = (uint32_t)(b * S::kStage);
-        const uint32_t sa = __builtin_amdgcn_readfirstlane((uint32_t)u * (2 * kRecBytes));
-        const uint32_t sw = __builtin_amdgcn_readfirstlane((uint32_t)(S::UPS == 1 ? 36 * u - 4 * (u & 3) : 36 * u));
+        const int rbl = u / upr, ur = u - rbl * upr;
+        const uint32_t sa = __builtin_amdgcn_readfirstlane((uint32_t)ur * (2 * kRecBytes));
+        const uint32_t sw = __builtin_amdgcn_readfirstlane((uint32_t)(S::UPS == 1 ? 36 * ur - 4 * (ur & 3) : 36 * ur));
+        const uint32_t wofs = (uint32_t)rbl * rbs;
+        const i32x4 wr = buffer_rsrc(wbase + wofs, wbytes - wofs < rbs ? wbytes - wofs : rbs);
 #pragma unroll
         for (int m = 0; m < S::kASlots; ++m) {
             const uint32_t at = a_at[m] < 0 ? (uint32_t)S::kDummyAt : st + (uint32_t)a_at[m];
@@ -308,7 +322,7 @@ struct MmPlan {
 #pragma unroll
         for (int m = 0; m < S::kWSlots; ++m) {
             const uint32_t at = w_at[m] < 0 ? (uint32_t)S::kDummyAt : st + (uint32_t)w_at[m];
-            dma16(__builtin_amdgcn_readfirstlane(lds0 + at), w_off[m], w_rsrc[m], sw);
+            dma16(__builtin_amdgcn_readfirstlane(lds0 + at), w_off[m], wbase ? wr : w_rsrc[m], sw);
         }
     }
 };
@@ -349,21 +363,31 @@ __device__ __forceinline__ void mm_unit(f32x4 (&acc)[kMaxTiles][NS], const uint3
 }
 
 // The K loop of both kernels: stages of UPS units of 128 values through the ring, kStages - 1 stages in flight.
-// NT: the wave's live column tiles.
-template <int MODE, int NT>
+// NT: the wave's live column tiles.  With several row blocks (pl.upr units each, one unit per stage), epi(rbl) runs
+// after the last unit of row block rbl: it stores the wave's results of that block and clears acc, while the next
+// block's first stages are already in flight.
+struct NoEpi {
+    __device__ __forceinline__ void operator()(int) const {}
+};
+template <int MODE, int NT, class Epi>
 __device__ __forceinline__ void mm_loop_nt(f32x4 (&acc)[kMaxTiles][Shape<MODE>::NS], uint8_t* lds, const MmPlan<MODE>& pl,
                                            int units, i32x4 ra, const int (&rows)[Shape<MODE>::NS], int tok0, int i,
-                                           int q) {
+                                           int q, const Epi& epi) {
     using S = Shape<MODE>;
     constexpr int ST = S::kStages;
     const uint32_t lds0 = lds_addr(lds);
     const int nst = (units + S::UPS - 1) / S::UPS;
+    int ur = 0, rbl = 0;  // (UPS == 1) the consumed stage's unit within its row block, and that row block
     auto stage = [&](int g, int b) {  // the units of stage g, in ring stage b
         const uint8_t* stg = lds + b * S::kStage;
         const uint32_t* W = reinterpret_cast<const uint32_t*>(stg + S::kABytes);
         const uint4* A = reinterpret_cast<const uint4*>(stg);
         if constexpr (S::UPS == 1) {
-            mm_unit<S::NS, NT>(acc, W, g & 3, rows, A, tok0, i, q);
+            mm_unit<S::NS, NT>(acc, W, ur & 3, rows, A, tok0, i, q);
+            if (++ur == pl.upr) {
+                epi(rbl++);
+                ur = 0;
+            }
         } else {
 #pragma unroll
             for (int uu = 0; uu < S::UPS; ++uu)
@@ -403,30 +427,30 @@ __device__ __forceinline__ void mm_loop_nt(f32x4 (&acc)[kMaxTiles][Shape<MODE>::
     }
 }
 
-template <int MODE>
+template <int MODE, class Epi = NoEpi>
 __device__ __forceinline__ void mm_loop(f32x4 (&acc)[kMaxTiles][Shape<MODE>::NS], uint8_t* lds, const MmPlan<MODE>& pl,
                                         int units, i32x4 ra, const int (&rows)[Shape<MODE>::NS], int tok0, int ntiles,
-                                        int i, int q) {
+                                        int i, int q, const Epi& epi = Epi{}) {
 #pragma unroll
     for (int n = 0; n < kMaxTiles; ++n)
 #pragma unroll
         for (int s = 0; s < Shape<MODE>::NS; ++s) acc[n][s] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     if constexpr (Shape<MODE>::kIsThin) {  // one tile
-        mm_loop_nt<MODE, 1>(acc, lds, pl, units, ra, rows, tok0, i, q);
+        mm_loop_nt<MODE, 1>(acc, lds, pl, units, ra, rows, tok0, i, q, epi);
         return;
     } else if constexpr (MODE == kNarrow) {
         switch (ntiles) {  // work-group-uniform: 2 .. 4 live tiles
-            case 1: mm_loop_nt<MODE, 1>(acc, lds, pl, units, ra, rows, tok0, i, q); break;
-            case 2: mm_loop_nt<MODE, 2>(acc, lds, pl, units, ra, rows, tok0, i, q); break;
-            case 3: mm_loop_nt<MODE, 3>(acc, lds, pl, units, ra, rows, tok0, i, q); break;
-            default: mm_loop_nt<MODE, 4>(acc, lds, pl, units, ra, rows, tok0, i, q); break;
+            case 1: mm_loop_nt<MODE, 1>(acc, lds, pl, units, ra, rows, tok0, i, q, epi); break;
+            case 2: mm_loop_nt<MODE, 2>(acc, lds, pl, units, ra, rows, tok0, i, q, epi); break;
+            case 3: mm_loop_nt<MODE, 3>(acc, lds, pl, units, ra, rows, tok0, i, q, epi); break;
+            default: mm_loop_nt<MODE, 4>(acc, lds, pl, units, ra, rows, tok0, i, q, epi); break;
         }
     } else {
         switch (ntiles) {  // work-group-uniform: 5 .. 8 live tiles
-            case 5: mm_loop_nt<MODE, 5>(acc, lds, pl, units, ra, rows, tok0, i, q); break;
-            case 6: mm_loop_nt<MODE, 6>(acc, lds, pl, units, ra, rows, tok0, i, q); break;
-            case 7: mm_loop_nt<MODE, 7>(acc, lds, pl, units, ra, rows, tok0, i, q); break;
-            default: mm_loop_nt<MODE, 8>(acc, lds, pl, units, ra, rows, tok0, i, q); break;
+            case 5: mm_loop_nt<MODE, 5>(acc, lds, pl, units, ra, rows, tok0, i, q, epi); break;
+            case 6: mm_loop_nt<MODE, 6>(acc, lds, pl, units, ra, rows, tok0, i, q, epi); break;
+            case 7: mm_loop_nt<MODE, 7>(acc, lds, pl, units, ra, rows, tok0, i, q, epi); break;
+            default: mm_loop_nt<MODE, 8>(acc, lds, pl, units, ra, rows, tok0, i, q, epi); break;
         }
     }
 }
@@ -549,23 +573,30 @@ __global__ __launch_bounds__(512) void k_mm_gu(const uint8_t* __restrict__ gate_
 }
 
 // ------------------------------------------------------------------------------------------------ down
-// Grid (H / 256, work items), 8 waves.  Work-group rt computes down rows [256 rt, 256 rt + 256) of the item's
-// columns into Y[first + c] (the shared expert's rows times sigmoid(sg[t])).  Wave w has rows 32 w .. + 31
-// (two sets).
+// 8 waves.  A work-group computes down rows [256 rt, 256 rt + 256) of the item's columns for its nrb row blocks rt
+// from rt0 (k_mm_down: kDownRbw; k_mm_down_thin: one) into Y[first + c] (the shared expert's rows times
+// sigmoid(sg[t])).  Wave w has rows 32 w .. + 31 of each row block (two sets).
 template <int MODE>
 __device__ __forceinline__ void mm_down_body(uint8_t* lds, const int* rowidx, const Item& item, int ncol, int units,
-                                             int rt, const uint8_t* d0, const uint32_t* hrec, uint32_t hrec_bytes,
-                                             int h_rec, const float* sg, int H, float* Y, bool nt) {
+                                             int rt0, int nrb, const uint8_t* d0, const uint32_t* hrec,
+                                             uint32_t hrec_bytes, int h_rec, const float* sg, int H, float* Y, bool nt) {
     using S = Shape<MODE>;
     constexpr int NS = S::NS;
     const uint32_t rb = (uint32_t)units * 36u;
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, i = lane & 15,
               q = lane >> 4;
-    const int nrows = min(kWgRows, H - kWgRows * rt);
+    const int nrows = min(kWgRows * nrb, H - kWgRows * rt0);
     const i32x4 ra = buffer_rsrc(hrec, hrec_bytes);
-    const i32x4 rd = buffer_rsrc(d0 + (size_t)kWgRows * rt * rb, (uint32_t)nrows * rb);
+    const uint8_t* dr = d0 + (size_t)kWgRows * rt0 * rb;
+    const i32x4 rd = buffer_rsrc(dr, (uint32_t)min(kWgRows, nrows) * rb);
     MmPlan<MODE> pl;
     pl.init(rowidx, wave, lane, ncol, h_rec, rb, kWgRows, rd, rd);
+    pl.upr = units;  // (the K loop's epilogue hook stores each row block's results)
+    if (nrb > 1) {
+        pl.rbs = (uint32_t)kWgRows * rb;
+        pl.wbytes = (uint32_t)nrows * rb;
+        pl.wbase = dr;
+    }
     int rows[NS];
     const int r0 = 32 * wave;
 #pragma unroll
@@ -573,39 +604,53 @@ __device__ __forceinline__ void mm_down_body(uint8_t* lds, const int* rowidx, co
     const int tok0 = 0;
     const int ntiles = min(S::MT, (ncol + 15) >> 4);
     f32x4 acc[kMaxTiles][NS];
-    mm_loop<MODE>(acc, lds, pl, units, ra, rows, tok0, ntiles, i, q);
     // lane (q, i) holds rows r0 + 16 s + 4 q .. + 3 of column 16 n + i: one 16-byte store (H % 128 == 0); with `nt`
     // a streaming store (Y larger than the caches: its lines would evict the records and weights other work-groups of
     // this XCD still read)
+    auto store = [&](int rbl) {
 #pragma unroll
-    for (int n = 0; n < S::MT; ++n) {
-        const int c = tok0 + 16 * n + i;
-        if (n < ntiles && c < ncol) {
-            const float gs = item.shared ? sigmoid(sg[item.tok0 + c]) : 1.0f;
+        for (int n = 0; n < S::MT; ++n) {
+            const int c = tok0 + 16 * n + i;
+            if (n < ntiles && c < ncol) {
+                const float gs = item.shared ? sigmoid(sg[item.tok0 + c]) : 1.0f;
 #pragma unroll
-            for (int s = 0; s < NS; ++s) {
-                const int row = kWgRows * rt + r0 + 16 * s + 4 * q;
-                if (row < H) {
-                    f32x4 v = acc[n][s];
-                    if (item.shared) v = f32x4{v[0] * gs, v[1] * gs, v[2] * gs, v[3] * gs};
-                    f32x4* dst = reinterpret_cast<f32x4*>(Y + (size_t)(item.first + c) * H + row);
-                    if (nt) __builtin_nontemporal_store(v, dst);
-                    else *dst = v;
+                for (int s = 0; s < NS; ++s) {
+                    const int row = kWgRows * (rt0 + rbl) + r0 + 16 * s + 4 * q;
+                    if (row < H) {
+                        f32x4 v = acc[n][s];
+                        if (item.shared) v = f32x4{v[0] * gs, v[1] * gs, v[2] * gs, v[3] * gs};
+                        f32x4* dst = reinterpret_cast<f32x4*>(Y + (size_t)(item.first + c) * H + row);
+                        if (nt) __builtin_nontemporal_store(v, dst);
+                        else *dst = v;
+                    }
                 }
             }
         }
+    };
+    if constexpr (S::UPS == 1) {  // each row block's results leave from inside the K loop
+        auto epi = [&](int rbl) {
+            store(rbl);
+#pragma unroll
+            for (int n = 0; n < kMaxTiles; ++n)
+#pragma unroll
+                for (int s = 0; s < NS; ++s) acc[n][s] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        };
+        mm_loop<MODE>(acc, lds, pl, nrb * units, ra, rows, tok0, ntiles, i, q, epi);
+    } else {  // (one row block)
+        mm_loop<MODE>(acc, lds, pl, units, ra, rows, tok0, ntiles, i, q);
+        store(0);
     }
 }
 
 __global__ __launch_bounds__(512) void k_mm_down(const uint8_t* __restrict__ down_exps, const uint8_t* __restrict__ down_sh,
                                                  const uint32_t* __restrict__ hrec, uint32_t hrec_bytes, int h_rec,
                                                  const float* __restrict__ sg, const int4* __restrict__ items,
-                                                 int max_items, int n_rb, int H, int F, int Fs,
+                                                 int max_items, int n_rg, int n_rb, int H, int F, int Fs,
                                                  float* __restrict__ Y, int nt) {
     __shared__ __align__(16) uint8_t lds[kLds];
     __shared__ int rowidx[kChunk];
-    int y, rt;
-    if (!xcd_item(n_rb, max_items, y, rt)) return;
+    int y, rg;
+    if (!xcd_item(n_rg, max_items, y, rg)) return;
     Item item;
     if (!work_item(items, y, item)) return;
     const int Fe = item.shared ? Fs : F;
@@ -615,8 +660,10 @@ __global__ __launch_bounds__(512) void k_mm_down(const uint8_t* __restrict__ dow
     __syncthreads();
     const int units = Fe >> 7;
     const uint8_t* d0 = item.shared ? down_sh : down_exps + (size_t)item.e * H * ((size_t)(F >> 7) * 36);
-    if (ncol > 64) mm_down_body<kWide>(lds, rowidx, item, ncol, units, rt, d0, hrec, hrec_bytes, h_rec, sg, H, Y, nt);
-    else mm_down_body<kNarrow>(lds, rowidx, item, ncol, units, rt, d0, hrec, hrec_bytes, h_rec, sg, H, Y, nt);
+    const int rt0 = kDownRbw * rg, nrb = min(kDownRbw, n_rb - rt0);
+    if (ncol > 64)
+        mm_down_body<kWide>(lds, rowidx, item, ncol, units, rt0, nrb, d0, hrec, hrec_bytes, h_rec, sg, H, Y, nt);
+    else mm_down_body<kNarrow>(lds, rowidx, item, ncol, units, rt0, nrb, d0, hrec, hrec_bytes, h_rec, sg, H, Y, nt);
 }
 
 // The thin items (<= kThinCols columns) on k_mm_down's grid, launched after it: one-stage ring (55 KB of LDS), two
@@ -640,7 +687,7 @@ __global__ __launch_bounds__(512) void k_mm_down_thin(const uint8_t* __restrict_
     __syncthreads();
     const int units = Fe >> 7;
     const uint8_t* d0 = item.shared ? down_sh : down_exps + (size_t)item.e * H * ((size_t)(F >> 7) * 36);
-    mm_down_body<kThin1>(lds, rowidx, item, ncol, units, rt, d0, hrec, hrec_bytes, h_rec, sg, H, Y, nt);
+    mm_down_body<kThin1>(lds, rowidx, item, ncol, units, rt, 1, d0, hrec, hrec_bytes, h_rec, sg, H, Y, nt);
 }
 
 // ------------------------------------------------------------------------------------------------ launchers
@@ -679,7 +726,7 @@ hipError_t launch_act_records(const float* x, int64_t n_rec, uint32_t* rec, uint
 // the chunk is as deep as the registers of two chunks in flight allow.  The work-groups of one token block take
 // consecutive row blocks on one XCD (linear id mod 8), so that the block's x rows are read from memory once per XCD
 // and then from its L2.
-constexpr int kRtTok = 32, kRtRows = 64, kRtK = 128, kRtPitch = kRtK * 2 + 16;
+constexpr int kRtTok = 32, kRtRows = 64, kRtK = 128, kRtPitch = kRtK * 2 + 16, kRtM = kRtTok / 16;
 constexpr int kRtPieces = kRtK / 8, kRtPass = 256 / kRtPieces;  // 16-byte pieces per row; rows per pass of 256 threads
 constexpr int kRtLa = kRtTok / kRtPass, kRtLb = kRtRows / kRtPass;  // a thread's x and weight pieces per chunk
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -733,9 +780,9 @@ __global__ __launch_bounds__(256) void k_router_mfma(const uint16_t* __restrict_
     load(One{}, min(1, nk - 1) * kRtK);
     stash(Zero{});
     __syncthreads();
-    f32x4 acc[2];
+    f32x4 acc[kRtM];
 #pragma unroll
-    for (int m = 0; m < 2; ++m) acc[m] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int m = 0; m < kRtM; ++m) acc[m] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     // chunk c lives in register slot c & 1 and LDS buffer c & 1; the loop is unrolled by two so that every register
     // slot is a constant (an indexed slot would wait for its loads at once)
     auto chunk = [&](int kc, auto parity) {
@@ -751,7 +798,7 @@ __global__ __launch_bounds__(256) void k_router_mfma(const uint16_t* __restrict_
             const bf16x8 b = __builtin_bit_cast(
                 bf16x8, *reinterpret_cast<const u32x4*>(&sb[P][(16 * wave + i) * kRtPitch + 2 * (32 * st + 8 * q)]));
 #pragma unroll
-            for (int m = 0; m < 2; ++m) {
+            for (int m = 0; m < kRtM; ++m) {
                 const bf16x8 a = __builtin_bit_cast(
                     bf16x8, *reinterpret_cast<const u32x4*>(&sa[P][(16 * m + i) * kRtPitch + 2 * (32 * st + 8 * q)]));
                 acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc[m], 0, 0, 0);
@@ -770,7 +817,7 @@ __global__ __launch_bounds__(256) void k_router_mfma(const uint16_t* __restrict_
     if (row >= rows_total) return;
     const float bv = (bias && row < E) ? bias[row] : 0.0f;
 #pragma unroll
-    for (int m = 0; m < 2; ++m)
+    for (int m = 0; m < kRtM; ++m)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int t = t0 + 16 * m + 4 * q + r;
@@ -844,12 +891,11 @@ hipError_t launch_mm_down(const uint8_t* down_exps, const uint8_t* down_sh, cons
     const size_t bytes = act_rec_bytes(n_hrec);
     if (bytes >= kOob) return hipErrorInvalidValue;
     // the thin items after the others: their kernel's smaller LDS lets two work-groups share a CU
-    const int n_rb = (H + kWgRows - 1) / kWgRows;
-    const dim3 grid(xcd_grid(n_rb, max_items));
-    hipLaunchKernelGGL(k_mm_down, grid, dim3(512), 0, s, down_exps, down_sh, hrec, (uint32_t)bytes, h_rec, sg, items,
-                       max_items, n_rb, H, F, Fs, Y, nt);
-    hipLaunchKernelGGL(k_mm_down_thin, grid, dim3(512), 0, s, down_exps, down_sh, hrec, (uint32_t)bytes, h_rec, sg,
-                       items, max_items, n_rb, H, F, Fs, Y, nt);
+    const int n_rb = (H + kWgRows - 1) / kWgRows, n_rg = (n_rb + kDownRbw - 1) / kDownRbw;
+    hipLaunchKernelGGL(k_mm_down, dim3(xcd_grid(n_rg, max_items)), dim3(512), 0, s, down_exps, down_sh, hrec,
+                       (uint32_t)bytes, h_rec, sg, items, max_items, n_rg, n_rb, H, F, Fs, Y, nt);
+    hipLaunchKernelGGL(k_mm_down_thin, dim3(xcd_grid(n_rb, max_items)), dim3(512), 0, s, down_exps, down_sh, hrec,
+                       (uint32_t)bytes, h_rec, sg, items, max_items, n_rb, H, F, Fs, Y, nt);
     return hipGetLastError();
 }
 

@@ -100,6 +100,12 @@ CASES = [
     # H 1536: 12 units (three four-unit thin stages); n_ff 384: three gate/up row blocks, down rows of three units
     ("H=1536 F=384, 150 tokens", dict(n_embd=1536, n_ff=384, n_ff_shared=384, n_expert=64, top_k=4), 150, 26, True,
      None, S.PATH_AUTO),
+    # H 384: one down work-group takes both row blocks, the second only half there (its rows past H read as zeros)
+    ("H=384, 140 tokens (a half down row block)", dict(n_embd=384, n_ff=256, n_ff_shared=256, n_expert=32, top_k=4),
+     140, 27, True, None, S.PATH_AUTO),
+    # H 640: three down row blocks, a pair and a half block alone
+    ("H=640, 140 tokens", dict(n_embd=640, n_ff=256, n_ff_shared=256, n_expert=32, top_k=4), 140, 28, True, None,
+     S.PATH_AUTO),
 ]
 
 _LAYERS = {}
