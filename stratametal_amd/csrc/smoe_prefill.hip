@@ -196,16 +196,19 @@ constexpr int kLds = kRing + 1024;
 // shape with a ring of one stage: k_mm_down_thin takes 55 KB of LDS, so two of its work-groups share a CU and one's
 // loads overlap the other's products (measured: the thin down items 8 us faster at the benchmark's prefill; the
 // same split of gate/up, whose thin work-groups stream four stages, gained nothing).
-enum { kThin = 0, kNarrow = 1, kWide = 2, kThin1 = 3 };
+// MODE 4 (k_mm_down_thin): MODE 3 over half the rows, 128 per work-group, one 16-row set per wave: 36 KB of LDS, so
+// four work-groups share a CU.
+enum { kThin = 0, kNarrow = 1, kWide = 2, kThin1 = 3, kThinH = 4 };
 constexpr int kMaxTiles = 8;  // column tiles of 16 per wave at most (the wide shape's 128 columns)
 constexpr int kThinCols = 16;
 template <int MODE>
 struct Shape {
-    static constexpr bool kIsThin = MODE == kThin || MODE == kThin1;
+    static constexpr bool kIsThin = MODE == kThin || MODE == kThin1 || MODE == kThinH;
     static constexpr int kTok = MODE == kWide ? 128 : MODE == kNarrow ? 64 : kThinCols;
     static constexpr int MT = (kTok + 15) / 16;  // column tiles of a wave: every wave has every column
     static constexpr int kStages = MODE == kWide ? 3 : MODE == kNarrow ? 5 : MODE == kThin ? 2 : 1;
-    static constexpr int NS = 2;
+    static constexpr int kRows = MODE == kThinH ? kWgRows / 2 : kWgRows;  // weight rows of a work-group
+    static constexpr int NS = kRows / (16 * kWaves);                       // 16-row sets of a wave
     // units of 128 values per stage: the thin shape streams weights, four units at a time, so that a row's
     // weights arrive as one 144-byte window (16-byte aligned, 9 pieces) instead of four 48-byte ones
     static constexpr int UPS = kIsThin ? 4 : 1;
@@ -214,14 +217,14 @@ struct Shape {
     static constexpr int kRowDw = 4 * kRowPieces;
     static constexpr int kAPieces = (kTok * kColPieces + 63) / 64 * 64;  // whole DMA instructions
     static constexpr int kAIns = kAPieces / 64;
-    static constexpr int kWPieces = kWgRows * kRowPieces;
+    static constexpr int kWPieces = kRows * kRowPieces;
     static constexpr int kWIns = kWPieces / 64;
     static constexpr int kASlots = (kAIns + kWaves - 1) / kWaves;
     static constexpr int kWSlots = (kWIns + kWaves - 1) / kWaves;
     static constexpr int kSlots = kASlots + kWSlots;
     static constexpr int kABytes = kAPieces * 16;
     static constexpr int kStage = kABytes + kWPieces * 16;
-    static constexpr int kDummyAt = MODE == kThin1 ? kStages * kStage : kDummy;  // the padding instructions' slot
+    static constexpr int kDummyAt = MODE == kThin1 || MODE == kThinH ? kStages * kStage : kDummy;  // padding's slot
     static constexpr int kLdsBytes = kDummyAt + 1024;
     static_assert(UPS == 1 || UPS == 4, "one or four units per stage");
     static_assert(kAPieces % 64 == 0 && kWPieces % 64 == 0, "whole DMA instructions");
@@ -573,9 +576,9 @@ __global__ __launch_bounds__(512) void k_mm_gu(const uint8_t* __restrict__ gate_
 }
 
 // ------------------------------------------------------------------------------------------------ down
-// 8 waves.  A work-group computes down rows [256 rt, 256 rt + 256) of the item's columns for its nrb row blocks rt
+// 8 waves.  A work-group computes down rows [R rt, R rt + R) (R = Shape::kRows) of the item's columns for its nrb row blocks rt
 // from rt0 (k_mm_down: kDownRbw; k_mm_down_thin: one) into Y[first + c] (the shared expert's rows times
-// sigmoid(sg[t])).  Wave w has rows 32 w .. + 31 of each row block (two sets).
+// sigmoid(sg[t])).  Wave w has rows 16 NS w .. + 16 NS - 1 of each row block (NS sets: two, one for kThinH).
 template <int MODE>
 __device__ __forceinline__ void mm_down_body(uint8_t* lds, const int* rowidx, const Item& item, int ncol, int units,
                                              int rt0, int nrb, const uint8_t* d0, const uint32_t* hrec,
@@ -585,20 +588,21 @@ __device__ __forceinline__ void mm_down_body(uint8_t* lds, const int* rowidx, co
     const uint32_t rb = (uint32_t)units * 36u;
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, i = lane & 15,
               q = lane >> 4;
-    const int nrows = min(kWgRows * nrb, H - kWgRows * rt0);
+    constexpr int RW = S::kRows;
+    const int nrows = min(RW * nrb, H - RW * rt0);
     const i32x4 ra = buffer_rsrc(hrec, hrec_bytes);
-    const uint8_t* dr = d0 + (size_t)kWgRows * rt0 * rb;
-    const i32x4 rd = buffer_rsrc(dr, (uint32_t)min(kWgRows, nrows) * rb);
+    const uint8_t* dr = d0 + (size_t)RW * rt0 * rb;
+    const i32x4 rd = buffer_rsrc(dr, (uint32_t)min(RW, nrows) * rb);
     MmPlan<MODE> pl;
-    pl.init(rowidx, wave, lane, ncol, h_rec, rb, kWgRows, rd, rd);
+    pl.init(rowidx, wave, lane, ncol, h_rec, rb, RW, rd, rd);
     pl.upr = units;  // (the K loop's epilogue hook stores each row block's results)
     if (nrb > 1) {
-        pl.rbs = (uint32_t)kWgRows * rb;
+        pl.rbs = (uint32_t)RW * rb;
         pl.wbytes = (uint32_t)nrows * rb;
         pl.wbase = dr;
     }
     int rows[NS];
-    const int r0 = 32 * wave;
+    const int r0 = 16 * NS * wave;
 #pragma unroll
     for (int s = 0; s < NS; ++s) rows[s] = r0 + 16 * s + i;
     const int tok0 = 0;
@@ -615,7 +619,7 @@ __device__ __forceinline__ void mm_down_body(uint8_t* lds, const int* rowidx, co
                 const float gs = item.shared ? sigmoid(sg[item.tok0 + c]) : 1.0f;
 #pragma unroll
                 for (int s = 0; s < NS; ++s) {
-                    const int row = kWgRows * (rt0 + rbl) + r0 + 16 * s + 4 * q;
+                    const int row = RW * (rt0 + rbl) + r0 + 16 * s + 4 * q;
                     if (row < H) {
                         f32x4 v = acc[n][s];
                         if (item.shared) v = f32x4{v[0] * gs, v[1] * gs, v[2] * gs, v[3] * gs};
@@ -666,16 +670,16 @@ __global__ __launch_bounds__(512) void k_mm_down(const uint8_t* __restrict__ dow
     else mm_down_body<kNarrow>(lds, rowidx, item, ncol, units, rt0, nrb, d0, hrec, hrec_bytes, h_rec, sg, H, Y, nt);
 }
 
-// The thin items (<= kThinCols columns) on k_mm_down's grid, launched after it: one-stage ring (55 KB of LDS), two
-// work-groups per CU.  A thin down work-group's K is one stage at n_ff <= 512, so it would otherwise hold a CU idle
-// while its only stage loads.
+// The thin items (<= kThinCols columns), launched after k_mm_down: 128 rows per work-group, one-stage ring (36 KB of
+// LDS), four work-groups per CU.  A thin down work-group's K is one stage at n_ff <= 512, so it would otherwise hold a
+// CU idle while its only stage loads.
 __global__ __launch_bounds__(512) void k_mm_down_thin(const uint8_t* __restrict__ down_exps,
                                                       const uint8_t* __restrict__ down_sh,
                                                       const uint32_t* __restrict__ hrec, uint32_t hrec_bytes, int h_rec,
                                                       const float* __restrict__ sg, const int4* __restrict__ items,
                                                       int max_items, int n_rb, int H, int F, int Fs,
                                                       float* __restrict__ Y, int nt) {
-    __shared__ __align__(16) uint8_t lds[Shape<kThin1>::kLdsBytes];
+    __shared__ __align__(16) uint8_t lds[Shape<kThinH>::kLdsBytes];
     __shared__ int rowidx[kThinCols];
     int y, rt;
     if (!xcd_item(n_rb, max_items, y, rt)) return;
@@ -687,7 +691,7 @@ __global__ __launch_bounds__(512) void k_mm_down_thin(const uint8_t* __restrict_
     __syncthreads();
     const int units = Fe >> 7;
     const uint8_t* d0 = item.shared ? down_sh : down_exps + (size_t)item.e * H * ((size_t)(F >> 7) * 36);
-    mm_down_body<kThin1>(lds, rowidx, item, ncol, units, rt, 1, d0, hrec, hrec_bytes, h_rec, sg, H, Y, nt);
+    mm_down_body<kThinH>(lds, rowidx, item, ncol, units, rt, 1, d0, hrec, hrec_bytes, h_rec, sg, H, Y, nt);
 }
 
 // ------------------------------------------------------------------------------------------------ launchers
@@ -894,8 +898,9 @@ hipError_t launch_mm_down(const uint8_t* down_exps, const uint8_t* down_sh, cons
     const int n_rb = (H + kWgRows - 1) / kWgRows, n_rg = (n_rb + kDownRbw - 1) / kDownRbw;
     hipLaunchKernelGGL(k_mm_down, dim3(xcd_grid(n_rg, max_items)), dim3(512), 0, s, down_exps, down_sh, hrec,
                        (uint32_t)bytes, h_rec, sg, items, max_items, n_rg, n_rb, H, F, Fs, Y, nt);
-    hipLaunchKernelGGL(k_mm_down_thin, dim3(xcd_grid(n_rb, max_items)), dim3(512), 0, s, down_exps, down_sh, hrec,
-                       (uint32_t)bytes, h_rec, sg, items, max_items, n_rb, H, F, Fs, Y, nt);
+    const int n_rb_thin = (H + Shape<kThinH>::kRows - 1) / Shape<kThinH>::kRows;
+    hipLaunchKernelGGL(k_mm_down_thin, dim3(xcd_grid(n_rb_thin, max_items)), dim3(512), 0, s, down_exps, down_sh,
+                       hrec, (uint32_t)bytes, h_rec, sg, items, max_items, n_rb_thin, H, F, Fs, Y, nt);
     return hipGetLastError();
 }
 
