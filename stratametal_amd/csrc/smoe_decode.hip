@@ -513,35 +513,28 @@ __device__ __forceinline__ void router_row_dot1f(const RouterRow<MAXC, true>& R,
 }
 
 template <int MAXC, bool F32>
-// (The arguments a work-group reads before its first loads come first: the library is built with kernel-argument
-// preloading, so the first 14 dwords arrive in SGPRs with the wave instead of by a scalar load from memory.)
-__global__ __launch_bounds__(256) void k_router(int H, int E, int rows_total, int T, int tok_tile, int clear_n16,
-                                                 const void* __restrict__ W, const uint16_t* __restrict__ w_inp,
-                                                 const float* __restrict__ bias, const float* __restrict__ xf,
-                                                 const uint16_t* __restrict__ xb, float* __restrict__ logits,
-                                                 int ld_logits, float* __restrict__ sg, uint32_t* __restrict__ ximg,
-                                                 int img_natural, const float* __restrict__ rprev, float eps,
+// (Every argument a row block reads before its first loads is among the first 14 dwords: the library is built with
+// kernel-argument preloading, so those arrive in SGPRs with the wave, and a scalar load of a later argument, a round
+// trip to memory, is waited for only after the loads are out.  The rows are E, and one more, the shared gate's, when
+// w_inp is given.)
+__global__ __launch_bounds__(256) void k_router(int H, int E, int T, int tok_tile, const void* __restrict__ W,
+                                                 const uint16_t* __restrict__ w_inp, const float* __restrict__ bias,
+                                                 const float* __restrict__ xf, const float* __restrict__ rprev,
+                                                 int clear_n16, const uint16_t* __restrict__ xb,
+                                                 float* __restrict__ logits, int ld_logits, float* __restrict__ sg,
+                                                 uint32_t* __restrict__ ximg, int img_natural, float eps,
                                                  float* __restrict__ xout, uint4* __restrict__ clear) {
     extern __shared__ __align__(16) uint32_t smem[];
     __shared__ uint8_t qsc[8][32];
     __shared__ float inv_s[16];
     __shared__ float wsum_s[4][4];
     SMOE_STAMP(0, 2);
+    const int rows_total = E + (w_inp ? 1 : 0);
     const int t0 = blockIdx.y * tok_tile;
     const int nt = min(tok_tile, T - t0);
     const int row_blocks = (rows_total + 3) / 4;
     const bool img_block = (int)blockIdx.x >= row_blocks;  // uniform
     const int tid = threadIdx.x;
-    // an image block: eight q8_1 blocks of the tile's x, one per half wave; its values are loaded first
-    const int hw = tid >> 5;
-    const int bb = ((int)blockIdx.x - row_blocks) * 8 + hw;
-    const bool live = img_block && ximg != nullptr && bb < nt * (H >> 5);  // (the grid may pad past the image blocks)
-    const size_t blk = (size_t)t0 * (H >> 5) + (live ? bb : 0);
-    float iv = 0.0f, ir = 0.0f;
-    if (img_block) {
-        iv = live ? xf[blk * 32 + (tid & 31)] : 0.0f;
-        if (rprev && live) ir = rprev[blk * 32 + (tid & 31)];
-    }
     // a row block: the wave's weight row (clamped, every load issued), in flight during the staging below
     RouterRow<MAXC, F32> R;
     if (!img_block) router_row_load<MAXC, F32>(W, w_inp, bias, H, E, rows_total, blockIdx.x, R);
@@ -554,6 +547,18 @@ __global__ __launch_bounds__(256) void k_router(int H, int E, int rows_total, in
     } else {
         if (x1 && !img_block) router_x1_load<MAXC>(xf + (size_t)t0 * H, H, X1);
     }
+    // an image block: eight q8_1 blocks of the tile's x, one per half wave (blocks past the tile, where the grid pads,
+    // load block 0 and store nothing; without f32 x there are no images, and padding blocks load nothing)
+    const int hw = tid >> 5;
+    const int bb = ((int)blockIdx.x - row_blocks) * 8 + hw;
+    const bool in_tile = bb < nt * (H >> 5);
+    const size_t blk = (size_t)t0 * (H >> 5) + (in_tile ? bb : 0);
+    float iv = 0.0f, ir = 0.0f;
+    if (img_block && xf) {
+        iv = xf[blk * 32 + (tid & 31)];
+        if (rprev) ir = rprev[blk * 32 + (tid & 31)];
+    }
+    const bool live = img_block && ximg != nullptr && in_tile;
     // the exchange words of the kernel after this one (k_q2_moe_small), cleared: no launch reads them before it
     for (int i = ((int)blockIdx.y * (int)gridDim.x + (int)blockIdx.x) * 256 + (int)threadIdx.x; i < clear_n16;
          i += (int)(gridDim.x * gridDim.y) * 256)
@@ -1809,6 +1814,7 @@ __device__ __forceinline__ bool gu_route_wg(
 #pragma unroll
     for (int j = 0; j < 6; ++j)
         pre[j] = reinterpret_cast<const u32x4*>(ximg)[min(min(j, npre - 1) * 256 + tid, pieces - 1)];
+    SMOE_STAMP(1, 15);  // the image loads are issued
     GuRouteLds& L = *reinterpret_cast<GuRouteLds*>(smem + kGuCols * qb * kImgLdsDw + 4);
     Item item;
     bool synced;
@@ -2640,6 +2646,8 @@ hipError_t launch_router(const float* xf, const uint16_t* xb, const void* W, con
                          float* xout, uint4* clear, int clear_n16, int w_f32) {
     // the fused junction is the row-per-wave path's, for rows up to 4096; so is the clearing of the exchange
     if (rprev && (tile_rows || !xf || H > 4096)) return hipErrorInvalidValue;
+    // the rows are E and, with w_inp, the shared gate's (the kernels count them so); images are made from f32 x
+    if (rows_total != E + (w_inp ? 1 : 0) || (ximg && !xf)) return hipErrorInvalidValue;
     if (clear_n16 && (tile_rows || !clear)) return hipErrorInvalidValue;
     // the f32 router runs on the row-per-wave path from f32 x
     if (w_f32 && (tile_rows || !xf || H % 4 || H > 4096)) return hipErrorInvalidValue;
@@ -2653,8 +2661,8 @@ hipError_t launch_router(const float* xf, const uint16_t* xb, const void* W, con
         dim3 grid(router_grid_x((rows_total + 3) / 4 + img_blocks, T, tile), (unsigned)((T + tile - 1) / tile));
         const size_t lds = (size_t)tile * H * 4;
 #define SMOE_ROUTER_F32(C)                                                                                          \
-    hipLaunchKernelGGL((k_router<C, true>), grid, dim3(256), lds, s, H, E, rows_total, T, tile, clear_n16, W, w_inp, \
-                       bias, xf, xb, logits, ld_logits, sg, ximg, img_natural, rprev, eps, xout, clear)
+    hipLaunchKernelGGL((k_router<C, true>), grid, dim3(256), lds, s, H, E, T, tile, W, w_inp, bias, xf, rprev,     \
+                       clear_n16, xb, logits, ld_logits, sg, ximg, img_natural, eps, xout, clear)
         if (maxc4 <= 2) SMOE_ROUTER_F32(2);
         else if (maxc4 <= 4) SMOE_ROUTER_F32(4);
         else if (maxc4 <= 8) SMOE_ROUTER_F32(8);
@@ -2677,8 +2685,8 @@ hipError_t launch_router(const float* xf, const uint16_t* xb, const void* W, con
     dim3 grid(router_grid_x((rows_total + 3) / 4 + img_blocks, T, tile), (unsigned)((T + tile - 1) / tile));
     const size_t lds = (size_t)tile * H * 2;
 #define SMOE_ROUTER(C)                                                                                          \
-    hipLaunchKernelGGL((k_router<C, false>), grid, dim3(256), lds, s, H, E, rows_total, T, tile, clear_n16, W, w_inp, \
-                       bias, xf, xb, logits, ld_logits, sg, ximg, img_natural, rprev, eps, xout, clear)
+    hipLaunchKernelGGL((k_router<C, false>), grid, dim3(256), lds, s, H, E, T, tile, W, w_inp, bias, xf, rprev,    \
+                       clear_n16, xb, logits, ld_logits, sg, ximg, img_natural, eps, xout, clear)
     if (maxc <= 2) SMOE_ROUTER(2);
     else if (maxc <= 4) SMOE_ROUTER(4);
     else if (maxc <= 8) SMOE_ROUTER(8);

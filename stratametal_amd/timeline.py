@@ -7,7 +7,8 @@ stamps compiled in (SMOE_STAMPS; lib/libsmoe_stamps.so, never the product librar
 
 The layer is configs[0]'s geometry (hidden 2048, 512 experts + the shared one, top-10, n_ff 512, Q2_0), twelve
 distinct synthetic layers taken in turn so that the weights come from HBM, and the memory-side cache flushed
-(a 1 GiB read) before each call.  Per phase: the median and the maximum over the role's work-groups, each the
+(a 1 GiB read) before each call; with `--no-flush --layers 48` the calls follow each other as in the benchmark's
+replay (the code and the workspace stay cached, the weights of 48 layers do not).  Per phase: the median and the maximum over the role's work-groups, each the
 median over the measured calls; times from the first router work-group's start.  A stamp costs its work-group
 a clock read and a store (~0.1-0.3 us), so the phases run later than in the product build by up to that much per
 stamp passed.
@@ -24,7 +25,8 @@ from . import build as B
 LIB_STAMPS = os.path.join(B.LIBDIR, "libsmoe_stamps.so")
 ROLES = {0: "router", 1: "gate/up (shared)", 2: "gate/up (routed)", 9: "gate/up (no expert)", 3: "writer",
          4: "down"}
-PHASES = [(2, "start"), (3, "dots begin"), (4, "sg loaded"), (13, "logits in registers"), (14, "routed"),
+PHASES = [(2, "start"), (3, "dots begin"), (15, "image loads issued"), (4, "sg loaded"), (13, "logits in registers"),
+          (14, "routed"),
           (6, "item known"), (7, "weights in registers"), (8, "h words polled"), (9, "h seen"),
           (11, "first rows formed"), (12, "rows parked"), (10, "end")]
 
@@ -53,7 +55,7 @@ def build(verbose: bool = True) -> str:
     return LIB_STAMPS
 
 
-def run(tokens: int = 1, reps: int = 12, warm: int = 4) -> str:
+def run(tokens: int = 1, reps: int = 12, warm: int = 4, n_layers: int = 12, flush_each: bool = True) -> str:
     import ctypes as C
 
     import numpy as np
@@ -68,7 +70,6 @@ def run(tokens: int = 1, reps: int = 12, warm: int = 4) -> str:
     L.smoe_debug_set_stamps.argtypes = [C.c_void_p]
     L.smoe_debug_set_stamps.restype = C.c_int
     g = S.Geom()
-    n_layers = 12
     layers = [S.synth_layer(g, 1000 + i) for i in range(n_layers)]
     ml = S.MoELayer(g, layers[0], max_tokens=tokens)
     flush = torch.zeros((1 << 30) // 4, dtype=torch.float32, device="cuda")
@@ -80,7 +81,8 @@ def run(tokens: int = 1, reps: int = 12, warm: int = 4) -> str:
     try:
         for rep in range(reps + warm):
             ml._wc = S._weights_c(layers[rep % n_layers])
-            sink = flush.sum()
+            if flush_each or rep == 0:
+                sink = flush.sum()
             torch.cuda.synchronize()
             st.zero_()
             torch.cuda.synchronize()
@@ -106,8 +108,10 @@ def run(tokens: int = 1, reps: int = 12, warm: int = 4) -> str:
         del sink
     finally:
         L.smoe_debug_set_stamps(None)
-    lines = [f"decode T={tokens}, configs[0] geometry, {reps} calls after {warm} warm-up calls; last work-group "
-             f"end {np.median(ends):.2f} us (median over calls, from the first router work-group's start)", "",
+    lines = [f"decode T={tokens}, configs[0] geometry, {n_layers} layers in turn, "
+             f"{'memory-side cache flushed before each call' if flush_each else 'no flush between calls'}, {reps} calls "
+             f"after {warm} warm-up calls; last work-group end {np.median(ends):.2f} us (median over calls, from the "
+             f"first router work-group's start)", "",
              "| role | work-groups | phase | median us | max us |", "|---|---|---|---|---|"]
     for role, name in ROLES.items():
         if (role, "n") not in acc:
@@ -129,11 +133,14 @@ def main(argv=None) -> int:
     ap.add_argument("what", choices=("build", "run"))
     ap.add_argument("--tokens", type=int, default=1)
     ap.add_argument("--reps", type=int, default=12)
+    ap.add_argument("--layers", type=int, default=12, help="distinct synthetic layers taken in turn")
+    ap.add_argument("--no-flush", action="store_true", help="no cache flush between calls (the bench's replay: "
+                    "use enough layers that their weights exceed the Infinity Cache)")
     a = ap.parse_args(argv)
     if a.what == "build":
         build()
     else:
-        print(run(a.tokens, a.reps), flush=True)
+        print(run(a.tokens, a.reps, n_layers=a.layers, flush_each=not a.no_flush), flush=True)
     return 0
 
 
