@@ -2320,18 +2320,20 @@ __device__ __forceinline__ void down_wg(int r0, uint32_t* smem, const float* lg,
 }
 
 template <int NIT, int MAXUPL, int DMAXUPL, int DNT>
-// (The arguments of the role split, the image loads and the routing come first: the first 14 dwords arrive
-// preloaded in SGPRs.)
+// (The arguments of the role split, the image loads, the routing and the exchange come first, T, k and has_shared
+// packed into one dword (tkh = T | k << 8 | has_shared << 16), so that they fit the first 14 dwords, which arrive
+// preloaded in SGPRs: a later argument is a scalar load, a round trip to memory, and the exchange pointer, which
+// both roles hold from the start, would otherwise be waited for before the first loads.)
 __global__ __launch_bounds__(256) void k_q2_moe_small(
-    int max_items, int h_blocks, int T, int E, int k, int H, int F, int Fs, int has_shared,
-    const uint32_t* __restrict__ ximg, const float* __restrict__ logits, const float* __restrict__ sg,
+    int max_items, int h_blocks, int E, int H, int F, int Fs, int tkh, int npass, const uint32_t* __restrict__ ximg,
+    const float* __restrict__ logits, uint64_t* __restrict__ xchg, const float* __restrict__ sg,
     const uint8_t* __restrict__ gate_exps, const uint8_t* __restrict__ up_exps, const uint8_t* __restrict__ gate_sh,
     const uint8_t* __restrict__ up_sh, const uint8_t* __restrict__ down_exps, const uint8_t* __restrict__ down_sh,
     int32_t* __restrict__ ids, float* __restrict__ wts, int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
     int32_t* __restrict__ perm, int32_t* __restrict__ slot, int32_t* __restrict__ elist, int32_t* __restrict__ n_list,
-    int4* __restrict__ items, uint64_t* __restrict__ xchg, int npass, int add_shared, float* __restrict__ y,
-    int spin_limit, int32_t* __restrict__ status) {
+    int4* __restrict__ items, int add_shared, float* __restrict__ y, int spin_limit, int32_t* __restrict__ status) {
     extern __shared__ __align__(16) uint32_t smem[];
+    const int T = tkh & 0xFF, k = (tkh >> 8) & 0xFF, has_shared = (tkh >> 16) & 1;
     const int hbn = h_blocks;  // rows blocks of the widest expert
     const int n_gu = max_items * hbn + 1;
     const int id = blockIdx.x;
@@ -2910,9 +2912,10 @@ hipError_t launch_q2_moe_small(const uint8_t* gate_exps, const uint8_t* up_exps,
                                int32_t* offsets, int32_t* perm, int32_t* slot, int32_t* elist, int32_t* n_list,
                                int4* items, int max_items, int h_blocks, uint8_t* xchg, int add_shared, float* y,
                                int32_t* status, hipStream_t s) {
-    if (T < 1 || T > kShCols || T * k > kSmallPairs || E > 1024 || max_items + 1 > kDcItems ||
+    if (T < 1 || T > kShCols || T * k > kSmallPairs || E > 1024 || max_items + 1 > kDcItems || k < 1 || k > 255 ||
         !moe_small_ok(T, k, H, F, Fs, has_shared, h_blocks))
         return hipErrorInvalidValue;
+    const int tkh = T | (k << 8) | ((has_shared ? 1 : 0) << 16);  // (the kernel's packed T, k, has_shared)
     int npass, dmaxupl;
     small_down_shape(F, Fs, has_shared, npass, dmaxupl);
     uint64_t* xw = reinterpret_cast<uint64_t*>(xchg);
@@ -2927,20 +2930,20 @@ hipError_t launch_q2_moe_small(const uint8_t* gate_exps, const uint8_t* up_exps,
 #define SMOE_MS(N, U)                                                                                                \
     do {                                                                                                             \
         if (d3)                                                                                                      \
-            hipLaunchKernelGGL((k_q2_moe_small<N, U, 1, 3>), grid, dim3(256), lds, s, max_items, h_blocks, T, E, k,  \
-                               H, F, Fs, has_shared, ximg, logits, sg, gate_exps, up_exps, gate_sh, up_sh, down_exps, \
-                               down_sh, ids, wts, counts, offsets, perm, slot, elist, n_list, items, xw, npass,       \
-                               add_shared, y, spin, status);                                                          \
+            hipLaunchKernelGGL((k_q2_moe_small<N, U, 1, 3>), grid, dim3(256), lds, s, max_items, h_blocks, E, H, F,  \
+                               Fs, tkh, npass, ximg, logits, xw, sg, gate_exps, up_exps, gate_sh, up_sh, down_exps,   \
+                               down_sh, ids, wts, counts, offsets, perm, slot, elist, n_list, items, add_shared, y,   \
+                               spin, status);                                                                         \
         else if (dmaxupl == 1)                                                                                       \
-            hipLaunchKernelGGL((k_q2_moe_small<N, U, 1, 4>), grid, dim3(256), lds, s, max_items, h_blocks, T, E, k,  \
-                               H, F, Fs, has_shared, ximg, logits, sg, gate_exps, up_exps, gate_sh, up_sh, down_exps, \
-                               down_sh, ids, wts, counts, offsets, perm, slot, elist, n_list, items, xw, npass,       \
-                               add_shared, y, spin, status);                                                          \
+            hipLaunchKernelGGL((k_q2_moe_small<N, U, 1, 4>), grid, dim3(256), lds, s, max_items, h_blocks, E, H, F,  \
+                               Fs, tkh, npass, ximg, logits, xw, sg, gate_exps, up_exps, gate_sh, up_sh, down_exps,   \
+                               down_sh, ids, wts, counts, offsets, perm, slot, elist, n_list, items, add_shared, y,   \
+                               spin, status);                                                                         \
         else                                                                                                         \
-            hipLaunchKernelGGL((k_q2_moe_small<N, U, 2, 4>), grid, dim3(256), lds, s, max_items, h_blocks, T, E, k,  \
-                               H, F, Fs, has_shared, ximg, logits, sg, gate_exps, up_exps, gate_sh, up_sh, down_exps, \
-                               down_sh, ids, wts, counts, offsets, perm, slot, elist, n_list, items, xw, npass,       \
-                               add_shared, y, spin, status);                                                          \
+            hipLaunchKernelGGL((k_q2_moe_small<N, U, 2, 4>), grid, dim3(256), lds, s, max_items, h_blocks, E, H, F,  \
+                               Fs, tkh, npass, ximg, logits, xw, sg, gate_exps, up_exps, gate_sh, up_sh, down_exps,   \
+                               down_sh, ids, wts, counts, offsets, perm, slot, elist, n_list, items, add_shared, y,   \
+                               spin, status);                                                                         \
     } while (0)
     SMOE_SHAPE_DISPATCH(SMOE_MS)
 #undef SMOE_MS
