@@ -1499,7 +1499,7 @@ __device__ __forceinline__ bool gu_issue(const Item& item, int hb, const uint8_t
                                          int F, StagePieces& sp, uint32_t (&w)[NIT][MAXUPL][9]) {
     const int nc0 = min(kGuCols, item.ncol);
     const bool direct = stage_direct(item, 0, nc0, true);
-    if (direct) stage_issue_direct(sp, ximg, H >> 5, 0, nc0, kGuCols, 0, item, true);
+    if (direct) stage_issue_direct<256>(sp, ximg, H >> 5, 0, nc0, kGuCols, 0, item, true);
     __builtin_amdgcn_sched_barrier(0);
     gu_load_weights<NIT, MAXUPL>(item, hb, gate_exps, up_exps, gate_sh, up_sh, H, F, w);
     __builtin_amdgcn_sched_barrier(0);
@@ -1512,8 +1512,8 @@ __device__ __forceinline__ void gu_commit(const Item& item, bool direct, const S
                                           int H) {
     const int qb = H >> 5, nc0 = min(kGuCols, item.ncol);
     if (direct) stage_commit_direct(sp, smem);
-    else stage_images(smem, ximg, qb, 0, nc0, kGuCols, item, perm, k, true, 0, 4 * 256);
-    stage_images(smem, ximg, qb, 0, nc0, kGuCols, item, perm, k, true, 4 * 256);  // rounds beyond the first
+    else stage_images<256>(smem, ximg, qb, 0, nc0, kGuCols, item, perm, k, true, 0, 4 * 256);
+    stage_images<256>(smem, ximg, qb, 0, nc0, kGuCols, item, perm, k, true, 4 * 256);  // rounds beyond the first
 }
 
 // Dots of every column of the unit (the first batch already in `smem`, later batches staged here), SwiGLU, q8_1
@@ -1536,7 +1536,7 @@ __device__ __forceinline__ void gu_compute(const Item& item, int hb, uint32_t* s
     for (int c0 = 0; c0 < item.ncol; c0 += kGuCols) {
         const int nc = min(kGuCols, item.ncol - c0);
         if (!PRESTAGED && c0 > 0) {
-            stage_images(smem, ximg, qb, c0, nc, kGuCols, item, perm, k, true);
+            stage_images<256>(smem, ximg, qb, c0, nc, kGuCols, item, perm, k, true);
             __syncthreads();
         }
         for (int c = 0; c < nc; ++c) {
@@ -1612,15 +1612,16 @@ __device__ __forceinline__ void q2_gu_item(const Item& item, int hb, uint32_t* s
 }
 
 template <int NIT, int MAXUPL, bool HQ>
-__global__ __launch_bounds__(256) void k_q2_gu(const uint8_t* __restrict__ gate_exps, const uint8_t* __restrict__ up_exps,
+// (What a routed item's work-group reads before its image and weight loads is in the first 14 dwords, which arrive
+// preloaded in SGPRs: the item's entry is the one scalar round trip before those loads; the shared expert's weights
+// and the later arguments are scalar loads waited for where they are used.)
+__global__ __launch_bounds__(256) void k_q2_gu(const int4* __restrict__ items, const uint32_t* __restrict__ ximg,
+                                                const uint8_t* __restrict__ gate_exps, const uint8_t* __restrict__ up_exps,
+                                                const uint64_t* __restrict__ eptr, int H, int F, int Fs, int k,
                                                 const uint8_t* __restrict__ gate_sh, const uint8_t* __restrict__ up_sh,
-                                                const uint32_t* __restrict__ ximg, const int4* __restrict__ items,
-                                                const int32_t* __restrict__ perm, int k, int H, int F, int Fs,
-                                                uint32_t* __restrict__ himg, int h_blocks, const StageOut so,
-                                                const uint64_t* __restrict__ eptr) {
+                                                const int32_t* __restrict__ perm, uint32_t* __restrict__ himg,
+                                                int h_blocks, const StageOut so) {
     extern __shared__ __align__(16) uint32_t smem[];
-    asm volatile("" ::"s"(gate_exps), "s"(up_exps), "s"(gate_sh), "s"(up_sh), "s"(ximg), "s"(himg), "s"(perm), "s"(k),
-                 "s"(H), "s"(F), "s"(Fs), "s"(h_blocks));  // every kernarg loaded before the item
     Item item;
     if (!work_item_uniform(items, blockIdx.y, item)) return;
     if ((int)blockIdx.x * 32 >= (item.shared ? Fs : F)) return;
@@ -1856,14 +1857,14 @@ __global__ __launch_bounds__(256) void k_q2_gu_route(
 // The item's h images are copied to LDS `cps` columns at a time; each group leader writes its row's value to
 // Y[first + c][row] (the shared rows times sigmoid(sg[t])).
 template <int NIT, int MAXUPL>
-__global__ __launch_bounds__(256) void k_q2_down(const uint8_t* __restrict__ down_exps, const uint8_t* __restrict__ down_sh,
-                                                  const uint32_t* __restrict__ himg, int h_blocks, const float* __restrict__ sg,
-                                                  const int4* __restrict__ items, int H, int F, int Fs, int cps,
-                                                  float* __restrict__ Y, const uint64_t* __restrict__ eptr,
+// (As k_q2_gu: what a routed item's work-group reads before its image and weight loads is in the first 14 dwords.)
+__global__ __launch_bounds__(256) void k_q2_down(const int4* __restrict__ items, const uint32_t* __restrict__ himg,
+                                                  const uint8_t* __restrict__ down_exps,
+                                                  const uint64_t* __restrict__ eptr, int H, int F, int Fs, int h_blocks,
+                                                  int cps, const uint8_t* __restrict__ down_sh,
+                                                  const float* __restrict__ sg, float* __restrict__ Y,
                                                   const int32_t* __restrict__ dmap) {
     extern __shared__ __align__(16) uint32_t smem[];
-    asm volatile("" ::"s"(down_exps), "s"(down_sh), "s"(himg), "s"(sg), "s"(Y), "s"(h_blocks), "s"(H), "s"(F),
-                 "s"(Fs), "s"(cps));  // every kernarg loaded before the item
     Item item;
     if (!work_item_uniform(items, blockIdx.y, item)) return;
     const int Fe = item.shared ? Fs : F;
@@ -1882,7 +1883,7 @@ __global__ __launch_bounds__(256) void k_q2_down(const uint8_t* __restrict__ dow
     // past H reloads row H - 1; see k_q2_gu)
     const int nc0 = min(cps, item.ncol);
     StagePieces sp;
-    stage_issue_direct(sp, himg, h_blocks, 0, nc0, cps, 0, item, false);
+    stage_issue_direct<256>(sp, himg, h_blocks, 0, nc0, cps, 0, item, false);
     __builtin_amdgcn_sched_barrier(0);
     uint32_t w[NIT][MAXUPL][9];
 #pragma unroll
@@ -1894,14 +1895,14 @@ __global__ __launch_bounds__(256) void k_q2_down(const uint8_t* __restrict__ dow
     }
     __builtin_amdgcn_sched_barrier(0);
     stage_commit_direct(sp, smem);
-    stage_images(smem, himg, h_blocks, 0, nc0, cps, item, nullptr, 1, false, 4 * 256);  // rounds beyond the first
+    stage_images<256>(smem, himg, h_blocks, 0, nc0, cps, item, nullptr, 1, false, 4 * 256);  // rounds beyond the first
     __syncthreads();
     float dw[NIT][MAXUPL][2];
     unit_scales(w, dw);
     for (int c0 = 0; c0 < item.ncol; c0 += cps) {
         const int nc = min(cps, item.ncol - c0);
         if (c0 > 0) {
-            stage_images(smem, himg, h_blocks, c0, nc, cps, item, nullptr, 1, false);
+            stage_images<256>(smem, himg, h_blocks, c0, nc, cps, item, nullptr, 1, false);
             __syncthreads();
         }
         for (int c = 0; c < nc; ++c) {
@@ -2765,11 +2766,11 @@ hipError_t launch_q2_gu(const uint8_t* gate_exps, const uint8_t* up_exps, const 
     const bool traced = so && so->any();
 #define SMOE_GU(N, U)                                                                                                \
     if (traced)                                                                                                      \
-        hipLaunchKernelGGL((k_q2_gu<N, U, true>), grid, dim3(256), lds, s, gate_exps, up_exps, gate_sh, up_sh, ximg,  \
-                           items, perm, k, H, F, Fs, himg, h_blocks, *so, eptr);                                     \
+        hipLaunchKernelGGL((k_q2_gu<N, U, true>), grid, dim3(256), lds, s, items, ximg, gate_exps, up_exps, eptr, H,  \
+                           F, Fs, k, gate_sh, up_sh, perm, himg, h_blocks, *so);                                     \
     else                                                                                                             \
-        hipLaunchKernelGGL((k_q2_gu<N, U, false>), grid, dim3(256), lds, s, gate_exps, up_exps, gate_sh, up_sh, ximg, \
-                           items, perm, k, H, F, Fs, himg, h_blocks, none, eptr)
+        hipLaunchKernelGGL((k_q2_gu<N, U, false>), grid, dim3(256), lds, s, items, ximg, gate_exps, up_exps, eptr, H, \
+                           F, Fs, k, gate_sh, up_sh, perm, himg, h_blocks, none)
     SMOE_SHAPE_DISPATCH(SMOE_GU)
 #undef SMOE_GU
     return hipGetLastError();
@@ -2792,8 +2793,8 @@ hipError_t launch_q2_down(const uint8_t* down_exps, const uint8_t* down_sh, cons
     cps = cps < 1 ? 1 : cps > 16 ? 16 : cps;
     const size_t lds = (size_t)cps * col_bytes + 16;  // + the dead staging slot
 #define SMOE_DOWN(N, U)                                                                                            \
-    hipLaunchKernelGGL((k_q2_down<N, U>), grid, dim3(256), lds, s, down_exps, down_sh, himg, h_blocks, sg, items, H, F, \
-                       Fs, cps, Y, eptr, dmap)
+    hipLaunchKernelGGL((k_q2_down<N, U>), grid, dim3(256), lds, s, items, himg, down_exps, eptr, H, F, Fs, h_blocks, \
+                       cps, down_sh, sg, Y, dmap)
     SMOE_SHAPE_DISPATCH(SMOE_DOWN)
 #undef SMOE_DOWN
     return hipGetLastError();

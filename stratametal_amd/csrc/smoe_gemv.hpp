@@ -348,7 +348,8 @@ __device__ __forceinline__ void load_act_std(const uint8_t* __restrict__ blk, Ac
 }
 
 // Copying the images of columns c0 .. c0 + nc of the item (x rows by token, or h rows first + c) into LDS,
-// column-major, in rounds of four 16-byte pieces per thread (pieces base + j * blockDim.x + tid).  A round is
+// column-major, in rounds of four 16-byte pieces per thread (pieces base + j * NT + tid; NT the work-group's threads,
+// a constant, so that no kernel reads its group size, a scalar load, before these loads).  A round is
 // issued into registers (stage_issue) and stored (stage_commit) separately, so that a kernel can issue its
 // weight loads in between and the stores wait for the image loads only.  Within a round every load and store
 // is unconditional (a piece past the end reloads the last one and lands in slot cap_cols * per-column pieces,
@@ -359,12 +360,13 @@ struct StagePieces {
     img_u32x4 v[4];
     int dst[4];
 };
+template <int NT>
 __device__ __forceinline__ void stage_issue(StagePieces& sp, const uint32_t* __restrict__ img, int qb, int c0, int nc,
                                             int cap_cols, int base, const Item& it, const int32_t* perm, int k,
                                             bool by_token) {
     const int per_col = qb * (kImgDw / 4);  // uint4 per column
     const int total = nc * per_col, dead = cap_cols * per_col;
-    const int nt = (int)blockDim.x;
+    constexpr int nt = NT;
     // rows without memory reads (h rows, shared tokens, or a routed item's first four columns), so that the
     // image loads of all rounds go out together; otherwise item_token reads perm
     const bool direct = !by_token || it.shared || c0 + nc <= 4;
@@ -382,9 +384,10 @@ __device__ __forceinline__ void stage_issue(StagePieces& sp, const uint32_t* __r
         }
     }
 }
+template <int NT>
 __device__ __forceinline__ void stage_commit(const StagePieces& sp, uint32_t* act, int qb, int nc, int base) {
     const int total = nc * qb * (kImgDw / 4);
-    const int nt = (int)blockDim.x;
+    constexpr int nt = NT;
 #pragma unroll
     for (int j = 0; j < 4; ++j)
         if (base + j * nt < total) reinterpret_cast<img_u32x4*>(act)[lds_piece(sp.dst[j])] = sp.v[j];
@@ -393,11 +396,12 @@ __device__ __forceinline__ void stage_commit(const StagePieces& sp, uint32_t* ac
 // unconditional (a piece past the end, or a whole j past the end, reloads the last piece and is stored to the
 // dead slot), so that the compiler counts the loads in flight exactly and a later store waits for its own load
 // alone.
+template <int NT>
 __device__ __forceinline__ void stage_issue_direct(StagePieces& sp, const uint32_t* __restrict__ img, int qb, int c0,
                                                    int nc, int cap_cols, int base, const Item& it, bool by_token) {
     const int per_col = qb * (kImgDw / 4);
     const int total = nc * per_col, dead = cap_cols * per_col;
-    const int nt = (int)blockDim.x;
+    constexpr int nt = NT;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int raw = base + j * nt + (int)threadIdx.x;
@@ -418,14 +422,15 @@ __device__ __forceinline__ bool stage_direct(const Item& it, int c0, int nc, boo
 }
 
 // The rounds from `from` on, each issued and stored in turn.
+template <int NT>
 __device__ __forceinline__ void stage_images(uint32_t* act, const uint32_t* __restrict__ img, int qb, int c0, int nc,
                                              int cap_cols, const Item& it, const int32_t* perm, int k, bool by_token,
                                              int from = 0, int to = 1 << 30) {
     const int total = min(nc * qb * (kImgDw / 4), to);
-    for (int base = from; base < total; base += 4 * (int)blockDim.x) {
+    for (int base = from; base < total; base += 4 * NT) {
         StagePieces sp;
-        stage_issue(sp, img, qb, c0, nc, cap_cols, base, it, perm, k, by_token);
-        stage_commit(sp, act, qb, nc, base);
+        stage_issue<NT>(sp, img, qb, c0, nc, cap_cols, base, it, perm, k, by_token);
+        stage_commit<NT>(sp, act, qb, nc, base);
     }
 }
 

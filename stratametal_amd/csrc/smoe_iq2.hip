@@ -184,13 +184,16 @@ __device__ __forceinline__ float iq2_block_dot_std(const Iq2Block& B, const uint
 // nb lanes per row, one block per lane, decoded once.  Columns go in stages of 2 NW: their x images are
 // copied to LDS, every column's 64 row values parked in LDS, then each half wave quantises one column's 32 h
 // values into natural-order image block hb.
+// (What a routed item's work-group reads before its image and weight loads is in the first 14 dwords of the
+// arguments, which arrive preloaded in SGPRs; the later ones are scalar loads waited for where they are used.)
 template <int NW>
-__global__ __launch_bounds__(64 * NW) void k_iq2_gu(const uint8_t* __restrict__ gate_exps, const uint8_t* __restrict__ up_exps,
-                                                     const uint8_t* __restrict__ gate_sh, const uint8_t* __restrict__ up_sh,
-                                                     const uint32_t* __restrict__ ximg, const int4* __restrict__ items,
-                                                     const int32_t* __restrict__ perm, int k, int H, int F, int Fs,
-                                                     uint32_t* __restrict__ himg, int h_blocks, const StageOut so,
-                                                     const uint64_t* __restrict__ eptr) {
+__global__ __launch_bounds__(64 * NW) void k_iq2_gu(const int4* __restrict__ items, const uint32_t* __restrict__ ximg,
+                                                     const uint8_t* __restrict__ gate_exps,
+                                                     const uint8_t* __restrict__ up_exps,
+                                                     const uint64_t* __restrict__ eptr, int H, int F, int Fs, int k,
+                                                     const uint8_t* __restrict__ gate_sh,
+                                                     const uint8_t* __restrict__ up_sh, const int32_t* __restrict__ perm,
+                                                     uint32_t* __restrict__ himg, int h_blocks, const StageOut so) {
     constexpr int kCols = 2 * NW;
     extern __shared__ __align__(16) uint32_t smem[];
     __shared__ uint2 tab[kIq2sTabEntries];
@@ -224,7 +227,7 @@ __global__ __launch_bounds__(64 * NW) void k_iq2_gu(const uint8_t* __restrict__ 
     uint32_t off;
     if (stage_direct(item, 0, nc0, true)) {  // straight-line inside each branch, so no wait lands between the loads
         StagePieces sp;
-        stage_issue_direct(sp, ximg, qb, 0, nc0, kCols, 0, item, true);
+        stage_issue_direct<64 * NW>(sp, ximg, qb, 0, nc0, kCols, 0, item, true);
         __builtin_amdgcn_sched_barrier(0);
         off = load_block_raw(rowp, b, raw);
         __builtin_amdgcn_sched_barrier(0);
@@ -233,9 +236,9 @@ __global__ __launch_bounds__(64 * NW) void k_iq2_gu(const uint8_t* __restrict__ 
     } else {
         off = load_block_raw(rowp, b, raw);
         grid_table_store<64 * NW>(codes, tab);
-        stage_images(smem, ximg, qb, 0, nc0, kCols, item, perm, k, true, 0, 4 * 64 * NW);
+        stage_images<64 * NW>(smem, ximg, qb, 0, nc0, kCols, item, perm, k, true, 0, 4 * 64 * NW);
     }
-    stage_images(smem, ximg, qb, 0, nc0, kCols, item, perm, k, true, 4 * 64 * NW);  // rounds beyond the first
+    stage_images<64 * NW>(smem, ximg, qb, 0, nc0, kCols, item, perm, k, true, 4 * 64 * NW);  // rounds beyond the first
     __syncthreads();
     Iq2Block B[1];
     decode_block(raw, off, tab, B[0]);
@@ -243,7 +246,7 @@ __global__ __launch_bounds__(64 * NW) void k_iq2_gu(const uint8_t* __restrict__ 
     for (int c0 = 0; c0 < item.ncol; c0 += kCols) {
         const int nc = min(kCols, item.ncol - c0);
         if (c0 > 0) {
-            stage_images(smem, ximg, qb, c0, nc, kCols, item, perm, k, true);
+            stage_images<64 * NW>(smem, ximg, qb, c0, nc, kCols, item, perm, k, true);
             __syncthreads();
         }
         for (int c = 0; c < nc; ++c) {
@@ -271,11 +274,13 @@ __global__ __launch_bounds__(64 * NW) void k_iq2_gu(const uint8_t* __restrict__ 
 // Grid (H / (4 * 64 / nbf), work items); nbf = F / 256 lanes per row, 64 / nbf rows per wave.  The item's h
 // images are copied to LDS `cps` columns at a time; each group leader writes Y[first + c][row] (the shared
 // rows times sigmoid(sg[t])).
-__global__ __launch_bounds__(256) void k_iq2_down(const uint8_t* __restrict__ down_exps, const uint8_t* __restrict__ down_sh,
-                                                   const uint32_t* __restrict__ himg, int h_blocks,
-                                                   const float* __restrict__ sg, const int4* __restrict__ items, int H,
-                                                   int F, int Fs, int cps, float* __restrict__ Y,
-                                                   const uint64_t* __restrict__ eptr, const int32_t* __restrict__ dmap) {
+// (Arguments ordered as k_iq2_gu's.)
+__global__ __launch_bounds__(256) void k_iq2_down(const int4* __restrict__ items, const uint32_t* __restrict__ himg,
+                                                   const uint8_t* __restrict__ down_exps,
+                                                   const uint64_t* __restrict__ eptr, int H, int F, int Fs,
+                                                   int h_blocks, int cps, const uint8_t* __restrict__ down_sh,
+                                                   const float* __restrict__ sg, float* __restrict__ Y,
+                                                   const int32_t* __restrict__ dmap) {
     extern __shared__ __align__(16) uint32_t smem[];
     __shared__ uint2 tab[kIq2sTabEntries];
     Item item;
@@ -297,7 +302,7 @@ __global__ __launch_bounds__(256) void k_iq2_down(const uint8_t* __restrict__ do
     grid_codes_load<256>(codes);
     const int nc0 = min(cps, item.ncol);
     StagePieces sp;
-    stage_issue_direct(sp, himg, h_blocks, 0, nc0, cps, 0, item, false);
+    stage_issue_direct<256>(sp, himg, h_blocks, 0, nc0, cps, 0, item, false);
     __builtin_amdgcn_sched_barrier(0);
     uint32_t raw[21];
     uint32_t off;
@@ -305,14 +310,14 @@ __global__ __launch_bounds__(256) void k_iq2_down(const uint8_t* __restrict__ do
     __builtin_amdgcn_sched_barrier(0);
     grid_table_store<256>(codes, tab);
     stage_commit_direct(sp, smem);
-    stage_images(smem, himg, h_blocks, 0, nc0, cps, item, nullptr, 1, false, 4 * 256);  // rounds beyond the first
+    stage_images<256>(smem, himg, h_blocks, 0, nc0, cps, item, nullptr, 1, false, 4 * 256);  // rounds beyond the first
     __syncthreads();
     Iq2Block B[1];
     decode_block(raw, off, tab, B[0]);
     for (int c0 = 0; c0 < item.ncol; c0 += cps) {
         const int nc = min(cps, item.ncol - c0);
         if (c0 > 0) {
-            stage_images(smem, himg, h_blocks, c0, nc, cps, item, nullptr, 1, false);
+            stage_images<256>(smem, himg, h_blocks, c0, nc, cps, item, nullptr, 1, false);
             __syncthreads();
         }
         for (int c = 0; c < nc; ++c) {
@@ -376,8 +381,8 @@ hipError_t launch_iq2_gu(const uint8_t* gate_exps, const uint8_t* up_exps, const
     const int nb = H / 256;
     const size_t lds = (size_t)(2 * nb) * (H >> 5) * kImgLdsDw * 4 + 16;  // + the dead staging slot
 #define SMOE_IQ2_GU(NW)                                                                                           \
-    hipLaunchKernelGGL((k_iq2_gu<NW>), grid, dim3(64 * (NW)), lds, s, gate_exps, up_exps, gate_sh, up_sh, ximg, items, \
-                       perm, k, H, F, Fs, himg, h_blocks, so ? *so : StageOut{}, eptr)
+    hipLaunchKernelGGL((k_iq2_gu<NW>), grid, dim3(64 * (NW)), lds, s, items, ximg, gate_exps, up_exps, eptr, H, F, Fs, \
+                       k, gate_sh, up_sh, perm, himg, h_blocks, so ? *so : StageOut{})
     if (nb == 2) SMOE_IQ2_GU(2);
     else if (nb == 4) SMOE_IQ2_GU(4);
     else SMOE_IQ2_GU(8);
@@ -393,8 +398,8 @@ hipError_t launch_iq2_down(const uint8_t* down_exps, const uint8_t* down_sh, con
     const size_t col_bytes = (size_t)h_blocks * kImgLdsDw * 4;
     int cps = (int)(24576 / col_bytes);
     cps = cps < 1 ? 1 : cps > 16 ? 16 : cps;
-    hipLaunchKernelGGL(k_iq2_down, grid, dim3(256), (size_t)cps * col_bytes + 16, s, down_exps, down_sh, himg, h_blocks, sg,
-                       items, H, F, Fs, cps, Y, eptr, dmap);
+    hipLaunchKernelGGL(k_iq2_down, grid, dim3(256), (size_t)cps * col_bytes + 16, s, items, himg, down_exps, eptr, H, F,
+                       Fs, h_blocks, cps, down_sh, sg, Y, dmap);
     return hipGetLastError();
 }
 
