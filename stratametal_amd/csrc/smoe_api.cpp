@@ -172,7 +172,7 @@ Layout layout(const smoe_geom& g, int64_t T) {
     L.xchg = take(smoe::moe_small_xchg_bytes(kFusedRouteTokens, (int)K, max_items_gemv(g, kFusedRouteTokens),
                                              L.h_blocks));
     L.n_xflags = most(smoe::act_records_blocks(T * (H / 64)), T);
-    L.n_hflags = (Fmax / 128) * (int64_t)max_items_mfma(g, T);
+    L.n_hflags = (Fmax / 64) * (int64_t)max_items_mfma(g, T);  // one per 64 h rows of every work item
     L.oflags = take((size_t)(L.n_xflags + L.n_hflags) * 4);
     L.status = take((size_t)smoe::fused_status_words((int)H) * 4);  // the fused decode launch's wait flags
     if (sh_native(g)) {  // the native shared expert's chain: x as q8_1 blocks, gate and up rows, q8_1 of h
@@ -519,7 +519,7 @@ smoe_status forward_impl(const smoe_geom* g, const smoe_weights* w, float* x_io,
     }
     if (mfma) {
         SMOE_TRY(smoe::launch_mm_gu(ge, ue, gs, us, ximg, (int64_t)T * (H / 64), items, perm, K, H, F, Fs,
-                                    shf ? 1 : 0, n_items, himg, L.h_rec, st, hflags),
+                                    shf ? 1 : 0, n_items, himg, L.h_rec, st, hflags, E),
                  "gate/up");
         SMOE_MARK();
         SMOE_TRY(smoe::launch_mm_down(de, ds, himg, (int64_t)(P + T) * L.h_rec, L.h_rec, sg, items, H, F, Fs, n_items,

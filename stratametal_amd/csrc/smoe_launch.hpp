@@ -133,7 +133,7 @@ hipError_t launch_act_records(const float* x, int64_t n_rec, uint32_t* rec, uint
 hipError_t launch_mm_gu(const uint8_t* gate_exps, const uint8_t* up_exps, const uint8_t* gate_sh, const uint8_t* up_sh,
                         const uint32_t* xrec, int64_t n_xrec, const int4* items, const int32_t* perm, int k, int H,
                         int F, int Fs, int has_shared, int max_items, uint32_t* hrec, int h_rec, hipStream_t s,
-                        int32_t* flags = nullptr);
+                        int32_t* flags, int n_expert);  // n_expert: picks where the thin items run
 // dst[i] = src[i] for n floats (trace copies)
 hipError_t launch_copy_f32(const float* src, int64_t n, float* dst, hipStream_t s);
 hipError_t launch_flags_mask(const int32_t* fx, int64_t nx, const int32_t* fh, int64_t nh, int32_t* out,

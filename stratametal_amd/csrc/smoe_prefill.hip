@@ -198,16 +198,26 @@ constexpr int kLds = kRing + 1024;
 // same split of gate/up, whose thin work-groups stream four stages, gained nothing).
 // MODE 4 (k_mm_down_thin): MODE 3 over half the rows, 128 per work-group, one 16-row set per wave: 36 KB of LDS, so
 // four work-groups share a CU.
-enum { kThin = 0, kNarrow = 1, kWide = 2, kThin1 = 3, kThinH = 4 };
+// MODE 5 (k_mm_gu_thin): the thin gate/up shape over 64 gate and 64 up rows per work-group, one 16-row set per wave
+// (waves 0-3 gate, 4-7 up), kThinGStages stages: several work-groups share a CU (one stage: 37 KB, four per CU;
+// measured at prefill 512: thin items 68 us against 74 with two stages and two per CU, and the whole gate/up stage
+// 110 us against 123 with the thin items inside k_mm_gu).
+enum { kThin = 0, kNarrow = 1, kWide = 2, kThin1 = 3, kThinH = 4, kThinG = 5 };
+constexpr int kThinGStages = 1;
+// Thin gate/up items run in k_mm_gu_thin below this many routed pairs per expert on average (prefill 512 of the
+// benchmark: 10, the thin items the bulk of the work; 4096 tokens: 80, a few thin remainders that k_mm_gu's tail hides,
+// where the extra launch after it cost ~6 us per layer).
+constexpr int kThinApartPairs = 32;
 constexpr int kMaxTiles = 8;  // column tiles of 16 per wave at most (the wide shape's 128 columns)
 constexpr int kThinCols = 16;
 template <int MODE>
 struct Shape {
-    static constexpr bool kIsThin = MODE == kThin || MODE == kThin1 || MODE == kThinH;
+    static constexpr bool kIsThin = MODE == kThin || MODE == kThin1 || MODE == kThinH || MODE == kThinG;
     static constexpr int kTok = MODE == kWide ? 128 : MODE == kNarrow ? 64 : kThinCols;
     static constexpr int MT = (kTok + 15) / 16;  // column tiles of a wave: every wave has every column
-    static constexpr int kStages = MODE == kWide ? 3 : MODE == kNarrow ? 5 : MODE == kThin ? 2 : 1;
-    static constexpr int kRows = MODE == kThinH ? kWgRows / 2 : kWgRows;  // weight rows of a work-group
+    static constexpr int kStages =
+        MODE == kWide ? 3 : MODE == kNarrow ? 5 : MODE == kThin ? 2 : MODE == kThinG ? kThinGStages : 1;
+    static constexpr int kRows = MODE == kThinH || MODE == kThinG ? kWgRows / 2 : kWgRows;  // a work-group's weight rows
     static constexpr int NS = kRows / (16 * kWaves);                       // 16-row sets of a wave
     // units of 128 values per stage: the thin shape streams weights, four units at a time, so that a row's
     // weights arrive as one 144-byte window (16-byte aligned, 9 pieces) instead of four 48-byte ones
@@ -224,7 +234,8 @@ struct Shape {
     static constexpr int kSlots = kASlots + kWSlots;
     static constexpr int kABytes = kAPieces * 16;
     static constexpr int kStage = kABytes + kWPieces * 16;
-    static constexpr int kDummyAt = MODE == kThin1 || MODE == kThinH ? kStages * kStage : kDummy;  // padding's slot
+    static constexpr int kDummyAt =
+        MODE == kThin1 || MODE == kThinH || MODE == kThinG ? kStages * kStage : kDummy;  // the padding's slot
     static constexpr int kLdsBytes = kDummyAt + 1024;
     static_assert(UPS == 1 || UPS == 4, "one or four units per stage");
     static_assert(kAPieces % 64 == 0 && kWPieces % 64 == 0, "whole DMA instructions");
@@ -480,7 +491,9 @@ __device__ __forceinline__ bool xcd_item(int n_rb, int max_items, int& y, int& r
     rb = slot - n_rb * g;
     return y < max_items;
 }
-inline unsigned xcd_grid(int n_rb, int max_items) { return (unsigned)(n_rb * ((max_items + 7) / 8) * 8); }
+__host__ __device__ inline unsigned xcd_grid(int n_rb, int max_items) {
+    return (unsigned)(n_rb * ((max_items + 7) / 8) * 8);
+}
 
 template <int MODE>
 __device__ __forceinline__ void mm_gu_body(uint8_t* lds, const int* rowidx, const Item& item, int ncol, int rt,
@@ -530,7 +543,10 @@ __device__ __forceinline__ void mm_gu_body(uint8_t* lds, const int* rowidx, cons
     }
     if (flag) {
         const int any = __syncthreads_or(ovf ? 1 : 0);
-        if (threadIdx.x == 0) *flag = any ? 1 : 0;
+        if (threadIdx.x == 0) {
+            flag[0] = any ? 1 : 0;
+            flag[1] = 0;
+        }
     } else {
         __syncthreads();
     }
@@ -546,21 +562,23 @@ __global__ __launch_bounds__(512) void k_mm_gu(const uint8_t* __restrict__ gate_
                                                const uint32_t* __restrict__ xrec, uint32_t xrec_bytes,
                                                const int4* __restrict__ items, int max_items, int n_rb,
                                                const int32_t* __restrict__ perm, int k, int H, int F, int Fs,
-                                               uint32_t* __restrict__ hrec, int h_rec, int32_t* __restrict__ flags) {
+                                               uint32_t* __restrict__ hrec, int h_rec, int32_t* __restrict__ flags,
+                                               int thin_apart) {
     __shared__ __align__(16) uint8_t lds[kLds];
     __shared__ int rowidx[kChunk];
     int y, rt;
     if (!xcd_item(n_rb, max_items, y, rt)) return;
-    // with `flags`, this work-group's word: whether one of its h values is an fp16 overflow (0 when it has no work)
-    int32_t* flag = flags ? flags + (size_t)y * n_rb + rt : nullptr;
+    // with `flags`, this work-group's words (per 64 h rows, as k_mm_gu_thin writes them: the block's two): whether
+    // one of its h values is an fp16 overflow (0 when it has no work; a thin item's, k_mm_gu_thin writes after this)
+    int32_t* flag = flags ? flags + ((size_t)y * n_rb + rt) * 2 : nullptr;
     Item item;
     if (!work_item(items, y, item)) {
-        if (flag && threadIdx.x == 0) *flag = 0;
+        if (flag && threadIdx.x == 0) flag[0] = flag[1] = 0;
         return;
     }
     const int Fe = item.shared ? Fs : F;
-    if (128 * rt >= Fe) {
-        if (flag && threadIdx.x == 0) *flag = 0;
+    if (128 * rt >= Fe || (thin_apart && item.ncol <= kThinCols)) {  // (thin items apart: k_mm_gu_thin's)
+        if (flag && threadIdx.x == 0) flag[0] = flag[1] = 0;
         return;
     }
     const int ncol = item.ncol;
@@ -573,6 +591,90 @@ __global__ __launch_bounds__(512) void k_mm_gu(const uint8_t* __restrict__ gate_
     else if (ncol > kThinCols)
         mm_gu_body<kNarrow>(lds, rowidx, item, ncol, rt, g0, u0, xrec, xrec_bytes, H, hrec, h_rec, flag);
     else mm_gu_body<kThin>(lds, rowidx, item, ncol, rt, g0, u0, xrec, xrec_bytes, H, hrec, h_rec, flag);
+}
+
+// The thin gate/up items (<= kThinCols columns), launched after k_mm_gu: 64 h rows per work-group (waves 0-3 own
+// 16 gate rows each, waves 4-7 the same up rows), a ring of kThinGStages stages of four units, so that several
+// work-groups share a CU and one's weight stream overlaps the others' products and epilogues.  After the K
+// loop the up waves hand their sums to the gate waves through LDS; h = bf16(silu(gate) * up) goes to record rt of
+// each column's h row.
+__device__ __forceinline__ void mm_gu_thin_body(uint8_t* lds, const int* rowidx, const Item& item, int ncol, int rt,
+                                                const uint8_t* g0, const uint8_t* u0, const uint32_t* xrec,
+                                                uint32_t xrec_bytes, int H, uint32_t* hrec, int h_rec, int32_t* flag) {
+    using S = Shape<kThinG>;
+    static_assert(S::NS == 1 && S::MT == 1, "one 16-row set and one column tile per wave");
+    const int units = H >> 7;
+    const uint32_t rb = (uint32_t)units * 36u;
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, i = lane & 15,
+              q = lane >> 4;
+    const i32x4 ra = buffer_rsrc(xrec, xrec_bytes);
+    const i32x4 rg0 = buffer_rsrc(g0 + (size_t)64 * rt * rb, 64u * rb);
+    const i32x4 ru0 = buffer_rsrc(u0 + (size_t)64 * rt * rb, 64u * rb);
+    MmPlan<kThinG> pl;
+    pl.init(rowidx, wave, lane, ncol, H >> 6, rb, 64, rg0, ru0);
+    const bool up_wave = wave >= kWaves / 2;
+    const int fbase = 16 * (wave & 3);  // the wave's 16 rows within the work-group's 64 h rows
+    int rows[1];
+    rows[0] = (up_wave ? 64 : 0) + fbase + i;
+    f32x4 acc[kMaxTiles][1];
+    mm_loop<kThinG>(acc, lds, pl, units, ra, rows, 0, 1, i, q);
+    __syncthreads();  // every wave is done with the ring
+    f32x4* xs = reinterpret_cast<f32x4*>(lds + 4096);  // the up waves' sums (after the h tile)
+    if (up_wave) xs[(wave - kWaves / 2) * 64 + lane] = acc[0][0];
+    __syncthreads();
+    // h tile [column][64 rows in record order] as fp16 bits of bf16 values; lane (q, i) of a gate wave holds rows
+    // fbase + 4 q .. + 3 of column i, one aligned group of four record positions in the order (0 2 1 3)
+    uint16_t* ht = reinterpret_cast<uint16_t*>(lds);
+    bool ovf = false;
+    if (!up_wave && i < ncol) {
+        const f32x4 up = xs[wave * 64 + lane];
+        const int pos4 = rec_pos(fbase + 4 * q);
+        uint32_t hb[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float h = silu_mul_fast(acc[0][0][r], up[r]);
+            hb[r] = bf16_as_f16(h);
+            if (flag) ovf |= f16_overflow(h);
+        }
+        *reinterpret_cast<uint2*>(ht + i * 64 + pos4) = make_uint2(hb[0] | (hb[2] << 16), hb[1] | (hb[3] << 16));
+    }
+    if (flag) {
+        const int any = __syncthreads_or(ovf ? 1 : 0);
+        if (threadIdx.x == 0) *flag = any ? 1 : 0;
+    } else {
+        __syncthreads();
+    }
+    for (int idx = tid; idx < ncol * 8; idx += 512) {  // 8 chunks (one record) per column
+        const int c = idx >> 3, ch = idx & 7;
+        const uint4 v = reinterpret_cast<const uint4*>(ht + c * 64)[ch];
+        reinterpret_cast<uint4*>(hrec + ((size_t)(item.first + c) * h_rec + rt) * (kRecBytes / 4))[ch] = v;
+    }
+}
+
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(8))) void k_mm_gu_thin(const uint8_t* __restrict__ gate_exps,
+                                                    const uint8_t* __restrict__ up_exps,
+                                                    const uint8_t* __restrict__ gate_sh,
+                                                    const uint8_t* __restrict__ up_sh,
+                                                    const uint32_t* __restrict__ xrec, uint32_t xrec_bytes,
+                                                    const int4* __restrict__ items, int max_items, int n_rb,
+                                                    const int32_t* __restrict__ perm, int k, int H, int F, int Fs,
+                                                    uint32_t* __restrict__ hrec, int h_rec, int32_t* __restrict__ flags) {
+    __shared__ __align__(16) uint8_t lds[Shape<kThinG>::kLdsBytes];
+    __shared__ int rowidx[kThinCols];
+    int y, rt;
+    if (!xcd_item(n_rb, max_items, y, rt)) return;
+    Item item;
+    if (!work_item(items, y, item) || item.ncol > kThinCols) return;
+    const int Fe = item.shared ? Fs : F;
+    if (64 * rt >= Fe) return;
+    int32_t* flag = flags ? flags + (size_t)y * n_rb + rt : nullptr;
+    const int ncol = item.ncol;
+    if ((int)threadIdx.x < ncol) rowidx[threadIdx.x] = item_token(item, perm, k, threadIdx.x);
+    __syncthreads();
+    const size_t rb = (size_t)(H >> 7) * 36;
+    const uint8_t* g0 = item.shared ? gate_sh : gate_exps + (size_t)item.e * F * rb;
+    const uint8_t* u0 = item.shared ? up_sh : up_exps + (size_t)item.e * F * rb;
+    mm_gu_thin_body(lds, rowidx, item, ncol, rt, g0, u0, xrec, xrec_bytes, H, hrec, h_rec, flag);
 }
 
 // ------------------------------------------------------------------------------------------------ down
@@ -845,13 +947,22 @@ hipError_t launch_router_mfma(const uint16_t* xb, const uint16_t* W, const uint1
 hipError_t launch_mm_gu(const uint8_t* gate_exps, const uint8_t* up_exps, const uint8_t* gate_sh, const uint8_t* up_sh,
                         const uint32_t* xrec, int64_t n_xrec, const int4* items, const int32_t* perm, int k, int H,
                         int F, int Fs, int has_shared, int max_items, uint32_t* hrec, int h_rec, hipStream_t s,
-                        int32_t* flags) {
+                        int32_t* flags, int n_expert) {
     const int Fmax = has_shared && Fs > F ? Fs : F;
     const size_t bytes = act_rec_bytes(n_xrec);
     if (bytes >= kOob) return hipErrorInvalidValue;  // buffer offsets are 31-bit
     const int n_rb = Fmax / 128;
+    // the thin items in a kernel of their own when they are many (fewer than kThinApartPairs pairs per expert on
+    // average); with many pairs per expert they are few, and inside k_mm_gu they run in its tail instead of after it
+    const int P = (int)(n_xrec / (H / 64)) * k;
+    const int thin_apart = P < kThinApartPairs * n_expert ? 1 : 0;
     hipLaunchKernelGGL(k_mm_gu, dim3(xcd_grid(n_rb, max_items)), dim3(512), 0, s, gate_exps, up_exps, gate_sh, up_sh,
-                       xrec, (uint32_t)bytes, items, max_items, n_rb, perm, k, H, F, Fs, hrec, h_rec, flags);
+                       xrec, (uint32_t)bytes, items, max_items, n_rb, perm, k, H, F, Fs, hrec, h_rec, flags,
+                       thin_apart);
+    if (thin_apart)
+        hipLaunchKernelGGL(k_mm_gu_thin, dim3(xcd_grid(2 * n_rb, max_items)), dim3(512), 0, s, gate_exps, up_exps,
+                           gate_sh, up_sh, xrec, (uint32_t)bytes, items, max_items, 2 * n_rb, perm, k, H, F, Fs, hrec,
+                           h_rec, flags);
     return hipGetLastError();
 }
 
