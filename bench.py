@@ -319,7 +319,8 @@ def prefill(S, torch, g, a, flush):
     t_hbm_us = gu_bytes / (HBM_PEAK_GBS * 1e9) * 1e6
     t_mfma_us = gu_flops / (BF16_PEAK_TFLOPS * 1e12) * 1e6
     gu_gbs = gu_bytes / (st["gate_up"] * 1e-3) / 1e9
-    common = {"kernel": "k_mm_gu (routed + shared gate/up, SwiGLU, bf16 h records)", "traffic": None,
+    common = {"kernel": "k_mm_gu + k_mm_gu_thin (the gate/up stage: routed + shared gate/up, SwiGLU, bf16 h "
+                        "records; the items of at most 16 columns in a kernel of their own)", "traffic": None,
               "algorithmic_bytes_per_launch": gu_bytes, "useful_flops_per_launch": gu_flops,
               "avg_launch_ms": st["gate_up"], "roof_us": {"hbm": t_hbm_us, "mfma": t_mfma_us},
               "mfma_tflops": gu_tf, "mfma_frac": gu_tf / BF16_PEAK_TFLOPS, "hbm_gbs": gu_gbs,
