@@ -2968,6 +2968,7 @@ hipError_t launch_combine(const float* Y, const int32_t* slot, const float* wts,
     } while (0)
         if (k <= 4) SMOE_C4(4);
         else if (k <= 8) SMOE_C4(8);
+        else if (k == 10) SMOE_C4(10);  // (the configs' top-k: no batch slot reloads a row)
         else if (k <= 12) SMOE_C4(12);
         else SMOE_C4(16);
 #undef SMOE_C4
