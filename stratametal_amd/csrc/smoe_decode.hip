@@ -1158,8 +1158,10 @@ __global__ __launch_bounds__(1024) void k_dispatch(const int32_t* __restrict__ i
 }
 
 // ------------------------------------------------------------------------------------------------ dispatch (many pairs)
-// The same stable counting sort in three launches, for many pairs: chunk c holds pairs 1024 c .. 1024 c + 1023.
-//   k_dispatch_hist:  per chunk, the expert histogram (LDS atomics) -> hist[c][e];
+// The same stable counting sort in three launches (two for at most kScanLdsChunks chunks), for many pairs: chunk c
+// holds pairs 1024 c .. 1024 c + 1023.
+//   k_dispatch_hist:  per chunk, the expert histogram (LDS atomics) -> hist[c][e] (for few chunks, k_dispatch_scan
+//                     forms the same counts in its own LDS instead);
 //   k_dispatch_scan:  one work-group: per expert the total, the offsets, the touched list and the work-item table
 //                     (dispatch_block's classes and order), then hist[c][e] <- the position of chunk c's first pair
 //                     of expert e (offset + the counts of the chunks before), and each expert's first full item and
@@ -1168,6 +1170,11 @@ __global__ __launch_bounds__(1024) void k_dispatch(const int32_t* __restrict__ i
 //                     tokens of every work item.
 // Within an expert the pairs stay in ascending pair order: chunks in order, and inside a chunk by ballot ranks.
 constexpr int kDispatchChunk = 1024;
+// k_dispatch_scan counts the pairs itself, in LDS, for at most this many chunks (at 512 tokens x top-10: 5 chunks,
+// one launch fewer; at 40 chunks the one work-group's 40 id loads and LDS atomics per thread cost more than the
+// separate k_dispatch_hist launch)
+constexpr int kScanLdsChunks = 8;
+constexpr int kScanLdsCounts = kScanLdsChunks * 1024;
 
 __global__ __launch_bounds__(1024) void k_dispatch_hist(const int32_t* __restrict__ ids, int P, int E,
                                                          int32_t* __restrict__ hist) {
@@ -1186,20 +1193,44 @@ __global__ __launch_bounds__(1024) void k_dispatch_scan(int32_t* __restrict__ hi
                                                          int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
                                                          int32_t* __restrict__ elist, int32_t* __restrict__ n_list,
                                                          int4* __restrict__ items, int32_t* __restrict__ item_of,
-                                                         int max_items, int T, int has_shared, int chunk, int sh_chunk) {
+                                                         int max_items, int T, int has_shared, int chunk, int sh_chunk,
+                                                         const int32_t* __restrict__ ids) {
     __shared__ int scan[4 * 17];
+    __shared__ int lh[kScanLdsCounts];
     const int tid = threadIdx.x;
+    // with `ids`: the chunks' expert counts formed here in LDS (n_chunks * E <= kScanLdsCounts; LDS atomics, whose
+    // order does not change a count), instead of read from hist as k_dispatch_hist left them
+    const bool in_lds = ids != nullptr;
+    if (in_lds) {
+        for (int i = tid; i < n_chunks * E; i += 1024) lh[i] = 0;
+        __syncthreads();
+        for (int i0 = 0; i0 < P; i0 += 8 * 1024) {  // eight loads in flight per thread
+            int e[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int i = i0 + 1024 * u + tid;
+                e[u] = i < P ? ids[i] : -1;
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int i = i0 + 1024 * u + tid;
+                if (e[u] >= 0 && e[u] < E) atomicAdd(&lh[(i / kDispatchChunk) * E + e[u]], 1);
+            }
+        }
+        __syncthreads();
+    }
+    auto count_of = [&](int ch) { return in_lds ? lh[ch * E + tid] : hist[(size_t)ch * E + tid]; };
     int c = 0;
     if (tid < E) {  // the chunks' counts, eight loads in flight at a time
         int ch = 0;
         for (; ch + 8 <= n_chunks; ch += 8) {
             int h[8];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) h[u] = hist[(size_t)(ch + u) * E + tid];
+            for (int u = 0; u < 8; ++u) h[u] = count_of(ch + u);
 #pragma unroll
             for (int u = 0; u < 8; ++u) c += h[u];
         }
-        for (; ch < n_chunks; ++ch) c += hist[(size_t)ch * E + tid];
+        for (; ch < n_chunks; ++ch) c += count_of(ch);
     }
     const int flag = c > 0 ? 1 : 0;
     const int nfull = c / chunk;
@@ -1218,7 +1249,7 @@ __global__ __launch_bounds__(1024) void k_dispatch_scan(int32_t* __restrict__ hi
         for (; ch + 8 <= n_chunks; ch += 8) {
             int h[8];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) h[u] = hist[(size_t)(ch + u) * E + tid];
+            for (int u = 0; u < 8; ++u) h[u] = count_of(ch + u);
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
                 hist[(size_t)(ch + u) * E + tid] = run;
@@ -1226,7 +1257,7 @@ __global__ __launch_bounds__(1024) void k_dispatch_scan(int32_t* __restrict__ hi
             }
         }
         for (; ch < n_chunks; ++ch) {
-            const int h = hist[(size_t)ch * E + tid];
+            const int h = count_of(ch);
             hist[(size_t)ch * E + tid] = run;
             run += h;
         }
@@ -2726,9 +2757,11 @@ hipError_t launch_dispatch_multi(const int32_t* ids, int P, int E, int32_t* coun
     const int chunks = (P + kDispatchChunk - 1) / kDispatchChunk;
     int32_t* hist = work;
     int32_t* item_of = work + (size_t)chunks * E;
-    hipLaunchKernelGGL(k_dispatch_hist, dim3((unsigned)chunks), dim3(1024), 0, s, ids, P, E, hist);
+    // the chunk counts in the scan's own LDS for few chunks (one launch fewer), else by k_dispatch_hist
+    const bool in_lds = chunks <= kScanLdsChunks && chunks * E <= kScanLdsCounts;
+    if (!in_lds) hipLaunchKernelGGL(k_dispatch_hist, dim3((unsigned)chunks), dim3(1024), 0, s, ids, P, E, hist);
     hipLaunchKernelGGL(k_dispatch_scan, dim3(1), dim3(1024), 0, s, hist, chunks, P, E, counts, offsets, elist, n_list,
-                       items, item_of, max_items, T, has_shared, chunk, sh_chunk);
+                       items, item_of, max_items, T, has_shared, chunk, sh_chunk, in_lds ? ids : nullptr);
     hipLaunchKernelGGL(k_dispatch_rank, dim3((unsigned)chunks), dim3(1024), 0, s, ids, P, E, hist, counts, offsets,
                        item_of, perm, slot, items, k, chunk);
     return hipGetLastError();

@@ -81,6 +81,9 @@ CASES = [
     # reach 1024 (the packed scan fields must hold it)
     ("1024 experts all touched", dict(n_embd=256, n_ff=128, n_ff_shared=128, n_expert=1024, top_k=8), 2048, 18,
      True, None, S.PATH_AUTO),
+    # 8000 pairs: eight dispatch chunks over 1024 experts, the most that the dispatch scan counts in its own LDS
+    ("8 dispatch chunks over 1024 experts", dict(n_embd=256, n_ff=128, n_ff_shared=128, n_expert=1024, top_k=8),
+     1000, 29, True, None, S.PATH_AUTO),
     # the f32 router (router_dtype 1) on the prefill path: the row-per-wave router over f32 token tiles
     ("f32 router, prefill 512 Zipf 1.2", dict(router_dtype=1), 512, 19, True, "zipf", S.PATH_AUTO),
     ("f32 router, 200 tokens", dict(router_dtype=1, n_embd=512, n_ff=256, n_expert=64, top_k=6), 200, 20, True, None,
