@@ -1219,18 +1219,19 @@ __global__ __launch_bounds__(1024) void k_dispatch_scan(int32_t* __restrict__ hi
         }
         __syncthreads();
     }
-    auto count_of = [&](int ch) { return in_lds ? lh[ch * E + tid] : hist[(size_t)ch * E + tid]; };
     int c = 0;
-    if (tid < E) {  // the chunks' counts, eight loads in flight at a time
+    if (tid < E && in_lds) {
+        for (int ch = 0; ch < n_chunks; ++ch) c += lh[ch * E + tid];
+    } else if (tid < E) {  // the chunks' counts, eight loads in flight at a time
         int ch = 0;
         for (; ch + 8 <= n_chunks; ch += 8) {
             int h[8];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) h[u] = count_of(ch + u);
+            for (int u = 0; u < 8; ++u) h[u] = hist[(size_t)(ch + u) * E + tid];
 #pragma unroll
             for (int u = 0; u < 8; ++u) c += h[u];
         }
-        for (; ch < n_chunks; ++ch) c += count_of(ch);
+        for (; ch < n_chunks; ++ch) c += hist[(size_t)ch * E + tid];
     }
     const int flag = c > 0 ? 1 : 0;
     const int nfull = c / chunk;
@@ -1246,10 +1247,16 @@ __global__ __launch_bounds__(1024) void k_dispatch_scan(int32_t* __restrict__ hi
         item_of[E + tid] = n_sh + rbase;  // its remainder item
         int run = off;
         int ch = 0;
+        if (in_lds) {
+            for (; ch < n_chunks; ++ch) {
+                hist[(size_t)ch * E + tid] = run;
+                run += lh[ch * E + tid];
+            }
+        }
         for (; ch + 8 <= n_chunks; ch += 8) {
             int h[8];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) h[u] = count_of(ch + u);
+            for (int u = 0; u < 8; ++u) h[u] = hist[(size_t)(ch + u) * E + tid];
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
                 hist[(size_t)(ch + u) * E + tid] = run;
@@ -1257,7 +1264,7 @@ __global__ __launch_bounds__(1024) void k_dispatch_scan(int32_t* __restrict__ hi
             }
         }
         for (; ch < n_chunks; ++ch) {
-            const int h = count_of(ch);
+            const int h = hist[(size_t)ch * E + tid];
             hist[(size_t)ch * E + tid] = run;
             run += h;
         }
